@@ -1,0 +1,264 @@
+"""Benchmark of the MI355X GroupNorm+SiLU path (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one forward + backward of fused GroupNorm+SiLU at BASELINE
+config 3 (N=1, C=64, H=W=2048, G=16, fp32), inputs resident in HBM, run
+through the C-ABI of libsoar_gn.so on one GPU.  Prints one JSON line:
+
+  value      algorithmic HBM bytes of the step (8 tensor passes: fwd 3T,
+             bwd 5T, T = N*C*H*W*4) / measured step time, in GB/s;
+  roofline   the dominant kernel's algorithmic bytes per launch / its mean
+             hipEvent-timed duration over the timed region, against the
+             8 TB/s HBM peak; `traffic` is the rocprofv3-measured bytes per
+             launch from profiles/ when present;
+  cpu_baseline  the fp32 statement of the reference's CPU loops
+             (oracle/soar_oracle.c, single thread) on a bounded sample.
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "soar.cpp_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+METRIC = "GN+SiLU fwd+bwd achieved HBM GB/s (% of peak), 1×64×2048² fp32"
+PEAK_GBS = 8000.0
+SEED = 20261201
+
+CONFIGS = {
+    # name: (N, C, HW, G, passes, residual, blocks)
+    "cfg2_fwd": (1, 32, 2048 * 2048, 8, "fwd", False, 1),
+    "cfg3": (1, 64, 2048 * 2048, 16, "fwdbwd", False, 1),
+    "cfg4_chain": (2, 128, 1024 * 1024, 32, "fwdbwd", True, 6),
+    "cfg5": (1, 16, 2048 * 2048, 4, "fwdbwd", False, 1),
+}
+SEED_OF = {"cfg2_fwd": SEED + 2, "cfg3": SEED + 3, "cfg4_chain": SEED + 4, "cfg5": SEED + 5}
+
+# algorithmic tensor passes (units of T) per kernel launch
+PASSES = {"gn_stats_partial": 1, "gn_silu_apply": 2, "gn_silu_bwd_reduce": 2,
+          "gn_silu_bwd_dx": 3, "gn_stats_finish": 0, "gn_bwd_finish": 0}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-kernel-timing", action="store_true",
+                    help="time the steps without per-kernel events")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run a plain 1 GiB copy kernel (for rocprofv3 counter scaling)")
+    return ap.parse_args()
+
+
+def traffic_from_profiles(config):
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 PMC summary (a `TRAFFIC_JSON:` line), else None."""
+    path = os.path.join(ROOT, "profiles", f"pmc_{config}.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            m = re.match(r"\s*TRAFFIC_JSON:\s*(\{.*\})", line)
+            if m:
+                return json.loads(m.group(1))
+    return None
+
+
+def make_inputs(gn, N, C, HW, G, seed, blocks):
+    import torch
+    x = torch.empty((N, C, HW), device="cuda")
+    dy = torch.empty_like(x)
+    gn.synth_normal(x, seed, 1, 0.0, 1.0)
+    gn.synth_normal(dy, seed, 4, 0.0, 1e-2)
+    params = []
+    for b in range(blocks):
+        gamma = torch.empty(C, device="cuda")
+        beta = torch.empty(C, device="cuda")
+        gn.synth_uniform(gamma, seed + 1000 * b, 2, 0.5, 1.5)
+        gn.synth_normal(beta, seed + 1000 * b, 3, 0.0, 0.1)
+        params.append((gamma, beta))
+    return x, dy, params
+
+
+class Step:
+    """Preallocated buffers and the launch sequence of one step."""
+
+    def __init__(self, gn, N, C, HW, G, passes, residual, blocks, seed):
+        import torch
+        self.gn, self.G, self.passes, self.residual = gn, G, passes, residual
+        self.x, self.dy, self.params = make_inputs(gn, N, C, HW, G, seed, blocks)
+        # activations of a chain: acts[0] = input, acts[b+1] = block b output
+        self.acts = [self.x] + [torch.empty_like(self.x) for _ in range(blocks)]
+        self.mean = [torch.empty(N * G, device="cuda") for _ in range(blocks)]
+        self.rstd = [torch.empty(N * G, device="cuda") for _ in range(blocks)]
+        self.ws = gn.workspace(N, C, HW, G)
+        self.grads = [torch.empty_like(self.x) for _ in range(2)] if passes == "fwdbwd" else []
+        self.dparams = [(torch.zeros(C, device="cuda"), torch.zeros(C, device="cuda"))
+                        for _ in range(blocks)]
+        self.T = N * C * HW * 4
+
+    def algorithmic_bytes(self):
+        per_block = 3 if self.passes == "fwd" else 8
+        return per_block * len(self.params) * self.T
+
+    def __call__(self):
+        gn = self.gn
+        for b, (gamma, beta) in enumerate(self.params):
+            gn.gn_silu_forward(self.acts[b], gamma, beta, self.G, eps=1e-5,
+                               residual=self.residual, y=self.acts[b + 1], mean=self.mean[b],
+                               rstd=self.rstd[b], ws=self.ws)
+        if self.passes == "fwd":
+            return
+        g_in = self.dy
+        for b in reversed(range(len(self.params))):
+            gamma, beta = self.params[b]
+            g_out = self.grads[b % 2]
+            dg, db = self.dparams[b]
+            gn.gn_silu_backward(g_in, self.acts[b], gamma, beta, self.mean[b], self.rstd[b],
+                                self.G, residual=self.residual, dx=g_out, dgamma=dg, dbeta=db,
+                                ws=self.ws)
+            g_in = g_out
+
+
+def cpu_baseline():
+    """fp32 statement of the reference CPU path, one thread, on 4 of config
+    3's 16 groups (the same per-group size, 1/4 of the tensor)."""
+    import numpy as np
+    import soar_oracle as orc
+    N, C, HW, G = 1, 16, 2048 * 2048, 4
+    n = N * C * HW
+    x = orc.fill_normal(n, SEED + 3, 1)
+    gamma = orc.fill_uniform(C, SEED + 3, 2, 0.5, 1.5)
+    beta = orc.fill_normal(C, SEED + 3, 3, 0.0, 0.1)
+    dy = orc.fill_normal(n, SEED + 3, 4, 0.0, 1e-2)
+    eps = float(np.float32(1e-5))
+    orc.ref_gn_silu_fwd_bwd_f32(x, gamma, beta, dy, N, C, HW, G, eps)  # warm-up
+    runs = [orc.ref_gn_silu_fwd_bwd_f32(x, gamma, beta, dy, N, C, HW, G, eps) for _ in range(2)]
+    t = sorted(r["fwd_s"] + r["bwd_s"] for r in runs)[0]
+    tf = min(r["fwd_s"] for r in runs)
+    tb = min(r["bwd_s"] for r in runs)
+    alg = 8 * n * 4
+    return {"value": round(alg / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"N=1 C=16 H=W=2048 G=4 (4 of config 3's 16 groups), fwd+bwd, "
+                      f"best of 2 after 1 warm-up; fwd {tf * 1e3:.1f} ms, bwd {tb * 1e3:.1f} ms,"
+                      f" 1 thread of {os.cpu_count()} host CPUs"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has "
+              "no multi-GPU path.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import soar_gn as gn
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    gn.lib()
+    torch.cuda.set_device(0)
+
+    if args.copy_calibration:
+        n = 1 << 28
+        a = torch.empty(n, device="cuda")
+        b = torch.empty(n, device="cuda")
+        gn.synth_normal(a, 1, 1)
+        for _ in range(5):
+            gn.synth_copy(a, b)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4}))
+        return
+
+    N, C, HW, G, passes, residual, blocks = CONFIGS[args.config]
+    step = Step(gn, N, C, HW, G, passes, residual, blocks, SEED_OF[args.config])
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    timing = not args.no_kernel_timing
+    if timing:
+        gn.prof_summary()  # drop anything recorded so far
+        gn.prof_enable(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    if timing:
+        gn.prof_enable(False)
+        kernels = gn.prof_summary()
+    else:
+        kernels = []
+    ms = start.elapsed_time(stop) / args.steps
+    alg = step.algorithmic_bytes()
+    value = alg / (ms * 1e-3) / 1e9
+
+    roofline = None
+    kinfo = {}
+    for k in kernels:
+        avg = k["total_ms"] / k["launches"]
+        passes_k = PASSES.get(k["kernel"], 0)
+        kinfo[k["kernel"]] = {"launches_per_step": k["launches"] / args.steps,
+                              "avg_ms": round(avg, 5),
+                              "GBps": round(passes_k * step.T / (avg * 1e-3) / 1e9, 1)
+                              if passes_k else None}
+    if kernels:
+        dom = max(kernels, key=lambda k: k["total_ms"])
+        avg = dom["total_ms"] / dom["launches"]
+        per_launch = PASSES.get(dom["kernel"], 0) * step.T
+        achieved = per_launch / (avg * 1e-3) / 1e9
+        tr = traffic_from_profiles(args.config)
+        roofline = {"bound": "hbm", "kernel": dom["kernel"], "achieved": round(achieved, 1),
+                    "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
+                    "algorithmic_bytes_per_launch": per_launch,
+                    "avg_launch_ms": round(avg, 5),
+                    "traffic": tr.get(dom["kernel"]) if tr else None}
+
+    cpu = None
+    if not args.no_cpu_baseline and args.config == "cfg3":
+        cpu = cpu_baseline()
+
+    out = {
+        "metric": METRIC if args.config == "cfg3" else f"{args.config} achieved HBM GB/s",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": f"synthetic: x~N(0,1), gamma~U(0.5,1.5), beta~N(0,0.1), dy~N(0,1e-2); "
+                f"splitmix64/Box-Muller seed {SEED_OF[args.config]}",
+        "config": {"workload": {"cfg3": "GroupNorm+SiLU fwd+bwd, BASELINE config 3",
+                                "cfg2_fwd": "GroupNorm+SiLU fwd, BASELINE config 2",
+                                "cfg4_chain": "6 x (x + SiLU(GN(x))) fwd+bwd, BASELINE config 4",
+                                "cfg5": "GroupNorm+SiLU fwd+bwd shape of BASELINE config 5"}
+                   [args.config],
+                   "N": N, "C": C, "H": int(HW ** 0.5), "W": int(HW ** 0.5), "G": G,
+                   "eps": 1e-5, "blocks": blocks, "residual": residual,
+                   "algorithmic_bytes_per_step": alg},
+        "frac_of_peak": round(value / PEAK_GBS, 4),
+        "wall_s_timed": round(wall, 4),
+        "roofline": roofline,
+        "kernels": kinfo,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,213 @@
+/*
+ * soar_gn.h - C-ABI of the MI355X (gfx950) GroupNorm+SiLU path.
+ *
+ * One shared library, libsoar_gn.so, exports every function below with
+ * C linkage, plain pointers and sizes.  Pointers named x, y, dy, dx, gamma,
+ * beta, mean, rstd, dgamma, dbeta, workspace are DEVICE pointers (HBM);
+ * `stream` is a hipStream_t passed as void* (NULL = the null stream).  All
+ * kernels are enqueued asynchronously on that stream; no entry point
+ * synchronises the device except where stated.
+ *
+ * Layout: fp32, NCHW contiguous.  G groups split C channels into runs of
+ * C/G consecutive channels; a "unit" (n, g) is the M = (C/G)*H*W contiguous
+ * floats those channels occupy in sample n.  mean and rstd are float[N*G]
+ * indexed n*G + g.
+ *
+ * Every entry point returns an int status: SOAR_OK (0) or a negative code,
+ * and records a message retrievable with soar_last_error() on the calling
+ * thread.  Nothing is launched when a call returns an error.
+ *
+ * Reference interfaces replaced (pomagrenate/soar.cpp):
+ *   include/soar/cuda/cuda_kernels.hpp:8-20,82-88   operator API nn calls
+ *   src/cuda/ops/normalization_kernels.cu:93-289     GN forward/backward
+ *   src/cuda/ops/activation_kernels.cu:99-130        SiLU forward/backward
+ *   src/cuda/ops/binary_ops_kernels.cu:6-102         zero/fill/add
+ *   shaders/group_norm_stats.comp, group_norm_affine_silu.comp,
+ *   shaders/tensor_add.comp                          Vulkan GN+SiLU pair
+ *   src/memory/device_slab.cpp:6-56, src/vulkan/buffer.cpp:8-75,
+ *   src/cuda/cuda_allocator.cpp:24-77                device buffers
+ */
+#ifndef SOAR_GN_H
+#define SOAR_GN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SOAR_API __attribute__((visibility("default")))
+
+/* ---- status codes --------------------------------------------------- */
+#define SOAR_OK 0
+#define SOAR_EINVAL (-1) /* bad pointer, shape, flag or workspace size     */
+#define SOAR_ENOMEM (-2) /* device or arena allocation failed              */
+#define SOAR_EHIP (-3)   /* a HIP runtime call or kernel launch failed     */
+#define SOAR_ENODEV (-4) /* no HIP device visible                          */
+
+/* ---- flags for the fused entry points -------------------------------- */
+#define SOAR_GN_SILU 1u          /* apply SiLU after the affine GroupNorm     */
+#define SOAR_GN_RESIDUAL 2u      /* fwd: y += x;  bwd: dx += dy (x + f(x))    */
+#define SOAR_GN_ACCUMULATE_DX 4u /* bwd: dx += result instead of dx = result  */
+
+/* Message for the last failing call on this thread ("" if none). */
+SOAR_API const char* soar_last_error(void);
+
+/* 1 if a HIP device is visible, else 0.
+ * Replaces: soar::cuda::kernels::is_cuda_available (cuda_kernels.hpp:8). */
+SOAR_API int soar_is_device_available(void);
+
+/* ---- fused GroupNorm(+SiLU) ------------------------------------------- */
+
+/* Bytes of device workspace the fused entry points need for this shape
+ * (0 for an empty tensor).  The workspace holds per-chunk partial moments
+ * and per-plane sums; it carries nothing between calls. */
+SOAR_API size_t soar_gn_workspace_bytes(int64_t N, int64_t C, int64_t HW,
+                                        int64_t G);
+
+/* Forward: per unit mean and rstd = 1/sqrt(var + eps) (biased variance),
+ * then y = f(gamma_c*(x - mean)*rstd + beta_c) [+ x], f = SiLU when
+ * SOAR_GN_SILU is set, identity otherwise.  gamma/beta may be NULL (1 / 0,
+ * the affine=false module).  y may alias x.  Writes mean/rstd for the
+ * backward.
+ * Replaces: group_norm_forward (cuda_kernels.hpp:82-84) followed by
+ * silu_forward (:19), the Vulkan pair group_norm_stats.comp +
+ * group_norm_affine_silu.comp, and with SOAR_GN_RESIDUAL the add_forward
+ * (:15) of a residual block (src/nn/blocks.cpp:478-480). */
+SOAR_API int soar_gn_silu_forward(const float* x, const float* gamma,
+                                  const float* beta, float* y, float* mean,
+                                  float* rstd, int64_t N, int64_t C,
+                                  int64_t HW, int64_t G, float eps,
+                                  unsigned flags, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
+/* Backward of soar_gn_silu_forward given upstream gradient dy, the forward
+ * input x and the saved mean/rstd.  SiLU is recomputed from x (nothing but
+ * x, mean and rstd is saved by the forward).
+ *   dgamma[c] += sum_{n,hw} dz * xhat,  dbeta[c] += sum_{n,hw} dz
+ *   dx = rstd*(gamma_c*dz - (S1 + xhat*S2)/M) [+ dy] [+ previous dx]
+ * with dz the gradient at the GroupNorm output, xhat = (x-mean)*rstd,
+ * S1 = sum_{c in g} gamma_c*sum dz, S2 = sum_{c in g} gamma_c*sum dz*xhat.
+ * dx, dgamma, dbeta may be NULL (not wanted); dgamma and dbeta must be both
+ * NULL or both non-NULL.  dgamma/dbeta always accumulate (+=), summing over
+ * samples, as the reference's parameter-gradient kernels do
+ * (normalization_kernels.cu:151-152, tensor.cpp:173-192).
+ * Replaces: silu_backward (cuda_kernels.hpp:20) followed by
+ * group_norm_backward (:85-88), GroupNormNode::backward / SiLUNode::backward
+ * (src/nn/layers.cpp:502-618, 749-771) and, with SOAR_GN_RESIDUAL, the
+ * AddNode gradient merge (src/nn/blocks.cpp:28-31, tensor.cpp:194-213). */
+SOAR_API int soar_gn_silu_backward(const float* dy, const float* x,
+                                   const float* gamma, const float* beta,
+                                   const float* mean, const float* rstd,
+                                   float* dx, float* dgamma, float* dbeta,
+                                   int64_t N, int64_t C, int64_t HW,
+                                   int64_t G, unsigned flags, void* workspace,
+                                   size_t workspace_bytes, void* stream);
+
+/* ---- the reference's operator API, same argument meaning -------------- */
+/* These take the reference's exact arguments (one sample, [C,H,W]); their
+ * workspace is owned by the library (one buffer per device, grown on
+ * demand with hipMalloc, kept until process exit), so concurrent calls on
+ * different streams of one device must not overlap. */
+
+/* Replaces: group_norm_forward (cuda_kernels.hpp:82-84,
+ * normalization_kernels.cu:93-111).  gamma/beta nullable. */
+SOAR_API int soar_group_norm_forward(const float* in, const float* gamma,
+                                     const float* beta, float* out,
+                                     float* saved_mean, float* saved_rstd,
+                                     size_t num_groups, size_t C, size_t HW,
+                                     float eps, void* stream);
+
+/* Replaces: group_norm_backward (cuda_kernels.hpp:85-88,
+ * normalization_kernels.cu:251-289).  grad_in, grad_gamma, grad_beta are
+ * accumulated into (+=) and each may be NULL; gamma nullable. */
+SOAR_API int soar_group_norm_backward(const float* grad_out, const float* in,
+                                      const float* gamma,
+                                      const float* saved_mean,
+                                      const float* saved_rstd, float* grad_in,
+                                      float* grad_gamma, float* grad_beta,
+                                      size_t num_groups, size_t C, size_t HW,
+                                      void* stream);
+
+/* Replaces: silu_forward (cuda_kernels.hpp:19): y = x/(1+exp(-x)). */
+SOAR_API int soar_silu_forward(const float* x, float* y, size_t n,
+                               void* stream);
+
+/* Replaces: silu_backward (cuda_kernels.hpp:20):
+ * grad_x += grad_y * s*(1 + x*(1-s)), s = sigmoid(x).  (The reference's
+ * scalar kernel accumulates, its float4 kernel overwrites; every caller
+ * passes a zeroed grad_x, where both agree.  This one accumulates.) */
+SOAR_API int soar_silu_backward(const float* grad_y, const float* x,
+                                float* grad_x, size_t n, void* stream);
+
+/* Replaces: add_forward (cuda_kernels.hpp:15), tensor_add.comp: y = a + b. */
+SOAR_API int soar_add_forward(const float* a, const float* b, float* y,
+                              size_t n, void* stream);
+
+/* Replaces: add_backward (cuda_kernels.hpp:16): grad_a += grad_y,
+ * grad_b += grad_y; either may be NULL.  Also the device gradient
+ * accumulate of Tensor::add_grad (tensor.cpp:183, 203). */
+SOAR_API int soar_add_backward(const float* grad_y, float* grad_a,
+                               float* grad_b, size_t n, void* stream);
+
+/* Replaces: cuda_zero / cuda_fill (cuda_kernels.hpp:11-12). */
+SOAR_API int soar_zero(float* ptr, size_t n, void* stream);
+SOAR_API int soar_fill(float* ptr, float value, size_t n, void* stream);
+
+/* ---- device arena (replaces VulkanBuffer / CudaMemoryPool storage) ---- */
+/* One hipMalloc'd slab per arena, bump-allocated at `alignment` (a power
+ * of two, 256 in the reference).  Allocations made before
+ * soar_arena_freeze_static() are the static region (parameters and their
+ * gradients); soar_arena_reset_dynamic() drops everything after it in O(1),
+ * so the next step's allocations land at the same offsets.
+ * Replaces: DeviceSlabSubAllocator (src/memory/device_slab.cpp:6-56,
+ * include/soar/memory/device_slab.hpp:21-47) backed by device memory, in
+ * place of VulkanBuffer (src/vulkan/buffer.cpp:8-75) and
+ * CudaMemoryPool::allocate (src/cuda/cuda_allocator.cpp:24-77). */
+typedef struct soar_arena soar_arena;
+
+SOAR_API int soar_arena_create(size_t capacity_bytes, size_t alignment,
+                               soar_arena** arena);
+/* Zero bytes is an error (SOAR_EINVAL) as in device_slab.cpp:13-15;
+ * exhaustion is SOAR_ENOMEM (device_slab.cpp:20-25). */
+SOAR_API int soar_arena_alloc(soar_arena* arena, size_t bytes, void** dptr,
+                              size_t* offset);
+SOAR_API int soar_arena_freeze_static(soar_arena* arena);
+SOAR_API int soar_arena_reset_dynamic(soar_arena* arena);
+SOAR_API int soar_arena_info(const soar_arena* arena, size_t* capacity,
+                             size_t* current_offset, size_t* static_boundary,
+                             void** base);
+SOAR_API int soar_arena_destroy(soar_arena* arena);
+
+/* Host <-> device copies on `stream` (the Tensor::to_cuda / sync_to_host
+ * boundary, src/tensor/tensor.cpp:146-165).  These synchronise `stream`
+ * before returning, so the host buffer is free to reuse. */
+SOAR_API int soar_memcpy_h2d(void* dst, const void* src, size_t bytes,
+                             void* stream);
+SOAR_API int soar_memcpy_d2h(void* dst, const void* src, size_t bytes,
+                             void* stream);
+
+/* ---- kernel timing (no counterpart in the reference) ------------------ */
+/* When enabled, every kernel this library launches is bracketed by a pair
+ * of hipEvents recorded on the launch stream.  soar_prof_summary()
+ * synchronises those events and writes a JSON array
+ * [{"kernel":name,"launches":n,"total_ms":t},...] into buf (truncated to
+ * buflen), then clears the record.  Returns the number of kernels. */
+SOAR_API int soar_prof_enable(int on);
+SOAR_API int soar_prof_summary(char* buf, size_t buflen);
+
+/* ---- tuning (no counterpart in the reference) ------------------------- */
+/* Launch-shape knobs of the streaming kernels, set process-wide; the
+ * defaults are the measured best on MI355X.  Values are validated. */
+#define SOAR_TUNE_CHUNK 1   /* elements per block-chunk (multiple of 1024) */
+#define SOAR_TUNE_REVERSE 2 /* 1: second passes walk chunks in reverse    */
+#define SOAR_TUNE_NT_STORE 3 /* 1: non-temporal stores for y / dx         */
+SOAR_API int soar_gn_tune(int key, int64_t value);
+SOAR_API int64_t soar_gn_tune_get(int key);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SOAR_GN_H */

@@ -1,0 +1,107 @@
+/*
+ * soar_oracle.h - CPU oracle for the fused GroupNorm+SiLU path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product path links, loads or
+ * calls this library: it is the checker that tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg compare the HIP kernels against.
+ *
+ * Two families of functions live here:
+ *
+ *  orc_*_f64  float64 "truth": two-pass statistics and the exact derivative
+ *             of y = silu(gamma*(x-mean)*rstd + beta) [+ x].  Parity gates
+ *             compare the GPU path against these.
+ *
+ *  ref_*_f32  a statement, in fp32 with the same operation order, of the
+ *             reference's CPU loops (pomagrenate/soar.cpp src/nn/layers.cpp,
+ *             src/nn/blocks.cpp).  This is the "port" CPU baseline and the
+ *             second column of every parity report.
+ *
+ * Layout: fp32 NCHW contiguous; a "unit" is one (n, g) reduction domain of
+ * M = (C/G)*HW contiguous elements; mean/rstd are indexed [n*G + g].
+ *
+ * Every function's header comment cites the reference lines it follows and
+ * the test that pins it.
+ */
+#ifndef SOAR_ORACLE_H
+#define SOAR_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- synthetic inputs (splitmix64 -> 53-bit uniform -> Box-Muller) ---- */
+
+/* splitmix64 output function applied to counter `ctr` of stream `key`. */
+uint64_t orc_splitmix64_at(uint64_t key, uint64_t ctr);
+/* Key for (seed, tensor stream id); stream ids: x=1 gamma=2 beta=3 dy=4
+ * outlier_mask=5 outlier_val=6. */
+uint64_t orc_stream_key(uint64_t seed, uint32_t stream);
+/* out[i] = mean + std * N(0,1), pairs (2p, 2p+1) from one Box-Muller draw. */
+void orc_fill_normal(float* out, int64_t n, uint64_t seed, uint32_t stream,
+                     double mean, double std_dev);
+/* out[i] = lo + (hi - lo) * U[0,1). */
+void orc_fill_uniform(float* out, int64_t n, uint64_t seed, uint32_t stream,
+                      double lo, double hi);
+/* Stress input: x = center + N(0, std); with probability p per element the
+ * value is replaced by out_mean + N(0, out_std). */
+void orc_fill_stress(float* out, int64_t n, uint64_t seed, double center,
+                     double std_dev, double p, double out_mean, double out_std);
+
+/* ---- float64 truth ---- */
+
+/* Two-pass mean and biased variance of every (n,g) unit. */
+int orc_gn_stats_f64(const float* x, int64_t N, int64_t C, int64_t HW,
+                     int64_t G, double* mean, double* var);
+
+/* y = silu(gamma_c*(x-mean)*rstd + beta_c) (or without silu) [+ x].
+ * gamma/beta may be NULL (1 / 0).  y may be NULL (stats only). */
+int orc_gn_silu_fwd_f64(const float* x, const float* gamma, const float* beta,
+                        int64_t N, int64_t C, int64_t HW, int64_t G,
+                        double eps, int apply_silu, int residual, double* y,
+                        double* mean, double* rstd);
+
+/* Exact backward of orc_gn_silu_fwd_f64 at (mean, rstd) from the same call.
+ * dx may be NULL; dgamma/dbeta are written (not accumulated), may be NULL. */
+int orc_gn_silu_bwd_f64(const float* dy, const float* x, const float* gamma,
+                        const float* beta, const double* mean,
+                        const double* rstd, int64_t N, int64_t C, int64_t HW,
+                        int64_t G, int apply_silu, int residual, double* dx,
+                        double* dgamma, double* dbeta);
+
+/* ---- fp32 statement of the reference CPU path (one sample, [C,H,W]) ---- */
+
+int ref_group_norm_forward_f32(const float* x, const float* gamma,
+                               const float* beta, float* y, float* means,
+                               float* rstds, int64_t C, int64_t HW,
+                               int64_t G, float eps);
+void ref_silu_forward_f32(const float* x, float* y, int64_t n);
+void ref_silu_backward_f32(const float* grad_y, const float* x, float* grad_x,
+                           int64_t n);
+int ref_group_norm_backward_f32(const float* grad_out, const float* x,
+                                const float* gamma, const float* means,
+                                const float* rstds, float* grad_x,
+                                float* grad_gamma, float* grad_beta,
+                                int64_t C, int64_t HW, int64_t G);
+void ref_add_f32(const float* a, const float* b, float* y, int64_t n);
+void ref_accumulate_f32(const float* g, float* acc, int64_t n);
+
+/* The reference's unfused GN -> SiLU [-> residual add] sequence over N
+ * samples (per-sample loop, dgamma/dbeta summed over samples).  `gn_out`,
+ * `silu_out`, `dz` are caller scratch of N*C*HW floats (dz may alias
+ * nothing else).  dgamma/dbeta are written. */
+int ref_gn_silu_fwd_bwd_f32(const float* x, const float* gamma,
+                            const float* beta, const float* dy, int64_t N,
+                            int64_t C, int64_t HW, int64_t G, float eps,
+                            int residual, float* gn_out, float* y,
+                            float* means, float* rstds, float* dz, float* dx,
+                            float* dgamma, float* dbeta, double* fwd_seconds,
+                            double* bwd_seconds);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SOAR_ORACLE_H */

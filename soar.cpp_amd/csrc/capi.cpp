@@ -1,0 +1,585 @@
+// capi.cpp - the C-ABI of libsoar_gn.so (declared in include/soar_gn.h).
+//
+// Responsibilities: argument validation (shapes, flags, and that every
+// device pointer lies inside one device allocation large enough for the
+// bytes the kernels will touch), status codes with a per-thread message,
+// the library-owned workspace of the reference-signature entry points,
+// the device arena, and optional per-kernel hipEvent timing.
+//
+// Error convention: the reference returns silently on empty input
+// (normalization_kernels.cu:96,255) and aborts on CUDA failure
+// (cuda_common.cuh:35-43); the C boundary of the reference maps exceptions
+// to -1 (src/api/c_api.cpp:33-35).  Here empty input is SOAR_OK with no
+// launch, and every failure is a negative status, never an abort.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "gn_internal.hpp"
+#include "soar_gn.h"
+
+using soar::gn::Plan;
+using soar::gn::Tuning;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int ok() {
+    g_err.clear();
+    return SOAR_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(SOAR_EHIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+int device_count() {
+    static std::once_flag once;
+    static int count = 0;
+    std::call_once(once, [] {
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+        count = n;
+        (void)hipGetLastError();
+    });
+    return count;
+}
+
+int require_device() {
+    if (device_count() <= 0) return fail(SOAR_ENODEV, "no HIP device is visible");
+    return SOAR_OK;
+}
+
+// `p` must be device memory with at least `bytes` bytes from p to the end
+// of its allocation.  A host pointer or a too-short buffer is rejected here
+// rather than faulting the GPU.
+int check_dev(const void* p, size_t bytes, const char* name) {
+    if (!p) return fail(SOAR_EINVAL, "%s is NULL", name);
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    hipError_t e = hipMemGetAddressRange(&base, &size, const_cast<void*>(p));
+    if (e != hipSuccess || !base) {
+        (void)hipGetLastError();
+        return fail(SOAR_EINVAL, "%s (%p) is not device memory", name, p);
+    }
+    const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+    const uintptr_t q = reinterpret_cast<uintptr_t>(p);
+    if (q < b || q - b > size || size - (q - b) < bytes)
+        return fail(SOAR_EINVAL,
+                    "%s (%p) needs %zu bytes but its allocation holds %zu from there",
+                    name, p, bytes, (size_t)(size - (q - b)));
+    return SOAR_OK;
+}
+
+int check_dev_opt(const void* p, size_t bytes, const char* name) {
+    return p ? check_dev(p, bytes, name) : SOAR_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---- tuning ---------------------------------------------------------------
+std::mutex g_tune_mu;
+Tuning g_tune;
+
+Tuning current_tuning() {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    return g_tune;
+}
+
+// ---- shape validation shared by the fused entry points ---------------------
+int check_shape(int64_t N, int64_t C, int64_t HW, int64_t G, int64_t* elems) {
+    if (N < 0 || C < 0 || HW < 0)
+        return fail(SOAR_EINVAL, "negative dimension (N=%lld C=%lld HW=%lld)",
+                    (long long)N, (long long)C, (long long)HW);
+    if (G <= 0) return fail(SOAR_EINVAL, "num_groups must be positive (G=%lld)", (long long)G);
+    if (C % G != 0)
+        return fail(SOAR_EINVAL, "C=%lld is not divisible by num_groups=%lld",
+                    (long long)C, (long long)G);
+    int64_t nc = 0, e = 0;
+    if (__builtin_mul_overflow(N, C, &nc) || __builtin_mul_overflow(nc, HW, &e) ||
+        e > INT64_MAX / 4)
+        return fail(SOAR_EINVAL, "N*C*HW overflows");
+    *elems = e;
+    return SOAR_OK;
+}
+
+int check_ws(const Plan& p, void* ws, size_t ws_bytes) {
+    const size_t need = soar::gn::workspace_bytes(p);
+    if (ws_bytes < need)
+        return fail(SOAR_EINVAL, "workspace of %zu bytes is smaller than the %zu this shape needs",
+                    ws_bytes, need);
+    return check_dev(ws, need, "workspace");
+}
+
+// ---- library-owned workspace of the reference-signature entry points ------
+struct OwnedWs {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+std::vector<OwnedWs> g_ws;
+
+int owned_workspace(size_t need, void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
+    OwnedWs& w = g_ws[dev];
+    if (w.bytes < need) {
+        if (w.ptr) {
+            e = hipFree(w.ptr);  // waits for work still using the old buffer
+            w.ptr = nullptr;
+            w.bytes = 0;
+            if (e != hipSuccess) return hip_fail(e, "hipFree(workspace)");
+        }
+        size_t grow = std::max(need, (size_t)1 << 20);
+        e = hipMalloc(&w.ptr, grow);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            w.ptr = nullptr;
+            return fail(SOAR_ENOMEM, "hipMalloc of %zu workspace bytes failed", grow);
+        }
+        w.bytes = grow;
+    }
+    *out = w.ptr;
+    return SOAR_OK;
+}
+
+// ---- per-kernel hipEvent timing --------------------------------------------
+struct ProfRec {
+    const char* name;
+    hipEvent_t start, stop;
+};
+std::atomic<bool> g_prof_on{false};
+std::mutex g_prof_mu;
+std::vector<ProfRec> g_prof;
+std::vector<hipEvent_t> g_event_pool;
+
+hipEvent_t take_event() {
+    if (!g_event_pool.empty()) {
+        hipEvent_t e = g_event_pool.back();
+        g_event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return e;
+}
+
+}  // namespace
+
+namespace soar {
+namespace gn {
+
+int prof_begin(hipStream_t s, const char* kernel) {
+    if (!g_prof_on.load(std::memory_order_relaxed)) return -1;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    ProfRec r{kernel, take_event(), take_event()};
+    if (!r.start || !r.stop) return -1;
+    if (hipEventRecord(r.start, s) != hipSuccess) {
+        (void)hipGetLastError();
+        g_event_pool.push_back(r.start);
+        g_event_pool.push_back(r.stop);
+        return -1;
+    }
+    g_prof.push_back(r);
+    return (int)g_prof.size() - 1;
+}
+
+void prof_end(hipStream_t s, int token) {
+    if (token < 0) return;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    if (token < (int)g_prof.size() && hipEventRecord(g_prof[token].stop, s) != hipSuccess)
+        (void)hipGetLastError();
+}
+
+}  // namespace gn
+}  // namespace soar
+
+extern "C" {
+
+SOAR_API const char* soar_last_error(void) { return g_err.c_str(); }
+
+SOAR_API int soar_is_device_available(void) { return device_count() > 0 ? 1 : 0; }
+
+SOAR_API size_t soar_gn_workspace_bytes(int64_t N, int64_t C, int64_t HW, int64_t G) {
+    int64_t elems = 0;
+    if (check_shape(N, C, HW, G, &elems) != SOAR_OK || elems == 0) return 0;
+    Plan p;
+    if (!soar::gn::make_plan(N, C, HW, G, current_tuning(), &p)) return 0;
+    return soar::gn::workspace_bytes(p);
+}
+
+SOAR_API int soar_gn_silu_forward(const float* x, const float* gamma, const float* beta,
+                                  float* y, float* mean, float* rstd, int64_t N, int64_t C,
+                                  int64_t HW, int64_t G, float eps, unsigned flags,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+    int64_t elems = 0;
+    int rc = check_shape(N, C, HW, G, &elems);
+    if (rc) return rc;
+    if (flags & ~(SOAR_GN_SILU | SOAR_GN_RESIDUAL))
+        return fail(SOAR_EINVAL, "unsupported forward flags 0x%x", flags);
+    if (!(eps >= 0.0f)) return fail(SOAR_EINVAL, "eps must be >= 0");
+    if (elems == 0) return ok();
+    if ((rc = require_device())) return rc;
+    const size_t tb = (size_t)elems * sizeof(float);
+    const size_t sb = (size_t)(N * G) * sizeof(float);
+    if ((rc = check_dev(x, tb, "x")) || (rc = check_dev(y, tb, "y")) ||
+        (rc = check_dev(mean, sb, "mean")) || (rc = check_dev(rstd, sb, "rstd")) ||
+        (rc = check_dev_opt(gamma, (size_t)C * 4, "gamma")) ||
+        (rc = check_dev_opt(beta, (size_t)C * 4, "beta")))
+        return rc;
+    const Tuning t = current_tuning();
+    Plan p;
+    if (!soar::gn::make_plan(N, C, HW, G, t, &p))
+        return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    p.vec4 = p.vec4 && aligned16(x) && aligned16(y);
+    if ((rc = check_ws(p, workspace, workspace_bytes))) return rc;
+    soar::gn::FwdArgs a{x, gamma, beta, y, mean, rstd, eps, flags, workspace};
+    hipError_t e = soar::gn::launch_forward(p, t, a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "GroupNorm forward launch");
+    return ok();
+}
+
+SOAR_API int soar_gn_silu_backward(const float* dy, const float* x, const float* gamma,
+                                   const float* beta, const float* mean, const float* rstd,
+                                   float* dx, float* dgamma, float* dbeta, int64_t N,
+                                   int64_t C, int64_t HW, int64_t G, unsigned flags,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+    int64_t elems = 0;
+    int rc = check_shape(N, C, HW, G, &elems);
+    if (rc) return rc;
+    if (flags & ~(SOAR_GN_SILU | SOAR_GN_RESIDUAL | SOAR_GN_ACCUMULATE_DX))
+        return fail(SOAR_EINVAL, "unsupported backward flags 0x%x", flags);
+    if ((dgamma == nullptr) != (dbeta == nullptr))
+        return fail(SOAR_EINVAL, "dgamma and dbeta must be both NULL or both set");
+    if (elems == 0 || (!dx && !dgamma)) return ok();
+    if ((rc = require_device())) return rc;
+    const size_t tb = (size_t)elems * sizeof(float);
+    const size_t sb = (size_t)(N * G) * sizeof(float);
+    const size_t cb = (size_t)C * sizeof(float);
+    if ((rc = check_dev(dy, tb, "dy")) || (rc = check_dev(x, tb, "x")) ||
+        (rc = check_dev(mean, sb, "mean")) || (rc = check_dev(rstd, sb, "rstd")) ||
+        (rc = check_dev_opt(dx, tb, "dx")) || (rc = check_dev_opt(gamma, cb, "gamma")) ||
+        (rc = check_dev_opt(beta, cb, "beta")) || (rc = check_dev_opt(dgamma, cb, "dgamma")) ||
+        (rc = check_dev_opt(dbeta, cb, "dbeta")))
+        return rc;
+    const Tuning t = current_tuning();
+    Plan p;
+    if (!soar::gn::make_plan(N, C, HW, G, t, &p))
+        return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    p.vec4 = p.vec4 && aligned16(x) && aligned16(dy) && aligned16(dx);
+    if ((rc = check_ws(p, workspace, workspace_bytes))) return rc;
+    soar::gn::BwdArgs a{dy, x, gamma, beta, mean, rstd, dx, dgamma, dbeta, flags, workspace};
+    hipError_t e = soar::gn::launch_backward(p, t, a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "GroupNorm backward launch");
+    return ok();
+}
+
+SOAR_API int soar_group_norm_forward(const float* in, const float* gamma, const float* beta,
+                                     float* out, float* saved_mean, float* saved_rstd,
+                                     size_t num_groups, size_t C, size_t HW, float eps,
+                                     void* stream) {
+    if (C == 0 || HW == 0) return ok();
+    if (num_groups == 0 || C % num_groups)
+        return fail(SOAR_EINVAL, "C=%zu is not divisible by num_groups=%zu", C, num_groups);
+    int rc = require_device();
+    if (rc) return rc;
+    size_t need = soar_gn_workspace_bytes(1, (int64_t)C, (int64_t)HW, (int64_t)num_groups);
+    if (need == 0) return fail(SOAR_EINVAL, "shape is too large");
+    void* ws = nullptr;
+    if ((rc = owned_workspace(need, &ws))) return rc;
+    return soar_gn_silu_forward(in, gamma, beta, out, saved_mean, saved_rstd, 1, (int64_t)C,
+                                (int64_t)HW, (int64_t)num_groups, eps, 0u, ws, need, stream);
+}
+
+SOAR_API int soar_group_norm_backward(const float* grad_out, const float* in,
+                                      const float* gamma, const float* saved_mean,
+                                      const float* saved_rstd, float* grad_in,
+                                      float* grad_gamma, float* grad_beta, size_t num_groups,
+                                      size_t C, size_t HW, void* stream) {
+    if (C == 0 || HW == 0) return ok();
+    if (num_groups == 0 || C % num_groups)
+        return fail(SOAR_EINVAL, "C=%zu is not divisible by num_groups=%zu", C, num_groups);
+    int rc = require_device();
+    if (rc) return rc;
+    size_t need = soar_gn_workspace_bytes(1, (int64_t)C, (int64_t)HW, (int64_t)num_groups);
+    if (need == 0) return fail(SOAR_EINVAL, "shape is too large");
+    void* ws = nullptr;
+    if ((rc = owned_workspace(need, &ws))) return rc;
+    return soar_gn_silu_backward(grad_out, in, gamma, nullptr, saved_mean, saved_rstd, grad_in,
+                                 grad_gamma, grad_beta, 1, (int64_t)C, (int64_t)HW,
+                                 (int64_t)num_groups, SOAR_GN_ACCUMULATE_DX, ws, need, stream);
+}
+
+#define SOAR_ELEMWISE_PRELUDE(n)                                   \
+    if ((n) == 0) return ok();                                     \
+    if ((size_t)(n) > (size_t)INT64_MAX / 4)                       \
+        return fail(SOAR_EINVAL, "element count %zu is too large", (size_t)(n)); \
+    {                                                              \
+        int rc0 = require_device();                                \
+        if (rc0) return rc0;                                       \
+    }
+
+SOAR_API int soar_silu_forward(const float* x, float* y, size_t n, void* stream) {
+    SOAR_ELEMWISE_PRELUDE(n);
+    int rc;
+    if ((rc = check_dev(x, n * 4, "x")) || (rc = check_dev(y, n * 4, "y"))) return rc;
+    hipError_t e = soar::gn::launch_silu_forward(x, y, (int64_t)n, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "silu_forward launch");
+}
+
+SOAR_API int soar_silu_backward(const float* grad_y, const float* x, float* grad_x, size_t n,
+                                void* stream) {
+    SOAR_ELEMWISE_PRELUDE(n);
+    int rc;
+    if ((rc = check_dev(grad_y, n * 4, "grad_y")) || (rc = check_dev(x, n * 4, "x")) ||
+        (rc = check_dev(grad_x, n * 4, "grad_x")))
+        return rc;
+    hipError_t e = soar::gn::launch_silu_backward(grad_y, x, grad_x, (int64_t)n,
+                                                  static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "silu_backward launch");
+}
+
+SOAR_API int soar_add_forward(const float* a, const float* b, float* y, size_t n, void* stream) {
+    SOAR_ELEMWISE_PRELUDE(n);
+    int rc;
+    if ((rc = check_dev(a, n * 4, "a")) || (rc = check_dev(b, n * 4, "b")) ||
+        (rc = check_dev(y, n * 4, "y")))
+        return rc;
+    hipError_t e = soar::gn::launch_add_forward(a, b, y, (int64_t)n, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "add_forward launch");
+}
+
+SOAR_API int soar_add_backward(const float* grad_y, float* grad_a, float* grad_b, size_t n,
+                               void* stream) {
+    if (!grad_a && !grad_b) return ok();
+    SOAR_ELEMWISE_PRELUDE(n);
+    int rc;
+    if ((rc = check_dev(grad_y, n * 4, "grad_y")) || (rc = check_dev_opt(grad_a, n * 4, "grad_a")) ||
+        (rc = check_dev_opt(grad_b, n * 4, "grad_b")))
+        return rc;
+    hipError_t e = soar::gn::launch_add_backward(grad_y, grad_a, grad_b, (int64_t)n,
+                                                 static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "add_backward launch");
+}
+
+SOAR_API int soar_fill(float* ptr, float value, size_t n, void* stream) {
+    SOAR_ELEMWISE_PRELUDE(n);
+    int rc;
+    if ((rc = check_dev(ptr, n * 4, "ptr"))) return rc;
+    hipError_t e = soar::gn::launch_fill(ptr, value, (int64_t)n, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "fill launch");
+}
+
+SOAR_API int soar_zero(float* ptr, size_t n, void* stream) { return soar_fill(ptr, 0.0f, n, stream); }
+
+// ---- arena -------------------------------------------------------------------
+
+struct soar_arena {
+    void* base = nullptr;
+    size_t capacity = 0;
+    size_t alignment = 256;
+    size_t offset = 0;
+    size_t static_boundary = 0;
+    size_t live = 0;  // allocations since the last reset (bookkeeping only)
+};
+
+SOAR_API int soar_arena_create(size_t capacity_bytes, size_t alignment, soar_arena** arena) {
+    if (!arena) return fail(SOAR_EINVAL, "arena out-pointer is NULL");
+    *arena = nullptr;
+    if (capacity_bytes == 0) return fail(SOAR_EINVAL, "arena capacity must be positive");
+    if (alignment == 0 || (alignment & (alignment - 1)))
+        return fail(SOAR_EINVAL, "alignment %zu is not a power of two", alignment);
+    int rc = require_device();
+    if (rc) return rc;
+    soar_arena* a = new (std::nothrow) soar_arena;
+    if (!a) return fail(SOAR_ENOMEM, "host allocation failed");
+    hipError_t e = hipMalloc(&a->base, capacity_bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        delete a;
+        return fail(SOAR_ENOMEM, "hipMalloc of %zu arena bytes failed", capacity_bytes);
+    }
+    a->capacity = capacity_bytes;
+    a->alignment = alignment;
+    *arena = a;
+    return ok();
+}
+
+SOAR_API int soar_arena_alloc(soar_arena* a, size_t bytes, void** dptr, size_t* offset) {
+    if (!a) return fail(SOAR_EINVAL, "arena is NULL");
+    if (bytes == 0) return fail(SOAR_EINVAL, "cannot allocate 0 bytes in the arena");
+    const size_t at = (a->offset + a->alignment - 1) & ~(a->alignment - 1);
+    if (at < a->offset || at > a->capacity || a->capacity - at < bytes)
+        return fail(SOAR_ENOMEM, "arena capacity exceeded (%zu + %zu > %zu)", at, bytes,
+                    a->capacity);
+    a->offset = at + bytes;
+    a->live += 1;
+    if (dptr) *dptr = static_cast<char*>(a->base) + at;
+    if (offset) *offset = at;
+    return ok();
+}
+
+SOAR_API int soar_arena_freeze_static(soar_arena* a) {
+    if (!a) return fail(SOAR_EINVAL, "arena is NULL");
+    const size_t b = (a->offset + a->alignment - 1) & ~(a->alignment - 1);
+    a->static_boundary = b < a->capacity ? b : a->capacity;
+    a->offset = a->static_boundary;
+    a->live = 0;
+    return ok();
+}
+
+SOAR_API int soar_arena_reset_dynamic(soar_arena* a) {
+    if (!a) return fail(SOAR_EINVAL, "arena is NULL");
+    a->offset = a->static_boundary;
+    a->live = 0;
+    return ok();
+}
+
+SOAR_API int soar_arena_info(const soar_arena* a, size_t* capacity, size_t* current_offset,
+                             size_t* static_boundary, void** base) {
+    if (!a) return fail(SOAR_EINVAL, "arena is NULL");
+    if (capacity) *capacity = a->capacity;
+    if (current_offset) *current_offset = a->offset;
+    if (static_boundary) *static_boundary = a->static_boundary;
+    if (base) *base = a->base;
+    return ok();
+}
+
+SOAR_API int soar_arena_destroy(soar_arena* a) {
+    if (!a) return ok();
+    hipError_t e = hipFree(a->base);
+    delete a;
+    if (e != hipSuccess) return hip_fail(e, "hipFree(arena)");
+    return ok();
+}
+
+SOAR_API int soar_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return ok();
+    if (!src) return fail(SOAR_EINVAL, "src is NULL");
+    int rc = require_device();
+    if (rc || (rc = check_dev(dst, bytes, "dst"))) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return e == hipSuccess ? ok() : hip_fail(e, "host-to-device copy");
+}
+
+SOAR_API int soar_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return ok();
+    if (!dst) return fail(SOAR_EINVAL, "dst is NULL");
+    int rc = require_device();
+    if (rc || (rc = check_dev(src, bytes, "src"))) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return e == hipSuccess ? ok() : hip_fail(e, "device-to-host copy");
+}
+
+// ---- timing ------------------------------------------------------------------
+
+SOAR_API int soar_prof_enable(int on) {
+    g_prof_on.store(on != 0);
+    return ok();
+}
+
+SOAR_API int soar_prof_summary(char* buf, size_t buflen) {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    struct Agg {
+        std::string name;
+        long launches;
+        double ms;
+    };
+    std::vector<Agg> agg;
+    hipError_t first_err = hipSuccess;
+    for (ProfRec& r : g_prof) {
+        float ms = 0.0f;
+        hipError_t e = hipEventSynchronize(r.stop);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.start, r.stop);
+        if (e != hipSuccess && first_err == hipSuccess) first_err = e;
+        auto it = std::find_if(agg.begin(), agg.end(),
+                               [&](const Agg& a) { return a.name == r.name; });
+        if (it == agg.end()) agg.push_back({r.name, 1, (double)ms});
+        else {
+            it->launches += 1;
+            it->ms += ms;
+        }
+        g_event_pool.push_back(r.start);
+        g_event_pool.push_back(r.stop);
+    }
+    g_prof.clear();
+    if (first_err != hipSuccess) {
+        (void)hipGetLastError();
+        return hip_fail(first_err, "reading kernel timing events");
+    }
+    std::string js = "[";
+    for (size_t i = 0; i < agg.size(); ++i) {
+        char item[256];
+        std::snprintf(item, sizeof item, "%s{\"kernel\":\"%s\",\"launches\":%ld,\"total_ms\":%.6f}",
+                      i ? "," : "", agg[i].name.c_str(), agg[i].launches, agg[i].ms);
+        js += item;
+    }
+    js += "]";
+    if (buf && buflen) {
+        std::strncpy(buf, js.c_str(), buflen - 1);
+        buf[buflen - 1] = '\0';
+    }
+    g_err.clear();
+    return (int)agg.size();
+}
+
+SOAR_API int soar_gn_tune(int key, int64_t value) {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    switch (key) {
+        case SOAR_TUNE_CHUNK:
+            if (value < 1024 || value % 1024 || value > (1 << 24))
+                return fail(SOAR_EINVAL, "chunk must be a multiple of 1024 in [1024, 2^24]");
+            g_tune.chunk = value;
+            return ok();
+        case SOAR_TUNE_REVERSE:
+            if (value != 0 && value != 1) return fail(SOAR_EINVAL, "reverse must be 0 or 1");
+            g_tune.reverse = (int)value;
+            return ok();
+        case SOAR_TUNE_NT_STORE:
+            if (value != 0 && value != 1) return fail(SOAR_EINVAL, "nt_store must be 0 or 1");
+            g_tune.nt_store = (int)value;
+            return ok();
+        default:
+            return fail(SOAR_EINVAL, "unknown tuning key %d", key);
+    }
+}
+
+SOAR_API int64_t soar_gn_tune_get(int key) {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    switch (key) {
+        case SOAR_TUNE_CHUNK: return g_tune.chunk;
+        case SOAR_TUNE_REVERSE: return g_tune.reverse;
+        case SOAR_TUNE_NT_STORE: return g_tune.nt_store;
+        default: return -1;
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,86 @@
+// gn_internal.hpp - launch plans and launchers shared by the HIP kernels
+// (gn_kernels.hip, elementwise.hip) and the C-ABI (capi.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace soar {
+namespace gn {
+
+// Launch geometry of the four streaming kernels.  Every (n, c) plane of HW
+// floats is cut into `cpp` chunks of `chunk` floats (the last one ragged);
+// one 256-thread block streams one chunk.  Blocks are numbered
+// plane * cpp + chunk_in_plane, so a unit (n, g) owns a contiguous range.
+struct Plan {
+    int64_t N = 0, C = 0, HW = 0, G = 0, cpg = 0;
+    int64_t planes = 0;  // N * C
+    int64_t chunk = 0;   // floats per block-chunk
+    int64_t cpp = 0;     // chunks per plane
+    int64_t blocks = 0;  // planes * cpp
+    bool vec4 = false;   // float4 path (HW % 4 == 0 and 16-byte pointers)
+};
+
+struct Tuning {
+    int64_t chunk = 32768;  // floats per block-chunk, multiple of 1024
+    int reverse = 0;        // second passes walk blocks in reverse order
+    int nt_store = 1;       // non-temporal stores of y / dx
+};
+
+constexpr int kThreads = 256;
+
+// Plan for a non-empty tensor.  Returns false if the grid would not fit.
+bool make_plan(int64_t N, int64_t C, int64_t HW, int64_t G,
+               const Tuning& t, Plan* p);
+size_t workspace_bytes(const Plan& p);
+
+struct FwdArgs {
+    const float* x;
+    const float* gamma;  // nullable
+    const float* beta;   // nullable
+    float* y;
+    float* mean;
+    float* rstd;
+    float eps;
+    unsigned flags;
+    void* ws;
+};
+
+struct BwdArgs {
+    const float* dy;
+    const float* x;
+    const float* gamma;  // nullable
+    const float* beta;   // nullable
+    const float* mean;
+    const float* rstd;
+    float* dx;      // nullable
+    float* dgamma;  // nullable (with dbeta)
+    float* dbeta;
+    unsigned flags;
+    void* ws;
+};
+
+hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a,
+                          hipStream_t s);
+hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a,
+                           hipStream_t s);
+
+// Elementwise kernels (elementwise.hip).
+hipError_t launch_silu_forward(const float* x, float* y, int64_t n,
+                               hipStream_t s);
+hipError_t launch_silu_backward(const float* gy, const float* x, float* gx,
+                                int64_t n, hipStream_t s);
+hipError_t launch_add_forward(const float* a, const float* b, float* y,
+                              int64_t n, hipStream_t s);
+hipError_t launch_add_backward(const float* gy, float* ga, float* gb,
+                               int64_t n, hipStream_t s);
+hipError_t launch_fill(float* p, float v, int64_t n, hipStream_t s);
+
+// Kernel timing hooks (capi.cpp).  prof_begin returns a token passed to
+// prof_end; both are no-ops while timing is off.
+int prof_begin(hipStream_t s, const char* kernel);
+void prof_end(hipStream_t s, int token);
+
+}  // namespace gn
+}  // namespace soar

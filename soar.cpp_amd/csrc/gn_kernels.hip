@@ -1,0 +1,661 @@
+// gn_kernels.hip - fused GroupNorm(+SiLU) forward and backward for gfx950.
+//
+// The path is HBM-bound (about 1 flop per byte, no contraction), so every
+// kernel is a streaming pass built for CDNA4's memory system:
+//   * one 256-thread block (four wave64s) streams one contiguous chunk of
+//     one (n, c) plane with 128-bit loads, four in flight per thread;
+//   * per-block partial results go to a small workspace and a tiny finish
+//     kernel combines them in float64 in a fixed order, so results are
+//     bitwise reproducible and no float atomics are used;
+//   * per-block coefficients (mean, rstd, gamma, beta, S1, S2) are uniform
+//     across the block and live in scalar registers;
+//   * SiLU is recomputed in the backward from x and the saved statistics
+//     instead of storing the pre-activation.
+//
+// Forward  (3 tensor passes):  k_stats_partial -> k_stats_finish -> k_apply
+// Backward (5 tensor passes):  k_bwd_reduce -> k_bwd_finish -> k_bwd_dx
+//
+// Reference algorithms (pomagrenate/soar.cpp):
+//   statistics  shaders/group_norm_stats.comp:25-73 (sum/sumsq, one
+//               workgroup per group), src/cuda/ops/normalization_kernels.cu
+//               :12-64 (Welford + Chan, one block per group),
+//               src/nn/layers.cpp:690-710 (double sums).  Here: per-thread
+//               shifted sums, Chan combine in float64 across threads, blocks
+//               and chunks; rstd = 1/sqrt(max(var,0)+eps), biased variance.
+//   apply       shaders/group_norm_affine_silu.comp:33-65,
+//               normalization_kernels.cu:70-91 + activation_kernels.cu:11-49,
+//               layers.cpp:712-721,789-795.  Here (x-mean)*(gamma*rstd)+beta
+//               (not the alpha*x+delta form, which loses digits when |mean|
+//               is large), then z/(1+exp(-z)).
+//   backward    layers.cpp:545-617 (GN) and :760-769 (SiLU),
+//               normalization_kernels.cu:116-249.  Here one reduction pass
+//               gives per-plane sum(dz) and sum(dz*xhat); dgamma/dbeta and
+//               the per-group S1/S2 both derive from them.
+#include "gn_internal.hpp"
+
+#include "soar_gn.h"
+
+namespace soar {
+namespace gn {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWaves = kThreads / 64;
+
+// sigmoid(z) = 1/(1+exp(-z)) with the hardware 2^x (v_exp_f32) and
+// reciprocal (v_rcp_f32).  exp overflow to +inf gives 0, underflow gives 1.
+__device__ __forceinline__ float sigmoid_fast(float z) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * kLog2e));
+}
+
+__device__ __forceinline__ float silu_fast(float z) { return z * sigmoid_fast(z); }
+
+// Gradient at the SiLU input: g * s * (1 + z*(1-s)), s = sigmoid(z).
+__device__ __forceinline__ float dsilu_fast(float g, float z) {
+    float s = sigmoid_fast(z);
+    return g * s * fmaf(z, 1.0f - s, 1.0f);
+}
+
+// ---- float64 moment triples (count, mean, M2) and Chan's combine ------
+
+struct Moments {
+    double n, mean, m2;
+};
+
+__device__ __forceinline__ Moments chan(const Moments& a, const Moments& b) {
+    if (b.n == 0.0) return a;
+    if (a.n == 0.0) return b;
+    Moments r;
+    r.n = a.n + b.n;
+    double f = b.n / r.n;
+    double d = b.mean - a.mean;
+    r.mean = a.mean + d * f;
+    r.m2 = a.m2 + b.m2 + d * d * a.n * f;
+    return r;
+}
+
+// Tree to lane 0 of the wave.  Lanes whose partner is past lane 63 read
+// their own value, but those lanes never feed lane 0.
+__device__ __forceinline__ Moments wave_reduce(Moments m) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        Moments o;
+        o.n = __shfl_down(m.n, off);
+        o.mean = __shfl_down(m.mean, off);
+        o.m2 = __shfl_down(m.m2, off);
+        m = chan(m, o);
+    }
+    return m;
+}
+
+// Result valid in thread 0.  Ends with the block synchronised.
+__device__ __forceinline__ Moments block_reduce(Moments m, Moments* lds) {
+    m = wave_reduce(m);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) lds[w] = m;
+    __syncthreads();
+    Moments r = lds[0];
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int i = 1; i < kWaves; ++i) r = chan(r, lds[i]);
+    }
+    __syncthreads();
+    return r;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off);
+    return v;
+}
+
+// Sum of (a, b) over the block in a fixed order; valid in thread 0.
+template <typename T>
+__device__ __forceinline__ void block_sum2(T& a, T& b, T* lds /*[2*kWaves]*/) {
+    a = wave_sum(a);
+    b = wave_sum(b);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) {
+        lds[w] = a;
+        lds[kWaves + w] = b;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        a = lds[0];
+        b = lds[kWaves];
+#pragma unroll
+        for (int i = 1; i < kWaves; ++i) {
+            a += lds[i];
+            b += lds[kWaves + i];
+        }
+    }
+    __syncthreads();
+}
+
+// Chunk geometry of block `b`: plane index, element offset in the plane
+// and length.
+struct Chunk {
+    int64_t plane, off, len;
+};
+
+__device__ __forceinline__ Chunk chunk_of(int64_t b, int64_t HW, int64_t chunk,
+                                          int64_t cpp) {
+    Chunk k;
+    k.plane = b / cpp;
+    k.off = (b - k.plane * cpp) * chunk;
+    k.len = min(chunk, HW - k.off);
+    return k;
+}
+
+template <bool NT>
+__device__ __forceinline__ void store4(f4* p, f4 v) {
+    if (NT)
+        __builtin_nontemporal_store(v, p);
+    else
+        *p = v;
+}
+
+template <bool NT>
+__device__ __forceinline__ void store1(float* p, float v) {
+    if (NT)
+        __builtin_nontemporal_store(v, p);
+    else
+        *p = v;
+}
+
+// ======================================================================
+// Forward pass 1: per-chunk moments.
+// Each thread shifts its elements by its own first element K (so sums of
+// d = x - K stay near the data's spread even when |mean| >> std), keeps
+// fp32 sums of d and d*d in four independent lanes of accumulation, then
+// converts to a float64 (n, mean, M2) triple that is Chan-combined over
+// the block.  part[b] = (mean, M2) of chunk b; its count is implied by the
+// chunk geometry.
+// ======================================================================
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void k_stats_partial(
+    const float* __restrict__ x, double2* __restrict__ part, int64_t HW,
+    int64_t chunk, int64_t cpp) {
+    __shared__ Moments lds[kWaves];
+    const Chunk ck = chunk_of(blockIdx.x, HW, chunk, cpp);
+    const float* p = x + ck.plane * HW + ck.off;
+    const int t = threadIdx.x;
+
+    float K = 0.0f;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f;
+    int64_t cnt = 0;
+    if (VEC) {
+        const f4* p4 = reinterpret_cast<const f4*>(p);
+        const int64_t n4 = ck.len >> 2;
+        int64_t i = t;
+        if (i < n4) {
+            cnt = 4 * ((n4 - 1 - i) / kThreads + 1);
+            f4 v = p4[i];
+            K = v.x;
+            float d1 = v.y - K, d2 = v.z - K, d3 = v.w - K;
+            s1 = d1; s2 = d2; s3 = d3;
+            q1 = d1 * d1; q2 = d2 * d2; q3 = d3 * d3;
+            i += kThreads;
+        }
+#define SOAR_ACC4(v)                                                     \
+    {                                                                    \
+        float d0 = (v).x - K, d1 = (v).y - K, d2 = (v).z - K,            \
+              d3 = (v).w - K;                                            \
+        s0 += d0; s1 += d1; s2 += d2; s3 += d3;                          \
+        q0 = fmaf(d0, d0, q0); q1 = fmaf(d1, d1, q1);                    \
+        q2 = fmaf(d2, d2, q2); q3 = fmaf(d3, d3, q3);                    \
+    }
+        for (; i + 3 * kThreads < n4; i += 4 * kThreads) {
+            f4 a = p4[i], b = p4[i + kThreads], c = p4[i + 2 * kThreads],
+               d = p4[i + 3 * kThreads];
+            SOAR_ACC4(a);
+            SOAR_ACC4(b);
+            SOAR_ACC4(c);
+            SOAR_ACC4(d);
+        }
+        for (; i < n4; i += kThreads) {
+            f4 a = p4[i];
+            SOAR_ACC4(a);
+        }
+#undef SOAR_ACC4
+    } else {
+        int64_t i = t;
+        if (i < ck.len) {
+            cnt = (ck.len - 1 - i) / kThreads + 1;
+            K = p[i];
+            i += kThreads;
+        }
+        for (; i + 3 * kThreads < ck.len; i += 4 * kThreads) {
+            float d0 = p[i] - K, d1 = p[i + kThreads] - K,
+                  d2 = p[i + 2 * kThreads] - K, d3 = p[i + 3 * kThreads] - K;
+            s0 += d0; s1 += d1; s2 += d2; s3 += d3;
+            q0 = fmaf(d0, d0, q0); q1 = fmaf(d1, d1, q1);
+            q2 = fmaf(d2, d2, q2); q3 = fmaf(d3, d3, q3);
+        }
+        for (; i < ck.len; i += kThreads) {
+            float d0 = p[i] - K;
+            s0 += d0;
+            q0 = fmaf(d0, d0, q0);
+        }
+    }
+    Moments m{0.0, 0.0, 0.0};
+    if (cnt > 0) {
+        const double s = (double)((s0 + s1) + (s2 + s3));
+        const double q = (double)((q0 + q1) + (q2 + q3));
+        m.n = (double)cnt;
+        m.mean = (double)K + s / m.n;
+        m.m2 = fmax(q - s * s / m.n, 0.0);
+    }
+    Moments r = block_reduce(m, lds);
+    if (t == 0) part[blockIdx.x] = make_double2(r.mean, r.m2);
+}
+
+// Forward finish: one block per unit (n, g) combines its cpg*cpp chunk
+// partials in a fixed order and writes mean and rstd.
+__global__ __launch_bounds__(kThreads) void k_stats_finish(
+    const double2* __restrict__ part, float* __restrict__ mean,
+    float* __restrict__ rstd, int64_t C, int64_t G, int64_t cpg, int64_t HW,
+    int64_t chunk, int64_t cpp, float eps) {
+    __shared__ Moments lds[kWaves];
+    const int64_t u = blockIdx.x;
+    const int64_t n = u / G, g = u - n * G;
+    const int64_t first = (n * C + g * cpg) * cpp;
+    const int64_t P = cpg * cpp;
+    Moments m{0.0, 0.0, 0.0};
+    for (int64_t j = threadIdx.x; j < P; j += kThreads) {
+        const int64_t k = j % cpp;
+        const double2 v = part[first + j];
+        Moments o{(double)min(chunk, HW - k * chunk), v.x, v.y};
+        m = chan(m, o);
+    }
+    Moments r = block_reduce(m, lds);
+    if (threadIdx.x == 0) {
+        const double var = r.n > 0.0 ? fmax(r.m2 / r.n, 0.0) : 0.0;
+        mean[u] = (float)r.mean;
+        rstd[u] = (float)(1.0 / sqrt(var + (double)eps));
+    }
+}
+
+// Per-block coefficients of plane `plane`.
+struct PlaneCoef {
+    int64_t c, n, u;
+    float mu, r, gm, bt;
+};
+
+__device__ __forceinline__ PlaneCoef plane_coef(
+    int64_t plane, int64_t C, int64_t G, int64_t cpg,
+    const float* __restrict__ gamma, const float* __restrict__ beta,
+    const float* __restrict__ mean, const float* __restrict__ rstd) {
+    PlaneCoef k;
+    k.n = plane / C;
+    k.c = plane - k.n * C;
+    k.u = k.n * G + k.c / cpg;
+    k.mu = mean[k.u];
+    k.r = rstd[k.u];
+    k.gm = gamma ? gamma[k.c] : 1.0f;
+    k.bt = beta ? beta[k.c] : 0.0f;
+    return k;
+}
+
+// ======================================================================
+// Forward pass 2: y = f((x - mean) * (gamma*rstd) + beta) [+ x].
+// ======================================================================
+template <bool VEC, bool SILU, bool RES, bool NT>
+__global__ __launch_bounds__(kThreads) void k_apply(
+    const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ beta, const float* __restrict__ mean,
+    const float* __restrict__ rstd, float* __restrict__ y, int64_t C,
+    int64_t G, int64_t cpg, int64_t HW, int64_t chunk, int64_t cpp,
+    int64_t nblocks, int reverse) {
+    const int64_t b = reverse ? nblocks - 1 - (int64_t)blockIdx.x : (int64_t)blockIdx.x;
+    const Chunk ck = chunk_of(b, HW, chunk, cpp);
+    const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd);
+    const float a = k.gm * k.r, mu = k.mu, bt = k.bt;
+    const int64_t base = ck.plane * HW + ck.off;
+    const int t = threadIdx.x;
+    auto f = [&](float v) {
+        float z = fmaf(v - mu, a, bt);
+        float o = SILU ? silu_fast(z) : z;
+        return RES ? o + v : o;
+    };
+    if (VEC) {
+        const f4* x4 = reinterpret_cast<const f4*>(x + base);
+        f4* y4 = reinterpret_cast<f4*>(y + base);
+        const int64_t n4 = ck.len >> 2;
+        int64_t i = t;
+        for (; i + 3 * kThreads < n4; i += 4 * kThreads) {
+            f4 v0 = x4[i], v1 = x4[i + kThreads], v2 = x4[i + 2 * kThreads],
+               v3 = x4[i + 3 * kThreads];
+            f4 o0 = {f(v0.x), f(v0.y), f(v0.z), f(v0.w)};
+            f4 o1 = {f(v1.x), f(v1.y), f(v1.z), f(v1.w)};
+            f4 o2 = {f(v2.x), f(v2.y), f(v2.z), f(v2.w)};
+            f4 o3 = {f(v3.x), f(v3.y), f(v3.z), f(v3.w)};
+            store4<NT>(&y4[i], o0);
+            store4<NT>(&y4[i + kThreads], o1);
+            store4<NT>(&y4[i + 2 * kThreads], o2);
+            store4<NT>(&y4[i + 3 * kThreads], o3);
+        }
+        for (; i < n4; i += kThreads) {
+            f4 v = x4[i];
+            f4 o = {f(v.x), f(v.y), f(v.z), f(v.w)};
+            store4<NT>(&y4[i], o);
+        }
+    } else {
+        const float* xp = x + base;
+        float* yp = y + base;
+        for (int64_t i = t; i < ck.len; i += kThreads) store1<NT>(&yp[i], f(xp[i]));
+    }
+}
+
+// ======================================================================
+// Backward pass 1: per-chunk sum(dz) and sum(dz * xhat), dz the gradient
+// at the GroupNorm output (SiLU derivative recomputed from x).
+// ======================================================================
+template <bool VEC, bool SILU>
+__global__ __launch_bounds__(kThreads) void k_bwd_reduce(
+    const float* __restrict__ dy, const float* __restrict__ x,
+    const float* __restrict__ gamma, const float* __restrict__ beta,
+    const float* __restrict__ mean, const float* __restrict__ rstd,
+    double2* __restrict__ part, int64_t C, int64_t G, int64_t cpg, int64_t HW,
+    int64_t chunk, int64_t cpp) {
+    __shared__ float lds[2 * kWaves];
+    const Chunk ck = chunk_of(blockIdx.x, HW, chunk, cpp);
+    const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd);
+    const float mu = k.mu, r = k.r, gm = k.gm, bt = k.bt;
+    const int64_t base = ck.plane * HW + ck.off;
+    const int t = threadIdx.x;
+    float sa0 = 0.f, sa1 = 0.f, sb0 = 0.f, sb1 = 0.f;
+    auto acc = [&](float g, float v, float& sa, float& sb) {
+        float xh = (v - mu) * r;
+        float dz = SILU ? dsilu_fast(g, fmaf(gm, xh, bt)) : g;
+        sa += dz;
+        sb = fmaf(dz, xh, sb);
+    };
+    if (VEC) {
+        const f4* x4 = reinterpret_cast<const f4*>(x + base);
+        const f4* g4 = reinterpret_cast<const f4*>(dy + base);
+        const int64_t n4 = ck.len >> 2;
+        int64_t i = t;
+        for (; i + kThreads < n4; i += 2 * kThreads) {
+            f4 v0 = x4[i], v1 = x4[i + kThreads];
+            f4 g0 = g4[i], g1 = g4[i + kThreads];
+            acc(g0.x, v0.x, sa0, sb0); acc(g0.y, v0.y, sa1, sb1);
+            acc(g0.z, v0.z, sa0, sb0); acc(g0.w, v0.w, sa1, sb1);
+            acc(g1.x, v1.x, sa0, sb0); acc(g1.y, v1.y, sa1, sb1);
+            acc(g1.z, v1.z, sa0, sb0); acc(g1.w, v1.w, sa1, sb1);
+        }
+        for (; i < n4; i += kThreads) {
+            f4 v0 = x4[i], g0 = g4[i];
+            acc(g0.x, v0.x, sa0, sb0); acc(g0.y, v0.y, sa1, sb1);
+            acc(g0.z, v0.z, sa0, sb0); acc(g0.w, v0.w, sa1, sb1);
+        }
+    } else {
+        const float* xp = x + base;
+        const float* gp = dy + base;
+        for (int64_t i = t; i < ck.len; i += kThreads) acc(gp[i], xp[i], sa0, sb0);
+    }
+    float sa = sa0 + sa1, sb = sb0 + sb1;
+    block_sum2(sa, sb, lds);
+    if (t == 0) part[blockIdx.x] = make_double2((double)sa, (double)sb);
+}
+
+// Backward finish: one block per channel c sums the chunk partials of every
+// plane (n, c) in float64, stores the per-plane sums for the dx pass and
+// accumulates dbeta[c] += sum_n A, dgamma[c] += sum_n B.
+__global__ __launch_bounds__(kThreads) void k_bwd_finish(
+    const double2* __restrict__ part, double2* __restrict__ plane_sums,
+    float* __restrict__ dgamma, float* __restrict__ dbeta, int64_t N,
+    int64_t C, int64_t cpp) {
+    __shared__ double lds[2 * kWaves];
+    const int64_t c = blockIdx.x;
+    double tot_a = 0.0, tot_b = 0.0;
+    for (int64_t n = 0; n < N; ++n) {
+        const int64_t plane = n * C + c;
+        const double2* pp = part + plane * cpp;
+        double a = 0.0, b = 0.0;
+        for (int64_t j = threadIdx.x; j < cpp; j += kThreads) {
+            a += pp[j].x;
+            b += pp[j].y;
+        }
+        block_sum2(a, b, lds);
+        if (threadIdx.x == 0) {
+            plane_sums[plane] = make_double2(a, b);
+            tot_a += a;
+            tot_b += b;
+        }
+    }
+    if (threadIdx.x == 0 && dbeta) {
+        dbeta[c] = (float)((double)dbeta[c] + tot_a);
+        dgamma[c] = (float)((double)dgamma[c] + tot_b);
+    }
+}
+
+// ======================================================================
+// Backward pass 2: dx = A*dz + D*xhat + B [+ dy] [+ dx_old] with
+// A = gamma_c*rstd, B = -rstd*S1/M, D = -rstd*S2/M.
+// ======================================================================
+template <bool VEC, bool SILU, bool RES, bool ACC, bool NT>
+__global__ __launch_bounds__(kThreads) void k_bwd_dx(
+    const float* __restrict__ dy, const float* __restrict__ x,
+    const float* __restrict__ gamma, const float* __restrict__ beta,
+    const float* __restrict__ mean, const float* __restrict__ rstd,
+    const double2* __restrict__ plane_sums, float* __restrict__ dx, int64_t C,
+    int64_t G, int64_t cpg, int64_t HW, int64_t chunk, int64_t cpp,
+    int64_t nblocks, int reverse) {
+    const int64_t b = reverse ? nblocks - 1 - (int64_t)blockIdx.x : (int64_t)blockIdx.x;
+    const Chunk ck = chunk_of(b, HW, chunk, cpp);
+    const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd);
+    double S1 = 0.0, S2 = 0.0;
+    const int64_t c0 = (k.c / cpg) * cpg;
+    for (int64_t j = 0; j < cpg; ++j) {
+        const double gj = gamma ? (double)gamma[c0 + j] : 1.0;
+        const double2 ps = plane_sums[k.n * C + c0 + j];
+        S1 += gj * ps.x;
+        S2 += gj * ps.y;
+    }
+    const double Md = (double)(cpg * HW);
+    const float mu = k.mu, r = k.r, gm = k.gm, bt = k.bt;
+    const float A = gm * r;
+    const float B = (float)(-(double)r * S1 / Md);
+    const float D = (float)(-(double)r * S2 / Md);
+    const int64_t base = ck.plane * HW + ck.off;
+    const int t = threadIdx.x;
+    auto f = [&](float g, float v, float old) {
+        float xh = (v - mu) * r;
+        float dz = SILU ? dsilu_fast(g, fmaf(gm, xh, bt)) : g;
+        float o = fmaf(A, dz, fmaf(D, xh, B));
+        if (RES) o += g;
+        if (ACC) o += old;
+        return o;
+    };
+    if (VEC) {
+        const f4* x4 = reinterpret_cast<const f4*>(x + base);
+        const f4* g4 = reinterpret_cast<const f4*>(dy + base);
+        f4* o4 = reinterpret_cast<f4*>(dx + base);
+        const int64_t n4 = ck.len >> 2;
+        int64_t i = t;
+        for (; i + kThreads < n4; i += 2 * kThreads) {
+            f4 v0 = x4[i], v1 = x4[i + kThreads];
+            f4 g0 = g4[i], g1 = g4[i + kThreads];
+            f4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0;
+            if (ACC) {
+                p0 = o4[i];
+                p1 = o4[i + kThreads];
+            }
+            f4 r0 = {f(g0.x, v0.x, p0.x), f(g0.y, v0.y, p0.y),
+                     f(g0.z, v0.z, p0.z), f(g0.w, v0.w, p0.w)};
+            f4 r1 = {f(g1.x, v1.x, p1.x), f(g1.y, v1.y, p1.y),
+                     f(g1.z, v1.z, p1.z), f(g1.w, v1.w, p1.w)};
+            store4<NT>(&o4[i], r0);
+            store4<NT>(&o4[i + kThreads], r1);
+        }
+        for (; i < n4; i += kThreads) {
+            f4 v0 = x4[i], g0 = g4[i];
+            f4 p0 = {0.f, 0.f, 0.f, 0.f};
+            if (ACC) p0 = o4[i];
+            f4 r0 = {f(g0.x, v0.x, p0.x), f(g0.y, v0.y, p0.y),
+                     f(g0.z, v0.z, p0.z), f(g0.w, v0.w, p0.w)};
+            store4<NT>(&o4[i], r0);
+        }
+    } else {
+        const float* xp = x + base;
+        const float* gp = dy + base;
+        float* op = dx + base;
+        for (int64_t i = t; i < ck.len; i += kThreads)
+            store1<NT>(&op[i], f(gp[i], xp[i], ACC ? op[i] : 0.0f));
+    }
+}
+
+// ---- host-side dispatch over the template flags -------------------------
+
+template <bool VEC>
+void apply_dispatch(bool silu, bool res, bool nt, dim3 grid, hipStream_t s,
+                    const Plan& p, const FwdArgs& a, int reverse) {
+#define SOAR_APPLY(S, R, N)                                                  \
+    k_apply<VEC, S, R, N><<<grid, kThreads, 0, s>>>(                         \
+        a.x, a.gamma, a.beta, a.mean, a.rstd, a.y, p.C, p.G, p.cpg, p.HW,    \
+        p.chunk, p.cpp, p.blocks, reverse)
+    const int sel = (silu ? 4 : 0) | (res ? 2 : 0) | (nt ? 1 : 0);
+    switch (sel) {
+        case 0: SOAR_APPLY(false, false, false); break;
+        case 1: SOAR_APPLY(false, false, true); break;
+        case 2: SOAR_APPLY(false, true, false); break;
+        case 3: SOAR_APPLY(false, true, true); break;
+        case 4: SOAR_APPLY(true, false, false); break;
+        case 5: SOAR_APPLY(true, false, true); break;
+        case 6: SOAR_APPLY(true, true, false); break;
+        default: SOAR_APPLY(true, true, true); break;
+    }
+#undef SOAR_APPLY
+}
+
+template <bool VEC, bool SILU>
+void dx_dispatch(bool res, bool accum, bool nt, dim3 grid, hipStream_t s,
+                 const Plan& p, const BwdArgs& a, const double2* plane_sums,
+                 int reverse) {
+#define SOAR_DX(R, A, N)                                                     \
+    k_bwd_dx<VEC, SILU, R, A, N><<<grid, kThreads, 0, s>>>(                  \
+        a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, plane_sums, a.dx, p.C,   \
+        p.G, p.cpg, p.HW, p.chunk, p.cpp, p.blocks, reverse)
+    const int sel = (res ? 4 : 0) | (accum ? 2 : 0) | (nt ? 1 : 0);
+    switch (sel) {
+        case 0: SOAR_DX(false, false, false); break;
+        case 1: SOAR_DX(false, false, true); break;
+        case 2: SOAR_DX(false, true, false); break;
+        case 3: SOAR_DX(false, true, true); break;
+        case 4: SOAR_DX(true, false, false); break;
+        case 5: SOAR_DX(true, false, true); break;
+        case 6: SOAR_DX(true, true, false); break;
+        default: SOAR_DX(true, true, true); break;
+    }
+#undef SOAR_DX
+}
+
+inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+}  // namespace
+
+bool make_plan(int64_t N, int64_t C, int64_t HW, int64_t G, const Tuning& t,
+               Plan* p) {
+    p->N = N;
+    p->C = C;
+    p->HW = HW;
+    p->G = G;
+    p->cpg = C / G;
+    p->planes = N * C;
+    // A chunk never exceeds the plane: small planes get one block each.
+    const int64_t hw_up = (HW + 1023) / 1024 * 1024;
+    p->chunk = t.chunk < hw_up ? t.chunk : hw_up;
+    p->cpp = (HW + p->chunk - 1) / p->chunk;
+    if (p->planes > (int64_t)0x7fffffff / p->cpp) return false;
+    p->blocks = p->planes * p->cpp;
+    if (p->blocks > 0x7fffffff || N * G > 0x7fffffff || C > 0x7fffffff) return false;
+    p->vec4 = (HW % 4) == 0;
+    return true;
+}
+
+size_t workspace_bytes(const Plan& p) {
+    return align256(sizeof(double2) * (size_t)p.blocks) +
+           align256(sizeof(double2) * (size_t)p.planes);
+}
+
+hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a,
+                          hipStream_t s) {
+    double2* part = static_cast<double2*>(a.ws);
+    const bool vec = p.vec4;
+    const bool silu = (a.flags & SOAR_GN_SILU) != 0;
+    const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
+    const dim3 grid((unsigned)p.blocks);
+
+    int tok = prof_begin(s, "gn_stats_partial");
+    if (vec)
+        k_stats_partial<true><<<grid, kThreads, 0, s>>>(a.x, part, p.HW, p.chunk, p.cpp);
+    else
+        k_stats_partial<false><<<grid, kThreads, 0, s>>>(a.x, part, p.HW, p.chunk, p.cpp);
+    prof_end(s, tok);
+
+    tok = prof_begin(s, "gn_stats_finish");
+    k_stats_finish<<<dim3((unsigned)(p.N * p.G)), kThreads, 0, s>>>(
+        part, a.mean, a.rstd, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, a.eps);
+    prof_end(s, tok);
+
+    tok = prof_begin(s, silu ? "gn_silu_apply" : "gn_apply");
+    if (vec)
+        apply_dispatch<true>(silu, res, t.nt_store != 0, grid, s, p, a, t.reverse);
+    else
+        apply_dispatch<false>(silu, res, t.nt_store != 0, grid, s, p, a, t.reverse);
+    prof_end(s, tok);
+    return hipGetLastError();
+}
+
+hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a,
+                           hipStream_t s) {
+    double2* part = static_cast<double2*>(a.ws);
+    double2* plane_sums = reinterpret_cast<double2*>(
+        static_cast<char*>(a.ws) + align256(sizeof(double2) * (size_t)p.blocks));
+    const bool vec = p.vec4;
+    const bool silu = (a.flags & SOAR_GN_SILU) != 0;
+    const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
+    const bool accum = (a.flags & SOAR_GN_ACCUMULATE_DX) != 0;
+    const dim3 grid((unsigned)p.blocks);
+
+    int tok = prof_begin(s, silu ? "gn_silu_bwd_reduce" : "gn_bwd_reduce");
+#define SOAR_RED(V, S)                                                        \
+    k_bwd_reduce<V, S><<<grid, kThreads, 0, s>>>(a.dy, a.x, a.gamma, a.beta,  \
+                                                 a.mean, a.rstd, part, p.C,  \
+                                                 p.G, p.cpg, p.HW, p.chunk,  \
+                                                 p.cpp)
+    if (vec) {
+        if (silu) SOAR_RED(true, true); else SOAR_RED(true, false);
+    } else {
+        if (silu) SOAR_RED(false, true); else SOAR_RED(false, false);
+    }
+#undef SOAR_RED
+    prof_end(s, tok);
+
+    tok = prof_begin(s, "gn_bwd_finish");
+    k_bwd_finish<<<dim3((unsigned)p.C), kThreads, 0, s>>>(part, plane_sums, a.dgamma,
+                                                          a.dbeta, p.N, p.C, p.cpp);
+    prof_end(s, tok);
+
+    if (a.dx) {
+        tok = prof_begin(s, silu ? "gn_silu_bwd_dx" : "gn_bwd_dx");
+        const bool nt = t.nt_store != 0 && !accum;
+        if (vec) {
+            if (silu) dx_dispatch<true, true>(res, accum, nt, grid, s, p, a, plane_sums, t.reverse);
+            else dx_dispatch<true, false>(res, accum, nt, grid, s, p, a, plane_sums, t.reverse);
+        } else {
+            if (silu) dx_dispatch<false, true>(res, accum, nt, grid, s, p, a, plane_sums, t.reverse);
+            else dx_dispatch<false, false>(res, accum, nt, grid, s, p, a, plane_sums, t.reverse);
+        }
+        prof_end(s, tok);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace gn
+}  // namespace soar

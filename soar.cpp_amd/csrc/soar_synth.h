@@ -1,0 +1,35 @@
+/*
+ * soar_synth.h - seeded synthetic inputs on the device, for tests and the
+ * benchmark (no counterpart in the reference, which draws its test inputs
+ * from std::random_device).  Same generator as the CPU oracle: splitmix64
+ * counter stream per (seed, tensor id), 53-bit uniforms, Box-Muller in
+ * float64, rounded to fp32.  Tensor ids: x=1 gamma=2 beta=3 dy=4
+ * outlier_mask=5 outlier_val=6.  Built into libsoar_synth.so, separate from
+ * the product library.
+ */
+#ifndef SOAR_SYNTH_H
+#define SOAR_SYNTH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int soar_synth_normal(float* out, int64_t n, uint64_t seed, uint32_t stream_id,
+                      double mean, double std_dev, void* stream);
+int soar_synth_uniform(float* out, int64_t n, uint64_t seed, uint32_t stream_id,
+                       double lo, double hi, void* stream);
+int soar_synth_stress(float* out, int64_t n, uint64_t seed, double center,
+                      double std_dev, double p, double out_mean, double out_std,
+                      void* stream);
+/* Plain 128-bit copy dst[i] = src[i] (n a multiple of 4, 16-byte aligned):
+ * the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE. */
+int soar_synth_copy(const float* src, float* dst, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,125 @@
+// synth.hip - device-side seeded input generator and a plain copy kernel
+// (see soar_synth.h).  Mirrors orc_fill_* of the CPU oracle element for
+// element: value i of a stream depends only on (seed, stream id, i).
+#include <hip/hip_runtime.h>
+
+#include "soar_synth.h"
+
+namespace {
+
+
+__host__ __device__ inline uint64_t splitmix_at(uint64_t key, uint64_t ctr) {
+    uint64_t z = key + (ctr + 1ULL) * 0x9E3779B97F4A7C15ULL;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ double uniform53(uint64_t bits) {
+    return (double)(bits >> 11) * (1.0 / 9007199254740992.0);
+}
+
+__device__ __forceinline__ void box_muller(uint64_t key, int64_t p, double* z0, double* z1) {
+    double u1 = 1.0 - uniform53(splitmix_at(key, 2ULL * (uint64_t)p));
+    double u2 = uniform53(splitmix_at(key, 2ULL * (uint64_t)p + 1ULL));
+    double r = sqrt(-2.0 * log(u1));
+    double t = 6.283185307179586 * u2;
+    *z0 = r * cos(t);
+    *z1 = r * sin(t);
+}
+
+__global__ void k_normal(float* out, int64_t n, uint64_t key, double mean, double sd) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; 2 * p < n; p += stride) {
+        double z0, z1;
+        box_muller(key, p, &z0, &z1);
+        out[2 * p] = (float)(mean + sd * z0);
+        if (2 * p + 1 < n) out[2 * p + 1] = (float)(mean + sd * z1);
+    }
+}
+
+__global__ void k_uniform(float* out, int64_t n, uint64_t key, double lo, double hi) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = (float)(lo + (hi - lo) * uniform53(splitmix_at(key, (uint64_t)i)));
+}
+
+__global__ void k_stress(float* out, int64_t n, uint64_t kx, uint64_t km, uint64_t kv,
+                         double center, double sd, double prob, double om, double osd) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; 2 * q < n; q += stride) {
+        double z[2], w[2];
+        box_muller(kx, q, &z[0], &z[1]);
+        box_muller(kv, q, &w[0], &w[1]);
+        for (int k = 0; k < 2; ++k) {
+            int64_t i = 2 * q + k;
+            if (i >= n) break;
+            double u = uniform53(splitmix_at(km, (uint64_t)i));
+            out[i] = (u < prob) ? (float)(om + osd * w[k]) : (float)(center + sd * z[k]);
+        }
+    }
+}
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void k_copy(const f4* __restrict__ src, f4* __restrict__ dst,
+                                              int64_t n4) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
+        dst[i] = src[i];
+}
+
+inline uint64_t stream_key(uint64_t seed, uint32_t id) { return splitmix_at(seed, id); }
+
+inline dim3 grid_for(int64_t items) {
+    int64_t b = (items + 255) / 256;
+    if (b < 1) b = 1;
+    if (b > 16384) b = 16384;
+    return dim3((unsigned)b);
+}
+
+int status() { return hipGetLastError() == hipSuccess ? 0 : -3; }
+
+}  // namespace
+
+extern "C" {
+
+__attribute__((visibility("default"))) int soar_synth_normal(float* out, int64_t n, uint64_t seed,
+                                                             uint32_t id, double mean, double sd,
+                                                             void* stream) {
+    if (n <= 0) return 0;
+    if (!out) return -1;
+    k_normal<<<grid_for((n + 1) / 2), 256, 0, (hipStream_t)stream>>>(out, n, stream_key(seed, id),
+                                                                     mean, sd);
+    return status();
+}
+
+__attribute__((visibility("default"))) int soar_synth_uniform(float* out, int64_t n, uint64_t seed,
+                                                              uint32_t id, double lo, double hi,
+                                                              void* stream) {
+    if (n <= 0) return 0;
+    if (!out) return -1;
+    k_uniform<<<grid_for(n), 256, 0, (hipStream_t)stream>>>(out, n, stream_key(seed, id), lo, hi);
+    return status();
+}
+
+__attribute__((visibility("default"))) int soar_synth_stress(float* out, int64_t n, uint64_t seed,
+                                                             double center, double sd, double p,
+                                                             double om, double osd, void* stream) {
+    if (n <= 0) return 0;
+    if (!out) return -1;
+    k_stress<<<grid_for((n + 1) / 2), 256, 0, (hipStream_t)stream>>>(
+        out, n, stream_key(seed, 1), stream_key(seed, 5), stream_key(seed, 6), center, sd, p, om,
+        osd);
+    return status();
+}
+
+__attribute__((visibility("default"))) int soar_synth_copy(const float* src, float* dst, int64_t n,
+                                                           void* stream) {
+    if (n <= 0) return 0;
+    if (!src || !dst || (n % 4) || ((uintptr_t)src & 15) || ((uintptr_t)dst & 15)) return -1;
+    k_copy<<<grid_for(n / 4), 256, 0, (hipStream_t)stream>>>((const f4*)src, (f4*)dst, n / 4);
+    return status();
+}
+
+}  // extern "C"

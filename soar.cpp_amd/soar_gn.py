@@ -1,0 +1,295 @@
+"""ctypes binding of libsoar_gn.so, the MI355X GroupNorm+SiLU library.
+
+The reference ships the same kind of thin ctypes layer over its C-ABI
+(pomagrenate/soar.cpp ``soar/__init__.py:16-96``).  This one binds the
+operator-level C-ABI of ``include/soar_gn.h`` and adds helpers that take
+torch tensors (torch is only the device-memory and stream plumbing here:
+every computation runs in the HIP kernels of ``csrc/``).
+
+Importing this module never falls back to anything: if the library is not
+built, :func:`lib` raises :class:`SoarUnavailable`.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "lib", "libsoar_gn.so")
+SYNTH_PATH = os.path.join(HERE, "lib", "libsoar_synth.so")
+HEADER_PATH = os.path.join(ROOT, "include", "soar_gn.h")
+
+SOAR_OK = 0
+SOAR_EINVAL = -1
+SOAR_ENOMEM = -2
+SOAR_EHIP = -3
+SOAR_ENODEV = -4
+
+GN_SILU = 1
+GN_RESIDUAL = 2
+GN_ACCUMULATE_DX = 4
+
+TUNE_CHUNK = 1
+TUNE_REVERSE = 2
+TUNE_NT_STORE = 3
+
+
+class SoarUnavailable(RuntimeError):
+    """The HIP library is not built or cannot be loaded."""
+
+
+class SoarError(RuntimeError):
+    """A C-ABI call returned a negative status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"soar status {code}: {message}")
+        self.code = code
+        self.message = message
+
+
+_c = ctypes
+_P = _c.c_void_p
+_I64 = _c.c_int64
+_SZ = _c.c_size_t
+
+# name -> (restype, argtypes); every function include/soar_gn.h declares.
+SIGNATURES = {
+    "soar_last_error": (_c.c_char_p, []),
+    "soar_is_device_available": (_c.c_int, []),
+    "soar_gn_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "soar_gn_silu_forward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                        _c.c_float, _c.c_uint, _P, _SZ, _P]),
+    "soar_gn_silu_backward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
+                                         _I64, _I64, _c.c_uint, _P, _SZ, _P]),
+    "soar_group_norm_forward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ,
+                                           _c.c_float, _P]),
+    "soar_group_norm_backward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ,
+                                            _P]),
+    "soar_silu_forward": (_c.c_int, [_P, _P, _SZ, _P]),
+    "soar_silu_backward": (_c.c_int, [_P, _P, _P, _SZ, _P]),
+    "soar_add_forward": (_c.c_int, [_P, _P, _P, _SZ, _P]),
+    "soar_add_backward": (_c.c_int, [_P, _P, _P, _SZ, _P]),
+    "soar_zero": (_c.c_int, [_P, _SZ, _P]),
+    "soar_fill": (_c.c_int, [_P, _c.c_float, _SZ, _P]),
+    "soar_arena_create": (_c.c_int, [_SZ, _SZ, _c.POINTER(_P)]),
+    "soar_arena_alloc": (_c.c_int, [_P, _SZ, _c.POINTER(_P), _c.POINTER(_SZ)]),
+    "soar_arena_freeze_static": (_c.c_int, [_P]),
+    "soar_arena_reset_dynamic": (_c.c_int, [_P]),
+    "soar_arena_info": (_c.c_int, [_P, _c.POINTER(_SZ), _c.POINTER(_SZ), _c.POINTER(_SZ),
+                                   _c.POINTER(_P)]),
+    "soar_arena_destroy": (_c.c_int, [_P]),
+    "soar_memcpy_h2d": (_c.c_int, [_P, _P, _SZ, _P]),
+    "soar_memcpy_d2h": (_c.c_int, [_P, _P, _SZ, _P]),
+    "soar_prof_enable": (_c.c_int, [_c.c_int]),
+    "soar_prof_summary": (_c.c_int, [_c.c_char_p, _SZ]),
+    "soar_gn_tune": (_c.c_int, [_c.c_int, _I64]),
+    "soar_gn_tune_get": (_I64, [_c.c_int]),
+}
+
+SYNTH_SIGNATURES = {
+    "soar_synth_normal": (_c.c_int, [_P, _I64, _c.c_uint64, _c.c_uint32, _c.c_double,
+                                     _c.c_double, _P]),
+    "soar_synth_uniform": (_c.c_int, [_P, _I64, _c.c_uint64, _c.c_uint32, _c.c_double,
+                                      _c.c_double, _P]),
+    "soar_synth_stress": (_c.c_int, [_P, _I64, _c.c_uint64, _c.c_double, _c.c_double,
+                                     _c.c_double, _c.c_double, _c.c_double, _P]),
+    "soar_synth_copy": (_c.c_int, [_P, _P, _I64, _P]),
+}
+
+_LIB = None
+_SYNTH = None
+
+
+def header_symbols(path: str = HEADER_PATH) -> list[str]:
+    """Names of every function declared with SOAR_API in include/soar_gn.h."""
+    with open(path) as f:
+        text = f.read()
+    return re.findall(r"SOAR_API\s+[^;(]*?\b(soar_\w+)\s*\(", text)
+
+
+def _bind(path, signatures):
+    if not os.path.exists(path):
+        raise SoarUnavailable(
+            f"{path} is not built; run `make -C soar.cpp_amd` or __graft_entry__.build()")
+    try:
+        handle = ctypes.CDLL(path)
+    except OSError as e:  # pragma: no cover - depends on the machine
+        raise SoarUnavailable(f"cannot load {path}: {e}") from e
+    for name, (res, args) in signatures.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    return handle
+
+
+def lib():
+    """The loaded libsoar_gn.so (raises SoarUnavailable if absent)."""
+    global _LIB
+    if _LIB is None:
+        _LIB = _bind(LIB_PATH, SIGNATURES)
+    return _LIB
+
+
+def synth_lib():
+    global _SYNTH
+    if _SYNTH is None:
+        _SYNTH = _bind(SYNTH_PATH, SYNTH_SIGNATURES)
+    return _SYNTH
+
+
+def last_error() -> str:
+    return lib().soar_last_error().decode()
+
+
+def check(rc: int) -> int:
+    if rc < 0:
+        raise SoarError(rc, last_error())
+    return rc
+
+
+# ---- torch helpers ---------------------------------------------------------
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _nchw(x):
+    if x.dim() == 4:
+        N, C, H, W = x.shape
+        return N, C, H * W
+    if x.dim() == 3:
+        N, C, HW = x.shape
+        return N, C, HW
+    raise ValueError("expected [N,C,H,W] or [N,C,HW]")
+
+
+def _check_tensor(t, name):
+    import torch
+    if t is None:
+        return
+    if t.dtype != torch.float32 or not t.is_cuda or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float32 device tensor")
+
+
+def workspace_bytes(N, C, HW, G) -> int:
+    return int(lib().soar_gn_workspace_bytes(N, C, HW, G))
+
+
+def workspace(N, C, HW, G, device=None):
+    import torch
+    n = max(workspace_bytes(N, C, HW, G), 1)
+    return torch.empty(n, dtype=torch.uint8, device=device or "cuda")
+
+
+def gn_silu_forward(x, gamma, beta, G, eps=1e-5, silu=True, residual=False, y=None,
+                    mean=None, rstd=None, ws=None, stream=None):
+    """y = silu(group_norm(x)) [+ x] through soar_gn_silu_forward.
+
+    Returns (y, mean, rstd); mean/rstd are float32[N*G]."""
+    import torch
+    N, C, HW = _nchw(x)
+    for t, n in ((x, "x"), (gamma, "gamma"), (beta, "beta"), (y, "y"), (mean, "mean"),
+                 (rstd, "rstd")):
+        _check_tensor(t, n)
+    y = torch.empty_like(x) if y is None else y
+    mean = torch.empty(N * G, dtype=torch.float32, device=x.device) if mean is None else mean
+    rstd = torch.empty(N * G, dtype=torch.float32, device=x.device) if rstd is None else rstd
+    ws = workspace(N, C, HW, G, x.device) if ws is None else ws
+    flags = (GN_SILU if silu else 0) | (GN_RESIDUAL if residual else 0)
+    check(lib().soar_gn_silu_forward(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(y), _ptr(mean),
+                                     _ptr(rstd), N, C, HW, G, eps, flags, _ptr(ws),
+                                     ws.numel(), _stream(stream)))
+    return y, mean, rstd
+
+
+def gn_silu_backward(dy, x, gamma, beta, mean, rstd, G, silu=True, residual=False,
+                     dx=None, dgamma=None, dbeta=None, want_dx=True, want_params=True,
+                     accumulate_dx=False, ws=None, stream=None):
+    """Backward through soar_gn_silu_backward; returns (dx, dgamma, dbeta).
+
+    dgamma/dbeta are accumulated into (fresh zeros when not given)."""
+    import torch
+    N, C, HW = _nchw(x)
+    for t, n in ((dy, "dy"), (x, "x"), (gamma, "gamma"), (beta, "beta"), (dx, "dx"),
+                 (dgamma, "dgamma"), (dbeta, "dbeta")):
+        _check_tensor(t, n)
+    if want_dx and dx is None:
+        dx = torch.empty_like(x) if not accumulate_dx else torch.zeros_like(x)
+    if want_params:
+        if dgamma is None:
+            dgamma = torch.zeros(C, dtype=torch.float32, device=x.device)
+        if dbeta is None:
+            dbeta = torch.zeros(C, dtype=torch.float32, device=x.device)
+    ws = workspace(N, C, HW, G, x.device) if ws is None else ws
+    flags = ((GN_SILU if silu else 0) | (GN_RESIDUAL if residual else 0)
+             | (GN_ACCUMULATE_DX if accumulate_dx else 0))
+    check(lib().soar_gn_silu_backward(_ptr(dy), _ptr(x), _ptr(gamma), _ptr(beta),
+                                      _ptr(mean), _ptr(rstd),
+                                      _ptr(dx) if want_dx else None,
+                                      _ptr(dgamma) if want_params else None,
+                                      _ptr(dbeta) if want_params else None,
+                                      N, C, HW, G, flags, _ptr(ws), ws.numel(),
+                                      _stream(stream)))
+    return (dx if want_dx else None, dgamma if want_params else None,
+            dbeta if want_params else None)
+
+
+def prof_enable(on: bool = True):
+    check(lib().soar_prof_enable(1 if on else 0))
+
+
+def prof_summary() -> list[dict]:
+    buf = ctypes.create_string_buffer(1 << 16)
+    check(lib().soar_prof_summary(buf, len(buf)))
+    return json.loads(buf.value.decode() or "[]")
+
+
+def tune(key: int, value: int):
+    check(lib().soar_gn_tune(key, value))
+
+
+def tune_get(key: int) -> int:
+    return int(lib().soar_gn_tune_get(key))
+
+
+# ---- synthetic inputs (libsoar_synth.so) ------------------------------------
+
+def synth_normal(t, seed, stream_id, mean=0.0, std=1.0, stream=None):
+    rc = synth_lib().soar_synth_normal(_ptr(t), t.numel(), seed, stream_id, mean, std,
+                                       _stream(stream))
+    if rc:
+        raise SoarError(rc, "soar_synth_normal failed")
+    return t
+
+
+def synth_uniform(t, seed, stream_id, lo, hi, stream=None):
+    rc = synth_lib().soar_synth_uniform(_ptr(t), t.numel(), seed, stream_id, lo, hi,
+                                        _stream(stream))
+    if rc:
+        raise SoarError(rc, "soar_synth_uniform failed")
+    return t
+
+
+def synth_stress(t, seed, center=1e3, std=1e-2, p=1e-3, out_mean=0.0, out_std=50.0,
+                 stream=None):
+    rc = synth_lib().soar_synth_stress(_ptr(t), t.numel(), seed, center, std, p, out_mean,
+                                       out_std, _stream(stream))
+    if rc:
+        raise SoarError(rc, "soar_synth_stress failed")
+    return t
+
+
+def synth_copy(src, dst, stream=None):
+    rc = synth_lib().soar_synth_copy(_ptr(src), _ptr(dst), src.numel(), _stream(stream))
+    if rc:
+        raise SoarError(rc, "soar_synth_copy failed")
+    return dst

@@ -1,0 +1,104 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol the header
+declares, and validates arguments without touching a GPU."""
+import ctypes
+
+import pytest
+
+import soar_gn
+
+
+@pytest.fixture(scope="module")
+def L():
+    return soar_gn.lib()
+
+
+def test_exports_every_header_symbol(L):
+    names = soar_gn.header_symbols()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    # and the binding declares exactly those
+    assert set(names) == set(soar_gn.SIGNATURES)
+
+
+def test_synth_library_exports(L):
+    S = soar_gn.synth_lib()
+    for n in soar_gn.SYNTH_SIGNATURES:
+        assert hasattr(S, n)
+
+
+def test_workspace_bytes_is_host_arithmetic(L):
+    # cfg 3: 64 planes x 128 chunks of 32768 floats -> 8192 partials of 16 B
+    # plus 64 plane sums of 16 B, each region 256-byte aligned.
+    assert soar_gn.tune_get(soar_gn.TUNE_CHUNK) == 32768
+    assert soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) == 8192 * 16 + 1024
+    # small planes get one block each (chunk clipped to the plane)
+    assert soar_gn.workspace_bytes(2, 6, 10, 3) == 256 + 256
+    assert soar_gn.workspace_bytes(0, 6, 10, 3) == 0
+    assert soar_gn.workspace_bytes(1, 6, 10, 4) == 0  # C % G != 0
+
+
+def _fwd(L, N, C, HW, G, flags=1, eps=1e-5):
+    return L.soar_gn_silu_forward(None, None, None, None, None, None, N, C, HW, G, eps,
+                                  flags, None, 0, None)
+
+
+def test_forward_validation_without_gpu(L):
+    assert _fwd(L, 1, 6, 16, 4) == soar_gn.SOAR_EINVAL
+    assert "divisible" in soar_gn.last_error()
+    assert _fwd(L, 1, 6, 16, 0) == soar_gn.SOAR_EINVAL
+    assert _fwd(L, -1, 6, 16, 3) == soar_gn.SOAR_EINVAL
+    assert _fwd(L, 1, 6, 16, 3, flags=4) == soar_gn.SOAR_EINVAL  # ACCUMULATE_DX is bwd-only
+    assert _fwd(L, 1, 6, 16, 3, eps=-1.0) == soar_gn.SOAR_EINVAL
+    assert _fwd(L, 1 << 40, 1 << 20, 1 << 20, 1) == soar_gn.SOAR_EINVAL  # overflow
+    # empty tensors are a successful no-op, as the reference returns early
+    assert _fwd(L, 0, 6, 16, 3) == soar_gn.SOAR_OK
+    assert _fwd(L, 1, 6, 0, 3) == soar_gn.SOAR_OK
+    assert soar_gn.last_error() == ""
+
+
+def test_no_device_is_reported_not_faulted(L):
+    if L.soar_is_device_available():
+        pytest.skip("a device is visible")
+    assert _fwd(L, 1, 6, 16, 3) == soar_gn.SOAR_ENODEV
+    p = ctypes.c_void_p()
+    assert L.soar_arena_create(1 << 20, 256, ctypes.byref(p)) == soar_gn.SOAR_ENODEV
+    assert L.soar_silu_forward(None, None, 16, None) == soar_gn.SOAR_ENODEV
+
+
+def test_backward_validation_without_gpu(L):
+    f = L.soar_gn_silu_backward
+    dummy = ctypes.c_void_p(0x1000)
+    # dgamma without dbeta
+    rc = f(None, None, None, None, None, None, None, dummy, None, 1, 6, 16, 3, 1, None, 0, None)
+    assert rc == soar_gn.SOAR_EINVAL and "both" in soar_gn.last_error()
+    rc = f(None, None, None, None, None, None, None, None, None, 1, 6, 16, 3, 8, None, 0, None)
+    assert rc == soar_gn.SOAR_EINVAL  # unknown flag
+    # nothing requested -> no-op
+    rc = f(None, None, None, None, None, None, None, None, None, 1, 6, 16, 3, 1, None, 0, None)
+    assert rc == soar_gn.SOAR_OK
+
+
+def test_tuning_knobs(L):
+    old = soar_gn.tune_get(soar_gn.TUNE_CHUNK)
+    assert L.soar_gn_tune(soar_gn.TUNE_CHUNK, 1000) == soar_gn.SOAR_EINVAL
+    assert L.soar_gn_tune(soar_gn.TUNE_REVERSE, 2) == soar_gn.SOAR_EINVAL
+    assert L.soar_gn_tune(99, 1) == soar_gn.SOAR_EINVAL
+    soar_gn.tune(soar_gn.TUNE_CHUNK, 4096)
+    assert soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) == 65536 * 16 + 1024
+    soar_gn.tune(soar_gn.TUNE_CHUNK, old)
+    assert soar_gn.tune_get(soar_gn.TUNE_CHUNK) == old
+
+
+def test_prof_summary_empty(L):
+    soar_gn.prof_enable(False)
+    assert soar_gn.prof_summary() == []
+
+
+def test_reference_signature_validation(L):
+    rc = L.soar_group_norm_forward(None, None, None, None, None, None, 4, 6, 16, 1e-5, None)
+    assert rc == soar_gn.SOAR_EINVAL
+    rc = L.soar_group_norm_forward(None, None, None, None, None, None, 3, 6, 0, 1e-5, None)
+    assert rc == soar_gn.SOAR_OK
+    assert L.soar_add_backward(None, None, None, 10, None) == soar_gn.SOAR_OK
+    assert L.soar_fill(None, 1.0, 0, None) == soar_gn.SOAR_OK
