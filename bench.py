@@ -99,6 +99,7 @@ class Step:
         self.acts = [self.x] + [torch.empty_like(self.x) for _ in range(blocks)]
         self.mean = [torch.empty(N * G, device="cuda") for _ in range(blocks)]
         self.rstd = [torch.empty(N * G, device="cuda") for _ in range(blocks)]
+        self.mean_lo = [torch.empty(N * G, device="cuda") for _ in range(blocks)]
         self.ws = gn.workspace(N, C, HW, G)
         self.grads = [torch.empty_like(self.x) for _ in range(2)] if passes == "fwdbwd" else []
         self.dparams = [(torch.zeros(C, device="cuda"), torch.zeros(C, device="cuda"))
@@ -114,7 +115,7 @@ class Step:
         for b, (gamma, beta) in enumerate(self.params):
             gn.gn_silu_forward(self.acts[b], gamma, beta, self.G, eps=1e-5,
                                residual=self.residual, y=self.acts[b + 1], mean=self.mean[b],
-                               rstd=self.rstd[b], ws=self.ws)
+                               rstd=self.rstd[b], mean_lo=self.mean_lo[b], ws=self.ws)
         if self.passes == "fwd":
             return
         g_in = self.dy
@@ -122,8 +123,8 @@ class Step:
             gamma, beta = self.params[b]
             g_out = self.grads[b % 2]
             dg, db = self.dparams[b]
-            gn.gn_silu_backward(g_in, self.acts[b], gamma, beta, self.mean[b], self.rstd[b],
-                                self.G, residual=self.residual, dx=g_out, dgamma=dg, dbeta=db,
+            gn.gn_silu_backward(g_in, self.acts[b], gamma, beta,
+                                (self.mean[b], self.rstd[b], self.mean_lo[b]), self.G, residual=self.residual, dx=g_out, dgamma=dg, dbeta=db,
                                 ws=self.ws)
             g_in = g_out
 

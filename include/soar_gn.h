@@ -69,22 +69,28 @@ SOAR_API size_t soar_gn_workspace_bytes(int64_t N, int64_t C, int64_t HW,
 /* Forward: per unit mean and rstd = 1/sqrt(var + eps) (biased variance),
  * then y = f(gamma_c*(x - mean)*rstd + beta_c) [+ x], f = SiLU when
  * SOAR_GN_SILU is set, identity otherwise.  gamma/beta may be NULL (1 / 0,
- * the affine=false module).  y may alias x.  Writes mean/rstd for the
- * backward.
+ * the affine=false module).  y must not overlap x.  Writes mean/rstd (fp32,
+ * as the reference saves them) for the backward, and, when mean_lo is not
+ * NULL, mean_lo[u] = exact mean - mean[u]: the fp32 rounding residual of
+ * the mean.  Passing mean_lo back to the backward keeps xhat exact to fp32
+ * rounding even when std << |mean| (e.g. x = 1e3 + N(0, 1e-2)), where the
+ * rounded mean alone shifts xhat by up to ulp(mean)/2 * rstd.  The forward
+ * output y always uses the exact mean.
  * Replaces: group_norm_forward (cuda_kernels.hpp:82-84) followed by
  * silu_forward (:19), the Vulkan pair group_norm_stats.comp +
  * group_norm_affine_silu.comp, and with SOAR_GN_RESIDUAL the add_forward
  * (:15) of a residual block (src/nn/blocks.cpp:478-480). */
 SOAR_API int soar_gn_silu_forward(const float* x, const float* gamma,
                                   const float* beta, float* y, float* mean,
-                                  float* rstd, int64_t N, int64_t C,
-                                  int64_t HW, int64_t G, float eps,
+                                  float* rstd, float* mean_lo, int64_t N,
+                                  int64_t C, int64_t HW, int64_t G, float eps,
                                   unsigned flags, void* workspace,
                                   size_t workspace_bytes, void* stream);
 
 /* Backward of soar_gn_silu_forward given upstream gradient dy, the forward
- * input x and the saved mean/rstd.  SiLU is recomputed from x (nothing but
- * x, mean and rstd is saved by the forward).
+ * input x and the saved mean/rstd (and mean_lo, NULL = 0).  SiLU is
+ * recomputed from x (nothing but x and the statistics is saved by the
+ * forward).
  *   dgamma[c] += sum_{n,hw} dz * xhat,  dbeta[c] += sum_{n,hw} dz
  *   dx = rstd*(gamma_c*dz - (S1 + xhat*S2)/M) [+ dy] [+ previous dx]
  * with dz the gradient at the GroupNorm output, xhat = (x-mean)*rstd,
@@ -100,7 +106,8 @@ SOAR_API int soar_gn_silu_forward(const float* x, const float* gamma,
 SOAR_API int soar_gn_silu_backward(const float* dy, const float* x,
                                    const float* gamma, const float* beta,
                                    const float* mean, const float* rstd,
-                                   float* dx, float* dgamma, float* dbeta,
+                                   const float* mean_lo, float* dx,
+                                   float* dgamma, float* dbeta,
                                    int64_t N, int64_t C, int64_t HW,
                                    int64_t G, unsigned flags, void* workspace,
                                    size_t workspace_bytes, void* stream);
@@ -112,7 +119,9 @@ SOAR_API int soar_gn_silu_backward(const float* dy, const float* x,
  * different streams of one device must not overlap. */
 
 /* Replaces: group_norm_forward (cuda_kernels.hpp:82-84,
- * normalization_kernels.cu:93-111).  gamma/beta nullable. */
+ * normalization_kernels.cu:93-111).  gamma/beta nullable.  Saves only the
+ * fp32 mean, as the reference does, so its backward has the reference's
+ * precision when std << |mean|. */
 SOAR_API int soar_group_norm_forward(const float* in, const float* gamma,
                                      const float* beta, float* out,
                                      float* saved_mean, float* saved_rstd,

@@ -233,9 +233,10 @@ SOAR_API size_t soar_gn_workspace_bytes(int64_t N, int64_t C, int64_t HW, int64_
 }
 
 SOAR_API int soar_gn_silu_forward(const float* x, const float* gamma, const float* beta,
-                                  float* y, float* mean, float* rstd, int64_t N, int64_t C,
-                                  int64_t HW, int64_t G, float eps, unsigned flags,
-                                  void* workspace, size_t workspace_bytes, void* stream) {
+                                  float* y, float* mean, float* rstd, float* mean_lo,
+                                  int64_t N, int64_t C, int64_t HW, int64_t G, float eps,
+                                  unsigned flags, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
     int64_t elems = 0;
     int rc = check_shape(N, C, HW, G, &elems);
     if (rc) return rc;
@@ -248,6 +249,7 @@ SOAR_API int soar_gn_silu_forward(const float* x, const float* gamma, const floa
     const size_t sb = (size_t)(N * G) * sizeof(float);
     if ((rc = check_dev(x, tb, "x")) || (rc = check_dev(y, tb, "y")) ||
         (rc = check_dev(mean, sb, "mean")) || (rc = check_dev(rstd, sb, "rstd")) ||
+        (rc = check_dev_opt(mean_lo, sb, "mean_lo")) ||
         (rc = check_dev_opt(gamma, (size_t)C * 4, "gamma")) ||
         (rc = check_dev_opt(beta, (size_t)C * 4, "beta")))
         return rc;
@@ -257,7 +259,7 @@ SOAR_API int soar_gn_silu_forward(const float* x, const float* gamma, const floa
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     p.vec4 = p.vec4 && aligned16(x) && aligned16(y);
     if ((rc = check_ws(p, workspace, workspace_bytes))) return rc;
-    soar::gn::FwdArgs a{x, gamma, beta, y, mean, rstd, eps, flags, workspace};
+    soar::gn::FwdArgs a{x, gamma, beta, y, mean, rstd, mean_lo, eps, flags, workspace};
     hipError_t e = soar::gn::launch_forward(p, t, a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "GroupNorm forward launch");
     return ok();
@@ -265,7 +267,8 @@ SOAR_API int soar_gn_silu_forward(const float* x, const float* gamma, const floa
 
 SOAR_API int soar_gn_silu_backward(const float* dy, const float* x, const float* gamma,
                                    const float* beta, const float* mean, const float* rstd,
-                                   float* dx, float* dgamma, float* dbeta, int64_t N,
+                                   const float* mean_lo, float* dx, float* dgamma,
+                                   float* dbeta, int64_t N,
                                    int64_t C, int64_t HW, int64_t G, unsigned flags,
                                    void* workspace, size_t workspace_bytes, void* stream) {
     int64_t elems = 0;
@@ -282,7 +285,7 @@ SOAR_API int soar_gn_silu_backward(const float* dy, const float* x, const float*
     const size_t cb = (size_t)C * sizeof(float);
     if ((rc = check_dev(dy, tb, "dy")) || (rc = check_dev(x, tb, "x")) ||
         (rc = check_dev(mean, sb, "mean")) || (rc = check_dev(rstd, sb, "rstd")) ||
-        (rc = check_dev_opt(dx, tb, "dx")) || (rc = check_dev_opt(gamma, cb, "gamma")) ||
+        (rc = check_dev_opt(mean_lo, sb, "mean_lo")) || (rc = check_dev_opt(dx, tb, "dx")) || (rc = check_dev_opt(gamma, cb, "gamma")) ||
         (rc = check_dev_opt(beta, cb, "beta")) || (rc = check_dev_opt(dgamma, cb, "dgamma")) ||
         (rc = check_dev_opt(dbeta, cb, "dbeta")))
         return rc;
@@ -292,7 +295,8 @@ SOAR_API int soar_gn_silu_backward(const float* dy, const float* x, const float*
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     p.vec4 = p.vec4 && aligned16(x) && aligned16(dy) && aligned16(dx);
     if ((rc = check_ws(p, workspace, workspace_bytes))) return rc;
-    soar::gn::BwdArgs a{dy, x, gamma, beta, mean, rstd, dx, dgamma, dbeta, flags, workspace};
+    soar::gn::BwdArgs a{dy, x, gamma, beta, mean, rstd, mean_lo, dx, dgamma, dbeta, flags,
+                        workspace};
     hipError_t e = soar::gn::launch_backward(p, t, a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "GroupNorm backward launch");
     return ok();
@@ -311,8 +315,9 @@ SOAR_API int soar_group_norm_forward(const float* in, const float* gamma, const 
     if (need == 0) return fail(SOAR_EINVAL, "shape is too large");
     void* ws = nullptr;
     if ((rc = owned_workspace(need, &ws))) return rc;
-    return soar_gn_silu_forward(in, gamma, beta, out, saved_mean, saved_rstd, 1, (int64_t)C,
-                                (int64_t)HW, (int64_t)num_groups, eps, 0u, ws, need, stream);
+    return soar_gn_silu_forward(in, gamma, beta, out, saved_mean, saved_rstd, nullptr, 1,
+                                (int64_t)C, (int64_t)HW, (int64_t)num_groups, eps, 0u, ws, need,
+                                stream);
 }
 
 SOAR_API int soar_group_norm_backward(const float* grad_out, const float* in,
@@ -329,8 +334,8 @@ SOAR_API int soar_group_norm_backward(const float* grad_out, const float* in,
     if (need == 0) return fail(SOAR_EINVAL, "shape is too large");
     void* ws = nullptr;
     if ((rc = owned_workspace(need, &ws))) return rc;
-    return soar_gn_silu_backward(grad_out, in, gamma, nullptr, saved_mean, saved_rstd, grad_in,
-                                 grad_gamma, grad_beta, 1, (int64_t)C, (int64_t)HW,
+    return soar_gn_silu_backward(grad_out, in, gamma, nullptr, saved_mean, saved_rstd, nullptr,
+                                 grad_in, grad_gamma, grad_beta, 1, (int64_t)C, (int64_t)HW,
                                  (int64_t)num_groups, SOAR_GN_ACCUMULATE_DX, ws, need, stream);
 }
 

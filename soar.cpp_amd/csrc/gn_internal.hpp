@@ -42,6 +42,7 @@ struct FwdArgs {
     float* y;
     float* mean;
     float* rstd;
+    float* mean_lo;  // nullable: mean - (float)mean
     float eps;
     unsigned flags;
     void* ws;
@@ -54,6 +55,7 @@ struct BwdArgs {
     const float* beta;   // nullable
     const float* mean;
     const float* rstd;
+    const float* mean_lo;  // nullable (treated as 0)
     float* dx;      // nullable
     float* dgamma;  // nullable (with dbeta)
     float* dbeta;

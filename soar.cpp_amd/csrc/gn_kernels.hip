@@ -255,10 +255,16 @@ __global__ __launch_bounds__(kThreads) void k_stats_partial(
 }
 
 // Forward finish: one block per unit (n, g) combines its cpg*cpp chunk
-// partials in a fixed order and writes mean and rstd.
+// partials in a fixed order and writes mean and rstd.  The mean is also
+// kept as hi + lo (hi = fp32 mean, lo = the fp32 rounding residual): when
+// std << |mean| the residual of hi alone, times rstd, would shift xhat by
+// up to ulp(mean)/2 * rstd, far above the 1e-4 output tolerance.  The lo
+// part goes to the caller's optional mean_lo (for the backward) and to the
+// workspace (for the apply kernel of the same call).
 __global__ __launch_bounds__(kThreads) void k_stats_finish(
     const double2* __restrict__ part, float* __restrict__ mean,
-    float* __restrict__ rstd, int64_t C, int64_t G, int64_t cpg, int64_t HW,
+    float* __restrict__ rstd, float* __restrict__ mean_lo,
+    float* __restrict__ lo_ws, int64_t C, int64_t G, int64_t cpg, int64_t HW,
     int64_t chunk, int64_t cpp, float eps) {
     __shared__ Moments lds[kWaves];
     const int64_t u = blockIdx.x;
@@ -275,27 +281,35 @@ __global__ __launch_bounds__(kThreads) void k_stats_finish(
     Moments r = block_reduce(m, lds);
     if (threadIdx.x == 0) {
         const double var = r.n > 0.0 ? fmax(r.m2 / r.n, 0.0) : 0.0;
-        mean[u] = (float)r.mean;
+        const float hi = (float)r.mean;
+        const float lo = (float)(r.mean - (double)hi);
+        mean[u] = hi;
         rstd[u] = (float)(1.0 / sqrt(var + (double)eps));
+        lo_ws[u] = lo;
+        if (mean_lo) mean_lo[u] = lo;
     }
 }
 
-// Per-block coefficients of plane `plane`.
+// Per-block coefficients of plane `plane`: xhat = fma(x - mu, r, e) with
+// mu the fp32 mean and e = -mean_lo * r.  (x - mu is exact whenever x is
+// within a factor two of mu, Sterbenz.)
 struct PlaneCoef {
     int64_t c, n, u;
-    float mu, r, gm, bt;
+    float mu, r, e, gm, bt;
 };
 
 __device__ __forceinline__ PlaneCoef plane_coef(
     int64_t plane, int64_t C, int64_t G, int64_t cpg,
     const float* __restrict__ gamma, const float* __restrict__ beta,
-    const float* __restrict__ mean, const float* __restrict__ rstd) {
+    const float* __restrict__ mean, const float* __restrict__ rstd,
+    const float* __restrict__ mean_lo) {
     PlaneCoef k;
     k.n = plane / C;
     k.c = plane - k.n * C;
     k.u = k.n * G + k.c / cpg;
     k.mu = mean[k.u];
     k.r = rstd[k.u];
+    k.e = mean_lo ? -mean_lo[k.u] * k.r : 0.0f;
     k.gm = gamma ? gamma[k.c] : 1.0f;
     k.bt = beta ? beta[k.c] : 0.0f;
     return k;
@@ -308,13 +322,14 @@ template <bool VEC, bool SILU, bool RES, bool NT>
 __global__ __launch_bounds__(kThreads) void k_apply(
     const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ mean,
-    const float* __restrict__ rstd, float* __restrict__ y, int64_t C,
-    int64_t G, int64_t cpg, int64_t HW, int64_t chunk, int64_t cpp,
-    int64_t nblocks, int reverse) {
+    const float* __restrict__ rstd, const float* __restrict__ mean_lo,
+    float* __restrict__ y, int64_t C, int64_t G, int64_t cpg, int64_t HW,
+    int64_t chunk, int64_t cpp, int64_t nblocks, int reverse) {
     const int64_t b = reverse ? nblocks - 1 - (int64_t)blockIdx.x : (int64_t)blockIdx.x;
     const Chunk ck = chunk_of(b, HW, chunk, cpp);
-    const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd);
-    const float a = k.gm * k.r, mu = k.mu, bt = k.bt;
+    const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
+    // z = gamma*xhat + beta = (x - mu)*(gamma*r) + (beta + gamma*e)
+    const float a = k.gm * k.r, mu = k.mu, bt = fmaf(k.gm, k.e, k.bt);
     const int64_t base = ck.plane * HW + ck.off;
     const int t = threadIdx.x;
     auto f = [&](float v) {
@@ -360,17 +375,17 @@ __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ gamma, const float* __restrict__ beta,
     const float* __restrict__ mean, const float* __restrict__ rstd,
-    double2* __restrict__ part, int64_t C, int64_t G, int64_t cpg, int64_t HW,
-    int64_t chunk, int64_t cpp) {
+    const float* __restrict__ mean_lo, double2* __restrict__ part, int64_t C,
+    int64_t G, int64_t cpg, int64_t HW, int64_t chunk, int64_t cpp) {
     __shared__ float lds[2 * kWaves];
     const Chunk ck = chunk_of(blockIdx.x, HW, chunk, cpp);
-    const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd);
-    const float mu = k.mu, r = k.r, gm = k.gm, bt = k.bt;
+    const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
+    const float mu = k.mu, r = k.r, e = k.e, gm = k.gm, bt = k.bt;
     const int64_t base = ck.plane * HW + ck.off;
     const int t = threadIdx.x;
     float sa0 = 0.f, sa1 = 0.f, sb0 = 0.f, sb1 = 0.f;
     auto acc = [&](float g, float v, float& sa, float& sb) {
-        float xh = (v - mu) * r;
+        float xh = fmaf(v - mu, r, e);
         float dz = SILU ? dsilu_fast(g, fmaf(gm, xh, bt)) : g;
         sa += dz;
         sb = fmaf(dz, xh, sb);
@@ -443,12 +458,12 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ gamma, const float* __restrict__ beta,
     const float* __restrict__ mean, const float* __restrict__ rstd,
-    const double2* __restrict__ plane_sums, float* __restrict__ dx, int64_t C,
-    int64_t G, int64_t cpg, int64_t HW, int64_t chunk, int64_t cpp,
-    int64_t nblocks, int reverse) {
+    const float* __restrict__ mean_lo, const double2* __restrict__ plane_sums,
+    float* __restrict__ dx, int64_t C, int64_t G, int64_t cpg, int64_t HW,
+    int64_t chunk, int64_t cpp, int64_t nblocks, int reverse) {
     const int64_t b = reverse ? nblocks - 1 - (int64_t)blockIdx.x : (int64_t)blockIdx.x;
     const Chunk ck = chunk_of(b, HW, chunk, cpp);
-    const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd);
+    const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
     double S1 = 0.0, S2 = 0.0;
     const int64_t c0 = (k.c / cpg) * cpg;
     for (int64_t j = 0; j < cpg; ++j) {
@@ -458,14 +473,14 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(
         S2 += gj * ps.y;
     }
     const double Md = (double)(cpg * HW);
-    const float mu = k.mu, r = k.r, gm = k.gm, bt = k.bt;
+    const float mu = k.mu, r = k.r, e = k.e, gm = k.gm, bt = k.bt;
     const float A = gm * r;
     const float B = (float)(-(double)r * S1 / Md);
     const float D = (float)(-(double)r * S2 / Md);
     const int64_t base = ck.plane * HW + ck.off;
     const int t = threadIdx.x;
     auto f = [&](float g, float v, float old) {
-        float xh = (v - mu) * r;
+        float xh = fmaf(v - mu, r, e);
         float dz = SILU ? dsilu_fast(g, fmaf(gm, xh, bt)) : g;
         float o = fmaf(A, dz, fmaf(D, xh, B));
         if (RES) o += g;
@@ -514,11 +529,11 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(
 
 template <bool VEC>
 void apply_dispatch(bool silu, bool res, bool nt, dim3 grid, hipStream_t s,
-                    const Plan& p, const FwdArgs& a, int reverse) {
+                    const Plan& p, const FwdArgs& a, const float* lo_ws, int reverse) {
 #define SOAR_APPLY(S, R, N)                                                  \
     k_apply<VEC, S, R, N><<<grid, kThreads, 0, s>>>(                         \
-        a.x, a.gamma, a.beta, a.mean, a.rstd, a.y, p.C, p.G, p.cpg, p.HW,    \
-        p.chunk, p.cpp, p.blocks, reverse)
+        a.x, a.gamma, a.beta, a.mean, a.rstd, lo_ws, a.y, p.C, p.G, p.cpg,   \
+        p.HW, p.chunk, p.cpp, p.blocks, reverse)
     const int sel = (silu ? 4 : 0) | (res ? 2 : 0) | (nt ? 1 : 0);
     switch (sel) {
         case 0: SOAR_APPLY(false, false, false); break;
@@ -539,8 +554,8 @@ void dx_dispatch(bool res, bool accum, bool nt, dim3 grid, hipStream_t s,
                  int reverse) {
 #define SOAR_DX(R, A, N)                                                     \
     k_bwd_dx<VEC, SILU, R, A, N><<<grid, kThreads, 0, s>>>(                  \
-        a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, plane_sums, a.dx, p.C,   \
-        p.G, p.cpg, p.HW, p.chunk, p.cpp, p.blocks, reverse)
+        a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, plane_sums,   \
+        a.dx, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, p.blocks, reverse)
     const int sel = (res ? 4 : 0) | (accum ? 2 : 0) | (nt ? 1 : 0);
     switch (sel) {
         case 0: SOAR_DX(false, false, false); break;
@@ -578,14 +593,21 @@ bool make_plan(int64_t N, int64_t C, int64_t HW, int64_t G, const Tuning& t,
     return true;
 }
 
+// Workspace regions: [chunk partials: double2 x blocks]
+//                    [plane sums: double2 x planes]
+//                    [mean residuals of this call: float x N*G]
 size_t workspace_bytes(const Plan& p) {
     return align256(sizeof(double2) * (size_t)p.blocks) +
-           align256(sizeof(double2) * (size_t)p.planes);
+           align256(sizeof(double2) * (size_t)p.planes) +
+           align256(sizeof(float) * (size_t)(p.N * p.G));
 }
 
 hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a,
                           hipStream_t s) {
     double2* part = static_cast<double2*>(a.ws);
+    float* lo_ws = reinterpret_cast<float*>(
+        static_cast<char*>(a.ws) + align256(sizeof(double2) * (size_t)p.blocks) +
+        align256(sizeof(double2) * (size_t)p.planes));
     const bool vec = p.vec4;
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
     const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
@@ -600,14 +622,15 @@ hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a,
 
     tok = prof_begin(s, "gn_stats_finish");
     k_stats_finish<<<dim3((unsigned)(p.N * p.G)), kThreads, 0, s>>>(
-        part, a.mean, a.rstd, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, a.eps);
+        part, a.mean, a.rstd, a.mean_lo, lo_ws, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp,
+        a.eps);
     prof_end(s, tok);
 
     tok = prof_begin(s, silu ? "gn_silu_apply" : "gn_apply");
     if (vec)
-        apply_dispatch<true>(silu, res, t.nt_store != 0, grid, s, p, a, t.reverse);
+        apply_dispatch<true>(silu, res, t.nt_store != 0, grid, s, p, a, lo_ws, t.reverse);
     else
-        apply_dispatch<false>(silu, res, t.nt_store != 0, grid, s, p, a, t.reverse);
+        apply_dispatch<false>(silu, res, t.nt_store != 0, grid, s, p, a, lo_ws, t.reverse);
     prof_end(s, tok);
     return hipGetLastError();
 }
@@ -625,10 +648,9 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a,
 
     int tok = prof_begin(s, silu ? "gn_silu_bwd_reduce" : "gn_bwd_reduce");
 #define SOAR_RED(V, S)                                                        \
-    k_bwd_reduce<V, S><<<grid, kThreads, 0, s>>>(a.dy, a.x, a.gamma, a.beta,  \
-                                                 a.mean, a.rstd, part, p.C,  \
-                                                 p.G, p.cpg, p.HW, p.chunk,  \
-                                                 p.cpp)
+    k_bwd_reduce<V, S><<<grid, kThreads, 0, s>>>(                             \
+        a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, part, p.C, p.G, \
+        p.cpg, p.HW, p.chunk, p.cpp)
     if (vec) {
         if (silu) SOAR_RED(true, true); else SOAR_RED(true, false);
     } else {

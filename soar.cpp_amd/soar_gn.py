@@ -60,9 +60,9 @@ SIGNATURES = {
     "soar_last_error": (_c.c_char_p, []),
     "soar_is_device_available": (_c.c_int, []),
     "soar_gn_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
-    "soar_gn_silu_forward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+    "soar_gn_silu_forward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                         _c.c_float, _c.c_uint, _P, _SZ, _P]),
-    "soar_gn_silu_backward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
+    "soar_gn_silu_backward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
                                          _I64, _I64, _c.c_uint, _P, _SZ, _P]),
     "soar_group_norm_forward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ,
                                            _c.c_float, _P]),
@@ -190,34 +190,53 @@ def workspace(N, C, HW, G, device=None):
     return torch.empty(n, dtype=torch.uint8, device=device or "cuda")
 
 
+class Stats(tuple):
+    """Saved statistics of a forward: (mean, rstd, mean_lo), float32[N*G]
+    each; mean_lo is the fp32 rounding residual of the mean."""
+
+    def __new__(cls, mean, rstd, mean_lo):
+        return super().__new__(cls, (mean, rstd, mean_lo))
+
+    mean = property(lambda s: s[0])
+    rstd = property(lambda s: s[1])
+    mean_lo = property(lambda s: s[2])
+
+
 def gn_silu_forward(x, gamma, beta, G, eps=1e-5, silu=True, residual=False, y=None,
-                    mean=None, rstd=None, ws=None, stream=None):
+                    mean=None, rstd=None, mean_lo=None, keep_lo=True, ws=None, stream=None):
     """y = silu(group_norm(x)) [+ x] through soar_gn_silu_forward.
 
-    Returns (y, mean, rstd); mean/rstd are float32[N*G]."""
+    Returns (y, Stats(mean, rstd, mean_lo)); mean_lo is None when keep_lo is
+    False (the reference's fp32-mean-only saving)."""
     import torch
     N, C, HW = _nchw(x)
     for t, n in ((x, "x"), (gamma, "gamma"), (beta, "beta"), (y, "y"), (mean, "mean"),
-                 (rstd, "rstd")):
+                 (rstd, "rstd"), (mean_lo, "mean_lo")):
         _check_tensor(t, n)
+    new = lambda: torch.empty(N * G, dtype=torch.float32, device=x.device)
     y = torch.empty_like(x) if y is None else y
-    mean = torch.empty(N * G, dtype=torch.float32, device=x.device) if mean is None else mean
-    rstd = torch.empty(N * G, dtype=torch.float32, device=x.device) if rstd is None else rstd
+    mean = new() if mean is None else mean
+    rstd = new() if rstd is None else rstd
+    if keep_lo and mean_lo is None:
+        mean_lo = new()
     ws = workspace(N, C, HW, G, x.device) if ws is None else ws
     flags = (GN_SILU if silu else 0) | (GN_RESIDUAL if residual else 0)
     check(lib().soar_gn_silu_forward(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(y), _ptr(mean),
-                                     _ptr(rstd), N, C, HW, G, eps, flags, _ptr(ws),
-                                     ws.numel(), _stream(stream)))
-    return y, mean, rstd
+                                     _ptr(rstd), _ptr(mean_lo), N, C, HW, G, eps, flags,
+                                     _ptr(ws), ws.numel(), _stream(stream)))
+    return y, Stats(mean, rstd, mean_lo)
 
 
-def gn_silu_backward(dy, x, gamma, beta, mean, rstd, G, silu=True, residual=False,
+def gn_silu_backward(dy, x, gamma, beta, stats, G, silu=True, residual=False,
                      dx=None, dgamma=None, dbeta=None, want_dx=True, want_params=True,
                      accumulate_dx=False, ws=None, stream=None):
     """Backward through soar_gn_silu_backward; returns (dx, dgamma, dbeta).
 
+    `stats` is the Stats of the forward (or a (mean, rstd[, mean_lo]) tuple).
     dgamma/dbeta are accumulated into (fresh zeros when not given)."""
     import torch
+    mean, rstd = stats[0], stats[1]
+    mean_lo = stats[2] if len(stats) > 2 else None
     N, C, HW = _nchw(x)
     for t, n in ((dy, "dy"), (x, "x"), (gamma, "gamma"), (beta, "beta"), (dx, "dx"),
                  (dgamma, "dgamma"), (dbeta, "dbeta")):
@@ -233,7 +252,7 @@ def gn_silu_backward(dy, x, gamma, beta, mean, rstd, G, silu=True, residual=Fals
     flags = ((GN_SILU if silu else 0) | (GN_RESIDUAL if residual else 0)
              | (GN_ACCUMULATE_DX if accumulate_dx else 0))
     check(lib().soar_gn_silu_backward(_ptr(dy), _ptr(x), _ptr(gamma), _ptr(beta),
-                                      _ptr(mean), _ptr(rstd),
+                                      _ptr(mean), _ptr(rstd), _ptr(mean_lo),
                                       _ptr(dx) if want_dx else None,
                                       _ptr(dgamma) if want_params else None,
                                       _ptr(dbeta) if want_params else None,

@@ -29,17 +29,18 @@ def test_synth_library_exports(L):
 
 def test_workspace_bytes_is_host_arithmetic(L):
     # cfg 3: 64 planes x 128 chunks of 32768 floats -> 8192 partials of 16 B
-    # plus 64 plane sums of 16 B, each region 256-byte aligned.
     assert soar_gn.tune_get(soar_gn.TUNE_CHUNK) == 32768
-    assert soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) == 8192 * 16 + 1024
+    # plus 64 plane sums of 16 B plus 16 mean residuals of 4 B, each region
+    # 256-byte aligned.
+    assert soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) == 8192 * 16 + 1024 + 256
     # small planes get one block each (chunk clipped to the plane)
-    assert soar_gn.workspace_bytes(2, 6, 10, 3) == 256 + 256
+    assert soar_gn.workspace_bytes(2, 6, 10, 3) == 256 + 256 + 256
     assert soar_gn.workspace_bytes(0, 6, 10, 3) == 0
     assert soar_gn.workspace_bytes(1, 6, 10, 4) == 0  # C % G != 0
 
 
 def _fwd(L, N, C, HW, G, flags=1, eps=1e-5):
-    return L.soar_gn_silu_forward(None, None, None, None, None, None, N, C, HW, G, eps,
+    return L.soar_gn_silu_forward(None, None, None, None, None, None, None, N, C, HW, G, eps,
                                   flags, None, 0, None)
 
 
@@ -70,12 +71,15 @@ def test_backward_validation_without_gpu(L):
     f = L.soar_gn_silu_backward
     dummy = ctypes.c_void_p(0x1000)
     # dgamma without dbeta
-    rc = f(None, None, None, None, None, None, None, dummy, None, 1, 6, 16, 3, 1, None, 0, None)
+    rc = f(None, None, None, None, None, None, None, None, dummy, None, 1, 6, 16, 3, 1, None, 0,
+           None)
     assert rc == soar_gn.SOAR_EINVAL and "both" in soar_gn.last_error()
-    rc = f(None, None, None, None, None, None, None, None, None, 1, 6, 16, 3, 8, None, 0, None)
+    rc = f(None, None, None, None, None, None, None, None, None, None, 1, 6, 16, 3, 8, None, 0,
+           None)
     assert rc == soar_gn.SOAR_EINVAL  # unknown flag
     # nothing requested -> no-op
-    rc = f(None, None, None, None, None, None, None, None, None, 1, 6, 16, 3, 1, None, 0, None)
+    rc = f(None, None, None, None, None, None, None, None, None, None, 1, 6, 16, 3, 1, None, 0,
+           None)
     assert rc == soar_gn.SOAR_OK
 
 
@@ -85,7 +89,7 @@ def test_tuning_knobs(L):
     assert L.soar_gn_tune(soar_gn.TUNE_REVERSE, 2) == soar_gn.SOAR_EINVAL
     assert L.soar_gn_tune(99, 1) == soar_gn.SOAR_EINVAL
     soar_gn.tune(soar_gn.TUNE_CHUNK, 4096)
-    assert soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) == 65536 * 16 + 1024
+    assert soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) == 65536 * 16 + 1024 + 256
     soar_gn.tune(soar_gn.TUNE_CHUNK, old)
     assert soar_gn.tune_get(soar_gn.TUNE_CHUNK) == old
 

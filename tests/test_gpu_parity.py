@@ -67,11 +67,11 @@ def test_golden_fixture_forward_backward(gpu, name):
     x, dy = dev(g["x"]), dev(g["dy"])
     gamma = dev(g["gamma"]) if affine else None
     beta = dev(g["beta"]) if affine else None
-    y, mean, rstd = gpu.gn_silu_forward(x, gamma, beta, G, eps=1e-5, silu=bool(silu),
+    y, st = gpu.gn_silu_forward(x, gamma, beta, G, eps=1e-5, silu=bool(silu),
                                         residual=bool(res))
-    assert_stats(host(mean), host(rstd), g["mean"], g["rstd"], name)
+    assert_stats(host(st.mean), host(st.rstd), g["mean"], g["rstd"], name)
     assert_vals(host(y), g["y"], name + " y")
-    dx, dgamma, dbeta = gpu.gn_silu_backward(dy, x, gamma, beta, mean, rstd, G,
+    dx, dgamma, dbeta = gpu.gn_silu_backward(dy, x, gamma, beta, st, G,
                                              silu=bool(silu), residual=bool(res),
                                              want_params=bool(affine))
     assert_vals(host(dx), g["dx"], name + " dx")
@@ -86,11 +86,11 @@ def test_reference_known_answer(gpu):
     absolute of the CPU formula."""
     k = np.load(os.path.join(GOLDEN, "kat_test_operators.npz"))
     x = dev(k["x"])
-    y, mean, rstd = gpu.gn_silu_forward(x, dev(k["gamma"]), dev(k["beta"]), 4, eps=1e-5)
+    y, st = gpu.gn_silu_forward(x, dev(k["gamma"]), dev(k["beta"]), 4, eps=1e-5)
     yh = host(y).reshape(-1)
     assert np.abs(yh - k["y"].reshape(-1)).max() < 1e-4
     assert_vals(yh, k["y"], "kat y")
-    assert_stats(host(mean), host(rstd), k["mean"], k["rstd"], "kat")
+    assert_stats(host(st.mean), host(st.rstd), k["mean"], k["rstd"], "kat")
 
 
 # ------------------------------------------------------ seeded shapes vs oracle
@@ -135,11 +135,11 @@ def test_seeded_shapes_vs_oracle(gpu, oracle, shape, residual):
     dxt, dgt, dbt = oracle.gn_silu_bwd_f64(dy, x, gamma, beta, mt, rt, N, C, HW, G, True,
                                            residual)
     xd, dyd = dev(x).view(N, C, HW), dev(dy).view(N, C, HW)
-    y, mean, rstd = gpu.gn_silu_forward(xd, dev(gamma), dev(beta), G, eps=EPS,
+    y, st = gpu.gn_silu_forward(xd, dev(gamma), dev(beta), G, eps=EPS,
                                         residual=residual)
-    assert_stats(host(mean), host(rstd), mt, rt, "stats")
+    assert_stats(host(st.mean), host(st.rstd), mt, rt, "stats")
     assert_vals(host(y), yt, "y")
-    dx, dg, db = gpu.gn_silu_backward(dyd, xd, dev(gamma), dev(beta), mean, rstd, G,
+    dx, dg, db = gpu.gn_silu_backward(dyd, xd, dev(gamma), dev(beta), st, G,
                                       residual=residual)
     assert_vals(host(dx), dxt, "dx")
     assert_vals(host(dg), dgt, "dgamma")
@@ -153,9 +153,9 @@ def test_no_affine_and_plain_groupnorm(gpu, oracle, silu):
     yt, mt, rt = oracle.gn_silu_fwd_f64(x, None, None, N, C, HW, G, EPS, silu, False)
     dxt, dgt, dbt = oracle.gn_silu_bwd_f64(dy, x, None, None, mt, rt, N, C, HW, G, silu)
     xd, dyd = dev(x).view(N, C, HW), dev(dy).view(N, C, HW)
-    y, mean, rstd = gpu.gn_silu_forward(xd, None, None, G, eps=EPS, silu=silu)
+    y, st = gpu.gn_silu_forward(xd, None, None, G, eps=EPS, silu=silu)
     assert_vals(host(y), yt, "y")
-    dx, dg, db = gpu.gn_silu_backward(dyd, xd, None, None, mean, rstd, G, silu=silu)
+    dx, dg, db = gpu.gn_silu_backward(dyd, xd, None, None, st, G, silu=silu)
     assert_vals(host(dx), dxt, "dx")
     assert_vals(host(dg), dgt, "dgamma")
     assert_vals(host(db), dbt, "dbeta")
@@ -168,9 +168,9 @@ def test_constant_groups(gpu):
     x = torch.full((N, C, HW), 3.0, device="cuda")
     beta = torch.tensor([0.25, -0.5, 0.0, 1.0], device="cuda")
     gamma = torch.ones(C, device="cuda")
-    y, mean, rstd = gpu.gn_silu_forward(x, gamma, beta, G, eps=EPS)
-    assert np.all(host(mean) == 3.0)
-    np.testing.assert_allclose(host(rstd), np.float32(1 / np.sqrt(EPS)), rtol=1e-7)
+    y, st = gpu.gn_silu_forward(x, gamma, beta, G, eps=EPS)
+    assert np.all(host(st.mean) == 3.0)
+    np.testing.assert_allclose(host(st.rstd), np.float32(1 / np.sqrt(EPS)), rtol=1e-7)
     b = beta.cpu().numpy().astype(np.float64)
     want = b / (1 + np.exp(-b))
     assert_vals(host(y)[0, :, 7], want, "y")
@@ -196,12 +196,12 @@ def _full_size_check(gpu, oracle, N, C, HW, G, kind, seed, samples=200000):
     beta = torch.empty(C, device="cuda")
     gpu.synth_uniform(gamma, seed, 2, 0.5, 1.5)
     gpu.synth_normal(beta, seed, 3, 0.0, 0.1)
-    y, mean, rstd = gpu.gn_silu_forward(x, gamma, beta, G, eps=EPS)
-    dx, dg, db = gpu.gn_silu_backward(dy, x, gamma, beta, mean, rstd, G)
+    y, st = gpu.gn_silu_forward(x, gamma, beta, G, eps=EPS)
+    dx, dg, db = gpu.gn_silu_backward(dy, x, gamma, beta, st, G)
     # determinism: a second run is bitwise identical
-    y2, mean2, rstd2 = gpu.gn_silu_forward(x, gamma, beta, G, eps=EPS)
-    dx2, dg2, db2 = gpu.gn_silu_backward(dy, x, gamma, beta, mean2, rstd2, G)
-    assert torch.equal(y, y2) and torch.equal(mean, mean2) and torch.equal(rstd, rstd2)
+    y2, st2 = gpu.gn_silu_forward(x, gamma, beta, G, eps=EPS)
+    dx2, dg2, db2 = gpu.gn_silu_backward(dy, x, gamma, beta, st2, G)
+    assert torch.equal(y, y2) and all(torch.equal(a, b) for a, b in zip(st, st2))
     assert torch.equal(dx, dx2) and torch.equal(dg, dg2) and torch.equal(db, db2)
     # size-independent property: sum of dx over each unit vanishes
     dxu = dx.view(N * G, -1).double()
@@ -210,7 +210,7 @@ def _full_size_check(gpu, oracle, N, C, HW, G, kind, seed, samples=200000):
     gh, bh = host(gamma), host(beta)
     _, mt, rt = oracle.gn_silu_fwd_f64(xh_, gh, bh, N, C, HW, G, EPS, True, False,
                                        want_y=False)
-    assert_stats(host(mean), host(rstd), mt, rt, "full stats")
+    assert_stats(host(st.mean), host(st.rstd), mt, rt, "full stats")
     _, dgt, dbt = oracle.gn_silu_bwd_f64(dyh, xh_, gh, bh, mt, rt, N, C, HW, G, want_dx=False)
     assert_vals(host(dg), dgt, "full dgamma")
     assert_vals(host(db), dbt, "full dbeta")
@@ -264,10 +264,10 @@ def test_accumulate_semantics(gpu, oracle):
     N, C, HW, G = 1, 8, 8192, 2
     x, gamma, beta, dy = make_inputs(oracle, N, C, HW, G, "normal", 5)
     xd, dyd, gd, bd = dev(x).view(N, C, HW), dev(dy).view(N, C, HW), dev(gamma), dev(beta)
-    y, mean, rstd = gpu.gn_silu_forward(xd, gd, bd, G, eps=EPS)
-    dx1, dg, db = gpu.gn_silu_backward(dyd, xd, gd, bd, mean, rstd, G)
+    y, st = gpu.gn_silu_forward(xd, gd, bd, G, eps=EPS)
+    dx1, dg, db = gpu.gn_silu_backward(dyd, xd, gd, bd, st, G)
     base = dev(np.full(N * C * HW, 0.5, np.float32)).view(N, C, HW)
-    dx2, dg, db = gpu.gn_silu_backward(dyd, xd, gd, bd, mean, rstd, G, dx=base,
+    dx2, dg, db = gpu.gn_silu_backward(dyd, xd, gd, bd, st, G, dx=base,
                                        dgamma=dg, dbeta=db, accumulate_dx=True)
     np.testing.assert_allclose(host(dx2), host(dx1) + 0.5, rtol=0, atol=2e-7)
     _, dgt, dbt = oracle.gn_silu_bwd_f64(dy, x, gamma, beta, *oracle.gn_silu_fwd_f64(
@@ -275,10 +275,10 @@ def test_accumulate_semantics(gpu, oracle):
     assert_vals(host(dg), 2 * dgt, "dgamma x2")
     assert_vals(host(db), 2 * dbt, "dbeta x2")
     # only parameters / only dx
-    none_dx, dgp, dbp = gpu.gn_silu_backward(dyd, xd, gd, bd, mean, rstd, G, want_dx=False)
+    none_dx, dgp, dbp = gpu.gn_silu_backward(dyd, xd, gd, bd, st, G, want_dx=False)
     assert none_dx is None
     assert_vals(host(dgp), dgt, "dgamma only")
-    dxo, ng, nb = gpu.gn_silu_backward(dyd, xd, gd, bd, mean, rstd, G, want_params=False)
+    dxo, ng, nb = gpu.gn_silu_backward(dyd, xd, gd, bd, st, G, want_params=False)
     assert ng is None and nb is None
     assert torch_equal(dxo, dx1)
 
@@ -298,11 +298,11 @@ def test_misaligned_pointers_take_scalar_path(gpu, oracle):
     dbuf = torch.empty_like(buf)
     dbuf[1:] = dev(dy)
     dyo = dbuf[1:].view(N, C, HW)
-    y, mean, rstd = gpu.gn_silu_forward(xo, dev(gamma), dev(beta), G, eps=EPS)
+    y, st = gpu.gn_silu_forward(xo, dev(gamma), dev(beta), G, eps=EPS)
     yt, mt, rt = oracle.gn_silu_fwd_f64(x, gamma, beta, N, C, HW, G, EPS)
-    assert_stats(host(mean), host(rstd), mt, rt)
+    assert_stats(host(st.mean), host(st.rstd), mt, rt)
     assert_vals(host(y), yt, "y")
-    dx, dg, db = gpu.gn_silu_backward(dyo, xo, dev(gamma), dev(beta), mean, rstd, G)
+    dx, dg, db = gpu.gn_silu_backward(dyo, xo, dev(gamma), dev(beta), st, G)
     dxt, dgt, dbt = oracle.gn_silu_bwd_f64(dy, x, gamma, beta, mt, rt, N, C, HW, G)
     assert_vals(host(dx), dxt, "dx")
     assert_vals(host(dg), dgt, "dgamma")
@@ -320,16 +320,16 @@ def test_errors_are_statuses_not_faults(gpu):
     P = lambda t: ctypes.c_void_p(t.data_ptr())
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     # workspace one byte too small
-    rc = L.soar_gn_silu_forward(P(x), None, None, P(y), P(mean), P(rstd), N, C, HW, G, EPS,
+    rc = L.soar_gn_silu_forward(P(x), None, None, P(y), P(mean), P(rstd), None, N, C, HW, G, EPS,
                                 1, P(ws), gpu.workspace_bytes(N, C, HW, G) - 1, s)
     assert rc == gpu.SOAR_EINVAL and "workspace" in gpu.last_error()
     # a host pointer is refused before any launch
     hx = np.zeros(N * C * HW, np.float32)
     rc = L.soar_gn_silu_forward(ctypes.c_void_p(hx.ctypes.data), None, None, P(y), P(mean),
-                                P(rstd), N, C, HW, G, EPS, 1, P(ws), ws.numel(), s)
+                                P(rstd), None, N, C, HW, G, EPS, 1, P(ws), ws.numel(), s)
     assert rc == gpu.SOAR_EINVAL and "not device memory" in gpu.last_error()
     # C % G
-    rc = L.soar_gn_silu_forward(P(x), None, None, P(y), P(mean), P(rstd), N, C, HW, 3, EPS,
+    rc = L.soar_gn_silu_forward(P(x), None, None, P(y), P(mean), P(rstd), None, N, C, HW, 3, EPS,
                                 1, P(ws), ws.numel(), s)
     assert rc == gpu.SOAR_EINVAL
     torch.cuda.synchronize()
@@ -476,8 +476,8 @@ def test_kernel_timing_records(gpu):
     x = torch.randn(1, 8, 65536, device="cuda")
     gpu.prof_enable(True)
     try:
-        y, mean, rstd = gpu.gn_silu_forward(x, None, None, 2)
-        gpu.gn_silu_backward(torch.randn_like(x), x, None, None, mean, rstd, 2)
+        y, st = gpu.gn_silu_forward(x, None, None, 2)
+        gpu.gn_silu_backward(torch.randn_like(x), x, None, None, st, 2)
         recs = {r["kernel"]: r for r in gpu.prof_summary()}
     finally:
         gpu.prof_enable(False)
