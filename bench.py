@@ -39,9 +39,11 @@ CONFIGS = {
 }
 SEED_OF = {"cfg2_fwd": SEED + 2, "cfg3": SEED + 3, "cfg4_chain": SEED + 4, "cfg5": SEED + 5}
 
-# algorithmic tensor passes (units of T) per kernel launch
+# algorithmic tensor passes (units of T) each kernel makes per block of the
+# step, summed over its launches (a kernel runs once per unit batch)
 PASSES = {"gn_stats_partial": 1, "gn_silu_apply": 2, "gn_silu_bwd_reduce": 2,
-          "gn_silu_bwd_dx": 3, "gn_stats_finish": 0, "gn_bwd_finish": 0}
+          "gn_silu_bwd_dx": 3, "gn_stats_finish": 0, "gn_bwd_finish": 0,
+          "gn_param_finish": 0}
 
 
 def parse():
@@ -207,23 +209,26 @@ def main():
 
     roofline = None
     kinfo = {}
+    blocks = len(step.params)
     for k in kernels:
         avg = k["total_ms"] / k["launches"]
-        passes_k = PASSES.get(k["kernel"], 0)
-        kinfo[k["kernel"]] = {"launches_per_step": k["launches"] / args.steps,
-                              "avg_ms": round(avg, 5),
-                              "GBps": round(passes_k * step.T / (avg * 1e-3) / 1e9, 1)
-                              if passes_k else None}
+        per_step = k["launches"] / args.steps
+        # bytes of one launch: the kernel's passes over the tensor, split
+        # evenly over its launches (equal-sized unit batches)
+        per_launch = PASSES.get(k["kernel"], 0) * step.T * blocks / per_step
+        kinfo[k["kernel"]] = {"launches_per_step": per_step, "avg_launch_ms": round(avg, 5),
+                              "bytes_per_launch": int(per_launch),
+                              "GBps": round(per_launch / (avg * 1e-3) / 1e9, 1)
+                              if per_launch else None}
     if kernels:
         dom = max(kernels, key=lambda k: k["total_ms"])
-        avg = dom["total_ms"] / dom["launches"]
-        per_launch = PASSES.get(dom["kernel"], 0) * step.T
-        achieved = per_launch / (avg * 1e-3) / 1e9
+        kd = kinfo[dom["kernel"]]
+        achieved = kd["GBps"]
         tr = traffic_from_profiles(args.config)
-        roofline = {"bound": "hbm", "kernel": dom["kernel"], "achieved": round(achieved, 1),
+        roofline = {"bound": "hbm", "kernel": dom["kernel"], "achieved": achieved,
                     "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
-                    "algorithmic_bytes_per_launch": per_launch,
-                    "avg_launch_ms": round(avg, 5),
+                    "algorithmic_bytes_per_launch": kd["bytes_per_launch"],
+                    "avg_launch_ms": kd["avg_launch_ms"],
                     "traffic": tr.get(dom["kernel"]) if tr else None}
 
     cpu = None

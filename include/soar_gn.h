@@ -61,8 +61,10 @@ SOAR_API int soar_is_device_available(void);
 /* ---- fused GroupNorm(+SiLU) ------------------------------------------- */
 
 /* Bytes of device workspace the fused entry points need for this shape
- * (0 for an empty tensor).  The workspace holds per-chunk partial moments
- * and per-plane sums; it carries nothing between calls. */
+ * (0 for an empty tensor).  The workspace holds per-chunk partial moments,
+ * per-plane and per-unit sums and per-unit tickets; it carries nothing
+ * between calls, and two calls that overlap in time on the device must not
+ * share one. */
 SOAR_API size_t soar_gn_workspace_bytes(int64_t N, int64_t C, int64_t HW,
                                         int64_t G);
 
@@ -209,9 +211,10 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
 /* ---- tuning (no counterpart in the reference) ------------------------- */
 /* Launch-shape knobs of the streaming kernels, set process-wide; the
  * defaults are the measured best on MI355X.  Values are validated. */
-#define SOAR_TUNE_CHUNK 1   /* elements per block-chunk (multiple of 1024) */
-#define SOAR_TUNE_REVERSE 2 /* 1: second passes walk chunks in reverse    */
-#define SOAR_TUNE_NT_STORE 3 /* 1: non-temporal stores for y / dx         */
+#define SOAR_TUNE_CHUNK 1    /* elements per block-chunk (multiple of 1024) */
+#define SOAR_TUNE_REVERSE 2  /* 1: second passes walk chunks in reverse    */
+#define SOAR_TUNE_NT_STORE 3 /* 1: non-temporal stores for y / dx          */
+#define SOAR_TUNE_BATCH_MB 4 /* MiB per two-pass batch, 0 = whole tensor   */
 SOAR_API int soar_gn_tune(int key, int64_t value);
 SOAR_API int64_t soar_gn_tune_get(int key);
 

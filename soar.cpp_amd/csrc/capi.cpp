@@ -572,6 +572,11 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
             if (value != 0 && value != 1) return fail(SOAR_EINVAL, "nt_store must be 0 or 1");
             g_tune.nt_store = (int)value;
             return ok();
+        case SOAR_TUNE_BATCH_MB:
+            if (value < 0 || value > (1 << 20))
+                return fail(SOAR_EINVAL, "batch_mb must be in [0, 2^20]");
+            g_tune.batch_mb = value;
+            return ok();
         default:
             return fail(SOAR_EINVAL, "unknown tuning key %d", key);
     }
@@ -583,6 +588,7 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
         case SOAR_TUNE_CHUNK: return g_tune.chunk;
         case SOAR_TUNE_REVERSE: return g_tune.reverse;
         case SOAR_TUNE_NT_STORE: return g_tune.nt_store;
+        case SOAR_TUNE_BATCH_MB: return g_tune.batch_mb;
         default: return -1;
     }
 }

@@ -9,23 +9,42 @@
 namespace soar {
 namespace gn {
 
-// Launch geometry of the four streaming kernels.  Every (n, c) plane of HW
+// Launch geometry of the streaming kernels.  Every (n, c) plane of HW
 // floats is cut into `cpp` chunks of `chunk` floats (the last one ragged);
 // one 256-thread block streams one chunk.  Blocks are numbered
-// plane * cpp + chunk_in_plane, so a unit (n, g) owns a contiguous range.
+// plane * cpp + chunk_in_plane, so unit u = (n, g) owns the contiguous
+// block range [u*cpg*cpp, (u+1)*cpg*cpp).
+//
+// Units are processed in batches: both passes of a batch (statistics then
+// apply; reduction then dx) run before the next batch starts, so the second
+// pass re-reads data the first pass just brought into the 256 MB MALL
+// instead of streaming the whole tensor from HBM twice.
 struct Plan {
     int64_t N = 0, C = 0, HW = 0, G = 0, cpg = 0;
-    int64_t planes = 0;  // N * C
-    int64_t chunk = 0;   // floats per block-chunk
-    int64_t cpp = 0;     // chunks per plane
-    int64_t blocks = 0;  // planes * cpp
-    bool vec4 = false;   // float4 path (HW % 4 == 0 and 16-byte pointers)
+    int64_t planes = 0;      // N * C
+    int64_t units = 0;       // N * G
+    int64_t chunk = 0;       // floats per block-chunk
+    int64_t cpp = 0;         // chunks per plane
+    int64_t blocks = 0;      // planes * cpp
+    int64_t upb_fwd = 0;     // units per forward batch
+    int64_t upb_bwd = 0;     // units per backward batch
+    bool vec4 = false;       // float4 path (HW % 4 == 0 and 16-byte pointers)
 };
 
+// Defaults measured on MI355X at 1x64x2048^2, fwd+bwd per step:
+//   chunk 8192, forward order, cached stores            1.541 ms
+//   + reverse order + non-temporal stores                1.469 ms
+//   chunk 16384 / 32768                                  +1.5% / +3%
+//   unit batches of 64 / 128 / 256 / 512 MiB             1.635 / 1.589 /
+//                                                        1.536 / 1.511 ms
+// (each extra pair of launches costs ~2.7 us, more than the MALL saves).
 struct Tuning {
-    int64_t chunk = 32768;  // floats per block-chunk, multiple of 1024
-    int reverse = 0;        // second passes walk blocks in reverse order
-    int nt_store = 1;       // non-temporal stores of y / dx
+    int64_t chunk = 8192;     // floats per block-chunk, multiple of 1024
+    int reverse = 1;          // second passes walk a batch's blocks in
+                              // reverse, starting on what was read last
+    int nt_store = 1;         // non-temporal stores of y / dx
+    int64_t batch_mb = 0;     // MiB read by the first pass of a batch
+                              // (0: the whole tensor is one batch)
 };
 
 constexpr int kThreads = 256;

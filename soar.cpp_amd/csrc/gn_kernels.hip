@@ -4,16 +4,26 @@
 // kernel is a streaming pass built for CDNA4's memory system:
 //   * one 256-thread block (four wave64s) streams one contiguous chunk of
 //     one (n, c) plane with 128-bit loads, four in flight per thread;
-//   * per-block partial results go to a small workspace and a tiny finish
-//     kernel combines them in float64 in a fixed order, so results are
-//     bitwise reproducible and no float atomics are used;
+//   * per-block partial results go to a small workspace and are combined
+//     in float64 in a fixed order by one "finish" block per unit, so results
+//     are bitwise reproducible and no atomics or fences are used;
+//   * the second pass (apply / dx) walks the chunks in reverse, so it
+//     starts on what the first pass read last, still in the 256 MB MALL;
+//   * units can be processed in batches (a tuning knob, off by default):
+//     a batch's second pass then runs right after the first pass of the
+//     next batch.  The finish blocks of batch b are the first blocks of the
+//     first-pass kernel of batch b+1 (a kernel boundary makes batch b's
+//     partials visible to them), so a batch costs two launches;
 //   * per-block coefficients (mean, rstd, gamma, beta, S1, S2) are uniform
 //     across the block and live in scalar registers;
 //   * SiLU is recomputed in the backward from x and the saved statistics
 //     instead of storing the pre-activation.
 //
-// Forward  (3 tensor passes):  k_stats_partial -> k_stats_finish -> k_apply
-// Backward (5 tensor passes):  k_bwd_reduce -> k_bwd_finish -> k_bwd_dx
+// Forward  (3 tensor passes): per batch k_stats (finish of the previous
+//                             batch + partials), k_apply of the previous batch
+// Backward (5 tensor passes): per batch k_bwd_reduce (finish of the previous
+//                             batch + partials), k_bwd_dx of the previous
+//                             batch; then k_param_finish for dgamma/dbeta
 //
 // Reference algorithms (pomagrenate/soar.cpp):
 //   statistics  shaders/group_norm_stats.comp:25-73 (sum/sumsq, one
@@ -31,8 +41,9 @@
 //               normalization_kernels.cu:116-249.  Here one reduction pass
 //               gives per-plane sum(dz) and sum(dz*xhat); dgamma/dbeta and
 //               the per-group S1/S2 both derive from them.
-#include "gn_internal.hpp"
+#include <algorithm>
 
+#include "gn_internal.hpp"
 #include "soar_gn.h"
 
 namespace soar {
@@ -112,7 +123,8 @@ __device__ __forceinline__ T wave_sum(T v) {
     return v;
 }
 
-// Sum of (a, b) over the block in a fixed order; valid in thread 0.
+// Sum of (a, b) over the block in a fixed order; valid in thread 0.  Ends
+// with the block synchronised.
 template <typename T>
 __device__ __forceinline__ void block_sum2(T& a, T& b, T* lds /*[2*kWaves]*/) {
     a = wave_sum(a);
@@ -150,6 +162,11 @@ __device__ __forceinline__ Chunk chunk_of(int64_t b, int64_t HW, int64_t chunk,
     return k;
 }
 
+// Block index of this block inside its batch [block0, block0 + nb).
+__device__ __forceinline__ int64_t batch_block(int64_t block0, int64_t nb, int reverse) {
+    return block0 + (reverse ? nb - 1 - (int64_t)blockIdx.x : (int64_t)blockIdx.x);
+}
+
 template <bool NT>
 __device__ __forceinline__ void store4(f4* p, f4 v) {
     if (NT)
@@ -167,20 +184,64 @@ __device__ __forceinline__ void store1(float* p, float v) {
 }
 
 // ======================================================================
-// Forward pass 1: per-chunk moments.
-// Each thread shifts its elements by its own first element K (so sums of
-// d = x - K stay near the data's spread even when |mean| >> std), keeps
-// fp32 sums of d and d*d in four independent lanes of accumulation, then
-// converts to a float64 (n, mean, M2) triple that is Chan-combined over
-// the block.  part[b] = (mean, M2) of chunk b; its count is implied by the
-// chunk geometry.
+// Forward pass 1: unit statistics of the previous batch, then per-chunk
+// moments of this batch.
+//
+// Chunk blocks: each thread shifts its elements by its own first element K
+// (so sums of d = x - K stay near the data's spread even when |mean| >>
+// std), keeps fp32 sums of d and d*d in four independent lanes of
+// accumulation, then converts to a float64 (n, mean, M2) triple that is
+// Chan-combined over the block.  part[b] = (mean, M2) of chunk b; its count
+// is implied by the chunk geometry.
+//
+// Finish blocks (blockIdx.x < fin_nu): one per unit of the previous batch;
+// combines the unit's cpg*cpp partials in a fixed order and writes mean and
+// rstd.  The mean is also kept as hi + lo (hi = fp32 mean, lo = its fp32
+// rounding residual): when std << |mean| the rounding of hi alone, times
+// rstd, would shift xhat by up to ulp(mean)/2 * rstd, far above the 1e-4
+// output tolerance.  lo goes to the caller's optional mean_lo (for the
+// backward) and to the workspace (for the apply kernel of the same call).
 // ======================================================================
+__device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
+                                  float* __restrict__ mean, float* __restrict__ rstd,
+                                  float* __restrict__ mean_lo, float* __restrict__ lo_ws,
+                                  int64_t HW, int64_t chunk, int64_t cpp, int64_t cpg,
+                                  float eps, Moments* lds) {
+    const int64_t P = cpg * cpp;  // chunk blocks per unit
+    const int64_t first = u * P;
+    Moments um{0.0, 0.0, 0.0};
+    for (int64_t j = threadIdx.x; j < P; j += kThreads) {
+        const int64_t k = j % cpp;
+        const double2 v = part[first + j];
+        Moments o{(double)min(chunk, HW - k * chunk), v.x, v.y};
+        um = chan(um, o);
+    }
+    Moments ur = block_reduce(um, lds);
+    if (threadIdx.x == 0) {
+        const double var = ur.n > 0.0 ? fmax(ur.m2 / ur.n, 0.0) : 0.0;
+        const float hi = (float)ur.mean;
+        const float lo = (float)(ur.mean - (double)hi);
+        mean[u] = hi;
+        rstd[u] = (float)(1.0 / sqrt(var + (double)eps));
+        lo_ws[u] = lo;
+        if (mean_lo) mean_lo[u] = lo;
+    }
+}
+
 template <bool VEC>
-__global__ __launch_bounds__(kThreads) void k_stats_partial(
-    const float* __restrict__ x, double2* __restrict__ part, int64_t HW,
-    int64_t chunk, int64_t cpp) {
+__global__ __launch_bounds__(kThreads) void k_stats(
+    const float* __restrict__ x, double2* __restrict__ part, float* __restrict__ mean,
+    float* __restrict__ rstd, float* __restrict__ mean_lo, float* __restrict__ lo_ws,
+    int64_t HW, int64_t chunk, int64_t cpp, int64_t cpg, int64_t fin_u0, int64_t fin_nu,
+    int64_t block0, float eps) {
     __shared__ Moments lds[kWaves];
-    const Chunk ck = chunk_of(blockIdx.x, HW, chunk, cpp);
+    if ((int64_t)blockIdx.x < fin_nu) {
+        finish_stats_unit(fin_u0 + blockIdx.x, part, mean, rstd, mean_lo, lo_ws, HW, chunk,
+                          cpp, cpg, eps, lds);
+        return;
+    }
+    const int64_t b = block0 + (int64_t)blockIdx.x - fin_nu;
+    const Chunk ck = chunk_of(b, HW, chunk, cpp);
     const float* p = x + ck.plane * HW + ck.off;
     const int t = threadIdx.x;
 
@@ -210,10 +271,10 @@ __global__ __launch_bounds__(kThreads) void k_stats_partial(
         q2 = fmaf(d2, d2, q2); q3 = fmaf(d3, d3, q3);                    \
     }
         for (; i + 3 * kThreads < n4; i += 4 * kThreads) {
-            f4 a = p4[i], b = p4[i + kThreads], c = p4[i + 2 * kThreads],
+            f4 a = p4[i], b4 = p4[i + kThreads], c = p4[i + 2 * kThreads],
                d = p4[i + 3 * kThreads];
             SOAR_ACC4(a);
-            SOAR_ACC4(b);
+            SOAR_ACC4(b4);
             SOAR_ACC4(c);
             SOAR_ACC4(d);
         }
@@ -251,43 +312,7 @@ __global__ __launch_bounds__(kThreads) void k_stats_partial(
         m.m2 = fmax(q - s * s / m.n, 0.0);
     }
     Moments r = block_reduce(m, lds);
-    if (t == 0) part[blockIdx.x] = make_double2(r.mean, r.m2);
-}
-
-// Forward finish: one block per unit (n, g) combines its cpg*cpp chunk
-// partials in a fixed order and writes mean and rstd.  The mean is also
-// kept as hi + lo (hi = fp32 mean, lo = the fp32 rounding residual): when
-// std << |mean| the residual of hi alone, times rstd, would shift xhat by
-// up to ulp(mean)/2 * rstd, far above the 1e-4 output tolerance.  The lo
-// part goes to the caller's optional mean_lo (for the backward) and to the
-// workspace (for the apply kernel of the same call).
-__global__ __launch_bounds__(kThreads) void k_stats_finish(
-    const double2* __restrict__ part, float* __restrict__ mean,
-    float* __restrict__ rstd, float* __restrict__ mean_lo,
-    float* __restrict__ lo_ws, int64_t C, int64_t G, int64_t cpg, int64_t HW,
-    int64_t chunk, int64_t cpp, float eps) {
-    __shared__ Moments lds[kWaves];
-    const int64_t u = blockIdx.x;
-    const int64_t n = u / G, g = u - n * G;
-    const int64_t first = (n * C + g * cpg) * cpp;
-    const int64_t P = cpg * cpp;
-    Moments m{0.0, 0.0, 0.0};
-    for (int64_t j = threadIdx.x; j < P; j += kThreads) {
-        const int64_t k = j % cpp;
-        const double2 v = part[first + j];
-        Moments o{(double)min(chunk, HW - k * chunk), v.x, v.y};
-        m = chan(m, o);
-    }
-    Moments r = block_reduce(m, lds);
-    if (threadIdx.x == 0) {
-        const double var = r.n > 0.0 ? fmax(r.m2 / r.n, 0.0) : 0.0;
-        const float hi = (float)r.mean;
-        const float lo = (float)(r.mean - (double)hi);
-        mean[u] = hi;
-        rstd[u] = (float)(1.0 / sqrt(var + (double)eps));
-        lo_ws[u] = lo;
-        if (mean_lo) mean_lo[u] = lo;
-    }
+    if (t == 0) part[b] = make_double2(r.mean, r.m2);
 }
 
 // Per-block coefficients of plane `plane`: xhat = fma(x - mu, r, e) with
@@ -324,8 +349,8 @@ __global__ __launch_bounds__(kThreads) void k_apply(
     const float* __restrict__ beta, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ mean_lo,
     float* __restrict__ y, int64_t C, int64_t G, int64_t cpg, int64_t HW,
-    int64_t chunk, int64_t cpp, int64_t nblocks, int reverse) {
-    const int64_t b = reverse ? nblocks - 1 - (int64_t)blockIdx.x : (int64_t)blockIdx.x;
+    int64_t chunk, int64_t cpp, int64_t block0, int64_t nb, int reverse) {
+    const int64_t b = batch_block(block0, nb, reverse);
     const Chunk ck = chunk_of(b, HW, chunk, cpp);
     const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
     // z = gamma*xhat + beta = (x - mu)*(gamma*r) + (beta + gamma*e)
@@ -367,18 +392,57 @@ __global__ __launch_bounds__(kThreads) void k_apply(
 }
 
 // ======================================================================
-// Backward pass 1: per-chunk sum(dz) and sum(dz * xhat), dz the gradient
-// at the GroupNorm output (SiLU derivative recomputed from x).
+// Backward pass 1: finish of the previous batch's units, then per-chunk
+// sum(dz) and sum(dz * xhat) of this batch, dz the gradient at the
+// GroupNorm output (SiLU derivative recomputed from x).
+// A finish block sums each plane of its unit over the plane's chunks
+// (plane_sums, float64, fixed order) and forms
+//   S1 = sum_c gamma_c * sum dz,   S2 = sum_c gamma_c * sum dz*xhat.
 // ======================================================================
+__device__ void finish_bwd_unit(int64_t u, const double2* __restrict__ part,
+                                const float* __restrict__ gamma,
+                                double2* __restrict__ plane_sums,
+                                double2* __restrict__ unit_sums, int64_t C, int64_t cpp,
+                                int64_t cpg, double* lds) {
+    double S1 = 0.0, S2 = 0.0;  // meaningful in thread 0
+    for (int64_t j = 0; j < cpg; ++j) {
+        const int64_t plane = u * cpg + j;
+        const double2* pp = part + plane * cpp;
+        double A = 0.0, B = 0.0;
+        for (int64_t q = threadIdx.x; q < cpp; q += kThreads) {
+            const double2 v = pp[q];
+            A += v.x;
+            B += v.y;
+        }
+        block_sum2(A, B, lds);
+        if (threadIdx.x == 0) {
+            plane_sums[plane] = make_double2(A, B);
+            const double gj = gamma ? (double)gamma[plane % C] : 1.0;
+            S1 += gj * A;
+            S2 += gj * B;
+        }
+    }
+    if (threadIdx.x == 0) unit_sums[u] = make_double2(S1, S2);
+}
+
 template <bool VEC, bool SILU>
 __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ gamma, const float* __restrict__ beta,
     const float* __restrict__ mean, const float* __restrict__ rstd,
-    const float* __restrict__ mean_lo, double2* __restrict__ part, int64_t C,
-    int64_t G, int64_t cpg, int64_t HW, int64_t chunk, int64_t cpp) {
+    const float* __restrict__ mean_lo, double2* __restrict__ part,
+    double2* __restrict__ plane_sums, double2* __restrict__ unit_sums, int64_t C, int64_t G,
+    int64_t cpg, int64_t HW, int64_t chunk, int64_t cpp, int64_t fin_u0, int64_t fin_nu,
+    int64_t block0) {
     __shared__ float lds[2 * kWaves];
-    const Chunk ck = chunk_of(blockIdx.x, HW, chunk, cpp);
+    __shared__ double ldsd[2 * kWaves];
+    if ((int64_t)blockIdx.x < fin_nu) {
+        finish_bwd_unit(fin_u0 + blockIdx.x, part, gamma, plane_sums, unit_sums, C, cpp, cpg,
+                        ldsd);
+        return;
+    }
+    const int64_t b = block0 + (int64_t)blockIdx.x - fin_nu;
+    const Chunk ck = chunk_of(b, HW, chunk, cpp);
     const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
     const float mu = k.mu, r = k.r, e = k.e, gm = k.gm, bt = k.bt;
     const int64_t base = ck.plane * HW + ck.off;
@@ -415,38 +479,25 @@ __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
     }
     float sa = sa0 + sa1, sb = sb0 + sb1;
     block_sum2(sa, sb, lds);
-    if (t == 0) part[blockIdx.x] = make_double2((double)sa, (double)sb);
+    if (t == 0) part[b] = make_double2((double)sa, (double)sb);
 }
 
-// Backward finish: one block per channel c sums the chunk partials of every
-// plane (n, c) in float64, stores the per-plane sums for the dx pass and
-// accumulates dbeta[c] += sum_n A, dgamma[c] += sum_n B.
-__global__ __launch_bounds__(kThreads) void k_bwd_finish(
-    const double2* __restrict__ part, double2* __restrict__ plane_sums,
-    float* __restrict__ dgamma, float* __restrict__ dbeta, int64_t N,
-    int64_t C, int64_t cpp) {
-    __shared__ double lds[2 * kWaves];
-    const int64_t c = blockIdx.x;
-    double tot_a = 0.0, tot_b = 0.0;
+// dgamma[c] += sum_n sum dz*xhat, dbeta[c] += sum_n sum dz, in sample
+// order (the reference accumulates parameter gradients per sample,
+// tensor.cpp:173-192).
+__global__ void k_param_finish(const double2* __restrict__ plane_sums,
+                               float* __restrict__ dgamma, float* __restrict__ dbeta,
+                               int64_t N, int64_t C) {
+    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= C) return;
+    double a = 0.0, b = 0.0;
     for (int64_t n = 0; n < N; ++n) {
-        const int64_t plane = n * C + c;
-        const double2* pp = part + plane * cpp;
-        double a = 0.0, b = 0.0;
-        for (int64_t j = threadIdx.x; j < cpp; j += kThreads) {
-            a += pp[j].x;
-            b += pp[j].y;
-        }
-        block_sum2(a, b, lds);
-        if (threadIdx.x == 0) {
-            plane_sums[plane] = make_double2(a, b);
-            tot_a += a;
-            tot_b += b;
-        }
+        const double2 v = plane_sums[n * C + c];
+        a += v.x;
+        b += v.y;
     }
-    if (threadIdx.x == 0 && dbeta) {
-        dbeta[c] = (float)((double)dbeta[c] + tot_a);
-        dgamma[c] = (float)((double)dgamma[c] + tot_b);
-    }
+    dbeta[c] = (float)((double)dbeta[c] + a);
+    dgamma[c] = (float)((double)dgamma[c] + b);
 }
 
 // ======================================================================
@@ -458,25 +509,18 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ gamma, const float* __restrict__ beta,
     const float* __restrict__ mean, const float* __restrict__ rstd,
-    const float* __restrict__ mean_lo, const double2* __restrict__ plane_sums,
+    const float* __restrict__ mean_lo, const double2* __restrict__ unit_sums,
     float* __restrict__ dx, int64_t C, int64_t G, int64_t cpg, int64_t HW,
-    int64_t chunk, int64_t cpp, int64_t nblocks, int reverse) {
-    const int64_t b = reverse ? nblocks - 1 - (int64_t)blockIdx.x : (int64_t)blockIdx.x;
+    int64_t chunk, int64_t cpp, int64_t block0, int64_t nb, int reverse) {
+    const int64_t b = batch_block(block0, nb, reverse);
     const Chunk ck = chunk_of(b, HW, chunk, cpp);
     const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
-    double S1 = 0.0, S2 = 0.0;
-    const int64_t c0 = (k.c / cpg) * cpg;
-    for (int64_t j = 0; j < cpg; ++j) {
-        const double gj = gamma ? (double)gamma[c0 + j] : 1.0;
-        const double2 ps = plane_sums[k.n * C + c0 + j];
-        S1 += gj * ps.x;
-        S2 += gj * ps.y;
-    }
+    const double2 S = unit_sums[k.u];
     const double Md = (double)(cpg * HW);
     const float mu = k.mu, r = k.r, e = k.e, gm = k.gm, bt = k.bt;
     const float A = gm * r;
-    const float B = (float)(-(double)r * S1 / Md);
-    const float D = (float)(-(double)r * S2 / Md);
+    const float B = (float)(-(double)r * S.x / Md);
+    const float D = (float)(-(double)r * S.y / Md);
     const int64_t base = ck.plane * HW + ck.off;
     const int t = threadIdx.x;
     auto f = [&](float g, float v, float old) {
@@ -527,13 +571,35 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(
 
 // ---- host-side dispatch over the template flags -------------------------
 
+struct WsView {
+    double2* part;        // [blocks]
+    double2* plane_sums;  // [planes]
+    double2* unit_sums;   // [units]
+    float* lo;            // [units]
+};
+
+inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+WsView ws_view(const Plan& p, void* ws) {
+    char* c = static_cast<char*>(ws);
+    WsView v;
+    v.part = reinterpret_cast<double2*>(c);
+    c += align256(sizeof(double2) * (size_t)p.blocks);
+    v.plane_sums = reinterpret_cast<double2*>(c);
+    c += align256(sizeof(double2) * (size_t)p.planes);
+    v.unit_sums = reinterpret_cast<double2*>(c);
+    c += align256(sizeof(double2) * (size_t)p.units);
+    v.lo = reinterpret_cast<float*>(c);
+    return v;
+}
+
 template <bool VEC>
-void apply_dispatch(bool silu, bool res, bool nt, dim3 grid, hipStream_t s,
-                    const Plan& p, const FwdArgs& a, const float* lo_ws, int reverse) {
-#define SOAR_APPLY(S, R, N)                                                  \
-    k_apply<VEC, S, R, N><<<grid, kThreads, 0, s>>>(                         \
-        a.x, a.gamma, a.beta, a.mean, a.rstd, lo_ws, a.y, p.C, p.G, p.cpg,   \
-        p.HW, p.chunk, p.cpp, p.blocks, reverse)
+void apply_dispatch(bool silu, bool res, bool nt, dim3 grid, hipStream_t s, const Plan& p,
+                    const FwdArgs& a, const float* lo, int64_t block0, int reverse) {
+#define SOAR_APPLY(S, R, N)                                                   \
+    k_apply<VEC, S, R, N><<<grid, kThreads, 0, s>>>(                          \
+        a.x, a.gamma, a.beta, a.mean, a.rstd, lo, a.y, p.C, p.G, p.cpg, p.HW, \
+        p.chunk, p.cpp, block0, (int64_t)grid.x, reverse)
     const int sel = (silu ? 4 : 0) | (res ? 2 : 0) | (nt ? 1 : 0);
     switch (sel) {
         case 0: SOAR_APPLY(false, false, false); break;
@@ -549,13 +615,12 @@ void apply_dispatch(bool silu, bool res, bool nt, dim3 grid, hipStream_t s,
 }
 
 template <bool VEC, bool SILU>
-void dx_dispatch(bool res, bool accum, bool nt, dim3 grid, hipStream_t s,
-                 const Plan& p, const BwdArgs& a, const double2* plane_sums,
-                 int reverse) {
-#define SOAR_DX(R, A, N)                                                     \
-    k_bwd_dx<VEC, SILU, R, A, N><<<grid, kThreads, 0, s>>>(                  \
-        a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, plane_sums,   \
-        a.dx, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, p.blocks, reverse)
+void dx_dispatch(bool res, bool accum, bool nt, dim3 grid, hipStream_t s, const Plan& p,
+                 const BwdArgs& a, const double2* unit_sums, int64_t block0, int reverse) {
+#define SOAR_DX(R, A, N)                                                        \
+    k_bwd_dx<VEC, SILU, R, A, N><<<grid, kThreads, 0, s>>>(                     \
+        a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, unit_sums, a.dx, \
+        p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, block0, (int64_t)grid.x, reverse)
     const int sel = (res ? 4 : 0) | (accum ? 2 : 0) | (nt ? 1 : 0);
     switch (sel) {
         case 0: SOAR_DX(false, false, false); break;
@@ -570,110 +635,140 @@ void dx_dispatch(bool res, bool accum, bool nt, dim3 grid, hipStream_t s,
 #undef SOAR_DX
 }
 
-inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+int64_t units_per_batch(const Plan& p, const Tuning& t, int tensors_read) {
+    if (t.batch_mb <= 0) return p.units;
+    const double unit_bytes = (double)p.cpg * (double)p.HW * 4.0 * tensors_read;
+    int64_t k = (int64_t)((double)t.batch_mb * 1048576.0 / unit_bytes);
+    return std::max<int64_t>(1, std::min<int64_t>(k, p.units));
+}
 
 }  // namespace
 
-bool make_plan(int64_t N, int64_t C, int64_t HW, int64_t G, const Tuning& t,
-               Plan* p) {
+bool make_plan(int64_t N, int64_t C, int64_t HW, int64_t G, const Tuning& t, Plan* p) {
     p->N = N;
     p->C = C;
     p->HW = HW;
     p->G = G;
     p->cpg = C / G;
     p->planes = N * C;
+    p->units = N * G;
     // A chunk never exceeds the plane: small planes get one block each.
     const int64_t hw_up = (HW + 1023) / 1024 * 1024;
     p->chunk = t.chunk < hw_up ? t.chunk : hw_up;
     p->cpp = (HW + p->chunk - 1) / p->chunk;
     if (p->planes > (int64_t)0x7fffffff / p->cpp) return false;
     p->blocks = p->planes * p->cpp;
-    if (p->blocks > 0x7fffffff || N * G > 0x7fffffff || C > 0x7fffffff) return false;
+    // a first-pass grid holds a batch's chunk blocks plus one finish block
+    // per unit of the previous batch
+    if (p->blocks + p->units > 0x7fffffff || C > 0x7fffffff) return false;
     p->vec4 = (HW % 4) == 0;
+    p->upb_fwd = units_per_batch(*p, t, 1);
+    p->upb_bwd = units_per_batch(*p, t, 2);
     return true;
 }
 
-// Workspace regions: [chunk partials: double2 x blocks]
-//                    [plane sums: double2 x planes]
-//                    [mean residuals of this call: float x N*G]
+// Workspace regions, each 256-byte aligned:
+//   chunk partials   double2 x blocks
+//   plane sums       double2 x planes
+//   unit S1/S2       double2 x units
+//   mean residuals   float   x units
 size_t workspace_bytes(const Plan& p) {
     return align256(sizeof(double2) * (size_t)p.blocks) +
            align256(sizeof(double2) * (size_t)p.planes) +
-           align256(sizeof(float) * (size_t)(p.N * p.G));
+           align256(sizeof(double2) * (size_t)p.units) +
+           align256(sizeof(float) * (size_t)p.units);
 }
 
-hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a,
-                          hipStream_t s) {
-    double2* part = static_cast<double2*>(a.ws);
-    float* lo_ws = reinterpret_cast<float*>(
-        static_cast<char*>(a.ws) + align256(sizeof(double2) * (size_t)p.blocks) +
-        align256(sizeof(double2) * (size_t)p.planes));
-    const bool vec = p.vec4;
+// Launch order for batches 0..B-1 (S = first pass, F = finish, A = second
+// pass):  S0, F0+S1, A0, F1+S2, A1, ..., F(B-1), A(B-1).
+hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a, hipStream_t s) {
+    const WsView w = ws_view(p, a.ws);
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
     const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
-    const dim3 grid((unsigned)p.blocks);
-
-    int tok = prof_begin(s, "gn_stats_partial");
-    if (vec)
-        k_stats_partial<true><<<grid, kThreads, 0, s>>>(a.x, part, p.HW, p.chunk, p.cpp);
-    else
-        k_stats_partial<false><<<grid, kThreads, 0, s>>>(a.x, part, p.HW, p.chunk, p.cpp);
-    prof_end(s, tok);
-
-    tok = prof_begin(s, "gn_stats_finish");
-    k_stats_finish<<<dim3((unsigned)(p.N * p.G)), kThreads, 0, s>>>(
-        part, a.mean, a.rstd, a.mean_lo, lo_ws, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp,
-        a.eps);
-    prof_end(s, tok);
-
-    tok = prof_begin(s, silu ? "gn_silu_apply" : "gn_apply");
-    if (vec)
-        apply_dispatch<true>(silu, res, t.nt_store != 0, grid, s, p, a, lo_ws, t.reverse);
-    else
-        apply_dispatch<false>(silu, res, t.nt_store != 0, grid, s, p, a, lo_ws, t.reverse);
-    prof_end(s, tok);
+    const bool nt = t.nt_store != 0;
+    const int64_t bpu = p.cpg * p.cpp;  // chunk blocks per unit
+    int64_t prev_u0 = 0, prev_nu = 0;
+    for (int64_t u0 = 0;; u0 += p.upb_fwd) {
+        const int64_t nu = u0 < p.units ? std::min(p.upb_fwd, p.units - u0) : 0;
+        if (nu + prev_nu > 0) {
+            const dim3 grid((unsigned)(prev_nu + nu * bpu));
+            const int tok = prof_begin(s, nu ? "gn_stats_partial" : "gn_stats_finish");
+            if (p.vec4)
+                k_stats<true><<<grid, kThreads, 0, s>>>(a.x, w.part, a.mean, a.rstd, a.mean_lo,
+                                                        w.lo, p.HW, p.chunk, p.cpp, p.cpg,
+                                                        prev_u0, prev_nu, u0 * bpu, a.eps);
+            else
+                k_stats<false><<<grid, kThreads, 0, s>>>(a.x, w.part, a.mean, a.rstd, a.mean_lo,
+                                                         w.lo, p.HW, p.chunk, p.cpp, p.cpg,
+                                                         prev_u0, prev_nu, u0 * bpu, a.eps);
+            prof_end(s, tok);
+        }
+        if (prev_nu > 0) {
+            const dim3 grid((unsigned)(prev_nu * bpu));
+            const int tok = prof_begin(s, silu ? "gn_silu_apply" : "gn_apply");
+            if (p.vec4)
+                apply_dispatch<true>(silu, res, nt, grid, s, p, a, w.lo, prev_u0 * bpu, t.reverse);
+            else
+                apply_dispatch<false>(silu, res, nt, grid, s, p, a, w.lo, prev_u0 * bpu, t.reverse);
+            prof_end(s, tok);
+        }
+        if (nu == 0) break;
+        prev_u0 = u0;
+        prev_nu = nu;
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a,
-                           hipStream_t s) {
-    double2* part = static_cast<double2*>(a.ws);
-    double2* plane_sums = reinterpret_cast<double2*>(
-        static_cast<char*>(a.ws) + align256(sizeof(double2) * (size_t)p.blocks));
-    const bool vec = p.vec4;
+// Same batch order as the forward with R = reduction, D = dx:
+//   R0, F0+R1, D0, F1+R2, D1, ..., F(B-1), D(B-1), then the dgamma/dbeta
+// finish over all planes.
+hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hipStream_t s) {
+    const WsView w = ws_view(p, a.ws);
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
     const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
     const bool accum = (a.flags & SOAR_GN_ACCUMULATE_DX) != 0;
-    const dim3 grid((unsigned)p.blocks);
-
-    int tok = prof_begin(s, silu ? "gn_silu_bwd_reduce" : "gn_bwd_reduce");
-#define SOAR_RED(V, S)                                                        \
-    k_bwd_reduce<V, S><<<grid, kThreads, 0, s>>>(                             \
-        a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, part, p.C, p.G, \
-        p.cpg, p.HW, p.chunk, p.cpp)
-    if (vec) {
-        if (silu) SOAR_RED(true, true); else SOAR_RED(true, false);
-    } else {
-        if (silu) SOAR_RED(false, true); else SOAR_RED(false, false);
-    }
+    const bool nt = t.nt_store != 0 && !accum;
+    const int64_t bpu = p.cpg * p.cpp;
+    int64_t prev_u0 = 0, prev_nu = 0;
+    for (int64_t u0 = 0;; u0 += p.upb_bwd) {
+        const int64_t nu = u0 < p.units ? std::min(p.upb_bwd, p.units - u0) : 0;
+        if (nu + prev_nu > 0) {
+            const dim3 grid((unsigned)(prev_nu + nu * bpu));
+            const int tok = prof_begin(s, nu ? (silu ? "gn_silu_bwd_reduce" : "gn_bwd_reduce")
+                                             : "gn_bwd_finish");
+#define SOAR_RED(V, S)                                                                 \
+    k_bwd_reduce<V, S><<<grid, kThreads, 0, s>>>(                                      \
+        a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, w.part, w.plane_sums,   \
+        w.unit_sums, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, prev_u0, prev_nu, u0 * bpu)
+            if (p.vec4) {
+                if (silu) SOAR_RED(true, true); else SOAR_RED(true, false);
+            } else {
+                if (silu) SOAR_RED(false, true); else SOAR_RED(false, false);
+            }
 #undef SOAR_RED
-    prof_end(s, tok);
-
-    tok = prof_begin(s, "gn_bwd_finish");
-    k_bwd_finish<<<dim3((unsigned)p.C), kThreads, 0, s>>>(part, plane_sums, a.dgamma,
-                                                          a.dbeta, p.N, p.C, p.cpp);
-    prof_end(s, tok);
-
-    if (a.dx) {
-        tok = prof_begin(s, silu ? "gn_silu_bwd_dx" : "gn_bwd_dx");
-        const bool nt = t.nt_store != 0 && !accum;
-        if (vec) {
-            if (silu) dx_dispatch<true, true>(res, accum, nt, grid, s, p, a, plane_sums, t.reverse);
-            else dx_dispatch<true, false>(res, accum, nt, grid, s, p, a, plane_sums, t.reverse);
-        } else {
-            if (silu) dx_dispatch<false, true>(res, accum, nt, grid, s, p, a, plane_sums, t.reverse);
-            else dx_dispatch<false, false>(res, accum, nt, grid, s, p, a, plane_sums, t.reverse);
+            prof_end(s, tok);
         }
+        if (prev_nu > 0 && a.dx) {
+            const dim3 grid((unsigned)(prev_nu * bpu));
+            const int64_t block0 = prev_u0 * bpu;
+            const int tok = prof_begin(s, silu ? "gn_silu_bwd_dx" : "gn_bwd_dx");
+            if (p.vec4) {
+                if (silu) dx_dispatch<true, true>(res, accum, nt, grid, s, p, a, w.unit_sums, block0, t.reverse);
+                else dx_dispatch<true, false>(res, accum, nt, grid, s, p, a, w.unit_sums, block0, t.reverse);
+            } else {
+                if (silu) dx_dispatch<false, true>(res, accum, nt, grid, s, p, a, w.unit_sums, block0, t.reverse);
+                else dx_dispatch<false, false>(res, accum, nt, grid, s, p, a, w.unit_sums, block0, t.reverse);
+            }
+            prof_end(s, tok);
+        }
+        if (nu == 0) break;
+        prev_u0 = u0;
+        prev_nu = nu;
+    }
+    if (a.dgamma) {
+        const int tok = prof_begin(s, "gn_param_finish");
+        k_param_finish<<<dim3((unsigned)((p.C + 255) / 256)), 256, 0, s>>>(
+            w.plane_sums, a.dgamma, a.dbeta, p.N, p.C);
         prof_end(s, tok);
     }
     return hipGetLastError();

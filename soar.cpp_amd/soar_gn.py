@@ -35,6 +35,7 @@ GN_ACCUMULATE_DX = 4
 TUNE_CHUNK = 1
 TUNE_REVERSE = 2
 TUNE_NT_STORE = 3
+TUNE_BATCH_MB = 4
 
 
 class SoarUnavailable(RuntimeError):

@@ -28,13 +28,13 @@ def test_synth_library_exports(L):
 
 
 def test_workspace_bytes_is_host_arithmetic(L):
-    # cfg 3: 64 planes x 128 chunks of 32768 floats -> 8192 partials of 16 B
-    assert soar_gn.tune_get(soar_gn.TUNE_CHUNK) == 32768
-    # plus 64 plane sums of 16 B plus 16 mean residuals of 4 B, each region
-    # 256-byte aligned.
-    assert soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) == 8192 * 16 + 1024 + 256
+    # cfg 3: 64 planes x 512 chunks of 8192 floats -> 32768 partials of 16 B
+    assert soar_gn.tune_get(soar_gn.TUNE_CHUNK) == 8192
+    # plus 64 plane sums of 16 B, 16 unit sums of 16 B and 16 mean residuals
+    # of 4 B, each region 256-byte aligned.
+    assert soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) == 32768 * 16 + 1024 + 2 * 256
     # small planes get one block each (chunk clipped to the plane)
-    assert soar_gn.workspace_bytes(2, 6, 10, 3) == 256 + 256 + 256
+    assert soar_gn.workspace_bytes(2, 6, 10, 3) == 4 * 256
     assert soar_gn.workspace_bytes(0, 6, 10, 3) == 0
     assert soar_gn.workspace_bytes(1, 6, 10, 4) == 0  # C % G != 0
 
@@ -89,7 +89,9 @@ def test_tuning_knobs(L):
     assert L.soar_gn_tune(soar_gn.TUNE_REVERSE, 2) == soar_gn.SOAR_EINVAL
     assert L.soar_gn_tune(99, 1) == soar_gn.SOAR_EINVAL
     soar_gn.tune(soar_gn.TUNE_CHUNK, 4096)
-    assert soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) == 65536 * 16 + 1024 + 256
+    assert soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) == 65536 * 16 + 1024 + 2 * 256
+    assert L.soar_gn_tune(soar_gn.TUNE_BATCH_MB, -1) == soar_gn.SOAR_EINVAL
+    assert soar_gn.tune_get(soar_gn.TUNE_BATCH_MB) == 0
     soar_gn.tune(soar_gn.TUNE_CHUNK, old)
     assert soar_gn.tune_get(soar_gn.TUNE_CHUNK) == old
 

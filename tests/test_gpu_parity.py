@@ -481,6 +481,57 @@ def test_kernel_timing_records(gpu):
         recs = {r["kernel"]: r for r in gpu.prof_summary()}
     finally:
         gpu.prof_enable(False)
+    # one unit batch covers this small tensor: one launch of each pass, plus
+    # the finish-only launch of the last (here: only) batch
     for k in ("gn_stats_partial", "gn_stats_finish", "gn_silu_apply", "gn_silu_bwd_reduce",
-              "gn_bwd_finish", "gn_silu_bwd_dx"):
+              "gn_bwd_finish", "gn_silu_bwd_dx", "gn_param_finish"):
         assert recs[k]["launches"] == 1 and recs[k]["total_ms"] > 0
+
+
+# ------------------------------------------------------------ tuning knobs
+
+@pytest.fixture
+def restore_tuning(gpu):
+    keys = (gpu.TUNE_CHUNK, gpu.TUNE_REVERSE, gpu.TUNE_NT_STORE, gpu.TUNE_BATCH_MB)
+    old = {k: gpu.tune_get(k) for k in keys}
+    yield
+    for k, v in old.items():
+        gpu.tune(k, v)
+
+
+def _fwd_bwd(gpu, x, gamma, beta, dy, G, residual=False):
+    N, C, HW = x.shape
+    ws = gpu.workspace(N, C, HW, G)
+    y, st = gpu.gn_silu_forward(x, gamma, beta, G, eps=EPS, residual=residual, ws=ws)
+    dx, dg, db = gpu.gn_silu_backward(dy, x, gamma, beta, st, G, residual=residual, ws=ws)
+    return [y, st.mean, st.rstd, st.mean_lo, dx, dg, db]
+
+
+@pytest.mark.parametrize("residual", [False, True])
+def test_tuning_variants_match(gpu, oracle, restore_tuning, residual):
+    """Unit batches, reverse order and store flavour change only the launch
+    schedule: results are bitwise identical to the default.  Other chunk
+    sizes change the summation tree: results stay within the parity bar."""
+    import torch
+    N, C, HW, G = 2, 12, 65536 + 4096, 6   # unit = 2 x 69632 floats (544 KiB)
+    x, gamma, beta, dy = make_inputs(oracle, N, C, HW, G, "normal", 41)
+    xd, dyd = dev(x).view(N, C, HW), dev(dy).view(N, C, HW)
+    gd, bd = dev(gamma), dev(beta)
+    base = _fwd_bwd(gpu, xd, gd, bd, dyd, G, residual)
+    for key, val in ((gpu.TUNE_BATCH_MB, 1), (gpu.TUNE_BATCH_MB, 2), (gpu.TUNE_REVERSE, 0),
+                     (gpu.TUNE_NT_STORE, 0)):
+        gpu.tune(key, val)
+        got = _fwd_bwd(gpu, xd, gd, bd, dyd, G, residual)
+        for a, b in zip(base, got):
+            assert torch.equal(a, b), (key, val)
+    yt, mt, rt = oracle.gn_silu_fwd_f64(x, gamma, beta, N, C, HW, G, EPS, True, residual)
+    dxt, dgt, dbt = oracle.gn_silu_bwd_f64(dy, x, gamma, beta, mt, rt, N, C, HW, G, True,
+                                           residual)
+    for chunk in (1024, 4096, 16384):
+        gpu.tune(gpu.TUNE_CHUNK, chunk)
+        y, mean, rstd, lo, dx, dg, db = _fwd_bwd(gpu, xd, gd, bd, dyd, G, residual)
+        assert_stats(host(mean), host(rstd), mt, rt, f"chunk {chunk}")
+        assert_vals(host(y), yt, f"y chunk {chunk}")
+        assert_vals(host(dx), dxt, f"dx chunk {chunk}")
+        assert_vals(host(dg), dgt, f"dgamma chunk {chunk}")
+        assert_vals(host(db), dbt, f"dbeta chunk {chunk}")
