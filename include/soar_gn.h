@@ -198,6 +198,11 @@ SOAR_API int soar_memcpy_h2d(void* dst, const void* src, size_t bytes,
                              void* stream);
 SOAR_API int soar_memcpy_d2h(void* dst, const void* src, size_t bytes,
                              void* stream);
+/* Device-to-device copy, asynchronous on `stream` (Tensor::clone and the
+ * per-sample slicing of Trainer::train_step, src/tensor/tensor.cpp and
+ * src/engine/trainer.cpp:182, which call cudaMemcpyAsync DtoD). */
+SOAR_API int soar_memcpy_d2d(void* dst, const void* src, size_t bytes,
+                             void* stream);
 
 /* ---- kernel timing (no counterpart in the reference) ------------------ */
 /* When enabled, every kernel this library launches is bracketed by a pair

@@ -504,6 +504,15 @@ SOAR_API int soar_memcpy_d2h(void* dst, const void* src, size_t bytes, void* str
     return e == hipSuccess ? ok() : hip_fail(e, "device-to-host copy");
 }
 
+SOAR_API int soar_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return ok();
+    int rc = require_device();
+    if (rc || (rc = check_dev(dst, bytes, "dst")) || (rc = check_dev(src, bytes, "src"))) return rc;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
+                                  static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "device-to-device copy");
+}
+
 // ---- timing ------------------------------------------------------------------
 
 SOAR_API int soar_prof_enable(int on) {

@@ -84,6 +84,7 @@ SIGNATURES = {
     "soar_arena_destroy": (_c.c_int, [_P]),
     "soar_memcpy_h2d": (_c.c_int, [_P, _P, _SZ, _P]),
     "soar_memcpy_d2h": (_c.c_int, [_P, _P, _SZ, _P]),
+    "soar_memcpy_d2d": (_c.c_int, [_P, _P, _SZ, _P]),
     "soar_prof_enable": (_c.c_int, [_c.c_int]),
     "soar_prof_summary": (_c.c_int, [_c.c_char_p, _SZ]),
     "soar_gn_tune": (_c.c_int, [_c.c_int, _I64]),

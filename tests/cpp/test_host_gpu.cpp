@@ -1,0 +1,284 @@
+// Device tests of the C++ host layer (run on the MI355X by
+// tests/test_host_cpp.py).  Every result is checked against the float64
+// oracle (oracle/soar_oracle.c) with the path's parity bar
+// |d| <= 1e-4 * (1 + |truth|) (statistics 1e-5 relative).
+#include <cmath>
+#include <cstdio>
+#include <vector>
+
+#include "check.hpp"
+#include "soar/autograd.hpp"
+#include "soar/kernels.hpp"
+#include "soar/memory.hpp"
+#include "soar/nn.hpp"
+#include "soar_oracle.h"
+
+using namespace soar;
+
+static const float kEps = 1e-5f;
+
+static double max_err(const std::vector<float>& got, const std::vector<double>& truth) {
+    CHECK(got.size() == truth.size());
+    double m = 0.0;
+    for (size_t i = 0; i < got.size(); ++i)
+        m = std::max(m, std::fabs((double)got[i] - truth[i]) / (1.0 + std::fabs(truth[i])));
+    return m;
+}
+
+struct Data {
+    int64_t N, C, H, W, G;
+    std::vector<float> x, gamma, beta, dy;
+    int64_t n() const { return N * C * H * W; }
+};
+
+static Data make_data(int64_t N, int64_t C, int64_t H, int64_t W, int64_t G, uint64_t seed) {
+    Data d{N, C, H, W, G, {}, {}, {}, {}};
+    d.x.resize(d.n());
+    d.dy.resize(d.n());
+    d.gamma.resize(C);
+    d.beta.resize(C);
+    orc_fill_normal(d.x.data(), d.n(), seed, 1, 0.0, 1.0);
+    orc_fill_uniform(d.gamma.data(), C, seed, 2, 0.5, 1.5);
+    orc_fill_normal(d.beta.data(), C, seed, 3, 0.0, 0.1);
+    orc_fill_normal(d.dy.data(), d.n(), seed, 4, 0.0, 1e-2);
+    return d;
+}
+
+static void set_params(nn::GroupNorm& m, const std::vector<float>& g, const std::vector<float>& b) {
+    for (size_t c = 0; c < g.size(); ++c) {
+        m.weight()->data()[c] = g[c];
+        m.bias()->data()[c] = b[c];
+    }
+    m.to_device();
+}
+
+struct Truth {
+    std::vector<double> y, dx, dg, db, mean, rstd;
+};
+
+static Truth oracle_block(const std::vector<float>& x, const Data& d, const std::vector<float>& dy,
+                          const float* gamma, const float* beta, int silu, int residual) {
+    Truth t;
+    const int64_t HW = d.H * d.W;
+    t.y.resize(x.size());
+    t.dx.resize(x.size());
+    t.dg.resize(d.C);
+    t.db.resize(d.C);
+    t.mean.resize(d.N * d.G);
+    t.rstd.resize(d.N * d.G);
+    CHECK(orc_gn_silu_fwd_f64(x.data(), gamma, beta, d.N, d.C, HW, d.G, (double)kEps, silu,
+                              residual, t.y.data(), t.mean.data(), t.rstd.data()) == 0);
+    CHECK(orc_gn_silu_bwd_f64(dy.data(), x.data(), gamma, beta, t.mean.data(), t.rstd.data(), d.N,
+                              d.C, HW, d.G, silu, residual, t.dx.data(), t.dg.data(),
+                              t.db.data()) == 0);
+    return t;
+}
+
+static void check_close(const char* what, const std::vector<float>& got,
+                        const std::vector<double>& truth) {
+    const double e = max_err(got, truth);
+    if (!(e <= 1e-4)) {
+        char buf[160];
+        std::snprintf(buf, sizeof buf, "%s: max error %.3e above 1e-4", what, e);
+        throw std::runtime_error(buf);
+    }
+}
+
+// GroupNorm -> SiLU as two modules and as the fused GNSiLU, through the
+// engine, against float64 truth.
+static void test_fused_and_unfused_layers() {
+    memory::DeviceArena arena(512u << 20);
+    memory::ArenaScope scope(arena);
+    const Data d = make_data(2, 16, 64, 64, 4, 101);
+    const Truth t = oracle_block(d.x, d, d.dy, d.gamma.data(), d.beta.data(), 1, 0);
+    const Shape shape{d.N, d.C, d.H, d.W};
+    for (int fused = 0; fused < 2; ++fused) {
+        std::unique_ptr<nn::GroupNorm> gn;
+        if (fused)
+            gn = std::make_unique<nn::GNSiLU>(d.G, d.C);
+        else
+            gn = std::make_unique<nn::GroupNorm>(d.G, d.C);
+        set_params(*gn, d.gamma, d.beta);
+        nn::SiLU act;
+        auto x = Tensor::from_blob(d.x.data(), shape, true, true);
+        auto y = fused ? gn->forward(x) : act.forward(gn->forward(x));
+        CHECK(y->grad_fn() != nullptr);
+        check_close(fused ? "fused y" : "unfused y", y->to_host(), t.y);
+        y->backward(Tensor::from_blob(d.dy.data(), shape, false, true));
+        check_close(fused ? "fused dx" : "unfused dx", x->grad()->to_host(), t.dx);
+        check_close("dgamma", gn->weight()->grad()->to_host(), t.dg);
+        check_close("dbeta", gn->bias()->grad()->to_host(), t.db);
+    }
+}
+
+// The SOAR residual block x + silu(gn(x)), three in a row: fused
+// (GNSiLU with residual) and unfused (GroupNorm, SiLU, add_tensors).
+static void test_residual_chain() {
+    memory::DeviceArena arena(512u << 20);
+    memory::ArenaScope scope(arena);
+    const int B = 3;
+    Data d = make_data(1, 8, 32, 32, 2, 202);
+    std::vector<std::vector<float>> gam(B), bet(B);
+    for (int b = 0; b < B; ++b) {
+        gam[b].resize(d.C);
+        bet[b].resize(d.C);
+        orc_fill_uniform(gam[b].data(), d.C, 300 + b, 2, 0.5, 1.5);
+        orc_fill_normal(bet[b].data(), d.C, 300 + b, 3, 0.0, 0.1);
+    }
+    // float64 truth block by block, activations rounded to fp32 between
+    // blocks as the device stores them
+    std::vector<std::vector<float>> acts{d.x};
+    for (int b = 0; b < B; ++b) {
+        Truth t = oracle_block(acts.back(), d, d.dy, gam[b].data(), bet[b].data(), 1, 1);
+        std::vector<float> nx(t.y.begin(), t.y.end());
+        acts.push_back(nx);
+    }
+    std::vector<float> g = d.dy;
+    std::vector<Truth> tb(B);
+    for (int b = B - 1; b >= 0; --b) {
+        tb[b] = oracle_block(acts[b], d, g, gam[b].data(), bet[b].data(), 1, 1);
+        g.assign(tb[b].dx.begin(), tb[b].dx.end());
+    }
+    const Shape shape{d.C, d.H, d.W};  // the reference's [C,H,W] layout
+    for (int fused = 0; fused < 2; ++fused) {
+        std::vector<std::unique_ptr<nn::GroupNorm>> gns;
+        nn::SiLU act;
+        auto x0 = Tensor::from_blob(d.x.data(), shape, true, true);
+        TensorPtr h = x0;
+        for (int b = 0; b < B; ++b) {
+            if (fused)
+                gns.push_back(std::make_unique<nn::GNSiLU>(d.G, d.C, kEps, true, true));
+            else
+                gns.push_back(std::make_unique<nn::GroupNorm>(d.G, d.C));
+            set_params(*gns.back(), gam[b], bet[b]);
+            h = fused ? gns.back()->forward(h) : nn::add_tensors(h, act.forward(gns.back()->forward(h)));
+        }
+        std::vector<double> yt(acts.back().begin(), acts.back().end());
+        check_close("chain y", h->to_host(), yt);
+        h->backward(Tensor::from_blob(d.dy.data(), shape, false, true));
+        std::vector<double> dxt(g.begin(), g.end());
+        check_close(fused ? "fused chain dx" : "unfused chain dx", x0->grad()->to_host(), dxt);
+        for (int b = 0; b < B; ++b) {
+            check_close("chain dgamma", gns[b]->weight()->grad()->to_host(), tb[b].dg);
+            check_close("chain dbeta", gns[b]->bias()->grad()->to_host(), tb[b].db);
+        }
+    }
+}
+
+// [N,C,H,W] in one call equals the reference's per-sample loop over
+// [C,H,W] with parameter gradients accumulated across samples
+// (src/engine/trainer.cpp:179-220), and gradients accumulate in place into
+// a buffer that keeps its address.
+static void test_batch_equals_per_sample_and_accumulates() {
+    memory::DeviceArena arena(512u << 20);
+    memory::ArenaScope scope(arena);
+    const Data d = make_data(3, 8, 32, 48, 4, 303);
+    const Truth t = oracle_block(d.x, d, d.dy, d.gamma.data(), d.beta.data(), 1, 0);
+    nn::GNSiLU per_sample(d.G, d.C);
+    set_params(per_sample, d.gamma, d.beta);
+    const int64_t S = d.C * d.H * d.W;
+    std::vector<float> dx_all;
+    for (int64_t n = 0; n < d.N; ++n) {
+        auto xn = Tensor::from_blob(d.x.data() + n * S, {d.C, d.H, d.W}, true, true);
+        auto yn = per_sample.forward(xn);
+        yn->backward(Tensor::from_blob(d.dy.data() + n * S, {d.C, d.H, d.W}, false, true));
+        auto g = xn->grad()->to_host();
+        dx_all.insert(dx_all.end(), g.begin(), g.end());
+    }
+    check_close("per-sample dx", dx_all, t.dx);
+    check_close("per-sample dgamma", per_sample.weight()->grad()->to_host(), t.dg);
+    check_close("per-sample dbeta", per_sample.bias()->grad()->to_host(), t.db);
+
+    nn::GNSiLU batched(d.G, d.C);
+    set_params(batched, d.gamma, d.beta);
+    const Shape shape{d.N, d.C, d.H, d.W};
+    auto dy = Tensor::from_blob(d.dy.data(), shape, false, true);
+    auto x = Tensor::from_blob(d.x.data(), shape, true, true);
+    batched.forward(x)->backward(dy);
+    check_close("batched dgamma", batched.weight()->grad()->to_host(), t.dg);
+    const float* buf = batched.weight()->grad()->cuda_data();
+    auto x2 = Tensor::from_blob(d.x.data(), shape, true, true);
+    batched.forward(x2)->backward(dy);
+    CHECK(batched.weight()->grad()->cuda_data() == buf);
+    std::vector<double> twice(t.dg.size());
+    for (size_t i = 0; i < twice.size(); ++i) twice[i] = 2.0 * t.dg[i];
+    check_close("accumulated dgamma", batched.weight()->grad()->to_host(), twice);
+    batched.zero_grad();
+    for (float v : batched.weight()->grad()->to_host()) CHECK(v == 0.0f);
+}
+
+// Parameters in the static region; per-step activations reuse identical
+// offsets after reset_dynamic_allocations (device_slab.cpp:39-56).
+static void test_arena_step_reuse() {
+    memory::DeviceArena arena(64u << 20);
+    memory::ArenaScope scope(arena);
+    const Data d = make_data(1, 8, 16, 16, 2, 404);
+    nn::GNSiLU m(d.G, d.C);
+    set_params(m, d.gamma, d.beta);
+    arena.freeze_static_parameters();
+    const size_t sb = arena.slab().static_boundary();
+    CHECK(sb > 0);
+    const float* out_ptr[2] = {nullptr, nullptr};
+    std::vector<float> outs[2];
+    for (int step = 0; step < 2; ++step) {
+        arena.reset_dynamic_allocations();
+        CHECK(arena.slab().current_offset() == sb);
+        auto x = Tensor::from_blob(d.x.data(), {d.C, d.H, d.W}, true, true);
+        auto y = m.forward(x);
+        out_ptr[step] = y->cuda_data();
+        outs[step] = y->to_host();
+    }
+    CHECK(out_ptr[0] == out_ptr[1]);
+    CHECK(outs[0] == outs[1]);  // bitwise reproducible
+    {
+        autograd::NoGradGuard ng;
+        auto x = Tensor::from_blob(d.x.data(), {d.C, d.H, d.W}, true, true);
+        CHECK(m.forward(x)->grad_fn() == nullptr);
+    }
+    CHECK_THROWS(arena.allocate(128u << 20), OutOfMemory);
+}
+
+// The reference-named operator API (cuda_kernels.hpp) on one sample.
+static void test_reference_operator_api() {
+    memory::DeviceArena arena(64u << 20);
+    memory::ArenaScope scope(arena);
+    CHECK(hip::kernels::is_cuda_available());
+    const Data d = make_data(1, 16, 32, 32, 4, 505);
+    const Truth t = oracle_block(d.x, d, d.dy, d.gamma.data(), d.beta.data(), 0, 0);
+    const Shape shape{d.C, d.H * d.W};
+    auto x = Tensor::from_blob(d.x.data(), shape, false, true);
+    auto gm = Tensor::from_blob(d.gamma.data(), {d.C}, false, true);
+    auto bt = Tensor::from_blob(d.beta.data(), {d.C}, false, true);
+    auto out = Tensor::create(shape, false, true);
+    auto mean = Tensor::create({d.G}, false, true), rstd = Tensor::create({d.G}, false, true);
+    hip::kernels::group_norm_forward(x->cuda_data(), gm->cuda_data(), bt->cuda_data(),
+                                     out->cuda_data(), mean->cuda_data(), rstd->cuda_data(),
+                                     d.G, d.C, d.H * d.W, kEps);
+    check_close("group_norm_forward", out->to_host(), t.y);
+    auto dy = Tensor::from_blob(d.dy.data(), shape, false, true);
+    auto gx = Tensor::zeros(shape, false, true);
+    auto gw = Tensor::zeros({d.C}, false, true), gb = Tensor::zeros({d.C}, false, true);
+    hip::kernels::group_norm_backward(dy->cuda_data(), x->cuda_data(), gm->cuda_data(),
+                                      mean->cuda_data(), rstd->cuda_data(), gx->cuda_data(),
+                                      gw->cuda_data(), gb->cuda_data(), d.G, d.C, d.H * d.W);
+    check_close("group_norm_backward dx", gx->to_host(), t.dx);
+    check_close("group_norm_backward dgamma", gw->to_host(), t.dg);
+    check_close("group_norm_backward dbeta", gb->to_host(), t.db);
+    CHECK_THROWS(hip::kernels::group_norm_forward(x->cuda_data(), nullptr, nullptr,
+                                                  out->cuda_data(), mean->cuda_data(),
+                                                  rstd->cuda_data(), 3, d.C, d.H * d.W, kEps),
+                 InvalidArgument);
+}
+
+int main() {
+    std::printf("=== host layer: device tests ===\n");
+    int fails = 0;
+    fails += run_test("fused_and_unfused_layers", test_fused_and_unfused_layers);
+    fails += run_test("residual_chain", test_residual_chain);
+    fails += run_test("batch_equals_per_sample_and_accumulates",
+                      test_batch_equals_per_sample_and_accumulates);
+    fails += run_test("arena_step_reuse", test_arena_step_reuse);
+    fails += run_test("reference_operator_api", test_reference_operator_api);
+    std::printf("%s (%d failed)\n", fails ? "FAILED" : "ALL PASSED", fails);
+    return fails ? 1 : 0;
+}
