@@ -586,6 +586,14 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
                 return fail(SOAR_EINVAL, "batch_mb must be in [0, 2^20]");
             g_tune.batch_mb = value;
             return ok();
+        case SOAR_TUNE_STREAMS:
+            if (value != 1 && value != 2) return fail(SOAR_EINVAL, "streams must be 1 or 2");
+            g_tune.streams = (int)value;
+            return ok();
+        case SOAR_TUNE_NT_LOAD:
+            if (value != 0 && value != 1) return fail(SOAR_EINVAL, "nt_load must be 0 or 1");
+            g_tune.nt_load = (int)value;
+            return ok();
         default:
             return fail(SOAR_EINVAL, "unknown tuning key %d", key);
     }
@@ -598,6 +606,8 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
         case SOAR_TUNE_REVERSE: return g_tune.reverse;
         case SOAR_TUNE_NT_STORE: return g_tune.nt_store;
         case SOAR_TUNE_BATCH_MB: return g_tune.batch_mb;
+        case SOAR_TUNE_STREAMS: return g_tune.streams;
+        case SOAR_TUNE_NT_LOAD: return g_tune.nt_load;
         default: return -1;
     }
 }

@@ -34,9 +34,12 @@ struct Plan {
 // Defaults measured on MI355X at 1x64x2048^2, fwd+bwd per step:
 //   chunk 8192, forward order, cached stores            1.541 ms
 //   + reverse order + non-temporal stores                1.469 ms
+//   + non-temporal loads in the second passes            1.447 ms
 //   chunk 16384 / 32768                                  +1.5% / +3%
-//   unit batches of 64 / 128 / 256 / 512 MiB             1.635 / 1.589 /
-//                                                        1.536 / 1.511 ms
+//   unit batches of 64 / 128 / 256 MiB (with nt loads)   1.525 / 1.475 /
+//                                                        1.465 ms
+//   same batches pipelined on two streams                1.740 / 1.628 /
+//                                                        1.544 ms
 // (each extra pair of launches costs ~2.7 us, more than the MALL saves).
 struct Tuning {
     int64_t chunk = 8192;     // floats per block-chunk, multiple of 1024
@@ -45,6 +48,8 @@ struct Tuning {
     int nt_store = 1;         // non-temporal stores of y / dx
     int64_t batch_mb = 0;     // MiB read by the first pass of a batch
                               // (0: the whole tensor is one batch)
+    int streams = 1;          // 2: pipeline batches over a helper stream
+    int nt_load = 1;          // non-temporal loads in the second passes
 };
 
 constexpr int kThreads = 256;

@@ -42,6 +42,8 @@
 //               gives per-plane sum(dz) and sum(dz*xhat); dgamma/dbeta and
 //               the per-group S1/S2 both derive from them.
 #include <algorithm>
+#include <mutex>
+#include <type_traits>
 
 #include "gn_internal.hpp"
 #include "soar_gn.h"
@@ -165,6 +167,12 @@ __device__ __forceinline__ Chunk chunk_of(int64_t b, int64_t HW, int64_t chunk,
 // Block index of this block inside its batch [block0, block0 + nb).
 __device__ __forceinline__ int64_t batch_block(int64_t block0, int64_t nb, int reverse) {
     return block0 + (reverse ? nb - 1 - (int64_t)blockIdx.x : (int64_t)blockIdx.x);
+}
+
+template <bool NTL>
+__device__ __forceinline__ f4 load4(const f4* p) {
+    if (NTL) return __builtin_nontemporal_load(p);
+    return *p;
 }
 
 template <bool NT>
@@ -343,7 +351,7 @@ __device__ __forceinline__ PlaneCoef plane_coef(
 // ======================================================================
 // Forward pass 2: y = f((x - mean) * (gamma*rstd) + beta) [+ x].
 // ======================================================================
-template <bool VEC, bool SILU, bool RES, bool NT>
+template <bool VEC, bool SILU, bool RES, bool NT, bool NTL>
 __global__ __launch_bounds__(kThreads) void k_apply(
     const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ mean,
@@ -368,8 +376,8 @@ __global__ __launch_bounds__(kThreads) void k_apply(
         const int64_t n4 = ck.len >> 2;
         int64_t i = t;
         for (; i + 3 * kThreads < n4; i += 4 * kThreads) {
-            f4 v0 = x4[i], v1 = x4[i + kThreads], v2 = x4[i + 2 * kThreads],
-               v3 = x4[i + 3 * kThreads];
+            f4 v0 = load4<NTL>(&x4[i]), v1 = load4<NTL>(&x4[i + kThreads]),
+               v2 = load4<NTL>(&x4[i + 2 * kThreads]), v3 = load4<NTL>(&x4[i + 3 * kThreads]);
             f4 o0 = {f(v0.x), f(v0.y), f(v0.z), f(v0.w)};
             f4 o1 = {f(v1.x), f(v1.y), f(v1.z), f(v1.w)};
             f4 o2 = {f(v2.x), f(v2.y), f(v2.z), f(v2.w)};
@@ -380,7 +388,7 @@ __global__ __launch_bounds__(kThreads) void k_apply(
             store4<NT>(&y4[i + 3 * kThreads], o3);
         }
         for (; i < n4; i += kThreads) {
-            f4 v = x4[i];
+            f4 v = load4<NTL>(&x4[i]);
             f4 o = {f(v.x), f(v.y), f(v.z), f(v.w)};
             store4<NT>(&y4[i], o);
         }
@@ -504,7 +512,7 @@ __global__ void k_param_finish(const double2* __restrict__ plane_sums,
 // Backward pass 2: dx = A*dz + D*xhat + B [+ dy] [+ dx_old] with
 // A = gamma_c*rstd, B = -rstd*S1/M, D = -rstd*S2/M.
 // ======================================================================
-template <bool VEC, bool SILU, bool RES, bool ACC, bool NT>
+template <bool VEC, bool SILU, bool RES, bool ACC, bool NT, bool NTL>
 __global__ __launch_bounds__(kThreads) void k_bwd_dx(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ gamma, const float* __restrict__ beta,
@@ -538,8 +546,8 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(
         const int64_t n4 = ck.len >> 2;
         int64_t i = t;
         for (; i + kThreads < n4; i += 2 * kThreads) {
-            f4 v0 = x4[i], v1 = x4[i + kThreads];
-            f4 g0 = g4[i], g1 = g4[i + kThreads];
+            f4 v0 = load4<NTL>(&x4[i]), v1 = load4<NTL>(&x4[i + kThreads]);
+            f4 g0 = load4<NTL>(&g4[i]), g1 = load4<NTL>(&g4[i + kThreads]);
             f4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0;
             if (ACC) {
                 p0 = o4[i];
@@ -553,7 +561,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(
             store4<NT>(&o4[i + kThreads], r1);
         }
         for (; i < n4; i += kThreads) {
-            f4 v0 = x4[i], g0 = g4[i];
+            f4 v0 = load4<NTL>(&x4[i]), g0 = load4<NTL>(&g4[i]);
             f4 p0 = {0.f, 0.f, 0.f, 0.f};
             if (ACC) p0 = o4[i];
             f4 r0 = {f(g0.x, v0.x, p0.x), f(g0.y, v0.y, p0.y),
@@ -593,47 +601,138 @@ WsView ws_view(const Plan& p, void* ws) {
     return v;
 }
 
-template <bool VEC>
-void apply_dispatch(bool silu, bool res, bool nt, dim3 grid, hipStream_t s, const Plan& p,
-                    const FwdArgs& a, const float* lo, int64_t block0, int reverse) {
-#define SOAR_APPLY(S, R, N)                                                   \
-    k_apply<VEC, S, R, N><<<grid, kThreads, 0, s>>>(                          \
-        a.x, a.gamma, a.beta, a.mean, a.rstd, lo, a.y, p.C, p.G, p.cpg, p.HW, \
-        p.chunk, p.cpp, block0, (int64_t)grid.x, reverse)
-    const int sel = (silu ? 4 : 0) | (res ? 2 : 0) | (nt ? 1 : 0);
-    switch (sel) {
-        case 0: SOAR_APPLY(false, false, false); break;
-        case 1: SOAR_APPLY(false, false, true); break;
-        case 2: SOAR_APPLY(false, true, false); break;
-        case 3: SOAR_APPLY(false, true, true); break;
-        case 4: SOAR_APPLY(true, false, false); break;
-        case 5: SOAR_APPLY(true, false, true); break;
-        case 6: SOAR_APPLY(true, true, false); break;
-        default: SOAR_APPLY(true, true, true); break;
-    }
-#undef SOAR_APPLY
+// Calls f(std::true_type) or f(std::false_type): turns a runtime flag into
+// a template argument.
+template <typename F>
+void bsel(bool b, F&& f) {
+    if (b)
+        f(std::true_type{});
+    else
+        f(std::false_type{});
 }
 
-template <bool VEC, bool SILU>
-void dx_dispatch(bool res, bool accum, bool nt, dim3 grid, hipStream_t s, const Plan& p,
-                 const BwdArgs& a, const double2* unit_sums, int64_t block0, int reverse) {
-#define SOAR_DX(R, A, N)                                                        \
-    k_bwd_dx<VEC, SILU, R, A, N><<<grid, kThreads, 0, s>>>(                     \
-        a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, unit_sums, a.dx, \
-        p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, block0, (int64_t)grid.x, reverse)
-    const int sel = (res ? 4 : 0) | (accum ? 2 : 0) | (nt ? 1 : 0);
-    switch (sel) {
-        case 0: SOAR_DX(false, false, false); break;
-        case 1: SOAR_DX(false, false, true); break;
-        case 2: SOAR_DX(false, true, false); break;
-        case 3: SOAR_DX(false, true, true); break;
-        case 4: SOAR_DX(true, false, false); break;
-        case 5: SOAR_DX(true, false, true); break;
-        case 6: SOAR_DX(true, true, false); break;
-        default: SOAR_DX(true, true, true); break;
-    }
-#undef SOAR_DX
+void launch_apply(const Plan& p, const Tuning& t, const FwdArgs& a, const float* lo,
+                  int64_t block0, int64_t nb, hipStream_t s) {
+    const bool silu = (a.flags & SOAR_GN_SILU) != 0;
+    const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
+    const dim3 grid((unsigned)nb);
+    bsel(p.vec4, [&](auto V) {
+        bsel(silu, [&](auto S) {
+            bsel(res, [&](auto R) {
+                bsel(t.nt_store != 0, [&](auto N) {
+                    bsel(V() && t.nt_load != 0, [&](auto L) {
+                        k_apply<V(), S(), R(), N(), L()><<<grid, kThreads, 0, s>>>(
+                            a.x, a.gamma, a.beta, a.mean, a.rstd, lo, a.y, p.C, p.G, p.cpg,
+                            p.HW, p.chunk, p.cpp, block0, nb, t.reverse);
+                    });
+                });
+            });
+        });
+    });
 }
+
+void launch_dx(const Plan& p, const Tuning& t, const BwdArgs& a, const double2* unit_sums,
+               int64_t block0, int64_t nb, hipStream_t s) {
+    const bool silu = (a.flags & SOAR_GN_SILU) != 0;
+    const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
+    const bool accum = (a.flags & SOAR_GN_ACCUMULATE_DX) != 0;
+    const dim3 grid((unsigned)nb);
+    bsel(p.vec4, [&](auto V) {
+        bsel(silu, [&](auto S) {
+            bsel(res, [&](auto R) {
+                bsel(accum, [&](auto A) {
+                    bsel(t.nt_store != 0 && !accum, [&](auto N) {
+                        bsel(V() && t.nt_load != 0, [&](auto L) {
+                            k_bwd_dx<V(), S(), R(), A(), N(), L()><<<grid, kThreads, 0, s>>>(
+                                a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo,
+                                unit_sums, a.dx, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, block0,
+                                nb, t.reverse);
+                        });
+                    });
+                });
+            });
+        });
+    });
+}
+
+// First-pass kernels: `fin_nu` finish blocks for units [fin_u0, fin_u0 +
+// fin_nu), then chunk blocks for units [u0, u0 + nu).
+void launch_stats(const Plan& p, const FwdArgs& a, const WsView& w, int64_t fin_u0,
+                  int64_t fin_nu, int64_t u0, int64_t nu, hipStream_t s) {
+    const int64_t bpu = p.cpg * p.cpp;
+    const dim3 grid((unsigned)(fin_nu + nu * bpu));
+    const int tok = prof_begin(s, nu ? "gn_stats_partial" : "gn_stats_finish");
+    bsel(p.vec4, [&](auto V) {
+        k_stats<V()><<<grid, kThreads, 0, s>>>(a.x, w.part, a.mean, a.rstd, a.mean_lo, w.lo,
+                                               p.HW, p.chunk, p.cpp, p.cpg, fin_u0, fin_nu,
+                                               u0 * bpu, a.eps);
+    });
+    prof_end(s, tok);
+}
+
+void launch_reduce(const Plan& p, const BwdArgs& a, const WsView& w, int64_t fin_u0,
+                   int64_t fin_nu, int64_t u0, int64_t nu, hipStream_t s) {
+    const int64_t bpu = p.cpg * p.cpp;
+    const bool silu = (a.flags & SOAR_GN_SILU) != 0;
+    const dim3 grid((unsigned)(fin_nu + nu * bpu));
+    const int tok = prof_begin(s, nu ? (silu ? "gn_silu_bwd_reduce" : "gn_bwd_reduce")
+                                     : "gn_bwd_finish");
+    bsel(p.vec4, [&](auto V) {
+        bsel(silu, [&](auto S) {
+            k_bwd_reduce<V(), S()><<<grid, kThreads, 0, s>>>(
+                a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, w.part, w.plane_sums,
+                w.unit_sums, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, fin_u0, fin_nu, u0 * bpu);
+        });
+    });
+    prof_end(s, tok);
+}
+
+// ---- two-stream pipeline --------------------------------------------------
+// A helper stream (default priority) runs the first pass of batch b+1
+// while the caller's stream runs the finish and second pass of batch b:
+//
+//   helper:  S0 --ev-- S1 --ev-- S2 ...            (S(b) waits for A(b-2))
+//   caller:       F0 A0     F1 A1     F2 A2 ...
+//
+// Events fork the helper off the caller's stream and every helper kernel
+// is waited on by the caller's stream, so when the call returns all work
+// is ordered before anything later on the caller's stream.
+struct Pipe {
+    std::mutex mu;
+    hipStream_t helper = nullptr;
+    hipEvent_t fork = nullptr;
+    hipEvent_t first[2] = {nullptr, nullptr};
+    hipEvent_t second[4] = {nullptr, nullptr, nullptr, nullptr};
+};
+
+hipError_t pipe_for_device(Pipe** out) {
+    static std::mutex mu;
+    static Pipe* pipes[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!pipes[dev]) {
+        Pipe* p = new Pipe;
+        e = hipStreamCreateWithFlags(&p->helper, hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&p->fork, hipEventDisableTiming);
+        for (auto& ev : p->first)
+            if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        for (auto& ev : p->second)
+            if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e != hipSuccess) return e;  // leaks the partial Pipe; the device is unusable anyway
+        pipes[dev] = p;
+    }
+    *out = pipes[dev];
+    return hipSuccess;
+}
+
+#define SOAR_TRY(x)                       \
+    do {                                  \
+        hipError_t e_ = (x);              \
+        if (e_ != hipSuccess) return e_;  \
+    } while (0)
 
 int64_t units_per_batch(const Plan& p, const Tuning& t, int tensors_read) {
     if (t.batch_mb <= 0) return p.units;
@@ -679,37 +778,43 @@ size_t workspace_bytes(const Plan& p) {
            align256(sizeof(float) * (size_t)p.units);
 }
 
-// Launch order for batches 0..B-1 (S = first pass, F = finish, A = second
-// pass):  S0, F0+S1, A0, F1+S2, A1, ..., F(B-1), A(B-1).
+// Single-stream launch order for batches 0..B-1 (S = first pass, F =
+// finish, A = second pass):  S0, F0+S1, A0, F1+S2, A1, ..., F(B-1), A(B-1).
+// With two streams (tuning `streams` = 2 and more than one batch) the
+// helper-stream pipeline above is used instead.
 hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a, hipStream_t s) {
     const WsView w = ws_view(p, a.ws);
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
-    const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
-    const bool nt = t.nt_store != 0;
     const int64_t bpu = p.cpg * p.cpp;  // chunk blocks per unit
+    const char* apply_name = silu ? "gn_silu_apply" : "gn_apply";
+    if (t.streams >= 2 && p.units > p.upb_fwd) {
+        Pipe* pp = nullptr;
+        SOAR_TRY(pipe_for_device(&pp));
+        std::lock_guard<std::mutex> lk(pp->mu);
+        SOAR_TRY(hipEventRecord(pp->fork, s));
+        SOAR_TRY(hipStreamWaitEvent(pp->helper, pp->fork, 0));
+        int64_t bi = 0;
+        for (int64_t u0 = 0; u0 < p.units; u0 += p.upb_fwd, ++bi) {
+            const int64_t nu = std::min(p.upb_fwd, p.units - u0);
+            if (bi >= 2) SOAR_TRY(hipStreamWaitEvent(pp->helper, pp->second[(bi - 2) % 4], 0));
+            launch_stats(p, a, w, 0, 0, u0, nu, pp->helper);
+            SOAR_TRY(hipEventRecord(pp->first[bi % 2], pp->helper));
+            SOAR_TRY(hipStreamWaitEvent(s, pp->first[bi % 2], 0));
+            launch_stats(p, a, w, u0, nu, 0, 0, s);
+            const int tok = prof_begin(s, apply_name);
+            launch_apply(p, t, a, w.lo, u0 * bpu, nu * bpu, s);
+            prof_end(s, tok);
+            SOAR_TRY(hipEventRecord(pp->second[bi % 4], s));
+        }
+        return hipGetLastError();
+    }
     int64_t prev_u0 = 0, prev_nu = 0;
     for (int64_t u0 = 0;; u0 += p.upb_fwd) {
         const int64_t nu = u0 < p.units ? std::min(p.upb_fwd, p.units - u0) : 0;
-        if (nu + prev_nu > 0) {
-            const dim3 grid((unsigned)(prev_nu + nu * bpu));
-            const int tok = prof_begin(s, nu ? "gn_stats_partial" : "gn_stats_finish");
-            if (p.vec4)
-                k_stats<true><<<grid, kThreads, 0, s>>>(a.x, w.part, a.mean, a.rstd, a.mean_lo,
-                                                        w.lo, p.HW, p.chunk, p.cpp, p.cpg,
-                                                        prev_u0, prev_nu, u0 * bpu, a.eps);
-            else
-                k_stats<false><<<grid, kThreads, 0, s>>>(a.x, w.part, a.mean, a.rstd, a.mean_lo,
-                                                         w.lo, p.HW, p.chunk, p.cpp, p.cpg,
-                                                         prev_u0, prev_nu, u0 * bpu, a.eps);
-            prof_end(s, tok);
-        }
+        if (nu + prev_nu > 0) launch_stats(p, a, w, prev_u0, prev_nu, u0, nu, s);
         if (prev_nu > 0) {
-            const dim3 grid((unsigned)(prev_nu * bpu));
-            const int tok = prof_begin(s, silu ? "gn_silu_apply" : "gn_apply");
-            if (p.vec4)
-                apply_dispatch<true>(silu, res, nt, grid, s, p, a, w.lo, prev_u0 * bpu, t.reverse);
-            else
-                apply_dispatch<false>(silu, res, nt, grid, s, p, a, w.lo, prev_u0 * bpu, t.reverse);
+            const int tok = prof_begin(s, apply_name);
+            launch_apply(p, t, a, w.lo, prev_u0 * bpu, prev_nu * bpu, s);
             prof_end(s, tok);
         }
         if (nu == 0) break;
@@ -719,51 +824,48 @@ hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a, hipS
     return hipGetLastError();
 }
 
-// Same batch order as the forward with R = reduction, D = dx:
-//   R0, F0+R1, D0, F1+R2, D1, ..., F(B-1), D(B-1), then the dgamma/dbeta
-// finish over all planes.
+// Same orders as the forward with R = reduction, D = dx, then the
+// dgamma/dbeta finish over all planes.
 hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hipStream_t s) {
     const WsView w = ws_view(p, a.ws);
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
-    const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
-    const bool accum = (a.flags & SOAR_GN_ACCUMULATE_DX) != 0;
-    const bool nt = t.nt_store != 0 && !accum;
     const int64_t bpu = p.cpg * p.cpp;
-    int64_t prev_u0 = 0, prev_nu = 0;
-    for (int64_t u0 = 0;; u0 += p.upb_bwd) {
-        const int64_t nu = u0 < p.units ? std::min(p.upb_bwd, p.units - u0) : 0;
-        if (nu + prev_nu > 0) {
-            const dim3 grid((unsigned)(prev_nu + nu * bpu));
-            const int tok = prof_begin(s, nu ? (silu ? "gn_silu_bwd_reduce" : "gn_bwd_reduce")
-                                             : "gn_bwd_finish");
-#define SOAR_RED(V, S)                                                                 \
-    k_bwd_reduce<V, S><<<grid, kThreads, 0, s>>>(                                      \
-        a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, w.part, w.plane_sums,   \
-        w.unit_sums, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, prev_u0, prev_nu, u0 * bpu)
-            if (p.vec4) {
-                if (silu) SOAR_RED(true, true); else SOAR_RED(true, false);
-            } else {
-                if (silu) SOAR_RED(false, true); else SOAR_RED(false, false);
+    const char* dx_name = silu ? "gn_silu_bwd_dx" : "gn_bwd_dx";
+    if (t.streams >= 2 && p.units > p.upb_bwd) {
+        Pipe* pp = nullptr;
+        SOAR_TRY(pipe_for_device(&pp));
+        std::lock_guard<std::mutex> lk(pp->mu);
+        SOAR_TRY(hipEventRecord(pp->fork, s));
+        SOAR_TRY(hipStreamWaitEvent(pp->helper, pp->fork, 0));
+        int64_t bi = 0;
+        for (int64_t u0 = 0; u0 < p.units; u0 += p.upb_bwd, ++bi) {
+            const int64_t nu = std::min(p.upb_bwd, p.units - u0);
+            if (bi >= 2) SOAR_TRY(hipStreamWaitEvent(pp->helper, pp->second[(bi - 2) % 4], 0));
+            launch_reduce(p, a, w, 0, 0, u0, nu, pp->helper);
+            SOAR_TRY(hipEventRecord(pp->first[bi % 2], pp->helper));
+            SOAR_TRY(hipStreamWaitEvent(s, pp->first[bi % 2], 0));
+            launch_reduce(p, a, w, u0, nu, 0, 0, s);
+            if (a.dx) {
+                const int tok = prof_begin(s, dx_name);
+                launch_dx(p, t, a, w.unit_sums, u0 * bpu, nu * bpu, s);
+                prof_end(s, tok);
             }
-#undef SOAR_RED
-            prof_end(s, tok);
+            SOAR_TRY(hipEventRecord(pp->second[bi % 4], s));
         }
-        if (prev_nu > 0 && a.dx) {
-            const dim3 grid((unsigned)(prev_nu * bpu));
-            const int64_t block0 = prev_u0 * bpu;
-            const int tok = prof_begin(s, silu ? "gn_silu_bwd_dx" : "gn_bwd_dx");
-            if (p.vec4) {
-                if (silu) dx_dispatch<true, true>(res, accum, nt, grid, s, p, a, w.unit_sums, block0, t.reverse);
-                else dx_dispatch<true, false>(res, accum, nt, grid, s, p, a, w.unit_sums, block0, t.reverse);
-            } else {
-                if (silu) dx_dispatch<false, true>(res, accum, nt, grid, s, p, a, w.unit_sums, block0, t.reverse);
-                else dx_dispatch<false, false>(res, accum, nt, grid, s, p, a, w.unit_sums, block0, t.reverse);
+    } else {
+        int64_t prev_u0 = 0, prev_nu = 0;
+        for (int64_t u0 = 0;; u0 += p.upb_bwd) {
+            const int64_t nu = u0 < p.units ? std::min(p.upb_bwd, p.units - u0) : 0;
+            if (nu + prev_nu > 0) launch_reduce(p, a, w, prev_u0, prev_nu, u0, nu, s);
+            if (prev_nu > 0 && a.dx) {
+                const int tok = prof_begin(s, dx_name);
+                launch_dx(p, t, a, w.unit_sums, prev_u0 * bpu, prev_nu * bpu, s);
+                prof_end(s, tok);
             }
-            prof_end(s, tok);
+            if (nu == 0) break;
+            prev_u0 = u0;
+            prev_nu = nu;
         }
-        if (nu == 0) break;
-        prev_u0 = u0;
-        prev_nu = nu;
     }
     if (a.dgamma) {
         const int tok = prof_begin(s, "gn_param_finish");

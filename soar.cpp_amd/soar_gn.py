@@ -36,6 +36,8 @@ TUNE_CHUNK = 1
 TUNE_REVERSE = 2
 TUNE_NT_STORE = 3
 TUNE_BATCH_MB = 4
+TUNE_STREAMS = 5
+TUNE_NT_LOAD = 6
 
 
 class SoarUnavailable(RuntimeError):

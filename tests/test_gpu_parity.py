@@ -492,7 +492,8 @@ def test_kernel_timing_records(gpu):
 
 @pytest.fixture
 def restore_tuning(gpu):
-    keys = (gpu.TUNE_CHUNK, gpu.TUNE_REVERSE, gpu.TUNE_NT_STORE, gpu.TUNE_BATCH_MB)
+    keys = (gpu.TUNE_CHUNK, gpu.TUNE_REVERSE, gpu.TUNE_NT_STORE, gpu.TUNE_BATCH_MB,
+            gpu.TUNE_STREAMS, gpu.TUNE_NT_LOAD)
     old = {k: gpu.tune_get(k) for k in keys}
     yield
     for k, v in old.items():
@@ -518,7 +519,8 @@ def test_tuning_variants_match(gpu, oracle, restore_tuning, residual):
     xd, dyd = dev(x).view(N, C, HW), dev(dy).view(N, C, HW)
     gd, bd = dev(gamma), dev(beta)
     base = _fwd_bwd(gpu, xd, gd, bd, dyd, G, residual)
-    for key, val in ((gpu.TUNE_BATCH_MB, 1), (gpu.TUNE_BATCH_MB, 2), (gpu.TUNE_REVERSE, 0),
+    for key, val in ((gpu.TUNE_BATCH_MB, 1), (gpu.TUNE_STREAMS, 2), (gpu.TUNE_BATCH_MB, 2),
+                     (gpu.TUNE_NT_LOAD, 1), (gpu.TUNE_STREAMS, 1), (gpu.TUNE_REVERSE, 0),
                      (gpu.TUNE_NT_STORE, 0)):
         gpu.tune(key, val)
         got = _fwd_bwd(gpu, xd, gd, bd, dyd, G, residual)
