@@ -537,3 +537,59 @@ def test_tuning_variants_match(gpu, oracle, restore_tuning, residual):
         assert_vals(host(dx), dxt, f"dx chunk {chunk}")
         assert_vals(host(dg), dgt, f"dgamma chunk {chunk}")
         assert_vals(host(db), dbt, f"dbeta chunk {chunk}")
+
+
+def test_full_size_config4_chain(gpu, oracle):
+    """six SOAR blocks x <- x + silu(gn(x)) at N=2, C=128,
+    H=W=1024, G=32, forward then backward, fused (SOAR_GN_RESIDUAL).
+    Every block: dgamma/dbeta over the whole tensor against the oracle fed
+    with that block's device input and upstream gradient; sum over each unit
+    of (dx - dy) vanishes; the first and last blocks' outputs at sampled
+    indices against closed forms."""
+    import torch
+    N, C, HW, G, B = 2, 128, 1024 * 1024, 32, 6
+    seed = 20261201 + 4
+    x0 = torch.empty((N, C, HW), device="cuda")
+    gpu.synth_normal(x0, seed, 1, 0.0, 1.0)
+    dy = torch.empty_like(x0)
+    gpu.synth_normal(dy, seed, 4, 0.0, 1e-2)
+    params = []
+    for b in range(B):
+        g = torch.empty(C, device="cuda")
+        be = torch.empty(C, device="cuda")
+        gpu.synth_uniform(g, seed + 1000 * b, 2, 0.5, 1.5)
+        gpu.synth_normal(be, seed + 1000 * b, 3, 0.0, 0.1)
+        params.append((g, be))
+    ws = gpu.workspace(N, C, HW, G)
+    acts, stats = [x0], []
+    for b in range(B):
+        y, st = gpu.gn_silu_forward(acts[-1], *params[b], G, eps=EPS, residual=True, ws=ws)
+        acts.append(y)
+        stats.append(st)
+    g_in = dy
+    rng = np.random.default_rng(seed)
+    idx = rng.integers(0, N * C * HW, 100000)
+    for b in reversed(range(B)):
+        dx, dg, db = gpu.gn_silu_backward(g_in, acts[b], *params[b], stats[b], G, residual=True,
+                                          ws=ws)
+        # sum over each unit of dx - dy = sum of the GroupNorm part = 0
+        d = (dx - g_in).view(N * G, -1).double()
+        assert torch.all(d.sum(1).abs() <= 1e-5 * d.abs().sum(1)), b
+        xh, gh = host(acts[b]).reshape(-1), host(g_in).reshape(-1)
+        gm, bt = host(params[b][0]), host(params[b][1])
+        _, mt, rt = oracle.gn_silu_fwd_f64(xh, gm, bt, N, C, HW, G, EPS, True, True,
+                                           want_y=False)
+        assert_stats(host(stats[b].mean), host(stats[b].rstd), mt, rt, f"block {b}")
+        _, dgt, dbt = oracle.gn_silu_bwd_f64(gh, xh, gm, bt, mt, rt, N, C, HW, G, True, True,
+                                             want_dx=False)
+        assert_vals(host(dg), dgt, f"block {b} dgamma")
+        assert_vals(host(db), dbt, f"block {b} dbeta")
+        if b in (0, B - 1):
+            c = (idx // HW) % C
+            u = (idx // (HW * C)) * G + c // (C // G)
+            xs = xh[idx].astype(np.float64)
+            z = gm[c] * ((xs - mt[u]) * rt[u]) + bt[c]
+            assert_vals(host(acts[b + 1]).reshape(-1)[idx], xs + z / (1 + np.exp(-z)),
+                        f"block {b} y")
+        del xh, gh
+        g_in = dx
