@@ -222,6 +222,7 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
 #define SOAR_TUNE_BATCH_MB 4 /* MiB per two-pass batch, 0 = whole tensor   */
 #define SOAR_TUNE_STREAMS 5  /* 2: overlap batches on a helper stream      */
 #define SOAR_TUNE_NT_LOAD 6  /* 1: non-temporal loads in the second passes */
+#define SOAR_TUNE_CHUNK2 7   /* elements per block-chunk of apply / dx     */
 SOAR_API int soar_gn_tune(int key, int64_t value);
 SOAR_API int64_t soar_gn_tune_get(int key);
 

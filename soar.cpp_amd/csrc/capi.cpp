@@ -573,6 +573,11 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
                 return fail(SOAR_EINVAL, "chunk must be a multiple of 1024 in [1024, 2^24]");
             g_tune.chunk = value;
             return ok();
+        case SOAR_TUNE_CHUNK2:
+            if (value < 1024 || value % 1024 || value > (1 << 24))
+                return fail(SOAR_EINVAL, "chunk2 must be a multiple of 1024 in [1024, 2^24]");
+            g_tune.chunk2 = value;
+            return ok();
         case SOAR_TUNE_REVERSE:
             if (value != 0 && value != 1) return fail(SOAR_EINVAL, "reverse must be 0 or 1");
             g_tune.reverse = (int)value;
@@ -603,6 +608,7 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
     std::lock_guard<std::mutex> lk(g_tune_mu);
     switch (key) {
         case SOAR_TUNE_CHUNK: return g_tune.chunk;
+        case SOAR_TUNE_CHUNK2: return g_tune.chunk2;
         case SOAR_TUNE_REVERSE: return g_tune.reverse;
         case SOAR_TUNE_NT_STORE: return g_tune.nt_store;
         case SOAR_TUNE_BATCH_MB: return g_tune.batch_mb;

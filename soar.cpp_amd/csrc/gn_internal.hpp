@@ -23,9 +23,12 @@ struct Plan {
     int64_t N = 0, C = 0, HW = 0, G = 0, cpg = 0;
     int64_t planes = 0;      // N * C
     int64_t units = 0;       // N * G
-    int64_t chunk = 0;       // floats per block-chunk
+    int64_t chunk = 0;       // floats per block-chunk (first passes)
     int64_t cpp = 0;         // chunks per plane
     int64_t blocks = 0;      // planes * cpp
+    int64_t chunk2 = 0;      // floats per block-chunk of the second passes
+    int64_t cpp2 = 0;        // (apply / dx), which need no partials and
+    int64_t blocks2 = 0;     // so may cut the planes differently
     int64_t upb_fwd = 0;     // units per forward batch
     int64_t upb_bwd = 0;     // units per backward batch
     bool vec4 = false;       // float4 path (HW % 4 == 0 and 16-byte pointers)
@@ -43,6 +46,8 @@ struct Plan {
 // (each extra pair of launches costs ~2.7 us, more than the MALL saves).
 struct Tuning {
     int64_t chunk = 8192;     // floats per block-chunk, multiple of 1024
+    int64_t chunk2 = 4096;    // same for the second passes (128-thread
+                              // blocks; 2.5-3.5% faster there than 256 / 8192)
     int reverse = 1;          // second passes walk a batch's blocks in
                               // reverse, starting on what was read last
     int nt_store = 1;         // non-temporal stores of y / dx
@@ -52,7 +57,8 @@ struct Tuning {
     int nt_load = 1;          // non-temporal loads in the second passes
 };
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;   // first passes (stats, reduction)
+constexpr int kThreads2 = 128;  // second passes (apply, dx)
 
 // Plan for a non-empty tensor.  Returns false if the grid would not fit.
 bool make_plan(int64_t N, int64_t C, int64_t HW, int64_t G,

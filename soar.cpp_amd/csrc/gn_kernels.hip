@@ -352,14 +352,14 @@ __device__ __forceinline__ PlaneCoef plane_coef(
 // Forward pass 2: y = f((x - mean) * (gamma*rstd) + beta) [+ x].
 // ======================================================================
 template <bool VEC, bool SILU, bool RES, bool NT, bool NTL>
-__global__ __launch_bounds__(kThreads) void k_apply(
+__global__ __launch_bounds__(kThreads2) void k_apply(
     const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ mean_lo,
     float* __restrict__ y, int64_t C, int64_t G, int64_t cpg, int64_t HW,
-    int64_t chunk, int64_t cpp, int64_t block0, int64_t nb, int reverse) {
+    int64_t chunk2, int64_t cpp2, int64_t block0, int64_t nb, int reverse) {
     const int64_t b = batch_block(block0, nb, reverse);
-    const Chunk ck = chunk_of(b, HW, chunk, cpp);
+    const Chunk ck = chunk_of(b, HW, chunk2, cpp2);
     const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
     // z = gamma*xhat + beta = (x - mu)*(gamma*r) + (beta + gamma*e)
     const float a = k.gm * k.r, mu = k.mu, bt = fmaf(k.gm, k.e, k.bt);
@@ -375,19 +375,19 @@ __global__ __launch_bounds__(kThreads) void k_apply(
         f4* y4 = reinterpret_cast<f4*>(y + base);
         const int64_t n4 = ck.len >> 2;
         int64_t i = t;
-        for (; i + 3 * kThreads < n4; i += 4 * kThreads) {
-            f4 v0 = load4<NTL>(&x4[i]), v1 = load4<NTL>(&x4[i + kThreads]),
-               v2 = load4<NTL>(&x4[i + 2 * kThreads]), v3 = load4<NTL>(&x4[i + 3 * kThreads]);
+        for (; i + 3 * kThreads2 < n4; i += 4 * kThreads2) {
+            f4 v0 = load4<NTL>(&x4[i]), v1 = load4<NTL>(&x4[i + kThreads2]),
+               v2 = load4<NTL>(&x4[i + 2 * kThreads2]), v3 = load4<NTL>(&x4[i + 3 * kThreads2]);
             f4 o0 = {f(v0.x), f(v0.y), f(v0.z), f(v0.w)};
             f4 o1 = {f(v1.x), f(v1.y), f(v1.z), f(v1.w)};
             f4 o2 = {f(v2.x), f(v2.y), f(v2.z), f(v2.w)};
             f4 o3 = {f(v3.x), f(v3.y), f(v3.z), f(v3.w)};
             store4<NT>(&y4[i], o0);
-            store4<NT>(&y4[i + kThreads], o1);
-            store4<NT>(&y4[i + 2 * kThreads], o2);
-            store4<NT>(&y4[i + 3 * kThreads], o3);
+            store4<NT>(&y4[i + kThreads2], o1);
+            store4<NT>(&y4[i + 2 * kThreads2], o2);
+            store4<NT>(&y4[i + 3 * kThreads2], o3);
         }
-        for (; i < n4; i += kThreads) {
+        for (; i < n4; i += kThreads2) {
             f4 v = load4<NTL>(&x4[i]);
             f4 o = {f(v.x), f(v.y), f(v.z), f(v.w)};
             store4<NT>(&y4[i], o);
@@ -395,7 +395,7 @@ __global__ __launch_bounds__(kThreads) void k_apply(
     } else {
         const float* xp = x + base;
         float* yp = y + base;
-        for (int64_t i = t; i < ck.len; i += kThreads) store1<NT>(&yp[i], f(xp[i]));
+        for (int64_t i = t; i < ck.len; i += kThreads2) store1<NT>(&yp[i], f(xp[i]));
     }
 }
 
@@ -513,15 +513,15 @@ __global__ void k_param_finish(const double2* __restrict__ plane_sums,
 // A = gamma_c*rstd, B = -rstd*S1/M, D = -rstd*S2/M.
 // ======================================================================
 template <bool VEC, bool SILU, bool RES, bool ACC, bool NT, bool NTL>
-__global__ __launch_bounds__(kThreads) void k_bwd_dx(
+__global__ __launch_bounds__(kThreads2) void k_bwd_dx(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ gamma, const float* __restrict__ beta,
     const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ mean_lo, const double2* __restrict__ unit_sums,
     float* __restrict__ dx, int64_t C, int64_t G, int64_t cpg, int64_t HW,
-    int64_t chunk, int64_t cpp, int64_t block0, int64_t nb, int reverse) {
+    int64_t chunk2, int64_t cpp2, int64_t block0, int64_t nb, int reverse) {
     const int64_t b = batch_block(block0, nb, reverse);
-    const Chunk ck = chunk_of(b, HW, chunk, cpp);
+    const Chunk ck = chunk_of(b, HW, chunk2, cpp2);
     const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
     const double2 S = unit_sums[k.u];
     const double Md = (double)(cpg * HW);
@@ -545,22 +545,22 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(
         f4* o4 = reinterpret_cast<f4*>(dx + base);
         const int64_t n4 = ck.len >> 2;
         int64_t i = t;
-        for (; i + kThreads < n4; i += 2 * kThreads) {
-            f4 v0 = load4<NTL>(&x4[i]), v1 = load4<NTL>(&x4[i + kThreads]);
-            f4 g0 = load4<NTL>(&g4[i]), g1 = load4<NTL>(&g4[i + kThreads]);
+        for (; i + kThreads2 < n4; i += 2 * kThreads2) {
+            f4 v0 = load4<NTL>(&x4[i]), v1 = load4<NTL>(&x4[i + kThreads2]);
+            f4 g0 = load4<NTL>(&g4[i]), g1 = load4<NTL>(&g4[i + kThreads2]);
             f4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0;
             if (ACC) {
                 p0 = o4[i];
-                p1 = o4[i + kThreads];
+                p1 = o4[i + kThreads2];
             }
             f4 r0 = {f(g0.x, v0.x, p0.x), f(g0.y, v0.y, p0.y),
                      f(g0.z, v0.z, p0.z), f(g0.w, v0.w, p0.w)};
             f4 r1 = {f(g1.x, v1.x, p1.x), f(g1.y, v1.y, p1.y),
                      f(g1.z, v1.z, p1.z), f(g1.w, v1.w, p1.w)};
             store4<NT>(&o4[i], r0);
-            store4<NT>(&o4[i + kThreads], r1);
+            store4<NT>(&o4[i + kThreads2], r1);
         }
-        for (; i < n4; i += kThreads) {
+        for (; i < n4; i += kThreads2) {
             f4 v0 = load4<NTL>(&x4[i]), g0 = load4<NTL>(&g4[i]);
             f4 p0 = {0.f, 0.f, 0.f, 0.f};
             if (ACC) p0 = o4[i];
@@ -572,7 +572,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(
         const float* xp = x + base;
         const float* gp = dy + base;
         float* op = dx + base;
-        for (int64_t i = t; i < ck.len; i += kThreads)
+        for (int64_t i = t; i < ck.len; i += kThreads2)
             store1<NT>(&op[i], f(gp[i], xp[i], ACC ? op[i] : 0.0f));
     }
 }
@@ -621,9 +621,9 @@ void launch_apply(const Plan& p, const Tuning& t, const FwdArgs& a, const float*
             bsel(res, [&](auto R) {
                 bsel(t.nt_store != 0, [&](auto N) {
                     bsel(V() && t.nt_load != 0, [&](auto L) {
-                        k_apply<V(), S(), R(), N(), L()><<<grid, kThreads, 0, s>>>(
+                        k_apply<V(), S(), R(), N(), L()><<<grid, kThreads2, 0, s>>>(
                             a.x, a.gamma, a.beta, a.mean, a.rstd, lo, a.y, p.C, p.G, p.cpg,
-                            p.HW, p.chunk, p.cpp, block0, nb, t.reverse);
+                            p.HW, p.chunk2, p.cpp2, block0, nb, t.reverse);
                     });
                 });
             });
@@ -643,10 +643,10 @@ void launch_dx(const Plan& p, const Tuning& t, const BwdArgs& a, const double2* 
                 bsel(accum, [&](auto A) {
                     bsel(t.nt_store != 0 && !accum, [&](auto N) {
                         bsel(V() && t.nt_load != 0, [&](auto L) {
-                            k_bwd_dx<V(), S(), R(), A(), N(), L()><<<grid, kThreads, 0, s>>>(
+                            k_bwd_dx<V(), S(), R(), A(), N(), L()><<<grid, kThreads2, 0, s>>>(
                                 a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo,
-                                unit_sums, a.dx, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, block0,
-                                nb, t.reverse);
+                                unit_sums, a.dx, p.C, p.G, p.cpg, p.HW, p.chunk2, p.cpp2,
+                                block0, nb, t.reverse);
                         });
                     });
                 });
@@ -757,6 +757,10 @@ bool make_plan(int64_t N, int64_t C, int64_t HW, int64_t G, const Tuning& t, Pla
     p->cpp = (HW + p->chunk - 1) / p->chunk;
     if (p->planes > (int64_t)0x7fffffff / p->cpp) return false;
     p->blocks = p->planes * p->cpp;
+    p->chunk2 = t.chunk2 < hw_up ? t.chunk2 : hw_up;
+    p->cpp2 = (HW + p->chunk2 - 1) / p->chunk2;
+    if (p->planes > (int64_t)0x7fffffff / p->cpp2) return false;
+    p->blocks2 = p->planes * p->cpp2;
     // a first-pass grid holds a batch's chunk blocks plus one finish block
     // per unit of the previous batch
     if (p->blocks + p->units > 0x7fffffff || C > 0x7fffffff) return false;
@@ -785,7 +789,7 @@ size_t workspace_bytes(const Plan& p) {
 hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a, hipStream_t s) {
     const WsView w = ws_view(p, a.ws);
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
-    const int64_t bpu = p.cpg * p.cpp;  // chunk blocks per unit
+    const int64_t bpu2 = p.cpg * p.cpp2;  // second-pass blocks per unit
     const char* apply_name = silu ? "gn_silu_apply" : "gn_apply";
     if (t.streams >= 2 && p.units > p.upb_fwd) {
         Pipe* pp = nullptr;
@@ -802,7 +806,7 @@ hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a, hipS
             SOAR_TRY(hipStreamWaitEvent(s, pp->first[bi % 2], 0));
             launch_stats(p, a, w, u0, nu, 0, 0, s);
             const int tok = prof_begin(s, apply_name);
-            launch_apply(p, t, a, w.lo, u0 * bpu, nu * bpu, s);
+            launch_apply(p, t, a, w.lo, u0 * bpu2, nu * bpu2, s);
             prof_end(s, tok);
             SOAR_TRY(hipEventRecord(pp->second[bi % 4], s));
         }
@@ -814,7 +818,7 @@ hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a, hipS
         if (nu + prev_nu > 0) launch_stats(p, a, w, prev_u0, prev_nu, u0, nu, s);
         if (prev_nu > 0) {
             const int tok = prof_begin(s, apply_name);
-            launch_apply(p, t, a, w.lo, prev_u0 * bpu, prev_nu * bpu, s);
+            launch_apply(p, t, a, w.lo, prev_u0 * bpu2, prev_nu * bpu2, s);
             prof_end(s, tok);
         }
         if (nu == 0) break;
@@ -829,7 +833,7 @@ hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a, hipS
 hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hipStream_t s) {
     const WsView w = ws_view(p, a.ws);
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
-    const int64_t bpu = p.cpg * p.cpp;
+    const int64_t bpu2 = p.cpg * p.cpp2;  // second-pass blocks per unit
     const char* dx_name = silu ? "gn_silu_bwd_dx" : "gn_bwd_dx";
     if (t.streams >= 2 && p.units > p.upb_bwd) {
         Pipe* pp = nullptr;
@@ -847,7 +851,7 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hip
             launch_reduce(p, a, w, u0, nu, 0, 0, s);
             if (a.dx) {
                 const int tok = prof_begin(s, dx_name);
-                launch_dx(p, t, a, w.unit_sums, u0 * bpu, nu * bpu, s);
+                launch_dx(p, t, a, w.unit_sums, u0 * bpu2, nu * bpu2, s);
                 prof_end(s, tok);
             }
             SOAR_TRY(hipEventRecord(pp->second[bi % 4], s));
@@ -859,7 +863,7 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hip
             if (nu + prev_nu > 0) launch_reduce(p, a, w, prev_u0, prev_nu, u0, nu, s);
             if (prev_nu > 0 && a.dx) {
                 const int tok = prof_begin(s, dx_name);
-                launch_dx(p, t, a, w.unit_sums, prev_u0 * bpu, prev_nu * bpu, s);
+                launch_dx(p, t, a, w.unit_sums, prev_u0 * bpu2, prev_nu * bpu2, s);
                 prof_end(s, tok);
             }
             if (nu == 0) break;

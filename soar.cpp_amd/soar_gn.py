@@ -38,6 +38,7 @@ TUNE_NT_STORE = 3
 TUNE_BATCH_MB = 4
 TUNE_STREAMS = 5
 TUNE_NT_LOAD = 6
+TUNE_CHUNK2 = 7
 
 
 class SoarUnavailable(RuntimeError):

@@ -91,6 +91,9 @@ def test_tuning_knobs(L):
     soar_gn.tune(soar_gn.TUNE_CHUNK, 4096)
     assert soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) == 65536 * 16 + 1024 + 2 * 256
     assert L.soar_gn_tune(soar_gn.TUNE_BATCH_MB, -1) == soar_gn.SOAR_EINVAL
+    assert L.soar_gn_tune(soar_gn.TUNE_CHUNK2, 1536) == soar_gn.SOAR_EINVAL
+    assert L.soar_gn_tune(soar_gn.TUNE_STREAMS, 3) == soar_gn.SOAR_EINVAL
+    assert soar_gn.tune_get(soar_gn.TUNE_CHUNK2) == 4096
     assert soar_gn.tune_get(soar_gn.TUNE_BATCH_MB) == 0
     soar_gn.tune(soar_gn.TUNE_CHUNK, old)
     assert soar_gn.tune_get(soar_gn.TUNE_CHUNK) == old
