@@ -36,8 +36,14 @@ CONFIGS = {
     "cfg3": (1, 64, 2048 * 2048, 16, "fwdbwd", False, 1),
     "cfg4_chain": (2, 128, 1024 * 1024, 32, "fwdbwd", True, 6),
     "cfg5": (1, 16, 2048 * 2048, 4, "fwdbwd", False, 1),
+    # CBA block with a pointwise conv (64 -> 64 channels) feeding config 3's
+    # GroupNorm+SiLU; C is C_out, the conv's C_in is CBA_C_IN
+    "cba_pw": (1, 64, 2048 * 2048, 16, "fwd", False, 1),
 }
-SEED_OF = {"cfg2_fwd": SEED + 2, "cfg3": SEED + 3, "cfg4_chain": SEED + 4, "cfg5": SEED + 5}
+SEED_OF = {"cfg2_fwd": SEED + 2, "cfg3": SEED + 3, "cfg4_chain": SEED + 4, "cfg5": SEED + 5,
+           "cba_pw": SEED + 6}
+CBA_C_IN = 64
+PEAK_MFMA_F32 = 157.3  # TFLOP/s, dense fp32 matrix
 
 # algorithmic tensor passes (units of T) each kernel makes per block of the
 # step, summed over its launches (a kernel runs once per unit batch)
@@ -131,6 +137,51 @@ class Step:
             g_in = g_out
 
 
+class CBAStep:
+    """Forward of a CBA block whose conv is pointwise: z = conv1x1(x),
+    y = SiLU(GroupNorm(z)), the GroupNorm statistics computed in the conv
+    epilogue (soar_pw_conv_gn_silu_forward)."""
+
+    def __init__(self, gn, N, C, HW, G, seed):
+        import torch
+        self.gn, self.G = gn, G
+        self.C_in, self.C_out, self.N, self.HW = CBA_C_IN, C, N, HW
+        self.x = torch.empty((N, self.C_in, HW), device="cuda")
+        gn.synth_normal(self.x, seed, 1, 0.0, 1.0)
+        self.w = torch.empty((C, self.C_in), device="cuda")
+        gn.synth_uniform(self.w, seed, 7, -self.C_in ** -0.5, self.C_in ** -0.5)
+        self.gamma = torch.empty(C, device="cuda")
+        self.beta = torch.empty(C, device="cuda")
+        gn.synth_uniform(self.gamma, seed, 2, 0.5, 1.5)
+        gn.synth_normal(self.beta, seed, 3, 0.0, 0.1)
+        self.z = torch.empty((N, C, HW), device="cuda")
+        self.y = torch.empty_like(self.z)
+        self.mean = torch.empty(N * G, device="cuda")
+        self.rstd = torch.empty(N * G, device="cuda")
+        self.mean_lo = torch.empty(N * G, device="cuda")
+        self.ws = torch.empty(gn.pw_conv_gn_workspace_bytes(N, C, HW, G), dtype=torch.uint8,
+                              device="cuda")
+        self.params = [None]
+        self.T = N * C * HW * 4
+
+    def algorithmic_bytes(self):
+        # conv: read x, write z; apply: read z, write y (weights are noise)
+        return (self.C_in + 3 * self.C_out) * self.N * self.HW * 4
+
+    def kernel_bytes(self, name):
+        nb = self.N * self.HW * 4
+        return {"pw_conv_gn_stats": (self.C_in + self.C_out) * nb,
+                "gn_silu_apply": 2 * self.C_out * nb}.get(name, 0)
+
+    def kernel_flops(self, name):
+        return 2 * self.C_in * self.C_out * self.N * self.HW if name == "pw_conv_gn_stats" else 0
+
+    def __call__(self):
+        self.gn.pw_conv_gn_silu_forward(self.x, self.w, None, self.gamma, self.beta, self.G,
+                                        eps=1e-5, z=self.z, y=self.y, mean=self.mean,
+                                        rstd=self.rstd, mean_lo=self.mean_lo, ws=self.ws)
+
+
 def cpu_baseline():
     """fp32 statement of the reference CPU path, one thread, on 4 of config
     3's 16 groups (the same per-group size, 1/4 of the tensor)."""
@@ -180,7 +231,10 @@ def main():
         return
 
     N, C, HW, G, passes, residual, blocks = CONFIGS[args.config]
-    step = Step(gn, N, C, HW, G, passes, residual, blocks, SEED_OF[args.config])
+    if args.config == "cba_pw":
+        step = CBAStep(gn, N, C, HW, G, SEED_OF[args.config])
+    else:
+        step = Step(gn, N, C, HW, G, passes, residual, blocks, SEED_OF[args.config])
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -223,11 +277,19 @@ def main():
         per_step = k["launches"] / args.steps
         # bytes of one launch: the kernel's passes over the tensor, split
         # evenly over its launches (equal-sized unit batches)
-        per_launch = PASSES.get(k["kernel"], 0) * step.T * blocks / per_step
+        if hasattr(step, "kernel_bytes"):
+            per_launch = step.kernel_bytes(k["kernel"])
+        else:
+            per_launch = PASSES.get(k["kernel"], 0) * step.T * blocks / per_step
         kinfo[k["kernel"]] = {"launches_per_step": per_step, "avg_launch_ms": round(avg, 5),
                               "bytes_per_launch": int(per_launch),
                               "GBps": round(per_launch / (avg * 1e-3) / 1e9, 1)
                               if per_launch else None}
+        flops = step.kernel_flops(k["kernel"]) if hasattr(step, "kernel_flops") else 0
+        if flops:
+            tf = flops / (avg * 1e-3) / 1e12
+            kinfo[k["kernel"]]["TFLOPs"] = round(tf, 2)
+            kinfo[k["kernel"]]["mfma_frac"] = round(tf / PEAK_MFMA_F32, 4)
     if kernels:
         dom = max(kernels, key=lambda k: k["total_ms"])
         kd = kinfo[dom["kernel"]]
@@ -238,6 +300,11 @@ def main():
                     "algorithmic_bytes_per_launch": kd["bytes_per_launch"],
                     "avg_launch_ms": kd["avg_launch_ms"],
                     "traffic": tr.get(dom["kernel"]) if tr else None}
+        if "mfma_frac" in kd:
+            # the conv is near the ridge: also its place under the fp32
+            # matrix-core roof
+            roofline["mfma"] = {"achieved": kd["TFLOPs"], "peak": PEAK_MFMA_F32,
+                                "unit": "TFLOP/s", "frac": kd["mfma_frac"]}
 
     cpu = None
     if not args.no_cpu_baseline and args.config == "cfg3":
@@ -260,10 +327,13 @@ def main():
         "config": {"workload": {"cfg3": "GroupNorm+SiLU fwd+bwd, BASELINE config 3",
                                 "cfg2_fwd": "GroupNorm+SiLU fwd, BASELINE config 2",
                                 "cfg4_chain": "6 x (x + SiLU(GN(x))) fwd+bwd, BASELINE config 4",
-                                "cfg5": "GroupNorm+SiLU fwd+bwd shape of BASELINE config 5"}
+                                "cfg5": "GroupNorm+SiLU fwd+bwd shape of BASELINE config 5",
+                                "cba_pw": "CBA fwd: pointwise conv 64->64 + GN + SiLU, GN stats "
+                                          "in the conv epilogue, config 3 GroupNorm shape"}
                    [args.config],
                    "N": N, "C": C, "H": int(HW ** 0.5), "W": int(HW ** 0.5), "G": G,
                    "eps": 1e-5, "blocks": blocks, "residual": residual,
+                   **({"C_in": CBA_C_IN} if args.config == "cba_pw" else {}),
                    "algorithmic_bytes_per_step": alg},
         "frac_of_peak": round(value / PEAK_GBS, 4),
         "wall_s_timed": round(wall, 4),

@@ -166,6 +166,46 @@ SOAR_API int soar_add_backward(const float* grad_y, float* grad_a,
 SOAR_API int soar_zero(float* ptr, size_t n, void* stream);
 SOAR_API int soar_fill(float* ptr, float value, size_t n, void* stream);
 
+/* ---- pointwise convolution, the producer of CBA's GroupNorm ---------- */
+/* The 1x1 / stride 1 / no-padding / groups 1 convolution of CBA blocks
+ * (Down.pw, LKR.pw1/pw2, Ctx.cv1/cv2; src/nn/blocks.cpp:429-480) is a GEMM
+ * over the pixel axis; it runs on the fp32 matrix cores (v_mfma_f32_32x32x2
+ * f32: fp32 products, fp32 accumulation).  weight is [C_out][C_in], bias
+ * [C_out] or NULL; activations are [C][HW] per sample. */
+
+/* out[co][p] = bias[co] + sum_ci weight[co][ci] * in[ci][p], one sample.
+ * Replaces: conv2d_1x1_forward (cuda_kernels.hpp:57-58,
+ * src/cuda/ops/convolution_kernels.cu:10-40), called by Conv2d::forward
+ * (src/nn/layers.cpp:351-352) when groups == 1, k == 1, stride 1, pad 0. */
+SOAR_API int soar_conv2d_1x1_forward(const float* in, const float* weight,
+                                     const float* bias, float* out,
+                                     size_t C_in, size_t C_out, size_t HW,
+                                     void* stream);
+
+/* Bytes of workspace soar_pw_conv_gn_silu_forward needs for this shape
+ * (0 for an invalid or empty shape). */
+SOAR_API size_t soar_pw_conv_gn_workspace_bytes(int64_t N, int64_t C_out,
+                                                int64_t HW, int64_t G);
+
+/* CBA forward of a pointwise convolution over N samples:
+ *   z = conv1x1(x; weight, bias)            [N][C_out][HW]
+ *   y = silu(GroupNorm_G(z; gamma, beta))   with SOAR_GN_SILU, else the
+ *                                           GroupNorm alone (CBA, act=false)
+ * The GroupNorm statistics of z are computed in the convolution's
+ * epilogue, so z is written once and read once (by the apply) instead of
+ * being read again for a statistics pass.  z, mean, rstd and mean_lo are
+ * what soar_gn_silu_backward(dy, z, ...) needs for the backward of the
+ * normalisation.  Flags: SOAR_GN_SILU only.
+ * Replaces: CBA::forward (src/nn/blocks.cpp:442-445) = Conv2d::forward
+ * (src/nn/layers.cpp:326-372) + GroupNorm::forward (layers.cpp:641-739)
+ * + SiLU::forward (layers.cpp:778-800). */
+SOAR_API int soar_pw_conv_gn_silu_forward(
+    const float* x, const float* weight, const float* bias,
+    const float* gamma, const float* beta, float* z, float* y, float* mean,
+    float* rstd, float* mean_lo, int64_t N, int64_t C_in, int64_t C_out,
+    int64_t HW, int64_t G, float eps, unsigned flags, void* workspace,
+    size_t workspace_bytes, void* stream);
+
 /* ---- device arena (replaces VulkanBuffer / CudaMemoryPool storage) ---- */
 /* One hipMalloc'd slab per arena, bump-allocated at `alignment` (a power
  * of two, 256 in the reference).  Allocations made before
@@ -223,6 +263,8 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
 #define SOAR_TUNE_STREAMS 5  /* 2: overlap batches on a helper stream      */
 #define SOAR_TUNE_NT_LOAD 6  /* 1: non-temporal loads in the second passes */
 #define SOAR_TUNE_CHUNK2 7   /* elements per block-chunk of apply / dx     */
+#define SOAR_TUNE_PW_CHUNK 8 /* pixels per wave of the pointwise conv      */
+                             /* (multiple of 128)                          */
 SOAR_API int soar_gn_tune(int key, int64_t value);
 SOAR_API int64_t soar_gn_tune_get(int key);
 

@@ -454,3 +454,39 @@ int ref_gn_silu_fwd_bwd_f32(const float* x, const float* gamma,
     if (bwd_seconds) *bwd_seconds = t2 - t1;
     return 0;
 }
+
+/* ------------------------------------------------------------------ */
+/* pointwise convolution                                               */
+/* ------------------------------------------------------------------ */
+
+int orc_conv1x1_fwd_f64(const float* x, const float* w, const float* b, int64_t N,
+                        int64_t C_in, int64_t C_out, int64_t HW, double* y) {
+    if (N < 0 || C_in <= 0 || C_out <= 0 || HW < 0) return -1;
+    double* acc = (double*)malloc(sizeof(double) * (size_t)(HW > 0 ? HW : 1));
+    if (!acc) return -2;
+    for (int64_t n = 0; n < N; ++n) {
+        for (int64_t co = 0; co < C_out; ++co) {
+            const double bias = b ? (double)b[co] : 0.0;
+            for (int64_t p = 0; p < HW; ++p) acc[p] = bias;
+            for (int64_t ci = 0; ci < C_in; ++ci) {
+                const double wv = (double)w[co * C_in + ci];
+                const float* xr = x + (n * C_in + ci) * HW;
+                for (int64_t p = 0; p < HW; ++p) acc[p] += wv * (double)xr[p];
+            }
+            memcpy(y + (n * C_out + co) * HW, acc, sizeof(double) * (size_t)HW);
+        }
+    }
+    free(acc);
+    return 0;
+}
+
+void ref_conv1x1_fwd_f32(const float* x, const float* w, const float* b, float* y,
+                         int64_t C_in, int64_t C_out, int64_t HW) {
+    for (int64_t idx = 0; idx < C_out * HW; ++idx) {
+        const int64_t co = idx / HW, hw = idx % HW;
+        float sum = b ? b[co] : 0.0f;
+        const float* w_row = w + co * C_in;
+        for (int64_t ci = 0; ci < C_in; ++ci) sum += w_row[ci] * x[ci * HW + hw];
+        y[idx] = sum;
+    }
+}

@@ -100,6 +100,18 @@ int ref_gn_silu_fwd_bwd_f32(const float* x, const float* gamma,
                             float* dgamma, float* dbeta, double* fwd_seconds,
                             double* bwd_seconds);
 
+/* ---- pointwise (1x1) convolution, the producer of CBA's GroupNorm ---- */
+
+/* float64 truth: y[n][co][p] = sum_ci w[co][ci] * x[n][ci][p] + b[co]
+ * (b may be NULL).  y is double[N*C_out*HW]. */
+int orc_conv1x1_fwd_f64(const float* x, const float* w, const float* b, int64_t N,
+                        int64_t C_in, int64_t C_out, int64_t HW, double* y);
+/* fp32 statement of the reference's k_conv2d_1x1_forward
+ * (src/cuda/ops/convolution_kernels.cu:10-31): sum = bias, then
+ * sum += w*x over ci in order, one sample. */
+void ref_conv1x1_fwd_f32(const float* x, const float* w, const float* b,
+                         float* y, int64_t C_in, int64_t C_out, int64_t HW);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,8 @@ def lib():
                                                   _opt(_F), _opt(_F), _I64, _I64, _I64]
         L.ref_add_f32.argtypes = [_F, _F, _F, _I64]
         L.ref_accumulate_f32.argtypes = [_F, _F, _I64]
+        L.orc_conv1x1_fwd_f64.argtypes = [_F, _F, _opt(_F), _I64, _I64, _I64, _I64, _D]
+        L.ref_conv1x1_fwd_f32.argtypes = [_F, _F, _opt(_F), _F, _I64, _I64, _I64]
         L.ref_gn_silu_fwd_bwd_f32.argtypes = [_F, _opt(_F), _opt(_F), _opt(_F), _I64, _I64,
                                               _I64, _I64, ctypes.c_float, ctypes.c_int, _F,
                                               _F, _F, _F, _F, _F, _opt(_F), _opt(_F),
@@ -193,3 +195,20 @@ def ref_gn_silu_fwd_bwd_f32(x, gamma, beta, dy, N, C, HW, G, eps, residual=False
     out["fwd_s"] = tf.value
     out["bwd_s"] = tb.value
     return out
+
+
+# ---- pointwise convolution ------------------------------------------------------
+
+def conv1x1_fwd_f64(x, w, b, N, C_in, C_out, HW):
+    y = np.empty(N * C_out * HW)
+    rc = lib().orc_conv1x1_fwd_f64(_f32(x).reshape(-1), _f32(w).reshape(-1), _f32(b), N, C_in,
+                                   C_out, HW, y)
+    assert rc == 0, rc
+    return y
+
+
+def ref_conv1x1_fwd_f32(x, w, b, C_in, C_out, HW):
+    y = np.empty(C_out * HW, dtype=np.float32)
+    lib().ref_conv1x1_fwd_f32(_f32(x).reshape(-1), _f32(w).reshape(-1), _f32(b), y, C_in, C_out,
+                              HW)
+    return y

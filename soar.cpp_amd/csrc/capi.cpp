@@ -339,6 +339,115 @@ SOAR_API int soar_group_norm_backward(const float* grad_out, const float* in,
                                  (int64_t)num_groups, SOAR_GN_ACCUMULATE_DX, ws, need, stream);
 }
 
+// ---- pointwise convolution --------------------------------------------------
+
+namespace {
+
+int check_pw_shape(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t* in_elems,
+                   int64_t* out_elems) {
+    if (N < 0 || C_in < 0 || C_out < 0 || HW < 0)
+        return fail(SOAR_EINVAL, "negative dimension (N=%lld C_in=%lld C_out=%lld HW=%lld)",
+                    (long long)N, (long long)C_in, (long long)C_out, (long long)HW);
+    int64_t a = 0, b = 0, c = 0, d = 0, wsz = 0;
+    if (__builtin_mul_overflow(N, C_in, &a) || __builtin_mul_overflow(a, HW, &b) ||
+        __builtin_mul_overflow(N, C_out, &c) || __builtin_mul_overflow(c, HW, &d) ||
+        __builtin_mul_overflow(C_in, C_out, &wsz) || b > INT64_MAX / 4 || d > INT64_MAX / 4 ||
+        wsz > INT64_MAX / 4)
+        return fail(SOAR_EINVAL, "pointwise convolution shape overflows");
+    if (!soar::gn::pw_offsets_fit(C_in, HW))
+        return fail(SOAR_EINVAL,
+                    "HW=%lld or C_in=%lld exceeds the pointwise kernel's 32-bit in-sample offsets",
+                    (long long)HW, (long long)C_in);
+    *in_elems = b;
+    *out_elems = d;
+    return SOAR_OK;
+}
+
+// Grid of the convolution: one wave per (sample, pixel chunk).
+bool pw_grid_fits(int64_t N, int64_t HW, int64_t chunk) {
+    const int64_t cpp = (HW + chunk - 1) / chunk;
+    return N <= (int64_t)0x7fffffff / std::max<int64_t>(cpp, 1);
+}
+
+}  // namespace
+
+SOAR_API int soar_conv2d_1x1_forward(const float* in, const float* weight, const float* bias,
+                                     float* out, size_t C_in, size_t C_out, size_t HW,
+                                     void* stream) {
+    if (C_in > (size_t)INT64_MAX || C_out > (size_t)INT64_MAX || HW > (size_t)INT64_MAX)
+        return fail(SOAR_EINVAL, "dimension too large");
+    int64_t ie = 0, oe = 0;
+    int rc = check_pw_shape(1, (int64_t)C_in, (int64_t)C_out, (int64_t)HW, &ie, &oe);
+    if (rc) return rc;
+    if (oe == 0) return ok();
+    if (C_in == 0) return fail(SOAR_EINVAL, "C_in must be positive");
+    if ((rc = require_device())) return rc;
+    if ((rc = check_dev(in, (size_t)ie * 4, "in")) ||
+        (rc = check_dev(weight, C_in * C_out * 4, "weight")) ||
+        (rc = check_dev_opt(bias, C_out * 4, "bias")) || (rc = check_dev(out, (size_t)oe * 4, "out")))
+        return rc;
+    const Tuning t = current_tuning();
+    if (!pw_grid_fits(1, (int64_t)HW, t.pw_chunk))
+        return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    soar::gn::PwArgs a{in, weight, bias, out};
+    hipError_t e = soar::gn::launch_pw_conv(a, 1, (int64_t)C_in, (int64_t)C_out, (int64_t)HW,
+                                            t.pw_chunk, nullptr, t,
+                                            static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "conv2d_1x1_forward launch");
+}
+
+SOAR_API size_t soar_pw_conv_gn_workspace_bytes(int64_t N, int64_t C_out, int64_t HW, int64_t G) {
+    int64_t elems = 0;
+    if (check_shape(N, C_out, HW, G, &elems) != SOAR_OK || elems == 0) return 0;
+    Plan p;
+    if (!soar::gn::make_pw_plan(N, C_out, HW, G, current_tuning(), &p)) return 0;
+    return soar::gn::workspace_bytes(p);
+}
+
+SOAR_API int soar_pw_conv_gn_silu_forward(const float* x, const float* weight,
+                                          const float* bias, const float* gamma,
+                                          const float* beta, float* z, float* y, float* mean,
+                                          float* rstd, float* mean_lo, int64_t N, int64_t C_in,
+                                          int64_t C_out, int64_t HW, int64_t G, float eps,
+                                          unsigned flags, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+    int64_t ie = 0, oe = 0, elems = 0;
+    int rc = check_pw_shape(N, C_in, C_out, HW, &ie, &oe);
+    if (rc) return rc;
+    if ((rc = check_shape(N, C_out, HW, G, &elems))) return rc;
+    if (flags & ~SOAR_GN_SILU)
+        return fail(SOAR_EINVAL, "unsupported flags 0x%x (SOAR_GN_SILU only)", flags);
+    if (!(eps >= 0.0f)) return fail(SOAR_EINVAL, "eps must be >= 0");
+    if (oe == 0) return ok();
+    if (C_in == 0) return fail(SOAR_EINVAL, "C_in must be positive");
+    if ((rc = require_device())) return rc;
+    const size_t sb = (size_t)(N * G) * sizeof(float);
+    if ((rc = check_dev(x, (size_t)ie * 4, "x")) ||
+        (rc = check_dev(weight, (size_t)(C_in * C_out) * 4, "weight")) ||
+        (rc = check_dev_opt(bias, (size_t)C_out * 4, "bias")) ||
+        (rc = check_dev_opt(gamma, (size_t)C_out * 4, "gamma")) ||
+        (rc = check_dev_opt(beta, (size_t)C_out * 4, "beta")) ||
+        (rc = check_dev(z, (size_t)oe * 4, "z")) || (rc = check_dev(y, (size_t)oe * 4, "y")) ||
+        (rc = check_dev(mean, sb, "mean")) || (rc = check_dev(rstd, sb, "rstd")) ||
+        (rc = check_dev_opt(mean_lo, sb, "mean_lo")))
+        return rc;
+    const Tuning t = current_tuning();
+    Plan p;
+    if (!soar::gn::make_pw_plan(N, C_out, HW, G, t, &p) || !pw_grid_fits(N, HW, p.chunk))
+        return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    p.vec4 = p.vec4 && aligned16(z) && aligned16(y);
+    if ((rc = check_ws(p, workspace, workspace_bytes))) return rc;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    soar::gn::PwArgs pa{x, weight, bias, z};
+    hipError_t e = soar::gn::launch_pw_conv(pa, N, C_in, C_out, HW, p.chunk,
+                                            soar::gn::ws_partials(p, workspace), t, s);
+    if (e != hipSuccess) return hip_fail(e, "pointwise convolution launch");
+    soar::gn::FwdArgs a{z, gamma, beta, y, mean, rstd, mean_lo, eps, flags, workspace};
+    e = soar::gn::launch_forward_from_partials(p, t, a, s);
+    if (e != hipSuccess) return hip_fail(e, "GroupNorm apply launch");
+    return ok();
+}
+
 #define SOAR_ELEMWISE_PRELUDE(n)                                   \
     if ((n) == 0) return ok();                                     \
     if ((size_t)(n) > (size_t)INT64_MAX / 4)                       \
@@ -599,6 +708,11 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
             if (value != 0 && value != 1) return fail(SOAR_EINVAL, "nt_load must be 0 or 1");
             g_tune.nt_load = (int)value;
             return ok();
+        case SOAR_TUNE_PW_CHUNK:
+            if (value < 128 || value % 128 || value > (1 << 20))
+                return fail(SOAR_EINVAL, "pw_chunk must be a multiple of 128 in [128, 2^20]");
+            g_tune.pw_chunk = value;
+            return ok();
         default:
             return fail(SOAR_EINVAL, "unknown tuning key %d", key);
     }
@@ -614,6 +728,7 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
         case SOAR_TUNE_BATCH_MB: return g_tune.batch_mb;
         case SOAR_TUNE_STREAMS: return g_tune.streams;
         case SOAR_TUNE_NT_LOAD: return g_tune.nt_load;
+        case SOAR_TUNE_PW_CHUNK: return g_tune.pw_chunk;
         default: return -1;
     }
 }

@@ -55,6 +55,9 @@ struct Tuning {
                               // (0: the whole tensor is one batch)
     int streams = 1;          // 2: pipeline batches over a helper stream
     int nt_load = 1;          // non-temporal loads in the second passes
+    int64_t pw_chunk = 1024;  // pixels per wave of the pointwise convolution
+                              // (multiple of 128); also its GroupNorm
+                              // partials' chunk
 };
 
 constexpr int kThreads = 256;   // first passes (stats, reduction)
@@ -97,6 +100,35 @@ hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a,
                           hipStream_t s);
 hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a,
                            hipStream_t s);
+
+// GroupNorm forward whose chunk partials are already in the workspace (the
+// pointwise convolution wrote them): the finish, then the apply, over all
+// units.
+hipError_t launch_forward_from_partials(const Plan& p, const Tuning& t, const FwdArgs& a,
+                                        hipStream_t s);
+// Chunk-partial region of the workspace (double2 x p.blocks).
+double2* ws_partials(const Plan& p, void* ws);
+// Plan of the GroupNorm that follows a pointwise convolution: the chunk is
+// the convolution's pixel chunk, so its epilogue partials are the plan's.
+bool make_pw_plan(int64_t N, int64_t C_out, int64_t HW, int64_t G, const Tuning& t, Plan* p);
+
+// Pointwise convolution (pw_conv.hip).
+struct PwArgs {
+    const float* x;     // [N][C_in][HW]
+    const float* w;     // [C_out][C_in]
+    const float* bias;  // [C_out], nullable
+    float* z;           // [N][C_out][HW]
+};
+// C_in rounded up to a multiple of 8 (the kernel's K step).
+int pw_kpad(int64_t C_in);
+// The kernel addresses one sample's planes with 32-bit byte offsets.
+bool pw_offsets_fit(int64_t C_in, int64_t HW);
+// z = w * x + bias.  With `part` non-null the kernel also writes the
+// GroupNorm chunk partials of z for chunks of `chunk` pixels (a multiple of
+// 128), part[(n*C_out + co)*cpp + k].
+hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
+                          int64_t HW, int64_t chunk, double2* part, const Tuning& t,
+                          hipStream_t s);
 
 // Elementwise kernels (elementwise.hip).
 hipError_t launch_silu_forward(const float* x, float* y, int64_t n,

@@ -218,11 +218,26 @@ __device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
     const int64_t P = cpg * cpp;  // chunk blocks per unit
     const int64_t first = u * P;
     Moments um{0.0, 0.0, 0.0};
-    for (int64_t j = threadIdx.x; j < P; j += kThreads) {
-        const int64_t k = j % cpp;
-        const double2 v = part[first + j];
-        Moments o{(double)min(chunk, HW - k * chunk), v.x, v.y};
-        um = chan(um, o);
+    // Eight independent loads in flight per thread, then their combine in
+    // index order (a load-combine-load loop would wait a full memory
+    // latency per partial).
+    constexpr int kUnroll = 8;
+    for (int64_t j0 = threadIdx.x; j0 < P; j0 += kUnroll * kThreads) {
+        double2 v[kUnroll];
+#pragma unroll
+        for (int i = 0; i < kUnroll; ++i) {
+            const int64_t j = j0 + (int64_t)i * kThreads;
+            v[i] = j < P ? part[first + j] : make_double2(0.0, 0.0);
+        }
+#pragma unroll
+        for (int i = 0; i < kUnroll; ++i) {
+            const int64_t j = j0 + (int64_t)i * kThreads;
+            if (j < P) {
+                const int64_t k = j % cpp;
+                Moments o{(double)min(chunk, HW - k * chunk), v[i].x, v[i].y};
+                um = chan(um, o);
+            }
+        }
     }
     Moments ur = block_reduce(um, lds);
     if (threadIdx.x == 0) {
@@ -826,6 +841,26 @@ hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a, hipS
         prev_nu = nu;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_forward_from_partials(const Plan& p, const Tuning& t, const FwdArgs& a,
+                                        hipStream_t s) {
+    const WsView w = ws_view(p, a.ws);
+    launch_stats(p, a, w, 0, p.units, 0, 0, s);
+    const int tok = prof_begin(s, (a.flags & SOAR_GN_SILU) ? "gn_silu_apply" : "gn_apply");
+    launch_apply(p, t, a, w.lo, 0, p.blocks2, s);
+    prof_end(s, tok);
+    return hipGetLastError();
+}
+
+double2* ws_partials(const Plan& p, void* ws) { return ws_view(p, ws).part; }
+
+bool make_pw_plan(int64_t N, int64_t C_out, int64_t HW, int64_t G, const Tuning& t, Plan* p) {
+    Tuning tp = t;
+    tp.chunk = t.pw_chunk;
+    tp.batch_mb = 0;
+    if (!make_plan(N, C_out, HW, G, tp, p)) return false;
+    return p->chunk % 128 == 0;
 }
 
 // Same orders as the forward with R = reduction, D = dx, then the

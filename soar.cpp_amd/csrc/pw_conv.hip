@@ -1,0 +1,362 @@
+// pw_conv.hip - pointwise (1x1, stride 1, no padding) convolution on the
+// fp32 matrix cores of gfx950, with the GroupNorm statistics of its output
+// computed in the epilogue.
+//
+// The convolution of one sample is a GEMM  z[co][p] = b[co] + sum_ci
+// w[co][ci] * x[ci][p]  with the pixel axis p contiguous in HBM.  It runs on
+// v_mfma_f32_32x32x2f32 (full fp32 products and sums, no reduced-precision
+// inputs), so results stay within fp32 rounding of the reference's scalar
+// loop (src/cuda/ops/convolution_kernels.cu:10-31, src/nn/layers.cpp
+// :380-395).
+//
+// Work split.  One wave (a 64-thread block) owns one pixel chunk of one
+// sample, cut into 128-pixel items, and computes every output row for it,
+// 64 rows (two 32-row MFMA tiles) at a time.  Operand layout of the MFMA
+// (lane l = 32*h + j):
+//   a = W[row j of the tile][k = h]      b = X[k = h][pixel column j]
+//   c[r] = Z[row (r%4) + 8*(r/4) + 4*h][pixel column j]
+// The K axis is walked eight channels at a time: at k-step q half-wave h
+// supplies channel 4h + q, so the four k-steps of one half read four
+// consecutive channels of W with one 16-byte load.  Pixel column j of n-tile t is pixel
+// 4*j + t of the item, so one 16-byte load of x gives lane j its b operand
+// for all four n-tiles, and the four n-tile results of one row are again
+// four consecutive pixels: z is written with 16-byte stores.
+//
+// GroupNorm statistics (optional).  For each row the epilogue shifts the
+// item's values by the row's value at the item's first pixel (an exact
+// data value, so differences stay small when |mean| >> std), sums the
+// shifted values and their squares per lane, and transposes the per-lane
+// sums through LDS so lane l ends up owning row l of the tile.  Lane l then
+// folds the item into a float64 (count, mean, M2) triple with Chan's
+// formula.  After the chunk, lane l writes the row's triple as the chunk
+// partial part[(n*C_out + row)*cpp + chunk] - the layout the GroupNorm
+// finish kernel combines - so GroupNorm needs no separate statistics pass
+// over z.
+#include <algorithm>
+#include <type_traits>
+
+#include "gn_internal.hpp"
+#include "soar_gn.h"
+
+namespace soar {
+namespace gn {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16 __attribute__((ext_vector_type(16)));
+
+constexpr int kRowTile = 64;    // output rows per pass (two 32-row tiles)
+constexpr int kItem = 128;      // pixels per item (four 32-column tiles)
+constexpr int kRowGroup = 4;    // row tiles whose statistics a lane keeps
+constexpr int kLdsStride = 34;  // float2 per LDS row: 32 lanes + 2 pad
+
+struct Mom {
+    double n, mean, m2;
+};
+
+__device__ __forceinline__ Mom chan_merge(const Mom& a, const Mom& b) {
+    if (b.n == 0.0) return a;
+    if (a.n == 0.0) return b;
+    Mom r;
+    r.n = a.n + b.n;
+    const double f = b.n / r.n;
+    const double d = b.mean - a.mean;
+    r.mean = a.mean + d * f;
+    r.m2 = a.m2 + b.m2 + d * d * a.n * f;
+    return r;
+}
+
+// Row of the 64-row tile held in accumulator register r of m-tile mt by a
+// lane of half-wave h.
+__device__ __forceinline__ int tile_row(int mt, int r, int h) {
+    return mt * 32 + (r & 3) + 8 * (r >> 2) + 4 * h;
+}
+
+__device__ __forceinline__ f4 ld4(const float* base, uint32_t byte_off) {
+    return *reinterpret_cast<const f4*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+
+// One 64-row x 128-pixel item: z rows [row0, row0 + 64) of pixels
+// [p0, p0 + 128) of sample n, plus (STATS) the item's per-row shifted sums
+// transposed through LDS and the per-row shifts in ldsK.
+//
+// Addressing: every pointer below is uniform across the wave (scalar
+// registers) and each lane adds a 32-bit byte offset, so the loads and
+// stores use the scalar-base + vector-offset form and no 64-bit per-lane
+// addresses are held.  K is walked in steps of 8 channels: at k-step q of
+// step kk, half-wave h supplies channel kk + 4h + q.
+//
+// FAST (HW % 4 == 0, C_in % 8 == 0, 16-byte aligned x, w, z): no divergent
+// branch in the K loop.  A lane past the end of the plane loads the plane's
+// last 16 bytes and weight rows past C_out load row C_out - 1.  The general
+// path guards every scalar access and loads zeros instead.
+template <bool FAST, bool STATS, bool BIAS>
+__device__ __forceinline__ void pw_item(const float* __restrict__ xs, const float* __restrict__ ws,
+                                        const float* __restrict__ bias, float* __restrict__ zs,
+                                        int64_t row0, int64_t p0, int h, int j, int64_t C_in,
+                                        int64_t C_out, int64_t HW, int Kpad, float2* lds,
+                                        float* ldsK) {
+    // xs = x + n*C_in*HW + p0, ws = w + row0*C_in, zs = z + (n*C_out + row0)*HW + p0
+    const bool lane_px = p0 + 4 * j < HW;
+    const uint32_t hw4 = (uint32_t)HW * 4u;  // bytes per channel plane
+    // lane byte offsets: x at channel 4h, pixel 4j (clamped into the plane)
+    const uint32_t xo = (uint32_t)h * 4u * hw4 +
+                        4u * (uint32_t)(lane_px ? 4 * j : (FAST ? (int)(HW - 4 - p0) : 0));
+    const int64_t rlim = C_out - 1 - row0;  // last valid tile row
+    const bool w0ok = j <= rlim, w1ok = 32 + j <= rlim;
+    const uint32_t wo0 = ((uint32_t)(w0ok ? j : (int)rlim) * (uint32_t)C_in + 4u * h) * 4u;
+    const uint32_t wo1 = ((uint32_t)(w1ok ? 32 + j : (int)rlim) * (uint32_t)C_in + 4u * h) * 4u;
+    const uint32_t zo = (uint32_t)h * 4u * hw4 + 16u * (uint32_t)j;
+
+    // (the bias loads stay inside the item instead of being hoisted out of
+    // the pixel loop, where 32 bias values would stay live in registers)
+    const float* bias_i = bias;
+    asm volatile("" : "+s"(bias_i));
+    f16 acc[2][4];
+    {
+        const float* bb = bias_i + row0 + 4 * h;  // bias of tile row 4h
+        const bool full = rlim >= kRowTile - 1;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int c = tile_row(mt, r, 0);
+                float bv = 0.0f;
+                if (BIAS) bv = (full || c + 4 * h <= rlim) ? bb[c] : 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) acc[mt][t][r] = bv;
+            }
+        }
+    }
+
+    auto load_step = [&](int kk, f4 (&a)[2], f4 (&b)[4]) {
+        if (FAST) {
+            // Clamped lanes and rows load valid but unrelated data.  An MFMA
+            // output column depends only on its own b column and an output
+            // row only on its own a row, so those values only reach outputs
+            // that are neither stored nor counted in the statistics.
+            a[0] = ld4(ws + kk, wo0);
+            a[1] = ld4(ws + kk, wo1);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) b[q] = ld4(xs + (int64_t)(kk + q) * HW, xo);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t ci = kk + 4 * h + q;
+                const bool cv = ci < C_in;
+                a[0][q] = (cv && w0ok) ? ws[(int64_t)j * C_in + ci] : 0.0f;
+                a[1][q] = (cv && w1ok) ? ws[(int64_t)(32 + j) * C_in + ci] : 0.0f;
+                const float* xr = xs + ci * HW + 4 * j;
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    b[q][t] = (cv && p0 + 4 * j + t < HW) ? xr[t] : 0.0f;
+            }
+        }
+    };
+    auto mfma_step = [&](const f4 (&a)[2], const f4 (&b)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    acc[mt][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[mt][q], b[q][t],
+                                                                      acc[mt][t], 0, 0, 0);
+            }
+        }
+    };
+    // Ping-pong operand buffers: the loads of the next step are issued
+    // before the MFMAs of the current one, so their latency hides behind 32
+    // MFMAs.  Loads are never under a branch (past the end they reload the
+    // last step) and buffers are never copied, so the wait before each MFMA
+    // group covers only the older buffer.  sched_group_barrier keeps the
+    // order (the scheduler would otherwise sink each load next to its use).
+    const int klast = Kpad - 8;
+    auto sched = [] {
+        if (FAST) {
+            __builtin_amdgcn_sched_group_barrier(0x020, 6, 0);  // 6 vector loads
+            __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);  // then 32 MFMAs
+        }
+    };
+    f4 a0[2], b0[4], a1[2], b1[4];
+    load_step(0, a0, b0);
+    int kk = 0;
+    for (; kk + 8 < Kpad; kk += 16) {
+        load_step(kk + 8, a1, b1);
+        mfma_step(a0, b0);
+        sched();
+        load_step(min(kk + 16, klast), a0, b0);
+        mfma_step(a1, b1);
+        sched();
+    }
+    if (kk < Kpad) mfma_step(a0, b0);  // odd number of steps
+
+    // ---- epilogue.  The row offsets below are computed here, not hoisted
+    // out of the item loop where 32 of them would stay live in registers.
+    int64_t hw_e = HW;
+    asm volatile("" : "+s"(hw_e));
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int tr0 = tile_row(mt, r, 0);  // half 1 holds row tr0 + 4
+            float* zr = reinterpret_cast<float*>(
+                reinterpret_cast<char*>(zs + (int64_t)tr0 * hw_e) + zo);
+            if (tr0 + 4 * h <= rlim) {
+                if (FAST) {
+                    if (lane_px) {
+                        const f4 v = {acc[mt][0][r], acc[mt][1][r], acc[mt][2][r],
+                                      acc[mt][3][r]};
+                        *reinterpret_cast<f4*>(zr) = v;
+                    }
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        if (p0 + 4 * j + t < HW) zr[t] = acc[mt][t][r];
+                }
+            }
+        }
+    }
+    if (STATS) {
+        // shift of each row: its value at the item's first pixel, which
+        // lane j = 0 of each half-wave holds; passed on through LDS
+        if (j == 0) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) ldsK[tile_row(mt, r, h)] = acc[mt][0][r];
+            }
+        }
+        __syncthreads();
+        // LDS addresses: one lane base plus constants, formed here so they
+        // are not hoisted out of the item loop
+        int lb = 4 * h;
+        asm volatile("" : "+v"(lb));
+        const float* kb = ldsK + lb;
+        float2* sb = lds + lb * kLdsStride + j;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int c = tile_row(mt, r, 0);
+                const float K = kb[c];
+                float s = 0.f, q = 0.f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const bool ok = FAST ? lane_px : (p0 + 4 * j + t < HW);
+                    const float d = ok ? acc[mt][t][r] - K : 0.0f;
+                    s += d;
+                    q = fmaf(d, d, q);
+                }
+                sb[c * kLdsStride] = make_float2(s, q);
+            }
+        }
+    }
+}
+
+// STATS: write GroupNorm chunk partials.  BIAS: bias is non-null.
+// Byte offsets inside one sample's planes must fit in 32 bits
+// (checked by the host with pw_offsets_fit).
+template <bool FAST, bool STATS, bool BIAS>
+__global__ __launch_bounds__(64, 2) void k_pw_conv(
+    const float* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ bias, float* __restrict__ z, double2* __restrict__ part,
+    int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk, int64_t cpp, int Kpad) {
+    __shared__ __attribute__((aligned(16))) float2 lds[kRowTile * kLdsStride];
+    __shared__ float ldsK[kRowTile];            // per-row shifts of the item
+    __shared__ Mom ldsM[kRowGroup * kRowTile];  // row-owner running moments
+
+    const int lane = threadIdx.x;
+    const int h = lane >> 5, j = lane & 31;
+    const int64_t n = (int64_t)blockIdx.x / cpp;
+    const int64_t kc = (int64_t)blockIdx.x - n * cpp;
+    const int64_t px0 = kc * chunk;
+    const int64_t pend = min(px0 + chunk, HW);
+    const int64_t R = (C_out + kRowTile - 1) / kRowTile;
+    const float* xn = x + n * C_in * HW;
+    float* zn = z + n * C_out * HW;
+
+    for (int64_t rg = 0; rg < R; rg += kRowGroup) {
+        const int nrt = (int)min<int64_t>(kRowGroup, R - rg);
+        if (STATS) {
+#pragma unroll
+            for (int g = 0; g < kRowGroup; ++g) ldsM[g * kRowTile + lane] = Mom{0.0, 0.0, 0.0};
+        }
+        for (int64_t p0 = px0; p0 < pend; p0 += kItem) {
+            const int nvalid = (int)min<int64_t>(kItem, HW - p0);
+            for (int g = 0; g < nrt; ++g) {
+                const int64_t row0 = (rg + g) * kRowTile;
+                pw_item<FAST, STATS, BIAS>(xn + p0, w + row0 * C_in, bias, zn + row0 * HW + p0,
+                                           row0, p0, h, j, C_in, C_out, HW, Kpad, lds, ldsK);
+                if (STATS) {
+                    __syncthreads();
+                    // lane owns row `lane` of the tile
+                    float S = 0.f, Q = 0.f;
+                    const float4* src = reinterpret_cast<const float4*>(lds + lane * kLdsStride);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const float4 u = src[i];
+                        S += u.x + u.z;
+                        Q += u.y + u.w;
+                    }
+                    const double cnt = (double)nvalid;
+                    Mom m;
+                    m.n = cnt;
+                    m.mean = (double)ldsK[lane] + (double)S / cnt;
+                    m.m2 = fmax((double)Q - (double)S * (double)S / cnt, 0.0);
+                    Mom& acc = ldsM[g * kRowTile + lane];
+                    acc = chan_merge(acc, m);
+                    __syncthreads();
+                }
+            }
+        }
+        if (STATS) {
+            for (int g = 0; g < nrt; ++g) {
+                const int64_t row = (rg + g) * kRowTile + lane;
+                const Mom m = ldsM[g * kRowTile + lane];
+                if (row < C_out) part[(n * C_out + row) * cpp + kc] = make_double2(m.mean, m.m2);
+            }
+        }
+    }
+}
+
+template <typename F>
+void bsel(bool b, F&& f) {
+    if (b)
+        f(std::true_type{});
+    else
+        f(std::false_type{});
+}
+
+}  // namespace
+
+int pw_kpad(int64_t C_in) { return (int)((C_in + 7) / 8 * 8); }
+
+bool pw_offsets_fit(int64_t C_in, int64_t HW) {
+    return HW <= ((int64_t)1 << 32) / 20 - 4 && C_in <= ((int64_t)1 << 32) / 256;
+}
+
+hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
+                          int64_t HW, int64_t chunk, double2* part, const Tuning& t,
+                          hipStream_t s) {
+    if (N == 0 || HW == 0 || C_out == 0) return hipSuccess;
+    const int64_t cpp = (HW + chunk - 1) / chunk;
+    const dim3 grid((unsigned)(N * cpp));
+    const bool fast = (HW % 4 == 0) && (C_in % 8 == 0) && ((uintptr_t)a.x % 16 == 0) &&
+                      ((uintptr_t)a.z % 16 == 0) && ((uintptr_t)a.w % 16 == 0);
+    const int Kpad = pw_kpad(C_in);
+    const int tok = prof_begin(s, part ? "pw_conv_gn_stats" : "pw_conv");
+    bsel(fast, [&](auto F) {
+        bsel(part != nullptr, [&](auto S) {
+            bsel(a.bias != nullptr, [&](auto B) {
+                k_pw_conv<F(), S(), B()><<<grid, 64, 0, s>>>(a.x, a.w, a.bias, a.z, part, C_in,
+                                                            C_out, HW, chunk, cpp, Kpad);
+            });
+        });
+    });
+    prof_end(s, tok);
+    return hipGetLastError();
+}
+
+}  // namespace gn
+}  // namespace soar

@@ -39,6 +39,7 @@ TUNE_BATCH_MB = 4
 TUNE_STREAMS = 5
 TUNE_NT_LOAD = 6
 TUNE_CHUNK2 = 7
+TUNE_PW_CHUNK = 8
 
 
 class SoarUnavailable(RuntimeError):
@@ -78,6 +79,11 @@ SIGNATURES = {
     "soar_add_backward": (_c.c_int, [_P, _P, _P, _SZ, _P]),
     "soar_zero": (_c.c_int, [_P, _SZ, _P]),
     "soar_fill": (_c.c_int, [_P, _c.c_float, _SZ, _P]),
+    "soar_conv2d_1x1_forward": (_c.c_int, [_P, _P, _P, _P, _SZ, _SZ, _SZ, _P]),
+    "soar_pw_conv_gn_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "soar_pw_conv_gn_silu_forward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+                                                _I64, _I64, _I64, _I64, _c.c_float, _c.c_uint,
+                                                _P, _SZ, _P]),
     "soar_arena_create": (_c.c_int, [_SZ, _SZ, _c.POINTER(_P)]),
     "soar_arena_alloc": (_c.c_int, [_P, _SZ, _c.POINTER(_P), _c.POINTER(_SZ)]),
     "soar_arena_freeze_static": (_c.c_int, [_P]),
@@ -265,6 +271,75 @@ def gn_silu_backward(dy, x, gamma, beta, stats, G, silu=True, residual=False,
                                       _stream(stream)))
     return (dx if want_dx else None, dgamma if want_params else None,
             dbeta if want_params else None)
+
+
+# ---- pointwise convolution ----------------------------------------------------
+
+def conv1x1_forward(x, weight, bias=None, out=None, stream=None):
+    """out[n] = weight @ x[n] + bias through soar_conv2d_1x1_forward, one call
+    per sample (the reference operator's signature is per sample).
+
+    x: [N, C_in, H, W], or one sample [C_in, H, W] / [C_in, HW]; weight:
+    [C_out, C_in] (or [C_out, C_in, 1, 1]); bias: [C_out] or None."""
+    import torch
+    if x.dim() not in (2, 3, 4):
+        raise ValueError("expected [N,C,H,W], [C,H,W] or [C,HW]")
+    squeeze = x.dim() < 4
+    xs = x.unsqueeze(0) if squeeze else x
+    N, C_in = xs.shape[0], xs.shape[1]
+    HW = 1
+    for d in xs.shape[2:]:
+        HW *= d
+    w = weight.reshape(weight.shape[0], -1)
+    C_out = w.shape[0]
+    if w.shape[1] != C_in:
+        raise ValueError("weight does not match the input channels")
+    for t, n in ((xs, "x"), (w, "weight"), (bias, "bias"), (out, "out")):
+        _check_tensor(t, n)
+    if out is None:
+        out = torch.empty((N, C_out) + tuple(xs.shape[2:]), dtype=torch.float32,
+                          device=x.device)
+    for n in range(N):
+        check(lib().soar_conv2d_1x1_forward(_ptr(xs[n]), _ptr(w), _ptr(bias), _ptr(out[n]),
+                                            C_in, C_out, HW, _stream(stream)))
+    return out[0] if squeeze else out
+
+
+def pw_conv_gn_workspace_bytes(N, C_out, HW, G) -> int:
+    return int(lib().soar_pw_conv_gn_workspace_bytes(N, C_out, HW, G))
+
+
+def pw_conv_gn_silu_forward(x, weight, bias, gamma, beta, G, eps=1e-5, silu=True, z=None,
+                            y=None, mean=None, rstd=None, mean_lo=None, ws=None,
+                            stream=None):
+    """CBA forward of a pointwise conv through soar_pw_conv_gn_silu_forward.
+
+    Returns (z, y, Stats): z the convolution output (the GroupNorm input the
+    backward needs), y = silu(group_norm(z)) (or group_norm(z))."""
+    import torch
+    N, C_in, HW = _nchw(x)
+    w = weight.reshape(weight.shape[0], -1)
+    C_out = w.shape[0]
+    if w.shape[1] != C_in:
+        raise ValueError("weight does not match the input channels")
+    for t, n in ((x, "x"), (w, "weight"), (bias, "bias"), (gamma, "gamma"), (beta, "beta"),
+                 (z, "z"), (y, "y"), (mean, "mean"), (rstd, "rstd"), (mean_lo, "mean_lo")):
+        _check_tensor(t, n)
+    shape = (N, C_out) + tuple(x.shape[2:])
+    new = lambda: torch.empty(N * G, dtype=torch.float32, device=x.device)
+    z = torch.empty(shape, dtype=torch.float32, device=x.device) if z is None else z
+    y = torch.empty(shape, dtype=torch.float32, device=x.device) if y is None else y
+    mean = new() if mean is None else mean
+    rstd = new() if rstd is None else rstd
+    mean_lo = new() if mean_lo is None else mean_lo
+    if ws is None:
+        ws = torch.empty(max(pw_conv_gn_workspace_bytes(N, C_out, HW, G), 1),
+                         dtype=torch.uint8, device=x.device)
+    check(lib().soar_pw_conv_gn_silu_forward(
+        _ptr(x), _ptr(w), _ptr(bias), _ptr(gamma), _ptr(beta), _ptr(z), _ptr(y), _ptr(mean),
+        _ptr(rstd), _ptr(mean_lo), N, C_in, C_out, HW, G, eps, GN_SILU if silu else 0,
+        _ptr(ws), ws.numel(), _stream(stream)))
+    return z, y, Stats(mean, rstd, mean_lo)
 
 
 def prof_enable(on: bool = True):

@@ -111,3 +111,54 @@ def test_reference_signature_validation(L):
     assert rc == soar_gn.SOAR_OK
     assert L.soar_add_backward(None, None, None, 10, None) == soar_gn.SOAR_OK
     assert L.soar_fill(None, 1.0, 0, None) == soar_gn.SOAR_OK
+
+
+# ---- pointwise convolution -------------------------------------------------------
+
+def _pw(L, N, C_in, C_out, HW, G, flags=1, eps=1e-5):
+    return L.soar_pw_conv_gn_silu_forward(None, None, None, None, None, None, None, None, None,
+                                          None, N, C_in, C_out, HW, G, eps, flags, None, 0,
+                                          None)
+
+
+def test_pw_conv_workspace_bytes(L):
+    assert soar_gn.tune_get(soar_gn.TUNE_PW_CHUNK) == 1024
+    # 64 output planes x 4096 chunks of 1024 pixels -> 262144 partials of
+    # 16 B, then plane sums, unit sums and mean residuals (256-byte aligned)
+    assert soar_gn.pw_conv_gn_workspace_bytes(1, 64, 2048 * 2048, 16) == (
+        262144 * 16 + 1024 + 2 * 256)
+    # a plane shorter than the chunk is one chunk
+    assert soar_gn.pw_conv_gn_workspace_bytes(2, 8, 100, 2) == 256 + 256 + 256 + 256
+    assert soar_gn.pw_conv_gn_workspace_bytes(1, 6, 10, 4) == 0  # C_out % G != 0
+    assert soar_gn.pw_conv_gn_workspace_bytes(0, 6, 10, 3) == 0
+
+
+def test_pw_conv_validation_without_gpu(L):
+    assert _pw(L, 1, 8, 6, 16, 4) == soar_gn.SOAR_EINVAL
+    assert "divisible" in soar_gn.last_error()
+    assert _pw(L, -1, 8, 6, 16, 3) == soar_gn.SOAR_EINVAL
+    assert _pw(L, 1, -8, 6, 16, 3) == soar_gn.SOAR_EINVAL
+    assert _pw(L, 1, 8, 6, 16, 3, flags=2) == soar_gn.SOAR_EINVAL  # residual is not fused here
+    assert "flags" in soar_gn.last_error()
+    assert _pw(L, 1, 8, 6, 16, 3, eps=-1.0) == soar_gn.SOAR_EINVAL
+    assert _pw(L, 1, 0, 6, 16, 3) == soar_gn.SOAR_EINVAL  # no input channels
+    assert _pw(L, 1, 1 << 42, 1 << 20, 1 << 20, 1) == soar_gn.SOAR_EINVAL  # overflow
+    # planes too long for the kernel's 32-bit in-sample offsets
+    assert _pw(L, 1, 8, 6, 1 << 28, 3) == soar_gn.SOAR_EINVAL
+    assert "32-bit" in soar_gn.last_error()
+    assert _pw(L, 0, 8, 6, 16, 3) == soar_gn.SOAR_OK  # empty
+    assert _pw(L, 1, 8, 6, 0, 3) == soar_gn.SOAR_OK
+    f = L.soar_conv2d_1x1_forward
+    assert f(None, None, None, None, 8, 6, 0, None) == soar_gn.SOAR_OK
+    assert f(None, None, None, None, 0, 6, 16, None) == soar_gn.SOAR_EINVAL
+    assert f(None, None, None, None, 8, 6, 1 << 28, None) == soar_gn.SOAR_EINVAL
+
+
+def test_pw_chunk_tuning(L):
+    assert L.soar_gn_tune(soar_gn.TUNE_PW_CHUNK, 100) == soar_gn.SOAR_EINVAL
+    assert L.soar_gn_tune(soar_gn.TUNE_PW_CHUNK, 0) == soar_gn.SOAR_EINVAL
+    soar_gn.tune(soar_gn.TUNE_PW_CHUNK, 2048)
+    assert soar_gn.pw_conv_gn_workspace_bytes(1, 64, 2048 * 2048, 16) == (
+        131072 * 16 + 1024 + 2 * 256)
+    soar_gn.tune(soar_gn.TUNE_PW_CHUNK, 1024)
+    assert soar_gn.tune_get(soar_gn.TUNE_PW_CHUNK) == 1024

@@ -1,0 +1,216 @@
+"""Parity of the pointwise convolution and the fused CBA forward
+(conv -> GroupNorm -> SiLU with the statistics in the conv epilogue) against
+the oracle, through the C-ABI of libsoar_gn.so.
+
+Bars (written here, used by every check):
+  z (fp32 GEMM, K = C_in terms): |z - z64| <= (C_in + 2) * 2^-24 * (|W| |x| + |b|)
+      (the fp32 bound of a K-term dot product, whatever the summation order)
+  stats of GroupNorm(z):  as tests/test_gpu_parity.py, 1e-5 relative
+  y:                      |d| <= 1e-4 * (1 + |truth|)
+The GroupNorm truth is computed by the oracle from the device's own z, so
+the GroupNorm bars are not loosened by the convolution's rounding.
+"""
+import numpy as np
+import pytest
+
+from test_gpu_parity import EPS, assert_stats, assert_vals, dev, host
+
+pytestmark = pytest.mark.gpu
+
+U32 = 2.0 ** -24
+
+
+def rng_inputs(seed, N, C_in, C_out, HW, bias=True, kind="normal"):
+    r = np.random.default_rng(seed)
+    if kind == "offset":
+        x = (1e3 + 1e-2 * r.standard_normal((N, C_in, HW))).astype(np.float32)
+    else:
+        x = r.standard_normal((N, C_in, HW)).astype(np.float32)
+    w = (r.uniform(-1.0, 1.0, (C_out, C_in)) / np.sqrt(C_in)).astype(np.float32)
+    b = r.uniform(-0.5, 0.5, C_out).astype(np.float32) if bias else None
+    return x, w, b
+
+
+def z_bound(x, w, b, C_in):
+    mag = np.einsum("oc,ncp->nop", np.abs(w).astype(np.float64), np.abs(x).astype(np.float64))
+    if b is not None:
+        mag += np.abs(b).astype(np.float64)[None, :, None]
+    return (C_in + 2) * U32 * mag
+
+
+def assert_z(z, x, w, b, oracle, what=""):
+    N, C_in, HW = x.shape
+    C_out = w.shape[0]
+    truth = oracle.conv1x1_fwd_f64(x, w, b, N, C_in, C_out, HW).reshape(N, C_out, HW)
+    err = np.abs(np.asarray(z, np.float64).reshape(N, C_out, HW) - truth)
+    bound = z_bound(x, w, b, C_in) + 1e-30
+    ratio = err / bound
+    i = np.unravel_index(int(np.argmax(ratio)), ratio.shape)
+    assert ratio[i] <= 1.0, f"{what} z err {err[i]:.3e} > bound {bound[i]:.3e} at {i}"
+
+
+CONV_SHAPES = [
+    # (C_in, C_out, HW, bias)
+    (64, 64, 4096, False),    # fast path, one full 64-row tile
+    (64, 64, 4096, True),
+    (16, 32, 1000, True),     # fast, partial row tile, ragged item
+    (24, 40, 4100, True),     # fast, odd number of K steps (3), partial tile
+    (8, 64, 128, False),      # a single K step
+    (64, 128, 2048, False),   # two row tiles
+    (128, 64, 3000, True),
+    (3, 5, 17, True),         # general path: C_in % 8, HW % 4
+    (72, 300, 515, True),     # general, five row tiles (two row groups)
+    (40, 24, 1, True),        # one pixel
+]
+
+
+@pytest.mark.parametrize("C_in,C_out,HW,bias", CONV_SHAPES)
+def test_conv1x1_matches_oracle(gpu, oracle, C_in, C_out, HW, bias):
+    print(f"conv1x1 C_in={C_in} C_out={C_out} HW={HW} bias={bias}", flush=True)
+    x, w, b = rng_inputs(C_in * 7 + HW, 1, C_in, C_out, HW, bias)
+    out = gpu.conv1x1_forward(dev(x[0]), dev(w), dev(b) if bias else None)
+    assert tuple(out.shape) == (C_out, HW)
+    assert_z(host(out)[None], x, w, b, oracle, f"C_in={C_in} C_out={C_out} HW={HW}")
+
+
+def test_conv1x1_per_sample_loop(gpu, oracle):
+    x, w, b = rng_inputs(5, 3, 16, 24, 777)
+    out = gpu.conv1x1_forward(dev(x).reshape(3, 16, 777, 1), dev(w), dev(b))
+    assert tuple(out.shape) == (3, 24, 777, 1)
+    assert_z(host(out), x, w, b, oracle, "N=3")
+
+
+FUSED_SHAPES = [
+    # (N, C_in, C_out, HW, G, kind, silu)
+    (1, 64, 64, 4096, 16, "normal", True),
+    (2, 32, 48, 2500, 12, "normal", True),     # partial tile, ragged last chunk
+    (1, 16, 24, 1030, 6, "normal", False),     # no activation (CBA act=False)
+    (1, 8, 16, 17, 4, "normal", True),         # general path
+    (1, 64, 64, 70000, 16, "offset", True),    # |mean| / std ~ 1e5
+    (1, 130, 72, 4096, 8, "normal", True),     # general path, two row tiles
+    (3, 16, 32, 1024, 8, "normal", True),      # exactly one chunk per plane
+]
+
+
+def fused_case(gpu, oracle, N, C_in, C_out, HW, G, kind, silu, seed=3):
+    x, w, b = rng_inputs(seed + HW, N, C_in, C_out, HW, True, kind)
+    r = np.random.default_rng(seed)
+    gamma = r.uniform(0.5, 1.5, C_out).astype(np.float32)
+    beta = (0.1 * r.standard_normal(C_out)).astype(np.float32)
+    z, y, st = gpu.pw_conv_gn_silu_forward(dev(x), dev(w), dev(b), dev(gamma), dev(beta), G,
+                                           eps=EPS, silu=silu)
+    return x, w, b, gamma, beta, z, y, st
+
+
+@pytest.mark.parametrize("N,C_in,C_out,HW,G,kind,silu", FUSED_SHAPES)
+def test_pw_conv_gn_silu_matches_oracle(gpu, oracle, N, C_in, C_out, HW, G, kind, silu):
+    print(f"pw_conv_gn N={N} C_in={C_in} C_out={C_out} HW={HW} G={G} {kind}", flush=True)
+    x, w, b, gamma, beta, z, y, st = fused_case(gpu, oracle, N, C_in, C_out, HW, G, kind,
+                                                silu)
+    zh = host(z)
+    assert_z(zh, x, w, b, oracle, "fused")
+    y_t, mean_t, rstd_t = oracle.gn_silu_fwd_f64(zh, gamma, beta, N, C_out, HW, G, EPS,
+                                                 silu=silu)
+    assert_stats(host(st.mean), host(st.rstd), mean_t, rstd_t, "fused")
+    assert_vals(host(y), y_t, "fused y")
+    # the saved statistics drive the existing backward: mean + mean_lo is
+    # the float64 mean to far below fp32 resolution
+    full = host(st.mean).astype(np.float64) + host(st.mean_lo)
+    sd = 1.0 / rstd_t
+    assert np.all(np.abs(full - mean_t) <= 1e-6 * sd + 1e-9 * np.abs(mean_t))
+
+
+@pytest.mark.parametrize("N,C_in,C_out,HW,G,kind,silu", FUSED_SHAPES[:3])
+def test_pw_conv_gn_matches_unfused_device_path(gpu, oracle, N, C_in, C_out, HW, G, kind,
+                                                silu):
+    """conv (reference signature) then soar_gn_silu_forward on the same z."""
+    x, w, b, gamma, beta, z, y, st = fused_case(gpu, oracle, N, C_in, C_out, HW, G, kind,
+                                                silu)
+    z2 = gpu.conv1x1_forward(dev(x).reshape(N, C_in, HW, 1), dev(w), dev(b)).reshape(z.shape)
+    assert np.array_equal(host(z), host(z2))  # same kernel, same operation order
+    y2, st2 = gpu.gn_silu_forward(z2, dev(gamma), dev(beta), G, eps=EPS, silu=silu)
+    assert_stats(host(st.mean), host(st.rstd), host(st2.mean).astype(np.float64),
+                 host(st2.rstd).astype(np.float64), "fused vs unfused")
+    assert_vals(host(y), host(y2), "fused vs unfused y")
+
+
+@pytest.mark.parametrize("chunk", [128, 512, 4096])
+def test_pw_chunk_changes_only_partial_order(gpu, oracle, chunk):
+    args = (1, 32, 32, 10000, 8, "normal", True)
+    _, _, _, _, _, z0, y0, st0 = fused_case(gpu, oracle, *args)
+    old = gpu.tune_get(gpu.TUNE_PW_CHUNK)
+    try:
+        gpu.tune(gpu.TUNE_PW_CHUNK, chunk)
+        _, _, _, _, _, z1, y1, st1 = fused_case(gpu, oracle, *args)
+    finally:
+        gpu.tune(gpu.TUNE_PW_CHUNK, old)
+    assert np.array_equal(host(z0), host(z1))
+    assert_stats(host(st1.mean), host(st1.rstd), host(st0.mean).astype(np.float64),
+                 host(st0.rstd).astype(np.float64), f"chunk {chunk}")
+    assert_vals(host(y1), host(y0), f"chunk {chunk} y")
+
+
+def test_pw_conv_full_size_cba(gpu):
+    """CBA pointwise conv at config 3's GroupNorm shape: 64 -> 64 channels at
+    2048x2048, G = 16.  z is spot-checked against float64 on 4096 random
+    pixel columns; statistics and y against the unfused device path (which
+    test_gpu_parity.py pins to the oracle at this size)."""
+    import torch
+    C, HW, G = 64, 2048 * 2048, 16
+    print("pw_conv full size 64->64 2048^2", flush=True)
+    x = torch.empty((1, C, 2048, 2048), dtype=torch.float32, device="cuda")
+    gpu.synth_normal(x, 1234, 1)
+    r = np.random.default_rng(9)
+    w = (r.uniform(-1, 1, (C, C)) / 8.0).astype(np.float32)
+    gamma = r.uniform(0.5, 1.5, C).astype(np.float32)
+    beta = (0.1 * r.standard_normal(C)).astype(np.float32)
+    z, y, st = gpu.pw_conv_gn_silu_forward(x, dev(w), None, dev(gamma), dev(beta), G, eps=EPS)
+    torch.cuda.synchronize()
+    cols = torch.from_numpy(np.sort(r.choice(HW, 4096, replace=False))).cuda()
+    xs = host(x.reshape(C, HW).index_select(1, cols)).astype(np.float64)
+    zs = host(z.reshape(C, HW).index_select(1, cols)).astype(np.float64)
+    truth = w.astype(np.float64) @ xs
+    bound = (C + 2) * U32 * (np.abs(w).astype(np.float64) @ np.abs(xs))
+    assert np.all(np.abs(zs - truth) <= bound)
+    y2, st2 = gpu.gn_silu_forward(z, dev(gamma), dev(beta), G, eps=EPS)
+    assert_stats(host(st.mean), host(st.rstd), host(st2.mean).astype(np.float64),
+                 host(st2.rstd).astype(np.float64), "full size")
+    d = (y - y2).abs().max().item()
+    assert d <= 1e-4 * (1.0 + y2.abs().max().item()), d
+    del x, z, y, y2
+
+
+def test_pw_conv_errors(gpu):
+    import ctypes
+    import torch
+    L = gpu.lib()
+    x = torch.zeros((1, 8, 16), device="cuda")
+    w = torch.zeros((16, 8), device="cuda")
+    out = torch.zeros((16, 16), device="cuda")
+    rc = L.soar_conv2d_1x1_forward(None, ctypes.c_void_p(w.data_ptr()), None,
+                                   ctypes.c_void_p(out.data_ptr()), 8, 16, 16, None)
+    assert rc == gpu.SOAR_EINVAL and "NULL" in gpu.last_error()
+    hostbuf = np.zeros(8 * 16, np.float32)
+    rc = L.soar_conv2d_1x1_forward(ctypes.c_void_p(hostbuf.ctypes.data),
+                                   ctypes.c_void_p(w.data_ptr()), None,
+                                   ctypes.c_void_p(out.data_ptr()), 8, 16, 16, None)
+    assert rc == gpu.SOAR_EINVAL and "not device memory" in gpu.last_error()
+    # an output whose allocation ends before the shape does (the arena gives
+    # an allocation whose end is known exactly): 16 x 16 floats do not fit
+    # in the last 512 bytes
+    arena = ctypes.c_void_p()
+    gpu.check(L.soar_arena_create(1 << 20, 256, ctypes.byref(arena)))
+    try:
+        p = ctypes.c_void_p()
+        gpu.check(L.soar_arena_alloc(arena, (1 << 20) - 512, ctypes.byref(p), None))
+        gpu.check(L.soar_arena_alloc(arena, 512, ctypes.byref(p), None))
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = L.soar_conv2d_1x1_forward(ctypes.c_void_p(x.data_ptr()),
+                                       ctypes.c_void_p(w.data_ptr()), None, p, 8, 16, 16, s)
+        assert rc == gpu.SOAR_EINVAL and "allocation holds" in gpu.last_error()
+        rc = L.soar_conv2d_1x1_forward(ctypes.c_void_p(x.data_ptr()),
+                                       ctypes.c_void_p(w.data_ptr()), None, p, 8, 8, 16, s)
+        assert rc == gpu.SOAR_OK  # 8 x 16 floats fit exactly
+        torch.cuda.synchronize()
+    finally:
+        gpu.check(L.soar_arena_destroy(arena))
