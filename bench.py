@@ -38,7 +38,7 @@ CONFIGS = {
     "cfg5": (1, 16, 2048 * 2048, 4, "fwdbwd", False, 1),
     # CBA block with a pointwise conv (64 -> 64 channels) feeding config 3's
     # GroupNorm+SiLU; C is C_out, the conv's C_in is CBA_C_IN
-    "cba_pw": (1, 64, 2048 * 2048, 16, "fwd", False, 1),
+    "cba_pw": (1, 64, 2048 * 2048, 16, "fwdbwd", False, 1),
 }
 SEED_OF = {"cfg2_fwd": SEED + 2, "cfg3": SEED + 3, "cfg4_chain": SEED + 4, "cfg5": SEED + 5,
            "cba_pw": SEED + 6}
@@ -138,9 +138,11 @@ class Step:
 
 
 class CBAStep:
-    """Forward of a CBA block whose conv is pointwise: z = conv1x1(x),
-    y = SiLU(GroupNorm(z)), the GroupNorm statistics computed in the conv
-    epilogue (soar_pw_conv_gn_silu_forward)."""
+    """Forward and backward of a CBA block whose conv is pointwise:
+    z = conv1x1(x), y = SiLU(GroupNorm(z)) with the GroupNorm statistics in
+    the conv epilogue (soar_pw_conv_gn_silu_forward); backward
+    soar_gn_silu_backward (dy -> dz, dgamma, dbeta) then
+    soar_pw_conv_backward (dz -> dx, dW)."""
 
     def __init__(self, gn, N, C, HW, G, seed):
         import torch
@@ -161,25 +163,47 @@ class CBAStep:
         self.mean_lo = torch.empty(N * G, device="cuda")
         self.ws = torch.empty(gn.pw_conv_gn_workspace_bytes(N, C, HW, G), dtype=torch.uint8,
                               device="cuda")
+        self.dy = torch.empty((N, C, HW), device="cuda")
+        gn.synth_normal(self.dy, seed, 4, 0.0, 1e-2)
+        self.dz = torch.empty_like(self.z)
+        self.dx = torch.empty_like(self.x)
+        self.dw = torch.zeros_like(self.w)
+        self.dgamma = torch.zeros(C, device="cuda")
+        self.dbeta = torch.zeros(C, device="cuda")
+        self.ws_gn = gn.workspace(N, C, HW, G)
+        self.ws_bwd = torch.empty(gn.pw_conv_backward_workspace_bytes(N, self.C_in, C, HW),
+                                  dtype=torch.uint8, device="cuda")
         self.params = [None]
         self.T = N * C * HW * 4
 
     def algorithmic_bytes(self):
-        # conv: read x, write z; apply: read z, write y (weights are noise)
-        return (self.C_in + 3 * self.C_out) * self.N * self.HW * 4
+        # fwd: conv reads x, writes z; apply reads z, writes y.
+        # bwd: GN reduce reads dy, z; GN dx reads dy, z, writes dz; conv dx
+        # reads dz, writes dx; conv dW reads dz, x.  (Weights are noise.)
+        ti, to = self.C_in, self.C_out
+        return (ti + 3 * to + 7 * to + 2 * ti) * self.N * self.HW * 4
 
     def kernel_bytes(self, name):
         nb = self.N * self.HW * 4
-        return {"pw_conv_gn_stats": (self.C_in + self.C_out) * nb,
-                "gn_silu_apply": 2 * self.C_out * nb}.get(name, 0)
+        ti, to = self.C_in * nb, self.C_out * nb
+        return {"pw_conv_gn_stats": ti + to, "gn_silu_apply": 2 * to,
+                "gn_silu_bwd_reduce": 2 * to, "gn_silu_bwd_dx": 3 * to,
+                "pw_conv_dgrad": to + ti, "pw_conv_wgrad": to + ti}.get(name, 0)
 
     def kernel_flops(self, name):
-        return 2 * self.C_in * self.C_out * self.N * self.HW if name == "pw_conv_gn_stats" else 0
+        f = 2 * self.C_in * self.C_out * self.N * self.HW
+        return f if name in ("pw_conv_gn_stats", "pw_conv_dgrad", "pw_conv_wgrad") else 0
 
     def __call__(self):
-        self.gn.pw_conv_gn_silu_forward(self.x, self.w, None, self.gamma, self.beta, self.G,
-                                        eps=1e-5, z=self.z, y=self.y, mean=self.mean,
-                                        rstd=self.rstd, mean_lo=self.mean_lo, ws=self.ws)
+        gn = self.gn
+        gn.pw_conv_gn_silu_forward(self.x, self.w, None, self.gamma, self.beta, self.G,
+                                   eps=1e-5, z=self.z, y=self.y, mean=self.mean, rstd=self.rstd,
+                                   mean_lo=self.mean_lo, ws=self.ws)
+        gn.gn_silu_backward(self.dy, self.z, self.gamma, self.beta,
+                            (self.mean, self.rstd, self.mean_lo), self.G, dx=self.dz,
+                            dgamma=self.dgamma, dbeta=self.dbeta, ws=self.ws_gn)
+        gn.pw_conv_backward(self.dz, self.x, self.w, dx=self.dx, dweight=self.dw, want_db=False,
+                            ws=self.ws_bwd)
 
 
 def cpu_baseline():
@@ -328,8 +352,8 @@ def main():
                                 "cfg2_fwd": "GroupNorm+SiLU fwd, BASELINE config 2",
                                 "cfg4_chain": "6 x (x + SiLU(GN(x))) fwd+bwd, BASELINE config 4",
                                 "cfg5": "GroupNorm+SiLU fwd+bwd shape of BASELINE config 5",
-                                "cba_pw": "CBA fwd: pointwise conv 64->64 + GN + SiLU, GN stats "
-                                          "in the conv epilogue, config 3 GroupNorm shape"}
+                                "cba_pw": "CBA fwd+bwd: pointwise conv 64->64 + GN + SiLU, GN "
+                                          "stats in the conv epilogue, config 3 GroupNorm shape"}
                    [args.config],
                    "N": N, "C": C, "H": int(HW ** 0.5), "W": int(HW ** 0.5), "G": G,
                    "eps": 1e-5, "blocks": blocks, "residual": residual,

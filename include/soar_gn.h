@@ -206,6 +206,38 @@ SOAR_API int soar_pw_conv_gn_silu_forward(
     int64_t HW, int64_t G, float eps, unsigned flags, void* workspace,
     size_t workspace_bytes, void* stream);
 
+/* Bytes of workspace soar_pw_conv_backward needs (0 for a bad shape). */
+SOAR_API size_t soar_pw_conv_backward_workspace_bytes(int64_t N, int64_t C_in,
+                                                      int64_t C_out, int64_t HW);
+
+/* Backward of the pointwise convolution over N samples, dz = dL/dz:
+ *   dx   = W^T dz   [N][C_in][HW]; written, or added with
+ *                   SOAR_GN_ACCUMULATE_DX; NULL skips it
+ *   dw  += sum_n dz x^T  [C_out][C_in]; NULL skips it
+ *   db  += sum_n,p dz    [C_out];       NULL skips it
+ * dx runs on the same fp32 matrix-core kernel as the forward (with W^T);
+ * dw is a split-K matrix-core product over pixel chunks whose fp32 partials
+ * are added in a fixed order in float64, so results are reproducible.
+ * Replaces: conv2d_1x1_backward (cuda_kernels.hpp:59-61,
+ * src/cuda/ops/convolution_kernels.cu:42-133) as Conv2dNode::backward calls
+ * it (src/nn/layers.cpp:34-85), batched over samples. */
+SOAR_API int soar_pw_conv_backward(const float* dz, const float* x,
+                                   const float* weight, float* dx,
+                                   float* dweight, float* dbias, int64_t N,
+                                   int64_t C_in, int64_t C_out, int64_t HW,
+                                   unsigned flags, void* workspace,
+                                   size_t workspace_bytes, void* stream);
+
+/* Reference signature, one sample: grad_in += W^T grad_out,
+ * grad_weight += grad_out in^T, grad_bias += sum grad_out; any of the
+ * three may be NULL.  Workspace owned by the library.
+ * Replaces: conv2d_1x1_backward (cuda_kernels.hpp:59-61). */
+SOAR_API int soar_conv2d_1x1_backward(const float* grad_out, const float* in,
+                                      const float* weight, float* grad_in,
+                                      float* grad_weight, float* grad_bias,
+                                      size_t C_in, size_t C_out, size_t HW,
+                                      void* stream);
+
 /* ---- device arena (replaces VulkanBuffer / CudaMemoryPool storage) ---- */
 /* One hipMalloc'd slab per arena, bump-allocated at `alignment` (a power
  * of two, 256 in the reference).  Allocations made before

@@ -490,3 +490,71 @@ void ref_conv1x1_fwd_f32(const float* x, const float* w, const float* b, float* 
         y[idx] = sum;
     }
 }
+
+int orc_conv1x1_bwd_f64(const float* dz, const float* x, const float* w, int64_t N,
+                        int64_t C_in, int64_t C_out, int64_t HW, double* dx, double* dw,
+                        double* db) {
+    if (N < 0 || C_in <= 0 || C_out <= 0 || HW < 0) return -1;
+    if (dx) {
+        for (int64_t n = 0; n < N; ++n)
+            for (int64_t ci = 0; ci < C_in; ++ci) {
+                double* o = dx + (n * C_in + ci) * HW;
+                for (int64_t p = 0; p < HW; ++p) o[p] = 0.0;
+                for (int64_t co = 0; co < C_out; ++co) {
+                    const double wv = (double)w[co * C_in + ci];
+                    const float* g = dz + (n * C_out + co) * HW;
+                    for (int64_t p = 0; p < HW; ++p) o[p] += wv * (double)g[p];
+                }
+            }
+    }
+    if (dw) {
+        for (int64_t co = 0; co < C_out; ++co)
+            for (int64_t ci = 0; ci < C_in; ++ci) {
+                double acc = 0.0;
+                for (int64_t n = 0; n < N; ++n) {
+                    const float* g = dz + (n * C_out + co) * HW;
+                    const float* xr = x + (n * C_in + ci) * HW;
+                    double part = 0.0;
+                    for (int64_t p = 0; p < HW; ++p) part += (double)g[p] * (double)xr[p];
+                    acc += part;
+                }
+                dw[co * C_in + ci] = acc;
+            }
+    }
+    if (db) {
+        for (int64_t co = 0; co < C_out; ++co) {
+            double acc = 0.0;
+            for (int64_t n = 0; n < N; ++n) acc += span_sum(dz + (n * C_out + co) * HW, HW);
+            db[co] = acc;
+        }
+    }
+    return 0;
+}
+
+void ref_conv1x1_bwd_f32(const float* grad_out, const float* in, const float* w,
+                         float* grad_in, float* grad_weight, float* grad_bias,
+                         int64_t C_in, int64_t C_out, int64_t HW) {
+    if (grad_in && w) {
+        for (int64_t idx = 0; idx < C_in * HW; ++idx) {
+            const int64_t ci = idx / HW, hw = idx % HW;
+            float sum = 0.0f;
+            for (int64_t co = 0; co < C_out; ++co) sum += w[co * C_in + ci] * grad_out[co * HW + hw];
+            grad_in[idx] += sum;
+        }
+    }
+    if (grad_weight && in) {
+        for (int64_t co = 0; co < C_out; ++co)
+            for (int64_t ci = 0; ci < C_in; ++ci) {
+                float sum = 0.0f;
+                for (int64_t p = 0; p < HW; ++p) sum += grad_out[co * HW + p] * in[ci * HW + p];
+                grad_weight[co * C_in + ci] += sum;
+            }
+    }
+    if (grad_bias) {
+        for (int64_t co = 0; co < C_out; ++co) {
+            float sum = 0.0f;
+            for (int64_t p = 0; p < HW; ++p) sum += grad_out[co * HW + p];
+            grad_bias[co] += sum;
+        }
+    }
+}

@@ -112,6 +112,20 @@ int orc_conv1x1_fwd_f64(const float* x, const float* w, const float* b, int64_t 
 void ref_conv1x1_fwd_f32(const float* x, const float* w, const float* b,
                          float* y, int64_t C_in, int64_t C_out, int64_t HW);
 
+/* float64 truth of the backward, N samples: dx = W^T dz, dw = sum_n dz x^T,
+ * db = sum_n,p dz.  Outputs are written (not accumulated); any may be NULL. */
+int orc_conv1x1_bwd_f64(const float* dz, const float* x, const float* w, int64_t N,
+                        int64_t C_in, int64_t C_out, int64_t HW, double* dx, double* dw,
+                        double* db);
+/* fp32 statement of the reference's conv2d_1x1_backward kernels
+ * (src/cuda/ops/convolution_kernels.cu:42-133), one sample, accumulating:
+ * grad_in[ci][p] += sum_co w[co][ci]*go[co][p] (co ascending),
+ * grad_weight[co][ci] += sum_p go[co][p]*x[ci][p], grad_bias[co] += sum_p go.
+ * Pointers may be NULL (that gradient is skipped). */
+void ref_conv1x1_bwd_f32(const float* grad_out, const float* in, const float* w,
+                         float* grad_in, float* grad_weight, float* grad_bias,
+                         int64_t C_in, int64_t C_out, int64_t HW);
+
 #ifdef __cplusplus
 }
 #endif

@@ -68,6 +68,10 @@ def lib():
         L.ref_accumulate_f32.argtypes = [_F, _F, _I64]
         L.orc_conv1x1_fwd_f64.argtypes = [_F, _F, _opt(_F), _I64, _I64, _I64, _I64, _D]
         L.ref_conv1x1_fwd_f32.argtypes = [_F, _F, _opt(_F), _F, _I64, _I64, _I64]
+        L.orc_conv1x1_bwd_f64.argtypes = [_F, _F, _F, _I64, _I64, _I64, _I64, _opt(_D),
+                                          _opt(_D), _opt(_D)]
+        L.ref_conv1x1_bwd_f32.argtypes = [_F, _F, _F, _opt(_F), _opt(_F), _opt(_F), _I64, _I64,
+                                          _I64]
         L.ref_gn_silu_fwd_bwd_f32.argtypes = [_F, _opt(_F), _opt(_F), _opt(_F), _I64, _I64,
                                               _I64, _I64, ctypes.c_float, ctypes.c_int, _F,
                                               _F, _F, _F, _F, _F, _opt(_F), _opt(_F),
@@ -212,3 +216,24 @@ def ref_conv1x1_fwd_f32(x, w, b, C_in, C_out, HW):
     lib().ref_conv1x1_fwd_f32(_f32(x).reshape(-1), _f32(w).reshape(-1), _f32(b), y, C_in, C_out,
                               HW)
     return y
+
+
+def conv1x1_bwd_f64(dz, x, w, N, C_in, C_out, HW, want=("dx", "dw", "db")):
+    dx = np.empty(N * C_in * HW) if "dx" in want else None
+    dw = np.empty(C_out * C_in) if "dw" in want else None
+    db = np.empty(C_out) if "db" in want else None
+    rc = lib().orc_conv1x1_bwd_f64(_f32(dz).reshape(-1), _f32(x).reshape(-1),
+                                   _f32(w).reshape(-1), N, C_in, C_out, HW, dx, dw, db)
+    assert rc == 0, rc
+    return dx, dw, db
+
+
+def ref_conv1x1_bwd_f32(go, x, w, C_in, C_out, HW, grad_in=None, grad_weight=None,
+                        grad_bias=None):
+    """Accumulates into the given arrays (zeros when None)."""
+    gi = np.zeros(C_in * HW, np.float32) if grad_in is None else grad_in
+    gw = np.zeros(C_out * C_in, np.float32) if grad_weight is None else grad_weight
+    gb = np.zeros(C_out, np.float32) if grad_bias is None else grad_bias
+    lib().ref_conv1x1_bwd_f32(_f32(go).reshape(-1), _f32(x).reshape(-1), _f32(w).reshape(-1),
+                              gi, gw, gb, C_in, C_out, HW)
+    return gi, gw, gb

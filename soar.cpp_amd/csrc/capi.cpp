@@ -354,10 +354,11 @@ int check_pw_shape(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t* 
         __builtin_mul_overflow(C_in, C_out, &wsz) || b > INT64_MAX / 4 || d > INT64_MAX / 4 ||
         wsz > INT64_MAX / 4)
         return fail(SOAR_EINVAL, "pointwise convolution shape overflows");
-    if (!soar::gn::pw_offsets_fit(C_in, HW))
+    // (the backward runs the same kernel with C_out as its reduction axis)
+    if (!soar::gn::pw_offsets_fit(std::max(C_in, C_out), HW))
         return fail(SOAR_EINVAL,
-                    "HW=%lld or C_in=%lld exceeds the pointwise kernel's 32-bit in-sample offsets",
-                    (long long)HW, (long long)C_in);
+                    "HW=%lld or C=%lld exceeds the pointwise kernel's 32-bit in-sample offsets",
+                    (long long)HW, (long long)std::max(C_in, C_out));
     *in_elems = b;
     *out_elems = d;
     return SOAR_OK;
@@ -391,7 +392,7 @@ SOAR_API int soar_conv2d_1x1_forward(const float* in, const float* weight, const
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     soar::gn::PwArgs a{in, weight, bias, out};
     hipError_t e = soar::gn::launch_pw_conv(a, 1, (int64_t)C_in, (int64_t)C_out, (int64_t)HW,
-                                            t.pw_chunk, nullptr, t,
+                                            t.pw_chunk, nullptr, false,
                                             static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "conv2d_1x1_forward launch");
 }
@@ -440,12 +441,84 @@ SOAR_API int soar_pw_conv_gn_silu_forward(const float* x, const float* weight,
     const hipStream_t s = static_cast<hipStream_t>(stream);
     soar::gn::PwArgs pa{x, weight, bias, z};
     hipError_t e = soar::gn::launch_pw_conv(pa, N, C_in, C_out, HW, p.chunk,
-                                            soar::gn::ws_partials(p, workspace), t, s);
+                                            soar::gn::ws_partials(p, workspace), false, s);
     if (e != hipSuccess) return hip_fail(e, "pointwise convolution launch");
     soar::gn::FwdArgs a{z, gamma, beta, y, mean, rstd, mean_lo, eps, flags, workspace};
     e = soar::gn::launch_forward_from_partials(p, t, a, s);
     if (e != hipSuccess) return hip_fail(e, "GroupNorm apply launch");
     return ok();
+}
+
+SOAR_API size_t soar_pw_conv_backward_workspace_bytes(int64_t N, int64_t C_in, int64_t C_out,
+                                                      int64_t HW) {
+    int64_t ie = 0, oe = 0;
+    if (check_pw_shape(N, C_in, C_out, HW, &ie, &oe) != SOAR_OK || oe == 0 || C_in == 0) {
+        g_err.clear();
+        return 0;
+    }
+    const soar::gn::PwBwdPlan p = soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW);
+    return soar::gn::pw_bwd_workspace_bytes(p);
+}
+
+SOAR_API int soar_pw_conv_backward(const float* dz, const float* x, const float* weight,
+                                   float* dx, float* dweight, float* dbias, int64_t N,
+                                   int64_t C_in, int64_t C_out, int64_t HW, unsigned flags,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+    int64_t ie = 0, oe = 0;
+    int rc = check_pw_shape(N, C_in, C_out, HW, &ie, &oe);
+    if (rc) return rc;
+    if (flags & ~SOAR_GN_ACCUMULATE_DX)
+        return fail(SOAR_EINVAL, "unsupported flags 0x%x (SOAR_GN_ACCUMULATE_DX only)", flags);
+    if (oe == 0 || (!dx && !dweight && !dbias)) return ok();
+    if (C_in == 0) return fail(SOAR_EINVAL, "C_in must be positive");
+    if ((rc = require_device())) return rc;
+    const size_t wb = (size_t)(C_in * C_out) * 4;
+    if ((rc = check_dev(dz, (size_t)oe * 4, "dz")) ||
+        (dx && (rc = check_dev(weight, wb, "weight"))) ||
+        ((dweight) && (rc = check_dev(x, (size_t)ie * 4, "x"))) ||
+        (rc = check_dev_opt(dx, (size_t)ie * 4, "dx")) ||
+        (rc = check_dev_opt(dweight, wb, "dweight")) ||
+        (rc = check_dev_opt(dbias, (size_t)C_out * 4, "dbias")))
+        return rc;
+    const Tuning t = current_tuning();
+    const soar::gn::PwBwdPlan p = soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW);
+    if (!pw_grid_fits(N, HW, t.pw_chunk) || p.G > 65535 ||
+        p.tiles_co * p.tiles_ci > (int64_t)0x7fffffff)
+        return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    const size_t need = soar::gn::pw_bwd_workspace_bytes(p);
+    if (workspace_bytes < need)
+        return fail(SOAR_EINVAL, "workspace of %zu bytes is smaller than the %zu this shape needs",
+                    workspace_bytes, need);
+    if ((rc = check_dev(workspace, need, "workspace"))) return rc;
+    soar::gn::PwBwdArgs a{dz, x, weight, dx, dweight, dbias, workspace};
+    hipError_t e = soar::gn::launch_pw_backward(p, a, N, C_in, C_out, HW, t.pw_chunk,
+                                                (flags & SOAR_GN_ACCUMULATE_DX) != 0,
+                                                static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "pointwise convolution backward launch");
+    return ok();
+}
+
+SOAR_API int soar_conv2d_1x1_backward(const float* grad_out, const float* in, const float* weight,
+                                      float* grad_in, float* grad_weight, float* grad_bias,
+                                      size_t C_in, size_t C_out, size_t HW, void* stream) {
+    if (C_in > (size_t)INT64_MAX || C_out > (size_t)INT64_MAX || HW > (size_t)INT64_MAX)
+        return fail(SOAR_EINVAL, "dimension too large");
+    if (C_out == 0 || HW == 0 || (!grad_in && !grad_weight && !grad_bias)) return ok();
+    if (C_in == 0) return fail(SOAR_EINVAL, "C_in must be positive");
+    const size_t need =
+        soar_pw_conv_backward_workspace_bytes(1, (int64_t)C_in, (int64_t)C_out, (int64_t)HW);
+    if (need == 0) {
+        int64_t ie = 0, oe = 0;
+        int rc = check_pw_shape(1, (int64_t)C_in, (int64_t)C_out, (int64_t)HW, &ie, &oe);
+        return rc ? rc : fail(SOAR_EINVAL, "shape is too large");
+    }
+    int rc = require_device();
+    if (rc) return rc;
+    void* ws = nullptr;
+    if ((rc = owned_workspace(need, &ws))) return rc;
+    return soar_pw_conv_backward(grad_out, in, weight, grad_in, grad_weight, grad_bias, 1,
+                                 (int64_t)C_in, (int64_t)C_out, (int64_t)HW,
+                                 SOAR_GN_ACCUMULATE_DX, ws, need, stream);
 }
 
 #define SOAR_ELEMWISE_PRELUDE(n)                                   \

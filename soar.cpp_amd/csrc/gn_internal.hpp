@@ -123,12 +123,36 @@ struct PwArgs {
 int pw_kpad(int64_t C_in);
 // The kernel addresses one sample's planes with 32-bit byte offsets.
 bool pw_offsets_fit(int64_t C_in, int64_t HW);
-// z = w * x + bias.  With `part` non-null the kernel also writes the
-// GroupNorm chunk partials of z for chunks of `chunk` pixels (a multiple of
-// 128), part[(n*C_out + co)*cpp + k].
+// z = w * x + bias (z += w * x with `accumulate`).  With `part` non-null
+// the kernel also writes the GroupNorm chunk partials of z for chunks of
+// `chunk` pixels (a multiple of 128), part[(n*C_out + co)*cpp + k].
+// `name` labels the launch for the kernel timers (null: a default).
 hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
-                          int64_t HW, int64_t chunk, double2* part, const Tuning& t,
-                          hipStream_t s);
+                          int64_t HW, int64_t chunk, double2* part, bool accumulate,
+                          hipStream_t s, const char* name = nullptr);
+
+// Backward of the pointwise convolution: dx = W^T dz (written, or added
+// with `accumulate_dx`), dw += sum dz x^T, db += sum dz; any output may be
+// null.  Workspace: W^T, then the per-chunk dW and db partials.
+struct PwBwdArgs {
+    const float* dz;  // [N][C_out][HW]
+    const float* x;   // [N][C_in][HW]
+    const float* w;   // [C_out][C_in]
+    float* dx;        // [N][C_in][HW], nullable
+    float* dw;        // [C_out][C_in], nullable
+    float* db;        // [C_out], nullable
+    void* ws;
+};
+struct PwBwdPlan {
+    int64_t tiles_co = 0, tiles_ci = 0;  // 64x64 tiles of dW
+    int64_t chunk = 0, cpp = 0, G = 0;   // pixel chunks of the dW waves
+    size_t wt_bytes = 0, pw_bytes = 0, pb_bytes = 0;
+};
+PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW);
+size_t pw_bwd_workspace_bytes(const PwBwdPlan& p);
+hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N, int64_t C_in,
+                              int64_t C_out, int64_t HW, int64_t chunk_dx, bool accumulate_dx,
+                              hipStream_t s);
 
 // Elementwise kernels (elementwise.hip).
 hipError_t launch_silu_forward(const float* x, float* y, int64_t n,

@@ -90,13 +90,16 @@ __device__ __forceinline__ f4 ld4(const float* base, uint32_t byte_off) {
 // branch in the K loop.  A lane past the end of the plane loads the plane's
 // last 16 bytes and weight rows past C_out load row C_out - 1.  The general
 // path guards every scalar access and loads zeros instead.
-template <bool FAST, bool STATS, bool BIAS>
+enum PwMode { kPlain = 0, kStats = 1, kAccum = 2 };
+
+template <bool FAST, int MODE, bool BIAS>
 __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const float* __restrict__ ws,
                                         const float* __restrict__ bias, float* __restrict__ zs,
                                         int64_t row0, int64_t p0, int h, int j, int64_t C_in,
                                         int64_t C_out, int64_t HW, int Kpad, float2* lds,
                                         float* ldsK) {
     // xs = x + n*C_in*HW + p0, ws = w + row0*C_in, zs = z + (n*C_out + row0)*HW + p0
+    constexpr bool STATS = MODE == kStats, ACC = MODE == kAccum;
     const bool lane_px = p0 + 4 * j < HW;
     const uint32_t hw4 = (uint32_t)HW * 4u;  // bytes per channel plane
     // lane byte offsets: x at channel 4h, pixel 4j (clamped into the plane)
@@ -205,14 +208,14 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
             if (tr0 + 4 * h <= rlim) {
                 if (FAST) {
                     if (lane_px) {
-                        const f4 v = {acc[mt][0][r], acc[mt][1][r], acc[mt][2][r],
-                                      acc[mt][3][r]};
+                        f4 v = {acc[mt][0][r], acc[mt][1][r], acc[mt][2][r], acc[mt][3][r]};
+                        if (ACC) v += *reinterpret_cast<const f4*>(zr);
                         *reinterpret_cast<f4*>(zr) = v;
                     }
                 } else {
 #pragma unroll
                     for (int t = 0; t < 4; ++t)
-                        if (p0 + 4 * j + t < HW) zr[t] = acc[mt][t][r];
+                        if (p0 + 4 * j + t < HW) zr[t] = ACC ? zr[t] + acc[mt][t][r] : acc[mt][t][r];
                 }
             }
         }
@@ -254,10 +257,11 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
     }
 }
 
-// STATS: write GroupNorm chunk partials.  BIAS: bias is non-null.
-// Byte offsets inside one sample's planes must fit in 32 bits
-// (checked by the host with pw_offsets_fit).
-template <bool FAST, bool STATS, bool BIAS>
+// MODE kPlain: z = w x + b;  kStats: also the GroupNorm chunk partials;
+// kAccum: z += w x.  BIAS: bias is non-null.  Byte offsets inside one
+// sample's planes must fit in 32 bits (checked by the host with
+// pw_offsets_fit).
+template <bool FAST, int MODE, bool BIAS>
 __global__ __launch_bounds__(64, 2) void k_pw_conv(
     const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ bias, float* __restrict__ z, double2* __restrict__ part,
@@ -266,6 +270,7 @@ __global__ __launch_bounds__(64, 2) void k_pw_conv(
     __shared__ float ldsK[kRowTile];            // per-row shifts of the item
     __shared__ Mom ldsM[kRowGroup * kRowTile];  // row-owner running moments
 
+    constexpr bool STATS = MODE == kStats;
     const int lane = threadIdx.x;
     const int h = lane >> 5, j = lane & 31;
     const int64_t n = (int64_t)blockIdx.x / cpp;
@@ -286,7 +291,7 @@ __global__ __launch_bounds__(64, 2) void k_pw_conv(
             const int nvalid = (int)min<int64_t>(kItem, HW - p0);
             for (int g = 0; g < nrt; ++g) {
                 const int64_t row0 = (rg + g) * kRowTile;
-                pw_item<FAST, STATS, BIAS>(xn + p0, w + row0 * C_in, bias, zn + row0 * HW + p0,
+                pw_item<FAST, MODE, BIAS>(xn + p0, w + row0 * C_in, bias, zn + row0 * HW + p0,
                                            row0, p0, h, j, C_in, C_out, HW, Kpad, lds, ldsK);
                 if (STATS) {
                     __syncthreads();
@@ -320,6 +325,174 @@ __global__ __launch_bounds__(64, 2) void k_pw_conv(
     }
 }
 
+// ======================================================================
+// Weight and bias gradients: dW[co][ci] = sum_(n,p) dz[n][co][p] x[n][ci][p],
+// db[co] = sum_(n,p) dz[n][co][p].  A GEMM whose K axis is the pixels:
+// C[m = co][n = ci] = sum_k A[m][k] B[k][n], A = dz rows, B = x rows.
+//
+// One wave per (64x64 tile of dW, pixel chunk of one sample).  At k-steps
+// (i, q) of a 32-pixel step, lane l = 32h + j supplies pixel p + 16h + 4i + q
+// of row j of each operand tile, so each lane reads one 64-byte run of its
+// row per tile per step.  The wave writes its fp32 partial tile (and, for
+// the ci tile 0, the partial dz row sums) to the workspace; a finish kernel
+// adds the partials in a fixed order in float64.
+// ======================================================================
+template <bool FAST>
+__global__ __launch_bounds__(64, 2) void k_pw_wgrad(
+    const float* __restrict__ dz, const float* __restrict__ x, float* __restrict__ part_w,
+    float* __restrict__ part_b, int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk,
+    int64_t cpp, int64_t tiles_ci) {
+    const int lane = threadIdx.x;
+    const int h = lane >> 5, j = lane & 31;
+    const int64_t tco = (int64_t)blockIdx.x / tiles_ci;
+    const int64_t tci = (int64_t)blockIdx.x - tco * tiles_ci;
+    const int64_t g = blockIdx.y;  // n * cpp + chunk index
+    const int64_t n = g / cpp, kc = g - n * cpp;
+    const int64_t px0 = kc * chunk, pend = min(px0 + chunk, HW);
+    const int64_t co0 = tco * kRowTile, ci0 = tci * kRowTile;
+    // operand rows (rows past the matrix are clamped to its last row: their
+    // products land only in outputs that are not written)
+    const float* ra[2];
+    const float* rb[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        ra[t] = dz + (n * C_out + min<int64_t>(co0 + 32 * t + j, C_out - 1)) * HW + 16 * h;
+        rb[t] = x + (n * C_in + min<int64_t>(ci0 + 32 * t + j, C_in - 1)) * HW + 16 * h;
+    }
+    const bool want_b = tci == 0;
+
+    f16 acc[2][2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.0f;
+    float sb[2] = {0.0f, 0.0f};
+
+    auto load_step = [&](int64_t p, f4 (&A)[2][4], f4 (&B)[2][4]) {
+        if (FAST && p + 32 <= pend) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    A[t][i] = *reinterpret_cast<const f4*>(ra[t] + p + 4 * i);
+                    B[t][i] = *reinterpret_cast<const f4*>(rb[t] + p + 4 * i);
+                }
+        } else {
+            // ragged step (or a plane that is not 16-byte aligned)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int64_t px = p + 16 * h + 4 * i + q;
+                        const bool ok = px < pend;
+                        A[t][i][q] = ok ? ra[t][p + 4 * i + q] : 0.0f;
+                        B[t][i][q] = ok ? rb[t][p + 4 * i + q] : 0.0f;
+                    }
+        }
+    };
+    auto mfma_step = [&](const f4 (&A)[2][4], const f4 (&B)[2][4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt)
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                            A[mt][i][q], B[nt][i][q], acc[mt][nt], 0, 0, 0);
+        if (want_b) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    sb[mt] += (A[mt][i][0] + A[mt][i][1]) + (A[mt][i][2] + A[mt][i][3]);
+        }
+    };
+    auto sched = [] {
+        if (FAST) {
+            __builtin_amdgcn_sched_group_barrier(0x020, 16, 0);  // 16 vector loads
+            __builtin_amdgcn_sched_group_barrier(0x008, 64, 0);  // then 64 MFMAs
+        }
+    };
+    // ping-pong operand buffers, loads one step ahead (see k_pw_conv)
+    const int64_t plast = px0 + ((pend - px0 - 1) / 32) * 32;  // last step
+    f4 A0[2][4], B0[2][4], A1[2][4], B1[2][4];
+    load_step(px0, A0, B0);
+    int64_t p = px0;
+    for (; p + 32 < pend; p += 64) {
+        load_step(p + 32, A1, B1);
+        mfma_step(A0, B0);
+        sched();
+        load_step(min(p + 64, plast), A0, B0);
+        mfma_step(A1, B1);
+        sched();
+    }
+    if (p < pend) mfma_step(A0, B0);
+
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t co = co0 + tile_row(mt, r, h);
+                const int64_t ci = ci0 + 32 * nt + j;
+                if (co < C_out && ci < C_in) part_w[(g * C_out + co) * C_in + ci] = acc[mt][nt][r];
+            }
+    if (want_b) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const float tot = sb[mt] + __shfl_xor(sb[mt], 32);
+            const int64_t co = co0 + 32 * mt + j;
+            if (h == 0 && co < C_out) part_b[g * C_out + co] = tot;
+        }
+    }
+}
+
+// out[e] += sum_g part[g][e] for e < E, g ascending in float64.  A block is
+// 16 elements x 16 g-segments; the segments are added in order.
+__global__ __launch_bounds__(256) void k_sum_partials(const float* __restrict__ part,
+                                                      float* __restrict__ out, int64_t E,
+                                                      int64_t G) {
+    __shared__ double lds[16][16];
+    const int el = threadIdx.x & 15, seg = threadIdx.x >> 4;
+    const int64_t e = (int64_t)blockIdx.x * 16 + el;
+    const int64_t g0 = seg * G / 16, g1 = (seg + 1) * G / 16;
+    double sum = 0.0;
+    if (e < E) {
+        constexpr int kU = 8;  // loads in flight per thread
+        for (int64_t gg = g0; gg < g1; gg += kU) {
+            float v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) v[u] = gg + u < g1 ? part[(gg + u) * E + e] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < kU; ++u) sum += (double)v[u];
+        }
+    }
+    lds[seg][el] = sum;
+    __syncthreads();
+    if (seg == 0 && e < E) {
+        double t = 0.0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) t += lds[i][el];
+        out[e] = (float)((double)out[e] + t);
+    }
+}
+
+// wt[ci][co] = w[co][ci]
+__global__ void k_transpose(const float* __restrict__ w, float* __restrict__ wt, int64_t R,
+                            int64_t Cc) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= R * Cc) return;
+    const int64_t r = i / Cc, c = i - r * Cc;
+    wt[c * R + r] = w[i];
+}
+
 template <typename F>
 void bsel(bool b, F&& f) {
     if (b)
@@ -337,24 +510,100 @@ bool pw_offsets_fit(int64_t C_in, int64_t HW) {
 }
 
 hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
-                          int64_t HW, int64_t chunk, double2* part, const Tuning& t,
-                          hipStream_t s) {
+                          int64_t HW, int64_t chunk, double2* part, bool accumulate,
+                          hipStream_t s, const char* name) {
     if (N == 0 || HW == 0 || C_out == 0) return hipSuccess;
     const int64_t cpp = (HW + chunk - 1) / chunk;
     const dim3 grid((unsigned)(N * cpp));
     const bool fast = (HW % 4 == 0) && (C_in % 8 == 0) && ((uintptr_t)a.x % 16 == 0) &&
                       ((uintptr_t)a.z % 16 == 0) && ((uintptr_t)a.w % 16 == 0);
     const int Kpad = pw_kpad(C_in);
-    const int tok = prof_begin(s, part ? "pw_conv_gn_stats" : "pw_conv");
+    const int mode = part ? kStats : (accumulate ? kAccum : kPlain);
+    if (!name) name = part ? "pw_conv_gn_stats" : "pw_conv";
+    const int tok = prof_begin(s, name);
+    auto go = [&](auto F, auto M, auto B) {
+        k_pw_conv<F(), M(), B()><<<grid, 64, 0, s>>>(a.x, a.w, a.bias, a.z, part, C_in, C_out,
+                                                    HW, chunk, cpp, Kpad);
+    };
+    using P = std::integral_constant<int, kPlain>;
+    using S = std::integral_constant<int, kStats>;
+    using A = std::integral_constant<int, kAccum>;
     bsel(fast, [&](auto F) {
-        bsel(part != nullptr, [&](auto S) {
+        if (mode == kAccum) {
+            go(F, A{}, std::false_type{});
+        } else {
             bsel(a.bias != nullptr, [&](auto B) {
-                k_pw_conv<F(), S(), B()><<<grid, 64, 0, s>>>(a.x, a.w, a.bias, a.z, part, C_in,
-                                                            C_out, HW, chunk, cpp, Kpad);
+                if (mode == kStats)
+                    go(F, S{}, B);
+                else
+                    go(F, P{}, B);
             });
-        });
+        }
     });
     prof_end(s, tok);
+    return hipGetLastError();
+}
+
+PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW) {
+    PwBwdPlan p;
+    p.tiles_co = (C_out + kRowTile - 1) / kRowTile;
+    p.tiles_ci = (C_in + kRowTile - 1) / kRowTile;
+    // about 2048 waves (two per SIMD), chunks of at least 256 pixels
+    const int64_t total = N * HW * p.tiles_co * p.tiles_ci;
+    int64_t chunk = (total / 2048 + 31) / 32 * 32;
+    chunk = std::max<int64_t>(chunk, 256);
+    const int64_t hw32 = (HW + 31) / 32 * 32;
+    p.chunk = std::min(chunk, std::max<int64_t>(hw32, 32));
+    p.cpp = (HW + p.chunk - 1) / p.chunk;
+    p.G = N * p.cpp;
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    p.wt_bytes = al(sizeof(float) * (size_t)(C_in * C_out));
+    p.pw_bytes = al(sizeof(float) * (size_t)(p.G * C_out * C_in));
+    p.pb_bytes = al(sizeof(float) * (size_t)(p.G * C_out));
+    return p;
+}
+
+size_t pw_bwd_workspace_bytes(const PwBwdPlan& p) { return p.wt_bytes + p.pw_bytes + p.pb_bytes; }
+
+hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N, int64_t C_in,
+                              int64_t C_out, int64_t HW, int64_t chunk_dx, bool accumulate_dx,
+                              hipStream_t s) {
+    if (N == 0 || HW == 0 || C_out == 0 || C_in == 0) return hipSuccess;
+    char* ws = static_cast<char*>(a.ws);
+    float* wt = reinterpret_cast<float*>(ws);
+    float* part_w = reinterpret_cast<float*>(ws + p.wt_bytes);
+    float* part_b = reinterpret_cast<float*>(ws + p.wt_bytes + p.pw_bytes);
+    if (a.dx) {
+        const int64_t E = C_in * C_out;
+        int tok = prof_begin(s, "pw_transpose");
+        k_transpose<<<dim3((unsigned)((E + 255) / 256)), 256, 0, s>>>(a.w, wt, C_out, C_in);
+        prof_end(s, tok);
+        // dx = W^T dz: the forward kernel with dz as input and W^T as weights
+        PwArgs fa{a.dz, wt, nullptr, a.dx};
+        hipError_t e = launch_pw_conv(fa, N, C_out, C_in, HW, chunk_dx, nullptr, accumulate_dx,
+                                      s, "pw_conv_dgrad");
+        if (e != hipSuccess) return e;
+    }
+    if (a.dw || a.db) {
+        const bool fast = (HW % 4 == 0) && ((uintptr_t)a.dz % 16 == 0) &&
+                          ((uintptr_t)a.x % 16 == 0);
+        const dim3 grid((unsigned)(p.tiles_co * p.tiles_ci), (unsigned)p.G);
+        int tok = prof_begin(s, "pw_conv_wgrad");
+        bsel(fast, [&](auto F) {
+            k_pw_wgrad<F()><<<grid, 64, 0, s>>>(a.dz, a.x, part_w, part_b, C_in, C_out, HW,
+                                                p.chunk, p.cpp, p.tiles_ci);
+        });
+        prof_end(s, tok);
+        tok = prof_begin(s, "pw_conv_wgrad_finish");
+        if (a.dw) {
+            const int64_t E = C_out * C_in;
+            k_sum_partials<<<dim3((unsigned)((E + 15) / 16)), 256, 0, s>>>(part_w, a.dw, E, p.G);
+        }
+        if (a.db)
+            k_sum_partials<<<dim3((unsigned)((C_out + 15) / 16)), 256, 0, s>>>(part_b, a.db,
+                                                                               C_out, p.G);
+        prof_end(s, tok);
+    }
     return hipGetLastError();
 }
 

@@ -84,6 +84,10 @@ SIGNATURES = {
     "soar_pw_conv_gn_silu_forward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                                                 _I64, _I64, _I64, _I64, _c.c_float, _c.c_uint,
                                                 _P, _SZ, _P]),
+    "soar_pw_conv_backward_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "soar_pw_conv_backward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                         _c.c_uint, _P, _SZ, _P]),
+    "soar_conv2d_1x1_backward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _P]),
     "soar_arena_create": (_c.c_int, [_SZ, _SZ, _c.POINTER(_P)]),
     "soar_arena_alloc": (_c.c_int, [_P, _SZ, _c.POINTER(_P), _c.POINTER(_SZ)]),
     "soar_arena_freeze_static": (_c.c_int, [_P]),
@@ -340,6 +344,40 @@ def pw_conv_gn_silu_forward(x, weight, bias, gamma, beta, G, eps=1e-5, silu=True
         _ptr(rstd), _ptr(mean_lo), N, C_in, C_out, HW, G, eps, GN_SILU if silu else 0,
         _ptr(ws), ws.numel(), _stream(stream)))
     return z, y, Stats(mean, rstd, mean_lo)
+
+
+def pw_conv_backward_workspace_bytes(N, C_in, C_out, HW) -> int:
+    return int(lib().soar_pw_conv_backward_workspace_bytes(N, C_in, C_out, HW))
+
+
+def pw_conv_backward(dz, x, weight, dx=None, dweight=None, dbias=None, want_dx=True,
+                     want_dw=True, want_db=True, accumulate_dx=False, ws=None, stream=None):
+    """Backward of the pointwise conv through soar_pw_conv_backward; returns
+    (dx, dweight, dbias).  dweight/dbias accumulate (fresh zeros when not
+    given); dx is written, or added to with accumulate_dx."""
+    import torch
+    N, C_out, HW = _nchw(dz)
+    w = weight.reshape(weight.shape[0], -1)
+    C_in = w.shape[1]
+    for t, n in ((dz, "dz"), (x, "x"), (w, "weight"), (dx, "dx"), (dweight, "dweight"),
+                 (dbias, "dbias")):
+        _check_tensor(t, n)
+    if want_dx and dx is None:
+        shape = (N, C_in) + tuple(dz.shape[2:])
+        dx = (torch.zeros if accumulate_dx else torch.empty)(shape, dtype=torch.float32,
+                                                             device=dz.device)
+    if want_dw and dweight is None:
+        dweight = torch.zeros((C_out, C_in), dtype=torch.float32, device=dz.device)
+    if want_db and dbias is None:
+        dbias = torch.zeros(C_out, dtype=torch.float32, device=dz.device)
+    if ws is None:
+        ws = torch.empty(max(pw_conv_backward_workspace_bytes(N, C_in, C_out, HW), 1),
+                         dtype=torch.uint8, device=dz.device)
+    check(lib().soar_pw_conv_backward(
+        _ptr(dz), _ptr(x), _ptr(w), _ptr(dx) if want_dx else None,
+        _ptr(dweight) if want_dw else None, _ptr(dbias) if want_db else None, N, C_in, C_out,
+        HW, GN_ACCUMULATE_DX if accumulate_dx else 0, _ptr(ws), ws.numel(), _stream(stream)))
+    return (dx if want_dx else None, dweight if want_dw else None, dbias if want_db else None)
 
 
 def prof_enable(on: bool = True):

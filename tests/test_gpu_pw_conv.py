@@ -214,3 +214,136 @@ def test_pw_conv_errors(gpu):
         torch.cuda.synchronize()
     finally:
         gpu.check(L.soar_arena_destroy(arena))
+
+
+# ---- backward ----------------------------------------------------------------------
+
+def bwd_bounds(dz, x, w):
+    """fp32 bounds of dx (C_out-term sums) and of dw, db (pixel sums)."""
+    N, C_out, HW = dz.shape
+    C_in = x.shape[1]
+    ad, ax, aw = (np.abs(a).astype(np.float64) for a in (dz, x, w))
+    bx = (C_out + 2) * U32 * np.einsum("oc,nop->ncp", aw, ad)
+    mw = np.einsum("nop,ncp->oc", ad, ax)
+    mb = ad.sum(axis=(0, 2))
+    K = N * HW + 2
+    return bx, K * U32 * mw, K * U32 * mb
+
+
+BWD_SHAPES = [
+    # (N, C_in, C_out, HW)
+    (1, 64, 64, 4096),
+    (2, 32, 48, 2500),      # partial dW tiles, ragged chunks
+    (1, 16, 24, 1030),
+    (1, 8, 16, 17),         # general paths (HW % 4)
+    (1, 64, 128, 2048),     # two row tiles of dW / dx
+    (1, 130, 72, 4096),     # C_in % 8 != 0 for the forward; dx K = 72
+    (3, 24, 8, 333),
+]
+
+
+@pytest.mark.parametrize("N,C_in,C_out,HW", BWD_SHAPES)
+def test_pw_conv_backward_matches_oracle(gpu, oracle, N, C_in, C_out, HW):
+    print(f"pw_conv_backward N={N} C_in={C_in} C_out={C_out} HW={HW}", flush=True)
+    r = np.random.default_rng(N * 1000 + C_in + HW)
+    dz = r.standard_normal((N, C_out, HW)).astype(np.float32)
+    x = r.standard_normal((N, C_in, HW)).astype(np.float32)
+    w = (r.uniform(-1, 1, (C_out, C_in)) / np.sqrt(C_in)).astype(np.float32)
+    dx, dw, db = gpu.pw_conv_backward(dev(dz), dev(x), dev(w))
+    tx, tw, tb = oracle.conv1x1_bwd_f64(dz, x, w, N, C_in, C_out, HW)
+    bx, bw, bb = bwd_bounds(dz, x, w)
+    for got, t, b, name in ((dx, tx, bx, "dx"), (dw, tw, bw, "dw"), (db, tb, bb, "db")):
+        err = np.abs(host(got).astype(np.float64).reshape(-1) - t)
+        ratio = err / (b.reshape(-1) + 1e-30)
+        i = int(np.argmax(ratio))
+        assert ratio[i] <= 1.0, f"{name} err {err[i]:.3e} > bound {b.reshape(-1)[i]:.3e} at {i}"
+
+
+def test_pw_conv_backward_accumulates(gpu, oracle):
+    N, C_in, C_out, HW = 1, 32, 32, 1000
+    r = np.random.default_rng(4)
+    dz = r.standard_normal((N, C_out, HW)).astype(np.float32)
+    x = r.standard_normal((N, C_in, HW)).astype(np.float32)
+    w = r.uniform(-0.2, 0.2, (C_out, C_in)).astype(np.float32)
+    dx0 = r.standard_normal((N, C_in, HW)).astype(np.float32)
+    dw0 = r.standard_normal((C_out, C_in)).astype(np.float32)
+    db0 = r.standard_normal(C_out).astype(np.float32)
+    dx, dw, db = gpu.pw_conv_backward(dev(dz), dev(x), dev(w), dx=dev(dx0), dweight=dev(dw0),
+                                      dbias=dev(db0), accumulate_dx=True)
+    tx, tw, tb = oracle.conv1x1_bwd_f64(dz, x, w, N, C_in, C_out, HW)
+    bx, bw, bb = bwd_bounds(dz, x, w)
+    assert np.all(np.abs(host(dx).reshape(-1) - (dx0.reshape(-1) + tx)) <=
+                  bx.reshape(-1) + U32 * np.abs(dx0).reshape(-1) * 2)
+    assert np.all(np.abs(host(dw).reshape(-1) - (dw0.reshape(-1) + tw)) <=
+                  bw.reshape(-1) + U32 * np.abs(dw0).reshape(-1) * 2 + 1e-30)
+    assert np.all(np.abs(host(db) - (db0 + tb)) <= bb + U32 * np.abs(db0) * 2 + 1e-30)
+    # only some gradients
+    dx2, dw2, db2 = gpu.pw_conv_backward(dev(dz), dev(x), dev(w), want_dx=False, want_db=False)
+    assert dx2 is None and db2 is None
+    assert np.all(np.abs(host(dw2).reshape(-1) - tw) <= bw.reshape(-1) + 1e-30)
+
+
+def test_conv2d_1x1_backward_reference_signature(gpu, oracle):
+    """grad_in/grad_weight/grad_bias += as the reference kernels, one sample."""
+    import ctypes
+    import torch
+    C_in, C_out, HW = 24, 40, 1500
+    r = np.random.default_rng(5)
+    go = r.standard_normal((C_out, HW)).astype(np.float32)
+    x = r.standard_normal((C_in, HW)).astype(np.float32)
+    w = r.uniform(-0.3, 0.3, (C_out, C_in)).astype(np.float32)
+    gi0 = r.standard_normal((C_in, HW)).astype(np.float32)
+    gi, gw, gb = dev(gi0), torch.zeros((C_out, C_in), device="cuda"), torch.zeros(C_out,
+                                                                                 device="cuda")
+    go_d, x_d, w_d = dev(go), dev(x), dev(w)  # kept alive across the calls
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    gpu.check(gpu.lib().soar_conv2d_1x1_backward(P(go_d), P(x_d), P(w_d), P(gi), P(gw),
+                                                 P(gb), C_in, C_out, HW, None))
+    torch.cuda.synchronize()
+    ri, rw, rb = oracle.ref_conv1x1_bwd_f32(go, x, w, C_in, C_out, HW, grad_in=gi0.copy())
+    tx, tw, tb = oracle.conv1x1_bwd_f64(go[None], x[None], w, 1, C_in, C_out, HW)
+    bx, bw, bb = bwd_bounds(go[None], x[None], w)
+    assert np.all(np.abs(host(gi).reshape(-1) - (gi0.reshape(-1) + tx)) <=
+                  bx.reshape(-1) + 2 * U32 * np.abs(gi0).reshape(-1))
+    assert np.all(np.abs(host(gw).reshape(-1) - tw) <= bw.reshape(-1) + 1e-30)
+    assert np.all(np.abs(host(gb) - tb) <= bb + 1e-30)
+    # and the reference's own fp32 loops agree within the same bounds
+    assert np.all(np.abs(rw - tw) <= bw.reshape(-1) + 1e-30)
+    # NULL outputs are skipped
+    gpu.check(gpu.lib().soar_conv2d_1x1_backward(P(go_d), P(x_d), P(w_d), None, None,
+                                                 P(gb), C_in, C_out, HW, None))
+    torch.cuda.synchronize()
+    assert np.all(np.abs(host(gb) - 2 * tb) <= 2 * bb + 1e-30)
+
+
+def test_pw_conv_backward_full_size_adjoint(gpu):
+    """64 -> 64 at 2048x2048: dx on 4096 random pixel columns against float64,
+    and the adjoint identities <W, dW> = <z, dz> = <x, dx> (z = W x) that
+    tie dW and dx to the forward at full size."""
+    import torch
+    C, HW = 64, 2048 * 2048
+    print("pw_conv_backward full size", flush=True)
+    x = torch.empty((1, C, HW), device="cuda")
+    dz = torch.empty((1, C, HW), device="cuda")
+    gpu.synth_normal(x, 77, 1)
+    gpu.synth_normal(dz, 77, 4)
+    r = np.random.default_rng(10)
+    w = dev((r.uniform(-1, 1, (C, C)) / 8.0).astype(np.float32))
+    dx, dw, db = gpu.pw_conv_backward(dz, x, w)
+    z = gpu.conv1x1_forward(x.reshape(1, C, HW, 1), w).reshape(1, C, HW)
+    torch.cuda.synchronize()
+    zdz = torch.dot(z.reshape(-1).double(), dz.reshape(-1).double()).item()
+    wdw = torch.dot(w.reshape(-1).double(), dw.reshape(-1).double()).item()
+    xdx = torch.dot(x.reshape(-1).double(), dx.reshape(-1).double()).item()
+    scale = torch.dot(z.reshape(-1).double().abs(), dz.reshape(-1).double().abs()).item()
+    assert abs(wdw - zdz) <= 1e-5 * scale, (wdw, zdz, scale)
+    assert abs(xdx - zdz) <= 1e-5 * scale, (xdx, zdz, scale)
+    assert abs(db.double().sum().item() - dz.double().sum().item()) <= 1e-5 * (
+        dz.double().abs().sum().item())
+    cols = torch.from_numpy(np.sort(r.choice(HW, 4096, replace=False))).cuda()
+    ds = host(dz.reshape(C, HW).index_select(1, cols)).astype(np.float64)
+    xs = host(dx.reshape(C, HW).index_select(1, cols)).astype(np.float64)
+    wh = host(w).astype(np.float64)
+    bound = (C + 2) * U32 * (np.abs(wh).T @ np.abs(ds))
+    assert np.all(np.abs(xs - wh.T @ ds) <= bound)
+    del x, dz, dx, z

@@ -77,3 +77,56 @@ def test_reference_conv_port_tracks_truth(oracle, C_in, C_out, HW):
     t = oracle.conv1x1_fwd_f64(x, w, b, 1, C_in, C_out, HW)
     mag = np.abs(w).astype(np.float64) @ np.abs(x).astype(np.float64) + np.abs(b)[:, None]
     assert np.all(np.abs(y - t) <= (C_in + 1) * U32 * mag.reshape(-1) + 1e-30)
+
+
+@pytest.mark.parametrize("N,C_in,C_out,HW", [(1, 3, 5, 7), (2, 16, 24, 33)])
+def test_conv_bwd_f64_matches_numpy(oracle, N, C_in, C_out, HW):
+    dz = rand((N, C_out, HW), 11)
+    x = rand((N, C_in, HW), 12)
+    w = rand((C_out, C_in), 13)
+    dx, dw, db = oracle.conv1x1_bwd_f64(dz, x, w, N, C_in, C_out, HW)
+    d64, x64, w64 = (a.astype(np.float64) for a in (dz, x, w))
+    np.testing.assert_allclose(dx.reshape(N, C_in, HW), np.einsum("oc,nop->ncp", w64, d64),
+                               rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(dw.reshape(C_out, C_in), np.einsum("nop,ncp->oc", d64, x64),
+                               rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(db, d64.sum(axis=(0, 2)), rtol=1e-13, atol=1e-13)
+
+
+def test_conv_bwd_f64_is_the_adjoint(oracle):
+    """<conv(x), dz> = <x, conv^T(dz)> and d<conv(x), dz>/dW = dW: the
+    backward is the exact adjoint of the forward (catches a transposed W)."""
+    N, C_in, C_out, HW = 2, 5, 7, 19
+    x = rand((N, C_in, HW), 14)
+    w = rand((C_out, C_in), 15)
+    b = rand((C_out,), 16)
+    dz = rand((N, C_out, HW), 17)
+    z = oracle.conv1x1_fwd_f64(x, w, b, N, C_in, C_out, HW)
+    dx, dw, db = oracle.conv1x1_bwd_f64(dz, x, w, N, C_in, C_out, HW)
+    lhs = float(np.dot(z, dz.reshape(-1).astype(np.float64)))
+    rhs = float(np.dot(x.reshape(-1).astype(np.float64), dx)) + float(
+        np.dot(b.astype(np.float64), db))
+    assert abs(lhs - rhs) <= 1e-10 * (1 + abs(lhs))
+    # <z, dz> is linear in W with gradient dw
+    h = 1e-3
+    w2 = w.copy()
+    w2[3, 2] += h
+    z2 = oracle.conv1x1_fwd_f64(x, w2, b, N, C_in, C_out, HW)
+    fd = (float(np.dot(z2, dz.reshape(-1).astype(np.float64))) - lhs) / (float(w2[3, 2]) -
+                                                                         float(w[3, 2]))
+    assert abs(fd - dw[3 * C_in + 2]) <= 1e-6 * (1 + abs(fd))
+
+
+@pytest.mark.parametrize("C_in,C_out,HW", [(1, 1, 5), (7, 3, 50), (32, 16, 300)])
+def test_reference_conv_bwd_port_tracks_truth(oracle, C_in, C_out, HW):
+    go = rand((C_out, HW), 18)
+    x = rand((C_in, HW), 19)
+    w = rand((C_out, C_in), 20)
+    gi0 = rand((C_in * HW,), 21)  # accumulates into what is there
+    gi, gw, gb = oracle.ref_conv1x1_bwd_f32(go, x, w, C_in, C_out, HW, grad_in=gi0.copy())
+    dx, dw, db = oracle.conv1x1_bwd_f64(go, x, w, 1, C_in, C_out, HW)
+    magx = np.abs(w).astype(np.float64).T @ np.abs(go).astype(np.float64)
+    assert np.all(np.abs(gi - (gi0 + dx)) <= (C_out + 2) * U32 * (magx.reshape(-1) + np.abs(gi0)))
+    magw = np.abs(go).astype(np.float64) @ np.abs(x).astype(np.float64).T
+    assert np.all(np.abs(gw - dw) <= (HW + 1) * U32 * magw.reshape(-1) + 1e-30)
+    assert np.all(np.abs(gb - db) <= (HW + 1) * U32 * np.abs(go).sum(axis=1) + 1e-30)
