@@ -238,6 +238,66 @@ SOAR_API int soar_conv2d_1x1_backward(const float* grad_out, const float* in,
                                       size_t C_in, size_t C_out, size_t HW,
                                       void* stream);
 
+/* ---- depthwise convolution (groups = C_in = C_out) ------------------- */
+/* The K x K depthwise convolutions of CBA blocks: Down.dw (k3, stride 2),
+ * LKR.dw (k5, k7), the Ctx branches (k3, dilation 1/3/5)
+ * (src/nn/blocks.cpp:449-500).  x [N][C][H_in][W_in], y [N][C][H_out][W_out],
+ * weight [C][K][K] (the reference's [C][1][K][K]), bias [C] or NULL.
+ * y[n][c][yo][xo] = bias[c] + sum_(ky,kx) w[c][ky][kx] *
+ *                   x[n][c][yo*stride - pad + ky*dil][xo*stride - pad + kx*dil],
+ * taps outside the input skipped.  H_out/W_out are the caller's (Conv2d
+ * computes (H + 2*pad - dil*(K-1) - 1)/stride + 1, layers.cpp:330-332).
+ * Tiled LDS kernels for (K, stride, dil) = (3,1,1) (3,2,1) (5,1,1) (7,1,1)
+ * (3,1,2) (3,1,3) (3,1,5); other shapes run generic kernels. */
+SOAR_API int soar_dw_conv_forward(const float* x, const float* weight,
+                                  const float* bias, float* y, int64_t N,
+                                  int64_t C, int64_t H_in, int64_t W_in,
+                                  int64_t H_out, int64_t W_out, int64_t K,
+                                  int64_t pad, int64_t stride, int64_t dil,
+                                  void* stream);
+
+/* Bytes of workspace soar_dw_conv_backward needs (0 is a valid answer: the
+ * generic kernels need none; (size_t)-1 for an invalid shape). */
+SOAR_API size_t soar_dw_conv_backward_workspace_bytes(
+    int64_t N, int64_t C, int64_t H_in, int64_t W_in, int64_t H_out,
+    int64_t W_out, int64_t K, int64_t stride, int64_t dil);
+
+/* Backward over N samples: dx written (added with SOAR_GN_ACCUMULATE_DX),
+ * dweight += and dbias += (summed over samples); any output may be NULL.
+ * dweight/dbias come from per-tile partials added in a fixed order in
+ * float64, so results are reproducible.
+ * Replaces: conv2d_dw_backward (cuda_kernels.hpp:67-70,
+ * src/cuda/ops/convolution_kernels.cu:184-333) as Conv2dNode::backward
+ * calls it (src/nn/layers.cpp:73-77), batched over samples. */
+SOAR_API int soar_dw_conv_backward(const float* dy, const float* x,
+                                   const float* weight, float* dx,
+                                   float* dweight, float* dbias, int64_t N,
+                                   int64_t C, int64_t H_in, int64_t W_in,
+                                   int64_t H_out, int64_t W_out, int64_t K,
+                                   int64_t pad, int64_t stride, int64_t dil,
+                                   unsigned flags, void* workspace,
+                                   size_t workspace_bytes, void* stream);
+
+/* Reference signatures, one sample.
+ * Replaces: conv2d_dw_forward (cuda_kernels.hpp:64-66,
+ * convolution_kernels.cu:138-182), called by Conv2d::forward
+ * (layers.cpp:353-355) when groups == C_in == C_out. */
+SOAR_API int soar_conv2d_dw_forward(const float* in, const float* weight,
+                                    const float* bias, float* out, size_t C,
+                                    size_t H_in, size_t W_in, size_t H_out,
+                                    size_t W_out, size_t K, size_t pad,
+                                    size_t stride, size_t dil, void* stream);
+/* grad_in +=, grad_weight +=, grad_bias += (any may be NULL); workspace
+ * owned by the library.  Replaces: conv2d_dw_backward
+ * (cuda_kernels.hpp:67-70). */
+SOAR_API int soar_conv2d_dw_backward(const float* grad_out, const float* in,
+                                     const float* weight, float* grad_in,
+                                     float* grad_weight, float* grad_bias,
+                                     size_t C, size_t H_in, size_t W_in,
+                                     size_t H_out, size_t W_out, size_t K,
+                                     size_t pad, size_t stride, size_t dil,
+                                     void* stream);
+
 /* ---- device arena (replaces VulkanBuffer / CudaMemoryPool storage) ---- */
 /* One hipMalloc'd slab per arena, bump-allocated at `alignment` (a power
  * of two, 256 in the reference).  Allocations made before

@@ -558,3 +558,147 @@ void ref_conv1x1_bwd_f32(const float* grad_out, const float* in, const float* w,
         }
     }
 }
+
+/* ------------------------------------------------------------------ */
+/* depthwise convolution                                               */
+/* ------------------------------------------------------------------ */
+
+static int bad_dw(int64_t N, int64_t C, int64_t H_in, int64_t W_in, int64_t H_out,
+                  int64_t W_out, int64_t K, int64_t pad, int64_t stride, int64_t dil) {
+    return N < 0 || C < 0 || H_in < 0 || W_in < 0 || H_out < 0 || W_out < 0 || K <= 0 ||
+           pad < 0 || stride <= 0 || dil <= 0;
+}
+
+int orc_dw_fwd_f64(const float* x, const float* w, const float* b, int64_t N, int64_t C,
+                   int64_t H_in, int64_t W_in, int64_t H_out, int64_t W_out, int64_t K,
+                   int64_t pad, int64_t stride, int64_t dil, double* y) {
+    if (bad_dw(N, C, H_in, W_in, H_out, W_out, K, pad, stride, dil)) return -1;
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t c = 0; c < C; ++c) {
+            const float* xc = x + (n * C + c) * H_in * W_in;
+            const float* wc = w + c * K * K;
+            double* yc = y + (n * C + c) * H_out * W_out;
+            for (int64_t yo = 0; yo < H_out; ++yo)
+                for (int64_t xo = 0; xo < W_out; ++xo) {
+                    double acc = b ? (double)b[c] : 0.0;
+                    for (int64_t ky = 0; ky < K; ++ky) {
+                        const int64_t yi = yo * stride - pad + ky * dil;
+                        if (yi < 0 || yi >= H_in) continue;
+                        for (int64_t kx = 0; kx < K; ++kx) {
+                            const int64_t xi = xo * stride - pad + kx * dil;
+                            if (xi < 0 || xi >= W_in) continue;
+                            acc += (double)wc[ky * K + kx] * (double)xc[yi * W_in + xi];
+                        }
+                    }
+                    yc[yo * W_out + xo] = acc;
+                }
+        }
+    return 0;
+}
+
+int orc_dw_bwd_f64(const float* dy, const float* x, const float* w, int64_t N, int64_t C,
+                   int64_t H_in, int64_t W_in, int64_t H_out, int64_t W_out, int64_t K,
+                   int64_t pad, int64_t stride, int64_t dil, double* dx, double* dw, double* db) {
+    if (bad_dw(N, C, H_in, W_in, H_out, W_out, K, pad, stride, dil)) return -1;
+    if (dx)
+        for (int64_t i = 0; i < N * C * H_in * W_in; ++i) dx[i] = 0.0;
+    if (dw)
+        for (int64_t i = 0; i < C * K * K; ++i) dw[i] = 0.0;
+    if (db)
+        for (int64_t i = 0; i < C; ++i) db[i] = 0.0;
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t c = 0; c < C; ++c) {
+            const float* xc = x + (n * C + c) * H_in * W_in;
+            const float* gc = dy + (n * C + c) * H_out * W_out;
+            const float* wc = w + c * K * K;
+            for (int64_t yo = 0; yo < H_out; ++yo)
+                for (int64_t xo = 0; xo < W_out; ++xo) {
+                    const double g = (double)gc[yo * W_out + xo];
+                    if (db) db[c] += g;
+                    for (int64_t ky = 0; ky < K; ++ky) {
+                        const int64_t yi = yo * stride - pad + ky * dil;
+                        if (yi < 0 || yi >= H_in) continue;
+                        for (int64_t kx = 0; kx < K; ++kx) {
+                            const int64_t xi = xo * stride - pad + kx * dil;
+                            if (xi < 0 || xi >= W_in) continue;
+                            if (dx)
+                                dx[(n * C + c) * H_in * W_in + yi * W_in + xi] +=
+                                    g * (double)wc[ky * K + kx];
+                            if (dw) dw[c * K * K + ky * K + kx] += g * (double)xc[yi * W_in + xi];
+                        }
+                    }
+                }
+        }
+    return 0;
+}
+
+void ref_dw_fwd_f32(const float* x, const float* w, const float* b, float* y, int64_t C,
+                    int64_t H_in, int64_t W_in, int64_t H_out, int64_t W_out, int64_t K,
+                    int64_t pad, int64_t stride, int64_t dil) {
+    for (int64_t idx = 0; idx < C * H_out * W_out; ++idx) {
+        const int64_t w_out = idx % W_out, t = idx / W_out;
+        const int64_t h_out = t % H_out, c = t / H_out;
+        float sum = b ? b[c] : 0.0f;
+        const float* wc = w + c * K * K;
+        const float* in_c = x + c * H_in * W_in;
+        const int64_t hb = h_out * stride - pad, wb = w_out * stride - pad;
+        for (int64_t kh = 0; kh < K; ++kh) {
+            const int64_t hi = hb + kh * dil;
+            if (hi < 0 || hi >= H_in) continue;
+            for (int64_t kw = 0; kw < K; ++kw) {
+                const int64_t wi = wb + kw * dil;
+                if (wi >= 0 && wi < W_in) sum += in_c[hi * W_in + wi] * wc[kh * K + kw];
+            }
+        }
+        y[idx] = sum;
+    }
+}
+
+void ref_dw_bwd_f32(const float* dy, const float* x, const float* w, float* grad_in,
+                    float* grad_weight, float* grad_bias, int64_t C, int64_t H_in, int64_t W_in,
+                    int64_t H_out, int64_t W_out, int64_t K, int64_t pad, int64_t stride,
+                    int64_t dil) {
+    if (grad_in && w) {
+        for (int64_t idx = 0; idx < C * H_in * W_in; ++idx) {
+            const int64_t wi = idx % W_in, t = idx / W_in;
+            const int64_t hi = t % H_in, c = t / H_in;
+            float sum = 0.0f;
+            const float* wc = w + c * K * K;
+            const float* go = dy + c * H_out * W_out;
+            for (int64_t kh = 0; kh < K; ++kh) {
+                const int64_t nh = hi + pad - kh * dil;
+                if (nh < 0 || nh % stride) continue;
+                const int64_t ho = nh / stride;
+                if (ho >= H_out) continue;
+                for (int64_t kw = 0; kw < K; ++kw) {
+                    const int64_t nw = wi + pad - kw * dil;
+                    if (nw < 0 || nw % stride) continue;
+                    const int64_t wo = nw / stride;
+                    if (wo < W_out) sum += go[ho * W_out + wo] * wc[kh * K + kw];
+                }
+            }
+            grad_in[idx] += sum;
+        }
+    }
+    if (grad_weight && x) {
+        for (int64_t p = 0; p < C * K * K; ++p) {
+            const int64_t kw = p % K, t = p / K, kh = t % K, c = t / K;
+            const float* go = dy + c * H_out * W_out;
+            const float* xc = x + c * H_in * W_in;
+            float sum = 0.0f;
+            for (int64_t i = 0; i < H_out * W_out; ++i) {
+                const int64_t ho = i / W_out, wo = i % W_out;
+                const int64_t hi = ho * stride - pad + kh * dil, wi = wo * stride - pad + kw * dil;
+                if (hi >= 0 && hi < H_in && wi >= 0 && wi < W_in) sum += go[i] * xc[hi * W_in + wi];
+            }
+            grad_weight[p] += sum;
+        }
+    }
+    if (grad_bias) {
+        for (int64_t c = 0; c < C; ++c) {
+            float sum = 0.0f;
+            for (int64_t i = 0; i < H_out * W_out; ++i) sum += dy[c * H_out * W_out + i];
+            grad_bias[c] += sum;
+        }
+    }
+}

@@ -126,6 +126,32 @@ void ref_conv1x1_bwd_f32(const float* grad_out, const float* in, const float* w,
                          float* grad_in, float* grad_weight, float* grad_bias,
                          int64_t C_in, int64_t C_out, int64_t HW);
 
+/* ---- depthwise convolution (groups = C_in = C_out) ---- */
+
+/* float64 truth, N samples: y[n][c][yo][xo] = b[c] + sum_(ky,kx)
+ * w[c][ky][kx] * x[n][c][yo*s - pad + ky*d][xo*s - pad + kx*d], taps outside
+ * the input skipped (zero padding).  b may be NULL. */
+int orc_dw_fwd_f64(const float* x, const float* w, const float* b, int64_t N, int64_t C,
+                   int64_t H_in, int64_t W_in, int64_t H_out, int64_t W_out, int64_t K,
+                   int64_t pad, int64_t stride, int64_t dil, double* y);
+/* float64 truth of the backward: dx (scatter of dy through the taps),
+ * dw[c][ky][kx] = sum_(n,yo,xo) dy * x at the tap, db[c] = sum dy; written,
+ * any may be NULL. */
+int orc_dw_bwd_f64(const float* dy, const float* x, const float* w, int64_t N, int64_t C,
+                   int64_t H_in, int64_t W_in, int64_t H_out, int64_t W_out, int64_t K,
+                   int64_t pad, int64_t stride, int64_t dil, double* dx, double* dw, double* db);
+/* fp32 statements of the reference's depthwise kernels, one sample
+ * (src/cuda/ops/convolution_kernels.cu:138-333): forward (sum = bias, taps
+ * in ky, kx order), and the accumulating backward (grad_in += gather over
+ * taps; grad_weight += per-tap sums; grad_bias += sum).  NULL skips. */
+void ref_dw_fwd_f32(const float* x, const float* w, const float* b, float* y, int64_t C,
+                    int64_t H_in, int64_t W_in, int64_t H_out, int64_t W_out, int64_t K,
+                    int64_t pad, int64_t stride, int64_t dil);
+void ref_dw_bwd_f32(const float* dy, const float* x, const float* w, float* grad_in,
+                    float* grad_weight, float* grad_bias, int64_t C, int64_t H_in, int64_t W_in,
+                    int64_t H_out, int64_t W_out, int64_t K, int64_t pad, int64_t stride,
+                    int64_t dil);
+
 #ifdef __cplusplus
 }
 #endif

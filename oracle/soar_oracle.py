@@ -72,6 +72,11 @@ def lib():
                                           _opt(_D), _opt(_D)]
         L.ref_conv1x1_bwd_f32.argtypes = [_F, _F, _F, _opt(_F), _opt(_F), _opt(_F), _I64, _I64,
                                           _I64]
+        _DWS = [_I64] * 9
+        L.orc_dw_fwd_f64.argtypes = [_F, _F, _opt(_F), _I64] + _DWS + [_D]
+        L.orc_dw_bwd_f64.argtypes = [_F, _F, _F, _I64] + _DWS + [_opt(_D), _opt(_D), _opt(_D)]
+        L.ref_dw_fwd_f32.argtypes = [_F, _F, _opt(_F), _F] + _DWS
+        L.ref_dw_bwd_f32.argtypes = [_F, _F, _F, _opt(_F), _opt(_F), _opt(_F)] + _DWS
         L.ref_gn_silu_fwd_bwd_f32.argtypes = [_F, _opt(_F), _opt(_F), _opt(_F), _I64, _I64,
                                               _I64, _I64, ctypes.c_float, ctypes.c_int, _F,
                                               _F, _F, _F, _F, _F, _opt(_F), _opt(_F),
@@ -237,3 +242,48 @@ def ref_conv1x1_bwd_f32(go, x, w, C_in, C_out, HW, grad_in=None, grad_weight=Non
     lib().ref_conv1x1_bwd_f32(_f32(go).reshape(-1), _f32(x).reshape(-1), _f32(w).reshape(-1),
                               gi, gw, gb, C_in, C_out, HW)
     return gi, gw, gb
+
+
+# ---- depthwise convolution --------------------------------------------------------
+
+def dw_out_size(H, K, pad, stride, dil):
+    """Conv2d::forward's output size (src/nn/layers.cpp:330-332)."""
+    return (H + 2 * pad - (dil * (K - 1) + 1)) // stride + 1
+
+
+def dw_fwd_f64(x, w, b, N, C, H, W, K, pad, stride, dil):
+    Ho, Wo = dw_out_size(H, K, pad, stride, dil), dw_out_size(W, K, pad, stride, dil)
+    y = np.empty(N * C * Ho * Wo)
+    rc = lib().orc_dw_fwd_f64(_f32(x).reshape(-1), _f32(w).reshape(-1), _f32(b), N, C, H, W,
+                              Ho, Wo, K, pad, stride, dil, y)
+    assert rc == 0, rc
+    return y.reshape(N, C, Ho, Wo)
+
+
+def dw_bwd_f64(dy, x, w, N, C, H, W, K, pad, stride, dil):
+    Ho, Wo = dw_out_size(H, K, pad, stride, dil), dw_out_size(W, K, pad, stride, dil)
+    dx = np.empty(N * C * H * W)
+    dw = np.empty(C * K * K)
+    db = np.empty(C)
+    rc = lib().orc_dw_bwd_f64(_f32(dy).reshape(-1), _f32(x).reshape(-1), _f32(w).reshape(-1),
+                              N, C, H, W, Ho, Wo, K, pad, stride, dil, dx, dw, db)
+    assert rc == 0, rc
+    return dx.reshape(N, C, H, W), dw.reshape(C, K, K), db
+
+
+def ref_dw_fwd_f32(x, w, b, C, H, W, K, pad, stride, dil):
+    Ho, Wo = dw_out_size(H, K, pad, stride, dil), dw_out_size(W, K, pad, stride, dil)
+    y = np.empty(C * Ho * Wo, np.float32)
+    lib().ref_dw_fwd_f32(_f32(x).reshape(-1), _f32(w).reshape(-1), _f32(b), y, C, H, W, Ho, Wo,
+                         K, pad, stride, dil)
+    return y.reshape(C, Ho, Wo)
+
+
+def ref_dw_bwd_f32(dy, x, w, C, H, W, K, pad, stride, dil, grad_in=None):
+    Ho, Wo = dw_out_size(H, K, pad, stride, dil), dw_out_size(W, K, pad, stride, dil)
+    gi = np.zeros(C * H * W, np.float32) if grad_in is None else grad_in
+    gw = np.zeros(C * K * K, np.float32)
+    gb = np.zeros(C, np.float32)
+    lib().ref_dw_bwd_f32(_f32(dy).reshape(-1), _f32(x).reshape(-1), _f32(w).reshape(-1), gi, gw,
+                         gb, C, H, W, Ho, Wo, K, pad, stride, dil)
+    return gi.reshape(C, H, W), gw.reshape(C, K, K), gb

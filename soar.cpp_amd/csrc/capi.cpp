@@ -218,6 +218,80 @@ void prof_end(hipStream_t s, int token) {
 }  // namespace gn
 }  // namespace soar
 
+namespace {
+
+int check_pw_shape(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t* in_elems,
+                   int64_t* out_elems) {
+    if (N < 0 || C_in < 0 || C_out < 0 || HW < 0)
+        return fail(SOAR_EINVAL, "negative dimension (N=%lld C_in=%lld C_out=%lld HW=%lld)",
+                    (long long)N, (long long)C_in, (long long)C_out, (long long)HW);
+    int64_t a = 0, b = 0, c = 0, d = 0, wsz = 0;
+    if (__builtin_mul_overflow(N, C_in, &a) || __builtin_mul_overflow(a, HW, &b) ||
+        __builtin_mul_overflow(N, C_out, &c) || __builtin_mul_overflow(c, HW, &d) ||
+        __builtin_mul_overflow(C_in, C_out, &wsz) || b > INT64_MAX / 4 || d > INT64_MAX / 4 ||
+        wsz > INT64_MAX / 4)
+        return fail(SOAR_EINVAL, "pointwise convolution shape overflows");
+    // (the backward runs the same kernel with C_out as its reduction axis)
+    if (!soar::gn::pw_offsets_fit(std::max(C_in, C_out), HW))
+        return fail(SOAR_EINVAL,
+                    "HW=%lld or C=%lld exceeds the pointwise kernel's 32-bit in-sample offsets",
+                    (long long)HW, (long long)std::max(C_in, C_out));
+    *in_elems = b;
+    *out_elems = d;
+    return SOAR_OK;
+}
+
+// Grid of the convolution: one wave per (sample, pixel chunk).
+bool pw_grid_fits(int64_t N, int64_t HW, int64_t chunk) {
+    const int64_t cpp = (HW + chunk - 1) / chunk;
+    return N <= (int64_t)0x7fffffff / std::max<int64_t>(cpp, 1);
+}
+
+}  // namespace
+
+namespace {
+
+int check_dw_shape(const soar::gn::DwShape& sh, int64_t* in_elems, int64_t* out_elems) {
+    if (sh.N < 0 || sh.C < 0 || sh.Hi < 0 || sh.Wi < 0 || sh.Ho < 0 || sh.Wo < 0)
+        return fail(SOAR_EINVAL, "negative dimension");
+    if (sh.K <= 0 || sh.S <= 0 || sh.D <= 0 || sh.pad < 0)
+        return fail(SOAR_EINVAL, "kernel size, stride and dilation must be positive, pad >= 0");
+    int64_t nc = 0, a = 0, b = 0, c = 0, d = 0, kk = 0, span = 0;
+    if (__builtin_mul_overflow(sh.N, sh.C, &nc) || __builtin_mul_overflow(nc, sh.Hi, &a) ||
+        __builtin_mul_overflow(a, sh.Wi, &b) || __builtin_mul_overflow(nc, sh.Ho, &c) ||
+        __builtin_mul_overflow(c, sh.Wo, &d) || __builtin_mul_overflow(sh.K, sh.K, &kk) ||
+        __builtin_mul_overflow(sh.K - 1, sh.D, &span) || b > INT64_MAX / 4 ||
+        d > INT64_MAX / 4 || kk > (1 << 20) || sh.pad > (1 << 30) || span > (1 << 30) ||
+        sh.S > (1 << 20))
+        return fail(SOAR_EINVAL, "depthwise convolution shape overflows");
+    *in_elems = b;
+    *out_elems = d;
+    return SOAR_OK;
+}
+
+soar::gn::DwShape dw_shape(int64_t N, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho,
+                           int64_t Wo, int64_t K, int64_t pad, int64_t S, int64_t D) {
+    soar::gn::DwShape sh;
+    sh.N = N;
+    sh.C = C;
+    sh.Hi = Hi;
+    sh.Wi = Wi;
+    sh.Ho = Ho;
+    sh.Wo = Wo;
+    sh.K = K;
+    sh.pad = pad;
+    sh.S = S;
+    sh.D = D;
+    return sh;
+}
+
+bool dw_grids_fit(const soar::gn::DwShape& sh) {
+    return soar::gn::dw_grid_blocks(sh, true) <= 0x7fffffff &&
+           soar::gn::dw_grid_blocks(sh, false) <= 0x7fffffff;
+}
+
+}  // namespace
+
 extern "C" {
 
 SOAR_API const char* soar_last_error(void) { return g_err.c_str(); }
@@ -341,36 +415,6 @@ SOAR_API int soar_group_norm_backward(const float* grad_out, const float* in,
 
 // ---- pointwise convolution --------------------------------------------------
 
-namespace {
-
-int check_pw_shape(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t* in_elems,
-                   int64_t* out_elems) {
-    if (N < 0 || C_in < 0 || C_out < 0 || HW < 0)
-        return fail(SOAR_EINVAL, "negative dimension (N=%lld C_in=%lld C_out=%lld HW=%lld)",
-                    (long long)N, (long long)C_in, (long long)C_out, (long long)HW);
-    int64_t a = 0, b = 0, c = 0, d = 0, wsz = 0;
-    if (__builtin_mul_overflow(N, C_in, &a) || __builtin_mul_overflow(a, HW, &b) ||
-        __builtin_mul_overflow(N, C_out, &c) || __builtin_mul_overflow(c, HW, &d) ||
-        __builtin_mul_overflow(C_in, C_out, &wsz) || b > INT64_MAX / 4 || d > INT64_MAX / 4 ||
-        wsz > INT64_MAX / 4)
-        return fail(SOAR_EINVAL, "pointwise convolution shape overflows");
-    // (the backward runs the same kernel with C_out as its reduction axis)
-    if (!soar::gn::pw_offsets_fit(std::max(C_in, C_out), HW))
-        return fail(SOAR_EINVAL,
-                    "HW=%lld or C=%lld exceeds the pointwise kernel's 32-bit in-sample offsets",
-                    (long long)HW, (long long)std::max(C_in, C_out));
-    *in_elems = b;
-    *out_elems = d;
-    return SOAR_OK;
-}
-
-// Grid of the convolution: one wave per (sample, pixel chunk).
-bool pw_grid_fits(int64_t N, int64_t HW, int64_t chunk) {
-    const int64_t cpp = (HW + chunk - 1) / chunk;
-    return N <= (int64_t)0x7fffffff / std::max<int64_t>(cpp, 1);
-}
-
-}  // namespace
 
 SOAR_API int soar_conv2d_1x1_forward(const float* in, const float* weight, const float* bias,
                                      float* out, size_t C_in, size_t C_out, size_t HW,
@@ -519,6 +563,127 @@ SOAR_API int soar_conv2d_1x1_backward(const float* grad_out, const float* in, co
     return soar_pw_conv_backward(grad_out, in, weight, grad_in, grad_weight, grad_bias, 1,
                                  (int64_t)C_in, (int64_t)C_out, (int64_t)HW,
                                  SOAR_GN_ACCUMULATE_DX, ws, need, stream);
+}
+
+// ---- depthwise convolution -----------------------------------------------------
+
+
+SOAR_API int soar_dw_conv_forward(const float* x, const float* weight, const float* bias,
+                                  float* y, int64_t N, int64_t C, int64_t H_in, int64_t W_in,
+                                  int64_t H_out, int64_t W_out, int64_t K, int64_t pad,
+                                  int64_t stride, int64_t dil, void* stream) {
+    const soar::gn::DwShape sh = dw_shape(N, C, H_in, W_in, H_out, W_out, K, pad, stride, dil);
+    int64_t ie = 0, oe = 0;
+    int rc = check_dw_shape(sh, &ie, &oe);
+    if (rc) return rc;
+    if (oe == 0) return ok();
+    if ((rc = require_device())) return rc;
+    if ((rc = check_dev(y, (size_t)oe * 4, "y")) ||
+        (rc = check_dev(weight, (size_t)(C * K * K) * 4, "weight")) ||
+        (rc = check_dev_opt(bias, (size_t)C * 4, "bias")) ||
+        (ie > 0 && (rc = check_dev(x, (size_t)ie * 4, "x"))))
+        return rc;
+    if (!dw_grids_fit(sh)) return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    hipError_t e = soar::gn::launch_dw_forward(sh, x, weight, bias, y,
+                                               static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "depthwise convolution launch");
+}
+
+SOAR_API size_t soar_dw_conv_backward_workspace_bytes(int64_t N, int64_t C, int64_t H_in,
+                                                      int64_t W_in, int64_t H_out,
+                                                      int64_t W_out, int64_t K, int64_t stride,
+                                                      int64_t dil) {
+    const soar::gn::DwShape sh = dw_shape(N, C, H_in, W_in, H_out, W_out, K, 0, stride, dil);
+    int64_t ie = 0, oe = 0;
+    if (check_dw_shape(sh, &ie, &oe) != SOAR_OK) {
+        g_err.clear();
+        return (size_t)-1;
+    }
+    return soar::gn::dw_bwd_workspace_bytes(sh);
+}
+
+SOAR_API int soar_dw_conv_backward(const float* dy, const float* x, const float* weight,
+                                   float* dx, float* dweight, float* dbias, int64_t N, int64_t C,
+                                   int64_t H_in, int64_t W_in, int64_t H_out, int64_t W_out,
+                                   int64_t K, int64_t pad, int64_t stride, int64_t dil,
+                                   unsigned flags, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    const soar::gn::DwShape sh = dw_shape(N, C, H_in, W_in, H_out, W_out, K, pad, stride, dil);
+    int64_t ie = 0, oe = 0;
+    int rc = check_dw_shape(sh, &ie, &oe);
+    if (rc) return rc;
+    if (flags & ~SOAR_GN_ACCUMULATE_DX)
+        return fail(SOAR_EINVAL, "unsupported flags 0x%x (SOAR_GN_ACCUMULATE_DX only)", flags);
+    if ((!dx && !dweight && !dbias) || N * C == 0) return ok();
+    if ((rc = require_device())) return rc;
+    const size_t wb = (size_t)(C * K * K) * 4;
+    if ((oe > 0 && (rc = check_dev(dy, (size_t)oe * 4, "dy"))) ||
+        (dx && ie > 0 && (rc = check_dev(weight, wb, "weight"))) ||
+        (dweight && ie > 0 && (rc = check_dev(x, (size_t)ie * 4, "x"))) ||
+        (ie > 0 && (rc = check_dev_opt(dx, (size_t)ie * 4, "dx"))) ||
+        (rc = check_dev_opt(dweight, wb, "dweight")) ||
+        (rc = check_dev_opt(dbias, (size_t)C * 4, "dbias")))
+        return rc;
+    if (!dw_grids_fit(sh)) return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    const size_t need = (dweight || dbias) ? soar::gn::dw_bwd_workspace_bytes(sh) : 0;
+    if (need) {
+        if (workspace_bytes < need)
+            return fail(SOAR_EINVAL,
+                        "workspace of %zu bytes is smaller than the %zu this shape needs",
+                        workspace_bytes, need);
+        if ((rc = check_dev(workspace, need, "workspace"))) return rc;
+    }
+    // with no input pixels, dweight gets nothing and dx is empty
+    hipError_t e = soar::gn::launch_dw_backward(sh, dy, x, weight, ie > 0 ? dx : nullptr,
+                                                ie > 0 ? dweight : nullptr, oe > 0 ? dbias : nullptr,
+                                                (flags & SOAR_GN_ACCUMULATE_DX) != 0, workspace,
+                                                static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "depthwise convolution backward launch");
+    return ok();
+}
+
+SOAR_API int soar_conv2d_dw_forward(const float* in, const float* weight, const float* bias,
+                                    float* out, size_t C, size_t H_in, size_t W_in,
+                                    size_t H_out, size_t W_out, size_t K, size_t pad,
+                                    size_t stride, size_t dil, void* stream) {
+    const size_t lim = (size_t)1 << 40;
+    if (C > lim || H_in > lim || W_in > lim || H_out > lim || W_out > lim || K > lim ||
+        pad > lim || stride > lim || dil > lim)
+        return fail(SOAR_EINVAL, "dimension too large");
+    return soar_dw_conv_forward(in, weight, bias, out, 1, (int64_t)C, (int64_t)H_in,
+                                (int64_t)W_in, (int64_t)H_out, (int64_t)W_out, (int64_t)K,
+                                (int64_t)pad, (int64_t)stride, (int64_t)dil, stream);
+}
+
+SOAR_API int soar_conv2d_dw_backward(const float* grad_out, const float* in, const float* weight,
+                                     float* grad_in, float* grad_weight, float* grad_bias,
+                                     size_t C, size_t H_in, size_t W_in, size_t H_out,
+                                     size_t W_out, size_t K, size_t pad, size_t stride,
+                                     size_t dil, void* stream) {
+    const size_t lim = (size_t)1 << 40;
+    if (C > lim || H_in > lim || W_in > lim || H_out > lim || W_out > lim || K > lim ||
+        pad > lim || stride > lim || dil > lim)
+        return fail(SOAR_EINVAL, "dimension too large");
+    const size_t need = soar_dw_conv_backward_workspace_bytes(
+        1, (int64_t)C, (int64_t)H_in, (int64_t)W_in, (int64_t)H_out, (int64_t)W_out, (int64_t)K,
+        (int64_t)stride, (int64_t)dil);
+    if (need == (size_t)-1) {
+        int64_t ie = 0, oe = 0;
+        return check_dw_shape(dw_shape(1, (int64_t)C, (int64_t)H_in, (int64_t)W_in,
+                                       (int64_t)H_out, (int64_t)W_out, (int64_t)K, (int64_t)pad,
+                                       (int64_t)stride, (int64_t)dil),
+                              &ie, &oe);
+    }
+    void* ws = nullptr;
+    if (need && (grad_weight || grad_bias)) {
+        int rc = require_device();
+        if (rc) return rc;
+        if ((rc = owned_workspace(need, &ws))) return rc;
+    }
+    return soar_dw_conv_backward(grad_out, in, weight, grad_in, grad_weight, grad_bias, 1,
+                                 (int64_t)C, (int64_t)H_in, (int64_t)W_in, (int64_t)H_out,
+                                 (int64_t)W_out, (int64_t)K, (int64_t)pad, (int64_t)stride,
+                                 (int64_t)dil, SOAR_GN_ACCUMULATE_DX, ws, need, stream);
 }
 
 #define SOAR_ELEMWISE_PRELUDE(n)                                   \

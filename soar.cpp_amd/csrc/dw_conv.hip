@@ -1,0 +1,485 @@
+// dw_conv.hip - depthwise convolution (groups = C_in = C_out) forward and
+// backward for gfx950: the K x K / stride / dilation convolutions of the
+// CBA blocks Down.dw (k3 s2), LKR.dw (k5, k7) and the Ctx branches (k3 with
+// dilation 1, 3, 5) of pomagrenate/soar.cpp (src/nn/blocks.cpp:449-500).
+//
+// Reference: src/cuda/ops/convolution_kernels.cu:138-333 (one thread per
+// output reading every tap from global memory) and the CPU loops of
+// src/nn/layers.cpp:400-428, 150-230.  Output size and zero padding follow
+// Conv2d (layers.cpp:326-332): taps outside the input are skipped.
+//
+// Fast kernels (template K, S, D for the configurations the model uses):
+// a 256-thread block owns a 32 x 64 output tile of one (n, c) plane.  The
+// input tile it needs, halo included, is staged once in LDS with coalesced
+// row loads (zeros outside the image); each thread then computes 8
+// consecutive outputs of one row, reading each of the K input row segments
+// it touches with 16-byte LDS loads into registers and applying all K
+// taps of that row from registers.  Per output that is about K*(8S+(K-1)D)/8
+// LDS floats instead of K*K, and the weights are wave-uniform scalars.
+//   forward  y  = b + w (*) x
+//   dx, S=1  dx (+)= flip(w) (*) dy with pad' = (K-1)*D - pad (the adjoint
+//            of a stride-1 convolution is the convolution with the flipped
+//            kernel), same kernel
+//   dx, S>1  gather per input element over the taps that divide (as the
+//            reference's k_conv2d_dw_backward_input)
+//   dw, db   the block's K*K tap sums and its dy sum over its tile, reduced
+//            in the block in a fixed order, written as per-tile partials and
+//            added by a fixed-order float64 finish
+// Other (K, S, D): generic kernels with the same results up to summation
+// order.
+#include <algorithm>
+#include <type_traits>
+
+#include "gn_internal.hpp"
+#include "soar_gn.h"
+
+namespace soar {
+namespace gn {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTH = 32;       // output rows per tile
+constexpr int kTW = 64;       // output columns per tile
+constexpr int kPer = 8;       // consecutive outputs per thread
+constexpr int kDwThreads = 256;
+
+constexpr int round4(int v) { return (v + 3) / 4 * 4; }
+
+template <int K, int S, int D>
+struct Tile {
+    static constexpr int IH = (kTH - 1) * S + (K - 1) * D + 1;   // input rows
+    static constexpr int IW = (kTW - 1) * S + (K - 1) * D + 1;   // input columns
+    static constexpr int SL = (kPer - 1) * S + (K - 1) * D + 1;  // a thread's row segment
+    static constexpr int SL4 = round4(SL);
+    // row pitch: every thread's 16-byte segment reads stay inside the row
+    static constexpr int IWP = round4(IW) > (kTW - kPer) * S + SL4 ? round4(IW)
+                                                                   : (kTW - kPer) * S + SL4;
+    static constexpr int floats = IH * IWP;
+};
+
+struct TileIdx {
+    int64_t plane, n, c, tix, oy0, ox0;
+};
+
+__device__ __forceinline__ TileIdx tile_idx(int64_t C, int64_t tiles_x, int64_t tpp) {
+    TileIdx t;
+    const int64_t b = blockIdx.x;
+    t.plane = b / tpp;
+    t.tix = b - t.plane * tpp;
+    t.n = t.plane / C;
+    t.c = t.plane - t.n * C;
+    const int64_t ty = t.tix / tiles_x;
+    t.oy0 = ty * kTH;
+    t.ox0 = (t.tix - ty * tiles_x) * kTW;
+    return t;
+}
+
+// Stage input rows [iy0, iy0 + IH) x columns [ix0, ix0 + IWP) of plane `ip`
+// (zeros outside the image and past column IW).
+template <int K, int S, int D>
+__device__ __forceinline__ void fill_tile(float* tile, const float* __restrict__ ip, int64_t iy0,
+                                          int64_t ix0, int64_t Hi, int64_t Wi) {
+    using T = Tile<K, S, D>;
+    for (int i = threadIdx.x; i < T::floats; i += kDwThreads) {
+        const int r = i / T::IWP, col = i - r * T::IWP;
+        const int64_t yy = iy0 + r, xx = ix0 + col;
+        float v = 0.0f;
+        if (col < T::IW && yy >= 0 && yy < Hi && xx >= 0 && xx < Wi) v = ip[yy * Wi + xx];
+        tile[i] = v;
+    }
+}
+
+// Row segment of a thread: SL4 floats of LDS row `lrow` from column c0*S.
+template <int K, int S, int D>
+__device__ __forceinline__ void load_seg(const float* tile, int lrow, int c0,
+                                         float (&seg)[Tile<K, S, D>::SL4]) {
+    using T = Tile<K, S, D>;
+    const f4* p = reinterpret_cast<const f4*>(tile + lrow * T::IWP + c0 * S);
+#pragma unroll
+    for (int q = 0; q < T::SL4 / 4; ++q) {
+        const f4 v = p[q];
+        seg[4 * q] = v.x;
+        seg[4 * q + 1] = v.y;
+        seg[4 * q + 2] = v.z;
+        seg[4 * q + 3] = v.w;
+    }
+}
+
+// out (+)= bias + w (*) in over one 32 x 64 output tile per block.  FLIP
+// applies the kernel rotated by 180 degrees (the stride-1 input gradient).
+template <int K, int S, int D, bool FLIP, bool ACC, bool BIAS>
+__global__ __launch_bounds__(kDwThreads) void k_dw_conv(
+    const float* __restrict__ in, const float* __restrict__ w, const float* __restrict__ bias,
+    float* __restrict__ out, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo,
+    int64_t pad, int64_t tiles_x, int64_t tpp) {
+    using T = Tile<K, S, D>;
+    __shared__ __attribute__((aligned(16))) float tile[T::floats];
+    const TileIdx ti = tile_idx(C, tiles_x, tpp);
+    fill_tile<K, S, D>(tile, in + ti.plane * Hi * Wi, ti.oy0 * S - pad, ti.ox0 * S - pad, Hi,
+                       Wi);
+    float wr[K * K];
+#pragma unroll
+    for (int k = 0; k < K * K; ++k) wr[k] = w[ti.c * K * K + (FLIP ? K * K - 1 - k : k)];
+    const int t = threadIdx.x, r = t >> 3, c0 = (t & 7) * kPer;
+    float acc[kPer];
+    const float b0 = BIAS ? bias[ti.c] : 0.0f;
+#pragma unroll
+    for (int c = 0; c < kPer; ++c) acc[c] = b0;
+    __syncthreads();
+#pragma unroll
+    for (int ky = 0; ky < K; ++ky) {
+        float seg[T::SL4];
+        load_seg<K, S, D>(tile, r * S + ky * D, c0, seg);
+#pragma unroll
+        for (int kx = 0; kx < K; ++kx)
+#pragma unroll
+            for (int c = 0; c < kPer; ++c)
+                acc[c] = fmaf(wr[ky * K + kx], seg[c * S + kx * D], acc[c]);
+    }
+    const int64_t oy = ti.oy0 + r;
+    if (oy >= Ho) return;
+    float* orow = out + ti.plane * Ho * Wo + oy * Wo;
+    const int64_t ox = ti.ox0 + c0;
+    if (ox + kPer <= Wo && ((reinterpret_cast<uintptr_t>(orow + ox) & 15) == 0)) {
+        f4* o4 = reinterpret_cast<f4*>(orow + ox);
+        f4 v0 = {acc[0], acc[1], acc[2], acc[3]}, v1 = {acc[4], acc[5], acc[6], acc[7]};
+        if (ACC) {
+            v0 += o4[0];
+            v1 += o4[1];
+        }
+        o4[0] = v0;
+        o4[1] = v1;
+    } else {
+#pragma unroll
+        for (int c = 0; c < kPer; ++c)
+            if (ox + c < Wo) orow[ox + c] = ACC ? orow[ox + c] + acc[c] : acc[c];
+    }
+}
+
+// Per-tile weight and bias gradient partials: part[g][c*(K*K+1) + k] with
+// g = n*tpp + tile, k < K*K the tap sums sum dy*x, k = K*K the dy sum.
+template <int K, int S, int D>
+__global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
+    const float* __restrict__ dy, const float* __restrict__ x, float* __restrict__ part,
+    int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x,
+    int64_t tpp) {
+    using T = Tile<K, S, D>;
+    constexpr int KK1 = K * K + 1;
+    __shared__ __attribute__((aligned(16))) float tile[T::floats];
+    __shared__ float red[kDwThreads / 64][KK1];
+    const TileIdx ti = tile_idx(C, tiles_x, tpp);
+    fill_tile<K, S, D>(tile, x + ti.plane * Hi * Wi, ti.oy0 * S - pad, ti.ox0 * S - pad, Hi, Wi);
+    const int t = threadIdx.x, r = t >> 3, c0 = (t & 7) * kPer;
+    const int64_t oy = ti.oy0 + r, ox = ti.ox0 + c0;
+    float g[kPer];
+    const float* grow = dy + ti.plane * Ho * Wo + oy * Wo;
+#pragma unroll
+    for (int c = 0; c < kPer; ++c) g[c] = (oy < Ho && ox + c < Wo) ? grow[ox + c] : 0.0f;
+    float sw[KK1];
+#pragma unroll
+    for (int k = 0; k < KK1; ++k) sw[k] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kPer; ++c) sw[K * K] += g[c];
+    __syncthreads();
+#pragma unroll
+    for (int ky = 0; ky < K; ++ky) {
+        float seg[T::SL4];
+        load_seg<K, S, D>(tile, r * S + ky * D, c0, seg);
+#pragma unroll
+        for (int kx = 0; kx < K; ++kx)
+#pragma unroll
+            for (int c = 0; c < kPer; ++c)
+                sw[ky * K + kx] = fmaf(g[c], seg[c * S + kx * D], sw[ky * K + kx]);
+    }
+    // block sum in a fixed order: wave trees, then the four waves in order
+#pragma unroll
+    for (int k = 0; k < KK1; ++k) {
+        float v = sw[k];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off);
+        sw[k] = v;
+    }
+    const int lane = t & 63, wv = t >> 6;
+    if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < KK1; ++k) red[wv][k] = sw[k];
+    }
+    __syncthreads();
+    if (t < KK1) {
+        const float v = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
+        part[(ti.n * tpp + ti.tix) * (C * KK1) + ti.c * KK1 + t] = v;
+    }
+}
+
+// ---- generic kernels (any K, S, D): one thread per output element --------
+
+template <bool FLIP, bool ACC>
+__global__ void k_dw_conv_generic(const float* __restrict__ in, const float* __restrict__ w,
+                                  const float* __restrict__ bias, float* __restrict__ out,
+                                  int64_t NC, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho,
+                                  int64_t Wo, int64_t K, int64_t pad, int64_t S, int64_t D) {
+    const int64_t total = NC * Ho * Wo;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t xo = i % Wo, tt = i / Wo, yo = tt % Ho, plane = tt / Ho, c = plane % C;
+        const float* ip = in + plane * Hi * Wi;
+        const float* wc = w + c * K * K;
+        float acc = bias ? bias[c] : 0.0f;
+        for (int64_t ky = 0; ky < K; ++ky) {
+            const int64_t yi = yo * S - pad + ky * D;
+            if (yi < 0 || yi >= Hi) continue;
+            for (int64_t kx = 0; kx < K; ++kx) {
+                const int64_t xi = xo * S - pad + kx * D;
+                if (xi < 0 || xi >= Wi) continue;
+                const int64_t k = ky * K + kx;
+                acc = fmaf(wc[FLIP ? K * K - 1 - k : k], ip[yi * Wi + xi], acc);
+            }
+        }
+        out[i] = ACC ? out[i] + acc : acc;
+    }
+}
+
+// dx (+)= gather of dy over the taps of each input element (any stride).
+template <bool ACC>
+__global__ void k_dw_dx_gather(const float* __restrict__ dy, const float* __restrict__ w,
+                               float* __restrict__ dx, int64_t NC, int64_t C, int64_t Hi,
+                               int64_t Wi, int64_t Ho, int64_t Wo, int64_t K, int64_t pad,
+                               int64_t S, int64_t D) {
+    const int64_t total = NC * Hi * Wi;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t xi = i % Wi, tt = i / Wi, yi = tt % Hi, plane = tt / Hi, c = plane % C;
+        const float* gp = dy + plane * Ho * Wo;
+        const float* wc = w + c * K * K;
+        float acc = 0.0f;
+        for (int64_t ky = 0; ky < K; ++ky) {
+            const int64_t nh = yi + pad - ky * D;
+            if (nh < 0 || nh % S) continue;
+            const int64_t yo = nh / S;
+            if (yo >= Ho) continue;
+            for (int64_t kx = 0; kx < K; ++kx) {
+                const int64_t nw = xi + pad - kx * D;
+                if (nw < 0 || nw % S) continue;
+                const int64_t xo = nw / S;
+                if (xo < Wo) acc = fmaf(gp[yo * Wo + xo], wc[ky * K + kx], acc);
+            }
+        }
+        dx[i] = ACC ? dx[i] + acc : acc;
+    }
+}
+
+// One block per (c, k): k < K*K the tap sum of dy*x over all samples and
+// outputs, k = K*K the dy sum; added into dw / db (fixed order).
+__global__ __launch_bounds__(256) void k_dw_wgrad_generic(
+    const float* __restrict__ dy, const float* __restrict__ x, float* __restrict__ dw,
+    float* __restrict__ db, int64_t N, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo,
+    int64_t K, int64_t pad, int64_t S, int64_t D) {
+    __shared__ double red[256];
+    const int64_t KK1 = K * K + 1;
+    const int64_t c = blockIdx.x / KK1, k = blockIdx.x - c * KK1;
+    if ((k < K * K && !dw) || (k == K * K && !db)) return;
+    const int64_t ky = k / K, kx = k - ky * K;
+    double acc = 0.0;
+    for (int64_t n = 0; n < N; ++n) {
+        const float* gp = dy + (n * C + c) * Ho * Wo;
+        const float* xp = x + (n * C + c) * Hi * Wi;
+        for (int64_t i = threadIdx.x; i < Ho * Wo; i += 256) {
+            if (k == K * K) {
+                acc += (double)gp[i];
+                continue;
+            }
+            const int64_t yo = i / Wo, xo = i - yo * Wo;
+            const int64_t yi = yo * S - pad + ky * D, xi = xo * S - pad + kx * D;
+            if (yi >= 0 && yi < Hi && xi >= 0 && xi < Wi)
+                acc += (double)gp[i] * (double)xp[yi * Wi + xi];
+        }
+    }
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        float* o = k < K * K ? &dw[c * K * K + k] : &db[c];
+        *o = (float)((double)*o + red[0]);
+    }
+}
+
+// dw[c*K*K + k] += sum_g part[g][c*KK1 + k], db[c] += sum_g part[g][c*KK1 + K*K]
+// (float64, g ascending in 16 fixed segments; see k_sum_partials).
+__global__ __launch_bounds__(1024) void k_dw_wgrad_finish(const float* __restrict__ part,
+                                                          float* __restrict__ dw,
+                                                          float* __restrict__ db, int64_t E,
+                                                          int64_t G, int64_t KK1) {
+    __shared__ double lds[16][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+    const int64_t g0 = wv * G / 16, g1 = (wv + 1) * G / 16;
+    double sum = 0.0;
+    if (e < E) {
+        constexpr int kU = 8;
+        int64_t gg = g0;
+        for (; gg + kU <= g1; gg += kU) {
+            float v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) v[u] = part[(gg + u) * E + e];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) sum += (double)v[u];
+        }
+        for (; gg < g1; ++gg) sum += (double)part[gg * E + e];
+    }
+    lds[wv][lane] = sum;
+    __syncthreads();
+    if (wv == 0 && e < E) {
+        double tsum = 0.0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tsum += lds[i][lane];
+        const int64_t c = e / KK1, k = e - c * KK1;
+        float* o = k < KK1 - 1 ? (dw ? &dw[c * (KK1 - 1) + k] : nullptr) : db ? &db[c] : nullptr;
+        if (o) *o = (float)((double)*o + tsum);
+    }
+}
+
+template <typename F>
+void bsel(bool b, F&& f) {
+    if (b)
+        f(std::true_type{});
+    else
+        f(std::false_type{});
+}
+
+template <int K, int S, int D>
+struct Cfg {
+    static constexpr int k = K, s = S, d = D;
+};
+
+// Calls f(Cfg<K,S,D>{}) for a configuration with a fast kernel; false if
+// there is none.
+template <typename F>
+bool fast_cfg(int64_t K, int64_t S, int64_t D, F&& f) {
+    if (K == 3 && S == 1 && D == 1) return f(Cfg<3, 1, 1>{}), true;
+    if (K == 3 && S == 2 && D == 1) return f(Cfg<3, 2, 1>{}), true;
+    if (K == 5 && S == 1 && D == 1) return f(Cfg<5, 1, 1>{}), true;
+    if (K == 7 && S == 1 && D == 1) return f(Cfg<7, 1, 1>{}), true;
+    if (K == 3 && S == 1 && D == 2) return f(Cfg<3, 1, 2>{}), true;
+    if (K == 3 && S == 1 && D == 3) return f(Cfg<3, 1, 3>{}), true;
+    if (K == 3 && S == 1 && D == 5) return f(Cfg<3, 1, 5>{}), true;
+    return false;
+}
+
+int64_t tiles_of(int64_t H, int64_t W, int64_t* tiles_x) {
+    *tiles_x = (W + kTW - 1) / kTW;
+    return ((H + kTH - 1) / kTH) * *tiles_x;
+}
+
+unsigned grid_stride_blocks(int64_t total) {
+    const int64_t b = (total + 255) / 256;
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(b, 65536));
+}
+
+}  // namespace
+
+bool dw_has_fast(int64_t K, int64_t S, int64_t D) {
+    return fast_cfg(K, S, D, [](auto) {});
+}
+
+size_t dw_bwd_workspace_bytes(const DwShape& sh) {
+    if (!dw_has_fast(sh.K, sh.S, sh.D)) return 0;
+    int64_t tx = 0;
+    const int64_t tpp = tiles_of(sh.Ho, sh.Wo, &tx);
+    const size_t b = sizeof(float) * (size_t)(sh.N * tpp) * (size_t)(sh.C * (sh.K * sh.K + 1));
+    return (b + 255) & ~(size_t)255;
+}
+
+int64_t dw_grid_blocks(const DwShape& sh, bool output_tiles) {
+    int64_t tx = 0;
+    const int64_t tpp = output_tiles ? tiles_of(sh.Ho, sh.Wo, &tx) : tiles_of(sh.Hi, sh.Wi, &tx);
+    return sh.N * sh.C * tpp;
+}
+
+hipError_t launch_dw_forward(const DwShape& sh, const float* x, const float* w,
+                             const float* bias, float* y, hipStream_t s) {
+    if (sh.N * sh.C * sh.Ho * sh.Wo == 0) return hipSuccess;
+    int64_t tiles_x = 0;
+    const int64_t tpp = tiles_of(sh.Ho, sh.Wo, &tiles_x);
+    const int tok = prof_begin(s, "dw_conv");
+    const bool fast = fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
+        using CF = decltype(cf);
+        bsel(bias != nullptr, [&](auto B) {
+            k_dw_conv<CF::k, CF::s, CF::d, false, false, B()>
+                <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
+                    x, w, bias, y, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tpp);
+        });
+    });
+    if (!fast)
+        k_dw_conv_generic<false, false>
+            <<<grid_stride_blocks(sh.N * sh.C * sh.Ho * sh.Wo), 256, 0, s>>>(
+                x, w, bias, y, sh.N * sh.C, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.K, sh.pad, sh.S,
+                sh.D);
+    prof_end(s, tok);
+    return hipGetLastError();
+}
+
+hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x,
+                              const float* w, float* dx, float* dw, float* db,
+                              bool accumulate_dx, void* ws, hipStream_t s) {
+    if (sh.N * sh.C == 0) return hipSuccess;
+    if (dx && sh.Hi * sh.Wi > 0) {
+        const int tok = prof_begin(s, "dw_conv_dgrad");
+        bool done = false;
+        if (sh.S == 1) {
+            // the adjoint of a stride-1 convolution: the flipped kernel over
+            // dy with pad' = (K-1)*D - pad, producing dx's plane
+            int64_t tiles_x = 0;
+            const int64_t tpp = tiles_of(sh.Hi, sh.Wi, &tiles_x);
+            const int64_t padf = (sh.K - 1) * sh.D - sh.pad;
+            done = fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
+                using CF = decltype(cf);
+                bsel(accumulate_dx, [&](auto A) {
+                    k_dw_conv<CF::k, CF::s, CF::d, true, A(), false>
+                        <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
+                            dy, w, nullptr, dx, sh.C, sh.Ho, sh.Wo, sh.Hi, sh.Wi, padf, tiles_x,
+                            tpp);
+                });
+            });
+        }
+        if (!done) {
+            bsel(accumulate_dx, [&](auto A) {
+                k_dw_dx_gather<A()><<<grid_stride_blocks(sh.N * sh.C * sh.Hi * sh.Wi), 256, 0,
+                                      s>>>(dy, w, dx, sh.N * sh.C, sh.C, sh.Hi, sh.Wi, sh.Ho,
+                                           sh.Wo, sh.K, sh.pad, sh.S, sh.D);
+            });
+        }
+        prof_end(s, tok);
+    }
+    if ((dw || db) && sh.Ho * sh.Wo > 0) {
+        const int64_t KK1 = sh.K * sh.K + 1;
+        int64_t tiles_x = 0;
+        const int64_t tpp = tiles_of(sh.Ho, sh.Wo, &tiles_x);
+        float* part = static_cast<float*>(ws);
+        int tok = prof_begin(s, "dw_conv_wgrad");
+        const bool fast = fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
+            using CF = decltype(cf);
+            k_dw_wgrad<CF::k, CF::s, CF::d>
+                <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
+                    dy, x, part, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tpp);
+        });
+        prof_end(s, tok);
+        tok = prof_begin(s, "dw_conv_wgrad_finish");
+        if (fast) {
+            const int64_t E = sh.C * KK1;
+            k_dw_wgrad_finish<<<dim3((unsigned)((E + 63) / 64)), 1024, 0, s>>>(
+                part, dw, db, E, sh.N * tpp, KK1);
+        } else {
+            k_dw_wgrad_generic<<<dim3((unsigned)(sh.C * KK1)), 256, 0, s>>>(
+                dy, x, dw, db, sh.N, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.K, sh.pad, sh.S, sh.D);
+        }
+        prof_end(s, tok);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace gn
+}  // namespace soar

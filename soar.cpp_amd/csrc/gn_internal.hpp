@@ -154,6 +154,26 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
                               int64_t C_out, int64_t HW, int64_t chunk_dx, bool accumulate_dx,
                               hipStream_t s);
 
+// Depthwise convolution (dw_conv.hip): groups = C_in = C_out, weights
+// [C][K][K], output size given by the caller, taps outside the input skipped.
+struct DwShape {
+    int64_t N = 0, C = 0, Hi = 0, Wi = 0, Ho = 0, Wo = 0;
+    int64_t K = 0, pad = 0, S = 1, D = 1;
+};
+// True if (K, S, D) has a tiled kernel (else the generic kernels run).
+bool dw_has_fast(int64_t K, int64_t S, int64_t D);
+// Workspace of the backward (per-tile weight-gradient partials).
+size_t dw_bwd_workspace_bytes(const DwShape& sh);
+// Blocks of the tiled kernels over the output (or, for dx, input) planes.
+int64_t dw_grid_blocks(const DwShape& sh, bool output_tiles);
+hipError_t launch_dw_forward(const DwShape& sh, const float* x, const float* w,
+                             const float* bias, float* y, hipStream_t s);
+// dx (+)= input gradient, dw += weight gradient, db += bias gradient; any
+// output may be null.
+hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x,
+                              const float* w, float* dx, float* dw, float* db,
+                              bool accumulate_dx, void* ws, hipStream_t s);
+
 // Elementwise kernels (elementwise.hip).
 hipError_t launch_silu_forward(const float* x, float* y, int64_t n,
                                hipStream_t s);

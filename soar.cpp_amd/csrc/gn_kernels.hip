@@ -221,23 +221,26 @@ __device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
     // Eight independent loads in flight per thread, then their combine in
     // index order (a load-combine-load loop would wait a full memory
     // latency per partial).
+    // (full batches carry no bounds test between the loads: a test per load
+    // makes the compiler wait for each one)
     constexpr int kUnroll = 8;
-    for (int64_t j0 = threadIdx.x; j0 < P; j0 += kUnroll * kThreads) {
+    int64_t j0 = threadIdx.x;
+    for (; j0 + (kUnroll - 1) * kThreads < P; j0 += kUnroll * kThreads) {
         double2 v[kUnroll];
 #pragma unroll
-        for (int i = 0; i < kUnroll; ++i) {
-            const int64_t j = j0 + (int64_t)i * kThreads;
-            v[i] = j < P ? part[first + j] : make_double2(0.0, 0.0);
-        }
+        for (int i = 0; i < kUnroll; ++i) v[i] = part[first + j0 + (int64_t)i * kThreads];
 #pragma unroll
         for (int i = 0; i < kUnroll; ++i) {
-            const int64_t j = j0 + (int64_t)i * kThreads;
-            if (j < P) {
-                const int64_t k = j % cpp;
-                Moments o{(double)min(chunk, HW - k * chunk), v[i].x, v[i].y};
-                um = chan(um, o);
-            }
+            const int64_t k = (j0 + (int64_t)i * kThreads) % cpp;
+            Moments o{(double)min(chunk, HW - k * chunk), v[i].x, v[i].y};
+            um = chan(um, o);
         }
+    }
+    for (; j0 < P; j0 += kThreads) {
+        const double2 v = part[first + j0];
+        const int64_t k = j0 % cpp;
+        Moments o{(double)min(chunk, HW - k * chunk), v.x, v.y};
+        um = chan(um, o);
     }
     Moments ur = block_reduce(um, lds);
     if (threadIdx.x == 0) {

@@ -330,18 +330,27 @@ __global__ __launch_bounds__(64, 2) void k_pw_conv(
 // db[co] = sum_(n,p) dz[n][co][p].  A GEMM whose K axis is the pixels:
 // C[m = co][n = ci] = sum_k A[m][k] B[k][n], A = dz rows, B = x rows.
 //
-// One wave per (64x64 tile of dW, pixel chunk of one sample).  At k-steps
-// (i, q) of a 32-pixel step, lane l = 32h + j supplies pixel p + 16h + 4i + q
-// of row j of each operand tile, so each lane reads one 64-byte run of its
-// row per tile per step.  The wave writes its fp32 partial tile (and, for
-// the ci tile 0, the partial dz row sums) to the workspace; a finish kernel
-// adds the partials in a fixed order in float64.
+// One wave per (64x64 tile of dW, pixel chunk of one sample).  Both MFMA
+// operands put channels across lanes, so a step of 32 pixels is staged
+// through LDS: the wave reads the 64 dz rows and 64 x rows of the step with
+// row-contiguous 16-byte loads (8 rows per instruction), writes them to LDS
+// (row stride 144 bytes: conflict-free for the reads below), and each lane
+// then reads its operand runs back (lane l = 32h + j: row j, pixels
+// 16h + 4i .. +3 for k-steps (i, q)).  The next step's global loads are in
+// flight during the current step's MFMAs.  The wave writes its fp32 partial
+// tile (and, for the ci tile 0, the partial dz row sums) to the workspace; a
+// finish kernel adds the partials in a fixed order in float64.
 // ======================================================================
+constexpr int kWgStep = 32;                 // pixels per step
+constexpr int kWgStride = kWgStep + 4;      // floats per LDS row (144 bytes)
+
 template <bool FAST>
 __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
     const float* __restrict__ dz, const float* __restrict__ x, float* __restrict__ part_w,
     float* __restrict__ part_b, int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk,
     int64_t cpp, int64_t tiles_ci) {
+    // rows 0..63: dz rows co0.., rows 64..127: x rows ci0..
+    __shared__ __attribute__((aligned(16))) float lds[2 * kRowTile * kWgStride];
     const int lane = threadIdx.x;
     const int h = lane >> 5, j = lane & 31;
     const int64_t tco = (int64_t)blockIdx.x / tiles_ci;
@@ -350,16 +359,39 @@ __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
     const int64_t n = g / cpp, kc = g - n * cpp;
     const int64_t px0 = kc * chunk, pend = min(px0 + chunk, HW);
     const int64_t co0 = tco * kRowTile, ci0 = tci * kRowTile;
-    // operand rows (rows past the matrix are clamped to its last row: their
-    // products land only in outputs that are not written)
-    const float* ra[2];
-    const float* rb[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        ra[t] = dz + (n * C_out + min<int64_t>(co0 + 32 * t + j, C_out - 1)) * HW + 16 * h;
-        rb[t] = x + (n * C_in + min<int64_t>(ci0 + 32 * t + j, C_in - 1)) * HW + 16 * h;
-    }
     const bool want_b = tci == 0;
+
+    // staging: load slot s (0..15) of lane l covers row 8s + l/8, pixels
+    // 4*(l%8) .. +3 of the step (rows past the matrix are clamped to its last
+    // row; their products reach only outputs that are not written)
+    const int srow = lane >> 3, scol = 4 * (lane & 7);
+    const float* src[16];
+#pragma unroll
+    for (int sl = 0; sl < 16; ++sl) {
+        const int r = 8 * sl + srow;  // 0..127
+        if (r < kRowTile)
+            src[sl] = dz + (n * C_out + min<int64_t>(co0 + r, C_out - 1)) * HW + scol;
+        else
+            src[sl] = x + (n * C_in + min<int64_t>(ci0 + r - kRowTile, C_in - 1)) * HW + scol;
+    }
+    auto gload = [&](int64_t p, f4 (&st)[16]) {
+        const bool full = FAST && p + kWgStep <= pend;
+#pragma unroll
+        for (int sl = 0; sl < 16; ++sl) {
+            if (full) {
+                st[sl] = *reinterpret_cast<const f4*>(src[sl] + p);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    st[sl][q] = p + scol + q < pend ? src[sl][p + q] : 0.0f;
+            }
+        }
+    };
+    auto lwrite = [&](const f4 (&st)[16]) {
+#pragma unroll
+        for (int sl = 0; sl < 16; ++sl)
+            *reinterpret_cast<f4*>(&lds[(8 * sl + srow) * kWgStride + scol]) = st[sl];
+    };
 
     f16 acc[2][2];
 #pragma unroll
@@ -370,69 +402,46 @@ __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
             for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.0f;
     float sb[2] = {0.0f, 0.0f};
 
-    auto load_step = [&](int64_t p, f4 (&A)[2][4], f4 (&B)[2][4]) {
-        if (FAST && p + 32 <= pend) {
+    auto compute = [&]() {
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+        for (int i = 0; i < 4; ++i) {
+            f4 A[2], B[2];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    A[t][i] = *reinterpret_cast<const f4*>(ra[t] + p + 4 * i);
-                    B[t][i] = *reinterpret_cast<const f4*>(rb[t] + p + 4 * i);
-                }
-        } else {
-            // ragged step (or a plane that is not 16-byte aligned)
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int64_t px = p + 16 * h + 4 * i + q;
-                        const bool ok = px < pend;
-                        A[t][i][q] = ok ? ra[t][p + 4 * i + q] : 0.0f;
-                        B[t][i][q] = ok ? rb[t][p + 4 * i + q] : 0.0f;
-                    }
-        }
-    };
-    auto mfma_step = [&](const f4 (&A)[2][4], const f4 (&B)[2][4]) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int t = 0; t < 2; ++t) {
+                A[t] = *reinterpret_cast<const f4*>(
+                    &lds[(32 * t + j) * kWgStride + 16 * h + 4 * i]);
+                B[t] = *reinterpret_cast<const f4*>(
+                    &lds[(kRowTile + 32 * t + j) * kWgStride + 16 * h + 4 * i]);
+            }
 #pragma unroll
             for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                     for (int nt = 0; nt < 2; ++nt)
-                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                            A[mt][i][q], B[nt][i][q], acc[mt][nt], 0, 0, 0);
-        if (want_b) {
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(A[mt][q], B[nt][q],
+                                                                           acc[mt][nt], 0, 0, 0);
+            if (want_b) {
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    sb[mt] += (A[mt][i][0] + A[mt][i][1]) + (A[mt][i][2] + A[mt][i][3]);
+                for (int mt = 0; mt < 2; ++mt) sb[mt] += (A[mt][0] + A[mt][1]) + (A[mt][2] + A[mt][3]);
+            }
         }
     };
-    auto sched = [] {
+
+    f4 st[16];
+    gload(px0, st);
+    for (int64_t p = px0; p < pend; p += kWgStep) {
+        lwrite(st);
+        // next step's loads (the last step reloads itself: no branch, so the
+        // wait before the LDS write above only covers these)
+        const int64_t pn = p + kWgStep < pend ? p + kWgStep : p;
+        gload(pn, st);
         if (FAST) {
-            __builtin_amdgcn_sched_group_barrier(0x020, 16, 0);  // 16 vector loads
-            __builtin_amdgcn_sched_group_barrier(0x008, 64, 0);  // then 64 MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x200, 16, 0);  // 16 LDS writes
+            __builtin_amdgcn_sched_group_barrier(0x020, 16, 0);  // 16 global loads
         }
-    };
-    // ping-pong operand buffers, loads one step ahead (see k_pw_conv)
-    const int64_t plast = px0 + ((pend - px0 - 1) / 32) * 32;  // last step
-    f4 A0[2][4], B0[2][4], A1[2][4], B1[2][4];
-    load_step(px0, A0, B0);
-    int64_t p = px0;
-    for (; p + 32 < pend; p += 64) {
-        load_step(p + 32, A1, B1);
-        mfma_step(A0, B0);
-        sched();
-        load_step(min(p + 64, plast), A0, B0);
-        mfma_step(A1, B1);
-        sched();
+        compute();
     }
-    if (p < pend) mfma_step(A0, B0);
 
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -454,32 +463,39 @@ __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
     }
 }
 
-// out[e] += sum_g part[g][e] for e < E, g ascending in float64.  A block is
-// 16 elements x 16 g-segments; the segments are added in order.
-__global__ __launch_bounds__(256) void k_sum_partials(const float* __restrict__ part,
-                                                      float* __restrict__ out, int64_t E,
-                                                      int64_t G) {
-    __shared__ double lds[16][16];
-    const int el = threadIdx.x & 15, seg = threadIdx.x >> 4;
-    const int64_t e = (int64_t)blockIdx.x * 16 + el;
-    const int64_t g0 = seg * G / 16, g1 = (seg + 1) * G / 16;
+// out[e] += sum_g part[g][e] for e < E, in float64 and a fixed order.  A
+// block of 16 waves owns 64 consecutive columns: wave w adds rows
+// [w*G/16, (w+1)*G/16) with each lane on one column (a 256-byte row segment
+// per load, eight loads in flight), then the 16 wave sums are added in
+// order.
+__global__ __launch_bounds__(1024) void k_sum_partials(const float* __restrict__ part,
+                                                       float* __restrict__ out, int64_t E,
+                                                       int64_t G) {
+    __shared__ double lds[16][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+    const int64_t g0 = wv * G / 16, g1 = (wv + 1) * G / 16;
     double sum = 0.0;
     if (e < E) {
-        constexpr int kU = 8;  // loads in flight per thread
-        for (int64_t gg = g0; gg < g1; gg += kU) {
+        // full batches of loads with no bounds test between them (a test per
+        // load makes the compiler wait for each one), then the tail
+        constexpr int kU = 8;
+        int64_t gg = g0;
+        for (; gg + kU <= g1; gg += kU) {
             float v[kU];
 #pragma unroll
-            for (int u = 0; u < kU; ++u) v[u] = gg + u < g1 ? part[(gg + u) * E + e] : 0.0f;
+            for (int u = 0; u < kU; ++u) v[u] = part[(gg + u) * E + e];
 #pragma unroll
             for (int u = 0; u < kU; ++u) sum += (double)v[u];
         }
+        for (; gg < g1; ++gg) sum += (double)part[gg * E + e];
     }
-    lds[seg][el] = sum;
+    lds[wv][lane] = sum;
     __syncthreads();
-    if (seg == 0 && e < E) {
+    if (wv == 0 && e < E) {
         double t = 0.0;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) t += lds[i][el];
+        for (int i = 0; i < 16; ++i) t += lds[i][lane];
         out[e] = (float)((double)out[e] + t);
     }
 }
@@ -597,11 +613,11 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
         tok = prof_begin(s, "pw_conv_wgrad_finish");
         if (a.dw) {
             const int64_t E = C_out * C_in;
-            k_sum_partials<<<dim3((unsigned)((E + 15) / 16)), 256, 0, s>>>(part_w, a.dw, E, p.G);
+            k_sum_partials<<<dim3((unsigned)((E + 63) / 64)), 1024, 0, s>>>(part_w, a.dw, E, p.G);
         }
         if (a.db)
-            k_sum_partials<<<dim3((unsigned)((C_out + 15) / 16)), 256, 0, s>>>(part_b, a.db,
-                                                                               C_out, p.G);
+            k_sum_partials<<<dim3((unsigned)((C_out + 63) / 64)), 1024, 0, s>>>(part_b, a.db,
+                                                                                C_out, p.G);
         prof_end(s, tok);
     }
     return hipGetLastError();

@@ -88,6 +88,11 @@ SIGNATURES = {
     "soar_pw_conv_backward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                          _c.c_uint, _P, _SZ, _P]),
     "soar_conv2d_1x1_backward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _P]),
+    "soar_dw_conv_forward": (_c.c_int, [_P, _P, _P, _P] + [_I64] * 10 + [_P]),
+    "soar_dw_conv_backward_workspace_bytes": (_SZ, [_I64] * 9),
+    "soar_dw_conv_backward": (_c.c_int, [_P] * 6 + [_I64] * 10 + [_c.c_uint, _P, _SZ, _P]),
+    "soar_conv2d_dw_forward": (_c.c_int, [_P, _P, _P, _P] + [_SZ] * 9 + [_P]),
+    "soar_conv2d_dw_backward": (_c.c_int, [_P] * 6 + [_SZ] * 9 + [_P]),
     "soar_arena_create": (_c.c_int, [_SZ, _SZ, _c.POINTER(_P)]),
     "soar_arena_alloc": (_c.c_int, [_P, _SZ, _c.POINTER(_P), _c.POINTER(_SZ)]),
     "soar_arena_freeze_static": (_c.c_int, [_P]),
@@ -377,6 +382,59 @@ def pw_conv_backward(dz, x, weight, dx=None, dweight=None, dbias=None, want_dx=T
         _ptr(dz), _ptr(x), _ptr(w), _ptr(dx) if want_dx else None,
         _ptr(dweight) if want_dw else None, _ptr(dbias) if want_db else None, N, C_in, C_out,
         HW, GN_ACCUMULATE_DX if accumulate_dx else 0, _ptr(ws), ws.numel(), _stream(stream)))
+    return (dx if want_dx else None, dweight if want_dw else None, dbias if want_db else None)
+
+
+# ---- depthwise convolution -------------------------------------------------------
+
+def conv_out_size(H, K, pad, stride, dil):
+    """Conv2d's output size (src/nn/layers.cpp:330-332)."""
+    return (H + 2 * pad - (dil * (K - 1) + 1)) // stride + 1
+
+
+def dw_conv_forward(x, weight, bias, pad, stride=1, dil=1, y=None, stream=None):
+    """Depthwise conv through soar_dw_conv_forward.  x [N,C,H,W], weight
+    [C,K,K] (or [C,1,K,K]), bias [C] or None; returns y [N,C,Ho,Wo]."""
+    import torch
+    N, C, H, W = x.shape
+    K = weight.shape[-1]
+    Ho, Wo = conv_out_size(H, K, pad, stride, dil), conv_out_size(W, K, pad, stride, dil)
+    for t, n in ((x, "x"), (weight, "weight"), (bias, "bias"), (y, "y")):
+        _check_tensor(t, n)
+    if y is None:
+        y = torch.empty((N, C, Ho, Wo), dtype=torch.float32, device=x.device)
+    check(lib().soar_dw_conv_forward(_ptr(x), _ptr(weight), _ptr(bias), _ptr(y), N, C, H, W,
+                                     Ho, Wo, K, pad, stride, dil, _stream(stream)))
+    return y
+
+
+def dw_conv_backward(dy, x, weight, pad, stride=1, dil=1, dx=None, dweight=None, dbias=None,
+                     want_dx=True, want_dw=True, want_db=True, accumulate_dx=False, ws=None,
+                     stream=None):
+    """Backward through soar_dw_conv_backward; returns (dx, dweight, dbias).
+    dweight/dbias accumulate (fresh zeros when not given)."""
+    import torch
+    N, C, H, W = x.shape
+    K = weight.shape[-1]
+    Ho, Wo = dy.shape[2], dy.shape[3]
+    for t, n in ((dy, "dy"), (x, "x"), (weight, "weight"), (dx, "dx"), (dweight, "dweight"),
+                 (dbias, "dbias")):
+        _check_tensor(t, n)
+    if want_dx and dx is None:
+        dx = (torch.zeros if accumulate_dx else torch.empty)((N, C, H, W), dtype=torch.float32,
+                                                             device=x.device)
+    if want_dw and dweight is None:
+        dweight = torch.zeros((C, K, K), dtype=torch.float32, device=x.device)
+    if want_db and dbias is None:
+        dbias = torch.zeros(C, dtype=torch.float32, device=x.device)
+    if ws is None:
+        n = int(lib().soar_dw_conv_backward_workspace_bytes(N, C, H, W, Ho, Wo, K, stride, dil))
+        ws = torch.empty(max(n, 1), dtype=torch.uint8, device=x.device)
+    check(lib().soar_dw_conv_backward(
+        _ptr(dy), _ptr(x), _ptr(weight), _ptr(dx) if want_dx else None,
+        _ptr(dweight) if want_dw else None, _ptr(dbias) if want_db else None, N, C, H, W, Ho,
+        Wo, K, pad, stride, dil, GN_ACCUMULATE_DX if accumulate_dx else 0, _ptr(ws), ws.numel(),
+        _stream(stream)))
     return (dx if want_dx else None, dweight if want_dw else None, dbias if want_db else None)
 
 
