@@ -49,6 +49,9 @@ constexpr int kRowTile = 64;    // output rows per pass (two 32-row tiles)
 constexpr int kItem = 128;      // pixels per item (four 32-column tiles)
 constexpr int kRowGroup = 4;    // row tiles whose statistics a lane keeps
 constexpr int kLdsStride = 34;  // float2 per LDS row: 32 lanes + 2 pad
+// Word 3 of a raw buffer descriptor on gfx9-family parts (gfx950 included):
+// 32-bit float data format, no swizzle, no stride.
+constexpr int kRsrcWord3 = 0x00020000;
 
 struct Mom {
     double n, mean, m2;
@@ -70,10 +73,6 @@ __device__ __forceinline__ Mom chan_merge(const Mom& a, const Mom& b) {
 // lane of half-wave h.
 __device__ __forceinline__ int tile_row(int mt, int r, int h) {
     return mt * 32 + (r & 3) + 8 * (r >> 2) + 4 * h;
-}
-
-__device__ __forceinline__ f4 ld4(const float* base, uint32_t byte_off) {
-    return *reinterpret_cast<const f4*>(reinterpret_cast<const char*>(base) + byte_off);
 }
 
 // One 64-row x 128-pixel item: z rows [row0, row0 + 64) of pixels
@@ -134,14 +133,27 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
 
     auto load_step = [&](int kk, f4 (&a)[2], f4 (&b)[4]) {
         if (FAST) {
-            // Clamped lanes and rows load valid but unrelated data.  An MFMA
-            // output column depends only on its own b column and an output
-            // row only on its own a row, so those values only reach outputs
-            // that are neither stored nor counted in the statistics.
-            a[0] = ld4(ws + kk, wo0);
-            a[1] = ld4(ws + kk, wo1);
+            // Raw buffer loads: the descriptor holds the step's wave-uniform
+            // base, each lane adds its 32-bit offset and the channel offset
+            // q*HW*4 is a scalar.  A step past the end (kk >= Kpad) gets an
+            // empty descriptor, so its loads return zeros without touching
+            // memory.  Clamped lanes and rows load valid but unrelated data:
+            // an MFMA output column depends only on its own b column and an
+            // output row only on its own a row, so those values only reach
+            // outputs that are neither stored nor counted in the statistics.
+            const bool live = kk < Kpad;
+            const int kc = live ? kk : 0;
+            const auto rw = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(ws + kc), (short)0, live ? 0x7fffffff : 0, kRsrcWord3);
+            const auto rx = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(xs + (int64_t)kc * HW), (short)0, live ? 0x7fffffff : 0,
+                kRsrcWord3);
+            a[0] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo0, 0, 0));
+            a[1] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo1, 0, 0));
 #pragma unroll
-            for (int q = 0; q < 4; ++q) b[q] = ld4(xs + (int64_t)(kk + q) * HW, xo);
+            for (int q = 0; q < 4; ++q)
+                b[q] = __builtin_bit_cast(
+                    f4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo, q * hw4, 0));
         } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -170,11 +182,12 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
     };
     // Ping-pong operand buffers: the loads of the next step are issued
     // before the MFMAs of the current one, so their latency hides behind 32
-    // MFMAs.  Loads are never under a branch (past the end they reload the
-    // last step) and buffers are never copied, so the wait before each MFMA
-    // group covers only the older buffer.  sched_group_barrier keeps the
-    // order (the scheduler would otherwise sink each load next to its use).
-    const int klast = Kpad - 8;
+    // MFMAs.  Loads are never under a branch (past the end they load zeros,
+    // or on the general path reload the last step) and buffers are never
+    // copied, so the wait before each MFMA group covers only the older
+    // buffer.  sched_group_barrier keeps the order (the scheduler would
+    // otherwise sink each load next to its use).
+    const int klast = FAST ? Kpad : Kpad - 8;
     auto sched = [] {
         if (FAST) {
             __builtin_amdgcn_sched_group_barrier(0x020, 6, 0);  // 6 vector loads
@@ -522,7 +535,9 @@ void bsel(bool b, F&& f) {
 int pw_kpad(int64_t C_in) { return (int)((C_in + 7) / 8 * 8); }
 
 bool pw_offsets_fit(int64_t C_in, int64_t HW) {
-    return HW <= ((int64_t)1 << 32) / 20 - 4 && C_in <= ((int64_t)1 << 32) / 256;
+    // lane byte offsets (at most 20*HW for x and z, 256*C for w) stay below
+    // 2^31: the buffer descriptors' range is 0x7fffffff bytes
+    return HW <= ((int64_t)1 << 31) / 20 - 4 && C_in <= ((int64_t)1 << 31) / 256;
 }
 
 hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
