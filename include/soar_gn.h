@@ -182,6 +182,15 @@ SOAR_API int soar_conv2d_1x1_forward(const float* in, const float* weight,
                                      size_t C_in, size_t C_out, size_t HW,
                                      void* stream);
 
+/* z[n] = weight x[n] + bias for N samples at once (the batched form of
+ * soar_conv2d_1x1_forward; no workspace).
+ * Replaces: conv2d_1x1_forward (cuda_kernels.hpp:57-58) in a loop over the
+ * samples of a batch. */
+SOAR_API int soar_pw_conv_forward(const float* x, const float* weight,
+                                  const float* bias, float* z, int64_t N,
+                                  int64_t C_in, int64_t C_out, int64_t HW,
+                                  void* stream);
+
 /* Bytes of workspace soar_pw_conv_gn_silu_forward needs for this shape
  * (0 for an invalid or empty shape). */
 SOAR_API size_t soar_pw_conv_gn_workspace_bytes(int64_t N, int64_t C_out,

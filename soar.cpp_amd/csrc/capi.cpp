@@ -441,6 +441,29 @@ SOAR_API int soar_conv2d_1x1_forward(const float* in, const float* weight, const
     return e == hipSuccess ? ok() : hip_fail(e, "conv2d_1x1_forward launch");
 }
 
+SOAR_API int soar_pw_conv_forward(const float* x, const float* weight, const float* bias,
+                                  float* z, int64_t N, int64_t C_in, int64_t C_out, int64_t HW,
+                                  void* stream) {
+    int64_t ie = 0, oe = 0;
+    int rc = check_pw_shape(N, C_in, C_out, HW, &ie, &oe);
+    if (rc) return rc;
+    if (oe == 0) return ok();
+    if (C_in == 0) return fail(SOAR_EINVAL, "C_in must be positive");
+    if ((rc = require_device())) return rc;
+    if ((rc = check_dev(x, (size_t)ie * 4, "x")) ||
+        (rc = check_dev(weight, (size_t)(C_in * C_out) * 4, "weight")) ||
+        (rc = check_dev_opt(bias, (size_t)C_out * 4, "bias")) ||
+        (rc = check_dev(z, (size_t)oe * 4, "z")))
+        return rc;
+    const Tuning t = current_tuning();
+    if (!pw_grid_fits(N, HW, t.pw_chunk))
+        return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    soar::gn::PwArgs a{x, weight, bias, z};
+    hipError_t e = soar::gn::launch_pw_conv(a, N, C_in, C_out, HW, t.pw_chunk, nullptr, false,
+                                            static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "pointwise convolution launch");
+}
+
 SOAR_API size_t soar_pw_conv_gn_workspace_bytes(int64_t N, int64_t C_out, int64_t HW, int64_t G) {
     int64_t elems = 0;
     if (check_shape(N, C_out, HW, G, &elems) != SOAR_OK || elems == 0) return 0;

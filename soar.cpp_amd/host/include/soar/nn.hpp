@@ -1,5 +1,6 @@
-// nn.hpp - the GroupNorm / SiLU layers and the residual add of the SOAR
-// blocks, running on the MI355X kernels of libsoar_gn.so.
+// nn.hpp - the GroupNorm / SiLU layers, the pointwise and depthwise
+// convolutions, the CBA block and the residual add of the SOAR blocks,
+// running on the MI355X kernels of libsoar_gn.so.
 //
 // Mirrors include/soar/nn/layers.hpp:9-14,61-91 and src/nn/blocks.cpp:
 // 17-72,429-445 of the reference: GroupNorm(num_groups, num_channels,
@@ -16,6 +17,7 @@
 // do when a parameter lives on the device).
 #pragma once
 
+#include <cstdint>
 #include <map>
 #include <memory>
 #include <string>
@@ -33,6 +35,12 @@ inline int select_group_count(int channels, int max_groups = 8) {
     return 1;
 }
 
+// Autopadding of Conv2d (layers.hpp:16-19): half the dilated kernel.
+inline int autopad(int k, int p = -1, int d = 1) {
+    if (d > 1) k = d * (k - 1) + 1;
+    return p < 0 ? k / 2 : p;
+}
+
 class Module {
 public:
     explicit Module(std::string name) : name_(std::move(name)) {}
@@ -40,8 +48,12 @@ public:
     virtual TensorPtr forward(const TensorPtr& input) = 0;
 
     void register_parameter(const std::string& name, TensorPtr p);
+    // Parameters of a submodule are named "<name>.<parameter>"
+    // (the reference's register_submodule naming).
+    void register_submodule(const std::string& name, std::shared_ptr<Module> m);
     [[nodiscard]] std::vector<std::pair<std::string, TensorPtr>> named_parameters(
         const std::string& prefix = "") const;
+    [[nodiscard]] std::vector<TensorPtr> parameters() const;
     // Moves every parameter to the device (allocated from the current
     // arena: do this before freeze_static_parameters()).
     void to_device();
@@ -51,6 +63,7 @@ public:
 private:
     std::string name_;
     std::vector<std::pair<std::string, TensorPtr>> params_;
+    std::vector<std::pair<std::string, std::shared_ptr<Module>>> subs_;
 };
 
 class GroupNorm : public Module {
@@ -64,9 +77,12 @@ public:
     [[nodiscard]] TensorPtr weight() const { return weight_; }
     [[nodiscard]] TensorPtr bias() const { return bias_; }
 
+    // The layer with the soar_gn_silu_forward flags (SOAR_GN_SILU,
+    // SOAR_GN_RESIDUAL): GroupNorm -> SiLU in one pass for CBA.
+    TensorPtr run(const TensorPtr& input, unsigned flags);
+
 protected:
     GroupNorm(std::string name, size_t num_groups, size_t num_channels, float eps, bool affine);
-    TensorPtr run(const TensorPtr& input, unsigned flags);
 
     size_t num_groups_;
     size_t num_channels_;
@@ -92,6 +108,66 @@ public:
 
 private:
     bool residual_;
+};
+
+// Conv2d(in, out, kernel_size, stride = 1, padding = -1 (autopad),
+// dilation = 1, groups = 1, bias = true) of layers.hpp:24-58: weight
+// [out][in/groups][k][k] with Kaiming-uniform initialisation
+// U(-1/sqrt(fan_in), 1/sqrt(fan_in)) (layers.cpp:303-317; drawn from a
+// seeded generator, where the reference seeds from std::random_device),
+// bias zeros.  Runs on the device for the two forms of the SOAR blocks:
+// pointwise (k = 1, stride 1, no padding, groups 1) and depthwise (groups =
+// in = out); other forms throw InvalidArgument.  Input [C,H,W] or
+// [N,C,H,W]; the output size is (H + 2p - d(k-1) - 1)/s + 1
+// (layers.cpp:330-332).
+class Conv2d : public Module {
+public:
+    Conv2d(size_t in_channels, size_t out_channels, size_t kernel_size, size_t stride = 1,
+           int padding = -1, size_t dilation = 1, size_t groups = 1, bool bias = true,
+           uint64_t seed = 0x50a4c0de);
+    TensorPtr forward(const TensorPtr& input) override;
+
+    [[nodiscard]] bool pointwise() const noexcept {
+        return groups_ == 1 && kernel_ == 1 && stride_ == 1 && padding_ == 0;
+    }
+    [[nodiscard]] bool depthwise() const noexcept {
+        return groups_ == in_ && in_ == out_;
+    }
+    [[nodiscard]] TensorPtr weight() const { return weight_; }
+    [[nodiscard]] TensorPtr bias() const { return bias_; }
+    [[nodiscard]] size_t in_channels() const noexcept { return in_; }
+    [[nodiscard]] size_t out_channels() const noexcept { return out_; }
+    [[nodiscard]] size_t kernel_size() const noexcept { return kernel_; }
+    [[nodiscard]] size_t stride() const noexcept { return stride_; }
+    [[nodiscard]] size_t padding() const noexcept { return padding_; }
+    [[nodiscard]] size_t dilation() const noexcept { return dilation_; }
+
+private:
+    size_t in_, out_, kernel_, stride_, padding_, dilation_, groups_;
+    TensorPtr weight_;
+    TensorPtr bias_;
+};
+
+// CBA(c1, c2, k = 1, s = 1, p = -1, d = 1, g = 1, act = true) of
+// blocks.cpp:429-445: Conv2d (no bias) -> GroupNorm(select_group_count(c2),
+// c2) -> SiLU when act.  Submodules "conv" and "norm" as in the reference.
+// With a pointwise conv the whole block is one forward call whose GroupNorm
+// statistics come from the conv's epilogue, and one backward node; with a
+// depthwise conv the conv runs, then GroupNorm(+SiLU) in one pass.
+class CBA : public Module {
+public:
+    CBA(size_t c1, size_t c2, size_t k = 1, size_t s = 1, int p = -1, size_t d = 1,
+        size_t g = 1, bool act = true);
+    TensorPtr forward(const TensorPtr& input) override;
+
+    [[nodiscard]] std::shared_ptr<Conv2d> conv() const { return conv_; }
+    [[nodiscard]] std::shared_ptr<GroupNorm> norm() const { return norm_; }
+    [[nodiscard]] bool act() const noexcept { return act_; }
+
+private:
+    std::shared_ptr<Conv2d> conv_;
+    std::shared_ptr<GroupNorm> norm_;
+    bool act_;
 };
 
 // y = a + b (blocks.cpp:39-72); shapes must match (ShapeError otherwise).

@@ -1,4 +1,4 @@
-// GroupNorm / SiLU / GNSiLU / add_tensors on libsoar_gn.so.
+// GroupNorm / SiLU / GNSiLU / Conv2d / CBA / add_tensors on libsoar_gn.so.
 //
 // Forward/backward structure follows src/nn/layers.cpp:483-802 and
 // src/nn/blocks.cpp:17-72 of the reference: the layer allocates its output
@@ -12,6 +12,9 @@
 //   * the statistics are saved as mean, rstd and the mean's fp32 rounding
 //     residual, so the backward's xhat is exact when std << |mean|.
 #include "soar/nn.hpp"
+
+#include <cmath>
+#include <random>
 
 #include "soar/autograd.hpp"
 #include "soar/kernels.hpp"
@@ -27,19 +30,34 @@ void Module::register_parameter(const std::string& name, TensorPtr p) {
     params_.emplace_back(name, std::move(p));
 }
 
+void Module::register_submodule(const std::string& name, std::shared_ptr<Module> m) {
+    subs_.emplace_back(name, std::move(m));
+}
+
 std::vector<std::pair<std::string, TensorPtr>> Module::named_parameters(
     const std::string& prefix) const {
     std::vector<std::pair<std::string, TensorPtr>> out;
     for (const auto& [n, p] : params_) out.emplace_back(prefix.empty() ? n : prefix + "." + n, p);
+    for (const auto& [n, m] : subs_)
+        for (auto& np : m->named_parameters(prefix.empty() ? n : prefix + "." + n))
+            out.push_back(std::move(np));
+    return out;
+}
+
+std::vector<TensorPtr> Module::parameters() const {
+    std::vector<TensorPtr> out;
+    for (auto& [n, p] : named_parameters()) out.push_back(p);
     return out;
 }
 
 void Module::to_device() {
     for (auto& [n, p] : params_) p->to_cuda();
+    for (auto& [n, m] : subs_) m->to_device();
 }
 
 void Module::zero_grad() {
     for (auto& [n, p] : params_) p->zero_grad();
+    for (auto& [n, m] : subs_) m->zero_grad();
 }
 
 namespace {
@@ -114,6 +132,166 @@ struct GroupNormNode : autograd::AutogradNode {
     void release_variables() override {
         input = nullptr;
         mean = rstd = mean_lo = nullptr;
+    }
+};
+
+// Gradient buffer of parameter `p` for a kernel that accumulates (+=):
+// its existing device .grad when p is a leaf that has one (no temporary,
+// no merge pass), else fresh zeros that the caller propagates.
+TensorPtr param_grad_target(const TensorPtr& p, bool* direct) {
+    if (!p->grad_fn() && p->grad() && p->grad()->is_cuda()) {
+        *direct = true;
+        return p->grad();
+    }
+    *direct = false;
+    return Tensor::zeros(p->shape(), false, true);
+}
+
+struct ConvGeom {
+    int64_t N, C_in, H, W, C_out, Ho, Wo;
+};
+
+ConvGeom conv_geom(const TensorPtr& x, const Conv2d& c) {
+    ConvGeom g{};
+    if (x->ndim() == 3) {
+        g.N = 1;
+        g.C_in = x->dim(0);
+        g.H = x->dim(1);
+        g.W = x->dim(2);
+    } else if (x->ndim() == 4) {
+        g.N = x->dim(0);
+        g.C_in = x->dim(1);
+        g.H = x->dim(2);
+        g.W = x->dim(3);
+    } else {
+        throw ShapeError("Conv2d expects [C,H,W] or [N,C,H,W], got " + to_string(x->shape()));
+    }
+    if (g.C_in != (int64_t)c.in_channels())
+        throw ShapeError("Conv2d: expected " + std::to_string(c.in_channels()) +
+                         " input channels, got " + to_string(x->shape()));
+    const int64_t ek = (int64_t)(c.dilation() * (c.kernel_size() - 1) + 1);
+    const int64_t p2 = 2 * (int64_t)c.padding();
+    if (g.H + p2 < ek || g.W + p2 < ek)
+        throw ShapeError("Conv2d: input " + to_string(x->shape()) + " is smaller than the kernel");
+    g.C_out = (int64_t)c.out_channels();
+    g.Ho = (g.H + p2 - ek) / (int64_t)c.stride() + 1;
+    g.Wo = (g.W + p2 - ek) / (int64_t)c.stride() + 1;
+    return g;
+}
+
+Shape conv_out_shape(const TensorPtr& x, const ConvGeom& g) {
+    if (x->ndim() == 3) return {g.C_out, g.Ho, g.Wo};
+    return {g.N, g.C_out, g.Ho, g.Wo};
+}
+
+// Backward of Conv2d (layers.cpp:17-292, the pointwise and depthwise
+// branches): dx written fresh, dW and db accumulated by the kernels.
+struct Conv2dNode : autograd::AutogradNode {
+    TensorPtr input, weight, bias;
+    ConvGeom g{};
+    int64_t K = 1, pad = 0, stride = 1, dil = 1;
+    bool pointwise = true;
+
+    std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
+        std::vector<std::shared_ptr<AutogradNode>> r;
+        for (const auto& t : {input, weight, bias})
+            if (t && t->grad_fn()) r.push_back(t->grad_fn());
+        return r;
+    }
+
+    void backward(const TensorPtr& go) override {
+        const bool want_x = input->requires_grad();
+        const bool want_w = weight->requires_grad();
+        const bool want_b = bias && bias->requires_grad();
+        if (!want_x && !want_w && !want_b) return;
+        if (!go->is_cuda()) go->to_cuda();
+        TensorPtr gx = want_x ? Tensor::create(input->shape(), false, true) : nullptr;
+        bool dw_direct = false, db_direct = false;
+        TensorPtr gw = want_w ? param_grad_target(weight, &dw_direct) : nullptr;
+        TensorPtr gb = want_b ? param_grad_target(bias, &db_direct) : nullptr;
+        float* px = gx ? gx->cuda_data() : nullptr;
+        float* pw = gw ? gw->cuda_data() : nullptr;
+        float* pb = gb ? gb->cuda_data() : nullptr;
+        if (pointwise) {
+            const size_t wsb =
+                soar_pw_conv_backward_workspace_bytes(g.N, g.C_in, g.C_out, g.H * g.W);
+            check(soar_pw_conv_backward(go->cuda_data(), input->cuda_data(), weight->cuda_data(),
+                                        px, pw, pb, g.N, g.C_in, g.C_out, g.H * g.W, 0u,
+                                        workspace(wsb), wsb, nullptr),
+                  "pointwise convolution backward");
+        } else {
+            const size_t wsb = soar_dw_conv_backward_workspace_bytes(g.N, g.C_in, g.H, g.W, g.Ho,
+                                                                     g.Wo, K, stride, dil);
+            check(soar_dw_conv_backward(go->cuda_data(), input->cuda_data(), weight->cuda_data(),
+                                        px, pw, pb, g.N, g.C_in, g.H, g.W, g.Ho, g.Wo, K, pad,
+                                        stride, dil, 0u, wsb ? workspace(wsb) : nullptr, wsb,
+                                        nullptr),
+                  "depthwise convolution backward");
+        }
+        if (gb && !db_direct) propagate_grad(bias, std::move(gb));
+        if (gw && !dw_direct) propagate_grad(weight, std::move(gw));
+        if (gx) propagate_grad(input, std::move(gx));
+    }
+
+    void release_variables() override { input = nullptr; }
+};
+
+// Backward of the fused pointwise CBA: GroupNorm(+SiLU) on the saved conv
+// output z gives dz (and dgamma, dbeta), then the conv backward gives dx
+// and dW.
+struct CBAPointwiseNode : autograd::AutogradNode {
+    TensorPtr input, conv_w, gamma, beta, z, mean, rstd, mean_lo;
+    ConvGeom g{};
+    int64_t G = 1;
+    unsigned flags = 0;
+
+    std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
+        std::vector<std::shared_ptr<AutogradNode>> r;
+        for (const auto& t : {input, conv_w, gamma, beta})
+            if (t && t->grad_fn()) r.push_back(t->grad_fn());
+        return r;
+    }
+
+    void backward(const TensorPtr& go) override {
+        const bool want_x = input->requires_grad();
+        const bool want_w = conv_w->requires_grad();
+        const bool want_p = gamma && gamma->requires_grad();
+        if (!want_x && !want_w && !want_p) return;
+        if (!go->is_cuda()) go->to_cuda();
+        const int64_t HW = g.H * g.W;
+        TensorPtr dz = (want_x || want_w) ? Tensor::create(z->shape(), false, true) : nullptr;
+        bool g_direct = false, b_direct = false;
+        TensorPtr dg = want_p ? param_grad_target(gamma, &g_direct) : nullptr;
+        TensorPtr db = want_p ? param_grad_target(beta, &b_direct) : nullptr;
+        const size_t gwsb = soar_gn_workspace_bytes(g.N, g.C_out, HW, G);
+        check(soar_gn_silu_backward(go->cuda_data(), z->cuda_data(), dptr(gamma), dptr(beta),
+                                    mean->cuda_data(), rstd->cuda_data(), dptr(mean_lo),
+                                    dz ? dz->cuda_data() : nullptr,
+                                    dg ? dg->cuda_data() : nullptr,
+                                    db ? db->cuda_data() : nullptr, g.N, g.C_out, HW, G, flags,
+                                    workspace(gwsb), gwsb, nullptr),
+              "CBA GroupNorm backward");
+        TensorPtr gx, gw;
+        bool w_direct = false;
+        if (dz) {
+            gx = want_x ? Tensor::create(input->shape(), false, true) : nullptr;
+            gw = want_w ? param_grad_target(conv_w, &w_direct) : nullptr;
+            const size_t wsb = soar_pw_conv_backward_workspace_bytes(g.N, g.C_in, g.C_out, HW);
+            check(soar_pw_conv_backward(dz->cuda_data(), input->cuda_data(), conv_w->cuda_data(),
+                                        gx ? gx->cuda_data() : nullptr,
+                                        gw ? gw->cuda_data() : nullptr, nullptr, g.N, g.C_in,
+                                        g.C_out, HW, 0u, workspace(wsb), wsb, nullptr),
+                  "CBA convolution backward");
+        }
+        if (dg && !g_direct) propagate_grad(gamma, std::move(dg));
+        if (db && !b_direct) propagate_grad(beta, std::move(db));
+        if (gw && !w_direct) propagate_grad(conv_w, std::move(gw));
+        if (gx) propagate_grad(input, std::move(gx));
+    }
+
+    void release_variables() override {
+        input = nullptr;
+        z = mean = rstd = mean_lo = nullptr;
     }
 };
 
@@ -229,6 +407,130 @@ TensorPtr SiLU::forward(const TensorPtr& input) {
         out->set_grad_fn(node);
     }
     return out;
+}
+
+Conv2d::Conv2d(size_t in_channels, size_t out_channels, size_t kernel_size, size_t stride,
+               int padding, size_t dilation, size_t groups, bool bias, uint64_t seed)
+    : Module("Conv2d"),
+      in_(in_channels),
+      out_(out_channels),
+      kernel_(kernel_size),
+      stride_(stride),
+      padding_((size_t)(padding < 0 ? autopad((int)kernel_size, -1, (int)dilation) : padding)),
+      dilation_(dilation),
+      groups_(groups) {
+    if (in_ == 0 || out_ == 0 || kernel_ == 0 || stride_ == 0 || dilation_ == 0 || groups_ == 0 ||
+        in_ % groups_ != 0 || out_ % groups_ != 0)
+        throw InvalidArgument("Conv2d: invalid channel / kernel / stride / group arguments");
+    const size_t cig = in_ / groups_;
+    weight_ = Tensor::create({(int64_t)out_, (int64_t)cig, (int64_t)kernel_, (int64_t)kernel_},
+                             true);
+    const float bound = std::sqrt(1.0f / (float)(cig * kernel_ * kernel_));
+    std::mt19937_64 gen(seed);
+    std::uniform_real_distribution<float> dist(-bound, bound);
+    float* w = weight_->data();
+    for (int64_t i = 0; i < weight_->numel(); ++i) w[i] = dist(gen);
+    register_parameter("weight", weight_);
+    if (bias) {
+        bias_ = Tensor::zeros({(int64_t)out_}, true);
+        register_parameter("bias", bias_);
+    }
+}
+
+TensorPtr Conv2d::forward(const TensorPtr& input) {
+    if (!pointwise() && !depthwise())
+        throw InvalidArgument(
+            "Conv2d: only pointwise (k=1, stride 1, no padding, groups 1) and depthwise "
+            "(groups = in = out) convolutions run on the device");
+    const ConvGeom g = conv_geom(input, *this);
+    if (!input->is_cuda()) input->to_cuda();
+    weight_->to_cuda();
+    if (bias_) bias_->to_cuda();
+    const bool record = (input->requires_grad() || weight_->requires_grad() ||
+                         (bias_ && bias_->requires_grad())) &&
+                        GradMode::is_enabled();
+    TensorPtr out = Tensor::create(conv_out_shape(input, g), record, true);
+    if (pointwise()) {
+        check(soar_pw_conv_forward(input->cuda_data(), weight_->cuda_data(), dptr(bias_),
+                                   out->cuda_data(), g.N, g.C_in, g.C_out, g.H * g.W, nullptr),
+              "pointwise convolution");
+    } else {
+        check(soar_dw_conv_forward(input->cuda_data(), weight_->cuda_data(), dptr(bias_),
+                                   out->cuda_data(), g.N, g.C_in, g.H, g.W, g.Ho, g.Wo,
+                                   (int64_t)kernel_, (int64_t)padding_, (int64_t)stride_,
+                                   (int64_t)dilation_, nullptr),
+              "depthwise convolution");
+    }
+    if (record) {
+        auto node = std::make_shared<Conv2dNode>();
+        node->input = input;
+        node->weight = weight_;
+        node->bias = bias_;
+        node->g = g;
+        node->K = (int64_t)kernel_;
+        node->pad = (int64_t)padding_;
+        node->stride = (int64_t)stride_;
+        node->dil = (int64_t)dilation_;
+        node->pointwise = pointwise();
+        out->set_grad_fn(node);
+    }
+    return out;
+}
+
+CBA::CBA(size_t c1, size_t c2, size_t k, size_t s, int p, size_t d, size_t g, bool act)
+    : Module("CBA"), act_(act) {
+    conv_ = std::make_shared<Conv2d>(c1, c2, k, s, p, d, g, false);
+    norm_ = std::make_shared<GroupNorm>((size_t)select_group_count((int)c2), c2);
+    register_submodule("conv", conv_);
+    register_submodule("norm", norm_);
+}
+
+TensorPtr CBA::forward(const TensorPtr& input) {
+    const unsigned flags = act_ ? SOAR_GN_SILU : 0u;
+    if (!conv_->pointwise()) return norm_->run(conv_->forward(input), flags);
+    // pointwise conv: one call, the GroupNorm statistics from the conv epilogue
+    const ConvGeom g = conv_geom(input, *conv_);
+    if (!input->is_cuda()) input->to_cuda();
+    const TensorPtr w = conv_->weight();
+    const TensorPtr gamma = norm_->weight(), beta = norm_->bias();
+    w->to_cuda();
+    if (gamma) {
+        gamma->to_cuda();
+        beta->to_cuda();
+    }
+    const int64_t G = (int64_t)norm_->num_groups(), HW = g.H * g.W;
+    const bool record = (input->requires_grad() || w->requires_grad() ||
+                         (gamma && gamma->requires_grad())) &&
+                        GradMode::is_enabled();
+    const Shape os = conv_out_shape(input, g);
+    TensorPtr z = Tensor::create(os, false, true);
+    TensorPtr y = Tensor::create(os, record, true);
+    TensorPtr mean = Tensor::create({g.N * G}, false, true);
+    TensorPtr rstd = Tensor::create({g.N * G}, false, true);
+    TensorPtr lo = Tensor::create({g.N * G}, false, true);
+    const size_t wsb = soar_pw_conv_gn_workspace_bytes(g.N, g.C_out, HW, G);
+    check(soar_pw_conv_gn_silu_forward(input->cuda_data(), w->cuda_data(), nullptr, dptr(gamma),
+                                       dptr(beta), z->cuda_data(), y->cuda_data(),
+                                       mean->cuda_data(), rstd->cuda_data(), lo->cuda_data(), g.N,
+                                       g.C_in, g.C_out, HW, G, norm_->eps(), flags,
+                                       workspace(wsb), wsb, nullptr),
+          "CBA forward");
+    if (record) {
+        auto node = std::make_shared<CBAPointwiseNode>();
+        node->input = input;
+        node->conv_w = w;
+        node->gamma = gamma;
+        node->beta = beta;
+        node->z = z;
+        node->mean = mean;
+        node->rstd = rstd;
+        node->mean_lo = lo;
+        node->g = g;
+        node->G = G;
+        node->flags = flags;
+        y->set_grad_fn(node);
+    }
+    return y;
 }
 
 TensorPtr add_tensors(const TensorPtr& a, const TensorPtr& b) {

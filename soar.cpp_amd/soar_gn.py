@@ -80,6 +80,7 @@ SIGNATURES = {
     "soar_zero": (_c.c_int, [_P, _SZ, _P]),
     "soar_fill": (_c.c_int, [_P, _c.c_float, _SZ, _P]),
     "soar_conv2d_1x1_forward": (_c.c_int, [_P, _P, _P, _P, _SZ, _SZ, _SZ, _P]),
+    "soar_pw_conv_forward": (_c.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "soar_pw_conv_gn_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "soar_pw_conv_gn_silu_forward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                                                 _I64, _I64, _I64, _I64, _c.c_float, _c.c_uint,

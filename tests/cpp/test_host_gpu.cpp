@@ -270,6 +270,140 @@ static void test_reference_operator_api() {
                  InvalidArgument);
 }
 
+static std::vector<float> host_copy(const TensorPtr& t) {
+    return std::vector<float>(t->data(), t->data() + t->numel());
+}
+
+static std::vector<float> to_float(const std::vector<double>& v) {
+    return std::vector<float>(v.begin(), v.end());
+}
+
+// Conv2d on the device: pointwise (with bias, N = 2) and depthwise (k7 and
+// k3 stride 2), forward and backward through the engine, against float64
+// truth (layers.cpp:17-372 semantics: dx fresh, dW/db accumulated).
+static void test_conv2d_layers() {
+    memory::DeviceArena arena(256u << 20);
+    memory::ArenaScope scope(arena);
+    {  // pointwise 16 -> 24
+        const int64_t N = 2, Ci = 16, Co = 24, H = 20, W = 30, HW = H * W;
+        nn::Conv2d conv(Ci, Co, 1, 1, -1, 1, 1, true);
+        CHECK(conv.pointwise() && conv.padding() == 0);
+        std::vector<float> x(N * Ci * HW), dy(N * Co * HW), b(Co);
+        orc_fill_normal(x.data(), (int64_t)x.size(), 601, 1, 0.0, 1.0);
+        orc_fill_normal(dy.data(), (int64_t)dy.size(), 601, 4, 0.0, 1.0);
+        orc_fill_uniform(b.data(), Co, 601, 3, -0.5, 0.5);
+        for (int64_t c = 0; c < Co; ++c) conv.bias()->data()[c] = b[c];
+        const std::vector<float> w = host_copy(conv.weight());
+        auto xt = Tensor::from_blob(x.data(), {N, Ci, H, W}, true, true);
+        auto y = conv.forward(xt);
+        CHECK(y->shape() == (Shape{N, Co, H, W}));
+        std::vector<double> yt(N * Co * HW), dxt(N * Ci * HW), dwt(Co * Ci), dbt(Co);
+        CHECK(orc_conv1x1_fwd_f64(x.data(), w.data(), b.data(), N, Ci, Co, HW, yt.data()) == 0);
+        check_close("pw conv y", y->to_host(), yt);
+        y->backward(Tensor::from_blob(dy.data(), {N, Co, H, W}, false, true));
+        CHECK(orc_conv1x1_bwd_f64(dy.data(), x.data(), w.data(), N, Ci, Co, HW, dxt.data(),
+                                  dwt.data(), dbt.data()) == 0);
+        check_close("pw conv dx", xt->grad()->to_host(), dxt);
+        check_close("pw conv dW", conv.weight()->grad()->to_host(), dwt);
+        check_close("pw conv db", conv.bias()->grad()->to_host(), dbt);
+    }
+    struct Dw {
+        int64_t N, C, H, W, K, S;
+    };
+    for (const Dw& c : {Dw{1, 8, 40, 50, 7, 1}, Dw{2, 8, 33, 47, 3, 2}}) {
+        nn::Conv2d conv(c.C, c.C, c.K, c.S, -1, 1, c.C, true);
+        CHECK(conv.depthwise() && conv.padding() == (size_t)(c.K / 2));
+        const int64_t pad = c.K / 2;
+        const int64_t Ho = (c.H + 2 * pad - c.K) / c.S + 1, Wo = (c.W + 2 * pad - c.K) / c.S + 1;
+        std::vector<float> x(c.N * c.C * c.H * c.W), dy(c.N * c.C * Ho * Wo), b(c.C);
+        orc_fill_normal(x.data(), (int64_t)x.size(), 602, 1, 0.0, 1.0);
+        orc_fill_normal(dy.data(), (int64_t)dy.size(), 602, 4, 0.0, 1.0);
+        orc_fill_uniform(b.data(), c.C, 602, 3, -0.5, 0.5);
+        for (int64_t i = 0; i < c.C; ++i) conv.bias()->data()[i] = b[i];
+        const std::vector<float> w = host_copy(conv.weight());
+        auto xt = Tensor::from_blob(x.data(), {c.N, c.C, c.H, c.W}, true, true);
+        auto y = conv.forward(xt);
+        CHECK(y->shape() == (Shape{c.N, c.C, Ho, Wo}));
+        std::vector<double> yt(dy.size()), dxt(x.size()), dwt(c.C * c.K * c.K), dbt(c.C);
+        CHECK(orc_dw_fwd_f64(x.data(), w.data(), b.data(), c.N, c.C, c.H, c.W, Ho, Wo, c.K, pad,
+                             c.S, 1, yt.data()) == 0);
+        check_close("dw conv y", y->to_host(), yt);
+        y->backward(Tensor::from_blob(dy.data(), {c.N, c.C, Ho, Wo}, false, true));
+        CHECK(orc_dw_bwd_f64(dy.data(), x.data(), w.data(), c.N, c.C, c.H, c.W, Ho, Wo, c.K, pad,
+                             c.S, 1, dxt.data(), dwt.data(), dbt.data()) == 0);
+        check_close("dw conv dx", xt->grad()->to_host(), dxt);
+        check_close("dw conv dW", conv.weight()->grad()->to_host(), dwt);
+        check_close("dw conv db", conv.bias()->grad()->to_host(), dbt);
+    }
+    // a general grouped convolution is not built on the device
+    nn::Conv2d general(8, 16, 3);
+    auto xg = Tensor::zeros({8, 10, 10}, false, true);
+    CHECK_THROWS(general.forward(xg), InvalidArgument);
+}
+
+// CBA: pointwise (one fused call, GroupNorm statistics in the conv
+// epilogue) with SiLU, and depthwise k7 without activation (LKR.dw),
+// against float64 truth composed block by block (conv, rounded to fp32 as
+// stored, then GroupNorm(+SiLU), then the conv backward on the fp32-rounded
+// dz).
+static void test_cba_blocks() {
+    memory::DeviceArena arena(256u << 20);
+    memory::ArenaScope scope(arena);
+    struct Case {
+        int64_t N, c1, c2, H, W, k, g;
+        bool act;
+    };
+    for (const Case& c : {Case{2, 16, 32, 24, 40, 1, 1, true}, Case{1, 8, 8, 30, 36, 7, 8, false}}) {
+        nn::CBA cba(c.c1, c.c2, c.k, 1, -1, 1, c.g, c.act);
+        const auto names = cba.named_parameters();
+        CHECK(names.size() == 3 && names[0].first == "conv.weight" &&
+              names[1].first == "norm.weight" && names[2].first == "norm.bias");
+        const int64_t G = nn::select_group_count((int)c.c2), HW = c.H * c.W;
+        std::vector<float> x(c.N * c.c1 * HW), dy(c.N * c.c2 * HW), gam(c.c2), bet(c.c2);
+        orc_fill_normal(x.data(), (int64_t)x.size(), 700 + c.k, 1, 0.0, 1.0);
+        orc_fill_normal(dy.data(), (int64_t)dy.size(), 700 + c.k, 4, 0.0, 1e-2);
+        orc_fill_uniform(gam.data(), c.c2, 700 + c.k, 2, 0.5, 1.5);
+        orc_fill_normal(bet.data(), c.c2, 700 + c.k, 3, 0.0, 0.1);
+        for (int64_t i = 0; i < c.c2; ++i) {
+            cba.norm()->weight()->data()[i] = gam[i];
+            cba.norm()->bias()->data()[i] = bet[i];
+        }
+        const std::vector<float> w = host_copy(cba.conv()->weight());
+        const int64_t pad = c.k / 2;
+        std::vector<double> z64(c.N * c.c2 * HW);
+        if (c.k == 1)
+            CHECK(orc_conv1x1_fwd_f64(x.data(), w.data(), nullptr, c.N, c.c1, c.c2, HW,
+                                      z64.data()) == 0);
+        else
+            CHECK(orc_dw_fwd_f64(x.data(), w.data(), nullptr, c.N, c.c1, c.H, c.W, c.H, c.W, c.k,
+                                 pad, 1, 1, z64.data()) == 0);
+        const std::vector<float> zf = to_float(z64);
+        std::vector<double> yt(zf.size()), mean(c.N * G), rstd(c.N * G), dz(zf.size()),
+            dgt(c.c2), dbt(c.c2), dxt(x.size()), dwt(w.size());
+        const int s = c.act ? 1 : 0;
+        CHECK(orc_gn_silu_fwd_f64(zf.data(), gam.data(), bet.data(), c.N, c.c2, HW, G,
+                                  (double)kEps, s, 0, yt.data(), mean.data(), rstd.data()) == 0);
+        CHECK(orc_gn_silu_bwd_f64(dy.data(), zf.data(), gam.data(), bet.data(), mean.data(),
+                                  rstd.data(), c.N, c.c2, HW, G, s, 0, dz.data(), dgt.data(),
+                                  dbt.data()) == 0);
+        const std::vector<float> dzf = to_float(dz);
+        if (c.k == 1)
+            CHECK(orc_conv1x1_bwd_f64(dzf.data(), x.data(), w.data(), c.N, c.c1, c.c2, HW,
+                                      dxt.data(), dwt.data(), nullptr) == 0);
+        else
+            CHECK(orc_dw_bwd_f64(dzf.data(), x.data(), w.data(), c.N, c.c1, c.H, c.W, c.H, c.W,
+                                 c.k, pad, 1, 1, dxt.data(), dwt.data(), nullptr) == 0);
+        auto xt = Tensor::from_blob(x.data(), {c.N, c.c1, c.H, c.W}, true, true);
+        auto y = cba.forward(xt);
+        check_close(c.k == 1 ? "cba pw y" : "cba dw y", y->to_host(), yt);
+        y->backward(Tensor::from_blob(dy.data(), {c.N, c.c2, c.H, c.W}, false, true));
+        check_close("cba dx", xt->grad()->to_host(), dxt);
+        check_close("cba conv dW", cba.conv()->weight()->grad()->to_host(), dwt);
+        check_close("cba dgamma", cba.norm()->weight()->grad()->to_host(), dgt);
+        check_close("cba dbeta", cba.norm()->bias()->grad()->to_host(), dbt);
+    }
+}
+
 int main() {
     std::printf("=== host layer: device tests ===\n");
     int fails = 0;
@@ -279,6 +413,8 @@ int main() {
                       test_batch_equals_per_sample_and_accumulates);
     fails += run_test("arena_step_reuse", test_arena_step_reuse);
     fails += run_test("reference_operator_api", test_reference_operator_api);
+    fails += run_test("conv2d_layers", test_conv2d_layers);
+    fails += run_test("cba_blocks", test_cba_blocks);
     std::printf("%s (%d failed)\n", fails ? "FAILED" : "ALL PASSED", fails);
     return fails ? 1 : 0;
 }
