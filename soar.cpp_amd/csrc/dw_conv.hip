@@ -21,7 +21,8 @@
 //            of a stride-1 convolution is the convolution with the flipped
 //            kernel), same kernel
 //   dx, S>1  gather per input element over the taps that divide (as the
-//            reference's k_conv2d_dw_backward_input)
+//            reference's k_conv2d_dw_backward_input), over a dy region
+//            staged in LDS
 //   dw, db   the block's K*K tap sums and its dy sum over its tile, reduced
 //            in the block in a fixed order, written as per-tile partials and
 //            added by a fixed-order float64 finish
@@ -157,40 +158,61 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_conv(
     }
 }
 
-// Per-tile weight and bias gradient partials: part[g][c*(K*K+1) + k] with
-// g = n*tpp + tile, k < K*K the tap sums sum dy*x, k = K*K the dy sum.
+// Weight and bias gradient partials: a block walks wg_tiles<K>() tiles down
+// one plane (tile rows ty = tyg*wg_tiles + i), accumulating in registers, then
+// reduces once: part[g][c*(K*K+1) + k] with g = n*tpp + tyg*tiles_x + tx
+// (tpp counting tile groups), k < K*K the tap sums sum dy*x, k = K*K the
+// dy sum.  (The (K*K+1)-value block reduction costs about as much as a
+// tile's FMAs for k7, so it is amortized over several tiles: 8 for K >= 7,
+// 4 below, where more blocks per plane measured faster.)
+template <int K>
+constexpr int wg_tiles() {
+    return K >= 7 ? 8 : 4;
+}
+
 template <int K, int S, int D>
 __global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
     const float* __restrict__ dy, const float* __restrict__ x, float* __restrict__ part,
     int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x,
-    int64_t tpp) {
+    int64_t tiles_y, int64_t tpp) {
     using T = Tile<K, S, D>;
     constexpr int KK1 = K * K + 1;
     __shared__ __attribute__((aligned(16))) float tile[T::floats];
     __shared__ float red[kDwThreads / 64][KK1];
-    const TileIdx ti = tile_idx(C, tiles_x, tpp);
-    fill_tile<K, S, D>(tile, x + ti.plane * Hi * Wi, ti.oy0 * S - pad, ti.ox0 * S - pad, Hi, Wi);
+    const int64_t b = blockIdx.x;
+    const int64_t plane = b / tpp, gix = b - plane * tpp;
+    const int64_t n = plane / C, c = plane - n * C;
+    const int64_t tyg = gix / tiles_x, tx = gix - tyg * tiles_x;
     const int t = threadIdx.x, r = t >> 3, c0 = (t & 7) * kPer;
-    const int64_t oy = ti.oy0 + r, ox = ti.ox0 + c0;
-    float g[kPer];
-    const float* grow = dy + ti.plane * Ho * Wo + oy * Wo;
-#pragma unroll
-    for (int c = 0; c < kPer; ++c) g[c] = (oy < Ho && ox + c < Wo) ? grow[ox + c] : 0.0f;
+    const float* xp = x + plane * Hi * Wi;
+    const float* gp = dy + plane * Ho * Wo;
     float sw[KK1];
 #pragma unroll
     for (int k = 0; k < KK1; ++k) sw[k] = 0.0f;
+    for (int i = 0; i < wg_tiles<K>(); ++i) {
+        const int64_t ty = tyg * wg_tiles<K>() + i;
+        if (ty * kTH >= Ho) break;  // uniform across the block
+        const int64_t oy0 = ty * kTH, ox0 = tx * kTW;
+        if (i > 0) __syncthreads();  // the previous tile's LDS reads are done
+        fill_tile<K, S, D>(tile, xp, oy0 * S - pad, ox0 * S - pad, Hi, Wi);
+        const int64_t oy = oy0 + r, ox = ox0 + c0;
+        float g[kPer];
 #pragma unroll
-    for (int c = 0; c < kPer; ++c) sw[K * K] += g[c];
-    __syncthreads();
+        for (int cc = 0; cc < kPer; ++cc)
+            g[cc] = (oy < Ho && ox + cc < Wo) ? gp[oy * Wo + ox + cc] : 0.0f;
 #pragma unroll
-    for (int ky = 0; ky < K; ++ky) {
-        float seg[T::SL4];
-        load_seg<K, S, D>(tile, r * S + ky * D, c0, seg);
+        for (int cc = 0; cc < kPer; ++cc) sw[K * K] += g[cc];
+        __syncthreads();
 #pragma unroll
-        for (int kx = 0; kx < K; ++kx)
+        for (int ky = 0; ky < K; ++ky) {
+            float seg[T::SL4];
+            load_seg<K, S, D>(tile, r * S + ky * D, c0, seg);
 #pragma unroll
-            for (int c = 0; c < kPer; ++c)
-                sw[ky * K + kx] = fmaf(g[c], seg[c * S + kx * D], sw[ky * K + kx]);
+            for (int kx = 0; kx < K; ++kx)
+#pragma unroll
+                for (int cc = 0; cc < kPer; ++cc)
+                    sw[ky * K + kx] = fmaf(g[cc], seg[cc * S + kx * D], sw[ky * K + kx]);
+        }
     }
     // block sum in a fixed order: wave trees, then the four waves in order
 #pragma unroll
@@ -208,8 +230,75 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
     __syncthreads();
     if (t < KK1) {
         const float v = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
-        part[(ti.n * tpp + ti.tix) * (C * KK1) + ti.c * KK1 + t] = v;
+        part[(n * tpp + gix) * (C * KK1) + c * KK1 + t] = v;
     }
+}
+
+// Input gradient for stride S > 1 over one 32 x 64 tile of dx per block:
+//   dx[yi][xi] (+)= sum over taps with S | (yi + pad - ky*D) and
+//   S | (xi + pad - kx*D) of w[ky][kx] * dy[(yi+pad-ky*D)/S][(xi+pad-kx*D)/S]
+// (the reference's gather, k_conv2d_dw_backward_input).  The dy region the
+// tile needs is staged in LDS (zeros outside dy, so no bounds tests in the
+// sum).  For S = 2 the threads of a wave share one row parity and one
+// column parity, so every tap test is uniform across the wave.
+template <int K, int S, int D>
+struct DTile {
+    static constexpr int R = (kTH - 1 + (K - 1) * D) / S + 2;      // dy rows
+    static constexpr int W = round4((kTW - 1 + (K - 1) * D) / S + 2);  // dy columns
+};
+
+__device__ __forceinline__ int64_t floor_div(int64_t a, int64_t b) {
+    return a >= 0 ? a / b : -((-a + b - 1) / b);
+}
+
+template <int K, int S, int D, bool ACC>
+__global__ __launch_bounds__(kDwThreads) void k_dw_dgrad_strided(
+    const float* __restrict__ dy, const float* __restrict__ w, float* __restrict__ dx,
+    int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x,
+    int64_t tpp) {
+    using T = DTile<K, S, D>;
+    __shared__ float tile[T::R * T::W];
+    const TileIdx ti = tile_idx(C, tiles_x, tpp);  // tiles over dx here
+    const int64_t ylo = floor_div(ti.oy0 + pad - (K - 1) * D, S);
+    const int64_t xlo = floor_div(ti.ox0 + pad - (K - 1) * D, S);
+    const float* gp = dy + ti.plane * Ho * Wo;
+    for (int i = threadIdx.x; i < T::R * T::W; i += kDwThreads) {
+        const int rr = i / T::W, cc = i - rr * T::W;
+        const int64_t yo = ylo + rr, xo = xlo + cc;
+        tile[i] = (yo >= 0 && yo < Ho && xo >= 0 && xo < Wo) ? gp[yo * Wo + xo] : 0.0f;
+    }
+    float wr[K * K];
+#pragma unroll
+    for (int k = 0; k < K * K; ++k) wr[k] = w[ti.c * K * K + k];
+    const int t = threadIdx.x, wv = t >> 6, l = t & 63;
+    // rows 2*(l/8) + (wv & 1) + 16*(wv >> 1) give each wave one row parity
+    const int r = S == 2 ? 2 * (l >> 3) + (wv & 1) + 16 * (wv >> 1) : t >> 3;
+    const int c0 = (l & 7) * kPer;
+    const int64_t yi = ti.oy0 + r, xb = ti.ox0 + c0;
+    float acc[kPer];
+#pragma unroll
+    for (int c = 0; c < kPer; ++c) acc[c] = 0.0f;
+    __syncthreads();
+#pragma unroll
+    for (int ky = 0; ky < K; ++ky) {
+        const int64_t vy = yi + pad - ky * D;
+        if (vy % S != 0) continue;
+        const float* row = tile + (vy / S - ylo) * T::W;
+#pragma unroll
+        for (int kx = 0; kx < K; ++kx) {
+            const float wk = wr[ky * K + kx];
+#pragma unroll
+            for (int c = 0; c < kPer; ++c) {
+                const int64_t vx = xb + c + pad - kx * D;
+                if (vx % S == 0) acc[c] = fmaf(wk, row[vx / S - xlo], acc[c]);
+            }
+        }
+    }
+    if (yi >= Hi) return;
+    float* orow = dx + ti.plane * Hi * Wi + yi * Wi;
+#pragma unroll
+    for (int c = 0; c < kPer; ++c)
+        if (xb + c < Wi) orow[xb + c] = ACC ? orow[xb + c] + acc[c] : acc[c];
 }
 
 // ---- generic kernels (any K, S, D): one thread per output element --------
@@ -385,10 +474,18 @@ bool dw_has_fast(int64_t K, int64_t S, int64_t D) {
     return fast_cfg(K, S, D, [](auto) {});
 }
 
+// Tile groups of the weight-gradient kernel over an Ho x Wo plane.
+int64_t wgrad_groups(int64_t Ho, int64_t Wo, int64_t K, int64_t* tiles_x, int64_t* tiles_y) {
+    const int64_t per = K >= 7 ? wg_tiles<7>() : wg_tiles<3>();
+    *tiles_x = (Wo + kTW - 1) / kTW;
+    *tiles_y = (Ho + kTH - 1) / kTH;
+    return ((*tiles_y + per - 1) / per) * *tiles_x;
+}
+
 size_t dw_bwd_workspace_bytes(const DwShape& sh) {
     if (!dw_has_fast(sh.K, sh.S, sh.D)) return 0;
-    int64_t tx = 0;
-    const int64_t tpp = tiles_of(sh.Ho, sh.Wo, &tx);
+    int64_t tx = 0, ty = 0;
+    const int64_t tpp = wgrad_groups(sh.Ho, sh.Wo, sh.K, &tx, &ty);
     const size_t b = sizeof(float) * (size_t)(sh.N * tpp) * (size_t)(sh.C * (sh.K * sh.K + 1));
     return (b + 255) & ~(size_t)255;
 }
@@ -445,6 +542,21 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
                 });
             });
         }
+        if (!done && sh.S > 1) {
+            int64_t tiles_x = 0;
+            const int64_t tpp = tiles_of(sh.Hi, sh.Wi, &tiles_x);
+            done = fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
+                using CF = decltype(cf);
+                if constexpr (CF::s > 1) {
+                    bsel(accumulate_dx, [&](auto A) {
+                        k_dw_dgrad_strided<CF::k, CF::s, CF::d, A()>
+                            <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
+                                dy, w, dx, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x,
+                                tpp);
+                    });
+                }
+            });
+        }
         if (!done) {
             bsel(accumulate_dx, [&](auto A) {
                 k_dw_dx_gather<A()><<<grid_stride_blocks(sh.N * sh.C * sh.Hi * sh.Wi), 256, 0,
@@ -456,15 +568,15 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
     }
     if ((dw || db) && sh.Ho * sh.Wo > 0) {
         const int64_t KK1 = sh.K * sh.K + 1;
-        int64_t tiles_x = 0;
-        const int64_t tpp = tiles_of(sh.Ho, sh.Wo, &tiles_x);
+        int64_t tiles_x = 0, tiles_y = 0;
+        const int64_t tpp = wgrad_groups(sh.Ho, sh.Wo, sh.K, &tiles_x, &tiles_y);
         float* part = static_cast<float*>(ws);
         int tok = prof_begin(s, "dw_conv_wgrad");
         const bool fast = fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
             using CF = decltype(cf);
             k_dw_wgrad<CF::k, CF::s, CF::d>
                 <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
-                    dy, x, part, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tpp);
+                    dy, x, part, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tiles_y, tpp);
         });
         prof_end(s, tok);
         tok = prof_begin(s, "dw_conv_wgrad_finish");
