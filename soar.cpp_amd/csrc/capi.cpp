@@ -22,13 +22,14 @@
 #include <string>
 #include <vector>
 
+#include "capi_common.hpp"
 #include "gn_internal.hpp"
 #include "soar_gn.h"
 
 using soar::gn::Plan;
 using soar::gn::Tuning;
 
-namespace {
+namespace soar::capi {
 
 thread_local std::string g_err;
 
@@ -95,40 +96,6 @@ int check_dev_opt(const void* p, size_t bytes, const char* name) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// ---- tuning ---------------------------------------------------------------
-std::mutex g_tune_mu;
-Tuning g_tune;
-
-Tuning current_tuning() {
-    std::lock_guard<std::mutex> lk(g_tune_mu);
-    return g_tune;
-}
-
-// ---- shape validation shared by the fused entry points ---------------------
-int check_shape(int64_t N, int64_t C, int64_t HW, int64_t G, int64_t* elems) {
-    if (N < 0 || C < 0 || HW < 0)
-        return fail(SOAR_EINVAL, "negative dimension (N=%lld C=%lld HW=%lld)",
-                    (long long)N, (long long)C, (long long)HW);
-    if (G <= 0) return fail(SOAR_EINVAL, "num_groups must be positive (G=%lld)", (long long)G);
-    if (C % G != 0)
-        return fail(SOAR_EINVAL, "C=%lld is not divisible by num_groups=%lld",
-                    (long long)C, (long long)G);
-    int64_t nc = 0, e = 0;
-    if (__builtin_mul_overflow(N, C, &nc) || __builtin_mul_overflow(nc, HW, &e) ||
-        e > INT64_MAX / 4)
-        return fail(SOAR_EINVAL, "N*C*HW overflows");
-    *elems = e;
-    return SOAR_OK;
-}
-
-int check_ws(const Plan& p, void* ws, size_t ws_bytes) {
-    const size_t need = soar::gn::workspace_bytes(p);
-    if (ws_bytes < need)
-        return fail(SOAR_EINVAL, "workspace of %zu bytes is smaller than the %zu this shape needs",
-                    ws_bytes, need);
-    return check_dev(ws, need, "workspace");
-}
-
 // ---- library-owned workspace of the reference-signature entry points ------
 struct OwnedWs {
     void* ptr = nullptr;
@@ -162,6 +129,47 @@ int owned_workspace(size_t need, void** out) {
     }
     *out = w.ptr;
     return SOAR_OK;
+}
+
+
+}  // namespace soar::capi
+
+using namespace soar::capi;
+
+namespace {
+
+// ---- tuning ---------------------------------------------------------------
+std::mutex g_tune_mu;
+Tuning g_tune;
+
+Tuning current_tuning() {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    return g_tune;
+}
+
+// ---- shape validation shared by the fused entry points ---------------------
+int check_shape(int64_t N, int64_t C, int64_t HW, int64_t G, int64_t* elems) {
+    if (N < 0 || C < 0 || HW < 0)
+        return fail(SOAR_EINVAL, "negative dimension (N=%lld C=%lld HW=%lld)",
+                    (long long)N, (long long)C, (long long)HW);
+    if (G <= 0) return fail(SOAR_EINVAL, "num_groups must be positive (G=%lld)", (long long)G);
+    if (C % G != 0)
+        return fail(SOAR_EINVAL, "C=%lld is not divisible by num_groups=%lld",
+                    (long long)C, (long long)G);
+    int64_t nc = 0, e = 0;
+    if (__builtin_mul_overflow(N, C, &nc) || __builtin_mul_overflow(nc, HW, &e) ||
+        e > INT64_MAX / 4)
+        return fail(SOAR_EINVAL, "N*C*HW overflows");
+    *elems = e;
+    return SOAR_OK;
+}
+
+int check_ws(const Plan& p, void* ws, size_t ws_bytes) {
+    const size_t need = soar::gn::workspace_bytes(p);
+    if (ws_bytes < need)
+        return fail(SOAR_EINVAL, "workspace of %zu bytes is smaller than the %zu this shape needs",
+                    ws_bytes, need);
+    return check_dev(ws, need, "workspace");
 }
 
 // ---- per-kernel hipEvent timing --------------------------------------------

@@ -1,0 +1,38 @@
+// capi_common.hpp - validation and status helpers shared by the C-ABI
+// translation units of libsoar_gn.so (capi.cpp, ops_capi.cpp).
+//
+// Every entry point returns SOAR_OK or a negative SOAR_E* status and leaves
+// a message for soar_last_error() on the calling thread.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+namespace soar::capi {
+
+extern thread_local std::string g_err;
+
+// Records a printf-style message and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the message and returns SOAR_OK.
+int ok();
+int hip_fail(hipError_t e, const char* what);
+int device_count();
+// SOAR_ENODEV when no HIP device is visible.
+int require_device();
+// `p` must be device memory with at least `bytes` bytes from p to the end
+// of its allocation (a host pointer or a too-short buffer is rejected here
+// rather than faulting the GPU).
+int check_dev(const void* p, size_t bytes, const char* name);
+// Same, a null pointer allowed.
+int check_dev_opt(const void* p, size_t bytes, const char* name);
+bool aligned16(const void* p);
+// Library-owned workspace of the current device, grown to `need` bytes
+// (used by the entry points with the reference's workspace-free
+// signatures).  Callers on one device share it.
+int owned_workspace(size_t need, void** out);
+
+}  // namespace soar::capi

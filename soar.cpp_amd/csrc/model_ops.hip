@@ -1,0 +1,878 @@
+// model_ops.hip - the device operators of the SOAR model around the
+// GroupNorm / convolution path: the general grouped convolution of the
+// stem, sigmoid, channel-broadcast multiply, convex combination, global
+// average pool, bilinear resize, pixel shuffle, spatial pad/crop, the
+// Dice+BCE loss, and the multi-tensor gradient-norm / AdamW updates.
+//
+// Reference kernels (pomagrenate/soar.cpp): src/cuda/ops/
+// convolution_kernels.cu (general conv2d), activation_kernels.cu (sigmoid),
+// binary_ops_kernels.cu (mul_broadcast, convex_combination),
+// pooling_kernels.cu (global_avg_pool), upsample_kernels.cu:11-135,
+// loss_kernels.cu:29-265, optimizer_kernels.cu, and the host loops of
+// src/nn/layers.cpp:807-1345, src/nn/soar_model.cpp:15-172,
+// src/optim/adamw.cpp:28-108.
+//
+// All of these are small, HBM- or launch-bound passes.  Every reduction
+// runs in a fixed order (per-thread sums, then a fixed-shape block tree,
+// then a fixed-order finish), so results do not depend on scheduling; the
+// reference's float atomics (loss_kernels.cu:46,131, upsample_kernels.cu:
+// 97-100) are replaced by fp64 partials or by gathers.
+#include "ops_internal.hpp"
+
+#include <algorithm>
+#include <cmath>
+
+namespace soar::ops {
+namespace {
+
+constexpr int kThreads = 256;
+
+int blocks_for(int64_t n, int64_t per_block = kThreads, int64_t cap = 8192) {
+    int64_t b = (n + per_block - 1) / per_block;
+    return (int)std::max<int64_t>(1, std::min<int64_t>(b, cap));
+}
+
+// Sum of `v` over a 256-thread block, the same tree every call; the result
+// is valid in thread 0.
+__device__ double block_sum(double v, double* sh) {
+    const int t = threadIdx.x;
+    sh[t] = v;
+    __syncthreads();
+    for (int w = kThreads / 2; w > 0; w >>= 1) {
+        if (t < w) sh[t] += sh[t + w];
+        __syncthreads();
+    }
+    const double r = sh[0];
+    __syncthreads();  // sh may be reused as soon as this returns
+    return r;
+}
+
+__device__ __forceinline__ float sigmoidf_exact(float z) { return 1.0f / (1.0f + expf(-z)); }
+
+// ---------------------------------------------------------------------------
+// General grouped convolution (convolution_kernels.cu conv2d_forward /
+// conv2d_backward; layers.cpp:17-292 general branch).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void k_conv_fwd(const float* __restrict__ in,
+                                                       const float* __restrict__ w,
+                                                       const float* __restrict__ bias,
+                                                       float* __restrict__ out, ConvShape c) {
+    const int64_t total = c.N * c.C_out * c.Ho * c.Wo;
+    const int64_t cig = c.C_in / c.groups, cog = c.C_out / c.groups;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kThreads) {
+        const int64_t ox = i % c.Wo;
+        int64_t t = i / c.Wo;
+        const int64_t oy = t % c.Ho;
+        t /= c.Ho;
+        const int64_t co = t % c.C_out;
+        const int64_t n = t / c.C_out;
+        const int64_t ci0 = (co / cog) * cig;
+        float acc = 0.0f;
+        for (int64_t q = 0; q < cig; ++q) {
+            const float* plane = in + ((n * c.C_in + ci0 + q) * c.H) * c.W;
+            const float* wk = w + (co * cig + q) * c.K * c.K;
+            for (int64_t ky = 0; ky < c.K; ++ky) {
+                const int64_t iy = oy * c.S - c.pad + ky * c.D;
+                if (iy < 0 || iy >= c.H) continue;
+                for (int64_t kx = 0; kx < c.K; ++kx) {
+                    const int64_t ix = ox * c.S - c.pad + kx * c.D;
+                    if (ix < 0 || ix >= c.W) continue;
+                    acc = fmaf(wk[ky * c.K + kx], plane[iy * c.W + ix], acc);
+                }
+            }
+        }
+        out[i] = bias ? acc + bias[co] : acc;
+    }
+}
+
+// dx: every input element gathers the outputs its taps reach.
+template <bool ACC>
+__global__ __launch_bounds__(kThreads) void k_conv_dx(const float* __restrict__ go,
+                                                      const float* __restrict__ w,
+                                                      float* __restrict__ gx, ConvShape c) {
+    const int64_t total = c.N * c.C_in * c.H * c.W;
+    const int64_t cig = c.C_in / c.groups, cog = c.C_out / c.groups;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kThreads) {
+        const int64_t ix = i % c.W;
+        int64_t t = i / c.W;
+        const int64_t iy = t % c.H;
+        t /= c.H;
+        const int64_t ci = t % c.C_in;
+        const int64_t n = t / c.C_in;
+        const int64_t g = ci / cig, q = ci - g * cig;
+        float acc = 0.0f;
+        for (int64_t co = g * cog; co < (g + 1) * cog; ++co) {
+            const float* gp = go + ((n * c.C_out + co) * c.Ho) * c.Wo;
+            const float* wk = w + (co * cig + q) * c.K * c.K;
+            for (int64_t ky = 0; ky < c.K; ++ky) {
+                const int64_t ty = iy + c.pad - ky * c.D;
+                if (ty < 0 || ty % c.S) continue;
+                const int64_t oy = ty / c.S;
+                if (oy >= c.Ho) continue;
+                for (int64_t kx = 0; kx < c.K; ++kx) {
+                    const int64_t tx = ix + c.pad - kx * c.D;
+                    if (tx < 0 || tx % c.S) continue;
+                    const int64_t ox = tx / c.S;
+                    if (ox >= c.Wo) continue;
+                    acc = fmaf(wk[ky * c.K + kx], gp[oy * c.Wo + ox], acc);
+                }
+            }
+        }
+        if (ACC)
+            gx[i] += acc;
+        else
+            gx[i] = acc;
+    }
+}
+
+constexpr int64_t kConvChunk = 16384;  // output positions per dW block
+
+int64_t conv_chunks(const ConvShape& c) {
+    return (c.N * c.Ho * c.Wo + kConvChunk - 1) / kConvChunk;
+}
+
+// dW / db partials: block x = (co*cig+q)*(K*K+1) + tap, block y = chunk;
+// tap == K*K is the bias sum (only for q == 0).
+// part[(co*cig+q)*(K*K+1)+tap][chunk].
+__global__ __launch_bounds__(kThreads) void k_conv_dw(const float* __restrict__ go,
+                                                      const float* __restrict__ in,
+                                                      double* __restrict__ part, ConvShape c,
+                                                      int64_t chunks) {
+    __shared__ double sh[kThreads];
+    const int64_t chunk = blockIdx.y;
+    const int64_t KK = c.K * c.K;
+    const int64_t tap = (int64_t)blockIdx.x % (KK + 1);
+    const int64_t cig = c.C_in / c.groups, cog = c.C_out / c.groups;
+    const int64_t wq = (int64_t)blockIdx.x / (KK + 1);  // co*cig + q
+    const int64_t co = wq / cig, q = wq - co * cig;
+    const bool is_bias = tap == KK;
+    double s = 0.0;
+    if (!is_bias || q == 0) {
+        const int64_t ci = (co / cog) * cig + q;
+        const int64_t ky = is_bias ? 0 : tap / c.K, kx = is_bias ? 0 : tap % c.K;
+        const int64_t HWo = c.Ho * c.Wo;
+        const int64_t end = std::min((chunk + 1) * kConvChunk, c.N * HWo);
+        for (int64_t p = chunk * kConvChunk + threadIdx.x; p < end; p += kThreads) {
+            const int64_t n = p / HWo, r = p - n * HWo;
+            const int64_t oy = r / c.Wo, ox = r - oy * c.Wo;
+            const float g = go[(n * c.C_out + co) * HWo + r];
+            if (is_bias) {
+                s += g;
+                continue;
+            }
+            const int64_t iy = oy * c.S - c.pad + ky * c.D;
+            const int64_t ix = ox * c.S - c.pad + kx * c.D;
+            if (iy < 0 || iy >= c.H || ix < 0 || ix >= c.W) continue;
+            s += (double)g * in[((n * c.C_in + ci) * c.H + iy) * c.W + ix];
+        }
+    }
+    s = block_sum(s, sh);
+    if (threadIdx.x == 0) part[(wq * (KK + 1) + tap) * chunks + chunk] = s;
+}
+
+// Adds the chunk sums in order: gw[co][q][tap] += ..., gb[co] += ...
+__global__ __launch_bounds__(kThreads) void k_conv_dw_finish(const double* __restrict__ part,
+                                                             float* __restrict__ gw,
+                                                             float* __restrict__ gb,
+                                                             ConvShape c, int64_t chunks) {
+    const int64_t KK = c.K * c.K;
+    const int64_t cig = c.C_in / c.groups;
+    const int64_t rows = c.C_out * cig * (KK + 1);
+    for (int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x; r < rows;
+         r += (int64_t)gridDim.x * kThreads) {
+        const int64_t wq = r / (KK + 1), tap = r - wq * (KK + 1);
+        const int64_t co = wq / cig, q = wq - co * cig;
+        double s = 0.0;
+        for (int64_t k = 0; k < chunks; ++k) s += part[r * chunks + k];
+        if (tap < KK) {
+            if (gw) gw[wq * KK + tap] += (float)s;
+        } else if (q == 0 && gb) {
+            gb[co] += (float)s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise operators.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void k_sigmoid_fwd(const float* __restrict__ x,
+                                                          float* __restrict__ y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads)
+        y[i] = sigmoidf_exact(x[i]);
+}
+
+// gx += gy * y * (1 - y)   (activation_kernels.cu:173, layers.cpp:826-831)
+__global__ __launch_bounds__(kThreads) void k_sigmoid_bwd(const float* __restrict__ gy,
+                                                          const float* __restrict__ y,
+                                                          float* __restrict__ gx, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads) {
+        const float v = y[i];
+        gx[i] += gy[i] * v * (1.0f - v);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_mul_bcast_fwd(const float* __restrict__ a,
+                                                            const float* __restrict__ b,
+                                                            float* __restrict__ y, int64_t rows,
+                                                            int64_t HW) {
+    const int64_t n = rows * HW;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads)
+        y[i] = a[i] * b[i / HW];
+}
+
+// ga += gy * b[row]; gb[row] += sum gy*a (one block per row; the
+// reference's per-element atomicAdd, binary_ops_kernels.cu:129, becomes a
+// fixed-order block sum).
+__global__ __launch_bounds__(kThreads) void k_mul_bcast_bwd(const float* __restrict__ gy,
+                                                            const float* __restrict__ a,
+                                                            const float* __restrict__ b,
+                                                            float* __restrict__ ga,
+                                                            float* __restrict__ gb, int64_t HW) {
+    __shared__ double sh[kThreads];
+    const int64_t row = blockIdx.x;
+    const float* g = gy + row * HW;
+    const float* ar = a + row * HW;
+    const float bv = b[row];
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < HW; i += kThreads) {
+        const float gv = g[i];
+        if (ga) ga[row * HW + i] += gv * bv;
+        if (gb) s += (double)gv * ar[i];
+    }
+    if (gb) {
+        s = block_sum(s, sh);
+        if (threadIdx.x == 0) gb[row] += (float)s;
+    }
+}
+
+// y = g*a + (1-g)*b   (blocks.cpp:333)
+__global__ __launch_bounds__(kThreads) void k_convex_fwd(const float* __restrict__ g,
+                                                         const float* __restrict__ a,
+                                                         const float* __restrict__ b,
+                                                         float* __restrict__ y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads) {
+        const float gv = g[i];
+        y[i] = gv * a[i] + (1.0f - gv) * b[i];
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_convex_bwd(const float* __restrict__ gy,
+                                                         const float* __restrict__ g,
+                                                         const float* __restrict__ a,
+                                                         const float* __restrict__ b,
+                                                         float* __restrict__ gg,
+                                                         float* __restrict__ ga,
+                                                         float* __restrict__ gb, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads) {
+        const float d = gy[i], gv = g[i];
+        if (ga) ga[i] += d * gv;
+        if (gb) gb[i] += d * (1.0f - gv);
+        if (gg) gg[i] += d * (a[i] - b[i]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Global average pool: one block per plane (layers.cpp:1306-1345).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void k_avg_pool_fwd(const float* __restrict__ in,
+                                                           float* __restrict__ out, int64_t HW) {
+    __shared__ double sh[kThreads];
+    const float* p = in + (int64_t)blockIdx.x * HW;
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < HW; i += kThreads) s += p[i];
+    s = block_sum(s, sh);
+    if (threadIdx.x == 0) out[blockIdx.x] = (float)(s / (double)HW);
+}
+
+// gi += go[row] / HW   (pooling_kernels.cu:27-33)
+__global__ __launch_bounds__(kThreads) void k_avg_pool_bwd(const float* __restrict__ go,
+                                                           float* __restrict__ gi, int64_t rows,
+                                                           int64_t HW) {
+    const int64_t n = rows * HW;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads)
+        gi[i] += go[i / HW] / (float)HW;
+}
+
+// ---------------------------------------------------------------------------
+// Bilinear resize, half-pixel centres, no corner alignment
+// (upsample_kernels.cu:11-66, layers.cpp:1073-1150).
+// ---------------------------------------------------------------------------
+struct Src {
+    int64_t i0, i1;  // the two source taps (equal at the last row / column)
+    float l0, l1;    // their weights
+};
+
+__device__ __forceinline__ Src src_index(float scale, int64_t dst, int64_t n_in) {
+    float r = scale * ((float)dst + 0.5f) - 0.5f;
+    r = r < 0.0f ? 0.0f : r;
+    const int64_t i0 = min((int64_t)r, n_in - 1);
+    const int64_t step = i0 < n_in - 1 ? 1 : 0;
+    const float l1 = r - (float)i0;
+    return {i0, i0 + step, 1.0f - l1, l1};
+}
+
+__global__ __launch_bounds__(kThreads) void k_upsample_fwd(const float* __restrict__ in,
+                                                           float* __restrict__ out, int64_t rows,
+                                                           int64_t H_in, int64_t W_in,
+                                                           int64_t H_out, int64_t W_out,
+                                                           float sh, float sw) {
+    const int64_t total = rows * H_out * W_out;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kThreads) {
+        const int64_t x = i % W_out;
+        int64_t t = i / W_out;
+        const int64_t y = t % H_out;
+        const int64_t row = t / H_out;
+        const Src sy = src_index(sh, y, H_in), sx = src_index(sw, x, W_in);
+        const float* p = in + row * H_in * W_in;
+        const float v00 = p[sy.i0 * W_in + sx.i0], v01 = p[sy.i0 * W_in + sx.i1];
+        const float v10 = p[sy.i1 * W_in + sx.i0], v11 = p[sy.i1 * W_in + sx.i1];
+        out[i] = sy.l0 * (sx.l0 * v00 + sx.l1 * v01) + sy.l1 * (sx.l0 * v10 + sx.l1 * v11);
+    }
+}
+
+// Range of destination indices whose taps can reach source index `s`
+// (conservative by one on each side; callers re-test each candidate).
+__device__ __forceinline__ void dst_range(float scale, int64_t s, int64_t n_out, int64_t* lo,
+                                          int64_t* hi) {
+    const float a = ((float)s - 0.5f) / scale - 0.5f;
+    const float b = ((float)s + 1.5f) / scale - 0.5f;
+    *lo = std::max<int64_t>(0, (int64_t)floorf(a) - 1);
+    *hi = std::min<int64_t>(n_out - 1, (int64_t)ceilf(b) + 1);
+}
+
+__device__ __forceinline__ float tap_weight(const Src& s, int64_t idx) {
+    return (s.i0 == idx ? s.l0 : 0.0f) + (s.i1 == idx ? s.l1 : 0.0f);
+}
+
+// Backward as a gather: each source pixel sums the destination pixels that
+// read it, with the forward's weights (no atomics).
+__global__ __launch_bounds__(kThreads) void k_upsample_bwd(const float* __restrict__ go,
+                                                           float* __restrict__ gi, int64_t rows,
+                                                           int64_t H_in, int64_t W_in,
+                                                           int64_t H_out, int64_t W_out,
+                                                           float sh, float sw) {
+    const int64_t total = rows * H_in * W_in;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kThreads) {
+        const int64_t ix = i % W_in;
+        int64_t t = i / W_in;
+        const int64_t iy = t % H_in;
+        const int64_t row = t / H_in;
+        int64_t y0, y1, x0, x1;
+        dst_range(sh, iy, H_out, &y0, &y1);
+        dst_range(sw, ix, W_out, &x0, &x1);
+        const float* g = go + row * H_out * W_out;
+        float acc = 0.0f;
+        for (int64_t y = y0; y <= y1; ++y) {
+            const float wy = tap_weight(src_index(sh, y, H_in), iy);
+            if (wy == 0.0f) continue;
+            float rs = 0.0f;
+            for (int64_t x = x0; x <= x1; ++x) {
+                const float wx = tap_weight(src_index(sw, x, W_in), ix);
+                if (wx != 0.0f) rs += wx * g[y * W_out + x];
+            }
+            acc += wy * rs;
+        }
+        gi[i] += acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Pixel shuffle (layers.cpp:928-989): out[c][y][x] =
+// in[c*r*r + (y%r)*r + x%r][y/r][x/r]; the backward adds each output
+// gradient to the input element it came from (a permutation, no
+// collisions).
+// ---------------------------------------------------------------------------
+template <bool BWD>
+__global__ __launch_bounds__(kThreads) void k_pixel_shuffle(const float* __restrict__ src,
+                                                            float* __restrict__ dst, int64_t N,
+                                                            int64_t C_out, int64_t H_in,
+                                                            int64_t W_in, int64_t r) {
+    const int64_t H_out = H_in * r, W_out = W_in * r;
+    const int64_t total = N * C_out * H_out * W_out;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kThreads) {
+        const int64_t x = i % W_out;
+        int64_t t = i / W_out;
+        const int64_t y = t % H_out;
+        t /= H_out;  // n*C_out + c
+        const int64_t cin = t * r * r + (y % r) * r + (x % r);
+        const int64_t j = (cin * H_in + y / r) * W_in + x / r;
+        if (BWD)
+            dst[j] += src[i];
+        else
+            dst[i] = src[j];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Spatial pad to a multiple of the model stride (soar_model.cpp:74-135):
+// rows past H (columns past W) copy the reflected row 2(H-1)-y, or the last
+// row when the pad is not smaller than the image.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int64_t pad_src(int64_t y, int64_t H, bool reflect) {
+    return y < H ? y : (reflect ? 2 * (H - 1) - y : H - 1);
+}
+
+__global__ __launch_bounds__(kThreads) void k_pad_fwd(const float* __restrict__ in,
+                                                      float* __restrict__ out, int64_t rows,
+                                                      int64_t H, int64_t W, int64_t Hp,
+                                                      int64_t Wp, bool reflect) {
+    const int64_t total = rows * Hp * Wp;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kThreads) {
+        const int64_t x = i % Wp;
+        int64_t t = i / Wp;
+        const int64_t y = t % Hp;
+        const int64_t row = t / Hp;
+        out[i] = in[(row * H + pad_src(y, H, reflect)) * W + pad_src(x, W, reflect)];
+    }
+}
+
+// Padded rows that read source row `s`: s itself plus, when reflecting,
+// 2(H-1)-s if it lies in [H, Hp); when clamping, every row >= H for s=H-1.
+__device__ __forceinline__ int pad_dsts(int64_t s, int64_t H, int64_t Hp, bool reflect,
+                                        int64_t* first, int64_t* extra_lo, int64_t* extra_hi) {
+    *first = s;
+    *extra_lo = 1;
+    *extra_hi = 0;  // empty range
+    if (reflect) {
+        const int64_t d = 2 * (H - 1) - s;
+        if (d >= H && d < Hp) *extra_lo = *extra_hi = d;
+    } else if (s == H - 1 && Hp > H) {
+        *extra_lo = H;
+        *extra_hi = Hp - 1;
+    }
+    return 0;
+}
+
+__global__ __launch_bounds__(kThreads) void k_pad_bwd(const float* __restrict__ go,
+                                                      float* __restrict__ gi, int64_t rows,
+                                                      int64_t H, int64_t W, int64_t Hp,
+                                                      int64_t Wp, bool reflect) {
+    const int64_t total = rows * H * W;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kThreads) {
+        const int64_t x = i % W;
+        int64_t t = i / W;
+        const int64_t y = t % H;
+        const int64_t row = t / H;
+        int64_t fy, ylo, yhi, fx, xlo, xhi;
+        pad_dsts(y, H, Hp, reflect, &fy, &ylo, &yhi);
+        pad_dsts(x, W, Wp, reflect, &fx, &xlo, &xhi);
+        const float* g = go + row * Hp * Wp;
+        auto row_sum = [&](int64_t yy) {
+            float s = g[yy * Wp + fx];
+            for (int64_t xx = xlo; xx <= xhi; ++xx) s += g[yy * Wp + xx];
+            return s;
+        };
+        float acc = row_sum(fy);
+        for (int64_t yy = ylo; yy <= yhi; ++yy) acc += row_sum(yy);
+        gi[i] += acc;
+    }
+}
+
+template <bool BWD>
+__global__ __launch_bounds__(kThreads) void k_crop(const float* __restrict__ src,
+                                                   float* __restrict__ dst, int64_t rows,
+                                                   int64_t Hp, int64_t Wp, int64_t H,
+                                                   int64_t W) {
+    // forward: dst [rows][H][W] from src [rows][Hp][Wp];
+    // backward: dst [rows][Hp][Wp] += src [rows][H][W] (nothing outside).
+    const int64_t total = BWD ? rows * Hp * Wp : rows * H * W;
+    const int64_t ow = BWD ? Wp : W, oh = BWD ? Hp : H;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kThreads) {
+        const int64_t x = i % ow;
+        int64_t t = i / ow;
+        const int64_t y = t % oh;
+        const int64_t row = t / oh;
+        if (BWD)
+            dst[i] += (y < H && x < W) ? src[(row * H + y) * W + x] : 0.0f;
+        else
+            dst[i] = src[(row * Hp + y) * Wp + x];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Dice + BCE loss (loss_kernels.cu:29-265; losses.cpp:80-122,207-262).
+// ---------------------------------------------------------------------------
+constexpr int kLossBlocks = 1024;
+
+__global__ __launch_bounds__(kThreads) void k_loss_sums(const float* __restrict__ z,
+                                                        const float* __restrict__ y, int64_t n,
+                                                        float pos_weight,
+                                                        double* __restrict__ part) {
+    __shared__ double sh[kThreads];
+    double bce = 0.0, inter = 0.0, sp = 0.0, sy = 0.0;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads) {
+        const float zi = z[i], yi = y[i];
+        const float w = 1.0f + (pos_weight - 1.0f) * yi;
+        const float term = fmaxf(-zi, 0.0f) + log1pf(expf(-fabsf(zi)));
+        bce += (double)((1.0f - yi) * zi + w * term);
+        const float p = sigmoidf_exact(zi);
+        inter += (double)(p * yi);
+        sp += p;
+        sy += yi;
+    }
+    const double v[4] = {bce, inter, sp, sy};
+    for (int k = 0; k < 4; ++k) {
+        const double s = block_sum(v[k], sh);
+        if (threadIdx.x == 0) part[k * gridDim.x + blockIdx.x] = s;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_loss_finish(const double* __restrict__ part,
+                                                          int nparts, double* __restrict__ out) {
+    // thread k < 4 adds quantity k over the blocks in order
+    const int k = threadIdx.x;
+    if (k < 4) {
+        double s = 0.0;
+        for (int b = 0; b < nparts; ++b) s += part[k * nparts + b];
+        out[k] = s;
+    }
+}
+
+// gz += BCE gradient * scale_bce + Dice gradient * scale_dice
+// (loss_kernels.cu:212-252; losses.cpp:497-541)
+__global__ __launch_bounds__(kThreads) void k_dice_bce_bwd(const float* __restrict__ z,
+                                                           const float* __restrict__ y,
+                                                           float* __restrict__ gz, int64_t n,
+                                                           float scale_bce, float scale_dice,
+                                                           float pos_weight, float denom,
+                                                           float numer) {
+    const float denom_sq = denom * denom;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads) {
+        const float zi = z[i], yi = y[i];
+        const float sig = sigmoidf_exact(zi);
+        float g = 0.0f;
+        if (scale_bce != 0.0f) {
+            const float w_pos = 1.0f + (pos_weight - 1.0f) * yi;
+            g += (sig * w_pos - pos_weight * yi) * scale_bce;
+        }
+        if (scale_dice != 0.0f) {
+            const float dp_dz = sig * (1.0f - sig);
+            const float d_dice_dp = (2.0f * yi * denom - numer) / denom_sq;
+            g += scale_dice * (-d_dice_dp * dp_dz);
+        }
+        gz[i] += g;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_sigmoid_threshold(const float* __restrict__ z,
+                                                                float* __restrict__ p,
+                                                                uint8_t* __restrict__ mask,
+                                                                int64_t n, float threshold) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads) {
+        const float v = sigmoidf_exact(z[i]);
+        if (p) p[i] = v;
+        if (mask) mask[i] = v >= threshold ? 1 : 0;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Multi-tensor operators: every block walks every tensor with a grid
+// stride, so one launch covers the whole parameter list.
+// ---------------------------------------------------------------------------
+constexpr int kMultiBlocks = 512;
+
+__global__ __launch_bounds__(kThreads) void k_multi_norm_sq(const float* const* __restrict__ t,
+                                                            const int64_t* __restrict__ numel,
+                                                            int n_tensors,
+                                                            double* __restrict__ part) {
+    __shared__ double sh[kThreads];
+    double s = 0.0;
+    const int64_t start = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int k = 0; k < n_tensors; ++k) {
+        const float* p = t[k];
+        const int64_t n = numel[k];
+        for (int64_t i = start; i < n; i += stride) {
+            const double v = p[i];
+            s += v * v;
+        }
+    }
+    s = block_sum(s, sh);
+    if (threadIdx.x == 0) part[blockIdx.x] = s;
+}
+
+__global__ __launch_bounds__(64) void k_multi_norm_finish(const double* __restrict__ part,
+                                                          int nparts, double* __restrict__ out) {
+    if (threadIdx.x == 0) {
+        double s = 0.0;
+        for (int b = 0; b < nparts; ++b) s += part[b];
+        out[0] = s;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_multi_scale(float* const* __restrict__ t,
+                                                          const int64_t* __restrict__ numel,
+                                                          int n_tensors, float scale) {
+    const int64_t start = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int k = 0; k < n_tensors; ++k) {
+        float* p = t[k];
+        const int64_t n = numel[k];
+        for (int64_t i = start; i < n; i += stride) p[i] *= scale;
+    }
+}
+
+// The AdamW update of adamw.cpp:60-108, operation by operation in fp32
+// with no fused multiply-adds, so it matches a scalar IEEE evaluation of
+// the same expressions bit for bit.
+__global__ __launch_bounds__(kThreads) void k_adamw_multi(
+    float* const* __restrict__ P, const float* const* __restrict__ G, float* const* __restrict__ M,
+    float* const* __restrict__ V, const int64_t* __restrict__ numel, int n_tensors, float lr,
+    float beta1, float beta2, float eps, float wd, float step_size, float sqrt_bc2) {
+#pragma clang fp contract(off)
+    const int64_t start = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    const float one_m_b1 = 1.0f - beta1, one_m_b2 = 1.0f - beta2;
+    const float lr_wd = lr * wd;
+    for (int k = 0; k < n_tensors; ++k) {
+        float* theta = P[k];
+        const float* g = G[k];
+        float* m = M[k];
+        float* v = V[k];
+        const int64_t n = numel[k];
+        for (int64_t i = start; i < n; i += stride) {
+            const float gv = g[i];
+            float th = theta[i];
+            if (wd != 0.0f) th = th - lr_wd * th;
+            const float mv = beta1 * m[i] + one_m_b1 * gv;
+            const float vv = beta2 * v[i] + one_m_b2 * gv * gv;
+            const float denom = (sqrtf(vv) / sqrt_bc2) + eps;
+            th = th - step_size * (mv / denom);
+            m[i] = mv;
+            v[i] = vv;
+            theta[i] = th;
+        }
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Launchers.
+// ---------------------------------------------------------------------------
+hipError_t launch_conv_forward(const float* in, const float* w, const float* bias, float* out,
+                               const ConvShape& c, hipStream_t s) {
+    const int64_t total = c.N * c.C_out * c.Ho * c.Wo;
+    k_conv_fwd<<<blocks_for(total), kThreads, 0, s>>>(in, w, bias, out, c);
+    return hipGetLastError();
+}
+
+size_t conv_backward_workspace_bytes(const ConvShape& c) {
+    const int64_t rows = c.C_out * (c.C_in / c.groups) * (c.K * c.K + 1);
+    return (size_t)(rows * conv_chunks(c)) * sizeof(double);
+}
+
+hipError_t launch_conv_backward(const float* go, const float* in, const float* w, float* gx,
+                                float* gw, float* gb, const ConvShape& c, bool accumulate_dx,
+                                void* ws, hipStream_t s) {
+    if (gx) {
+        const int64_t total = c.N * c.C_in * c.H * c.W;
+        if (accumulate_dx)
+            k_conv_dx<true><<<blocks_for(total), kThreads, 0, s>>>(go, w, gx, c);
+        else
+            k_conv_dx<false><<<blocks_for(total), kThreads, 0, s>>>(go, w, gx, c);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (gw || gb) {
+        const int64_t chunks = conv_chunks(c);
+        const int64_t cig = c.C_in / c.groups;
+        double* part = static_cast<double*>(ws);
+        dim3 grid((unsigned)(c.C_out * cig * (c.K * c.K + 1)), (unsigned)chunks);
+        k_conv_dw<<<grid, kThreads, 0, s>>>(go, in, part, c, chunks);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const int64_t rows = c.C_out * cig * (c.K * c.K + 1);
+        k_conv_dw_finish<<<blocks_for(rows), kThreads, 0, s>>>(part, gw, gb, c, chunks);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_sigmoid_forward(const float* x, float* y, int64_t n, hipStream_t s) {
+    k_sigmoid_fwd<<<blocks_for(n), kThreads, 0, s>>>(x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_sigmoid_backward(const float* gy, const float* y, float* gx, int64_t n,
+                                   hipStream_t s) {
+    k_sigmoid_bwd<<<blocks_for(n), kThreads, 0, s>>>(gy, y, gx, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_mul_broadcast_forward(const float* a, const float* b, float* y, int64_t rows,
+                                        int64_t HW, hipStream_t s) {
+    k_mul_bcast_fwd<<<blocks_for(rows * HW), kThreads, 0, s>>>(a, b, y, rows, HW);
+    return hipGetLastError();
+}
+
+hipError_t launch_mul_broadcast_backward(const float* gy, const float* a, const float* b,
+                                         float* ga, float* gb, int64_t rows, int64_t HW,
+                                         hipStream_t s) {
+    k_mul_bcast_bwd<<<(unsigned)rows, kThreads, 0, s>>>(gy, a, b, ga, gb, HW);
+    return hipGetLastError();
+}
+
+hipError_t launch_convex_forward(const float* g, const float* a, const float* b, float* y,
+                                 int64_t n, hipStream_t s) {
+    k_convex_fwd<<<blocks_for(n), kThreads, 0, s>>>(g, a, b, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_convex_backward(const float* gy, const float* g, const float* a,
+                                  const float* b, float* gg, float* ga, float* gb, int64_t n,
+                                  hipStream_t s) {
+    k_convex_bwd<<<blocks_for(n), kThreads, 0, s>>>(gy, g, a, b, gg, ga, gb, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_avg_pool_forward(const float* in, float* out, int64_t rows, int64_t HW,
+                                   hipStream_t s) {
+    k_avg_pool_fwd<<<(unsigned)rows, kThreads, 0, s>>>(in, out, HW);
+    return hipGetLastError();
+}
+
+hipError_t launch_avg_pool_backward(const float* go, float* gi, int64_t rows, int64_t HW,
+                                    hipStream_t s) {
+    k_avg_pool_bwd<<<blocks_for(rows * HW), kThreads, 0, s>>>(go, gi, rows, HW);
+    return hipGetLastError();
+}
+
+hipError_t launch_upsample_forward(const float* in, float* out, int64_t rows, int64_t H_in,
+                                   int64_t W_in, int64_t H_out, int64_t W_out, hipStream_t s) {
+    const float sh = (float)H_in / (float)H_out, sw = (float)W_in / (float)W_out;
+    k_upsample_fwd<<<blocks_for(rows * H_out * W_out), kThreads, 0, s>>>(in, out, rows, H_in,
+                                                                          W_in, H_out, W_out,
+                                                                          sh, sw);
+    return hipGetLastError();
+}
+
+hipError_t launch_upsample_backward(const float* go, float* gi, int64_t rows, int64_t H_in,
+                                    int64_t W_in, int64_t H_out, int64_t W_out, hipStream_t s) {
+    const float sh = (float)H_in / (float)H_out, sw = (float)W_in / (float)W_out;
+    k_upsample_bwd<<<blocks_for(rows * H_in * W_in), kThreads, 0, s>>>(go, gi, rows, H_in,
+                                                                        W_in, H_out, W_out, sh,
+                                                                        sw);
+    return hipGetLastError();
+}
+
+hipError_t launch_pixel_shuffle(const float* in, float* out, int64_t N, int64_t C_in,
+                                int64_t H_in, int64_t W_in, int64_t r, bool backward,
+                                hipStream_t s) {
+    const int64_t C_out = C_in / (r * r);
+    const int64_t total = N * C_out * H_in * r * W_in * r;
+    if (backward)
+        k_pixel_shuffle<true><<<blocks_for(total), kThreads, 0, s>>>(in, out, N, C_out, H_in,
+                                                                      W_in, r);
+    else
+        k_pixel_shuffle<false><<<blocks_for(total), kThreads, 0, s>>>(in, out, N, C_out, H_in,
+                                                                       W_in, r);
+    return hipGetLastError();
+}
+
+hipError_t launch_pad_forward(const float* in, float* out, int64_t rows, int64_t H, int64_t W,
+                              int64_t ph, int64_t pw, bool reflect, hipStream_t s) {
+    const int64_t Hp = H + ph, Wp = W + pw;
+    k_pad_fwd<<<blocks_for(rows * Hp * Wp), kThreads, 0, s>>>(in, out, rows, H, W, Hp, Wp,
+                                                                reflect);
+    return hipGetLastError();
+}
+
+hipError_t launch_pad_backward(const float* go, float* gi, int64_t rows, int64_t H, int64_t W,
+                               int64_t ph, int64_t pw, bool reflect, hipStream_t s) {
+    const int64_t Hp = H + ph, Wp = W + pw;
+    k_pad_bwd<<<blocks_for(rows * H * W), kThreads, 0, s>>>(go, gi, rows, H, W, Hp, Wp,
+                                                             reflect);
+    return hipGetLastError();
+}
+
+hipError_t launch_crop(const float* in, float* out, int64_t rows, int64_t Hp, int64_t Wp,
+                       int64_t H, int64_t W, bool backward, hipStream_t s) {
+    if (backward)
+        k_crop<true><<<blocks_for(rows * Hp * Wp), kThreads, 0, s>>>(in, out, rows, Hp, Wp, H,
+                                                                      W);
+    else
+        k_crop<false><<<blocks_for(rows * H * W), kThreads, 0, s>>>(in, out, rows, Hp, Wp, H,
+                                                                     W);
+    return hipGetLastError();
+}
+
+size_t loss_sums_workspace_bytes(int64_t n) {
+    return (size_t)(4 * blocks_for(n, kThreads, kLossBlocks) + 4) * sizeof(double);
+}
+
+hipError_t launch_loss_sums(const float* z, const float* y, int64_t n, float pos_weight,
+                            double* out, void* ws, hipStream_t s) {
+    const int nb = blocks_for(n, kThreads, kLossBlocks);
+    double* part = static_cast<double*>(ws);
+    k_loss_sums<<<nb, kThreads, 0, s>>>(z, y, n, pos_weight, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    k_loss_finish<<<1, kThreads, 0, s>>>(part, nb, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_dice_bce_backward(const float* z, const float* y, float* gz, int64_t n,
+                                    float go, float w, float bw, float dw, float pos_weight,
+                                    float smooth, float inter, float sum_p, float sum_y,
+                                    hipStream_t s) {
+    const float scale_bce = bw > 0.0f ? (go * w * bw) / (float)n : 0.0f;
+    const float scale_dice = dw > 0.0f ? go * w * dw : 0.0f;
+    const float denom = sum_p + sum_y + smooth;
+    const float numer = 2.0f * inter + smooth;
+    k_dice_bce_bwd<<<blocks_for(n), kThreads, 0, s>>>(z, y, gz, n, scale_bce, scale_dice,
+                                                       pos_weight, denom, numer);
+    return hipGetLastError();
+}
+
+hipError_t launch_sigmoid_threshold(const float* z, float* p, uint8_t* mask, int64_t n,
+                                    float threshold, hipStream_t s) {
+    k_sigmoid_threshold<<<blocks_for(n), kThreads, 0, s>>>(z, p, mask, n, threshold);
+    return hipGetLastError();
+}
+
+size_t multi_norm_workspace_bytes() { return (size_t)(kMultiBlocks + 1) * sizeof(double); }
+
+hipError_t launch_multi_norm_sq(const float* const* t, const int64_t* numel, int n_tensors,
+                                double* out, void* ws, hipStream_t s) {
+    double* part = static_cast<double*>(ws);
+    k_multi_norm_sq<<<kMultiBlocks, kThreads, 0, s>>>(t, numel, n_tensors, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    k_multi_norm_finish<<<1, 64, 0, s>>>(part, kMultiBlocks, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_multi_scale(float* const* t, const int64_t* numel, int n_tensors, float scale,
+                              hipStream_t s) {
+    k_multi_scale<<<kMultiBlocks, kThreads, 0, s>>>(t, numel, n_tensors, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_adamw_multi(float* const* p, const float* const* g, float* const* m,
+                              float* const* v, const int64_t* numel, int n_tensors, float lr,
+                              float beta1, float beta2, float eps, float wd, float step_size,
+                              float sqrt_bc2, hipStream_t s) {
+    k_adamw_multi<<<kMultiBlocks, kThreads, 0, s>>>(p, g, m, v, numel, n_tensors, lr, beta1,
+                                                     beta2, eps, wd, step_size, sqrt_bc2);
+    return hipGetLastError();
+}
+
+}  // namespace soar::ops

@@ -15,6 +15,11 @@
 // These layers run on device tensors only; there is no host fallback (a
 // host tensor is moved to the device on entry, as the reference's layers
 // do when a parameter lives on the device).
+//
+// Also here: the other layers and tensor helpers of the SOAR blocks
+// (layers.hpp:96-159, blocks.hpp:10-14): Sigmoid, PixelShuffle, Upsample
+// (bilinear), AdaptiveAvgPool2d, mul_tensors (channel broadcast),
+// convex_combination, concat_channels and resize_bilinear.
 #pragma once
 
 #include <cstdint>
@@ -41,11 +46,18 @@ inline int autopad(int k, int p = -1, int d = 1) {
     return p < 0 ? k / 2 : p;
 }
 
+// Module base (module.hpp:15-137): parameters and submodules live in
+// name-sorted maps, so parameters() / named_parameters() list a module's own
+// parameters by name, then each submodule's by submodule name, recursively,
+// in the reference's order (which is also the order of a .soar file).
 class Module {
 public:
     explicit Module(std::string name) : name_(std::move(name)) {}
     virtual ~Module() = default;
-    virtual TensorPtr forward(const TensorPtr& input) = 0;
+    // Single- and multi-input forward; each defaults to the other
+    // (module.hpp:21-29), so a module overrides at least one.
+    virtual TensorPtr forward(const TensorPtr& input);
+    virtual TensorPtr forward(const std::vector<TensorPtr>& inputs);
 
     void register_parameter(const std::string& name, TensorPtr p);
     // Parameters of a submodule are named "<name>.<parameter>"
@@ -58,17 +70,22 @@ public:
     // arena: do this before freeze_static_parameters()).
     void to_device();
     void zero_grad();
+    virtual void train(bool mode = true);
+    void eval() { train(false); }
+    [[nodiscard]] bool is_training() const noexcept { return training_; }
     [[nodiscard]] const std::string& name() const noexcept { return name_; }
 
 private:
     std::string name_;
-    std::vector<std::pair<std::string, TensorPtr>> params_;
-    std::vector<std::pair<std::string, std::shared_ptr<Module>>> subs_;
+    bool training_ = true;
+    std::map<std::string, TensorPtr> params_;
+    std::map<std::string, std::shared_ptr<Module>> subs_;
 };
 
 class GroupNorm : public Module {
 public:
     GroupNorm(size_t num_groups, size_t num_channels, float eps = 1e-5f, bool affine = true);
+    using Module::forward;
     TensorPtr forward(const TensorPtr& input) override;
 
     [[nodiscard]] size_t num_groups() const noexcept { return num_groups_; }
@@ -95,6 +112,7 @@ protected:
 class SiLU : public Module {
 public:
     SiLU() : Module("SiLU") {}
+    using Module::forward;
     TensorPtr forward(const TensorPtr& input) override;
 };
 
@@ -103,6 +121,7 @@ class GNSiLU : public GroupNorm {
 public:
     GNSiLU(size_t num_groups, size_t num_channels, float eps = 1e-5f, bool affine = true,
            bool residual = false);
+    using Module::forward;
     TensorPtr forward(const TensorPtr& input) override;
     [[nodiscard]] bool residual() const noexcept { return residual_; }
 
@@ -114,25 +133,33 @@ private:
 // dilation = 1, groups = 1, bias = true) of layers.hpp:24-58: weight
 // [out][in/groups][k][k] with Kaiming-uniform initialisation
 // U(-1/sqrt(fan_in), 1/sqrt(fan_in)) (layers.cpp:303-317; drawn from a
-// seeded generator, where the reference seeds from std::random_device),
-// bias zeros.  Runs on the device for the two forms of the SOAR blocks:
-// pointwise (k = 1, stride 1, no padding, groups 1) and depthwise (groups =
-// in = out); other forms throw InvalidArgument.  Input [C,H,W] or
-// [N,C,H,W]; the output size is (H + 2p - d(k-1) - 1)/s + 1
+// seeded generator, where the reference seeds from std::random_device:
+// seed 0 takes the next seed of a process-wide sequence started by
+// set_init_seed, so layers of one model differ and a model is reproducible),
+// bias zeros.  Three device paths, chosen as the reference chooses its
+// kernels (layers.cpp:59-72): pointwise (k = 1, stride 1, no padding,
+// groups 1) on the MFMA kernel, depthwise (groups = in = out) on the tiled
+// depthwise kernels, anything else on the general grouped convolution.
+// Input [C,H,W] or [N,C,H,W]; the output size is (H + 2p - d(k-1) - 1)/s + 1
 // (layers.cpp:330-332).
+// Restarts the sequence of initialisation seeds of Conv2d(seed = 0).
+void set_init_seed(uint64_t seed);
+
 class Conv2d : public Module {
 public:
     Conv2d(size_t in_channels, size_t out_channels, size_t kernel_size, size_t stride = 1,
            int padding = -1, size_t dilation = 1, size_t groups = 1, bool bias = true,
-           uint64_t seed = 0x50a4c0de);
+           uint64_t seed = 0);
+    using Module::forward;
     TensorPtr forward(const TensorPtr& input) override;
 
     [[nodiscard]] bool pointwise() const noexcept {
         return groups_ == 1 && kernel_ == 1 && stride_ == 1 && padding_ == 0;
     }
     [[nodiscard]] bool depthwise() const noexcept {
-        return groups_ == in_ && in_ == out_;
+        return !pointwise() && groups_ == in_ && in_ == out_;
     }
+    [[nodiscard]] size_t groups() const noexcept { return groups_; }
     [[nodiscard]] TensorPtr weight() const { return weight_; }
     [[nodiscard]] TensorPtr bias() const { return bias_; }
     [[nodiscard]] size_t in_channels() const noexcept { return in_; }
@@ -158,6 +185,7 @@ class CBA : public Module {
 public:
     CBA(size_t c1, size_t c2, size_t k = 1, size_t s = 1, int p = -1, size_t d = 1,
         size_t g = 1, bool act = true);
+    using Module::forward;
     TensorPtr forward(const TensorPtr& input) override;
 
     [[nodiscard]] std::shared_ptr<Conv2d> conv() const { return conv_; }
@@ -172,5 +200,57 @@ private:
 
 // y = a + b (blocks.cpp:39-72); shapes must match (ShapeError otherwise).
 TensorPtr add_tensors(const TensorPtr& a, const TensorPtr& b);
+
+// y = 1 / (1 + exp(-x)) (layers.cpp:807-870).
+class Sigmoid : public Module {
+public:
+    Sigmoid() : Module("Sigmoid") {}
+    using Module::forward;
+    TensorPtr forward(const TensorPtr& input) override;
+};
+
+// [C*r*r, H, W] -> [C, H*r, W*r] (layers.cpp:875-989).
+class PixelShuffle : public Module {
+public:
+    explicit PixelShuffle(size_t upscale_factor = 2)
+        : Module("PixelShuffle"), r_(upscale_factor) {}
+    using Module::forward;
+    TensorPtr forward(const TensorPtr& input) override;
+    [[nodiscard]] size_t upscale_factor() const noexcept { return r_; }
+
+private:
+    size_t r_;
+};
+
+// Bilinear resize to round(H*scale) x round(W*scale), half-pixel centres
+// (layers.cpp:991-1150).
+class Upsample : public Module {
+public:
+    explicit Upsample(float scale_factor = 2.0f) : Module("Upsample"), scale_(scale_factor) {}
+    using Module::forward;
+    TensorPtr forward(const TensorPtr& input) override;
+
+private:
+    float scale_;
+};
+
+// [C, H, W] -> [C, 1, 1] plane means (layers.cpp:1274-1345).
+class AdaptiveAvgPool2d : public Module {
+public:
+    AdaptiveAvgPool2d() : Module("AdaptiveAvgPool2d") {}
+    using Module::forward;
+    TensorPtr forward(const TensorPtr& input) override;
+};
+
+// a [C,H,W] times b [C,1,1] (or [C]) per channel (blocks.cpp:148-212; the
+// elementwise branch of the reference's CPU path is not used by the model).
+TensorPtr mul_tensors(const TensorPtr& a, const TensorPtr& b);
+// g*a + (1-g)*b (blocks.cpp:280-320).
+TensorPtr convex_combination(const TensorPtr& g, const TensorPtr& a, const TensorPtr& b);
+// Channel concatenation of [C_i, H, W] tensors (blocks.cpp:363-418).
+TensorPtr concat_channels(const std::vector<TensorPtr>& tensors);
+// Bilinear resize to target_h x target_w through Upsample(target_h / H)
+// (blocks.cpp:420-427); the input itself when the size already matches.
+TensorPtr resize_bilinear(const TensorPtr& input, size_t target_h, size_t target_w);
 
 }  // namespace soar::nn

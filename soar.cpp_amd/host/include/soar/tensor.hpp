@@ -57,6 +57,8 @@ public:
     void to_cuda();
     // Copy of the values on the host (synchronous).
     [[nodiscard]] std::vector<float> to_host() const;
+    // Overwrites the values from numel() host floats (device or host).
+    void copy_from_host(const float* src);
     [[nodiscard]] TensorPtr clone() const;
     void zero_();
     void fill_(float value);

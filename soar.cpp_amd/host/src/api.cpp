@@ -1,0 +1,341 @@
+// The model-level C-ABI of include/soar_api.h: a handle around SOARModel,
+// Trainer and Predictor with two device arenas (parameters + optimizer
+// state; per-call activations).  Mirrors src/api/c_api.cpp:11-154 of the
+// reference: exceptions become -1 / NULL; the message is kept for
+// soar_api_last_error().
+#include <algorithm>
+#include <cstring>
+#include <memory>
+#include <string>
+
+#include "soar/autograd.hpp"
+#include "soar/engine.hpp"
+#include "soar/memory.hpp"
+#include "soar/model.hpp"
+#include "soar_api.h"
+
+namespace {
+
+thread_local std::string g_api_err;
+
+using soar::TensorPtr;
+using soar::memory::ArenaScope;
+using soar::memory::DeviceArena;
+
+constexpr size_t kAlign = 256;
+constexpr size_t kMinActivationBytes = size_t(64) << 20;
+
+size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+
+struct SoarModelHandle {
+    std::unique_ptr<DeviceArena> params;
+    std::unique_ptr<DeviceArena> acts;
+    size_t act_peak = 0;
+    std::shared_ptr<soar::nn::SOARModel> model;
+    std::unique_ptr<soar::engine::Trainer> trainer;
+    soar::engine::StepMetrics last;
+    std::vector<std::pair<std::string, TensorPtr>> named;
+};
+
+SoarModelHandle* H(void* h) { return static_cast<SoarModelHandle*>(h); }
+
+// Activation bytes for one training step on an H x W image: about 2 KiB
+// per input pixel covers the Nano..Large widths at the sizes tried; a
+// step that needs more grows the arena and runs again.
+size_t activation_estimate(int64_t h, int64_t w) {
+    const size_t px = (size_t)std::max<int64_t>(h, 32) * (size_t)std::max<int64_t>(w, 32);
+    return std::max(kMinActivationBytes, align_up(px * 2048));
+}
+
+void ensure_acts(SoarModelHandle* s, size_t need) {
+    if (s->acts && s->acts->slab().total_capacity() >= need) return;
+    s->acts.reset();
+    s->acts = std::make_unique<DeviceArena>(need, kAlign);
+}
+
+// Runs fn() with the activation arena reset and current; on OutOfMemory
+// the arena doubles and fn runs again (at most four times).  `undo` is
+// called before a retry (e.g. to clear partially accumulated gradients).
+template <typename F, typename U>
+void with_acts(SoarModelHandle* s, int64_t h, int64_t w, F&& fn, U&& undo) {
+    ensure_acts(s, activation_estimate(h, w));
+    for (int attempt = 0;; ++attempt) {
+        try {
+            ArenaScope scope(*s->acts);
+            s->acts->reset_dynamic_allocations();
+            fn();
+            s->act_peak = std::max(s->act_peak, s->acts->slab().current_offset());
+            return;
+        } catch (const soar::OutOfMemory&) {
+            if (attempt >= 3) throw;
+            undo();
+            ensure_acts(s, s->acts->slab().total_capacity() * 2);
+        }
+    }
+}
+
+void check_image(int c, int h, int w) {
+    if (c <= 0 || h <= 0 || w <= 0)
+        throw soar::InvalidArgument("image dimensions must be positive");
+}
+
+float* metrics_out(const soar::engine::StepMetrics& m, float* out) {
+    if (out) {
+        out[0] = m.loss;
+        out[1] = m.bce_loss;
+        out[2] = m.dice_loss;
+        out[3] = m.dice_score;
+        out[4] = m.iou_score;
+        out[5] = m.lr;
+        out[6] = m.grad_norm;
+    }
+    return out;
+}
+
+template <typename F>
+int guarded(F&& fn) {
+    try {
+        fn();
+        g_api_err.clear();
+        return 0;
+    } catch (const std::exception& e) {
+        g_api_err = e.what();
+        return -1;
+    } catch (...) {
+        g_api_err = "unknown error";
+        return -1;
+    }
+}
+
+void* create(int in_channels, int num_classes, int variant, bool seeded, uint64_t seed) {
+    try {
+        if (in_channels <= 0 || num_classes <= 0 || variant < 0 || variant > 4)
+            throw soar::InvalidArgument("soar_create_model: invalid channels or variant");
+        auto h = std::make_unique<SoarModelHandle>();
+        if (seeded) soar::nn::set_init_seed(seed);
+        h->model = std::make_shared<soar::nn::SOARModel>(
+            (size_t)in_channels, (size_t)num_classes,
+            static_cast<soar::nn::ModelVariant>(variant));
+        h->named = h->model->named_parameters();
+        // parameter, gradient, two moments per tensor, plus the optimizer's
+        // tables and the norm workspace
+        size_t bytes = size_t(1) << 20;
+        for (auto& [n, p] : h->named) bytes += 4 * align_up(p->bytes()) ;
+        bytes += align_up(5 * h->named.size() * sizeof(void*)) + (size_t(64) << 10);
+        h->params = std::make_unique<DeviceArena>(bytes, kAlign);
+        {
+            ArenaScope scope(*h->params);
+            h->model->to_device();
+            soar::optim::AdamWOptions opts;
+            opts.lr = 1e-3f;
+            auto opt = std::make_unique<soar::optim::AdamW>(h->model->parameters(), opts);
+            h->trainer = std::make_unique<soar::engine::Trainer>(
+                h->model, soar::losses::CompositeLoss(0.5f, 0.5f), std::move(opt));
+        }
+        g_api_err.clear();
+        return h.release();
+    } catch (const std::exception& e) {
+        g_api_err = e.what();
+        return nullptr;
+    } catch (...) {
+        g_api_err = "unknown error";
+        return nullptr;
+    }
+}
+
+TensorPtr host_image(const float* data, int64_t c, int64_t h, int64_t w) {
+    return soar::Tensor::from_blob(data, {c, h, w}, false, true);
+}
+
+}  // namespace
+
+extern "C" {
+
+SOAR_API const char* soar_api_last_error(void) { return g_api_err.c_str(); }
+
+SOAR_API void* soar_create_model(int in_channels, int num_classes, int variant) {
+    return create(in_channels, num_classes, variant, false, 0);
+}
+
+SOAR_API void* soar_create_model_seeded(int in_channels, int num_classes, int variant,
+                                        uint64_t seed) {
+    return create(in_channels, num_classes, variant, true, seed);
+}
+
+SOAR_API void soar_destroy_model(void* handle) {
+    if (!handle) return;
+    auto* s = H(handle);
+    // the model and optimizer first: their tensors point into the arenas
+    s->trainer.reset();
+    s->named.clear();
+    s->model.reset();
+    delete s;
+}
+
+SOAR_API size_t soar_get_parameter_count(void* handle) {
+    return handle ? H(handle)->model->parameter_count() : 0;
+}
+
+SOAR_API int soar_save_weights(void* handle, const char* path) {
+    if (!handle || !path) return -1;
+    return guarded([&] { H(handle)->model->save_weights(path); });
+}
+
+SOAR_API int soar_load_weights(void* handle, const char* path) {
+    if (!handle || !path) return -1;
+    return guarded([&] { H(handle)->model->load_weights(path); });
+}
+
+SOAR_API int soar_train_step(void* handle, const float* image_data, const float* mask_data,
+                             int channels, int height, int width, float learning_rate,
+                             float* out_loss, float* out_dice, float* out_iou) {
+    if (!handle || !image_data || !mask_data) return -1;
+    auto* s = H(handle);
+    return guarded([&] {
+        check_image(channels, height, width);
+        s->trainer->optimizer().set_lr(learning_rate);
+        with_acts(
+            s, height, width,
+            [&] {
+                TensorPtr img = host_image(image_data, channels, height, width);
+                TensorPtr msk = host_image(mask_data, 1, height, width);
+                s->last = s->trainer->train_step(img, msk);
+            },
+            [&] { s->trainer->optimizer().zero_grad(); });
+        if (out_loss) *out_loss = s->last.loss;
+        if (out_dice) *out_dice = s->last.dice_score;
+        if (out_iou) *out_iou = s->last.iou_score;
+    });
+}
+
+SOAR_API int soar_predict(void* handle, const float* image_data, int channels, int height,
+                          int width, float threshold, float* out_probs, uint8_t* out_mask,
+                          char* out_rle, size_t max_rle_len) {
+    if (!handle || !image_data) return -1;
+    auto* s = H(handle);
+    return guarded([&] {
+        check_image(channels, height, width);
+        soar::engine::PredictionResult r;
+        with_acts(
+            s, height, width,
+            [&] {
+                soar::engine::Predictor p(s->model, threshold);
+                r = p.predict(host_image(image_data, channels, height, width));
+            },
+            [] {});
+        const size_t n = r.height * r.width;
+        if (out_probs) std::memcpy(out_probs, r.probabilities.data(), n * sizeof(float));
+        if (out_mask) std::memcpy(out_mask, r.binary_mask.data(), n);
+        if (out_rle && max_rle_len > 0) {
+            std::strncpy(out_rle, r.rle_string.c_str(), max_rle_len - 1);
+            out_rle[max_rle_len - 1] = '\0';
+        }
+    });
+}
+
+SOAR_API int soar_encode_rle(const uint8_t* mask, size_t height, size_t width, char* out_rle,
+                             size_t max_rle_len) {
+    if (!mask || !out_rle || max_rle_len == 0) return -1;
+    return guarded([&] {
+        const std::string rle = soar::engine::Predictor::encode_rle(mask, height, width);
+        std::strncpy(out_rle, rle.c_str(), max_rle_len - 1);
+        out_rle[max_rle_len - 1] = '\0';
+    });
+}
+
+SOAR_API int soar_model_num_tensors(void* handle) {
+    return handle ? (int)H(handle)->named.size() : -1;
+}
+
+SOAR_API int soar_model_tensor_info(void* handle, int index, char* name, size_t name_len,
+                                    int* ndim, int64_t shape[4]) {
+    if (!handle) return -1;
+    auto* s = H(handle);
+    if (index < 0 || (size_t)index >= s->named.size()) return -1;
+    const auto& [n, p] = s->named[(size_t)index];
+    if (name && name_len > 0) {
+        std::strncpy(name, n.c_str(), name_len - 1);
+        name[name_len - 1] = '\0';
+    }
+    if (ndim) *ndim = (int)p->ndim();
+    if (shape)
+        for (int d = 0; d < 4; ++d) shape[d] = d < p->ndim() ? p->dim(d) : 1;
+    return 0;
+}
+
+SOAR_API int soar_model_read_tensor(void* handle, int index, int what, float* out) {
+    if (!handle || !out || (what != 0 && what != 1)) return -1;
+    auto* s = H(handle);
+    if (index < 0 || (size_t)index >= s->named.size()) return -1;
+    return guarded([&] {
+        const TensorPtr& p = s->named[(size_t)index].second;
+        const TensorPtr t = what == 0 ? p : p->grad();
+        if (!t) throw soar::InvalidArgument("tensor has no gradient");
+        const std::vector<float> v = t->to_host();
+        std::memcpy(out, v.data(), v.size() * sizeof(float));
+    });
+}
+
+SOAR_API int soar_model_forward_backward(void* handle, const float* image_data,
+                                         const float* mask_data, int channels, int height,
+                                         int width, float* out_metrics) {
+    if (!handle || !image_data || !mask_data) return -1;
+    auto* s = H(handle);
+    return guarded([&] {
+        check_image(channels, height, width);
+        soar::engine::StepMetrics m;
+        with_acts(
+            s, height, width,
+            [&] {
+                s->trainer->optimizer().zero_grad();
+                s->model->train(true);
+                TensorPtr img = host_image(image_data, channels, height, width);
+                TensorPtr msk = host_image(mask_data, 1, height, width);
+                m = s->trainer->forward_backward(img, msk, 1.0f);
+            },
+            [&] { s->trainer->optimizer().zero_grad(); });
+        metrics_out(m, out_metrics);
+    });
+}
+
+SOAR_API int soar_model_zero_grad(void* handle) {
+    if (!handle) return -1;
+    return guarded([&] { H(handle)->trainer->optimizer().zero_grad(); });
+}
+
+SOAR_API int soar_model_last_metrics(void* handle, float* out_metrics) {
+    if (!handle || !out_metrics) return -1;
+    metrics_out(H(handle)->last, out_metrics);
+    return 0;
+}
+
+SOAR_API int soar_model_forward(void* handle, const float* image_data, int channels, int height,
+                                int width, float* out_logits) {
+    if (!handle || !image_data || !out_logits) return -1;
+    auto* s = H(handle);
+    return guarded([&] {
+        check_image(channels, height, width);
+        with_acts(
+            s, height, width,
+            [&] {
+                soar::autograd::NoGradGuard guard;
+                s->model->eval();
+                TensorPtr out = s->model->forward(host_image(image_data, channels, height, width));
+                const std::vector<float> v = out->to_host();
+                std::memcpy(out_logits, v.data(), v.size() * sizeof(float));
+            },
+            [] {});
+    });
+}
+
+SOAR_API int soar_model_memory_info(void* handle, size_t* param_bytes,
+                                    size_t* activation_capacity, size_t* activation_peak) {
+    if (!handle) return -1;
+    auto* s = H(handle);
+    if (param_bytes) *param_bytes = s->params->slab().current_offset();
+    if (activation_capacity) *activation_capacity = s->acts ? s->acts->slab().total_capacity() : 0;
+    if (activation_peak) *activation_peak = s->act_peak;
+    return 0;
+}
+
+}  // extern "C"

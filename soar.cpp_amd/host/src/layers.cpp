@@ -1,0 +1,396 @@
+// Sigmoid / PixelShuffle / Upsample / AdaptiveAvgPool2d and the tensor
+// helpers of the SOAR blocks (mul_tensors, convex_combination,
+// concat_channels, resize_bilinear) on libsoar_gn.so.
+//
+// Structure follows src/nn/layers.cpp:807-1345 and src/nn/blocks.cpp:
+// 75-427 of the reference: each op allocates its output on the device,
+// runs one operator of include/soar_ops.h, and records a node when the
+// output requires grad and grad mode is on.  Gradients of the operators
+// are accumulated into zero-filled buffers, as the reference's kernels do.
+// Inputs are [C,H,W] (the reference's layout) or [N,C,H,W].
+#include <algorithm>
+#include <cmath>
+
+#include "soar/autograd.hpp"
+#include "soar/kernels.hpp"
+#include "soar/nn.hpp"
+#include "soar_gn.h"
+#include "soar_ops.h"
+
+namespace soar::nn {
+
+using autograd::GradMode;
+using hip::kernels::check;
+
+namespace {
+
+struct Planes {
+    int64_t rows, H, W;
+};
+
+Planes planes_of(const TensorPtr& t, const char* what) {
+    if (t->ndim() == 3) return {t->dim(0), t->dim(1), t->dim(2)};
+    if (t->ndim() == 4) return {t->dim(0) * t->dim(1), t->dim(2), t->dim(3)};
+    throw ShapeError(std::string(what) + " expects [C,H,W] or [N,C,H,W], got " +
+                     to_string(t->shape()));
+}
+
+void to_dev(const TensorPtr& t) {
+    if (t && !t->is_cuda()) t->to_cuda();
+}
+
+bool wants(const TensorPtr& t) { return t && t->requires_grad(); }
+
+TensorPtr zeros_like_dev(const TensorPtr& t) { return Tensor::zeros(t->shape(), false, true); }
+
+// ---- nodes ------------------------------------------------------------------
+struct SigmoidNode : autograd::AutogradNode {
+    TensorPtr input, output;
+    std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
+        if (input && input->grad_fn()) return {input->grad_fn()};
+        return {};
+    }
+    void backward(const TensorPtr& go) override {
+        if (!wants(input)) return;
+        to_dev(go);
+        TensorPtr gx = zeros_like_dev(input);
+        check(soar_sigmoid_backward(go->cuda_data(), output->cuda_data(), gx->cuda_data(),
+                                    (size_t)input->numel(), nullptr),
+              "sigmoid backward");
+        propagate_grad(input, std::move(gx));
+    }
+    void release_variables() override { input = output = nullptr; }
+};
+
+struct PixelShuffleNode : autograd::AutogradNode {
+    TensorPtr input;
+    int64_t r = 2;
+    std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
+        if (input && input->grad_fn()) return {input->grad_fn()};
+        return {};
+    }
+    void backward(const TensorPtr& go) override {
+        if (!wants(input)) return;
+        to_dev(go);
+        const Planes p = planes_of(input, "PixelShuffle");
+        TensorPtr gx = zeros_like_dev(input);
+        check(soar_pixel_shuffle_backward(go->cuda_data(), gx->cuda_data(), (size_t)p.rows,
+                                          (size_t)p.H, (size_t)p.W, (size_t)r, nullptr),
+              "pixel shuffle backward");
+        propagate_grad(input, std::move(gx));
+    }
+    void release_variables() override { input = nullptr; }
+};
+
+struct UpsampleNode : autograd::AutogradNode {
+    TensorPtr input;
+    int64_t H_out = 0, W_out = 0;
+    std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
+        if (input && input->grad_fn()) return {input->grad_fn()};
+        return {};
+    }
+    void backward(const TensorPtr& go) override {
+        if (!wants(input)) return;
+        to_dev(go);
+        const Planes p = planes_of(input, "Upsample");
+        TensorPtr gx = zeros_like_dev(input);
+        check(soar_upsample_bilinear_backward(go->cuda_data(), gx->cuda_data(), (size_t)p.rows,
+                                              (size_t)p.H, (size_t)p.W, (size_t)H_out,
+                                              (size_t)W_out, nullptr),
+              "upsample backward");
+        propagate_grad(input, std::move(gx));
+    }
+    void release_variables() override { input = nullptr; }
+};
+
+struct AvgPoolNode : autograd::AutogradNode {
+    TensorPtr input;
+    std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
+        if (input && input->grad_fn()) return {input->grad_fn()};
+        return {};
+    }
+    void backward(const TensorPtr& go) override {
+        if (!wants(input)) return;
+        to_dev(go);
+        const Planes p = planes_of(input, "AdaptiveAvgPool2d");
+        TensorPtr gx = zeros_like_dev(input);
+        check(soar_global_avg_pool_backward(go->cuda_data(), gx->cuda_data(), (size_t)p.rows,
+                                            (size_t)(p.H * p.W), nullptr),
+              "average pool backward");
+        propagate_grad(input, std::move(gx));
+    }
+    void release_variables() override { input = nullptr; }
+};
+
+struct MulBroadcastNode : autograd::AutogradNode {
+    TensorPtr a, b;
+    std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
+        std::vector<std::shared_ptr<AutogradNode>> r;
+        if (a && a->grad_fn()) r.push_back(a->grad_fn());
+        if (b && b->grad_fn()) r.push_back(b->grad_fn());
+        return r;
+    }
+    void backward(const TensorPtr& go) override {
+        const bool wa = wants(a), wb = wants(b);
+        if (!wa && !wb) return;
+        to_dev(go);
+        const Planes p = planes_of(a, "mul_tensors");
+        TensorPtr ga = wa ? zeros_like_dev(a) : nullptr;
+        TensorPtr gb = wb ? zeros_like_dev(b) : nullptr;
+        check(soar_mul_broadcast_backward(go->cuda_data(), a->cuda_data(), b->cuda_data(),
+                                          ga ? ga->cuda_data() : nullptr,
+                                          gb ? gb->cuda_data() : nullptr, (size_t)p.rows,
+                                          (size_t)(p.H * p.W), nullptr),
+              "mul_broadcast backward");
+        if (ga) propagate_grad(a, std::move(ga));
+        if (gb) propagate_grad(b, std::move(gb));
+    }
+    void release_variables() override { a = b = nullptr; }
+};
+
+struct ConvexNode : autograd::AutogradNode {
+    TensorPtr g, a, b;
+    std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
+        std::vector<std::shared_ptr<AutogradNode>> r;
+        for (const auto& t : {g, a, b})
+            if (t && t->grad_fn()) r.push_back(t->grad_fn());
+        return r;
+    }
+    void backward(const TensorPtr& go) override {
+        const bool wg = wants(g), wa = wants(a), wb = wants(b);
+        if (!wg && !wa && !wb) return;
+        to_dev(go);
+        TensorPtr gg = wg ? zeros_like_dev(g) : nullptr;
+        TensorPtr ga = wa ? zeros_like_dev(a) : nullptr;
+        TensorPtr gb = wb ? zeros_like_dev(b) : nullptr;
+        check(soar_convex_combination_backward(
+                  go->cuda_data(), g->cuda_data(), a->cuda_data(), b->cuda_data(),
+                  gg ? gg->cuda_data() : nullptr, ga ? ga->cuda_data() : nullptr,
+                  gb ? gb->cuda_data() : nullptr, (size_t)a->numel(), nullptr),
+              "convex combination backward");
+        // the reference's order (blocks.cpp:258-262): a, b, then g
+        if (ga) propagate_grad(a, std::move(ga));
+        if (gb) propagate_grad(b, std::move(gb));
+        if (gg) propagate_grad(g, std::move(gg));
+    }
+    void release_variables() override { g = a = b = nullptr; }
+};
+
+struct ConcatNode : autograd::AutogradNode {
+    std::vector<TensorPtr> inputs;
+    std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
+        std::vector<std::shared_ptr<AutogradNode>> r;
+        for (const auto& t : inputs)
+            if (t && t->grad_fn()) r.push_back(t->grad_fn());
+        return r;
+    }
+    void backward(const TensorPtr& go) override {
+        to_dev(go);
+        const bool batched = go->ndim() == 4;
+        const int64_t N = batched ? go->dim(0) : 1;
+        const int64_t C_total = batched ? go->dim(1) : go->dim(0);
+        const int64_t HW = go->dim(-1) * go->dim(-2);
+        int64_t c_off = 0;
+        for (const auto& t : inputs) {
+            const int64_t c = batched ? t->dim(1) : t->dim(0);
+            if (wants(t)) {
+                TensorPtr gi = Tensor::create(t->shape(), false, true);
+                for (int64_t n = 0; n < N; ++n)
+                    check(soar_memcpy_d2d(gi->cuda_data() + n * c * HW,
+                                          go->cuda_data() + (n * C_total + c_off) * HW,
+                                          (size_t)(c * HW) * sizeof(float), nullptr),
+                          "concat backward");
+                propagate_grad(t, std::move(gi));
+            }
+            c_off += c;
+        }
+    }
+    void release_variables() override { inputs.clear(); }
+};
+
+bool recording(std::initializer_list<TensorPtr> ts) {
+    if (!GradMode::is_enabled()) return false;
+    for (const auto& t : ts)
+        if (t && t->requires_grad()) return true;
+    return false;
+}
+
+}  // namespace
+
+TensorPtr Sigmoid::forward(const TensorPtr& input) {
+    to_dev(input);
+    const bool record = recording({input});
+    TensorPtr out = Tensor::create(input->shape(), record, true);
+    check(soar_sigmoid_forward(input->cuda_data(), out->cuda_data(), (size_t)input->numel(),
+                               nullptr),
+          "sigmoid");
+    if (record) {
+        auto node = std::make_shared<SigmoidNode>();
+        node->input = input;
+        node->output = out;
+        out->set_grad_fn(node);
+    }
+    return out;
+}
+
+TensorPtr PixelShuffle::forward(const TensorPtr& input) {
+    const Planes p = planes_of(input, "PixelShuffle");
+    const int64_t r = (int64_t)r_, r2 = r * r;
+    const int64_t C_in = input->ndim() == 4 ? input->dim(1) : input->dim(0);
+    if (r <= 0 || C_in % r2 != 0)
+        throw ShapeError("PixelShuffle channels must be divisible by upscale_factor squared");
+    to_dev(input);
+    Shape os = input->shape();
+    const size_t cdim = input->ndim() == 4 ? 1 : 0;
+    os[cdim] = C_in / r2;
+    os[cdim + 1] = p.H * r;
+    os[cdim + 2] = p.W * r;
+    const bool record = recording({input});
+    TensorPtr out = Tensor::create(os, record, true);
+    check(soar_pixel_shuffle_forward(input->cuda_data(), out->cuda_data(), (size_t)p.rows,
+                                     (size_t)p.H, (size_t)p.W, (size_t)r, nullptr),
+          "pixel shuffle");
+    if (record) {
+        auto node = std::make_shared<PixelShuffleNode>();
+        node->input = input;
+        node->r = r;
+        out->set_grad_fn(node);
+    }
+    return out;
+}
+
+TensorPtr Upsample::forward(const TensorPtr& input) {
+    const Planes p = planes_of(input, "Upsample");
+    // layers.cpp:1078-1079: round(H_in * scale) in float
+    const int64_t H_out = (int64_t)std::round((float)p.H * scale_);
+    const int64_t W_out = (int64_t)std::round((float)p.W * scale_);
+    if (H_out <= 0 || W_out <= 0) throw ShapeError("Upsample: empty output");
+    to_dev(input);
+    Shape os = input->shape();
+    os[os.size() - 2] = H_out;
+    os[os.size() - 1] = W_out;
+    const bool record = recording({input});
+    TensorPtr out = Tensor::create(os, record, true);
+    check(soar_upsample_bilinear_forward(input->cuda_data(), out->cuda_data(), (size_t)p.rows,
+                                         (size_t)p.H, (size_t)p.W, (size_t)H_out, (size_t)W_out,
+                                         nullptr),
+          "upsample");
+    if (record) {
+        auto node = std::make_shared<UpsampleNode>();
+        node->input = input;
+        node->H_out = H_out;
+        node->W_out = W_out;
+        out->set_grad_fn(node);
+    }
+    return out;
+}
+
+TensorPtr AdaptiveAvgPool2d::forward(const TensorPtr& input) {
+    const Planes p = planes_of(input, "AdaptiveAvgPool2d");
+    to_dev(input);
+    Shape os = input->shape();
+    os[os.size() - 2] = 1;
+    os[os.size() - 1] = 1;
+    const bool record = recording({input});
+    TensorPtr out = Tensor::create(os, record, true);
+    check(soar_global_avg_pool_forward(input->cuda_data(), out->cuda_data(), (size_t)p.rows,
+                                       (size_t)(p.H * p.W), nullptr),
+          "average pool");
+    if (record) {
+        auto node = std::make_shared<AvgPoolNode>();
+        node->input = input;
+        out->set_grad_fn(node);
+    }
+    return out;
+}
+
+TensorPtr mul_tensors(const TensorPtr& a, const TensorPtr& b) {
+    const Planes p = planes_of(a, "mul_tensors");
+    if (b->numel() != p.rows)
+        throw ShapeError("mul_tensors: b " + to_string(b->shape()) +
+                         " must hold one value per channel of " + to_string(a->shape()));
+    to_dev(a);
+    to_dev(b);
+    const bool record = recording({a, b});
+    TensorPtr out = Tensor::create(a->shape(), record, true);
+    check(soar_mul_broadcast_forward(a->cuda_data(), b->cuda_data(), out->cuda_data(),
+                                     (size_t)p.rows, (size_t)(p.H * p.W), nullptr),
+          "mul_broadcast");
+    if (record) {
+        auto node = std::make_shared<MulBroadcastNode>();
+        node->a = a;
+        node->b = b;
+        out->set_grad_fn(node);
+    }
+    return out;
+}
+
+TensorPtr convex_combination(const TensorPtr& g, const TensorPtr& a, const TensorPtr& b) {
+    if (g->shape() != a->shape() || a->shape() != b->shape())
+        throw ShapeError("convex_combination: shapes differ");
+    to_dev(g);
+    to_dev(a);
+    to_dev(b);
+    const bool record = recording({g, a, b});
+    TensorPtr out = Tensor::create(a->shape(), record, true);
+    check(soar_convex_combination_forward(g->cuda_data(), a->cuda_data(), b->cuda_data(),
+                                          out->cuda_data(), (size_t)a->numel(), nullptr),
+          "convex combination");
+    if (record) {
+        auto node = std::make_shared<ConvexNode>();
+        node->g = g;
+        node->a = a;
+        node->b = b;
+        out->set_grad_fn(node);
+    }
+    return out;
+}
+
+TensorPtr concat_channels(const std::vector<TensorPtr>& tensors) {
+    if (tensors.empty()) throw ShapeError("Cannot concatenate empty tensor list");
+    const TensorPtr& t0 = tensors[0];
+    const bool batched = t0->ndim() == 4;
+    if (t0->ndim() != 3 && !batched)
+        throw ShapeError("concat_channels expects [C,H,W] or [N,C,H,W] tensors");
+    const int64_t N = batched ? t0->dim(0) : 1;
+    const int64_t H = t0->dim(-2), W = t0->dim(-1);
+    int64_t C_total = 0;
+    for (const auto& t : tensors) {
+        if (t->ndim() != t0->ndim() || t->dim(-2) != H || t->dim(-1) != W ||
+            (batched && t->dim(0) != N))
+            throw ShapeError("concat_channels: tensors differ in batch or spatial size");
+        C_total += batched ? t->dim(1) : t->dim(0);
+        to_dev(t);
+    }
+    const bool record = GradMode::is_enabled() &&
+                        std::any_of(tensors.begin(), tensors.end(),
+                                    [](const TensorPtr& t) { return t->requires_grad(); });
+    Shape os = batched ? Shape{N, C_total, H, W} : Shape{C_total, H, W};
+    TensorPtr out = Tensor::create(os, record, true);
+    const int64_t HW = H * W;
+    int64_t c_off = 0;
+    for (const auto& t : tensors) {
+        const int64_t c = batched ? t->dim(1) : t->dim(0);
+        for (int64_t n = 0; n < N; ++n)
+            check(soar_memcpy_d2d(out->cuda_data() + (n * C_total + c_off) * HW,
+                                  t->cuda_data() + n * c * HW, (size_t)(c * HW) * sizeof(float),
+                                  nullptr),
+                  "concat");
+        c_off += c;
+    }
+    if (record) {
+        auto node = std::make_shared<ConcatNode>();
+        node->inputs = tensors;
+        out->set_grad_fn(node);
+    }
+    return out;
+}
+
+TensorPtr resize_bilinear(const TensorPtr& input, size_t target_h, size_t target_w) {
+    if (input->dim(-2) == (int64_t)target_h && input->dim(-1) == (int64_t)target_w) return input;
+    const float scale = (float)target_h / (float)input->dim(-2);
+    Upsample up(scale);
+    return up.forward(input);
+}
+
+}  // namespace soar::nn

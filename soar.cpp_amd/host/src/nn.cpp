@@ -13,6 +13,7 @@
 //     residual, so the backward's xhat is exact when std << |mean|.
 #include "soar/nn.hpp"
 
+#include <atomic>
 #include <cmath>
 #include <random>
 
@@ -20,18 +21,33 @@
 #include "soar/kernels.hpp"
 #include "soar/memory.hpp"
 #include "soar_gn.h"
+#include "soar_ops.h"
 
 namespace soar::nn {
 
 using autograd::GradMode;
 using hip::kernels::check;
 
+TensorPtr Module::forward(const TensorPtr& input) {
+    return forward(std::vector<TensorPtr>{input});
+}
+
+TensorPtr Module::forward(const std::vector<TensorPtr>& inputs) {
+    if (inputs.empty()) throw ShapeError("Forward called with empty input vector");
+    return forward(inputs[0]);
+}
+
 void Module::register_parameter(const std::string& name, TensorPtr p) {
-    params_.emplace_back(name, std::move(p));
+    params_[name] = std::move(p);
 }
 
 void Module::register_submodule(const std::string& name, std::shared_ptr<Module> m) {
-    subs_.emplace_back(name, std::move(m));
+    subs_[name] = std::move(m);
+}
+
+void Module::train(bool mode) {
+    training_ = mode;
+    for (auto& [n, m] : subs_) m->train(mode);
 }
 
 std::vector<std::pair<std::string, TensorPtr>> Module::named_parameters(
@@ -184,13 +200,15 @@ Shape conv_out_shape(const TensorPtr& x, const ConvGeom& g) {
     return {g.N, g.C_out, g.Ho, g.Wo};
 }
 
-// Backward of Conv2d (layers.cpp:17-292, the pointwise and depthwise
-// branches): dx written fresh, dW and db accumulated by the kernels.
+// Backward of Conv2d (layers.cpp:17-292): dx written fresh, dW and db
+// accumulated by the kernels.
+enum class ConvKind { Pointwise, Depthwise, General };
+
 struct Conv2dNode : autograd::AutogradNode {
     TensorPtr input, weight, bias;
     ConvGeom g{};
-    int64_t K = 1, pad = 0, stride = 1, dil = 1;
-    bool pointwise = true;
+    int64_t K = 1, pad = 0, stride = 1, dil = 1, groups = 1;
+    ConvKind kind = ConvKind::Pointwise;
 
     std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
         std::vector<std::shared_ptr<AutogradNode>> r;
@@ -212,13 +230,20 @@ struct Conv2dNode : autograd::AutogradNode {
         float* px = gx ? gx->cuda_data() : nullptr;
         float* pw = gw ? gw->cuda_data() : nullptr;
         float* pb = gb ? gb->cuda_data() : nullptr;
-        if (pointwise) {
+        if (kind == ConvKind::Pointwise) {
             const size_t wsb =
                 soar_pw_conv_backward_workspace_bytes(g.N, g.C_in, g.C_out, g.H * g.W);
             check(soar_pw_conv_backward(go->cuda_data(), input->cuda_data(), weight->cuda_data(),
                                         px, pw, pb, g.N, g.C_in, g.C_out, g.H * g.W, 0u,
                                         workspace(wsb), wsb, nullptr),
                   "pointwise convolution backward");
+        } else if (kind == ConvKind::General) {
+            const size_t wsb = soar_conv_backward_workspace_bytes(
+                g.N, g.C_in, g.C_out, g.H, g.W, g.Ho, g.Wo, K, pad, stride, dil, groups);
+            check(soar_conv_backward(go->cuda_data(), input->cuda_data(), weight->cuda_data(), px,
+                                     pw, pb, g.N, g.C_in, g.C_out, g.H, g.W, g.Ho, g.Wo, K, pad,
+                                     stride, dil, groups, 0u, workspace(wsb), wsb, nullptr),
+                  "convolution backward");
         } else {
             const size_t wsb = soar_dw_conv_backward_workspace_bytes(g.N, g.C_in, g.H, g.W, g.Ho,
                                                                      g.Wo, K, stride, dil);
@@ -409,6 +434,20 @@ TensorPtr SiLU::forward(const TensorPtr& input) {
     return out;
 }
 
+namespace {
+std::atomic<uint64_t> g_init_counter{0x50a4c0deull};
+
+// splitmix64 of a process-wide counter
+uint64_t next_init_seed() {
+    uint64_t z = (g_init_counter.fetch_add(1) + 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+}  // namespace
+
+void set_init_seed(uint64_t seed) { g_init_counter.store(seed); }
+
 Conv2d::Conv2d(size_t in_channels, size_t out_channels, size_t kernel_size, size_t stride,
                int padding, size_t dilation, size_t groups, bool bias, uint64_t seed)
     : Module("Conv2d"),
@@ -426,7 +465,7 @@ Conv2d::Conv2d(size_t in_channels, size_t out_channels, size_t kernel_size, size
     weight_ = Tensor::create({(int64_t)out_, (int64_t)cig, (int64_t)kernel_, (int64_t)kernel_},
                              true);
     const float bound = std::sqrt(1.0f / (float)(cig * kernel_ * kernel_));
-    std::mt19937_64 gen(seed);
+    std::mt19937_64 gen(seed ? seed : next_init_seed());
     std::uniform_real_distribution<float> dist(-bound, bound);
     float* w = weight_->data();
     for (int64_t i = 0; i < weight_->numel(); ++i) w[i] = dist(gen);
@@ -438,10 +477,6 @@ Conv2d::Conv2d(size_t in_channels, size_t out_channels, size_t kernel_size, size
 }
 
 TensorPtr Conv2d::forward(const TensorPtr& input) {
-    if (!pointwise() && !depthwise())
-        throw InvalidArgument(
-            "Conv2d: only pointwise (k=1, stride 1, no padding, groups 1) and depthwise "
-            "(groups = in = out) convolutions run on the device");
     const ConvGeom g = conv_geom(input, *this);
     if (!input->is_cuda()) input->to_cuda();
     weight_->to_cuda();
@@ -450,10 +485,19 @@ TensorPtr Conv2d::forward(const TensorPtr& input) {
                          (bias_ && bias_->requires_grad())) &&
                         GradMode::is_enabled();
     TensorPtr out = Tensor::create(conv_out_shape(input, g), record, true);
-    if (pointwise()) {
+    const ConvKind kind = pointwise()   ? ConvKind::Pointwise
+                          : depthwise() ? ConvKind::Depthwise
+                                        : ConvKind::General;
+    if (kind == ConvKind::Pointwise) {
         check(soar_pw_conv_forward(input->cuda_data(), weight_->cuda_data(), dptr(bias_),
                                    out->cuda_data(), g.N, g.C_in, g.C_out, g.H * g.W, nullptr),
               "pointwise convolution");
+    } else if (kind == ConvKind::General) {
+        check(soar_conv_forward(input->cuda_data(), weight_->cuda_data(), dptr(bias_),
+                                out->cuda_data(), g.N, g.C_in, g.C_out, g.H, g.W, g.Ho, g.Wo,
+                                (int64_t)kernel_, (int64_t)padding_, (int64_t)stride_,
+                                (int64_t)dilation_, (int64_t)groups_, nullptr),
+              "convolution");
     } else {
         check(soar_dw_conv_forward(input->cuda_data(), weight_->cuda_data(), dptr(bias_),
                                    out->cuda_data(), g.N, g.C_in, g.H, g.W, g.Ho, g.Wo,
@@ -471,7 +515,8 @@ TensorPtr Conv2d::forward(const TensorPtr& input) {
         node->pad = (int64_t)padding_;
         node->stride = (int64_t)stride_;
         node->dil = (int64_t)dilation_;
-        node->pointwise = pointwise();
+        node->groups = (int64_t)groups_;
+        node->kind = kind;
         out->set_grad_fn(node);
     }
     return out;

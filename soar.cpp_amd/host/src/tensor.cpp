@@ -102,6 +102,14 @@ std::vector<float> Tensor::to_host() const {
     return out;
 }
 
+void Tensor::copy_from_host(const float* src) {
+    if (numel_ == 0) return;
+    if (dev_)
+        hip::kernels::check(soar_memcpy_h2d(dev_, src, bytes(), nullptr), "copy_from_host");
+    else
+        std::memcpy(host_.data(), src, bytes());
+}
+
 TensorPtr Tensor::clone() const {
     TensorPtr t = create(shape_, false, dev_ != nullptr);
     if (numel_ == 0) return t;

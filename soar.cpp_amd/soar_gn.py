@@ -108,6 +108,51 @@ SIGNATURES = {
     "soar_prof_summary": (_c.c_int, [_c.c_char_p, _SZ]),
     "soar_gn_tune": (_c.c_int, [_c.c_int, _I64]),
     "soar_gn_tune_get": (_I64, [_c.c_int]),
+    # include/soar_ops.h
+    "soar_conv2d_forward": (_c.c_int, [_P, _P, _P, _P] + [_SZ] * 11 + [_P]),
+    "soar_conv2d_backward": (_c.c_int, [_P] * 6 + [_SZ] * 11 + [_P]),
+    "soar_conv_forward": (_c.c_int, [_P, _P, _P, _P] + [_I64] * 12 + [_P]),
+    "soar_conv_backward_workspace_bytes": (_SZ, [_I64] * 12),
+    "soar_conv_backward": (_c.c_int, [_P] * 6 + [_I64] * 12 + [_c.c_uint, _P, _SZ, _P]),
+    "soar_sigmoid_forward": (_c.c_int, [_P, _P, _SZ, _P]),
+    "soar_sigmoid_backward": (_c.c_int, [_P, _P, _P, _SZ, _P]),
+    "soar_mul_broadcast_forward": (_c.c_int, [_P, _P, _P, _SZ, _SZ, _P]),
+    "soar_mul_broadcast_backward": (_c.c_int, [_P, _P, _P, _P, _P, _SZ, _SZ, _P]),
+    "soar_convex_combination_forward": (_c.c_int, [_P, _P, _P, _P, _SZ, _P]),
+    "soar_convex_combination_backward": (_c.c_int, [_P] * 7 + [_SZ, _P]),
+    "soar_global_avg_pool_forward": (_c.c_int, [_P, _P, _SZ, _SZ, _P]),
+    "soar_global_avg_pool_backward": (_c.c_int, [_P, _P, _SZ, _SZ, _P]),
+    "soar_upsample_bilinear_forward": (_c.c_int, [_P, _P] + [_SZ] * 5 + [_P]),
+    "soar_upsample_bilinear_2x_forward": (_c.c_int, [_P, _P] + [_SZ] * 3 + [_P]),
+    "soar_upsample_bilinear_backward": (_c.c_int, [_P, _P] + [_SZ] * 5 + [_P]),
+    "soar_upsample_bilinear_2x_backward": (_c.c_int, [_P, _P] + [_SZ] * 3 + [_P]),
+    "soar_pixel_shuffle_forward": (_c.c_int, [_P, _P] + [_SZ] * 4 + [_P]),
+    "soar_pixel_shuffle_backward": (_c.c_int, [_P, _P] + [_SZ] * 4 + [_P]),
+    "soar_pad_spatial_forward": (_c.c_int, [_P, _P] + [_SZ] * 5 + [_P]),
+    "soar_pad_spatial_backward": (_c.c_int, [_P, _P] + [_SZ] * 5 + [_P]),
+    "soar_unpad_spatial_forward": (_c.c_int, [_P, _P] + [_SZ] * 5 + [_P]),
+    "soar_unpad_spatial_backward": (_c.c_int, [_P, _P] + [_SZ] * 5 + [_P]),
+    "soar_bce_with_logits_forward": (_c.c_int, [_P, _P, _c.c_float, _c.c_float, _SZ,
+                                                _c.POINTER(_c.c_float), _P]),
+    "soar_bce_with_logits_backward": (_c.c_int, [_P, _P, _P, _c.c_float, _c.c_float,
+                                                 _c.c_float, _SZ, _P]),
+    "soar_dice_loss_forward": (_c.c_int, [_P, _P, _c.c_float, _c.c_float,
+                                          _c.POINTER(_c.c_float), _c.POINTER(_c.c_float),
+                                          _c.POINTER(_c.c_float), _SZ,
+                                          _c.POINTER(_c.c_float), _P]),
+    "soar_dice_loss_backward": (_c.c_int, [_P, _P, _P] + [_c.c_float] * 6 + [_SZ, _P]),
+    "soar_dice_bce_loss_forward": (_c.c_int, [_P, _P, _SZ] + [_c.c_float] * 5 +
+                                   [_c.POINTER(_c.c_float), _P]),
+    "soar_dice_bce_loss_backward": (_c.c_int, [_P, _P, _P] + [_c.c_float] * 9 + [_SZ, _P]),
+    "soar_sigmoid_threshold": (_c.c_int, [_P, _P, _P, _SZ, _c.c_float, _P]),
+    "soar_adamw_step": (_c.c_int, [_P, _P, _P, _P] + [_c.c_float] * 7 + [_SZ, _P]),
+    "soar_adamw_step_multi_tensor": (_c.c_int, [_P, _P, _P, _P, _P, _c.c_int] +
+                                     [_c.c_float] * 7 + [_P]),
+    "soar_adamw_multi_tensor_device": (_c.c_int, [_P, _P, _P, _P, _P, _c.c_int] +
+                                       [_c.c_float] * 7 + [_P]),
+    "soar_multi_tensor_norm_workspace_bytes": (_SZ, []),
+    "soar_multi_tensor_norm_sq_device": (_c.c_int, [_P, _P, _c.c_int, _P, _P, _SZ, _P]),
+    "soar_multi_tensor_scale_device": (_c.c_int, [_P, _P, _c.c_int, _c.c_float, _P]),
 }
 
 SYNTH_SIGNATURES = {
@@ -124,8 +169,12 @@ _LIB = None
 _SYNTH = None
 
 
+OPS_HEADER_PATH = os.path.join(ROOT, "include", "soar_ops.h")
+
+
 def header_symbols(path: str = HEADER_PATH) -> list[str]:
-    """Names of every function declared with SOAR_API in include/soar_gn.h."""
+    """Names of every function declared with SOAR_API in a header
+    (include/soar_gn.h by default)."""
     with open(path) as f:
         text = f.read()
     return re.findall(r"SOAR_API\s+[^;(]*?\b(soar_\w+)\s*\(", text)

@@ -133,8 +133,9 @@ static void test_layers_need_a_device() {
     CHECK_THROWS(nn::GroupNorm(3, 8), InvalidArgument);
     nn::GroupNorm gn(2, 4);
     auto names = gn.named_parameters("norm");
-    CHECK(names.size() == 2 && names[0].first == "norm.weight" && names[1].first == "norm.bias");
-    CHECK(names[0].second->data()[3] == 1.0f && names[1].second->data()[0] == 0.0f);
+    // name-sorted like the reference's std::map (module.hpp:133-134)
+    CHECK(names.size() == 2 && names[0].first == "norm.bias" && names[1].first == "norm.weight");
+    CHECK(names[1].second->data()[3] == 1.0f && names[0].second->data()[0] == 0.0f);
     auto x = Tensor::create({4, 8, 8}, true);
     CHECK_THROWS(gn.forward(Tensor::create({3, 8, 8})), ShapeError);
     if (!hip::kernels::is_cuda_available()) {

@@ -357,7 +357,7 @@ static void test_cba_blocks() {
         nn::CBA cba(c.c1, c.c2, c.k, 1, -1, 1, c.g, c.act);
         const auto names = cba.named_parameters();
         CHECK(names.size() == 3 && names[0].first == "conv.weight" &&
-              names[1].first == "norm.weight" && names[2].first == "norm.bias");
+              names[1].first == "norm.bias" && names[2].first == "norm.weight");
         const int64_t G = nn::select_group_count((int)c.c2), HW = c.H * c.W;
         std::vector<float> x(c.N * c.c1 * HW), dy(c.N * c.c2 * HW), gam(c.c2), bet(c.c2);
         orc_fill_normal(x.data(), (int64_t)x.size(), 700 + c.k, 1, 0.0, 1.0);

@@ -13,12 +13,35 @@ def L():
 
 
 def test_exports_every_header_symbol(L):
-    names = soar_gn.header_symbols()
-    assert len(names) >= 20
+    names = soar_gn.header_symbols() + soar_gn.header_symbols(soar_gn.OPS_HEADER_PATH)
+    assert len(names) >= 60
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing, missing
     # and the binding declares exactly those
     assert set(names) == set(soar_gn.SIGNATURES)
+
+
+def test_ops_validate_on_the_host(L):
+    """Shape errors of the model operators are caught before any device
+    call (so they hold without a GPU)."""
+    # output size that does not match the input / kernel / stride
+    assert L.soar_conv2d_forward(None, None, None, None, 1, 16, 64, 64, 31, 32, 3, 1, 2, 1,
+                                 1, None) == soar_gn.SOAR_EINVAL
+    assert b"does not match" in L.soar_last_error()
+    # channels not divisible by groups
+    assert L.soar_conv_forward(None, None, None, None, 1, 6, 4, 8, 8, 8, 8, 3, 1, 1, 1, 4,
+                               None) == soar_gn.SOAR_EINVAL
+    # pixel shuffle needs C_in divisible by r*r
+    assert L.soar_pixel_shuffle_forward(None, None, 6, 4, 4, 2, None) == soar_gn.SOAR_EINVAL
+    # crop larger than the padded plane
+    assert L.soar_unpad_spatial_forward(None, None, 1, 4, 4, 5, 4, None) == soar_gn.SOAR_EINVAL
+    # conv workspace is pure host arithmetic: one fp64 partial per
+    # (weight tap or bias, 16384-position chunk)
+    assert L.soar_conv_backward_workspace_bytes(1, 1, 16, 64, 64, 32, 32, 3, 1, 2, 1, 1) == \
+        16 * 10 * 1 * 8
+    assert L.soar_conv_backward_workspace_bytes(2, 1, 16, 256, 256, 128, 128, 3, 1, 2, 1, 1) == \
+        16 * 10 * 2 * 8
+    assert L.soar_multi_tensor_norm_workspace_bytes() == (512 + 1) * 8
 
 
 def test_synth_library_exports(L):

@@ -1,0 +1,239 @@
+"""End-to-end parity of the SOAR model on the MI355X (libsoar_host.so over
+libsoar_gn.so) against the CPU restatement oracle/soar_model_ref.py.
+
+The gate is the Nano model at 64 x 64: one image, random weights loaded
+from a .soar file (so LKR's zero-initialised scales and every branch carry
+signal), then forward logits, the Dice+BCE loss, every parameter gradient,
+two AdamW steps with gradient clipping, prediction and RLE, and the .soar
+round trip.
+
+Tolerances (fp32 device arithmetic against the float64 oracle):
+  * logits and losses: the device's fp32 forward runs ~70 normalised
+    layers; each contributes a relative error of order K * 2^-24 (K the
+    reduction length, <= a few thousand), so |dz| <= 2e-4 * (1 + |z|max)
+    and the losses within 1e-4 relative;
+  * gradients: per tensor, ||g - g_ref|| <= 2e-3 * ||g_ref|| + 1e-6 *
+    ||g_ref||_global (the backward doubles the depth and divides by small
+    GroupNorm spreads);
+  * AdamW: bit-exact given the device's own gradients (the update is
+    scalar fp32 arithmetic with no fused multiply-add on both sides);
+  * masks: identical wherever the oracle's probability is more than 1e-4
+    from the threshold; RLE: identical to the oracle's encoding of the
+    device's mask.
+"""
+import numpy as np
+import pytest
+
+import soar_model_ref as smr
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+H = W = 64
+SEED = 20261201
+
+
+@pytest.fixture(scope="module")
+def sm():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    import soar_model
+    soar_model.lib()
+    return soar_model
+
+
+@pytest.fixture(scope="module")
+def weights():
+    return smr.random_weights(smr.model_spec(1, 1, 0), SEED)
+
+
+@pytest.fixture(scope="module")
+def wfile(tmp_path_factory, weights):
+    p = tmp_path_factory.mktemp("w") / "nano_random.soar"
+    smr.write_soar(p, [(n, weights[n]) for n, _, _ in smr.model_spec(1, 1, 0)], variant=0)
+    return p
+
+
+def sample(seed, h=H, w=W, c=1):
+    r = np.random.default_rng(seed)
+    img = r.normal(0.5, 0.25, size=(c, h, w)).astype(F32)
+    yy, xx = np.mgrid[0:h, 0:w]
+    mask = (((yy - h / 2) ** 2 + (xx - w / 3) ** 2) < (min(h, w) / 3) ** 2).astype(F32)[None]
+    return img, mask
+
+
+def model_with(sm, wfile, seed=1):
+    m = sm.SOAR(1, 1, "nano", seed=seed)
+    m.load_weights(str(wfile))
+    return m
+
+
+def rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def test_names_shapes_and_initialisation(sm):
+    """Parameter names, shapes and order equal named_parameters() of the
+    reference, and the initial values follow its constructors."""
+    print("case: nano construction", flush=True)
+    spec = smr.model_spec(1, 1, 0)
+    m = sm.SOAR(1, 1, "nano", seed=7)
+    assert m.tensors() == [(n, tuple(s)) for n, s, _ in spec]
+    assert m.parameter_count == sum(int(np.prod(s)) for _, s, _ in spec) > 200000
+    st = m.state()
+    for name, shape, init in spec:
+        v = st[name]
+        if init == "ones":
+            assert np.all(v == 1.0), name
+        elif init == "zeros":
+            assert np.all(v == 0.0), name
+        elif isinstance(init, tuple):
+            np.testing.assert_allclose(v, init[1], rtol=1e-6)
+        else:  # Kaiming uniform U(-1/sqrt(fan_in), 1/sqrt(fan_in))
+            bound = 1.0 / np.sqrt(np.prod(shape[1:]))
+            assert np.abs(v).max() <= bound * (1 + 1e-6) and v.std() > 0.3 * bound, name
+    # seeded creation is reproducible; another seed differs
+    m2 = sm.SOAR(1, 1, "nano", seed=7)
+    np.testing.assert_array_equal(m2.read(0), st[spec[0][0]])
+    m3 = sm.SOAR(1, 1, "nano", seed=8)
+    assert not np.array_equal(m3.read(0), st[spec[0][0]])
+
+
+@pytest.mark.parametrize("variant,idx", [("small", 1), ("medium", 2)])
+def test_variant_parameter_counts(sm, variant, idx):
+    print(f"case: {variant} construction", flush=True)
+    m = sm.SOAR(1, 1, variant, seed=3)
+    assert m.parameter_count == sum(int(np.prod(s)) for _, s, _ in smr.model_spec(1, 1, idx))
+    m.close()
+
+
+def test_forward_matches_oracle(sm, wfile, weights):
+    print("case: forward 64x64", flush=True)
+    img, _ = sample(1)
+    m = model_with(sm, wfile)
+    z = m.forward(img)
+    ref = smr.Model(weights, requires_grad=False).forward(img).detach().numpy()
+    err = np.abs(z - ref).max()
+    print(f"  logits max|dz| = {err:.3e}  max|z| = {np.abs(ref).max():.3f}  rel = {rel(z, ref):.3e}")
+    assert err <= 2e-4 * (1 + np.abs(ref).max())
+
+
+@pytest.mark.parametrize("h,w", [(32, 32), (40, 50), (96, 64)])
+def test_forward_other_sizes(sm, wfile, weights, h, w):
+    """The smallest size the strides allow, a padded size (reflection pad
+    to 64 x 64, then crop) and a non-square one."""
+    print(f"case: forward {h}x{w}", flush=True)
+    img, _ = sample(2, h, w)
+    m = model_with(sm, wfile)
+    z = m.forward(img)
+    ref = smr.Model(weights, requires_grad=False).forward(img).detach().numpy()
+    assert z.shape == (1, h, w)
+    err = np.abs(z - ref).max()
+    print(f"  max|dz| = {err:.3e}")
+    assert err <= 2e-4 * (1 + np.abs(ref).max())
+
+
+def test_gradients_match_oracle(sm, wfile, weights):
+    print("case: forward_backward 64x64", flush=True)
+    img, mask = sample(3)
+    m = model_with(sm, wfile)
+    met = m.forward_backward(img, mask)
+    lo, _, grads = smr.forward_backward(weights, img, mask)
+    for k, v in (("loss", lo.total), ("bce", lo.bce), ("dice_loss", lo.dice)):
+        assert abs(met[k] - v) <= 1e-4 * abs(v) + 1e-6, (k, met[k], v)
+    gnorm = np.sqrt(sum(float(np.sum(g.astype(np.float64) ** 2)) for g in grads.values()))
+    worst = []
+    for i, (name, shape) in enumerate(m.tensors()):
+        g = m.read(i, grad=True, shape=shape)
+        ref = grads[name]
+        d = float(np.linalg.norm(g.astype(np.float64) - ref))
+        bound = 2e-3 * float(np.linalg.norm(ref)) + 1e-6 * gnorm
+        worst.append((d / max(bound, 1e-300), name, d, float(np.linalg.norm(ref))))
+        assert d <= bound, (name, d, float(np.linalg.norm(ref)))
+    worst.sort(reverse=True)
+    print("  worst gradient ratios:", [(f"{w[0]:.3f}", w[1]) for w in worst[:4]])
+
+
+def test_two_train_steps_match_adamw(sm, wfile):
+    """train_step = clip(2.0) + AdamW + zero_grad on the step's gradients:
+    bit-exact against the scalar fp32 update on the device's gradients,
+    with the moments carried into the second step."""
+    print("case: train_step x2", flush=True)
+    img, mask = sample(4)
+    m = model_with(sm, wfile)
+    names = [n for n, _ in m.tensors()]
+    theta = m.state()
+    mom = {n: np.zeros_like(v) for n, v in theta.items()}
+    vel = {n: np.zeros_like(v) for n, v in theta.items()}
+    for step, lr in ((1, 1e-3), (2, 5e-4)):
+        m.zero_grad()
+        fb = m.forward_backward(img, mask)
+        g = m.state(grad=True)
+        m.zero_grad()
+        out = m.train_step(img, mask, lr=lr)
+        met = m.last_metrics()
+        assert out["loss"] == fb["loss"] and met["lr"] == np.float32(lr)
+        norm = smr.grad_norm([g[n] for n in names])
+        assert abs(float(met["grad_norm"]) - float(norm)) <= 1e-6 * float(norm)
+        coef = smr.clip_coef(met["grad_norm"], 2.0)
+        new = m.state()
+        for n in names:
+            gn = g[n] if coef is None else (g[n] * coef).astype(F32)
+            t, mom[n], vel[n] = smr.adamw_step(theta[n], gn, mom[n], vel[n], step, lr=lr)
+            np.testing.assert_array_equal(new[n], t, err_msg=f"step {step} {n}")
+        # zero_grad after the step
+        assert all(not np.any(m.read(i, grad=True)) for i in (0, len(names) // 2))
+        theta = new
+    # device-path metrics (trainer.cpp:80-86)
+    d = min(1.0, max(0.0, 1.0 - met["dice_loss"]))
+    assert abs(met["dice"] - d) < 1e-6 and abs(met["iou"] - d / (2 - d + 1e-7)) < 1e-6
+
+
+def test_predict_matches_oracle(sm, wfile, weights):
+    print("case: predict", flush=True)
+    img, _ = sample(5)
+    m = model_with(sm, wfile)
+    probs, mask, rle = m.predict(img, threshold=0.5)
+    z = smr.Model(weights, requires_grad=False).forward(img).detach().numpy()[0]
+    p = 1.0 / (1.0 + np.exp(-z))
+    np.testing.assert_allclose(probs[0], p, rtol=0, atol=5e-5)
+    sure = np.abs(p - 0.5) > 1e-4
+    np.testing.assert_array_equal(mask[sure], (p >= 0.5)[sure])
+    assert rle == smr.encode_rle(mask, H, W)
+    # the threshold moves the mask as it should
+    _, mask_hi, _ = m.predict(img, threshold=0.9)
+    assert mask_hi.sum() <= mask.sum()
+
+
+def test_save_load_roundtrip(sm, wfile, weights, tmp_path):
+    print("case: .soar round trip", flush=True)
+    m = model_with(sm, wfile)
+    out = tmp_path / "saved.soar"
+    m.save_weights(str(out))
+    hdr, items = smr.read_soar(out)
+    spec = smr.model_spec(1, 1, 0)
+    assert hdr == (0x534F4152, 1, 0, len(spec))
+    for (name, ndim, shape4, data), (sname, sshape, _) in zip(items, spec):
+        assert name == sname and ndim == len(sshape)
+        assert shape4 == tuple(list(sshape) + [1] * (4 - len(sshape)))
+        np.testing.assert_array_equal(data, weights[name].ravel())
+    # a fresh model that loads the file computes the same logits, bit for bit
+    img, _ = sample(6)
+    m2 = sm.SOAR(1, 1, "nano", seed=99)
+    m2.load_weights(str(out))
+    np.testing.assert_array_equal(m2.forward(img), m.forward(img))
+
+
+def test_rle_and_errors(sm):
+    print("case: rle / errors", flush=True)
+    r = np.random.default_rng(8)
+    for h, w in ((3, 3), (7, 5), (64, 64)):
+        mk = (r.uniform(size=(h, w)) < 0.4).astype(np.uint8)
+        assert sm.encode_rle(mk) == smr.encode_rle(mk, h, w)
+    m = sm.SOAR(1, 1, "nano", seed=1)
+    with pytest.raises(RuntimeError):
+        m.load_weights("/nonexistent/file.soar")
+    with pytest.raises(RuntimeError):
+        m.train_step(np.zeros((1, 64, 64), F32)[:, :0], np.zeros((1, 64, 64), F32))
