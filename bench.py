@@ -45,6 +45,15 @@ SEED_OF = {"cfg2_fwd": SEED + 2, "cfg3": SEED + 3, "cfg4_chain": SEED + 4, "cfg5
 CBA_C_IN = 64
 PEAK_MFMA_F32 = 157.3  # TFLOP/s, dense fp32 matrix
 
+# End-to-end training steps of the SOAR model through libsoar_host.so
+# (soar_train_step: forward, Dice+BCE loss, backward, clip, AdamW), one
+# 1-channel image per step: name -> (variant, H, W)
+TRAIN_CONFIGS = {
+    "train_nano64": ("nano", 64, 64),
+    "train_nano512": ("nano", 512, 512),
+    "train_nano1024": ("nano", 1024, 1024),
+}
+
 # algorithmic tensor passes (units of T) each kernel makes per block of the
 # step, summed over its launches (a kernel runs once per unit batch)
 PASSES = {"gn_stats_partial": 1, "gn_silu_apply": 2, "gn_silu_bwd_reduce": 2,
@@ -57,7 +66,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + sorted(TRAIN_CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="time the steps without per-kernel events")
@@ -230,12 +239,96 @@ def cpu_baseline():
                       f" 1 thread of {os.cpu_count()} host CPUs"}
 
 
+def train_cpu_baseline(H, W, variant):
+    """The float64 CPU restatement of one training step (oracle/
+    soar_model_ref.py on torch's CPU kernels), best of 2 after a warm-up."""
+    import numpy as np
+    import torch
+    import soar_model_ref as smr
+    spec = smr.model_spec(1, 1, {"nano": 0}[variant])
+    w = smr.random_weights(spec, SEED)
+    img = np.random.default_rng(SEED).normal(0.5, 0.25, size=(1, H, W)).astype(np.float32)
+    mask = (np.random.default_rng(SEED + 1).uniform(size=(1, H, W)) < 0.3).astype(np.float32)
+    smr.forward_backward(w, img, mask)
+    ts = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        smr.forward_backward(w, img, mask)
+        ts.append(time.perf_counter() - t0)
+    t = min(ts)
+    return {"value": round(1.0 / t, 3), "unit": "images/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"forward+loss+backward of one {H}x{W} image in float64 on the CPU "
+                      f"(the oracle's restatement; no optimizer step), best of 2 after 1 "
+                      f"warm-up, {t * 1e3:.1f} ms"}
+
+
+def bench_train(args):
+    """Images/s of soar_train_step on one GPU (inputs are host arrays, as
+    the C-ABI takes them: the timed step includes their copy to the
+    device and the loss read-back, as in the reference's train_step)."""
+    import numpy as np
+    import torch
+    import soar_gn as gn
+    import soar_model as sm
+    variant, H, W = TRAIN_CONFIGS[args.config]
+    m = sm.SOAR(1, 1, variant, seed=SEED)
+    r = np.random.default_rng(SEED)
+    img = r.normal(0.5, 0.25, size=(1, H, W)).astype(np.float32)
+    yy, xx = np.mgrid[0:H, 0:W]
+    mask = (((yy - H / 2) ** 2 + (xx - W / 3) ** 2) < (min(H, W) / 3) ** 2).astype(np.float32)
+    mask = mask[None]
+    for _ in range(args.warmup):
+        m.train_step(img, mask, 1e-3)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        m.train_step(img, mask, 1e-3)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    kernels = []
+    if not args.no_kernel_timing:
+        gn.prof_summary()  # drop anything recorded so far
+        gn.prof_enable(True)
+        for _ in range(args.steps):
+            m.train_step(img, mask, 1e-3)
+        torch.cuda.synchronize()
+        gn.prof_enable(False)
+        recs = gn.prof_summary()
+        total = sum(k["total_ms"] for k in recs) / args.steps
+        kernels = [{"kernel": k["kernel"], "ms_per_step": round(k["total_ms"] / args.steps, 4),
+                    "launches_per_step": k["launches"] // args.steps}
+                   for k in sorted(recs, key=lambda k: -k["total_ms"])[:10]]
+        kernels.append({"kernel": "(all timed kernels)", "ms_per_step": round(total, 4)})
+    mem = m.memory_info()
+    out = {
+        "metric": f"SOAR {variant} train_step images/s, 1x{H}x{W} fp32",
+        "value": round(1.0 / dt, 3), "unit": "images/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": args.config, "variant": variant, "image": [1, H, W],
+                   "loss": "CompositeLoss(0.5, 0.5)", "optimizer": "AdamW lr 1e-3, clip 2.0"},
+        "roofline": None,
+        "kernels_top": kernels,
+        "memory": mem,
+    }
+    if not args.no_cpu_baseline and H * W <= 512 * 512:
+        out["cpu_baseline"] = train_cpu_baseline(H, W, variant)
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has "
               "no multi-GPU path.", file=sys.stderr)
         sys.exit(2)
+    if args.config in TRAIN_CONFIGS:
+        import torch
+        assert torch.cuda.is_available(), "bench.py needs a GPU"
+        torch.cuda.set_device(0)
+        bench_train(args)
+        return
     import torch
     import soar_gn as gn
 

@@ -285,6 +285,12 @@ SOAR_API int soar_multi_tensor_scale_device(float* const* tensors,
                                             int n_tensors, float scale,
                                             void* stream);
 
+/* tensors[k][i] = value (one launch for a whole gradient list:
+ * Module::zero_grad, module.hpp:71-75, without a launch per tensor). */
+SOAR_API int soar_multi_tensor_fill_device(float* const* tensors,
+                                           const int64_t* numel, int n_tensors,
+                                           float value, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

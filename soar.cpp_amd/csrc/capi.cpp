@@ -440,11 +440,12 @@ SOAR_API int soar_conv2d_1x1_forward(const float* in, const float* weight, const
         (rc = check_dev_opt(bias, C_out * 4, "bias")) || (rc = check_dev(out, (size_t)oe * 4, "out")))
         return rc;
     const Tuning t = current_tuning();
-    if (!pw_grid_fits(1, (int64_t)HW, t.pw_chunk))
+    const int64_t chunk = soar::gn::pw_pick_chunk(1, (int64_t)C_out, (int64_t)HW, t.pw_chunk);
+    if (!pw_grid_fits(1, (int64_t)HW, chunk))
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     soar::gn::PwArgs a{in, weight, bias, out};
     hipError_t e = soar::gn::launch_pw_conv(a, 1, (int64_t)C_in, (int64_t)C_out, (int64_t)HW,
-                                            t.pw_chunk, nullptr, false,
+                                            chunk, nullptr, false,
                                             static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "conv2d_1x1_forward launch");
 }
@@ -464,10 +465,11 @@ SOAR_API int soar_pw_conv_forward(const float* x, const float* weight, const flo
         (rc = check_dev(z, (size_t)oe * 4, "z")))
         return rc;
     const Tuning t = current_tuning();
-    if (!pw_grid_fits(N, HW, t.pw_chunk))
+    const int64_t chunk = soar::gn::pw_pick_chunk(N, C_out, HW, t.pw_chunk);
+    if (!pw_grid_fits(N, HW, chunk))
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     soar::gn::PwArgs a{x, weight, bias, z};
-    hipError_t e = soar::gn::launch_pw_conv(a, N, C_in, C_out, HW, t.pw_chunk, nullptr, false,
+    hipError_t e = soar::gn::launch_pw_conv(a, N, C_in, C_out, HW, chunk, nullptr, false,
                                             static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "pointwise convolution launch");
 }
@@ -557,7 +559,7 @@ SOAR_API int soar_pw_conv_backward(const float* dz, const float* x, const float*
         return rc;
     const Tuning t = current_tuning();
     const soar::gn::PwBwdPlan p = soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW);
-    if (!pw_grid_fits(N, HW, t.pw_chunk) || p.G > 65535 ||
+    if (!pw_grid_fits(N, HW, soar::gn::pw_pick_chunk(N, C_in, HW, t.pw_chunk)) || p.G > 65535 ||
         p.tiles_co * p.tiles_ci > (int64_t)0x7fffffff)
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     const size_t need = soar::gn::pw_bwd_workspace_bytes(p);

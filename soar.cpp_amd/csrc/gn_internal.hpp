@@ -123,9 +123,13 @@ struct PwArgs {
 int pw_kpad(int64_t C_in);
 // The kernel addresses one sample's planes with 32-bit byte offsets.
 bool pw_offsets_fit(int64_t C_in, int64_t HW);
+// Pixels per wave of the pointwise convolution for this shape: at most
+// max_chunk, a multiple of 128, small enough that about 2048 waves run.
+int64_t pw_pick_chunk(int64_t N, int64_t C_out, int64_t HW, int64_t max_chunk);
 // z = w * x + bias (z += w * x with `accumulate`).  With `part` non-null
 // the kernel also writes the GroupNorm chunk partials of z for chunks of
-// `chunk` pixels (a multiple of 128), part[(n*C_out + co)*cpp + k].
+// `chunk` pixels (a multiple of 128, normally from pw_pick_chunk),
+// part[(n*C_out + co)*cpp + k].
 // `name` labels the launch for the kernel timers (null: a default).
 hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
                           int64_t HW, int64_t chunk, double2* part, bool accumulate,
@@ -133,7 +137,8 @@ hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_ou
 
 // Backward of the pointwise convolution: dx = W^T dz (written, or added
 // with `accumulate_dx`), dw += sum dz x^T, db += sum dz; any output may be
-// null.  Workspace: W^T, then the per-chunk dW and db partials.
+// null.  Workspace: W^T, then the per-chunk dW and db partials.  The dx
+// chunk is pw_pick_chunk(N, C_in, HW, chunk_dx).
 struct PwBwdArgs {
     const float* dz;  // [N][C_out][HW]
     const float* x;   // [N][C_in][HW]

@@ -860,7 +860,7 @@ double2* ws_partials(const Plan& p, void* ws) { return ws_view(p, ws).part; }
 
 bool make_pw_plan(int64_t N, int64_t C_out, int64_t HW, int64_t G, const Tuning& t, Plan* p) {
     Tuning tp = t;
-    tp.chunk = t.pw_chunk;
+    tp.chunk = pw_pick_chunk(N, C_out, HW, t.pw_chunk);
     tp.batch_mb = 0;
     if (!make_plan(N, C_out, HW, G, tp, p)) return false;
     return p->chunk % 128 == 0;

@@ -629,6 +629,18 @@ __global__ __launch_bounds__(kThreads) void k_multi_scale(float* const* __restri
     }
 }
 
+__global__ __launch_bounds__(kThreads) void k_multi_fill(float* const* __restrict__ t,
+                                                         const int64_t* __restrict__ numel,
+                                                         int n_tensors, float value) {
+    const int64_t start = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int k = 0; k < n_tensors; ++k) {
+        float* p = t[k];
+        const int64_t n = numel[k];
+        for (int64_t i = start; i < n; i += stride) p[i] = value;
+    }
+}
+
 // The AdamW update of adamw.cpp:60-108, operation by operation in fp32
 // with no fused multiply-adds, so it matches a scalar IEEE evaluation of
 // the same expressions bit for bit.
@@ -863,6 +875,12 @@ hipError_t launch_multi_norm_sq(const float* const* t, const int64_t* numel, int
 hipError_t launch_multi_scale(float* const* t, const int64_t* numel, int n_tensors, float scale,
                               hipStream_t s) {
     k_multi_scale<<<kMultiBlocks, kThreads, 0, s>>>(t, numel, n_tensors, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_multi_fill(float* const* t, const int64_t* numel, int n_tensors, float value,
+                             hipStream_t s) {
+    k_multi_fill<<<kMultiBlocks, kThreads, 0, s>>>(t, numel, n_tensors, value);
     return hipGetLastError();
 }
 

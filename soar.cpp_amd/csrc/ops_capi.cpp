@@ -777,4 +777,16 @@ SOAR_API int soar_multi_tensor_scale_device(float* const* tensors, const int64_t
                     "multi-tensor scale launch");
 }
 
+SOAR_API int soar_multi_tensor_fill_device(float* const* tensors, const int64_t* numel,
+                                           int n_tensors, float value, void* stream) {
+    if (n_tensors == 0) return ok();
+    if (n_tensors < 0) return fail(SOAR_EINVAL, "n_tensors is negative");
+    int rc;
+    if ((rc = require_device()) || (rc = check_table(tensors, n_tensors, "tensors")) ||
+        (rc = check_table(numel, n_tensors, "numel")))
+        return rc;
+    return launched(soar::ops::launch_multi_fill(tensors, numel, n_tensors, value, S(stream)),
+                    "multi-tensor fill launch");
+}
+
 }  // extern "C"

@@ -92,6 +92,8 @@ hipError_t launch_multi_norm_sq(const float* const* t, const int64_t* numel, int
                                 double* out, void* ws, hipStream_t s);
 hipError_t launch_multi_scale(float* const* t, const int64_t* numel, int n_tensors, float scale,
                               hipStream_t s);
+hipError_t launch_multi_fill(float* const* t, const int64_t* numel, int n_tensors, float value,
+                             hipStream_t s);
 hipError_t launch_adamw_multi(float* const* p, const float* const* g, float* const* m,
                               float* const* v, const int64_t* numel, int n_tensors, float lr,
                               float beta1, float beta2, float eps, float wd, float step_size,

@@ -278,7 +278,7 @@ template <bool FAST, int MODE, bool BIAS>
 __global__ __launch_bounds__(64, 2) void k_pw_conv(
     const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ bias, float* __restrict__ z, double2* __restrict__ part,
-    int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk, int64_t cpp, int Kpad) {
+    int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk, int64_t cpp, int Kpad, int rpw) {
     __shared__ __attribute__((aligned(16))) float2 lds[kRowTile * kLdsStride];
     __shared__ float ldsK[kRowTile];            // per-row shifts of the item
     __shared__ Mom ldsM[kRowGroup * kRowTile];  // row-owner running moments
@@ -290,11 +290,12 @@ __global__ __launch_bounds__(64, 2) void k_pw_conv(
     const int64_t kc = (int64_t)blockIdx.x - n * cpp;
     const int64_t px0 = kc * chunk;
     const int64_t pend = min(px0 + chunk, HW);
-    const int64_t R = (C_out + kRowTile - 1) / kRowTile;
+    // this wave's row tiles: [blockIdx.y * rpw, +rpw) of the R tiles
+    const int64_t R = min<int64_t>((C_out + kRowTile - 1) / kRowTile, ((int64_t)blockIdx.y + 1) * rpw);
     const float* xn = x + n * C_in * HW;
     float* zn = z + n * C_out * HW;
 
-    for (int64_t rg = 0; rg < R; rg += kRowGroup) {
+    for (int64_t rg = (int64_t)blockIdx.y * rpw; rg < R; rg += kRowGroup) {
         const int nrt = (int)min<int64_t>(kRowGroup, R - rg);
         if (STATS) {
 #pragma unroll
@@ -540,12 +541,28 @@ bool pw_offsets_fit(int64_t C_in, int64_t HW) {
     return HW <= ((int64_t)1 << 31) / 20 - 4 && C_in <= ((int64_t)1 << 31) / 256;
 }
 
+int64_t pw_pick_chunk(int64_t N, int64_t C_out, int64_t HW, int64_t max_chunk) {
+    // enough waves to fill the chip (about 2048, two per SIMD): when the
+    // planes are small, smaller chunks, down to one 128-pixel item
+    const int64_t R = (C_out + kRowTile - 1) / kRowTile;
+    const int64_t want = (2048 + N * R - 1) / std::max<int64_t>(N * R, 1);  // chunks per plane
+    int64_t c = (HW + want - 1) / want;
+    c = (c + kItem - 1) / kItem * kItem;
+    return std::max<int64_t>(kItem, std::min<int64_t>(c, max_chunk));
+}
+
 hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
                           int64_t HW, int64_t chunk, double2* part, bool accumulate,
                           hipStream_t s, const char* name) {
     if (N == 0 || HW == 0 || C_out == 0) return hipSuccess;
     const int64_t cpp = (HW + chunk - 1) / chunk;
-    const dim3 grid((unsigned)(N * cpp));
+    // A wave walks up to kRowGroup row tiles of its chunk (the chunk's x
+    // stays in cache across them); when that leaves too few waves, each row
+    // tile gets its own wave.
+    const int64_t R = (C_out + kRowTile - 1) / kRowTile;
+    const int64_t groups = (R + kRowGroup - 1) / kRowGroup;
+    const int rpw = N * cpp * groups >= 1024 ? kRowGroup : 1;
+    const dim3 grid((unsigned)(N * cpp), (unsigned)((R + rpw - 1) / rpw));
     const bool fast = (HW % 4 == 0) && (C_in % 8 == 0) && ((uintptr_t)a.x % 16 == 0) &&
                       ((uintptr_t)a.z % 16 == 0) && ((uintptr_t)a.w % 16 == 0);
     const int Kpad = pw_kpad(C_in);
@@ -554,7 +571,7 @@ hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_ou
     const int tok = prof_begin(s, name);
     auto go = [&](auto F, auto M, auto B) {
         k_pw_conv<F(), M(), B()><<<grid, 64, 0, s>>>(a.x, a.w, a.bias, a.z, part, C_in, C_out,
-                                                    HW, chunk, cpp, Kpad);
+                                                    HW, chunk, cpp, Kpad, rpw);
     };
     using P = std::integral_constant<int, kPlain>;
     using S = std::integral_constant<int, kStats>;
@@ -611,8 +628,9 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
         prof_end(s, tok);
         // dx = W^T dz: the forward kernel with dz as input and W^T as weights
         PwArgs fa{a.dz, wt, nullptr, a.dx};
-        hipError_t e = launch_pw_conv(fa, N, C_out, C_in, HW, chunk_dx, nullptr, accumulate_dx,
-                                      s, "pw_conv_dgrad");
+        hipError_t e = launch_pw_conv(fa, N, C_out, C_in, HW,
+                                      pw_pick_chunk(N, C_in, HW, chunk_dx), nullptr,
+                                      accumulate_dx, s, "pw_conv_dgrad");
         if (e != hipSuccess) return e;
     }
     if (a.dw || a.db) {

@@ -167,8 +167,18 @@ void AdamW::sync_tables() {
               "AdamW gradient table");
 }
 
+// One fill launch over the gradient table (the reference zeroes each
+// gradient in turn, adamw.cpp:20-26).
 void AdamW::zero_grad() {
-    for (auto& p : params_) p->zero_grad();
+    const int n = (int)params_.size();
+    if (n == 0) return;
+    sync_tables();
+    auto* t = static_cast<char*>(table_);
+    const size_t nb = (size_t)n * sizeof(void*);
+    check(soar_multi_tensor_fill_device(reinterpret_cast<float* const*>(t + nb),
+                                        reinterpret_cast<const int64_t*>(t + 4 * nb), n, 0.0f,
+                                        nullptr),
+          "zero_grad");
 }
 
 float AdamW::clip_grad_norm(float max_norm) {

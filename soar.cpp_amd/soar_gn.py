@@ -153,6 +153,7 @@ SIGNATURES = {
     "soar_multi_tensor_norm_workspace_bytes": (_SZ, []),
     "soar_multi_tensor_norm_sq_device": (_c.c_int, [_P, _P, _c.c_int, _P, _P, _SZ, _P]),
     "soar_multi_tensor_scale_device": (_c.c_int, [_P, _P, _c.c_int, _c.c_float, _P]),
+    "soar_multi_tensor_fill_device": (_c.c_int, [_P, _P, _c.c_int, _c.c_float, _P]),
 }
 
 SYNTH_SIGNATURES = {

@@ -278,9 +278,10 @@ static std::vector<float> to_float(const std::vector<double>& v) {
     return std::vector<float>(v.begin(), v.end());
 }
 
-// Conv2d on the device: pointwise (with bias, N = 2) and depthwise (k7 and
-// k3 stride 2), forward and backward through the engine, against float64
-// truth (layers.cpp:17-372 semantics: dx fresh, dW/db accumulated).
+// Conv2d on the device: pointwise (with bias, N = 2), depthwise (k7 and
+// k3 stride 2) and general grouped, forward and backward through the
+// engine, against float64 truth (layers.cpp:17-372 semantics: dx fresh,
+// dW/db accumulated).
 static void test_conv2d_layers() {
     memory::DeviceArena arena(256u << 20);
     memory::ArenaScope scope(arena);
@@ -335,10 +336,49 @@ static void test_conv2d_layers() {
         check_close("dw conv dW", conv.weight()->grad()->to_host(), dwt);
         check_close("dw conv db", conv.bias()->grad()->to_host(), dbt);
     }
-    // a general grouped convolution is not built on the device
-    nn::Conv2d general(8, 16, 3);
-    auto xg = Tensor::zeros({8, 10, 10}, false, true);
-    CHECK_THROWS(general.forward(xg), InvalidArgument);
+    // a general grouped convolution (groups 2, k3, stride 2, bias) against
+    // a direct float64 loop of its definition and of its adjoint
+    {
+        const int64_t Ci = 4, Co = 6, G = 2, K = 3, S = 2, P = 1, Hh = 9, Ww = 11;
+        const int64_t Ho = (Hh + 2 * P - K) / S + 1, Wo = (Ww + 2 * P - K) / S + 1;
+        nn::Conv2d general((size_t)Ci, (size_t)Co, (size_t)K, (size_t)S, -1, 1, (size_t)G, true);
+        std::vector<float> x(Ci * Hh * Ww), dy(Co * Ho * Wo), b(Co);
+        orc_fill_normal(x.data(), x.size(), 31, 1, 0.0, 1.0);
+        orc_fill_normal(dy.data(), dy.size(), 31, 2, 0.0, 1.0);
+        orc_fill_normal(b.data(), b.size(), 31, 3, 0.0, 0.5);
+        std::copy(b.begin(), b.end(), general.bias()->data());
+        const std::vector<float> w = host_copy(general.weight());
+        auto xt = Tensor::from_blob(x.data(), {Ci, Hh, Ww}, true, true);
+        auto y = general.forward(xt);
+        CHECK(y->shape() == (Shape{Co, Ho, Wo}));
+        const int64_t cig = Ci / G, cog = Co / G;
+        std::vector<double> yt(dy.size()), dxt(x.size(), 0.0), dwt(w.size(), 0.0), dbt(Co, 0.0);
+        for (int64_t co = 0; co < Co; ++co)
+            for (int64_t oy = 0; oy < Ho; ++oy)
+                for (int64_t ox = 0; ox < Wo; ++ox) {
+                    double acc = b[co];
+                    const double g = dy[(co * Ho + oy) * Wo + ox];
+                    dbt[co] += g;
+                    for (int64_t q = 0; q < cig; ++q)
+                        for (int64_t ky = 0; ky < K; ++ky)
+                            for (int64_t kx = 0; kx < K; ++kx) {
+                                const int64_t iy = oy * S - P + ky, ix = ox * S - P + kx;
+                                if (iy < 0 || iy >= Hh || ix < 0 || ix >= Ww) continue;
+                                const int64_t ci = (co / cog) * cig + q;
+                                const int64_t wi = ((co * cig + q) * K + ky) * K + kx;
+                                const int64_t xi = (ci * Hh + iy) * Ww + ix;
+                                acc += (double)w[wi] * x[xi];
+                                dxt[xi] += (double)w[wi] * g;
+                                dwt[wi] += (double)x[xi] * g;
+                            }
+                    yt[(co * Ho + oy) * Wo + ox] = acc;
+                }
+        check_close("general conv y", y->to_host(), yt);
+        y->backward(Tensor::from_blob(dy.data(), {Co, Ho, Wo}, false, true));
+        check_close("general conv dx", xt->grad()->to_host(), dxt);
+        check_close("general conv dW", general.weight()->grad()->to_host(), dwt);
+        check_close("general conv db", general.bias()->grad()->to_host(), dbt);
+    }
 }
 
 // CBA: pointwise (one fused call, GroupNorm statistics in the conv

@@ -7,18 +7,18 @@ signal), then forward logits, the Dice+BCE loss, every parameter gradient,
 two AdamW steps with gradient clipping, prediction and RLE, and the .soar
 round trip.
 
-Tolerances (fp32 device arithmetic against the float64 oracle):
-  * logits and losses: the device's fp32 forward runs ~70 normalised
-    layers; each contributes a relative error of order K * 2^-24 (K the
-    reduction length, <= a few thousand), so |dz| <= 2e-4 * (1 + |z|max)
-    and the losses within 1e-4 relative;
-  * gradients: per tensor, ||g - g_ref|| <= 2e-3 * ||g_ref|| + 1e-6 *
-    ||g_ref||_global (the backward doubles the depth and divides by small
-    GroupNorm spreads);
+Tolerances (fp32 device arithmetic against the float64 oracle; measured
+values on MI355X in brackets):
+  * logits and losses: the fp32 forward runs ~70 normalised layers, each
+    adding a relative error of order 2^-24 * sqrt(K) for its length-K
+    reductions, so |dz| <= 2e-5 * (1 + |z|max) [2.2e-6 at |z|max 1.7] and
+    the losses within 1e-5 relative;
+  * gradients: per tensor, ||g - g_ref|| <= 5e-5 * ||g_ref|| + 1e-7 *
+    ||g_ref||_global [worst tensor 2e-6 relative];
   * AdamW: bit-exact given the device's own gradients (the update is
     scalar fp32 arithmetic with no fused multiply-add on both sides);
-  * masks: identical wherever the oracle's probability is more than 1e-4
-    from the threshold; RLE: identical to the oracle's encoding of the
+  * probabilities within 1e-5; masks identical wherever the oracle's
+    probability is more than 1e-5 from the threshold; RLE: identical to the oracle's encoding of the
     device's mask.
 """
 import numpy as np
@@ -117,7 +117,7 @@ def test_forward_matches_oracle(sm, wfile, weights):
     ref = smr.Model(weights, requires_grad=False).forward(img).detach().numpy()
     err = np.abs(z - ref).max()
     print(f"  logits max|dz| = {err:.3e}  max|z| = {np.abs(ref).max():.3f}  rel = {rel(z, ref):.3e}")
-    assert err <= 2e-4 * (1 + np.abs(ref).max())
+    assert err <= 2e-5 * (1 + np.abs(ref).max())
 
 
 @pytest.mark.parametrize("h,w", [(32, 32), (40, 50), (96, 64)])
@@ -132,7 +132,7 @@ def test_forward_other_sizes(sm, wfile, weights, h, w):
     assert z.shape == (1, h, w)
     err = np.abs(z - ref).max()
     print(f"  max|dz| = {err:.3e}")
-    assert err <= 2e-4 * (1 + np.abs(ref).max())
+    assert err <= 2e-5 * (1 + np.abs(ref).max())
 
 
 def test_gradients_match_oracle(sm, wfile, weights):
@@ -142,14 +142,15 @@ def test_gradients_match_oracle(sm, wfile, weights):
     met = m.forward_backward(img, mask)
     lo, _, grads = smr.forward_backward(weights, img, mask)
     for k, v in (("loss", lo.total), ("bce", lo.bce), ("dice_loss", lo.dice)):
-        assert abs(met[k] - v) <= 1e-4 * abs(v) + 1e-6, (k, met[k], v)
+        print(f"  {k}: device {met[k]:.8f} oracle {v:.8f}")
+        assert abs(met[k] - v) <= 1e-5 * abs(v) + 1e-7, (k, met[k], v)
     gnorm = np.sqrt(sum(float(np.sum(g.astype(np.float64) ** 2)) for g in grads.values()))
     worst = []
     for i, (name, shape) in enumerate(m.tensors()):
         g = m.read(i, grad=True, shape=shape)
         ref = grads[name]
         d = float(np.linalg.norm(g.astype(np.float64) - ref))
-        bound = 2e-3 * float(np.linalg.norm(ref)) + 1e-6 * gnorm
+        bound = 5e-5 * float(np.linalg.norm(ref)) + 1e-7 * gnorm
         worst.append((d / max(bound, 1e-300), name, d, float(np.linalg.norm(ref))))
         assert d <= bound, (name, d, float(np.linalg.norm(ref)))
     worst.sort(reverse=True)
@@ -198,8 +199,8 @@ def test_predict_matches_oracle(sm, wfile, weights):
     probs, mask, rle = m.predict(img, threshold=0.5)
     z = smr.Model(weights, requires_grad=False).forward(img).detach().numpy()[0]
     p = 1.0 / (1.0 + np.exp(-z))
-    np.testing.assert_allclose(probs[0], p, rtol=0, atol=5e-5)
-    sure = np.abs(p - 0.5) > 1e-4
+    np.testing.assert_allclose(probs[0], p, rtol=0, atol=1e-5)
+    sure = np.abs(p - 0.5) > 1e-5
     np.testing.assert_array_equal(mask[sure], (p >= 0.5)[sure])
     assert rle == smr.encode_rle(mask, H, W)
     # the threshold moves the mask as it should
