@@ -260,8 +260,10 @@ SOAR_API int soar_adamw_step_multi_tensor(float** params, const float** grads,
 
 /* Device-table forms for callers that keep the table resident (e.g. the
  * parameter list of a model): the arrays themselves are DEVICE arrays of
- * n_tensors entries.  The pointers inside the table are not validated (the
- * table is not read on the host); only the arrays' own extents are.
+ * n_tensors entries (at most 2048 tensors; the summed chunk count of 4096
+ * elements must stay below 2^31).  The pointers inside the table are not
+ * validated (the table is not read on the host); only the arrays' own
+ * extents are.
  * No counterpart in the reference (its optimizer copies a host table per
  * launch, optimizer_kernels.cu:211-240). */
 SOAR_API int soar_adamw_multi_tensor_device(

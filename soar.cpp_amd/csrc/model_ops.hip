@@ -583,23 +583,86 @@ __global__ __launch_bounds__(kThreads) void k_sigmoid_threshold(const float* __r
 }
 
 // ---------------------------------------------------------------------------
-// Multi-tensor operators: every block walks every tensor with a grid
-// stride, so one launch covers the whole parameter list.
+// Multi-tensor operators.  The tensors are cut into chunks of kMtChunk
+// elements; every block first builds, in LDS, the prefix count of chunks
+// per tensor from the size table, then walks chunks blockIdx.x,
+// blockIdx.x + gridDim.x, ... and finds each chunk's tensor by binary
+// search.  Work is balanced over blocks whatever the tensor sizes, and no
+// block reads more of the table than the prologue does.
 // ---------------------------------------------------------------------------
 constexpr int kMultiBlocks = 512;
+constexpr int64_t kMtChunk = 4096;
+
+struct ChunkMap {
+    int* pref;  // LDS: pref[k] = chunks before tensor k, pref[n] = total
+    int n;
+    __device__ int total() const { return pref[n]; }
+    // tensor holding chunk c, and the chunk's first element in it
+    __device__ void locate(int c, int* k, int64_t* first) const {
+        int lo = 0, hi = n;  // pref[lo] <= c < pref[hi]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (pref[mid] <= c)
+                lo = mid;
+            else
+                hi = mid;
+        }
+        *k = lo;
+        *first = (int64_t)(c - pref[lo]) * kMtChunk;
+    }
+};
+
+// Builds the chunk prefix of `numel` (n <= kMaxMultiTensors) in `pref`.
+__device__ ChunkMap build_chunk_map(const int64_t* __restrict__ numel, int n, int* pref) {
+    const int t = threadIdx.x;
+    constexpr int kSeg = (kMaxMultiTensors + kThreads - 1) / kThreads;
+    // each thread counts a contiguous segment, then a scan over the 256
+    // segment totals gives each segment's offset
+    __shared__ int seg[kThreads];
+    int local[kSeg];
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < kSeg; ++i) {
+        const int k = t * kSeg + i;
+        const int c = k < n ? (int)((numel[k] + kMtChunk - 1) / kMtChunk) : 0;
+        local[i] = c;
+        sum += c;
+    }
+    seg[t] = sum;
+    __syncthreads();
+    for (int off = 1; off < kThreads; off <<= 1) {  // inclusive Hillis-Steele scan
+        const int v = t >= off ? seg[t - off] : 0;
+        __syncthreads();
+        seg[t] += v;
+        __syncthreads();
+    }
+    int run = seg[t] - sum;  // exclusive prefix of this segment
+#pragma unroll
+    for (int i = 0; i < kSeg; ++i) {
+        const int k = t * kSeg + i;
+        if (k < n) pref[k] = run;
+        run += local[i];
+    }
+    if (t == kThreads - 1) pref[n] = seg[kThreads - 1];
+    __syncthreads();
+    return ChunkMap{pref, n};
+}
 
 __global__ __launch_bounds__(kThreads) void k_multi_norm_sq(const float* const* __restrict__ t,
                                                             const int64_t* __restrict__ numel,
                                                             int n_tensors,
                                                             double* __restrict__ part) {
+    __shared__ int pref[kMaxMultiTensors + 1];
     __shared__ double sh[kThreads];
+    const ChunkMap map = build_chunk_map(numel, n_tensors, pref);
     double s = 0.0;
-    const int64_t start = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int k = 0; k < n_tensors; ++k) {
+    for (int c = blockIdx.x; c < map.total(); c += gridDim.x) {
+        int k;
+        int64_t first;
+        map.locate(c, &k, &first);
         const float* p = t[k];
-        const int64_t n = numel[k];
-        for (int64_t i = start; i < n; i += stride) {
+        const int64_t end = min(first + kMtChunk, numel[k]);
+        for (int64_t i = first + threadIdx.x; i < end; i += kThreads) {
             const double v = p[i];
             s += v * v;
         }
@@ -608,36 +671,30 @@ __global__ __launch_bounds__(kThreads) void k_multi_norm_sq(const float* const* 
     if (threadIdx.x == 0) part[blockIdx.x] = s;
 }
 
-__global__ __launch_bounds__(64) void k_multi_norm_finish(const double* __restrict__ part,
-                                                          int nparts, double* __restrict__ out) {
-    if (threadIdx.x == 0) {
-        double s = 0.0;
-        for (int b = 0; b < nparts; ++b) s += part[b];
-        out[0] = s;
-    }
+__global__ __launch_bounds__(kThreads) void k_multi_norm_finish(const double* __restrict__ part,
+                                                                int nparts,
+                                                                double* __restrict__ out) {
+    __shared__ double sh[kThreads];
+    double s = 0.0;
+    for (int b = threadIdx.x; b < nparts; b += kThreads) s += part[b];
+    s = block_sum(s, sh);
+    if (threadIdx.x == 0) out[0] = s;
 }
 
-__global__ __launch_bounds__(kThreads) void k_multi_scale(float* const* __restrict__ t,
-                                                          const int64_t* __restrict__ numel,
-                                                          int n_tensors, float scale) {
-    const int64_t start = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int k = 0; k < n_tensors; ++k) {
+// t[k][i] = value (FILL) or t[k][i] *= value
+template <bool FILL>
+__global__ __launch_bounds__(kThreads) void k_multi_set(float* const* __restrict__ t,
+                                                        const int64_t* __restrict__ numel,
+                                                        int n_tensors, float value) {
+    __shared__ int pref[kMaxMultiTensors + 1];
+    const ChunkMap map = build_chunk_map(numel, n_tensors, pref);
+    for (int c = blockIdx.x; c < map.total(); c += gridDim.x) {
+        int k;
+        int64_t first;
+        map.locate(c, &k, &first);
         float* p = t[k];
-        const int64_t n = numel[k];
-        for (int64_t i = start; i < n; i += stride) p[i] *= scale;
-    }
-}
-
-__global__ __launch_bounds__(kThreads) void k_multi_fill(float* const* __restrict__ t,
-                                                         const int64_t* __restrict__ numel,
-                                                         int n_tensors, float value) {
-    const int64_t start = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int k = 0; k < n_tensors; ++k) {
-        float* p = t[k];
-        const int64_t n = numel[k];
-        for (int64_t i = start; i < n; i += stride) p[i] = value;
+        const int64_t end = min(first + kMtChunk, numel[k]);
+        for (int64_t i = first + threadIdx.x; i < end; i += kThreads) p[i] = FILL ? value : p[i] * value;
     }
 }
 
@@ -649,17 +706,20 @@ __global__ __launch_bounds__(kThreads) void k_adamw_multi(
     float* const* __restrict__ V, const int64_t* __restrict__ numel, int n_tensors, float lr,
     float beta1, float beta2, float eps, float wd, float step_size, float sqrt_bc2) {
 #pragma clang fp contract(off)
-    const int64_t start = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    __shared__ int pref[kMaxMultiTensors + 1];
+    const ChunkMap map = build_chunk_map(numel, n_tensors, pref);
     const float one_m_b1 = 1.0f - beta1, one_m_b2 = 1.0f - beta2;
     const float lr_wd = lr * wd;
-    for (int k = 0; k < n_tensors; ++k) {
+    for (int c = blockIdx.x; c < map.total(); c += gridDim.x) {
+        int k;
+        int64_t first;
+        map.locate(c, &k, &first);
         float* theta = P[k];
         const float* g = G[k];
         float* m = M[k];
         float* v = V[k];
-        const int64_t n = numel[k];
-        for (int64_t i = start; i < n; i += stride) {
+        const int64_t end = min(first + kMtChunk, numel[k]);
+        for (int64_t i = first + threadIdx.x; i < end; i += kThreads) {
             const float gv = g[i];
             float th = theta[i];
             if (wd != 0.0f) th = th - lr_wd * th;
@@ -868,19 +928,19 @@ hipError_t launch_multi_norm_sq(const float* const* t, const int64_t* numel, int
     k_multi_norm_sq<<<kMultiBlocks, kThreads, 0, s>>>(t, numel, n_tensors, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_multi_norm_finish<<<1, 64, 0, s>>>(part, kMultiBlocks, out);
+    k_multi_norm_finish<<<1, kThreads, 0, s>>>(part, kMultiBlocks, out);
     return hipGetLastError();
 }
 
 hipError_t launch_multi_scale(float* const* t, const int64_t* numel, int n_tensors, float scale,
                               hipStream_t s) {
-    k_multi_scale<<<kMultiBlocks, kThreads, 0, s>>>(t, numel, n_tensors, scale);
+    k_multi_set<false><<<kMultiBlocks, kThreads, 0, s>>>(t, numel, n_tensors, scale);
     return hipGetLastError();
 }
 
 hipError_t launch_multi_fill(float* const* t, const int64_t* numel, int n_tensors, float value,
                              hipStream_t s) {
-    k_multi_fill<<<kMultiBlocks, kThreads, 0, s>>>(t, numel, n_tensors, value);
+    k_multi_set<true><<<kMultiBlocks, kThreads, 0, s>>>(t, numel, n_tensors, value);
     return hipGetLastError();
 }
 

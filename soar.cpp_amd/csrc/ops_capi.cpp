@@ -234,6 +234,9 @@ int table_buffer(size_t need, void** out) {
 }
 
 int check_table(const void* arr, int n_tensors, const char* name) {
+    if (n_tensors > soar::ops::kMaxMultiTensors)
+        return fail(SOAR_EINVAL, "%d tensors exceed the multi-tensor limit of %d", n_tensors,
+                    soar::ops::kMaxMultiTensors);
     return check_dev(arr, (size_t)n_tensors * 8, name);
 }
 
@@ -686,12 +689,14 @@ SOAR_API int soar_adamw_step_multi_tensor(float** params, const float** grads, f
                                           float lr, float beta1, float beta2, float eps, float wd,
                                           float step_size, float sqrt_bc2, void* stream) {
     if (n_tensors == 0) return ok();
-    if (n_tensors < 0 || !params || !grads || !m || !v || !numel)
-        return fail(SOAR_EINVAL, "adamw_step_multi_tensor: bad table");
+    if (n_tensors < 0 || n_tensors > soar::ops::kMaxMultiTensors || !params || !grads || !m ||
+        !v || !numel)
+        return fail(SOAR_EINVAL, "adamw_step_multi_tensor: bad table (at most %d tensors)",
+                    soar::ops::kMaxMultiTensors);
     int rc;
     if ((rc = require_device())) return rc;
     for (int k = 0; k < n_tensors; ++k) {
-        if (numel[k] < 0 || numel[k] > INT64_MAX / 8)
+        if (numel[k] < 0 || numel[k] > ((int64_t)1 << 42))
             return fail(SOAR_EINVAL, "adamw_step_multi_tensor: numel[%d] is invalid", k);
         if (numel[k] == 0) continue;
         const size_t b = (size_t)numel[k] * 4;
@@ -699,6 +704,10 @@ SOAR_API int soar_adamw_step_multi_tensor(float** params, const float** grads, f
             (rc = check_dev(m[k], b, "m[k]")) || (rc = check_dev(v[k], b, "v[k]")))
             return fail(rc, "adamw_step_multi_tensor: tensor %d: %s", k, g_err.c_str());
     }
+    int64_t chunks = 0;
+    for (int k = 0; k < n_tensors; ++k) chunks += (numel[k] + 4095) / 4096;
+    if (chunks >= ((int64_t)1 << 31))
+        return fail(SOAR_EINVAL, "adamw_step_multi_tensor: too many elements for one launch");
     const size_t nb = (size_t)n_tensors * 8;
     void* buf = nullptr;
     if ((rc = table_buffer(5 * nb, &buf))) return rc;

@@ -86,7 +86,9 @@ hipError_t launch_dice_bce_backward(const float* z, const float* y, float* gz, i
 hipError_t launch_sigmoid_threshold(const float* z, float* p, uint8_t* mask, int64_t n,
                                     float threshold, hipStream_t s);
 
-// Multi-tensor operators over device arrays of tensor pointers and sizes.
+// Multi-tensor operators over device arrays of tensor pointers and sizes
+// (at most kMaxMultiTensors tensors, each under 2^31 * 4096 elements).
+constexpr int kMaxMultiTensors = 2048;
 size_t multi_norm_workspace_bytes();
 hipError_t launch_multi_norm_sq(const float* const* t, const int64_t* numel, int n_tensors,
                                 double* out, void* ws, hipStream_t s);

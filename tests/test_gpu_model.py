@@ -157,6 +157,27 @@ def test_gradients_match_oracle(sm, wfile, weights):
     print("  worst gradient ratios:", [(f"{w[0]:.3f}", w[1]) for w in worst[:4]])
 
 
+@pytest.mark.parametrize("h,w,c", [(40, 50, 1), (64, 64, 3)])
+def test_gradients_other_shapes(sm, tmp_path, h, w, c):
+    """Gradients through the reflection pad / crop (40 x 50) and with a
+    3-channel stem (the general convolution's C_in > 1)."""
+    print(f"case: forward_backward {c}x{h}x{w}", flush=True)
+    spec = smr.model_spec(c, 1, 0)
+    wts = smr.random_weights(spec, SEED + c)
+    f = tmp_path / "w.soar"
+    smr.write_soar(f, [(n, wts[n]) for n, _, _ in spec])
+    m = sm.SOAR(c, 1, "nano", seed=2)
+    m.load_weights(str(f))
+    img, mask = sample(9, h, w, c)
+    met = m.forward_backward(img, mask)
+    lo, _, grads = smr.forward_backward(wts, img, mask)
+    assert abs(met["loss"] - lo.total) <= 1e-5 * abs(lo.total)
+    gnorm = np.sqrt(sum(float(np.sum(g.astype(np.float64) ** 2)) for g in grads.values()))
+    for i, (name, shape) in enumerate(m.tensors()):
+        d = float(np.linalg.norm(m.read(i, grad=True, shape=shape).astype(np.float64) - grads[name]))
+        assert d <= 5e-5 * float(np.linalg.norm(grads[name])) + 1e-7 * gnorm, name
+
+
 def test_two_train_steps_match_adamw(sm, wfile):
     """train_step = clip(2.0) + AdamW + zero_grad on the step's gradients:
     bit-exact against the scalar fp32 update on the device's gradients,

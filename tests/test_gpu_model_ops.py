@@ -1,0 +1,407 @@
+"""The model operators of include/soar_ops.h on the MI355X, one by one,
+through the C-ABI, against float64 statements of the reference's formulas.
+
+Bars: index permutations (pixel shuffle, pad, crop, fill) bit-exact;
+elementwise fp32 formulas within a few ulps of float64; reductions
+(conv, pooling, loss sums, norms) within (K+2) * 2^-24 * sum|terms| for a
+K-term sum; AdamW bit-exact against scalar fp32 (numpy) arithmetic.
+Backward entry points add into their outputs, so every gradient buffer is
+pre-filled with a known value and the test checks output - prefill.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import soar_model_ref as smr
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+U32 = 2.0 ** -24
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    import soar_gn
+    soar_gn.lib()
+    return soar_gn, torch
+
+
+def dev(torch, a):
+    return torch.tensor(np.ascontiguousarray(a, dtype=F32), device="cuda")
+
+
+def P(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def host(torch, t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def ok(gn, rc):
+    assert rc == 0, gn.last_error()
+
+
+# ---- general grouped convolution ---------------------------------------------
+def conv_ref(x, w, b, S, pad, D, G):
+    """float64 direct convolution (and the magnitudes for the bound)."""
+    N, Ci, H, W = x.shape
+    Co, cig, K, _ = w.shape
+    Ho = (H + 2 * pad - D * (K - 1) - 1) // S + 1
+    Wo = (W + 2 * pad - D * (K - 1) - 1) // S + 1
+    xp = np.zeros((N, Ci, H + 2 * pad, W + 2 * pad))
+    xp[:, :, pad:pad + H, pad:pad + W] = x
+    y = np.zeros((N, Co, Ho, Wo))
+    mag = np.zeros_like(y)
+    cog = Co // G
+    for co in range(Co):
+        g = co // cog
+        for q in range(cig):
+            for ky in range(K):
+                for kx in range(K):
+                    sl = xp[:, g * cig + q, ky * D: ky * D + S * (Ho - 1) + 1: S,
+                            kx * D: kx * D + S * (Wo - 1) + 1: S]
+                    y[:, co] += w[co, q, ky, kx] * sl
+                    mag[:, co] += abs(w[co, q, ky, kx]) * np.abs(sl)
+    if b is not None:
+        y += b[None, :, None, None]
+        mag += np.abs(b)[None, :, None, None]
+    return y, mag
+
+
+@pytest.mark.parametrize("N,Ci,Co,H,W,K,S,D,G,bias", [
+    (1, 1, 16, 64, 64, 3, 2, 1, 1, False),   # the model's stem
+    (2, 3, 16, 33, 47, 3, 2, 1, 1, True),    # odd sizes, RGB stem
+    (1, 8, 12, 20, 18, 3, 1, 2, 4, True),    # grouped, dilated
+    (1, 6, 6, 11, 9, 5, 3, 1, 2, False),     # stride 3, K 5
+])
+def test_general_conv(env, N, Ci, Co, H, W, K, S, D, G, bias):
+    gn, torch = env
+    print(f"case: conv N={N} {Ci}->{Co} {H}x{W} K={K} S={S} D={D} G={G}", flush=True)
+    r = np.random.default_rng(H * W + K)
+    pad = smr.autopad(K, -1, D)
+    x = r.normal(size=(N, Ci, H, W)).astype(F32)
+    w = r.uniform(-0.5, 0.5, size=(Co, Ci // G, K, K)).astype(F32)
+    b = r.normal(size=Co).astype(F32) if bias else None
+    y_ref, mag = conv_ref(x.astype(np.float64), w.astype(np.float64),
+                          None if b is None else b.astype(np.float64), S, pad, D, G)
+    Ho, Wo = y_ref.shape[2:]
+    L = gn.lib()
+    xd, wd = dev(torch, x), dev(torch, w)
+    bd = dev(torch, b) if bias else None
+    yd = torch.empty((N, Co, Ho, Wo), device="cuda")
+    ok(gn, L.soar_conv_forward(P(xd), P(wd), P(bd) if bias else None, P(yd), N, Ci, Co, H, W,
+                               Ho, Wo, K, pad, S, D, G, None))
+    nterm = Ci // G * K * K + 2
+    assert np.all(np.abs(host(torch, yd) - y_ref) <= nterm * U32 * mag + 1e-30)
+    # backward: the adjoint identities against float64 and a direct dW
+    dy = r.normal(size=(N, Co, Ho, Wo)).astype(F32)
+    dyd = dev(torch, dy)
+    dx = torch.full((N, Ci, H, W), 0.25, device="cuda")
+    dw = torch.full(w.shape, -1.0, device="cuda")
+    db = torch.full((Co,), 2.0, device="cuda")
+    wsb = L.soar_conv_backward_workspace_bytes(N, Ci, Co, H, W, Ho, Wo, K, pad, S, D, G)
+    ws = torch.empty(max(wsb, 8), dtype=torch.uint8, device="cuda")
+    ok(gn, L.soar_conv_backward(P(dyd), P(xd), P(wd), P(dx), P(dw), P(db), N, Ci, Co, H, W, Ho,
+                                Wo, K, pad, S, D, G, gn.GN_ACCUMULATE_DX, P(ws), wsb, None))
+    dxh = host(torch, dx).astype(np.float64) - 0.25
+    dwh = host(torch, dw).astype(np.float64) + 1.0
+    dbh = host(torch, db).astype(np.float64) - 2.0
+    # <conv(x), dy> = <x, dx> + <b, db> identities, each term in float64
+    y0, _ = conv_ref(x.astype(np.float64), w.astype(np.float64), None, S, pad, D, G)
+    lhs = float(np.sum(y0 * dy))
+    assert abs(float(np.sum(x * dxh)) - lhs) <= 1e-4 * np.sum(np.abs(y0 * dy))
+    assert abs(float(np.sum(w * dwh)) - lhs) <= 1e-4 * np.sum(np.abs(y0 * dy))
+    np.testing.assert_allclose(dbh, dy.astype(np.float64).sum(axis=(0, 2, 3)), rtol=1e-5,
+                               atol=1e-4)
+    # dW directly: dW[co,q,ky,kx] = sum dy * shifted x (float64)
+    xp = np.zeros((N, Ci, H + 2 * pad, W + 2 * pad))
+    xp[:, :, pad:pad + H, pad:pad + W] = x
+    cog = Co // G
+    for co in (0, Co - 1):
+        for q in range(Ci // G):
+            ci = (co // cog) * (Ci // G) + q
+            for ky in range(K):
+                for kx in range(K):
+                    sl = xp[:, ci, ky * D: ky * D + S * (Ho - 1) + 1: S,
+                            kx * D: kx * D + S * (Wo - 1) + 1: S]
+                    t = float(np.sum(dy[:, co] * sl))
+                    m = float(np.sum(np.abs(dy[:, co] * sl)))
+                    assert abs(dwh[co, q, ky, kx] - t) <= (N * Ho * Wo + 3) * U32 * m + 1e-6
+
+
+def dw_ones(x):
+    """dW of the stem conv (16 outputs, k3 s2 p1) for dy = 1: per tap, the
+    sum of the input pixels that tap reads."""
+    xp = np.zeros((34, 34))
+    xp[1:33, 1:33] = x[0, 0]
+    t = np.array([[xp[ky:ky + 31:2, kx:kx + 31:2].sum() for kx in range(3)] for ky in range(3)])
+    return np.broadcast_to(t, (16, 1, 3, 3))
+
+
+def test_conv_reference_signature(env):
+    """soar_conv2d_forward/backward (one sample, library workspace, all
+    gradients added)."""
+    gn, torch = env
+    L = gn.lib()
+    r = np.random.default_rng(5)
+    x = r.normal(size=(1, 1, 32, 32)).astype(F32)
+    w = r.uniform(-0.5, 0.5, size=(16, 1, 3, 3)).astype(F32)
+    y_ref, mag = conv_ref(x.astype(np.float64), w.astype(np.float64), None, 2, 1, 1, 1)
+    xd, wd = dev(torch, x), dev(torch, w)
+    yd = torch.empty((16, 16, 16), device="cuda")
+    ok(gn, L.soar_conv2d_forward(P(xd), P(wd), None, P(yd), 1, 16, 32, 32, 16, 16, 3, 1, 2, 1, 1,
+                                 None))
+    assert np.all(np.abs(host(torch, yd) - y_ref[0]) <= 11 * U32 * mag[0] + 1e-30)
+    dy = dev(torch, np.ones((16, 16, 16), F32))
+    dx = torch.zeros((1, 32, 32), device="cuda")
+    dw = torch.zeros((16, 1, 3, 3), device="cuda")
+    ok(gn, L.soar_conv2d_backward(P(dy), P(xd), P(wd), P(dx), P(dw), None, 1, 16, 32, 32, 16, 16,
+                                  3, 1, 2, 1, 1, None))
+    ok(gn, L.soar_conv2d_backward(P(dy), P(xd), P(wd), P(dx), P(dw), None, 1, 16, 32, 32, 16, 16,
+                                  3, 1, 2, 1, 1, None))
+    # two calls add twice; with dy = 1, dx at an input pixel is the sum of
+    # the taps that reach it: at stride 2 / pad 1, rows and columns 5 are
+    # reached by taps 0 and 2, rows and columns 4 by tap 1 only
+    dx1 = host(torch, dx) / 2
+    assert abs(float(dx1[0, 5, 5]) - float(w[:, 0, ::2, ::2].sum())) < 1e-5
+    assert abs(float(dx1[0, 4, 4]) - float(w[:, 0, 1, 1].sum())) < 1e-5
+    np.testing.assert_allclose(host(torch, dw) / 2, dw_ones(x), rtol=1e-5, atol=1e-4)
+
+
+# ---- elementwise / per-plane -------------------------------------------------------
+def test_sigmoid_convex_broadcast_pool(env):
+    gn, torch = env
+    L = gn.lib()
+    r = np.random.default_rng(6)
+    n = 10007
+    x = (r.normal(size=n) * 8).astype(F32)
+    xd, yd = dev(torch, x), torch.empty(n, device="cuda")
+    ok(gn, L.soar_sigmoid_forward(P(xd), P(yd), n, None))
+    y = host(torch, yd)
+    yt = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+    assert np.all(np.abs(y - yt) <= 4 * U32 * yt + 1e-38)
+    gy = r.normal(size=n).astype(F32)
+    gx = torch.full((n,), 1.0, device="cuda")
+    ok(gn, L.soar_sigmoid_backward(P(dev(torch, gy)), P(yd), P(gx), n, None))
+    gxt = 1.0 + gy * y.astype(np.float64) * (1.0 - y)
+    np.testing.assert_allclose(host(torch, gx), gxt, rtol=1e-6, atol=1e-7)
+
+    a, b, g = (r.normal(size=n).astype(F32) for _ in range(3))
+    ad, bd, gd = dev(torch, a), dev(torch, b), dev(torch, g)
+    ok(gn, L.soar_convex_combination_forward(P(gd), P(ad), P(bd), P(yd), n, None))
+    np.testing.assert_allclose(host(torch, yd), g.astype(np.float64) * a + (1 - g.astype(np.float64)) * b,
+                               rtol=1e-6, atol=1e-6)
+    ga, gb, gg = (torch.zeros(n, device="cuda") for _ in range(3))
+    ok(gn, L.soar_convex_combination_backward(P(dev(torch, gy)), P(gd), P(ad), P(bd), P(gg), P(ga),
+                                              P(gb), n, None))
+    np.testing.assert_allclose(host(torch, ga), gy * g.astype(np.float64), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(host(torch, gb), gy * (1 - g.astype(np.float64)), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(host(torch, gg), gy * (a.astype(np.float64) - b), rtol=1e-6, atol=1e-6)
+
+    C, HW = 37, 1023
+    A = r.normal(size=(C, HW)).astype(F32)
+    B = r.normal(size=C).astype(F32)
+    Ad, Bd, Yd = dev(torch, A), dev(torch, B), torch.empty((C, HW), device="cuda")
+    ok(gn, L.soar_mul_broadcast_forward(P(Ad), P(Bd), P(Yd), C, HW, None))
+    np.testing.assert_array_equal(host(torch, Yd), A * B[:, None])
+    GY = r.normal(size=(C, HW)).astype(F32)
+    GA, GB = torch.zeros((C, HW), device="cuda"), torch.full((C,), 3.0, device="cuda")
+    ok(gn, L.soar_mul_broadcast_backward(P(dev(torch, GY)), P(Ad), P(Bd), P(GA), P(GB), C, HW, None))
+    np.testing.assert_array_equal(host(torch, GA), GY * B[:, None])
+    gbt = (GY.astype(np.float64) * A).sum(axis=1)
+    assert np.all(np.abs(host(torch, GB) - 3.0 - gbt) <= 4 * U32 * (np.abs(GY * A).sum(axis=1) + 3))
+
+    pooled = torch.empty(C, device="cuda")
+    ok(gn, L.soar_global_avg_pool_forward(P(Ad), P(pooled), C, HW, None))
+    np.testing.assert_allclose(host(torch, pooled), A.astype(np.float64).mean(axis=1), rtol=1e-6,
+                               atol=1e-7)
+    gi = torch.zeros((C, HW), device="cuda")
+    ok(gn, L.soar_global_avg_pool_backward(P(Bd), P(gi), C, HW, None))
+    np.testing.assert_allclose(host(torch, gi), np.broadcast_to((B / F32(HW))[:, None], (C, HW)),
+                               rtol=1e-7)
+
+
+@pytest.mark.parametrize("C,H,W,Ho,Wo", [(3, 2, 2, 4, 4), (5, 4, 4, 16, 16), (2, 7, 5, 14, 10),
+                                         (2, 6, 9, 9, 13), (1, 32, 32, 64, 64)])
+def test_upsample(env, C, H, W, Ho, Wo):
+    """Forward and the gathered backward against float64 loops of the
+    reference's index arithmetic (fp32 source coordinates)."""
+    gn, torch = env
+    L = gn.lib()
+    r = np.random.default_rng(H * Ho)
+    x = r.normal(size=(C, H, W)).astype(F32)
+    xd, yd = dev(torch, x), torch.empty((C, Ho, Wo), device="cuda")
+    ok(gn, L.soar_upsample_bilinear_forward(P(xd), P(yd), C, H, W, Ho, Wo, None))
+    sy, sx = F32(H) / F32(Ho), F32(W) / F32(Wo)
+
+    def taps(sc, d, n):
+        f = max(F32(sc * (F32(d) + F32(0.5)) - F32(0.5)), F32(0))
+        i0 = min(int(f), n - 1)
+        i1 = i0 + (1 if i0 < n - 1 else 0)
+        l1 = float(f) - i0
+        return i0, i1, 1 - l1, l1
+
+    yt = np.zeros((C, Ho, Wo))
+    gt = np.zeros((C, H, W))
+    go = r.normal(size=(C, Ho, Wo))
+    for y in range(Ho):
+        y0, y1, a0, a1 = taps(sy, y, H)
+        for xx in range(Wo):
+            x0, x1, b0, b1 = taps(sx, xx, W)
+            yt[:, y, xx] = (a0 * (b0 * x[:, y0, x0] + b1 * x[:, y0, x1]) +
+                            a1 * (b0 * x[:, y1, x0] + b1 * x[:, y1, x1]))
+            for (yy, wy) in ((y0, a0), (y1, a1)):
+                for (xs, wx) in ((x0, b0), (x1, b1)):
+                    gt[:, yy, xs] += wy * wx * go[:, y, xx]
+    np.testing.assert_allclose(host(torch, yd), yt, rtol=1e-6, atol=1e-6)
+    gi = torch.full((C, H, W), -0.5, device="cuda")
+    ok(gn, L.soar_upsample_bilinear_backward(P(dev(torch, go)), P(gi), C, H, W, Ho, Wo, None))
+    np.testing.assert_allclose(host(torch, gi) + 0.5, gt, rtol=1e-5, atol=2e-5)
+
+
+def test_pixel_shuffle_pad_crop(env):
+    gn, torch = env
+    L = gn.lib()
+    r = np.random.default_rng(7)
+    x = r.normal(size=(8, 5, 3)).astype(F32)
+    xd, yd = dev(torch, x), torch.empty((2, 10, 6), device="cuda")
+    ok(gn, L.soar_pixel_shuffle_forward(P(xd), P(yd), 8, 5, 3, 2, None))
+    ref = torch.nn.functional.pixel_shuffle(torch.tensor(x)[None], 2)[0].numpy()
+    np.testing.assert_array_equal(host(torch, yd), ref)
+    gx = torch.full((8, 5, 3), 1.0, device="cuda")
+    ok(gn, L.soar_pixel_shuffle_backward(P(yd), P(gx), 8, 5, 3, 2, None))
+    np.testing.assert_array_equal(host(torch, gx), x + F32(1.0))
+    assert L.soar_pixel_shuffle_forward(P(xd), P(yd), 6, 5, 3, 2, None) == gn.SOAR_EINVAL
+
+    for (H, W, ph, pw) in ((5, 7, 3, 1), (2, 3, 30, 29)):
+        x = r.normal(size=(2, H, W)).astype(F32)
+        t = torch.tensor(x[None].astype(np.float64), requires_grad=True)
+        pt = smr.pad_spatial(t, ph, pw)
+        xd = dev(torch, x)
+        out = torch.empty((2, H + ph, W + pw), device="cuda")
+        ok(gn, L.soar_pad_spatial_forward(P(xd), P(out), 2, H, W, ph, pw, None))
+        np.testing.assert_array_equal(host(torch, out), pt.detach().numpy()[0].astype(F32))
+        go = r.normal(size=(2, H + ph, W + pw)).astype(F32)
+        pt.backward(torch.tensor(go[None].astype(np.float64)))
+        gi = torch.zeros((2, H, W), device="cuda")
+        ok(gn, L.soar_pad_spatial_backward(P(dev(torch, go)), P(gi), 2, H, W, ph, pw, None))
+        np.testing.assert_allclose(host(torch, gi), t.grad.numpy()[0], rtol=1e-6, atol=1e-6)
+        crop = torch.empty((2, H, W), device="cuda")
+        ok(gn, L.soar_unpad_spatial_forward(P(out), P(crop), 2, H + ph, W + pw, H, W, None))
+        np.testing.assert_array_equal(host(torch, crop), x)
+        gp = torch.full((2, H + ph, W + pw), 1.0, device="cuda")
+        ok(gn, L.soar_unpad_spatial_backward(P(xd), P(gp), 2, H + ph, W + pw, H, W, None))
+        exp = np.ones((2, H + ph, W + pw), F32)
+        exp[:, :H, :W] += x
+        np.testing.assert_array_equal(host(torch, gp), exp)
+
+
+# ---- losses ------------------------------------------------------------------------
+def test_losses(env):
+    gn, torch = env
+    L = gn.lib()
+    r = np.random.default_rng(8)
+    n = 64 * 64
+    z = (r.normal(size=n) * 3).astype(F32)
+    y = (r.uniform(size=n) < 0.3).astype(F32)
+    zd, yd = dev(torch, z), dev(torch, y)
+    out = (ctypes.c_float * 6)()
+    ok(gn, L.soar_dice_bce_loss_forward(P(zd), P(yd), n, 1.0, 0.5, 0.5, 3.0, 1.0, out, None))
+    lo = smr.dice_bce_forward(z, y)
+    vals = list(out)
+    for got, want in zip(vals, (lo.total, lo.bce, lo.dice, lo.inter, lo.sum_p, lo.sum_y)):
+        assert abs(got - want) <= 2e-6 * abs(want) + 1e-7, (got, want)
+    f = ctypes.c_float()
+    ok(gn, L.soar_bce_with_logits_forward(P(zd), P(yd), 2.0, 3.0, n, ctypes.byref(f), None))
+    assert abs(f.value - 2 * lo.bce) <= 2e-6 * lo.bce
+    # (gradients are ~1e-6 here: accumulate onto zeros, then a second call
+    # doubles them, rather than subtract a large prefill)
+    gz = torch.zeros(n, device="cuda")
+    ok(gn, L.soar_dice_bce_loss_backward(P(zd), P(yd), P(gz), 1.0, 1.0, 0.5, 0.5, 3.0, 1.0,
+                                         vals[3], vals[4], vals[5], n, None))
+    st = smr.LossOut(0, 0, 0, vals[3], vals[4], vals[5])
+    g = smr.dice_bce_grad(z, y, st)
+    # fp32 bound of the reference's formula (loss_kernels.cu:234-246): its
+    # sums cancel (3*sig - 3 as sig -> 1, 2y*denom - numer), so the bound
+    # is in the magnitudes of their terms
+    z64, y64 = z.astype(np.float64), y.astype(np.float64)
+    sig = 1.0 / (1.0 + np.exp(-z64))
+    denom = st.sum_p + st.sum_y + 1.0
+    numer = 2.0 * st.inter + 1.0
+    mag = ((sig * (1 + 2 * y64) + 3 * y64) * 0.5 / n +
+           0.5 * (2 * y64 * denom + numer) / denom ** 2 * sig * (1 - sig))
+    g1 = host(torch, gz)
+    assert np.all(np.abs(g1 - g) <= 16 * U32 * mag)
+    ok(gn, L.soar_dice_bce_loss_backward(P(zd), P(yd), P(gz), 1.0, 1.0, 0.5, 0.5, 3.0, 1.0,
+                                         vals[3], vals[4], vals[5], n, None))
+    np.testing.assert_array_equal(host(torch, gz), g1 + g1)
+    p = torch.empty(n, device="cuda")
+    m = torch.empty(n, dtype=torch.uint8, device="cuda")
+    ok(gn, L.soar_sigmoid_threshold(P(zd), P(p), P(m), n, 0.5, None))
+    pt = 1.0 / (1.0 + np.exp(-z.astype(np.float64)))
+    np.testing.assert_allclose(host(torch, p), pt, rtol=1e-6, atol=1e-7)
+    np.testing.assert_array_equal(host(torch, m), (z >= 0).astype(np.uint8))
+
+
+# ---- AdamW and multi-tensor ---------------------------------------------------------
+def test_adamw_and_multi_tensor(env):
+    gn, torch = env
+    L = gn.lib()
+    r = np.random.default_rng(9)
+    sizes = [1, 3, 4095, 4096, 4097, 70000, 16, 0, 300000] + [int(s) for s in r.integers(1, 5000, 200)]
+    th = [r.normal(size=s).astype(F32) for s in sizes]
+    g = [(r.normal(size=s) * 10.0 ** r.uniform(-4, 1)).astype(F32) for s in sizes]
+    td = [dev(torch, a) if a.size else torch.empty(1, device="cuda") for a in th]
+    gd = [dev(torch, a) if a.size else torch.empty(1, device="cuda") for a in g]
+    md = [torch.zeros(max(s, 1), device="cuda") for s in sizes]
+    vd = [torch.zeros(max(s, 1), device="cuda") for s in sizes]
+    n = len(sizes)
+    arr = lambda ts: (ctypes.c_void_p * n)(*[t.data_ptr() for t in ts])  # noqa: E731
+    numel = (ctypes.c_int64 * n)(*sizes)
+    m_ref = [np.zeros(s, F32) for s in sizes]
+    v_ref = [np.zeros(s, F32) for s in sizes]
+    for step in (1, 2, 3):
+        lr = 1e-3 / step
+        b1c = F32(1) - np.power(F32(0.9), F32(step), dtype=F32)
+        b2c = F32(1) - np.power(F32(0.999), F32(step), dtype=F32)
+        ok(gn, L.soar_adamw_step_multi_tensor(arr(td), arr(gd), arr(md), arr(vd), numel, n, lr, 0.9,
+                                              0.999, 1e-8, 1e-2, F32(F32(lr) / b1c),
+                                              np.sqrt(b2c, dtype=F32), None))
+        for i in range(n):
+            th[i], m_ref[i], v_ref[i] = smr.adamw_step(th[i], g[i], m_ref[i], v_ref[i], step, lr=lr)
+        got = [host(torch, t)[:s] for t, s in zip(td, sizes)]
+        for i in range(n):
+            np.testing.assert_array_equal(got[i], th[i], err_msg=f"step {step} tensor {i}")
+    # device-table forms: norm, scale, fill
+    tab = torch.tensor([t.data_ptr() for t in gd], dtype=torch.int64, device="cuda")
+    nm = torch.tensor(sizes, dtype=torch.int64, device="cuda")
+    out = torch.zeros(1, dtype=torch.float64, device="cuda")
+    wsb = L.soar_multi_tensor_norm_workspace_bytes()
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    ok(gn, L.soar_multi_tensor_norm_sq_device(P(tab), P(nm), n, P(out), P(ws), wsb, None))
+    want = sum(float(np.dot(a.astype(np.float64), a)) for a in g)
+    assert abs(float(host(torch, out)[0]) - want) <= 1e-12 * want
+    ok(gn, L.soar_multi_tensor_scale_device(P(tab), P(nm), n, F32(0.5), None))
+    for t, a in zip(gd, g):
+        np.testing.assert_array_equal(host(torch, t)[:a.size], a * F32(0.5))
+    ok(gn, L.soar_multi_tensor_fill_device(P(tab), P(nm), n, 0.0, None))
+    assert all(not np.any(host(torch, t)[:s]) for t, s in zip(gd, sizes))
+    # the single-tensor form
+    x = r.normal(size=1000).astype(F32)
+    gg = r.normal(size=1000).astype(F32)
+    xd, ggd = dev(torch, x), dev(torch, gg)
+    m1, v1 = torch.zeros(1000, device="cuda"), torch.zeros(1000, device="cuda")
+    ok(gn, L.soar_adamw_step(P(xd), P(ggd), P(m1), P(v1), 1e-3, 0.9, 0.999, 1e-8, 1e-2,
+                             F32(F32(1e-3) / (F32(1) - F32(0.9))),
+                             np.sqrt(F32(1) - F32(0.999), dtype=F32), 1000, None))
+    t1, _, _ = smr.adamw_step(x, gg, np.zeros(1000, F32), np.zeros(1000, F32), 1)
+    np.testing.assert_array_equal(host(torch, xd), t1)
+    # a table over the limit is refused before any launch
+    assert L.soar_multi_tensor_fill_device(P(tab), P(nm), 4096, 0.0, None) == gn.SOAR_EINVAL
