@@ -366,6 +366,9 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
 #define SOAR_TUNE_CHUNK2 7   /* elements per block-chunk of apply / dx     */
 #define SOAR_TUNE_PW_CHUNK 8 /* pixels per wave of the pointwise conv      */
                              /* (multiple of 128)                          */
+#define SOAR_TUNE_SMALL_UNIT 9 /* units of <= this many elements run the   */
+                               /* one-launch GroupNorm; 0 = never; the     */
+                               /* default is 32768                         */
 SOAR_API int soar_gn_tune(int key, int64_t value);
 SOAR_API int64_t soar_gn_tune_get(int key);
 

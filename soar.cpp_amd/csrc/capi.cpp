@@ -984,6 +984,11 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
                 return fail(SOAR_EINVAL, "pw_chunk must be a multiple of 128 in [128, 2^20]");
             g_tune.pw_chunk = value;
             return ok();
+        case SOAR_TUNE_SMALL_UNIT:
+            if (value < 0 || value > (1 << 20))
+                return fail(SOAR_EINVAL, "small_unit must be in [0, 2^20]");
+            g_tune.small_unit = value;
+            return ok();
         default:
             return fail(SOAR_EINVAL, "unknown tuning key %d", key);
     }
@@ -1000,6 +1005,7 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
         case SOAR_TUNE_STREAMS: return g_tune.streams;
         case SOAR_TUNE_NT_LOAD: return g_tune.nt_load;
         case SOAR_TUNE_PW_CHUNK: return g_tune.pw_chunk;
+        case SOAR_TUNE_SMALL_UNIT: return g_tune.small_unit;
         default: return -1;
     }
 }

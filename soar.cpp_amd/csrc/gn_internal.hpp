@@ -58,6 +58,8 @@ struct Tuning {
     int64_t pw_chunk = 1024;  // pixels per wave of the pointwise convolution
                               // (multiple of 128); also its GroupNorm
                               // partials' chunk
+    int64_t small_unit = 32768;  // units of at most this many elements run
+                                 // the one-launch GroupNorm (0: never)
 };
 
 constexpr int kThreads = 256;   // first passes (stats, reduction)

@@ -595,6 +595,325 @@ __global__ __launch_bounds__(kThreads2) void k_bwd_dx(
     }
 }
 
+// ======================================================================
+// Small units: the whole layer in one launch per direction.  The SOAR
+// model's GroupNorms at small images are a few thousand elements per unit;
+// there the multi-kernel path is dominated by its launches.
+//
+// One 1024-thread block owns a unit (forward) or a group across samples
+// (backward).  Channel j of the unit goes to tpc = 1024 / cpgp consecutive
+// threads (cpgp = cpg rounded up to a power of two), each holding up to 32
+// of the channel's HW elements in registers: x (and dy) are read once and
+// y (dx) written once.  Per-channel sums reduce over the tpc threads of a
+// channel with shuffles (and LDS across waves when tpc > 64), whole-unit
+// sums over the block, always in a fixed order.
+//
+// Forward statistics are float64 sums of x - K (K = the unit's first
+// element) and of its square; the apply is k_apply's (fp32 mean, its
+// rounding residual folded into the shift).
+// ======================================================================
+// Block sizes: NT = 256 for units of at most 256 * 32 elements, else 1024.
+constexpr int kSmallThreads = 1024;
+constexpr int kSmallPer = 32;  // elements per thread
+constexpr int kSmallHalf = 16;  // elements per load batch of the backward
+constexpr int kMaxSmallCpg = 256;  // channels per group (>= 4 threads each)
+
+struct SmallMap {
+    int tpc;   // threads per channel (power of two, >= 4)
+    int j, r;  // this thread's channel and its rank in the channel
+    int nk;    // this thread's elements: r + k*tpc for k < nk (0 if j >= cpg)
+};
+
+// (32-bit indices: a channel holds at most kSmallPer * 1024 elements)
+__device__ __forceinline__ SmallMap small_map(int lg, int64_t cpg, int64_t HW) {
+    SmallMap m;
+    m.tpc = 1 << lg;
+    m.j = (int)threadIdx.x >> lg;
+    m.r = (int)threadIdx.x & (m.tpc - 1);
+    m.nk = m.j < cpg ? ((int)HW - m.r + m.tpc - 1) >> lg : 0;
+    return m;
+}
+
+// Loads this thread's elements of a unit through a raw buffer descriptor on
+// the unit (wave-uniform base, 32-bit lane offset, the element step as a
+// scalar offset: no 64-bit address per element).  Lanes past the unit read
+// 0; lanes past their channel read the next channel's values, which the
+// callers never use (they test k < m.nk).
+constexpr int kSmallRsrcWord3 = 0x00020000;  // gfx9-family raw buffer descriptor
+
+template <int NV = kSmallPer>
+__device__ __forceinline__ void small_load(const float* unit, int64_t M, int64_t HW,
+                                           const SmallMap& m, float (&v)[NV], int k0 = 0) {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(unit), (short)0,
+                                                      (int)(M * 4), kSmallRsrcWord3);
+    int vo = (m.j * (int)HW + m.r) * 4;
+    asm volatile("" : "+v"(vo));  // each call loads anew (no reuse across calls)
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+        v[k] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(rs, vo, (k0 + k) * m.tpc * 4, 0));
+}
+
+// Sum of v over the block, fixed order, returned to every thread.
+template <int NT, typename T>
+__device__ __forceinline__ T small_block_sum(T v, T* lds /*[NT / 64]*/) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) lds[w] = v;
+    __syncthreads();
+    T r = lds[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i) r += lds[i];
+    __syncthreads();
+    return r;
+}
+
+// Sum of v over the tpc threads of each channel; valid in the channel's
+// rank-0 thread (wave tree within 64 lanes, then the channel's waves in
+// order through LDS).
+__device__ __forceinline__ double channel_sum(double v, const SmallMap& m, double* lds) {
+    if (m.tpc <= 64) {
+        for (int off = m.tpc >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off);
+        return v;
+    }
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) lds[w] = v;
+    __syncthreads();
+    double r = 0.0;
+    if (m.r == 0) {
+        const int w0 = w, nw = m.tpc >> 6;
+        for (int i = 0; i < nw; ++i) r += lds[w0 + i];
+    }
+    __syncthreads();
+    return r;
+}
+
+template <bool SILU, bool RES>
+__device__ __forceinline__ void small_apply_regs(const float (&xv)[kSmallPer], float* __restrict__ yc,
+                                                 const SmallMap& m, float gm, float bt, float mu,
+                                                 float r, float lo) {
+    const float a = gm * r;
+    const float b = fmaf(gm, -lo * r, bt);
+#pragma unroll
+    for (int k = 0; k < kSmallPer; ++k) {
+        if (k < m.nk) {
+            const float z = fmaf(xv[k] - mu, a, b);
+            float o = SILU ? silu_fast(z) : z;
+            if (RES) o += xv[k];
+            yc[m.r + k * m.tpc] = o;
+        }
+    }
+}
+
+template <int NT, bool SILU, bool RES>
+__global__ __launch_bounds__(NT) void k_small_fwd(
+    const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float* __restrict__ y, float* __restrict__ mean,
+    float* __restrict__ rstd, float* __restrict__ mean_lo, int64_t G, int64_t cpg, int64_t HW,
+    int lg, float eps) {
+    __shared__ double lds[NT / 64];
+    const int64_t u = blockIdx.x;
+    const SmallMap m = small_map(lg, cpg, HW);
+    const bool live = m.j < cpg;
+    float xv[kSmallPer];
+    small_load(x + u * cpg * HW, cpg * HW, HW, m, xv);  // a unit is contiguous in NCHW
+    const double K = (double)x[u * cpg * HW];
+    double s = 0.0, q = 0.0;
+#pragma unroll
+    for (int k = 0; k < kSmallPer; ++k) {
+        if (k < m.nk) {
+            const double d = (double)xv[k] - K;
+            s += d;
+            q = fma(d, d, q);
+        }
+    }
+    const double M = (double)(cpg * HW);
+    s = small_block_sum<NT>(s, lds);
+    q = small_block_sum<NT>(q, lds);
+    const double sm = s / M;
+    const double md = K + sm;
+    const double var = fmax(q / M - sm * sm, 0.0);
+    const float hi = (float)md;
+    const float lo = (float)(md - (double)hi);
+    const float r = (float)(1.0 / sqrt(var + (double)eps));
+    if (threadIdx.x == 0) {
+        mean[u] = hi;
+        rstd[u] = r;
+        if (mean_lo) mean_lo[u] = lo;
+    }
+    const int64_t c = (u % G) * cpg + m.j;
+    const float gm = (live && gamma) ? gamma[c] : 1.0f;
+    const float bt = (live && beta) ? beta[c] : 0.0f;
+    small_apply_regs<SILU, RES>(xv, y + (u * cpg + (live ? m.j : 0)) * HW, m, gm, bt, hi, r, lo);
+}
+
+// Chan combine over the block, fixed order; valid in thread 0.
+template <int NT>
+__device__ __forceinline__ Moments small_block_moments(Moments v, Moments* lds) {
+    v = wave_reduce(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) lds[w] = v;
+    __syncthreads();
+    Moments r = lds[0];
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int i = 1; i < NT / 64; ++i) r = chan(r, lds[i]);
+    }
+    __syncthreads();
+    return r;
+}
+
+// The GroupNorm after a pointwise convolution whose epilogue wrote the
+// chunk partials: the unit's finish (its cpg*cpp partials, combined in a
+// fixed order), then its apply, in one block.
+template <int NT, bool SILU, bool RES>
+__global__ __launch_bounds__(NT) void k_small_finish_apply(
+    const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float* __restrict__ y, const double2* __restrict__ part,
+    float* __restrict__ mean, float* __restrict__ rstd, float* __restrict__ mean_lo,
+    float* __restrict__ lo_ws, int64_t G, int64_t cpg, int64_t HW, int64_t chunk, int64_t cpp,
+    int lg, float eps) {
+    __shared__ Moments ldsm[NT / 64];
+    __shared__ float bc[3];
+    const int64_t u = blockIdx.x;
+    const SmallMap m = small_map(lg, cpg, HW);
+    const bool live = m.j < cpg;
+    float xv[kSmallPer];  // loads in flight while the partials combine
+    small_load(x + u * cpg * HW, cpg * HW, HW, m, xv);
+    const int64_t P = cpg * cpp;
+    Moments um{0.0, 0.0, 0.0};
+    for (int64_t q = threadIdx.x; q < P; q += NT) {
+        const double2 v = part[u * P + q];
+        const int64_t k = q % cpp;
+        um = chan(um, Moments{(double)min(chunk, HW - k * chunk), v.x, v.y});
+    }
+    const Moments ur = small_block_moments<NT>(um, ldsm);
+    if (threadIdx.x == 0) {
+        const double var = ur.n > 0.0 ? fmax(ur.m2 / ur.n, 0.0) : 0.0;
+        const float hi = (float)ur.mean;
+        const float lo = (float)(ur.mean - (double)hi);
+        const float r = (float)(1.0 / sqrt(var + (double)eps));
+        mean[u] = hi;
+        rstd[u] = r;
+        lo_ws[u] = lo;
+        if (mean_lo) mean_lo[u] = lo;
+        bc[0] = hi;
+        bc[1] = r;
+        bc[2] = lo;
+    }
+    __syncthreads();
+    const int64_t c = (u % G) * cpg + m.j;
+    const float gm = (live && gamma) ? gamma[c] : 1.0f;
+    const float bt = (live && beta) ? beta[c] : 0.0f;
+    small_apply_regs<SILU, RES>(xv, y + (u * cpg + (live ? m.j : 0)) * HW, m, gm, bt, bc[0],
+                                bc[1], bc[2]);
+}
+
+// Backward: one block per group g walks the samples in order.  Per unit:
+// per-channel float64 sums of dz and dz*xhat, S1 and S2 from them in
+// channel order, then dx from the registers; the channel sums are added
+// over samples in order into dgamma / dbeta at the end (as k_param_finish).
+template <int NT, bool SILU, bool RES, bool ACC>
+__global__ __launch_bounds__(NT) void k_small_bwd(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ beta, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ mean_lo, float* __restrict__ dx,
+    float* __restrict__ dgamma, float* __restrict__ dbeta, int64_t N, int64_t C, int64_t G,
+    int64_t cpg, int64_t HW, int lg) {
+    __shared__ double chA[kMaxSmallCpg], chB[kMaxSmallCpg];
+    __shared__ double lds[NT / 64];
+    __shared__ double S[2];
+    const int64_t g = blockIdx.x;
+    const SmallMap m = small_map(lg, cpg, HW);
+    const bool live = m.j < cpg;
+    const int64_t c = g * cpg + m.j;
+    const float gm = (live && gamma) ? gamma[c] : 1.0f;
+    const float bt = (live && beta) ? beta[c] : 0.0f;
+    double accA = 0.0, accB = 0.0;  // rank-0 thread of each channel: sums over samples
+    for (int64_t n = 0; n < N; ++n) {
+        const int64_t u = n * G + g;
+        const int64_t off = (u * cpg + (live ? m.j : 0)) * HW;
+        const float* xu = x + u * cpg * HW;
+        const float* gu = dy + u * cpg * HW;
+        const float mu = mean[u], r = rstd[u];
+        const float e = mean_lo ? -mean_lo[u] * r : 0.0f;
+        double sa = 0.0, sb = 0.0;
+        // two halves of 16 elements keep the loads and their products
+        // within 128 registers
+#pragma unroll
+        for (int h = 0; h < kSmallPer; h += kSmallHalf) {
+            float xv[kSmallHalf], gv[kSmallHalf];
+            small_load<kSmallHalf>(xu, cpg * HW, HW, m, xv, h);
+            small_load<kSmallHalf>(gu, cpg * HW, HW, m, gv, h);
+#pragma unroll
+            for (int k = 0; k < kSmallHalf; ++k) {
+                if (h + k < m.nk) {
+                    const float xh = fmaf(xv[k] - mu, r, e);
+                    const float dz = SILU ? dsilu_fast(gv[k], fmaf(gm, xh, bt)) : gv[k];
+                    sa += (double)dz;
+                    sb = fma((double)dz, (double)xh, sb);
+                }
+            }
+        }
+        sa = channel_sum(sa, m, lds);
+        sb = channel_sum(sb, m, lds);
+        if (live && m.r == 0) {
+            chA[m.j] = sa;
+            chB[m.j] = sb;
+            accA += sa;
+            accB += sb;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double s1 = 0.0, s2 = 0.0;
+            for (int64_t j = 0; j < cpg; ++j) {
+                const double gj = gamma ? (double)gamma[g * cpg + j] : 1.0;
+                s1 += gj * chA[j];
+                s2 += gj * chB[j];
+            }
+            S[0] = s1;
+            S[1] = s2;
+        }
+        __syncthreads();
+        if (dx) {
+            const double Md = (double)(cpg * HW);
+            const float B = (float)(-(double)r * S[0] / Md);
+            const float D = (float)(-(double)r * S[1] / Md);
+            // reload x and dy (L2-resident) and recompute xhat and dz:
+            // keeping the first loop's values alive across the reductions
+            // would not fit in 128 registers
+            float mu2 = mu, r2 = r, e2 = e, gm2 = gm, bt2 = bt;
+            asm volatile("" : "+v"(mu2), "+v"(r2), "+v"(e2), "+v"(gm2), "+v"(bt2));
+            const float A = gm2 * r2;
+            float* dc = dx + off;
+#pragma unroll
+            for (int h = 0; h < kSmallPer; h += kSmallHalf) {
+                float xv[kSmallHalf], gv[kSmallHalf];
+                small_load<kSmallHalf>(xu, cpg * HW, HW, m, xv, h);
+                small_load<kSmallHalf>(gu, cpg * HW, HW, m, gv, h);
+#pragma unroll
+                for (int k = 0; k < kSmallHalf; ++k) {
+                    const int i = m.r + (h + k) * m.tpc;
+                    if (h + k < m.nk) {
+                        const float xh = fmaf(xv[k] - mu2, r2, e2);
+                        const float dz = SILU ? dsilu_fast(gv[k], fmaf(gm2, xh, bt2)) : gv[k];
+                        float o = fmaf(A, dz, fmaf(D, xh, B));
+                        if (RES) o += gv[k];
+                        if (ACC) o += dc[i];
+                        dc[i] = o;
+                    }
+                }
+            }
+        }
+        __syncthreads();  // chA / chB / S are rewritten by the next sample
+    }
+    if (dgamma && live && m.r == 0) {
+        dbeta[c] = (float)((double)dbeta[c] + accA);
+        dgamma[c] = (float)((double)dgamma[c] + accB);
+    }
+}
+
 // ---- host-side dispatch over the template flags -------------------------
 
 struct WsView {
@@ -804,9 +1123,64 @@ size_t workspace_bytes(const Plan& p) {
 // finish, A = second pass):  S0, F0+S1, A0, F1+S2, A1, ..., F(B-1), A(B-1).
 // With two streams (tuning `streams` = 2 and more than one batch) the
 // helper-stream pipeline above is used instead.
+// The one-launch paths above apply when a unit is at most t.small_unit
+// elements; the backward also bounds the samples a block walks.
+// log2 of the threads per channel of the small kernels, or -1 when the
+// unit does not fit: cpg rounded up to a power of two times HW must fit
+// kSmallPer elements per thread.
+int small_lg(const Plan& p, const Tuning& t, int nt) {
+    if (t.small_unit <= 0 || p.cpg > kMaxSmallCpg || p.cpg * p.HW > t.small_unit) return -1;
+    int lc = 0;
+    while ((int64_t(1) << lc) < p.cpg) ++lc;
+    int ln = 0;
+    while ((1 << ln) < nt) ++ln;
+    const int lg = ln - lc;  // log2(nt / cpgp)
+    if (lg < 2 || p.HW > (int64_t)kSmallPer << lg) return -1;
+    return lg;
+}
+
+// Threads of the small kernels' block for this plan: 256 when that many
+// hold the unit, else 1024; 0 when the unit is not small.
+int small_threads(const Plan& p, const Tuning& t) {
+    if (small_lg(p, t, 256) >= 0) return 256;
+    return small_lg(p, t, kSmallThreads) >= 0 ? kSmallThreads : 0;
+}
+
+// Runs f(std::integral_constant<int, NT>) for the plan's block size.
+template <typename F>
+void nt_sel(int nt, F&& f) {
+    if (nt == 256)
+        f(std::integral_constant<int, 256>{});
+    else
+        f(std::integral_constant<int, kSmallThreads>{});
+}
+
+bool small_fwd(const Plan& p, const Tuning& t) {
+    return small_threads(p, t) > 0 && p.units <= 0x7fffffff;
+}
+
+bool small_bwd(const Plan& p, const Tuning& t) {
+    return small_fwd(p, t) && p.N * p.cpg * p.HW <= 8 * t.small_unit && p.G <= 0x7fffffff;
+}
+
 hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a, hipStream_t s) {
     const WsView w = ws_view(p, a.ws);
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
+    if (small_fwd(p, t)) {
+        const int tok = prof_begin(s, "gn_small_fwd");
+        const int nt = small_threads(p, t);
+        nt_sel(nt, [&](auto NT) {
+            bsel(silu, [&](auto S) {
+                bsel((a.flags & SOAR_GN_RESIDUAL) != 0, [&](auto R) {
+                    k_small_fwd<NT(), S(), R()><<<dim3((unsigned)p.units), NT(), 0, s>>>(
+                        a.x, a.gamma, a.beta, a.y, a.mean, a.rstd, a.mean_lo, p.G, p.cpg, p.HW,
+                        small_lg(p, t, nt), a.eps);
+                });
+            });
+        });
+        prof_end(s, tok);
+        return hipGetLastError();
+    }
     const int64_t bpu2 = p.cpg * p.cpp2;  // second-pass blocks per unit
     const char* apply_name = silu ? "gn_silu_apply" : "gn_apply";
     if (t.streams >= 2 && p.units > p.upb_fwd) {
@@ -849,6 +1223,21 @@ hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a, hipS
 hipError_t launch_forward_from_partials(const Plan& p, const Tuning& t, const FwdArgs& a,
                                         hipStream_t s) {
     const WsView w = ws_view(p, a.ws);
+    if (small_fwd(p, t)) {
+        const int tok = prof_begin(s, "gn_small_finish_apply");
+        const int nt = small_threads(p, t);
+        nt_sel(nt, [&](auto NT) {
+            bsel((a.flags & SOAR_GN_SILU) != 0, [&](auto S) {
+                bsel((a.flags & SOAR_GN_RESIDUAL) != 0, [&](auto R) {
+                    k_small_finish_apply<NT(), S(), R()><<<dim3((unsigned)p.units), NT(), 0, s>>>(
+                        a.x, a.gamma, a.beta, a.y, w.part, a.mean, a.rstd, a.mean_lo, w.lo, p.G,
+                        p.cpg, p.HW, p.chunk, p.cpp, small_lg(p, t, nt), a.eps);
+                });
+            });
+        });
+        prof_end(s, tok);
+        return hipGetLastError();
+    }
     launch_stats(p, a, w, 0, p.units, 0, 0, s);
     const int tok = prof_begin(s, (a.flags & SOAR_GN_SILU) ? "gn_silu_apply" : "gn_apply");
     launch_apply(p, t, a, w.lo, 0, p.blocks2, s);
@@ -871,6 +1260,23 @@ bool make_pw_plan(int64_t N, int64_t C_out, int64_t HW, int64_t G, const Tuning&
 hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hipStream_t s) {
     const WsView w = ws_view(p, a.ws);
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
+    if (small_bwd(p, t)) {
+        const int tok = prof_begin(s, "gn_small_bwd");
+        const int nt = small_threads(p, t);
+        nt_sel(nt, [&](auto NT) {
+            bsel(silu, [&](auto S) {
+                bsel((a.flags & SOAR_GN_RESIDUAL) != 0, [&](auto R) {
+                    bsel((a.flags & SOAR_GN_ACCUMULATE_DX) != 0, [&](auto A) {
+                        k_small_bwd<NT(), S(), R(), A()><<<dim3((unsigned)p.G), NT(), 0, s>>>(
+                            a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, a.dx,
+                            a.dgamma, a.dbeta, p.N, p.C, p.G, p.cpg, p.HW, small_lg(p, t, nt));
+                    });
+                });
+            });
+        });
+        prof_end(s, tok);
+        return hipGetLastError();
+    }
     const int64_t bpu2 = p.cpg * p.cpp2;  // second-pass blocks per unit
     const char* dx_name = silu ? "gn_silu_bwd_dx" : "gn_bwd_dx";
     if (t.streams >= 2 && p.units > p.upb_bwd) {

@@ -40,6 +40,7 @@ TUNE_STREAMS = 5
 TUNE_NT_LOAD = 6
 TUNE_CHUNK2 = 7
 TUNE_PW_CHUNK = 8
+TUNE_SMALL_UNIT = 9
 
 
 class SoarUnavailable(RuntimeError):

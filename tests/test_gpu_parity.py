@@ -493,7 +493,7 @@ def test_kernel_timing_records(gpu):
 @pytest.fixture
 def restore_tuning(gpu):
     keys = (gpu.TUNE_CHUNK, gpu.TUNE_REVERSE, gpu.TUNE_NT_STORE, gpu.TUNE_BATCH_MB,
-            gpu.TUNE_STREAMS, gpu.TUNE_NT_LOAD, gpu.TUNE_CHUNK2)
+            gpu.TUNE_STREAMS, gpu.TUNE_NT_LOAD, gpu.TUNE_CHUNK2, gpu.TUNE_SMALL_UNIT)
     old = {k: gpu.tune_get(k) for k in keys}
     yield
     for k, v in old.items():
@@ -538,6 +538,59 @@ def test_tuning_variants_match(gpu, oracle, restore_tuning, residual):
         assert_vals(host(dx), dxt, f"dx chunk {chunk}")
         assert_vals(host(dg), dgt, f"dgamma chunk {chunk}")
         assert_vals(host(db), dbt, f"dbeta chunk {chunk}")
+
+
+SMALL_SHAPES = [
+    # (N, C, HW, G, kind): units of at most 32768 elements
+    (1, 16, 1024, 8, "normal"),       # SOAR Nano, stride 2 at a 64x64 image
+    (1, 256, 4, 8, "normal"),         # stride 32 at 64x64
+    (1, 256, 1024, 8, "normal"),      # stride 32 at 1024x1024: unit = 32768
+    (2, 64, 255, 8, "normal"),        # ragged HW, two samples
+    (5, 12, 100, 4, "offset"),        # large mean, five samples walked in order
+    (1, 4, 1, 2, "offset"),           # HW = 1
+]
+
+
+@pytest.mark.parametrize("shape", SMALL_SHAPES, ids=lambda s: "x".join(map(str, s[:4])) + s[4])
+@pytest.mark.parametrize("residual", [False, True])
+def test_small_unit_path(gpu, oracle, restore_tuning, shape, residual):
+    """The one-launch GroupNorm for small units against the oracle, and
+    against the multi-kernel path (SOAR_TUNE_SMALL_UNIT = 0) on the same
+    input, with accumulation into dx and into dgamma / dbeta."""
+    import torch
+    N, C, HW, G, kind = shape
+    x, gamma, beta, dy = make_inputs(oracle, N, C, HW, G, kind, 77 + C + HW)
+    yt, mt, rt = oracle.gn_silu_fwd_f64(x, gamma, beta, N, C, HW, G, EPS, True, residual)
+    dxt, dgt, dbt = oracle.gn_silu_bwd_f64(dy, x, gamma, beta, mt, rt, N, C, HW, G, True,
+                                           residual)
+    xd, dyd = dev(x).view(N, C, HW), dev(dy).view(N, C, HW)
+    gd, bd = dev(gamma), dev(beta)
+    runs = []
+    for small in (32768, 0):
+        gpu.tune(gpu.TUNE_SMALL_UNIT, small)
+        y, mean, rstd, lo, dx, dg, db = _fwd_bwd(gpu, xd, gd, bd, dyd, G, residual)
+        assert_stats(host(mean), host(rstd), mt, rt, f"small={small}")
+        assert_vals(host(y), yt, f"y small={small}")
+        assert_vals(host(dx), dxt, f"dx small={small}")
+        assert_vals(host(dg), dgt, f"dgamma small={small}")
+        assert_vals(host(db), dbt, f"dbeta small={small}")
+        runs.append([host(t).astype(np.float64) for t in (y, dx, dg, db)])
+    for a, b in zip(*runs):  # the two paths agree far inside the bar
+        assert np.abs(a - b).max() <= 2e-6 * (1 + np.abs(b).max())
+    # accumulation: dx += and dgamma / dbeta += (the backward's contract)
+    gpu.tune(gpu.TUNE_SMALL_UNIT, 32768)
+    ws = gpu.workspace(N, C, HW, G)
+    y, st = gpu.gn_silu_forward(xd, gd, bd, G, eps=EPS, residual=residual, ws=ws)
+    dx0 = torch.full_like(xd, 0.5)
+    dg0, db0 = torch.full_like(gd, -1.0), torch.full_like(bd, 2.0)
+    gpu.check(gpu.lib().soar_gn_silu_backward(
+        gpu._ptr(dyd), gpu._ptr(xd), gpu._ptr(gd), gpu._ptr(bd), gpu._ptr(st.mean),
+        gpu._ptr(st.rstd), gpu._ptr(st.mean_lo), gpu._ptr(dx0), gpu._ptr(dg0), gpu._ptr(db0),
+        N, C, HW, G, gpu.GN_SILU | gpu.GN_ACCUMULATE_DX | (gpu.GN_RESIDUAL if residual else 0),
+        gpu._ptr(ws), ws.numel(), gpu._stream()))
+    assert_vals(host(dx0) - 0.5, dxt, "accumulated dx")
+    assert_vals(host(dg0) + 1.0, dgt, "accumulated dgamma")
+    assert_vals(host(db0) - 2.0, dbt, "accumulated dbeta")
 
 
 def test_full_size_config4_chain(gpu, oracle):
