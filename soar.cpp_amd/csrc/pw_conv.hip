@@ -523,6 +523,147 @@ __global__ void k_transpose(const float* __restrict__ w, float* __restrict__ wt,
     wt[c * R + r] = w[i];
 }
 
+// ======================================================================
+// Small planes (HW <= Tuning::pw_small_hw).  The MFMA kernels above give a
+// wave 128-pixel items and walk K one 8-channel step at a time; on planes of
+// a few pixels most of each item is empty and a handful of waves wait on one
+// load after another.  Here one lane owns one output element z[n][m][p]
+// (64 consecutive elements of a sample per wave: pixels fastest, then rows)
+// and the K axis is split over the S waves of a block: wave v sums its
+// contiguous k segment in fp32, then wave 0 adds the S partial sums in
+// order and the bias (or adds the total to z with ACC).
+//
+// TRANS reads the weight as w[k][m], so dx = W^T dz needs no transposed
+// copy.  V4 (not TRANS; K and the segment a multiple of 4, w 16-byte
+// aligned) reads four weights of a row with one 16-byte load.  Element
+// offsets inside one sample fit in 32 bits (checked by pw_small_fits).
+// ======================================================================
+constexpr int kSmallMaxWaves = 16;
+
+template <bool TRANS, bool V4, bool ACC, bool BIAS>
+__global__ __launch_bounds__(1024) void k_pw_small(const float* __restrict__ x,
+                                                   const float* __restrict__ w,
+                                                   const float* __restrict__ bias,
+                                                   float* __restrict__ z, int M, int K, int HW,
+                                                   int seg) {
+    __shared__ float part[kSmallMaxWaves][64];
+    const int lane = threadIdx.x & 63, v = threadIdx.x >> 6;
+    const int S = blockDim.x >> 6;
+    const int64_t n = blockIdx.y;
+    const int MH = M * HW;
+    const int o = (int)blockIdx.x * 64 + lane;  // element of the sample's output
+    const bool live = o < MH;
+    const int oc = live ? o : MH - 1;  // lanes past the end compute a copy
+    const int m = oc / HW, p = oc - m * HW;
+    const float* xs = x + n * (int64_t)K * HW + p;
+    const int k0 = v * seg, k1 = min(K, k0 + seg);
+    float acc = 0.0f;
+    int k = k0;
+    if (V4) {
+        const float* wr = w + (int64_t)m * K;
+        for (; k + 8 <= k1; k += 8) {
+            const float4 wa = *reinterpret_cast<const float4*>(wr + k);
+            const float4 wb = *reinterpret_cast<const float4*>(wr + k + 4);
+            float xv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) xv[u] = xs[(k + u) * HW];
+            acc = fmaf(wa.x, xv[0], acc);
+            acc = fmaf(wa.y, xv[1], acc);
+            acc = fmaf(wa.z, xv[2], acc);
+            acc = fmaf(wa.w, xv[3], acc);
+            acc = fmaf(wb.x, xv[4], acc);
+            acc = fmaf(wb.y, xv[5], acc);
+            acc = fmaf(wb.z, xv[6], acc);
+            acc = fmaf(wb.w, xv[7], acc);
+        }
+        for (; k < k1; ++k) acc = fmaf(wr[k], xs[k * HW], acc);
+    } else {
+        // weight of (m, k): w[m*K + k], or w[k*M + m] with TRANS
+        const int64_t wstep = TRANS ? M : 1;
+        const float* wp = TRANS ? w + m : w + (int64_t)m * K;
+        for (; k + 8 <= k1; k += 8) {
+            float wv[8], xv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                wv[u] = wp[(k + u) * wstep];
+                xv[u] = xs[(k + u) * HW];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = fmaf(wv[u], xv[u], acc);
+        }
+        for (; k < k1; ++k) acc = fmaf(wp[k * wstep], xs[k * HW], acc);
+    }
+    if (S == 1) {
+        if (live) {
+            float* zo = z + n * (int64_t)MH + o;
+            if (ACC)
+                *zo = *zo + acc;
+            else
+                *zo = BIAS ? bias[m] + acc : acc;
+        }
+        return;
+    }
+    part[v][lane] = acc;
+    __syncthreads();
+    if (v == 0 && live) {
+        float t = part[0][lane];
+        for (int i = 1; i < S; ++i) t += part[i][lane];
+        float* zo = z + n * (int64_t)MH + o;
+        if (ACC)
+            *zo = *zo + t;
+        else
+            *zo = BIAS ? bias[m] + t : t;
+    }
+}
+
+// dW[co][ci] += sum_(n,p) dz[n][co][p] x[n][ci][p], db[co] += sum_(n,p)
+// dz[n][co][p] for small planes: one lane per weight (ci fastest, so a
+// wave's x loads are consecutive rows), the (n, p) sum in float64 in a
+// fixed order.  Lanes e in [E, E + C_out) own the bias entries; the grid
+// starts at e0 (E when only db is wanted).  V4: HW % 4 == 0 and 16-byte
+// aligned dz and x.
+template <bool V4>
+__global__ __launch_bounds__(256) void k_pw_wgrad_small(const float* __restrict__ dz,
+                                                        const float* __restrict__ x,
+                                                        float* __restrict__ dw,
+                                                        float* __restrict__ db, int N, int C_in,
+                                                        int C_out, int HW, int64_t e0,
+                                                        int64_t e1) {
+    const int64_t e = e0 + (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= e1) return;
+    const int64_t E = (int64_t)C_out * C_in;
+    const bool wt = e < E;
+    const int co = wt ? (int)(e / C_in) : (int)(e - E);
+    const int ci = wt ? (int)(e - (int64_t)co * C_in) : 0;
+    double acc = 0.0;
+    for (int n = 0; n < N; ++n) {
+        const float* a = dz + ((int64_t)n * C_out + co) * HW;
+        const float* b = x + ((int64_t)n * C_in + ci) * HW;
+        if (V4) {
+            for (int p = 0; p < HW; p += 4) {
+                const float4 av = *reinterpret_cast<const float4*>(a + p);
+                if (wt) {
+                    const float4 bv = *reinterpret_cast<const float4*>(b + p);
+                    acc += (double)av.x * (double)bv.x;
+                    acc += (double)av.y * (double)bv.y;
+                    acc += (double)av.z * (double)bv.z;
+                    acc += (double)av.w * (double)bv.w;
+                } else {
+                    acc += (double)av.x;
+                    acc += (double)av.y;
+                    acc += (double)av.z;
+                    acc += (double)av.w;
+                }
+            }
+        } else {
+            for (int p = 0; p < HW; ++p)
+                acc += wt ? (double)a[p] * (double)b[p] : (double)a[p];
+        }
+    }
+    float* out = wt ? dw + e : db + co;
+    *out = (float)((double)*out + acc);
+}
+
 template <typename F>
 void bsel(bool b, F&& f) {
     if (b)
@@ -551,10 +692,54 @@ int64_t pw_pick_chunk(int64_t N, int64_t C_out, int64_t HW, int64_t max_chunk) {
     return std::max<int64_t>(kItem, std::min<int64_t>(c, max_chunk));
 }
 
+bool pw_small_fits(int64_t N, int64_t M, int64_t K, int64_t HW) {
+    const int64_t lim = (int64_t)1 << 31;
+    return N <= 65535 && M * HW < lim && K * HW < lim && M < lim && K < lim;
+}
+
+namespace {
+
+// z = W x (+ bias), or z += W x; TRANS: z = W^T x.  M output rows, K input
+// rows.  Each wave sums about 32 values of K.
+hipError_t launch_pw_small(const float* x, const float* w, const float* bias, float* z,
+                           int64_t N, int64_t K, int64_t M, int64_t HW, bool trans,
+                           bool accumulate, hipStream_t s, const char* name) {
+    int S = (int)std::min<int64_t>(kSmallMaxWaves, std::max<int64_t>(1, (K + 31) / 32));
+    int64_t seg = (K + S - 1) / S;
+    seg = (seg + 3) / 4 * 4;
+    S = (int)((K + seg - 1) / seg);
+    const bool v4 = !trans && K % 4 == 0 && (uintptr_t)w % 16 == 0;
+    const dim3 grid((unsigned)((M * HW + 63) / 64), (unsigned)N);
+    const int tok = prof_begin(s, name);
+    auto go = [&](auto T, auto V, auto A, auto B) {
+        k_pw_small<T(), V(), A(), B()><<<grid, 64 * S, 0, s>>>(x, w, bias, z, (int)M, (int)K,
+                                                               (int)HW, (int)seg);
+    };
+    using F = std::false_type;
+    using Tr = std::true_type;
+    if (trans) {
+        bsel(accumulate, [&](auto A) { go(Tr{}, F{}, A, F{}); });
+    } else {
+        bsel(v4, [&](auto V) {
+            if (accumulate)
+                go(F{}, V, Tr{}, F{});
+            else
+                bsel(bias != nullptr, [&](auto B) { go(F{}, V, F{}, B); });
+        });
+    }
+    prof_end(s, tok);
+    return hipGetLastError();
+}
+
+}  // namespace
+
 hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
                           int64_t HW, int64_t chunk, double2* part, bool accumulate,
-                          hipStream_t s, const char* name) {
+                          int64_t small_hw, hipStream_t s, const char* name) {
     if (N == 0 || HW == 0 || C_out == 0) return hipSuccess;
+    if (!part && HW <= small_hw && pw_small_fits(N, C_out, C_in, HW))
+        return launch_pw_small(a.x, a.w, a.bias, a.z, N, C_in, C_out, HW, false, accumulate, s,
+                               name ? name : "pw_conv_small");
     const int64_t cpp = (HW + chunk - 1) / chunk;
     // A wave walks up to kRowGroup row tiles of its chunk (the chunk's x
     // stays in cache across them); when that leaves too few waves, each row
@@ -615,13 +800,18 @@ size_t pw_bwd_workspace_bytes(const PwBwdPlan& p) { return p.wt_bytes + p.pw_byt
 
 hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N, int64_t C_in,
                               int64_t C_out, int64_t HW, int64_t chunk_dx, bool accumulate_dx,
-                              hipStream_t s) {
+                              int64_t small_hw, hipStream_t s) {
     if (N == 0 || HW == 0 || C_out == 0 || C_in == 0) return hipSuccess;
     char* ws = static_cast<char*>(a.ws);
     float* wt = reinterpret_cast<float*>(ws);
     float* part_w = reinterpret_cast<float*>(ws + p.wt_bytes);
     float* part_b = reinterpret_cast<float*>(ws + p.wt_bytes + p.pw_bytes);
-    if (a.dx) {
+    if (a.dx && HW <= small_hw && pw_small_fits(N, C_in, C_out, HW)) {
+        // dx = W^T dz, reading W transposed in place
+        hipError_t e = launch_pw_small(a.dz, a.w, nullptr, a.dx, N, C_out, C_in, HW, true,
+                                       accumulate_dx, s, "pw_conv_dgrad_small");
+        if (e != hipSuccess) return e;
+    } else if (a.dx) {
         const int64_t E = C_in * C_out;
         int tok = prof_begin(s, "pw_transpose");
         k_transpose<<<dim3((unsigned)((E + 255) / 256)), 256, 0, s>>>(a.w, wt, C_out, C_in);
@@ -630,10 +820,20 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
         PwArgs fa{a.dz, wt, nullptr, a.dx};
         hipError_t e = launch_pw_conv(fa, N, C_out, C_in, HW,
                                       pw_pick_chunk(N, C_in, HW, chunk_dx), nullptr,
-                                      accumulate_dx, s, "pw_conv_dgrad");
+                                      accumulate_dx, 0, s, "pw_conv_dgrad");
         if (e != hipSuccess) return e;
     }
-    if (a.dw || a.db) {
+    if ((a.dw || a.db) && N * HW <= small_hw && pw_small_fits(N, C_out, C_in, HW)) {
+        const int64_t E = C_out * C_in;
+        const int64_t e0 = a.dw ? 0 : E, e1 = a.db ? E + C_out : E;
+        const bool v4 = (HW % 4 == 0) && ((uintptr_t)a.dz % 16 == 0) && ((uintptr_t)a.x % 16 == 0);
+        const int tok = prof_begin(s, "pw_conv_wgrad_small");
+        bsel(v4, [&](auto V) {
+            k_pw_wgrad_small<V()><<<dim3((unsigned)((e1 - e0 + 255) / 256)), 256, 0, s>>>(
+                a.dz, a.x, a.dw, a.db, (int)N, (int)C_in, (int)C_out, (int)HW, e0, e1);
+        });
+        prof_end(s, tok);
+    } else if (a.dw || a.db) {
         const bool fast = (HW % 4 == 0) && ((uintptr_t)a.dz % 16 == 0) &&
                           ((uintptr_t)a.x % 16 == 0);
         const dim3 grid((unsigned)(p.tiles_co * p.tiles_ci), (unsigned)p.G);

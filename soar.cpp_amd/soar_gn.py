@@ -41,6 +41,7 @@ TUNE_NT_LOAD = 6
 TUNE_CHUNK2 = 7
 TUNE_PW_CHUNK = 8
 TUNE_SMALL_UNIT = 9
+TUNE_PW_SMALL_HW = 10
 
 
 class SoarUnavailable(RuntimeError):
@@ -364,6 +365,24 @@ def conv1x1_forward(x, weight, bias=None, out=None, stream=None):
         check(lib().soar_conv2d_1x1_forward(_ptr(xs[n]), _ptr(w), _ptr(bias), _ptr(out[n]),
                                             C_in, C_out, HW, _stream(stream)))
     return out[0] if squeeze else out
+
+
+def pw_conv_forward(x, weight, bias=None, z=None, stream=None):
+    """z[n] = weight @ x[n] + bias for all samples in one soar_pw_conv_forward
+    call.  x: [N, C_in, H, W] or [N, C_in, HW]; weight [C_out, C_in]."""
+    import torch
+    N, C_in, HW = _nchw(x)
+    w = weight.reshape(weight.shape[0], -1)
+    C_out = w.shape[0]
+    if w.shape[1] != C_in:
+        raise ValueError("weight does not match the input channels")
+    for t, n in ((x, "x"), (w, "weight"), (bias, "bias"), (z, "z")):
+        _check_tensor(t, n)
+    if z is None:
+        z = torch.empty((N, C_out) + tuple(x.shape[2:]), dtype=torch.float32, device=x.device)
+    check(lib().soar_pw_conv_forward(_ptr(x), _ptr(w), _ptr(bias), _ptr(z), N, C_in, C_out, HW,
+                                     _stream(stream)))
+    return z
 
 
 def pw_conv_gn_workspace_bytes(N, C_out, HW, G) -> int:

@@ -347,3 +347,88 @@ def test_pw_conv_backward_full_size_adjoint(gpu):
     bound = (C + 2) * U32 * (np.abs(wh).T @ np.abs(ds))
     assert np.all(np.abs(xs - wh.T @ ds) <= bound)
     del x, dz, dx, z
+
+
+# ---- small planes: the SIMT kernels (HW <= SOAR_TUNE_PW_SMALL_HW) -------------------
+
+SMALL_PW_SHAPES = [
+    # (N, C_in, C_out, HW, bias)
+    (1, 256, 512, 4, True),    # SOAR Nano stride-32 pointwise convs at a 64x64 image
+    (1, 128, 256, 16, False),  # stride 16
+    (2, 64, 128, 64, True),
+    (1, 32, 64, 256, True),    # the default limit
+    (3, 5, 7, 9, True),        # C_in % 4 != 0: scalar weight loads; rows straddle waves
+    (1, 600, 40, 3, True),     # K split over 15 waves of 40 channels
+    (4, 24, 8, 1, False),      # one pixel
+    (2, 1, 3, 5, True),        # K = 1
+]
+
+
+@pytest.fixture
+def restore_pw_small(gpu):
+    old = gpu.tune_get(gpu.TUNE_PW_SMALL_HW)
+    yield
+    gpu.tune(gpu.TUNE_PW_SMALL_HW, old)
+
+
+def _assert_bwd(got, truth, bounds, what, base=None):
+    for g, t, b, name in zip(got, truth, bounds, ("dx", "dw", "db")):
+        if g is None:
+            continue
+        h = host(g).astype(np.float64).reshape(-1)
+        lim = b.reshape(-1) + 1e-30
+        if base is not None:
+            b0 = base[name].astype(np.float64).reshape(-1)
+            h = h - b0
+            lim = lim + 2 * U32 * np.abs(b0)
+        err = np.abs(h - t)
+        i = int(np.argmax(err / lim))
+        assert err[i] <= lim[i], f"{what} {name} err {err[i]:.3e} > bound {lim[i]:.3e} at {i}"
+
+
+@pytest.mark.parametrize("N,C_in,C_out,HW,bias", SMALL_PW_SHAPES)
+def test_pw_small_planes_match_oracle(gpu, oracle, restore_pw_small, N, C_in, C_out, HW, bias):
+    """Forward, fused CBA forward and backward on small planes, through the
+    SIMT kernels (limit 2^20) and through the MFMA kernels (limit 0), each
+    against the oracle's float64 results within the fp32 bounds above."""
+    print(f"pw small N={N} C_in={C_in} C_out={C_out} HW={HW}", flush=True)
+    x, w, b = rng_inputs(N * 31 + C_in + HW, N, C_in, C_out, HW, bias)
+    r = np.random.default_rng(HW + C_out)
+    dz = r.standard_normal((N, C_out, HW)).astype(np.float32)
+    gamma = r.uniform(0.5, 1.5, C_out).astype(np.float32)
+    beta = (0.1 * r.standard_normal(C_out)).astype(np.float32)
+    G = 2 if C_out % 2 == 0 else 1
+    bd = dev(b) if bias else None
+    truth_b = oracle.conv1x1_bwd_f64(dz, x, w, N, C_in, C_out, HW)
+    bounds = bwd_bounds(dz, x, w)
+    for lim in (1 << 20, 0):
+        gpu.tune(gpu.TUNE_PW_SMALL_HW, lim)
+        what = f"limit {lim}"
+        z = gpu.pw_conv_forward(dev(x), dev(w), bd)
+        assert_z(host(z), x, w, b, oracle, what)
+        zf, y, st = gpu.pw_conv_gn_silu_forward(dev(x), dev(w), bd, dev(gamma), dev(beta), G,
+                                                eps=EPS)
+        assert np.array_equal(host(zf), host(z)), what  # one kernel behind both entries
+        y_t, mean_t, rstd_t = oracle.gn_silu_fwd_f64(host(zf), gamma, beta, N, C_out, HW, G,
+                                                     EPS, silu=True)
+        assert_stats(host(st.mean), host(st.rstd), mean_t, rstd_t, what)
+        assert_vals(host(y), y_t, what + " y")
+        got = gpu.pw_conv_backward(dev(dz), dev(x), dev(w))
+        _assert_bwd(got, truth_b, bounds, what)
+    # the SIMT path's accumulation contract, and each gradient alone
+    gpu.tune(gpu.TUNE_PW_SMALL_HW, 1 << 20)
+    base = {"dx": r.standard_normal((N, C_in, HW)).astype(np.float32),
+            "dw": r.standard_normal((C_out, C_in)).astype(np.float32),
+            "db": r.standard_normal(C_out).astype(np.float32)}
+    got = gpu.pw_conv_backward(dev(dz), dev(x), dev(w), dx=dev(base["dx"]),
+                               dweight=dev(base["dw"]), dbias=dev(base["db"]),
+                               accumulate_dx=True)
+    _assert_bwd(got, truth_b, bounds, "accumulate", base)
+    for want in ("dx", "dw", "db"):
+        got = gpu.pw_conv_backward(dev(dz), dev(x), dev(w), want_dx=want == "dx",
+                                   want_dw=want == "dw", want_db=want == "db")
+        _assert_bwd(got, truth_b, bounds, f"only {want}")
+        assert sum(g is not None for g in got) == 1
+    z0 = dev(np.full((N, C_out, HW), 0.25, np.float32))
+    gpu.pw_conv_forward(dev(x), dev(w), bd, z=z0)
+    assert_z(host(z0), x, w, b, oracle, "into a given z")
