@@ -445,7 +445,7 @@ SOAR_API int soar_conv2d_1x1_forward(const float* in, const float* weight, const
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     soar::gn::PwArgs a{in, weight, bias, out};
     hipError_t e = soar::gn::launch_pw_conv(a, 1, (int64_t)C_in, (int64_t)C_out, (int64_t)HW,
-                                            chunk, nullptr, false, t.pw_small_hw,
+                                            chunk, nullptr, false, t.pw_small,
                                             static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "conv2d_1x1_forward launch");
 }
@@ -470,7 +470,7 @@ SOAR_API int soar_pw_conv_forward(const float* x, const float* weight, const flo
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     soar::gn::PwArgs a{x, weight, bias, z};
     hipError_t e = soar::gn::launch_pw_conv(a, N, C_in, C_out, HW, chunk, nullptr, false,
-                                            t.pw_small_hw, static_cast<hipStream_t>(stream));
+                                            t.pw_small, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "pointwise convolution launch");
 }
 
@@ -482,7 +482,8 @@ SOAR_API size_t soar_pw_conv_gn_workspace_bytes(int64_t N, int64_t C_out, int64_
     if (!soar::gn::make_pw_plan(N, C_out, HW, G, t, &p)) return 0;
     size_t b = soar::gn::workspace_bytes(p);
     // small planes: a plain convolution, then the GroupNorm's own plan
-    if (HW <= t.pw_small_hw && soar::gn::make_plan(N, C_out, HW, G, t, &q))
+    if (soar::gn::pw_use_small(N, C_out, 1, HW, t.pw_small) &&
+        soar::gn::make_plan(N, C_out, HW, G, t, &q))
         b = std::max(b, soar::gn::workspace_bytes(q));
     return b;
 }
@@ -523,14 +524,14 @@ SOAR_API int soar_pw_conv_gn_silu_forward(const float* x, const float* weight,
     const hipStream_t s = static_cast<hipStream_t>(stream);
     soar::gn::PwArgs pa{x, weight, bias, z};
     Plan q;
-    if (HW <= t.pw_small_hw && soar::gn::pw_small_fits(N, C_out, C_in, HW) &&
+    if (soar::gn::pw_use_small(N, C_out, C_in, HW, t.pw_small) &&
         soar::gn::make_plan(N, C_out, HW, G, t, &q)) {
         // Small planes: the SIMT convolution (no statistics epilogue), then
         // the GroupNorm forward over z with its own plan.
         q.vec4 = q.vec4 && aligned16(z) && aligned16(y);
         if ((rc = check_ws(q, workspace, workspace_bytes))) return rc;
         hipError_t e = soar::gn::launch_pw_conv(pa, N, C_in, C_out, HW, p.chunk, nullptr, false,
-                                                t.pw_small_hw, s);
+                                                t.pw_small, s);
         if (e != hipSuccess) return hip_fail(e, "pointwise convolution launch");
         soar::gn::FwdArgs a{z, gamma, beta, y, mean, rstd, mean_lo, eps, flags, workspace};
         e = soar::gn::launch_forward(q, t, a, s);
@@ -590,7 +591,7 @@ SOAR_API int soar_pw_conv_backward(const float* dz, const float* x, const float*
     soar::gn::PwBwdArgs a{dz, x, weight, dx, dweight, dbias, workspace};
     hipError_t e = soar::gn::launch_pw_backward(p, a, N, C_in, C_out, HW, t.pw_chunk,
                                                 (flags & SOAR_GN_ACCUMULATE_DX) != 0,
-                                                t.pw_small_hw, static_cast<hipStream_t>(stream));
+                                                t.pw_small, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "pointwise convolution backward launch");
     return ok();
 }
@@ -1009,10 +1010,10 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
                 return fail(SOAR_EINVAL, "small_unit must be in [0, 2^20]");
             g_tune.small_unit = value;
             return ok();
-        case SOAR_TUNE_PW_SMALL_HW:
-            if (value < 0 || value > (1 << 20))
-                return fail(SOAR_EINVAL, "pw_small_hw must be in [0, 2^20]");
-            g_tune.pw_small_hw = value;
+        case SOAR_TUNE_PW_SMALL:
+            if (value < 0 || value > ((int64_t)1 << 40))
+                return fail(SOAR_EINVAL, "pw_small must be in [0, 2^40]");
+            g_tune.pw_small = value;
             return ok();
         default:
             return fail(SOAR_EINVAL, "unknown tuning key %d", key);
@@ -1031,7 +1032,7 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
         case SOAR_TUNE_NT_LOAD: return g_tune.nt_load;
         case SOAR_TUNE_PW_CHUNK: return g_tune.pw_chunk;
         case SOAR_TUNE_SMALL_UNIT: return g_tune.small_unit;
-        case SOAR_TUNE_PW_SMALL_HW: return g_tune.pw_small_hw;
+        case SOAR_TUNE_PW_SMALL: return g_tune.pw_small;
         default: return -1;
     }
 }

@@ -60,9 +60,10 @@ struct Tuning {
                               // partials' chunk
     int64_t small_unit = 32768;  // units of at most this many elements run
                                  // the one-launch GroupNorm (0: never)
-    int64_t pw_small_hw = 256;   // pointwise convolutions over planes of at
-                                 // most this many pixels (weight gradient:
-                                 // N*HW) run the SIMT kernels (0: never)
+    int64_t pw_small = 262144;   // pointwise convolutions with at most this
+                                 // many output elements (weight gradient:
+                                 // 64x this many multiply-adds) run the SIMT
+                                 // kernels (0: never)
 };
 
 constexpr int kThreads = 256;   // first passes (stats, reduction)
@@ -136,14 +137,15 @@ int64_t pw_pick_chunk(int64_t N, int64_t C_out, int64_t HW, int64_t max_chunk);
 // `chunk` pixels (a multiple of 128, normally from pw_pick_chunk),
 // part[(n*C_out + co)*cpp + k].
 // `name` labels the launch for the kernel timers (null: a default).
-// Without `part`, planes of at most `small_hw` pixels run the SIMT kernel
-// (K split over the waves of a block) when pw_small_fits.
+// Without `part`, the SIMT kernel (K split over the waves of a block) runs
+// when pw_use_small(N, C_out, C_in, HW, small).
 hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
                           int64_t HW, int64_t chunk, double2* part, bool accumulate,
-                          int64_t small_hw, hipStream_t s, const char* name = nullptr);
-// The SIMT kernels index one sample with 32-bit element offsets and put the
-// samples on grid.y.
-bool pw_small_fits(int64_t N, int64_t M, int64_t K, int64_t HW);
+                          int64_t small, hipStream_t s, const char* name = nullptr);
+// True when the SIMT kernel computes the M x HW outputs of N samples (K
+// terms each): at most `small` output elements, and offsets inside a sample
+// fit in 32 bits.
+bool pw_use_small(int64_t N, int64_t M, int64_t K, int64_t HW, int64_t small);
 
 // Backward of the pointwise convolution: dx = W^T dz (written, or added
 // with `accumulate_dx`), dw += sum dz x^T, db += sum dz; any output may be
@@ -165,11 +167,12 @@ struct PwBwdPlan {
 };
 PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW);
 size_t pw_bwd_workspace_bytes(const PwBwdPlan& p);
-// dx runs the SIMT kernel when HW <= small_hw, dW/db when N*HW <= small_hw
-// (then the workspace is not touched).
+// dx runs the SIMT kernel when pw_use_small(N, C_in, C_out, HW, small),
+// dW/db when the weight gradient has at most 64*small multiply-adds (then
+// the workspace is not touched).
 hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N, int64_t C_in,
                               int64_t C_out, int64_t HW, int64_t chunk_dx, bool accumulate_dx,
-                              int64_t small_hw, hipStream_t s);
+                              int64_t small, hipStream_t s);
 
 // Depthwise convolution (dw_conv.hip): groups = C_in = C_out, weights
 // [C][K][K], output size given by the caller, taps outside the input skipped.

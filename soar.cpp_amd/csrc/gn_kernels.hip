@@ -654,39 +654,34 @@ __device__ __forceinline__ void small_load(const float* unit, int64_t M, int64_t
             float, __builtin_amdgcn_raw_buffer_load_b32(rs, vo, (k0 + k) * m.tpc * 4, 0));
 }
 
-// Sum of v over the block, fixed order, returned to every thread.
-template <int NT, typename T>
-__device__ __forceinline__ T small_block_sum(T v, T* lds /*[NT / 64]*/) {
-    v = wave_sum(v);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    if (lane == 0) lds[w] = v;
-    __syncthreads();
-    T r = lds[0];
-#pragma unroll
-    for (int i = 1; i < NT / 64; ++i) r += lds[i];
-    __syncthreads();
-    return r;
-}
-
-// Sum of v over the tpc threads of each channel; valid in the channel's
-// rank-0 thread (wave tree within 64 lanes, then the channel's waves in
-// order through LDS).
-__device__ __forceinline__ double channel_sum(double v, const SmallMap& m, double* lds) {
+// Sums of (a, b) over the tpc threads of each channel; valid in the
+// channel's rank-0 thread (xor tree within 64 lanes, else wave trees and
+// then the channel's waves in order through LDS).
+__device__ __forceinline__ void channel_sum2(double& a, double& b, const SmallMap& m,
+                                             double2* lds) {
     if (m.tpc <= 64) {
-        for (int off = m.tpc >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off);
-        return v;
+        for (int off = m.tpc >> 1; off > 0; off >>= 1) {
+            a += __shfl_xor(a, off);
+            b += __shfl_xor(b, off);
+        }
+        return;
     }
-    v = wave_sum(v);
+    a = wave_sum(a);
+    b = wave_sum(b);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    if (lane == 0) lds[w] = v;
+    if (lane == 0) lds[w] = make_double2(a, b);
     __syncthreads();
-    double r = 0.0;
+    double ra = 0.0, rb = 0.0;
     if (m.r == 0) {
-        const int w0 = w, nw = m.tpc >> 6;
-        for (int i = 0; i < nw; ++i) r += lds[w0 + i];
+        const int nw = m.tpc >> 6;
+        for (int i = 0; i < nw; ++i) {
+            ra += lds[w + i].x;
+            rb += lds[w + i].y;
+        }
     }
     __syncthreads();
-    return r;
+    a = ra;
+    b = rb;
 }
 
 template <bool SILU, bool RES>
@@ -712,10 +707,14 @@ __global__ __launch_bounds__(NT) void k_small_fwd(
     const float* __restrict__ beta, float* __restrict__ y, float* __restrict__ mean,
     float* __restrict__ rstd, float* __restrict__ mean_lo, int64_t G, int64_t cpg, int64_t HW,
     int lg, float eps) {
-    __shared__ double lds[NT / 64];
+    __shared__ double2 lds[NT / 64];
     const int64_t u = blockIdx.x;
     const SmallMap m = small_map(lg, cpg, HW);
     const bool live = m.j < cpg;
+    // the affine parameters' loads go out with the unit's
+    const int64_t c = (u % G) * cpg + m.j;
+    const float gm = (live && gamma) ? gamma[c] : 1.0f;
+    const float bt = (live && beta) ? beta[c] : 0.0f;
     float xv[kSmallPer];
     small_load(x + u * cpg * HW, cpg * HW, HW, m, xv);  // a unit is contiguous in NCHW
     const double K = (double)x[u * cpg * HW];
@@ -728,9 +727,19 @@ __global__ __launch_bounds__(NT) void k_small_fwd(
             q = fma(d, d, q);
         }
     }
+    // both sums over the block in one exchange, waves added in order
+    s = wave_sum(s);
+    q = wave_sum(q);
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = make_double2(s, q);
+    __syncthreads();
+    s = lds[0].x;
+    q = lds[0].y;
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i) {
+        s += lds[i].x;
+        q += lds[i].y;
+    }
     const double M = (double)(cpg * HW);
-    s = small_block_sum<NT>(s, lds);
-    q = small_block_sum<NT>(q, lds);
     const double sm = s / M;
     const double md = K + sm;
     const double var = fmax(q / M - sm * sm, 0.0);
@@ -742,9 +751,6 @@ __global__ __launch_bounds__(NT) void k_small_fwd(
         rstd[u] = r;
         if (mean_lo) mean_lo[u] = lo;
     }
-    const int64_t c = (u % G) * cpg + m.j;
-    const float gm = (live && gamma) ? gamma[c] : 1.0f;
-    const float bt = (live && beta) ? beta[c] : 0.0f;
     small_apply_regs<SILU, RES>(xv, y + (u * cpg + (live ? m.j : 0)) * HW, m, gm, bt, hi, r, lo);
 }
 
@@ -811,22 +817,28 @@ __global__ __launch_bounds__(NT) void k_small_finish_apply(
 }
 
 // Backward: one block per group g walks the samples in order.  Per unit:
-// per-channel float64 sums of dz and dz*xhat, S1 and S2 from them in
-// channel order, then dx from the registers; the channel sums are added
-// over samples in order into dgamma / dbeta at the end (as k_param_finish).
-template <int NT, bool SILU, bool RES, bool ACC>
+// per-channel float64 sums of dz and dz*xhat, S1 = sum_j gamma_j sum(dz)_j
+// and S2 likewise (every wave forms them from LDS in the same fixed order,
+// so no broadcast is needed), then dx.  ONE: a thread holds at most 16
+// elements, kept in registers for dx; otherwise the elements come in two
+// halves of 16 and dx reloads them (L2-resident): keeping both halves
+// alive across the reductions would not fit in 128 registers.  The channel
+// sums are added over samples in order into dgamma / dbeta at the end (as
+// k_param_finish).
+template <int NT, bool SILU, bool RES, bool ACC, bool ONE>
 __global__ __launch_bounds__(NT) void k_small_bwd(
     const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ mean_lo, float* __restrict__ dx,
     float* __restrict__ dgamma, float* __restrict__ dbeta, int64_t N, int64_t C, int64_t G,
     int64_t cpg, int64_t HW, int lg) {
+    constexpr int kHalves = ONE ? 1 : kSmallPer / kSmallHalf;
     __shared__ double chA[kMaxSmallCpg], chB[kMaxSmallCpg];
-    __shared__ double lds[NT / 64];
-    __shared__ double S[2];
+    __shared__ double2 lds[NT / 64];
     const int64_t g = blockIdx.x;
     const SmallMap m = small_map(lg, cpg, HW);
     const bool live = m.j < cpg;
+    const int lane = threadIdx.x & 63;
     const int64_t c = g * cpg + m.j;
     const float gm = (live && gamma) ? gamma[c] : 1.0f;
     const float bt = (live && beta) ? beta[c] : 0.0f;
@@ -839,11 +851,10 @@ __global__ __launch_bounds__(NT) void k_small_bwd(
         const float mu = mean[u], r = rstd[u];
         const float e = mean_lo ? -mean_lo[u] * r : 0.0f;
         double sa = 0.0, sb = 0.0;
-        // two halves of 16 elements keep the loads and their products
-        // within 128 registers
+        float xv[kSmallHalf], gv[kSmallHalf];
 #pragma unroll
-        for (int h = 0; h < kSmallPer; h += kSmallHalf) {
-            float xv[kSmallHalf], gv[kSmallHalf];
+        for (int hh = 0; hh < kHalves; ++hh) {
+            const int h = hh * kSmallHalf;
             small_load<kSmallHalf>(xu, cpg * HW, HW, m, xv, h);
             small_load<kSmallHalf>(gu, cpg * HW, HW, m, gv, h);
 #pragma unroll
@@ -856,57 +867,65 @@ __global__ __launch_bounds__(NT) void k_small_bwd(
                 }
             }
         }
-        sa = channel_sum(sa, m, lds);
-        sb = channel_sum(sb, m, lds);
+        channel_sum2(sa, sb, m, lds);
         if (live && m.r == 0) {
-            chA[m.j] = sa;
-            chB[m.j] = sb;
+            chA[m.j] = (double)gm * sa;
+            chB[m.j] = (double)gm * sb;
             accA += sa;
             accB += sb;
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            double s1 = 0.0, s2 = 0.0;
-            for (int64_t j = 0; j < cpg; ++j) {
-                const double gj = gamma ? (double)gamma[g * cpg + j] : 1.0;
-                s1 += gj * chA[j];
-                s2 += gj * chB[j];
-            }
-            S[0] = s1;
-            S[1] = s2;
-        }
-        __syncthreads();
         if (dx) {
+            double s1 = 0.0, s2 = 0.0;
+            for (int64_t j = lane; j < cpg; j += 64) {
+                s1 += chA[j];
+                s2 += chB[j];
+            }
+            s1 = __shfl(wave_sum(s1), 0);
+            s2 = __shfl(wave_sum(s2), 0);
             const double Md = (double)(cpg * HW);
-            const float B = (float)(-(double)r * S[0] / Md);
-            const float D = (float)(-(double)r * S[1] / Md);
-            // reload x and dy (L2-resident) and recompute xhat and dz:
-            // keeping the first loop's values alive across the reductions
-            // would not fit in 128 registers
-            float mu2 = mu, r2 = r, e2 = e, gm2 = gm, bt2 = bt;
-            asm volatile("" : "+v"(mu2), "+v"(r2), "+v"(e2), "+v"(gm2), "+v"(bt2));
-            const float A = gm2 * r2;
+            const float B = (float)(-(double)r * s1 / Md);
+            const float D = (float)(-(double)r * s2 / Md);
             float* dc = dx + off;
-#pragma unroll
-            for (int h = 0; h < kSmallPer; h += kSmallHalf) {
-                float xv[kSmallHalf], gv[kSmallHalf];
-                small_load<kSmallHalf>(xu, cpg * HW, HW, m, xv, h);
-                small_load<kSmallHalf>(gu, cpg * HW, HW, m, gv, h);
+            if (ONE) {
+                const float A = gm * r;
 #pragma unroll
                 for (int k = 0; k < kSmallHalf; ++k) {
-                    const int i = m.r + (h + k) * m.tpc;
-                    if (h + k < m.nk) {
-                        const float xh = fmaf(xv[k] - mu2, r2, e2);
-                        const float dz = SILU ? dsilu_fast(gv[k], fmaf(gm2, xh, bt2)) : gv[k];
+                    const int i = m.r + k * m.tpc;
+                    if (k < m.nk) {
+                        const float xh = fmaf(xv[k] - mu, r, e);
+                        const float dz = SILU ? dsilu_fast(gv[k], fmaf(gm, xh, bt)) : gv[k];
                         float o = fmaf(A, dz, fmaf(D, xh, B));
                         if (RES) o += gv[k];
                         if (ACC) o += dc[i];
                         dc[i] = o;
                     }
                 }
+            } else {
+                float mu2 = mu, r2 = r, e2 = e, gm2 = gm, bt2 = bt;
+                asm volatile("" : "+v"(mu2), "+v"(r2), "+v"(e2), "+v"(gm2), "+v"(bt2));
+                const float A = gm2 * r2;
+#pragma unroll
+                for (int h = 0; h < kSmallPer; h += kSmallHalf) {
+                    small_load<kSmallHalf>(xu, cpg * HW, HW, m, xv, h);
+                    small_load<kSmallHalf>(gu, cpg * HW, HW, m, gv, h);
+#pragma unroll
+                    for (int k = 0; k < kSmallHalf; ++k) {
+                        const int i = m.r + (h + k) * m.tpc;
+                        if (h + k < m.nk) {
+                            const float xh = fmaf(xv[k] - mu2, r2, e2);
+                            const float dz =
+                                SILU ? dsilu_fast(gv[k], fmaf(gm2, xh, bt2)) : gv[k];
+                            float o = fmaf(A, dz, fmaf(D, xh, B));
+                            if (RES) o += gv[k];
+                            if (ACC) o += dc[i];
+                            dc[i] = o;
+                        }
+                    }
+                }
             }
         }
-        __syncthreads();  // chA / chB / S are rewritten by the next sample
+        if (n + 1 < N) __syncthreads();  // chA / chB are rewritten by the next sample
     }
     if (dgamma && live && m.r == 0) {
         dbeta[c] = (float)((double)dbeta[c] + accA);
@@ -1263,13 +1282,17 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hip
     if (small_bwd(p, t)) {
         const int tok = prof_begin(s, "gn_small_bwd");
         const int nt = small_threads(p, t);
+        const int lg = small_lg(p, t, nt);
         nt_sel(nt, [&](auto NT) {
             bsel(silu, [&](auto S) {
                 bsel((a.flags & SOAR_GN_RESIDUAL) != 0, [&](auto R) {
                     bsel((a.flags & SOAR_GN_ACCUMULATE_DX) != 0, [&](auto A) {
-                        k_small_bwd<NT(), S(), R(), A()><<<dim3((unsigned)p.G), NT(), 0, s>>>(
-                            a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, a.dx,
-                            a.dgamma, a.dbeta, p.N, p.C, p.G, p.cpg, p.HW, small_lg(p, t, nt));
+                        bsel(p.HW <= ((int64_t)kSmallHalf << lg), [&](auto O) {
+                            k_small_bwd<NT(), S(), R(), A(), O()>
+                                <<<dim3((unsigned)p.G), NT(), 0, s>>>(
+                                    a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, a.dx,
+                                    a.dgamma, a.dbeta, p.N, p.C, p.G, p.cpg, p.HW, lg);
+                        });
                     });
                 });
             });

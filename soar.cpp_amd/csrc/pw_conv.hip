@@ -524,10 +524,11 @@ __global__ void k_transpose(const float* __restrict__ w, float* __restrict__ wt,
 }
 
 // ======================================================================
-// Small planes (HW <= Tuning::pw_small_hw).  The MFMA kernels above give a
-// wave 128-pixel items and walk K one 8-channel step at a time; on planes of
-// a few pixels most of each item is empty and a handful of waves wait on one
-// load after another.  Here one lane owns one output element z[n][m][p]
+// Small convolutions (Tuning::pw_small).  The MFMA kernels above give a
+// wave a 64-row x 128-pixel tile and walk all of K on it; a small output
+// has few such tiles, so a few waves run K/8 dependent MFMA steps each
+// (about 0.1 us per channel of K) while the chip idles, and on planes of a
+// few pixels most of each tile is empty.  Here one lane owns one output element z[n][m][p]
 // (64 consecutive elements of a sample per wave: pixels fastest, then rows)
 // and the K axis is split over the S waves of a block: wave v sums its
 // contiguous k segment in fp32, then wave 0 adds the S partial sums in
@@ -617,51 +618,83 @@ __global__ __launch_bounds__(1024) void k_pw_small(const float* __restrict__ x,
 }
 
 // dW[co][ci] += sum_(n,p) dz[n][co][p] x[n][ci][p], db[co] += sum_(n,p)
-// dz[n][co][p] for small planes: one lane per weight (ci fastest, so a
-// wave's x loads are consecutive rows), the (n, p) sum in float64 in a
-// fixed order.  Lanes e in [E, E + C_out) own the bias entries; the grid
-// starts at e0 (E when only db is wanted).  V4: HW % 4 == 0 and 16-byte
-// aligned dz and x.
+// dz[n][co][p] for small planes.  Entry e (weights ci-fastest, then the
+// C_out bias entries from E = C_out*C_in on) belongs to T = 2^lgT
+// consecutive lanes; lane t sums the flattened (n, p) range [t*seg,
+// (t+1)*seg) in float64, and the T partial sums meet in a fixed xor tree.
+// A wave's x loads are consecutive pixels of consecutive rows; dz loads of
+// one entry are shared by its lanes.  The grid covers entries [e0, e1)
+// (e0 = E when only db is wanted).  V4: HW % 4 == 0, seg % 4 == 0 and
+// 16-byte aligned dz and x.
 template <bool V4>
 __global__ __launch_bounds__(256) void k_pw_wgrad_small(const float* __restrict__ dz,
                                                         const float* __restrict__ x,
                                                         float* __restrict__ dw,
                                                         float* __restrict__ db, int N, int C_in,
                                                         int C_out, int HW, int64_t e0,
-                                                        int64_t e1) {
-    const int64_t e = e0 + (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (e >= e1) return;
+                                                        int64_t e1, int lgT, int seg) {
+    constexpr int W = V4 ? 4 : 1;  // pixels per load
+    constexpr int U = 4;           // loads in flight per operand
+    const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int t = (int)(tid & ((1 << lgT) - 1));
+    const int64_t e = e0 + (tid >> lgT);
+    const bool valid = e < e1;
     const int64_t E = (int64_t)C_out * C_in;
-    const bool wt = e < E;
-    const int co = wt ? (int)(e / C_in) : (int)(e - E);
-    const int ci = wt ? (int)(e - (int64_t)co * C_in) : 0;
+    const int64_t ec = valid ? e : e1 - 1;
+    const bool wt = ec < E;
+    const int co = wt ? (int)(ec / C_in) : (int)(ec - E);
+    const int ci = wt ? (int)(ec - (int64_t)co * C_in) : 0;
+    const int64_t total = (int64_t)N * HW;
+    int64_t q = (int64_t)t * seg;
+    const int64_t qe = min(total, q + seg);
     double acc = 0.0;
-    for (int n = 0; n < N; ++n) {
-        const float* a = dz + ((int64_t)n * C_out + co) * HW;
-        const float* b = x + ((int64_t)n * C_in + ci) * HW;
-        if (V4) {
-            for (int p = 0; p < HW; p += 4) {
-                const float4 av = *reinterpret_cast<const float4*>(a + p);
+    if (q < qe) {
+        const int n0 = (int)(q / HW);
+        int p = (int)(q - (int64_t)n0 * HW);
+        const float* a = dz + ((int64_t)n0 * C_out + co) * HW;
+        const float* b = x + ((int64_t)n0 * C_in + ci) * HW;
+        const int64_t astep = (int64_t)C_out * HW, bstep = (int64_t)C_in * HW;
+        auto fetch = [&](float (&av)[W], float (&bv)[W]) {
+            if (V4) {
+                const float4 u = *reinterpret_cast<const float4*>(a + p);
+                av[0] = u.x, av[1] = u.y, av[2] = u.z, av[3] = u.w;
                 if (wt) {
-                    const float4 bv = *reinterpret_cast<const float4*>(b + p);
-                    acc += (double)av.x * (double)bv.x;
-                    acc += (double)av.y * (double)bv.y;
-                    acc += (double)av.z * (double)bv.z;
-                    acc += (double)av.w * (double)bv.w;
-                } else {
-                    acc += (double)av.x;
-                    acc += (double)av.y;
-                    acc += (double)av.z;
-                    acc += (double)av.w;
+                    const float4 v = *reinterpret_cast<const float4*>(b + p);
+                    bv[0] = v.x, bv[1] = v.y, bv[2] = v.z, bv[3] = v.w;
                 }
+            } else {
+                av[0] = a[p];
+                if (wt) bv[0] = b[p];
             }
-        } else {
-            for (int p = 0; p < HW; ++p)
-                acc += wt ? (double)a[p] * (double)b[p] : (double)a[p];
+            // next position: wrap to the following sample's plane
+            p += W;
+            const bool wrap = p == HW;
+            p = wrap ? 0 : p;
+            a = wrap ? a + astep : a;
+            b = wrap ? b + bstep : b;
+        };
+        auto add = [&](const float (&av)[W], const float (&bv)[W]) {
+#pragma unroll
+            for (int i = 0; i < W; ++i) acc += wt ? (double)av[i] * (double)bv[i] : (double)av[i];
+        };
+        for (; q + U * W <= qe; q += U * W) {
+            float av[U][W], bv[U][W];
+#pragma unroll
+            for (int u = 0; u < U; ++u) fetch(av[u], bv[u]);
+#pragma unroll
+            for (int u = 0; u < U; ++u) add(av[u], bv[u]);
+        }
+        for (; q < qe; q += W) {
+            float av[W], bv[W];
+            fetch(av, bv);
+            add(av, bv);
         }
     }
-    float* out = wt ? dw + e : db + co;
-    *out = (float)((double)*out + acc);
+    for (int off = (1 << lgT) >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (valid && t == 0) {
+        float* out = wt ? dw + ec : db + co;
+        *out = (float)((double)*out + acc);
+    }
 }
 
 template <typename F>
@@ -692,9 +725,29 @@ int64_t pw_pick_chunk(int64_t N, int64_t C_out, int64_t HW, int64_t max_chunk) {
     return std::max<int64_t>(kItem, std::min<int64_t>(c, max_chunk));
 }
 
+namespace {
 bool pw_small_fits(int64_t N, int64_t M, int64_t K, int64_t HW) {
     const int64_t lim = (int64_t)1 << 31;
     return N <= 65535 && M * HW < lim && K * HW < lim && M < lim && K < lim;
+}
+
+// Weight gradient on the SIMT kernel: at most 64*small multiply-adds.
+// Measured on MI355X (one sample, single launches): the SIMT kernel wins up
+// to about 2^24 multiply-adds (e.g. 64x128 channels at 2048 pixels: 24 vs
+// 30 us), the MFMA tiles from about 2^25 on.
+bool pw_use_small_wgrad(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t small) {
+    return small > 0 &&
+           (double)N * (double)HW * (double)C_in * (double)C_out <= 64.0 * (double)small &&
+           pw_small_fits(N, C_out, C_in, HW);
+}
+}  // namespace
+
+// Measured on MI355X (one sample, single launches): the SIMT kernel wins up
+// to about 2^18 output elements whatever K is (e.g. 512 -> 256 channels at
+// 1024 pixels: 35 vs 60 us; 64 -> 128 at 4096: 11 vs 12 us), ties at 2^19
+// and loses above (128 -> 256 at 4096: 35 vs 19 us).
+bool pw_use_small(int64_t N, int64_t M, int64_t K, int64_t HW, int64_t small) {
+    return small > 0 && pw_small_fits(N, M, K, HW) && N * M * HW <= small;
 }
 
 namespace {
@@ -735,9 +788,9 @@ hipError_t launch_pw_small(const float* x, const float* w, const float* bias, fl
 
 hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
                           int64_t HW, int64_t chunk, double2* part, bool accumulate,
-                          int64_t small_hw, hipStream_t s, const char* name) {
+                          int64_t small, hipStream_t s, const char* name) {
     if (N == 0 || HW == 0 || C_out == 0) return hipSuccess;
-    if (!part && HW <= small_hw && pw_small_fits(N, C_out, C_in, HW))
+    if (!part && pw_use_small(N, C_out, C_in, HW, small))
         return launch_pw_small(a.x, a.w, a.bias, a.z, N, C_in, C_out, HW, false, accumulate, s,
                                name ? name : "pw_conv_small");
     const int64_t cpp = (HW + chunk - 1) / chunk;
@@ -800,13 +853,13 @@ size_t pw_bwd_workspace_bytes(const PwBwdPlan& p) { return p.wt_bytes + p.pw_byt
 
 hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N, int64_t C_in,
                               int64_t C_out, int64_t HW, int64_t chunk_dx, bool accumulate_dx,
-                              int64_t small_hw, hipStream_t s) {
+                              int64_t small, hipStream_t s) {
     if (N == 0 || HW == 0 || C_out == 0 || C_in == 0) return hipSuccess;
     char* ws = static_cast<char*>(a.ws);
     float* wt = reinterpret_cast<float*>(ws);
     float* part_w = reinterpret_cast<float*>(ws + p.wt_bytes);
     float* part_b = reinterpret_cast<float*>(ws + p.wt_bytes + p.pw_bytes);
-    if (a.dx && HW <= small_hw && pw_small_fits(N, C_in, C_out, HW)) {
+    if (a.dx && pw_use_small(N, C_in, C_out, HW, small)) {
         // dx = W^T dz, reading W transposed in place
         hipError_t e = launch_pw_small(a.dz, a.w, nullptr, a.dx, N, C_out, C_in, HW, true,
                                        accumulate_dx, s, "pw_conv_dgrad_small");
@@ -823,14 +876,22 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
                                       accumulate_dx, 0, s, "pw_conv_dgrad");
         if (e != hipSuccess) return e;
     }
-    if ((a.dw || a.db) && N * HW <= small_hw && pw_small_fits(N, C_out, C_in, HW)) {
+    if ((a.dw || a.db) && pw_use_small_wgrad(N, C_in, C_out, HW, small)) {
         const int64_t E = C_out * C_in;
         const int64_t e0 = a.dw ? 0 : E, e1 = a.db ? E + C_out : E;
         const bool v4 = (HW % 4 == 0) && ((uintptr_t)a.dz % 16 == 0) && ((uintptr_t)a.x % 16 == 0);
+        // lanes per entry: about 64K lanes in all, segments of >= 8 pixels
+        const int64_t nhw = N * HW, ne = e1 - e0;
+        int lgT = 0;
+        while (lgT < 6 && (ne << lgT) < 65536 && nhw > ((int64_t)8 << lgT)) ++lgT;
+        int64_t seg = (nhw + (1 << lgT) - 1) >> lgT;
+        if (v4) seg = (seg + 3) / 4 * 4;
+        const int64_t lanes = ne << lgT;
         const int tok = prof_begin(s, "pw_conv_wgrad_small");
         bsel(v4, [&](auto V) {
-            k_pw_wgrad_small<V()><<<dim3((unsigned)((e1 - e0 + 255) / 256)), 256, 0, s>>>(
-                a.dz, a.x, a.dw, a.db, (int)N, (int)C_in, (int)C_out, (int)HW, e0, e1);
+            k_pw_wgrad_small<V()><<<dim3((unsigned)((lanes + 255) / 256)), 256, 0, s>>>(
+                a.dz, a.x, a.dw, a.db, (int)N, (int)C_in, (int)C_out, (int)HW, e0, e1, lgT,
+                (int)seg);
         });
         prof_end(s, tok);
     } else if (a.dw || a.db) {

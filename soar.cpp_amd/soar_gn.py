@@ -41,7 +41,7 @@ TUNE_NT_LOAD = 6
 TUNE_CHUNK2 = 7
 TUNE_PW_CHUNK = 8
 TUNE_SMALL_UNIT = 9
-TUNE_PW_SMALL_HW = 10
+TUNE_PW_SMALL = 10
 
 
 class SoarUnavailable(RuntimeError):

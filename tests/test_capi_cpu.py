@@ -187,14 +187,14 @@ def test_pw_chunk_tuning(L):
     assert soar_gn.tune_get(soar_gn.TUNE_PW_CHUNK) == 1024
 
 
-def test_pw_small_hw_tuning(L):
-    old = soar_gn.tune_get(soar_gn.TUNE_PW_SMALL_HW)
-    assert old == 256
-    assert L.soar_gn_tune(soar_gn.TUNE_PW_SMALL_HW, -1) == soar_gn.SOAR_EINVAL
-    assert L.soar_gn_tune(soar_gn.TUNE_PW_SMALL_HW, (1 << 20) + 1) == soar_gn.SOAR_EINVAL
+def test_pw_small_tuning(L):
+    old = soar_gn.tune_get(soar_gn.TUNE_PW_SMALL)
+    assert old == 262144
+    assert L.soar_gn_tune(soar_gn.TUNE_PW_SMALL, -1) == soar_gn.SOAR_EINVAL
+    assert L.soar_gn_tune(soar_gn.TUNE_PW_SMALL, (1 << 40) + 1) == soar_gn.SOAR_EINVAL
     # small planes: the workspace also covers the GroupNorm's own plan
     big = soar_gn.pw_conv_gn_workspace_bytes(1, 512, 4, 8)
-    soar_gn.tune(soar_gn.TUNE_PW_SMALL_HW, 0)
+    soar_gn.tune(soar_gn.TUNE_PW_SMALL, 0)
     assert soar_gn.pw_conv_gn_workspace_bytes(1, 512, 4, 8) <= big
-    soar_gn.tune(soar_gn.TUNE_PW_SMALL_HW, old)
-    assert soar_gn.tune_get(soar_gn.TUNE_PW_SMALL_HW) == old
+    soar_gn.tune(soar_gn.TUNE_PW_SMALL, old)
+    assert soar_gn.tune_get(soar_gn.TUNE_PW_SMALL) == old

@@ -548,6 +548,8 @@ SMALL_SHAPES = [
     (2, 64, 255, 8, "normal"),        # ragged HW, two samples
     (5, 12, 100, 4, "offset"),        # large mean, five samples walked in order
     (1, 4, 1, 2, "offset"),           # HW = 1
+    (2, 4, 8000, 4, "offset"),        # 256 threads, 32 elements each: two halves in dx
+    (1, 2, 30000, 2, "normal"),       # 1024 threads on one channel, two halves
 ]
 
 

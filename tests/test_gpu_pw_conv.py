@@ -349,26 +349,28 @@ def test_pw_conv_backward_full_size_adjoint(gpu):
     del x, dz, dx, z
 
 
-# ---- small planes: the SIMT kernels (HW <= SOAR_TUNE_PW_SMALL_HW) -------------------
+# ---- small convolutions: the SIMT kernels (SOAR_TUNE_PW_SMALL) ---------------------
 
 SMALL_PW_SHAPES = [
     # (N, C_in, C_out, HW, bias)
     (1, 256, 512, 4, True),    # SOAR Nano stride-32 pointwise convs at a 64x64 image
     (1, 128, 256, 16, False),  # stride 16
     (2, 64, 128, 64, True),
-    (1, 32, 64, 256, True),    # the default limit
+    (1, 32, 64, 256, True),
+    (1, 64, 128, 2048, True),  # 2^18 outputs: the default limit
     (3, 5, 7, 9, True),        # C_in % 4 != 0: scalar weight loads; rows straddle waves
     (1, 600, 40, 3, True),     # K split over 15 waves of 40 channels
     (4, 24, 8, 1, False),      # one pixel
     (2, 1, 3, 5, True),        # K = 1
+    (3, 16, 24, 100, True),    # weight-gradient segments cross sample planes
 ]
 
 
 @pytest.fixture
 def restore_pw_small(gpu):
-    old = gpu.tune_get(gpu.TUNE_PW_SMALL_HW)
+    old = gpu.tune_get(gpu.TUNE_PW_SMALL)
     yield
-    gpu.tune(gpu.TUNE_PW_SMALL_HW, old)
+    gpu.tune(gpu.TUNE_PW_SMALL, old)
 
 
 def _assert_bwd(got, truth, bounds, what, base=None):
@@ -388,9 +390,9 @@ def _assert_bwd(got, truth, bounds, what, base=None):
 
 @pytest.mark.parametrize("N,C_in,C_out,HW,bias", SMALL_PW_SHAPES)
 def test_pw_small_planes_match_oracle(gpu, oracle, restore_pw_small, N, C_in, C_out, HW, bias):
-    """Forward, fused CBA forward and backward on small planes, through the
-    SIMT kernels (limit 2^20) and through the MFMA kernels (limit 0), each
-    against the oracle's float64 results within the fp32 bounds above."""
+    """Forward, fused CBA forward and backward of small convolutions, through
+    the SIMT kernels (limit 2^40) and through the MFMA kernels (limit 0),
+    each against the oracle's float64 results within the fp32 bounds above."""
     print(f"pw small N={N} C_in={C_in} C_out={C_out} HW={HW}", flush=True)
     x, w, b = rng_inputs(N * 31 + C_in + HW, N, C_in, C_out, HW, bias)
     r = np.random.default_rng(HW + C_out)
@@ -401,8 +403,8 @@ def test_pw_small_planes_match_oracle(gpu, oracle, restore_pw_small, N, C_in, C_
     bd = dev(b) if bias else None
     truth_b = oracle.conv1x1_bwd_f64(dz, x, w, N, C_in, C_out, HW)
     bounds = bwd_bounds(dz, x, w)
-    for lim in (1 << 20, 0):
-        gpu.tune(gpu.TUNE_PW_SMALL_HW, lim)
+    for lim in (1 << 40, 0):
+        gpu.tune(gpu.TUNE_PW_SMALL, lim)
         what = f"limit {lim}"
         z = gpu.pw_conv_forward(dev(x), dev(w), bd)
         assert_z(host(z), x, w, b, oracle, what)
@@ -416,7 +418,7 @@ def test_pw_small_planes_match_oracle(gpu, oracle, restore_pw_small, N, C_in, C_
         got = gpu.pw_conv_backward(dev(dz), dev(x), dev(w))
         _assert_bwd(got, truth_b, bounds, what)
     # the SIMT path's accumulation contract, and each gradient alone
-    gpu.tune(gpu.TUNE_PW_SMALL_HW, 1 << 20)
+    gpu.tune(gpu.TUNE_PW_SMALL, 1 << 40)
     base = {"dx": r.standard_normal((N, C_in, HW)).astype(np.float32),
             "dw": r.standard_normal((C_out, C_in)).astype(np.float32),
             "db": r.standard_normal(C_out).astype(np.float32)}
