@@ -369,10 +369,10 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
 #define SOAR_TUNE_SMALL_UNIT 9 /* units of <= this many elements run the   */
                                /* one-launch GroupNorm; 0 = never; the     */
                                /* default is 32768                         */
-#define SOAR_TUNE_PW_SMALL 10 /* pointwise convs with <= this many output  */
-                              /* elements (weight gradient: <= 64x this   */
-                              /* many multiply-adds) run the SIMT kernels; */
-                              /* 0 = never; the default is 262144          */
+#define SOAR_TUNE_PW_SMALL 10 /* pointwise convs of <= this many multiply- */
+                              /* adds (weight gradient: half as many) run */
+                              /* the SIMT kernels; 0 = never; the default */
+                              /* is 2^25                                  */
 SOAR_API int soar_gn_tune(int key, int64_t value);
 SOAR_API int64_t soar_gn_tune_get(int key);
 

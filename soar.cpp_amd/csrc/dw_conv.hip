@@ -158,23 +158,20 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_conv(
     }
 }
 
-// Weight and bias gradient partials: a block walks wg_tiles<K>() tiles down
-// one plane (tile rows ty = tyg*wg_tiles + i), accumulating in registers, then
+// Weight and bias gradient partials: a block walks `per` tiles down one
+// plane (tile rows ty = tyg*per + i), accumulating in registers, then
 // reduces once: part[g][c*(K*K+1) + k] with g = n*tpp + tyg*tiles_x + tx
 // (tpp counting tile groups), k < K*K the tap sums sum dy*x, k = K*K the
 // dy sum.  (The (K*K+1)-value block reduction costs about as much as a
 // tile's FMAs for k7, so it is amortized over several tiles: 8 for K >= 7,
-// 4 below, where more blocks per plane measured faster.)
-template <int K>
-constexpr int wg_tiles() {
-    return K >= 7 ? 8 : 4;
-}
+// 4 below, where more blocks per plane measured faster; fewer when that
+// leaves the grid short of blocks, see wgrad_per.)
 
 template <int K, int S, int D>
 __global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
     const float* __restrict__ dy, const float* __restrict__ x, float* __restrict__ part,
     int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x,
-    int64_t tiles_y, int64_t tpp) {
+    int64_t tiles_y, int64_t tpp, int per) {
     using T = Tile<K, S, D>;
     constexpr int KK1 = K * K + 1;
     __shared__ __attribute__((aligned(16))) float tile[T::floats];
@@ -189,8 +186,8 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
     float sw[KK1];
 #pragma unroll
     for (int k = 0; k < KK1; ++k) sw[k] = 0.0f;
-    for (int i = 0; i < wg_tiles<K>(); ++i) {
-        const int64_t ty = tyg * wg_tiles<K>() + i;
+    for (int i = 0; i < per; ++i) {
+        const int64_t ty = tyg * per + i;
         if (ty * kTH >= Ho) break;  // uniform across the block
         const int64_t oy0 = ty * kTH, ox0 = tx * kTW;
         if (i > 0) __syncthreads();  // the previous tile's LDS reads are done
@@ -474,18 +471,28 @@ bool dw_has_fast(int64_t K, int64_t S, int64_t D) {
     return fast_cfg(K, S, D, [](auto) {});
 }
 
+// Tiles per weight-gradient block: 8 for K >= 7, 4 below, halved while
+// the grid would hold fewer than 2048 blocks (a block walks its tiles one
+// after another: few large planes, e.g. 16 channels at 256 x 256 with k3
+// s2, ran 64 blocks of 4 tiles in 55 us).
+int64_t wgrad_per(const DwShape& sh) {
+    int64_t per = sh.K >= 7 ? 8 : 4;
+    const int64_t tx = (sh.Wo + kTW - 1) / kTW, ty = (sh.Ho + kTH - 1) / kTH;
+    while (per > 1 && sh.N * sh.C * ((ty + per - 1) / per) * tx < 2048) per /= 2;
+    return per;
+}
+
 // Tile groups of the weight-gradient kernel over an Ho x Wo plane.
-int64_t wgrad_groups(int64_t Ho, int64_t Wo, int64_t K, int64_t* tiles_x, int64_t* tiles_y) {
-    const int64_t per = K >= 7 ? wg_tiles<7>() : wg_tiles<3>();
-    *tiles_x = (Wo + kTW - 1) / kTW;
-    *tiles_y = (Ho + kTH - 1) / kTH;
+int64_t wgrad_groups(const DwShape& sh, int64_t per, int64_t* tiles_x, int64_t* tiles_y) {
+    *tiles_x = (sh.Wo + kTW - 1) / kTW;
+    *tiles_y = (sh.Ho + kTH - 1) / kTH;
     return ((*tiles_y + per - 1) / per) * *tiles_x;
 }
 
 size_t dw_bwd_workspace_bytes(const DwShape& sh) {
     if (!dw_has_fast(sh.K, sh.S, sh.D)) return 0;
     int64_t tx = 0, ty = 0;
-    const int64_t tpp = wgrad_groups(sh.Ho, sh.Wo, sh.K, &tx, &ty);
+    const int64_t tpp = wgrad_groups(sh, wgrad_per(sh), &tx, &ty);
     const size_t b = sizeof(float) * (size_t)(sh.N * tpp) * (size_t)(sh.C * (sh.K * sh.K + 1));
     return (b + 255) & ~(size_t)255;
 }
@@ -569,14 +576,16 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
     if ((dw || db) && sh.Ho * sh.Wo > 0) {
         const int64_t KK1 = sh.K * sh.K + 1;
         int64_t tiles_x = 0, tiles_y = 0;
-        const int64_t tpp = wgrad_groups(sh.Ho, sh.Wo, sh.K, &tiles_x, &tiles_y);
+        const int64_t per = wgrad_per(sh);
+        const int64_t tpp = wgrad_groups(sh, per, &tiles_x, &tiles_y);
         float* part = static_cast<float*>(ws);
         int tok = prof_begin(s, "dw_conv_wgrad");
         const bool fast = fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
             using CF = decltype(cf);
             k_dw_wgrad<CF::k, CF::s, CF::d>
                 <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
-                    dy, x, part, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tiles_y, tpp);
+                    dy, x, part, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tiles_y, tpp,
+                    (int)per);
         });
         prof_end(s, tok);
         tok = prof_begin(s, "dw_conv_wgrad_finish");

@@ -60,10 +60,9 @@ struct Tuning {
                               // partials' chunk
     int64_t small_unit = 32768;  // units of at most this many elements run
                                  // the one-launch GroupNorm (0: never)
-    int64_t pw_small = 262144;   // pointwise convolutions with at most this
-                                 // many output elements (weight gradient:
-                                 // 64x this many multiply-adds) run the SIMT
-                                 // kernels (0: never)
+    int64_t pw_small = 1 << 25;  // pointwise convolutions of at most this
+                                 // many multiply-adds (weight gradient: half
+                                 // as many) run the SIMT kernels (0: never)
 };
 
 constexpr int kThreads = 256;   // first passes (stats, reduction)
@@ -143,7 +142,7 @@ hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_ou
                           int64_t HW, int64_t chunk, double2* part, bool accumulate,
                           int64_t small, hipStream_t s, const char* name = nullptr);
 // True when the SIMT kernel computes the M x HW outputs of N samples (K
-// terms each): at most `small` output elements, and offsets inside a sample
+// terms each): at most `small` multiply-adds, and offsets inside a sample
 // fit in 32 bits.
 bool pw_use_small(int64_t N, int64_t M, int64_t K, int64_t HW, int64_t small);
 
@@ -168,8 +167,8 @@ struct PwBwdPlan {
 PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW);
 size_t pw_bwd_workspace_bytes(const PwBwdPlan& p);
 // dx runs the SIMT kernel when pw_use_small(N, C_in, C_out, HW, small),
-// dW/db when the weight gradient has at most 64*small multiply-adds (then
-// the workspace is not touched).
+// dW/db when the weight gradient has at most small/2 multiply-adds and
+// N*HW <= 16384 (then the workspace is not touched).
 hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N, int64_t C_in,
                               int64_t C_out, int64_t HW, int64_t chunk_dx, bool accumulate_dx,
                               int64_t small, hipStream_t s);

@@ -424,31 +424,71 @@ __global__ __launch_bounds__(kThreads2) void k_apply(
 // A finish block sums each plane of its unit over the plane's chunks
 // (plane_sums, float64, fixed order) and forms
 //   S1 = sum_c gamma_c * sum dz,   S2 = sum_c gamma_c * sum dz*xhat.
+// The block's lanes form groups of gs = min(64, cpp rounded up to a power
+// of two) lanes, one plane per group at a time (group g takes planes
+// g, g + ngroups, ...), so the planes' loads are in flight together
+// instead of one plane after another; each group adds its planes'
+// weighted sums in plane order and thread 0 adds the groups in order.
 // ======================================================================
 __device__ void finish_bwd_unit(int64_t u, const double2* __restrict__ part,
                                 const float* __restrict__ gamma,
                                 double2* __restrict__ plane_sums,
                                 double2* __restrict__ unit_sums, int64_t C, int64_t cpp,
-                                int64_t cpg, double* lds) {
-    double S1 = 0.0, S2 = 0.0;  // meaningful in thread 0
-    for (int64_t j = 0; j < cpg; ++j) {
-        const int64_t plane = u * cpg + j;
+                                int64_t cpg, double* lds /*[2 * kThreads]*/) {
+    int gs = 1;
+    while (gs < 64 && gs < cpp) gs <<= 1;
+    const int ngroups = kThreads / gs;
+    const int grp = (int)threadIdx.x / gs, r = (int)threadIdx.x & (gs - 1);
+    double S1 = 0.0, S2 = 0.0;  // meaningful in each group's lane r == 0
+    for (int64_t j = grp; j - grp < cpg; j += ngroups) {
+        const bool live = j < cpg;
+        const int64_t plane = u * cpg + (live ? j : 0);
         const double2* pp = part + plane * cpp;
         double A = 0.0, B = 0.0;
-        for (int64_t q = threadIdx.x; q < cpp; q += kThreads) {
-            const double2 v = pp[q];
-            A += v.x;
-            B += v.y;
+        if (live) {
+            int64_t q = r;
+            for (; q + 3 * gs < cpp; q += 4 * gs) {
+                const double2 v0 = pp[q], v1 = pp[q + gs], v2 = pp[q + 2 * gs],
+                              v3 = pp[q + 3 * gs];
+                A += v0.x;
+                B += v0.y;
+                A += v1.x;
+                B += v1.y;
+                A += v2.x;
+                B += v2.y;
+                A += v3.x;
+                B += v3.y;
+            }
+            for (; q < cpp; q += gs) {
+                const double2 v = pp[q];
+                A += v.x;
+                B += v.y;
+            }
         }
-        block_sum2(A, B, lds);
-        if (threadIdx.x == 0) {
+        for (int off = gs >> 1; off > 0; off >>= 1) {
+            A += __shfl_xor(A, off);
+            B += __shfl_xor(B, off);
+        }
+        if (live && r == 0) {
             plane_sums[plane] = make_double2(A, B);
             const double gj = gamma ? (double)gamma[plane % C] : 1.0;
             S1 += gj * A;
             S2 += gj * B;
         }
     }
-    if (threadIdx.x == 0) unit_sums[u] = make_double2(S1, S2);
+    if (r == 0) {
+        lds[grp] = S1;
+        lds[kThreads + grp] = S2;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double s1 = 0.0, s2 = 0.0;
+        for (int g = 0; g < ngroups; ++g) {
+            s1 += lds[g];
+            s2 += lds[kThreads + g];
+        }
+        unit_sums[u] = make_double2(s1, s2);
+    }
 }
 
 template <bool VEC, bool SILU>
@@ -461,7 +501,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
     int64_t cpg, int64_t HW, int64_t chunk, int64_t cpp, int64_t fin_u0, int64_t fin_nu,
     int64_t block0) {
     __shared__ float lds[2 * kWaves];
-    __shared__ double ldsd[2 * kWaves];
+    __shared__ double ldsd[2 * kThreads];
     if ((int64_t)blockIdx.x < fin_nu) {
         finish_bwd_unit(fin_u0 + blockIdx.x, part, gamma, plane_sums, unit_sums, C, cpp, cpg,
                         ldsd);

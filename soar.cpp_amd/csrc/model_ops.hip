@@ -172,6 +172,67 @@ __global__ __launch_bounds__(kThreads) void k_conv_dw(const float* __restrict__ 
     if (threadIdx.x == 0) part[(wq * (KK + 1) + tap) * chunks + chunk] = s;
 }
 
+// The same partials for K in {1, 3, 5, 7}: one block computes all K*K tap
+// sums and the bias sum of one (co, q) over one chunk, so the position
+// arithmetic (32-bit: N*Ho*Wo < 2^31, checked by the host) and the dy load
+// are shared by the taps.  Thread t walks positions t, t + 256, ... as
+// above; the block adds its waves' trees in order.
+template <int K>
+__global__ __launch_bounds__(kThreads) void k_conv_dw_taps(const float* __restrict__ go,
+                                                           const float* __restrict__ in,
+                                                           double* __restrict__ part,
+                                                           ConvShape c, int64_t chunks) {
+    constexpr int KK = K * K, KK1 = KK + 1;
+    __shared__ double red[kThreads / 64][KK1];
+    const int64_t chunk = blockIdx.y;
+    const int64_t wq = blockIdx.x;  // co*cig + q
+    const int64_t cig = c.C_in / c.groups, cog = c.C_out / c.groups;
+    const int64_t co = wq / cig, q = wq - co * cig;
+    const int64_t ci = (co / cog) * cig + q;
+    const uint32_t HWo = (uint32_t)(c.Ho * c.Wo), Wo = (uint32_t)c.Wo;
+    const int H = (int)c.H, W = (int)c.W;
+    const int S = (int)c.S, D = (int)c.D, pad = (int)c.pad;
+    double sw[KK1];
+#pragma unroll
+    for (int k = 0; k < KK1; ++k) sw[k] = 0.0;
+    const uint32_t p0 = (uint32_t)(chunk * kConvChunk);
+    const uint32_t end = (uint32_t)std::min<int64_t>((chunk + 1) * kConvChunk, c.N * c.Ho * c.Wo);
+    for (uint32_t p = p0 + threadIdx.x; p < end; p += kThreads) {
+        const uint32_t n = p / HWo, r = p - n * HWo;
+        const uint32_t oy = r / Wo, ox = r - oy * Wo;
+        const float g = go[((int64_t)n * c.C_out + co) * HWo + r];
+        sw[KK] += (double)g;
+        const float* ip = in + ((int64_t)n * c.C_in + ci) * c.H * c.W;
+        const int iy0 = (int)oy * S - pad, ix0 = (int)ox * S - pad;
+#pragma unroll
+        for (int ky = 0; ky < K; ++ky) {
+            const int iy = iy0 + ky * D;
+            if (iy < 0 || iy >= H) continue;
+#pragma unroll
+            for (int kx = 0; kx < K; ++kx) {
+                const int ix = ix0 + kx * D;
+                if (ix < 0 || ix >= W) continue;
+                sw[ky * K + kx] += (double)g * ip[(int64_t)iy * W + ix];
+            }
+        }
+    }
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int k = 0; k < KK1; ++k) {
+        double v = sw[k];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off);
+        if (lane == 0) red[wv][k] = v;
+    }
+    __syncthreads();
+    for (int k = threadIdx.x; k < KK1; k += kThreads) {
+        double v = red[0][k];
+#pragma unroll
+        for (int i = 1; i < kThreads / 64; ++i) v += red[i][k];
+        part[(wq * KK1 + k) * chunks + chunk] = (k < KK || q == 0) ? v : 0.0;
+    }
+}
+
 // Adds the chunk sums in order: gw[co][q][tap] += ..., gb[co] += ...
 __global__ __launch_bounds__(kThreads) void k_conv_dw_finish(const double* __restrict__ part,
                                                              float* __restrict__ gw,
@@ -767,8 +828,21 @@ hipError_t launch_conv_backward(const float* go, const float* in, const float* w
         const int64_t chunks = conv_chunks(c);
         const int64_t cig = c.C_in / c.groups;
         double* part = static_cast<double*>(ws);
-        dim3 grid((unsigned)(c.C_out * cig * (c.K * c.K + 1)), (unsigned)chunks);
-        k_conv_dw<<<grid, kThreads, 0, s>>>(go, in, part, c, chunks);
+        const bool taps = (c.K == 1 || c.K == 3 || c.K == 5 || c.K == 7) &&
+                          c.N * c.Ho * c.Wo < ((int64_t)1 << 31) && c.H < ((int64_t)1 << 30) &&
+                          c.W < ((int64_t)1 << 30);
+        if (taps) {
+            const dim3 grid((unsigned)(c.C_out * cig), (unsigned)chunks);
+            switch (c.K) {
+                case 1: k_conv_dw_taps<1><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks); break;
+                case 3: k_conv_dw_taps<3><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks); break;
+                case 5: k_conv_dw_taps<5><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks); break;
+                default: k_conv_dw_taps<7><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks); break;
+            }
+        } else {
+            dim3 grid((unsigned)(c.C_out * cig * (c.K * c.K + 1)), (unsigned)chunks);
+            k_conv_dw<<<grid, kThreads, 0, s>>>(go, in, part, c, chunks);
+        }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const int64_t rows = c.C_out * cig * (c.K * c.K + 1);

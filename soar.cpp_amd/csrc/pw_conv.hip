@@ -91,12 +91,12 @@ __device__ __forceinline__ int tile_row(int mt, int r, int h) {
 // path guards every scalar access and loads zeros instead.
 enum PwMode { kPlain = 0, kStats = 1, kAccum = 2 };
 
-template <bool FAST, int MODE, bool BIAS>
+template <bool FAST, int MODE, bool BIAS, int KS>
 __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const float* __restrict__ ws,
                                         const float* __restrict__ bias, float* __restrict__ zs,
                                         int64_t row0, int64_t p0, int h, int j, int64_t C_in,
-                                        int64_t C_out, int64_t HW, int Kpad, float2* lds,
-                                        float* ldsK) {
+                                        int64_t C_out, int64_t HW, int Kpad, int kb, int ke,
+                                        int v, float2* lds, float* ldsK, float* red) {
     // xs = x + n*C_in*HW + p0, ws = w + row0*C_in, zs = z + (n*C_out + row0)*HW + p0
     constexpr bool STATS = MODE == kStats, ACC = MODE == kAccum;
     const bool lane_px = p0 + 4 * j < HW;
@@ -124,7 +124,7 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
             for (int r = 0; r < 16; ++r) {
                 const int c = tile_row(mt, r, 0);
                 float bv = 0.0f;
-                if (BIAS) bv = (full || c + 4 * h <= rlim) ? bb[c] : 0.0f;
+                if (BIAS && v == 0) bv = (full || c + 4 * h <= rlim) ? bb[c] : 0.0f;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) acc[mt][t][r] = bv;
             }
@@ -187,7 +187,8 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
     // copied, so the wait before each MFMA group covers only the older
     // buffer.  sched_group_barrier keeps the order (the scheduler would
     // otherwise sink each load next to its use).
-    const int klast = FAST ? Kpad : Kpad - 8;
+    // This wave's K steps are [kb, ke) (split-K: KS waves share the item).
+    const int klast = FAST ? ke : ke - 8;
     auto sched = [] {
         if (FAST) {
             __builtin_amdgcn_sched_group_barrier(0x020, 6, 0);  // 6 vector loads
@@ -195,9 +196,9 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
         }
     };
     f4 a0[2], b0[4], a1[2], b1[4];
-    load_step(0, a0, b0);
-    int kk = 0;
-    for (; kk + 8 < Kpad; kk += 16) {
+    load_step(kb, a0, b0);
+    int kk = kb;
+    for (; kk + 8 < ke; kk += 16) {
         load_step(kk + 8, a1, b1);
         mfma_step(a0, b0);
         sched();
@@ -205,7 +206,35 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
         mfma_step(a1, b1);
         sched();
     }
-    if (kk < Kpad) mfma_step(a0, b0);  // odd number of steps
+    if (kk < ke) mfma_step(a0, b0);  // odd number of steps
+
+    if (KS > 1) {
+        // Wave 0 adds the other waves' accumulators in wave order, one
+        // m-tile at a time through LDS ([wave - 1][register][lane]:
+        // consecutive lanes, consecutive words).
+        const int lane = 32 * h + j;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            __syncthreads();
+            if (v > 0) {
+                float* dst = red + (v - 1) * 4096 + lane;
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) dst[(t * 16 + r) * 64] = acc[mt][t][r];
+            }
+            __syncthreads();
+            if (v == 0) {
+                for (int w = 1; w < KS; ++w) {
+                    const float* src = red + (w - 1) * 4096 + lane;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[mt][t][r] += src[(t * 16 + r) * 64];
+                }
+            }
+        }
+    }
 
     // ---- epilogue.  The row offsets below are computed here, not hoisted
     // out of the item loop where 32 of them would stay live in registers.
@@ -218,7 +247,7 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
             const int tr0 = tile_row(mt, r, 0);  // half 1 holds row tr0 + 4
             float* zr = reinterpret_cast<float*>(
                 reinterpret_cast<char*>(zs + (int64_t)tr0 * hw_e) + zo);
-            if (tr0 + 4 * h <= rlim) {
+            if (v == 0 && tr0 + 4 * h <= rlim) {
                 if (FAST) {
                     if (lane_px) {
                         f4 v = {acc[mt][0][r], acc[mt][1][r], acc[mt][2][r], acc[mt][3][r]};
@@ -236,7 +265,7 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
     if (STATS) {
         // shift of each row: its value at the item's first pixel, which
         // lane j = 0 of each half-wave holds; passed on through LDS
-        if (j == 0) {
+        if (j == 0 && v == 0) {
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
@@ -244,6 +273,7 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
             }
         }
         __syncthreads();
+        if (v != 0) return;
         // LDS addresses: one lane base plus constants, formed here so they
         // are not hoisted out of the item loop
         int lb = 4 * h;
@@ -271,21 +301,27 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
 }
 
 // MODE kPlain: z = w x + b;  kStats: also the GroupNorm chunk partials;
-// kAccum: z += w x.  BIAS: bias is non-null.  Byte offsets inside one
-// sample's planes must fit in 32 bits (checked by the host with
-// pw_offsets_fit).
-template <bool FAST, int MODE, bool BIAS>
-__global__ __launch_bounds__(64, 2) void k_pw_conv(
+// kAccum: z += w x.  BIAS: bias is non-null.  KS waves per block split the
+// K steps of every item (kseg channels each, wave 0 adds the others'
+// accumulators in order and runs the epilogue): used when the output has
+// too few tiles to occupy the chip.  Byte offsets inside one sample's
+// planes must fit in 32 bits (checked by the host with pw_offsets_fit).
+template <bool FAST, int MODE, bool BIAS, int KS>
+__global__ __launch_bounds__(64 * KS, 2) void k_pw_conv(
     const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ bias, float* __restrict__ z, double2* __restrict__ part,
-    int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk, int64_t cpp, int Kpad, int rpw) {
+    int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk, int64_t cpp, int Kpad, int rpw,
+    int kseg) {
     __shared__ __attribute__((aligned(16))) float2 lds[kRowTile * kLdsStride];
     __shared__ float ldsK[kRowTile];            // per-row shifts of the item
     __shared__ Mom ldsM[kRowGroup * kRowTile];  // row-owner running moments
+    __shared__ float red[KS > 1 ? (KS - 1) * 4096 : 1];  // split-K accumulators
 
     constexpr bool STATS = MODE == kStats;
-    const int lane = threadIdx.x;
+    // (KS == 1: compile-time wave 0 and the whole K range)
+    const int lane = threadIdx.x & 63, v = KS > 1 ? (int)threadIdx.x >> 6 : 0;
     const int h = lane >> 5, j = lane & 31;
+    const int kb = KS > 1 ? v * kseg : 0, ke = KS > 1 ? min(Kpad, kb + kseg) : Kpad;
     const int64_t n = (int64_t)blockIdx.x / cpp;
     const int64_t kc = (int64_t)blockIdx.x - n * cpp;
     const int64_t px0 = kc * chunk;
@@ -297,7 +333,7 @@ __global__ __launch_bounds__(64, 2) void k_pw_conv(
 
     for (int64_t rg = (int64_t)blockIdx.y * rpw; rg < R; rg += kRowGroup) {
         const int nrt = (int)min<int64_t>(kRowGroup, R - rg);
-        if (STATS) {
+        if (STATS && v == 0) {
 #pragma unroll
             for (int g = 0; g < kRowGroup; ++g) ldsM[g * kRowTile + lane] = Mom{0.0, 0.0, 0.0};
         }
@@ -305,10 +341,13 @@ __global__ __launch_bounds__(64, 2) void k_pw_conv(
             const int nvalid = (int)min<int64_t>(kItem, HW - p0);
             for (int g = 0; g < nrt; ++g) {
                 const int64_t row0 = (rg + g) * kRowTile;
-                pw_item<FAST, MODE, BIAS>(xn + p0, w + row0 * C_in, bias, zn + row0 * HW + p0,
-                                           row0, p0, h, j, C_in, C_out, HW, Kpad, lds, ldsK);
+                pw_item<FAST, MODE, BIAS, KS>(xn + p0, w + row0 * C_in, bias,
+                                               zn + row0 * HW + p0, row0, p0, h, j, C_in, C_out,
+                                               HW, Kpad, kb, ke, v, lds, ldsK, red);
                 if (STATS) {
                     __syncthreads();
+                }
+                if (STATS && v == 0) {
                     // lane owns row `lane` of the tile
                     float S = 0.f, Q = 0.f;
                     const float4* src = reinterpret_cast<const float4*>(lds + lane * kLdsStride);
@@ -325,11 +364,11 @@ __global__ __launch_bounds__(64, 2) void k_pw_conv(
                     m.m2 = fmax((double)Q - (double)S * (double)S / cnt, 0.0);
                     Mom& acc = ldsM[g * kRowTile + lane];
                     acc = chan_merge(acc, m);
-                    __syncthreads();
                 }
+                if (STATS) __syncthreads();
             }
         }
-        if (STATS) {
+        if (STATS && v == 0) {
             for (int g = 0; g < nrt; ++g) {
                 const int64_t row = (rg + g) * kRowTile + lane;
                 const Mom m = ldsM[g * kRowTile + lane];
@@ -731,23 +770,28 @@ bool pw_small_fits(int64_t N, int64_t M, int64_t K, int64_t HW) {
     return N <= 65535 && M * HW < lim && K * HW < lim && M < lim && K < lim;
 }
 
-// Weight gradient on the SIMT kernel: at most 64*small multiply-adds.
-// Measured on MI355X (one sample, single launches): the SIMT kernel wins up
-// to about 2^24 multiply-adds (e.g. 64x128 channels at 2048 pixels: 24 vs
-// 30 us), the MFMA tiles from about 2^25 on.
+// Weight gradient on the SIMT kernel: at most small/2 multiply-adds, and
+// at most 16384 (n, p) terms per entry (at most 256 per lane with 64 lanes
+// per entry: a lane's sum is a chain of dependent loads).  Measured on
+// MI355X (one sample, single launches): the SIMT kernel wins up to about
+// 2^24 multiply-adds (e.g. 64x128 channels at 2048 pixels: 24 vs 30 us),
+// the MFMA tiles from about 2^25 on; 16x4 channels at 262144 pixels (2^24
+// multiply-adds, 4096 terms per lane) took 238 us against 25.
 bool pw_use_small_wgrad(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t small) {
-    return small > 0 &&
-           (double)N * (double)HW * (double)C_in * (double)C_out <= 64.0 * (double)small &&
+    return small > 0 && N * HW <= 16384 &&
+           (double)N * (double)HW * (double)C_in * (double)C_out <= 0.25 * (double)small &&
            pw_small_fits(N, C_out, C_in, HW);
 }
 }  // namespace
 
-// Measured on MI355X (one sample, single launches): the SIMT kernel wins up
-// to about 2^18 output elements whatever K is (e.g. 512 -> 256 channels at
-// 1024 pixels: 35 vs 60 us; 64 -> 128 at 4096: 11 vs 12 us), ties at 2^19
-// and loses above (128 -> 256 at 4096: 35 vs 19 us).
+// Measured on MI355X against the split-K MFMA kernel (one sample, single
+// launches): the SIMT kernel wins up to about 2^25 multiply-adds (256 ->
+// 128 channels at 1024 pixels: 11 vs 19 us; 64 -> 128 at 4096: 10 vs 13
+// us), ties at 2^26 and loses above (512 -> 256 at 1024: 34 vs 28 us; 128
+// -> 256 at 4096: 35 vs 16 us).
 bool pw_use_small(int64_t N, int64_t M, int64_t K, int64_t HW, int64_t small) {
-    return small > 0 && pw_small_fits(N, M, K, HW) && N * M * HW <= small;
+    return small > 0 && pw_small_fits(N, M, K, HW) &&
+           (double)N * (double)M * (double)K * (double)HW <= (double)small;
 }
 
 namespace {
@@ -806,10 +850,25 @@ hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_ou
     const int Kpad = pw_kpad(C_in);
     const int mode = part ? kStats : (accumulate ? kAccum : kPlain);
     if (!name) name = part ? "pw_conv_gn_stats" : "pw_conv";
+    // Split K over 2 or 4 waves of a block while the grid stays within
+    // 2048 waves and each wave keeps at least 4 K steps: a wave's time is
+    // its K/8 dependent MFMA steps, so a small grid finishes sooner.
+    const int64_t waves = (int64_t)grid.x * grid.y, ksteps = Kpad / 8;
+    int ks = 1;
+    while (ks < 4 && waves * ks * 2 <= 2048 && ksteps >= 8 * ks) ks *= 2;
+    const int kseg = (int)((ksteps + ks - 1) / ks) * 8;
     const int tok = prof_begin(s, name);
     auto go = [&](auto F, auto M, auto B) {
-        k_pw_conv<F(), M(), B()><<<grid, 64, 0, s>>>(a.x, a.w, a.bias, a.z, part, C_in, C_out,
-                                                    HW, chunk, cpp, Kpad, rpw);
+        auto run = [&](auto K) {
+            k_pw_conv<F(), M(), B(), K()><<<grid, 64 * K(), 0, s>>>(
+                a.x, a.w, a.bias, a.z, part, C_in, C_out, HW, chunk, cpp, Kpad, rpw, kseg);
+        };
+        if (ks == 4)
+            run(std::integral_constant<int, 4>{});
+        else if (ks == 2)
+            run(std::integral_constant<int, 2>{});
+        else
+            run(std::integral_constant<int, 1>{});
     };
     using P = std::integral_constant<int, kPlain>;
     using S = std::integral_constant<int, kStats>;
@@ -834,10 +893,12 @@ PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW) {
     PwBwdPlan p;
     p.tiles_co = (C_out + kRowTile - 1) / kRowTile;
     p.tiles_ci = (C_in + kRowTile - 1) / kRowTile;
-    // about 2048 waves (two per SIMD), chunks of at least 256 pixels
+    // about 2048 waves (two per SIMD), chunks of at least 64 pixels (a wave
+    // spends about 1.7 us per 32-pixel step on its 64x64 tile, so small
+    // grids get short chunks; each chunk adds a partial tile to the finish)
     const int64_t total = N * HW * p.tiles_co * p.tiles_ci;
     int64_t chunk = (total / 2048 + 31) / 32 * 32;
-    chunk = std::max<int64_t>(chunk, 256);
+    chunk = std::max<int64_t>(chunk, 64);
     const int64_t hw32 = (HW + 31) / 32 * 32;
     p.chunk = std::min(chunk, std::max<int64_t>(hw32, 32));
     p.cpp = (HW + p.chunk - 1) / p.chunk;

@@ -189,7 +189,7 @@ def test_pw_chunk_tuning(L):
 
 def test_pw_small_tuning(L):
     old = soar_gn.tune_get(soar_gn.TUNE_PW_SMALL)
-    assert old == 262144
+    assert old == 1 << 25
     assert L.soar_gn_tune(soar_gn.TUNE_PW_SMALL, -1) == soar_gn.SOAR_EINVAL
     assert L.soar_gn_tune(soar_gn.TUNE_PW_SMALL, (1 << 40) + 1) == soar_gn.SOAR_EINVAL
     # small planes: the workspace also covers the GroupNorm's own plan

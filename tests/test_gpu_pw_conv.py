@@ -20,6 +20,18 @@ pytestmark = pytest.mark.gpu
 U32 = 2.0 ** -24
 
 
+@pytest.fixture(params=["default", "mfma"])
+def pw_path(request, gpu):
+    """Runs a test with the default choice between the SIMT and the MFMA
+    kernels, and with the MFMA kernels forced (SOAR_TUNE_PW_SMALL = 0; small
+    grids then split K over the waves of a block)."""
+    old = gpu.tune_get(gpu.TUNE_PW_SMALL)
+    if request.param == "mfma":
+        gpu.tune(gpu.TUNE_PW_SMALL, 0)
+    yield request.param
+    gpu.tune(gpu.TUNE_PW_SMALL, old)
+
+
 def rng_inputs(seed, N, C_in, C_out, HW, bias=True, kind="normal"):
     r = np.random.default_rng(seed)
     if kind == "offset":
@@ -65,7 +77,7 @@ CONV_SHAPES = [
 
 
 @pytest.mark.parametrize("C_in,C_out,HW,bias", CONV_SHAPES)
-def test_conv1x1_matches_oracle(gpu, oracle, C_in, C_out, HW, bias):
+def test_conv1x1_matches_oracle(gpu, oracle, pw_path, C_in, C_out, HW, bias):
     print(f"conv1x1 C_in={C_in} C_out={C_out} HW={HW} bias={bias}", flush=True)
     x, w, b = rng_inputs(C_in * 7 + HW, 1, C_in, C_out, HW, bias)
     out = gpu.conv1x1_forward(dev(x[0]), dev(w), dev(b) if bias else None)
@@ -103,7 +115,8 @@ def fused_case(gpu, oracle, N, C_in, C_out, HW, G, kind, silu, seed=3):
 
 
 @pytest.mark.parametrize("N,C_in,C_out,HW,G,kind,silu", FUSED_SHAPES)
-def test_pw_conv_gn_silu_matches_oracle(gpu, oracle, N, C_in, C_out, HW, G, kind, silu):
+def test_pw_conv_gn_silu_matches_oracle(gpu, oracle, pw_path, N, C_in, C_out, HW, G, kind,
+                                        silu):
     print(f"pw_conv_gn N={N} C_in={C_in} C_out={C_out} HW={HW} G={G} {kind}", flush=True)
     x, w, b, gamma, beta, z, y, st = fused_case(gpu, oracle, N, C_in, C_out, HW, G, kind,
                                                 silu)
@@ -121,8 +134,8 @@ def test_pw_conv_gn_silu_matches_oracle(gpu, oracle, N, C_in, C_out, HW, G, kind
 
 
 @pytest.mark.parametrize("N,C_in,C_out,HW,G,kind,silu", FUSED_SHAPES[:3])
-def test_pw_conv_gn_matches_unfused_device_path(gpu, oracle, N, C_in, C_out, HW, G, kind,
-                                                silu):
+def test_pw_conv_gn_matches_unfused_device_path(gpu, oracle, pw_path, N, C_in, C_out, HW, G,
+                                                kind, silu):
     """conv (reference signature) then soar_gn_silu_forward on the same z."""
     x, w, b, gamma, beta, z, y, st = fused_case(gpu, oracle, N, C_in, C_out, HW, G, kind,
                                                 silu)
@@ -243,7 +256,7 @@ BWD_SHAPES = [
 
 
 @pytest.mark.parametrize("N,C_in,C_out,HW", BWD_SHAPES)
-def test_pw_conv_backward_matches_oracle(gpu, oracle, N, C_in, C_out, HW):
+def test_pw_conv_backward_matches_oracle(gpu, oracle, pw_path, N, C_in, C_out, HW):
     print(f"pw_conv_backward N={N} C_in={C_in} C_out={C_out} HW={HW}", flush=True)
     r = np.random.default_rng(N * 1000 + C_in + HW)
     dz = r.standard_normal((N, C_out, HW)).astype(np.float32)
@@ -259,7 +272,7 @@ def test_pw_conv_backward_matches_oracle(gpu, oracle, N, C_in, C_out, HW):
         assert ratio[i] <= 1.0, f"{name} err {err[i]:.3e} > bound {b.reshape(-1)[i]:.3e} at {i}"
 
 
-def test_pw_conv_backward_accumulates(gpu, oracle):
+def test_pw_conv_backward_accumulates(gpu, oracle, pw_path):
     N, C_in, C_out, HW = 1, 32, 32, 1000
     r = np.random.default_rng(4)
     dz = r.standard_normal((N, C_out, HW)).astype(np.float32)
@@ -357,7 +370,7 @@ SMALL_PW_SHAPES = [
     (1, 128, 256, 16, False),  # stride 16
     (2, 64, 128, 64, True),
     (1, 32, 64, 256, True),
-    (1, 64, 128, 2048, True),  # 2^18 outputs: the default limit
+    (1, 64, 128, 2048, True),  # 2^24 multiply-adds: SIMT by default
     (3, 5, 7, 9, True),        # C_in % 4 != 0: scalar weight loads; rows straddle waves
     (1, 600, 40, 3, True),     # K split over 15 waves of 40 channels
     (4, 24, 8, 1, False),      # one pixel
