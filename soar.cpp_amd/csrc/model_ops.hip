@@ -127,10 +127,25 @@ __global__ __launch_bounds__(kThreads) void k_conv_dx(const float* __restrict__ 
     }
 }
 
-constexpr int64_t kConvChunk = 16384;  // output positions per dW block
+constexpr int64_t kConvChunk = 16384;  // largest output-position chunk of a dW block
+
+// Output positions per dW block: about 2048 blocks over the (co, q) rows
+// and chunks, chunks of 1024..16384 positions (a thread walks its chunk's
+// positions one after another, each a round of dependent loads), and at
+// most 65535 chunks.
+int64_t conv_chunk(const ConvShape& c) {
+    const int64_t pos = c.N * c.Ho * c.Wo;
+    const int64_t rows = std::max<int64_t>(1, c.C_out * (c.C_in / c.groups));
+    const int64_t want = std::max<int64_t>(1, 2048 / rows);
+    int64_t ch = (pos + want - 1) / want;
+    ch = (ch + 1023) / 1024 * 1024;
+    ch = std::max<int64_t>(1024, std::min<int64_t>(ch, kConvChunk));
+    return std::max<int64_t>(ch, (pos + 65534) / 65535);
+}
 
 int64_t conv_chunks(const ConvShape& c) {
-    return (c.N * c.Ho * c.Wo + kConvChunk - 1) / kConvChunk;
+    const int64_t ch = conv_chunk(c);
+    return (c.N * c.Ho * c.Wo + ch - 1) / ch;
 }
 
 // dW / db partials: block x = (co*cig+q)*(K*K+1) + tap, block y = chunk;
@@ -139,7 +154,7 @@ int64_t conv_chunks(const ConvShape& c) {
 __global__ __launch_bounds__(kThreads) void k_conv_dw(const float* __restrict__ go,
                                                       const float* __restrict__ in,
                                                       double* __restrict__ part, ConvShape c,
-                                                      int64_t chunks) {
+                                                      int64_t chunks, int64_t csize) {
     __shared__ double sh[kThreads];
     const int64_t chunk = blockIdx.y;
     const int64_t KK = c.K * c.K;
@@ -153,8 +168,8 @@ __global__ __launch_bounds__(kThreads) void k_conv_dw(const float* __restrict__ 
         const int64_t ci = (co / cog) * cig + q;
         const int64_t ky = is_bias ? 0 : tap / c.K, kx = is_bias ? 0 : tap % c.K;
         const int64_t HWo = c.Ho * c.Wo;
-        const int64_t end = std::min((chunk + 1) * kConvChunk, c.N * HWo);
-        for (int64_t p = chunk * kConvChunk + threadIdx.x; p < end; p += kThreads) {
+        const int64_t end = std::min((chunk + 1) * csize, c.N * HWo);
+        for (int64_t p = chunk * csize + threadIdx.x; p < end; p += kThreads) {
             const int64_t n = p / HWo, r = p - n * HWo;
             const int64_t oy = r / c.Wo, ox = r - oy * c.Wo;
             const float g = go[(n * c.C_out + co) * HWo + r];
@@ -181,7 +196,8 @@ template <int K>
 __global__ __launch_bounds__(kThreads) void k_conv_dw_taps(const float* __restrict__ go,
                                                            const float* __restrict__ in,
                                                            double* __restrict__ part,
-                                                           ConvShape c, int64_t chunks) {
+                                                           ConvShape c, int64_t chunks,
+                                                           int64_t csize) {
     constexpr int KK = K * K, KK1 = KK + 1;
     __shared__ double red[kThreads / 64][KK1];
     const int64_t chunk = blockIdx.y;
@@ -195,8 +211,8 @@ __global__ __launch_bounds__(kThreads) void k_conv_dw_taps(const float* __restri
     double sw[KK1];
 #pragma unroll
     for (int k = 0; k < KK1; ++k) sw[k] = 0.0;
-    const uint32_t p0 = (uint32_t)(chunk * kConvChunk);
-    const uint32_t end = (uint32_t)std::min<int64_t>((chunk + 1) * kConvChunk, c.N * c.Ho * c.Wo);
+    const uint32_t p0 = (uint32_t)(chunk * csize);
+    const uint32_t end = (uint32_t)std::min<int64_t>((chunk + 1) * csize, c.N * c.Ho * c.Wo);
     for (uint32_t p = p0 + threadIdx.x; p < end; p += kThreads) {
         const uint32_t n = p / HWo, r = p - n * HWo;
         const uint32_t oy = r / Wo, ox = r - oy * Wo;
@@ -825,7 +841,7 @@ hipError_t launch_conv_backward(const float* go, const float* in, const float* w
         if (e != hipSuccess) return e;
     }
     if (gw || gb) {
-        const int64_t chunks = conv_chunks(c);
+        const int64_t chunks = conv_chunks(c), csize = conv_chunk(c);
         const int64_t cig = c.C_in / c.groups;
         double* part = static_cast<double*>(ws);
         const bool taps = (c.K == 1 || c.K == 3 || c.K == 5 || c.K == 7) &&
@@ -834,14 +850,14 @@ hipError_t launch_conv_backward(const float* go, const float* in, const float* w
         if (taps) {
             const dim3 grid((unsigned)(c.C_out * cig), (unsigned)chunks);
             switch (c.K) {
-                case 1: k_conv_dw_taps<1><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks); break;
-                case 3: k_conv_dw_taps<3><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks); break;
-                case 5: k_conv_dw_taps<5><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks); break;
-                default: k_conv_dw_taps<7><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks); break;
+                case 1: k_conv_dw_taps<1><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks, csize); break;
+                case 3: k_conv_dw_taps<3><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks, csize); break;
+                case 5: k_conv_dw_taps<5><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks, csize); break;
+                default: k_conv_dw_taps<7><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks, csize); break;
             }
         } else {
             dim3 grid((unsigned)(c.C_out * cig * (c.K * c.K + 1)), (unsigned)chunks);
-            k_conv_dw<<<grid, kThreads, 0, s>>>(go, in, part, c, chunks);
+            k_conv_dw<<<grid, kThreads, 0, s>>>(go, in, part, c, chunks, csize);
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
