@@ -1010,6 +1010,10 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
                 return fail(SOAR_EINVAL, "small_unit must be in [0, 2^20]");
             g_tune.small_unit = value;
             return ok();
+        case SOAR_TUNE_FOLD_MAX:
+            if (value < 0 || value > 128) return fail(SOAR_EINVAL, "fold_max must be in [0, 128]");
+            g_tune.fold_max = value;
+            return ok();
         case SOAR_TUNE_PW_SMALL:
             if (value < 0 || value > ((int64_t)1 << 40))
                 return fail(SOAR_EINVAL, "pw_small must be in [0, 2^40]");
@@ -1033,6 +1037,7 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
         case SOAR_TUNE_PW_CHUNK: return g_tune.pw_chunk;
         case SOAR_TUNE_SMALL_UNIT: return g_tune.small_unit;
         case SOAR_TUNE_PW_SMALL: return g_tune.pw_small;
+        case SOAR_TUNE_FOLD_MAX: return g_tune.fold_max;
         default: return -1;
     }
 }

@@ -60,6 +60,9 @@ struct Tuning {
                               // partials' chunk
     int64_t small_unit = 32768;  // units of at most this many elements run
                                  // the one-launch GroupNorm (0: never)
+    int64_t fold_max = 128;      // units of at most this many chunk partials
+                                 // (one batch) fold the finish into the
+                                 // second pass (0: never; at most 128)
     int64_t pw_small = 1 << 25;  // pointwise convolutions of at most this
                                  // many multiply-adds (weight gradient: half
                                  // as many) run the SIMT kernels (0: never)

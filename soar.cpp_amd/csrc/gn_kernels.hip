@@ -367,18 +367,147 @@ __device__ __forceinline__ PlaneCoef plane_coef(
 }
 
 // ======================================================================
-// Forward pass 2: y = f((x - mean) * (gamma*rstd) + beta) [+ x].
+// Folded finish for mid-size units (at most kFoldMax chunk partials per
+// unit, one batch): instead of a finish launch between the passes, every
+// second-pass block combines its own unit's partials before its work.
+// All blocks of a unit run the same combine in the same order, so they
+// agree bit for bit.  The statistics also equal finish_stats_unit's: there
+// thread q < P holds partial q alone and the other threads hold empty
+// moments, which chan() passes through, and the waves meet in order.
 // ======================================================================
-template <bool VEC, bool SILU, bool RES, bool NT, bool NTL>
+constexpr int64_t kFoldMax = kThreads2;  // partials per unit (one per thread)
+
+struct UnitStats {
+    float hi, r, lo;
+};
+
+__device__ UnitStats fold_unit_stats(int64_t u, const double2* __restrict__ part, int64_t HW,
+                                     int64_t chunk, int64_t cpp, int64_t cpg, float eps) {
+    __shared__ Moments lds[kThreads2 / 64];
+    __shared__ float bc[3];
+    const int64_t P = cpg * cpp;
+    const int q = threadIdx.x;
+    Moments m{0.0, 0.0, 0.0};
+    if (q < P) {
+        const double2 v = part[u * P + q];
+        const int64_t k = q % cpp;
+        m = Moments{(double)min(chunk, HW - k * chunk), v.x, v.y};
+    }
+    m = wave_reduce(m);
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Moments r = lds[0];
+#pragma unroll
+        for (int i = 1; i < kThreads2 / 64; ++i) r = chan(r, lds[i]);
+        const double var = r.n > 0.0 ? fmax(r.m2 / r.n, 0.0) : 0.0;
+        const float hi = (float)r.mean;
+        bc[0] = hi;
+        bc[1] = (float)(1.0 / sqrt(var + (double)eps));
+        bc[2] = (float)(r.mean - (double)hi);
+    }
+    __syncthreads();
+    return UnitStats{bc[0], bc[1], bc[2]};
+}
+
+// Sum of (a, b) over a kThreads2 block in a fixed order (wave trees, then
+// the waves in order), returned to every thread.
+__device__ __forceinline__ double2 fold_block_sum2(double a, double b) {
+    __shared__ double2 lds[kThreads2 / 64];
+    a = wave_sum(a);
+    b = wave_sum(b);
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = make_double2(a, b);
+    __syncthreads();
+    double2 r = lds[0];
+#pragma unroll
+    for (int i = 1; i < kThreads2 / 64; ++i) {
+        r.x += lds[i].x;
+        r.y += lds[i].y;
+    }
+    __syncthreads();
+    return r;
+}
+
+// (S1, S2) of unit u from its backward partials: thread q < P adds
+// gamma_j * partial q, j = q / cpp the partial's channel.
+__device__ double2 fold_unit_sums(int64_t u, const double2* __restrict__ part,
+                                  const float* __restrict__ gamma, int64_t C, int64_t cpg,
+                                  int64_t cpp) {
+    const int64_t P = cpg * cpp;
+    const int q = threadIdx.x;
+    double a = 0.0, b = 0.0;
+    if (q < P) {
+        const double2 v = part[u * P + q];
+        const int64_t plane = u * cpg + q / cpp;
+        const double g = gamma ? (double)gamma[plane % C] : 1.0;
+        a = g * v.x;
+        b = g * v.y;
+    }
+    return fold_block_sum2(a, b);
+}
+
+// dbeta[c] += sum over samples and chunks of channel c's sum(dz), dgamma[c]
+// += the same of sum(dz * xhat) (the k_param_finish step, for one channel).
+__device__ void fold_param(int64_t c, const double2* __restrict__ part, int64_t N, int64_t C,
+                           int64_t cpp, float* __restrict__ dgamma, float* __restrict__ dbeta) {
+    double a = 0.0, b = 0.0;
+    for (int64_t i = threadIdx.x; i < N * cpp; i += kThreads2) {
+        const int64_t n = i / cpp, q = i - n * cpp;
+        const double2 v = part[(n * C + c) * cpp + q];
+        a += v.x;
+        b += v.y;
+    }
+    const double2 r = fold_block_sum2(a, b);
+    if (threadIdx.x == 0) {
+        dbeta[c] = (float)((double)dbeta[c] + r.x);
+        dgamma[c] = (float)((double)dgamma[c] + r.y);
+    }
+}
+
+// ======================================================================
+// Forward pass 2: y = f((x - mean) * (gamma*rstd) + beta) [+ x].
+// FOLD: the unit's statistics come from its chunk partials (see above);
+// the unit's first block also writes them out.
+// ======================================================================
+struct FoldArgs {
+    const double2* part;  // chunk partials of the first pass
+    float* mean;          // statistics out (forward)
+    float* rstd;
+    float* mean_lo;       // nullable
+    float* dgamma;        // parameter gradients (backward), nullable
+    float* dbeta;
+    int64_t N, chunk, cpp;
+    float eps;
+};
+
+template <bool VEC, bool SILU, bool RES, bool NT, bool NTL, bool FOLD>
 __global__ __launch_bounds__(kThreads2) void k_apply(
     const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ mean_lo,
     float* __restrict__ y, int64_t C, int64_t G, int64_t cpg, int64_t HW,
-    int64_t chunk2, int64_t cpp2, int64_t block0, int64_t nb, int reverse) {
+    int64_t chunk2, int64_t cpp2, int64_t block0, int64_t nb, int reverse, FoldArgs fa) {
     const int64_t b = batch_block(block0, nb, reverse);
     const Chunk ck = chunk_of(b, HW, chunk2, cpp2);
-    const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
+    PlaneCoef k;
+    if (FOLD) {
+        k.n = ck.plane / C;
+        k.c = ck.plane - k.n * C;
+        k.u = k.n * G + k.c / cpg;
+        const UnitStats st = fold_unit_stats(k.u, fa.part, HW, fa.chunk, fa.cpp, cpg, fa.eps);
+        k.mu = st.hi;
+        k.r = st.r;
+        k.e = -st.lo * st.r;
+        k.gm = gamma ? gamma[k.c] : 1.0f;
+        k.bt = beta ? beta[k.c] : 0.0f;
+        if (threadIdx.x == 0 && ck.plane % cpg == 0 && ck.off == 0) {
+            fa.mean[k.u] = st.hi;
+            fa.rstd[k.u] = st.r;
+            if (fa.mean_lo) fa.mean_lo[k.u] = st.lo;
+        }
+    } else {
+        k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
+    }
     // z = gamma*xhat + beta = (x - mu)*(gamma*r) + (beta + gamma*e)
     const float a = k.gm * k.r, mu = k.mu, bt = fmaf(k.gm, k.e, k.bt);
     const int64_t base = ck.plane * HW + ck.off;
@@ -570,18 +699,28 @@ __global__ void k_param_finish(const double2* __restrict__ plane_sums,
 // Backward pass 2: dx = A*dz + D*xhat + B [+ dy] [+ dx_old] with
 // A = gamma_c*rstd, B = -rstd*S1/M, D = -rstd*S2/M.
 // ======================================================================
-template <bool VEC, bool SILU, bool RES, bool ACC, bool NT, bool NTL>
+// FOLD: S1 / S2 come from the unit's chunk partials, and the block of
+// channel c's first chunk in sample 0 also adds channel c's dgamma / dbeta
+// (the folded k_param_finish).
+template <bool VEC, bool SILU, bool RES, bool ACC, bool NT, bool NTL, bool FOLD>
 __global__ __launch_bounds__(kThreads2) void k_bwd_dx(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ gamma, const float* __restrict__ beta,
     const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ mean_lo, const double2* __restrict__ unit_sums,
     float* __restrict__ dx, int64_t C, int64_t G, int64_t cpg, int64_t HW,
-    int64_t chunk2, int64_t cpp2, int64_t block0, int64_t nb, int reverse) {
+    int64_t chunk2, int64_t cpp2, int64_t block0, int64_t nb, int reverse, FoldArgs fa) {
     const int64_t b = batch_block(block0, nb, reverse);
     const Chunk ck = chunk_of(b, HW, chunk2, cpp2);
     const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
-    const double2 S = unit_sums[k.u];
+    double2 S;
+    if (FOLD) {
+        S = fold_unit_sums(k.u, fa.part, gamma, C, cpg, fa.cpp);
+        if (fa.dgamma && k.n == 0 && ck.off == 0)
+            fold_param(k.c, fa.part, fa.N, C, fa.cpp, fa.dgamma, fa.dbeta);
+    } else {
+        S = unit_sums[k.u];
+    }
     const double Md = (double)(cpg * HW);
     const float mu = k.mu, r = k.r, e = k.e, gm = k.gm, bt = k.bt;
     const float A = gm * r;
@@ -1007,19 +1146,25 @@ void bsel(bool b, F&& f) {
         f(std::false_type{});
 }
 
+// fold: the statistics come from the partials in the workspace (see
+// fold_unit_stats) and are written out by the kernel.
 void launch_apply(const Plan& p, const Tuning& t, const FwdArgs& a, const float* lo,
-                  int64_t block0, int64_t nb, hipStream_t s) {
+                  int64_t block0, int64_t nb, hipStream_t s, bool fold = false) {
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
     const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
     const dim3 grid((unsigned)nb);
+    const FoldArgs fa{ws_view(p, a.ws).part, a.mean, a.rstd, a.mean_lo, nullptr, nullptr,
+                      p.N, p.chunk, p.cpp, a.eps};
     bsel(p.vec4, [&](auto V) {
         bsel(silu, [&](auto S) {
             bsel(res, [&](auto R) {
                 bsel(t.nt_store != 0, [&](auto N) {
                     bsel(V() && t.nt_load != 0, [&](auto L) {
-                        k_apply<V(), S(), R(), N(), L()><<<grid, kThreads2, 0, s>>>(
-                            a.x, a.gamma, a.beta, a.mean, a.rstd, lo, a.y, p.C, p.G, p.cpg,
-                            p.HW, p.chunk2, p.cpp2, block0, nb, t.reverse);
+                        bsel(fold, [&](auto F) {
+                            k_apply<V(), S(), R(), N(), L(), F()><<<grid, kThreads2, 0, s>>>(
+                                a.x, a.gamma, a.beta, a.mean, a.rstd, lo, a.y, p.C, p.G, p.cpg,
+                                p.HW, p.chunk2, p.cpp2, block0, nb, t.reverse, fa);
+                        });
                     });
                 });
             });
@@ -1027,28 +1172,41 @@ void launch_apply(const Plan& p, const Tuning& t, const FwdArgs& a, const float*
     });
 }
 
+// fold: S1 / S2 and dgamma / dbeta come from the partials in the workspace.
 void launch_dx(const Plan& p, const Tuning& t, const BwdArgs& a, const double2* unit_sums,
-               int64_t block0, int64_t nb, hipStream_t s) {
+               int64_t block0, int64_t nb, hipStream_t s, bool fold = false) {
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
     const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
     const bool accum = (a.flags & SOAR_GN_ACCUMULATE_DX) != 0;
     const dim3 grid((unsigned)nb);
+    const FoldArgs fa{ws_view(p, a.ws).part, nullptr, nullptr, nullptr, a.dgamma, a.dbeta,
+                      p.N, p.chunk, p.cpp, 0.0f};
     bsel(p.vec4, [&](auto V) {
         bsel(silu, [&](auto S) {
             bsel(res, [&](auto R) {
                 bsel(accum, [&](auto A) {
                     bsel(t.nt_store != 0 && !accum, [&](auto N) {
                         bsel(V() && t.nt_load != 0, [&](auto L) {
-                            k_bwd_dx<V(), S(), R(), A(), N(), L()><<<grid, kThreads2, 0, s>>>(
-                                a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo,
-                                unit_sums, a.dx, p.C, p.G, p.cpg, p.HW, p.chunk2, p.cpp2,
-                                block0, nb, t.reverse);
+                            bsel(fold, [&](auto F) {
+                                k_bwd_dx<V(), S(), R(), A(), N(), L(), F()>
+                                    <<<grid, kThreads2, 0, s>>>(
+                                        a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo,
+                                        unit_sums, a.dx, p.C, p.G, p.cpg, p.HW, p.chunk2,
+                                        p.cpp2, block0, nb, t.reverse, fa);
+                            });
                         });
                     });
                 });
             });
         });
     });
+}
+
+// Mid-size units fold the finish into the second pass: one batch, at most
+// t.fold_max (<= kFoldMax) partials per unit.
+bool fold_ok(const Plan& p, const Tuning& t, int64_t upb) {
+    return t.fold_max > 0 && p.cpg * p.cpp <= std::min<int64_t>(t.fold_max, kFoldMax) &&
+           upb >= p.units;
 }
 
 // First-pass kernels: `fin_nu` finish blocks for units [fin_u0, fin_u0 +
@@ -1242,6 +1400,13 @@ hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a, hipS
     }
     const int64_t bpu2 = p.cpg * p.cpp2;  // second-pass blocks per unit
     const char* apply_name = silu ? "gn_silu_apply" : "gn_apply";
+    if (fold_ok(p, t, p.upb_fwd)) {
+        launch_stats(p, a, w, 0, 0, 0, p.units, s);
+        const int tok = prof_begin(s, apply_name);
+        launch_apply(p, t, a, w.lo, 0, p.blocks2, s, true);
+        prof_end(s, tok);
+        return hipGetLastError();
+    }
     if (t.streams >= 2 && p.units > p.upb_fwd) {
         Pipe* pp = nullptr;
         SOAR_TRY(pipe_for_device(&pp));
@@ -1342,6 +1507,13 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hip
     }
     const int64_t bpu2 = p.cpg * p.cpp2;  // second-pass blocks per unit
     const char* dx_name = silu ? "gn_silu_bwd_dx" : "gn_bwd_dx";
+    if (a.dx && fold_ok(p, t, p.upb_bwd)) {
+        launch_reduce(p, a, w, 0, 0, 0, p.units, s);
+        const int tok = prof_begin(s, dx_name);
+        launch_dx(p, t, a, w.unit_sums, 0, p.blocks2, s, true);
+        prof_end(s, tok);
+        return hipGetLastError();
+    }
     if (t.streams >= 2 && p.units > p.upb_bwd) {
         Pipe* pp = nullptr;
         SOAR_TRY(pipe_for_device(&pp));

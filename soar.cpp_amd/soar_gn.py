@@ -42,6 +42,7 @@ TUNE_CHUNK2 = 7
 TUNE_PW_CHUNK = 8
 TUNE_SMALL_UNIT = 9
 TUNE_PW_SMALL = 10
+TUNE_FOLD_MAX = 11
 
 
 class SoarUnavailable(RuntimeError):

@@ -35,12 +35,16 @@ def test_ops_validate_on_the_host(L):
     assert L.soar_pixel_shuffle_forward(None, None, 6, 4, 4, 2, None) == soar_gn.SOAR_EINVAL
     # crop larger than the padded plane
     assert L.soar_unpad_spatial_forward(None, None, 1, 4, 4, 5, 4, None) == soar_gn.SOAR_EINVAL
-    # conv workspace is pure host arithmetic: one fp64 partial per
-    # (weight tap or bias, 16384-position chunk)
+    # conv workspace is pure host arithmetic: one fp64 partial per (weight
+    # tap or bias, position chunk); chunks of 1024..16384 positions, sized
+    # for about 2048 blocks over the 16 (co, q) rows: 1024 here
     assert L.soar_conv_backward_workspace_bytes(1, 1, 16, 64, 64, 32, 32, 3, 1, 2, 1, 1) == \
         16 * 10 * 1 * 8
     assert L.soar_conv_backward_workspace_bytes(2, 1, 16, 256, 256, 128, 128, 3, 1, 2, 1, 1) == \
-        16 * 10 * 2 * 8
+        16 * 10 * 32 * 8
+    # one row (co, q) wants 2048 chunks, capped below by 1024 positions
+    assert L.soar_conv_backward_workspace_bytes(1, 1, 1, 1024, 1024, 512, 512, 3, 1, 2, 1, 1) == \
+        1 * 10 * 256 * 8
     assert L.soar_multi_tensor_norm_workspace_bytes() == (512 + 1) * 8
 
 
@@ -198,3 +202,13 @@ def test_pw_small_tuning(L):
     assert soar_gn.pw_conv_gn_workspace_bytes(1, 512, 4, 8) <= big
     soar_gn.tune(soar_gn.TUNE_PW_SMALL, old)
     assert soar_gn.tune_get(soar_gn.TUNE_PW_SMALL) == old
+
+
+def test_fold_max_tuning(L):
+    old = soar_gn.tune_get(soar_gn.TUNE_FOLD_MAX)
+    assert old == 128
+    assert L.soar_gn_tune(soar_gn.TUNE_FOLD_MAX, 129) == soar_gn.SOAR_EINVAL
+    assert L.soar_gn_tune(soar_gn.TUNE_FOLD_MAX, -1) == soar_gn.SOAR_EINVAL
+    soar_gn.tune(soar_gn.TUNE_FOLD_MAX, 0)
+    assert soar_gn.tune_get(soar_gn.TUNE_FOLD_MAX) == 0
+    soar_gn.tune(soar_gn.TUNE_FOLD_MAX, old)

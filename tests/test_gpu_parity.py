@@ -471,9 +471,11 @@ def test_reference_signature_elementwise(gpu, oracle, n, offset):
     assert not host(y).any()
 
 
-def test_kernel_timing_records(gpu):
+@pytest.mark.parametrize("fold", [0, 128])
+def test_kernel_timing_records(gpu, restore_tuning, fold):
     import torch
     x = torch.randn(1, 8, 65536, device="cuda")
+    gpu.tune(gpu.TUNE_FOLD_MAX, fold)  # the units hold 32 chunk partials
     gpu.prof_enable(True)
     try:
         y, st = gpu.gn_silu_forward(x, None, None, 2)
@@ -482,10 +484,14 @@ def test_kernel_timing_records(gpu):
     finally:
         gpu.prof_enable(False)
     # one unit batch covers this small tensor: one launch of each pass, plus
-    # the finish-only launch of the last (here: only) batch
-    for k in ("gn_stats_partial", "gn_stats_finish", "gn_silu_apply", "gn_silu_bwd_reduce",
-              "gn_bwd_finish", "gn_silu_bwd_dx", "gn_param_finish"):
+    # (without the fold) the finish-only launch of the last (here: only) batch
+    # and the parameter finish
+    passes = ["gn_stats_partial", "gn_silu_apply", "gn_silu_bwd_reduce", "gn_silu_bwd_dx"]
+    finishes = ["gn_stats_finish", "gn_bwd_finish", "gn_param_finish"]
+    for k in passes + ([] if fold else finishes):
         assert recs[k]["launches"] == 1 and recs[k]["total_ms"] > 0
+    if fold:
+        assert not set(finishes) & set(recs)
 
 
 # ------------------------------------------------------------ tuning knobs
@@ -493,7 +499,8 @@ def test_kernel_timing_records(gpu):
 @pytest.fixture
 def restore_tuning(gpu):
     keys = (gpu.TUNE_CHUNK, gpu.TUNE_REVERSE, gpu.TUNE_NT_STORE, gpu.TUNE_BATCH_MB,
-            gpu.TUNE_STREAMS, gpu.TUNE_NT_LOAD, gpu.TUNE_CHUNK2, gpu.TUNE_SMALL_UNIT)
+            gpu.TUNE_STREAMS, gpu.TUNE_NT_LOAD, gpu.TUNE_CHUNK2, gpu.TUNE_SMALL_UNIT,
+            gpu.TUNE_FOLD_MAX)
     old = {k: gpu.tune_get(k) for k in keys}
     yield
     for k, v in old.items():
@@ -581,6 +588,65 @@ def test_small_unit_path(gpu, oracle, restore_tuning, shape, residual):
         assert np.abs(a - b).max() <= 2e-6 * (1 + np.abs(b).max())
     # accumulation: dx += and dgamma / dbeta += (the backward's contract)
     gpu.tune(gpu.TUNE_SMALL_UNIT, 32768)
+    ws = gpu.workspace(N, C, HW, G)
+    y, st = gpu.gn_silu_forward(xd, gd, bd, G, eps=EPS, residual=residual, ws=ws)
+    dx0 = torch.full_like(xd, 0.5)
+    dg0, db0 = torch.full_like(gd, -1.0), torch.full_like(bd, 2.0)
+    gpu.check(gpu.lib().soar_gn_silu_backward(
+        gpu._ptr(dyd), gpu._ptr(xd), gpu._ptr(gd), gpu._ptr(bd), gpu._ptr(st.mean),
+        gpu._ptr(st.rstd), gpu._ptr(st.mean_lo), gpu._ptr(dx0), gpu._ptr(dg0), gpu._ptr(db0),
+        N, C, HW, G, gpu.GN_SILU | gpu.GN_ACCUMULATE_DX | (gpu.GN_RESIDUAL if residual else 0),
+        gpu._ptr(ws), ws.numel(), gpu._stream()))
+    assert_vals(host(dx0) - 0.5, dxt, "accumulated dx")
+    assert_vals(host(dg0) + 1.0, dgt, "accumulated dgamma")
+    assert_vals(host(db0) - 2.0, dbt, "accumulated dbeta")
+
+
+FOLD_SHAPES = [
+    # (N, C, HW, G, kind): units above 32768 elements with at most 128
+    # chunk partials, so the finish folds into the second pass
+    (1, 16, 512 * 512, 8, "normal"),   # SOAR Nano stride 2 at 1024x1024: 64 partials
+    (2, 32, 256 * 256, 8, "normal"),   # 32 partials per unit, two samples
+    (1, 128, 64 * 64, 8, "normal"),    # 16 channels per group, one chunk each
+    (3, 24, 10000, 6, "offset"),       # ragged chunks, large mean, three samples
+]
+
+
+@pytest.mark.parametrize("shape", FOLD_SHAPES, ids=lambda s: "x".join(map(str, s[:4])) + s[4])
+@pytest.mark.parametrize("residual", [False, True])
+def test_folded_finish(gpu, oracle, restore_tuning, shape, residual):
+    """Mid-size units with the finish folded into the apply / dx pass
+    (SOAR_TUNE_FOLD_MAX = 128, the default) against the oracle, and against
+    the separate finish launches (0): the statistics and y are bitwise
+    identical (the same combine in the same order); dx, dgamma and dbeta
+    agree far inside the bar (S1 / S2 are summed in another order); the
+    parameter gradients accumulate."""
+    import torch
+    N, C, HW, G, kind = shape
+    print(f"folded finish N={N} C={C} HW={HW} G={G} {kind} residual={residual}", flush=True)
+    x, gamma, beta, dy = make_inputs(oracle, N, C, HW, G, kind, 5 + C)
+    yt, mt, rt = oracle.gn_silu_fwd_f64(x, gamma, beta, N, C, HW, G, EPS, True, residual)
+    dxt, dgt, dbt = oracle.gn_silu_bwd_f64(dy, x, gamma, beta, mt, rt, N, C, HW, G, True,
+                                           residual)
+    xd, dyd = dev(x).view(N, C, HW), dev(dy).view(N, C, HW)
+    gd, bd = dev(gamma), dev(beta)
+    runs = []
+    for fold in (128, 0):
+        gpu.tune(gpu.TUNE_FOLD_MAX, fold)
+        y, mean, rstd, lo, dx, dg, db = _fwd_bwd(gpu, xd, gd, bd, dyd, G, residual)
+        assert_stats(host(mean), host(rstd), mt, rt, f"fold={fold}")
+        assert_vals(host(y), yt, f"y fold={fold}")
+        assert_vals(host(dx), dxt, f"dx fold={fold}")
+        assert_vals(host(dg), dgt, f"dgamma fold={fold}")
+        assert_vals(host(db), dbt, f"dbeta fold={fold}")
+        runs.append([host(t) for t in (mean, rstd, lo, y, dx, dg, db)])
+    for a, b in zip(runs[0][:4], runs[1][:4]):
+        assert np.array_equal(a, b)
+    for a, b in zip(runs[0][4:], runs[1][4:]):
+        a, b = a.astype(np.float64), b.astype(np.float64)
+        assert np.abs(a - b).max() <= 2e-6 * (1 + np.abs(b).max())
+    # accumulation into dx and into dgamma / dbeta on the folded path
+    gpu.tune(gpu.TUNE_FOLD_MAX, 128)
     ws = gpu.workspace(N, C, HW, G)
     y, st = gpu.gn_silu_forward(xd, gd, bd, G, eps=EPS, residual=residual, ws=ws)
     dx0 = torch.full_like(xd, 0.5)
