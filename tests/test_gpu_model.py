@@ -178,6 +178,34 @@ def test_gradients_other_shapes(sm, tmp_path, h, w, c):
         assert d <= 5e-5 * float(np.linalg.norm(grads[name])) + 1e-7 * gnorm, name
 
 
+@pytest.mark.parametrize("variant,idx", [("small", 1)])
+def test_other_variant_matches_oracle(sm, tmp_path, variant, idx):
+    """Another architecture (24..192 channels, so 3..24 channels per group,
+    and more LKR blocks): logits, losses and every gradient against the
+    oracle at 64 x 64, under the same bars as Nano."""
+    print(f"case: {variant} forward_backward 64x64", flush=True)
+    spec = smr.model_spec(1, 1, idx)
+    wts = smr.random_weights(spec, SEED + 17)
+    f = tmp_path / f"{variant}.soar"
+    smr.write_soar(f, [(n, wts[n]) for n, _, _ in spec], variant=idx)
+    m = sm.SOAR(1, 1, variant, seed=5)
+    m.load_weights(str(f))
+    img, mask = sample(21)
+    z = m.forward(img)
+    met = m.forward_backward(img, mask)
+    lo, zt, grads = smr.forward_backward(wts, img, mask, variant=idx)
+    assert np.abs(z - zt.reshape(z.shape)).max() <= 2e-5 * (1 + np.abs(zt).max())
+    for k, v in (("loss", lo.total), ("bce", lo.bce), ("dice_loss", lo.dice)):
+        assert abs(met[k] - v) <= 1e-5 * abs(v) + 1e-7, (k, met[k], v)
+    gnorm = np.sqrt(sum(float(np.sum(g.astype(np.float64) ** 2)) for g in grads.values()))
+    names = [n for n, _ in m.tensors()]
+    assert names == [n for n, _, _ in spec]
+    for i, (name, shape) in enumerate(m.tensors()):
+        d = float(np.linalg.norm(m.read(i, grad=True, shape=shape).astype(np.float64) - grads[name]))
+        assert d <= 5e-5 * float(np.linalg.norm(grads[name])) + 1e-7 * gnorm, name
+    m.close()
+
+
 def test_two_train_steps_match_adamw(sm, wfile):
     """train_step = clip(2.0) + AdamW + zero_grad on the step's gradients:
     bit-exact against the scalar fp32 update on the device's gradients,
