@@ -9,9 +9,13 @@
 // Conv2d (layers.cpp:326-332): taps outside the input are skipped.
 //
 // Fast kernels (template K, S, D for the configurations the model uses):
-// a 256-thread block owns a 32 x 64 output tile of one (n, c) plane.  The
-// input tile it needs, halo included, is staged once in LDS with coalesced
-// row loads (zeros outside the image); each thread then computes 8
+// a 256-thread block owns a column of up to four 32 x 64 output tiles of
+// one (n, c) plane.  The input tile each needs, halo included, is staged in
+// LDS from coalesced loads (zeros outside the image); the loads of the next
+// tile go out into registers before the current tile is computed, so they
+// are in flight during its FMAs (one tile per block waited on its loads
+// about 80% of the time: 0.62 vs 0.47 ms for k3 at 64 x 2048^2).  Each
+// thread then computes 8
 // consecutive outputs of one row, reading each of the K input row segments
 // it touches with 16-byte LDS loads into registers and applying all K
 // taps of that row from registers.  Per output that is about K*(8S+(K-1)D)/8
@@ -59,38 +63,6 @@ struct Tile {
     static constexpr int floats = IH * IWP;
 };
 
-struct TileIdx {
-    int64_t plane, n, c, tix, oy0, ox0;
-};
-
-__device__ __forceinline__ TileIdx tile_idx(int64_t C, int64_t tiles_x, int64_t tpp) {
-    TileIdx t;
-    const int64_t b = blockIdx.x;
-    t.plane = b / tpp;
-    t.tix = b - t.plane * tpp;
-    t.n = t.plane / C;
-    t.c = t.plane - t.n * C;
-    const int64_t ty = t.tix / tiles_x;
-    t.oy0 = ty * kTH;
-    t.ox0 = (t.tix - ty * tiles_x) * kTW;
-    return t;
-}
-
-// Stage input rows [iy0, iy0 + IH) x columns [ix0, ix0 + IWP) of plane `ip`
-// (zeros outside the image and past column IW).
-template <int K, int S, int D>
-__device__ __forceinline__ void fill_tile(float* tile, const float* __restrict__ ip, int64_t iy0,
-                                          int64_t ix0, int64_t Hi, int64_t Wi) {
-    using T = Tile<K, S, D>;
-    for (int i = threadIdx.x; i < T::floats; i += kDwThreads) {
-        const int r = i / T::IWP, col = i - r * T::IWP;
-        const int64_t yy = iy0 + r, xx = ix0 + col;
-        float v = 0.0f;
-        if (col < T::IW && yy >= 0 && yy < Hi && xx >= 0 && xx < Wi) v = ip[yy * Wi + xx];
-        tile[i] = v;
-    }
-}
-
 // Row segment of a thread: SL4 floats of LDS row `lrow` from column c0*S.
 template <int K, int S, int D>
 __device__ __forceinline__ void load_seg(const float* tile, int lrow, int c0,
@@ -107,54 +79,107 @@ __device__ __forceinline__ void load_seg(const float* tile, int lrow, int c0,
     }
 }
 
-// out (+)= bias + w (*) in over one 32 x 64 output tile per block.  FLIP
+// A thread's share of a tile's input (element i = threadIdx.x + k*256 of
+// the LDS tile), fetched into registers so the loads of the next tile are
+// in flight while the current one is computed.
+template <int K, int S, int D>
+struct TilePrefetch {
+    static constexpr int NR = (Tile<K, S, D>::floats + kDwThreads - 1) / kDwThreads;
+    float v[NR];
+
+    // input rows [iy0, iy0 + IH) x columns [ix0, ix0 + IWP) of plane `ip`
+    // (zeros outside the image and past column IW).  32-bit offsets: a
+    // plane holds fewer than 2^31 elements (checked by the host).  The
+    // element index is recomputed for every tile (not hoisted out of the
+    // tile loop, where NR offsets would stay live in registers).
+    __device__ __forceinline__ void fetch(const float* __restrict__ ip, int iy0, int ix0, int Hi,
+                                          int Wi) {
+        using T = Tile<K, S, D>;
+        int t = (int)threadIdx.x;
+        asm volatile("" : "+v"(t));
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+            const int i = t + k * kDwThreads;
+            const int r = i / T::IWP, col = i - r * T::IWP;
+            const int yy = iy0 + r, xx = ix0 + col;
+            float x = 0.0f;
+            if (i < T::floats && col < T::IW && (unsigned)yy < (unsigned)Hi &&
+                (unsigned)xx < (unsigned)Wi)
+                x = ip[yy * Wi + xx];
+            v[k] = x;
+        }
+    }
+    __device__ __forceinline__ void stash(float* tile) const {
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+            const int i = (int)threadIdx.x + k * kDwThreads;
+            if (i < Tile<K, S, D>::floats) tile[i] = v[k];
+        }
+    }
+};
+
+// out (+)= bias + w (*) in over `per` 32 x 64 output tiles down one plane
+// per block (tile rows tyg*per ..): the input of tile i + 1 is fetched into
+// registers while tile i is computed from LDS.  FLIP
 // applies the kernel rotated by 180 degrees (the stride-1 input gradient).
 template <int K, int S, int D, bool FLIP, bool ACC, bool BIAS>
 __global__ __launch_bounds__(kDwThreads) void k_dw_conv(
     const float* __restrict__ in, const float* __restrict__ w, const float* __restrict__ bias,
     float* __restrict__ out, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo,
-    int64_t pad, int64_t tiles_x, int64_t tpp) {
+    int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per) {
     using T = Tile<K, S, D>;
     __shared__ __attribute__((aligned(16))) float tile[T::floats];
-    const TileIdx ti = tile_idx(C, tiles_x, tpp);
-    fill_tile<K, S, D>(tile, in + ti.plane * Hi * Wi, ti.oy0 * S - pad, ti.ox0 * S - pad, Hi,
-                       Wi);
+    const int64_t b = blockIdx.x;
+    const int64_t plane = b / tpp, gix = b - plane * tpp;
+    const int64_t c = plane % C;
+    const int64_t tyg = gix / tiles_x, tx = gix - tyg * tiles_x;
+    const int64_t ty0 = tyg * per, ty1 = min(ty0 + per, tiles_y);
+    const int64_t ox0 = tx * kTW;
+    const float* ip = in + plane * Hi * Wi;
+    TilePrefetch<K, S, D> pre;
+    const int ix0 = (int)(ox0 * S - pad), hi = (int)Hi, wi = (int)Wi;
+    pre.fetch(ip, (int)(ty0 * kTH * S - pad), ix0, hi, wi);
     float wr[K * K];
 #pragma unroll
-    for (int k = 0; k < K * K; ++k) wr[k] = w[ti.c * K * K + (FLIP ? K * K - 1 - k : k)];
+    for (int k = 0; k < K * K; ++k) wr[k] = w[c * K * K + (FLIP ? K * K - 1 - k : k)];
+    const float b0 = BIAS ? bias[c] : 0.0f;
     const int t = threadIdx.x, r = t >> 3, c0 = (t & 7) * kPer;
-    float acc[kPer];
-    const float b0 = BIAS ? bias[ti.c] : 0.0f;
+    for (int64_t ty = ty0; ty < ty1; ++ty) {
+        if (ty > ty0) __syncthreads();  // the previous tile's LDS reads are done
+        pre.stash(tile);
+        __syncthreads();
+        if (ty + 1 < ty1) pre.fetch(ip, (int)((ty + 1) * kTH * S - pad), ix0, hi, wi);
+        float acc[kPer];
 #pragma unroll
-    for (int c = 0; c < kPer; ++c) acc[c] = b0;
-    __syncthreads();
+        for (int q = 0; q < kPer; ++q) acc[q] = b0;
 #pragma unroll
-    for (int ky = 0; ky < K; ++ky) {
-        float seg[T::SL4];
-        load_seg<K, S, D>(tile, r * S + ky * D, c0, seg);
+        for (int ky = 0; ky < K; ++ky) {
+            float seg[T::SL4];
+            load_seg<K, S, D>(tile, r * S + ky * D, c0, seg);
 #pragma unroll
-        for (int kx = 0; kx < K; ++kx)
+            for (int kx = 0; kx < K; ++kx)
 #pragma unroll
-            for (int c = 0; c < kPer; ++c)
-                acc[c] = fmaf(wr[ky * K + kx], seg[c * S + kx * D], acc[c]);
-    }
-    const int64_t oy = ti.oy0 + r;
-    if (oy >= Ho) return;
-    float* orow = out + ti.plane * Ho * Wo + oy * Wo;
-    const int64_t ox = ti.ox0 + c0;
-    if (ox + kPer <= Wo && ((reinterpret_cast<uintptr_t>(orow + ox) & 15) == 0)) {
-        f4* o4 = reinterpret_cast<f4*>(orow + ox);
-        f4 v0 = {acc[0], acc[1], acc[2], acc[3]}, v1 = {acc[4], acc[5], acc[6], acc[7]};
-        if (ACC) {
-            v0 += o4[0];
-            v1 += o4[1];
+                for (int q = 0; q < kPer; ++q)
+                    acc[q] = fmaf(wr[ky * K + kx], seg[q * S + kx * D], acc[q]);
         }
-        o4[0] = v0;
-        o4[1] = v1;
-    } else {
+        const int64_t oy = ty * kTH + r;
+        if (oy >= Ho) continue;
+        float* orow = out + plane * Ho * Wo + oy * Wo;
+        const int64_t ox = ox0 + c0;
+        if (ox + kPer <= Wo && ((reinterpret_cast<uintptr_t>(orow + ox) & 15) == 0)) {
+            f4* o4 = reinterpret_cast<f4*>(orow + ox);
+            f4 v0 = {acc[0], acc[1], acc[2], acc[3]}, v1 = {acc[4], acc[5], acc[6], acc[7]};
+            if (ACC) {
+                v0 += o4[0];
+                v1 += o4[1];
+            }
+            o4[0] = v0;
+            o4[1] = v1;
+        } else {
 #pragma unroll
-        for (int c = 0; c < kPer; ++c)
-            if (ox + c < Wo) orow[ox + c] = ACC ? orow[ox + c] + acc[c] : acc[c];
+            for (int q = 0; q < kPer; ++q)
+                if (ox + q < Wo) orow[ox + q] = ACC ? orow[ox + q] + acc[q] : acc[q];
+        }
     }
 }
 
@@ -186,20 +211,33 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
     float sw[KK1];
 #pragma unroll
     for (int k = 0; k < KK1; ++k) sw[k] = 0.0f;
-    for (int i = 0; i < per; ++i) {
-        const int64_t ty = tyg * per + i;
-        if (ty * kTH >= Ho) break;  // uniform across the block
-        const int64_t oy0 = ty * kTH, ox0 = tx * kTW;
-        if (i > 0) __syncthreads();  // the previous tile's LDS reads are done
-        fill_tile<K, S, D>(tile, xp, oy0 * S - pad, ox0 * S - pad, Hi, Wi);
-        const int64_t oy = oy0 + r, ox = ox0 + c0;
-        float g[kPer];
+    // the next tile's x tile and dy values load while this tile's FMAs run
+    const int64_t ty0 = tyg * per, ty1 = min(ty0 + per, tiles_y);
+    const int64_t ox0 = tx * kTW;
+    const int ix0 = (int)(ox0 * S - pad), hi = (int)Hi, wi = (int)Wi;
+    TilePrefetch<K, S, D> pre;
+    float gn[kPer];
+    auto fetch_dy = [&](int64_t ty) {
+        const int64_t oy = ty * kTH + r, ox = ox0 + c0;
 #pragma unroll
         for (int cc = 0; cc < kPer; ++cc)
-            g[cc] = (oy < Ho && ox + cc < Wo) ? gp[oy * Wo + ox + cc] : 0.0f;
+            gn[cc] = (oy < Ho && ox + cc < Wo) ? gp[oy * Wo + ox + cc] : 0.0f;
+    };
+    pre.fetch(xp, (int)(ty0 * kTH * S - pad), ix0, hi, wi);
+    fetch_dy(ty0);
+    for (int64_t ty = ty0; ty < ty1; ++ty) {
+        if (ty > ty0) __syncthreads();  // the previous tile's LDS reads are done
+        pre.stash(tile);
+        float g[kPer];
+#pragma unroll
+        for (int cc = 0; cc < kPer; ++cc) g[cc] = gn[cc];
+        __syncthreads();
+        if (ty + 1 < ty1) {
+            pre.fetch(xp, (int)((ty + 1) * kTH * S - pad), ix0, hi, wi);
+            fetch_dy(ty + 1);
+        }
 #pragma unroll
         for (int cc = 0; cc < kPer; ++cc) sw[K * K] += g[cc];
-        __syncthreads();
 #pragma unroll
         for (int ky = 0; ky < K; ++ky) {
             float seg[T::SL4];
@@ -252,50 +290,93 @@ template <int K, int S, int D, bool ACC>
 __global__ __launch_bounds__(kDwThreads) void k_dw_dgrad_strided(
     const float* __restrict__ dy, const float* __restrict__ w, float* __restrict__ dx,
     int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x,
-    int64_t tpp) {
+    int64_t tiles_y, int64_t tpp, int per) {
     using T = DTile<K, S, D>;
+    constexpr int NR = (T::R * T::W + kDwThreads - 1) / kDwThreads;
     __shared__ float tile[T::R * T::W];
-    const TileIdx ti = tile_idx(C, tiles_x, tpp);  // tiles over dx here
-    const int64_t ylo = floor_div(ti.oy0 + pad - (K - 1) * D, S);
-    const int64_t xlo = floor_div(ti.ox0 + pad - (K - 1) * D, S);
-    const float* gp = dy + ti.plane * Ho * Wo;
-    for (int i = threadIdx.x; i < T::R * T::W; i += kDwThreads) {
-        const int rr = i / T::W, cc = i - rr * T::W;
-        const int64_t yo = ylo + rr, xo = xlo + cc;
-        tile[i] = (yo >= 0 && yo < Ho && xo >= 0 && xo < Wo) ? gp[yo * Wo + xo] : 0.0f;
-    }
+    // `per` dx tiles down one plane per block (tiles over dx here); the dy
+    // region of the next tile loads into registers while this one is summed
+    const int64_t b = blockIdx.x;
+    const int64_t plane = b / tpp, gix = b - plane * tpp;
+    const int64_t c = plane % C;
+    const int64_t tyg = gix / tiles_x, tx = gix - tyg * tiles_x;
+    const int64_t ty0 = tyg * per, ty1 = min(ty0 + per, tiles_y);
+    const int64_t ox0 = tx * kTW;
+    const int xlo = (int)floor_div(ox0 + pad - (K - 1) * D, S);
+    const int ho = (int)Ho, wo = (int)Wo;
+    const float* gp = dy + plane * Ho * Wo;
+    float pv[NR];
+    auto fetch = [&](int64_t ty) {
+        const int ylo = (int)floor_div(ty * kTH + pad - (K - 1) * D, S);
+        int t = (int)threadIdx.x;
+        asm volatile("" : "+v"(t));  // recomputed per tile, not hoisted
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+            const int i = t + k * kDwThreads;
+            const int rr = i / T::W, cc = i - rr * T::W;
+            const int yo = ylo + rr, xo = xlo + cc;
+            float v = 0.0f;
+            if (i < T::R * T::W && (unsigned)yo < (unsigned)ho && (unsigned)xo < (unsigned)wo)
+                v = gp[yo * wo + xo];
+            pv[k] = v;
+        }
+    };
+    fetch(ty0);
     float wr[K * K];
 #pragma unroll
-    for (int k = 0; k < K * K; ++k) wr[k] = w[ti.c * K * K + k];
+    for (int k = 0; k < K * K; ++k) wr[k] = w[c * K * K + k];
     const int t = threadIdx.x, wv = t >> 6, l = t & 63;
     // rows 2*(l/8) + (wv & 1) + 16*(wv >> 1) give each wave one row parity
     const int r = S == 2 ? 2 * (l >> 3) + (wv & 1) + 16 * (wv >> 1) : t >> 3;
     const int c0 = (l & 7) * kPer;
-    const int64_t yi = ti.oy0 + r, xb = ti.ox0 + c0;
-    float acc[kPer];
+    const int64_t xb = ox0 + c0;
+    for (int64_t ty = ty0; ty < ty1; ++ty) {
+        if (ty > ty0) __syncthreads();  // the previous tile's LDS reads are done
 #pragma unroll
-    for (int c = 0; c < kPer; ++c) acc[c] = 0.0f;
-    __syncthreads();
+        for (int k = 0; k < NR; ++k) {
+            const int i = t + k * kDwThreads;
+            if (i < T::R * T::W) tile[i] = pv[k];
+        }
+        __syncthreads();
+        if (ty + 1 < ty1) fetch(ty + 1);
+        const int64_t oy0 = ty * kTH;
+        const int64_t ylo = floor_div(oy0 + pad - (K - 1) * D, S);
+        const int64_t yi = oy0 + r;
+        float acc[kPer];
 #pragma unroll
-    for (int ky = 0; ky < K; ++ky) {
-        const int64_t vy = yi + pad - ky * D;
-        if (vy % S != 0) continue;
-        const float* row = tile + (vy / S - ylo) * T::W;
+        for (int q = 0; q < kPer; ++q) acc[q] = 0.0f;
 #pragma unroll
-        for (int kx = 0; kx < K; ++kx) {
-            const float wk = wr[ky * K + kx];
+        for (int ky = 0; ky < K; ++ky) {
+            const int64_t vy = yi + pad - ky * D;
+            if (vy % S != 0) continue;
+            const float* row = tile + (vy / S - ylo) * T::W;
 #pragma unroll
-            for (int c = 0; c < kPer; ++c) {
-                const int64_t vx = xb + c + pad - kx * D;
-                if (vx % S == 0) acc[c] = fmaf(wk, row[vx / S - xlo], acc[c]);
+            for (int kx = 0; kx < K; ++kx) {
+                const float wk = wr[ky * K + kx];
+#pragma unroll
+                for (int q = 0; q < kPer; ++q) {
+                    const int64_t vx = xb + q + pad - kx * D;
+                    if (vx % S == 0) acc[q] = fmaf(wk, row[vx / S - xlo], acc[q]);
+                }
             }
         }
-    }
-    if (yi >= Hi) return;
-    float* orow = dx + ti.plane * Hi * Wi + yi * Wi;
+        if (yi >= Hi) continue;
+        float* orow = dx + plane * Hi * Wi + yi * Wi;
+        if (xb + kPer <= Wi && ((reinterpret_cast<uintptr_t>(orow + xb) & 15) == 0)) {
+            f4* o4 = reinterpret_cast<f4*>(orow + xb);
+            f4 v0 = {acc[0], acc[1], acc[2], acc[3]}, v1 = {acc[4], acc[5], acc[6], acc[7]};
+            if (ACC) {
+                v0 += o4[0];
+                v1 += o4[1];
+            }
+            o4[0] = v0;
+            o4[1] = v1;
+        } else {
 #pragma unroll
-    for (int c = 0; c < kPer; ++c)
-        if (xb + c < Wi) orow[xb + c] = ACC ? orow[xb + c] + acc[c] : acc[c];
+            for (int q = 0; q < kPer; ++q)
+                if (xb + q < Wi) orow[xb + q] = ACC ? orow[xb + q] + acc[q] : acc[q];
+        }
+    }
 }
 
 // ---- generic kernels (any K, S, D): one thread per output element --------
@@ -460,6 +541,26 @@ int64_t tiles_of(int64_t H, int64_t W, int64_t* tiles_x) {
     return ((H + kTH - 1) / kTH) * *tiles_x;
 }
 
+// k_dw_conv addresses a plane with 32-bit element offsets.
+bool planes_fit_32(const DwShape& sh) {
+    const int64_t lim = (int64_t)1 << 31;
+    return sh.Hi * sh.Wi < lim && sh.Ho * sh.Wo < lim && sh.Hi < lim && sh.Wi < lim;
+}
+
+// Tile rows per block of k_dw_conv over `planes` planes of H x W outputs:
+// 4 (the next tile's input loads overlap the current tile's FMAs), halved
+// while the grid would hold fewer than 4096 blocks.  Returns the tile
+// groups per plane; *per the rows per group.
+int64_t conv_groups(int64_t planes, int64_t H, int64_t W, int64_t* tiles_x, int64_t* tiles_y,
+                    int* per) {
+    *tiles_x = (W + kTW - 1) / kTW;
+    *tiles_y = (H + kTH - 1) / kTH;
+    int p = 4;
+    while (p > 1 && planes * ((*tiles_y + p - 1) / p) * *tiles_x < 4096) p /= 2;
+    *per = p;
+    return ((*tiles_y + p - 1) / p) * *tiles_x;
+}
+
 unsigned grid_stride_blocks(int64_t total) {
     const int64_t b = (total + 255) / 256;
     return (unsigned)std::max<int64_t>(1, std::min<int64_t>(b, 65536));
@@ -506,15 +607,17 @@ int64_t dw_grid_blocks(const DwShape& sh, bool output_tiles) {
 hipError_t launch_dw_forward(const DwShape& sh, const float* x, const float* w,
                              const float* bias, float* y, hipStream_t s) {
     if (sh.N * sh.C * sh.Ho * sh.Wo == 0) return hipSuccess;
-    int64_t tiles_x = 0;
-    const int64_t tpp = tiles_of(sh.Ho, sh.Wo, &tiles_x);
+    int64_t tiles_x = 0, tiles_y = 0;
+    int per = 1;
+    const int64_t tpp = conv_groups(sh.N * sh.C, sh.Ho, sh.Wo, &tiles_x, &tiles_y, &per);
     const int tok = prof_begin(s, "dw_conv");
-    const bool fast = fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
+    const bool fast = planes_fit_32(sh) && fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
         using CF = decltype(cf);
         bsel(bias != nullptr, [&](auto B) {
             k_dw_conv<CF::k, CF::s, CF::d, false, false, B()>
                 <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
-                    x, w, bias, y, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tpp);
+                    x, w, bias, y, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tiles_y,
+                    tpp, per);
         });
     });
     if (!fast)
@@ -536,30 +639,32 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
         if (sh.S == 1) {
             // the adjoint of a stride-1 convolution: the flipped kernel over
             // dy with pad' = (K-1)*D - pad, producing dx's plane
-            int64_t tiles_x = 0;
-            const int64_t tpp = tiles_of(sh.Hi, sh.Wi, &tiles_x);
+            int64_t tiles_x = 0, tiles_y = 0;
+            int per = 1;
+            const int64_t tpp = conv_groups(sh.N * sh.C, sh.Hi, sh.Wi, &tiles_x, &tiles_y, &per);
             const int64_t padf = (sh.K - 1) * sh.D - sh.pad;
-            done = fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
+            done = planes_fit_32(sh) && fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
                 using CF = decltype(cf);
                 bsel(accumulate_dx, [&](auto A) {
                     k_dw_conv<CF::k, CF::s, CF::d, true, A(), false>
                         <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
                             dy, w, nullptr, dx, sh.C, sh.Ho, sh.Wo, sh.Hi, sh.Wi, padf, tiles_x,
-                            tpp);
+                            tiles_y, tpp, per);
                 });
             });
         }
         if (!done && sh.S > 1) {
-            int64_t tiles_x = 0;
-            const int64_t tpp = tiles_of(sh.Hi, sh.Wi, &tiles_x);
-            done = fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
+            int64_t tiles_x = 0, tiles_y = 0;
+            int per = 1;
+            const int64_t tpp = conv_groups(sh.N * sh.C, sh.Hi, sh.Wi, &tiles_x, &tiles_y, &per);
+            done = planes_fit_32(sh) && fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
                 using CF = decltype(cf);
                 if constexpr (CF::s > 1) {
                     bsel(accumulate_dx, [&](auto A) {
                         k_dw_dgrad_strided<CF::k, CF::s, CF::d, A()>
                             <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
                                 dy, w, dx, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x,
-                                tpp);
+                                tiles_y, tpp, per);
                     });
                 }
             });
@@ -580,7 +685,7 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
         const int64_t tpp = wgrad_groups(sh, per, &tiles_x, &tiles_y);
         float* part = static_cast<float*>(ws);
         int tok = prof_begin(s, "dw_conv_wgrad");
-        const bool fast = fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
+        const bool fast = planes_fit_32(sh) && fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
             using CF = decltype(cf);
             k_dw_wgrad<CF::k, CF::s, CF::d>
                 <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
