@@ -177,3 +177,26 @@ def test_dw_full_size_lkr(gpu):
                     mag += abs(v)
         assert abs(float(y[0, c, yo, xo]) - acc) <= (K * K + 2) * U32 * mag + 1e-30
     del x, dy, y, dx
+
+
+@pytest.mark.parametrize("K,S,D,H", [(7, 1, 1, 300), (3, 2, 1, 257), (3, 1, 5, 130)])
+def test_dw_paths_are_deterministic(gpu, K, S, D, H):
+    """Multi-tile depthwise kernels and the weight-gradient finish sum in a
+    fixed order: two runs are bitwise identical."""
+    import torch
+    print(f"dw determinism K={K} S={S} D={D} H={H}", flush=True)
+    C = 24
+    pad = (D * (K - 1) + 1) // 2 if D > 1 else K // 2
+    r = np.random.default_rng(K * 100 + H)
+    x = torch.from_numpy(r.standard_normal((2, C, H, H)).astype(np.float32)).cuda()
+    w = torch.from_numpy((r.standard_normal((C, K, K)) / K).astype(np.float32)).cuda()
+    b = torch.from_numpy(r.standard_normal(C).astype(np.float32)).cuda()
+    Ho = gpu.conv_out_size(H, K, pad, S, D)
+    dy = torch.from_numpy(r.standard_normal((2, C, Ho, Ho)).astype(np.float32)).cuda()
+    runs = []
+    for _ in range(2):
+        y = gpu.dw_conv_forward(x, w, b, pad, S, D)
+        dx, dw, db = gpu.dw_conv_backward(dy, x, w, pad, S, D)
+        runs.append([t.cpu().numpy() for t in (y, dx, dw, db)])
+    for a, c in zip(*runs):
+        assert np.array_equal(a, c)

@@ -447,3 +447,35 @@ def test_pw_small_planes_match_oracle(gpu, oracle, restore_pw_small, N, C_in, C_
     z0 = dev(np.full((N, C_out, HW), 0.25, np.float32))
     gpu.pw_conv_forward(dev(x), dev(w), bd, z=z0)
     assert_z(host(z0), x, w, b, oracle, "into a given z")
+
+
+DETERMINISM_CASES = [
+    # (N, C_in, C_out, HW, limit): which path runs
+    (1, 256, 512, 16, None),        # SIMT forward / dx / weight gradient (K split over waves)
+    (1, 256, 128, 4096, None),      # MFMA, split K over 4 waves (small grid), statistics
+    (1, 64, 64, 262144, None),      # MFMA, two K steps in flight (large grid)
+    (3, 24, 40, 1000, 0),           # MFMA forced, general shapes
+]
+
+
+@pytest.mark.parametrize("N,C_in,C_out,HW,limit", DETERMINISM_CASES)
+def test_pw_paths_are_deterministic(gpu, oracle, restore_pw_small, N, C_in, C_out, HW, limit):
+    """Every pointwise path sums in a fixed order (no atomics): two runs of the
+    fused forward and of the backward are bitwise identical."""
+    print(f"pw determinism N={N} C_in={C_in} C_out={C_out} HW={HW}", flush=True)
+    if limit is not None:
+        gpu.tune(gpu.TUNE_PW_SMALL, limit)
+    x, w, b = rng_inputs(HW + C_out, N, C_in, C_out, HW)
+    r = np.random.default_rng(C_in)
+    dz = r.standard_normal((N, C_out, HW)).astype(np.float32)
+    gamma = r.uniform(0.5, 1.5, C_out).astype(np.float32)
+    beta = (0.1 * r.standard_normal(C_out)).astype(np.float32)
+    G = 8 if C_out % 8 == 0 else 4
+    xd, wd, bd, dzd = dev(x), dev(w), dev(b), dev(dz)
+    runs = []
+    for _ in range(2):
+        z, y, st = gpu.pw_conv_gn_silu_forward(xd, wd, bd, dev(gamma), dev(beta), G, eps=EPS)
+        dx, dw, db = gpu.pw_conv_backward(dzd, xd, wd)
+        runs.append([host(t) for t in (z, y, st.mean, st.rstd, dx, dw, db)])
+    for a, c in zip(*runs):
+        assert np.array_equal(a, c)
