@@ -163,7 +163,8 @@ struct PwBwdArgs {
     void* ws;
 };
 struct PwBwdPlan {
-    int64_t tiles_co = 0, tiles_ci = 0;  // 64x64 tiles of dW
+    int tm = 2, tn = 2;                  // 32-row MFMA tiles per dW tile (C_out, C_in)
+    int64_t tiles_co = 0, tiles_ci = 0;  // (32 tm) x (32 tn) tiles of dW
     int64_t chunk = 0, cpp = 0, G = 0;   // pixel chunks of the dW waves
     size_t wt_bytes = 0, pw_bytes = 0, pb_bytes = 0;
 };

@@ -407,9 +407,10 @@ __global__ __launch_bounds__(64 * KS, PD > 1 ? 1 : 2) void k_pw_conv(
 // db[co] = sum_(n,p) dz[n][co][p].  A GEMM whose K axis is the pixels:
 // C[m = co][n = ci] = sum_k A[m][k] B[k][n], A = dz rows, B = x rows.
 //
-// One wave per (64x64 tile of dW, pixel chunk of one sample).  Both MFMA
-// operands put channels across lanes, so a step of 32 pixels is staged
-// through LDS: the wave reads the 64 dz rows and 64 x rows of the step with
+// One wave per (tile of dW: 64 x 64, or 32 rows / columns for a narrow
+// matrix; pixel chunk of one sample).  Both MFMA operands put channels
+// across lanes, so a step of 32 pixels is staged through LDS: the wave
+// reads the tile's dz rows and x rows of the step with
 // row-contiguous 16-byte loads (8 rows per instruction), writes them to LDS
 // (row stride 144 bytes: conflict-free for the reads below), and each lane
 // then reads its operand runs back (lane l = 32h + j: row j, pixels
@@ -421,13 +422,18 @@ __global__ __launch_bounds__(64 * KS, PD > 1 ? 1 : 2) void k_pw_conv(
 constexpr int kWgStep = 32;                 // pixels per step
 constexpr int kWgStride = kWgStep + 4;      // floats per LDS row (144 bytes)
 
-template <bool FAST>
+// TM, TN: 32-row MFMA tiles of dW along C_out and C_in (2 and 2: a 64 x 64
+// tile; 1 when the matrix has at most 32 rows / columns, so a 16 x 32 dW
+// does not pay for a 64 x 64 tile's MFMAs and loads).
+template <bool FAST, int TM, int TN>
 __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
     const float* __restrict__ dz, const float* __restrict__ x, float* __restrict__ part_w,
     float* __restrict__ part_b, int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk,
     int64_t cpp, int64_t tiles_ci) {
-    // rows 0..63: dz rows co0.., rows 64..127: x rows ci0..
+    // rows 0..32TM-1: dz rows co0.., rows 64..64+32TN-1: x rows ci0..
     __shared__ __attribute__((aligned(16))) float lds[2 * kRowTile * kWgStride];
+    constexpr int kSlots = 4 * (TM + TN);  // load slots in use
+    auto slot_used = [](int sl) { return sl < 8 ? sl < 4 * TM : sl - 8 < 4 * TN; };
     const int lane = threadIdx.x;
     const int h = lane >> 5, j = lane & 31;
     const int64_t tco = (int64_t)blockIdx.x / tiles_ci;
@@ -435,7 +441,7 @@ __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
     const int64_t g = blockIdx.y;  // n * cpp + chunk index
     const int64_t n = g / cpp, kc = g - n * cpp;
     const int64_t px0 = kc * chunk, pend = min(px0 + chunk, HW);
-    const int64_t co0 = tco * kRowTile, ci0 = tci * kRowTile;
+    const int64_t co0 = tco * 32 * TM, ci0 = tci * 32 * TN;
     const bool want_b = tci == 0;
 
     // staging: load slot s (0..15) of lane l covers row 8s + l/8, pixels
@@ -455,6 +461,7 @@ __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
         const bool full = FAST && p + kWgStep <= pend;
 #pragma unroll
         for (int sl = 0; sl < 16; ++sl) {
+            if (!slot_used(sl)) continue;
             if (full) {
                 st[sl] = *reinterpret_cast<const f4*>(src[sl] + p);
             } else {
@@ -467,40 +474,44 @@ __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
     auto lwrite = [&](const f4 (&st)[16]) {
 #pragma unroll
         for (int sl = 0; sl < 16; ++sl)
-            *reinterpret_cast<f4*>(&lds[(8 * sl + srow) * kWgStride + scol]) = st[sl];
+            if (slot_used(sl))
+                *reinterpret_cast<f4*>(&lds[(8 * sl + srow) * kWgStride + scol]) = st[sl];
     };
 
-    f16 acc[2][2];
+    f16 acc[TM][TN];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < TM; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < TN; ++nt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.0f;
-    float sb[2] = {0.0f, 0.0f};
+    float sb[TM];
+#pragma unroll
+    for (int mt = 0; mt < TM; ++mt) sb[mt] = 0.0f;
 
     auto compute = [&]() {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            f4 A[2], B[2];
+            f4 A[TM], B[TN];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < TM; ++t)
                 A[t] = *reinterpret_cast<const f4*>(
                     &lds[(32 * t + j) * kWgStride + 16 * h + 4 * i]);
+#pragma unroll
+            for (int t = 0; t < TN; ++t)
                 B[t] = *reinterpret_cast<const f4*>(
                     &lds[(kRowTile + 32 * t + j) * kWgStride + 16 * h + 4 * i]);
-            }
 #pragma unroll
             for (int q = 0; q < 4; ++q)
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
+                for (int mt = 0; mt < TM; ++mt)
 #pragma unroll
-                    for (int nt = 0; nt < 2; ++nt)
+                    for (int nt = 0; nt < TN; ++nt)
                         acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(A[mt][q], B[nt][q],
                                                                            acc[mt][nt], 0, 0, 0);
             if (want_b) {
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt) sb[mt] += (A[mt][0] + A[mt][1]) + (A[mt][2] + A[mt][3]);
+                for (int mt = 0; mt < TM; ++mt) sb[mt] += (A[mt][0] + A[mt][1]) + (A[mt][2] + A[mt][3]);
             }
         }
     };
@@ -514,16 +525,16 @@ __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
         const int64_t pn = p + kWgStep < pend ? p + kWgStep : p;
         gload(pn, st);
         if (FAST) {
-            __builtin_amdgcn_sched_group_barrier(0x200, 16, 0);  // 16 LDS writes
-            __builtin_amdgcn_sched_group_barrier(0x020, 16, 0);  // 16 global loads
+            __builtin_amdgcn_sched_group_barrier(0x200, kSlots, 0);  // the LDS writes
+            __builtin_amdgcn_sched_group_barrier(0x020, kSlots, 0);  // the global loads
         }
         compute();
     }
 
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < TM; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < TN; ++nt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int64_t co = co0 + tile_row(mt, r, h);
@@ -532,7 +543,7 @@ __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
             }
     if (want_b) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
+        for (int mt = 0; mt < TM; ++mt) {
             const float tot = sb[mt] + __shfl_xor(sb[mt], 32);
             const int64_t co = co0 + 32 * mt + j;
             if (h == 0 && co < C_out) part_b[g * C_out + co] = tot;
@@ -923,8 +934,10 @@ hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_ou
 
 PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW) {
     PwBwdPlan p;
-    p.tiles_co = (C_out + kRowTile - 1) / kRowTile;
-    p.tiles_ci = (C_in + kRowTile - 1) / kRowTile;
+    p.tm = C_out <= 32 ? 1 : 2;
+    p.tn = C_in <= 32 ? 1 : 2;
+    p.tiles_co = (C_out + 32 * p.tm - 1) / (32 * p.tm);
+    p.tiles_ci = (C_in + 32 * p.tn - 1) / (32 * p.tn);
     // about 2048 waves (two per SIMD), chunks of at least 64 pixels (a wave
     // spends about 1.7 us per 32-pixel step on its 64x64 tile, so small
     // grids get short chunks; each chunk adds a partial tile to the finish)
@@ -993,8 +1006,12 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
         const dim3 grid((unsigned)(p.tiles_co * p.tiles_ci), (unsigned)p.G);
         int tok = prof_begin(s, "pw_conv_wgrad");
         bsel(fast, [&](auto F) {
-            k_pw_wgrad<F()><<<grid, 64, 0, s>>>(a.dz, a.x, part_w, part_b, C_in, C_out, HW,
-                                                p.chunk, p.cpp, p.tiles_ci);
+            bsel(p.tm == 2, [&](auto M2) {
+                bsel(p.tn == 2, [&](auto N2) {
+                    k_pw_wgrad<F(), M2() ? 2 : 1, N2() ? 2 : 1><<<grid, 64, 0, s>>>(
+                        a.dz, a.x, part_w, part_b, C_in, C_out, HW, p.chunk, p.cpp, p.tiles_ci);
+                });
+            });
         });
         prof_end(s, tok);
         tok = prof_begin(s, "pw_conv_wgrad_finish");
