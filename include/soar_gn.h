@@ -368,7 +368,7 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
                              /* (multiple of 128)                          */
 #define SOAR_TUNE_SMALL_UNIT 9 /* units of <= this many elements run the   */
                                /* one-launch GroupNorm; 0 = never; the     */
-                               /* default is 32768                         */
+                               /* default is 16384                         */
 #define SOAR_TUNE_FOLD_MAX 11 /* units of <= this many chunk partials fold */
                               /* the finish into the second pass (one     */
                               /* launch less per direction); 0 = never,   */

@@ -603,7 +603,8 @@ def test_small_unit_path(gpu, oracle, restore_tuning, shape, residual):
 
 
 FOLD_SHAPES = [
-    # (N, C, HW, G, kind): units above 32768 elements with at most 128
+    # (N, C, HW, G, kind): units above 32768 elements (past the small-unit
+    # kernels whatever the setting) with at most 128
     # chunk partials, so the finish folds into the second pass
     (1, 16, 512 * 512, 8, "normal"),   # SOAR Nano stride 2 at 1024x1024: 64 partials
     (2, 32, 256 * 256, 8, "normal"),   # 32 partials per unit, two samples
