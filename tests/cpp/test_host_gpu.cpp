@@ -8,8 +8,10 @@
 
 #include "check.hpp"
 #include "soar/autograd.hpp"
+#include "soar/engine.hpp"
 #include "soar/kernels.hpp"
 #include "soar/memory.hpp"
+#include "soar/model.hpp"
 #include "soar/nn.hpp"
 #include "soar_oracle.h"
 
@@ -444,6 +446,85 @@ static void test_cba_blocks() {
     }
 }
 
+// Trainer::train_step semantics (trainer.cpp:110-245) on the Nano model at
+// 32 x 32: a [2,1,H,W] batch, two forward_backward calls at scale 1/2
+// followed by clip + AdamW + zero_grad, and two train_step calls with
+// accumulate_grad_batches = 2 (the first one accumulating) run the same
+// kernels in the same order, so the three models end bitwise equal.
+static void test_trainer_batch_and_accumulation() {
+    const int64_t H = 32, HW = H * H;
+    std::vector<float> img(2 * HW), msk(2 * HW);
+    orc_fill_normal(img.data(), 2 * HW, 91, 1, 0.5, 0.25);
+    for (int64_t b = 0; b < 2; ++b)
+        for (int64_t y = 0; y < H; ++y)
+            for (int64_t x = 0; x < H; ++x) {
+                const double dy = (double)y - H / 2.0, dx = (double)x - H / (3.0 + b);
+                msk[b * HW + y * H + x] = dy * dy + dx * dx < (H / 3.0) * (H / 3.0) ? 1.0f : 0.0f;
+            }
+    struct Run {
+        std::unique_ptr<memory::DeviceArena> params, acts;
+        std::shared_ptr<nn::SOARModel> model;
+        std::unique_ptr<engine::Trainer> trainer;
+    };
+    auto build = [](size_t accumulate) {
+        Run r;
+        r.params = std::make_unique<memory::DeviceArena>(size_t(96) << 20, 256);
+        r.acts = std::make_unique<memory::DeviceArena>(size_t(256) << 20, 256);
+        nn::set_init_seed(12345);
+        r.model = std::make_shared<nn::SOARModel>(1, 1, nn::ModelVariant::Nano);
+        memory::ArenaScope scope(*r.params);
+        r.model->to_device();
+        optim::AdamWOptions o;
+        o.lr = 1e-3f;
+        r.trainer = std::make_unique<engine::Trainer>(
+            r.model, losses::CompositeLoss(0.5f, 0.5f),
+            std::make_unique<optim::AdamW>(r.model->parameters(), o), accumulate);
+        return r;
+    };
+    Run a = build(1), b = build(1), c = build(2);
+    {
+        memory::ArenaScope scope(*a.acts);
+        a.trainer->train_step(Tensor::from_blob(img.data(), {2, 1, H, H}, false, true),
+                              Tensor::from_blob(msk.data(), {2, 1, H, H}, false, true));
+    }
+    {
+        memory::ArenaScope scope(*b.acts);
+        for (int64_t s = 0; s < 2; ++s)
+            b.trainer->forward_backward(
+                Tensor::from_blob(img.data() + s * HW, {1, H, H}, false, true),
+                Tensor::from_blob(msk.data() + s * HW, {1, H, H}, false, true), 0.5f);
+        b.trainer->optimizer().clip_grad_norm(b.trainer->grad_clip());
+        b.trainer->optimizer().step();
+        b.trainer->optimizer().zero_grad();
+    }
+    {
+        memory::ArenaScope scope(*c.acts);
+        for (int64_t s = 0; s < 2; ++s)
+            c.trainer->train_step(
+                Tensor::from_blob(img.data() + s * HW, {1, 1, H, H}, false, true),
+                Tensor::from_blob(msk.data() + s * HW, {1, 1, H, H}, false, true), s == 0);
+    }
+    const auto pa = a.model->named_parameters(), pb = b.model->named_parameters(),
+               pc = c.model->named_parameters();
+    CHECK(pa.size() == pb.size() && pa.size() == pc.size());
+    for (size_t i = 0; i < pa.size(); ++i) {
+        const auto va = pa[i].second->to_host(), vb = pb[i].second->to_host(),
+                   vc = pc[i].second->to_host();
+        CHECK(va == vb);
+        CHECK(va == vc);
+    }
+    // the step moved the weights, and the gradients are zero again
+    nn::set_init_seed(12345);
+    nn::SOARModel fresh(1, 1, nn::ModelVariant::Nano);
+    const auto pf = fresh.named_parameters();
+    size_t moved = 0;
+    for (size_t i = 0; i < pa.size(); ++i) {
+        if (pa[i].second->to_host() != pf[i].second->to_host()) ++moved;
+        for (float g : pa[i].second->grad()->to_host()) CHECK(g == 0.0f);
+    }
+    CHECK(moved > pa.size() / 2);
+}
+
 int main() {
     std::printf("=== host layer: device tests ===\n");
     int fails = 0;
@@ -455,6 +536,7 @@ int main() {
     fails += run_test("reference_operator_api", test_reference_operator_api);
     fails += run_test("conv2d_layers", test_conv2d_layers);
     fails += run_test("cba_blocks", test_cba_blocks);
+    fails += run_test("trainer_batch_and_accumulation", test_trainer_batch_and_accumulation);
     std::printf("%s (%d failed)\n", fails ? "FAILED" : "ALL PASSED", fails);
     return fails ? 1 : 0;
 }
