@@ -1,0 +1,144 @@
+"""HIP graph capture of the hot path.  The C-ABI entry points launch kernels
+only on the stream they are given: no host synchronisation, no allocation
+and no memset nodes (fills are kernels), so a GroupNorm+SiLU forward +
+backward and a CBA forward + backward captured on a stream replay to the
+eager results, bit for bit, every time.  Between replays the test does its
+own eager work (overwriting the outputs, zeroing the accumulated gradients)
+and synchronises, and it checks every replay."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GN_CASES = [
+    # (N, C, HW, G): which GroupNorm path the capture holds
+    (1, 64, 32 * 32, 8),        # one-launch small-unit kernels
+    (2, 32, 128 * 128, 8),      # multi-kernel, finish folded into the second pass
+    (1, 16, 1024 * 1024, 4),    # multi-kernel with separate finish launches
+]
+
+
+def _replay_and_check(g, outs, ref, reset):
+    import torch
+    for rep in range(3):
+        reset()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(outs, ref)):
+            assert torch.equal(a, b), (rep, i)
+
+
+def _capture(step):
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    return g
+
+
+@pytest.mark.parametrize("N,C,HW,G", GN_CASES)
+def test_gn_silu_graph_replays(gpu, N, C, HW, G):
+    import torch
+    print(f"graph GN N={N} C={C} HW={HW} G={G}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(7 + C)
+    x = torch.randn((N, C, HW), device="cuda", generator=gen)
+    dy = 1e-2 * torch.randn((N, C, HW), device="cuda", generator=gen)
+    gamma = 0.5 + torch.rand(C, device="cuda", generator=gen)
+    beta = 0.1 * torch.randn(C, device="cuda", generator=gen)
+    ws = gpu.workspace(N, C, HW, G)
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    mean, rstd, lo = (torch.empty(N * G, device="cuda") for _ in range(3))
+    dg, db = torch.zeros(C, device="cuda"), torch.zeros(C, device="cuda")
+
+    def step():
+        gpu.gn_silu_forward(x, gamma, beta, G, y=y, mean=mean, rstd=rstd, mean_lo=lo, ws=ws)
+        gpu.gn_silu_backward(dy, x, gamma, beta, (mean, rstd, lo), G, dx=dx, dgamma=dg,
+                             dbeta=db, ws=ws)
+
+    outs = (y, mean, rstd, lo, dx, dg, db)
+    step()
+    torch.cuda.synchronize()
+    ref = [t.clone() for t in outs]
+
+    def reset():
+        for t in (y, mean, rstd, lo, dx):
+            t.fill_(float("nan"))
+        dg.zero_()
+        db.zero_()
+
+    reset()
+    g = _capture(step)
+    _replay_and_check(g, outs, ref, reset)
+
+
+CBA_CASES = [
+    # (C_in, C_out, H, K): pointwise (K = 1) or depthwise CBA
+    (64, 64, 128, 1),    # MFMA conv, split K, statistics in the epilogue
+    (32, 64, 16, 1),     # SIMT conv, then the one-launch GroupNorm
+    (32, 32, 64, 7),     # depthwise k7 (multi-tile kernels), then GroupNorm
+]
+
+
+@pytest.mark.parametrize("C_in,C_out,H,K", CBA_CASES)
+def test_cba_graph_replays(gpu, C_in, C_out, H, K):
+    import torch
+    print(f"graph CBA C_in={C_in} C_out={C_out} H={H} K={K}", flush=True)
+    N, HW, G = 1, H * H, 8
+    gen = torch.Generator(device="cuda").manual_seed(K + H)
+    x = torch.randn((N, C_in, H, H), device="cuda", generator=gen)
+    dy = 1e-2 * torch.randn((N, C_out, H, H), device="cuda", generator=gen)
+    gamma = 0.5 + torch.rand(C_out, device="cuda", generator=gen)
+    beta = 0.1 * torch.randn(C_out, device="cuda", generator=gen)
+    if K == 1:
+        w = torch.randn((C_out, C_in), device="cuda", generator=gen) / C_in ** 0.5
+    else:
+        w = torch.randn((C_in, K, K), device="cuda", generator=gen) / K
+    z = torch.empty((N, C_out, H, H), device="cuda")
+    y, dz = torch.empty_like(z), torch.empty_like(z)
+    mean, rstd, lo = (torch.empty(N * G, device="cuda") for _ in range(3))
+    dx = torch.empty_like(x)
+    dw = torch.zeros_like(w)
+    dg, db = torch.zeros(C_out, device="cuda"), torch.zeros(C_out, device="cuda")
+    gws = gpu.workspace(N, C_out, HW, G)
+    if K == 1:
+        fws = torch.empty(max(gpu.pw_conv_gn_workspace_bytes(N, C_out, HW, G), 1),
+                          dtype=torch.uint8, device="cuda")
+        bws = torch.empty(max(gpu.pw_conv_backward_workspace_bytes(N, C_in, C_out, HW), 1),
+                          dtype=torch.uint8, device="cuda")
+    else:
+        n = int(gpu.lib().soar_dw_conv_backward_workspace_bytes(N, C_in, H, H, H, H, K, 1, 1))
+        bws = torch.empty(max(n, 1), dtype=torch.uint8, device="cuda")
+
+    def step():
+        if K == 1:
+            gpu.pw_conv_gn_silu_forward(x, w, None, gamma, beta, G, eps=1e-5, z=z, y=y,
+                                        mean=mean, rstd=rstd, mean_lo=lo, ws=fws)
+        else:
+            gpu.dw_conv_forward(x, w, None, K // 2, y=z)
+            gpu.gn_silu_forward(z, gamma, beta, G, y=y, mean=mean, rstd=rstd, mean_lo=lo,
+                                ws=gws)
+        gpu.gn_silu_backward(dy, z, gamma, beta, (mean, rstd, lo), G, dx=dz, dgamma=dg,
+                             dbeta=db, ws=gws)
+        if K == 1:
+            gpu.pw_conv_backward(dz, x, w, dx=dx, dweight=dw, want_db=False, ws=bws)
+        else:
+            gpu.dw_conv_backward(dz, x, w, K // 2, dx=dx, dweight=dw, want_db=False, ws=bws)
+
+    outs = (z, y, mean, rstd, lo, dz, dx, dw, dg, db)
+    step()
+    torch.cuda.synchronize()
+    ref = [t.clone() for t in outs]
+
+    def reset():
+        for t in (z, y, mean, rstd, lo, dz, dx):
+            t.fill_(float("nan"))
+        for t in (dw, dg, db):
+            t.zero_()
+
+    reset()
+    g = _capture(step)
+    _replay_and_check(g, outs, ref, reset)
