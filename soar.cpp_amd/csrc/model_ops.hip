@@ -383,83 +383,293 @@ __global__ __launch_bounds__(kThreads) void k_avg_pool_bwd(const float* __restri
 // (upsample_kernels.cu:11-66, layers.cpp:1073-1150).
 // ---------------------------------------------------------------------------
 struct Src {
-    int64_t i0, i1;  // the two source taps (equal at the last row / column)
-    float l0, l1;    // their weights
+    int i0, i1;    // the two source taps (equal at the last row / column)
+    float l0, l1;  // their weights
 };
 
-__device__ __forceinline__ Src src_index(float scale, int64_t dst, int64_t n_in) {
+// (plane sides are below 2^31: the C-ABI checks them)
+__device__ __forceinline__ Src src_index(float scale, int dst, int n_in) {
     float r = scale * ((float)dst + 0.5f) - 0.5f;
     r = r < 0.0f ? 0.0f : r;
-    const int64_t i0 = min((int64_t)r, n_in - 1);
-    const int64_t step = i0 < n_in - 1 ? 1 : 0;
+    const int i0 = min((int)r, n_in - 1);
+    const int step = i0 < n_in - 1 ? 1 : 0;
     const float l1 = r - (float)i0;
     return {i0, i0 + step, 1.0f - l1, l1};
 }
 
+// Element indices have type I (32-bit when both tensors' element counts
+// fit: the index arithmetic is most of this kernel's instructions).
+template <typename I>
 __global__ __launch_bounds__(kThreads) void k_upsample_fwd(const float* __restrict__ in,
-                                                           float* __restrict__ out, int64_t rows,
-                                                           int64_t H_in, int64_t W_in,
-                                                           int64_t H_out, int64_t W_out,
+                                                           float* __restrict__ out, I rows,
+                                                           I H_in, I W_in, I H_out, I W_out,
                                                            float sh, float sw) {
-    const int64_t total = rows * H_out * W_out;
-    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * kThreads) {
-        const int64_t x = i % W_out;
-        int64_t t = i / W_out;
-        const int64_t y = t % H_out;
-        const int64_t row = t / H_out;
-        const Src sy = src_index(sh, y, H_in), sx = src_index(sw, x, W_in);
-        const float* p = in + row * H_in * W_in;
-        const float v00 = p[sy.i0 * W_in + sx.i0], v01 = p[sy.i0 * W_in + sx.i1];
-        const float v10 = p[sy.i1 * W_in + sx.i0], v11 = p[sy.i1 * W_in + sx.i1];
+    const I total = rows * H_out * W_out;
+    for (I i = (I)blockIdx.x * kThreads + threadIdx.x; i < total; i += (I)gridDim.x * kThreads) {
+        const I x = i % W_out;
+        const I t = i / W_out;
+        const I y = t % H_out;
+        const I row = t / H_out;
+        const Src sy = src_index(sh, (int)y, (int)H_in), sx = src_index(sw, (int)x, (int)W_in);
+        const float* p = in + (int64_t)row * H_in * W_in;
+        const float v00 = p[(I)sy.i0 * W_in + sx.i0], v01 = p[(I)sy.i0 * W_in + sx.i1];
+        const float v10 = p[(I)sy.i1 * W_in + sx.i0], v11 = p[(I)sy.i1 * W_in + sx.i1];
         out[i] = sy.l0 * (sx.l0 * v00 + sx.l1 * v01) + sy.l1 * (sx.l0 * v10 + sx.l1 * v11);
     }
 }
 
-// Range of destination indices whose taps can reach source index `s`
-// (conservative by one on each side; callers re-test each candidate).
-__device__ __forceinline__ void dst_range(float scale, int64_t s, int64_t n_out, int64_t* lo,
-                                          int64_t* hi) {
+// Destinations along one axis whose taps reach source index `s`.  They form
+// one contiguous run: a destination's first tap is non-decreasing in the
+// destination index, and of the destinations whose first tap is s - 1 only
+// the first can give s a zero weight.  The run is found inside a candidate
+// window that is conservative by one on each side.  Returns the run length
+// (0 when no destination reads s, as when downsampling) and its first index.
+__device__ __forceinline__ void dst_window(float scale, int s, int n_out, int* lo, int* hi) {
+    // both bounds are non-decreasing in s
     const float a = ((float)s - 0.5f) / scale - 0.5f;
     const float b = ((float)s + 1.5f) / scale - 0.5f;
-    *lo = std::max<int64_t>(0, (int64_t)floorf(a) - 1);
-    *hi = std::min<int64_t>(n_out - 1, (int64_t)ceilf(b) + 1);
+    *lo = max(0, (int)floorf(a) - 1);
+    *hi = min(n_out - 1, (int)ceilf(b) + 1);
 }
 
-__device__ __forceinline__ float tap_weight(const Src& s, int64_t idx) {
+__device__ __forceinline__ int dst_run(float scale, int s, int n_in, int n_out, int* first) {
+    int d, hi;
+    dst_window(scale, s, n_out, &d, &hi);
+    auto w = [&](int i) {
+        const Src t = src_index(scale, i, n_in);
+        return (t.i0 == s ? t.l0 : 0.0f) + (t.i1 == s ? t.l1 : 0.0f);
+    };
+    while (d <= hi && w(d) == 0.0f) ++d;
+    int n = 0;
+    while (d + n <= hi && w(d + n) != 0.0f) ++n;
+    *first = d;
+    return n;
+}
+
+__device__ __forceinline__ float tap_weight(const Src& s, int idx) {
     return (s.i0 == idx ? s.l0 : 0.0f) + (s.i1 == idx ? s.l1 : 0.0f);
 }
 
 // Backward as a gather: each source pixel sums the destination pixels that
-// read it, with the forward's weights (no atomics).
+// read it, with the forward's weights, rows in order and within a row
+// columns in order (no atomics).  The column weights of a run of at most R
+// destinations are computed once and kept in registers, and each row's R
+// loads are issued together (clamped to the run, the extra lanes weighted
+// out); longer runs take the plain loop.  Element indices have type I
+// (32-bit when both tensors' element counts fit); plane sides fit in int.
+template <int R>
+__device__ float gather_one(const float* __restrict__ g, int iy, int ix, int H_in, int W_in,
+                            int H_out, int W_out, float sh, float sw) {
+    int ya, xa;
+    const int ny = dst_run(sh, iy, H_in, H_out, &ya);
+    const int nx = dst_run(sw, ix, W_in, W_out, &xa);
+    float acc = 0.0f;
+    if (nx > 0 && nx <= R) {  // (a zero-length run may start past the row)
+        float wx[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+            wx[j] = j < nx ? tap_weight(src_index(sw, xa + j, W_in), ix) : 0.0f;
+        const int xl = xa + nx - 1;
+        for (int k = 0; k < ny; ++k) {
+            const int y = ya + k;
+            const float wy = tap_weight(src_index(sh, y, H_in), iy);
+            const float* gr = g + (int64_t)y * W_out;
+            float v[R];
+#pragma unroll
+            for (int j = 0; j < R; ++j) v[j] = gr[min(xa + j, xl)];
+            float rs = 0.0f;
+#pragma unroll
+            for (int j = 0; j < R; ++j)
+                if (j < nx) rs += wx[j] * v[j];
+            acc += wy * rs;
+        }
+    } else {
+        for (int k = 0; k < ny; ++k) {
+            const int y = ya + k;
+            const float wy = tap_weight(src_index(sh, y, H_in), iy);
+            const float* gr = g + (int64_t)y * W_out;
+            float rs = 0.0f;
+            for (int j = 0; j < nx; ++j)
+                rs += tap_weight(src_index(sw, xa + j, W_in), ix) * gr[xa + j];
+            acc += wy * rs;
+        }
+    }
+    return acc;
+}
+
+template <int R, typename I>
 __global__ __launch_bounds__(kThreads) void k_upsample_bwd(const float* __restrict__ go,
-                                                           float* __restrict__ gi, int64_t rows,
-                                                           int64_t H_in, int64_t W_in,
-                                                           int64_t H_out, int64_t W_out,
-                                                           float sh, float sw) {
-    const int64_t total = rows * H_in * W_in;
-    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * kThreads) {
-        const int64_t ix = i % W_in;
-        int64_t t = i / W_in;
-        const int64_t iy = t % H_in;
-        const int64_t row = t / H_in;
-        int64_t y0, y1, x0, x1;
-        dst_range(sh, iy, H_out, &y0, &y1);
-        dst_range(sw, ix, W_out, &x0, &x1);
-        const float* g = go + row * H_out * W_out;
+                                                           float* __restrict__ gi, I rows,
+                                                           int H_in, int W_in, int H_out,
+                                                           int W_out, float sh, float sw) {
+    const I total = rows * H_in * W_in;
+    for (I i = (I)blockIdx.x * kThreads + threadIdx.x; i < total; i += (I)gridDim.x * kThreads) {
+        const int ix = (int)(i % W_in);
+        const I t = i / W_in;
+        const int iy = (int)(t % H_in);
+        const I row = t / H_in;
+        gi[i] += gather_one<R>(go + (int64_t)row * H_out * W_out, iy, ix, H_in, W_in, H_out,
+                               W_out, sh, sw);
+    }
+}
+
+// Backward for exact integer factors F (2 or 4) on both axes: every
+// destination that reads source s lies in [F s - F/2, F s + 3F/2 - 1], 2F
+// candidates per axis, so the taps need no search (checked against every
+// destination for sides up to 299; the sides are capped at 2^22, where the
+// fp32 source coordinates are exact).  Zero-weight candidates are skipped,
+// so the terms and their order are gather_one's and the results identical.
+template <int F, typename I>
+__global__ __launch_bounds__(kThreads) void k_upsample_bwd_int(const float* __restrict__ go,
+                                                               float* __restrict__ gi, I rows,
+                                                               int H_in, int W_in, float sh,
+                                                               float sw) {
+    constexpr int NC = 2 * F, OFF = F / 2;
+    const int H_out = F * H_in, W_out = F * W_in;
+    const I total = rows * H_in * W_in;
+    for (I i = (I)blockIdx.x * kThreads + threadIdx.x; i < total; i += (I)gridDim.x * kThreads) {
+        const int ix = (int)(i % W_in);
+        const I t = i / W_in;
+        const int iy = (int)(t % H_in);
+        const I row = t / H_in;
+        const float* g = go + (int64_t)row * H_out * W_out;
+        float wx[NC];
+        int xs[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int x = F * ix - OFF + j;
+            const bool in = x >= 0 && x < W_out;
+            wx[j] = in ? tap_weight(src_index(sw, x, W_in), ix) : 0.0f;
+            xs[j] = in ? x : 0;
+        }
         float acc = 0.0f;
-        for (int64_t y = y0; y <= y1; ++y) {
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+            const int y = F * iy - OFF + k;
+            if (y < 0 || y >= H_out) continue;
             const float wy = tap_weight(src_index(sh, y, H_in), iy);
             if (wy == 0.0f) continue;
+            const float* gr = g + (int64_t)y * W_out;
+            float v[NC];
+#pragma unroll
+            for (int j = 0; j < NC; ++j) v[j] = gr[xs[j]];
             float rs = 0.0f;
-            for (int64_t x = x0; x <= x1; ++x) {
-                const float wx = tap_weight(src_index(sw, x, W_in), ix);
-                if (wx != 0.0f) rs += wx * g[y * W_out + x];
-            }
+#pragma unroll
+            for (int j = 0; j < NC; ++j)
+                if (wx[j] != 0.0f) rs += wx[j] * v[j];
             acc += wy * rs;
         }
         gi[i] += acc;
+    }
+}
+
+// Tiled backward for resizes by at most about 2x (or 4x) per axis.  A block
+// owns TY x 64 source pixels of one plane.  It stages the window of
+// destination rows and columns whose taps can reach them in LDS (coalesced
+// loads: each destination value is read from memory about once, against
+// once per tap in the per-pixel kernel), sums each window row over every
+// source column's run of destination columns, then each source pixel sums
+// its run of those row sums.  The terms and their order are the per-pixel
+// kernel's (columns in order within a row, then rows in order), so both
+// kernels give identical results.  A window larger than the LDS arrays
+// (not expected for the factors the host routes here) makes that tile
+// gather from global memory instead.
+template <int TY, int WR, int WC, int R>
+__global__ __launch_bounds__(kThreads) void k_upsample_bwd_tiled(
+    const float* __restrict__ go, float* __restrict__ gi, int64_t rows, int H_in, int W_in,
+    int H_out, int W_out, float sh, float sw, int tiles_y, int tiles_x) {
+    static_assert(kThreads % 64 == 0, "a thread keeps one source column");
+    constexpr int kRowStep = kThreads / 64;
+    __shared__ float win[WR][WC + 1];
+    __shared__ float rsum[WR][64];
+    const int c = threadIdx.x & 63;       // this thread's source column in the tile
+    const int r0 = threadIdx.x >> 6;      // and its first row (then every kRowStep-th)
+    const int64_t ntiles = rows * tiles_y * tiles_x;
+    for (int64_t b = blockIdx.x; b < ntiles; b += gridDim.x) {
+        const int tx = (int)(b % tiles_x);
+        const int64_t q = b / tiles_x;
+        const int ty = (int)(q % tiles_y);
+        const int64_t row = q / tiles_y;
+        const int iy0 = ty * TY, ix0 = tx * 64;
+        const int iy1 = min(iy0 + TY, H_in) - 1, ix1 = min(ix0 + 64, W_in) - 1;
+        int ylo, yhi, xlo, xhi, unused;
+        dst_window(sh, iy0, H_out, &ylo, &unused);
+        dst_window(sh, iy1, H_out, &unused, &yhi);
+        dst_window(sw, ix0, W_out, &xlo, &unused);
+        dst_window(sw, ix1, W_out, &unused, &xhi);
+        const int nr = yhi - ylo + 1, nc = xhi - xlo + 1;
+        const float* g = go + row * H_out * W_out;
+        float* gp = gi + row * H_in * W_in;
+        const int ix = ix0 + c;
+        if (nr > WR || nc > WC) {  // block-uniform
+            for (int rr = r0; rr < TY; rr += kRowStep) {
+                const int iy = iy0 + rr;
+                if (iy <= iy1 && ix <= ix1)
+                    gp[(int64_t)iy * W_in + ix] +=
+                        gather_one<R>(g, iy, ix, H_in, W_in, H_out, W_out, sh, sw);
+            }
+            continue;
+        }
+        {
+            // wave w stages rows w, w + kRowStep, ...; lane l columns l, l + 64,
+            // ...: every load is issued before the first LDS store
+            constexpr int kRows = (WR + kRowStep - 1) / kRowStep, kCols = (WC + 63) / 64;
+            float v[kRows][kCols];
+#pragma unroll
+            for (int i = 0; i < kRows; ++i) {
+                const int rr = r0 + i * kRowStep;
+                const float* src = g + (int64_t)(ylo + min(rr, nr - 1)) * W_out + xlo;
+#pragma unroll
+                for (int j = 0; j < kCols; ++j) v[i][j] = src[min(c + 64 * j, nc - 1)];
+            }
+#pragma unroll
+            for (int i = 0; i < kRows; ++i) {
+                const int rr = r0 + i * kRowStep;
+#pragma unroll
+                for (int j = 0; j < kCols; ++j)
+                    if (rr < nr && c + 64 * j < nc) win[rr][c + 64 * j] = v[i][j];
+            }
+        }
+        __syncthreads();
+        // this column's run of destination columns, inside [xlo, xhi]
+        int xa = 0, nx = 0;
+        if (ix <= ix1) nx = dst_run(sw, ix, W_in, W_out, &xa);
+        xa -= xlo;
+        if (nx > 0 && nx <= R) {
+            float wx[R];
+#pragma unroll
+            for (int j = 0; j < R; ++j)
+                wx[j] = j < nx ? tap_weight(src_index(sw, xlo + xa + j, W_in), ix) : 0.0f;
+            const int xl = xa + nx - 1;
+            for (int rr = r0; rr < nr; rr += kRowStep) {
+                float rs = 0.0f;
+#pragma unroll
+                for (int j = 0; j < R; ++j) {
+                    const float v = win[rr][min(xa + j, xl)];
+                    if (j < nx) rs += wx[j] * v;
+                }
+                rsum[rr][c] = rs;
+            }
+        } else {
+            for (int rr = r0; rr < nr; rr += kRowStep) {
+                float rs = 0.0f;
+                for (int j = 0; j < nx; ++j)
+                    rs += tap_weight(src_index(sw, xlo + xa + j, W_in), ix) * win[rr][xa + j];
+                rsum[rr][c] = rs;
+            }
+        }
+        __syncthreads();
+        for (int rr = r0; rr < TY; rr += kRowStep) {
+            const int iy = iy0 + rr;
+            if (iy > iy1 || ix > ix1) continue;
+            int ya;
+            const int ny = dst_run(sh, iy, H_in, H_out, &ya);
+            float acc = 0.0f;
+            for (int k = 0; k < ny; ++k)
+                acc += tap_weight(src_index(sh, ya + k, H_in), iy) * rsum[ya + k - ylo][c];
+            gp[(int64_t)iy * W_in + ix] += acc;
+        }
+        __syncthreads();  // win and rsum are refilled for the next tile
     }
 }
 
@@ -611,12 +821,14 @@ __global__ __launch_bounds__(kThreads) void k_loss_sums(const float* __restrict_
 
 __global__ __launch_bounds__(kThreads) void k_loss_finish(const double* __restrict__ part,
                                                           int nparts, double* __restrict__ out) {
-    // thread k < 4 adds quantity k over the blocks in order
-    const int k = threadIdx.x;
-    if (k < 4) {
-        double s = 0.0;
-        for (int b = 0; b < nparts; ++b) s += part[k * nparts + b];
-        out[k] = s;
+    // per quantity: thread t adds blocks t, t + kThreads, ... in order, then
+    // the fixed block tree (a lone thread walking 1024 partials took 80 us)
+    __shared__ double sh[kThreads];
+    for (int k = 0; k < 4; ++k) {
+        double v = 0.0;
+        for (int b = threadIdx.x; b < nparts; b += kThreads) v += part[k * nparts + b];
+        const double s = block_sum(v, sh);
+        if (threadIdx.x == 0) out[k] = s;
     }
 }
 
@@ -919,19 +1131,77 @@ hipError_t launch_avg_pool_backward(const float* go, float* gi, int64_t rows, in
 
 hipError_t launch_upsample_forward(const float* in, float* out, int64_t rows, int64_t H_in,
                                    int64_t W_in, int64_t H_out, int64_t W_out, hipStream_t s) {
+    if (std::max({H_in, W_in, H_out, W_out}) > INT32_MAX) return hipErrorInvalidValue;
     const float sh = (float)H_in / (float)H_out, sw = (float)W_in / (float)W_out;
-    k_upsample_fwd<<<blocks_for(rows * H_out * W_out), kThreads, 0, s>>>(in, out, rows, H_in,
-                                                                          W_in, H_out, W_out,
-                                                                          sh, sw);
+    const dim3 grid = blocks_for(rows * H_out * W_out);
+    auto run = [&](auto I) {
+        using T = decltype(I);
+        k_upsample_fwd<T><<<grid, kThreads, 0, s>>>(in, out, (T)rows, (T)H_in, (T)W_in,
+                                                    (T)H_out, (T)W_out, sh, sw);
+    };
+    if (rows * std::max(H_in * W_in, H_out * W_out) <= INT32_MAX)
+        run(int{});
+    else
+        run(int64_t{});
     return hipGetLastError();
 }
 
 hipError_t launch_upsample_backward(const float* go, float* gi, int64_t rows, int64_t H_in,
                                     int64_t W_in, int64_t H_out, int64_t W_out, hipStream_t s) {
+    if (std::max({H_in, W_in, H_out, W_out}) > INT32_MAX) return hipErrorInvalidValue;
     const float sh = (float)H_in / (float)H_out, sw = (float)W_in / (float)W_out;
-    k_upsample_bwd<<<blocks_for(rows * H_in * W_in), kThreads, 0, s>>>(go, gi, rows, H_in,
-                                                                        W_in, H_out, W_out, sh,
-                                                                        sw);
+    using std::integral_constant;
+    // Tiles: the window of a TY x 64 tile spans at most (TY + 1) f + 6 rows
+    // and 65 f + 6 columns at a factor f = out / in per axis; a column run
+    // holds at most about 2.5 f + 3 destinations.
+    auto tiled = [&](auto TY, auto WR, auto WC, auto R) {
+        const int64_t tiles_y = (H_in + TY() - 1) / TY(), tiles_x = (W_in + 63) / 64;
+        const int64_t nt = rows * tiles_y * tiles_x;
+        const unsigned grid = (unsigned)std::min<int64_t>(nt, (int64_t)1 << 20);
+        k_upsample_bwd_tiled<TY(), WR(), WC(), R()><<<grid, kThreads, 0, s>>>(
+            go, gi, rows, (int)H_in, (int)W_in, (int)H_out, (int)W_out, sh, sw, (int)tiles_y,
+            (int)tiles_x);
+    };
+    const bool i32 = rows * std::max(H_in * W_in, H_out * W_out) <= INT32_MAX;
+    const int64_t f = H_out / H_in;
+    if ((f == 2 || f == 4) && H_out == f * H_in && W_out == f * W_in &&
+        std::max(H_out, W_out) <= ((int64_t)1 << 22)) {
+        const dim3 grid = blocks_for(rows * H_in * W_in);
+        auto run = [&](auto F, auto I) {
+            using T = decltype(I);
+            k_upsample_bwd_int<F(), T><<<grid, kThreads, 0, s>>>(go, gi, (T)rows, (int)H_in,
+                                                                 (int)W_in, sh, sw);
+        };
+        auto pick = [&](auto I) {
+            if (f == 2)
+                run(integral_constant<int, 2>{}, I);
+            else
+                run(integral_constant<int, 4>{}, I);
+        };
+        if (i32)
+            pick(int{});
+        else
+            pick(int64_t{});
+    } else if (H_out <= 2 * H_in && W_out <= 2 * W_in) {
+        tiled(integral_constant<int, 8>{}, integral_constant<int, 24>{},
+              integral_constant<int, 136>{}, integral_constant<int, 6>{});
+    } else if (H_out <= 4 * H_in && W_out <= 4 * W_in) {
+        tiled(integral_constant<int, 4>{}, integral_constant<int, 26>{},
+              integral_constant<int, 266>{}, integral_constant<int, 10>{});
+    } else {
+        // larger factors: one thread per source pixel
+        const dim3 grid = blocks_for(rows * H_in * W_in);
+        auto run = [&](auto I) {
+            using T = decltype(I);
+            k_upsample_bwd<10, T><<<grid, kThreads, 0, s>>>(go, gi, (T)rows, (int)H_in,
+                                                            (int)W_in, (int)H_out, (int)W_out,
+                                                            sh, sw);
+        };
+        if (i32)
+            run(int{});
+        else
+            run(int64_t{});
+    }
     return hipGetLastError();
 }
 

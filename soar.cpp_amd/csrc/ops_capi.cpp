@@ -5,6 +5,7 @@
 // buffers are checked against their allocations before anything launches.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -140,6 +141,8 @@ int resize_check(const float* src, const float* dst, size_t C, size_t H_in, size
         return fail(SOAR_EINVAL, "upsample: sizes overflow");
     if (H_in == 0 || W_in == 0 || H_out == 0 || W_out == 0)
         return fail(SOAR_EINVAL, "upsample: empty input or output plane");
+    if (std::max({H_in, W_in, H_out, W_out}) > (size_t)INT32_MAX)
+        return fail(SOAR_EINVAL, "upsample: a plane side exceeds 2^31 - 1");
     int rc;
     if ((rc = require_device())) return rc;
     if (backward)

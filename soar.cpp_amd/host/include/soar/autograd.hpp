@@ -4,7 +4,7 @@
 // src/tensor/tensor.cpp:173-246):
 //   * dependency counting over get_inputs() edges, then a FIFO ready queue;
 //   * a node's incoming gradients are merged in add_grad_output (first
-//     arrival kept, later arrivals accumulated);
+//     arrival kept by reference, later arrivals added);
 //   * release_variables() right after a node's backward (eager release).
 #pragma once
 
@@ -21,8 +21,10 @@ struct AutogradNode : std::enable_shared_from_this<AutogradNode> {
     virtual void backward(const TensorPtr& grad_output) = 0;
     [[nodiscard]] virtual std::vector<std::shared_ptr<AutogradNode>> get_inputs() const = 0;
     virtual void release_variables() {}
-    // First arrival kept (a copy; the rvalue overload adopts a sole-owner
-    // tensor), later arrivals accumulated (tensor.cpp:194-213).
+    // Later arrivals are added to the first (tensor.cpp:194-213).  The
+    // first is kept by reference, not copied, so backward() must treat its
+    // grad_output as read-only; a later arrival adds in place only while
+    // this node holds the sole reference, else it sums into a new buffer.
     void add_grad_output(const TensorPtr& incoming);
     void add_grad_output(TensorPtr&& incoming);
 
@@ -83,4 +85,14 @@ void propagate_grad(const TensorPtr& tensor, const TensorPtr& incoming);
 // when the caller held the only reference).
 void propagate_grad(const TensorPtr& tensor, TensorPtr&& incoming);
 void run_backward(std::shared_ptr<AutogradNode> root, const TensorPtr& root_grad);
+// The pending gradient of `tensor` when a kernel may add into it directly,
+// in place of making a fresh gradient and propagating it (which costs a
+// separate merge pass): the grad_output of tensor's producing node, if
+// that node holds the only reference to it and it is a device tensor of
+// tensor's size.  nullptr otherwise (and for leaves).
+TensorPtr grad_sink(const TensorPtr& tensor);
+// Gradient buffer for a kernel that adds (+=) into it: grad_sink(tensor)
+// when there is one (*fresh = false), else fresh device zeros
+// (*fresh = true) that the caller hands to propagate_grad.
+TensorPtr add_target(const TensorPtr& tensor, bool* fresh);
 }  // namespace soar

@@ -5,25 +5,35 @@
 
 namespace soar::autograd {
 
-TensorPtr adopt_or_copy(TensorPtr&& incoming);
 void accumulate_into(const TensorPtr& acc, const TensorPtr& inc);
+TensorPtr sum_of(const TensorPtr& a, const TensorPtr& b);
 
+// A node's first incoming gradient is kept by reference, without a copy:
+// backward implementations only read their grad_output.  A later arrival
+// adds in place when the node holds the only reference to its buffer, and
+// otherwise (another node or the caller still reads that buffer) writes the
+// sum to a new buffer, which costs one pass where a copy on first arrival
+// plus an in-place add cost two.
 void AutogradNode::add_grad_output(const TensorPtr& incoming) {
     if (!incoming) return;
-    if (!grad_output_) {
-        grad_output_ = incoming->clone();
-        return;
-    }
-    accumulate_into(grad_output_, incoming);
+    if (!grad_output_)
+        grad_output_ = incoming;
+    else if (grad_output_.use_count() == 1)
+        accumulate_into(grad_output_, incoming);
+    else
+        grad_output_ = sum_of(grad_output_, incoming);
 }
 
 void AutogradNode::add_grad_output(TensorPtr&& incoming) {
     if (!incoming) return;
     if (!grad_output_) {
-        grad_output_ = adopt_or_copy(std::move(incoming));
-        return;
+        grad_output_ = std::move(incoming);
+    } else if (grad_output_.use_count() > 1 && incoming.use_count() == 1) {
+        accumulate_into(incoming, grad_output_);  // the sum lands in the sole-owner buffer
+        grad_output_ = std::move(incoming);
+    } else {
+        add_grad_output(static_cast<const TensorPtr&>(incoming));
     }
-    accumulate_into(grad_output_, incoming);
 }
 
 void AccumulateGradNode::backward(const TensorPtr& grad_output) {
@@ -109,6 +119,24 @@ void propagate_grad(const TensorPtr& tensor, TensorPtr&& incoming) {
         fn->add_grad_output(std::move(incoming));
     else
         tensor->add_grad(std::move(incoming));
+}
+
+TensorPtr grad_sink(const TensorPtr& tensor) {
+    if (!tensor || !tensor->requires_grad()) return nullptr;
+    const auto fn = tensor->grad_fn();
+    if (!fn || !fn->grad_output_ || fn->grad_output_.use_count() != 1) return nullptr;
+    const TensorPtr& g = fn->grad_output_;
+    if (!g->is_cuda() || g->numel() != tensor->numel()) return nullptr;
+    return g;
+}
+
+TensorPtr add_target(const TensorPtr& tensor, bool* fresh) {
+    if (TensorPtr s = grad_sink(tensor)) {
+        *fresh = false;
+        return s;
+    }
+    *fresh = true;
+    return Tensor::zeros(tensor->shape(), false, true);
 }
 
 void run_backward(std::shared_ptr<AutogradNode> root, const TensorPtr& root_grad) {

@@ -37,12 +37,13 @@ struct DiceBCENode : autograd::AutogradNode {
     void backward(const TensorPtr& grad_output) override {
         if (!logits || !logits->requires_grad()) return;
         const float go = grad_output->to_host()[0];
-        TensorPtr gz = Tensor::zeros(logits->shape(), false, true);
+        bool fresh = false;
+        TensorPtr gz = add_target(logits, &fresh);
         check(soar_dice_bce_loss_backward(logits->cuda_data(), targets->cuda_data(),
                                           gz->cuda_data(), go, w, bw, dw, pos_weight, smooth,
                                           inter, sum_p, sum_y, (size_t)logits->numel(), nullptr),
               "Dice+BCE backward");
-        propagate_grad(logits, std::move(gz));
+        if (fresh) propagate_grad(logits, std::move(gz));
     }
     void release_variables() override { logits = targets = nullptr; }
 };

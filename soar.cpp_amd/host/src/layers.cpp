@@ -41,8 +41,6 @@ void to_dev(const TensorPtr& t) {
 
 bool wants(const TensorPtr& t) { return t && t->requires_grad(); }
 
-TensorPtr zeros_like_dev(const TensorPtr& t) { return Tensor::zeros(t->shape(), false, true); }
-
 // ---- nodes ------------------------------------------------------------------
 struct SigmoidNode : autograd::AutogradNode {
     TensorPtr input, output;
@@ -53,11 +51,12 @@ struct SigmoidNode : autograd::AutogradNode {
     void backward(const TensorPtr& go) override {
         if (!wants(input)) return;
         to_dev(go);
-        TensorPtr gx = zeros_like_dev(input);
+        bool fresh = false;
+        TensorPtr gx = add_target(input, &fresh);
         check(soar_sigmoid_backward(go->cuda_data(), output->cuda_data(), gx->cuda_data(),
                                     (size_t)input->numel(), nullptr),
               "sigmoid backward");
-        propagate_grad(input, std::move(gx));
+        if (fresh) propagate_grad(input, std::move(gx));
     }
     void release_variables() override { input = output = nullptr; }
 };
@@ -73,11 +72,12 @@ struct PixelShuffleNode : autograd::AutogradNode {
         if (!wants(input)) return;
         to_dev(go);
         const Planes p = planes_of(input, "PixelShuffle");
-        TensorPtr gx = zeros_like_dev(input);
+        bool fresh = false;
+        TensorPtr gx = add_target(input, &fresh);
         check(soar_pixel_shuffle_backward(go->cuda_data(), gx->cuda_data(), (size_t)p.rows,
                                           (size_t)p.H, (size_t)p.W, (size_t)r, nullptr),
               "pixel shuffle backward");
-        propagate_grad(input, std::move(gx));
+        if (fresh) propagate_grad(input, std::move(gx));
     }
     void release_variables() override { input = nullptr; }
 };
@@ -93,12 +93,13 @@ struct UpsampleNode : autograd::AutogradNode {
         if (!wants(input)) return;
         to_dev(go);
         const Planes p = planes_of(input, "Upsample");
-        TensorPtr gx = zeros_like_dev(input);
+        bool fresh = false;
+        TensorPtr gx = add_target(input, &fresh);
         check(soar_upsample_bilinear_backward(go->cuda_data(), gx->cuda_data(), (size_t)p.rows,
                                               (size_t)p.H, (size_t)p.W, (size_t)H_out,
                                               (size_t)W_out, nullptr),
               "upsample backward");
-        propagate_grad(input, std::move(gx));
+        if (fresh) propagate_grad(input, std::move(gx));
     }
     void release_variables() override { input = nullptr; }
 };
@@ -113,11 +114,12 @@ struct AvgPoolNode : autograd::AutogradNode {
         if (!wants(input)) return;
         to_dev(go);
         const Planes p = planes_of(input, "AdaptiveAvgPool2d");
-        TensorPtr gx = zeros_like_dev(input);
+        bool fresh = false;
+        TensorPtr gx = add_target(input, &fresh);
         check(soar_global_avg_pool_backward(go->cuda_data(), gx->cuda_data(), (size_t)p.rows,
                                             (size_t)(p.H * p.W), nullptr),
               "average pool backward");
-        propagate_grad(input, std::move(gx));
+        if (fresh) propagate_grad(input, std::move(gx));
     }
     void release_variables() override { input = nullptr; }
 };
@@ -135,15 +137,16 @@ struct MulBroadcastNode : autograd::AutogradNode {
         if (!wa && !wb) return;
         to_dev(go);
         const Planes p = planes_of(a, "mul_tensors");
-        TensorPtr ga = wa ? zeros_like_dev(a) : nullptr;
-        TensorPtr gb = wb ? zeros_like_dev(b) : nullptr;
+        bool fa = false, fb = false;
+        TensorPtr ga = wa ? add_target(a, &fa) : nullptr;
+        TensorPtr gb = wb ? add_target(b, &fb) : nullptr;
         check(soar_mul_broadcast_backward(go->cuda_data(), a->cuda_data(), b->cuda_data(),
                                           ga ? ga->cuda_data() : nullptr,
                                           gb ? gb->cuda_data() : nullptr, (size_t)p.rows,
                                           (size_t)(p.H * p.W), nullptr),
               "mul_broadcast backward");
-        if (ga) propagate_grad(a, std::move(ga));
-        if (gb) propagate_grad(b, std::move(gb));
+        if (ga && fa) propagate_grad(a, std::move(ga));
+        if (gb && fb) propagate_grad(b, std::move(gb));
     }
     void release_variables() override { a = b = nullptr; }
 };
@@ -160,18 +163,19 @@ struct ConvexNode : autograd::AutogradNode {
         const bool wg = wants(g), wa = wants(a), wb = wants(b);
         if (!wg && !wa && !wb) return;
         to_dev(go);
-        TensorPtr gg = wg ? zeros_like_dev(g) : nullptr;
-        TensorPtr ga = wa ? zeros_like_dev(a) : nullptr;
-        TensorPtr gb = wb ? zeros_like_dev(b) : nullptr;
+        bool fg = false, fa = false, fb = false;
+        TensorPtr gg = wg ? add_target(g, &fg) : nullptr;
+        TensorPtr ga = wa ? add_target(a, &fa) : nullptr;
+        TensorPtr gb = wb ? add_target(b, &fb) : nullptr;
         check(soar_convex_combination_backward(
                   go->cuda_data(), g->cuda_data(), a->cuda_data(), b->cuda_data(),
                   gg ? gg->cuda_data() : nullptr, ga ? ga->cuda_data() : nullptr,
                   gb ? gb->cuda_data() : nullptr, (size_t)a->numel(), nullptr),
               "convex combination backward");
         // the reference's order (blocks.cpp:258-262): a, b, then g
-        if (ga) propagate_grad(a, std::move(ga));
-        if (gb) propagate_grad(b, std::move(gb));
-        if (gg) propagate_grad(g, std::move(gg));
+        if (ga && fa) propagate_grad(a, std::move(ga));
+        if (gb && fb) propagate_grad(b, std::move(gb));
+        if (gg && fg) propagate_grad(g, std::move(gg));
     }
     void release_variables() override { g = a = b = nullptr; }
 };

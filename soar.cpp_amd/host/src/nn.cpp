@@ -97,6 +97,23 @@ void* workspace(size_t bytes) {
 const float* dptr(const TensorPtr& t) { return t ? t->cuda_data() : nullptr; }
 
 // Backward node of GroupNorm and of the fused GN(+SiLU)(+residual) layer.
+// Input-gradient buffer for a kernel that writes dx, or adds it with
+// SOAR_GN_ACCUMULATE_DX: the input's pending gradient when a kernel may add
+// into it (*fresh = false, no merge pass later), else a new uninitialised
+// tensor that the kernel overwrites and the caller propagates.
+TensorPtr write_target(const TensorPtr& x, bool* fresh) {
+    if (TensorPtr s = grad_sink(x)) {
+        *fresh = false;
+        return s;
+    }
+    *fresh = true;
+    return Tensor::create(x->shape(), false, true);
+}
+
+unsigned dx_mode(const TensorPtr& gx, bool fresh) {
+    return gx && !fresh ? SOAR_GN_ACCUMULATE_DX : 0u;
+}
+
 struct GroupNormNode : autograd::AutogradNode {
     TensorPtr input, weight, bias, mean, rstd, mean_lo;
     int64_t num_groups = 1;
@@ -115,7 +132,8 @@ struct GroupNormNode : autograd::AutogradNode {
         const bool want_p = weight && weight->requires_grad();
         if (!want_x && !want_p) return;
         if (!go->is_cuda()) go->to_cuda();
-        TensorPtr gx = want_x ? Tensor::create(input->shape(), false, true) : nullptr;
+        bool fresh = false;
+        TensorPtr gx = want_x ? write_target(input, &fresh) : nullptr;
         TensorPtr gw, gb;
         bool direct = false;
         if (want_p) {
@@ -136,13 +154,13 @@ struct GroupNormNode : autograd::AutogradNode {
                                     gx ? gx->cuda_data() : nullptr,
                                     gw ? gw->cuda_data() : nullptr,
                                     gb ? gb->cuda_data() : nullptr, s.N, s.C, s.HW, num_groups,
-                                    flags, workspace(wsb), wsb, nullptr),
+                                    flags | dx_mode(gx, fresh), workspace(wsb), wsb, nullptr),
               "GroupNorm backward");
         if (want_p && !direct) {
             propagate_grad(weight, std::move(gw));
             propagate_grad(bias, std::move(gb));
         }
-        if (want_x) propagate_grad(input, std::move(gx));
+        if (want_x && fresh) propagate_grad(input, std::move(gx));
     }
 
     void release_variables() override {
@@ -223,7 +241,9 @@ struct Conv2dNode : autograd::AutogradNode {
         const bool want_b = bias && bias->requires_grad();
         if (!want_x && !want_w && !want_b) return;
         if (!go->is_cuda()) go->to_cuda();
-        TensorPtr gx = want_x ? Tensor::create(input->shape(), false, true) : nullptr;
+        bool fresh = false;
+        TensorPtr gx = want_x ? write_target(input, &fresh) : nullptr;
+        const unsigned fl = dx_mode(gx, fresh);
         bool dw_direct = false, db_direct = false;
         TensorPtr gw = want_w ? param_grad_target(weight, &dw_direct) : nullptr;
         TensorPtr gb = want_b ? param_grad_target(bias, &db_direct) : nullptr;
@@ -234,7 +254,7 @@ struct Conv2dNode : autograd::AutogradNode {
             const size_t wsb =
                 soar_pw_conv_backward_workspace_bytes(g.N, g.C_in, g.C_out, g.H * g.W);
             check(soar_pw_conv_backward(go->cuda_data(), input->cuda_data(), weight->cuda_data(),
-                                        px, pw, pb, g.N, g.C_in, g.C_out, g.H * g.W, 0u,
+                                        px, pw, pb, g.N, g.C_in, g.C_out, g.H * g.W, fl,
                                         workspace(wsb), wsb, nullptr),
                   "pointwise convolution backward");
         } else if (kind == ConvKind::General) {
@@ -242,20 +262,20 @@ struct Conv2dNode : autograd::AutogradNode {
                 g.N, g.C_in, g.C_out, g.H, g.W, g.Ho, g.Wo, K, pad, stride, dil, groups);
             check(soar_conv_backward(go->cuda_data(), input->cuda_data(), weight->cuda_data(), px,
                                      pw, pb, g.N, g.C_in, g.C_out, g.H, g.W, g.Ho, g.Wo, K, pad,
-                                     stride, dil, groups, 0u, workspace(wsb), wsb, nullptr),
+                                     stride, dil, groups, fl, workspace(wsb), wsb, nullptr),
                   "convolution backward");
         } else {
             const size_t wsb = soar_dw_conv_backward_workspace_bytes(g.N, g.C_in, g.H, g.W, g.Ho,
                                                                      g.Wo, K, stride, dil);
             check(soar_dw_conv_backward(go->cuda_data(), input->cuda_data(), weight->cuda_data(),
                                         px, pw, pb, g.N, g.C_in, g.H, g.W, g.Ho, g.Wo, K, pad,
-                                        stride, dil, 0u, wsb ? workspace(wsb) : nullptr, wsb,
+                                        stride, dil, fl, wsb ? workspace(wsb) : nullptr, wsb,
                                         nullptr),
                   "depthwise convolution backward");
         }
         if (gb && !db_direct) propagate_grad(bias, std::move(gb));
         if (gw && !dw_direct) propagate_grad(weight, std::move(gw));
-        if (gx) propagate_grad(input, std::move(gx));
+        if (gx && fresh) propagate_grad(input, std::move(gx));
     }
 
     void release_variables() override { input = nullptr; }
@@ -297,21 +317,22 @@ struct CBAPointwiseNode : autograd::AutogradNode {
                                     workspace(gwsb), gwsb, nullptr),
               "CBA GroupNorm backward");
         TensorPtr gx, gw;
-        bool w_direct = false;
+        bool w_direct = false, fresh = false;
         if (dz) {
-            gx = want_x ? Tensor::create(input->shape(), false, true) : nullptr;
+            gx = want_x ? write_target(input, &fresh) : nullptr;
             gw = want_w ? param_grad_target(conv_w, &w_direct) : nullptr;
             const size_t wsb = soar_pw_conv_backward_workspace_bytes(g.N, g.C_in, g.C_out, HW);
             check(soar_pw_conv_backward(dz->cuda_data(), input->cuda_data(), conv_w->cuda_data(),
                                         gx ? gx->cuda_data() : nullptr,
                                         gw ? gw->cuda_data() : nullptr, nullptr, g.N, g.C_in,
-                                        g.C_out, HW, 0u, workspace(wsb), wsb, nullptr),
+                                        g.C_out, HW, dx_mode(gx, fresh), workspace(wsb), wsb,
+                                        nullptr),
                   "CBA convolution backward");
         }
         if (dg && !g_direct) propagate_grad(gamma, std::move(dg));
         if (db && !b_direct) propagate_grad(beta, std::move(db));
         if (gw && !w_direct) propagate_grad(conv_w, std::move(gw));
-        if (gx) propagate_grad(input, std::move(gx));
+        if (gx && fresh) propagate_grad(input, std::move(gx));
     }
 
     void release_variables() override {
@@ -329,10 +350,11 @@ struct SiLUNode : autograd::AutogradNode {
     void backward(const TensorPtr& go) override {
         if (!input->requires_grad()) return;
         if (!go->is_cuda()) go->to_cuda();
-        TensorPtr gx = Tensor::zeros(input->shape(), false, true);
+        bool fresh = false;
+        TensorPtr gx = add_target(input, &fresh);
         hip::kernels::silu_backward(go->cuda_data(), input->cuda_data(), gx->cuda_data(),
                                     (size_t)input->numel());
-        propagate_grad(input, std::move(gx));
+        if (fresh) propagate_grad(input, std::move(gx));
     }
     void release_variables() override { input = nullptr; }
 };

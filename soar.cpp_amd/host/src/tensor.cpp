@@ -151,6 +151,27 @@ void accumulate_into(const TensorPtr& acc, const TensorPtr& inc) {
     }
 }
 
+// a + b into a new tensor, elementwise; both on the device or both on the
+// host.
+TensorPtr sum_of(const TensorPtr& a, const TensorPtr& b) {
+    if (a->numel() != b->numel())
+        throw ShapeError("gradient shape " + to_string(b->shape()) + " does not match " +
+                         to_string(a->shape()));
+    if (a->is_cuda() != b->is_cuda())
+        throw DeviceError("cannot add a host gradient to a device one (or back)");
+    TensorPtr out = Tensor::create(a->shape(), false, a->is_cuda());
+    if (a->is_cuda()) {
+        hip::kernels::add_forward(a->cuda_data(), b->cuda_data(), out->cuda_data(),
+                                  (size_t)a->numel());
+    } else {
+        const float* x = a->data();
+        const float* y = b->data();
+        float* o = out->data();
+        for (int64_t i = 0; i < a->numel(); ++i) o[i] = x[i] + y[i];
+    }
+    return out;
+}
+
 // First arrival of a handed-over tensor: adopt it when nobody else holds
 // it, else copy, so later in-place accumulation never changes a tensor
 // someone else still reads.

@@ -35,6 +35,12 @@ def test_ops_validate_on_the_host(L):
     assert L.soar_pixel_shuffle_forward(None, None, 6, 4, 4, 2, None) == soar_gn.SOAR_EINVAL
     # crop larger than the padded plane
     assert L.soar_unpad_spatial_forward(None, None, 1, 4, 4, 5, 4, None) == soar_gn.SOAR_EINVAL
+    # resize: plane sides must stay below 2^31 (the tap arithmetic is 32-bit)
+    assert L.soar_upsample_bilinear_forward(None, None, 1, 1, 1 << 31, 2, 2,
+                                            None) == soar_gn.SOAR_EINVAL
+    assert b"2^31" in L.soar_last_error()
+    assert L.soar_upsample_bilinear_backward(None, None, 1, 2, 2, 1 << 31, 1,
+                                             None) == soar_gn.SOAR_EINVAL
     # conv workspace is pure host arithmetic: one fp64 partial per (weight
     # tap or bias, position chunk); chunks of 1024..16384 positions, sized
     # for about 2048 blocks over the 16 (co, q) rows: 1024 here

@@ -229,10 +229,20 @@ def test_sigmoid_convex_broadcast_pool(env):
 
 
 @pytest.mark.parametrize("C,H,W,Ho,Wo", [(3, 2, 2, 4, 4), (5, 4, 4, 16, 16), (2, 7, 5, 14, 10),
-                                         (2, 6, 9, 9, 13), (1, 32, 32, 64, 64)])
+                                         (2, 6, 9, 9, 13), (1, 32, 32, 64, 64),
+                                         (2, 16, 12, 5, 7), (2, 3, 3, 24, 24), (2, 3, 2, 40, 37),
+                                         (2, 4, 8, 16, 16), (16, 16, 16, 32, 32), (3, 1, 1, 4, 6),
+                                         (2, 9, 70, 18, 140), (1, 3, 130, 11, 260),
+                                         (2, 20, 100, 7, 33), (1, 5, 66, 20, 264),
+                                         (2, 1, 3, 2, 6), (1, 1, 2, 4, 8), (2, 40, 70, 160, 280)])
 def test_upsample(env, C, H, W, Ho, Wo):
     """Forward and the gathered backward against float64 loops of the
-    reference's index arithmetic (fp32 source coordinates)."""
+    reference's index arithmetic (fp32 source coordinates).  The shapes
+    cover the exact 2x and 4x backward (one-pixel sides included), the
+    tiled backward at other factors up to 2x and up to 4x (one and several
+    64-column tiles, ragged last tiles), the per-pixel backward at 8x and
+    larger (column runs longer than its register window), downsampling
+    (sources no destination reads) and mixed axis factors."""
     gn, torch = env
     L = gn.lib()
     r = np.random.default_rng(H * Ho)
