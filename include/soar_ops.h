@@ -293,6 +293,45 @@ SOAR_API int soar_multi_tensor_fill_device(float* const* tensors,
                                            const int64_t* numel, int n_tensors,
                                            float value, void* stream);
 
+/* ---- backward entry points that may write instead of add -------------- */
+/* Each takes the arguments of the entry point of the same name without
+ * _ex, plus `flags`: SOAR_GN_ACCUMULATE_DX adds into the gradient outputs
+ * (exactly the entry point without _ex), 0 overwrites them, so a caller
+ * making a fresh gradient needs no zeroed buffer (one launch and one
+ * write pass fewer).  Any other flag bit is SOAR_EINVAL.  No counterpart in
+ * the reference (its kernels always add); the host layer's autograd uses
+ * them to write a tensor's first gradient and add the later ones. */
+SOAR_API int soar_sigmoid_backward_ex(const float* grad_y, const float* y,
+                                      float* grad_x, size_t n, unsigned flags,
+                                      void* stream);
+SOAR_API int soar_mul_broadcast_backward_ex(const float* grad_y,
+                                            const float* a, const float* b,
+                                            float* grad_a, float* grad_b,
+                                            size_t C, size_t HW, unsigned flags,
+                                            void* stream);
+SOAR_API int soar_convex_combination_backward_ex(
+    const float* grad_y, const float* g, const float* a, const float* b,
+    float* grad_g, float* grad_a, float* grad_b, size_t n, unsigned flags,
+    void* stream);
+SOAR_API int soar_global_avg_pool_backward_ex(const float* grad_out,
+                                              float* grad_in, size_t C,
+                                              size_t HW, unsigned flags,
+                                              void* stream);
+SOAR_API int soar_upsample_bilinear_backward_ex(const float* grad_out,
+                                                float* grad_in, size_t C,
+                                                size_t H_in, size_t W_in,
+                                                size_t H_out, size_t W_out,
+                                                unsigned flags, void* stream);
+SOAR_API int soar_pixel_shuffle_backward_ex(const float* grad_out,
+                                            float* grad_in, size_t C_in,
+                                            size_t H_in, size_t W_in, size_t r,
+                                            unsigned flags, void* stream);
+SOAR_API int soar_dice_bce_loss_backward_ex(
+    const float* logits, const float* targets, float* grad_logits,
+    float grad_out, float w, float bw, float dw, float pos_weight,
+    float smooth, float inter, float sum_p, float sum_y, size_t n,
+    unsigned flags, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,11 +21,22 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 namespace soar::ops {
 namespace {
 
 constexpr int kThreads = 256;
+
+// Calls f with std::true_type or std::false_type: a runtime flag picks a
+// kernel template instance.
+template <typename F>
+void bsel(bool b, F&& f) {
+    if (b)
+        f(std::true_type{});
+    else
+        f(std::false_type{});
+}
 
 int blocks_for(int64_t n, int64_t per_block = kThreads, int64_t cap = 8192) {
     int64_t b = (n + per_block - 1) / per_block;
@@ -48,6 +59,16 @@ __device__ double block_sum(double v, double* sh) {
 }
 
 __device__ __forceinline__ float sigmoidf_exact(float z) { return 1.0f / (1.0f + expf(-z)); }
+
+// Gradient store of the backward kernels: added (the reference's +=) or
+// written, which saves the caller zeroing a fresh buffer.
+template <bool ACC>
+__device__ __forceinline__ void put(float* p, float v) {
+    if (ACC)
+        *p += v;
+    else
+        *p = v;
+}
 
 // ---------------------------------------------------------------------------
 // General grouped convolution (convolution_kernels.cu conv2d_forward /
@@ -282,13 +303,14 @@ __global__ __launch_bounds__(kThreads) void k_sigmoid_fwd(const float* __restric
 }
 
 // gx += gy * y * (1 - y)   (activation_kernels.cu:173, layers.cpp:826-831)
+template <bool ACC>
 __global__ __launch_bounds__(kThreads) void k_sigmoid_bwd(const float* __restrict__ gy,
                                                           const float* __restrict__ y,
                                                           float* __restrict__ gx, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * kThreads) {
         const float v = y[i];
-        gx[i] += gy[i] * v * (1.0f - v);
+        put<ACC>(gx + i, gy[i] * v * (1.0f - v));
     }
 }
 
@@ -305,6 +327,7 @@ __global__ __launch_bounds__(kThreads) void k_mul_bcast_fwd(const float* __restr
 // ga += gy * b[row]; gb[row] += sum gy*a (one block per row; the
 // reference's per-element atomicAdd, binary_ops_kernels.cu:129, becomes a
 // fixed-order block sum).
+template <bool ACC>
 __global__ __launch_bounds__(kThreads) void k_mul_bcast_bwd(const float* __restrict__ gy,
                                                             const float* __restrict__ a,
                                                             const float* __restrict__ b,
@@ -318,12 +341,12 @@ __global__ __launch_bounds__(kThreads) void k_mul_bcast_bwd(const float* __restr
     double s = 0.0;
     for (int64_t i = threadIdx.x; i < HW; i += kThreads) {
         const float gv = g[i];
-        if (ga) ga[row * HW + i] += gv * bv;
+        if (ga) put<ACC>(ga + row * HW + i, gv * bv);
         if (gb) s += (double)gv * ar[i];
     }
     if (gb) {
         s = block_sum(s, sh);
-        if (threadIdx.x == 0) gb[row] += (float)s;
+        if (threadIdx.x == 0) put<ACC>(gb + row, (float)s);
     }
 }
 
@@ -339,6 +362,7 @@ __global__ __launch_bounds__(kThreads) void k_convex_fwd(const float* __restrict
     }
 }
 
+template <bool ACC>
 __global__ __launch_bounds__(kThreads) void k_convex_bwd(const float* __restrict__ gy,
                                                          const float* __restrict__ g,
                                                          const float* __restrict__ a,
@@ -349,9 +373,9 @@ __global__ __launch_bounds__(kThreads) void k_convex_bwd(const float* __restrict
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * kThreads) {
         const float d = gy[i], gv = g[i];
-        if (ga) ga[i] += d * gv;
-        if (gb) gb[i] += d * (1.0f - gv);
-        if (gg) gg[i] += d * (a[i] - b[i]);
+        if (ga) put<ACC>(ga + i, d * gv);
+        if (gb) put<ACC>(gb + i, d * (1.0f - gv));
+        if (gg) put<ACC>(gg + i, d * (a[i] - b[i]));
     }
 }
 
@@ -369,13 +393,14 @@ __global__ __launch_bounds__(kThreads) void k_avg_pool_fwd(const float* __restri
 }
 
 // gi += go[row] / HW   (pooling_kernels.cu:27-33)
+template <bool ACC>
 __global__ __launch_bounds__(kThreads) void k_avg_pool_bwd(const float* __restrict__ go,
                                                            float* __restrict__ gi, int64_t rows,
                                                            int64_t HW) {
     const int64_t n = rows * HW;
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * kThreads)
-        gi[i] += go[i / HW] / (float)HW;
+        put<ACC>(gi + i, go[i / HW] / (float)HW);
 }
 
 // ---------------------------------------------------------------------------
@@ -497,7 +522,7 @@ __device__ float gather_one(const float* __restrict__ g, int iy, int ix, int H_i
     return acc;
 }
 
-template <int R, typename I>
+template <int R, typename I, bool ACC>
 __global__ __launch_bounds__(kThreads) void k_upsample_bwd(const float* __restrict__ go,
                                                            float* __restrict__ gi, I rows,
                                                            int H_in, int W_in, int H_out,
@@ -508,8 +533,8 @@ __global__ __launch_bounds__(kThreads) void k_upsample_bwd(const float* __restri
         const I t = i / W_in;
         const int iy = (int)(t % H_in);
         const I row = t / H_in;
-        gi[i] += gather_one<R>(go + (int64_t)row * H_out * W_out, iy, ix, H_in, W_in, H_out,
-                               W_out, sh, sw);
+        put<ACC>(gi + i, gather_one<R>(go + (int64_t)row * H_out * W_out, iy, ix, H_in, W_in,
+                                       H_out, W_out, sh, sw));
     }
 }
 
@@ -519,7 +544,7 @@ __global__ __launch_bounds__(kThreads) void k_upsample_bwd(const float* __restri
 // destination for sides up to 299; the sides are capped at 2^22, where the
 // fp32 source coordinates are exact).  Zero-weight candidates are skipped,
 // so the terms and their order are gather_one's and the results identical.
-template <int F, typename I>
+template <int F, typename I, bool ACC>
 __global__ __launch_bounds__(kThreads) void k_upsample_bwd_int(const float* __restrict__ go,
                                                                float* __restrict__ gi, I rows,
                                                                int H_in, int W_in, float sh,
@@ -559,7 +584,7 @@ __global__ __launch_bounds__(kThreads) void k_upsample_bwd_int(const float* __re
                 if (wx[j] != 0.0f) rs += wx[j] * v[j];
             acc += wy * rs;
         }
-        gi[i] += acc;
+        put<ACC>(gi + i, acc);
     }
 }
 
@@ -574,7 +599,7 @@ __global__ __launch_bounds__(kThreads) void k_upsample_bwd_int(const float* __re
 // kernels give identical results.  A window larger than the LDS arrays
 // (not expected for the factors the host routes here) makes that tile
 // gather from global memory instead.
-template <int TY, int WR, int WC, int R>
+template <int TY, int WR, int WC, int R, bool ACC>
 __global__ __launch_bounds__(kThreads) void k_upsample_bwd_tiled(
     const float* __restrict__ go, float* __restrict__ gi, int64_t rows, int H_in, int W_in,
     int H_out, int W_out, float sh, float sw, int tiles_y, int tiles_x) {
@@ -605,8 +630,8 @@ __global__ __launch_bounds__(kThreads) void k_upsample_bwd_tiled(
             for (int rr = r0; rr < TY; rr += kRowStep) {
                 const int iy = iy0 + rr;
                 if (iy <= iy1 && ix <= ix1)
-                    gp[(int64_t)iy * W_in + ix] +=
-                        gather_one<R>(g, iy, ix, H_in, W_in, H_out, W_out, sh, sw);
+                    put<ACC>(gp + (int64_t)iy * W_in + ix,
+                             gather_one<R>(g, iy, ix, H_in, W_in, H_out, W_out, sh, sw));
             }
             continue;
         }
@@ -667,7 +692,7 @@ __global__ __launch_bounds__(kThreads) void k_upsample_bwd_tiled(
             float acc = 0.0f;
             for (int k = 0; k < ny; ++k)
                 acc += tap_weight(src_index(sh, ya + k, H_in), iy) * rsum[ya + k - ylo][c];
-            gp[(int64_t)iy * W_in + ix] += acc;
+            put<ACC>(gp + (int64_t)iy * W_in + ix, acc);
         }
         __syncthreads();  // win and rsum are refilled for the next tile
     }
@@ -679,7 +704,7 @@ __global__ __launch_bounds__(kThreads) void k_upsample_bwd_tiled(
 // gradient to the input element it came from (a permutation, no
 // collisions).
 // ---------------------------------------------------------------------------
-template <bool BWD>
+template <bool BWD, bool ACC>
 __global__ __launch_bounds__(kThreads) void k_pixel_shuffle(const float* __restrict__ src,
                                                             float* __restrict__ dst, int64_t N,
                                                             int64_t C_out, int64_t H_in,
@@ -695,7 +720,7 @@ __global__ __launch_bounds__(kThreads) void k_pixel_shuffle(const float* __restr
         const int64_t cin = t * r * r + (y % r) * r + (x % r);
         const int64_t j = (cin * H_in + y / r) * W_in + x / r;
         if (BWD)
-            dst[j] += src[i];
+            put<ACC>(dst + j, src[i]);
         else
             dst[i] = src[j];
     }
@@ -834,6 +859,7 @@ __global__ __launch_bounds__(kThreads) void k_loss_finish(const double* __restri
 
 // gz += BCE gradient * scale_bce + Dice gradient * scale_dice
 // (loss_kernels.cu:212-252; losses.cpp:497-541)
+template <bool ACC>
 __global__ __launch_bounds__(kThreads) void k_dice_bce_bwd(const float* __restrict__ z,
                                                            const float* __restrict__ y,
                                                            float* __restrict__ gz, int64_t n,
@@ -855,7 +881,7 @@ __global__ __launch_bounds__(kThreads) void k_dice_bce_bwd(const float* __restri
             const float d_dice_dp = (2.0f * yi * denom - numer) / denom_sq;
             g += scale_dice * (-d_dice_dp * dp_dz);
         }
-        gz[i] += g;
+        put<ACC>(gz + i, g);
     }
 }
 
@@ -1086,8 +1112,9 @@ hipError_t launch_sigmoid_forward(const float* x, float* y, int64_t n, hipStream
 }
 
 hipError_t launch_sigmoid_backward(const float* gy, const float* y, float* gx, int64_t n,
-                                   hipStream_t s) {
-    k_sigmoid_bwd<<<blocks_for(n), kThreads, 0, s>>>(gy, y, gx, n);
+                                   bool acc, hipStream_t s) {
+    bsel(acc,
+         [&](auto A) { k_sigmoid_bwd<A()><<<blocks_for(n), kThreads, 0, s>>>(gy, y, gx, n); });
     return hipGetLastError();
 }
 
@@ -1098,9 +1125,11 @@ hipError_t launch_mul_broadcast_forward(const float* a, const float* b, float* y
 }
 
 hipError_t launch_mul_broadcast_backward(const float* gy, const float* a, const float* b,
-                                         float* ga, float* gb, int64_t rows, int64_t HW,
+                                         float* ga, float* gb, int64_t rows, int64_t HW, bool acc,
                                          hipStream_t s) {
-    k_mul_bcast_bwd<<<(unsigned)rows, kThreads, 0, s>>>(gy, a, b, ga, gb, HW);
+    bsel(acc, [&](auto A) {
+        k_mul_bcast_bwd<A()><<<(unsigned)rows, kThreads, 0, s>>>(gy, a, b, ga, gb, HW);
+    });
     return hipGetLastError();
 }
 
@@ -1112,8 +1141,10 @@ hipError_t launch_convex_forward(const float* g, const float* a, const float* b,
 
 hipError_t launch_convex_backward(const float* gy, const float* g, const float* a,
                                   const float* b, float* gg, float* ga, float* gb, int64_t n,
-                                  hipStream_t s) {
-    k_convex_bwd<<<blocks_for(n), kThreads, 0, s>>>(gy, g, a, b, gg, ga, gb, n);
+                                  bool acc, hipStream_t s) {
+    bsel(acc, [&](auto A) {
+        k_convex_bwd<A()><<<blocks_for(n), kThreads, 0, s>>>(gy, g, a, b, gg, ga, gb, n);
+    });
     return hipGetLastError();
 }
 
@@ -1124,8 +1155,10 @@ hipError_t launch_avg_pool_forward(const float* in, float* out, int64_t rows, in
 }
 
 hipError_t launch_avg_pool_backward(const float* go, float* gi, int64_t rows, int64_t HW,
-                                    hipStream_t s) {
-    k_avg_pool_bwd<<<blocks_for(rows * HW), kThreads, 0, s>>>(go, gi, rows, HW);
+                                    bool acc, hipStream_t s) {
+    bsel(acc, [&](auto A) {
+        k_avg_pool_bwd<A()><<<blocks_for(rows * HW), kThreads, 0, s>>>(go, gi, rows, HW);
+    });
     return hipGetLastError();
 }
 
@@ -1147,7 +1180,8 @@ hipError_t launch_upsample_forward(const float* in, float* out, int64_t rows, in
 }
 
 hipError_t launch_upsample_backward(const float* go, float* gi, int64_t rows, int64_t H_in,
-                                    int64_t W_in, int64_t H_out, int64_t W_out, hipStream_t s) {
+                                    int64_t W_in, int64_t H_out, int64_t W_out, bool acc,
+                                    hipStream_t s) {
     if (std::max({H_in, W_in, H_out, W_out}) > INT32_MAX) return hipErrorInvalidValue;
     const float sh = (float)H_in / (float)H_out, sw = (float)W_in / (float)W_out;
     using std::integral_constant;
@@ -1158,9 +1192,11 @@ hipError_t launch_upsample_backward(const float* go, float* gi, int64_t rows, in
         const int64_t tiles_y = (H_in + TY() - 1) / TY(), tiles_x = (W_in + 63) / 64;
         const int64_t nt = rows * tiles_y * tiles_x;
         const unsigned grid = (unsigned)std::min<int64_t>(nt, (int64_t)1 << 20);
-        k_upsample_bwd_tiled<TY(), WR(), WC(), R()><<<grid, kThreads, 0, s>>>(
-            go, gi, rows, (int)H_in, (int)W_in, (int)H_out, (int)W_out, sh, sw, (int)tiles_y,
-            (int)tiles_x);
+        bsel(acc, [&](auto A) {
+            k_upsample_bwd_tiled<TY(), WR(), WC(), R(), A()><<<grid, kThreads, 0, s>>>(
+                go, gi, rows, (int)H_in, (int)W_in, (int)H_out, (int)W_out, sh, sw,
+                (int)tiles_y, (int)tiles_x);
+        });
     };
     const bool i32 = rows * std::max(H_in * W_in, H_out * W_out) <= INT32_MAX;
     const int64_t f = H_out / H_in;
@@ -1169,8 +1205,11 @@ hipError_t launch_upsample_backward(const float* go, float* gi, int64_t rows, in
         const dim3 grid = blocks_for(rows * H_in * W_in);
         auto run = [&](auto F, auto I) {
             using T = decltype(I);
-            k_upsample_bwd_int<F(), T><<<grid, kThreads, 0, s>>>(go, gi, (T)rows, (int)H_in,
-                                                                 (int)W_in, sh, sw);
+            bsel(acc, [&](auto A) {
+                k_upsample_bwd_int<F(), T, A()><<<grid, kThreads, 0, s>>>(go, gi, (T)rows,
+                                                                          (int)H_in, (int)W_in,
+                                                                          sh, sw);
+            });
         };
         auto pick = [&](auto I) {
             if (f == 2)
@@ -1193,9 +1232,10 @@ hipError_t launch_upsample_backward(const float* go, float* gi, int64_t rows, in
         const dim3 grid = blocks_for(rows * H_in * W_in);
         auto run = [&](auto I) {
             using T = decltype(I);
-            k_upsample_bwd<10, T><<<grid, kThreads, 0, s>>>(go, gi, (T)rows, (int)H_in,
-                                                            (int)W_in, (int)H_out, (int)W_out,
-                                                            sh, sw);
+            bsel(acc, [&](auto A) {
+                k_upsample_bwd<10, T, A()><<<grid, kThreads, 0, s>>>(
+                    go, gi, (T)rows, (int)H_in, (int)W_in, (int)H_out, (int)W_out, sh, sw);
+            });
         };
         if (i32)
             run(int{});
@@ -1206,16 +1246,18 @@ hipError_t launch_upsample_backward(const float* go, float* gi, int64_t rows, in
 }
 
 hipError_t launch_pixel_shuffle(const float* in, float* out, int64_t N, int64_t C_in,
-                                int64_t H_in, int64_t W_in, int64_t r, bool backward,
+                                int64_t H_in, int64_t W_in, int64_t r, bool backward, bool acc,
                                 hipStream_t s) {
     const int64_t C_out = C_in / (r * r);
     const int64_t total = N * C_out * H_in * r * W_in * r;
     if (backward)
-        k_pixel_shuffle<true><<<blocks_for(total), kThreads, 0, s>>>(in, out, N, C_out, H_in,
-                                                                      W_in, r);
+        bsel(acc, [&](auto A) {
+            k_pixel_shuffle<true, A()><<<blocks_for(total), kThreads, 0, s>>>(in, out, N, C_out,
+                                                                               H_in, W_in, r);
+        });
     else
-        k_pixel_shuffle<false><<<blocks_for(total), kThreads, 0, s>>>(in, out, N, C_out, H_in,
-                                                                       W_in, r);
+        k_pixel_shuffle<false, false><<<blocks_for(total), kThreads, 0, s>>>(in, out, N, C_out,
+                                                                              H_in, W_in, r);
     return hipGetLastError();
 }
 
@@ -1263,14 +1305,17 @@ hipError_t launch_loss_sums(const float* z, const float* y, int64_t n, float pos
 
 hipError_t launch_dice_bce_backward(const float* z, const float* y, float* gz, int64_t n,
                                     float go, float w, float bw, float dw, float pos_weight,
-                                    float smooth, float inter, float sum_p, float sum_y,
+                                    float smooth, float inter, float sum_p, float sum_y, bool acc,
                                     hipStream_t s) {
     const float scale_bce = bw > 0.0f ? (go * w * bw) / (float)n : 0.0f;
     const float scale_dice = dw > 0.0f ? go * w * dw : 0.0f;
     const float denom = sum_p + sum_y + smooth;
     const float numer = 2.0f * inter + smooth;
-    k_dice_bce_bwd<<<blocks_for(n), kThreads, 0, s>>>(z, y, gz, n, scale_bce, scale_dice,
-                                                       pos_weight, denom, numer);
+    bsel(acc, [&](auto A) {
+        k_dice_bce_bwd<A()><<<blocks_for(n), kThreads, 0, s>>>(z, y, gz, n, scale_bce,
+                                                               scale_dice, pos_weight, denom,
+                                                               numer);
+    });
     return hipGetLastError();
 }
 

@@ -186,9 +186,19 @@ void finish_losses(const double s[4], size_t n, float pos_weight_unused, float s
     *dice = (float)(1.0 * (1.0 - numer / (denom + 1e-7)));
 }
 
+// Flags of the _ex backward entry points: SOAR_GN_ACCUMULATE_DX adds into
+// the gradient outputs, 0 writes them.  *acc receives the choice.
+int grad_flags(unsigned flags, const char* what, bool* acc) {
+    if (flags & ~SOAR_GN_ACCUMULATE_DX)
+        return fail(SOAR_EINVAL, "%s: unsupported flags 0x%x (SOAR_GN_ACCUMULATE_DX only)", what,
+                    flags);
+    *acc = (flags & SOAR_GN_ACCUMULATE_DX) != 0;
+    return SOAR_OK;
+}
+
 int loss_bwd(const float* z, const float* y, float* gz, size_t n, float go, float w, float bw,
              float dw, float pw, float smooth, float inter, float sum_p, float sum_y,
-             void* stream) {
+             void* stream, bool acc = true) {
     if (n == 0) return ok();
     int rc;
     if ((rc = check_count(n))) return rc;
@@ -197,7 +207,8 @@ int loss_bwd(const float* z, const float* y, float* gz, size_t n, float go, floa
         return rc;
     const int tok = soar::gn::prof_begin(S(stream), "dice_bce_bwd");
     hipError_t e = soar::ops::launch_dice_bce_backward(z, y, gz, (int64_t)n, go, w, bw, dw, pw,
-                                                       smooth, inter, sum_p, sum_y, S(stream));
+                                                       smooth, inter, sum_p, sum_y, acc,
+                                                       S(stream));
     soar::gn::prof_end(S(stream), tok);
     return launched(e, "loss backward launch");
 }
@@ -326,15 +337,23 @@ SOAR_API int soar_sigmoid_forward(const float* x, float* y, size_t n, void* stre
                     "sigmoid_forward launch");
 }
 
-SOAR_API int soar_sigmoid_backward(const float* grad_y, const float* y, float* grad_x, size_t n,
-                                   void* stream) {
-    if (n == 0) return ok();
+SOAR_API int soar_sigmoid_backward_ex(const float* grad_y, const float* y, float* grad_x,
+                                      size_t n, unsigned flags, void* stream) {
+    bool acc;
     int rc;
+    if ((rc = grad_flags(flags, "sigmoid_backward", &acc))) return rc;
+    if (n == 0) return ok();
     if ((rc = check_count(n)) || (rc = check_dev(grad_y, n * 4, "grad_y")) ||
         (rc = check_dev(y, n * 4, "y")) || (rc = check_dev(grad_x, n * 4, "grad_x")))
         return rc;
-    return launched(soar::ops::launch_sigmoid_backward(grad_y, y, grad_x, (int64_t)n, S(stream)),
-                    "sigmoid_backward launch");
+    return launched(
+        soar::ops::launch_sigmoid_backward(grad_y, y, grad_x, (int64_t)n, acc, S(stream)),
+        "sigmoid_backward launch");
+}
+
+SOAR_API int soar_sigmoid_backward(const float* grad_y, const float* y, float* grad_x, size_t n,
+                                   void* stream) {
+    return soar_sigmoid_backward_ex(grad_y, y, grad_x, n, SOAR_GN_ACCUMULATE_DX, stream);
 }
 
 SOAR_API int soar_mul_broadcast_forward(const float* a, const float* b, float* y, size_t C,
@@ -351,11 +370,13 @@ SOAR_API int soar_mul_broadcast_forward(const float* a, const float* b, float* y
         "mul_broadcast_forward launch");
 }
 
-SOAR_API int soar_mul_broadcast_backward(const float* grad_y, const float* a, const float* b,
-                                         float* grad_a, float* grad_b, size_t C, size_t HW,
-                                         void* stream) {
+SOAR_API int soar_mul_broadcast_backward_ex(const float* grad_y, const float* a,
+                                            const float* b, float* grad_a, float* grad_b,
+                                            size_t C, size_t HW, unsigned flags, void* stream) {
     int64_t n;
+    bool acc;
     int rc;
+    if ((rc = grad_flags(flags, "mul_broadcast_backward", &acc))) return rc;
     if ((rc = check_planes(C, HW, &n))) return rc;
     if (n == 0 || (!grad_a && !grad_b)) return ok();
     if (C > 0x7fffffffu) return fail(SOAR_EINVAL, "mul_broadcast_backward: C too large");
@@ -365,8 +386,16 @@ SOAR_API int soar_mul_broadcast_backward(const float* grad_y, const float* a, co
         (rc = check_dev_opt(grad_b, C * 4, "grad_b")))
         return rc;
     return launched(soar::ops::launch_mul_broadcast_backward(grad_y, a, b, grad_a, grad_b,
-                                                             (int64_t)C, (int64_t)HW, S(stream)),
+                                                             (int64_t)C, (int64_t)HW, acc,
+                                                             S(stream)),
                     "mul_broadcast_backward launch");
+}
+
+SOAR_API int soar_mul_broadcast_backward(const float* grad_y, const float* a, const float* b,
+                                         float* grad_a, float* grad_b, size_t C, size_t HW,
+                                         void* stream) {
+    return soar_mul_broadcast_backward_ex(grad_y, a, b, grad_a, grad_b, C, HW,
+                                          SOAR_GN_ACCUMULATE_DX, stream);
 }
 
 SOAR_API int soar_convex_combination_forward(const float* g, const float* a, const float* b,
@@ -381,12 +410,14 @@ SOAR_API int soar_convex_combination_forward(const float* g, const float* a, con
                     "convex_combination_forward launch");
 }
 
-SOAR_API int soar_convex_combination_backward(const float* grad_y, const float* g,
-                                              const float* a, const float* b, float* grad_g,
-                                              float* grad_a, float* grad_b, size_t n,
-                                              void* stream) {
-    if (n == 0 || (!grad_g && !grad_a && !grad_b)) return ok();
+SOAR_API int soar_convex_combination_backward_ex(const float* grad_y, const float* g,
+                                                 const float* a, const float* b, float* grad_g,
+                                                 float* grad_a, float* grad_b, size_t n,
+                                                 unsigned flags, void* stream) {
+    bool acc;
     int rc;
+    if ((rc = grad_flags(flags, "convex_combination_backward", &acc))) return rc;
+    if (n == 0 || (!grad_g && !grad_a && !grad_b)) return ok();
     if ((rc = check_count(n)) || (rc = check_dev(grad_y, n * 4, "grad_y")) ||
         (rc = check_dev(g, n * 4, "g")) || (rc = check_dev(a, n * 4, "a")) ||
         (rc = check_dev(b, n * 4, "b")) || (rc = check_dev_opt(grad_g, n * 4, "grad_g")) ||
@@ -394,8 +425,16 @@ SOAR_API int soar_convex_combination_backward(const float* grad_y, const float* 
         (rc = check_dev_opt(grad_b, n * 4, "grad_b")))
         return rc;
     return launched(soar::ops::launch_convex_backward(grad_y, g, a, b, grad_g, grad_a, grad_b,
-                                                      (int64_t)n, S(stream)),
+                                                      (int64_t)n, acc, S(stream)),
                     "convex_combination_backward launch");
+}
+
+SOAR_API int soar_convex_combination_backward(const float* grad_y, const float* g,
+                                              const float* a, const float* b, float* grad_g,
+                                              float* grad_a, float* grad_b, size_t n,
+                                              void* stream) {
+    return soar_convex_combination_backward_ex(grad_y, g, a, b, grad_g, grad_a, grad_b, n,
+                                               SOAR_GN_ACCUMULATE_DX, stream);
 }
 
 SOAR_API int soar_global_avg_pool_forward(const float* in, float* out, size_t C, size_t HW,
@@ -414,18 +453,26 @@ SOAR_API int soar_global_avg_pool_forward(const float* in, float* out, size_t C,
         "global_avg_pool_forward launch");
 }
 
-SOAR_API int soar_global_avg_pool_backward(const float* grad_out, float* grad_in, size_t C,
-                                           size_t HW, void* stream) {
+SOAR_API int soar_global_avg_pool_backward_ex(const float* grad_out, float* grad_in, size_t C,
+                                              size_t HW, unsigned flags, void* stream) {
     int64_t n;
+    bool acc;
     int rc;
+    if ((rc = grad_flags(flags, "global_avg_pool_backward", &acc))) return rc;
     if ((rc = check_planes(C, HW, &n))) return rc;
     if (n == 0) return ok();
     if ((rc = require_device()) || (rc = check_dev(grad_out, C * 4, "grad_out")) ||
         (rc = check_dev(grad_in, n * 4, "grad_in")))
         return rc;
-    return launched(
-        soar::ops::launch_avg_pool_backward(grad_out, grad_in, (int64_t)C, (int64_t)HW, S(stream)),
-        "global_avg_pool_backward launch");
+    return launched(soar::ops::launch_avg_pool_backward(grad_out, grad_in, (int64_t)C,
+                                                        (int64_t)HW, acc, S(stream)),
+                    "global_avg_pool_backward launch");
+}
+
+SOAR_API int soar_global_avg_pool_backward(const float* grad_out, float* grad_in, size_t C,
+                                           size_t HW, void* stream) {
+    return soar_global_avg_pool_backward_ex(grad_out, grad_in, C, HW, SOAR_GN_ACCUMULATE_DX,
+                                            stream);
 }
 
 SOAR_API int soar_upsample_bilinear_forward(const float* in, float* out, size_t C, size_t H_in,
@@ -449,18 +496,29 @@ SOAR_API int soar_upsample_bilinear_2x_forward(const float* in, float* out, size
     return soar_upsample_bilinear_forward(in, out, C, H_in, W_in, 2 * H_in, 2 * W_in, stream);
 }
 
-SOAR_API int soar_upsample_bilinear_backward(const float* grad_out, float* grad_in, size_t C,
-                                             size_t H_in, size_t W_in, size_t H_out,
-                                             size_t W_out, void* stream) {
-    if (C == 0) return ok();
+SOAR_API int soar_upsample_bilinear_backward_ex(const float* grad_out, float* grad_in,
+                                                size_t C, size_t H_in, size_t W_in,
+                                                size_t H_out, size_t W_out, unsigned flags,
+                                                void* stream) {
+    bool acc;
     int rc;
+    if ((rc = grad_flags(flags, "upsample_bilinear_backward", &acc))) return rc;
+    if (C == 0) return ok();
     if ((rc = resize_check(grad_out, grad_in, C, H_in, W_in, H_out, W_out, true))) return rc;
     const int tok = soar::gn::prof_begin(S(stream), "upsample_bwd");
     hipError_t e = soar::ops::launch_upsample_backward(grad_out, grad_in, (int64_t)C,
                                                        (int64_t)H_in, (int64_t)W_in,
-                                                       (int64_t)H_out, (int64_t)W_out, S(stream));
+                                                       (int64_t)H_out, (int64_t)W_out, acc,
+                                                       S(stream));
     soar::gn::prof_end(S(stream), tok);
     return launched(e, "upsample_bilinear_backward launch");
+}
+
+SOAR_API int soar_upsample_bilinear_backward(const float* grad_out, float* grad_in, size_t C,
+                                             size_t H_in, size_t W_in, size_t H_out,
+                                             size_t W_out, void* stream) {
+    return soar_upsample_bilinear_backward_ex(grad_out, grad_in, C, H_in, W_in, H_out, W_out,
+                                              SOAR_GN_ACCUMULATE_DX, stream);
 }
 
 SOAR_API int soar_upsample_bilinear_2x_backward(const float* grad_out, float* grad_in, size_t C,
@@ -472,7 +530,7 @@ SOAR_API int soar_upsample_bilinear_2x_backward(const float* grad_out, float* gr
 }
 
 static int pixel_shuffle(const float* src, float* dst, size_t C_in, size_t H_in, size_t W_in,
-                         size_t r, bool backward, void* stream) {
+                         size_t r, bool backward, bool acc, void* stream) {
     int64_t n;
     if (r == 0 || !fits_i64({C_in, H_in, W_in, r}) ||
         !mul_ok({(int64_t)C_in, (int64_t)H_in, (int64_t)W_in}, &n))
@@ -486,19 +544,29 @@ static int pixel_shuffle(const float* src, float* dst, size_t C_in, size_t H_in,
         (rc = check_dev(dst, n * 4, backward ? "grad_in" : "out")))
         return rc;
     return launched(soar::ops::launch_pixel_shuffle(src, dst, 1, (int64_t)C_in, (int64_t)H_in,
-                                                    (int64_t)W_in, (int64_t)r, backward,
+                                                    (int64_t)W_in, (int64_t)r, backward, acc,
                                                     S(stream)),
                     "pixel_shuffle launch");
 }
 
 SOAR_API int soar_pixel_shuffle_forward(const float* in, float* out, size_t C_in, size_t H_in,
                                         size_t W_in, size_t r, void* stream) {
-    return pixel_shuffle(in, out, C_in, H_in, W_in, r, false, stream);
+    return pixel_shuffle(in, out, C_in, H_in, W_in, r, false, false, stream);
+}
+
+SOAR_API int soar_pixel_shuffle_backward_ex(const float* grad_out, float* grad_in, size_t C_in,
+                                            size_t H_in, size_t W_in, size_t r, unsigned flags,
+                                            void* stream) {
+    bool acc;
+    int rc;
+    if ((rc = grad_flags(flags, "pixel_shuffle_backward", &acc))) return rc;
+    return pixel_shuffle(grad_out, grad_in, C_in, H_in, W_in, r, true, acc, stream);
 }
 
 SOAR_API int soar_pixel_shuffle_backward(const float* grad_out, float* grad_in, size_t C_in,
                                          size_t H_in, size_t W_in, size_t r, void* stream) {
-    return pixel_shuffle(grad_out, grad_in, C_in, H_in, W_in, r, true, stream);
+    return soar_pixel_shuffle_backward_ex(grad_out, grad_in, C_in, H_in, W_in, r,
+                                          SOAR_GN_ACCUMULATE_DX, stream);
 }
 
 static int pad_op(const float* src, float* dst, size_t C, size_t H, size_t W, size_t ph,
@@ -639,12 +707,25 @@ SOAR_API int soar_dice_bce_loss_forward(const float* logits, const float* target
     return ok();
 }
 
+SOAR_API int soar_dice_bce_loss_backward_ex(const float* logits, const float* targets,
+                                            float* grad_logits, float grad_out, float w, float bw,
+                                            float dw, float pos_weight, float smooth, float inter,
+                                            float sum_p, float sum_y, size_t n, unsigned flags,
+                                            void* stream) {
+    bool acc;
+    int rc;
+    if ((rc = grad_flags(flags, "dice_bce_loss_backward", &acc))) return rc;
+    return loss_bwd(logits, targets, grad_logits, n, grad_out, w, bw, dw, pos_weight, smooth,
+                    inter, sum_p, sum_y, stream, acc);
+}
+
 SOAR_API int soar_dice_bce_loss_backward(const float* logits, const float* targets,
                                          float* grad_logits, float grad_out, float w, float bw,
                                          float dw, float pos_weight, float smooth, float inter,
                                          float sum_p, float sum_y, size_t n, void* stream) {
-    return loss_bwd(logits, targets, grad_logits, n, grad_out, w, bw, dw, pos_weight, smooth,
-                    inter, sum_p, sum_y, stream);
+    return soar_dice_bce_loss_backward_ex(logits, targets, grad_logits, grad_out, w, bw, dw,
+                                          pos_weight, smooth, inter, sum_p, sum_y, n,
+                                          SOAR_GN_ACCUMULATE_DX, stream);
 }
 
 SOAR_API int soar_sigmoid_threshold(const float* logits, float* probs, uint8_t* mask, size_t n,

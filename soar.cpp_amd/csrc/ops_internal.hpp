@@ -33,33 +33,36 @@ hipError_t launch_conv_backward(const float* go, const float* in, const float* w
                                 void* ws, hipStream_t s);
 
 hipError_t launch_sigmoid_forward(const float* x, float* y, int64_t n, hipStream_t s);
+// The backward launchers below add into their gradient outputs when `acc`,
+// else overwrite them.
 hipError_t launch_sigmoid_backward(const float* gy, const float* y, float* gx, int64_t n,
-                                   hipStream_t s);
+                                   bool acc, hipStream_t s);
 
 hipError_t launch_mul_broadcast_forward(const float* a, const float* b, float* y, int64_t rows,
                                         int64_t HW, hipStream_t s);
 hipError_t launch_mul_broadcast_backward(const float* gy, const float* a, const float* b,
-                                         float* ga, float* gb, int64_t rows, int64_t HW,
+                                         float* ga, float* gb, int64_t rows, int64_t HW, bool acc,
                                          hipStream_t s);
 
 hipError_t launch_convex_forward(const float* g, const float* a, const float* b, float* y,
                                  int64_t n, hipStream_t s);
 hipError_t launch_convex_backward(const float* gy, const float* g, const float* a,
                                   const float* b, float* gg, float* ga, float* gb, int64_t n,
-                                  hipStream_t s);
+                                  bool acc, hipStream_t s);
 
 hipError_t launch_avg_pool_forward(const float* in, float* out, int64_t rows, int64_t HW,
                                    hipStream_t s);
 hipError_t launch_avg_pool_backward(const float* go, float* gi, int64_t rows, int64_t HW,
-                                    hipStream_t s);
+                                    bool acc, hipStream_t s);
 
 hipError_t launch_upsample_forward(const float* in, float* out, int64_t rows, int64_t H_in,
                                    int64_t W_in, int64_t H_out, int64_t W_out, hipStream_t s);
 hipError_t launch_upsample_backward(const float* go, float* gi, int64_t rows, int64_t H_in,
-                                    int64_t W_in, int64_t H_out, int64_t W_out, hipStream_t s);
+                                    int64_t W_in, int64_t H_out, int64_t W_out, bool acc,
+                                    hipStream_t s);
 
 hipError_t launch_pixel_shuffle(const float* in, float* out, int64_t N, int64_t C_in,
-                                int64_t H_in, int64_t W_in, int64_t r, bool backward,
+                                int64_t H_in, int64_t W_in, int64_t r, bool backward, bool acc,
                                 hipStream_t s);
 
 hipError_t launch_pad_forward(const float* in, float* out, int64_t rows, int64_t H, int64_t W,
@@ -79,7 +82,7 @@ hipError_t launch_loss_sums(const float* z, const float* y, int64_t n, float pos
                             double* out, void* ws, hipStream_t s);
 hipError_t launch_dice_bce_backward(const float* z, const float* y, float* gz, int64_t n,
                                     float go, float w, float bw, float dw, float pos_weight,
-                                    float smooth, float inter, float sum_p, float sum_y,
+                                    float smooth, float inter, float sum_p, float sum_y, bool acc,
                                     hipStream_t s);
 
 // Probabilities and the thresholded mask of a logit map.

@@ -95,4 +95,9 @@ TensorPtr grad_sink(const TensorPtr& tensor);
 // when there is one (*fresh = false), else fresh device zeros
 // (*fresh = true) that the caller hands to propagate_grad.
 TensorPtr add_target(const TensorPtr& tensor, bool* fresh);
+// Gradient buffer for a kernel that can write or add its result:
+// grad_sink(tensor) when there is one (*fresh = false: the kernel adds),
+// else a new uninitialised device tensor (*fresh = true: the kernel
+// writes, and the caller hands the tensor to propagate_grad).
+TensorPtr write_target(const TensorPtr& tensor, bool* fresh);
 }  // namespace soar

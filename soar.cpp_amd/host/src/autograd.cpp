@@ -139,6 +139,15 @@ TensorPtr add_target(const TensorPtr& tensor, bool* fresh) {
     return Tensor::zeros(tensor->shape(), false, true);
 }
 
+TensorPtr write_target(const TensorPtr& tensor, bool* fresh) {
+    if (TensorPtr s = grad_sink(tensor)) {
+        *fresh = false;
+        return s;
+    }
+    *fresh = true;
+    return Tensor::create(tensor->shape(), false, true);
+}
+
 void run_backward(std::shared_ptr<AutogradNode> root, const TensorPtr& root_grad) {
     autograd::Engine::get_default_engine().execute(std::move(root), root_grad);
 }

@@ -38,10 +38,11 @@ struct DiceBCENode : autograd::AutogradNode {
         if (!logits || !logits->requires_grad()) return;
         const float go = grad_output->to_host()[0];
         bool fresh = false;
-        TensorPtr gz = add_target(logits, &fresh);
-        check(soar_dice_bce_loss_backward(logits->cuda_data(), targets->cuda_data(),
-                                          gz->cuda_data(), go, w, bw, dw, pos_weight, smooth,
-                                          inter, sum_p, sum_y, (size_t)logits->numel(), nullptr),
+        TensorPtr gz = write_target(logits, &fresh);
+        check(soar_dice_bce_loss_backward_ex(logits->cuda_data(), targets->cuda_data(),
+                                             gz->cuda_data(), go, w, bw, dw, pos_weight, smooth,
+                                             inter, sum_p, sum_y, (size_t)logits->numel(),
+                                             fresh ? 0u : SOAR_GN_ACCUMULATE_DX, nullptr),
               "Dice+BCE backward");
         if (fresh) propagate_grad(logits, std::move(gz));
     }

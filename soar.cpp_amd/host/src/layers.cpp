@@ -41,6 +41,22 @@ void to_dev(const TensorPtr& t) {
 
 bool wants(const TensorPtr& t) { return t && t->requires_grad(); }
 
+// Flags of the _ex backward entry points: add into a pending gradient,
+// write a fresh one.
+unsigned mode(bool fresh) { return fresh ? 0u : SOAR_GN_ACCUMULATE_DX; }
+
+// One mode for a kernel with several gradient outputs (null ones ignored):
+// write when every output is fresh, else zero the fresh ones and add.
+unsigned joint_mode(std::initializer_list<std::pair<const TensorPtr*, bool>> outs) {
+    bool all_fresh = true;
+    for (const auto& [t, fresh] : outs)
+        if (*t && !fresh) all_fresh = false;
+    if (all_fresh) return 0u;
+    for (const auto& [t, fresh] : outs)
+        if (*t && fresh) (*t)->zero_();
+    return SOAR_GN_ACCUMULATE_DX;
+}
+
 // ---- nodes ------------------------------------------------------------------
 struct SigmoidNode : autograd::AutogradNode {
     TensorPtr input, output;
@@ -52,9 +68,9 @@ struct SigmoidNode : autograd::AutogradNode {
         if (!wants(input)) return;
         to_dev(go);
         bool fresh = false;
-        TensorPtr gx = add_target(input, &fresh);
-        check(soar_sigmoid_backward(go->cuda_data(), output->cuda_data(), gx->cuda_data(),
-                                    (size_t)input->numel(), nullptr),
+        TensorPtr gx = write_target(input, &fresh);
+        check(soar_sigmoid_backward_ex(go->cuda_data(), output->cuda_data(), gx->cuda_data(),
+                                       (size_t)input->numel(), mode(fresh), nullptr),
               "sigmoid backward");
         if (fresh) propagate_grad(input, std::move(gx));
     }
@@ -73,9 +89,10 @@ struct PixelShuffleNode : autograd::AutogradNode {
         to_dev(go);
         const Planes p = planes_of(input, "PixelShuffle");
         bool fresh = false;
-        TensorPtr gx = add_target(input, &fresh);
-        check(soar_pixel_shuffle_backward(go->cuda_data(), gx->cuda_data(), (size_t)p.rows,
-                                          (size_t)p.H, (size_t)p.W, (size_t)r, nullptr),
+        TensorPtr gx = write_target(input, &fresh);
+        check(soar_pixel_shuffle_backward_ex(go->cuda_data(), gx->cuda_data(), (size_t)p.rows,
+                                             (size_t)p.H, (size_t)p.W, (size_t)r, mode(fresh),
+                                             nullptr),
               "pixel shuffle backward");
         if (fresh) propagate_grad(input, std::move(gx));
     }
@@ -94,10 +111,11 @@ struct UpsampleNode : autograd::AutogradNode {
         to_dev(go);
         const Planes p = planes_of(input, "Upsample");
         bool fresh = false;
-        TensorPtr gx = add_target(input, &fresh);
-        check(soar_upsample_bilinear_backward(go->cuda_data(), gx->cuda_data(), (size_t)p.rows,
-                                              (size_t)p.H, (size_t)p.W, (size_t)H_out,
-                                              (size_t)W_out, nullptr),
+        TensorPtr gx = write_target(input, &fresh);
+        check(soar_upsample_bilinear_backward_ex(go->cuda_data(), gx->cuda_data(),
+                                                 (size_t)p.rows, (size_t)p.H, (size_t)p.W,
+                                                 (size_t)H_out, (size_t)W_out, mode(fresh),
+                                                 nullptr),
               "upsample backward");
         if (fresh) propagate_grad(input, std::move(gx));
     }
@@ -115,9 +133,10 @@ struct AvgPoolNode : autograd::AutogradNode {
         to_dev(go);
         const Planes p = planes_of(input, "AdaptiveAvgPool2d");
         bool fresh = false;
-        TensorPtr gx = add_target(input, &fresh);
-        check(soar_global_avg_pool_backward(go->cuda_data(), gx->cuda_data(), (size_t)p.rows,
-                                            (size_t)(p.H * p.W), nullptr),
+        TensorPtr gx = write_target(input, &fresh);
+        check(soar_global_avg_pool_backward_ex(go->cuda_data(), gx->cuda_data(),
+                                               (size_t)p.rows, (size_t)(p.H * p.W), mode(fresh),
+                                               nullptr),
               "average pool backward");
         if (fresh) propagate_grad(input, std::move(gx));
     }
@@ -138,12 +157,13 @@ struct MulBroadcastNode : autograd::AutogradNode {
         to_dev(go);
         const Planes p = planes_of(a, "mul_tensors");
         bool fa = false, fb = false;
-        TensorPtr ga = wa ? add_target(a, &fa) : nullptr;
-        TensorPtr gb = wb ? add_target(b, &fb) : nullptr;
-        check(soar_mul_broadcast_backward(go->cuda_data(), a->cuda_data(), b->cuda_data(),
-                                          ga ? ga->cuda_data() : nullptr,
-                                          gb ? gb->cuda_data() : nullptr, (size_t)p.rows,
-                                          (size_t)(p.H * p.W), nullptr),
+        TensorPtr ga = wa ? write_target(a, &fa) : nullptr;
+        TensorPtr gb = wb ? write_target(b, &fb) : nullptr;
+        const unsigned fl = joint_mode({{&ga, fa}, {&gb, fb}});
+        check(soar_mul_broadcast_backward_ex(go->cuda_data(), a->cuda_data(), b->cuda_data(),
+                                             ga ? ga->cuda_data() : nullptr,
+                                             gb ? gb->cuda_data() : nullptr, (size_t)p.rows,
+                                             (size_t)(p.H * p.W), fl, nullptr),
               "mul_broadcast backward");
         if (ga && fa) propagate_grad(a, std::move(ga));
         if (gb && fb) propagate_grad(b, std::move(gb));
@@ -164,13 +184,14 @@ struct ConvexNode : autograd::AutogradNode {
         if (!wg && !wa && !wb) return;
         to_dev(go);
         bool fg = false, fa = false, fb = false;
-        TensorPtr gg = wg ? add_target(g, &fg) : nullptr;
-        TensorPtr ga = wa ? add_target(a, &fa) : nullptr;
-        TensorPtr gb = wb ? add_target(b, &fb) : nullptr;
-        check(soar_convex_combination_backward(
+        TensorPtr gg = wg ? write_target(g, &fg) : nullptr;
+        TensorPtr ga = wa ? write_target(a, &fa) : nullptr;
+        TensorPtr gb = wb ? write_target(b, &fb) : nullptr;
+        const unsigned fl = joint_mode({{&gg, fg}, {&ga, fa}, {&gb, fb}});
+        check(soar_convex_combination_backward_ex(
                   go->cuda_data(), g->cuda_data(), a->cuda_data(), b->cuda_data(),
                   gg ? gg->cuda_data() : nullptr, ga ? ga->cuda_data() : nullptr,
-                  gb ? gb->cuda_data() : nullptr, (size_t)a->numel(), nullptr),
+                  gb ? gb->cuda_data() : nullptr, (size_t)a->numel(), fl, nullptr),
               "convex combination backward");
         // the reference's order (blocks.cpp:258-262): a, b, then g
         if (ga && fa) propagate_grad(a, std::move(ga));

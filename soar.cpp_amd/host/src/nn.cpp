@@ -97,19 +97,8 @@ void* workspace(size_t bytes) {
 const float* dptr(const TensorPtr& t) { return t ? t->cuda_data() : nullptr; }
 
 // Backward node of GroupNorm and of the fused GN(+SiLU)(+residual) layer.
-// Input-gradient buffer for a kernel that writes dx, or adds it with
-// SOAR_GN_ACCUMULATE_DX: the input's pending gradient when a kernel may add
-// into it (*fresh = false, no merge pass later), else a new uninitialised
-// tensor that the kernel overwrites and the caller propagates.
-TensorPtr write_target(const TensorPtr& x, bool* fresh) {
-    if (TensorPtr s = grad_sink(x)) {
-        *fresh = false;
-        return s;
-    }
-    *fresh = true;
-    return Tensor::create(x->shape(), false, true);
-}
-
+// SOAR_GN_ACCUMULATE_DX when the kernel adds into a pending gradient (see
+// write_target), 0 when it writes a fresh one.
 unsigned dx_mode(const TensorPtr& gx, bool fresh) {
     return gx && !fresh ? SOAR_GN_ACCUMULATE_DX : 0u;
 }

@@ -157,6 +157,14 @@ SIGNATURES = {
     "soar_multi_tensor_norm_sq_device": (_c.c_int, [_P, _P, _c.c_int, _P, _P, _SZ, _P]),
     "soar_multi_tensor_scale_device": (_c.c_int, [_P, _P, _c.c_int, _c.c_float, _P]),
     "soar_multi_tensor_fill_device": (_c.c_int, [_P, _P, _c.c_int, _c.c_float, _P]),
+    "soar_sigmoid_backward_ex": (_c.c_int, [_P, _P, _P, _SZ, _c.c_uint, _P]),
+    "soar_mul_broadcast_backward_ex": (_c.c_int, [_P, _P, _P, _P, _P, _SZ, _SZ, _c.c_uint, _P]),
+    "soar_convex_combination_backward_ex": (_c.c_int, [_P] * 7 + [_SZ, _c.c_uint, _P]),
+    "soar_global_avg_pool_backward_ex": (_c.c_int, [_P, _P, _SZ, _SZ, _c.c_uint, _P]),
+    "soar_upsample_bilinear_backward_ex": (_c.c_int, [_P, _P] + [_SZ] * 5 + [_c.c_uint, _P]),
+    "soar_pixel_shuffle_backward_ex": (_c.c_int, [_P, _P] + [_SZ] * 4 + [_c.c_uint, _P]),
+    "soar_dice_bce_loss_backward_ex": (_c.c_int, [_P, _P, _P] + [_c.c_float] * 9 +
+                                       [_SZ, _c.c_uint, _P]),
 }
 
 SYNTH_SIGNATURES = {

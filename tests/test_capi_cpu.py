@@ -35,6 +35,11 @@ def test_ops_validate_on_the_host(L):
     assert L.soar_pixel_shuffle_forward(None, None, 6, 4, 4, 2, None) == soar_gn.SOAR_EINVAL
     # crop larger than the padded plane
     assert L.soar_unpad_spatial_forward(None, None, 1, 4, 4, 5, 4, None) == soar_gn.SOAR_EINVAL
+    # the _ex backward entry points know one flag (add instead of write)
+    assert L.soar_sigmoid_backward_ex(None, None, None, 4, 1, None) == soar_gn.SOAR_EINVAL
+    assert b"unsupported flags" in L.soar_last_error()
+    assert L.soar_convex_combination_backward_ex(None, None, None, None, None, None, None, 4,
+                                                 8, None) == soar_gn.SOAR_EINVAL
     # resize: plane sides must stay below 2^31 (the tap arithmetic is 32-bit)
     assert L.soar_upsample_bilinear_forward(None, None, 1, 1, 1 << 31, 2, 2,
                                             None) == soar_gn.SOAR_EINVAL

@@ -360,6 +360,83 @@ def test_losses(env):
     np.testing.assert_array_equal(host(torch, m), (z >= 0).astype(np.uint8))
 
 
+# ---- write-mode backward entry points ----------------------------------------------
+def test_backward_write_mode(env):
+    """Every _ex backward with flags 0 overwrites its outputs (prefilled
+    with NaN here) with exactly what the adding entry point adds to zeros,
+    and with SOAR_GN_ACCUMULATE_DX equals the adding entry point."""
+    gn, torch = env
+    L = gn.lib()
+    r = np.random.default_rng(11)
+    ACC = gn.GN_ACCUMULATE_DX
+    C, H, W = 6, 10, 12
+    n = C * H * W
+    gy = dev(torch, r.normal(size=n))
+    a = dev(torch, r.normal(size=n))
+    b = dev(torch, r.normal(size=n))
+    g = dev(torch, r.uniform(size=n))
+    bc = dev(torch, r.normal(size=C))
+    y01 = dev(torch, (r.uniform(size=n) < 0.4).astype(F32))
+    go_up = dev(torch, r.normal(size=C * (2 * H) * (2 * W)))
+    go_pool = dev(torch, r.normal(size=C))
+    cases = {
+        "sigmoid": ([n], lambda o, f: L.soar_sigmoid_backward_ex(P(gy), P(g), P(o[0]), n, f,
+                                                                  None),
+                    lambda o: L.soar_sigmoid_backward(P(gy), P(g), P(o[0]), n, None)),
+        "mul_broadcast": ([n, C],
+                          lambda o, f: L.soar_mul_broadcast_backward_ex(
+                              P(gy), P(a), P(bc), P(o[0]), P(o[1]), C, H * W, f, None),
+                          lambda o: L.soar_mul_broadcast_backward(
+                              P(gy), P(a), P(bc), P(o[0]), P(o[1]), C, H * W, None)),
+        "convex": ([n, n, n],
+                   lambda o, f: L.soar_convex_combination_backward_ex(
+                       P(gy), P(g), P(a), P(b), P(o[0]), P(o[1]), P(o[2]), n, f, None),
+                   lambda o: L.soar_convex_combination_backward(
+                       P(gy), P(g), P(a), P(b), P(o[0]), P(o[1]), P(o[2]), n, None)),
+        "avg_pool": ([n], lambda o, f: L.soar_global_avg_pool_backward_ex(
+                         P(go_pool), P(o[0]), C, H * W, f, None),
+                     lambda o: L.soar_global_avg_pool_backward(P(go_pool), P(o[0]), C, H * W,
+                                                               None)),
+        "upsample_2x": ([n], lambda o, f: L.soar_upsample_bilinear_backward_ex(
+                            P(go_up), P(o[0]), C, H, W, 2 * H, 2 * W, f, None),
+                        lambda o: L.soar_upsample_bilinear_backward(
+                            P(go_up), P(o[0]), C, H, W, 2 * H, 2 * W, None)),
+        "upsample_tiled": ([n], lambda o, f: L.soar_upsample_bilinear_backward_ex(
+                               P(go_up), P(o[0]), C, H, W, 2 * H - 1, 2 * W - 3, f, None),
+                           lambda o: L.soar_upsample_bilinear_backward(
+                               P(go_up), P(o[0]), C, H, W, 2 * H - 1, 2 * W - 3, None)),
+        "upsample_wide": ([C * 2 * 2], lambda o, f: L.soar_upsample_bilinear_backward_ex(
+                              P(go_up), P(o[0]), C, 2, 2, 2 * H, 2 * W, f, None),
+                          lambda o: L.soar_upsample_bilinear_backward(
+                              P(go_up), P(o[0]), C, 2, 2, 2 * H, 2 * W, None)),
+        # 24 channels of 5 x 6 <-> 6 channels of 10 x 12
+        "pixel_shuffle": ([n], lambda o, f: L.soar_pixel_shuffle_backward_ex(
+                              P(gy), P(o[0]), 24, H // 2, W // 2, 2, f, None),
+                          lambda o: L.soar_pixel_shuffle_backward(P(gy), P(o[0]), 24, H // 2,
+                                                                  W // 2, 2, None)),
+        "dice_bce": ([n], lambda o, f: L.soar_dice_bce_loss_backward_ex(
+                         P(a), P(y01), P(o[0]), 1.0, 1.0, 0.5, 0.5, 3.0, 1.0, 30.0, 200.0,
+                         250.0, n, f, None),
+                     lambda o: L.soar_dice_bce_loss_backward(
+                         P(a), P(y01), P(o[0]), 1.0, 1.0, 0.5, 0.5, 3.0, 1.0, 30.0, 200.0,
+                         250.0, n, None)),
+    }
+    for name, (sizes, ex, plain) in cases.items():
+        fresh = [torch.full((k,), float("nan"), device="cuda") for k in sizes]
+        ok(gn, ex(fresh, 0))
+        zeros = [torch.zeros(k, device="cuda") for k in sizes]
+        ok(gn, plain(zeros))
+        for f_, z_ in zip(fresh, zeros):
+            np.testing.assert_array_equal(host(torch, f_), host(torch, z_), err_msg=name)
+        pre = [dev(torch, r.normal(size=k)) for k in sizes]
+        pre2 = [t.clone() for t in pre]
+        ok(gn, ex(pre, ACC))
+        ok(gn, plain(pre2))
+        for p_, q_ in zip(pre, pre2):
+            np.testing.assert_array_equal(host(torch, p_), host(torch, q_), err_msg=name)
+        assert ex(fresh, 2) == gn.SOAR_EINVAL, name
+
+
 # ---- AdamW and multi-tensor ---------------------------------------------------------
 def test_adamw_and_multi_tensor(env):
     gn, torch = env
