@@ -293,6 +293,28 @@ SOAR_API int soar_multi_tensor_fill_device(float* const* tensors,
                                            const int64_t* numel, int n_tensors,
                                            float value, void* stream);
 
+/* ---- channel concatenation --------------------------------------------- */
+/* dst [N][C][HW] = the K pieces srcs[k] [N][channels[k]][HW] one after the
+ * other along channels (C = sum of channels), 1 <= K <= 16.  srcs and
+ * channels are HOST arrays of device pointers and counts.  One launch for
+ * all pieces and samples.
+ * Replaces: concat_channels (blocks.cpp), which copies each piece of each
+ * sample with its own device copy. */
+SOAR_API int soar_concat_channels_forward(const float* const* srcs,
+                                          const int64_t* channels, int K,
+                                          float* dst, int64_t N, int64_t HW,
+                                          void* stream);
+/* Its backward: grads[k] [N][channels[k]][HW] receives piece k's slice of
+ * grad_dst, written, or added with flags[k] = SOAR_GN_ACCUMULATE_DX (flags
+ * may be NULL: all written); a NULL grads[k] is skipped.  grads, channels
+ * and flags are HOST arrays.  Replaces: the ConcatNode backward's copies
+ * (blocks.cpp). */
+SOAR_API int soar_concat_channels_backward(const float* grad_dst,
+                                           float* const* grads,
+                                           const int64_t* channels,
+                                           const unsigned* flags, int K,
+                                           int64_t N, int64_t HW, void* stream);
+
 /* ---- backward entry points that may write instead of add -------------- */
 /* Each takes the arguments of the entry point of the same name without
  * _ex, plus `flags`: SOAR_GN_ACCUMULATE_DX adds into the gradient outputs

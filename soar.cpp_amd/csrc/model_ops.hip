@@ -898,6 +898,57 @@ __global__ __launch_bounds__(kThreads) void k_sigmoid_threshold(const float* __r
 }
 
 // ---------------------------------------------------------------------------
+// Channel concatenation of K tensors [N][C_k][HW] into [N][sum C_k][HW] and
+// its backward, one launch for every (sample, piece) copy (the reference
+// issues one copy per piece and sample, blocks.cpp concat_channels).  Block
+// row y takes the pieces y, y + gridDim.y, ... of the N*K (sample, piece)
+// pairs; its blocks stride over that piece's C_k*HW contiguous floats.
+// ---------------------------------------------------------------------------
+template <int V, bool BWD>
+__global__ __launch_bounds__(kThreads) void k_concat(CatArgs a, float* __restrict__ cat,
+                                                     const float* __restrict__ gcat, int64_t N,
+                                                     int64_t HW) {
+    using T = typename std::conditional<V == 4, float4, float>::type;
+    const int64_t C_total = a.c_off[a.K];
+    for (int64_t q = blockIdx.y; q < N * a.K; q += gridDim.y) {
+        const int k = (int)(q % a.K);
+        const int64_t n = q / a.K;
+        const int64_t Ck = a.c_off[k + 1] - a.c_off[k];
+        const int64_t len = Ck * HW / V;
+        const int64_t coff = (n * C_total + a.c_off[k]) * HW / V, poff = n * Ck * HW / V;
+        if (BWD) {
+            T* d = reinterpret_cast<T*>(a.piece[k]);
+            if (!d) continue;
+            d += poff;
+            const T* src = reinterpret_cast<const T*>(gcat) + coff;
+            const bool acc = (a.acc_mask >> k) & 1;
+            for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < len;
+                 i += (int64_t)gridDim.x * kThreads) {
+                T v = src[i];
+                if (acc) {
+                    const T o = d[i];
+                    if constexpr (V == 4) {
+                        v.x += o.x;
+                        v.y += o.y;
+                        v.z += o.z;
+                        v.w += o.w;
+                    } else {
+                        v += o;
+                    }
+                }
+                d[i] = v;
+            }
+        } else {
+            const T* src = reinterpret_cast<const T*>(a.piece[k]) + poff;
+            T* d = reinterpret_cast<T*>(cat) + coff;
+            for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < len;
+                 i += (int64_t)gridDim.x * kThreads)
+                d[i] = src[i];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Multi-tensor operators.  The tensors are cut into chunks of kMtChunk
 // elements; every block first builds, in LDS, the prefix count of chunks
 // per tensor from the size table, then walks chunks blockIdx.x,
@@ -1322,6 +1373,29 @@ hipError_t launch_dice_bce_backward(const float* z, const float* y, float* gz, i
 hipError_t launch_sigmoid_threshold(const float* z, float* p, uint8_t* mask, int64_t n,
                                     float threshold, hipStream_t s) {
     k_sigmoid_threshold<<<blocks_for(n), kThreads, 0, s>>>(z, p, mask, n, threshold);
+    return hipGetLastError();
+}
+
+hipError_t launch_concat(const CatArgs& a, float* cat, const float* gcat, int64_t N,
+                         int64_t HW, bool backward, hipStream_t s) {
+    int64_t max_len = 0;
+    bool v4 = HW % 4 == 0 && ((uintptr_t)cat % 16 == 0) && ((uintptr_t)gcat % 16 == 0);
+    for (int k = 0; k < a.K; ++k) {
+        max_len = std::max(max_len, (a.c_off[k + 1] - a.c_off[k]) * HW);
+        v4 = v4 && (uintptr_t)a.piece[k] % 16 == 0;
+    }
+    const int V = v4 ? 4 : 1;
+    const int64_t bx = std::min<int64_t>((max_len / V + kThreads - 1) / kThreads, 1024);
+    const dim3 grid((unsigned)std::max<int64_t>(bx, 1), (unsigned)std::min<int64_t>(N * a.K, 65535));
+    auto run = [&](auto VV, auto B) {
+        k_concat<VV(), B()><<<grid, kThreads, 0, s>>>(a, cat, gcat, N, HW);
+    };
+    bsel(backward, [&](auto B) {
+        if (v4)
+            run(std::integral_constant<int, 4>{}, B);
+        else
+            run(std::integral_constant<int, 1>{}, B);
+    });
     return hipGetLastError();
 }
 

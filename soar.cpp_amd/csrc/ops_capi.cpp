@@ -882,4 +882,69 @@ SOAR_API int soar_multi_tensor_fill_device(float* const* tensors, const int64_t*
                     "multi-tensor fill launch");
 }
 
+// ---- channel concatenation ------------------------------------------------------
+static int concat_args(const int64_t* channels, int K, int64_t N, int64_t HW,
+                       soar::ops::CatArgs* a, int64_t* total) {
+    if (K < 1 || K > soar::ops::kMaxCat)
+        return fail(SOAR_EINVAL, "concat: K=%d is outside [1, %d]", K, soar::ops::kMaxCat);
+    if (!channels) return fail(SOAR_EINVAL, "concat: channels is NULL");
+    if (N < 0 || HW < 0) return fail(SOAR_EINVAL, "concat: negative N or HW");
+    a->K = K;
+    a->c_off[0] = 0;
+    for (int k = 0; k < K; ++k) {
+        if (channels[k] < 0 ||
+            __builtin_add_overflow(a->c_off[k], channels[k], &a->c_off[k + 1]))
+            return fail(SOAR_EINVAL, "concat: invalid channel count %lld of piece %d",
+                        (long long)channels[k], k);
+    }
+    if (!mul_ok({N, a->c_off[K], HW}, total)) return fail(SOAR_EINVAL, "concat: sizes overflow");
+    return SOAR_OK;
+}
+
+SOAR_API int soar_concat_channels_forward(const float* const* srcs, const int64_t* channels,
+                                          int K, float* dst, int64_t N, int64_t HW,
+                                          void* stream) {
+    soar::ops::CatArgs a{};
+    int64_t total;
+    int rc;
+    if ((rc = concat_args(channels, K, N, HW, &a, &total))) return rc;
+    if (!srcs) return fail(SOAR_EINVAL, "concat: srcs is NULL");
+    if (total == 0) return ok();
+    if ((rc = require_device()) || (rc = check_dev(dst, (size_t)total * 4, "dst"))) return rc;
+    for (int k = 0; k < K; ++k) {
+        const int64_t e = N * channels[k] * HW;
+        if (e > 0 && (rc = check_dev(srcs[k], (size_t)e * 4, "srcs[k]"))) return rc;
+        a.piece[k] = const_cast<float*>(srcs[k]);
+    }
+    return launched(soar::ops::launch_concat(a, dst, nullptr, N, HW, false, S(stream)),
+                    "concat_channels_forward launch");
+}
+
+SOAR_API int soar_concat_channels_backward(const float* grad_dst, float* const* grads,
+                                           const int64_t* channels, const unsigned* flags,
+                                           int K, int64_t N, int64_t HW, void* stream) {
+    soar::ops::CatArgs a{};
+    int64_t total;
+    int rc;
+    if ((rc = concat_args(channels, K, N, HW, &a, &total))) return rc;
+    if (!grads) return fail(SOAR_EINVAL, "concat: grads is NULL");
+    for (int k = 0; flags && k < K; ++k) {
+        if (flags[k] & ~SOAR_GN_ACCUMULATE_DX)
+            return fail(SOAR_EINVAL,
+                        "concat: unsupported flags 0x%x of piece %d (SOAR_GN_ACCUMULATE_DX only)",
+                        flags[k], k);
+        if (flags[k] & SOAR_GN_ACCUMULATE_DX) a.acc_mask |= 1u << k;
+    }
+    if (total == 0) return ok();
+    if ((rc = require_device()) || (rc = check_dev(grad_dst, (size_t)total * 4, "grad_dst")))
+        return rc;
+    for (int k = 0; k < K; ++k) {
+        const int64_t e = N * channels[k] * HW;
+        if (e > 0 && (rc = check_dev_opt(grads[k], (size_t)e * 4, "grads[k]"))) return rc;
+        a.piece[k] = e > 0 ? grads[k] : nullptr;
+    }
+    return launched(soar::ops::launch_concat(a, nullptr, grad_dst, N, HW, true, S(stream)),
+                    "concat_channels_backward launch");
+}
+
 }  // extern "C"

@@ -89,6 +89,21 @@ hipError_t launch_dice_bce_backward(const float* z, const float* y, float* gz, i
 hipError_t launch_sigmoid_threshold(const float* z, float* p, uint8_t* mask, int64_t n,
                                     float threshold, hipStream_t s);
 
+// Channel concatenation of K <= kMaxCat pieces [N][C_k][HW] <-> [N][C][HW]
+// (C = c_off[K]).  Forward: piece[k] are the sources, `cat` the output.
+// Backward: `gcat` is the concatenation's gradient, piece[k] the pieces'
+// gradients (null: skipped), added into when bit k of acc_mask is set,
+// else written.
+constexpr int kMaxCat = 16;
+struct CatArgs {
+    float* piece[kMaxCat];
+    int64_t c_off[kMaxCat + 1];
+    unsigned acc_mask;
+    int K;
+};
+hipError_t launch_concat(const CatArgs& a, float* cat, const float* gcat, int64_t N,
+                         int64_t HW, bool backward, hipStream_t s);
+
 // Multi-tensor operators over device arrays of tensor pointers and sizes
 // (at most kMaxMultiTensors tensors, each under 2^31 * 4096 elements).
 constexpr int kMaxMultiTensors = 2048;

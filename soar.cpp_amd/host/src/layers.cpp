@@ -213,22 +213,29 @@ struct ConcatNode : autograd::AutogradNode {
         to_dev(go);
         const bool batched = go->ndim() == 4;
         const int64_t N = batched ? go->dim(0) : 1;
-        const int64_t C_total = batched ? go->dim(1) : go->dim(0);
         const int64_t HW = go->dim(-1) * go->dim(-2);
-        int64_t c_off = 0;
-        for (const auto& t : inputs) {
-            const int64_t c = batched ? t->dim(1) : t->dim(0);
-            if (wants(t)) {
-                TensorPtr gi = Tensor::create(t->shape(), false, true);
-                for (int64_t n = 0; n < N; ++n)
-                    check(soar_memcpy_d2d(gi->cuda_data() + n * c * HW,
-                                          go->cuda_data() + (n * C_total + c_off) * HW,
-                                          (size_t)(c * HW) * sizeof(float), nullptr),
-                          "concat backward");
-                propagate_grad(t, std::move(gi));
-            }
-            c_off += c;
+        const size_t K = inputs.size();
+        if (K > 16) throw ShapeError("concat_channels: at most 16 tensors");
+        std::vector<TensorPtr> gi(K);
+        std::vector<float*> ptr(K, nullptr);
+        std::vector<int64_t> ch(K);
+        std::vector<unsigned> fl(K, 0u);
+        std::vector<bool> fresh(K, false);
+        for (size_t k = 0; k < K; ++k) {
+            const TensorPtr& t = inputs[k];
+            ch[k] = batched ? t->dim(1) : t->dim(0);
+            if (!wants(t)) continue;
+            bool f = false;
+            gi[k] = write_target(t, &f);
+            fresh[k] = f;
+            fl[k] = mode(f);
+            ptr[k] = gi[k]->cuda_data();
         }
+        check(soar_concat_channels_backward(go->cuda_data(), ptr.data(), ch.data(), fl.data(),
+                                            (int)K, N, HW, nullptr),
+              "concat backward");
+        for (size_t k = 0; k < K; ++k)
+            if (gi[k] && fresh[k]) propagate_grad(inputs[k], std::move(gi[k]));
     }
     void release_variables() override { inputs.clear(); }
 };
@@ -390,19 +397,18 @@ TensorPtr concat_channels(const std::vector<TensorPtr>& tensors) {
     const bool record = GradMode::is_enabled() &&
                         std::any_of(tensors.begin(), tensors.end(),
                                     [](const TensorPtr& t) { return t->requires_grad(); });
+    if (tensors.size() > 16) throw ShapeError("concat_channels: at most 16 tensors");
     Shape os = batched ? Shape{N, C_total, H, W} : Shape{C_total, H, W};
     TensorPtr out = Tensor::create(os, record, true);
-    const int64_t HW = H * W;
-    int64_t c_off = 0;
+    std::vector<const float*> src;
+    std::vector<int64_t> ch;
     for (const auto& t : tensors) {
-        const int64_t c = batched ? t->dim(1) : t->dim(0);
-        for (int64_t n = 0; n < N; ++n)
-            check(soar_memcpy_d2d(out->cuda_data() + (n * C_total + c_off) * HW,
-                                  t->cuda_data() + n * c * HW, (size_t)(c * HW) * sizeof(float),
-                                  nullptr),
-                  "concat");
-        c_off += c;
+        src.push_back(t->cuda_data());
+        ch.push_back(batched ? t->dim(1) : t->dim(0));
     }
+    check(soar_concat_channels_forward(src.data(), ch.data(), (int)tensors.size(),
+                                       out->cuda_data(), N, H * W, nullptr),
+          "concat");
     if (record) {
         auto node = std::make_shared<ConcatNode>();
         node->inputs = tensors;

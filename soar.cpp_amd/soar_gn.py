@@ -157,6 +157,8 @@ SIGNATURES = {
     "soar_multi_tensor_norm_sq_device": (_c.c_int, [_P, _P, _c.c_int, _P, _P, _SZ, _P]),
     "soar_multi_tensor_scale_device": (_c.c_int, [_P, _P, _c.c_int, _c.c_float, _P]),
     "soar_multi_tensor_fill_device": (_c.c_int, [_P, _P, _c.c_int, _c.c_float, _P]),
+    "soar_concat_channels_forward": (_c.c_int, [_P, _P, _c.c_int, _P, _I64, _I64, _P]),
+    "soar_concat_channels_backward": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _I64, _I64, _P]),
     "soar_sigmoid_backward_ex": (_c.c_int, [_P, _P, _P, _SZ, _c.c_uint, _P]),
     "soar_mul_broadcast_backward_ex": (_c.c_int, [_P, _P, _P, _P, _P, _SZ, _SZ, _c.c_uint, _P]),
     "soar_convex_combination_backward_ex": (_c.c_int, [_P] * 7 + [_SZ, _c.c_uint, _P]),

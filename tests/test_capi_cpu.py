@@ -40,6 +40,17 @@ def test_ops_validate_on_the_host(L):
     assert b"unsupported flags" in L.soar_last_error()
     assert L.soar_convex_combination_backward_ex(None, None, None, None, None, None, None, 4,
                                                  8, None) == soar_gn.SOAR_EINVAL
+    # concatenation: 1..16 pieces, non-negative channel counts, one flag
+    ch = (ctypes.c_int64 * 17)(*([1] * 17))
+    ptrs = (ctypes.c_void_p * 17)()
+    assert L.soar_concat_channels_forward(ptrs, ch, 0, None, 1, 4, None) == soar_gn.SOAR_EINVAL
+    assert L.soar_concat_channels_forward(ptrs, ch, 17, None, 1, 4, None) == soar_gn.SOAR_EINVAL
+    neg = (ctypes.c_int64 * 2)(3, -1)
+    assert L.soar_concat_channels_forward(ptrs, neg, 2, None, 1, 4, None) == soar_gn.SOAR_EINVAL
+    fl = (ctypes.c_uint * 2)(0, 1)
+    assert L.soar_concat_channels_backward(None, ptrs, ch, fl, 2, 1, 4,
+                                           None) == soar_gn.SOAR_EINVAL
+    assert b"unsupported flags" in L.soar_last_error()
     # resize: plane sides must stay below 2^31 (the tap arithmetic is 32-bit)
     assert L.soar_upsample_bilinear_forward(None, None, 1, 1, 1 << 31, 2, 2,
                                             None) == soar_gn.SOAR_EINVAL

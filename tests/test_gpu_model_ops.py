@@ -360,6 +360,40 @@ def test_losses(env):
     np.testing.assert_array_equal(host(torch, m), (z >= 0).astype(np.uint8))
 
 
+# ---- channel concatenation -----------------------------------------------------------
+@pytest.mark.parametrize("N,HW", [(2, 7), (2, 16), (1, 4096), (3, 1)])
+def test_concat_channels(env, N, HW):
+    """One-launch concatenation: forward bit-exact against np.concatenate;
+    backward writes (NaN prefill), adds (flags), and skips NULL pieces."""
+    gn, torch = env
+    L = gn.lib()
+    r = np.random.default_rng(N * HW)
+    chans = [3, 5, 2, 8]
+    K = len(chans)
+    xs = [r.normal(size=(N, c, HW)).astype(F32) for c in chans]
+    xd = [dev(torch, x) for x in xs]
+    out = torch.empty((N, sum(chans), HW), device="cuda")
+    src = (ctypes.c_void_p * K)(*[t.data_ptr() for t in xd])
+    ch = (ctypes.c_int64 * K)(*chans)
+    ok(gn, L.soar_concat_channels_forward(src, ch, K, P(out), N, HW, None))
+    want = np.concatenate(xs, axis=1)
+    np.testing.assert_array_equal(host(torch, out), want)
+    g = r.normal(size=want.shape).astype(F32)
+    gd = dev(torch, g)
+    pre = [r.normal(size=(N, c, HW)).astype(F32) for c in chans]
+    gi = [torch.full((N, c, HW), float("nan"), device="cuda") for c in chans]
+    gi[1] = dev(torch, pre[1])  # added into
+    gi[3] = dev(torch, pre[3])  # skipped (NULL), must stay as it was
+    ptrs = (ctypes.c_void_p * K)(gi[0].data_ptr(), gi[1].data_ptr(), gi[2].data_ptr(), None)
+    flags = (ctypes.c_uint * K)(0, gn.GN_ACCUMULATE_DX, 0, 0)
+    ok(gn, L.soar_concat_channels_backward(P(gd), ptrs, ch, flags, K, N, HW, None))
+    offs = np.cumsum([0] + chans)
+    np.testing.assert_array_equal(host(torch, gi[0]), g[:, offs[0]:offs[1]])
+    np.testing.assert_array_equal(host(torch, gi[1]), pre[1] + g[:, offs[1]:offs[2]])
+    np.testing.assert_array_equal(host(torch, gi[2]), g[:, offs[2]:offs[3]])
+    np.testing.assert_array_equal(host(torch, gi[3]), pre[3])
+
+
 # ---- write-mode backward entry points ----------------------------------------------
 def test_backward_write_mode(env):
     """Every _ex backward with flags 0 overwrites its outputs (prefilled
