@@ -192,11 +192,15 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_conv(
 // 4 below, where more blocks per plane measured faster; fewer when that
 // leaves the grid short of blocks, see wgrad_per.)
 
+// With `direct` (one sample and one tile group per plane, so a block's sums
+// are the whole sums) the block adds them into dw and db itself, exactly as
+// k_dw_wgrad_finish would from its single partial, and no finish runs.
 template <int K, int S, int D>
 __global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
     const float* __restrict__ dy, const float* __restrict__ x, float* __restrict__ part,
-    int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x,
-    int64_t tiles_y, int64_t tpp, int per) {
+    float* __restrict__ dw, float* __restrict__ db, bool direct, int64_t C, int64_t Hi,
+    int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x, int64_t tiles_y,
+    int64_t tpp, int per) {
     using T = Tile<K, S, D>;
     constexpr int KK1 = K * K + 1;
     __shared__ __attribute__((aligned(16))) float tile[T::floats];
@@ -265,7 +269,12 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
     __syncthreads();
     if (t < KK1) {
         const float v = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
-        part[(n * tpp + gix) * (C * KK1) + c * KK1 + t] = v;
+        if (direct) {
+            float* o = t < K * K ? (dw ? dw + c * K * K + t : nullptr) : (db ? db + c : nullptr);
+            if (o) *o = (float)((double)*o + (double)v);
+        } else {
+            part[(n * tpp + gix) * (C * KK1) + c * KK1 + t] = v;
+        }
     }
 }
 
@@ -684,15 +693,17 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
         const int64_t per = wgrad_per(sh);
         const int64_t tpp = wgrad_groups(sh, per, &tiles_x, &tiles_y);
         float* part = static_cast<float*>(ws);
+        const bool direct = sh.N * tpp == 1;
         int tok = prof_begin(s, "dw_conv_wgrad");
         const bool fast = planes_fit_32(sh) && fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
             using CF = decltype(cf);
             k_dw_wgrad<CF::k, CF::s, CF::d>
                 <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
-                    dy, x, part, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tiles_y, tpp,
-                    (int)per);
+                    dy, x, part, dw, db, direct, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad,
+                    tiles_x, tiles_y, tpp, (int)per);
         });
         prof_end(s, tok);
+        if (fast && direct) return hipGetLastError();  // the blocks added the sums
         tok = prof_begin(s, "dw_conv_wgrad_finish");
         if (fast) {
             const int64_t E = sh.C * KK1;

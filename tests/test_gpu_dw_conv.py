@@ -34,6 +34,13 @@ CASES = [
     (1, 2, 20, 21, 4, 2, 2),      # generic kernels (even K, stride 2, dilation 2)
     (1, 2, 13, 17, 5, 3, 1),      # generic, stride 3
     (2, 3, 5, 7, 7, 1, 1),        # image smaller than the kernel
+    # one sample, one output tile per plane: the weight-gradient blocks add
+    # their sums into dw / db directly (no finish kernel)
+    (1, 4, 32, 64, 3, 1, 1),
+    (1, 3, 17, 30, 7, 1, 1),
+    (1, 5, 24, 40, 3, 2, 1),
+    (1, 2, 10, 12, 3, 1, 3),
+    (1, 2, 30, 60, 5, 1, 1),
 ]
 
 
@@ -80,8 +87,9 @@ def test_dw_backward_matches_oracle(gpu, oracle, N, C, H, W, K, s, d):
     check(host(db), tb, P * U32 * np.abs(dy).sum(axis=(0, 2, 3)), "db")
 
 
-def test_dw_backward_accumulates_and_skips(gpu, oracle):
-    N, C, H, W, K, s, d = 1, 3, 40, 70, 3, 1, 1
+@pytest.mark.parametrize("H,W", [(40, 70), (20, 30)])  # partials + finish, direct
+def test_dw_backward_accumulates_and_skips(gpu, oracle, H, W):
+    N, C, K, s, d = 1, 3, 3, 1, 1
     pad = autopad(K, d)
     x, w, _ = inputs(3, N, C, H, W, K)
     dy = np.random.default_rng(4).standard_normal((N, C, H, W)).astype(np.float32)
