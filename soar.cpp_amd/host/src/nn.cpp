@@ -356,9 +356,19 @@ struct AddNode : autograd::AutogradNode {
         if (b && b->grad_fn()) r.push_back(b->grad_fn());
         return r;
     }
+    // go goes to both inputs unchanged.  Inputs whose pending gradient may
+    // be added into directly get go added there, both in one launch; the
+    // others receive go itself (kept by reference, no copy).
     void backward(const TensorPtr& go) override {
-        if (a) propagate_grad(a, go);
-        if (b) propagate_grad(b, go);
+        TensorPtr sa = grad_sink(a);
+        TensorPtr sb = grad_sink(b);  // (null when b is a and sa holds its sink)
+        if (sa || sb) {
+            if (!go->is_cuda()) go->to_cuda();
+            hip::kernels::add_backward(go->cuda_data(), sa ? sa->cuda_data() : nullptr,
+                                       sb ? sb->cuda_data() : nullptr, (size_t)go->numel());
+        }
+        if (a && !sa) propagate_grad(a, go);
+        if (b && !sb) propagate_grad(b, go);
     }
     void release_variables() override { a = b = nullptr; }
 };
