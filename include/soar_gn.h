@@ -377,6 +377,12 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
                               /* adds (weight gradient: half as many) run */
                               /* the SIMT kernels; 0 = never; the default */
                               /* is 2^25                                  */
+#define SOAR_TUNE_PW_SPLITK 12 /* most blocks the fused conv + GroupNorm  */
+                               /* forward splits K over when its grid has  */
+                               /* fewer than 256 tiles (fp32 slices in the */
+                               /* workspace, added by a second kernel that */
+                               /* also writes the statistics); 1 = never;  */
+                               /* 1..8, the default is 8                   */
 SOAR_API int soar_gn_tune(int key, int64_t value);
 SOAR_API int64_t soar_gn_tune_get(int key);
 

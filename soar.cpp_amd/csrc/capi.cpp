@@ -445,7 +445,7 @@ SOAR_API int soar_conv2d_1x1_forward(const float* in, const float* weight, const
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     soar::gn::PwArgs a{in, weight, bias, out};
     hipError_t e = soar::gn::launch_pw_conv(a, 1, (int64_t)C_in, (int64_t)C_out, (int64_t)HW,
-                                            chunk, nullptr, false, t.pw_small,
+                                            chunk, nullptr, false, t.pw_small, nullptr, 1,
                                             static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "conv2d_1x1_forward launch");
 }
@@ -470,9 +470,14 @@ SOAR_API int soar_pw_conv_forward(const float* x, const float* weight, const flo
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     soar::gn::PwArgs a{x, weight, bias, z};
     hipError_t e = soar::gn::launch_pw_conv(a, N, C_in, C_out, HW, chunk, nullptr, false,
-                                            t.pw_small, static_cast<hipStream_t>(stream));
+                                            t.pw_small, nullptr, 1,
+                                            static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "pointwise convolution launch");
 }
+
+// Offset of the split-K slices in the fused forward's workspace: after the
+// GroupNorm's part, 256-byte aligned.
+static size_t kz_offset(size_t gn_bytes) { return (gn_bytes + 255) & ~(size_t)255; }
 
 SOAR_API size_t soar_pw_conv_gn_workspace_bytes(int64_t N, int64_t C_out, int64_t HW, int64_t G) {
     int64_t elems = 0;
@@ -485,6 +490,9 @@ SOAR_API size_t soar_pw_conv_gn_workspace_bytes(int64_t N, int64_t C_out, int64_
     if (soar::gn::pw_use_small(N, C_out, 1, HW, t.pw_small) &&
         soar::gn::make_plan(N, C_out, HW, G, t, &q))
         b = std::max(b, soar::gn::workspace_bytes(q));
+    // small grids: the split-K slices after the GroupNorm workspace
+    const size_t kz = soar::gn::pw_kz_max_bytes(N, C_out, HW, p.chunk, (int)t.pw_kz);
+    if (kz) b = std::max(b, kz_offset(soar::gn::workspace_bytes(p)) + kz);
     return b;
 }
 
@@ -531,15 +539,25 @@ SOAR_API int soar_pw_conv_gn_silu_forward(const float* x, const float* weight,
         q.vec4 = q.vec4 && aligned16(z) && aligned16(y);
         if ((rc = check_ws(q, workspace, workspace_bytes))) return rc;
         hipError_t e = soar::gn::launch_pw_conv(pa, N, C_in, C_out, HW, p.chunk, nullptr, false,
-                                                t.pw_small, s);
+                                                t.pw_small, nullptr, 1, s);
         if (e != hipSuccess) return hip_fail(e, "pointwise convolution launch");
         soar::gn::FwdArgs a{z, gamma, beta, y, mean, rstd, mean_lo, eps, flags, workspace};
         e = soar::gn::launch_forward(q, t, a, s);
         if (e != hipSuccess) return hip_fail(e, "GroupNorm forward launch");
         return ok();
     }
+    // small grids split K over blocks when the workspace holds the slices
+    // (after the GroupNorm's own workspace)
+    float* kz_ws = nullptr;
+    const soar::gn::PwKz kp = soar::gn::pw_kz_plan(N, C_in, C_out, HW, p.chunk, (int)t.pw_kz);
+    if (kp.kz > 1) {
+        const size_t off = kz_offset(soar::gn::workspace_bytes(p));
+        if (workspace_bytes >= off + soar::gn::pw_kz_bytes(N, C_out, HW, kp.kz))
+            kz_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + off);
+    }
     hipError_t e = soar::gn::launch_pw_conv(pa, N, C_in, C_out, HW, p.chunk,
-                                            soar::gn::ws_partials(p, workspace), false, 0, s);
+                                            soar::gn::ws_partials(p, workspace), false, 0, kz_ws,
+                                            kp.kz, s);
     if (e != hipSuccess) return hip_fail(e, "pointwise convolution launch");
     soar::gn::FwdArgs a{z, gamma, beta, y, mean, rstd, mean_lo, eps, flags, workspace};
     e = soar::gn::launch_forward_from_partials(p, t, a, s);
@@ -554,7 +572,9 @@ SOAR_API size_t soar_pw_conv_backward_workspace_bytes(int64_t N, int64_t C_in, i
         g_err.clear();
         return 0;
     }
-    const soar::gn::PwBwdPlan p = soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW);
+    const Tuning t = current_tuning();
+    const soar::gn::PwBwdPlan p =
+        soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW, t.pw_chunk, (int)t.pw_kz);
     return soar::gn::pw_bwd_workspace_bytes(p);
 }
 
@@ -579,17 +599,22 @@ SOAR_API int soar_pw_conv_backward(const float* dz, const float* x, const float*
         (rc = check_dev_opt(dbias, (size_t)C_out * 4, "dbias")))
         return rc;
     const Tuning t = current_tuning();
-    const soar::gn::PwBwdPlan p = soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW);
-    if (!pw_grid_fits(N, HW, soar::gn::pw_pick_chunk(N, C_in, HW, t.pw_chunk)) || p.G > 65535 ||
+    soar::gn::PwBwdPlan p =
+        soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW, t.pw_chunk, (int)t.pw_kz);
+    if (!pw_grid_fits(N, HW, p.chunk_dx) || p.G > 65535 ||
         p.tiles_co * p.tiles_ci > (int64_t)0x7fffffff)
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    // a workspace sized without the split-K slices (another tuning when it
+    // was queried) runs dx without them
+    if (p.kz_bytes && workspace_bytes < soar::gn::pw_bwd_workspace_bytes(p))
+        p = soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW, t.pw_chunk, 1);
     const size_t need = soar::gn::pw_bwd_workspace_bytes(p);
     if (workspace_bytes < need)
         return fail(SOAR_EINVAL, "workspace of %zu bytes is smaller than the %zu this shape needs",
                     workspace_bytes, need);
     if ((rc = check_dev(workspace, need, "workspace"))) return rc;
     soar::gn::PwBwdArgs a{dz, x, weight, dx, dweight, dbias, workspace};
-    hipError_t e = soar::gn::launch_pw_backward(p, a, N, C_in, C_out, HW, t.pw_chunk,
+    hipError_t e = soar::gn::launch_pw_backward(p, a, N, C_in, C_out, HW,
                                                 (flags & SOAR_GN_ACCUMULATE_DX) != 0,
                                                 t.pw_small, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "pointwise convolution backward launch");
@@ -1019,6 +1044,10 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
                 return fail(SOAR_EINVAL, "pw_small must be in [0, 2^40]");
             g_tune.pw_small = value;
             return ok();
+        case SOAR_TUNE_PW_SPLITK:
+            if (value < 1 || value > 8) return fail(SOAR_EINVAL, "pw_splitk must be in [1, 8]");
+            g_tune.pw_kz = value;
+            return ok();
         default:
             return fail(SOAR_EINVAL, "unknown tuning key %d", key);
     }
@@ -1038,6 +1067,7 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
         case SOAR_TUNE_SMALL_UNIT: return g_tune.small_unit;
         case SOAR_TUNE_PW_SMALL: return g_tune.pw_small;
         case SOAR_TUNE_FOLD_MAX: return g_tune.fold_max;
+        case SOAR_TUNE_PW_SPLITK: return g_tune.pw_kz;
         default: return -1;
     }
 }

@@ -69,6 +69,8 @@ struct Tuning {
     int64_t pw_small = 1 << 25;  // pointwise convolutions of at most this
                                  // many multiply-adds (weight gradient: half
                                  // as many) run the SIMT kernels (0: never)
+    int64_t pw_kz = 8;           // most blocks a small-grid pointwise
+                                 // convolution splits K over (1: never)
 };
 
 constexpr int kThreads = 256;   // first passes (stats, reduction)
@@ -143,10 +145,25 @@ int64_t pw_pick_chunk(int64_t N, int64_t C_out, int64_t HW, int64_t max_chunk);
 // part[(n*C_out + co)*cpp + k].
 // `name` labels the launch for the kernel timers (null: a default).
 // Without `part`, the SIMT kernel (K split over the waves of a block) runs
-// when pw_use_small(N, C_out, C_in, HW, small).
+// when pw_use_small(N, C_out, C_in, HW, small).  With `part` and `kz_ws`
+// (at least pw_kz_bytes(N, C_out, HW, pw_kz_plan(...).kz) bytes, 16-byte
+// aligned), a grid of few tiles splits K over up to kz_max blocks per tile
+// (pw_kz_plan) and a second kernel adds their fp32 slices and writes the
+// statistics (a 256 -> 128 output at 4096 pixels: 25.8 us with K over the
+// four waves of a block, 14.3 + 4.5 us this way).
 hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
                           int64_t HW, int64_t chunk, double2* part, bool accumulate,
-                          int64_t small, hipStream_t s, const char* name = nullptr);
+                          int64_t small, float* kz_ws, int kz_max, hipStream_t s,
+                          const char* name = nullptr);
+// Cross-block split-K of the MFMA convolution (kz = 1: not used).
+struct PwKz {
+    int kz = 1;
+};
+PwKz pw_kz_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk,
+                int kz_max);
+size_t pw_kz_bytes(int64_t N, int64_t C_out, int64_t HW, int kz);
+// Bound of pw_kz_bytes over every C_in (for workspace queries without it).
+size_t pw_kz_max_bytes(int64_t N, int64_t C_out, int64_t HW, int64_t chunk, int kz_max);
 // True when the SIMT kernel computes the M x HW outputs of N samples (K
 // terms each): at most `small` multiply-adds, and offsets inside a sample
 // fit in 32 bits.
@@ -170,15 +187,20 @@ struct PwBwdPlan {
     int64_t tiles_co = 0, tiles_ci = 0;  // (32 tm) x (32 tn) tiles of dW
     int64_t chunk = 0, cpp = 0, G = 0;   // pixel chunks of the dW waves
     size_t wt_bytes = 0, pw_bytes = 0, pb_bytes = 0;
+    int64_t chunk_dx = 0;  // pixels per wave of dx = W^T dz
+    int kz_dx = 1;         // its cross-block split-K (pw_kz_plan)
+    size_t kz_bytes = 0;   // and the slices' bytes, after the partials
 };
-PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW);
+PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW,
+                           int64_t chunk_dx, int kz_max);
 size_t pw_bwd_workspace_bytes(const PwBwdPlan& p);
 // dx runs the SIMT kernel when pw_use_small(N, C_in, C_out, HW, small),
 // dW/db when the weight gradient has at most small/2 multiply-adds and
-// N*HW <= 16384 (then the workspace is not touched).
+// N*HW <= 16384 (then the workspace is not touched).  `chunk_dx` and the
+// split-K of dx come from the plan (make_pw_bwd_plan).
 hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N, int64_t C_in,
-                              int64_t C_out, int64_t HW, int64_t chunk_dx, bool accumulate_dx,
-                              int64_t small, hipStream_t s);
+                              int64_t C_out, int64_t HW, bool accumulate_dx, int64_t small,
+                              hipStream_t s);
 
 // Depthwise convolution (dw_conv.hip): groups = C_in = C_out, weights
 // [C][K][K], output size given by the caller, taps outside the input skipped.

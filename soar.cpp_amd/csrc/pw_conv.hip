@@ -48,6 +48,7 @@ typedef float f16 __attribute__((ext_vector_type(16)));
 constexpr int kRowTile = 64;    // output rows per pass (two 32-row tiles)
 constexpr int kItem = 128;      // pixels per item (four 32-column tiles)
 constexpr int kRowGroup = 4;    // row tiles whose statistics a lane keeps
+constexpr int kKzTiles = 256;   // grids of fewer (64-row x chunk) tiles split K over blocks
 constexpr int kLdsStride = 34;  // float2 per LDS row: 32 lanes + 2 pad
 // Word 3 of a raw buffer descriptor on gfx9-family parts (gfx950 included):
 // 32-bit float data format, no swizzle, no stride.
@@ -329,13 +330,16 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
 // while a step's MFMAs run (PD > 1 runs one wave per SIMD, which leaves
 // room for the extra operand buffers and the accumulators in AGPRs).  Byte
 // offsets inside one sample's planes must fit in 32 bits (checked by the
-// host with pw_offsets_fit).
+// host with pw_offsets_fit).  Cross-block split-K: block z of a grid with
+// gridDim.z > 1 takes the K steps [z kzseg, (z + 1) kzseg) (its KS waves
+// split them again) and writes its products to the slice z + z * zslice;
+// k_pw_kz_reduce adds the slices.
 template <bool FAST, int MODE, bool BIAS, int KS, int PD>
 __global__ __launch_bounds__(64 * KS, PD > 1 ? 1 : 2) void k_pw_conv(
     const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ bias, float* __restrict__ z, double2* __restrict__ part,
     int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk, int64_t cpp, int Kpad, int rpw,
-    int kseg) {
+    int kseg, int kzseg, int64_t zslice) {
     __shared__ __attribute__((aligned(16))) float2 lds[kRowTile * kLdsStride];
     __shared__ float ldsK[kRowTile];            // per-row shifts of the item
     __shared__ Mom ldsM[kRowGroup * kRowTile];  // row-owner running moments
@@ -345,7 +349,9 @@ __global__ __launch_bounds__(64 * KS, PD > 1 ? 1 : 2) void k_pw_conv(
     // (KS == 1: compile-time wave 0 and the whole K range)
     const int lane = threadIdx.x & 63, v = KS > 1 ? (int)threadIdx.x >> 6 : 0;
     const int h = lane >> 5, j = lane & 31;
-    const int kb = KS > 1 ? v * kseg : 0, ke = KS > 1 ? min(Kpad, kb + kseg) : Kpad;
+    const int kzb = (int)blockIdx.z * kzseg, kze = min(Kpad, kzb + kzseg);
+    const int kb = KS > 1 ? kzb + v * kseg : kzb, ke = KS > 1 ? min(kze, kb + kseg) : kze;
+    z += (int64_t)blockIdx.z * zslice;
     const int64_t n = (int64_t)blockIdx.x / cpp;
     const int64_t kc = (int64_t)blockIdx.x - n * cpp;
     const int64_t px0 = kc * chunk;
@@ -398,6 +404,78 @@ __global__ __launch_bounds__(64 * KS, PD > 1 ? 1 : 2) void k_pw_conv(
                 const Mom m = ldsM[g * kRowTile + lane];
                 if (row < C_out) part[(n * C_out + row) * cpp + kc] = make_double2(m.mean, m.m2);
             }
+        }
+    }
+}
+
+// Adds the KZ split-K slices of the convolution: z = bias + s_0 + s_1 + ...
+// (+ the old z with ACC), slices in order.  One wave per (sample, output
+// row, pixel chunk); with STATS it also writes the row's GroupNorm chunk
+// partial part[(n*C_out + row)*cpp + chunk] = (mean, M2), shifted by the
+// chunk's first value as the convolution epilogue does, the lanes' float
+// sums combined in float64 by a fixed xor tree.
+template <bool STATS, bool BIAS, bool ACC, bool V4>
+__global__ __launch_bounds__(256) void k_pw_kz_reduce(const float* __restrict__ slices,
+                                                      const float* __restrict__ bias,
+                                                      float* __restrict__ z,
+                                                      double2* __restrict__ part, int kz,
+                                                      int64_t zslice, int64_t C_out, int64_t HW,
+                                                      int64_t chunk, int64_t cpp) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (row >= C_out) return;  // whole waves; no block barrier below
+    const int64_t n = blockIdx.z, kc = blockIdx.x;
+    const int64_t p0 = kc * chunk, p1 = min(p0 + chunk, HW);
+    const int64_t base = (n * C_out + row) * HW;
+    const float b = BIAS ? bias[row] : 0.0f;
+    constexpr int V = V4 ? 4 : 1;
+    float shift = 0.0f, s = 0.0f, q = 0.0f;
+    for (int64_t p = p0 + (int64_t)lane * V; p < p1; p += 64 * V) {
+        float v[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[e] = b;
+        for (int k = 0; k < kz; ++k) {
+            const float* src = slices + (int64_t)k * zslice + base + p;
+            if (V4) {
+                const float4 u = *reinterpret_cast<const float4*>(src);
+                v[0] += u.x;
+                v[1] += u.y;
+                v[2] += u.z;
+                v[3] += u.w;
+            } else {
+                v[0] += src[0];
+            }
+        }
+        float* dst = z + base + p;
+        if (ACC) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) v[e] += dst[e];
+        }
+        if (V4)
+            *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        else
+            dst[0] = v[0];
+        if (STATS) {
+            if (p == p0 + (int64_t)lane * V) shift = __shfl(v[0], 0);  // first round
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const float d = v[e] - shift;
+                s += d;
+                q = fmaf(d, d, q);
+            }
+        }
+    }
+    if (STATS) {
+        double S = s, Q = q;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            S += __shfl_xor(S, off);
+            Q += __shfl_xor(Q, off);
+        }
+        if (lane == 0) {
+            const double cnt = (double)(p1 - p0);
+            part[(n * C_out + row) * cpp + kc] =
+                make_double2((double)shift + S / cnt, fmax(Q - S * S / cnt, 0.0));
         }
     }
 }
@@ -865,13 +943,98 @@ hipError_t launch_pw_small(const float* x, const float* w, const float* bias, fl
 
 }  // namespace
 
+PwKz pw_kz_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk,
+                int kz_max) {
+    PwKz r;
+    if (kz_max < 2 || N == 0 || HW == 0 || C_out == 0 || N > 65535) return r;
+    const int64_t cpp = (HW + chunk - 1) / chunk;
+    const int64_t R = (C_out + kRowTile - 1) / kRowTile;
+    const int64_t groups = (R + kRowGroup - 1) / kRowGroup;
+    const int64_t rpw = N * cpp * groups >= 1024 ? kRowGroup : 1;
+    const int64_t tiles = N * cpp * ((R + rpw - 1) / rpw);
+    const int64_t ksteps = pw_kpad(C_in) / 8;
+    if (tiles >= kKzTiles) return r;
+    // four waves per block (one CU), blocks for about 2048 waves in all,
+    // at least two K steps per wave
+    int kz = 1;
+    while (2 * kz <= kz_max && tiles * 4 * (2 * kz) <= 2048 && ksteps >= 8 * (2 * kz)) kz *= 2;
+    if (kz > 1) r.kz = kz;
+    return r;
+}
+
+size_t pw_kz_bytes(int64_t N, int64_t C_out, int64_t HW, int kz) {
+    if (kz < 2) return 0;
+    return ((size_t)kz * (size_t)(N * C_out * HW) * sizeof(float) + 255) & ~(size_t)255;
+}
+
+size_t pw_kz_max_bytes(int64_t N, int64_t C_out, int64_t HW, int64_t chunk, int kz_max) {
+    // the largest C_in: any K big enough for kz_max
+    return pw_kz_bytes(N, C_out, HW, pw_kz_plan(N, (int64_t)1 << 20, C_out, HW, chunk, kz_max).kz);
+}
+
+namespace {
+// Small grids: KZ blocks per output tile, each taking a K segment with four
+// waves, write fp32 slices; k_pw_kz_reduce adds them (with the bias, the
+// old z, the GroupNorm partials).  Deterministic: fixed segments, slices
+// added in order.
+hipError_t launch_pw_kz(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out, int64_t HW,
+                        int64_t chunk, double2* part, bool accumulate, int kz, float* ws,
+                        hipStream_t s) {
+    const int64_t cpp = (HW + chunk - 1) / chunk;
+    const int64_t R = (C_out + kRowTile - 1) / kRowTile;
+    const int64_t groups = (R + kRowGroup - 1) / kRowGroup;
+    const int rpw = N * cpp * groups >= 1024 ? kRowGroup : 1;
+    const dim3 grid((unsigned)(N * cpp), (unsigned)((R + rpw - 1) / rpw), (unsigned)kz);
+    const bool fast = (HW % 4 == 0) && (C_in % 8 == 0) && ((uintptr_t)a.x % 16 == 0) &&
+                      ((uintptr_t)ws % 16 == 0) && ((uintptr_t)a.w % 16 == 0);
+    const int Kpad = pw_kpad(C_in), ksteps = Kpad / 8;
+    const int kzsteps = (ksteps + kz - 1) / kz;
+    const int kzseg = kzsteps * 8, kseg = (kzsteps + 3) / 4 * 8;
+    const int64_t zslice = N * C_out * HW;
+    bsel(fast, [&](auto F) {
+        k_pw_conv<F(), kPlain, false, 4, 1><<<grid, 256, 0, s>>>(
+            a.x, a.w, nullptr, ws, nullptr, C_in, C_out, HW, chunk, cpp, Kpad, rpw, kseg,
+            kzseg, zslice);
+    });
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const bool v4 = HW % 4 == 0 && (uintptr_t)a.z % 16 == 0 && (uintptr_t)ws % 16 == 0;
+    const dim3 rg((unsigned)cpp, (unsigned)((C_out + 3) / 4), (unsigned)N);
+    auto run = [&](auto ST, auto B, auto A) {
+        bsel(v4, [&](auto V) {
+            k_pw_kz_reduce<ST(), B(), A(), V()><<<rg, 256, 0, s>>>(ws, a.bias, a.z, part, kz,
+                                                                   zslice, C_out, HW, chunk, cpp);
+        });
+    };
+    bsel(a.bias != nullptr, [&](auto B) {
+        if (part)
+            run(std::true_type{}, B, std::false_type{});
+        else
+            bsel(accumulate, [&](auto A) { run(std::false_type{}, B, A); });
+    });
+    return hipGetLastError();
+}
+}  // namespace
+
 hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
                           int64_t HW, int64_t chunk, double2* part, bool accumulate,
-                          int64_t small, hipStream_t s, const char* name) {
+                          int64_t small, float* kz_ws, int kz_max, hipStream_t s,
+                          const char* name) {
     if (N == 0 || HW == 0 || C_out == 0) return hipSuccess;
     if (!part && pw_use_small(N, C_out, C_in, HW, small))
         return launch_pw_small(a.x, a.w, a.bias, a.z, N, C_in, C_out, HW, false, accumulate, s,
                                name ? name : "pw_conv_small");
+    if (kz_ws && part) {
+        const PwKz kp = pw_kz_plan(N, C_in, C_out, HW, chunk, kz_max);
+        if (kp.kz > 1) {
+            if (!name) name = part ? "pw_conv_gn_stats" : "pw_conv";
+            const int tok = prof_begin(s, name);
+            const hipError_t e =
+                launch_pw_kz(a, N, C_in, C_out, HW, chunk, part, accumulate, kp.kz, kz_ws, s);
+            prof_end(s, tok);
+            return e;
+        }
+    }
     const int64_t cpp = (HW + chunk - 1) / chunk;
     // A wave walks up to kRowGroup row tiles of its chunk (the chunk's x
     // stays in cache across them); when that leaves too few waves, each row
@@ -901,7 +1064,8 @@ hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_ou
     auto go = [&](auto F, auto M, auto B) {
         auto run = [&](auto K, auto D) {
             k_pw_conv<F(), M(), B(), K(), D()><<<grid, 64 * K(), 0, s>>>(
-                a.x, a.w, a.bias, a.z, part, C_in, C_out, HW, chunk, cpp, Kpad, rpw, kseg);
+                a.x, a.w, a.bias, a.z, part, C_in, C_out, HW, chunk, cpp, Kpad, rpw, kseg, Kpad,
+                0);
         };
         using D1 = std::integral_constant<int, 1>;
         if (ks == 4)
@@ -932,8 +1096,16 @@ hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_ou
     return hipGetLastError();
 }
 
-PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW) {
+PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW,
+                           int64_t chunk_dx, int kz_max) {
     PwBwdPlan p;
+    // dx = W^T dz: M = C_in outputs, K = C_out terms.  (Its split-K over
+    // blocks measured no gain: a plain 256 -> 128 output at 4096 pixels took
+    // 18.6 us with K over the four waves of a block, 14.3 + 4.2 us as four
+    // blocks' slices plus their reduce.  The statistics variant gains.)
+    p.chunk_dx = pw_pick_chunk(N, C_in, HW, chunk_dx);
+    p.kz_dx = pw_kz_plan(N, C_out, C_in, HW, p.chunk_dx, std::min(kz_max, 1)).kz;
+    p.kz_bytes = pw_kz_bytes(N, C_in, HW, p.kz_dx);
     p.tm = C_out <= 32 ? 1 : 2;
     p.tn = C_in <= 32 ? 1 : 2;
     p.tiles_co = (C_out + 32 * p.tm - 1) / (32 * p.tm);
@@ -955,11 +1127,13 @@ PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW) {
     return p;
 }
 
-size_t pw_bwd_workspace_bytes(const PwBwdPlan& p) { return p.wt_bytes + p.pw_bytes + p.pb_bytes; }
+size_t pw_bwd_workspace_bytes(const PwBwdPlan& p) {
+    return p.wt_bytes + p.pw_bytes + p.pb_bytes + p.kz_bytes;
+}
 
 hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N, int64_t C_in,
-                              int64_t C_out, int64_t HW, int64_t chunk_dx, bool accumulate_dx,
-                              int64_t small, hipStream_t s) {
+                              int64_t C_out, int64_t HW, bool accumulate_dx, int64_t small,
+                              hipStream_t s) {
     if (N == 0 || HW == 0 || C_out == 0 || C_in == 0) return hipSuccess;
     char* ws = static_cast<char*>(a.ws);
     float* wt = reinterpret_cast<float*>(ws);
@@ -977,9 +1151,11 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
         prof_end(s, tok);
         // dx = W^T dz: the forward kernel with dz as input and W^T as weights
         PwArgs fa{a.dz, wt, nullptr, a.dx};
-        hipError_t e = launch_pw_conv(fa, N, C_out, C_in, HW,
-                                      pw_pick_chunk(N, C_in, HW, chunk_dx), nullptr,
-                                      accumulate_dx, 0, s, "pw_conv_dgrad");
+        float* kz_ws = p.kz_dx > 1 ? reinterpret_cast<float*>(ws + p.wt_bytes + p.pw_bytes +
+                                                               p.pb_bytes)
+                                   : nullptr;
+        hipError_t e = launch_pw_conv(fa, N, C_out, C_in, HW, p.chunk_dx, nullptr,
+                                      accumulate_dx, 0, kz_ws, p.kz_dx, s, "pw_conv_dgrad");
         if (e != hipSuccess) return e;
     }
     if ((a.dw || a.db) && pw_use_small_wgrad(N, C_in, C_out, HW, small)) {

@@ -43,6 +43,7 @@ TUNE_PW_CHUNK = 8
 TUNE_SMALL_UNIT = 9
 TUNE_PW_SMALL = 10
 TUNE_FOLD_MAX = 11
+TUNE_PW_SPLITK = 12
 
 
 class SoarUnavailable(RuntimeError):

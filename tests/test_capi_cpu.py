@@ -176,8 +176,18 @@ def test_pw_conv_workspace_bytes(L):
     # 16 B, then plane sums, unit sums and mean residuals (256-byte aligned)
     assert soar_gn.pw_conv_gn_workspace_bytes(1, 64, 2048 * 2048, 16) == (
         262144 * 16 + 1024 + 2 * 256)
-    # a plane shorter than the chunk is one chunk
-    assert soar_gn.pw_conv_gn_workspace_bytes(2, 8, 100, 2) == 256 + 256 + 256 + 256
+    # a plane shorter than the chunk is one chunk; a grid this small (2
+    # tiles) may split K over up to 8 blocks, so 8 fp32 slices of z follow
+    assert soar_gn.pw_conv_gn_workspace_bytes(2, 8, 100, 2) == (
+        256 + 256 + 256 + 256 + 8 * 2 * 8 * 100 * 4)
+    soar_gn.tune(soar_gn.TUNE_PW_SPLITK, 1)
+    try:
+        assert soar_gn.pw_conv_gn_workspace_bytes(2, 8, 100, 2) == 256 + 256 + 256 + 256
+    finally:
+        soar_gn.tune(soar_gn.TUNE_PW_SPLITK, 8)
+    assert L.soar_gn_tune(soar_gn.TUNE_PW_SPLITK, 0) == soar_gn.SOAR_EINVAL
+    assert L.soar_gn_tune(soar_gn.TUNE_PW_SPLITK, 9) == soar_gn.SOAR_EINVAL
+    assert soar_gn.tune_get(soar_gn.TUNE_PW_SPLITK) == 8
     assert soar_gn.pw_conv_gn_workspace_bytes(1, 6, 10, 4) == 0  # C_out % G != 0
     assert soar_gn.pw_conv_gn_workspace_bytes(0, 6, 10, 3) == 0
 

@@ -20,16 +20,22 @@ pytestmark = pytest.mark.gpu
 U32 = 2.0 ** -24
 
 
-@pytest.fixture(params=["default", "mfma"])
+@pytest.fixture(params=["default", "mfma", "mfma_no_splitk"])
 def pw_path(request, gpu):
     """Runs a test with the default choice between the SIMT and the MFMA
-    kernels, and with the MFMA kernels forced (SOAR_TUNE_PW_SMALL = 0; small
-    grids then split K over the waves of a block)."""
+    kernels, with the MFMA kernels forced (SOAR_TUNE_PW_SMALL = 0; small
+    grids then split K over blocks where a workspace holds the slices, and
+    over the waves of a block), and with the MFMA kernels forced and K split
+    only inside blocks (SOAR_TUNE_PW_SPLITK = 1)."""
     old = gpu.tune_get(gpu.TUNE_PW_SMALL)
-    if request.param == "mfma":
+    old_kz = gpu.tune_get(gpu.TUNE_PW_SPLITK)
+    if request.param != "default":
         gpu.tune(gpu.TUNE_PW_SMALL, 0)
+    if request.param == "mfma_no_splitk":
+        gpu.tune(gpu.TUNE_PW_SPLITK, 1)
     yield request.param
     gpu.tune(gpu.TUNE_PW_SMALL, old)
+    gpu.tune(gpu.TUNE_PW_SPLITK, old_kz)
 
 
 def rng_inputs(seed, N, C_in, C_out, HW, bias=True, kind="normal"):
@@ -101,6 +107,10 @@ FUSED_SHAPES = [
     (1, 64, 64, 70000, 16, "offset", True),    # |mean| / std ~ 1e5
     (1, 130, 72, 4096, 8, "normal", True),     # general path, two row tiles
     (3, 16, 32, 1024, 8, "normal", True),      # exactly one chunk per plane
+    # small grids with K >= 128: K split over blocks (slices + reduce)
+    (1, 256, 128, 4096, 16, "normal", True),   # the Nano LKR at 1024^2, stride 16
+    (1, 512, 256, 1024, 32, "offset", True),   # stride 32; large |mean|
+    (1, 200, 72, 1000, 8, "normal", False),    # general path (C_in % 8), ragged HW
 ]
 
 
@@ -252,6 +262,8 @@ BWD_SHAPES = [
     (1, 64, 128, 2048),     # two row tiles of dW / dx
     (1, 130, 72, 4096),     # C_in % 8 != 0 for the forward; dx K = 72
     (3, 24, 8, 333),
+    (1, 128, 256, 4096),    # dx: K = 256 over the waves of a block (small grid)
+    (1, 72, 200, 1000),     # dx: general path, small grid
 ]
 
 
@@ -272,8 +284,9 @@ def test_pw_conv_backward_matches_oracle(gpu, oracle, pw_path, N, C_in, C_out, H
         assert ratio[i] <= 1.0, f"{name} err {err[i]:.3e} > bound {b.reshape(-1)[i]:.3e} at {i}"
 
 
-def test_pw_conv_backward_accumulates(gpu, oracle, pw_path):
-    N, C_in, C_out, HW = 1, 32, 32, 1000
+@pytest.mark.parametrize("C_in,C_out,HW", [(32, 32, 1000), (128, 256, 2048)])
+def test_pw_conv_backward_accumulates(gpu, oracle, pw_path, C_in, C_out, HW):
+    N = 1
     r = np.random.default_rng(4)
     dz = r.standard_normal((N, C_out, HW)).astype(np.float32)
     x = r.standard_normal((N, C_in, HW)).astype(np.float32)
@@ -382,8 +395,10 @@ SMALL_PW_SHAPES = [
 @pytest.fixture
 def restore_pw_small(gpu):
     old = gpu.tune_get(gpu.TUNE_PW_SMALL)
+    old_kz = gpu.tune_get(gpu.TUNE_PW_SPLITK)
     yield
     gpu.tune(gpu.TUNE_PW_SMALL, old)
+    gpu.tune(gpu.TUNE_PW_SPLITK, old_kz)
 
 
 def _assert_bwd(got, truth, bounds, what, base=None):
@@ -405,7 +420,8 @@ def _assert_bwd(got, truth, bounds, what, base=None):
 def test_pw_small_planes_match_oracle(gpu, oracle, restore_pw_small, N, C_in, C_out, HW, bias):
     """Forward, fused CBA forward and backward of small convolutions, through
     the SIMT kernels (limit 2^40) and through the MFMA kernels (limit 0),
-    each against the oracle's float64 results within the fp32 bounds above."""
+    with and without K split over blocks, each against the oracle's float64
+    results within the fp32 bounds above."""
     print(f"pw small N={N} C_in={C_in} C_out={C_out} HW={HW}", flush=True)
     x, w, b = rng_inputs(N * 31 + C_in + HW, N, C_in, C_out, HW, bias)
     r = np.random.default_rng(HW + C_out)
@@ -416,14 +432,20 @@ def test_pw_small_planes_match_oracle(gpu, oracle, restore_pw_small, N, C_in, C_
     bd = dev(b) if bias else None
     truth_b = oracle.conv1x1_bwd_f64(dz, x, w, N, C_in, C_out, HW)
     bounds = bwd_bounds(dz, x, w)
-    for lim in (1 << 40, 0):
+    for lim, kz in ((1 << 40, 8), (0, 8), (0, 1)):
         gpu.tune(gpu.TUNE_PW_SMALL, lim)
-        what = f"limit {lim}"
+        gpu.tune(gpu.TUNE_PW_SPLITK, kz)
+        what = f"limit {lim} splitk {kz}"
         z = gpu.pw_conv_forward(dev(x), dev(w), bd)
         assert_z(host(z), x, w, b, oracle, what)
         zf, y, st = gpu.pw_conv_gn_silu_forward(dev(x), dev(w), bd, dev(gamma), dev(beta), G,
                                                 eps=EPS)
-        assert np.array_equal(host(zf), host(z)), what  # one kernel behind both entries
+        if lim == 0 and kz > 1:
+            # the fused entry may split K over blocks (its workspace holds the
+            # slices), the plain entry has no workspace: other summation order
+            assert_z(host(zf), x, w, b, oracle, what + " fused")
+        else:
+            assert np.array_equal(host(zf), host(z)), what  # one kernel behind both entries
         y_t, mean_t, rstd_t = oracle.gn_silu_fwd_f64(host(zf), gamma, beta, N, C_out, HW, G,
                                                      EPS, silu=True)
         assert_stats(host(st.mean), host(st.rstd), mean_t, rstd_t, what)
@@ -452,7 +474,8 @@ def test_pw_small_planes_match_oracle(gpu, oracle, restore_pw_small, N, C_in, C_
 DETERMINISM_CASES = [
     # (N, C_in, C_out, HW, limit): which path runs
     (1, 256, 512, 16, None),        # SIMT forward / dx / weight gradient (K split over waves)
-    (1, 256, 128, 4096, None),      # MFMA, split K over 4 waves (small grid), statistics
+    (1, 256, 128, 4096, None),      # MFMA small grid: K over 4 blocks x 4 waves, slice reduce
+                                    # with the statistics; dx K over the waves of a block
     (1, 64, 64, 262144, None),      # MFMA, two K steps in flight (large grid)
     (3, 24, 40, 1000, 0),           # MFMA forced, general shapes
 ]
