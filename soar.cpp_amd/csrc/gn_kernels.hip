@@ -478,6 +478,9 @@ struct FoldArgs {
     float* dbeta;
     int64_t N, chunk, cpp;
     float eps;
+    // backward without FOLD: the per-plane sums, non-null when the dx
+    // launch also runs k_param_finish's sums (every plane sum is final)
+    const double2* plane_sums;
 };
 
 template <bool VEC, bool SILU, bool RES, bool NT, bool NTL, bool FOLD>
@@ -720,6 +723,17 @@ __global__ __launch_bounds__(kThreads2) void k_bwd_dx(
             fold_param(k.c, fa.part, fa.N, C, fa.cpp, fa.dgamma, fa.dbeta);
     } else {
         S = unit_sums[k.u];
+        if (fa.plane_sums && k.n == 0 && ck.off == 0 && threadIdx.x == 0) {
+            // k_param_finish for channel c, same sums in the same order
+            double sa = 0.0, sb = 0.0;
+            for (int64_t n = 0; n < fa.N; ++n) {
+                const double2 v = fa.plane_sums[n * C + k.c];
+                sa += v.x;
+                sb += v.y;
+            }
+            fa.dbeta[k.c] = (float)((double)fa.dbeta[k.c] + sa);
+            fa.dgamma[k.c] = (float)((double)fa.dgamma[k.c] + sb);
+        }
     }
     const double Md = (double)(cpg * HW);
     const float mu = k.mu, r = k.r, e = k.e, gm = k.gm, bt = k.bt;
@@ -1154,7 +1168,7 @@ void launch_apply(const Plan& p, const Tuning& t, const FwdArgs& a, const float*
     const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
     const dim3 grid((unsigned)nb);
     const FoldArgs fa{ws_view(p, a.ws).part, a.mean, a.rstd, a.mean_lo, nullptr, nullptr,
-                      p.N, p.chunk, p.cpp, a.eps};
+                      p.N, p.chunk, p.cpp, a.eps, nullptr};
     bsel(p.vec4, [&](auto V) {
         bsel(silu, [&](auto S) {
             bsel(res, [&](auto R) {
@@ -1174,13 +1188,14 @@ void launch_apply(const Plan& p, const Tuning& t, const FwdArgs& a, const float*
 
 // fold: S1 / S2 and dgamma / dbeta come from the partials in the workspace.
 void launch_dx(const Plan& p, const Tuning& t, const BwdArgs& a, const double2* unit_sums,
-               int64_t block0, int64_t nb, hipStream_t s, bool fold = false) {
+               int64_t block0, int64_t nb, hipStream_t s, bool fold = false,
+               const double2* param_sums = nullptr) {
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
     const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
     const bool accum = (a.flags & SOAR_GN_ACCUMULATE_DX) != 0;
     const dim3 grid((unsigned)nb);
     const FoldArgs fa{ws_view(p, a.ws).part, nullptr, nullptr, nullptr, a.dgamma, a.dbeta,
-                      p.N, p.chunk, p.cpp, 0.0f};
+                      p.N, p.chunk, p.cpp, 0.0f, fold ? nullptr : param_sums};
     bsel(p.vec4, [&](auto V) {
         bsel(silu, [&](auto S) {
             bsel(res, [&](auto R) {
@@ -1514,6 +1529,7 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hip
         prof_end(s, tok);
         return hipGetLastError();
     }
+    bool param_in_dx = false;
     if (t.streams >= 2 && p.units > p.upb_bwd) {
         Pipe* pp = nullptr;
         SOAR_TRY(pipe_for_device(&pp));
@@ -1536,13 +1552,17 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hip
             SOAR_TRY(hipEventRecord(pp->second[bi % 4], s));
         }
     } else {
+        // one batch: its dx launch runs after every plane sum is final, so
+        // it also finishes dgamma / dbeta (no k_param_finish launch)
+        param_in_dx = a.dx && a.dgamma && p.units <= p.upb_bwd;
         int64_t prev_u0 = 0, prev_nu = 0;
         for (int64_t u0 = 0;; u0 += p.upb_bwd) {
             const int64_t nu = u0 < p.units ? std::min(p.upb_bwd, p.units - u0) : 0;
             if (nu + prev_nu > 0) launch_reduce(p, a, w, prev_u0, prev_nu, u0, nu, s);
             if (prev_nu > 0 && a.dx) {
                 const int tok = prof_begin(s, dx_name);
-                launch_dx(p, t, a, w.unit_sums, prev_u0 * bpu2, prev_nu * bpu2, s);
+                launch_dx(p, t, a, w.unit_sums, prev_u0 * bpu2, prev_nu * bpu2, s, false,
+                          param_in_dx ? w.plane_sums : nullptr);
                 prof_end(s, tok);
             }
             if (nu == 0) break;
@@ -1550,7 +1570,7 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hip
             prev_nu = nu;
         }
     }
-    if (a.dgamma) {
+    if (a.dgamma && !param_in_dx) {
         const int tok = prof_begin(s, "gn_param_finish");
         k_param_finish<<<dim3((unsigned)((p.C + 255) / 256)), 256, 0, s>>>(
             w.plane_sums, a.dgamma, a.dbeta, p.N, p.C);
