@@ -110,7 +110,7 @@ FUSED_SHAPES = [
     # small grids with K >= 128: K split over blocks (slices + reduce)
     (1, 256, 128, 4096, 16, "normal", True),   # the Nano LKR at 1024^2, stride 16
     (1, 512, 256, 1024, 32, "offset", True),   # stride 32; large |mean|
-    (1, 200, 72, 1000, 8, "normal", False),    # general path (C_in % 8), ragged HW
+    (1, 300, 72, 1000, 8, "normal", False),    # general path (C_in % 8), ragged HW
 ]
 
 
