@@ -151,10 +151,12 @@ int64_t pw_pick_chunk(int64_t N, int64_t C_out, int64_t HW, int64_t max_chunk);
 // (pw_kz_plan) and a second kernel adds their fp32 slices and writes the
 // statistics (a 256 -> 128 output at 4096 pixels: 25.8 us with K over the
 // four waves of a block, 14.3 + 4.5 us this way).
+// `wt`: a.w holds the weights transposed, [C_in][C_out] (element (co, ci)
+// at w[ci * C_out + co]); no bias, no statistics, no split over blocks.
 hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
                           int64_t HW, int64_t chunk, double2* part, bool accumulate,
                           int64_t small, float* kz_ws, int kz_max, hipStream_t s,
-                          const char* name = nullptr);
+                          const char* name = nullptr, bool wt = false);
 // Cross-block split-K of the MFMA convolution (kz = 1: not used).
 struct PwKz {
     int kz = 1;

@@ -90,7 +90,11 @@ __device__ __forceinline__ int tile_row(int mt, int r, int h) {
 // branch in the K loop.  A lane past the end of the plane loads the plane's
 // last 16 bytes and weight rows past C_out load row C_out - 1.  The general
 // path guards every scalar access and loads zeros instead.
-enum PwMode { kPlain = 0, kStats = 1, kAccum = 2 };
+// kPlainT / kAccumT: kPlain / kAccum with the weights given transposed,
+// element (row m, channel k) at w[k * C_out + m] (dx = W^T dz straight from
+// W, no transpose kernel; the A operand then takes four 4-byte loads per
+// row and K step instead of one 16-byte load).
+enum PwMode { kPlain = 0, kStats = 1, kAccum = 2, kPlainT = 3, kAccumT = 4 };
 
 template <bool FAST, int MODE, bool BIAS, int KS, int PD>
 __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const float* __restrict__ ws,
@@ -99,7 +103,8 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
                                         int64_t C_out, int64_t HW, int Kpad, int kb, int ke,
                                         int v, float2* lds, float* ldsK, float* red) {
     // xs = x + n*C_in*HW + p0, ws = w + row0*C_in, zs = z + (n*C_out + row0)*HW + p0
-    constexpr bool STATS = MODE == kStats, ACC = MODE == kAccum;
+    constexpr bool STATS = MODE == kStats, ACC = MODE == kAccum || MODE == kAccumT;
+    constexpr bool TW = MODE == kPlainT || MODE == kAccumT;
     const bool lane_px = p0 + 4 * j < HW;
     const uint32_t hw4 = (uint32_t)HW * 4u;  // bytes per channel plane
     // lane byte offsets: x at channel 4h, pixel 4j (clamped into the plane)
@@ -107,8 +112,12 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
                         4u * (uint32_t)(lane_px ? 4 * j : (FAST ? (int)(HW - 4 - p0) : 0));
     const int64_t rlim = C_out - 1 - row0;  // last valid tile row
     const bool w0ok = j <= rlim, w1ok = 32 + j <= rlim;
-    const uint32_t wo0 = ((uint32_t)(w0ok ? j : (int)rlim) * (uint32_t)C_in + 4u * h) * 4u;
-    const uint32_t wo1 = ((uint32_t)(w1ok ? 32 + j : (int)rlim) * (uint32_t)C_in + 4u * h) * 4u;
+    // A-operand byte offsets: row-major W (channels 4h..4h+3 of the row in
+    // one 16-byte load), or with TW the row's element of channel 4h
+    const uint32_t r0 = (uint32_t)(w0ok ? j : (int)rlim), r1 = (uint32_t)(w1ok ? 32 + j : (int)rlim);
+    const uint32_t wo0 = TW ? (4u * h * (uint32_t)C_out + r0) * 4u : (r0 * (uint32_t)C_in + 4u * h) * 4u;
+    const uint32_t wo1 = TW ? (4u * h * (uint32_t)C_out + r1) * 4u : (r1 * (uint32_t)C_in + 4u * h) * 4u;
+    const uint32_t wq = (uint32_t)C_out * 4u;  // TW: bytes from one channel to the next
     const uint32_t zo = (uint32_t)h * 4u * hw4 + 16u * (uint32_t)j;
 
     // (the bias loads stay inside the item instead of being hoisted out of
@@ -145,12 +154,24 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
             const bool live = kk < Kpad;
             const int kc = live ? kk : 0;
             const auto rw = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<float*>(ws + kc), (short)0, live ? 0x7fffffff : 0, kRsrcWord3);
+                const_cast<float*>(TW ? ws + (int64_t)kc * C_out : ws + kc), (short)0,
+                live ? 0x7fffffff : 0, kRsrcWord3);
             const auto rx = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float*>(xs + (int64_t)kc * HW), (short)0, live ? 0x7fffffff : 0,
                 kRsrcWord3);
-            a[0] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo0, 0, 0));
-            a[1] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo1, 0, 0));
+            if (TW) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    // (the channel step as the scalar offset: no extra VGPRs)
+                    a[0][q] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rw, wo0, q * wq, 0));
+                    a[1][q] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rw, wo1, q * wq, 0));
+                }
+            } else {
+                a[0] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo0, 0, 0));
+                a[1] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo1, 0, 0));
+            }
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 b[q] = __builtin_bit_cast(
@@ -160,8 +181,10 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
             for (int q = 0; q < 4; ++q) {
                 const int64_t ci = kk + 4 * h + q;
                 const bool cv = ci < C_in;
-                a[0][q] = (cv && w0ok) ? ws[(int64_t)j * C_in + ci] : 0.0f;
-                a[1][q] = (cv && w1ok) ? ws[(int64_t)(32 + j) * C_in + ci] : 0.0f;
+                a[0][q] = (cv && w0ok) ? (TW ? ws[ci * C_out + j] : ws[(int64_t)j * C_in + ci]) : 0.0f;
+                a[1][q] = (cv && w1ok) ? (TW ? ws[ci * C_out + 32 + j]
+                                             : ws[(int64_t)(32 + j) * C_in + ci])
+                                       : 0.0f;
                 const float* xr = xs + ci * HW + 4 * j;
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
@@ -192,7 +215,7 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
     const int klast = FAST ? ke : ke - 8;
     auto sched = [] {
         if (FAST) {
-            __builtin_amdgcn_sched_group_barrier(0x020, 6, 0);  // 6 vector loads
+            __builtin_amdgcn_sched_group_barrier(0x020, TW ? 12 : 6, 0);  // the vector loads
             __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);  // then 32 MFMAs
         }
     };
@@ -328,14 +351,15 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
 // accumulators in order and runs the epilogue): used when the output has
 // too few tiles to occupy the chip.  PD: K steps whose loads are in flight
 // while a step's MFMAs run (PD > 1 runs one wave per SIMD, which leaves
-// room for the extra operand buffers and the accumulators in AGPRs).  Byte
+// room for the extra operand buffers and the accumulators in AGPRs; KS > 1
+// too: at two waves per SIMD those variants spilled 21-30 registers).  Byte
 // offsets inside one sample's planes must fit in 32 bits (checked by the
 // host with pw_offsets_fit).  Cross-block split-K: block z of a grid with
 // gridDim.z > 1 takes the K steps [z kzseg, (z + 1) kzseg) (its KS waves
 // split them again) and writes its products to the slice z + z * zslice;
 // k_pw_kz_reduce adds the slices.
 template <bool FAST, int MODE, bool BIAS, int KS, int PD>
-__global__ __launch_bounds__(64 * KS, PD > 1 ? 1 : 2) void k_pw_conv(
+__global__ __launch_bounds__(64 * KS, PD > 1 || KS > 1 ? 1 : 2) void k_pw_conv(
     const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ bias, float* __restrict__ z, double2* __restrict__ part,
     int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk, int64_t cpp, int Kpad, int rpw,
@@ -371,7 +395,8 @@ __global__ __launch_bounds__(64 * KS, PD > 1 ? 1 : 2) void k_pw_conv(
             const int nvalid = (int)min<int64_t>(kItem, HW - p0);
             for (int g = 0; g < nrt; ++g) {
                 const int64_t row0 = (rg + g) * kRowTile;
-                pw_item<FAST, MODE, BIAS, KS, PD>(xn + p0, w + row0 * C_in, bias,
+                constexpr bool TW = MODE == kPlainT || MODE == kAccumT;
+                pw_item<FAST, MODE, BIAS, KS, PD>(xn + p0, TW ? w + row0 : w + row0 * C_in, bias,
                                                zn + row0 * HW + p0, row0, p0, h, j, C_in, C_out,
                                                HW, Kpad, kb, ke, v, lds, ldsK, red);
                 if (STATS) {
@@ -1021,7 +1046,7 @@ hipError_t launch_pw_kz(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
 hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
                           int64_t HW, int64_t chunk, double2* part, bool accumulate,
                           int64_t small, float* kz_ws, int kz_max, hipStream_t s,
-                          const char* name) {
+                          const char* name, bool wt) {
     if (N == 0 || HW == 0 || C_out == 0) return hipSuccess;
     if (!part && pw_use_small(N, C_out, C_in, HW, small))
         return launch_pw_small(a.x, a.w, a.bias, a.z, N, C_in, C_out, HW, false, accumulate, s,
@@ -1083,7 +1108,12 @@ hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_ou
     using S = std::integral_constant<int, kStats>;
     using A = std::integral_constant<int, kAccum>;
     bsel(fast, [&](auto F) {
-        if (mode == kAccum) {
+        if (wt) {  // transposed weights: dx = W^T dz, no bias, no statistics
+            if (mode == kAccum)
+                go(F, std::integral_constant<int, kAccumT>{}, std::false_type{});
+            else
+                go(F, std::integral_constant<int, kPlainT>{}, std::false_type{});
+        } else if (mode == kAccum) {
             go(F, A{}, std::false_type{});
         } else {
             bsel(a.bias != nullptr, [&](auto B) {
@@ -1147,17 +1177,26 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
                                        accumulate_dx, s, "pw_conv_dgrad_small");
         if (e != hipSuccess) return e;
     } else if (a.dx) {
-        const int64_t E = C_in * C_out;
-        int tok = prof_begin(s, "pw_transpose");
-        k_transpose<<<dim3((unsigned)((E + 255) / 256)), 256, 0, s>>>(a.w, wt, C_out, C_in);
-        prof_end(s, tok);
-        // dx = W^T dz: the forward kernel with dz as input and W^T as weights
-        PwArgs fa{a.dz, wt, nullptr, a.dx};
+        // dx = W^T dz: the forward kernel with dz as input and W^T as
+        // weights.  Small grids read W in place (transposed-weight modes:
+        // no transpose launch, which costs them more than the extra
+        // loads); large grids transpose W into the workspace first.
+        const int64_t cpp = (HW + p.chunk_dx - 1) / p.chunk_dx;
+        const int64_t R = (C_in + kRowTile - 1) / kRowTile;
+        const bool in_place = N * cpp * R < kKzTiles;
+        if (!in_place) {
+            const int64_t E = C_in * C_out;
+            int tok = prof_begin(s, "pw_transpose");
+            k_transpose<<<dim3((unsigned)((E + 255) / 256)), 256, 0, s>>>(a.w, wt, C_out, C_in);
+            prof_end(s, tok);
+        }
+        PwArgs fa{a.dz, in_place ? a.w : wt, nullptr, a.dx};
         float* kz_ws = p.kz_dx > 1 ? reinterpret_cast<float*>(ws + p.wt_bytes + p.pw_bytes +
                                                                p.pb_bytes)
                                    : nullptr;
         hipError_t e = launch_pw_conv(fa, N, C_out, C_in, HW, p.chunk_dx, nullptr,
-                                      accumulate_dx, 0, kz_ws, p.kz_dx, s, "pw_conv_dgrad");
+                                      accumulate_dx, 0, kz_ws, p.kz_dx, s, "pw_conv_dgrad",
+                                      in_place);
         if (e != hipSuccess) return e;
     }
     if ((a.dw || a.db) && pw_use_small_wgrad(N, C_in, C_out, HW, small)) {
