@@ -352,14 +352,15 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
 // too few tiles to occupy the chip.  PD: K steps whose loads are in flight
 // while a step's MFMAs run (PD > 1 runs one wave per SIMD, which leaves
 // room for the extra operand buffers and the accumulators in AGPRs; KS > 1
-// too: at two waves per SIMD those variants spilled 21-30 registers).  Byte
+// and the general path too: at two waves per SIMD those variants spilled
+// 21-89 registers).  Byte
 // offsets inside one sample's planes must fit in 32 bits (checked by the
 // host with pw_offsets_fit).  Cross-block split-K: block z of a grid with
 // gridDim.z > 1 takes the K steps [z kzseg, (z + 1) kzseg) (its KS waves
 // split them again) and writes its products to the slice z + z * zslice;
 // k_pw_kz_reduce adds the slices.
 template <bool FAST, int MODE, bool BIAS, int KS, int PD>
-__global__ __launch_bounds__(64 * KS, PD > 1 || KS > 1 ? 1 : 2) void k_pw_conv(
+__global__ __launch_bounds__(64 * KS, PD > 1 || KS > 1 || !FAST ? 1 : 2) void k_pw_conv(
     const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ bias, float* __restrict__ z, double2* __restrict__ part,
     int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk, int64_t cpp, int Kpad, int rpw,
