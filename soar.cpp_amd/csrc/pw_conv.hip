@@ -660,12 +660,22 @@ __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
 // [w*G/16, (w+1)*G/16) with each lane on one column (a 256-byte row segment
 // per load, eight loads in flight), then the 16 wave sums are added in
 // order.
-__global__ __launch_bounds__(1024) void k_sum_partials(const float* __restrict__ part,
-                                                       float* __restrict__ out, int64_t E,
+// Two tables in one launch: blocks [0, nb0) add table 0 (part0 -> out0, E0
+// entries), the rest table 1 (the dW and db partials of one weight
+// gradient).
+__global__ __launch_bounds__(1024) void k_sum_partials(const float* __restrict__ part0,
+                                                       float* __restrict__ out0, int64_t E0,
+                                                       int64_t nb0,
+                                                       const float* __restrict__ part1,
+                                                       float* __restrict__ out1, int64_t E1,
                                                        int64_t G) {
     __shared__ double lds[16][64];
+    const bool first = (int64_t)blockIdx.x < nb0;
+    const float* __restrict__ part = first ? part0 : part1;
+    float* __restrict__ out = first ? out0 : out1;
+    const int64_t E = first ? E0 : E1;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+    const int64_t e = ((int64_t)blockIdx.x - (first ? 0 : nb0)) * 64 + lane;
     const int64_t g0 = wv * G / 16, g1 = (wv + 1) * G / 16;
     double sum = 0.0;
     if (e < E) {
@@ -1233,13 +1243,11 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
         });
         prof_end(s, tok);
         tok = prof_begin(s, "pw_conv_wgrad_finish");
-        if (a.dw) {
-            const int64_t E = C_out * C_in;
-            k_sum_partials<<<dim3((unsigned)((E + 63) / 64)), 1024, 0, s>>>(part_w, a.dw, E, p.G);
-        }
-        if (a.db)
-            k_sum_partials<<<dim3((unsigned)((C_out + 63) / 64)), 1024, 0, s>>>(part_b, a.db,
-                                                                                C_out, p.G);
+        // dW and db in one launch
+        const int64_t E = C_out * C_in;
+        const int64_t nbw = a.dw ? (E + 63) / 64 : 0, nbb = a.db ? (C_out + 63) / 64 : 0;
+        k_sum_partials<<<dim3((unsigned)(nbw + nbb)), 1024, 0, s>>>(part_w, a.dw, E, nbw, part_b,
+                                                                    a.db, C_out, p.G);
         prof_end(s, tok);
     }
     return hipGetLastError();
