@@ -48,6 +48,7 @@ typedef float f16 __attribute__((ext_vector_type(16)));
 constexpr int kRowTile = 64;    // output rows per pass (two 32-row tiles)
 constexpr int kItem = 128;      // pixels per item (four 32-column tiles)
 constexpr int kRowGroup = 4;    // row tiles whose statistics a lane keeps
+constexpr int kKzStepsPerWave = 2;  // least K steps per wave of a split over blocks (1 measured the same)
 constexpr int kKzTiles = 256;   // grids of fewer (64-row x chunk) tiles split K over blocks
 constexpr int kLdsStride = 34;  // float2 per LDS row: 32 lanes + 2 pad
 // Word 3 of a raw buffer descriptor on gfx9-family parts (gfx950 included):
@@ -995,7 +996,7 @@ PwKz pw_kz_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t chun
     // four waves per block (one CU), blocks for about 2048 waves in all,
     // at least two K steps per wave
     int kz = 1;
-    while (2 * kz <= kz_max && tiles * 4 * (2 * kz) <= 2048 && ksteps >= 8 * (2 * kz)) kz *= 2;
+    while (2 * kz <= kz_max && tiles * 4 * (2 * kz) <= 2048 && ksteps >= kKzStepsPerWave * 4 * (2 * kz)) kz *= 2;
     if (kz > 1) r.kz = kz;
     return r;
 }
