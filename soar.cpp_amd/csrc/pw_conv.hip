@@ -48,7 +48,7 @@ typedef float f16 __attribute__((ext_vector_type(16)));
 constexpr int kRowTile = 64;    // output rows per pass (two 32-row tiles)
 constexpr int kItem = 128;      // pixels per item (four 32-column tiles)
 constexpr int kRowGroup = 4;    // row tiles whose statistics a lane keeps
-constexpr int kKzStepsPerWave = 2;  // least K steps per wave of a split over blocks (1 measured the same)
+constexpr int kKzStepsPerWave = 2;  // least K steps per wave split over blocks (1: same time)
 constexpr int kKzTiles = 256;   // grids of fewer (64-row x chunk) tiles split K over blocks
 constexpr int kLdsStride = 34;  // float2 per LDS row: 32 lanes + 2 pad
 // Word 3 of a raw buffer descriptor on gfx9-family parts (gfx950 included):
