@@ -1045,12 +1045,10 @@ hipError_t launch_pw_kz(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_out,
                                                                    zslice, C_out, HW, chunk, cpp);
         });
     };
-    bsel(a.bias != nullptr, [&](auto B) {
-        if (part)
-            run(std::true_type{}, B, std::false_type{});
-        else
-            bsel(accumulate, [&](auto A) { run(std::false_type{}, B, A); });
-    });
+    // (launch_pw_conv splits over blocks only with the statistics; the
+    // kernel's plain and accumulate forms are kept for reuse)
+    (void)accumulate;
+    bsel(a.bias != nullptr, [&](auto B) { run(std::true_type{}, B, std::false_type{}); });
     return hipGetLastError();
 }
 }  // namespace
