@@ -80,6 +80,8 @@ CBA_CASES = [
     (64, 64, 128, 1),    # MFMA conv, split K, statistics in the epilogue
     (32, 64, 16, 1),     # SIMT conv, then the one-launch GroupNorm
     (32, 32, 64, 7),     # depthwise k7 (multi-tile kernels), then GroupNorm
+    (256, 128, 64, 1),   # MFMA conv, K split over blocks (slices + reduce with statistics),
+                         # dx reading W in place
 ]
 
 
