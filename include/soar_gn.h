@@ -61,10 +61,10 @@ SOAR_API int soar_is_device_available(void);
 /* ---- fused GroupNorm(+SiLU) ------------------------------------------- */
 
 /* Bytes of device workspace the fused entry points need for this shape
- * (0 for an empty tensor).  The workspace holds per-chunk partial moments,
- * per-plane and per-unit sums and per-unit tickets; it carries nothing
- * between calls, and two calls that overlap in time on the device must not
- * share one. */
+ * (0 for an empty tensor).  The workspace holds per-chunk partial moments
+ * and sums, per-plane and per-unit sums and the per-unit mean residuals; it
+ * carries nothing between calls, and two calls that overlap in time on the
+ * device must not share one. */
 SOAR_API size_t soar_gn_workspace_bytes(int64_t N, int64_t C, int64_t HW,
                                         int64_t G);
 
@@ -90,15 +90,19 @@ SOAR_API int soar_gn_silu_forward(const float* x, const float* gamma,
                                   size_t workspace_bytes, void* stream);
 
 /* Backward of soar_gn_silu_forward given upstream gradient dy, the forward
- * input x and the saved mean/rstd (and mean_lo, NULL = 0).  SiLU is
- * recomputed from x (nothing but x and the statistics is saved by the
- * forward).
+ * input x and the saved mean/rstd (and mean_lo).  SiLU is recomputed from
+ * x (nothing but x and the statistics is saved by the forward).
+ * mean_lo NULL: without SOAR_GN_SILU the backward recovers the residual
+ * itself (its reduction pass also sums x - mean, whose unit mean is the
+ * residual), so the results keep full accuracy when std << |mean|; with
+ * SOAR_GN_SILU it is taken as 0 (pass mean_lo for such inputs).
  *   dgamma[c] += sum_{n,hw} dz * xhat,  dbeta[c] += sum_{n,hw} dz
  *   dx = rstd*(gamma_c*dz - (S1 + xhat*S2)/M) [+ dy] [+ previous dx]
  * with dz the gradient at the GroupNorm output, xhat = (x-mean)*rstd,
  * S1 = sum_{c in g} gamma_c*sum dz, S2 = sum_{c in g} gamma_c*sum dz*xhat.
- * dx, dgamma, dbeta may be NULL (not wanted); dgamma and dbeta must be both
- * NULL or both non-NULL.  dgamma/dbeta always accumulate (+=), summing over
+ * dx, dgamma, dbeta may each be NULL (not wanted), as the reference guards
+ * each parameter gradient on its own (normalization_kernels.cu:142-152,
+ * 262-265).  dgamma/dbeta always accumulate (+=), summing over
  * samples, as the reference's parameter-gradient kernels do
  * (normalization_kernels.cu:151-152, tensor.cpp:173-192).
  * Replaces: silu_backward (cuda_kernels.hpp:20) followed by
@@ -121,9 +125,8 @@ SOAR_API int soar_gn_silu_backward(const float* dy, const float* x,
  * different streams of one device must not overlap. */
 
 /* Replaces: group_norm_forward (cuda_kernels.hpp:82-84,
- * normalization_kernels.cu:93-111).  gamma/beta nullable.  Saves only the
- * fp32 mean, as the reference does, so its backward has the reference's
- * precision when std << |mean|. */
+ * normalization_kernels.cu:93-111).  gamma/beta nullable.  Saves the fp32
+ * mean and rstd, as the reference does; the output uses the exact mean. */
 SOAR_API int soar_group_norm_forward(const float* in, const float* gamma,
                                      const float* beta, float* out,
                                      float* saved_mean, float* saved_rstd,
@@ -132,7 +135,11 @@ SOAR_API int soar_group_norm_forward(const float* in, const float* gamma,
 
 /* Replaces: group_norm_backward (cuda_kernels.hpp:85-88,
  * normalization_kernels.cu:251-289).  grad_in, grad_gamma, grad_beta are
- * accumulated into (+=) and each may be NULL; gamma nullable. */
+ * accumulated into (+=) and each may be NULL; gamma nullable.  The fp32
+ * rounding residual of the saved mean is recovered from `in` (see
+ * soar_gn_silu_backward), so dgamma and grad_in keep full accuracy when
+ * std << |mean|, where the reference's fp32 path does not
+ * (src/nn/layers.cpp:704-707). */
 SOAR_API int soar_group_norm_backward(const float* grad_out, const float* in,
                                       const float* gamma,
                                       const float* saved_mean,

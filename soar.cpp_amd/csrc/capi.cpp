@@ -104,7 +104,7 @@ struct OwnedWs {
 std::mutex g_ws_mu;
 std::vector<OwnedWs> g_ws;
 
-int owned_workspace(size_t need, void** out) {
+int owned_workspace(size_t need, void** out, void* stream) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
@@ -112,6 +112,15 @@ int owned_workspace(size_t need, void** out) {
     if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
     OwnedWs& w = g_ws[dev];
     if (w.bytes < need) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(SOAR_EINVAL,
+                        "the library-owned workspace must grow to %zu bytes (hipMalloc), which "
+                        "a stream capture forbids; make one call of this shape before the "
+                        "capture",
+                        need);
         if (w.ptr) {
             e = hipFree(w.ptr);  // waits for work still using the old buffer
             w.ptr = nullptr;
@@ -358,9 +367,7 @@ SOAR_API int soar_gn_silu_backward(const float* dy, const float* x, const float*
     if (rc) return rc;
     if (flags & ~(SOAR_GN_SILU | SOAR_GN_RESIDUAL | SOAR_GN_ACCUMULATE_DX))
         return fail(SOAR_EINVAL, "unsupported backward flags 0x%x", flags);
-    if ((dgamma == nullptr) != (dbeta == nullptr))
-        return fail(SOAR_EINVAL, "dgamma and dbeta must be both NULL or both set");
-    if (elems == 0 || (!dx && !dgamma)) return ok();
+    if (elems == 0 || (!dx && !dgamma && !dbeta)) return ok();
     if ((rc = require_device())) return rc;
     const size_t tb = (size_t)elems * sizeof(float);
     const size_t sb = (size_t)(N * G) * sizeof(float);
@@ -396,7 +403,7 @@ SOAR_API int soar_group_norm_forward(const float* in, const float* gamma, const 
     size_t need = soar_gn_workspace_bytes(1, (int64_t)C, (int64_t)HW, (int64_t)num_groups);
     if (need == 0) return fail(SOAR_EINVAL, "shape is too large");
     void* ws = nullptr;
-    if ((rc = owned_workspace(need, &ws))) return rc;
+    if ((rc = owned_workspace(need, &ws, stream))) return rc;
     return soar_gn_silu_forward(in, gamma, beta, out, saved_mean, saved_rstd, nullptr, 1,
                                 (int64_t)C, (int64_t)HW, (int64_t)num_groups, eps, 0u, ws, need,
                                 stream);
@@ -415,7 +422,7 @@ SOAR_API int soar_group_norm_backward(const float* grad_out, const float* in,
     size_t need = soar_gn_workspace_bytes(1, (int64_t)C, (int64_t)HW, (int64_t)num_groups);
     if (need == 0) return fail(SOAR_EINVAL, "shape is too large");
     void* ws = nullptr;
-    if ((rc = owned_workspace(need, &ws))) return rc;
+    if ((rc = owned_workspace(need, &ws, stream))) return rc;
     return soar_gn_silu_backward(grad_out, in, gamma, nullptr, saved_mean, saved_rstd, nullptr,
                                  grad_in, grad_gamma, grad_beta, 1, (int64_t)C, (int64_t)HW,
                                  (int64_t)num_groups, SOAR_GN_ACCUMULATE_DX, ws, need, stream);
@@ -552,8 +559,12 @@ SOAR_API int soar_pw_conv_gn_silu_forward(const float* x, const float* weight,
     const soar::gn::PwKz kp = soar::gn::pw_kz_plan(N, C_in, C_out, HW, p.chunk, (int)t.pw_kz);
     if (kp.kz > 1) {
         const size_t off = kz_offset(soar::gn::workspace_bytes(p));
-        if (workspace_bytes >= off + soar::gn::pw_kz_bytes(N, C_out, HW, kp.kz))
+        const size_t end = off + soar::gn::pw_kz_bytes(N, C_out, HW, kp.kz);
+        if (workspace_bytes >= end) {
+            // the slices lie past the GroupNorm part checked above
+            if ((rc = check_dev(workspace, end, "workspace"))) return rc;
             kz_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + off);
+        }
     }
     hipError_t e = soar::gn::launch_pw_conv(pa, N, C_in, C_out, HW, p.chunk,
                                             soar::gn::ws_partials(p, workspace), false, 0, kz_ws,
@@ -638,7 +649,7 @@ SOAR_API int soar_conv2d_1x1_backward(const float* grad_out, const float* in, co
     int rc = require_device();
     if (rc) return rc;
     void* ws = nullptr;
-    if ((rc = owned_workspace(need, &ws))) return rc;
+    if ((rc = owned_workspace(need, &ws, stream))) return rc;
     return soar_pw_conv_backward(grad_out, in, weight, grad_in, grad_weight, grad_bias, 1,
                                  (int64_t)C_in, (int64_t)C_out, (int64_t)HW,
                                  SOAR_GN_ACCUMULATE_DX, ws, need, stream);
@@ -757,7 +768,7 @@ SOAR_API int soar_conv2d_dw_backward(const float* grad_out, const float* in, con
     if (need && (grad_weight || grad_bias)) {
         int rc = require_device();
         if (rc) return rc;
-        if ((rc = owned_workspace(need, &ws))) return rc;
+        if ((rc = owned_workspace(need, &ws, stream))) return rc;
     }
     return soar_dw_conv_backward(grad_out, in, weight, grad_in, grad_weight, grad_bias, 1,
                                  (int64_t)C, (int64_t)H_in, (int64_t)W_in, (int64_t)H_out,

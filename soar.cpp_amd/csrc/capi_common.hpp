@@ -32,7 +32,10 @@ int check_dev_opt(const void* p, size_t bytes, const char* name);
 bool aligned16(const void* p);
 // Library-owned workspace of the current device, grown to `need` bytes
 // (used by the entry points with the reference's workspace-free
-// signatures).  Callers on one device share it.
-int owned_workspace(size_t need, void** out);
+// signatures).  Callers on one device share it.  Growing it would call
+// hipFree / hipMalloc, so while `stream` is being captured into a graph a
+// grow is refused with SOAR_EINVAL instead (a capture may reuse a buffer
+// that an earlier call outside the capture already grew).
+int owned_workspace(size_t need, void** out, void* stream);
 
 }  // namespace soar::capi

@@ -446,6 +446,15 @@ __device__ double2 fold_unit_sums(int64_t u, const double2* __restrict__ part,
     return fold_block_sum2(a, b);
 }
 
+// dbeta[c] += sdz, dgamma[c] += sdzx; either output may be null (the
+// reference guards each on its own, normalization_kernels.cu:142-152).
+__device__ __forceinline__ void add_params(int64_t c, double sdz, double sdzx,
+                                           float* __restrict__ dgamma,
+                                           float* __restrict__ dbeta) {
+    if (dbeta) dbeta[c] = (float)((double)dbeta[c] + sdz);
+    if (dgamma) dgamma[c] = (float)((double)dgamma[c] + sdzx);
+}
+
 // dbeta[c] += sum over samples and chunks of channel c's sum(dz), dgamma[c]
 // += the same of sum(dz * xhat) (the k_param_finish step, for one channel).
 __device__ void fold_param(int64_t c, const double2* __restrict__ part, int64_t N, int64_t C,
@@ -458,10 +467,7 @@ __device__ void fold_param(int64_t c, const double2* __restrict__ part, int64_t 
         b += v.y;
     }
     const double2 r = fold_block_sum2(a, b);
-    if (threadIdx.x == 0) {
-        dbeta[c] = (float)((double)dbeta[c] + r.x);
-        dgamma[c] = (float)((double)dgamma[c] + r.y);
-    }
+    if (threadIdx.x == 0) add_params(c, r.x, r.y, dgamma, dbeta);
 }
 
 // ======================================================================
@@ -561,12 +567,39 @@ __global__ __launch_bounds__(kThreads2) void k_apply(
 // g, g + ngroups, ...), so the planes' loads are in flight together
 // instead of one plane after another; each group adds its planes'
 // weighted sums in plane order and thread 0 adds the groups in order.
+//
+// Mean residual recovery (part_x non-null: no SiLU and no saved mean_lo,
+// as behind the reference-signature group_norm_backward, whose forward
+// saves the fp32 mean alone).  The chunks then hold sum(dy * xhat32) with
+// xhat32 = (x - mu32) * r, and part_x the chunk sums of x - mu32.  Their
+// unit sum over M is lo = mean - mu32, so the true xhat is xhat32 + e with
+// e = -lo * r; since dz = dy does not depend on xhat,
+//   sum dz * xhat = sum dz * xhat32 + e * sum dz
+// corrects every plane exactly.  lo goes to lo_ws for the dx pass.
 // ======================================================================
 __device__ void finish_bwd_unit(int64_t u, const double2* __restrict__ part,
+                                const double* __restrict__ part_x,
                                 const float* __restrict__ gamma,
+                                const float* __restrict__ rstd, float* __restrict__ lo_ws,
                                 double2* __restrict__ plane_sums,
-                                double2* __restrict__ unit_sums, int64_t C, int64_t cpp,
-                                int64_t cpg, double* lds /*[2 * kThreads]*/) {
+                                double2* __restrict__ unit_sums, int64_t C, int64_t HW,
+                                int64_t cpp, int64_t cpg, double* lds /*[2 * kThreads]*/) {
+    double e = 0.0;
+    if (part_x) {
+        const int64_t P = cpg * cpp;
+        double sx = 0.0;
+        for (int64_t q = threadIdx.x; q < P; q += kThreads) sx += part_x[u * P + q];
+        sx = wave_sum(sx);
+        if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = sx;
+        __syncthreads();
+        sx = lds[0];
+#pragma unroll
+        for (int i = 1; i < kWaves; ++i) sx += lds[i];
+        __syncthreads();
+        const float lo = (float)(sx / (double)(cpg * HW));
+        e = (double)(-lo * rstd[u]);  // the dx pass's e, in its fp32 form
+        if (threadIdx.x == 0) lo_ws[u] = lo;
+    }
     int gs = 1;
     while (gs < 64 && gs < cpp) gs <<= 1;
     const int ngroups = kThreads / gs;
@@ -602,6 +635,7 @@ __device__ void finish_bwd_unit(int64_t u, const double2* __restrict__ part,
             B += __shfl_xor(B, off);
         }
         if (live && r == 0) {
+            B = fma(e, A, B);
             plane_sums[plane] = make_double2(A, B);
             const double gj = gamma ? (double)gamma[plane % C] : 1.0;
             S1 += gj * A;
@@ -623,34 +657,41 @@ __device__ void finish_bwd_unit(int64_t u, const double2* __restrict__ part,
     }
 }
 
-template <bool VEC, bool SILU>
+// LOREC: mean residual recovery (see finish_bwd_unit); also writes the
+// chunk sums of x - mu to part_x.  Only without SiLU, so dz = dy.
+template <bool VEC, bool SILU, bool LOREC>
 __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ gamma, const float* __restrict__ beta,
     const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ mean_lo, double2* __restrict__ part,
+    double* __restrict__ part_x, float* __restrict__ lo_ws,
     double2* __restrict__ plane_sums, double2* __restrict__ unit_sums, int64_t C, int64_t G,
     int64_t cpg, int64_t HW, int64_t chunk, int64_t cpp, int64_t fin_u0, int64_t fin_nu,
     int64_t block0) {
+    static_assert(!(SILU && LOREC), "the mean residual is recovered only when dz = dy");
     __shared__ float lds[2 * kWaves];
     __shared__ double ldsd[2 * kThreads];
     if ((int64_t)blockIdx.x < fin_nu) {
-        finish_bwd_unit(fin_u0 + blockIdx.x, part, gamma, plane_sums, unit_sums, C, cpp, cpg,
-                        ldsd);
+        finish_bwd_unit(fin_u0 + blockIdx.x, part, LOREC ? part_x : nullptr, gamma, rstd,
+                        lo_ws, plane_sums, unit_sums, C, HW, cpp, cpg, ldsd);
         return;
     }
     const int64_t b = block0 + (int64_t)blockIdx.x - fin_nu;
     const Chunk ck = chunk_of(b, HW, chunk, cpp);
-    const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
+    const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd,
+                                   LOREC ? nullptr : mean_lo);
     const float mu = k.mu, r = k.r, e = k.e, gm = k.gm, bt = k.bt;
     const int64_t base = ck.plane * HW + ck.off;
     const int t = threadIdx.x;
-    float sa0 = 0.f, sa1 = 0.f, sb0 = 0.f, sb1 = 0.f;
-    auto acc = [&](float g, float v, float& sa, float& sb) {
-        float xh = fmaf(v - mu, r, e);
+    float sa0 = 0.f, sa1 = 0.f, sb0 = 0.f, sb1 = 0.f, sc0 = 0.f, sc1 = 0.f;
+    auto acc = [&](float g, float v, float& sa, float& sb, float& sc) {
+        const float d = v - mu;
+        float xh = fmaf(d, r, e);
         float dz = SILU ? dsilu_fast(g, fmaf(gm, xh, bt)) : g;
         sa += dz;
         sb = fmaf(dz, xh, sb);
+        if (LOREC) sc += d;
     };
     if (VEC) {
         const f4* x4 = reinterpret_cast<const f4*>(x + base);
@@ -660,22 +701,29 @@ __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
         for (; i + kThreads < n4; i += 2 * kThreads) {
             f4 v0 = x4[i], v1 = x4[i + kThreads];
             f4 g0 = g4[i], g1 = g4[i + kThreads];
-            acc(g0.x, v0.x, sa0, sb0); acc(g0.y, v0.y, sa1, sb1);
-            acc(g0.z, v0.z, sa0, sb0); acc(g0.w, v0.w, sa1, sb1);
-            acc(g1.x, v1.x, sa0, sb0); acc(g1.y, v1.y, sa1, sb1);
-            acc(g1.z, v1.z, sa0, sb0); acc(g1.w, v1.w, sa1, sb1);
+            acc(g0.x, v0.x, sa0, sb0, sc0); acc(g0.y, v0.y, sa1, sb1, sc1);
+            acc(g0.z, v0.z, sa0, sb0, sc0); acc(g0.w, v0.w, sa1, sb1, sc1);
+            acc(g1.x, v1.x, sa0, sb0, sc0); acc(g1.y, v1.y, sa1, sb1, sc1);
+            acc(g1.z, v1.z, sa0, sb0, sc0); acc(g1.w, v1.w, sa1, sb1, sc1);
         }
         for (; i < n4; i += kThreads) {
             f4 v0 = x4[i], g0 = g4[i];
-            acc(g0.x, v0.x, sa0, sb0); acc(g0.y, v0.y, sa1, sb1);
-            acc(g0.z, v0.z, sa0, sb0); acc(g0.w, v0.w, sa1, sb1);
+            acc(g0.x, v0.x, sa0, sb0, sc0); acc(g0.y, v0.y, sa1, sb1, sc1);
+            acc(g0.z, v0.z, sa0, sb0, sc0); acc(g0.w, v0.w, sa1, sb1, sc1);
         }
     } else {
         const float* xp = x + base;
         const float* gp = dy + base;
-        for (int64_t i = t; i < ck.len; i += kThreads) acc(gp[i], xp[i], sa0, sb0);
+        for (int64_t i = t; i < ck.len; i += kThreads) acc(gp[i], xp[i], sa0, sb0, sc0);
     }
     float sa = sa0 + sa1, sb = sb0 + sb1;
+    if (LOREC) {
+        // the chunk's sum of x - mu first (its own exchange: block_sum2
+        // below ends with the block synchronised before lds is reused)
+        float sc = sc0 + sc1, dummy = 0.0f;
+        block_sum2(sc, dummy, lds);
+        if (t == 0) part_x[b] = (double)sc;
+    }
     block_sum2(sa, sb, lds);
     if (t == 0) part[b] = make_double2((double)sa, (double)sb);
 }
@@ -694,8 +742,7 @@ __global__ void k_param_finish(const double2* __restrict__ plane_sums,
         a += v.x;
         b += v.y;
     }
-    dbeta[c] = (float)((double)dbeta[c] + a);
-    dgamma[c] = (float)((double)dgamma[c] + b);
+    add_params(c, a, b, dgamma, dbeta);
 }
 
 // ======================================================================
@@ -719,7 +766,7 @@ __global__ __launch_bounds__(kThreads2) void k_bwd_dx(
     double2 S;
     if (FOLD) {
         S = fold_unit_sums(k.u, fa.part, gamma, C, cpg, fa.cpp);
-        if (fa.dgamma && k.n == 0 && ck.off == 0)
+        if ((fa.dgamma || fa.dbeta) && k.n == 0 && ck.off == 0)
             fold_param(k.c, fa.part, fa.N, C, fa.cpp, fa.dgamma, fa.dbeta);
     } else {
         S = unit_sums[k.u];
@@ -731,8 +778,7 @@ __global__ __launch_bounds__(kThreads2) void k_bwd_dx(
                 sa += v.x;
                 sb += v.y;
             }
-            fa.dbeta[k.c] = (float)((double)fa.dbeta[k.c] + sa);
-            fa.dgamma[k.c] = (float)((double)fa.dgamma[k.c] + sb);
+            add_params(k.c, sa, sb, fa.dgamma, fa.dbeta);
         }
     }
     const double Md = (double)(cpg * HW);
@@ -1017,17 +1063,19 @@ __global__ __launch_bounds__(NT) void k_small_finish_apply(
 // halves of 16 and dx reloads them (L2-resident): keeping both halves
 // alive across the reductions would not fit in 128 registers.  The channel
 // sums are added over samples in order into dgamma / dbeta at the end (as
-// k_param_finish).
+// k_param_finish).  lorec (no SiLU, no saved mean_lo): the unit's mean
+// residual is recovered from its sum of x - mu, as in finish_bwd_unit.
 template <int NT, bool SILU, bool RES, bool ACC, bool ONE>
 __global__ __launch_bounds__(NT) void k_small_bwd(
     const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ mean_lo, float* __restrict__ dx,
     float* __restrict__ dgamma, float* __restrict__ dbeta, int64_t N, int64_t C, int64_t G,
-    int64_t cpg, int64_t HW, int lg) {
+    int64_t cpg, int64_t HW, int lg, int lorec) {
     constexpr int kHalves = ONE ? 1 : kSmallPer / kSmallHalf;
     __shared__ double chA[kMaxSmallCpg], chB[kMaxSmallCpg];
     __shared__ double2 lds[NT / 64];
+    __shared__ double ldx[NT / 64];
     const int64_t g = blockIdx.x;
     const SmallMap m = small_map(lg, cpg, HW);
     const bool live = m.j < cpg;
@@ -1042,8 +1090,8 @@ __global__ __launch_bounds__(NT) void k_small_bwd(
         const float* xu = x + u * cpg * HW;
         const float* gu = dy + u * cpg * HW;
         const float mu = mean[u], r = rstd[u];
-        const float e = mean_lo ? -mean_lo[u] * r : 0.0f;
-        double sa = 0.0, sb = 0.0;
+        float e = mean_lo ? -mean_lo[u] * r : 0.0f;
+        double sa = 0.0, sb = 0.0, sx = 0.0;
         float xv[kSmallHalf], gv[kSmallHalf];
 #pragma unroll
         for (int hh = 0; hh < kHalves; ++hh) {
@@ -1057,10 +1105,24 @@ __global__ __launch_bounds__(NT) void k_small_bwd(
                     const float dz = SILU ? dsilu_fast(gv[k], fmaf(gm, xh, bt)) : gv[k];
                     sa += (double)dz;
                     sb = fma((double)dz, (double)xh, sb);
+                    if (lorec) sx += (double)(xv[k] - mu);
                 }
             }
         }
         channel_sum2(sa, sb, m, lds);
+        if (lorec) {
+            // whole-unit sum of x - mu (waves in order) -> lo, e; the
+            // channel sums were formed with e = 0 and dz = dy
+            double tx = wave_sum(sx);
+            if (lane == 0) ldx[threadIdx.x >> 6] = tx;
+            __syncthreads();
+            tx = ldx[0];
+#pragma unroll
+            for (int i = 1; i < NT / 64; ++i) tx += ldx[i];
+            const float lo = (float)(tx / (double)(cpg * HW));
+            e = -lo * r;
+            sb = fma((double)e, sa, sb);
+        }
         if (live && m.r == 0) {
             chA[m.j] = (double)gm * sa;
             chB[m.j] = (double)gm * sb;
@@ -1120,10 +1182,7 @@ __global__ __launch_bounds__(NT) void k_small_bwd(
         }
         if (n + 1 < N) __syncthreads();  // chA / chB are rewritten by the next sample
     }
-    if (dgamma && live && m.r == 0) {
-        dbeta[c] = (float)((double)dbeta[c] + accA);
-        dgamma[c] = (float)((double)dgamma[c] + accB);
-    }
+    if ((dgamma || dbeta) && live && m.r == 0) add_params(c, accA, accB, dgamma, dbeta);
 }
 
 // ---- host-side dispatch over the template flags -------------------------
@@ -1133,6 +1192,7 @@ struct WsView {
     double2* plane_sums;  // [planes]
     double2* unit_sums;   // [units]
     float* lo;            // [units]
+    double* part_x;       // [blocks] chunk sums of x - mu (mean residual recovery)
 };
 
 inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -1147,6 +1207,8 @@ WsView ws_view(const Plan& p, void* ws) {
     v.unit_sums = reinterpret_cast<double2*>(c);
     c += align256(sizeof(double2) * (size_t)p.units);
     v.lo = reinterpret_cast<float*>(c);
+    c += align256(sizeof(float) * (size_t)p.units);
+    v.part_x = reinterpret_cast<double*>(c);
     return v;
 }
 
@@ -1239,6 +1301,10 @@ void launch_stats(const Plan& p, const FwdArgs& a, const WsView& w, int64_t fin_
     prof_end(s, tok);
 }
 
+// The backward recovers the mean residual itself (finish_bwd_unit) when
+// the caller saved none and there is no SiLU.
+bool recover_lo(const BwdArgs& a) { return !a.mean_lo && !(a.flags & SOAR_GN_SILU); }
+
 void launch_reduce(const Plan& p, const BwdArgs& a, const WsView& w, int64_t fin_u0,
                    int64_t fin_nu, int64_t u0, int64_t nu, hipStream_t s) {
     const int64_t bpu = p.cpg * p.cpp;
@@ -1246,12 +1312,17 @@ void launch_reduce(const Plan& p, const BwdArgs& a, const WsView& w, int64_t fin
     const dim3 grid((unsigned)(fin_nu + nu * bpu));
     const int tok = prof_begin(s, nu ? (silu ? "gn_silu_bwd_reduce" : "gn_bwd_reduce")
                                      : "gn_bwd_finish");
+    auto go = [&](auto V, auto S, auto L) {
+        k_bwd_reduce<V(), S(), L()><<<grid, kThreads, 0, s>>>(
+            a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, w.part, w.part_x, w.lo,
+            w.plane_sums, w.unit_sums, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, fin_u0, fin_nu,
+            u0 * bpu);
+    };
     bsel(p.vec4, [&](auto V) {
-        bsel(silu, [&](auto S) {
-            k_bwd_reduce<V(), S()><<<grid, kThreads, 0, s>>>(
-                a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, w.part, w.plane_sums,
-                w.unit_sums, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, fin_u0, fin_nu, u0 * bpu);
-        });
+        if (silu)
+            go(V, std::true_type{}, std::false_type{});
+        else
+            bsel(recover_lo(a), [&](auto L) { go(V, std::false_type{}, L); });
     });
     prof_end(s, tok);
 }
@@ -1344,11 +1415,14 @@ bool make_plan(int64_t N, int64_t C, int64_t HW, int64_t G, const Tuning& t, Pla
 //   plane sums       double2 x planes
 //   unit S1/S2       double2 x units
 //   mean residuals   float   x units
+//   chunk sums of x - mu   double x blocks (backward without SiLU and
+//                          without a saved mean residual)
 size_t workspace_bytes(const Plan& p) {
     return align256(sizeof(double2) * (size_t)p.blocks) +
            align256(sizeof(double2) * (size_t)p.planes) +
            align256(sizeof(double2) * (size_t)p.units) +
-           align256(sizeof(float) * (size_t)p.units);
+           align256(sizeof(float) * (size_t)p.units) +
+           align256(sizeof(double) * (size_t)p.blocks);
 }
 
 // Single-stream launch order for batches 0..B-1 (S = first pass, F =
@@ -1511,7 +1585,8 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hip
                             k_small_bwd<NT(), S(), R(), A(), O()>
                                 <<<dim3((unsigned)p.G), NT(), 0, s>>>(
                                     a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, a.dx,
-                                    a.dgamma, a.dbeta, p.N, p.C, p.G, p.cpg, p.HW, lg);
+                                    a.dgamma, a.dbeta, p.N, p.C, p.G, p.cpg, p.HW, lg,
+                                    recover_lo(a) ? 1 : 0);
                         });
                     });
                 });
@@ -1522,7 +1597,13 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hip
     }
     const int64_t bpu2 = p.cpg * p.cpp2;  // second-pass blocks per unit
     const char* dx_name = silu ? "gn_silu_bwd_dx" : "gn_bwd_dx";
-    if (a.dx && fold_ok(p, t, p.upb_bwd)) {
+    const bool lorec = recover_lo(a);
+    const bool params = a.dgamma || a.dbeta;
+    // with the mean residual recovered, the dx pass reads it from the
+    // workspace, where the finish put it
+    BwdArgs ad = a;
+    if (lorec) ad.mean_lo = w.lo;
+    if (a.dx && !lorec && fold_ok(p, t, p.upb_bwd)) {
         launch_reduce(p, a, w, 0, 0, 0, p.units, s);
         const int tok = prof_begin(s, dx_name);
         launch_dx(p, t, a, w.unit_sums, 0, p.blocks2, s, true);
@@ -1546,7 +1627,7 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hip
             launch_reduce(p, a, w, u0, nu, 0, 0, s);
             if (a.dx) {
                 const int tok = prof_begin(s, dx_name);
-                launch_dx(p, t, a, w.unit_sums, u0 * bpu2, nu * bpu2, s);
+                launch_dx(p, t, ad, w.unit_sums, u0 * bpu2, nu * bpu2, s);
                 prof_end(s, tok);
             }
             SOAR_TRY(hipEventRecord(pp->second[bi % 4], s));
@@ -1554,14 +1635,14 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hip
     } else {
         // one batch: its dx launch runs after every plane sum is final, so
         // it also finishes dgamma / dbeta (no k_param_finish launch)
-        param_in_dx = a.dx && a.dgamma && p.units <= p.upb_bwd;
+        param_in_dx = a.dx && params && p.units <= p.upb_bwd;
         int64_t prev_u0 = 0, prev_nu = 0;
         for (int64_t u0 = 0;; u0 += p.upb_bwd) {
             const int64_t nu = u0 < p.units ? std::min(p.upb_bwd, p.units - u0) : 0;
             if (nu + prev_nu > 0) launch_reduce(p, a, w, prev_u0, prev_nu, u0, nu, s);
             if (prev_nu > 0 && a.dx) {
                 const int tok = prof_begin(s, dx_name);
-                launch_dx(p, t, a, w.unit_sums, prev_u0 * bpu2, prev_nu * bpu2, s, false,
+                launch_dx(p, t, ad, w.unit_sums, prev_u0 * bpu2, prev_nu * bpu2, s, false,
                           param_in_dx ? w.plane_sums : nullptr);
                 prof_end(s, tok);
             }
@@ -1570,7 +1651,7 @@ hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hip
             prev_nu = nu;
         }
     }
-    if (a.dgamma && !param_in_dx) {
+    if (params && !param_in_dx) {
         const int tok = prof_begin(s, "gn_param_finish");
         k_param_finish<<<dim3((unsigned)((p.C + 255) / 256)), 256, 0, s>>>(
             w.plane_sums, a.dgamma, a.dbeta, p.N, p.C);

@@ -159,7 +159,7 @@ int loss_sums(const float* z, const float* y, size_t n, float pos_weight, double
     if ((rc = check_dev(z, n * 4, "logits")) || (rc = check_dev(y, n * 4, "targets"))) return rc;
     const size_t need = soar::ops::loss_sums_workspace_bytes((int64_t)n);
     void* ws = nullptr;
-    if ((rc = owned_workspace(need, &ws))) return rc;
+    if ((rc = owned_workspace(need, &ws, stream))) return rc;
     // the partials first, the 4 results at the end of the same buffer
     double* res = static_cast<double*>(ws) + (need / sizeof(double) - 4);
     const int tok = soar::gn::prof_begin(S(stream), "dice_bce_sums");
@@ -288,7 +288,7 @@ SOAR_API int soar_conv2d_backward(const float* grad_out, const float* in, const 
     if (grad_weight || grad_bias) {
         if ((rc = require_device())) return rc;
         need = soar::ops::conv_backward_workspace_bytes(c);
-        if ((rc = owned_workspace(need, &ws))) return rc;
+        if ((rc = owned_workspace(need, &ws, stream))) return rc;
     }
     return conv_backward(grad_out, in, weight, grad_in, grad_weight, grad_bias, c, true, ws,
                          need, stream);
