@@ -148,6 +148,30 @@ SOAR_API int soar_group_norm_backward(const float* grad_out, const float* in,
                                       size_t num_groups, size_t C, size_t HW,
                                       void* stream);
 
+/* Bytes of the static device scratch behind
+ * soar_group_norm_backward_noalloc, per device (held until process exit). */
+#define SOAR_GN_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
+
+/* No counterpart in the reference: soar_group_norm_backward for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, results and accumulate
+ * semantics as soar_group_norm_backward, and the same kernels, but the
+ * workspace is a static device array of SOAR_GN_NOALLOC_SCRATCH_BYTES per
+ * device instead of a library-owned hipMalloc buffer: the call allocates
+ * nothing (no hipMalloc / hipFree, no stream or event creation).  A shape
+ * whose workspace (soar_gn_workspace_bytes(1, C, HW, num_groups)) exceeds
+ * the scratch is refused with SOAR_EINVAL.  Every call on one device shares
+ * that device's scratch: calls that overlap in time on one device race. */
+SOAR_API int soar_group_norm_backward_noalloc(const float* grad_out,
+                                              const float* in,
+                                              const float* gamma,
+                                              const float* saved_mean,
+                                              const float* saved_rstd,
+                                              float* grad_in, float* grad_gamma,
+                                              float* grad_beta,
+                                              size_t num_groups, size_t C,
+                                              size_t HW, void* stream);
+
 /* Replaces: silu_forward (cuda_kernels.hpp:19): y = x/(1+exp(-x)). */
 SOAR_API int soar_silu_forward(const float* x, float* y, size_t n,
                                void* stream);

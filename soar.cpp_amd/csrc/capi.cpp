@@ -211,7 +211,7 @@ namespace soar {
 namespace gn {
 
 int prof_begin(hipStream_t s, const char* kernel) {
-    if (!g_prof_on.load(std::memory_order_relaxed)) return -1;
+    if (!g_prof_on.load(std::memory_order_relaxed) || soar::capi::g_quiet_call) return -1;
     std::lock_guard<std::mutex> lk(g_prof_mu);
     ProfRec r{kernel, take_event(), take_event()};
     if (!r.start || !r.stop) return -1;
@@ -362,6 +362,22 @@ SOAR_API int soar_gn_silu_backward(const float* dy, const float* x, const float*
                                    float* dbeta, int64_t N,
                                    int64_t C, int64_t HW, int64_t G, unsigned flags,
                                    void* workspace, size_t workspace_bytes, void* stream) {
+    return soar::capi::gn_backward(dy, x, gamma, beta, mean, rstd, mean_lo, dx, dgamma, dbeta,
+                                   N, C, HW, G, flags, workspace, workspace_bytes, stream,
+                                   false);
+}
+
+}  // extern "C"
+
+namespace soar::capi {
+
+thread_local bool g_quiet_call = false;
+
+int gn_backward(const float* dy, const float* x, const float* gamma, const float* beta,
+                const float* mean, const float* rstd, const float* mean_lo, float* dx,
+                float* dgamma, float* dbeta, int64_t N, int64_t C, int64_t HW, int64_t G,
+                unsigned flags, void* workspace, size_t workspace_bytes, void* stream,
+                bool ws_scratch) {
     int64_t elems = 0;
     int rc = check_shape(N, C, HW, G, &elems);
     if (rc) return rc;
@@ -383,13 +399,30 @@ SOAR_API int soar_gn_silu_backward(const float* dy, const float* x, const float*
     if (!soar::gn::make_plan(N, C, HW, G, t, &p))
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     p.vec4 = p.vec4 && aligned16(x) && aligned16(dy) && aligned16(dx);
-    if ((rc = check_ws(p, workspace, workspace_bytes))) return rc;
+    if (ws_scratch) {
+        // the library's static scratch: its size is known, and it is not a
+        // hipMalloc allocation to look up
+        const size_t need = soar::gn::workspace_bytes(p);
+        if (workspace_bytes < need)
+            return fail(SOAR_EINVAL, "scratch of %zu bytes is smaller than the %zu this shape needs",
+                        workspace_bytes, need);
+    } else if ((rc = check_ws(p, workspace, workspace_bytes))) {
+        return rc;
+    }
     soar::gn::BwdArgs a{dy, x, gamma, beta, mean, rstd, mean_lo, dx, dgamma, dbeta, flags,
                         workspace};
-    hipError_t e = soar::gn::launch_backward(p, t, a, static_cast<hipStream_t>(stream));
+    Tuning tl = t;
+    if (ws_scratch) tl.streams = 1;  // the helper-stream pipeline would create a stream
+    g_quiet_call = ws_scratch;       // and kernel timing would create events
+    hipError_t e = soar::gn::launch_backward(p, tl, a, static_cast<hipStream_t>(stream));
+    g_quiet_call = false;
     if (e != hipSuccess) return hip_fail(e, "GroupNorm backward launch");
     return ok();
 }
+
+}  // namespace soar::capi
+
+extern "C" {
 
 SOAR_API int soar_group_norm_forward(const float* in, const float* gamma, const float* beta,
                                      float* out, float* saved_mean, float* saved_rstd,

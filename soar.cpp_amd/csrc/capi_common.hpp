@@ -38,4 +38,16 @@ bool aligned16(const void* p);
 // that an earlier call outside the capture already grew).
 int owned_workspace(size_t need, void** out, void* stream);
 
+// Validation and launch of the fused GroupNorm(+SiLU) backward
+// (soar_gn_silu_backward).  ws_scratch: `workspace` is the library's static
+// device scratch of `workspace_bytes` bytes, so it is not looked up as an
+// allocation, and the call creates nothing (one stream, no timing events).
+int gn_backward(const float* dy, const float* x, const float* gamma, const float* beta,
+                const float* mean, const float* rstd, const float* mean_lo, float* dx,
+                float* dgamma, float* dbeta, int64_t N, int64_t C, int64_t HW, int64_t G,
+                unsigned flags, void* workspace, size_t workspace_bytes, void* stream,
+                bool ws_scratch);
+// Set while a ws_scratch call runs on this thread: kernel timing is skipped.
+extern thread_local bool g_quiet_call;
+
 }  // namespace soar::capi

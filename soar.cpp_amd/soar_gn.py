@@ -32,6 +32,10 @@ GN_SILU = 1
 GN_RESIDUAL = 2
 GN_ACCUMULATE_DX = 4
 
+# bytes of the static scratch behind soar_group_norm_backward_noalloc
+# (SOAR_GN_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 4 << 20
+
 TUNE_CHUNK = 1
 TUNE_REVERSE = 2
 TUNE_NT_STORE = 3
@@ -77,6 +81,8 @@ SIGNATURES = {
                                            _c.c_float, _P]),
     "soar_group_norm_backward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ,
                                             _P]),
+    "soar_group_norm_backward_noalloc": (_c.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _SZ,
+                                                    _SZ, _SZ, _P]),
     "soar_silu_forward": (_c.c_int, [_P, _P, _SZ, _P]),
     "soar_silu_backward": (_c.c_int, [_P, _P, _P, _SZ, _P]),
     "soar_add_forward": (_c.c_int, [_P, _P, _P, _SZ, _P]),
