@@ -13,7 +13,15 @@ through the C-ABI of libsoar_gn.so on one GPU.  Prints one JSON line:
              8 TB/s HBM peak; `traffic` is the rocprofv3-measured bytes per
              launch from profiles/ when present;
   cpu_baseline  the fp32 statement of the reference's CPU loops
-             (oracle/soar_oracle.c, single thread) on a bounded sample.
+             (oracle/soar_oracle.c, one pinned core, median of 3) on a
+             bounded sample of config 3, plus config 1 at full size.
+
+Other workloads (--config): the other BASELINE configs (cfg2_fwd,
+cfg4_chain, cfg5), the CBA block with a pointwise conv (cba_pw), the CBA
+depthwise convolutions at 1x64x2048^2 (dw_k3, dw_k5, dw_k7, dw_k3d5,
+dw_k3s2), SOAR training steps (train_nano64/512/1024) and the streaming
+ceilings of this memory system for plain kernels of the library's shape
+(stream_read, stream_copy, stream_2r1w, stream_2r over 1 GiB buffers).
 """
 import argparse
 import json
@@ -45,6 +53,18 @@ SEED_OF = {"cfg2_fwd": SEED + 2, "cfg3": SEED + 3, "cfg4_chain": SEED + 4, "cfg5
 CBA_C_IN = 64
 PEAK_MFMA_F32 = 157.3  # TFLOP/s, dense fp32 matrix
 
+# Streaming ceilings (libsoar_synth.so soar_synth_stream over 1 GiB
+# buffers): name -> pattern
+STREAM_CONFIGS = {"stream_read": "read", "stream_copy": "copy", "stream_2r1w": "2r1w",
+                  "stream_2r": "2r"}
+
+# Depthwise convolutions of the CBA blocks at 1x64x2048^2, forward + backward
+# (dx, dW, db): name -> (K, stride, dilation); pad = dilation*(K-1)/2
+DW_CONFIGS = {"dw_k3": (3, 1, 1), "dw_k5": (5, 1, 1), "dw_k7": (7, 1, 1),
+              "dw_k3d5": (3, 1, 5), "dw_k3s2": (3, 2, 1)}
+DW_SHAPE = (1, 64, 2048, 2048)
+PEAK_VALU_F32 = 157.3  # TFLOP/s, MI355X published vector fp32 (packed); 78.6 without
+
 # End-to-end training steps of the SOAR model through libsoar_host.so
 # (soar_train_step: forward, Dice+BCE loss, backward, clip, AdamW), one
 # 1-channel image per step: name -> (variant, H, W)
@@ -66,7 +86,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + sorted(TRAIN_CONFIGS))
+    ap.add_argument("--config", default="cfg3",
+                    choices=sorted(CONFIGS) + sorted(TRAIN_CONFIGS) + sorted(STREAM_CONFIGS)
+                    + sorted(DW_CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="time the steps without per-kernel events")
@@ -215,28 +237,159 @@ class CBAStep:
                             ws=self.ws_bwd)
 
 
+class DwStep:
+    """Forward and backward (dx, dW, db) of one depthwise convolution of the
+    CBA blocks at 1x64x2048^2 (soar_dw_conv_forward / soar_dw_conv_backward):
+    LKR's k5 / k7, Ctx's dilated k3, Down's stride-2 k3."""
+
+    def __init__(self, gn, name, seed):
+        import torch
+        K, S, D = DW_CONFIGS[name]
+        N, C, H, W = DW_SHAPE
+        self.gn, self.K, self.S, self.D, self.pad = gn, K, S, D, D * (K - 1) // 2
+        self.N, self.C, self.H, self.W = N, C, H, W
+        self.Ho = gn.conv_out_size(H, K, self.pad, S, D)
+        self.Wo = gn.conv_out_size(W, K, self.pad, S, D)
+        self.x = torch.empty((N, C, H, W), device="cuda")
+        gn.synth_normal(self.x, seed, 1, 0.0, 1.0)
+        self.w = torch.empty((C, K, K), device="cuda")
+        gn.synth_uniform(self.w, seed, 7, -1.0 / K, 1.0 / K)
+        self.b = torch.empty(C, device="cuda")
+        gn.synth_normal(self.b, seed, 3, 0.0, 0.1)
+        self.y = torch.empty((N, C, self.Ho, self.Wo), device="cuda")
+        self.dy = torch.empty_like(self.y)
+        gn.synth_normal(self.dy, seed, 4, 0.0, 1e-2)
+        self.dx = torch.empty_like(self.x)
+        self.dw = torch.zeros_like(self.w)
+        self.db = torch.zeros_like(self.b)
+        nws = int(gn.lib().soar_dw_conv_backward_workspace_bytes(N, C, H, W, self.Ho, self.Wo,
+                                                                 K, S, D))
+        self.ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
+        self.params = [None]
+        self.T_in = N * C * H * W * 4
+        self.T_out = N * C * self.Ho * self.Wo * 4
+
+    def algorithmic_bytes(self):
+        # fwd reads x, writes y; dgrad reads dy, writes dx; wgrad reads dy, x
+        return 3 * (self.T_in + self.T_out)
+
+    def kernel_bytes(self, name):
+        return {"dw_conv": self.T_in + self.T_out, "dw_conv_dgrad": self.T_in + self.T_out,
+                "dw_conv_wgrad": self.T_in + self.T_out}.get(name, 0)
+
+    def kernel_flops(self, name):
+        f = 2 * self.K * self.K * self.T_out // 4
+        return f if name in ("dw_conv", "dw_conv_dgrad", "dw_conv_wgrad") else 0
+
+    def config(self):
+        return {"workload": f"depthwise conv k{self.K} stride {self.S} dilation {self.D} pad "
+                            f"{self.pad}, fwd + bwd (dx, dW, db)",
+                "N": self.N, "C": self.C, "H": self.H, "W": self.W, "H_out": self.Ho,
+                "W_out": self.Wo}
+
+    def __call__(self):
+        gn = self.gn
+        gn.dw_conv_forward(self.x, self.w, self.b, self.pad, self.S, self.D, y=self.y)
+        gn.dw_conv_backward(self.dy, self.x, self.w, self.pad, self.S, self.D, dx=self.dx,
+                            dweight=self.dw, dbias=self.db, ws=self.ws)
+
+
+def bench_stream(args):
+    """Streaming ceilings: one synth_stream kernel over 1 GiB buffers, each
+    launch between hipEvents on the launch stream; value = tensor bytes of
+    the pattern / median launch time."""
+    import torch
+    import soar_gn as gn
+    pattern = STREAM_CONFIGS[args.config]
+    n = 1 << 28
+    a = torch.empty(n, device="cuda")
+    b = torch.empty(n, device="cuda")
+    out = torch.empty(n, device="cuda")
+    gn.synth_normal(a, SEED, 1)
+    gn.synth_normal(b, SEED, 4)
+    passes = gn.STREAM_KINDS[pattern][1]
+    for _ in range(args.warmup):
+        gn.synth_stream(pattern, a, b, out)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for e0, e1 in evs:
+        e0.record()
+        gn.synth_stream(pattern, a, b, out)
+        e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
+    med = ms[len(ms) // 2]
+    nbytes = passes * n * 4
+    value = nbytes / (med * 1e-3) / 1e9
+    kname = f"k_stream<{gn.STREAM_KINDS[pattern][0]}>"
+    print(json.dumps({
+        "metric": f"{args.config} achieved HBM GB/s (streaming ceiling, 1 GiB buffers)",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(med, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic N(0,1)",
+        "config": {"workload": f"streaming ceiling: {pattern} over 1 GiB buffers "
+                               f"({passes} tensor passes per launch)"},
+        "frac_of_peak": round(value / PEAK_GBS, 4), "wall_s_timed": round(wall, 4),
+        "best_ms": round(ms[0], 4),
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(value, 1),
+                     "peak": PEAK_GBS, "unit": "GB/s", "frac": round(value / PEAK_GBS, 4),
+                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_ms": round(med, 5),
+                     "traffic": None},
+        "cpu_baseline": None}), flush=True)
+
+
+def _host_cpu():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
 def cpu_baseline():
-    """fp32 statement of the reference CPU path, one thread, on 4 of config
-    3's 16 groups (the same per-group size, 1/4 of the tensor)."""
+    """fp32 statement of the reference CPU path (oracle/soar_oracle.c, the
+    unfused loops of src/nn/layers.cpp), on one core: this thread pinned to
+    one CPU (the lowest it may use), one warm-up then the median of 3 runs
+    (the reference's idiom, src/main.cpp:675-682).  Config 3 is sampled as
+    4 of its 16 groups (the same per-group size, 1/4 of the tensor) to keep
+    the run within seconds; config 1 runs at full size (forward only, its
+    workload)."""
     import numpy as np
     import soar_oracle as orc
-    N, C, HW, G = 1, 16, 2048 * 2048, 4
-    n = N * C * HW
-    x = orc.fill_normal(n, SEED + 3, 1)
-    gamma = orc.fill_uniform(C, SEED + 3, 2, 0.5, 1.5)
-    beta = orc.fill_normal(C, SEED + 3, 3, 0.0, 0.1)
-    dy = orc.fill_normal(n, SEED + 3, 4, 0.0, 1e-2)
     eps = float(np.float32(1e-5))
-    orc.ref_gn_silu_fwd_bwd_f32(x, gamma, beta, dy, N, C, HW, G, eps)  # warm-up
-    runs = [orc.ref_gn_silu_fwd_bwd_f32(x, gamma, beta, dy, N, C, HW, G, eps) for _ in range(2)]
-    t = sorted(r["fwd_s"] + r["bwd_s"] for r in runs)[0]
-    tf = min(r["fwd_s"] for r in runs)
-    tb = min(r["bwd_s"] for r in runs)
-    alg = 8 * n * 4
-    return {"value": round(alg / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"N=1 C=16 H=W=2048 G=4 (4 of config 3's 16 groups), fwd+bwd, "
-                      f"best of 2 after 1 warm-up; fwd {tf * 1e3:.1f} ms, bwd {tb * 1e3:.1f} ms,"
-                      f" 1 thread of {os.cpu_count()} host CPUs"}
+    allowed = os.sched_getaffinity(0)
+    core = min(allowed)
+    os.sched_setaffinity(0, {core})
+    try:
+        def run(N, C, HW, G, seed):
+            n = N * C * HW
+            x = orc.fill_normal(n, seed, 1)
+            gamma = orc.fill_uniform(C, seed, 2, 0.5, 1.5)
+            beta = orc.fill_normal(C, seed, 3, 0.0, 0.1)
+            dy = orc.fill_normal(n, seed, 4, 0.0, 1e-2)
+            orc.ref_gn_silu_fwd_bwd_f32(x, gamma, beta, dy, N, C, HW, G, eps)  # warm-up
+            runs = [orc.ref_gn_silu_fwd_bwd_f32(x, gamma, beta, dy, N, C, HW, G, eps)
+                    for _ in range(3)]
+            med = lambda k: sorted(r[k] for r in runs)[1]
+            return n, med("fwd_s"), med("bwd_s"), sorted(r["fwd_s"] + r["bwd_s"] for r in runs)[1]
+
+        n3, f3, b3, t3 = run(1, 16, 2048 * 2048, 4, SEED + 3)
+        n1, f1, _, _ = run(1, 32, 256 * 256, 8, SEED + 1)
+    finally:
+        os.sched_setaffinity(0, allowed)
+    return {"value": round(8 * n3 * 4 / t3 / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"config 3 as N=1 C=16 H=W=2048 G=4 (4 of its 16 groups), fwd+bwd, "
+                      f"1 warm-up + median of 3 on CPU {core} ({_host_cpu()}, {len(allowed)} "
+                      f"CPUs allowed): fwd {f3 * 1e3:.1f} ms, bwd {b3 * 1e3:.1f} ms",
+            "config1_fwd": {"ms": round(f1 * 1e3, 3), "GBps": round(3 * n1 * 4 / f1 / 1e9, 3),
+                            "shape": "N=1 C=32 H=W=256 G=8, full size, same method"},
+            "config3_fwd_ms": round(f3 * 1e3, 2), "config3_bwd_ms": round(b3 * 1e3, 2)}
 
 
 def train_cpu_baseline(H, W, variant):
@@ -323,11 +476,11 @@ def main():
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has "
               "no multi-GPU path.", file=sys.stderr)
         sys.exit(2)
-    if args.config in TRAIN_CONFIGS:
+    if args.config in TRAIN_CONFIGS or args.config in STREAM_CONFIGS:
         import torch
         assert torch.cuda.is_available(), "bench.py needs a GPU"
         torch.cuda.set_device(0)
-        bench_train(args)
+        (bench_train if args.config in TRAIN_CONFIGS else bench_stream)(args)
         return
     import torch
     import soar_gn as gn
@@ -347,10 +500,13 @@ def main():
         print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4}))
         return
 
-    N, C, HW, G, passes, residual, blocks = CONFIGS[args.config]
-    if args.config == "cba_pw":
+    if args.config in DW_CONFIGS:
+        step = DwStep(gn, args.config, SEED + 7)
+    elif args.config == "cba_pw":
+        N, C, HW, G, passes, residual, blocks = CONFIGS[args.config]
         step = CBAStep(gn, N, C, HW, G, SEED_OF[args.config])
     else:
+        N, C, HW, G, passes, residual, blocks = CONFIGS[args.config]
         step = Step(gn, N, C, HW, G, passes, residual, blocks, SEED_OF[args.config])
     for _ in range(args.warmup):
         step()
@@ -406,7 +562,10 @@ def main():
         if flops:
             tf = flops / (avg * 1e-3) / 1e12
             kinfo[k["kernel"]]["TFLOPs"] = round(tf, 2)
-            kinfo[k["kernel"]]["mfma_frac"] = round(tf / PEAK_MFMA_F32, 4)
+            if isinstance(step, DwStep):  # vector FMAs, not the matrix cores
+                kinfo[k["kernel"]]["valu_frac"] = round(tf / PEAK_VALU_F32, 4)
+            else:
+                kinfo[k["kernel"]]["mfma_frac"] = round(tf / PEAK_MFMA_F32, 4)
     if kernels:
         dom = max(kernels, key=lambda k: k["total_ms"])
         kd = kinfo[dom["kernel"]]
@@ -422,11 +581,32 @@ def main():
             # matrix-core roof
             roofline["mfma"] = {"achieved": kd["TFLOPs"], "peak": PEAK_MFMA_F32,
                                 "unit": "TFLOP/s", "frac": kd["mfma_frac"]}
+        if "valu_frac" in kd:
+            roofline["valu"] = {"achieved": kd["TFLOPs"], "peak": PEAK_VALU_F32,
+                                "unit": "TFLOP/s", "frac": kd["valu_frac"]}
 
     cpu = None
     if not args.no_cpu_baseline and args.config == "cfg3":
         cpu = cpu_baseline()
 
+    if isinstance(step, DwStep):
+        data = (f"synthetic: x~N(0,1), w~U(-1/K,1/K), b~N(0,0.1), dy~N(0,1e-2); "
+                f"splitmix64/Box-Muller seed {SEED + 7}")
+        cfg = {**step.config(), "algorithmic_bytes_per_step": alg}
+    else:
+        data = (f"synthetic: x~N(0,1), gamma~U(0.5,1.5), beta~N(0,0.1), dy~N(0,1e-2); "
+                f"splitmix64/Box-Muller seed {SEED_OF[args.config]}")
+        cfg = {"workload": {"cfg3": "GroupNorm+SiLU fwd+bwd, BASELINE config 3",
+                            "cfg2_fwd": "GroupNorm+SiLU fwd, BASELINE config 2",
+                            "cfg4_chain": "6 x (x + SiLU(GN(x))) fwd+bwd, BASELINE config 4",
+                            "cfg5": "GroupNorm+SiLU fwd+bwd shape of BASELINE config 5",
+                            "cba_pw": "CBA fwd+bwd: pointwise conv 64->64 + GN + SiLU, GN "
+                                      "stats in the conv epilogue, config 3 GroupNorm shape"}
+               [args.config],
+               "N": N, "C": C, "H": int(HW ** 0.5), "W": int(HW ** 0.5), "G": G,
+               "eps": 1e-5, "blocks": blocks, "residual": residual,
+               **({"C_in": CBA_C_IN} if args.config == "cba_pw" else {}),
+               "algorithmic_bytes_per_step": alg}
     out = {
         "metric": METRIC if args.config == "cfg3" else f"{args.config} achieved HBM GB/s",
         "value": round(value, 1),
@@ -439,19 +619,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": f"synthetic: x~N(0,1), gamma~U(0.5,1.5), beta~N(0,0.1), dy~N(0,1e-2); "
-                f"splitmix64/Box-Muller seed {SEED_OF[args.config]}",
-        "config": {"workload": {"cfg3": "GroupNorm+SiLU fwd+bwd, BASELINE config 3",
-                                "cfg2_fwd": "GroupNorm+SiLU fwd, BASELINE config 2",
-                                "cfg4_chain": "6 x (x + SiLU(GN(x))) fwd+bwd, BASELINE config 4",
-                                "cfg5": "GroupNorm+SiLU fwd+bwd shape of BASELINE config 5",
-                                "cba_pw": "CBA fwd+bwd: pointwise conv 64->64 + GN + SiLU, GN "
-                                          "stats in the conv epilogue, config 3 GroupNorm shape"}
-                   [args.config],
-                   "N": N, "C": C, "H": int(HW ** 0.5), "W": int(HW ** 0.5), "G": G,
-                   "eps": 1e-5, "blocks": blocks, "residual": residual,
-                   **({"C_in": CBA_C_IN} if args.config == "cba_pw" else {}),
-                   "algorithmic_bytes_per_step": alg},
+        "data": data,
+        "config": cfg,
         "frac_of_peak": round(value / PEAK_GBS, 4),
         "wall_s_timed": round(wall, 4),
         "roofline": roofline,

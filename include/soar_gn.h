@@ -414,6 +414,9 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
                                /* workspace, added by a second kernel that */
                                /* also writes the statistics); 1 = never;  */
                                /* 1..8, the default is 8                   */
+#define SOAR_TUNE_LOADS 13     /* 128-bit loads in flight per thread in */
+                               /* the GroupNorm statistics and reduction */
+                               /* passes: 4 or 8; results do not change  */
 SOAR_API int soar_gn_tune(int key, int64_t value);
 SOAR_API int64_t soar_gn_tune_get(int key);
 

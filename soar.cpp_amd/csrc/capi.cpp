@@ -1092,6 +1092,10 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
             if (value < 1 || value > 8) return fail(SOAR_EINVAL, "pw_splitk must be in [1, 8]");
             g_tune.pw_kz = value;
             return ok();
+        case SOAR_TUNE_LOADS:
+            if (value != 4 && value != 8) return fail(SOAR_EINVAL, "loads must be 4 or 8");
+            g_tune.loads = (int)value;
+            return ok();
         default:
             return fail(SOAR_EINVAL, "unknown tuning key %d", key);
     }
@@ -1112,6 +1116,7 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
         case SOAR_TUNE_PW_SMALL: return g_tune.pw_small;
         case SOAR_TUNE_FOLD_MAX: return g_tune.fold_max;
         case SOAR_TUNE_PW_SPLITK: return g_tune.pw_kz;
+        case SOAR_TUNE_LOADS: return g_tune.loads;
         default: return -1;
     }
 }

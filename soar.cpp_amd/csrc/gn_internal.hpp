@@ -32,6 +32,7 @@ struct Plan {
     int64_t upb_fwd = 0;     // units per forward batch
     int64_t upb_bwd = 0;     // units per backward batch
     bool vec4 = false;       // float4 path (HW % 4 == 0 and 16-byte pointers)
+    int loads = 4;           // 128-bit loads in flight per thread, first passes
 };
 
 // Defaults measured on MI355X at 1x64x2048^2, fwd+bwd per step:
@@ -71,6 +72,8 @@ struct Tuning {
                                  // as many) run the SIMT kernels (0: never)
     int64_t pw_kz = 8;           // most blocks a small-grid pointwise
                                  // convolution splits K over (1: never)
+    int loads = 4;               // 128-bit loads in flight per thread in the
+                                 // first passes (statistics, reduction): 4 or 8
 };
 
 constexpr int kThreads = 256;   // first passes (stats, reduction)

@@ -254,7 +254,12 @@ __device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
     }
 }
 
-template <bool VEC>
+// U: 128-bit loads in flight per thread.  The thread's first batch is
+// issued whole before its shift K (the first element) is taken from it, so
+// a chunk of 8 vectors per thread costs 8 / U memory round trips.  The
+// elements reach each of the four accumulation lanes in index order for
+// every U, so the partials do not depend on U.
+template <bool VEC, int U>
 __global__ __launch_bounds__(kThreads) void k_stats(
     const float* __restrict__ x, double2* __restrict__ part, float* __restrict__ mean,
     float* __restrict__ rstd, float* __restrict__ mean_lo, float* __restrict__ lo_ws,
@@ -278,16 +283,6 @@ __global__ __launch_bounds__(kThreads) void k_stats(
     if (VEC) {
         const f4* p4 = reinterpret_cast<const f4*>(p);
         const int64_t n4 = ck.len >> 2;
-        int64_t i = t;
-        if (i < n4) {
-            cnt = 4 * ((n4 - 1 - i) / kThreads + 1);
-            f4 v = p4[i];
-            K = v.x;
-            float d1 = v.y - K, d2 = v.z - K, d3 = v.w - K;
-            s1 = d1; s2 = d2; s3 = d3;
-            q1 = d1 * d1; q2 = d2 * d2; q3 = d3 * d3;
-            i += kThreads;
-        }
 #define SOAR_ACC4(v)                                                     \
     {                                                                    \
         float d0 = (v).x - K, d1 = (v).y - K, d2 = (v).z - K,            \
@@ -296,13 +291,30 @@ __global__ __launch_bounds__(kThreads) void k_stats(
         q0 = fmaf(d0, d0, q0); q1 = fmaf(d1, d1, q1);                    \
         q2 = fmaf(d2, d2, q2); q3 = fmaf(d3, d3, q3);                    \
     }
-        for (; i + 3 * kThreads < n4; i += 4 * kThreads) {
-            f4 a = p4[i], b4 = p4[i + kThreads], c = p4[i + 2 * kThreads],
-               d = p4[i + 3 * kThreads];
-            SOAR_ACC4(a);
-            SOAR_ACC4(b4);
-            SOAR_ACC4(c);
-            SOAR_ACC4(d);
+        int64_t i = t;
+        if (i < n4) {
+            cnt = 4 * ((n4 - 1 - i) / kThreads + 1);
+            if (i + (U - 1) * kThreads < n4) {
+                f4 v[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) v[u] = p4[i + u * kThreads];
+                K = v[0].x;
+#pragma unroll
+                for (int u = 0; u < U; ++u) SOAR_ACC4(v[u]);
+                i += U * kThreads;
+            } else {
+                const f4 v = p4[i];
+                K = v.x;
+                SOAR_ACC4(v);
+                i += kThreads;
+            }
+        }
+        for (; i + (U - 1) * kThreads < n4; i += U * kThreads) {
+            f4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) v[u] = p4[i + u * kThreads];
+#pragma unroll
+            for (int u = 0; u < U; ++u) SOAR_ACC4(v[u]);
         }
         for (; i < n4; i += kThreads) {
             f4 a = p4[i];
@@ -659,7 +671,9 @@ __device__ void finish_bwd_unit(int64_t u, const double2* __restrict__ part,
 
 // LOREC: mean residual recovery (see finish_bwd_unit); also writes the
 // chunk sums of x - mu to part_x.  Only without SiLU, so dz = dy.
-template <bool VEC, bool SILU, bool LOREC>
+// U: 128-bit loads in flight per thread, U/2 of each tensor (elements reach
+// each accumulation lane in index order for every U).
+template <bool VEC, bool SILU, bool LOREC, int U>
 __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ gamma, const float* __restrict__ beta,
@@ -697,14 +711,20 @@ __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
         const f4* x4 = reinterpret_cast<const f4*>(x + base);
         const f4* g4 = reinterpret_cast<const f4*>(dy + base);
         const int64_t n4 = ck.len >> 2;
+        constexpr int UH = U / 2;
         int64_t i = t;
-        for (; i + kThreads < n4; i += 2 * kThreads) {
-            f4 v0 = x4[i], v1 = x4[i + kThreads];
-            f4 g0 = g4[i], g1 = g4[i + kThreads];
-            acc(g0.x, v0.x, sa0, sb0, sc0); acc(g0.y, v0.y, sa1, sb1, sc1);
-            acc(g0.z, v0.z, sa0, sb0, sc0); acc(g0.w, v0.w, sa1, sb1, sc1);
-            acc(g1.x, v1.x, sa0, sb0, sc0); acc(g1.y, v1.y, sa1, sb1, sc1);
-            acc(g1.z, v1.z, sa0, sb0, sc0); acc(g1.w, v1.w, sa1, sb1, sc1);
+        for (; i + (UH - 1) * kThreads < n4; i += UH * kThreads) {
+            f4 v[UH], g[UH];
+#pragma unroll
+            for (int u = 0; u < UH; ++u) {
+                v[u] = x4[i + u * kThreads];
+                g[u] = g4[i + u * kThreads];
+            }
+#pragma unroll
+            for (int u = 0; u < UH; ++u) {
+                acc(g[u].x, v[u].x, sa0, sb0, sc0); acc(g[u].y, v[u].y, sa1, sb1, sc1);
+                acc(g[u].z, v[u].z, sa0, sb0, sc0); acc(g[u].w, v[u].w, sa1, sb1, sc1);
+            }
         }
         for (; i < n4; i += kThreads) {
             f4 v0 = x4[i], g0 = g4[i];
@@ -1212,6 +1232,15 @@ WsView ws_view(const Plan& p, void* ws) {
     return v;
 }
 
+// Calls f(std::integral_constant<int, U>) for U = 8 or 4 loads in flight.
+template <typename F>
+void loads_sel(int loads, F&& f) {
+    if (loads == 8)
+        f(std::integral_constant<int, 8>{});
+    else
+        f(std::integral_constant<int, 4>{});
+}
+
 // Calls f(std::true_type) or f(std::false_type): turns a runtime flag into
 // a template argument.
 template <typename F>
@@ -1294,9 +1323,11 @@ void launch_stats(const Plan& p, const FwdArgs& a, const WsView& w, int64_t fin_
     const dim3 grid((unsigned)(fin_nu + nu * bpu));
     const int tok = prof_begin(s, nu ? "gn_stats_partial" : "gn_stats_finish");
     bsel(p.vec4, [&](auto V) {
-        k_stats<V()><<<grid, kThreads, 0, s>>>(a.x, w.part, a.mean, a.rstd, a.mean_lo, w.lo,
-                                               p.HW, p.chunk, p.cpp, p.cpg, fin_u0, fin_nu,
-                                               u0 * bpu, a.eps);
+        loads_sel(p.loads, [&](auto U) {
+            k_stats<V(), U()><<<grid, kThreads, 0, s>>>(
+                a.x, w.part, a.mean, a.rstd, a.mean_lo, w.lo, p.HW, p.chunk, p.cpp, p.cpg,
+                fin_u0, fin_nu, u0 * bpu, a.eps);
+        });
     });
     prof_end(s, tok);
 }
@@ -1313,10 +1344,12 @@ void launch_reduce(const Plan& p, const BwdArgs& a, const WsView& w, int64_t fin
     const int tok = prof_begin(s, nu ? (silu ? "gn_silu_bwd_reduce" : "gn_bwd_reduce")
                                      : "gn_bwd_finish");
     auto go = [&](auto V, auto S, auto L) {
-        k_bwd_reduce<V(), S(), L()><<<grid, kThreads, 0, s>>>(
+        loads_sel(p.loads, [&](auto U) {
+        k_bwd_reduce<V(), S(), L(), U()><<<grid, kThreads, 0, s>>>(
             a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, w.part, w.part_x, w.lo,
             w.plane_sums, w.unit_sums, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, fin_u0, fin_nu,
             u0 * bpu);
+        });
     };
     bsel(p.vec4, [&](auto V) {
         if (silu)
@@ -1405,6 +1438,7 @@ bool make_plan(int64_t N, int64_t C, int64_t HW, int64_t G, const Tuning& t, Pla
     // per unit of the previous batch
     if (p->blocks + p->units > 0x7fffffff || C > 0x7fffffff) return false;
     p->vec4 = (HW % 4) == 0;
+    p->loads = t.loads;
     p->upb_fwd = units_per_batch(*p, t, 1);
     p->upb_bwd = units_per_batch(*p, t, 2);
     return true;

@@ -27,6 +27,13 @@ int soar_synth_stress(float* out, int64_t n, uint64_t seed, double center,
 /* Plain 128-bit copy dst[i] = src[i] (n a multiple of 4, 16-byte aligned):
  * the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE. */
 int soar_synth_copy(const float* src, float* dst, int64_t n, void* stream);
+/* Streaming-ceiling kernels over n floats (a multiple of 4, 16-byte aligned
+ * buffers of n floats each): kind 0 reads a, 1 copies a to out, 2 writes
+ * out = a + b, 3 reads a and b.  One 256-thread block per 8192-float chunk,
+ * like the library's streaming passes.  The read-only kinds leave out
+ * unchanged (they write it only if a block's sum is exactly 1234.5). */
+int soar_synth_stream(int kind, const float* a, const float* b, float* out,
+                      int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

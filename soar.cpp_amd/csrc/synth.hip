@@ -69,6 +69,58 @@ __global__ __launch_bounds__(256) void k_copy(const f4* __restrict__ src, f4* __
         dst[i] = src[i];
 }
 
+// Streaming ceilings: plain HBM patterns built like the library's
+// streaming passes (one 256-thread block per contiguous chunk of 8192
+// floats, 128-bit accesses, four loads in flight per thread, non-temporal
+// stores), so the GroupNorm kernels can be set against what this memory
+// system gives a simple kernel of the same shape.
+//   KIND 0  read a                     (1 tensor pass)
+//   KIND 1  out = a                    (2)
+//   KIND 2  out = a + b                (3)
+//   KIND 3  read a and b               (2)
+// The read-only kinds store only if the sum takes one exact value, which
+// keeps the loads alive (the store stays inside `out`, block-indexed).
+constexpr int64_t kStreamChunk4 = 8192 / 4;
+
+template <int KIND>
+__global__ __launch_bounds__(256) void k_stream(const f4* __restrict__ a,
+                                                const f4* __restrict__ b, f4* __restrict__ out,
+                                                int64_t n4) {
+    const int64_t base = (int64_t)blockIdx.x * kStreamChunk4;
+    const int64_t end = min(base + kStreamChunk4, n4);
+    float s = 0.f;
+    int64_t i = base + threadIdx.x;
+    for (; i + 3 * 256 < end; i += 4 * 256) {
+        f4 v[4], w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            v[u] = a[i + u * 256];
+            if (KIND >= 2) w[u] = b[i + u * 256];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (KIND == 0) s += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+            if (KIND == 3) s += (v[u].x * w[u].x + v[u].y * w[u].y) + (v[u].z * w[u].z + v[u].w * w[u].w);
+            if (KIND == 1) __builtin_nontemporal_store(v[u], &out[i + u * 256]);
+            if (KIND == 2) __builtin_nontemporal_store(v[u] + w[u], &out[i + u * 256]);
+        }
+    }
+    for (; i < end; i += 256) {
+        const f4 v = a[i];
+        if (KIND == 0) s += (v.x + v.y) + (v.z + v.w);
+        if (KIND == 3) {
+            const f4 w = b[i];
+            s += (v.x * w.x + v.y * w.y) + (v.z * w.z + v.w * w.w);
+        }
+        if (KIND == 1) __builtin_nontemporal_store(v, &out[i]);
+        if (KIND == 2) __builtin_nontemporal_store(v + b[i], &out[i]);
+    }
+    if ((KIND == 0 || KIND == 3) && s == 1234.5f) {
+        f4 o = {s, s, s, s};
+        out[base + threadIdx.x % (end - base)] = o;
+    }
+}
+
 inline uint64_t stream_key(uint64_t seed, uint32_t id) { return splitmix_at(seed, id); }
 
 inline dim3 grid_for(int64_t items) {
@@ -111,6 +163,30 @@ __attribute__((visibility("default"))) int soar_synth_stress(float* out, int64_t
     k_stress<<<grid_for((n + 1) / 2), 256, 0, (hipStream_t)stream>>>(
         out, n, stream_key(seed, 1), stream_key(seed, 5), stream_key(seed, 6), center, sd, p, om,
         osd);
+    return status();
+}
+
+__attribute__((visibility("default"))) int soar_synth_stream(int kind, const float* a,
+                                                             const float* b, float* out,
+                                                             int64_t n, void* stream) {
+    if (n <= 0) return 0;
+    if (kind < 0 || kind > 3 || !a || !out || (n % 4) || ((uintptr_t)a & 15) ||
+        ((uintptr_t)out & 15) || (kind >= 2 && (!b || ((uintptr_t)b & 15))))
+        return -1;
+    const int64_t n4 = n / 4;
+    const int64_t blocks = (n4 + kStreamChunk4 - 1) / kStreamChunk4;
+    if (blocks > 0x7fffffff) return -1;
+    const dim3 g((unsigned)blocks);
+    const hipStream_t s = (hipStream_t)stream;
+    const f4* a4 = (const f4*)a;
+    const f4* b4 = (const f4*)b;
+    f4* o4 = (f4*)out;
+    switch (kind) {
+        case 0: k_stream<0><<<g, 256, 0, s>>>(a4, b4, o4, n4); break;
+        case 1: k_stream<1><<<g, 256, 0, s>>>(a4, b4, o4, n4); break;
+        case 2: k_stream<2><<<g, 256, 0, s>>>(a4, b4, o4, n4); break;
+        default: k_stream<3><<<g, 256, 0, s>>>(a4, b4, o4, n4); break;
+    }
     return status();
 }
 

@@ -48,6 +48,7 @@ TUNE_SMALL_UNIT = 9
 TUNE_PW_SMALL = 10
 TUNE_FOLD_MAX = 11
 TUNE_PW_SPLITK = 12
+TUNE_LOADS = 13
 
 
 class SoarUnavailable(RuntimeError):
@@ -184,6 +185,7 @@ SYNTH_SIGNATURES = {
     "soar_synth_stress": (_c.c_int, [_P, _I64, _c.c_uint64, _c.c_double, _c.c_double,
                                      _c.c_double, _c.c_double, _c.c_double, _P]),
     "soar_synth_copy": (_c.c_int, [_P, _P, _I64, _P]),
+    "soar_synth_stream": (_c.c_int, [_c.c_int, _P, _P, _P, _I64, _P]),
 }
 
 _LIB = None
@@ -570,6 +572,24 @@ def synth_stress(t, seed, center=1e3, std=1e-2, p=1e-3, out_mean=0.0, out_std=50
     if rc:
         raise SoarError(rc, "soar_synth_stress failed")
     return t
+
+
+# kinds of synth_stream: name -> (kind, tensor passes per launch)
+STREAM_KINDS = {"read": (0, 1), "copy": (1, 2), "2r1w": (2, 3), "2r": (3, 2)}
+
+
+def synth_stream(kind, a, b, out, stream=None):
+    """One launch of a streaming-ceiling kernel (soar_synth_stream): kind
+    "read" reads a, "copy" copies a to out, "2r1w" writes out = a + b, "2r"
+    reads a and b.  Buffers: equal-sized contiguous float32."""
+    k = STREAM_KINDS[kind][0]
+    for t in (a, b, out):
+        if t is not None and t.numel() != a.numel():
+            raise ValueError("synth_stream buffers must have equal sizes")
+    rc = synth_lib().soar_synth_stream(k, _ptr(a), _ptr(b), _ptr(out), a.numel(),
+                                       _stream(stream))
+    if rc:
+        raise SoarError(rc, "soar_synth_stream failed")
 
 
 def synth_copy(src, dst, stream=None):
