@@ -13,7 +13,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "build", "libsoar_oracle.so")
+LIB_PATH = os.path.join(os.environ.get("SOAR_ORACLE_BUILD") or os.path.join(HERE, "build"),
+                        "libsoar_oracle.so")
 
 _F = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _D = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")

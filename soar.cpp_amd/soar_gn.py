@@ -18,8 +18,11 @@ import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-LIB_PATH = os.path.join(HERE, "lib", "libsoar_gn.so")
-SYNTH_PATH = os.path.join(HERE, "lib", "libsoar_synth.so")
+# SOAR_LIB_DIR selects another build of the two libraries (the sanitizer
+# build of `make sanitize`, for instance); the default is the in-tree lib/.
+LIB_DIR = os.environ.get("SOAR_LIB_DIR") or os.path.join(HERE, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libsoar_gn.so")
+SYNTH_PATH = os.path.join(LIB_DIR, "libsoar_synth.so")
 HEADER_PATH = os.path.join(ROOT, "include", "soar_gn.h")
 
 SOAR_OK = 0

@@ -7,7 +7,7 @@ import pytest
 
 from conftest import ROOT
 
-BUILD = os.path.join(ROOT, "soar.cpp_amd", "host", "build")
+BUILD = os.environ.get("SOAR_HOST_BUILD") or os.path.join(ROOT, "soar.cpp_amd", "host", "build")
 
 
 def run(name, timeout=300):
