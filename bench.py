@@ -21,7 +21,8 @@ cfg4_chain, cfg5), the CBA block with a pointwise conv (cba_pw), the CBA
 depthwise convolutions at 1x64x2048^2 (dw_k3, dw_k5, dw_k7, dw_k3d5,
 dw_k3s2), SOAR training steps (train_nano64/512/1024) and the streaming
 ceilings of this memory system for plain kernels of the library's shape
-(stream_read, stream_copy, stream_2r1w, stream_2r over 1 GiB buffers).
+(stream_read, stream_copy, stream_2r1w, stream_2r over 1 GiB buffers; stream_planes_read,
+stream_planes_copy, stream_planes_copy_pad4k: the pointwise convolution's 64-plane pattern).
 """
 import argparse
 import json
@@ -56,7 +57,12 @@ PEAK_MFMA_F32 = 157.3  # TFLOP/s, dense fp32 matrix
 # Streaming ceilings (libsoar_synth.so soar_synth_stream over 1 GiB
 # buffers): name -> pattern
 STREAM_CONFIGS = {"stream_read": "read", "stream_copy": "copy", "stream_2r1w": "2r1w",
-                  "stream_2r": "2r"}
+                  "stream_2r": "2r",
+                  # the pointwise convolution's access pattern over 64 planes of
+                  # 16 MiB (a 1 GiB NCHW tensor), at the tensor's plane stride and
+                  # with the stride padded by 4 KiB
+                  "stream_planes_read": "planes_read", "stream_planes_copy": "planes_copy",
+                  "stream_planes_copy_pad4k": "planes_copy_pad"}
 
 # Depthwise convolutions of the CBA blocks at 1x64x2048^2, forward + backward
 # (dx, dW, db): name -> (K, stride, dilation); pad = dilation*(K-1)/2
@@ -302,21 +308,37 @@ def bench_stream(args):
     import soar_gn as gn
     pattern = STREAM_CONFIGS[args.config]
     n = 1 << 28
-    a = torch.empty(n, device="cuda")
-    b = torch.empty(n, device="cuda")
-    out = torch.empty(n, device="cuda")
-    gn.synth_normal(a, SEED, 1)
-    gn.synth_normal(b, SEED, 4)
-    passes = gn.STREAM_KINDS[pattern][1]
+    if pattern.startswith("planes"):
+        plane = n // 64
+        stride = plane + (1024 if pattern.endswith("pad") else 0)
+        a = torch.empty(64 * stride, device="cuda")
+        out = torch.empty(64 * stride, device="cuda")
+        gn.synth_normal(a, SEED, 1)
+        write = pattern != "planes_read"
+        passes = 2 if write else 1
+        kname = f"k_planes<{str(write).lower()}>"
+        launch = lambda: gn.synth_planes(write, a, out, plane, stride)
+        what = (f"the pointwise convolution's pattern over 64 planes of 16 MiB, plane stride "
+                f"{stride * 4} bytes: {'copy' if write else 'read'}")
+    else:
+        a = torch.empty(n, device="cuda")
+        b = torch.empty(n, device="cuda")
+        out = torch.empty(n, device="cuda")
+        gn.synth_normal(a, SEED, 1)
+        gn.synth_normal(b, SEED, 4)
+        passes = gn.STREAM_KINDS[pattern][1]
+        kname = f"k_stream<{gn.STREAM_KINDS[pattern][0]}>"
+        launch = lambda: gn.synth_stream(pattern, a, b, out)
+        what = f"streaming ceiling: {pattern} over 1 GiB buffers ({passes} tensor passes)"
     for _ in range(args.warmup):
-        gn.synth_stream(pattern, a, b, out)
+        launch()
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
     t0 = time.perf_counter()
     for e0, e1 in evs:
         e0.record()
-        gn.synth_stream(pattern, a, b, out)
+        launch()
         e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -324,14 +346,12 @@ def bench_stream(args):
     med = ms[len(ms) // 2]
     nbytes = passes * n * 4
     value = nbytes / (med * 1e-3) / 1e9
-    kname = f"k_stream<{gn.STREAM_KINDS[pattern][0]}>"
     print(json.dumps({
         "metric": f"{args.config} achieved HBM GB/s (streaming ceiling, 1 GiB buffers)",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(med, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic N(0,1)",
-        "config": {"workload": f"streaming ceiling: {pattern} over 1 GiB buffers "
-                               f"({passes} tensor passes per launch)"},
+        "config": {"workload": what},
         "frac_of_peak": round(value / PEAK_GBS, 4), "wall_s_timed": round(wall, 4),
         "best_ms": round(ms[0], 4),
         "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(value, 1),

@@ -34,6 +34,13 @@ int soar_synth_copy(const float* src, float* dst, int64_t n, void* stream);
  * unchanged (they write it only if a block's sum is exactly 1234.5). */
 int soar_synth_stream(int kind, const float* a, const float* b, float* out,
                       int64_t n, void* stream);
+/* The pointwise convolution's access pattern over 64 planes of plane_floats
+ * floats (a multiple of 1024), plane c at a + c * stride_floats (buffers of
+ * 64 * stride_floats floats, 16-byte aligned): each block walks a 1024-float
+ * window of every plane in 512-byte runs, all planes per run.  write = 1
+ * copies a to out in that order, 0 only reads a. */
+int soar_synth_planes(int write, const float* a, float* out, int64_t plane_floats,
+                      int64_t stride_floats, void* stream);
 
 #ifdef __cplusplus
 }

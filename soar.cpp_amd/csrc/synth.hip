@@ -121,6 +121,39 @@ __global__ __launch_bounds__(256) void k_stream(const f4* __restrict__ a,
     }
 }
 
+// Multi-plane pattern of the pointwise convolution: 64 planes of
+// plane_floats floats each, plane c at a + c * stride_floats.  Block b owns
+// the 1024-float window [1024 b, 1024 b + 1024) of every plane and walks it
+// in 128-float (512-byte) runs, all 64 planes per run (32 planes' loads in
+// flight per thread group), as the convolution's K loop reads x.  WRITE:
+// out (same plane layout) = a; else read only (out written only if a sum
+// takes one exact value, inside block b's window of plane 0).
+template <bool WRITE>
+__global__ __launch_bounds__(256) void k_planes(const float* __restrict__ a,
+                                                float* __restrict__ out, int64_t stride_floats) {
+    const int t = threadIdx.x, pl = t >> 5, off = 4 * (t & 31);
+    const int64_t w0 = (int64_t)blockIdx.x * 1024;
+    float s = 0.f;
+    for (int64_t r = 0; r < 1024; r += 128) {
+        for (int pg = 0; pg < 64; pg += 32) {
+            f4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                v[u] = *reinterpret_cast<const f4*>(a + (int64_t)(pg + 8 * u + pl) * stride_floats +
+                                                    w0 + r + off);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (WRITE)
+                    __builtin_nontemporal_store(v[u], reinterpret_cast<f4*>(
+                        out + (int64_t)(pg + 8 * u + pl) * stride_floats + w0 + r + off));
+                else
+                    s += v[u].x + v[u].w;
+            }
+        }
+    }
+    if (!WRITE && s == 1234.5f) out[w0 + t] = s;
+}
+
 inline uint64_t stream_key(uint64_t seed, uint32_t id) { return splitmix_at(seed, id); }
 
 inline dim3 grid_for(int64_t items) {
@@ -187,6 +220,22 @@ __attribute__((visibility("default"))) int soar_synth_stream(int kind, const flo
         case 2: k_stream<2><<<g, 256, 0, s>>>(a4, b4, o4, n4); break;
         default: k_stream<3><<<g, 256, 0, s>>>(a4, b4, o4, n4); break;
     }
+    return status();
+}
+
+__attribute__((visibility("default"))) int soar_synth_planes(int write, const float* a,
+                                                             float* out, int64_t plane_floats,
+                                                             int64_t stride_floats,
+                                                             void* stream) {
+    if (plane_floats <= 0) return 0;
+    if (!a || !out || plane_floats % 1024 || stride_floats < plane_floats || stride_floats % 4 ||
+        ((uintptr_t)a & 15) || ((uintptr_t)out & 15) || plane_floats / 1024 > 0x7fffffff)
+        return -1;
+    const dim3 g((unsigned)(plane_floats / 1024));
+    if (write)
+        k_planes<true><<<g, 256, 0, (hipStream_t)stream>>>(a, out, stride_floats);
+    else
+        k_planes<false><<<g, 256, 0, (hipStream_t)stream>>>(a, out, stride_floats);
     return status();
 }
 

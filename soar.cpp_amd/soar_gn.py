@@ -189,6 +189,7 @@ SYNTH_SIGNATURES = {
                                      _c.c_double, _c.c_double, _c.c_double, _P]),
     "soar_synth_copy": (_c.c_int, [_P, _P, _I64, _P]),
     "soar_synth_stream": (_c.c_int, [_c.c_int, _P, _P, _P, _I64, _P]),
+    "soar_synth_planes": (_c.c_int, [_c.c_int, _P, _P, _I64, _I64, _P]),
 }
 
 _LIB = None
@@ -593,6 +594,19 @@ def synth_stream(kind, a, b, out, stream=None):
                                        _stream(stream))
     if rc:
         raise SoarError(rc, "soar_synth_stream failed")
+
+
+def synth_planes(write, a, out, plane_floats, stride_floats, stream=None):
+    """One launch of the 64-plane access pattern of the pointwise
+    convolution (soar_synth_planes); a and out hold 64 * stride_floats
+    floats."""
+    for t in (a, out):
+        if t.numel() < 64 * stride_floats:
+            raise ValueError("synth_planes buffers must hold 64 planes at the stride")
+    rc = synth_lib().soar_synth_planes(1 if write else 0, _ptr(a), _ptr(out), plane_floats,
+                                       stride_floats, _stream(stream))
+    if rc:
+        raise SoarError(rc, "soar_synth_planes failed")
 
 
 def synth_copy(src, dst, stream=None):
