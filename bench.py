@@ -439,32 +439,46 @@ def train_cpu_baseline(H, W, variant):
 def bench_train(args):
     """Images/s of soar_train_step on one GPU (inputs are host arrays, as
     the C-ABI takes them: the timed step includes their copy to the
-    device and the loss read-back, as in the reference's train_step)."""
+    device and the loss read-back, as in the reference's train_step).
+    `value` is the default handle, whose steps replay a HIP graph from the
+    second step on; `eager_ms_per_step` times a second handle with graphs
+    off, which also serves the per-kernel timing pass (a replayed graph
+    has no host calls to time)."""
     import numpy as np
     import torch
     import soar_gn as gn
     import soar_model as sm
     variant, H, W = TRAIN_CONFIGS[args.config]
-    m = sm.SOAR(1, 1, variant, seed=SEED)
     r = np.random.default_rng(SEED)
     img = r.normal(0.5, 0.25, size=(1, H, W)).astype(np.float32)
     yy, xx = np.mgrid[0:H, 0:W]
     mask = (((yy - H / 2) ** 2 + (xx - W / 3) ** 2) < (min(H, W) / 3) ** 2).astype(np.float32)
     mask = mask[None]
-    for _ in range(args.warmup):
-        m.train_step(img, mask, 1e-3)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        m.train_step(img, mask, 1e-3)
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / args.steps
+
+    def timed(m):
+        for _ in range(args.warmup):
+            m.train_step(img, mask, 1e-3)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            m.train_step(img, mask, 1e-3)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / args.steps
+
+    m = sm.SOAR(1, 1, variant, seed=SEED)
+    dt = timed(m)
+    graphed = m.graph_info()
+    mem = m.memory_info()
+    m.close()
+    me = sm.SOAR(1, 1, variant, seed=SEED)
+    me.set_graph_mode(False)
+    dt_eager = timed(me)
     kernels = []
     if not args.no_kernel_timing:
         gn.prof_summary()  # drop anything recorded so far
         gn.prof_enable(True)
         for _ in range(args.steps):
-            m.train_step(img, mask, 1e-3)
+            me.train_step(img, mask, 1e-3)
         torch.cuda.synchronize()
         gn.prof_enable(False)
         recs = gn.prof_summary()
@@ -473,14 +487,16 @@ def bench_train(args):
                     "launches_per_step": k["launches"] // args.steps}
                    for k in sorted(recs, key=lambda k: -k["total_ms"])[:10]]
         kernels.append({"kernel": "(all timed kernels)", "ms_per_step": round(total, 4)})
-    mem = m.memory_info()
+    me.close()
     out = {
         "metric": f"SOAR {variant} train_step images/s, 1x{H}x{W} fp32",
         "value": round(1.0 / dt, 3), "unit": "images/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": args.config, "variant": variant, "image": [1, H, W],
-                   "loss": "CompositeLoss(0.5, 0.5)", "optimizer": "AdamW lr 1e-3, clip 2.0"},
+                   "loss": "CompositeLoss(0.5, 0.5)", "optimizer": "AdamW lr 1e-3, clip 2.0",
+                   "hip_graph": {"on": graphed[0], "graphs": graphed[1]}},
+        "eager_ms_per_step": round(dt_eager * 1e3, 4),
         "roofline": None,
         "kernels_top": kernels,
         "memory": mem,

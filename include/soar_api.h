@@ -53,6 +53,11 @@ SOAR_API int soar_load_weights(void* handle, const char* path);
 
 /* One training step on one image: forward, Dice+BCE loss, backward, clip,
  * AdamW step with learning_rate, zero_grad.  out_* may be NULL.
+ * The step runs on the handle's own stream with the loss sums, the clip
+ * decision and AdamW's bias corrections on the device; from the second
+ * step of an image shape on it is captured into a HIP graph and replayed
+ * (one graph per shape; soar_model_set_graph_mode).  Results are the same
+ * bits with or without the graph.
  * Replaces: soar_train_step (c_api.h:24-32). */
 SOAR_API int soar_train_step(void* handle, const float* image_data,
                              const float* mask_data, int channels, int height,
@@ -101,6 +106,15 @@ SOAR_API int soar_model_forward_backward(void* handle, const float* image_data,
 /* Zeroes every parameter gradient (what the reference's Trainer does
  * after each optimizer step). */
 SOAR_API int soar_model_zero_grad(void* handle);
+/* on != 0 (the default, or SOAR_TRAIN_GRAPH=0 in the environment at
+ * creation for off): soar_train_step captures and replays its device work
+ * as a HIP graph per image shape.  Off drops the graphs held.  No
+ * counterpart in the reference (its step is eager). */
+SOAR_API int soar_model_set_graph_mode(void* handle, int on);
+/* Whether graph mode is on (it turns itself off when a capture fails) and
+ * how many training-step graphs the handle holds (either may be NULL). */
+SOAR_API int soar_model_graph_info(void* handle, int* graph_mode,
+                                   int* graphs_held);
 /* The 7 metrics of the last soar_train_step (the last entry is the global
  * gradient norm before clipping). */
 SOAR_API int soar_model_last_metrics(void* handle, float* out_metrics);

@@ -370,6 +370,12 @@ SOAR_API int soar_memcpy_h2d(void* dst, const void* src, size_t bytes,
                              void* stream);
 SOAR_API int soar_memcpy_d2h(void* dst, const void* src, size_t bytes,
                              void* stream);
+/* Asynchronous copy on `stream` with no synchronisation: kind 0 host to
+ * device, 1 device to host, 2 device to device.  The host buffer must stay
+ * valid (and, for a copy recorded into a graph, pinned) until the stream
+ * reaches the copy.  No counterpart in the reference. */
+SOAR_API int soar_memcpy_async(void* dst, const void* src, size_t bytes,
+                               int kind, void* stream);
 /* Device-to-device copy, asynchronous on `stream` (Tensor::clone and the
  * per-sample slicing of Trainer::train_step, src/tensor/tensor.cpp and
  * src/engine/trainer.cpp:182, which call cudaMemcpyAsync DtoD). */

@@ -287,6 +287,25 @@ SOAR_API int soar_multi_tensor_scale_device(float* const* tensors,
                                             int n_tensors, float scale,
                                             void* stream);
 
+/* The same AdamW step with lr, step_size and sqrt_bc2 read from a DEVICE
+ * array scalars[3] when the kernel runs, so a captured training step can
+ * replay with the next step's values (the caller writes them there, e.g.
+ * with a captured copy from pinned memory).  Arithmetic as above. */
+SOAR_API int soar_adamw_multi_tensor_device_scalars(
+    float* const* params, const float* const* grads, float* const* m,
+    float* const* v, const int64_t* numel, int n_tensors,
+    const float* scalars, float beta1, float beta2, float eps, float wd,
+    void* stream);
+/* The clip of AdamW::clip_grad_norm (adamw.cpp:44-54) with its decision on
+ * the device: total = (float)sqrt(*norm_sq) (norm_sq a DEVICE double, as
+ * soar_multi_tensor_norm_sq_device writes it); when total > max_norm and
+ * total > 1e-6 every tensor is scaled by max_norm / total, else nothing
+ * changes.  No host read-back (capture-safe). */
+SOAR_API int soar_multi_tensor_clip_device(float* const* tensors,
+                                           const int64_t* numel, int n_tensors,
+                                           const double* norm_sq,
+                                           float max_norm, void* stream);
+
 /* tensors[k][i] = value (one launch for a whole gradient list:
  * Module::zero_grad, module.hpp:71-75, without a launch per tensor). */
 SOAR_API int soar_multi_tensor_fill_device(float* const* tensors,
@@ -353,6 +372,32 @@ SOAR_API int soar_dice_bce_loss_backward_ex(
     float grad_out, float w, float bw, float dw, float pos_weight,
     float smooth, float inter, float sum_p, float sum_y, size_t n,
     unsigned flags, void* stream);
+
+/* ---- the Dice+BCE loss with its sums kept on the device ------------------ */
+/* No counterpart in the reference: the loss of soar_dice_bce_loss_forward
+ * split so that no host read-back sits inside a training step (for stream
+ * capture).  sums (DEVICE, 4 doubles) = the BCE sum, sum p*y, sum p, sum y
+ * (the same fixed-order fp64 sums); workspace from
+ * soar_dice_bce_loss_workspace_bytes(n).  soar_dice_bce_loss_from_sums
+ * finishes them on the HOST into the out[6] of soar_dice_bce_loss_forward,
+ * bit for bit.  The backward reads inter, sum_p and sum_y from the device
+ * sums, handed on as fp32 as the host finish does. */
+SOAR_API size_t soar_dice_bce_loss_workspace_bytes(size_t n);
+SOAR_API int soar_dice_bce_loss_sums_device(const float* logits,
+                                            const float* targets, size_t n,
+                                            float pos_weight, double* sums,
+                                            void* workspace,
+                                            size_t workspace_bytes,
+                                            void* stream);
+SOAR_API int soar_dice_bce_loss_from_sums(const double* sums, size_t n,
+                                          float weight, float bce_weight,
+                                          float dice_weight, float smooth,
+                                          float* out);
+SOAR_API int soar_dice_bce_loss_backward_device(
+    const float* logits, const float* targets, float* grad_logits,
+    float grad_out, float w, float bw, float dw, float pos_weight,
+    float smooth, const double* sums, size_t n, unsigned flags,
+    void* stream);
 
 #ifdef __cplusplus
 }

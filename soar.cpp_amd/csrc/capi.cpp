@@ -212,6 +212,13 @@ namespace gn {
 
 int prof_begin(hipStream_t s, const char* kernel) {
     if (!g_prof_on.load(std::memory_order_relaxed) || soar::capi::g_quiet_call) return -1;
+    // no timing events inside a graph being captured
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return -1;
+    }
+    if (cs != hipStreamCaptureStatusNone) return -1;
     std::lock_guard<std::mutex> lk(g_prof_mu);
     ProfRec r{kernel, take_event(), take_event()};
     if (!r.start || !r.stop) return -1;
@@ -961,6 +968,21 @@ SOAR_API int soar_memcpy_h2d(void* dst, const void* src, size_t bytes, void* str
     hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     return e == hipSuccess ? ok() : hip_fail(e, "host-to-device copy");
+}
+
+SOAR_API int soar_memcpy_async(void* dst, const void* src, size_t bytes, int kind,
+                               void* stream) {
+    if (bytes == 0) return ok();
+    if (!dst || !src) return fail(SOAR_EINVAL, "dst and src must not be NULL");
+    if (kind < 0 || kind > 2) return fail(SOAR_EINVAL, "kind must be 0, 1 or 2");
+    int rc = require_device();
+    if (rc) return rc;
+    if (kind != 1 && (rc = check_dev(dst, bytes, "dst"))) return rc;  // (kind 1: dst is host)
+    if (kind != 0 && (rc = check_dev(src, bytes, "src"))) return rc;  // (kind 0: src is host)
+    static const hipMemcpyKind kinds[3] = {hipMemcpyHostToDevice, hipMemcpyDeviceToHost,
+                                           hipMemcpyDeviceToDevice};
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, kinds[kind], static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "asynchronous copy");
 }
 
 SOAR_API int soar_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {

@@ -857,15 +857,28 @@ __global__ __launch_bounds__(kThreads) void k_loss_finish(const double* __restri
     }
 }
 
+// Dice terms from the loss sums (inter, sum_p, sum_y handed on as fp32, as
+// the host finish does), rounded as the host evaluates them.
+__device__ __forceinline__ void dice_terms(const double* __restrict__ sums, float smooth,
+                                           float* denom, float* numer) {
+#pragma clang fp contract(off)
+    const float inter = (float)sums[1], sum_p = (float)sums[2], sum_y = (float)sums[3];
+    *denom = sum_p + sum_y + smooth;
+    *numer = 2.0f * inter + smooth;
+}
+
 // gz += BCE gradient * scale_bce + Dice gradient * scale_dice
-// (loss_kernels.cu:212-252; losses.cpp:497-541)
+// (loss_kernels.cu:212-252; losses.cpp:497-541).  sums (device, optional):
+// denom and numer come from the loss sums there instead of the arguments.
 template <bool ACC>
 __global__ __launch_bounds__(kThreads) void k_dice_bce_bwd(const float* __restrict__ z,
                                                            const float* __restrict__ y,
                                                            float* __restrict__ gz, int64_t n,
                                                            float scale_bce, float scale_dice,
                                                            float pos_weight, float denom,
-                                                           float numer) {
+                                                           float numer, float smooth,
+                                                           const double* __restrict__ sums) {
+    if (sums) dice_terms(sums, smooth, &denom, &numer);
     const float denom_sq = denom * denom;
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * kThreads) {
@@ -1064,14 +1077,47 @@ __global__ __launch_bounds__(kThreads) void k_multi_set(float* const* __restrict
     }
 }
 
+// Gradient clip with the coefficient formed on the device from the squared
+// norm (norm_sq[0], float64), as the host does it: total = (float)sqrt(sq);
+// when total > max_norm and total > 1e-6 every tensor is scaled by
+// max_norm / total (one fp32 division), else nothing changes.
+__global__ __launch_bounds__(kThreads) void k_multi_clip(float* const* __restrict__ t,
+                                                         const int64_t* __restrict__ numel,
+                                                         int n_tensors,
+                                                         const double* __restrict__ norm_sq,
+                                                         float max_norm) {
+#pragma clang fp contract(off)
+    const float total = (float)sqrt(norm_sq[0]);
+    if (!(total > max_norm && total > 1e-6f)) return;  // uniform over the grid
+    const float coef = max_norm / total;
+    __shared__ int pref[kMaxMultiTensors + 1];
+    const ChunkMap map = build_chunk_map(numel, n_tensors, pref);
+    for (int c = blockIdx.x; c < map.total(); c += gridDim.x) {
+        int k;
+        int64_t first;
+        map.locate(c, &k, &first);
+        float* p = t[k];
+        const int64_t end = min(first + kMtChunk, numel[k]);
+        for (int64_t i = first + threadIdx.x; i < end; i += kThreads) p[i] = p[i] * coef;
+    }
+}
+
 // The AdamW update of adamw.cpp:60-108, operation by operation in fp32
 // with no fused multiply-adds, so it matches a scalar IEEE evaluation of
 // the same expressions bit for bit.
+// scalars (device, optional): lr, step_size, sqrt_bc2 are read there
+// instead of the arguments (a captured step replays with new values).
 __global__ __launch_bounds__(kThreads) void k_adamw_multi(
     float* const* __restrict__ P, const float* const* __restrict__ G, float* const* __restrict__ M,
     float* const* __restrict__ V, const int64_t* __restrict__ numel, int n_tensors, float lr,
-    float beta1, float beta2, float eps, float wd, float step_size, float sqrt_bc2) {
+    float beta1, float beta2, float eps, float wd, float step_size, float sqrt_bc2,
+    const float* __restrict__ scalars) {
 #pragma clang fp contract(off)
+    if (scalars) {
+        lr = scalars[0];
+        step_size = scalars[1];
+        sqrt_bc2 = scalars[2];
+    }
     __shared__ int pref[kMaxMultiTensors + 1];
     const ChunkMap map = build_chunk_map(numel, n_tensors, pref);
     const float one_m_b1 = 1.0f - beta1, one_m_b2 = 1.0f - beta2;
@@ -1357,7 +1403,7 @@ hipError_t launch_loss_sums(const float* z, const float* y, int64_t n, float pos
 hipError_t launch_dice_bce_backward(const float* z, const float* y, float* gz, int64_t n,
                                     float go, float w, float bw, float dw, float pos_weight,
                                     float smooth, float inter, float sum_p, float sum_y, bool acc,
-                                    hipStream_t s) {
+                                    hipStream_t s, const double* sums) {
     const float scale_bce = bw > 0.0f ? (go * w * bw) / (float)n : 0.0f;
     const float scale_dice = dw > 0.0f ? go * w * dw : 0.0f;
     const float denom = sum_p + sum_y + smooth;
@@ -1365,7 +1411,7 @@ hipError_t launch_dice_bce_backward(const float* z, const float* y, float* gz, i
     bsel(acc, [&](auto A) {
         k_dice_bce_bwd<A()><<<blocks_for(n), kThreads, 0, s>>>(z, y, gz, n, scale_bce,
                                                                scale_dice, pos_weight, denom,
-                                                               numer);
+                                                               numer, smooth, sums);
     });
     return hipGetLastError();
 }
@@ -1426,9 +1472,16 @@ hipError_t launch_multi_fill(float* const* t, const int64_t* numel, int n_tensor
 hipError_t launch_adamw_multi(float* const* p, const float* const* g, float* const* m,
                               float* const* v, const int64_t* numel, int n_tensors, float lr,
                               float beta1, float beta2, float eps, float wd, float step_size,
-                              float sqrt_bc2, hipStream_t s) {
+                              float sqrt_bc2, hipStream_t s, const float* scalars) {
     k_adamw_multi<<<kMultiBlocks, kThreads, 0, s>>>(p, g, m, v, numel, n_tensors, lr, beta1,
-                                                     beta2, eps, wd, step_size, sqrt_bc2);
+                                                     beta2, eps, wd, step_size, sqrt_bc2,
+                                                     scalars);
+    return hipGetLastError();
+}
+
+hipError_t launch_multi_clip(float* const* t, const int64_t* numel, int n_tensors,
+                             const double* norm_sq, float max_norm, hipStream_t s) {
+    k_multi_clip<<<kMultiBlocks, kThreads, 0, s>>>(t, numel, n_tensors, norm_sq, max_norm);
     return hipGetLastError();
 }
 

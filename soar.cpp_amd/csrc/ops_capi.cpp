@@ -719,6 +719,69 @@ SOAR_API int soar_dice_bce_loss_backward_ex(const float* logits, const float* ta
                     inter, sum_p, sum_y, stream, acc);
 }
 
+SOAR_API size_t soar_dice_bce_loss_workspace_bytes(size_t n) {
+    return n == 0 ? 0 : soar::ops::loss_sums_workspace_bytes((int64_t)n);
+}
+
+SOAR_API int soar_dice_bce_loss_sums_device(const float* logits, const float* targets, size_t n,
+                                            float pos_weight, double* sums, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+    int rc;
+    if ((rc = require_device()) || (rc = check_dev(sums, 4 * sizeof(double), "sums"))) return rc;
+    if (n == 0) return ok();  // (the caller's finish treats n == 0 itself)
+    if ((rc = check_count(n)) || (rc = check_dev(logits, n * 4, "logits")) ||
+        (rc = check_dev(targets, n * 4, "targets")))
+        return rc;
+    const size_t need = soar::ops::loss_sums_workspace_bytes((int64_t)n);
+    if (workspace_bytes < need)
+        return fail(SOAR_EINVAL, "workspace of %zu bytes is smaller than the %zu needed",
+                    workspace_bytes, need);
+    if ((rc = check_dev(workspace, need, "workspace"))) return rc;
+    const int tok = soar::gn::prof_begin(S(stream), "dice_bce_sums");
+    hipError_t e = soar::ops::launch_loss_sums(logits, targets, (int64_t)n, pos_weight, sums,
+                                               workspace, S(stream));
+    soar::gn::prof_end(S(stream), tok);
+    return launched(e, "loss sums launch");
+}
+
+SOAR_API int soar_dice_bce_loss_from_sums(const double* sums, size_t n, float weight,
+                                          float bce_weight, float dice_weight, float smooth,
+                                          float* out) {
+    if (!out || (n > 0 && !sums)) return fail(SOAR_EINVAL, "sums and out must not be NULL");
+    if (n == 0) {
+        for (int k = 0; k < 6; ++k) out[k] = 0.0f;
+        return ok();
+    }
+    float bce, dice;
+    finish_losses(sums, n, 1.0f, smooth, &bce, &dice, &out[3], &out[4], &out[5]);
+    out[0] = weight * (bce_weight * bce + dice_weight * dice);  // losses.cpp:477
+    out[1] = bce;
+    out[2] = dice;
+    return ok();
+}
+
+SOAR_API int soar_dice_bce_loss_backward_device(const float* logits, const float* targets,
+                                                float* grad_logits, float grad_out, float w,
+                                                float bw, float dw, float pos_weight,
+                                                float smooth, const double* sums, size_t n,
+                                                unsigned flags, void* stream) {
+    bool acc;
+    int rc;
+    if ((rc = grad_flags(flags, "dice_bce_loss_backward_device", &acc))) return rc;
+    if (n == 0) return ok();
+    if ((rc = require_device()) || (rc = check_count(n)) ||
+        (rc = check_dev(sums, 4 * sizeof(double), "sums")) ||
+        (rc = check_dev(logits, n * 4, "logits")) || (rc = check_dev(targets, n * 4, "targets")) ||
+        (rc = check_dev(grad_logits, n * 4, "grad_logits")))
+        return rc;
+    const int tok = soar::gn::prof_begin(S(stream), "dice_bce_bwd");
+    hipError_t e = soar::ops::launch_dice_bce_backward(logits, targets, grad_logits, (int64_t)n,
+                                                       grad_out, w, bw, dw, pos_weight, smooth,
+                                                       0.0f, 0.0f, 0.0f, acc, S(stream), sums);
+    soar::gn::prof_end(S(stream), tok);
+    return launched(e, "loss backward launch");
+}
+
 SOAR_API int soar_dice_bce_loss_backward(const float* logits, const float* targets,
                                          float* grad_logits, float grad_out, float w, float bw,
                                          float dw, float pos_weight, float smooth, float inter,
@@ -830,6 +893,43 @@ SOAR_API int soar_adamw_multi_tensor_device(float* const* params, const float* c
                                                  beta2, eps, wd, step_size, sqrt_bc2, S(stream));
     soar::gn::prof_end(S(stream), tok);
     return launched(e, "adamw multi-tensor launch");
+}
+
+SOAR_API int soar_adamw_multi_tensor_device_scalars(
+    float* const* params, const float* const* grads, float* const* m, float* const* v,
+    const int64_t* numel, int n_tensors, const float* scalars, float beta1, float beta2,
+    float eps, float wd, void* stream) {
+    if (n_tensors == 0) return ok();
+    if (n_tensors < 0) return fail(SOAR_EINVAL, "n_tensors is negative");
+    int rc;
+    if ((rc = require_device()) || (rc = check_dev(scalars, 3 * sizeof(float), "scalars")) ||
+        (rc = check_table(params, n_tensors, "params")) ||
+        (rc = check_table(grads, n_tensors, "grads")) || (rc = check_table(m, n_tensors, "m")) ||
+        (rc = check_table(v, n_tensors, "v")) || (rc = check_table(numel, n_tensors, "numel")))
+        return rc;
+    const int tok = soar::gn::prof_begin(S(stream), "adamw_multi");
+    hipError_t e = soar::ops::launch_adamw_multi(params, grads, m, v, numel, n_tensors, 0.0f,
+                                                 beta1, beta2, eps, wd, 0.0f, 1.0f, S(stream),
+                                                 scalars);
+    soar::gn::prof_end(S(stream), tok);
+    return launched(e, "adamw multi-tensor launch");
+}
+
+SOAR_API int soar_multi_tensor_clip_device(float* const* tensors, const int64_t* numel,
+                                           int n_tensors, const double* norm_sq, float max_norm,
+                                           void* stream) {
+    if (n_tensors == 0) return ok();
+    if (n_tensors < 0) return fail(SOAR_EINVAL, "n_tensors is negative");
+    int rc;
+    if ((rc = require_device()) || (rc = check_dev(norm_sq, sizeof(double), "norm_sq")) ||
+        (rc = check_table(tensors, n_tensors, "tensors")) ||
+        (rc = check_table(numel, n_tensors, "numel")))
+        return rc;
+    const int tok = soar::gn::prof_begin(S(stream), "grad_clip");
+    hipError_t e =
+        soar::ops::launch_multi_clip(tensors, numel, n_tensors, norm_sq, max_norm, S(stream));
+    soar::gn::prof_end(S(stream), tok);
+    return launched(e, "multi-tensor clip launch");
 }
 
 SOAR_API size_t soar_multi_tensor_norm_workspace_bytes(void) {

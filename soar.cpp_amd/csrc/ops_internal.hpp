@@ -80,10 +80,12 @@ hipError_t launch_crop(const float* in, float* out, int64_t rows, int64_t Hp, in
 size_t loss_sums_workspace_bytes(int64_t n);
 hipError_t launch_loss_sums(const float* z, const float* y, int64_t n, float pos_weight,
                             double* out, void* ws, hipStream_t s);
+// sums (device, nullable): inter, sum_p, sum_y taken from the loss sums
+// there (launch_loss_sums' out) instead of the arguments.
 hipError_t launch_dice_bce_backward(const float* z, const float* y, float* gz, int64_t n,
                                     float go, float w, float bw, float dw, float pos_weight,
                                     float smooth, float inter, float sum_p, float sum_y, bool acc,
-                                    hipStream_t s);
+                                    hipStream_t s, const double* sums = nullptr);
 
 // Probabilities and the thresholded mask of a logit map.
 hipError_t launch_sigmoid_threshold(const float* z, float* p, uint8_t* mask, int64_t n,
@@ -114,9 +116,14 @@ hipError_t launch_multi_scale(float* const* t, const int64_t* numel, int n_tenso
                               hipStream_t s);
 hipError_t launch_multi_fill(float* const* t, const int64_t* numel, int n_tensors, float value,
                              hipStream_t s);
+// scalars (device, nullable): lr, step_size, sqrt_bc2 read there instead.
 hipError_t launch_adamw_multi(float* const* p, const float* const* g, float* const* m,
                               float* const* v, const int64_t* numel, int n_tensors, float lr,
                               float beta1, float beta2, float eps, float wd, float step_size,
-                              float sqrt_bc2, hipStream_t s);
+                              float sqrt_bc2, hipStream_t s, const float* scalars = nullptr);
+// Clip by the coefficient formed on the device from norm_sq[0] (see
+// k_multi_clip).
+hipError_t launch_multi_clip(float* const* t, const int64_t* numel, int n_tensors,
+                             const double* norm_sq, float max_norm, hipStream_t s);
 
 }  // namespace soar::ops

@@ -70,4 +70,24 @@ struct ShapeError : SoarError {
     explicit ShapeError(const std::string& w) : SoarError(StatusCode::ShapeError, w) {}
 };
 
+// The stream (a hipStream_t) that the host layer's device work goes to:
+// every C-ABI call of the layers, the autograd nodes, the loss and the
+// optimizer passes exec::stream().  Thread-local; null (the device's
+// default stream) unless a StreamScope is active, as during a model
+// handle's training step, which runs on its own stream so that it can be
+// captured into a graph.
+namespace exec {
+void* stream() noexcept;
+class StreamScope {
+public:
+    explicit StreamScope(void* stream) noexcept;
+    ~StreamScope();
+    StreamScope(const StreamScope&) = delete;
+    StreamScope& operator=(const StreamScope&) = delete;
+
+private:
+    void* prev_;
+};
+}  // namespace exec
+
 }  // namespace soar

@@ -29,6 +29,16 @@ public:
                          float bce_pos_weight = 1.0f, float smooth = 1.0f);
     // Scalar loss tensor [1] on the host, with a backward node to logits.
     TensorPtr forward(const TensorPtr& logits, const TensorPtr& targets);
+    // The same with nothing read back (capture-safe): the loss sums go to
+    // `sums` (device, 4 doubles; workspace from the current arena), the
+    // returned scalar holds 0, and its backward reads the sums on the
+    // device.  soar_dice_bce_loss_from_sums finishes them into the values
+    // forward() returns.
+    TensorPtr forward_device(const TensorPtr& logits, const TensorPtr& targets, double* sums);
+    [[nodiscard]] float weight() const noexcept { return weight_; }
+    [[nodiscard]] float dice_weight() const noexcept { return dice_weight_; }
+    [[nodiscard]] float bce_weight() const noexcept { return bce_weight_; }
+    [[nodiscard]] float smooth() const noexcept { return smooth_; }
 
     [[nodiscard]] float last_bce() const noexcept { return last_bce_; }
     [[nodiscard]] float last_dice() const noexcept { return last_dice_; }
@@ -52,6 +62,11 @@ public:
                      float dice_smooth = 1.0f, float cldice_weight = 0.0f);
     TensorPtr forward(const TensorPtr& logits, const TensorPtr& targets, float& out_bce,
                       float& out_dice);
+    // Capture-safe form of forward (DiceBCELoss::forward_device).
+    TensorPtr forward_device(const TensorPtr& logits, const TensorPtr& targets, double* sums) {
+        return region_.forward_device(logits, targets, sums);
+    }
+    [[nodiscard]] const DiceBCELoss& region() const noexcept { return region_; }
     [[nodiscard]] float bce_weight() const noexcept { return bce_weight_; }
     [[nodiscard]] float dice_weight() const noexcept { return dice_weight_; }
     [[nodiscard]] float pos_weight() const noexcept { return pos_weight_; }
@@ -87,10 +102,23 @@ public:
     // (adamw.cpp:28-57).  Returns the norm before clipping.
     float clip_grad_norm(float max_norm);
     void step();
+    // Capture-safe forms: nothing is read back and nothing step-dependent is
+    // baked into a launch.  clip_grad_norm_device leaves the squared norm in
+    // norm_sq() (device) and takes the clip decision on the device.
+    // next_scalars advances the step count and writes the step's lr, step
+    // size and sqrt of bias correction 2 (as step() computes them) to
+    // out[3]; step_device runs the update with those three read from the
+    // device array `scalars` when the kernel executes.
+    void clip_grad_norm_device(float max_norm);
+    void next_scalars(float out[3]);
+    void step_device(const float* scalars);
+    [[nodiscard]] const double* norm_sq() const noexcept { return norm_; }
     [[nodiscard]] float get_lr() const noexcept { return options_.lr; }
     void set_lr(float lr) noexcept { options_.lr = lr; }
     [[nodiscard]] const AdamWOptions& options() const noexcept { return options_; }
     [[nodiscard]] int64_t step_count() const noexcept { return step_count_; }
+    // (to undo next_scalars of a step that was captured but never ran)
+    void set_step_count(int64_t n) noexcept { step_count_ = n; }
     [[nodiscard]] const std::vector<TensorPtr>& params() const noexcept { return params_; }
 
 private:
@@ -135,6 +163,18 @@ public:
                            bool is_accumulating = false);
     // Forward, loss and backward only (gradients accumulate; no step).
     StepMetrics forward_backward(const TensorPtr& image, const TensorPtr& mask, float scale);
+    // One step of one [C,H,W] sample with every scalar kept on the device,
+    // so the whole step can be captured into a graph and replayed: forward,
+    // loss sums to loss_sums (device, 4 doubles), backward, the clip
+    // decided on the device, the AdamW scalars written to pinned_scalars
+    // (host, pinned) and copied from there to dev_scalars (device) on the
+    // stream, the update, zero_grad.  Same arithmetic as train_step.  Read
+    // loss_sums and optimizer().norm_sq() back afterwards and pass them to
+    // device_step_metrics.
+    void train_step_device(const TensorPtr& image, const TensorPtr& mask, double* loss_sums,
+                           float* pinned_scalars, float* dev_scalars);
+    [[nodiscard]] StepMetrics device_step_metrics(const double loss_sums[4], double norm_sq,
+                                                  size_t numel) const;
 
     [[nodiscard]] optim::AdamW& optimizer() noexcept { return *optimizer_; }
     [[nodiscard]] losses::CompositeLoss& loss_fn() noexcept { return loss_fn_; }

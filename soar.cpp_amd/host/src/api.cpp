@@ -3,16 +3,23 @@
 // state; per-call activations).  Mirrors src/api/c_api.cpp:11-154 of the
 // reference: exceptions become -1 / NULL; the message is kept for
 // soar_api_last_error().
+#include <hip/hip_runtime_api.h>
+
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <string>
+#include <tuple>
 
 #include "soar/autograd.hpp"
 #include "soar/engine.hpp"
+#include "soar/kernels.hpp"
 #include "soar/memory.hpp"
 #include "soar/model.hpp"
 #include "soar_api.h"
+#include "soar_gn.h"
 
 namespace {
 
@@ -27,6 +34,20 @@ constexpr size_t kMinActivationBytes = size_t(64) << 20;
 
 size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
 
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        throw soar::DeviceError(std::string(what) + ": " + hipGetErrorString(e));
+    }
+}
+
+// A training step captured into a graph for one image shape; valid while
+// the activation arena it allocated from keeps its base address.
+struct StepGraph {
+    hipGraphExec_t exec = nullptr;
+    void* acts_base = nullptr;
+};
+
 struct SoarModelHandle {
     std::unique_ptr<DeviceArena> params;
     std::unique_ptr<DeviceArena> acts;
@@ -35,6 +56,26 @@ struct SoarModelHandle {
     std::unique_ptr<soar::engine::Trainer> trainer;
     soar::engine::StepMetrics last;
     std::vector<std::pair<std::string, TensorPtr>> named;
+    // ---- soar_train_step on the device, captured and replayed -----------
+    hipStream_t stream = nullptr;
+    bool graph_mode = true;
+    double* dev_sums = nullptr;     // loss sums (device, params arena)
+    float* dev_scalars = nullptr;   // AdamW lr, step size, sqrt(bc2) (device)
+    float* pin_scalars = nullptr;   // the same, pinned host staging
+    double* pin_out = nullptr;      // read-back: 4 loss sums + the squared norm
+    float* pin_img = nullptr;       // pinned staging of the image and mask
+    float* pin_msk = nullptr;
+    size_t pin_elems = 0;           // capacity of each, floats
+    std::map<std::tuple<int, int, int>, StepGraph> graphs;
+    std::map<std::tuple<int, int, int>, int> seen;  // eager steps run per shape
+
+    ~SoarModelHandle() {
+        for (auto& [k, g] : graphs)
+            if (g.exec) (void)hipGraphExecDestroy(g.exec);
+        for (void* p : {(void*)pin_scalars, (void*)pin_out, (void*)pin_img, (void*)pin_msk})
+            if (p) (void)hipHostFree(p);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
 };
 
 SoarModelHandle* H(void* h) { return static_cast<SoarModelHandle*>(h); }
@@ -47,8 +88,17 @@ size_t activation_estimate(int64_t h, int64_t w) {
     return std::max(kMinActivationBytes, align_up(px * 2048));
 }
 
+void drop_graphs(SoarModelHandle* s) {
+    for (auto& [k, g] : s->graphs)
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    s->graphs.clear();
+}
+
 void ensure_acts(SoarModelHandle* s, size_t need) {
     if (s->acts && s->acts->slab().total_capacity() >= need) return;
+    // the graphs point into the arena being replaced (the stream is idle
+    // at every C-ABI entry: each call ends with a synchronisation)
+    drop_graphs(s);
     s->acts.reset();
     s->acts = std::make_unique<DeviceArena>(need, kAlign);
 }
@@ -131,7 +181,17 @@ void* create(int in_channels, int num_classes, int variant, bool seeded, uint64_
             auto opt = std::make_unique<soar::optim::AdamW>(h->model->parameters(), opts);
             h->trainer = std::make_unique<soar::engine::Trainer>(
                 h->model, soar::losses::CompositeLoss(0.5f, 0.5f), std::move(opt));
+            h->dev_sums = static_cast<double*>(
+                h->params->allocate(4 * sizeof(double), {}, "loss_sums"));
+            h->dev_scalars = static_cast<float*>(
+                h->params->allocate(4 * sizeof(float), {}, "adamw_scalars"));
         }
+        hip_check(hipStreamCreate(&h->stream), "hipStreamCreate");
+        hip_check(hipHostMalloc(reinterpret_cast<void**>(&h->pin_scalars), 4 * sizeof(float)),
+                  "hipHostMalloc");
+        hip_check(hipHostMalloc(reinterpret_cast<void**>(&h->pin_out), 8 * sizeof(double)),
+                  "hipHostMalloc");
+        if (const char* g = std::getenv("SOAR_TRAIN_GRAPH")) h->graph_mode = std::atoi(g) != 0;
         g_api_err.clear();
         return h.release();
     } catch (const std::exception& e) {
@@ -145,6 +205,101 @@ void* create(int in_channels, int num_classes, int variant, bool seeded, uint64_
 
 TensorPtr host_image(const float* data, int64_t c, int64_t h, int64_t w) {
     return soar::Tensor::from_blob(data, {c, h, w}, false, true);
+}
+
+// Pinned staging for the image and mask of a step.
+void ensure_pinned(SoarModelHandle* s, size_t elems) {
+    if (s->pin_elems >= elems) return;
+    drop_graphs(s);  // their uploads read the old staging
+    for (float** p : {&s->pin_img, &s->pin_msk}) {
+        if (*p) hip_check(hipHostFree(*p), "hipHostFree");
+        *p = nullptr;
+    }
+    s->pin_elems = 0;
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&s->pin_img), elems * sizeof(float)),
+              "hipHostMalloc");
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&s->pin_msk), elems * sizeof(float)),
+              "hipHostMalloc");
+    s->pin_elems = elems;
+}
+
+// The device work of one training step from the pinned staging, on the
+// handle's stream (recorded into a graph while that stream is capturing).
+void device_step(SoarModelHandle* s, int64_t c, int64_t h, int64_t w) {
+    TensorPtr img = soar::Tensor::create({c, h, w}, false, true);
+    TensorPtr msk = soar::Tensor::create({1, h, w}, false, true);
+    soar::hip::kernels::check(soar_memcpy_async(img->cuda_data(), s->pin_img,
+                                                (size_t)(c * h * w) * sizeof(float), 0,
+                                                s->stream),
+                              "image upload");
+    soar::hip::kernels::check(soar_memcpy_async(msk->cuda_data(), s->pin_msk,
+                                                (size_t)(h * w) * sizeof(float), 0, s->stream),
+                              "mask upload");
+    s->trainer->train_step_device(img, msk, s->dev_sums, s->pin_scalars, s->dev_scalars);
+}
+
+// Runs one step: a graph replay when one is held for this shape, else the
+// step itself, captured (and then launched) from the second step of a
+// shape on.  A capture that fails is undone and the step runs uncaptured;
+// graphs stay off for the handle from then on.
+void run_train_step(SoarModelHandle* s, int c, int h, int w) {
+    const auto key = std::make_tuple(c, h, w);
+    auto it = s->graphs.find(key);
+    if (s->graph_mode && it != s->graphs.end() && s->acts &&
+        it->second.acts_base == s->acts->base()) {
+        s->trainer->optimizer().next_scalars(s->pin_scalars);
+        hip_check(hipGraphLaunch(it->second.exec, s->stream), "hipGraphLaunch");
+        return;
+    }
+    const bool capture = s->graph_mode && s->seen[key] > 0;
+    with_acts(
+        s, h, w,
+        [&] {
+            if (!capture) {
+                device_step(s, c, h, w);
+                return;
+            }
+            const int64_t step0 = s->trainer->optimizer().step_count();
+            hip_check(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal),
+                      "hipStreamBeginCapture");
+            hipGraph_t graph = nullptr;
+            try {
+                device_step(s, c, h, w);
+            } catch (const soar::OutOfMemory&) {
+                (void)hipStreamEndCapture(s->stream, &graph);
+                if (graph) (void)hipGraphDestroy(graph);
+                s->trainer->optimizer().set_step_count(step0);
+                throw;  // with_acts grows the arena and runs again
+            } catch (...) {
+                (void)hipStreamEndCapture(s->stream, &graph);
+                if (graph) (void)hipGraphDestroy(graph);
+                (void)hipGetLastError();
+                s->trainer->optimizer().set_step_count(step0);
+                s->graph_mode = false;
+                s->acts->reset_dynamic_allocations();
+                device_step(s, c, h, w);
+                return;
+            }
+            hipGraphExec_t exec = nullptr;
+            hipError_t e = hipStreamEndCapture(s->stream, &graph);
+            if (e == hipSuccess) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            if (graph) (void)hipGraphDestroy(graph);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                s->trainer->optimizer().set_step_count(step0);
+                s->graph_mode = false;
+                s->acts->reset_dynamic_allocations();
+                device_step(s, c, h, w);
+                return;
+            }
+            hip_check(hipGraphLaunch(exec, s->stream), "hipGraphLaunch");
+            StepGraph& g = s->graphs[key];
+            if (g.exec) (void)hipGraphExecDestroy(g.exec);
+            g.exec = exec;
+            g.acts_base = s->acts->base();
+        },
+        [&] { s->trainer->optimizer().zero_grad(); });
+    s->seen[key] += 1;
 }
 
 }  // namespace
@@ -194,14 +349,23 @@ SOAR_API int soar_train_step(void* handle, const float* image_data, const float*
     return guarded([&] {
         check_image(channels, height, width);
         s->trainer->optimizer().set_lr(learning_rate);
-        with_acts(
-            s, height, width,
-            [&] {
-                TensorPtr img = host_image(image_data, channels, height, width);
-                TensorPtr msk = host_image(mask_data, 1, height, width);
-                s->last = s->trainer->train_step(img, msk);
-            },
-            [&] { s->trainer->optimizer().zero_grad(); });
+        const size_t px = (size_t)height * (size_t)width;
+        ensure_pinned(s, (size_t)channels * px);
+        std::memcpy(s->pin_img, image_data, (size_t)channels * px * sizeof(float));
+        std::memcpy(s->pin_msk, mask_data, px * sizeof(float));
+        {
+            soar::exec::StreamScope scope(s->stream);
+            run_train_step(s, channels, height, width);
+        }
+        soar::hip::kernels::check(
+            soar_memcpy_async(s->pin_out, s->dev_sums, 4 * sizeof(double), 1, s->stream),
+            "loss read-back");
+        soar::hip::kernels::check(
+            soar_memcpy_async(s->pin_out + 4, s->trainer->optimizer().norm_sq(),
+                              sizeof(double), 1, s->stream),
+            "norm read-back");
+        hip_check(hipStreamSynchronize(s->stream), "hipStreamSynchronize");
+        s->last = s->trainer->device_step_metrics(s->pin_out, s->pin_out[4], px);
         if (out_loss) *out_loss = s->last.loss;
         if (out_dice) *out_dice = s->last.dice_score;
         if (out_iou) *out_iou = s->last.iou_score;
@@ -296,6 +460,23 @@ SOAR_API int soar_model_forward_backward(void* handle, const float* image_data,
             [&] { s->trainer->optimizer().zero_grad(); });
         metrics_out(m, out_metrics);
     });
+}
+
+SOAR_API int soar_model_set_graph_mode(void* handle, int on) {
+    if (!handle) return -1;
+    auto* s = H(handle);
+    return guarded([&] {
+        s->graph_mode = on != 0;
+        if (!on) drop_graphs(s);
+    });
+}
+
+SOAR_API int soar_model_graph_info(void* handle, int* graph_mode, int* graphs_held) {
+    if (!handle) return -1;
+    auto* s = H(handle);
+    if (graph_mode) *graph_mode = s->graph_mode ? 1 : 0;
+    if (graphs_held) *graphs_held = (int)s->graphs.size();
+    return 0;
 }
 
 SOAR_API int soar_model_zero_grad(void* handle) {

@@ -20,4 +20,13 @@ std::string to_string(const Shape& s) {
     return r + "]";
 }
 
+namespace exec {
+namespace {
+thread_local void* g_stream = nullptr;
+}
+void* stream() noexcept { return g_stream; }
+StreamScope::StreamScope(void* s) noexcept : prev_(g_stream) { g_stream = s; }
+StreamScope::~StreamScope() { g_stream = prev_; }
+}  // namespace exec
+
 }  // namespace soar

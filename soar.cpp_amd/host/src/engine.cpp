@@ -29,6 +29,7 @@ struct DiceBCENode : autograd::AutogradNode {
     TensorPtr logits, targets;
     float w = 1, bw = 1, dw = 1, pos_weight = 1, smooth = 1;
     float inter = 0, sum_p = 0, sum_y = 0;
+    const double* sums = nullptr;  // device loss sums (forward_device), else null
 
     std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
         if (logits && logits->grad_fn()) return {logits->grad_fn()};
@@ -39,11 +40,19 @@ struct DiceBCENode : autograd::AutogradNode {
         const float go = grad_output->to_host()[0];
         bool fresh = false;
         TensorPtr gz = write_target(logits, &fresh);
-        check(soar_dice_bce_loss_backward_ex(logits->cuda_data(), targets->cuda_data(),
-                                             gz->cuda_data(), go, w, bw, dw, pos_weight, smooth,
-                                             inter, sum_p, sum_y, (size_t)logits->numel(),
-                                             fresh ? 0u : SOAR_GN_ACCUMULATE_DX, nullptr),
-              "Dice+BCE backward");
+        const unsigned fl = fresh ? 0u : SOAR_GN_ACCUMULATE_DX;
+        if (sums)
+            check(soar_dice_bce_loss_backward_device(logits->cuda_data(), targets->cuda_data(),
+                                                     gz->cuda_data(), go, w, bw, dw, pos_weight,
+                                                     smooth, sums, (size_t)logits->numel(), fl,
+                                                     exec::stream()),
+                  "Dice+BCE backward");
+        else
+            check(soar_dice_bce_loss_backward_ex(logits->cuda_data(), targets->cuda_data(),
+                                                 gz->cuda_data(), go, w, bw, dw, pos_weight,
+                                                 smooth, inter, sum_p, sum_y,
+                                                 (size_t)logits->numel(), fl, exec::stream()),
+                  "Dice+BCE backward");
         if (fresh) propagate_grad(logits, std::move(gz));
     }
     void release_variables() override { logits = targets = nullptr; }
@@ -67,7 +76,7 @@ TensorPtr DiceBCELoss::forward(const TensorPtr& logits, const TensorPtr& targets
     float out[6];
     check(soar_dice_bce_loss_forward(logits->cuda_data(), targets->cuda_data(),
                                      (size_t)logits->numel(), weight_, bce_weight_, dice_weight_,
-                                     pos_weight_, smooth_, out, nullptr),
+                                     pos_weight_, smooth_, out, exec::stream()),
           "Dice+BCE forward");
     last_bce_ = out[1];
     last_dice_ = out[2];
@@ -89,6 +98,38 @@ TensorPtr DiceBCELoss::forward(const TensorPtr& logits, const TensorPtr& targets
         node->inter = inter_;
         node->sum_p = sum_p_;
         node->sum_y = sum_y_;
+        total->set_grad_fn(node);
+    }
+    return total;
+}
+
+TensorPtr DiceBCELoss::forward_device(const TensorPtr& logits, const TensorPtr& targets,
+                                      double* sums) {
+    if (logits->numel() != targets->numel())
+        throw ShapeError("DiceBCELoss: shape mismatch between logits and targets");
+    if (!logits->is_cuda() || !targets->is_cuda())
+        throw InvalidArgument("DiceBCELoss::forward_device needs device tensors");
+    auto* arena = memory::DeviceArena::current();
+    if (!arena) throw DeviceError("DiceBCELoss::forward_device needs a DeviceArena");
+    const size_t n = (size_t)logits->numel();
+    const size_t wsb = soar_dice_bce_loss_workspace_bytes(n);
+    void* ws = wsb ? arena->allocate(wsb, {}, "loss_ws") : nullptr;
+    check(soar_dice_bce_loss_sums_device(logits->cuda_data(), targets->cuda_data(), n,
+                                         pos_weight_, sums, ws, wsb, exec::stream()),
+          "Dice+BCE sums");
+    const bool record = logits->requires_grad() && autograd::GradMode::is_enabled();
+    TensorPtr total = Tensor::create({1}, record);
+    total->data()[0] = 0.0f;
+    if (record) {
+        auto node = std::make_shared<DiceBCENode>();
+        node->logits = logits;
+        node->targets = targets;
+        node->w = weight_;
+        node->bw = bce_weight_;
+        node->dw = dice_weight_;
+        node->pos_weight = pos_weight_;
+        node->smooth = smooth_;
+        node->sums = sums;
         total->set_grad_fn(node);
     }
     return total;
@@ -144,7 +185,7 @@ AdamW::AdamW(std::vector<TensorPtr> params, AdamWOptions options)
         host[3 * n + i] = v_[i]->cuda_data();
         std::memcpy(&host[4 * n + i], &numel[i], sizeof(int64_t));
     }
-    check(soar_memcpy_h2d(table_, host.data(), host.size() * sizeof(void*), nullptr),
+    check(soar_memcpy_h2d(table_, host.data(), host.size() * sizeof(void*), exec::stream()),
           "AdamW table");
     grad_ptrs_.assign(n, nullptr);
     sync_tables();
@@ -165,7 +206,7 @@ void AdamW::sync_tables() {
     }
     if (changed)
         check(soar_memcpy_h2d(static_cast<char*>(table_) + n * sizeof(void*), grad_ptrs_.data(),
-                              n * sizeof(void*), nullptr),
+                              n * sizeof(void*), exec::stream()),
               "AdamW gradient table");
 }
 
@@ -179,7 +220,7 @@ void AdamW::zero_grad() {
     const size_t nb = (size_t)n * sizeof(void*);
     check(soar_multi_tensor_fill_device(reinterpret_cast<float* const*>(t + nb),
                                         reinterpret_cast<const int64_t*>(t + 4 * nb), n, 0.0f,
-                                        nullptr),
+                                        exec::stream()),
           "zero_grad");
 }
 
@@ -191,19 +232,61 @@ float AdamW::clip_grad_norm(float max_norm) {
     const size_t nb = (size_t)n * sizeof(void*);
     check(soar_multi_tensor_norm_sq_device(reinterpret_cast<const float* const*>(t + nb),
                                            reinterpret_cast<const int64_t*>(t + 4 * nb), n, norm_,
-                                           norm_ws_, norm_ws_bytes_, nullptr),
+                                           norm_ws_, norm_ws_bytes_, exec::stream()),
           "gradient norm");
     double sq = 0.0;
-    check(soar_memcpy_d2h(&sq, norm_, sizeof sq, nullptr), "gradient norm read-back");
+    check(soar_memcpy_d2h(&sq, norm_, sizeof sq, exec::stream()), "gradient norm read-back");
     const float total_norm = static_cast<float>(std::sqrt(sq));
     if (total_norm > max_norm && total_norm > 1e-6f) {
         const float clip_coef = max_norm / total_norm;
         check(soar_multi_tensor_scale_device(reinterpret_cast<float* const*>(t + nb),
                                              reinterpret_cast<const int64_t*>(t + 4 * nb), n,
-                                             clip_coef, nullptr),
+                                             clip_coef, exec::stream()),
               "gradient clip");
     }
     return total_norm;
+}
+
+void AdamW::clip_grad_norm_device(float max_norm) {
+    const int n = (int)params_.size();
+    if (n == 0) return;
+    sync_tables();
+    auto* t = static_cast<char*>(table_);
+    const size_t nb = (size_t)n * sizeof(void*);
+    check(soar_multi_tensor_norm_sq_device(reinterpret_cast<const float* const*>(t + nb),
+                                           reinterpret_cast<const int64_t*>(t + 4 * nb), n, norm_,
+                                           norm_ws_, norm_ws_bytes_, exec::stream()),
+          "gradient norm");
+    check(soar_multi_tensor_clip_device(reinterpret_cast<float* const*>(t + nb),
+                                        reinterpret_cast<const int64_t*>(t + 4 * nb), n, norm_,
+                                        max_norm, exec::stream()),
+          "gradient clip");
+}
+
+void AdamW::next_scalars(float out[3]) {
+    step_count_++;
+    // adamw.cpp:67-70, in fp32, as step()
+    const float beta1 = options_.beta1, beta2 = options_.beta2;
+    const float bias_correction1 = 1.0f - std::pow(beta1, static_cast<float>(step_count_));
+    const float bias_correction2 = 1.0f - std::pow(beta2, static_cast<float>(step_count_));
+    out[0] = options_.lr;
+    out[1] = options_.lr / bias_correction1;
+    out[2] = std::sqrt(bias_correction2);
+}
+
+void AdamW::step_device(const float* scalars) {
+    const int n = (int)params_.size();
+    if (n == 0) return;
+    sync_tables();
+    auto* t = static_cast<char*>(table_);
+    const size_t nb = (size_t)n * sizeof(void*);
+    check(soar_adamw_multi_tensor_device_scalars(
+              reinterpret_cast<float* const*>(t), reinterpret_cast<const float* const*>(t + nb),
+              reinterpret_cast<float* const*>(t + 2 * nb),
+              reinterpret_cast<float* const*>(t + 3 * nb),
+              reinterpret_cast<const int64_t*>(t + 4 * nb), n, scalars, options_.beta1,
+              options_.beta2, options_.eps, options_.weight_decay, exec::stream()),
+          "AdamW step");
 }
 
 void AdamW::step() {
@@ -224,7 +307,7 @@ void AdamW::step() {
               reinterpret_cast<float* const*>(t + 2 * nb),
               reinterpret_cast<float* const*>(t + 3 * nb),
               reinterpret_cast<const int64_t*>(t + 4 * nb), n, lr, beta1, beta2, options_.eps,
-              options_.weight_decay, step_size, sqrt_bc2, nullptr),
+              options_.weight_decay, step_size, sqrt_bc2, exec::stream()),
           "AdamW step");
 }
 
@@ -272,7 +355,7 @@ TensorPtr sample(const TensorPtr& t, int64_t b) {
     const int64_t C = t->dim(1), H = t->dim(2), W = t->dim(3);
     TensorPtr s = Tensor::create({C, H, W}, false, true);
     check(soar_memcpy_d2d(s->cuda_data(), t->cuda_data() + b * C * H * W,
-                          (size_t)(C * H * W) * sizeof(float), nullptr),
+                          (size_t)(C * H * W) * sizeof(float), exec::stream()),
           "sample slice");
     return s;
 }
@@ -313,6 +396,47 @@ StepMetrics Trainer::train_step(const TensorPtr& images, const TensorPtr& masks,
         optimizer_->step();
         optimizer_->zero_grad();
     }
+    m.lr = optimizer_->get_lr();
+    return m;
+}
+
+void Trainer::train_step_device(const TensorPtr& image, const TensorPtr& mask,
+                                double* loss_sums, float* pinned_scalars, float* dev_scalars) {
+    model_->train(true);
+    if (!image->is_cuda() || !mask->is_cuda())
+        throw InvalidArgument("Trainer::train_step_device needs device tensors");
+    image->set_requires_grad(false);
+    TensorPtr logits = model_->forward(image);
+    TensorPtr loss = loss_fn_.forward_device(logits, mask, loss_sums);
+    TensorPtr grad_out = Tensor::create({1});
+    grad_out->data()[0] = 1.0f / (float)accumulate_;
+    loss->backward(grad_out);
+    logits->set_grad_fn(nullptr);
+    loss->set_grad_fn(nullptr);
+    optimizer_->clip_grad_norm_device(grad_clip_);
+    optimizer_->next_scalars(pinned_scalars);
+    check(soar_memcpy_async(dev_scalars, pinned_scalars, 3 * sizeof(float), 0, exec::stream()),
+          "AdamW scalars");
+    optimizer_->step_device(dev_scalars);
+    optimizer_->zero_grad();
+}
+
+StepMetrics Trainer::device_step_metrics(const double loss_sums[4], double norm_sq,
+                                         size_t numel) const {
+    const losses::DiceBCELoss& r = loss_fn_.region();
+    float out[6];
+    check(soar_dice_bce_loss_from_sums(loss_sums, numel, r.weight(), r.bce_weight(),
+                                       r.dice_weight(), r.smooth(), out),
+          "Dice+BCE finish");
+    StepMetrics m;
+    m.loss = out[0];
+    m.bce_loss = out[1];
+    m.dice_loss = out[2];
+    // device-path metrics (trainer.cpp:80-86), as forward_backward
+    const float d = std::max(0.0f, std::min(1.0f, 1.0f - out[2]));
+    m.dice_score = d;
+    m.iou_score = d / (2.0f - d + 1e-7f);
+    m.grad_norm = static_cast<float>(std::sqrt(norm_sq));
     m.lr = optimizer_->get_lr();
     return m;
 }
@@ -361,14 +485,14 @@ PredictionResult Predictor::predict(const TensorPtr& image) {
     if (!arena) throw DeviceError("Predictor needs a DeviceArena");
     auto* mask_dev = static_cast<uint8_t*>(arena->allocate((size_t)n, {}, "mask"));
     check(soar_sigmoid_threshold(logits->cuda_data(), probs->cuda_data(), mask_dev, (size_t)n,
-                                 threshold_, nullptr),
+                                 threshold_, exec::stream()),
           "sigmoid threshold");
     PredictionResult r;
     r.height = (size_t)H;
     r.width = (size_t)W;
     r.probabilities = probs->to_host();
     r.binary_mask.resize((size_t)n);
-    check(soar_memcpy_d2h(r.binary_mask.data(), mask_dev, (size_t)n, nullptr), "mask read-back");
+    check(soar_memcpy_d2h(r.binary_mask.data(), mask_dev, (size_t)n, exec::stream()), "mask read-back");
     for (uint8_t v : r.binary_mask) r.foreground_pixels += v;
     r.rle_string = encode_rle(r.binary_mask.data(), r.height, r.width);
     return r;

@@ -70,7 +70,7 @@ struct SigmoidNode : autograd::AutogradNode {
         bool fresh = false;
         TensorPtr gx = write_target(input, &fresh);
         check(soar_sigmoid_backward_ex(go->cuda_data(), output->cuda_data(), gx->cuda_data(),
-                                       (size_t)input->numel(), mode(fresh), nullptr),
+                                       (size_t)input->numel(), mode(fresh), exec::stream()),
               "sigmoid backward");
         if (fresh) propagate_grad(input, std::move(gx));
     }
@@ -92,7 +92,7 @@ struct PixelShuffleNode : autograd::AutogradNode {
         TensorPtr gx = write_target(input, &fresh);
         check(soar_pixel_shuffle_backward_ex(go->cuda_data(), gx->cuda_data(), (size_t)p.rows,
                                              (size_t)p.H, (size_t)p.W, (size_t)r, mode(fresh),
-                                             nullptr),
+                                             exec::stream()),
               "pixel shuffle backward");
         if (fresh) propagate_grad(input, std::move(gx));
     }
@@ -115,7 +115,7 @@ struct UpsampleNode : autograd::AutogradNode {
         check(soar_upsample_bilinear_backward_ex(go->cuda_data(), gx->cuda_data(),
                                                  (size_t)p.rows, (size_t)p.H, (size_t)p.W,
                                                  (size_t)H_out, (size_t)W_out, mode(fresh),
-                                                 nullptr),
+                                                 exec::stream()),
               "upsample backward");
         if (fresh) propagate_grad(input, std::move(gx));
     }
@@ -136,7 +136,7 @@ struct AvgPoolNode : autograd::AutogradNode {
         TensorPtr gx = write_target(input, &fresh);
         check(soar_global_avg_pool_backward_ex(go->cuda_data(), gx->cuda_data(),
                                                (size_t)p.rows, (size_t)(p.H * p.W), mode(fresh),
-                                               nullptr),
+                                               exec::stream()),
               "average pool backward");
         if (fresh) propagate_grad(input, std::move(gx));
     }
@@ -163,7 +163,7 @@ struct MulBroadcastNode : autograd::AutogradNode {
         check(soar_mul_broadcast_backward_ex(go->cuda_data(), a->cuda_data(), b->cuda_data(),
                                              ga ? ga->cuda_data() : nullptr,
                                              gb ? gb->cuda_data() : nullptr, (size_t)p.rows,
-                                             (size_t)(p.H * p.W), fl, nullptr),
+                                             (size_t)(p.H * p.W), fl, exec::stream()),
               "mul_broadcast backward");
         if (ga && fa) propagate_grad(a, std::move(ga));
         if (gb && fb) propagate_grad(b, std::move(gb));
@@ -191,7 +191,7 @@ struct ConvexNode : autograd::AutogradNode {
         check(soar_convex_combination_backward_ex(
                   go->cuda_data(), g->cuda_data(), a->cuda_data(), b->cuda_data(),
                   gg ? gg->cuda_data() : nullptr, ga ? ga->cuda_data() : nullptr,
-                  gb ? gb->cuda_data() : nullptr, (size_t)a->numel(), fl, nullptr),
+                  gb ? gb->cuda_data() : nullptr, (size_t)a->numel(), fl, exec::stream()),
               "convex combination backward");
         // the reference's order (blocks.cpp:258-262): a, b, then g
         if (ga && fa) propagate_grad(a, std::move(ga));
@@ -232,7 +232,7 @@ struct ConcatNode : autograd::AutogradNode {
             ptr[k] = gi[k]->cuda_data();
         }
         check(soar_concat_channels_backward(go->cuda_data(), ptr.data(), ch.data(), fl.data(),
-                                            (int)K, N, HW, nullptr),
+                                            (int)K, N, HW, exec::stream()),
               "concat backward");
         for (size_t k = 0; k < K; ++k)
             if (gi[k] && fresh[k]) propagate_grad(inputs[k], std::move(gi[k]));
@@ -254,7 +254,7 @@ TensorPtr Sigmoid::forward(const TensorPtr& input) {
     const bool record = recording({input});
     TensorPtr out = Tensor::create(input->shape(), record, true);
     check(soar_sigmoid_forward(input->cuda_data(), out->cuda_data(), (size_t)input->numel(),
-                               nullptr),
+                               exec::stream()),
           "sigmoid");
     if (record) {
         auto node = std::make_shared<SigmoidNode>();
@@ -280,7 +280,7 @@ TensorPtr PixelShuffle::forward(const TensorPtr& input) {
     const bool record = recording({input});
     TensorPtr out = Tensor::create(os, record, true);
     check(soar_pixel_shuffle_forward(input->cuda_data(), out->cuda_data(), (size_t)p.rows,
-                                     (size_t)p.H, (size_t)p.W, (size_t)r, nullptr),
+                                     (size_t)p.H, (size_t)p.W, (size_t)r, exec::stream()),
           "pixel shuffle");
     if (record) {
         auto node = std::make_shared<PixelShuffleNode>();
@@ -305,7 +305,7 @@ TensorPtr Upsample::forward(const TensorPtr& input) {
     TensorPtr out = Tensor::create(os, record, true);
     check(soar_upsample_bilinear_forward(input->cuda_data(), out->cuda_data(), (size_t)p.rows,
                                          (size_t)p.H, (size_t)p.W, (size_t)H_out, (size_t)W_out,
-                                         nullptr),
+                                         exec::stream()),
           "upsample");
     if (record) {
         auto node = std::make_shared<UpsampleNode>();
@@ -326,7 +326,7 @@ TensorPtr AdaptiveAvgPool2d::forward(const TensorPtr& input) {
     const bool record = recording({input});
     TensorPtr out = Tensor::create(os, record, true);
     check(soar_global_avg_pool_forward(input->cuda_data(), out->cuda_data(), (size_t)p.rows,
-                                       (size_t)(p.H * p.W), nullptr),
+                                       (size_t)(p.H * p.W), exec::stream()),
           "average pool");
     if (record) {
         auto node = std::make_shared<AvgPoolNode>();
@@ -346,7 +346,7 @@ TensorPtr mul_tensors(const TensorPtr& a, const TensorPtr& b) {
     const bool record = recording({a, b});
     TensorPtr out = Tensor::create(a->shape(), record, true);
     check(soar_mul_broadcast_forward(a->cuda_data(), b->cuda_data(), out->cuda_data(),
-                                     (size_t)p.rows, (size_t)(p.H * p.W), nullptr),
+                                     (size_t)p.rows, (size_t)(p.H * p.W), exec::stream()),
           "mul_broadcast");
     if (record) {
         auto node = std::make_shared<MulBroadcastNode>();
@@ -366,7 +366,7 @@ TensorPtr convex_combination(const TensorPtr& g, const TensorPtr& a, const Tenso
     const bool record = recording({g, a, b});
     TensorPtr out = Tensor::create(a->shape(), record, true);
     check(soar_convex_combination_forward(g->cuda_data(), a->cuda_data(), b->cuda_data(),
-                                          out->cuda_data(), (size_t)a->numel(), nullptr),
+                                          out->cuda_data(), (size_t)a->numel(), exec::stream()),
           "convex combination");
     if (record) {
         auto node = std::make_shared<ConvexNode>();
@@ -407,7 +407,7 @@ TensorPtr concat_channels(const std::vector<TensorPtr>& tensors) {
         ch.push_back(batched ? t->dim(1) : t->dim(0));
     }
     check(soar_concat_channels_forward(src.data(), ch.data(), (int)tensors.size(),
-                                       out->cuda_data(), N, H * W, nullptr),
+                                       out->cuda_data(), N, H * W, exec::stream()),
           "concat");
     if (record) {
         auto node = std::make_shared<ConcatNode>();

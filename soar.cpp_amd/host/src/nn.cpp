@@ -143,7 +143,7 @@ struct GroupNormNode : autograd::AutogradNode {
                                     gx ? gx->cuda_data() : nullptr,
                                     gw ? gw->cuda_data() : nullptr,
                                     gb ? gb->cuda_data() : nullptr, s.N, s.C, s.HW, num_groups,
-                                    flags | dx_mode(gx, fresh), workspace(wsb), wsb, nullptr),
+                                    flags | dx_mode(gx, fresh), workspace(wsb), wsb, exec::stream()),
               "GroupNorm backward");
         if (want_p && !direct) {
             propagate_grad(weight, std::move(gw));
@@ -244,14 +244,14 @@ struct Conv2dNode : autograd::AutogradNode {
                 soar_pw_conv_backward_workspace_bytes(g.N, g.C_in, g.C_out, g.H * g.W);
             check(soar_pw_conv_backward(go->cuda_data(), input->cuda_data(), weight->cuda_data(),
                                         px, pw, pb, g.N, g.C_in, g.C_out, g.H * g.W, fl,
-                                        workspace(wsb), wsb, nullptr),
+                                        workspace(wsb), wsb, exec::stream()),
                   "pointwise convolution backward");
         } else if (kind == ConvKind::General) {
             const size_t wsb = soar_conv_backward_workspace_bytes(
                 g.N, g.C_in, g.C_out, g.H, g.W, g.Ho, g.Wo, K, pad, stride, dil, groups);
             check(soar_conv_backward(go->cuda_data(), input->cuda_data(), weight->cuda_data(), px,
                                      pw, pb, g.N, g.C_in, g.C_out, g.H, g.W, g.Ho, g.Wo, K, pad,
-                                     stride, dil, groups, fl, workspace(wsb), wsb, nullptr),
+                                     stride, dil, groups, fl, workspace(wsb), wsb, exec::stream()),
                   "convolution backward");
         } else {
             const size_t wsb = soar_dw_conv_backward_workspace_bytes(g.N, g.C_in, g.H, g.W, g.Ho,
@@ -259,7 +259,7 @@ struct Conv2dNode : autograd::AutogradNode {
             check(soar_dw_conv_backward(go->cuda_data(), input->cuda_data(), weight->cuda_data(),
                                         px, pw, pb, g.N, g.C_in, g.H, g.W, g.Ho, g.Wo, K, pad,
                                         stride, dil, fl, wsb ? workspace(wsb) : nullptr, wsb,
-                                        nullptr),
+                                        exec::stream()),
                   "depthwise convolution backward");
         }
         if (gb && !db_direct) propagate_grad(bias, std::move(gb));
@@ -303,7 +303,7 @@ struct CBAPointwiseNode : autograd::AutogradNode {
                                     dz ? dz->cuda_data() : nullptr,
                                     dg ? dg->cuda_data() : nullptr,
                                     db ? db->cuda_data() : nullptr, g.N, g.C_out, HW, G, flags,
-                                    workspace(gwsb), gwsb, nullptr),
+                                    workspace(gwsb), gwsb, exec::stream()),
               "CBA GroupNorm backward");
         TensorPtr gx, gw;
         bool w_direct = false, fresh = false;
@@ -315,7 +315,7 @@ struct CBAPointwiseNode : autograd::AutogradNode {
                                         gx ? gx->cuda_data() : nullptr,
                                         gw ? gw->cuda_data() : nullptr, nullptr, g.N, g.C_in,
                                         g.C_out, HW, dx_mode(gx, fresh), workspace(wsb), wsb,
-                                        nullptr),
+                                        exec::stream()),
                   "CBA convolution backward");
         }
         if (dg && !g_direct) propagate_grad(gamma, std::move(dg));
@@ -418,7 +418,7 @@ TensorPtr GroupNorm::run(const TensorPtr& input, unsigned flags) {
     check(soar_gn_silu_forward(input->cuda_data(), dptr(weight_), dptr(bias_), out->cuda_data(),
                                mean->cuda_data(), rstd->cuda_data(),
                                lo ? lo->cuda_data() : nullptr, s.N, s.C, s.HW, G, eps_, flags,
-                               workspace(wsb), wsb, nullptr),
+                               workspace(wsb), wsb, exec::stream()),
           "GroupNorm forward");
     if (record) {
         auto node = std::make_shared<GroupNormNode>();
@@ -511,19 +511,19 @@ TensorPtr Conv2d::forward(const TensorPtr& input) {
                                         : ConvKind::General;
     if (kind == ConvKind::Pointwise) {
         check(soar_pw_conv_forward(input->cuda_data(), weight_->cuda_data(), dptr(bias_),
-                                   out->cuda_data(), g.N, g.C_in, g.C_out, g.H * g.W, nullptr),
+                                   out->cuda_data(), g.N, g.C_in, g.C_out, g.H * g.W, exec::stream()),
               "pointwise convolution");
     } else if (kind == ConvKind::General) {
         check(soar_conv_forward(input->cuda_data(), weight_->cuda_data(), dptr(bias_),
                                 out->cuda_data(), g.N, g.C_in, g.C_out, g.H, g.W, g.Ho, g.Wo,
                                 (int64_t)kernel_, (int64_t)padding_, (int64_t)stride_,
-                                (int64_t)dilation_, (int64_t)groups_, nullptr),
+                                (int64_t)dilation_, (int64_t)groups_, exec::stream()),
               "convolution");
     } else {
         check(soar_dw_conv_forward(input->cuda_data(), weight_->cuda_data(), dptr(bias_),
                                    out->cuda_data(), g.N, g.C_in, g.H, g.W, g.Ho, g.Wo,
                                    (int64_t)kernel_, (int64_t)padding_, (int64_t)stride_,
-                                   (int64_t)dilation_, nullptr),
+                                   (int64_t)dilation_, exec::stream()),
               "depthwise convolution");
     }
     if (record) {
@@ -579,7 +579,7 @@ TensorPtr CBA::forward(const TensorPtr& input) {
                                        dptr(beta), z->cuda_data(), y->cuda_data(),
                                        mean->cuda_data(), rstd->cuda_data(), lo->cuda_data(), g.N,
                                        g.C_in, g.C_out, HW, G, norm_->eps(), flags,
-                                       workspace(wsb), wsb, nullptr),
+                                       workspace(wsb), wsb, exec::stream()),
           "CBA forward");
     if (record) {
         auto node = std::make_shared<CBAPointwiseNode>();

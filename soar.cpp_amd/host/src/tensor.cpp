@@ -55,7 +55,7 @@ TensorPtr Tensor::from_blob(const float* host, const Shape& shape, bool requires
     TensorPtr t = create(shape, requires_grad, on_device);
     if (t->numel_ == 0) return t;
     if (on_device)
-        hip::kernels::check(soar_memcpy_h2d(t->dev_, host, t->bytes(), nullptr), "from_blob");
+        hip::kernels::check(soar_memcpy_h2d(t->dev_, host, t->bytes(), exec::stream()), "from_blob");
     else
         std::memcpy(t->host_.data(), host, t->bytes());
     return t;
@@ -88,7 +88,7 @@ void Tensor::to_cuda() {
     if (dev_) return;
     float* d = device_storage(numel_, shape_);
     if (numel_)
-        hip::kernels::check(soar_memcpy_h2d(d, host_.data(), bytes(), nullptr), "to_cuda");
+        hip::kernels::check(soar_memcpy_h2d(d, host_.data(), bytes(), exec::stream()), "to_cuda");
     dev_ = d;
     host_.clear();
     host_.shrink_to_fit();
@@ -98,14 +98,14 @@ std::vector<float> Tensor::to_host() const {
     if (!dev_) return host_;
     std::vector<float> out((size_t)numel_);
     if (numel_)
-        hip::kernels::check(soar_memcpy_d2h(out.data(), dev_, bytes(), nullptr), "to_host");
+        hip::kernels::check(soar_memcpy_d2h(out.data(), dev_, bytes(), exec::stream()), "to_host");
     return out;
 }
 
 void Tensor::copy_from_host(const float* src) {
     if (numel_ == 0) return;
     if (dev_)
-        hip::kernels::check(soar_memcpy_h2d(dev_, src, bytes(), nullptr), "copy_from_host");
+        hip::kernels::check(soar_memcpy_h2d(dev_, src, bytes(), exec::stream()), "copy_from_host");
     else
         std::memcpy(host_.data(), src, bytes());
 }
@@ -114,7 +114,7 @@ TensorPtr Tensor::clone() const {
     TensorPtr t = create(shape_, false, dev_ != nullptr);
     if (numel_ == 0) return t;
     if (dev_)
-        hip::kernels::check(soar_memcpy_d2d(t->dev_, dev_, bytes(), nullptr), "clone");
+        hip::kernels::check(soar_memcpy_d2d(t->dev_, dev_, bytes(), exec::stream()), "clone");
     else
         t->host_ = host_;
     return t;

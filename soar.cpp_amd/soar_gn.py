@@ -118,6 +118,7 @@ SIGNATURES = {
     "soar_memcpy_h2d": (_c.c_int, [_P, _P, _SZ, _P]),
     "soar_memcpy_d2h": (_c.c_int, [_P, _P, _SZ, _P]),
     "soar_memcpy_d2d": (_c.c_int, [_P, _P, _SZ, _P]),
+    "soar_memcpy_async": (_c.c_int, [_P, _P, _SZ, _c.c_int, _P]),
     "soar_prof_enable": (_c.c_int, [_c.c_int]),
     "soar_prof_summary": (_c.c_int, [_c.c_char_p, _SZ]),
     "soar_gn_tune": (_c.c_int, [_c.c_int, _I64]),
@@ -168,6 +169,14 @@ SIGNATURES = {
     "soar_multi_tensor_norm_sq_device": (_c.c_int, [_P, _P, _c.c_int, _P, _P, _SZ, _P]),
     "soar_multi_tensor_scale_device": (_c.c_int, [_P, _P, _c.c_int, _c.c_float, _P]),
     "soar_multi_tensor_fill_device": (_c.c_int, [_P, _P, _c.c_int, _c.c_float, _P]),
+    "soar_adamw_multi_tensor_device_scalars": (_c.c_int, [_P, _P, _P, _P, _P, _c.c_int, _P] +
+                                               [_c.c_float] * 4 + [_P]),
+    "soar_multi_tensor_clip_device": (_c.c_int, [_P, _P, _c.c_int, _P, _c.c_float, _P]),
+    "soar_dice_bce_loss_workspace_bytes": (_SZ, [_SZ]),
+    "soar_dice_bce_loss_sums_device": (_c.c_int, [_P, _P, _SZ, _c.c_float, _P, _P, _SZ, _P]),
+    "soar_dice_bce_loss_from_sums": (_c.c_int, [_P, _SZ] + [_c.c_float] * 4 + [_P]),
+    "soar_dice_bce_loss_backward_device": (_c.c_int, [_P, _P, _P] + [_c.c_float] * 6 +
+                                           [_P, _SZ, _c.c_uint, _P]),
     "soar_concat_channels_forward": (_c.c_int, [_P, _P, _c.c_int, _P, _I64, _I64, _P]),
     "soar_concat_channels_backward": (_c.c_int, [_P, _P, _P, _P, _c.c_int, _I64, _I64, _P]),
     "soar_sigmoid_backward_ex": (_c.c_int, [_P, _P, _P, _SZ, _c.c_uint, _P]),

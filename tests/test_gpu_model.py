@@ -241,6 +241,40 @@ def test_two_train_steps_match_adamw(sm, wfile):
     assert abs(met["dice"] - d) < 1e-6 and abs(met["iou"] - d / (2 - d + 1e-7)) < 1e-6
 
 
+def test_train_step_graph_replay_matches_eager(sm, wfile):
+    """soar_train_step replayed from its HIP graph gives the same bits as
+    the uncaptured step: over repeated steps of one shape (eager, captured,
+    replayed), a second shape, a return to the first, with inference calls
+    that reuse the activation memory in between, and a learning-rate change
+    (the graph reads AdamW's scalars from device memory)."""
+    print("case: train_step graph vs eager", flush=True)
+    mg = model_with(sm, wfile)
+    me = model_with(sm, wfile)
+    me.set_graph_mode(False)
+    assert mg.graph_info() == (True, 0) and me.graph_info() == (False, 0)
+    plan = [((64, 64), 1e-3)] * 4 + [((48, 80), 7e-4)] * 3 + [((64, 64), 5e-4)] * 2
+    for k, ((h, w), lr) in enumerate(plan):
+        img, mask = sample(100 + k, h, w)
+        og = mg.train_step(img, mask, lr=lr)
+        oe = me.train_step(img, mask, lr=lr)
+        assert og == oe, (k, og, oe)
+        np.testing.assert_array_equal(mg.last_metrics()["grad_norm"],
+                                      me.last_metrics()["grad_norm"])
+        if k in (2, 5):
+            probe, _ = sample(200 + k, 32, 40)
+            np.testing.assert_array_equal(mg.forward(probe), me.forward(probe))
+    sg, se = mg.state(), me.state()
+    for n in sg:
+        np.testing.assert_array_equal(sg[n], se[n], err_msg=n)
+    mode, held = mg.graph_info()
+    assert mode and held >= 1, (mode, held)
+    assert me.graph_info() == (False, 0)
+    # gradients are zero after a replayed step
+    assert all(not np.any(mg.read(i, grad=True)) for i in (0, len(sg) // 2))
+    mg.close()
+    me.close()
+
+
 def test_predict_matches_oracle(sm, wfile, weights):
     print("case: predict", flush=True)
     img, _ = sample(5)
