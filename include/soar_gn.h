@@ -423,6 +423,10 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
 #define SOAR_TUNE_LOADS 13     /* 128-bit loads in flight per thread in */
                                /* the GroupNorm statistics and reduction */
                                /* passes: 4 or 8; results do not change  */
+#define SOAR_TUNE_PW_WG_WAVES 14 /* pointwise weight gradient: waves per  */
+                                 /* block that add their tiles in LDS     */
+                                 /* before writing one partial: 1, 2, 4   */
+                                 /* or 8; the default is 4                */
 SOAR_API int soar_gn_tune(int key, int64_t value);
 SOAR_API int64_t soar_gn_tune_get(int key);
 

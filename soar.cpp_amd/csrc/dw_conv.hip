@@ -493,19 +493,7 @@ __global__ __launch_bounds__(1024) void k_dw_wgrad_finish(const float* __restric
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int64_t e = (int64_t)blockIdx.x * 64 + lane;
     const int64_t g0 = wv * G / 16, g1 = (wv + 1) * G / 16;
-    double sum = 0.0;
-    if (e < E) {
-        constexpr int kU = 8;
-        int64_t gg = g0;
-        for (; gg + kU <= g1; gg += kU) {
-            float v[kU];
-#pragma unroll
-            for (int u = 0; u < kU; ++u) v[u] = part[(gg + u) * E + e];
-#pragma unroll
-            for (int u = 0; u < kU; ++u) sum += (double)v[u];
-        }
-        for (; gg < g1; ++gg) sum += (double)part[gg * E + e];
-    }
+    const double sum = e < E ? segment_sum(part, E, e, g0, g1) : 0.0;
     lds[wv][lane] = sum;
     __syncthreads();
     if (wv == 0 && e < E) {

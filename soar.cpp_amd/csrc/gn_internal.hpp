@@ -74,6 +74,9 @@ struct Tuning {
                                  // convolution splits K over (1: never)
     int loads = 4;               // 128-bit loads in flight per thread in the
                                  // first passes (statistics, reduction): 4 or 8
+    int pw_wg_waves = 4;         // pointwise weight gradient: waves per block
+                                 // that add their tiles before writing one
+                                 // partial (1, 2, 4 or 8)
 };
 
 constexpr int kThreads = 256;   // first passes (stats, reduction)
@@ -191,13 +194,15 @@ struct PwBwdPlan {
     int tm = 2, tn = 2;                  // 32-row MFMA tiles per dW tile (C_out, C_in)
     int64_t tiles_co = 0, tiles_ci = 0;  // (32 tm) x (32 tn) tiles of dW
     int64_t chunk = 0, cpp = 0, G = 0;   // pixel chunks of the dW waves
+    int wpb = 1;                         // dW waves per block (1, 2, 4, 8)
+    int64_t chunk_b = 0, cpp_b = 0, Gb = 0;  // their chunks: pixels, per plane, partials
     size_t wt_bytes = 0, pw_bytes = 0, pb_bytes = 0;
     int64_t chunk_dx = 0;  // pixels per wave of dx = W^T dz
     int kz_dx = 1;         // its cross-block split-K (pw_kz_plan)
     size_t kz_bytes = 0;   // and the slices' bytes, after the partials
 };
 PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW,
-                           int64_t chunk_dx, int kz_max);
+                           int64_t chunk_dx, int kz_max, int wg_waves);
 size_t pw_bwd_workspace_bytes(const PwBwdPlan& p);
 // dx runs the SIMT kernel when pw_use_small(N, C_in, C_out, HW, small),
 // dW/db when the weight gradient has at most small/2 multiply-adds and
@@ -242,6 +247,26 @@ hipError_t launch_fill(float* p, float v, int64_t n, hipStream_t s);
 // prof_end; both are no-ops while timing is off.
 int prof_begin(hipStream_t s, const char* kernel);
 void prof_end(hipStream_t s, int token);
+
+// sum_{g0 <= g < g1} part[g * E + e] in float64, g ascending: full batches
+// of eight loads with no bounds test between them (a test per load makes
+// the compiler wait for each one), then the tail.  (Batches of 32, with the
+// tail in one batch, measured slower in the finish kernels.)
+__device__ __forceinline__ double segment_sum(const float* __restrict__ part, int64_t E,
+                                              int64_t e, int64_t g0, int64_t g1) {
+    constexpr int kU = 8;
+    double sum = 0.0;
+    int64_t gg = g0;
+    for (; gg + kU <= g1; gg += kU) {
+        float v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) v[u] = part[(gg + u) * E + e];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) sum += (double)v[u];
+    }
+    for (; gg < g1; ++gg) sum += (double)part[gg * E + e];
+    return sum;
+}
 
 }  // namespace gn
 }  // namespace soar

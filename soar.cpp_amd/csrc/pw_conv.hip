@@ -520,9 +520,18 @@ __global__ __launch_bounds__(256) void k_pw_kz_reduce(const float* __restrict__ 
 // (row stride 144 bytes: conflict-free for the reads below), and each lane
 // then reads its operand runs back (lane l = 32h + j: row j, pixels
 // 16h + 4i .. +3 for k-steps (i, q)).  The next step's global loads are in
-// flight during the current step's MFMAs.  The wave writes its fp32 partial
-// tile (and, for the ci tile 0, the partial dz row sums) to the workspace; a
-// finish kernel adds the partials in a fixed order in float64.
+// flight during the current step's MFMAs.
+// A block holds WPB waves on one pixel chunk of one sample, interleaved by
+// step: wave w takes the steps at chunk start + 32 (w + WPB s), so the
+// block's waves read adjacent 128-byte pieces of every row together (a
+// 32 WPB-pixel run per row and block step).  Each wave has its own staging
+// area and there is no barrier in the main loop.  At the end the waves
+// park their accumulators in LDS and each adds a 1/WPB share of the tile
+// over the WPB waves in wave order, so the block writes one fp32 partial
+// tile (and, for the ci tile 0, the partial dz row sums) to the workspace:
+// WPB times fewer partials than one per wave, which for deep layers are
+// more bytes than the inputs.  A finish kernel adds the block partials in a
+// fixed order in float64.
 // ======================================================================
 constexpr int kWgStep = 32;                 // pixels per step
 constexpr int kWgStride = kWgStep + 4;      // floats per LDS row (144 bytes)
@@ -530,22 +539,29 @@ constexpr int kWgStride = kWgStep + 4;      // floats per LDS row (144 bytes)
 // TM, TN: 32-row MFMA tiles of dW along C_out and C_in (2 and 2: a 64 x 64
 // tile; 1 when the matrix has at most 32 rows / columns, so a 16 x 32 dW
 // does not pay for a 64 x 64 tile's MFMAs and loads).
-template <bool FAST, int TM, int TN>
-__global__ __launch_bounds__(64, 2) void k_pw_wgrad(
+template <bool FAST, int TM, int TN, int WPB>
+__global__ __launch_bounds__(64 * WPB, 2) void k_pw_wgrad(
     const float* __restrict__ dz, const float* __restrict__ x, float* __restrict__ part_w,
     float* __restrict__ part_b, int64_t C_in, int64_t C_out, int64_t HW, int64_t chunk,
     int64_t cpp, int64_t tiles_ci) {
-    // rows 0..32TM-1: dz rows co0.., rows 64..64+32TN-1: x rows ci0..
-    __shared__ __attribute__((aligned(16))) float lds[2 * kRowTile * kWgStride];
+    constexpr int kStage = 2 * kRowTile * kWgStride;  // floats of one wave's staging
+    constexpr int kR = 16 * TM * TN;                   // accumulators per lane
+    static_assert(kR % WPB == 0 && WPB * kR * 64 <= WPB * kStage, "reduction layout");
+    // per wave: rows 0..32TM-1: dz rows co0.., rows 64..64+32TN-1: x rows ci0..
+    __shared__ __attribute__((aligned(16))) float lds_all[WPB * kStage];
+    __shared__ float lds_b[WPB > 1 ? WPB * TM * 32 : 1];
     constexpr int kSlots = 4 * (TM + TN);  // load slots in use
     auto slot_used = [](int sl) { return sl < 8 ? sl < 4 * TM : sl - 8 < 4 * TN; };
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wv = WPB > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;
+    float* __restrict__ lds = lds_all + wv * kStage;
     const int h = lane >> 5, j = lane & 31;
     const int64_t tco = (int64_t)blockIdx.x / tiles_ci;
     const int64_t tci = (int64_t)blockIdx.x - tco * tiles_ci;
-    const int64_t g = blockIdx.y;  // n * cpp + chunk index
-    const int64_t n = g / cpp, kc = g - n * cpp;
-    const int64_t px0 = kc * chunk, pend = min(px0 + chunk, HW);
+    const int64_t gb = blockIdx.y;  // n * cpp + chunk index (block partial)
+    const int64_t n = gb / cpp, kc = gb - n * cpp;
+    // this wave's first step; a wave with none loads nothing and adds zeros
+    const int64_t px0 = kc * chunk + kWgStep * wv, pend = min(kc * chunk + chunk, HW);
     const int64_t co0 = tco * 32 * TM, ci0 = tci * 32 * TN;
     const bool want_b = tci == 0;
 
@@ -621,13 +637,14 @@ __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
         }
     };
 
+    constexpr int64_t kStride = (int64_t)kWgStep * WPB;  // this wave's step stride
     f4 st[16];
     gload(px0, st);
-    for (int64_t p = px0; p < pend; p += kWgStep) {
+    for (int64_t p = px0; p < pend; p += kStride) {
         lwrite(st);
         // next step's loads (the last step reloads itself: no branch, so the
         // wait before the LDS write above only covers these)
-        const int64_t pn = p + kWgStep < pend ? p + kWgStep : p;
+        const int64_t pn = p + kStride < pend ? p + kStride : p;
         gload(pn, st);
         if (FAST) {
             __builtin_amdgcn_sched_group_barrier(0x200, kSlots, 0);  // the LDS writes
@@ -636,22 +653,66 @@ __global__ __launch_bounds__(64, 2) void k_pw_wgrad(
         compute();
     }
 
+    if constexpr (WPB == 1) {
 #pragma unroll
-    for (int mt = 0; mt < TM; ++mt)
+        for (int mt = 0; mt < TM; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < TN; ++nt)
+            for (int nt = 0; nt < TN; ++nt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t co = co0 + tile_row(mt, r, h);
-                const int64_t ci = ci0 + 32 * nt + j;
-                if (co < C_out && ci < C_in) part_w[(g * C_out + co) * C_in + ci] = acc[mt][nt][r];
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t co = co0 + tile_row(mt, r, h);
+                    const int64_t ci = ci0 + 32 * nt + j;
+                    if (co < C_out && ci < C_in)
+                        part_w[(gb * C_out + co) * C_in + ci] = acc[mt][nt][r];
+                }
+        if (want_b) {
+#pragma unroll
+            for (int mt = 0; mt < TM; ++mt) {
+                const float tot = sb[mt] + __shfl_xor(sb[mt], 32);
+                const int64_t co = co0 + 32 * mt + j;
+                if (h == 0 && co < C_out) part_b[gb * C_out + co] = tot;
             }
-    if (want_b) {
+        }
+    } else {
+        __syncthreads();  // every wave is done with its staging area
+        // accumulator k = (mt * TN + nt) * 16 + r of wave w at red[(w kR + k) 64 + lane]
+        float* __restrict__ red = lds_all;
 #pragma unroll
-        for (int mt = 0; mt < TM; ++mt) {
-            const float tot = sb[mt] + __shfl_xor(sb[mt], 32);
-            const int64_t co = co0 + 32 * mt + j;
-            if (h == 0 && co < C_out) part_b[g * C_out + co] = tot;
+        for (int mt = 0; mt < TM; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    red[(wv * kR + (mt * TN + nt) * 16 + r) * 64 + lane] = acc[mt][nt][r];
+        if (want_b) {
+#pragma unroll
+            for (int mt = 0; mt < TM; ++mt) {
+                const float tot = sb[mt] + __shfl_xor(sb[mt], 32);
+                if (h == 0) lds_b[(wv * TM + mt) * 32 + j] = tot;
+            }
+        }
+        __syncthreads();
+        constexpr int kShare = kR / WPB;
+#pragma unroll
+        for (int kk = 0; kk < kShare; ++kk) {
+            const int k = wv * kShare + kk;
+            float t = red[k * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < WPB; ++w) t += red[(w * kR + k) * 64 + lane];
+            const int mt = k / (16 * TN), nt = (k / 16) % TN, r = k % 16;
+            const int64_t co = co0 + tile_row(mt, r, h);
+            const int64_t ci = ci0 + 32 * nt + j;
+            if (co < C_out && ci < C_in) part_w[(gb * C_out + co) * C_in + ci] = t;
+        }
+        if (want_b && wv == 0 && h == 0) {
+#pragma unroll
+            for (int mt = 0; mt < TM; ++mt) {
+                float t = lds_b[mt * 32 + j];
+#pragma unroll
+                for (int w = 1; w < WPB; ++w) t += lds_b[(w * TM + mt) * 32 + j];
+                const int64_t co = co0 + 32 * mt + j;
+                if (co < C_out) part_b[gb * C_out + co] = t;
+            }
         }
     }
 }
@@ -678,21 +739,7 @@ __global__ __launch_bounds__(1024) void k_sum_partials(const float* __restrict__
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int64_t e = ((int64_t)blockIdx.x - (first ? 0 : nb0)) * 64 + lane;
     const int64_t g0 = wv * G / 16, g1 = (wv + 1) * G / 16;
-    double sum = 0.0;
-    if (e < E) {
-        // full batches of loads with no bounds test between them (a test per
-        // load makes the compiler wait for each one), then the tail
-        constexpr int kU = 8;
-        int64_t gg = g0;
-        for (; gg + kU <= g1; gg += kU) {
-            float v[kU];
-#pragma unroll
-            for (int u = 0; u < kU; ++u) v[u] = part[(gg + u) * E + e];
-#pragma unroll
-            for (int u = 0; u < kU; ++u) sum += (double)v[u];
-        }
-        for (; gg < g1; ++gg) sum += (double)part[gg * E + e];
-    }
+    const double sum = e < E ? segment_sum(part, E, e, g0, g1) : 0.0;
     lds[wv][lane] = sum;
     __syncthreads();
     if (wv == 0 && e < E) {
@@ -1139,7 +1186,7 @@ hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_ou
 }
 
 PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW,
-                           int64_t chunk_dx, int kz_max) {
+                           int64_t chunk_dx, int kz_max, int wg_waves) {
     PwBwdPlan p;
     // dx = W^T dz: M = C_in outputs, K = C_out terms.  (Its split-K over
     // blocks measured no gain: a plain 256 -> 128 output at 4096 pixels took
@@ -1162,6 +1209,14 @@ PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW,
     p.chunk = std::min(chunk, std::max<int64_t>(hw32, 32));
     p.cpp = (HW + p.chunk - 1) / p.chunk;
     p.G = N * p.cpp;
+    // waves per block (a power of two, each with at least one step of a
+    // plane) on chunks of wpb wave chunks; the partials are sized for one
+    // per wave chunk, which covers any wpb
+    p.wpb = 1;
+    while (p.wpb < wg_waves && 2 * p.wpb <= p.G && 2 * p.wpb * kWgStep <= hw32) p.wpb *= 2;
+    p.chunk_b = std::min(p.chunk * p.wpb, hw32);
+    p.cpp_b = (HW + p.chunk_b - 1) / p.chunk_b;
+    p.Gb = N * p.cpp_b;
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
     p.wt_bytes = al(sizeof(float) * (size_t)(C_in * C_out));
     p.pw_bytes = al(sizeof(float) * (size_t)(p.G * C_out * C_in));
@@ -1230,13 +1285,21 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
     } else if (a.dw || a.db) {
         const bool fast = (HW % 4 == 0) && ((uintptr_t)a.dz % 16 == 0) &&
                           ((uintptr_t)a.x % 16 == 0);
-        const dim3 grid((unsigned)(p.tiles_co * p.tiles_ci), (unsigned)p.G);
+        const dim3 grid((unsigned)(p.tiles_co * p.tiles_ci), (unsigned)p.Gb);
         int tok = prof_begin(s, "pw_conv_wgrad");
+        auto launch = [&](auto F, auto M2, auto N2, auto W) {
+            k_pw_wgrad<F(), M2() ? 2 : 1, N2() ? 2 : 1, W()><<<grid, 64 * W(), 0, s>>>(
+                a.dz, a.x, part_w, part_b, C_in, C_out, HW, p.chunk_b, p.cpp_b, p.tiles_ci);
+        };
         bsel(fast, [&](auto F) {
             bsel(p.tm == 2, [&](auto M2) {
                 bsel(p.tn == 2, [&](auto N2) {
-                    k_pw_wgrad<F(), M2() ? 2 : 1, N2() ? 2 : 1><<<grid, 64, 0, s>>>(
-                        a.dz, a.x, part_w, part_b, C_in, C_out, HW, p.chunk, p.cpp, p.tiles_ci);
+                    switch (p.wpb) {
+                        case 1: launch(F, M2, N2, std::integral_constant<int, 1>{}); break;
+                        case 2: launch(F, M2, N2, std::integral_constant<int, 2>{}); break;
+                        case 4: launch(F, M2, N2, std::integral_constant<int, 4>{}); break;
+                        default: launch(F, M2, N2, std::integral_constant<int, 8>{}); break;
+                    }
                 });
             });
         });
@@ -1246,7 +1309,7 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
         const int64_t E = C_out * C_in;
         const int64_t nbw = a.dw ? (E + 63) / 64 : 0, nbb = a.db ? (C_out + 63) / 64 : 0;
         k_sum_partials<<<dim3((unsigned)(nbw + nbb)), 1024, 0, s>>>(part_w, a.dw, E, nbw, part_b,
-                                                                    a.db, C_out, p.G);
+                                                                    a.db, C_out, p.Gb);
         prof_end(s, tok);
     }
     return hipGetLastError();

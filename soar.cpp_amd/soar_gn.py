@@ -52,6 +52,7 @@ TUNE_PW_SMALL = 10
 TUNE_FOLD_MAX = 11
 TUNE_PW_SPLITK = 12
 TUNE_LOADS = 13
+TUNE_PW_WG_WAVES = 14
 
 
 class SoarUnavailable(RuntimeError):

@@ -247,6 +247,20 @@ def test_pw_small_tuning(L):
     assert soar_gn.tune_get(soar_gn.TUNE_PW_SMALL) == old
 
 
+def test_pw_wg_waves_tuning(L):
+    old = soar_gn.tune_get(soar_gn.TUNE_PW_WG_WAVES)
+    assert old == 4
+    for bad in (0, 3, 16, -1):
+        assert L.soar_gn_tune(soar_gn.TUNE_PW_WG_WAVES, bad) == soar_gn.SOAR_EINVAL
+    # the workspace holds one partial per chunk whatever the setting
+    ws = soar_gn.pw_conv_backward_workspace_bytes(1, 64, 64, 65536)
+    for v in (1, 2, 8):
+        soar_gn.tune(soar_gn.TUNE_PW_WG_WAVES, v)
+        assert soar_gn.tune_get(soar_gn.TUNE_PW_WG_WAVES) == v
+        assert soar_gn.pw_conv_backward_workspace_bytes(1, 64, 64, 65536) == ws
+    soar_gn.tune(soar_gn.TUNE_PW_WG_WAVES, old)
+
+
 def test_fold_max_tuning(L):
     old = soar_gn.tune_get(soar_gn.TUNE_FOLD_MAX)
     assert old == 128

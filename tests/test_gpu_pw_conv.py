@@ -284,6 +284,49 @@ def test_pw_conv_backward_matches_oracle(gpu, oracle, pw_path, N, C_in, C_out, H
         assert ratio[i] <= 1.0, f"{name} err {err[i]:.3e} > bound {b.reshape(-1)[i]:.3e} at {i}"
 
 
+WGRAD_WAVE_SHAPES = [
+    # (N, C_in, C_out, HW)
+    (1, 64, 64, 65536),     # one 64 x 64 tile, 1024 wave chunks of 64 pixels
+    (3, 24, 8, 333),        # one block per plane: 11 steps over up to 8 waves
+    (1, 130, 72, 4096),     # 6 partial tiles, ragged rows and columns
+    (2, 32, 48, 2500),      # 32-column tiles; the last block of a plane is short
+]
+
+
+@pytest.mark.parametrize("N,C_in,C_out,HW", WGRAD_WAVE_SHAPES)
+def test_pw_wgrad_waves_per_block(gpu, oracle, restore_pw_small, N, C_in, C_out, HW):
+    """The MFMA weight gradient with 1, 2, 4 and 8 waves per block (the
+    waves of a block take interleaved steps of one chunk and add their
+    tiles in LDS before writing one partial):
+    every setting within the fp32 bound of the float64 oracle, and each
+    one bitwise repeatable."""
+    print(f"pw wgrad waves N={N} C_in={C_in} C_out={C_out} HW={HW}", flush=True)
+    old = gpu.tune_get(gpu.TUNE_PW_WG_WAVES)
+    gpu.tune(gpu.TUNE_PW_SMALL, 0)
+    r = np.random.default_rng(HW + C_in)
+    dz = r.standard_normal((N, C_out, HW)).astype(np.float32)
+    x = r.standard_normal((N, C_in, HW)).astype(np.float32)
+    w = (r.uniform(-1, 1, (C_out, C_in)) / np.sqrt(C_in)).astype(np.float32)
+    _, tw, tb = oracle.conv1x1_bwd_f64(dz, x, w, N, C_in, C_out, HW)
+    _, bw, bb = bwd_bounds(dz, x, w)
+    dzd, xd, wd = dev(dz), dev(x), dev(w)
+    try:
+        for waves in (1, 2, 4, 8):
+            gpu.tune(gpu.TUNE_PW_WG_WAVES, waves)
+            runs = []
+            for _ in range(2):
+                _, dw, db = gpu.pw_conv_backward(dzd, xd, wd, want_dx=False)
+                runs.append((host(dw), host(db)))
+            for got, t, bnd, name in ((runs[0][0], tw, bw, "dw"), (runs[0][1], tb, bb, "db")):
+                err = np.abs(got.astype(np.float64).reshape(-1) - t)
+                ratio = err / (bnd.reshape(-1) + 1e-30)
+                i = int(np.argmax(ratio))
+                assert ratio[i] <= 1.0, f"waves {waves} {name} err {err[i]:.3e} at {i}"
+            assert np.array_equal(runs[0][0], runs[1][0]) and np.array_equal(runs[0][1], runs[1][1])
+    finally:
+        gpu.tune(gpu.TUNE_PW_WG_WAVES, old)
+
+
 @pytest.mark.parametrize("C_in,C_out,HW", [(32, 32, 1000), (128, 256, 2048)])
 def test_pw_conv_backward_accumulates(gpu, oracle, pw_path, C_in, C_out, HW):
     N = 1
