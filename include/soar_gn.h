@@ -427,6 +427,10 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
                                  /* block that add their tiles in LDS     */
                                  /* before writing one partial: 1, 2, 4   */
                                  /* or 8; the default is 4                */
+#define SOAR_TUNE_PW_WG_TARGET 15 /* waves the pointwise weight gradient  */
+                                  /* sizes its pixel chunks for (at least */
+                                  /* 64 pixels each): 256..2^20, default  */
+                                  /* 2048; changes its workspace size     */
 SOAR_API int soar_gn_tune(int key, int64_t value);
 SOAR_API int64_t soar_gn_tune_get(int key);
 

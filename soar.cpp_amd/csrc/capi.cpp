@@ -625,7 +625,8 @@ SOAR_API size_t soar_pw_conv_backward_workspace_bytes(int64_t N, int64_t C_in, i
     }
     const Tuning t = current_tuning();
     const soar::gn::PwBwdPlan p =
-        soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW, t.pw_chunk, (int)t.pw_kz, t.pw_wg_waves);
+        soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW, t.pw_chunk, (int)t.pw_kz, t.pw_wg_waves,
+                                   t.pw_wg_target);
     return soar::gn::pw_bwd_workspace_bytes(p);
 }
 
@@ -651,14 +652,16 @@ SOAR_API int soar_pw_conv_backward(const float* dz, const float* x, const float*
         return rc;
     const Tuning t = current_tuning();
     soar::gn::PwBwdPlan p =
-        soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW, t.pw_chunk, (int)t.pw_kz, t.pw_wg_waves);
-    if (!pw_grid_fits(N, HW, p.chunk_dx) || p.G > 65535 ||
+        soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW, t.pw_chunk, (int)t.pw_kz, t.pw_wg_waves,
+                                   t.pw_wg_target);
+    if (!pw_grid_fits(N, HW, p.chunk_dx) || p.Gb > 65535 ||
         p.tiles_co * p.tiles_ci > (int64_t)0x7fffffff)
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     // a workspace sized without the split-K slices (another tuning when it
     // was queried) runs dx without them
     if (p.kz_bytes && workspace_bytes < soar::gn::pw_bwd_workspace_bytes(p))
-        p = soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW, t.pw_chunk, 1, t.pw_wg_waves);
+        p = soar::gn::make_pw_bwd_plan(N, C_in, C_out, HW, t.pw_chunk, 1, t.pw_wg_waves,
+                                         t.pw_wg_target);
     const size_t need = soar::gn::pw_bwd_workspace_bytes(p);
     if (workspace_bytes < need)
         return fail(SOAR_EINVAL, "workspace of %zu bytes is smaller than the %zu this shape needs",
@@ -1123,6 +1126,11 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
                 return fail(SOAR_EINVAL, "pw_wg_waves must be 1, 2, 4 or 8");
             g_tune.pw_wg_waves = (int)value;
             return ok();
+        case SOAR_TUNE_PW_WG_TARGET:
+            if (value < 256 || value > (1 << 20))
+                return fail(SOAR_EINVAL, "pw_wg_target must be in [256, 2^20]");
+            g_tune.pw_wg_target = value;
+            return ok();
         default:
             return fail(SOAR_EINVAL, "unknown tuning key %d", key);
     }
@@ -1145,6 +1153,7 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
         case SOAR_TUNE_PW_SPLITK: return g_tune.pw_kz;
         case SOAR_TUNE_LOADS: return g_tune.loads;
         case SOAR_TUNE_PW_WG_WAVES: return g_tune.pw_wg_waves;
+        case SOAR_TUNE_PW_WG_TARGET: return g_tune.pw_wg_target;
         default: return -1;
     }
 }

@@ -77,6 +77,7 @@ struct Tuning {
     int pw_wg_waves = 4;         // pointwise weight gradient: waves per block
                                  // that add their tiles before writing one
                                  // partial (1, 2, 4 or 8)
+    int64_t pw_wg_target = 2048;  // and the waves its pixel chunks aim for
 };
 
 constexpr int kThreads = 256;   // first passes (stats, reduction)
@@ -202,7 +203,7 @@ struct PwBwdPlan {
     size_t kz_bytes = 0;   // and the slices' bytes, after the partials
 };
 PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW,
-                           int64_t chunk_dx, int kz_max, int wg_waves);
+                           int64_t chunk_dx, int kz_max, int wg_waves, int64_t wg_target);
 size_t pw_bwd_workspace_bytes(const PwBwdPlan& p);
 // dx runs the SIMT kernel when pw_use_small(N, C_in, C_out, HW, small),
 // dW/db when the weight gradient has at most small/2 multiply-adds and

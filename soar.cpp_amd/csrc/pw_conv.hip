@@ -1186,7 +1186,7 @@ hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_ou
 }
 
 PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW,
-                           int64_t chunk_dx, int kz_max, int wg_waves) {
+                           int64_t chunk_dx, int kz_max, int wg_waves, int64_t wg_target) {
     PwBwdPlan p;
     // dx = W^T dz: M = C_in outputs, K = C_out terms.  (Its split-K over
     // blocks measured no gain: a plain 256 -> 128 output at 4096 pixels took
@@ -1203,7 +1203,7 @@ PwBwdPlan make_pw_bwd_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW,
     // spends about 1.7 us per 32-pixel step on its 64x64 tile, so small
     // grids get short chunks; each chunk adds a partial tile to the finish)
     const int64_t total = N * HW * p.tiles_co * p.tiles_ci;
-    int64_t chunk = (total / 2048 + 31) / 32 * 32;
+    int64_t chunk = (total / wg_target + 31) / 32 * 32;
     chunk = std::max<int64_t>(chunk, 64);
     const int64_t hw32 = (HW + 31) / 32 * 32;
     p.chunk = std::min(chunk, std::max<int64_t>(hw32, 32));

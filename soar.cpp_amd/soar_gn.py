@@ -53,6 +53,7 @@ TUNE_FOLD_MAX = 11
 TUNE_PW_SPLITK = 12
 TUNE_LOADS = 13
 TUNE_PW_WG_WAVES = 14
+TUNE_PW_WG_TARGET = 15
 
 
 class SoarUnavailable(RuntimeError):

@@ -261,6 +261,25 @@ def test_pw_wg_waves_tuning(L):
     soar_gn.tune(soar_gn.TUNE_PW_WG_WAVES, old)
 
 
+def test_pw_wg_target_tuning(L):
+    old = soar_gn.tune_get(soar_gn.TUNE_PW_WG_TARGET)
+    assert old == 2048
+    for bad in (0, 255, (1 << 20) + 1):
+        assert L.soar_gn_tune(soar_gn.TUNE_PW_WG_TARGET, bad) == soar_gn.SOAR_EINVAL
+    # 65536 pixels, one tile: a target of 2048 waves gives chunks of 32
+    # pixels, raised to the 64-pixel floor, so 1024 partial tiles.  A larger
+    # target stays at the floor (same workspace); a smaller one gives longer
+    # chunks and fewer partials.
+    base = soar_gn.pw_conv_backward_workspace_bytes(1, 64, 64, 65536)
+    try:
+        soar_gn.tune(soar_gn.TUNE_PW_WG_TARGET, 4096)
+        assert soar_gn.pw_conv_backward_workspace_bytes(1, 64, 64, 65536) == base
+        soar_gn.tune(soar_gn.TUNE_PW_WG_TARGET, 512)
+        assert soar_gn.pw_conv_backward_workspace_bytes(1, 64, 64, 65536) < base
+    finally:
+        soar_gn.tune(soar_gn.TUNE_PW_WG_TARGET, old)
+
+
 def test_fold_max_tuning(L):
     old = soar_gn.tune_get(soar_gn.TUNE_FOLD_MAX)
     assert old == 128
