@@ -777,18 +777,19 @@ __global__ void k_transpose(const float* __restrict__ w, float* __restrict__ wt,
 // ======================================================================
 constexpr int kSmallMaxWaves = 16;
 
+// The body for output group `bx` (64 elements) of sample n; the block's
+// blockDim.x / 64 waves split K.
 template <bool TRANS, bool V4, bool ACC, bool BIAS>
-__global__ __launch_bounds__(1024) void k_pw_small(const float* __restrict__ x,
-                                                   const float* __restrict__ w,
-                                                   const float* __restrict__ bias,
-                                                   float* __restrict__ z, int M, int K, int HW,
-                                                   int seg) {
-    __shared__ float part[kSmallMaxWaves][64];
+__device__ __forceinline__ void pw_small_body(const float* __restrict__ x,
+                                              const float* __restrict__ w,
+                                              const float* __restrict__ bias,
+                                              float* __restrict__ z, int M, int K, int HW,
+                                              int seg, int64_t bx, int64_t n,
+                                              float (*part)[64]) {
     const int lane = threadIdx.x & 63, v = threadIdx.x >> 6;
     const int S = blockDim.x >> 6;
-    const int64_t n = blockIdx.y;
     const int MH = M * HW;
-    const int o = (int)blockIdx.x * 64 + lane;  // element of the sample's output
+    const int o = (int)bx * 64 + lane;  // element of the sample's output
     const bool live = o < MH;
     const int oc = live ? o : MH - 1;  // lanes past the end compute a copy
     const int m = oc / HW, p = oc - m * HW;
@@ -853,6 +854,17 @@ __global__ __launch_bounds__(1024) void k_pw_small(const float* __restrict__ x,
     }
 }
 
+template <bool TRANS, bool V4, bool ACC, bool BIAS>
+__global__ __launch_bounds__(1024) void k_pw_small(const float* __restrict__ x,
+                                                   const float* __restrict__ w,
+                                                   const float* __restrict__ bias,
+                                                   float* __restrict__ z, int M, int K, int HW,
+                                                   int seg) {
+    __shared__ float part[kSmallMaxWaves][64];
+    pw_small_body<TRANS, V4, ACC, BIAS>(x, w, bias, z, M, K, HW, seg, blockIdx.x, blockIdx.y,
+                                        part);
+}
+
 // dW[co][ci] += sum_(n,p) dz[n][co][p] x[n][ci][p], db[co] += sum_(n,p)
 // dz[n][co][p] for small planes.  Entry e (weights ci-fastest, then the
 // C_out bias entries from E = C_out*C_in on) belongs to T = 2^lgT
@@ -862,16 +874,17 @@ __global__ __launch_bounds__(1024) void k_pw_small(const float* __restrict__ x,
 // one entry are shared by its lanes.  The grid covers entries [e0, e1)
 // (e0 = E when only db is wanted).  V4: HW % 4 == 0, seg % 4 == 0 and
 // 16-byte aligned dz and x.
+// The body for flat lane `tid` (any block size that is a multiple of 64:
+// the T lanes of an entry stay inside one wave).
 template <bool V4>
-__global__ __launch_bounds__(256) void k_pw_wgrad_small(const float* __restrict__ dz,
-                                                        const float* __restrict__ x,
-                                                        float* __restrict__ dw,
-                                                        float* __restrict__ db, int N, int C_in,
-                                                        int C_out, int HW, int64_t e0,
-                                                        int64_t e1, int lgT, int seg) {
+__device__ __forceinline__ void pw_wgrad_small_body(const float* __restrict__ dz,
+                                                    const float* __restrict__ x,
+                                                    float* __restrict__ dw,
+                                                    float* __restrict__ db, int N, int C_in,
+                                                    int C_out, int HW, int64_t e0, int64_t e1,
+                                                    int lgT, int seg, int64_t tid) {
     constexpr int W = V4 ? 4 : 1;  // pixels per load
     constexpr int U = 4;           // loads in flight per operand
-    const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int t = (int)(tid & ((1 << lgT) - 1));
     const int64_t e = e0 + (tid >> lgT);
     const bool valid = e < e1;
@@ -930,6 +943,41 @@ __global__ __launch_bounds__(256) void k_pw_wgrad_small(const float* __restrict_
     if (valid && t == 0) {
         float* out = wt ? dw + ec : db + co;
         *out = (float)((double)*out + acc);
+    }
+}
+
+template <bool V4>
+__global__ __launch_bounds__(256) void k_pw_wgrad_small(const float* __restrict__ dz,
+                                                        const float* __restrict__ x,
+                                                        float* __restrict__ dw,
+                                                        float* __restrict__ db, int N, int C_in,
+                                                        int C_out, int HW, int64_t e0,
+                                                        int64_t e1, int lgT, int seg) {
+    pw_wgrad_small_body<V4>(dz, x, dw, db, N, C_in, C_out, HW, e0, e1, lgT, seg,
+                            (int64_t)blockIdx.x * 256 + threadIdx.x);
+}
+
+// dx (+)= W^T dz and dW / db += the weight gradient of a small convolution
+// in one launch (the two are independent and each is a few microseconds of
+// mostly fixed cost): blocks [0, nbd) run k_pw_small's dx body over nbx
+// output groups per sample, the others k_pw_wgrad_small's body on flat
+// lanes.  Every output gets the same operations in the same order as from
+// the two kernels.
+template <bool ACC, bool V4W>
+__global__ __launch_bounds__(1024) void k_pw_small_bwd(
+    const float* __restrict__ dz, const float* __restrict__ w, float* __restrict__ dx,
+    const float* __restrict__ x, float* __restrict__ dw, float* __restrict__ db, int N,
+    int C_in, int C_out, int HW, int seg_d, int64_t nbx, int64_t nbd, int64_t e0, int64_t e1,
+    int lgT, int seg_w) {
+    __shared__ float part[kSmallMaxWaves][64];
+    const int64_t b = blockIdx.x;
+    if (b < nbd) {
+        const int64_t n = b / nbx;
+        pw_small_body<true, false, ACC, false>(dz, w, nullptr, dx, C_in, C_out, HW, seg_d,
+                                               b - n * nbx, n, part);
+    } else {
+        pw_wgrad_small_body<V4W>(dz, x, dw, db, N, C_in, C_out, HW, e0, e1, lgT, seg_w,
+                                 (b - nbd) * (int64_t)blockDim.x + threadIdx.x);
     }
 }
 
@@ -995,13 +1043,50 @@ namespace {
 
 // z = W x (+ bias), or z += W x; TRANS: z = W^T x.  M output rows, K input
 // rows.  Each wave sums about 32 values of K.
+// Waves per block (K split) and K per wave of the SIMT kernel.
+struct PwSmallSplit {
+    int S = 1;
+    int64_t seg = 0;
+};
+PwSmallSplit pw_small_split(int64_t K) {
+    PwSmallSplit r;
+    r.S = (int)std::min<int64_t>(kSmallMaxWaves, std::max<int64_t>(1, (K + 31) / 32));
+    r.seg = (K + r.S - 1) / r.S;
+    r.seg = (r.seg + 3) / 4 * 4;
+    r.S = (int)((K + r.seg - 1) / r.seg);
+    return r;
+}
+
+// Lanes of the SIMT weight gradient: entries [e0, e1) (dW then db), 2^lgT
+// lanes per entry over segments of `seg` pixels, about 64K lanes in all.
+struct PwWgSmallPlan {
+    int64_t e0 = 0, e1 = 0, lanes = 0;
+    int lgT = 0;
+    int64_t seg = 0;
+    bool v4 = false;
+};
+PwWgSmallPlan pw_wgrad_small_plan(const float* dz, const float* x, bool want_dw, bool want_db,
+                                  int64_t N, int64_t C_in, int64_t C_out, int64_t HW) {
+    PwWgSmallPlan p;
+    const int64_t E = C_out * C_in;
+    p.e0 = want_dw ? 0 : E;
+    p.e1 = want_db ? E + C_out : E;
+    p.v4 = (HW % 4 == 0) && ((uintptr_t)dz % 16 == 0) && ((uintptr_t)x % 16 == 0);
+    // segments of >= 8 pixels
+    const int64_t nhw = N * HW, ne = p.e1 - p.e0;
+    while (p.lgT < 6 && (ne << p.lgT) < 65536 && nhw > ((int64_t)8 << p.lgT)) ++p.lgT;
+    p.seg = (nhw + (1 << p.lgT) - 1) >> p.lgT;
+    if (p.v4) p.seg = (p.seg + 3) / 4 * 4;
+    p.lanes = ne << p.lgT;
+    return p;
+}
+
 hipError_t launch_pw_small(const float* x, const float* w, const float* bias, float* z,
                            int64_t N, int64_t K, int64_t M, int64_t HW, bool trans,
                            bool accumulate, hipStream_t s, const char* name) {
-    int S = (int)std::min<int64_t>(kSmallMaxWaves, std::max<int64_t>(1, (K + 31) / 32));
-    int64_t seg = (K + S - 1) / S;
-    seg = (seg + 3) / 4 * 4;
-    S = (int)((K + seg - 1) / seg);
+    const PwSmallSplit sp = pw_small_split(K);
+    const int S = sp.S;
+    const int64_t seg = sp.seg;
     const bool v4 = !trans && K % 4 == 0 && (uintptr_t)w % 16 == 0;
     const dim3 grid((unsigned)((M * HW + 63) / 64), (unsigned)N);
     const int tok = prof_begin(s, name);
@@ -1236,7 +1321,27 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
     float* wt = reinterpret_cast<float*>(ws);
     float* part_w = reinterpret_cast<float*>(ws + p.wt_bytes);
     float* part_b = reinterpret_cast<float*>(ws + p.wt_bytes + p.pw_bytes);
-    if (a.dx && pw_use_small(N, C_in, C_out, HW, small)) {
+    const bool small_dx = a.dx && pw_use_small(N, C_in, C_out, HW, small);
+    const bool small_dw = (a.dw || a.db) && pw_use_small_wgrad(N, C_in, C_out, HW, small);
+    if (small_dx && small_dw) {
+        // both SIMT kernels in one launch, on dx's block shape
+        const PwSmallSplit sp = pw_small_split(C_out);
+        const PwWgSmallPlan wp = pw_wgrad_small_plan(a.dz, a.x, a.dw, a.db, N, C_in, C_out, HW);
+        const int64_t threads = 64 * (int64_t)sp.S;
+        const int64_t nbx = (C_in * HW + 63) / 64, nbd = nbx * N;
+        const int64_t nbw = (wp.lanes + threads - 1) / threads;
+        const int tok = prof_begin(s, "pw_conv_bwd_small");
+        bsel(accumulate_dx, [&](auto A) {
+            bsel(wp.v4, [&](auto V) {
+                k_pw_small_bwd<A(), V()><<<dim3((unsigned)(nbd + nbw)), (unsigned)threads, 0, s>>>(
+                    a.dz, a.w, a.dx, a.x, a.dw, a.db, (int)N, (int)C_in, (int)C_out, (int)HW,
+                    (int)sp.seg, nbx, nbd, wp.e0, wp.e1, wp.lgT, (int)wp.seg);
+            });
+        });
+        prof_end(s, tok);
+        return hipGetLastError();
+    }
+    if (small_dx) {
         // dx = W^T dz, reading W transposed in place
         hipError_t e = launch_pw_small(a.dz, a.w, nullptr, a.dx, N, C_out, C_in, HW, true,
                                        accumulate_dx, s, "pw_conv_dgrad_small");
@@ -1264,22 +1369,13 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
                                       in_place);
         if (e != hipSuccess) return e;
     }
-    if ((a.dw || a.db) && pw_use_small_wgrad(N, C_in, C_out, HW, small)) {
-        const int64_t E = C_out * C_in;
-        const int64_t e0 = a.dw ? 0 : E, e1 = a.db ? E + C_out : E;
-        const bool v4 = (HW % 4 == 0) && ((uintptr_t)a.dz % 16 == 0) && ((uintptr_t)a.x % 16 == 0);
-        // lanes per entry: about 64K lanes in all, segments of >= 8 pixels
-        const int64_t nhw = N * HW, ne = e1 - e0;
-        int lgT = 0;
-        while (lgT < 6 && (ne << lgT) < 65536 && nhw > ((int64_t)8 << lgT)) ++lgT;
-        int64_t seg = (nhw + (1 << lgT) - 1) >> lgT;
-        if (v4) seg = (seg + 3) / 4 * 4;
-        const int64_t lanes = ne << lgT;
+    if (small_dw) {
+        const PwWgSmallPlan wp = pw_wgrad_small_plan(a.dz, a.x, a.dw, a.db, N, C_in, C_out, HW);
         const int tok = prof_begin(s, "pw_conv_wgrad_small");
-        bsel(v4, [&](auto V) {
-            k_pw_wgrad_small<V()><<<dim3((unsigned)((lanes + 255) / 256)), 256, 0, s>>>(
-                a.dz, a.x, a.dw, a.db, (int)N, (int)C_in, (int)C_out, (int)HW, e0, e1, lgT,
-                (int)seg);
+        bsel(wp.v4, [&](auto V) {
+            k_pw_wgrad_small<V()><<<dim3((unsigned)((wp.lanes + 255) / 256)), 256, 0, s>>>(
+                a.dz, a.x, a.dw, a.db, (int)N, (int)C_in, (int)C_out, (int)HW, wp.e0, wp.e1,
+                wp.lgT, (int)wp.seg);
         });
         prof_end(s, tok);
     } else if (a.dw || a.db) {

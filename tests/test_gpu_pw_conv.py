@@ -504,11 +504,15 @@ def test_pw_small_planes_match_oracle(gpu, oracle, restore_pw_small, N, C_in, C_
                                dweight=dev(base["dw"]), dbias=dev(base["db"]),
                                accumulate_dx=True)
     _assert_bwd(got, truth_b, bounds, "accumulate", base)
-    for want in ("dx", "dw", "db"):
+    # dx, dW and db together run as one launch (k_pw_small_bwd): the same
+    # bits as each gradient computed alone
+    together = [host(t) for t in gpu.pw_conv_backward(dev(dz), dev(x), dev(w))]
+    for k, want in enumerate(("dx", "dw", "db")):
         got = gpu.pw_conv_backward(dev(dz), dev(x), dev(w), want_dx=want == "dx",
                                    want_dw=want == "dw", want_db=want == "db")
         _assert_bwd(got, truth_b, bounds, f"only {want}")
         assert sum(g is not None for g in got) == 1
+        assert np.array_equal(host(got[k]), together[k]), f"{want} alone vs together"
     z0 = dev(np.full((N, C_out, HW), 0.25, np.float32))
     gpu.pw_conv_forward(dev(x), dev(w), bd, z=z0)
     assert_z(host(z0), x, w, b, oracle, "into a given z")
