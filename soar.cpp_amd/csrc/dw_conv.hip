@@ -122,14 +122,14 @@ struct TilePrefetch {
 // per block (tile rows tyg*per ..): the input of tile i + 1 is fetched into
 // registers while tile i is computed from LDS.  FLIP
 // applies the kernel rotated by 180 degrees (the stride-1 input gradient).
+// (body of block b; `tile` holds Tile<K, S, D>::floats floats)
 template <int K, int S, int D, bool FLIP, bool ACC, bool BIAS>
-__global__ __launch_bounds__(kDwThreads) void k_dw_conv(
+__device__ __forceinline__ void dw_conv_body(
     const float* __restrict__ in, const float* __restrict__ w, const float* __restrict__ bias,
     float* __restrict__ out, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo,
-    int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per) {
+    int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per, int64_t b,
+    float* __restrict__ tile) {
     using T = Tile<K, S, D>;
-    __shared__ __attribute__((aligned(16))) float tile[T::floats];
-    const int64_t b = blockIdx.x;
     const int64_t plane = b / tpp, gix = b - plane * tpp;
     const int64_t c = plane % C;
     const int64_t tyg = gix / tiles_x, tx = gix - tyg * tiles_x;
@@ -183,6 +183,16 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_conv(
     }
 }
 
+template <int K, int S, int D, bool FLIP, bool ACC, bool BIAS>
+__global__ __launch_bounds__(kDwThreads) void k_dw_conv(
+    const float* __restrict__ in, const float* __restrict__ w, const float* __restrict__ bias,
+    float* __restrict__ out, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo,
+    int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per) {
+    __shared__ __attribute__((aligned(16))) float tile[Tile<K, S, D>::floats];
+    dw_conv_body<K, S, D, FLIP, ACC, BIAS>(in, w, bias, out, C, Hi, Wi, Ho, Wo, pad, tiles_x,
+                                           tiles_y, tpp, per, blockIdx.x, tile);
+}
+
 // Weight and bias gradient partials: a block walks `per` tiles down one
 // plane (tile rows ty = tyg*per + i), accumulating in registers, then
 // reduces once: part[g][c*(K*K+1) + k] with g = n*tpp + tyg*tiles_x + tx
@@ -195,17 +205,16 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_conv(
 // With `direct` (one sample and one tile group per plane, so a block's sums
 // are the whole sums) the block adds them into dw and db itself, exactly as
 // k_dw_wgrad_finish would from its single partial, and no finish runs.
+// (body of block b; `tile` holds Tile<K, S, D>::floats floats)
 template <int K, int S, int D>
-__global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
+__device__ __forceinline__ void dw_wgrad_body(
     const float* __restrict__ dy, const float* __restrict__ x, float* __restrict__ part,
     float* __restrict__ dw, float* __restrict__ db, bool direct, int64_t C, int64_t Hi,
     int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x, int64_t tiles_y,
-    int64_t tpp, int per) {
+    int64_t tpp, int per, int64_t b, float* __restrict__ tile,
+    float (*red)[K * K + 1]) {
     using T = Tile<K, S, D>;
     constexpr int KK1 = K * K + 1;
-    __shared__ __attribute__((aligned(16))) float tile[T::floats];
-    __shared__ float red[kDwThreads / 64][KK1];
-    const int64_t b = blockIdx.x;
     const int64_t plane = b / tpp, gix = b - plane * tpp;
     const int64_t n = plane / C, c = plane - n * C;
     const int64_t tyg = gix / tiles_x, tx = gix - tyg * tiles_x;
@@ -278,6 +287,18 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
     }
 }
 
+template <int K, int S, int D>
+__global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
+    const float* __restrict__ dy, const float* __restrict__ x, float* __restrict__ part,
+    float* __restrict__ dw, float* __restrict__ db, bool direct, int64_t C, int64_t Hi,
+    int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x, int64_t tiles_y,
+    int64_t tpp, int per) {
+    __shared__ __attribute__((aligned(16))) float tile[Tile<K, S, D>::floats];
+    __shared__ float red[kDwThreads / 64][K * K + 1];
+    dw_wgrad_body<K, S, D>(dy, x, part, dw, db, direct, C, Hi, Wi, Ho, Wo, pad, tiles_x, tiles_y,
+                           tpp, per, blockIdx.x, tile, red);
+}
+
 // Input gradient for stride S > 1 over one 32 x 64 tile of dx per block:
 //   dx[yi][xi] (+)= sum over taps with S | (yi + pad - ky*D) and
 //   S | (xi + pad - kx*D) of w[ky][kx] * dy[(yi+pad-ky*D)/S][(xi+pad-kx*D)/S]
@@ -295,17 +316,16 @@ __device__ __forceinline__ int64_t floor_div(int64_t a, int64_t b) {
     return a >= 0 ? a / b : -((-a + b - 1) / b);
 }
 
+// (body of block b; `tile` holds DTile R * W floats)
 template <int K, int S, int D, bool ACC>
-__global__ __launch_bounds__(kDwThreads) void k_dw_dgrad_strided(
+__device__ __forceinline__ void dw_dgrad_strided_body(
     const float* __restrict__ dy, const float* __restrict__ w, float* __restrict__ dx,
     int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x,
-    int64_t tiles_y, int64_t tpp, int per) {
+    int64_t tiles_y, int64_t tpp, int per, int64_t b, float* __restrict__ tile) {
     using T = DTile<K, S, D>;
     constexpr int NR = (T::R * T::W + kDwThreads - 1) / kDwThreads;
-    __shared__ float tile[T::R * T::W];
     // `per` dx tiles down one plane per block (tiles over dx here); the dy
     // region of the next tile loads into registers while this one is summed
-    const int64_t b = blockIdx.x;
     const int64_t plane = b / tpp, gix = b - plane * tpp;
     const int64_t c = plane % C;
     const int64_t tyg = gix / tiles_x, tx = gix - tyg * tiles_x;
@@ -385,6 +405,49 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_dgrad_strided(
             for (int q = 0; q < kPer; ++q)
                 if (xb + q < Wi) orow[xb + q] = ACC ? orow[xb + q] + acc[q] : acc[q];
         }
+    }
+}
+
+template <int K, int S, int D, bool ACC>
+__global__ __launch_bounds__(kDwThreads) void k_dw_dgrad_strided(
+    const float* __restrict__ dy, const float* __restrict__ w, float* __restrict__ dx,
+    int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x,
+    int64_t tiles_y, int64_t tpp, int per) {
+    __shared__ float tile[DTile<K, S, D>::R * DTile<K, S, D>::W];
+    dw_dgrad_strided_body<K, S, D, ACC>(dy, w, dx, C, Hi, Wi, Ho, Wo, pad, tiles_x, tiles_y,
+                                        tpp, per, blockIdx.x, tile);
+}
+
+// The input gradient and the weight gradient of a small depthwise layer in
+// one launch (each is a few microseconds of mostly fixed cost at such
+// sizes): blocks [0, nbd) run the dx body (stride 1: the flipped-kernel
+// convolution over dy; stride 2: the staged gather), the others the weight
+// gradient's body on blocks b - nbd.  Each block does exactly what it does
+// in its own kernel.  Used for small grids only: the union of the two
+// bodies' registers would lower the larger grids' occupancy.
+template <int K, int S, int D, bool ACC>
+__global__ __launch_bounds__(kDwThreads) void k_dw_bwd_small(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
+    float* __restrict__ dx, float* __restrict__ part, float* __restrict__ dw,
+    float* __restrict__ db, bool direct, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho,
+    int64_t Wo, int64_t pad, int64_t dtx, int64_t dty, int64_t dtpp, int dper, int64_t wtx,
+    int64_t wty, int64_t wtpp, int wper, int64_t nbd) {
+    constexpr int TD = S == 1 ? Tile<K, 1, D>::floats : DTile<K, S, D>::R * DTile<K, S, D>::W;
+    constexpr int TW = Tile<K, S, D>::floats;
+    __shared__ __attribute__((aligned(16))) float tile[TD > TW ? TD : TW];
+    __shared__ float red[kDwThreads / 64][K * K + 1];
+    const int64_t b = blockIdx.x;
+    if (b < nbd) {
+        if constexpr (S == 1)
+            dw_conv_body<K, 1, D, true, ACC, false>(dy, w, nullptr, dx, C, Ho, Wo, Hi, Wi,
+                                                    (K - 1) * D - pad, dtx, dty, dtpp, dper, b,
+                                                    tile);
+        else
+            dw_dgrad_strided_body<K, S, D, ACC>(dy, w, dx, C, Hi, Wi, Ho, Wo, pad, dtx, dty,
+                                                dtpp, dper, b, tile);
+    } else {
+        dw_wgrad_body<K, S, D>(dy, x, part, dw, db, direct, C, Hi, Wi, Ho, Wo, pad, wtx, wty,
+                               wtpp, wper, b - nbd, tile, red);
     }
 }
 
@@ -558,6 +621,10 @@ int64_t conv_groups(int64_t planes, int64_t H, int64_t W, int64_t* tiles_x, int6
     return ((*tiles_y + p - 1) / p) * *tiles_x;
 }
 
+// Layers whose dx and weight-gradient grids hold at most this many blocks
+// together run both in one launch (k_dw_bwd_small).
+constexpr int64_t kDwFuseBlocks = 2048;
+
 unsigned grid_stride_blocks(int64_t total) {
     const int64_t b = (total + 255) / 256;
     return (unsigned)std::max<int64_t>(1, std::min<int64_t>(b, 65536));
@@ -630,6 +697,41 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
                               const float* w, float* dx, float* dw, float* db,
                               bool accumulate_dx, void* ws, hipStream_t s) {
     if (sh.N * sh.C == 0) return hipSuccess;
+    if (dx && (dw || db) && sh.Hi * sh.Wi > 0 && sh.Ho * sh.Wo > 0 && planes_fit_32(sh)) {
+        // a small layer: dx and the weight gradient in one launch
+        int64_t dtx = 0, dty = 0, wtx = 0, wty = 0;
+        int dper = 1;
+        const int64_t dtpp = conv_groups(sh.N * sh.C, sh.Hi, sh.Wi, &dtx, &dty, &dper);
+        const int64_t wper = wgrad_per(sh);
+        const int64_t wtpp = wgrad_groups(sh, wper, &wtx, &wty);
+        const int64_t nbd = sh.N * sh.C * dtpp, nbw = sh.N * sh.C * wtpp;
+        const bool direct = sh.N * wtpp == 1;
+        float* part = static_cast<float*>(ws);
+        bool fused = false;
+        if (nbd + nbw <= kDwFuseBlocks && (sh.S == 1 || sh.S == 2)) {
+            const int tok = prof_begin(s, "dw_conv_bwd_small");
+            fused = fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
+                using CF = decltype(cf);
+                bsel(accumulate_dx, [&](auto A) {
+                    k_dw_bwd_small<CF::k, CF::s, CF::d, A()>
+                        <<<dim3((unsigned)(nbd + nbw)), kDwThreads, 0, s>>>(
+                            dy, x, w, dx, part, dw, db, direct, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo,
+                            sh.pad, dtx, dty, dtpp, dper, wtx, wty, wtpp, (int)wper, nbd);
+                });
+            });
+            prof_end(s, tok);
+        }
+        if (fused) {
+            if (!direct) {
+                const int64_t KK1 = sh.K * sh.K + 1, E = sh.C * KK1;
+                const int tok = prof_begin(s, "dw_conv_wgrad_finish");
+                k_dw_wgrad_finish<<<dim3((unsigned)((E + 63) / 64)), 1024, 0, s>>>(
+                    part, dw, db, E, sh.N * wtpp, KK1);
+                prof_end(s, tok);
+            }
+            return hipGetLastError();
+        }
+    }
     if (dx && sh.Hi * sh.Wi > 0) {
         const int tok = prof_begin(s, "dw_conv_dgrad");
         bool done = false;

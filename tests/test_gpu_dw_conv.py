@@ -85,6 +85,13 @@ def test_dw_backward_matches_oracle(gpu, oracle, N, C, H, W, K, s, d):
     P = N * Ho * Wo + 2
     check(host(dw), tw, P * U32 * aw, "dw")
     check(host(db), tb, P * U32 * np.abs(dy).sum(axis=(0, 2, 3)), "db")
+    # small layers run dx and the weight gradient in one launch
+    # (k_dw_bwd_small): the same bits as each alone
+    dx1, _, _ = gpu.dw_conv_backward(dev(dy), dev(x), dev(w), pad, s, d, want_dw=False,
+                                     want_db=False)
+    _, dw1, db1 = gpu.dw_conv_backward(dev(dy), dev(x), dev(w), pad, s, d, want_dx=False)
+    for a, b_, name in ((dx1, dx, "dx"), (dw1, dw, "dw"), (db1, db, "db")):
+        assert np.array_equal(host(a), host(b_)), f"{name} alone vs together"
 
 
 @pytest.mark.parametrize("H,W", [(40, 70), (20, 30)])  # partials + finish, direct
