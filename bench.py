@@ -19,7 +19,8 @@ through the C-ABI of libsoar_gn.so on one GPU.  Prints one JSON line:
 Other workloads (--config): the other BASELINE configs (cfg2_fwd,
 cfg4_chain, cfg5), the CBA block with a pointwise conv (cba_pw), the CBA
 depthwise convolutions at 1x64x2048^2 (dw_k3, dw_k5, dw_k7, dw_k3d5,
-dw_k3s2), SOAR training steps (train_nano64/512/1024) and the streaming
+dw_k3s2), SOAR training steps (train_nano64/512/1024), SOAR predictions
+(predict_nano64/1024) and the streaming
 ceilings of this memory system for plain kernels of the library's shape
 (stream_read, stream_copy, stream_2r1w, stream_2r over 1 GiB buffers; stream_planes_read,
 stream_planes_copy, stream_planes_copy_pad4k: the pointwise convolution's 64-plane pattern).
@@ -79,6 +80,12 @@ TRAIN_CONFIGS = {
     "train_nano512": ("nano", 512, 512),
     "train_nano1024": ("nano", 1024, 1024),
 }
+# soar_predict of the same model: no-grad forward, sigmoid, threshold,
+# probabilities, mask and RLE back to the host
+PREDICT_CONFIGS = {
+    "predict_nano64": ("nano", 64, 64),
+    "predict_nano1024": ("nano", 1024, 1024),
+}
 
 # algorithmic tensor passes (units of T) each kernel makes per block of the
 # step, summed over its launches (a kernel runs once per unit batch)
@@ -93,7 +100,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg3",
-                    choices=sorted(CONFIGS) + sorted(TRAIN_CONFIGS) + sorted(STREAM_CONFIGS)
+                    choices=sorted(CONFIGS) + sorted(TRAIN_CONFIGS) + sorted(PREDICT_CONFIGS)
+                    + sorted(STREAM_CONFIGS)
                     + sorted(DW_CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-timing", action="store_true",
@@ -511,17 +519,53 @@ def bench_train(args):
     print(json.dumps(out))
 
 
+def bench_predict(args):
+    """Images/s of soar_predict on one GPU (host image in; probabilities,
+    mask and RLE string out, as the reference's C-ABI returns them)."""
+    import numpy as np
+    import torch
+    import soar_model as sm
+    variant, H, W = PREDICT_CONFIGS[args.config]
+    r = np.random.default_rng(SEED)
+    img = r.normal(0.5, 0.25, size=(1, H, W)).astype(np.float32)
+    m = sm.SOAR(1, 1, variant, seed=SEED)
+    for _ in range(args.warmup):
+        m.predict(img)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        m.predict(img)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    mem = m.memory_info()
+    m.close()
+    print(json.dumps({
+        "metric": f"SOAR {variant} predict images/s, 1x{H}x{W} fp32",
+        "value": round(1.0 / dt, 3), "unit": "images/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": args.config, "variant": variant, "image": [1, H, W],
+                   "threshold": 0.5},
+        "roofline": None, "memory": mem}))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has "
               "no multi-GPU path.", file=sys.stderr)
         sys.exit(2)
-    if args.config in TRAIN_CONFIGS or args.config in STREAM_CONFIGS:
+    if args.config in TRAIN_CONFIGS or args.config in STREAM_CONFIGS or \
+            args.config in PREDICT_CONFIGS:
         import torch
         assert torch.cuda.is_available(), "bench.py needs a GPU"
         torch.cuda.set_device(0)
-        (bench_train if args.config in TRAIN_CONFIGS else bench_stream)(args)
+        if args.config in TRAIN_CONFIGS:
+            bench_train(args)
+        elif args.config in PREDICT_CONFIGS:
+            bench_predict(args)
+        else:
+            bench_stream(args)
         return
     import torch
     import soar_gn as gn

@@ -67,6 +67,9 @@ SOAR_API int soar_train_step(void* handle, const float* image_data,
 /* Inference on one image: out_probs [H*W] sigmoid probabilities, out_mask
  * [H*W] 0/1 (prob >= threshold), out_rle the column-major RLE string
  * (truncated to max_rle_len - 1 characters).  Any output may be NULL.
+ * The device work runs on the handle's stream through pinned staging,
+ * replayed as a HIP graph from the second call of an image shape and
+ * threshold on (soar_model_set_graph_mode); results are the same bits.
  * Replaces: soar_predict (c_api.h:34-41). */
 SOAR_API int soar_predict(void* handle, const float* image_data, int channels,
                           int height, int width, float threshold,
@@ -108,11 +111,13 @@ SOAR_API int soar_model_forward_backward(void* handle, const float* image_data,
 SOAR_API int soar_model_zero_grad(void* handle);
 /* on != 0 (the default, or SOAR_TRAIN_GRAPH=0 in the environment at
  * creation for off): soar_train_step captures and replays its device work
- * as a HIP graph per image shape.  Off drops the graphs held.  No
- * counterpart in the reference (its step is eager). */
+ * as a HIP graph per image shape, and soar_predict per image shape and
+ * threshold.  Off drops the graphs held.  No counterpart in the reference
+ * (its calls are eager). */
 SOAR_API int soar_model_set_graph_mode(void* handle, int on);
 /* Whether graph mode is on (it turns itself off when a capture fails) and
- * how many training-step graphs the handle holds (either may be NULL). */
+ * how many training-step and predict graphs the handle holds (either may
+ * be NULL). */
 SOAR_API int soar_model_graph_info(void* handle, int* graph_mode,
                                    int* graphs_held);
 /* The 7 metrics of the last soar_train_step (the last entry is the global

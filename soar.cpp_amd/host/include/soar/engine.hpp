@@ -205,6 +205,12 @@ class Predictor {
 public:
     Predictor(std::shared_ptr<nn::SOARModel> model, float threshold = 0.5f);
     PredictionResult predict(const TensorPtr& image);
+    // The device part of predict on exec::stream(): no-grad forward, then
+    // probabilities (H*W floats) and the 0/1 mask (H*W bytes) into the
+    // given device buffers; nothing is read back (capturable).  Returns
+    // (H, W) of the logits.
+    std::pair<int64_t, int64_t> predict_device(const TensorPtr& image, float* probs,
+                                               uint8_t* mask);
     // Column-major, 1-indexed "start length" pairs of the non-zero runs
     // (predictor.cpp:10-48).
     static std::string encode_rle(const uint8_t* mask, size_t height, size_t width);

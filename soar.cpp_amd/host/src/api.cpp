@@ -68,11 +68,20 @@ struct SoarModelHandle {
     size_t pin_elems = 0;           // capacity of each, floats
     std::map<std::tuple<int, int, int>, StepGraph> graphs;
     std::map<std::tuple<int, int, int>, int> seen;  // eager steps run per shape
+    // ---- soar_predict the same way: graphs per (C, H, W, threshold bits) --
+    float* pin_probs = nullptr;     // pinned read-back of the probabilities
+    uint8_t* pin_mask = nullptr;    // and of the mask
+    size_t pin_out_elems = 0;
+    std::map<std::tuple<int, int, int, uint32_t>, StepGraph> pgraphs;
+    std::map<std::tuple<int, int, int, uint32_t>, int> pseen;
 
     ~SoarModelHandle() {
         for (auto& [k, g] : graphs)
             if (g.exec) (void)hipGraphExecDestroy(g.exec);
-        for (void* p : {(void*)pin_scalars, (void*)pin_out, (void*)pin_img, (void*)pin_msk})
+        for (auto& [k, g] : pgraphs)
+            if (g.exec) (void)hipGraphExecDestroy(g.exec);
+        for (void* p : {(void*)pin_scalars, (void*)pin_out, (void*)pin_img, (void*)pin_msk,
+                        (void*)pin_probs, (void*)pin_mask})
             if (p) (void)hipHostFree(p);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -92,6 +101,9 @@ void drop_graphs(SoarModelHandle* s) {
     for (auto& [k, g] : s->graphs)
         if (g.exec) (void)hipGraphExecDestroy(g.exec);
     s->graphs.clear();
+    for (auto& [k, g] : s->pgraphs)
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    s->pgraphs.clear();
 }
 
 void ensure_acts(SoarModelHandle* s, size_t need) {
@@ -122,6 +134,15 @@ void with_acts(SoarModelHandle* s, int64_t h, int64_t w, F&& fn, U&& undo) {
             ensure_acts(s, s->acts->slab().total_capacity() * 2);
         }
     }
+}
+
+// The RLE string into the caller's buffer, truncated to max_len - 1
+// characters and NUL-terminated (the bytes past the NUL are left as they
+// were: a zero fill of the whole buffer cost milliseconds per image).
+void copy_rle(const std::string& rle, char* out, size_t max_len) {
+    const size_t k = std::min(rle.size(), max_len - 1);
+    std::memcpy(out, rle.data(), k);
+    out[k] = '\0';
 }
 
 void check_image(int c, int h, int w) {
@@ -223,6 +244,21 @@ void ensure_pinned(SoarModelHandle* s, size_t elems) {
     s->pin_elems = elems;
 }
 
+// Pinned read-back buffers of predict's probabilities and mask.
+void ensure_pinned_out(SoarModelHandle* s, size_t elems) {
+    if (s->pin_out_elems >= elems) return;
+    drop_graphs(s);  // their copies write the old buffers
+    if (s->pin_probs) hip_check(hipHostFree(s->pin_probs), "hipHostFree");
+    if (s->pin_mask) hip_check(hipHostFree(s->pin_mask), "hipHostFree");
+    s->pin_probs = nullptr;
+    s->pin_mask = nullptr;
+    s->pin_out_elems = 0;
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&s->pin_probs), elems * sizeof(float)),
+              "hipHostMalloc");
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&s->pin_mask), elems), "hipHostMalloc");
+    s->pin_out_elems = elems;
+}
+
 // The device work of one training step from the pinned staging, on the
 // handle's stream (recorded into a graph while that stream is capturing).
 void device_step(SoarModelHandle* s, int64_t c, int64_t h, int64_t w) {
@@ -238,46 +274,54 @@ void device_step(SoarModelHandle* s, int64_t c, int64_t h, int64_t w) {
     s->trainer->train_step_device(img, msk, s->dev_sums, s->pin_scalars, s->dev_scalars);
 }
 
-// Runs one step: a graph replay when one is held for this shape, else the
-// step itself, captured (and then launched) from the second step of a
-// shape on.  A capture that fails is undone and the step runs uncaptured;
-// graphs stay off for the handle from then on.
-void run_train_step(SoarModelHandle* s, int c, int h, int w) {
-    const auto key = std::make_tuple(c, h, w);
-    auto it = s->graphs.find(key);
-    if (s->graph_mode && it != s->graphs.end() && s->acts &&
+// Runs `work` (one call's device work on the handle's stream) as a replay
+// of the graph held for `key`, else directly, captured (and then launched)
+// from the second call of a key on.  `before_replay` does the host part a
+// replay still needs (the graph holds device work only); `rollback` undoes
+// the host effects of a capture that is thrown away; `undo` is with_acts'
+// reset before a retry with a larger arena.  A capture that fails is
+// discarded and the call runs uncaptured; graphs stay off for the handle
+// from then on.
+template <typename K, typename W, typename B, typename R, typename U>
+void run_graphed(SoarModelHandle* s, std::map<K, StepGraph>& graphs, std::map<K, int>& seen,
+                 const K& key, int h, int w, W&& work, B&& before_replay, R&& rollback,
+                 U&& undo) {
+    auto it = graphs.find(key);
+    if (s->graph_mode && it != graphs.end() && s->acts &&
         it->second.acts_base == s->acts->base()) {
-        s->trainer->optimizer().next_scalars(s->pin_scalars);
+        before_replay();
         hip_check(hipGraphLaunch(it->second.exec, s->stream), "hipGraphLaunch");
         return;
     }
-    const bool capture = s->graph_mode && s->seen[key] > 0;
+    const bool capture = s->graph_mode && seen[key] > 0;
     with_acts(
         s, h, w,
         [&] {
             if (!capture) {
-                device_step(s, c, h, w);
+                work();
                 return;
             }
-            const int64_t step0 = s->trainer->optimizer().step_count();
             hip_check(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal),
                       "hipStreamBeginCapture");
             hipGraph_t graph = nullptr;
+            auto uncaptured = [&] {
+                (void)hipGetLastError();
+                rollback();
+                s->graph_mode = false;
+                s->acts->reset_dynamic_allocations();
+                work();
+            };
             try {
-                device_step(s, c, h, w);
+                work();
             } catch (const soar::OutOfMemory&) {
                 (void)hipStreamEndCapture(s->stream, &graph);
                 if (graph) (void)hipGraphDestroy(graph);
-                s->trainer->optimizer().set_step_count(step0);
+                rollback();
                 throw;  // with_acts grows the arena and runs again
             } catch (...) {
                 (void)hipStreamEndCapture(s->stream, &graph);
                 if (graph) (void)hipGraphDestroy(graph);
-                (void)hipGetLastError();
-                s->trainer->optimizer().set_step_count(step0);
-                s->graph_mode = false;
-                s->acts->reset_dynamic_allocations();
-                device_step(s, c, h, w);
+                uncaptured();
                 return;
             }
             hipGraphExec_t exec = nullptr;
@@ -285,21 +329,55 @@ void run_train_step(SoarModelHandle* s, int c, int h, int w) {
             if (e == hipSuccess) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
             if (graph) (void)hipGraphDestroy(graph);
             if (e != hipSuccess) {
-                (void)hipGetLastError();
-                s->trainer->optimizer().set_step_count(step0);
-                s->graph_mode = false;
-                s->acts->reset_dynamic_allocations();
-                device_step(s, c, h, w);
+                uncaptured();
                 return;
             }
             hip_check(hipGraphLaunch(exec, s->stream), "hipGraphLaunch");
-            StepGraph& g = s->graphs[key];
+            StepGraph& g = graphs[key];
             if (g.exec) (void)hipGraphExecDestroy(g.exec);
             g.exec = exec;
             g.acts_base = s->acts->base();
         },
-        [&] { s->trainer->optimizer().zero_grad(); });
-    s->seen[key] += 1;
+        undo);
+    seen[key] += 1;
+}
+
+void run_train_step(SoarModelHandle* s, int c, int h, int w) {
+    auto& opt = s->trainer->optimizer();
+    const int64_t step0 = opt.step_count();
+    run_graphed(
+        s, s->graphs, s->seen, std::make_tuple(c, h, w), h, w,
+        [&] { device_step(s, c, h, w); }, [&] { opt.next_scalars(s->pin_scalars); },
+        [&] { opt.set_step_count(step0); }, [&] { opt.zero_grad(); });
+}
+
+// The device work of one prediction from the pinned image: probabilities
+// and mask into arena buffers, then copied into the pinned read-back.
+void device_predict(SoarModelHandle* s, int64_t c, int64_t h, int64_t w, float threshold) {
+    TensorPtr img = soar::Tensor::create({c, h, w}, false, true);
+    soar::hip::kernels::check(soar_memcpy_async(img->cuda_data(), s->pin_img,
+                                                (size_t)(c * h * w) * sizeof(float), 0,
+                                                s->stream),
+                              "image upload");
+    const size_t n = (size_t)(h * w);
+    auto* probs = static_cast<float*>(s->acts->allocate(n * sizeof(float), {}, "probs"));
+    auto* mask = static_cast<uint8_t*>(s->acts->allocate(n, {}, "mask"));
+    soar::engine::Predictor p(s->model, threshold);
+    const auto [H, W] = p.predict_device(img, probs, mask);
+    if ((size_t)(H * W) != n) throw soar::ShapeError("predict: logits are not H x W");
+    soar::hip::kernels::check(
+        soar_memcpy_async(s->pin_probs, probs, n * sizeof(float), 1, s->stream),
+        "probabilities read-back");
+    soar::hip::kernels::check(soar_memcpy_async(s->pin_mask, mask, n, 1, s->stream),
+                              "mask read-back");
+}
+
+void run_predict(SoarModelHandle* s, int c, int h, int w, float threshold) {
+    uint32_t tb = 0;
+    std::memcpy(&tb, &threshold, sizeof tb);
+    run_graphed(
+        s, s->pgraphs, s->pseen, std::make_tuple(c, h, w, tb), h, w,
+        [&] { device_predict(s, c, h, w, threshold); }, [] {}, [] {}, [] {});
 }
 
 }  // namespace
@@ -379,21 +457,21 @@ SOAR_API int soar_predict(void* handle, const float* image_data, int channels, i
     auto* s = H(handle);
     return guarded([&] {
         check_image(channels, height, width);
-        soar::engine::PredictionResult r;
-        with_acts(
-            s, height, width,
-            [&] {
-                soar::engine::Predictor p(s->model, threshold);
-                r = p.predict(host_image(image_data, channels, height, width));
-            },
-            [] {});
-        const size_t n = r.height * r.width;
-        if (out_probs) std::memcpy(out_probs, r.probabilities.data(), n * sizeof(float));
-        if (out_mask) std::memcpy(out_mask, r.binary_mask.data(), n);
-        if (out_rle && max_rle_len > 0) {
-            std::strncpy(out_rle, r.rle_string.c_str(), max_rle_len - 1);
-            out_rle[max_rle_len - 1] = '\0';
+        const size_t n = (size_t)height * (size_t)width;
+        ensure_pinned(s, (size_t)channels * n);
+        ensure_pinned_out(s, n);
+        std::memcpy(s->pin_img, image_data, (size_t)channels * n * sizeof(float));
+        {
+            soar::exec::StreamScope scope(s->stream);
+            run_predict(s, channels, height, width, threshold);
         }
+        hip_check(hipStreamSynchronize(s->stream), "hipStreamSynchronize");
+        if (out_probs) std::memcpy(out_probs, s->pin_probs, n * sizeof(float));
+        if (out_mask) std::memcpy(out_mask, s->pin_mask, n);
+        if (out_rle && max_rle_len > 0)
+            copy_rle(soar::engine::Predictor::encode_rle(s->pin_mask, (size_t)height,
+                                                         (size_t)width),
+                     out_rle, max_rle_len);
     });
 }
 
@@ -401,9 +479,7 @@ SOAR_API int soar_encode_rle(const uint8_t* mask, size_t height, size_t width, c
                              size_t max_rle_len) {
     if (!mask || !out_rle || max_rle_len == 0) return -1;
     return guarded([&] {
-        const std::string rle = soar::engine::Predictor::encode_rle(mask, height, width);
-        std::strncpy(out_rle, rle.c_str(), max_rle_len - 1);
-        out_rle[max_rle_len - 1] = '\0';
+        copy_rle(soar::engine::Predictor::encode_rle(mask, height, width), out_rle, max_rle_len);
     });
 }
 
@@ -475,7 +551,7 @@ SOAR_API int soar_model_graph_info(void* handle, int* graph_mode, int* graphs_he
     if (!handle) return -1;
     auto* s = H(handle);
     if (graph_mode) *graph_mode = s->graph_mode ? 1 : 0;
-    if (graphs_held) *graphs_held = (int)s->graphs.size();
+    if (graphs_held) *graphs_held = (int)(s->graphs.size() + s->pgraphs.size());
     return 0;
 }
 

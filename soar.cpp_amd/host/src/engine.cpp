@@ -5,9 +5,11 @@
 #include "soar/engine.hpp"
 
 #include <algorithm>
+#include <charconv>
 #include <cmath>
 #include <cstring>
 #include <sstream>
+#include <vector>
 
 #include "soar/autograd.hpp"
 #include "soar/kernels.hpp"
@@ -444,34 +446,91 @@ StepMetrics Trainer::device_step_metrics(const double loss_sums[4], double norm_
 Predictor::Predictor(std::shared_ptr<nn::SOARModel> model, float threshold)
     : model_(std::move(model)), threshold_(threshold) {}
 
+namespace {
+// High bit of each byte of v set where that byte is nonzero.
+inline uint64_t nonzero_bytes(uint64_t v) {
+    const uint64_t lo7 = 0x7f7f7f7f7f7f7f7fULL;
+    return (((v & lo7) + lo7) | v) & ~lo7;
+}
+}  // namespace
+
+// Column-major (Fortran order), 1-indexed runs of nonzero pixels,
+// "start len start len ..." (predictor.cpp:10-47; a run may continue from
+// the bottom of one column into the top of the next).  The mask is read
+// once in row order: comparing each row with the one above it (8 columns
+// per word) gives, per column, the rows where the pixel turns on or off
+// (row -1 and row H count as off).  A counting sort by column puts those
+// transitions in column order, and consecutive on/off pairs are the runs;
+// a run that ends at the bottom of a column and one that starts at the top
+// of the next are joined, as the column-order scan would see them.
 std::string Predictor::encode_rle(const uint8_t* mask, size_t height, size_t width) {
-    std::ostringstream ss;
-    bool in_run = false, first = true;
-    size_t start = 0, len = 0;
-    auto emit = [&] {
-        if (!first) ss << ' ';
-        ss << start << ' ' << len;
-        first = false;
+    const size_t H = height, W = width;
+    if (H == 0 || W == 0) return std::string();
+    std::vector<uint32_t> tcol, trow;  // transitions, in row order
+    std::vector<size_t> first(W + 1, 0);
+    auto add = [&](size_t x, size_t y) {
+        tcol.push_back((uint32_t)x);
+        trow.push_back((uint32_t)y);
+        ++first[x + 1];
     };
-    for (size_t x = 0; x < width; ++x) {
-        for (size_t y = 0; y < height; ++y) {
-            const size_t pos = x * height + y + 1;  // column-major, 1-indexed
-            if (mask[y * width + x]) {
-                if (in_run) {
-                    ++len;
-                } else {
-                    in_run = true;
-                    start = pos;
-                    len = 1;
-                }
-            } else if (in_run) {
-                emit();
-                in_run = false;
+    const size_t W8 = W / 8 * 8;
+    for (size_t y = 0; y <= H; ++y) {
+        const uint8_t* cur = y < H ? mask + y * W : nullptr;
+        const uint8_t* above = y > 0 ? mask + (y - 1) * W : nullptr;
+        size_t x = 0;
+        for (; x < W8; x += 8) {
+            uint64_t a = 0, b = 0;
+            if (cur) std::memcpy(&a, cur + x, 8);
+            if (above) std::memcpy(&b, above + x, 8);
+            for (uint64_t d = nonzero_bytes(a) ^ nonzero_bytes(b); d; d &= d - 1)
+                add(x + (size_t)(__builtin_ctzll(d) >> 3), y);
+        }
+        for (; x < W; ++x)
+            if ((cur && cur[x]) != (above && above[x])) add(x, y);
+    }
+    for (size_t x = 0; x < W; ++x) first[x + 1] += first[x];
+    std::vector<uint32_t> rows(tcol.size());
+    {
+        std::vector<size_t> next(first.begin(), first.end() - 1);
+        for (size_t i = 0; i < tcol.size(); ++i) rows[next[tcol[i]]++] = trow[i];
+    }
+    std::string out;
+    char num[24];
+    auto emit = [&](size_t s, size_t e) {  // run [s, e) of column-order indices
+        if (!out.empty()) out.push_back(' ');
+        out.append(num, std::to_chars(num, num + sizeof num, s + 1).ptr);
+        out.push_back(' ');
+        out.append(num, std::to_chars(num, num + sizeof num, e - s).ptr);
+    };
+    size_t ps = 0, pe = 0;
+    bool pending = false;
+    for (size_t x = 0; x < W; ++x) {
+        for (size_t k = first[x]; k < first[x + 1]; k += 2) {  // on, off
+            const size_t s = x * H + rows[k], e = x * H + rows[k + 1];
+            if (pending && s == pe) {
+                pe = e;
+                continue;
             }
+            if (pending) emit(ps, pe);
+            ps = s;
+            pe = e;
+            pending = true;
         }
     }
-    if (in_run) emit();
-    return ss.str();
+    if (pending) emit(ps, pe);
+    return out;
+}
+
+std::pair<int64_t, int64_t> Predictor::predict_device(const TensorPtr& image, float* probs,
+                                                      uint8_t* mask) {
+    autograd::NoGradGuard guard;
+    model_->eval();
+    TensorPtr logits = model_->forward(image);
+    const int64_t H = logits->dim(-2), W = logits->dim(-1);
+    check(soar_sigmoid_threshold(logits->cuda_data(), probs, mask, (size_t)(H * W), threshold_,
+                                 exec::stream()),
+          "sigmoid threshold");
+    return {H, W};
 }
 
 PredictionResult Predictor::predict(const TensorPtr& image) {

@@ -275,6 +275,33 @@ def test_train_step_graph_replay_matches_eager(sm, wfile):
     me.close()
 
 
+def test_predict_graph_replay_matches_eager(sm, wfile):
+    """soar_predict replays a HIP graph from its second call of a shape and
+    threshold on: the same probabilities, mask and RLE as the uncaptured
+    call, with training steps on the same activation memory in between."""
+    print("case: predict graph vs eager", flush=True)
+    mg = model_with(sm, wfile)
+    me = model_with(sm, wfile)
+    me.set_graph_mode(False)
+    img, mask = sample(31)
+    for k in range(4):
+        thr = 0.5 if k < 3 else 0.4
+        pg, mg_, rg = mg.predict(img, threshold=thr)
+        pe, me_, re_ = me.predict(img, threshold=thr)
+        np.testing.assert_array_equal(pg, pe)
+        np.testing.assert_array_equal(mg_, me_)
+        assert rg == re_
+        if k == 1:
+            mg.train_step(img, mask, lr=1e-3)
+            me.train_step(img, mask, lr=1e-3)
+    probe, _ = sample(32, 40, 48)
+    np.testing.assert_array_equal(mg.predict(probe)[0], me.predict(probe)[0])
+    mode, held = mg.graph_info()
+    assert mode and held >= 1, (mode, held)  # the (64 x 64, 0.5) predict graph
+    mg.close()
+    me.close()
+
+
 def test_predict_matches_oracle(sm, wfile, weights):
     print("case: predict", flush=True)
     img, _ = sample(5)
