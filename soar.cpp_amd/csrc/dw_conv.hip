@@ -230,8 +230,18 @@ __device__ __forceinline__ void dw_wgrad_body(
     const int ix0 = (int)(ox0 * S - pad), hi = (int)Hi, wi = (int)Wi;
     TilePrefetch<K, S, D> pre;
     float gn[kPer];
+    // a thread's 8 dy values: two aligned 16-byte loads when the row is
+    // inside the plane and 16-byte aligned, else element by element
+    const bool dy_vec = Wo % 4 == 0 && (reinterpret_cast<uintptr_t>(gp) & 15) == 0;
     auto fetch_dy = [&](int64_t ty) {
         const int64_t oy = ty * kTH + r, ox = ox0 + c0;
+        if (dy_vec && oy < Ho && ox + kPer <= Wo) {
+            const f4* q = reinterpret_cast<const f4*>(gp + oy * Wo + ox);
+            const f4 a = q[0], b = q[1];
+            gn[0] = a.x, gn[1] = a.y, gn[2] = a.z, gn[3] = a.w;
+            gn[4] = b.x, gn[5] = b.y, gn[6] = b.z, gn[7] = b.w;
+            return;
+        }
 #pragma unroll
         for (int cc = 0; cc < kPer; ++cc)
             gn[cc] = (oy < Ho && ox + cc < Wo) ? gp[oy * Wo + ox + cc] : 0.0f;
