@@ -30,8 +30,9 @@
 //               workgroup per group), src/cuda/ops/normalization_kernels.cu
 //               :12-64 (Welford + Chan, one block per group),
 //               src/nn/layers.cpp:690-710 (double sums).  Here: per-thread
-//               shifted sums, Chan combine in float64 across threads, blocks
-//               and chunks; rstd = 1/sqrt(max(var,0)+eps), biased variance.
+//               shifted sums, combined across threads, blocks and chunks as
+//               float64 sums re-centred on a data value (the Chan combine
+//               unrolled); rstd = 1/sqrt(max(var,0)+eps), biased variance.
 //   apply       shaders/group_norm_affine_silu.comp:33-65,
 //               normalization_kernels.cu:70-91 + activation_kernels.cu:11-49,
 //               layers.cpp:712-721,789-795.  Here (x-mean)*(gamma*rstd)+beta
@@ -71,53 +72,6 @@ __device__ __forceinline__ float dsilu_fast(float g, float z) {
     return g * s * fmaf(z, 1.0f - s, 1.0f);
 }
 
-// ---- float64 moment triples (count, mean, M2) and Chan's combine ------
-
-struct Moments {
-    double n, mean, m2;
-};
-
-__device__ __forceinline__ Moments chan(const Moments& a, const Moments& b) {
-    if (b.n == 0.0) return a;
-    if (a.n == 0.0) return b;
-    Moments r;
-    r.n = a.n + b.n;
-    double f = b.n / r.n;
-    double d = b.mean - a.mean;
-    r.mean = a.mean + d * f;
-    r.m2 = a.m2 + b.m2 + d * d * a.n * f;
-    return r;
-}
-
-// Tree to lane 0 of the wave.  Lanes whose partner is past lane 63 read
-// their own value, but those lanes never feed lane 0.
-__device__ __forceinline__ Moments wave_reduce(Moments m) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        Moments o;
-        o.n = __shfl_down(m.n, off);
-        o.mean = __shfl_down(m.mean, off);
-        o.m2 = __shfl_down(m.m2, off);
-        m = chan(m, o);
-    }
-    return m;
-}
-
-// Result valid in thread 0.  Ends with the block synchronised.
-__device__ __forceinline__ Moments block_reduce(Moments m, Moments* lds) {
-    m = wave_reduce(m);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    if (lane == 0) lds[w] = m;
-    __syncthreads();
-    Moments r = lds[0];
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (int i = 1; i < kWaves; ++i) r = chan(r, lds[i]);
-    }
-    __syncthreads();
-    return r;
-}
-
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll
@@ -147,6 +101,38 @@ __device__ __forceinline__ void block_sum2(T& a, T& b, T* lds /*[2*kWaves]*/) {
         }
     }
     __syncthreads();
+}
+
+// ---- re-centred moment sums (no division per term) -------------------
+// Moments (n_k, mean_k, M2_k) about a common reference R: with
+// d_k = mean_k - R,
+//   S = sum n_k d_k,   Q = sum M2_k + n_k d_k^2,
+// the combined mean is R + S/N and M2 = Q - S^2/N (N = sum n_k).  This is
+// the Chan combine unrolled over all terms, as plain float64 sums in a
+// fixed order; with R a value of the data (one partial's mean) every d_k is
+// of the data's spread, so the final subtraction cancels nothing that
+// matters.
+__device__ __forceinline__ void centred_add(double& S, double& Q, double n, double mean,
+                                            double m2, double R) {
+    const double d = mean - R;
+    const double nd = n * d;
+    S += nd;
+    Q += fma(nd, d, m2);
+}
+
+// (mean, M2) from the sums about R over N elements.
+__device__ __forceinline__ double2 centred_moments(double S, double Q, double N, double R) {
+    const double m = S / N;
+    return make_double2(R + m, fmax(Q - S * m, 0.0));
+}
+
+// Element count of chunk partial j of a unit (partials are plane-major,
+// cpp per plane; only a plane's last chunk can be short).  j < 2^31: the
+// plan keeps every grid below that.
+__device__ __forceinline__ double partial_count(int64_t j, int64_t HW, int64_t chunk,
+                                                int64_t cpp) {
+    const int64_t k = (int64_t)((uint32_t)j % (uint32_t)cpp);
+    return (double)min(chunk, HW - k * chunk);
 }
 
 // Chunk geometry of block `b`: plane index, element offset in the plane
@@ -198,9 +184,9 @@ __device__ __forceinline__ void store1(float* p, float v) {
 // Chunk blocks: each thread shifts its elements by its own first element K
 // (so sums of d = x - K stay near the data's spread even when |mean| >>
 // std), keeps fp32 sums of d and d*d in four independent lanes of
-// accumulation, then converts to a float64 (n, mean, M2) triple that is
-// Chan-combined over the block.  part[b] = (mean, M2) of chunk b; its count
-// is implied by the chunk geometry.
+// accumulation, then the block combines them in float64 (re-centred sums,
+// no division per thread).  part[b] = (mean, M2) of chunk b; its count is
+// implied by the chunk geometry.
 //
 // Finish blocks (blockIdx.x < fin_nu): one per unit of the previous batch;
 // combines the unit's cpg*cpp partials in a fixed order and writes mean and
@@ -214,13 +200,16 @@ __device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
                                   float* __restrict__ mean, float* __restrict__ rstd,
                                   float* __restrict__ mean_lo, float* __restrict__ lo_ws,
                                   int64_t HW, int64_t chunk, int64_t cpp, int64_t cpg,
-                                  float eps, Moments* lds) {
+                                  float eps, double* lds /*[2 * kWaves]*/) {
     const int64_t P = cpg * cpp;  // chunk blocks per unit
     const int64_t first = u * P;
-    Moments um{0.0, 0.0, 0.0};
-    // Eight independent loads in flight per thread, then their combine in
-    // index order (a load-combine-load loop would wait a full memory
-    // latency per partial).
+    // Sums about partial 0's mean (centred_add), each thread over partials
+    // j, j + kThreads, ... in order, then the block in a fixed order.
+    const double R = part[first].x;
+    double S = 0.0, Q = 0.0;
+    // Eight independent loads in flight per thread, then their sums in
+    // index order (a load-add-load loop would wait a full memory latency
+    // per partial).
     // (full batches carry no bounds test between the loads: a test per load
     // makes the compiler wait for each one)
     constexpr int kUnroll = 8;
@@ -230,23 +219,21 @@ __device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
 #pragma unroll
         for (int i = 0; i < kUnroll; ++i) v[i] = part[first + j0 + (int64_t)i * kThreads];
 #pragma unroll
-        for (int i = 0; i < kUnroll; ++i) {
-            const int64_t k = (j0 + (int64_t)i * kThreads) % cpp;
-            Moments o{(double)min(chunk, HW - k * chunk), v[i].x, v[i].y};
-            um = chan(um, o);
-        }
+        for (int i = 0; i < kUnroll; ++i)
+            centred_add(S, Q, partial_count(j0 + (int64_t)i * kThreads, HW, chunk, cpp),
+                        v[i].x, v[i].y, R);
     }
     for (; j0 < P; j0 += kThreads) {
         const double2 v = part[first + j0];
-        const int64_t k = j0 % cpp;
-        Moments o{(double)min(chunk, HW - k * chunk), v.x, v.y};
-        um = chan(um, o);
+        centred_add(S, Q, partial_count(j0, HW, chunk, cpp), v.x, v.y, R);
     }
-    Moments ur = block_reduce(um, lds);
+    block_sum2(S, Q, lds);
     if (threadIdx.x == 0) {
-        const double var = ur.n > 0.0 ? fmax(ur.m2 / ur.n, 0.0) : 0.0;
-        const float hi = (float)ur.mean;
-        const float lo = (float)(ur.mean - (double)hi);
+        const double n = (double)(cpg * HW);
+        const double2 mm = centred_moments(S, Q, n, R);
+        const double var = mm.y / n;
+        const float hi = (float)mm.x;
+        const float lo = (float)(mm.x - (double)hi);
         mean[u] = hi;
         rstd[u] = (float)(1.0 / sqrt(var + (double)eps));
         lo_ws[u] = lo;
@@ -265,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void k_stats(
     float* __restrict__ rstd, float* __restrict__ mean_lo, float* __restrict__ lo_ws,
     int64_t HW, int64_t chunk, int64_t cpp, int64_t cpg, int64_t fin_u0, int64_t fin_nu,
     int64_t block0, float eps) {
-    __shared__ Moments lds[kWaves];
+    __shared__ double lds[4 * kWaves];
     if ((int64_t)blockIdx.x < fin_nu) {
         finish_stats_unit(fin_u0 + blockIdx.x, part, mean, rstd, mean_lo, lo_ws, HW, chunk,
                           cpp, cpg, eps, lds);
@@ -341,16 +328,50 @@ __global__ __launch_bounds__(kThreads) void k_stats(
             q0 = fmaf(d0, d0, q0);
         }
     }
-    Moments m{0.0, 0.0, 0.0};
+    // The block's (mean, M2) without a division per thread or per step of
+    // the tree: each thread's sums, about its own K, are re-centred on its
+    // wave's reference Rw (lane 0's K; when lane 0 has no elements, no lane
+    // of the wave has) as S = n d + s, Q = q + d (2 s + n d) with d = K - Rw
+    // (the sums of x - Rw and of its square), the wave adds them, and
+    // thread 0 re-centres the waves' sums on wave 0's reference in wave
+    // order (centred_add's terms with the wave's own S in place of n d).
+    const float Rw = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(K)));
+    double S = 0.0, Q = 0.0;
     if (cnt > 0) {
         const double s = (double)((s0 + s1) + (s2 + s3));
         const double q = (double)((q0 + q1) + (q2 + q3));
-        m.n = (double)cnt;
-        m.mean = (double)K + s / m.n;
-        m.m2 = fmax(q - s * s / m.n, 0.0);
+        const double d = (double)K - (double)Rw;
+        const double nd = (double)cnt * d;
+        S = nd + s;
+        Q = fma(d, 2.0 * s + nd, q);
     }
-    Moments r = block_reduce(m, lds);
-    if (t == 0) part[b] = make_double2(r.mean, r.m2);
+    int n = (int)cnt;
+    n = wave_sum(n);
+    S = wave_sum(S);
+    Q = wave_sum(Q);
+    const int lane = t & 63, w = t >> 6;
+    if (lane == 0) {
+        lds[w] = (double)n;
+        lds[kWaves + w] = S;
+        lds[2 * kWaves + w] = Q;
+        lds[3 * kWaves + w] = (double)Rw;
+    }
+    __syncthreads();
+    if (t == 0) {
+        const double R0 = lds[3 * kWaves];
+        double N = lds[0], S0 = lds[kWaves], Q0 = lds[2 * kWaves];
+#pragma unroll
+        for (int i = 1; i < kWaves; ++i) {
+            const double ni = lds[i], Si = lds[kWaves + i];
+            if (ni == 0.0) continue;
+            const double d = lds[3 * kWaves + i] - R0;
+            const double nd = ni * d;
+            Q0 += fma(d, 2.0 * Si + nd, lds[2 * kWaves + i]);
+            S0 += Si + nd;
+            N += ni;
+        }
+        part[b] = centred_moments(S0, Q0, N, R0);
+    }
 }
 
 // Per-block coefficients of plane `plane`: xhat = fma(x - mu, r, e) with
@@ -384,43 +405,10 @@ __device__ __forceinline__ PlaneCoef plane_coef(
 // second-pass block combines its own unit's partials before its work.
 // All blocks of a unit run the same combine in the same order, so they
 // agree bit for bit.  The statistics also equal finish_stats_unit's: there
-// thread q < P holds partial q alone and the other threads hold empty
-// moments, which chan() passes through, and the waves meet in order.
+// thread q < P holds partial q's terms alone (added to zero), the other
+// threads hold zeros, and the waves are added in order.
 // ======================================================================
 constexpr int64_t kFoldMax = kThreads2;  // partials per unit (one per thread)
-
-struct UnitStats {
-    float hi, r, lo;
-};
-
-__device__ UnitStats fold_unit_stats(int64_t u, const double2* __restrict__ part, int64_t HW,
-                                     int64_t chunk, int64_t cpp, int64_t cpg, float eps) {
-    __shared__ Moments lds[kThreads2 / 64];
-    __shared__ float bc[3];
-    const int64_t P = cpg * cpp;
-    const int q = threadIdx.x;
-    Moments m{0.0, 0.0, 0.0};
-    if (q < P) {
-        const double2 v = part[u * P + q];
-        const int64_t k = q % cpp;
-        m = Moments{(double)min(chunk, HW - k * chunk), v.x, v.y};
-    }
-    m = wave_reduce(m);
-    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        Moments r = lds[0];
-#pragma unroll
-        for (int i = 1; i < kThreads2 / 64; ++i) r = chan(r, lds[i]);
-        const double var = r.n > 0.0 ? fmax(r.m2 / r.n, 0.0) : 0.0;
-        const float hi = (float)r.mean;
-        bc[0] = hi;
-        bc[1] = (float)(1.0 / sqrt(var + (double)eps));
-        bc[2] = (float)(r.mean - (double)hi);
-    }
-    __syncthreads();
-    return UnitStats{bc[0], bc[1], bc[2]};
-}
 
 // Sum of (a, b) over a kThreads2 block in a fixed order (wave trees, then
 // the waves in order), returned to every thread.
@@ -439,6 +427,36 @@ __device__ __forceinline__ double2 fold_block_sum2(double a, double b) {
     __syncthreads();
     return r;
 }
+
+struct UnitStats {
+    float hi, r, lo;
+};
+
+__device__ UnitStats fold_unit_stats(int64_t u, const double2* __restrict__ part, int64_t HW,
+                                     int64_t chunk, int64_t cpp, int64_t cpg, float eps) {
+    __shared__ float bc[3];
+    const int64_t P = cpg * cpp;
+    const int q = threadIdx.x;
+    const double R = part[u * P].x;
+    double S = 0.0, Q = 0.0;
+    if (q < P) {
+        const double2 v = part[u * P + q];
+        centred_add(S, Q, partial_count(q, HW, chunk, cpp), v.x, v.y, R);
+    }
+    const double2 sq = fold_block_sum2(S, Q);
+    if (threadIdx.x == 0) {
+        const double n = (double)(cpg * HW);
+        const double2 mm = centred_moments(sq.x, sq.y, n, R);
+        const double var = mm.y / n;
+        const float hi = (float)mm.x;
+        bc[0] = hi;
+        bc[1] = (float)(1.0 / sqrt(var + (double)eps));
+        bc[2] = (float)(mm.x - (double)hi);
+    }
+    __syncthreads();
+    return UnitStats{bc[0], bc[1], bc[2]};
+}
+
 
 // (S1, S2) of unit u from its backward partials: thread q < P adds
 // gamma_j * partial q, j = q / cpp the partial's channel.
@@ -1013,22 +1031,6 @@ __global__ __launch_bounds__(NT) void k_small_fwd(
     small_apply_regs<SILU, RES>(xv, y + (u * cpg + (live ? m.j : 0)) * HW, m, gm, bt, hi, r, lo);
 }
 
-// Chan combine over the block, fixed order; valid in thread 0.
-template <int NT>
-__device__ __forceinline__ Moments small_block_moments(Moments v, Moments* lds) {
-    v = wave_reduce(v);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    if (lane == 0) lds[w] = v;
-    __syncthreads();
-    Moments r = lds[0];
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (int i = 1; i < NT / 64; ++i) r = chan(r, lds[i]);
-    }
-    __syncthreads();
-    return r;
-}
-
 // The GroupNorm after a pointwise convolution whose epilogue wrote the
 // chunk partials: the unit's finish (its cpg*cpp partials, combined in a
 // fixed order), then its apply, in one block.
@@ -1039,7 +1041,7 @@ __global__ __launch_bounds__(NT) void k_small_finish_apply(
     float* __restrict__ mean, float* __restrict__ rstd, float* __restrict__ mean_lo,
     float* __restrict__ lo_ws, int64_t G, int64_t cpg, int64_t HW, int64_t chunk, int64_t cpp,
     int lg, float eps) {
-    __shared__ Moments ldsm[NT / 64];
+    __shared__ double2 ldsq[NT / 64];
     __shared__ float bc[3];
     const int64_t u = blockIdx.x;
     const SmallMap m = small_map(lg, cpg, HW);
@@ -1047,17 +1049,28 @@ __global__ __launch_bounds__(NT) void k_small_finish_apply(
     float xv[kSmallPer];  // loads in flight while the partials combine
     small_load(x + u * cpg * HW, cpg * HW, HW, m, xv);
     const int64_t P = cpg * cpp;
-    Moments um{0.0, 0.0, 0.0};
+    // sums about partial 0's mean (centred_add), threads then waves in order
+    const double R = part[u * P].x;
+    double S = 0.0, Q = 0.0;
     for (int64_t q = threadIdx.x; q < P; q += NT) {
         const double2 v = part[u * P + q];
-        const int64_t k = q % cpp;
-        um = chan(um, Moments{(double)min(chunk, HW - k * chunk), v.x, v.y});
+        centred_add(S, Q, partial_count(q, HW, chunk, cpp), v.x, v.y, R);
     }
-    const Moments ur = small_block_moments<NT>(um, ldsm);
+    S = wave_sum(S);
+    Q = wave_sum(Q);
+    if ((threadIdx.x & 63) == 0) ldsq[threadIdx.x >> 6] = make_double2(S, Q);
+    __syncthreads();
     if (threadIdx.x == 0) {
-        const double var = ur.n > 0.0 ? fmax(ur.m2 / ur.n, 0.0) : 0.0;
-        const float hi = (float)ur.mean;
-        const float lo = (float)(ur.mean - (double)hi);
+#pragma unroll
+        for (int i = 1; i < NT / 64; ++i) {
+            S += ldsq[i].x;
+            Q += ldsq[i].y;
+        }
+        const double n = (double)(cpg * HW);
+        const double2 mm = centred_moments(S, Q, n, R);
+        const double var = mm.y / n;
+        const float hi = (float)mm.x;
+        const float lo = (float)(mm.x - (double)hi);
         const float r = (float)(1.0 / sqrt(var + (double)eps));
         mean[u] = hi;
         rstd[u] = r;
