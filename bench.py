@@ -49,9 +49,10 @@ CONFIGS = {
     # CBA block with a pointwise conv (64 -> 64 channels) feeding config 3's
     # GroupNorm+SiLU; C is C_out, the conv's C_in is CBA_C_IN
     "cba_pw": (1, 64, 2048 * 2048, 16, "fwdbwd", False, 1),
+    "cba_pw_unfused": (1, 64, 2048 * 2048, 16, "fwdbwd", False, 1),
 }
 SEED_OF = {"cfg2_fwd": SEED + 2, "cfg3": SEED + 3, "cfg4_chain": SEED + 4, "cfg5": SEED + 5,
-           "cba_pw": SEED + 6}
+           "cba_pw": SEED + 6, "cba_pw_unfused": SEED + 6}
 CBA_C_IN = 64
 PEAK_MFMA_F32 = 157.3  # TFLOP/s, dense fp32 matrix
 
@@ -187,13 +188,15 @@ class Step:
 class CBAStep:
     """Forward and backward of a CBA block whose conv is pointwise:
     z = conv1x1(x), y = SiLU(GroupNorm(z)) with the GroupNorm statistics in
-    the conv epilogue (soar_pw_conv_gn_silu_forward); backward
-    soar_gn_silu_backward (dy -> dz, dgamma, dbeta) then
-    soar_pw_conv_backward (dz -> dx, dW)."""
+    the conv epilogue (soar_pw_conv_gn_silu_forward).  Backward, fused
+    (cba_pw): soar_pw_cba_backward, the GroupNorm reduction over (z, dy) and
+    then one kernel that forms dz in registers and computes dx and dW from
+    it.  Unfused (cba_pw_unfused): soar_gn_silu_backward (dy -> dz, dgamma,
+    dbeta) then soar_pw_conv_backward (dz -> dx, dW)."""
 
-    def __init__(self, gn, N, C, HW, G, seed):
+    def __init__(self, gn, N, C, HW, G, seed, fused=True):
         import torch
-        self.gn, self.G = gn, G
+        self.gn, self.G, self.fused = gn, G, fused
         self.C_in, self.C_out, self.N, self.HW = CBA_C_IN, C, N, HW
         self.x = torch.empty((N, self.C_in, HW), device="cuda")
         gn.synth_normal(self.x, seed, 1, 0.0, 1.0)
@@ -218,27 +221,37 @@ class CBAStep:
         self.dgamma = torch.zeros(C, device="cuda")
         self.dbeta = torch.zeros(C, device="cuda")
         self.ws_gn = gn.workspace(N, C, HW, G)
-        self.ws_bwd = torch.empty(gn.pw_conv_backward_workspace_bytes(N, self.C_in, C, HW),
-                                  dtype=torch.uint8, device="cuda")
+        if fused:
+            self.ws_bwd = torch.empty(gn.pw_cba_backward_workspace_bytes(N, self.C_in, C, HW, G),
+                                      dtype=torch.uint8, device="cuda")
+        else:
+            self.ws_bwd = torch.empty(gn.pw_conv_backward_workspace_bytes(N, self.C_in, C, HW),
+                                      dtype=torch.uint8, device="cuda")
         self.params = [None]
         self.T = N * C * HW * 4
 
     def algorithmic_bytes(self):
         # fwd: conv reads x, writes z; apply reads z, writes y.
-        # bwd: GN reduce reads dy, z; GN dx reads dy, z, writes dz; conv dx
-        # reads dz, writes dx; conv dW reads dz, x.  (Weights are noise.)
+        # bwd fused: GN reduce reads dy, z; the fused kernel reads dy, z, x
+        # and writes dx.  Unfused: GN reduce reads dy, z; GN dx reads dy, z,
+        # writes dz; conv dx reads dz, writes dx; conv dW reads dz, x.
+        # (Weights are noise.)
         ti, to = self.C_in, self.C_out
-        return (ti + 3 * to + 7 * to + 2 * ti) * self.N * self.HW * 4
+        bwd = 4 * to + 2 * ti if self.fused else 7 * to + 2 * ti
+        return (ti + 3 * to + bwd) * self.N * self.HW * 4
 
     def kernel_bytes(self, name):
         nb = self.N * self.HW * 4
         ti, to = self.C_in * nb, self.C_out * nb
         return {"pw_conv_gn_stats": ti + to, "gn_silu_apply": 2 * to,
                 "gn_silu_bwd_reduce": 2 * to, "gn_silu_bwd_dx": 3 * to,
-                "pw_conv_dgrad": to + ti, "pw_conv_wgrad": to + ti}.get(name, 0)
+                "pw_conv_dgrad": to + ti, "pw_conv_wgrad": to + ti,
+                "pw_cba_bwd": 2 * to + 2 * ti}.get(name, 0)
 
     def kernel_flops(self, name):
         f = 2 * self.C_in * self.C_out * self.N * self.HW
+        if name == "pw_cba_bwd":
+            return 2 * f  # dx and dW
         return f if name in ("pw_conv_gn_stats", "pw_conv_dgrad", "pw_conv_wgrad") else 0
 
     def __call__(self):
@@ -246,8 +259,13 @@ class CBAStep:
         gn.pw_conv_gn_silu_forward(self.x, self.w, None, self.gamma, self.beta, self.G,
                                    eps=1e-5, z=self.z, y=self.y, mean=self.mean, rstd=self.rstd,
                                    mean_lo=self.mean_lo, ws=self.ws)
-        gn.gn_silu_backward(self.dy, self.z, self.gamma, self.beta,
-                            (self.mean, self.rstd, self.mean_lo), self.G, dx=self.dz,
+        st = gn.Stats(self.mean, self.rstd, self.mean_lo)
+        if self.fused:
+            gn.pw_cba_backward(self.dy, self.z, self.x, self.w, self.gamma, self.beta, st, self.G,
+                               dx=self.dx, dweight=self.dw, dgamma=self.dgamma,
+                               dbeta=self.dbeta, ws=self.ws_bwd)
+            return
+        gn.gn_silu_backward(self.dy, self.z, self.gamma, self.beta, st, self.G, dx=self.dz,
                             dgamma=self.dgamma, dbeta=self.dbeta, ws=self.ws_gn)
         gn.pw_conv_backward(self.dz, self.x, self.w, dx=self.dx, dweight=self.dw, want_db=False,
                             ws=self.ws_bwd)
@@ -587,9 +605,9 @@ def main():
 
     if args.config in DW_CONFIGS:
         step = DwStep(gn, args.config, SEED + 7)
-    elif args.config == "cba_pw":
+    elif args.config in ("cba_pw", "cba_pw_unfused"):
         N, C, HW, G, passes, residual, blocks = CONFIGS[args.config]
-        step = CBAStep(gn, N, C, HW, G, SEED_OF[args.config])
+        step = CBAStep(gn, N, C, HW, G, SEED_OF[args.config], fused=args.config == "cba_pw")
     else:
         N, C, HW, G, passes, residual, blocks = CONFIGS[args.config]
         step = Step(gn, N, C, HW, G, passes, residual, blocks, SEED_OF[args.config])
@@ -686,11 +704,16 @@ def main():
                             "cfg4_chain": "6 x (x + SiLU(GN(x))) fwd+bwd, BASELINE config 4",
                             "cfg5": "GroupNorm+SiLU fwd+bwd shape of BASELINE config 5",
                             "cba_pw": "CBA fwd+bwd: pointwise conv 64->64 + GN + SiLU, GN "
-                                      "stats in the conv epilogue, config 3 GroupNorm shape"}
+                                      "stats in the conv epilogue, fused backward (dz in "
+                                      "registers), config 3 GroupNorm shape",
+                            "cba_pw_unfused": "CBA fwd+bwd: pointwise conv 64->64 + GN + SiLU, "
+                                              "GN stats in the conv epilogue, backward as GN "
+                                              "backward then conv backward, config 3 GroupNorm "
+                                              "shape"}
                [args.config],
                "N": N, "C": C, "H": int(HW ** 0.5), "W": int(HW ** 0.5), "G": G,
                "eps": 1e-5, "blocks": blocks, "residual": residual,
-               **({"C_in": CBA_C_IN} if args.config == "cba_pw" else {}),
+               **({"C_in": CBA_C_IN} if args.config.startswith("cba_pw") else {}),
                "algorithmic_bytes_per_step": alg}
     out = {
         "metric": METRIC if args.config == "cfg3" else f"{args.config} achieved HBM GB/s",

@@ -278,6 +278,39 @@ SOAR_API int soar_conv2d_1x1_backward(const float* grad_out, const float* in,
                                       size_t C_in, size_t C_out, size_t HW,
                                       void* stream);
 
+/* Bytes of workspace soar_pw_cba_backward needs for this shape (0 for an
+ * invalid or empty shape).  It assumes 16-byte aligned dy, z, x and dx. */
+SOAR_API size_t soar_pw_cba_backward_workspace_bytes(int64_t N, int64_t C_in,
+                                                     int64_t C_out, int64_t HW,
+                                                     int64_t G);
+
+/* Backward of a pointwise CBA block whose forward was
+ * soar_pw_conv_gn_silu_forward(x, weight, NULL, gamma, beta, z, y, mean,
+ * rstd, mean_lo, ...): with dz the GroupNorm(+SiLU) input gradient at z,
+ *   dx      = W^T dz  [N][C_in][HW]; written, or added with
+ *                     SOAR_GN_ACCUMULATE_DX; NULL skips it
+ *   dweight += sum_n dz x^T  [C_out][C_in]; NULL skips it
+ *   dgamma  += sum dz_gn * xhat, dbeta += sum dz_gn  [C_out]; each nullable
+ * the same as soar_gn_silu_backward(dy, z, ..., dz, dgamma, dbeta) followed
+ * by soar_pw_conv_backward(dz, x, weight, dx, dweight, NULL).  With
+ * C_in, C_out <= 64, HW % 4 == 0 and at least SOAR_TUNE_PW_CBA_MIN samples
+ * x pixels, one matrix-core kernel forms dz from z and dy in registers and
+ * computes dx and the weight-gradient partials from it, so dz never
+ * reaches HBM: z, dy and x are read once and dx written once after the
+ * GroupNorm reduction pass.  Other shapes (or unaligned tensors with a
+ * workspace large enough for it) run the two calls above with dz in the
+ * workspace.  Flags: SOAR_GN_SILU, SOAR_GN_ACCUMULATE_DX.
+ * Replaces: CBA backward as the autograd engine runs it, SiLUNode::backward
+ * (src/nn/layers.cpp:749-771) + GroupNormNode::backward (:502-618) +
+ * Conv2dNode::backward (:34-85) for CBA::forward (src/nn/blocks.cpp:442-445)
+ * with a 1x1 convolution. */
+SOAR_API int soar_pw_cba_backward(
+    const float* dy, const float* z, const float* x, const float* weight,
+    const float* gamma, const float* beta, const float* mean, const float* rstd,
+    const float* mean_lo, float* dx, float* dweight, float* dgamma, float* dbeta,
+    int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t G,
+    unsigned flags, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- depthwise convolution (groups = C_in = C_out) ------------------- */
 /* The K x K depthwise convolutions of CBA blocks: Down.dw (k3, stride 2),
  * LKR.dw (k5, k7), the Ctx branches (k3, dilation 1/3/5)
@@ -431,6 +464,14 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
                                   /* sizes its pixel chunks for (at least */
                                   /* 64 pixels each): 256..2^20, default  */
                                   /* 2048; changes its workspace size     */
+#define SOAR_TUNE_PW_CBA_MIN 16 /* pointwise CBA backward: the fused    */
+                                /* kernel runs from this many samples x  */
+                                /* pixels on (0 = never); default 2^17;  */
+                                /* changes its workspace size            */
+#define SOAR_TUNE_PW_CBA_BLOCKS 17 /* blocks the fused CBA backward sizes */
+                                   /* its pixel chunks for: 64..2^20,    */
+                                   /* default 256; changes its workspace  */
+                                   /* size                                */
 SOAR_API int soar_gn_tune(int key, int64_t value);
 SOAR_API int64_t soar_gn_tune_get(int key);
 

@@ -701,6 +701,132 @@ SOAR_API int soar_conv2d_1x1_backward(const float* grad_out, const float* in, co
 // ---- depthwise convolution -----------------------------------------------------
 
 
+}  // extern "C"
+
+namespace {
+
+inline size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Workspace of soar_pw_cba_backward.  Fused: the GroupNorm workspace, then
+// the weight-gradient block partials.  Unfused: dz, then the GroupNorm
+// workspace, then the convolution backward's.
+struct CbaLayout {
+    bool fused = false;
+    Plan gp;
+    soar::gn::PwCbaPlan cp;
+    size_t gn_bytes = 0, dz_bytes = 0, pw_bytes = 0, fused_bytes = 0, unfused_bytes = 0;
+};
+
+bool cba_layout(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t G, const Tuning& t,
+                CbaLayout* L) {
+    if (!soar::gn::make_plan(N, C_out, HW, G, t, &L->gp)) return false;
+    L->gn_bytes = al256(soar::gn::workspace_bytes(L->gp));
+    L->dz_bytes = al256((size_t)(N * C_out * HW) * sizeof(float));
+    L->pw_bytes = soar_pw_conv_backward_workspace_bytes(N, C_in, C_out, HW);
+    L->unfused_bytes = L->dz_bytes + L->gn_bytes + L->pw_bytes;
+    L->fused = t.pw_cba_min > 0 && N * HW >= t.pw_cba_min &&
+               soar::gn::pw_cba_fused_fits(C_in, C_out, HW);
+    if (L->fused) {
+        L->cp = soar::gn::make_pw_cba_plan(N, C_in, C_out, HW, t.pw_cba_blocks);
+        L->fused = L->cp.blocks <= 0x7fffffff;
+        L->fused_bytes = L->gn_bytes + L->cp.part_bytes;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+SOAR_API size_t soar_pw_cba_backward_workspace_bytes(int64_t N, int64_t C_in, int64_t C_out,
+                                                     int64_t HW, int64_t G) {
+    int64_t ie = 0, oe = 0, elems = 0;
+    if (check_pw_shape(N, C_in, C_out, HW, &ie, &oe) != SOAR_OK ||
+        check_shape(N, C_out, HW, G, &elems) != SOAR_OK || oe == 0 || C_in == 0) {
+        g_err.clear();
+        return 0;
+    }
+    CbaLayout L;
+    if (!cba_layout(N, C_in, C_out, HW, G, current_tuning(), &L)) return 0;
+    return L.fused ? L.fused_bytes : L.unfused_bytes;
+}
+
+SOAR_API int soar_pw_cba_backward(const float* dy, const float* z, const float* x,
+                                  const float* weight, const float* gamma, const float* beta,
+                                  const float* mean, const float* rstd, const float* mean_lo,
+                                  float* dx, float* dweight, float* dgamma, float* dbeta,
+                                  int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t G,
+                                  unsigned flags, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+    int64_t ie = 0, oe = 0, elems = 0;
+    int rc = check_pw_shape(N, C_in, C_out, HW, &ie, &oe);
+    if (rc) return rc;
+    if ((rc = check_shape(N, C_out, HW, G, &elems))) return rc;
+    if (flags & ~(SOAR_GN_SILU | SOAR_GN_ACCUMULATE_DX))
+        return fail(SOAR_EINVAL,
+                    "unsupported flags 0x%x (SOAR_GN_SILU, SOAR_GN_ACCUMULATE_DX)", flags);
+    if (oe == 0 || (!dx && !dweight && !dgamma && !dbeta)) return ok();
+    if (C_in == 0) return fail(SOAR_EINVAL, "C_in must be positive");
+    if ((rc = require_device())) return rc;
+    const Tuning t = current_tuning();
+    CbaLayout L;
+    if (!cba_layout(N, C_in, C_out, HW, G, t, &L))
+        return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool aligned = aligned16(dy) && aligned16(z) && aligned16(x) && aligned16(dx);
+    if (L.fused && aligned && (dx || dweight)) {
+        const size_t sb = (size_t)(N * G) * sizeof(float), cb = (size_t)C_out * sizeof(float);
+        const size_t wb = (size_t)(C_in * C_out) * sizeof(float);
+        if ((rc = check_dev(dy, (size_t)oe * 4, "dy")) || (rc = check_dev(z, (size_t)oe * 4, "z")) ||
+            (rc = check_dev(x, (size_t)ie * 4, "x")) || (rc = check_dev(weight, wb, "weight")) ||
+            (rc = check_dev(mean, sb, "mean")) || (rc = check_dev(rstd, sb, "rstd")) ||
+            (rc = check_dev_opt(mean_lo, sb, "mean_lo")) ||
+            (rc = check_dev_opt(gamma, cb, "gamma")) || (rc = check_dev_opt(beta, cb, "beta")) ||
+            (rc = check_dev_opt(dx, (size_t)ie * 4, "dx")) ||
+            (rc = check_dev_opt(dweight, wb, "dweight")) ||
+            (rc = check_dev_opt(dgamma, cb, "dgamma")) || (rc = check_dev_opt(dbeta, cb, "dbeta")))
+            return rc;
+        if (workspace_bytes < L.fused_bytes)
+            return fail(SOAR_EINVAL,
+                        "workspace of %zu bytes is smaller than the %zu this shape needs",
+                        workspace_bytes, L.fused_bytes);
+        if ((rc = check_dev(workspace, L.fused_bytes, "workspace"))) return rc;
+        Plan gp = L.gp;
+        gp.vec4 = gp.vec4 && aligned16(z) && aligned16(dy);
+        const unsigned gflags = flags & SOAR_GN_SILU;
+        soar::gn::BwdArgs a{dy, z, gamma, beta, mean, rstd, mean_lo, nullptr, dgamma, dbeta,
+                            gflags, workspace};
+        soar::gn::BwdSums sums{};
+        hipError_t e = soar::gn::launch_backward_sums(gp, a, s, &sums);
+        if (e != hipSuccess) return hip_fail(e, "GroupNorm backward reduction launch");
+        float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + L.gn_bytes);
+        soar::gn::PwCbaArgs ca{dy,     z,         x,      weight,          gamma,
+                               beta,   mean,      rstd,   sums.mean_lo,    sums.unit_sums,
+                               sums.plane_sums, dgamma, dbeta, dx,         dweight,
+                               part};
+        e = soar::gn::launch_pw_cba_backward(L.cp, ca, N, C_in, C_out, HW, G, gflags != 0,
+                                             (flags & SOAR_GN_ACCUMULATE_DX) != 0, s);
+        if (e != hipSuccess) return hip_fail(e, "fused CBA backward launch");
+        return ok();
+    }
+    // the GroupNorm backward into dz (in the workspace), then the
+    // convolution backward
+    if (workspace_bytes < L.unfused_bytes)
+        return fail(SOAR_EINVAL,
+                    "workspace of %zu bytes is smaller than the %zu this call needs (%s)",
+                    workspace_bytes, L.unfused_bytes,
+                    L.fused ? "tensors not 16-byte aligned run the unfused path" : "unfused path");
+    char* ws = static_cast<char*>(workspace);
+    float* dz = (dx || dweight) ? reinterpret_cast<float*>(ws) : nullptr;
+    rc = soar_gn_silu_backward(dy, z, gamma, beta, mean, rstd, mean_lo, dz, dgamma, dbeta, N,
+                               C_out, HW, G, flags & SOAR_GN_SILU, ws + L.dz_bytes, L.gn_bytes,
+                               stream);
+    if (rc || !dz) return rc;
+    return soar_pw_conv_backward(dz, x, weight, dx, dweight, nullptr, N, C_in, C_out, HW,
+                                 flags & SOAR_GN_ACCUMULATE_DX, ws + L.dz_bytes + L.gn_bytes,
+                                 L.pw_bytes, stream);
+}
+
 SOAR_API int soar_dw_conv_forward(const float* x, const float* weight, const float* bias,
                                   float* y, int64_t N, int64_t C, int64_t H_in, int64_t W_in,
                                   int64_t H_out, int64_t W_out, int64_t K, int64_t pad,
@@ -1131,6 +1257,16 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
                 return fail(SOAR_EINVAL, "pw_wg_target must be in [256, 2^20]");
             g_tune.pw_wg_target = value;
             return ok();
+        case SOAR_TUNE_PW_CBA_MIN:
+            if (value < 0 || value > ((int64_t)1 << 40))
+                return fail(SOAR_EINVAL, "pw_cba_min must be in [0, 2^40]");
+            g_tune.pw_cba_min = value;
+            return ok();
+        case SOAR_TUNE_PW_CBA_BLOCKS:
+            if (value < 64 || value > (1 << 20))
+                return fail(SOAR_EINVAL, "pw_cba_blocks must be in [64, 2^20]");
+            g_tune.pw_cba_blocks = value;
+            return ok();
         default:
             return fail(SOAR_EINVAL, "unknown tuning key %d", key);
     }
@@ -1154,6 +1290,8 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
         case SOAR_TUNE_LOADS: return g_tune.loads;
         case SOAR_TUNE_PW_WG_WAVES: return g_tune.pw_wg_waves;
         case SOAR_TUNE_PW_WG_TARGET: return g_tune.pw_wg_target;
+        case SOAR_TUNE_PW_CBA_MIN: return g_tune.pw_cba_min;
+        case SOAR_TUNE_PW_CBA_BLOCKS: return g_tune.pw_cba_blocks;
         default: return -1;
     }
 }

@@ -7,18 +7,13 @@
 // All are one streaming pass; blocks walk the tensor with a grid stride in
 // 128-bit steps when every pointer is 16-byte aligned, else element-wise.
 #include "gn_internal.hpp"
+#include "gn_math.hpp"
 
 namespace soar {
 namespace gn {
 namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
-
-constexpr float kLog2e = 1.4426950408889634f;
-
-__device__ __forceinline__ float sigmoid_fast(float z) {
-    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * kLog2e));
-}
 
 struct SiluFwd {
     __device__ float operator()(float v) const { return v * sigmoid_fast(v); }

@@ -78,6 +78,13 @@ struct Tuning {
                                  // that add their tiles before writing one
                                  // partial (1, 2, 4 or 8)
     int64_t pw_wg_target = 2048;  // and the waves its pixel chunks aim for
+    int64_t pw_cba_min = (int64_t)1 << 17;  // pointwise CBA backward: samples x
+                                            // pixels from which the fused kernel
+                                            // runs (0: never)
+    int64_t pw_cba_blocks = 256;  // and the blocks its pixel chunks aim for
+                                  // (one per CU: at 64 -> 64 channels over
+                                  // 2048^2 pixels 1.03 ms, 1.13 at 512,
+                                  // 1.19 at 1024)
 };
 
 constexpr int kThreads = 256;   // first passes (stats, reduction)
@@ -120,6 +127,20 @@ hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a,
                           hipStream_t s);
 hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a,
                            hipStream_t s);
+
+// True when the backward of this plan runs the one-launch small-unit kernel.
+bool backward_is_small(const Plan& p, const Tuning& t);
+// The backward's reduction and its finish over every unit (one batch), no
+// dx pass: leaves per-plane (sum dz, sum dz xhat) and per-unit (S1, S2) in
+// the workspace for a fused consumer.  mean_lo is the residual the dx
+// arithmetic must use (the workspace's recovered one when the caller saved
+// none and there is no SiLU).
+struct BwdSums {
+    const double2* plane_sums;  // [N * C]
+    const double2* unit_sums;   // [N * G]
+    const float* mean_lo;       // [N * G], nullable
+};
+hipError_t launch_backward_sums(const Plan& p, const BwdArgs& a, hipStream_t s, BwdSums* out);
 
 // GroupNorm forward whose chunk partials are already in the workspace (the
 // pointwise convolution wrote them): the finish, then the apply, over all
@@ -212,6 +233,41 @@ size_t pw_bwd_workspace_bytes(const PwBwdPlan& p);
 hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N, int64_t C_in,
                               int64_t C_out, int64_t HW, bool accumulate_dx, int64_t small,
                               hipStream_t s);
+
+// Fused backward of a pointwise CBA block (pw_conv.hip): from the
+// GroupNorm input z, the upstream gradient dy and the convolution input x,
+// dx (=, or += with accumulate_dx) W^T dz and dw += sum dz x^T with dz the
+// GroupNorm(+SiLU) input gradient, never stored.  C_in, C_out <= 64, HW % 4
+// == 0, 16-byte aligned tensors (pw_cba_fused_fits).  The GroupNorm sums
+// come from launch_backward_sums; block 0 also adds dgamma / dbeta.
+struct PwCbaArgs {
+    const float* dy;  // [N][C_out][HW]
+    const float* z;   // [N][C_out][HW], the GroupNorm input
+    const float* x;   // [N][C_in][HW], the convolution input
+    const float* w;   // [C_out][C_in]
+    const float* gamma;
+    const float* beta;
+    const float* mean;
+    const float* rstd;
+    const float* mean_lo;
+    const double2* unit_sums;
+    const double2* plane_sums;
+    float* dgamma;  // nullable
+    float* dbeta;   // nullable
+    float* dx;      // nullable
+    float* dw;      // nullable
+    float* part_w;  // [blocks][C_out][C_in] workspace (with dw)
+};
+struct PwCbaPlan {
+    int64_t chunk = 0, cpp = 0, blocks = 0;  // pixels per block, per plane, all
+    size_t part_bytes = 0;                   // dW partials
+};
+bool pw_cba_fused_fits(int64_t C_in, int64_t C_out, int64_t HW);
+// About `target` blocks of 4 waves (a chunk of at least 128 pixels).
+PwCbaPlan make_pw_cba_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t target);
+hipError_t launch_pw_cba_backward(const PwCbaPlan& p, const PwCbaArgs& a, int64_t N,
+                                  int64_t C_in, int64_t C_out, int64_t HW, int64_t G, bool silu,
+                                  bool accumulate_dx, hipStream_t s);
 
 // Depthwise convolution (dw_conv.hip): groups = C_in = C_out, weights
 // [C][K][K], output size given by the caller, taps outside the input skipped.

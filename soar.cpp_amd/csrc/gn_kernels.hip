@@ -47,6 +47,7 @@
 #include <type_traits>
 
 #include "gn_internal.hpp"
+#include "gn_math.hpp"
 #include "soar_gn.h"
 
 namespace soar {
@@ -55,22 +56,7 @@ namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWaves = kThreads / 64;
-
-// sigmoid(z) = 1/(1+exp(-z)) with the hardware 2^x (v_exp_f32) and
-// reciprocal (v_rcp_f32).  exp overflow to +inf gives 0, underflow gives 1.
-__device__ __forceinline__ float sigmoid_fast(float z) {
-    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * kLog2e));
-}
-
-__device__ __forceinline__ float silu_fast(float z) { return z * sigmoid_fast(z); }
-
-// Gradient at the SiLU input: g * s * (1 + z*(1-s)), s = sigmoid(z).
-__device__ __forceinline__ float dsilu_fast(float g, float z) {
-    float s = sigmoid_fast(z);
-    return g * s * fmaf(z, 1.0f - s, 1.0f);
-}
 
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
@@ -1617,6 +1603,18 @@ bool make_pw_plan(int64_t N, int64_t C_out, int64_t HW, int64_t G, const Tuning&
 
 // Same orders as the forward with R = reduction, D = dx, then the
 // dgamma/dbeta finish over all planes.
+bool backward_is_small(const Plan& p, const Tuning& t) { return small_bwd(p, t); }
+
+hipError_t launch_backward_sums(const Plan& p, const BwdArgs& a, hipStream_t s, BwdSums* out) {
+    const WsView w = ws_view(p, a.ws);
+    launch_reduce(p, a, w, 0, 0, 0, p.units, s);
+    launch_reduce(p, a, w, 0, p.units, 0, 0, s);
+    out->plane_sums = w.plane_sums;
+    out->unit_sums = w.unit_sums;
+    out->mean_lo = recover_lo(a) ? w.lo : a.mean_lo;
+    return hipGetLastError();
+}
+
 hipError_t launch_backward(const Plan& p, const Tuning& t, const BwdArgs& a, hipStream_t s) {
     const WsView w = ws_view(p, a.ws);
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;

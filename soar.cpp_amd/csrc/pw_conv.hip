@@ -36,6 +36,7 @@
 #include <type_traits>
 
 #include "gn_internal.hpp"
+#include "gn_math.hpp"
 #include "soar_gn.h"
 
 namespace soar {
@@ -714,6 +715,252 @@ __global__ __launch_bounds__(64 * WPB, 2) void k_pw_wgrad(
                 if (co < C_out) part_b[gb * C_out + co] = t;
             }
         }
+    }
+}
+
+// ======================================================================
+// Fused backward of a pointwise CBA block (1x1 convolution without bias,
+// then GroupNorm, then optionally SiLU; blocks.cpp:429-445).  From the
+// GroupNorm input z, the upstream gradient dy and the convolution input x
+// one pass computes
+//   dz = A_c dzs + D_u xhat + B_u   k_bwd_dx's arithmetic, dzs = dy or
+//                                   dy silu'(gamma xhat + beta)
+//   dx = W^T dz                     the convolution's input gradient
+//   dW partial = sum dz x^T         one fp32 partial tile per block
+// so dz is never written to HBM and read back: four tensor passes (z, dy
+// and x in, dx out) instead of seven (GroupNorm dx 3, dgrad 2, wgrad 2).
+// C_in, C_out <= 64 (one dW tile); the GroupNorm reduction and its finish
+// run first and leave the per-unit S1 / S2 in unit_sums.
+//
+// Block = kFbWaves waves, one per SIMD, on one pixel chunk of one sample;
+// wave w takes the 32-pixel steps at chunk start + 32 (w + kFbWaves s).
+// Per step the wave loads z and dy (rows < 32 TM) and x (rows < 32 TN)
+// with row-contiguous 16-byte loads (k_pw_wgrad's slots) through buffer
+// descriptors bounded to the sample's planes (rows past C_out / C_in read
+// zeros), forms dz in registers from per-channel coefficients in LDS, and
+// stages the dz and x rows in its own LDS area (k_pw_wgrad's layout; no
+// barrier in the loop).  Then
+//   dW: k_pw_wgrad's MFMAs, A = dz rows, B = x rows, K = the 32 pixels;
+//   dx: C[ci][p] = sum_co W[co][ci] dz[co][p], A = W^T from registers
+//       (lane (h, j) holds W[2s + h][32 t + j], zero for co >= C_out),
+//       B = dz[2s + h][pixel j] read from LDS, K = the C_out channels, so
+//       lane (h, j) ends with pixel j of rows tile_row(t, r, h), stored as
+//       128-byte row pieces.
+// The next step's loads are in flight during the MFMAs.  At the end the
+// waves add their dW tiles through LDS in wave order and the block writes
+// one partial for k_sum_partials.  Block 0 also adds dgamma / dbeta from
+// the plane sums, in k_param_finish's order.
+// ======================================================================
+constexpr int kFbWaves = 4;
+// Cache policy of the buffer accesses: non-temporal (each byte is touched
+// once; at 64 -> 64 channels over 2048^2 pixels 1065 -> 1033 us).
+constexpr int kNt = 2;
+
+template <bool SILU, int TM, int TN, bool ACC>
+__global__ __launch_bounds__(64 * kFbWaves, 1) void k_pw_cba_bwd(
+    const float* __restrict__ dy, const float* __restrict__ z, const float* __restrict__ x,
+    const float* __restrict__ w, const float* __restrict__ gamma,
+    const float* __restrict__ beta, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ mean_lo,
+    const double2* __restrict__ unit_sums, const double2* __restrict__ plane_sums,
+    float* __restrict__ dgamma, float* __restrict__ dbeta, float* __restrict__ dx,
+    float* __restrict__ part_w, int64_t C_in, int64_t C_out, int64_t HW, int64_t G,
+    int64_t N, int64_t chunk, int64_t cpp) {
+    constexpr int kZr = 32 * TM, kXr = 32 * TN;      // staged dz rows, x rows
+    constexpr int kStage = (kZr + kXr) * kWgStride;  // floats of one wave's staging
+    constexpr int kR = 16 * TM * TN;                 // dW accumulators per lane
+    static_assert(kR * 64 <= kStage, "reduction layout");
+    __shared__ __attribute__((aligned(16))) float lds_all[kFbWaves * kStage];
+    __shared__ __attribute__((aligned(16))) float coef[64 * 8];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    float* __restrict__ lds = lds_all + wv * kStage;
+    const int h = lane >> 5, j = lane & 31;
+    const int64_t n = (int64_t)blockIdx.x / cpp, kc = (int64_t)blockIdx.x - n * cpp;
+    const int64_t cpg = C_out / G;
+
+    // Channel c's coefficients for sample n, as k_bwd_dx forms them:
+    // mu, r, e, gamma, beta, A = gamma r, B = -r S1 / M, D = -r S2 / M
+    // (zeros past C_out: those rows get dz = 0).
+    if (threadIdx.x < 64) {
+        const int c = threadIdx.x;
+        f4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
+        if (c < C_out) {
+            const int64_t u = n * G + c / cpg;
+            const float mu = mean[u], r = rstd[u];
+            const float e = mean_lo ? -mean_lo[u] * r : 0.0f;
+            const float gm = gamma ? gamma[c] : 1.0f, bt = beta ? beta[c] : 0.0f;
+            const double2 S = unit_sums[u];
+            const double Md = (double)(cpg * HW);
+            lo = f4{mu, r, e, gm};
+            hi = f4{bt, gm * r, (float)(-(double)r * S.x / Md), (float)(-(double)r * S.y / Md)};
+        }
+        *reinterpret_cast<f4*>(&coef[8 * c]) = lo;
+        *reinterpret_cast<f4*>(&coef[8 * c + 4]) = hi;
+    }
+    if (blockIdx.x == 0 && (int64_t)threadIdx.x < C_out && (dgamma || dbeta)) {
+        // k_param_finish for channel c: the same sums in sample order
+        const int64_t c = threadIdx.x;
+        double sa = 0.0, sb = 0.0;
+        for (int64_t s = 0; s < N; ++s) {
+            const double2 v = plane_sums[s * C_out + c];
+            sa += v.x;
+            sb += v.y;
+        }
+        if (dbeta) dbeta[c] = (float)((double)dbeta[c] + sa);
+        if (dgamma) dgamma[c] = (float)((double)dgamma[c] + sb);
+    }
+
+    // W^T operand of dx: k-step s, half h -> channel co = 2s + h
+    float wt[TN][16 * TM];
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int s = 0; s < 16 * TM; ++s) {
+            const int64_t co = 2 * s + h, ci = 32 * t + j;
+            wt[t][s] = (co < C_out && ci < C_in) ? w[co * C_in + ci] : 0.0f;
+        }
+    __syncthreads();
+
+    // staging slots (k_pw_wgrad's): slot sl of lane l covers row 8 sl + l/8,
+    // pixels 4 (l % 8) .. +3 of the step
+    const int srow = lane >> 3, scol = 4 * (lane & 7);
+    const auto rz = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(z + n * C_out * HW),
+                                                      (short)0, (int)(C_out * HW * 4), kRsrcWord3);
+    const auto rg = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(dy + n * C_out * HW),
+                                                      (short)0, (int)(C_out * HW * 4), kRsrcWord3);
+    const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x + n * C_in * HW),
+                                                      (short)0, (int)(C_in * HW * 4), kRsrcWord3);
+    const bool want_dx = dx != nullptr, want_dw = part_w != nullptr;  // wave-uniform
+    const auto ro = __builtin_amdgcn_make_buffer_rsrc(want_dx ? dx + n * C_in * HW : dx, (short)0,
+                                                      (int)(C_in * HW * 4), kRsrcWord3);
+    const uint32_t hw4 = (uint32_t)HW * 4u, row8 = 8u * hw4;
+    f4 sz[4 * TM], sg[4 * TM], sx[4 * TN];
+    auto gload = [&](int64_t p) {
+        // lanes past the plane read its last 16 bytes (zeroed below)
+        const uint32_t q = (uint32_t)min<int64_t>(p + scol, HW - 4);
+        const uint32_t vo = (uint32_t)srow * hw4 + 4u * q;
+#pragma unroll
+        for (int sl = 0; sl < 4 * TM; ++sl) {
+            sz[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rz, vo, sl * row8, kNt));
+            sg[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rg, vo, sl * row8, kNt));
+        }
+#pragma unroll
+        for (int sl = 0; sl < 4 * TN; ++sl)
+            sx[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rx, vo, sl * row8, kNt));
+    };
+
+    f16 accw[TM][TN], accx[TN];
+#pragma unroll
+    for (int mt = 0; mt < TM; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) accw[mt][nt][r] = 0.0f;
+
+    const int64_t pend = min(kc * chunk + chunk, HW);
+    const int64_t px0 = kc * chunk + kWgStep * wv;
+    constexpr int64_t kStride = (int64_t)kWgStep * kFbWaves;
+    gload(px0);
+    for (int64_t p = px0; p < pend; p += kStride) {
+        const bool live = p + scol < pend;  // all four pixels or none (HW % 4 == 0)
+#pragma unroll
+        for (int sl = 0; sl < 4 * TM; ++sl) {
+            const int co = 8 * sl + srow;
+            const f4 c0 = *reinterpret_cast<const f4*>(&coef[8 * co]);
+            const f4 c1 = *reinterpret_cast<const f4*>(&coef[8 * co + 4]);
+            f4 o;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float xh = fmaf(sz[sl][t] - c0[0], c0[1], c0[2]);
+                const float dzs = SILU ? dsilu_fast(sg[sl][t], fmaf(c0[3], xh, c1[0])) : sg[sl][t];
+                o[t] = live ? fmaf(c1[1], dzs, fmaf(c1[3], xh, c1[2])) : 0.0f;
+            }
+            *reinterpret_cast<f4*>(&lds[(8 * sl + srow) * kWgStride + scol]) = o;
+        }
+#pragma unroll
+        for (int sl = 0; sl < 4 * TN; ++sl) {
+            const f4 v = live ? sx[sl] : f4{0.f, 0.f, 0.f, 0.f};
+            *reinterpret_cast<f4*>(&lds[(kZr + 8 * sl + srow) * kWgStride + scol]) = v;
+        }
+        // the next step's loads (the last step reloads itself: no branch)
+        gload(p + kStride < pend ? p + kStride : p);
+        __builtin_amdgcn_sched_group_barrier(0x200, 4 * (TM + TN), 0);  // the LDS writes
+        __builtin_amdgcn_sched_group_barrier(0x020, 8 * TM + 4 * TN, 0);  // the global loads
+
+        // dW += dz x^T over the step's 32 pixels
+        if (want_dw) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f4 A[TM], B[TN];
+#pragma unroll
+                for (int t = 0; t < TM; ++t)
+                    A[t] = *reinterpret_cast<const f4*>(&lds[(32 * t + j) * kWgStride + 16 * h + 4 * i]);
+#pragma unroll
+                for (int t = 0; t < TN; ++t)
+                    B[t] = *reinterpret_cast<const f4*>(
+                        &lds[(kZr + 32 * t + j) * kWgStride + 16 * h + 4 * i]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int mt = 0; mt < TM; ++mt)
+#pragma unroll
+                        for (int nt = 0; nt < TN; ++nt)
+                            accw[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(A[mt][q], B[nt][q],
+                                                                                accw[mt][nt], 0, 0, 0);
+            }
+        }
+        if (!want_dx) continue;
+        // dx = W^T dz for the step's 32 pixels
+#pragma unroll
+        for (int t = 0; t < TN; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) accx[t][r] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 16 * TM; ++s) {
+            const float b = lds[(2 * s + h) * kWgStride + j];
+#pragma unroll
+            for (int t = 0; t < TN; ++t)
+                accx[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(wt[t][s], b, accx[t], 0, 0, 0);
+        }
+        if (p + j < pend) {
+            // rows past C_in fall outside the descriptor and are dropped
+            const uint32_t vo = (uint32_t)(4 * h) * hw4 + 4u * (uint32_t)(p + j);
+#pragma unroll
+            for (int t = 0; t < TN; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t so = (uint32_t)tile_row(t, r, 0) * hw4;
+                    float v = accx[t][r];
+                    if (ACC)
+                        v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, vo, so, 0));
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), ro, vo, so, kNt);
+                }
+        }
+    }
+
+    if (!want_dw) return;
+    // the waves' dW tiles added in wave order (k_pw_wgrad's reduction)
+    __syncthreads();  // every wave is done with its staging area
+    float* __restrict__ red = lds_all;
+#pragma unroll
+    for (int mt = 0; mt < TM; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                red[(wv * kR + (mt * TN + nt) * 16 + r) * 64 + lane] = accw[mt][nt][r];
+    __syncthreads();
+    constexpr int kShare = kR / kFbWaves;
+#pragma unroll
+    for (int kk = 0; kk < kShare; ++kk) {
+        const int k = wv * kShare + kk;
+        float t = red[k * 64 + lane];
+#pragma unroll
+        for (int v = 1; v < kFbWaves; ++v) t += red[(v * kR + k) * 64 + lane];
+        const int mt = k / (16 * TN), nt = (k / 16) % TN, r = k % 16;
+        const int64_t co = tile_row(mt, r, h), ci = 32 * nt + j;
+        if (co < C_out && ci < C_in) part_w[((int64_t)blockIdx.x * C_out + co) * C_in + ci] = t;
     }
 }
 
@@ -1406,6 +1653,55 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
         const int64_t nbw = a.dw ? (E + 63) / 64 : 0, nbb = a.db ? (C_out + 63) / 64 : 0;
         k_sum_partials<<<dim3((unsigned)(nbw + nbb)), 1024, 0, s>>>(part_w, a.dw, E, nbw, part_b,
                                                                     a.db, C_out, p.Gb);
+        prof_end(s, tok);
+    }
+    return hipGetLastError();
+}
+
+bool pw_cba_fused_fits(int64_t C_in, int64_t C_out, int64_t HW) {
+    // one dW tile; in-sample byte offsets (64 rows of HW floats) in 31 bits
+    return C_in >= 1 && C_in <= 64 && C_out >= 1 && C_out <= 64 && HW >= 4 && HW % 4 == 0 &&
+           HW <= ((int64_t)1 << 31) / 256 - 64;
+}
+
+PwCbaPlan make_pw_cba_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t target) {
+    PwCbaPlan p;
+    constexpr int64_t kStep = (int64_t)kWgStep * kFbWaves;  // pixels per block step
+    const int64_t per = (N * HW + std::max<int64_t>(target, 1) - 1) / std::max<int64_t>(target, 1);
+    int64_t chunk = (per + kStep - 1) / kStep * kStep;
+    chunk = std::max(chunk, kStep);
+    p.chunk = std::min(chunk, (HW + kStep - 1) / kStep * kStep);
+    p.cpp = (HW + p.chunk - 1) / p.chunk;
+    p.blocks = N * p.cpp;
+    p.part_bytes = ((size_t)p.blocks * (size_t)(C_out * C_in) * sizeof(float) + 255) & ~(size_t)255;
+    return p;
+}
+
+hipError_t launch_pw_cba_backward(const PwCbaPlan& p, const PwCbaArgs& a, int64_t N,
+                                  int64_t C_in, int64_t C_out, int64_t HW, int64_t G, bool silu,
+                                  bool accumulate_dx, hipStream_t s) {
+    if (N == 0 || HW == 0) return hipSuccess;
+    const int tm = C_out <= 32 ? 1 : 2, tn = C_in <= 32 ? 1 : 2;
+    float* part = a.dw ? a.part_w : nullptr;
+    int tok = prof_begin(s, "pw_cba_bwd");
+    auto go = [&](auto S, auto M2, auto N2, auto A) {
+        k_pw_cba_bwd<S(), M2() ? 2 : 1, N2() ? 2 : 1, A()>
+            <<<dim3((unsigned)p.blocks), 64 * kFbWaves, 0, s>>>(
+                a.dy, a.z, a.x, a.w, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, a.unit_sums,
+                a.plane_sums, a.dgamma, a.dbeta, a.dx, part, C_in, C_out, HW, G, N, p.chunk,
+                p.cpp);
+    };
+    bsel(silu, [&](auto S) {
+        bsel(tm == 2, [&](auto M2) {
+            bsel(tn == 2, [&](auto N2) { bsel(accumulate_dx, [&](auto A) { go(S, M2, N2, A); }); });
+        });
+    });
+    prof_end(s, tok);
+    if (a.dw) {
+        tok = prof_begin(s, "pw_cba_wgrad_finish");
+        const int64_t E = C_out * C_in;
+        k_sum_partials<<<dim3((unsigned)((E + 63) / 64)), 1024, 0, s>>>(
+            part, a.dw, E, (E + 63) / 64, nullptr, nullptr, 0, p.blocks);
         prof_end(s, tok);
     }
     return hipGetLastError();

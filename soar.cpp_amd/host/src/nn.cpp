@@ -270,9 +270,10 @@ struct Conv2dNode : autograd::AutogradNode {
     void release_variables() override { input = nullptr; }
 };
 
-// Backward of the fused pointwise CBA: GroupNorm(+SiLU) on the saved conv
-// output z gives dz (and dgamma, dbeta), then the conv backward gives dx
-// and dW.
+// Backward of the fused pointwise CBA: the GroupNorm(+SiLU) backward at the
+// saved conv output z and the conv backward in one call
+// (soar_pw_cba_backward: above its size switch one kernel forms dz in
+// registers and never stores it).
 struct CBAPointwiseNode : autograd::AutogradNode {
     TensorPtr input, conv_w, gamma, beta, z, mean, rstd, mean_lo;
     ConvGeom g{};
@@ -293,31 +294,22 @@ struct CBAPointwiseNode : autograd::AutogradNode {
         if (!want_x && !want_w && !want_p) return;
         if (!go->is_cuda()) go->to_cuda();
         const int64_t HW = g.H * g.W;
-        TensorPtr dz = (want_x || want_w) ? Tensor::create(z->shape(), false, true) : nullptr;
-        bool g_direct = false, b_direct = false;
+        bool g_direct = false, b_direct = false, w_direct = false, fresh = false;
         TensorPtr dg = want_p ? param_grad_target(gamma, &g_direct) : nullptr;
         TensorPtr db = want_p ? param_grad_target(beta, &b_direct) : nullptr;
-        const size_t gwsb = soar_gn_workspace_bytes(g.N, g.C_out, HW, G);
-        check(soar_gn_silu_backward(go->cuda_data(), z->cuda_data(), dptr(gamma), dptr(beta),
-                                    mean->cuda_data(), rstd->cuda_data(), dptr(mean_lo),
-                                    dz ? dz->cuda_data() : nullptr,
-                                    dg ? dg->cuda_data() : nullptr,
-                                    db ? db->cuda_data() : nullptr, g.N, g.C_out, HW, G, flags,
-                                    workspace(gwsb), gwsb, exec::stream()),
-              "CBA GroupNorm backward");
-        TensorPtr gx, gw;
-        bool w_direct = false, fresh = false;
-        if (dz) {
-            gx = want_x ? write_target(input, &fresh) : nullptr;
-            gw = want_w ? param_grad_target(conv_w, &w_direct) : nullptr;
-            const size_t wsb = soar_pw_conv_backward_workspace_bytes(g.N, g.C_in, g.C_out, HW);
-            check(soar_pw_conv_backward(dz->cuda_data(), input->cuda_data(), conv_w->cuda_data(),
-                                        gx ? gx->cuda_data() : nullptr,
-                                        gw ? gw->cuda_data() : nullptr, nullptr, g.N, g.C_in,
-                                        g.C_out, HW, dx_mode(gx, fresh), workspace(wsb), wsb,
-                                        exec::stream()),
-                  "CBA convolution backward");
-        }
+        TensorPtr gx = want_x ? write_target(input, &fresh) : nullptr;
+        TensorPtr gw = want_w ? param_grad_target(conv_w, &w_direct) : nullptr;
+        const size_t wsb = soar_pw_cba_backward_workspace_bytes(g.N, g.C_in, g.C_out, HW, G);
+        check(soar_pw_cba_backward(go->cuda_data(), z->cuda_data(), input->cuda_data(),
+                                   conv_w->cuda_data(), dptr(gamma), dptr(beta),
+                                   mean->cuda_data(), rstd->cuda_data(), dptr(mean_lo),
+                                   gx ? gx->cuda_data() : nullptr,
+                                   gw ? gw->cuda_data() : nullptr,
+                                   dg ? dg->cuda_data() : nullptr,
+                                   db ? db->cuda_data() : nullptr, g.N, g.C_in, g.C_out, HW, G,
+                                   (flags & SOAR_GN_SILU) | dx_mode(gx, fresh), workspace(wsb),
+                                   wsb, exec::stream()),
+              "CBA backward");
         if (dg && !g_direct) propagate_grad(gamma, std::move(dg));
         if (db && !b_direct) propagate_grad(beta, std::move(db));
         if (gw && !w_direct) propagate_grad(conv_w, std::move(gw));

@@ -54,6 +54,8 @@ TUNE_PW_SPLITK = 12
 TUNE_LOADS = 13
 TUNE_PW_WG_WAVES = 14
 TUNE_PW_WG_TARGET = 15
+TUNE_PW_CBA_MIN = 16
+TUNE_PW_CBA_BLOCKS = 17
 
 
 class SoarUnavailable(RuntimeError):
@@ -105,6 +107,8 @@ SIGNATURES = {
     "soar_pw_conv_backward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                          _c.c_uint, _P, _SZ, _P]),
     "soar_conv2d_1x1_backward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _P]),
+    "soar_pw_cba_backward_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "soar_pw_cba_backward": (_c.c_int, [_P] * 13 + [_I64] * 5 + [_c.c_uint, _P, _SZ, _P]),
     "soar_dw_conv_forward": (_c.c_int, [_P, _P, _P, _P] + [_I64] * 10 + [_P]),
     "soar_dw_conv_backward_workspace_bytes": (_SZ, [_I64] * 9),
     "soar_dw_conv_backward": (_c.c_int, [_P] * 6 + [_I64] * 10 + [_c.c_uint, _P, _SZ, _P]),
@@ -489,6 +493,52 @@ def pw_conv_backward(dz, x, weight, dx=None, dweight=None, dbias=None, want_dx=T
         _ptr(dweight) if want_dw else None, _ptr(dbias) if want_db else None, N, C_in, C_out,
         HW, GN_ACCUMULATE_DX if accumulate_dx else 0, _ptr(ws), ws.numel(), _stream(stream)))
     return (dx if want_dx else None, dweight if want_dw else None, dbias if want_db else None)
+
+
+def pw_cba_backward_workspace_bytes(N, C_in, C_out, HW, G) -> int:
+    return int(lib().soar_pw_cba_backward_workspace_bytes(N, C_in, C_out, HW, G))
+
+
+def pw_cba_backward(dy, z, x, weight, gamma, beta, stats, G, silu=True, dx=None, dweight=None,
+                    dgamma=None, dbeta=None, want_dx=True, want_dw=True, want_params=True,
+                    accumulate_dx=False, ws=None, stream=None):
+    """Backward of a pointwise CBA block through soar_pw_cba_backward.
+
+    z, stats: what pw_conv_gn_silu_forward returned; dy: the gradient at y.
+    Returns (dx, dweight, dgamma, dbeta).  dweight/dgamma/dbeta accumulate
+    (fresh zeros when not given); dx is written, or added to with
+    accumulate_dx."""
+    import torch
+    N, C_out, HW = _nchw(z)
+    w = weight.reshape(weight.shape[0], -1)
+    C_in = w.shape[1]
+    for t, n in ((dy, "dy"), (z, "z"), (x, "x"), (w, "weight"), (gamma, "gamma"),
+                 (beta, "beta"), (dx, "dx"), (dweight, "dweight"), (dgamma, "dgamma"),
+                 (dbeta, "dbeta")):
+        _check_tensor(t, n)
+    dev = z.device
+    if want_dx and dx is None:
+        shape = (N, C_in) + tuple(z.shape[2:])
+        dx = (torch.zeros if accumulate_dx else torch.empty)(shape, dtype=torch.float32,
+                                                             device=dev)
+    if want_dw and dweight is None:
+        dweight = torch.zeros((C_out, C_in), dtype=torch.float32, device=dev)
+    if want_params and dgamma is None:
+        dgamma = torch.zeros(C_out, dtype=torch.float32, device=dev)
+    if want_params and dbeta is None:
+        dbeta = torch.zeros(C_out, dtype=torch.float32, device=dev)
+    if ws is None:
+        ws = torch.empty(max(pw_cba_backward_workspace_bytes(N, C_in, C_out, HW, G), 1),
+                         dtype=torch.uint8, device=dev)
+    flags = (GN_SILU if silu else 0) | (GN_ACCUMULATE_DX if accumulate_dx else 0)
+    check(lib().soar_pw_cba_backward(
+        _ptr(dy), _ptr(z), _ptr(x), _ptr(w), _ptr(gamma), _ptr(beta), _ptr(stats.mean),
+        _ptr(stats.rstd), _ptr(stats.mean_lo), _ptr(dx) if want_dx else None,
+        _ptr(dweight) if want_dw else None, _ptr(dgamma) if want_params else None,
+        _ptr(dbeta) if want_params else None, N, C_in, C_out, HW, G, flags, _ptr(ws),
+        ws.numel(), _stream(stream)))
+    return (dx if want_dx else None, dweight if want_dw else None,
+            dgamma if want_params else None, dbeta if want_params else None)
 
 
 # ---- depthwise convolution -------------------------------------------------------

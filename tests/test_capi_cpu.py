@@ -288,3 +288,56 @@ def test_fold_max_tuning(L):
     soar_gn.tune(soar_gn.TUNE_FOLD_MAX, 0)
     assert soar_gn.tune_get(soar_gn.TUNE_FOLD_MAX) == 0
     soar_gn.tune(soar_gn.TUNE_FOLD_MAX, old)
+
+
+def _cba(L, N, C_in, C_out, HW, G, flags=1, ws_bytes=0):
+    """soar_pw_cba_backward with NULL tensors (validation runs first)."""
+    P = [None] * 13
+    P[9] = 1  # a non-NULL dx, so the call is not a no-op (never dereferenced)
+    return L.soar_pw_cba_backward(*P, N, C_in, C_out, HW, G, flags, None, ws_bytes, None)
+
+
+def test_pw_cba_backward_workspace_and_tuning(L):
+    assert soar_gn.tune_get(soar_gn.TUNE_PW_CBA_MIN) == 1 << 17
+    assert soar_gn.tune_get(soar_gn.TUNE_PW_CBA_BLOCKS) == 256
+    gn = soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16)
+    # fused: the GroupNorm workspace (256-aligned), then 256 block partials
+    # of the 64 x 64 weight gradient
+    assert soar_gn.pw_cba_backward_workspace_bytes(1, 64, 64, 2048 * 2048, 16) == (
+        (gn + 255) // 256 * 256 + 256 * 64 * 64 * 4)
+    # below the size limit, or more than 64 channels: dz, the GroupNorm
+    # workspace and the convolution backward's
+    small = soar_gn.pw_cba_backward_workspace_bytes(1, 64, 64, 4096, 16)
+    assert small >= 64 * 4096 * 4 + soar_gn.pw_conv_backward_workspace_bytes(1, 64, 64, 4096)
+    wide = soar_gn.pw_cba_backward_workspace_bytes(1, 64, 128, 1 << 18, 16)
+    assert wide >= 128 * (1 << 18) * 4
+    for bad in (-1, (1 << 40) + 1):
+        assert L.soar_gn_tune(soar_gn.TUNE_PW_CBA_MIN, bad) == soar_gn.SOAR_EINVAL
+    for bad in (63, (1 << 20) + 1):
+        assert L.soar_gn_tune(soar_gn.TUNE_PW_CBA_BLOCKS, bad) == soar_gn.SOAR_EINVAL
+    try:
+        soar_gn.tune(soar_gn.TUNE_PW_CBA_BLOCKS, 1024)
+        assert soar_gn.pw_cba_backward_workspace_bytes(1, 64, 64, 2048 * 2048, 16) == (
+            (gn + 255) // 256 * 256 + 1024 * 64 * 64 * 4)
+        soar_gn.tune(soar_gn.TUNE_PW_CBA_MIN, 0)  # never fused
+        assert soar_gn.pw_cba_backward_workspace_bytes(1, 64, 64, 2048 * 2048, 16) > (
+            64 * 2048 * 2048 * 4)
+    finally:
+        soar_gn.tune(soar_gn.TUNE_PW_CBA_BLOCKS, 256)
+        soar_gn.tune(soar_gn.TUNE_PW_CBA_MIN, 1 << 17)
+    assert soar_gn.pw_cba_backward_workspace_bytes(1, 64, 6, 4096, 4) == 0  # C_out % G
+    assert soar_gn.pw_cba_backward_workspace_bytes(0, 64, 64, 4096, 4) == 0
+
+
+def test_pw_cba_backward_validation_without_gpu(L):
+    assert _cba(L, 1, 8, 6, 16, 4) == soar_gn.SOAR_EINVAL
+    assert "divisible" in soar_gn.last_error()
+    assert _cba(L, 1, 8, 6, 16, 3, flags=2) == soar_gn.SOAR_EINVAL  # no residual here
+    assert "flags" in soar_gn.last_error()
+    assert _cba(L, -1, 8, 6, 16, 3) == soar_gn.SOAR_EINVAL
+    assert _cba(L, 1, 0, 6, 16, 3) == soar_gn.SOAR_EINVAL
+    assert _cba(L, 1, 8, 6, 1 << 28, 3) == soar_gn.SOAR_EINVAL  # 32-bit offsets
+    assert _cba(L, 0, 8, 6, 16, 3) == soar_gn.SOAR_OK  # empty
+    assert _cba(L, 1, 8, 6, 0, 3) == soar_gn.SOAR_OK
+    P = [None] * 13  # nothing requested
+    assert L.soar_pw_cba_backward(*P, 1, 8, 6, 16, 3, 1, None, 0, None) == soar_gn.SOAR_OK
