@@ -466,7 +466,7 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
                                   /* 2048; changes its workspace size     */
 #define SOAR_TUNE_PW_CBA_MIN 16 /* pointwise CBA backward: the fused    */
                                 /* kernel runs from this many samples x  */
-                                /* pixels on (0 = never); default 2^17;  */
+                                /* pixels on (0 = never); default 2^14;  */
                                 /* changes its workspace size            */
 #define SOAR_TUNE_PW_CBA_BLOCKS 17 /* blocks the fused CBA backward sizes */
                                    /* its pixel chunks for: 64..2^20,    */

@@ -78,9 +78,12 @@ struct Tuning {
                                  // that add their tiles before writing one
                                  // partial (1, 2, 4 or 8)
     int64_t pw_wg_target = 2048;  // and the waves its pixel chunks aim for
-    int64_t pw_cba_min = (int64_t)1 << 17;  // pointwise CBA backward: samples x
-                                            // pixels from which the fused kernel
-                                            // runs (0: never)
+    int64_t pw_cba_min = 16384;  // pointwise CBA backward: samples x pixels
+                                 // from which the fused kernel runs (0:
+                                 // never); Nano train step with graphs at
+                                 // 2^14 / 2^16 / 2^17 / never: 512^2 2.73 /
+                                 // 2.92 / 2.90 / 2.96 ms, 1024^2 4.34 /
+                                 // 4.36 / 4.45 / 4.54 ms
     int64_t pw_cba_blocks = 256;  // and the blocks its pixel chunks aim for
                                   // (one per CU: at 64 -> 64 channels over
                                   // 2048^2 pixels 1.03 ms, 1.13 at 512,

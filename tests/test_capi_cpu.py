@@ -298,7 +298,7 @@ def _cba(L, N, C_in, C_out, HW, G, flags=1, ws_bytes=0):
 
 
 def test_pw_cba_backward_workspace_and_tuning(L):
-    assert soar_gn.tune_get(soar_gn.TUNE_PW_CBA_MIN) == 1 << 17
+    assert soar_gn.tune_get(soar_gn.TUNE_PW_CBA_MIN) == 1 << 14
     assert soar_gn.tune_get(soar_gn.TUNE_PW_CBA_BLOCKS) == 256
     gn = soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16)
     # fused: the GroupNorm workspace (256-aligned), then 256 block partials
@@ -309,6 +309,8 @@ def test_pw_cba_backward_workspace_and_tuning(L):
     # workspace and the convolution backward's
     small = soar_gn.pw_cba_backward_workspace_bytes(1, 64, 64, 4096, 16)
     assert small >= 64 * 4096 * 4 + soar_gn.pw_conv_backward_workspace_bytes(1, 64, 64, 4096)
+    # HW not a multiple of 4 as well
+    assert soar_gn.pw_cba_backward_workspace_bytes(1, 64, 64, 65538, 16) >= 64 * 65538 * 4
     wide = soar_gn.pw_cba_backward_workspace_bytes(1, 64, 128, 1 << 18, 16)
     assert wide >= 128 * (1 << 18) * 4
     for bad in (-1, (1 << 40) + 1):
@@ -324,7 +326,7 @@ def test_pw_cba_backward_workspace_and_tuning(L):
             64 * 2048 * 2048 * 4)
     finally:
         soar_gn.tune(soar_gn.TUNE_PW_CBA_BLOCKS, 256)
-        soar_gn.tune(soar_gn.TUNE_PW_CBA_MIN, 1 << 17)
+        soar_gn.tune(soar_gn.TUNE_PW_CBA_MIN, 1 << 14)
     assert soar_gn.pw_cba_backward_workspace_bytes(1, 64, 6, 4096, 4) == 0  # C_out % G
     assert soar_gn.pw_cba_backward_workspace_bytes(0, 64, 64, 4096, 4) == 0
 
