@@ -65,25 +65,26 @@ __device__ __forceinline__ T wave_sum(T v) {
     return v;
 }
 
-// Sum of (a, b) over the block in a fixed order; valid in thread 0.  Ends
-// with the block synchronised.
-template <typename T>
-__device__ __forceinline__ void block_sum2(T& a, T& b, T* lds /*[2*kWaves]*/) {
+// Sum of (a, b) over a block of NT threads in a fixed order; valid in
+// thread 0.  Ends with the block synchronised.
+template <typename T, int NT = kThreads>
+__device__ __forceinline__ void block_sum2(T& a, T& b, T* lds /*[2 * NT / 64]*/) {
+    constexpr int W = NT / 64;
     a = wave_sum(a);
     b = wave_sum(b);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     if (lane == 0) {
         lds[w] = a;
-        lds[kWaves + w] = b;
+        lds[W + w] = b;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         a = lds[0];
-        b = lds[kWaves];
+        b = lds[W];
 #pragma unroll
-        for (int i = 1; i < kWaves; ++i) {
+        for (int i = 1; i < W; ++i) {
             a += lds[i];
-            b += lds[kWaves + i];
+            b += lds[W + i];
         }
     }
     __syncthreads();
@@ -182,15 +183,16 @@ __device__ __forceinline__ void store1(float* p, float v) {
 // output tolerance.  lo goes to the caller's optional mean_lo (for the
 // backward) and to the workspace (for the apply kernel of the same call).
 // ======================================================================
+template <int NT = kThreads>
 __device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
                                   float* __restrict__ mean, float* __restrict__ rstd,
                                   float* __restrict__ mean_lo, float* __restrict__ lo_ws,
                                   int64_t HW, int64_t chunk, int64_t cpp, int64_t cpg,
-                                  float eps, double* lds /*[2 * kWaves]*/) {
+                                  float eps, double* lds /*[2 * NT / 64]*/) {
     const int64_t P = cpg * cpp;  // chunk blocks per unit
     const int64_t first = u * P;
     // Sums about partial 0's mean (centred_add), each thread over partials
-    // j, j + kThreads, ... in order, then the block in a fixed order.
+    // j, j + NT, ... in order, then the block in a fixed order.
     const double R = part[first].x;
     double S = 0.0, Q = 0.0;
     // Eight independent loads in flight per thread, then their sums in
@@ -200,20 +202,20 @@ __device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
     // makes the compiler wait for each one)
     constexpr int kUnroll = 8;
     int64_t j0 = threadIdx.x;
-    for (; j0 + (kUnroll - 1) * kThreads < P; j0 += kUnroll * kThreads) {
+    for (; j0 + (kUnroll - 1) * NT < P; j0 += kUnroll * NT) {
         double2 v[kUnroll];
 #pragma unroll
-        for (int i = 0; i < kUnroll; ++i) v[i] = part[first + j0 + (int64_t)i * kThreads];
+        for (int i = 0; i < kUnroll; ++i) v[i] = part[first + j0 + (int64_t)i * NT];
 #pragma unroll
         for (int i = 0; i < kUnroll; ++i)
-            centred_add(S, Q, partial_count(j0 + (int64_t)i * kThreads, HW, chunk, cpp),
+            centred_add(S, Q, partial_count(j0 + (int64_t)i * NT, HW, chunk, cpp),
                         v[i].x, v[i].y, R);
     }
-    for (; j0 < P; j0 += kThreads) {
+    for (; j0 < P; j0 += NT) {
         const double2 v = part[first + j0];
         centred_add(S, Q, partial_count(j0, HW, chunk, cpp), v.x, v.y, R);
     }
-    block_sum2(S, Q, lds);
+    block_sum2<double, NT>(S, Q, lds);
     if (threadIdx.x == 0) {
         const double n = (double)(cpg * HW);
         const double2 mm = centred_moments(S, Q, n, R);
@@ -225,6 +227,22 @@ __device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
         lo_ws[u] = lo;
         if (mean_lo) mean_lo[u] = lo;
     }
+}
+
+// Finish-only grid for units of many chunk partials (a pointwise
+// convolution's epilogue writes one per pixel chunk of each plane: 16384
+// per unit at 4 x 2048^2): 1024 threads per unit instead of 256, so each
+// thread combines a quarter as many.  At 64 -> 64 channels over 2048^2
+// pixels, 16 units: 16.0 -> 8.4 us.
+constexpr int kWideThreads = 1024;
+constexpr int64_t kWideFinish = 8192;  // partials per unit from which it runs
+__global__ __launch_bounds__(kWideThreads) void k_stats_finish_wide(
+    const double2* __restrict__ part, float* __restrict__ mean, float* __restrict__ rstd,
+    float* __restrict__ mean_lo, float* __restrict__ lo_ws, int64_t HW, int64_t chunk,
+    int64_t cpp, int64_t cpg, int64_t fin_u0, float eps) {
+    __shared__ double lds[2 * kWideThreads / 64];
+    finish_stats_unit<kWideThreads>(fin_u0 + blockIdx.x, part, mean, rstd, mean_lo, lo_ws, HW,
+                                    chunk, cpp, cpg, eps, lds);
 }
 
 // U: 128-bit loads in flight per thread.  The thread's first batch is
@@ -1321,6 +1339,13 @@ void launch_stats(const Plan& p, const FwdArgs& a, const WsView& w, int64_t fin_
     const int64_t bpu = p.cpg * p.cpp;
     const dim3 grid((unsigned)(fin_nu + nu * bpu));
     const int tok = prof_begin(s, nu ? "gn_stats_partial" : "gn_stats_finish");
+    if (nu == 0 && bpu >= kWideFinish) {
+        k_stats_finish_wide<<<grid, kWideThreads, 0, s>>>(w.part, a.mean, a.rstd, a.mean_lo, w.lo,
+                                                          p.HW, p.chunk, p.cpp, p.cpg, fin_u0,
+                                                          a.eps);
+        prof_end(s, tok);
+        return;
+    }
     bsel(p.vec4, [&](auto V) {
         loads_sel(p.loads, [&](auto U) {
             k_stats<V(), U()><<<grid, kThreads, 0, s>>>(

@@ -883,8 +883,9 @@ __global__ __launch_bounds__(64 * kFbWaves, 1) void k_pw_cba_bwd(
             const f4 v = live ? sx[sl] : f4{0.f, 0.f, 0.f, 0.f};
             *reinterpret_cast<f4*>(&lds[(kZr + 8 * sl + srow) * kWgStride + scol]) = v;
         }
-        // the next step's loads (the last step reloads itself: no branch)
-        gload(p + kStride < pend ? p + kStride : p);
+        // the next step's loads (a wave-uniform branch: the last step loads
+        // nothing, which saved its reload's 0.6% of the traffic)
+        if (p + kStride < pend) gload(p + kStride);
         __builtin_amdgcn_sched_group_barrier(0x200, 4 * (TM + TN), 0);  // the LDS writes
         __builtin_amdgcn_sched_group_barrier(0x020, 8 * TM + 4 * TN, 0);  // the global loads
 
