@@ -144,3 +144,51 @@ def test_cba_graph_replays(gpu, C_in, C_out, H, K):
     reset()
     g = _capture(step)
     _replay_and_check(g, outs, ref, reset)
+
+
+@pytest.mark.parametrize("C_in,C_out,H", [(64, 64, 256), (32, 48, 128)])
+def test_fused_cba_backward_graph_replays(gpu, C_in, C_out, H):
+    """soar_pw_cba_backward on its fused kernel (the GroupNorm reduction and
+    finish, the fused dz / dx / dW kernel, the weight-gradient finish)
+    captured after the CBA forward."""
+    import torch
+    print(f"graph fused CBA backward C_in={C_in} C_out={C_out} H={H}", flush=True)
+    N, HW, G = 1, H * H, 8
+    assert N * HW >= gpu.tune_get(gpu.TUNE_PW_CBA_MIN)
+    gen = torch.Generator(device="cuda").manual_seed(H + C_out)
+    x = torch.randn((N, C_in, H, H), device="cuda", generator=gen)
+    dy = 1e-2 * torch.randn((N, C_out, H, H), device="cuda", generator=gen)
+    gamma = 0.5 + torch.rand(C_out, device="cuda", generator=gen)
+    beta = 0.1 * torch.randn(C_out, device="cuda", generator=gen)
+    w = torch.randn((C_out, C_in), device="cuda", generator=gen) / C_in ** 0.5
+    z, y = (torch.empty((N, C_out, H, H), device="cuda") for _ in range(2))
+    mean, rstd, lo = (torch.empty(N * G, device="cuda") for _ in range(3))
+    dx = torch.empty_like(x)
+    dw = torch.zeros_like(w)
+    dg, db = torch.zeros(C_out, device="cuda"), torch.zeros(C_out, device="cuda")
+    fws = torch.empty(max(gpu.pw_conv_gn_workspace_bytes(N, C_out, HW, G), 1),
+                      dtype=torch.uint8, device="cuda")
+    bws = torch.empty(max(gpu.pw_cba_backward_workspace_bytes(N, C_in, C_out, HW, G), 1),
+                      dtype=torch.uint8, device="cuda")
+    st = gpu.Stats(mean, rstd, lo)
+
+    def step():
+        gpu.pw_conv_gn_silu_forward(x, w, None, gamma, beta, G, eps=1e-5, z=z, y=y, mean=mean,
+                                    rstd=rstd, mean_lo=lo, ws=fws)
+        gpu.pw_cba_backward(dy, z, x, w, gamma, beta, st, G, dx=dx, dweight=dw, dgamma=dg,
+                            dbeta=db, ws=bws)
+
+    outs = (z, y, mean, rstd, lo, dx, dw, dg, db)
+    step()
+    torch.cuda.synchronize()
+    ref = [t.clone() for t in outs]
+
+    def reset():
+        for t in (z, y, mean, rstd, lo, dx):
+            t.fill_(float("nan"))
+        for t in (dw, dg, db):
+            t.zero_()
+
+    reset()
+    g = _capture(step)
+    _replay_and_check(g, outs, ref, reset)
