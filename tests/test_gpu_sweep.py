@@ -198,3 +198,27 @@ def test_cba_sweep_vs_oracle(gpu, oracle, pw_tuning, case):
         ratio = err / (bnd.reshape(-1) + 1e-30)
         i = int(np.argmax(ratio))
         assert ratio[i] <= 1.0, f"{name} err {err[i]:.3e} > bound {bnd.reshape(-1)[i]:.3e}"
+    # the fused CBA backward (soar_pw_cba_backward; its fused kernel wherever
+    # C_in, C_out <= 64 and HW % 4 == 0, else the two calls above), against
+    # the stand-alone GroupNorm backward's dz on its multi-kernel path, whose
+    # reduction and dx arithmetic the fused kernel shares
+    keys = (gpu.TUNE_PW_CBA_MIN, gpu.TUNE_SMALL_UNIT, gpu.TUNE_FOLD_MAX)
+    old = {k: gpu.tune_get(k) for k in keys}
+    try:
+        gpu.tune(gpu.TUNE_PW_CBA_MIN, 1)
+        gpu.tune(gpu.TUNE_SMALL_UNIT, 0)
+        gpu.tune(gpu.TUNE_FOLD_MAX, 0)
+        dz2, dg2, db2 = gpu.gn_silu_backward(dev(dy), z, gd, bd, st, G, silu=silu)
+        fx, fw, fg, fb = gpu.pw_cba_backward(dev(dy), z, xd, wd, gd, bd, st, G, silu=silu)
+    finally:
+        for k, v in old.items():
+            gpu.tune(k, v)
+    assert np.array_equal(host(fg), host(dg2)) and np.array_equal(host(fb), host(db2))
+    dzh2 = host(dz2)
+    tx, tw, _ = oracle.conv1x1_bwd_f64(dzh2, x, w, N, C_in, C_out, HW, want=("dx", "dw"))
+    bx, bw, _ = bwd_bounds(dzh2, x, w)
+    for got, t, bnd, name in ((fx, tx, bx, "fused dx"), (fw, tw, bw, "fused dw")):
+        err = np.abs(host(got).astype(np.float64).reshape(-1) - t)
+        ratio = err / (bnd.reshape(-1) + 1e-30)
+        i = int(np.argmax(ratio))
+        assert ratio[i] <= 1.0, f"{name} err {err[i]:.3e} > bound {bnd.reshape(-1)[i]:.3e}"
