@@ -351,6 +351,43 @@ SOAR_API int soar_dw_conv_backward(const float* dy, const float* x,
                                    unsigned flags, void* workspace,
                                    size_t workspace_bytes, void* stream);
 
+/* Bytes of workspace soar_dw_cba_backward needs for this shape (0 for an
+ * invalid or empty shape). */
+SOAR_API size_t soar_dw_cba_backward_workspace_bytes(
+    int64_t N, int64_t C, int64_t H_in, int64_t W_in, int64_t H_out,
+    int64_t W_out, int64_t K, int64_t pad, int64_t stride, int64_t dil,
+    int64_t G);
+
+/* Backward of a depthwise CBA block: z = dwconv(x; weight) without bias,
+ * y = silu(GroupNorm_G(z)) (SOAR_GN_SILU) or GroupNorm_G(z); mean, rstd,
+ * mean_lo are the GroupNorm forward's.  With dz the GroupNorm(+SiLU) input
+ * gradient at z:
+ *   dx      = the convolution's input gradient of dz; written, or added
+ *             with SOAR_GN_ACCUMULATE_DX; NULL skips it
+ *   dweight += its weight gradient [C][K][K]; NULL skips it
+ *   dgamma  += sum dz_gn * xhat, dbeta += sum dz_gn  [C]; each nullable
+ * the same as soar_gn_silu_backward(dy, z, ..., dz, dgamma, dbeta) followed
+ * by soar_dw_conv_backward(dz, x, weight, dx, dweight, NULL, ...).  For a
+ * stride-1 convolution with "same" padding, pad = (K-1)*dil/2, a
+ * configuration with a tiled kernel (K = 3, 5, 7; K = 3 with dil 2, 3, 5),
+ * dx requested and at least SOAR_TUNE_DW_CBA_MIN samples x pixels, one
+ * kernel forms dz over each tile and its halo in LDS and computes dx and
+ * the weight-gradient partials from it, so dz never reaches HBM.  Other
+ * calls run the two calls above with dz in the workspace.
+ * Flags: SOAR_GN_SILU, SOAR_GN_ACCUMULATE_DX.
+ * Replaces: CBA backward as the autograd engine runs it, SiLUNode::backward
+ * (src/nn/layers.cpp:749-771) + GroupNormNode::backward (:502-618) +
+ * Conv2dNode::backward (:34-85) for CBA::forward (src/nn/blocks.cpp:442-445)
+ * with a depthwise convolution. */
+SOAR_API int soar_dw_cba_backward(
+    const float* dy, const float* z, const float* x, const float* weight,
+    const float* gamma, const float* beta, const float* mean, const float* rstd,
+    const float* mean_lo, float* dx, float* dweight, float* dgamma, float* dbeta,
+    int64_t N, int64_t C, int64_t H_in, int64_t W_in, int64_t H_out,
+    int64_t W_out, int64_t K, int64_t pad, int64_t stride, int64_t dil,
+    int64_t G, unsigned flags, void* workspace, size_t workspace_bytes,
+    void* stream);
+
 /* Reference signatures, one sample.
  * Replaces: conv2d_dw_forward (cuda_kernels.hpp:64-66,
  * convolution_kernels.cu:138-182), called by Conv2d::forward
@@ -472,6 +509,10 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
                                    /* its pixel chunks for: 64..2^20,    */
                                    /* default 256; changes its workspace  */
                                    /* size                                */
+#define SOAR_TUNE_DW_CBA_MIN 18 /* depthwise CBA backward: the fused    */
+                                /* kernel runs from this many samples x  */
+                                /* pixels on (0 = never); changes its    */
+                                /* workspace size                        */
 SOAR_API int soar_gn_tune(int key, int64_t value);
 SOAR_API int64_t soar_gn_tune_get(int key);
 

@@ -901,6 +901,127 @@ SOAR_API int soar_dw_conv_backward(const float* dy, const float* x, const float*
     return ok();
 }
 
+}  // extern "C"
+
+namespace {
+
+// Workspace of soar_dw_cba_backward.  Fused: the GroupNorm workspace, then
+// the weight-gradient partials.  Unfused: dz, then the GroupNorm
+// workspace, then the depthwise backward's.
+struct DwCbaLayout {
+    bool fused = false;
+    Plan gp;
+    size_t gn_bytes = 0, dz_bytes = 0, dw_bytes = 0, fused_bytes = 0, unfused_bytes = 0;
+};
+
+bool dw_cba_layout(const soar::gn::DwShape& sh, int64_t G, const Tuning& t, DwCbaLayout* L) {
+    const int64_t HWo = sh.Ho * sh.Wo;
+    if (!soar::gn::make_plan(sh.N, sh.C, HWo, G, t, &L->gp)) return false;
+    L->gn_bytes = al256(soar::gn::workspace_bytes(L->gp));
+    L->dz_bytes = al256((size_t)(sh.N * sh.C * HWo) * sizeof(float));
+    L->dw_bytes = al256(soar::gn::dw_bwd_workspace_bytes(sh));
+    L->unfused_bytes = L->dz_bytes + L->gn_bytes + L->dw_bytes;
+    L->fused = t.dw_cba_min > 0 && sh.N * HWo >= t.dw_cba_min && soar::gn::dw_cba_fused_fits(sh) &&
+               soar::gn::dw_cba_grid_blocks(sh) <= 0x7fffffff;
+    L->fused_bytes = L->fused ? L->gn_bytes + soar::gn::dw_cba_part_bytes(sh) : 0;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+SOAR_API size_t soar_dw_cba_backward_workspace_bytes(int64_t N, int64_t C, int64_t H_in,
+                                                     int64_t W_in, int64_t H_out, int64_t W_out,
+                                                     int64_t K, int64_t pad, int64_t stride,
+                                                     int64_t dil, int64_t G) {
+    const soar::gn::DwShape sh = dw_shape(N, C, H_in, W_in, H_out, W_out, K, pad, stride, dil);
+    int64_t ie = 0, oe = 0, elems = 0;
+    if (check_dw_shape(sh, &ie, &oe) != SOAR_OK ||
+        check_shape(N, C, H_out * W_out, G, &elems) != SOAR_OK || oe == 0) {
+        g_err.clear();
+        return 0;
+    }
+    DwCbaLayout L;
+    if (!dw_cba_layout(sh, G, current_tuning(), &L)) return 0;
+    return L.fused ? L.fused_bytes : L.unfused_bytes;
+}
+
+SOAR_API int soar_dw_cba_backward(const float* dy, const float* z, const float* x,
+                                  const float* weight, const float* gamma, const float* beta,
+                                  const float* mean, const float* rstd, const float* mean_lo,
+                                  float* dx, float* dweight, float* dgamma, float* dbeta,
+                                  int64_t N, int64_t C, int64_t H_in, int64_t W_in, int64_t H_out,
+                                  int64_t W_out, int64_t K, int64_t pad, int64_t stride,
+                                  int64_t dil, int64_t G, unsigned flags, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+    const soar::gn::DwShape sh = dw_shape(N, C, H_in, W_in, H_out, W_out, K, pad, stride, dil);
+    int64_t ie = 0, oe = 0, elems = 0;
+    int rc = check_dw_shape(sh, &ie, &oe);
+    if (rc) return rc;
+    if ((rc = check_shape(N, C, H_out * W_out, G, &elems))) return rc;
+    if (flags & ~(SOAR_GN_SILU | SOAR_GN_ACCUMULATE_DX))
+        return fail(SOAR_EINVAL,
+                    "unsupported flags 0x%x (SOAR_GN_SILU, SOAR_GN_ACCUMULATE_DX)", flags);
+    if (oe == 0 || (!dx && !dweight && !dgamma && !dbeta)) return ok();
+    if ((rc = require_device())) return rc;
+    if (!dw_grids_fit(sh)) return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    const Tuning t = current_tuning();
+    DwCbaLayout L;
+    if (!dw_cba_layout(sh, G, t, &L))
+        return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (L.fused && dx) {
+        const size_t sb = (size_t)(N * G) * sizeof(float), cb = (size_t)C * sizeof(float);
+        const size_t wb = (size_t)(C * K * K) * sizeof(float);
+        if ((rc = check_dev(dy, (size_t)oe * 4, "dy")) || (rc = check_dev(z, (size_t)oe * 4, "z")) ||
+            (rc = check_dev(x, (size_t)ie * 4, "x")) || (rc = check_dev(weight, wb, "weight")) ||
+            (rc = check_dev(mean, sb, "mean")) || (rc = check_dev(rstd, sb, "rstd")) ||
+            (rc = check_dev_opt(mean_lo, sb, "mean_lo")) ||
+            (rc = check_dev_opt(gamma, cb, "gamma")) || (rc = check_dev_opt(beta, cb, "beta")) ||
+            (rc = check_dev(dx, (size_t)ie * 4, "dx")) ||
+            (rc = check_dev_opt(dweight, wb, "dweight")) ||
+            (rc = check_dev_opt(dgamma, cb, "dgamma")) || (rc = check_dev_opt(dbeta, cb, "dbeta")))
+            return rc;
+        if (workspace_bytes < L.fused_bytes)
+            return fail(SOAR_EINVAL,
+                        "workspace of %zu bytes is smaller than the %zu this shape needs",
+                        workspace_bytes, L.fused_bytes);
+        if ((rc = check_dev(workspace, L.fused_bytes, "workspace"))) return rc;
+        Plan gp = L.gp;
+        gp.vec4 = gp.vec4 && aligned16(z) && aligned16(dy);
+        const unsigned gflags = flags & SOAR_GN_SILU;
+        soar::gn::BwdArgs a{dy, z, gamma, beta, mean, rstd, mean_lo, nullptr, dgamma, dbeta,
+                            gflags, workspace};
+        soar::gn::BwdSums sums{};
+        hipError_t e = soar::gn::launch_backward_sums(gp, a, s, &sums);
+        if (e != hipSuccess) return hip_fail(e, "GroupNorm backward reduction launch");
+        float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + L.gn_bytes);
+        soar::gn::DwCbaArgs da{dy,    z,         x,        weight,       gamma,
+                               beta,  mean,      rstd,     sums.mean_lo, sums.unit_sums,
+                               sums.plane_sums,  dgamma,   dbeta,        dx,
+                               dweight, part};
+        e = soar::gn::launch_dw_cba_backward(sh, da, G, gflags != 0,
+                                             (flags & SOAR_GN_ACCUMULATE_DX) != 0, s);
+        if (e != hipSuccess) return hip_fail(e, "fused depthwise CBA backward launch");
+        return ok();
+    }
+    // the GroupNorm backward into dz (in the workspace), then the
+    // depthwise convolution's backward
+    if (workspace_bytes < L.unfused_bytes)
+        return fail(SOAR_EINVAL, "workspace of %zu bytes is smaller than the %zu this call needs",
+                    workspace_bytes, L.unfused_bytes);
+    char* ws = static_cast<char*>(workspace);
+    float* dz = (dx || dweight) ? reinterpret_cast<float*>(ws) : nullptr;
+    rc = soar_gn_silu_backward(dy, z, gamma, beta, mean, rstd, mean_lo, dz, dgamma, dbeta, N, C,
+                               H_out * W_out, G, flags & SOAR_GN_SILU, ws + L.dz_bytes,
+                               L.gn_bytes, stream);
+    if (rc || !dz) return rc;
+    return soar_dw_conv_backward(dz, x, weight, dx, dweight, nullptr, N, C, H_in, W_in, H_out,
+                                 W_out, K, pad, stride, dil, flags & SOAR_GN_ACCUMULATE_DX,
+                                 ws + L.dz_bytes + L.gn_bytes, L.dw_bytes, stream);
+}
+
 SOAR_API int soar_conv2d_dw_forward(const float* in, const float* weight, const float* bias,
                                     float* out, size_t C, size_t H_in, size_t W_in,
                                     size_t H_out, size_t W_out, size_t K, size_t pad,
@@ -1267,6 +1388,11 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
                 return fail(SOAR_EINVAL, "pw_cba_blocks must be in [64, 2^20]");
             g_tune.pw_cba_blocks = value;
             return ok();
+        case SOAR_TUNE_DW_CBA_MIN:
+            if (value < 0 || value > ((int64_t)1 << 40))
+                return fail(SOAR_EINVAL, "dw_cba_min must be in [0, 2^40]");
+            g_tune.dw_cba_min = value;
+            return ok();
         default:
             return fail(SOAR_EINVAL, "unknown tuning key %d", key);
     }
@@ -1292,6 +1418,7 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
         case SOAR_TUNE_PW_WG_TARGET: return g_tune.pw_wg_target;
         case SOAR_TUNE_PW_CBA_MIN: return g_tune.pw_cba_min;
         case SOAR_TUNE_PW_CBA_BLOCKS: return g_tune.pw_cba_blocks;
+        case SOAR_TUNE_DW_CBA_MIN: return g_tune.dw_cba_min;
         default: return -1;
     }
 }

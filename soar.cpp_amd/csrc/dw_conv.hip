@@ -36,6 +36,7 @@
 #include <type_traits>
 
 #include "gn_internal.hpp"
+#include "gn_math.hpp"
 #include "soar_gn.h"
 
 namespace soar {
@@ -461,6 +462,213 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_bwd_small(
     }
 }
 
+// ======================================================================
+// Fused backward of a depthwise CBA block whose convolution has stride 1
+// and "same" padding, pad = (K-1)*D/2 (LKR.dw, the Ctx branches, Fuse's
+// refine; blocks.cpp:449-500).  From the GroupNorm input z, the upstream
+// gradient dy and the convolution input x, one kernel forms dz (the
+// GroupNorm(+SiLU) input gradient, with k_bwd_dx's arithmetic from
+// gn_math.hpp) over a tile and its halo in LDS and runs from it both
+//   dx (+)= flip(w) (*) dz       the stride-1 adjoint (dw_conv_body's FMAs)
+//   dw, db partials += dz (x) x  dw_wgrad_body's FMAs
+// so dz never reaches HBM: z, dy and x are read once (with the halo) and
+// dx written once, instead of GroupNorm dx (3T) + dgrad (2T) + wgrad (2T).
+// With "same" padding, the dz region a dx tile reads and the x region the
+// weight gradient of that tile's dz reads are the same haloed tile (origin
+// (oy0 - pad, ox0 - pad)), so one fetch serves the three tensors.  dz is
+// zero outside the image (the adjoint's zero padding, and no weight-
+// gradient term there).  A block walks `per` tiles down one plane, keeps
+// the K*K+1 weight-gradient sums in registers across them and reduces once
+// (dw_wgrad_body's partial layout, added by k_dw_wgrad_finish or, with
+// `direct`, by the block itself).  The block of sample 0's first tile group
+// of channel c also adds dgamma[c] / dbeta[c] from the GroupNorm plane
+// sums in sample order (k_param_finish's sums).
+// ======================================================================
+template <int K, int D, bool SILU, bool ACC>
+__global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
+    const float* __restrict__ dy, const float* __restrict__ z, const float* __restrict__ x,
+    const float* __restrict__ w, const float* __restrict__ gamma,
+    const float* __restrict__ beta, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ mean_lo,
+    const double2* __restrict__ unit_sums, const double2* __restrict__ plane_sums,
+    float* __restrict__ dgamma, float* __restrict__ dbeta, float* __restrict__ dx,
+    float* __restrict__ part, float* __restrict__ dw, bool direct, int64_t N, int64_t C,
+    int64_t G, int64_t H, int64_t W, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per) {
+    using T = Tile<K, 1, D>;
+    constexpr int KK1 = K * K + 1;
+    constexpr int PAD = (K - 1) * D / 2;
+    constexpr int NR = (T::floats + kDwThreads - 1) / kDwThreads;
+    static_assert(NR <= 32, "one mask bit per prefetched element");
+    __shared__ __attribute__((aligned(16))) float tdz[T::floats];
+    __shared__ __attribute__((aligned(16))) float tx[T::floats];
+    __shared__ float red[kDwThreads / 64][KK1];
+    const int64_t plane = (int64_t)blockIdx.x / tpp, gix = (int64_t)blockIdx.x - plane * tpp;
+    const int64_t n = plane / C, c = plane - n * C;
+    const int64_t tyg = gix / tiles_x, txg = gix - tyg * tiles_x;
+    const int64_t ty0 = tyg * per, ty1 = min(ty0 + per, tiles_y);
+    const int64_t ox0 = txg * kTW;
+    const int64_t HW = H * W;
+    const int hi = (int)H, wi = (int)W, ix0 = (int)ox0 - PAD;
+
+    // this plane's GroupNorm dx coefficients, formed as k_bwd_dx forms them
+    const int64_t cpg = C / G, u = n * G + c / cpg;
+    const float mu = mean[u], r = rstd[u];
+    const float e = mean_lo ? -mean_lo[u] * r : 0.0f;
+    const float gm = gamma ? gamma[c] : 1.0f, bt = beta ? beta[c] : 0.0f;
+    const double2 S = unit_sums[u];
+    const double Md = (double)(cpg * HW);
+    const float A = gm * r;
+    const float B = (float)(-(double)r * S.x / Md);
+    const float Dc = (float)(-(double)r * S.y / Md);
+    if ((dgamma || dbeta) && n == 0 && gix == 0 && threadIdx.x == 0) {
+        double sa = 0.0, sb = 0.0;
+        for (int64_t s = 0; s < N; ++s) {
+            const double2 v = plane_sums[s * C + c];
+            sa += v.x;
+            sb += v.y;
+        }
+        if (dbeta) dbeta[c] = (float)((double)dbeta[c] + sa);
+        if (dgamma) dgamma[c] = (float)((double)dgamma[c] + sb);
+    }
+
+    const float* zp = z + plane * HW;
+    const float* gp = dy + plane * HW;
+    const float* xp = x + plane * HW;
+    // the haloed tile's elements of this thread (TilePrefetch's order) for
+    // the three tensors, and which of them lie inside the image
+    float pz[NR], pg[NR], px[NR];
+    uint32_t inside = 0;
+    auto fetch = [&](int64_t ty) {
+        const int iy0 = (int)(ty * kTH) - PAD;
+        int t = (int)threadIdx.x;
+        asm volatile("" : "+v"(t));  // recomputed per tile, not hoisted
+        inside = 0;
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+            const int i = t + k * kDwThreads;
+            const int rw = i / T::IWP, col = i - rw * T::IWP;
+            const int yy = iy0 + rw, xx = ix0 + col;
+            const bool in = i < T::floats && col < T::IW && (unsigned)yy < (unsigned)hi &&
+                            (unsigned)xx < (unsigned)wi;
+            float a = 0.0f, g = 0.0f, v = 0.0f;
+            if (in) {
+                const int off = yy * wi + xx;
+                a = zp[off];
+                g = gp[off];
+                v = xp[off];
+            }
+            pz[k] = a;
+            pg[k] = g;
+            px[k] = v;
+            inside |= (uint32_t)in << k;
+        }
+    };
+    float wr[K * K];
+#pragma unroll
+    for (int k = 0; k < K * K; ++k) wr[k] = w[c * K * K + K * K - 1 - k];  // flipped
+    float sw[KK1];
+#pragma unroll
+    for (int k = 0; k < KK1; ++k) sw[k] = 0.0f;
+    const int t = threadIdx.x, ro = t >> 3, c0 = (t & 7) * kPer;
+    const bool want_dw = dw != nullptr;  // block-uniform; without it `part` is null
+
+    fetch(ty0);
+    for (int64_t ty = ty0; ty < ty1; ++ty) {
+        if (ty > ty0) __syncthreads();  // the previous tile's LDS reads are done
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+            const int i = t + k * kDwThreads;
+            if (i < T::floats) {
+                float d = 0.0f;
+                if (inside & (1u << k)) {
+                    const float xh = fmaf(pz[k] - mu, r, e);
+                    const float dzs = SILU ? dsilu_fast(pg[k], fmaf(gm, xh, bt)) : pg[k];
+                    d = fmaf(A, dzs, fmaf(Dc, xh, B));
+                }
+                tdz[i] = d;
+                tx[i] = px[k];
+            }
+        }
+        __syncthreads();
+        if (ty + 1 < ty1) fetch(ty + 1);
+
+        // dx for rows ty*32 + ro, columns ox0 + c0 .. +7
+        float acc[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) acc[q] = 0.0f;
+#pragma unroll
+        for (int ky = 0; ky < K; ++ky) {
+            float seg[T::SL4];
+            load_seg<K, 1, D>(tdz, ro + ky * D, c0, seg);
+#pragma unroll
+            for (int kx = 0; kx < K; ++kx)
+#pragma unroll
+                for (int q = 0; q < kPer; ++q)
+                    acc[q] = fmaf(wr[ky * K + kx], seg[q + kx * D], acc[q]);
+        }
+        // weight gradient: this tile's dz (the halo's interior) against x
+        if (want_dw) {
+            float g[kPer];
+#pragma unroll
+            for (int q = 0; q < kPer; ++q) {
+                g[q] = tdz[(ro + PAD) * T::IWP + c0 + q + PAD];
+                sw[K * K] += g[q];
+            }
+#pragma unroll
+            for (int ky = 0; ky < K; ++ky) {
+                float seg[T::SL4];
+                load_seg<K, 1, D>(tx, ro + ky * D, c0, seg);
+#pragma unroll
+                for (int kx = 0; kx < K; ++kx)
+#pragma unroll
+                    for (int q = 0; q < kPer; ++q)
+                        sw[ky * K + kx] = fmaf(g[q], seg[q + kx * D], sw[ky * K + kx]);
+            }
+        }
+        const int64_t oy = ty * kTH + ro;
+        if (oy >= H) continue;
+        float* orow = dx + plane * HW + oy * W;
+        const int64_t ox = ox0 + c0;
+        if (ox + kPer <= W && ((reinterpret_cast<uintptr_t>(orow + ox) & 15) == 0)) {
+            f4* o4 = reinterpret_cast<f4*>(orow + ox);
+            f4 v0 = {acc[0], acc[1], acc[2], acc[3]}, v1 = {acc[4], acc[5], acc[6], acc[7]};
+            if (ACC) {
+                v0 += o4[0];
+                v1 += o4[1];
+            }
+            o4[0] = v0;
+            o4[1] = v1;
+        } else {
+#pragma unroll
+            for (int q = 0; q < kPer; ++q)
+                if (ox + q < W) orow[ox + q] = ACC ? orow[ox + q] + acc[q] : acc[q];
+        }
+    }
+    if (!want_dw) return;
+    // block sum of the weight-gradient terms in a fixed order (dw_wgrad_body's)
+#pragma unroll
+    for (int k = 0; k < KK1; ++k) {
+        float v = sw[k];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off);
+        sw[k] = v;
+    }
+    const int lane = t & 63, wv = t >> 6;
+    if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < KK1; ++k) red[wv][k] = sw[k];
+    }
+    __syncthreads();
+    if (t < KK1) {
+        const float v = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
+        if (direct) {
+            if (t < K * K) dw[c * K * K + t] = (float)((double)dw[c * K * K + t] + (double)v);
+        } else {
+            part[(n * tpp + gix) * (C * KK1) + c * KK1 + t] = v;
+        }
+    }
+}
+
 // ---- generic kernels (any K, S, D): one thread per output element --------
 
 template <bool FLIP, bool ACC>
@@ -813,6 +1021,73 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
             k_dw_wgrad_generic<<<dim3((unsigned)(sh.C * KK1)), 256, 0, s>>>(
                 dy, x, dw, db, sh.N, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.K, sh.pad, sh.S, sh.D);
         }
+        prof_end(s, tok);
+    }
+    return hipGetLastError();
+}
+
+bool dw_cba_fused_fits(const DwShape& sh) {
+    return sh.S == 1 && sh.Ho == sh.Hi && sh.Wo == sh.Wi && (sh.K - 1) * sh.D % 2 == 0 &&
+           sh.pad == (sh.K - 1) * sh.D / 2 && sh.Hi * sh.Wi > 0 && planes_fit_32(sh) &&
+           dw_has_fast(sh.K, sh.S, sh.D);
+}
+
+namespace {
+// Tiles per block of the fused CBA backward: as the weight gradient's (8
+// for K >= 7, else 4), halved while the grid would hold fewer than 2048
+// blocks.
+int64_t dw_cba_per(const DwShape& sh, int64_t* tiles_x, int64_t* tiles_y, int64_t* tpp) {
+    *tiles_x = (sh.Wi + kTW - 1) / kTW;
+    *tiles_y = (sh.Hi + kTH - 1) / kTH;
+    int64_t per = sh.K >= 7 ? 8 : 4;
+    while (per > 1 && sh.N * sh.C * ((*tiles_y + per - 1) / per) * *tiles_x < 2048) per /= 2;
+    *tpp = ((*tiles_y + per - 1) / per) * *tiles_x;
+    return per;
+}
+}  // namespace
+
+size_t dw_cba_part_bytes(const DwShape& sh) {
+    int64_t tx = 0, ty = 0, tpp = 0;
+    dw_cba_per(sh, &tx, &ty, &tpp);
+    const size_t b = sizeof(float) * (size_t)(sh.N * tpp) * (size_t)(sh.C * (sh.K * sh.K + 1));
+    return (b + 255) & ~(size_t)255;
+}
+
+int64_t dw_cba_grid_blocks(const DwShape& sh) {
+    int64_t tx = 0, ty = 0, tpp = 0;
+    dw_cba_per(sh, &tx, &ty, &tpp);
+    return sh.N * sh.C * tpp;
+}
+
+hipError_t launch_dw_cba_backward(const DwShape& sh, const DwCbaArgs& a, int64_t G, bool silu,
+                                  bool accumulate_dx, hipStream_t s) {
+    if (sh.N * sh.C * sh.Hi * sh.Wi == 0) return hipSuccess;
+    int64_t tiles_x = 0, tiles_y = 0, tpp = 0;
+    const int64_t per = dw_cba_per(sh, &tiles_x, &tiles_y, &tpp);
+    const bool direct = sh.N * tpp == 1;
+    float* part = a.dw ? a.part : nullptr;
+    int tok = prof_begin(s, "dw_cba_bwd");
+    fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
+        using CF = decltype(cf);
+        if constexpr (CF::s == 1) {
+            bsel(silu, [&](auto SI) {
+                bsel(accumulate_dx, [&](auto AC) {
+                    k_dw_cba_bwd<CF::k, CF::d, SI(), AC()>
+                        <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
+                            a.dy, a.z, a.x, a.w, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo,
+                            a.unit_sums, a.plane_sums, a.dgamma, a.dbeta, a.dx, part, a.dw,
+                            direct, sh.N, sh.C, G, sh.Hi, sh.Wi, tiles_x, tiles_y, tpp,
+                            (int)per);
+                });
+            });
+        }
+    });
+    prof_end(s, tok);
+    if (a.dw && !direct) {
+        const int64_t KK1 = sh.K * sh.K + 1, E = sh.C * KK1;
+        tok = prof_begin(s, "dw_cba_wgrad_finish");
+        k_dw_wgrad_finish<<<dim3((unsigned)((E + 63) / 64)), 1024, 0, s>>>(part, a.dw, nullptr, E,
+                                                                           sh.N * tpp, KK1);
         prof_end(s, tok);
     }
     return hipGetLastError();

@@ -84,6 +84,9 @@ struct Tuning {
                                  // 2^14 / 2^16 / 2^17 / never: 512^2 2.73 /
                                  // 2.92 / 2.90 / 2.96 ms, 1024^2 4.34 /
                                  // 4.36 / 4.45 / 4.54 ms
+    int64_t dw_cba_min = 16384;  // depthwise CBA backward: samples x pixels
+                                 // from which the fused kernel runs (0:
+                                 // never)
     int64_t pw_cba_blocks = 256;  // and the blocks its pixel chunks aim for
                                   // (one per CU: at 64 -> 64 channels over
                                   // 2048^2 pixels 1.03 ms, 1.13 at 512,
@@ -291,6 +294,37 @@ hipError_t launch_dw_forward(const DwShape& sh, const float* x, const float* w,
 hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x,
                               const float* w, float* dx, float* dw, float* db,
                               bool accumulate_dx, void* ws, hipStream_t s);
+
+// Fused backward of a depthwise CBA block with a stride-1 "same"
+// convolution (dw_conv.hip): from z (the GroupNorm input), dy and x, dx
+// (=, or += with accumulate_dx) flip(w) (*) dz and dw += the weight
+// gradient, with dz the GroupNorm(+SiLU) input gradient formed in LDS and
+// never stored.  The GroupNorm sums come from launch_backward_sums; the
+// kernel also adds dgamma / dbeta.  Needs dw_cba_fused_fits and, with dw,
+// dw_cba_part_bytes of workspace at `part`.
+struct DwCbaArgs {
+    const float* dy;  // [N][C][H][W]
+    const float* z;
+    const float* x;
+    const float* w;  // [C][K][K]
+    const float* gamma;
+    const float* beta;
+    const float* mean;
+    const float* rstd;
+    const float* mean_lo;
+    const double2* unit_sums;
+    const double2* plane_sums;
+    float* dgamma;  // nullable
+    float* dbeta;   // nullable
+    float* dx;      // [N][C][H][W]
+    float* dw;      // [C][K][K], nullable
+    float* part;    // weight-gradient block partials
+};
+bool dw_cba_fused_fits(const DwShape& sh);
+size_t dw_cba_part_bytes(const DwShape& sh);
+int64_t dw_cba_grid_blocks(const DwShape& sh);
+hipError_t launch_dw_cba_backward(const DwShape& sh, const DwCbaArgs& a, int64_t G, bool silu,
+                                  bool accumulate_dx, hipStream_t s);
 
 // Elementwise kernels (elementwise.hip).
 hipError_t launch_silu_forward(const float* x, float* y, int64_t n,

@@ -193,6 +193,8 @@ public:
     [[nodiscard]] bool act() const noexcept { return act_; }
 
 private:
+    TensorPtr forward_depthwise(const TensorPtr& input, unsigned flags);
+
     std::shared_ptr<Conv2d> conv_;
     std::shared_ptr<GroupNorm> norm_;
     bool act_;

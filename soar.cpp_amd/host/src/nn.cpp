@@ -322,6 +322,59 @@ struct CBAPointwiseNode : autograd::AutogradNode {
     }
 };
 
+// Backward of a CBA block with a depthwise conv: the GroupNorm(+SiLU)
+// backward at the saved conv output z and the conv backward in one call
+// (soar_dw_cba_backward: for stride 1 with "same" padding, one kernel forms
+// dz over each tile in LDS and never stores it).
+struct CBADepthwiseNode : autograd::AutogradNode {
+    TensorPtr input, conv_w, gamma, beta, z, mean, rstd, mean_lo;
+    ConvGeom g{};
+    int64_t K = 1, pad = 0, stride = 1, dil = 1, G = 1;
+    unsigned flags = 0;
+
+    std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
+        std::vector<std::shared_ptr<AutogradNode>> r;
+        for (const auto& t : {input, conv_w, gamma, beta})
+            if (t && t->grad_fn()) r.push_back(t->grad_fn());
+        return r;
+    }
+
+    void backward(const TensorPtr& go) override {
+        const bool want_x = input->requires_grad();
+        const bool want_w = conv_w->requires_grad();
+        const bool want_p = gamma && gamma->requires_grad();
+        if (!want_x && !want_w && !want_p) return;
+        if (!go->is_cuda()) go->to_cuda();
+        bool g_direct = false, b_direct = false, w_direct = false, fresh = false;
+        TensorPtr dg = want_p ? param_grad_target(gamma, &g_direct) : nullptr;
+        TensorPtr db = want_p ? param_grad_target(beta, &b_direct) : nullptr;
+        TensorPtr gx = want_x ? write_target(input, &fresh) : nullptr;
+        TensorPtr gw = want_w ? param_grad_target(conv_w, &w_direct) : nullptr;
+        const size_t wsb = soar_dw_cba_backward_workspace_bytes(g.N, g.C_in, g.H, g.W, g.Ho,
+                                                                g.Wo, K, pad, stride, dil, G);
+        check(soar_dw_cba_backward(go->cuda_data(), z->cuda_data(), input->cuda_data(),
+                                   conv_w->cuda_data(), dptr(gamma), dptr(beta),
+                                   mean->cuda_data(), rstd->cuda_data(), dptr(mean_lo),
+                                   gx ? gx->cuda_data() : nullptr,
+                                   gw ? gw->cuda_data() : nullptr,
+                                   dg ? dg->cuda_data() : nullptr,
+                                   db ? db->cuda_data() : nullptr, g.N, g.C_in, g.H, g.W, g.Ho,
+                                   g.Wo, K, pad, stride, dil, G,
+                                   (flags & SOAR_GN_SILU) | dx_mode(gx, fresh), workspace(wsb),
+                                   wsb, exec::stream()),
+              "depthwise CBA backward");
+        if (dg && !g_direct) propagate_grad(gamma, std::move(dg));
+        if (db && !b_direct) propagate_grad(beta, std::move(db));
+        if (gw && !w_direct) propagate_grad(conv_w, std::move(gw));
+        if (gx && fresh) propagate_grad(input, std::move(gx));
+    }
+
+    void release_variables() override {
+        input = nullptr;
+        z = mean = rstd = mean_lo = nullptr;
+    }
+};
+
 struct SiLUNode : autograd::AutogradNode {
     TensorPtr input;
     std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
@@ -545,6 +598,7 @@ CBA::CBA(size_t c1, size_t c2, size_t k, size_t s, int p, size_t d, size_t g, bo
 
 TensorPtr CBA::forward(const TensorPtr& input) {
     const unsigned flags = act_ ? SOAR_GN_SILU : 0u;
+    if (conv_->depthwise() && !conv_->pointwise()) return forward_depthwise(input, flags);
     if (!conv_->pointwise()) return norm_->run(conv_->forward(input), flags);
     // pointwise conv: one call, the GroupNorm statistics from the conv epilogue
     const ConvGeom g = conv_geom(input, *conv_);
@@ -584,6 +638,61 @@ TensorPtr CBA::forward(const TensorPtr& input) {
         node->rstd = rstd;
         node->mean_lo = lo;
         node->g = g;
+        node->G = G;
+        node->flags = flags;
+        y->set_grad_fn(node);
+    }
+    return y;
+}
+
+// Depthwise conv: the conv and the GroupNorm forward, recorded as one node
+// whose backward is soar_dw_cba_backward.
+TensorPtr CBA::forward_depthwise(const TensorPtr& input, unsigned flags) {
+    const ConvGeom g = conv_geom(input, *conv_);
+    if (!input->is_cuda()) input->to_cuda();
+    const TensorPtr w = conv_->weight();
+    const TensorPtr gamma = norm_->weight(), beta = norm_->bias();
+    w->to_cuda();
+    if (gamma) {
+        gamma->to_cuda();
+        beta->to_cuda();
+    }
+    const int64_t G = (int64_t)norm_->num_groups(), HWo = g.Ho * g.Wo;
+    const int64_t K = (int64_t)conv_->kernel_size(), pad = (int64_t)conv_->padding();
+    const int64_t S = (int64_t)conv_->stride(), D = (int64_t)conv_->dilation();
+    const bool record = (input->requires_grad() || w->requires_grad() ||
+                         (gamma && gamma->requires_grad())) &&
+                        GradMode::is_enabled();
+    const Shape os = conv_out_shape(input, g);
+    TensorPtr z = Tensor::create(os, false, true);
+    TensorPtr y = Tensor::create(os, record, true);
+    TensorPtr mean = Tensor::create({g.N * G}, false, true);
+    TensorPtr rstd = Tensor::create({g.N * G}, false, true);
+    TensorPtr lo = Tensor::create({g.N * G}, false, true);
+    check(soar_dw_conv_forward(input->cuda_data(), w->cuda_data(), nullptr, z->cuda_data(), g.N,
+                               g.C_in, g.H, g.W, g.Ho, g.Wo, K, pad, S, D, exec::stream()),
+          "depthwise convolution");
+    const size_t wsb = soar_gn_workspace_bytes(g.N, g.C_out, HWo, G);
+    check(soar_gn_silu_forward(z->cuda_data(), dptr(gamma), dptr(beta), y->cuda_data(),
+                               mean->cuda_data(), rstd->cuda_data(), lo->cuda_data(), g.N,
+                               g.C_out, HWo, G, norm_->eps(), flags, workspace(wsb), wsb,
+                               exec::stream()),
+          "CBA GroupNorm forward");
+    if (record) {
+        auto node = std::make_shared<CBADepthwiseNode>();
+        node->input = input;
+        node->conv_w = w;
+        node->gamma = gamma;
+        node->beta = beta;
+        node->z = z;
+        node->mean = mean;
+        node->rstd = rstd;
+        node->mean_lo = lo;
+        node->g = g;
+        node->K = K;
+        node->pad = pad;
+        node->stride = S;
+        node->dil = D;
         node->G = G;
         node->flags = flags;
         y->set_grad_fn(node);

@@ -56,6 +56,7 @@ TUNE_PW_WG_WAVES = 14
 TUNE_PW_WG_TARGET = 15
 TUNE_PW_CBA_MIN = 16
 TUNE_PW_CBA_BLOCKS = 17
+TUNE_DW_CBA_MIN = 18
 
 
 class SoarUnavailable(RuntimeError):
@@ -112,6 +113,8 @@ SIGNATURES = {
     "soar_dw_conv_forward": (_c.c_int, [_P, _P, _P, _P] + [_I64] * 10 + [_P]),
     "soar_dw_conv_backward_workspace_bytes": (_SZ, [_I64] * 9),
     "soar_dw_conv_backward": (_c.c_int, [_P] * 6 + [_I64] * 10 + [_c.c_uint, _P, _SZ, _P]),
+    "soar_dw_cba_backward_workspace_bytes": (_SZ, [_I64] * 11),
+    "soar_dw_cba_backward": (_c.c_int, [_P] * 13 + [_I64] * 11 + [_c.c_uint, _P, _SZ, _P]),
     "soar_conv2d_dw_forward": (_c.c_int, [_P, _P, _P, _P] + [_SZ] * 9 + [_P]),
     "soar_conv2d_dw_backward": (_c.c_int, [_P] * 6 + [_SZ] * 9 + [_P]),
     "soar_arena_create": (_c.c_int, [_SZ, _SZ, _c.POINTER(_P)]),
@@ -592,6 +595,52 @@ def dw_conv_backward(dy, x, weight, pad, stride=1, dil=1, dx=None, dweight=None,
         Wo, K, pad, stride, dil, GN_ACCUMULATE_DX if accumulate_dx else 0, _ptr(ws), ws.numel(),
         _stream(stream)))
     return (dx if want_dx else None, dweight if want_dw else None, dbias if want_db else None)
+
+
+def dw_cba_backward_workspace_bytes(N, C, H, W, Ho, Wo, K, pad, stride, dil, G) -> int:
+    return int(lib().soar_dw_cba_backward_workspace_bytes(N, C, H, W, Ho, Wo, K, pad, stride,
+                                                          dil, G))
+
+
+def dw_cba_backward(dy, z, x, weight, gamma, beta, stats, G, pad, stride=1, dil=1, silu=True,
+                    dx=None, dweight=None, dgamma=None, dbeta=None, want_dx=True, want_dw=True,
+                    want_params=True, accumulate_dx=False, ws=None, stream=None):
+    """Backward of a depthwise CBA block through soar_dw_cba_backward.
+
+    z: the convolution output (the GroupNorm input), stats: its GroupNorm
+    forward's Stats, dy: the gradient at the block's output.  Returns
+    (dx, dweight, dgamma, dbeta); dweight/dgamma/dbeta accumulate (fresh
+    zeros when not given); dx is written, or added to with accumulate_dx."""
+    import torch
+    N, C, H, W = x.shape
+    Ho, Wo = z.shape[2], z.shape[3]
+    K = weight.shape[-1]
+    for t, n in ((dy, "dy"), (z, "z"), (x, "x"), (weight, "weight"), (gamma, "gamma"),
+                 (beta, "beta"), (dx, "dx"), (dweight, "dweight"), (dgamma, "dgamma"),
+                 (dbeta, "dbeta")):
+        _check_tensor(t, n)
+    dev = x.device
+    if want_dx and dx is None:
+        dx = (torch.zeros if accumulate_dx else torch.empty)((N, C, H, W), dtype=torch.float32,
+                                                             device=dev)
+    if want_dw and dweight is None:
+        dweight = torch.zeros((C, K, K), dtype=torch.float32, device=dev)
+    if want_params and dgamma is None:
+        dgamma = torch.zeros(C, dtype=torch.float32, device=dev)
+    if want_params and dbeta is None:
+        dbeta = torch.zeros(C, dtype=torch.float32, device=dev)
+    if ws is None:
+        n = dw_cba_backward_workspace_bytes(N, C, H, W, Ho, Wo, K, pad, stride, dil, G)
+        ws = torch.empty(max(n, 1), dtype=torch.uint8, device=dev)
+    flags = (GN_SILU if silu else 0) | (GN_ACCUMULATE_DX if accumulate_dx else 0)
+    check(lib().soar_dw_cba_backward(
+        _ptr(dy), _ptr(z), _ptr(x), _ptr(weight), _ptr(gamma), _ptr(beta), _ptr(stats.mean),
+        _ptr(stats.rstd), _ptr(stats.mean_lo), _ptr(dx) if want_dx else None,
+        _ptr(dweight) if want_dw else None, _ptr(dgamma) if want_params else None,
+        _ptr(dbeta) if want_params else None, N, C, H, W, Ho, Wo, K, pad, stride, dil, G, flags,
+        _ptr(ws), ws.numel(), _stream(stream)))
+    return (dx if want_dx else None, dweight if want_dw else None,
+            dgamma if want_params else None, dbeta if want_params else None)
 
 
 def prof_enable(on: bool = True):
