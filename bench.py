@@ -71,6 +71,14 @@ STREAM_CONFIGS = {"stream_read": "read", "stream_copy": "copy", "stream_2r1w": "
 DW_CONFIGS = {"dw_k3": (3, 1, 1), "dw_k5": (5, 1, 1), "dw_k7": (7, 1, 1),
               "dw_k3d5": (3, 1, 5), "dw_k3s2": (3, 2, 1)}
 DW_SHAPE = (1, 64, 2048, 2048)
+# CBA blocks with a depthwise conv (stride 1, same padding) at 1x64x2048^2,
+# G = 16, forward + backward; the backward fused (soar_dw_cba_backward) or
+# as the GroupNorm backward then the depthwise backward: name -> (K, dil)
+CBA_DW_CONFIGS = {}
+for _k, _d in ((3, 1), (5, 1), (7, 1), (3, 5)):
+    _n = f"cba_dw_k{_k}" + (f"d{_d}" if _d > 1 else "")
+    CBA_DW_CONFIGS[_n] = (_k, _d, True)
+    CBA_DW_CONFIGS[_n + "_unfused"] = (_k, _d, False)
 PEAK_VALU_F32 = 157.3  # TFLOP/s, MI355X published vector fp32 (packed); 78.6 without
 
 # End-to-end training steps of the SOAR model through libsoar_host.so
@@ -103,7 +111,7 @@ def parse():
     ap.add_argument("--config", default="cfg3",
                     choices=sorted(CONFIGS) + sorted(TRAIN_CONFIGS) + sorted(PREDICT_CONFIGS)
                     + sorted(STREAM_CONFIGS)
-                    + sorted(DW_CONFIGS))
+                    + sorted(DW_CONFIGS) + sorted(CBA_DW_CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="time the steps without per-kernel events")
@@ -326,6 +334,87 @@ class DwStep:
         gn.dw_conv_forward(self.x, self.w, self.b, self.pad, self.S, self.D, y=self.y)
         gn.dw_conv_backward(self.dy, self.x, self.w, self.pad, self.S, self.D, dx=self.dx,
                             dweight=self.dw, dbias=self.db, ws=self.ws)
+
+
+class CBADwStep:
+    """Forward and backward of a CBA block with a depthwise conv (stride 1,
+    same padding, no bias) at 1x64x2048^2, G = 16: z = dwconv(x) (soar_dw_conv_forward),
+    y = SiLU(GroupNorm(z)) (soar_gn_silu_forward); backward fused
+    (soar_dw_cba_backward: the GroupNorm reduction, then one kernel that
+    forms dz per tile in LDS and computes dx and dW from it) or unfused
+    (soar_gn_silu_backward to dz, then soar_dw_conv_backward)."""
+
+    def __init__(self, gn, name, seed):
+        import torch
+        K, D, fused = CBA_DW_CONFIGS[name]
+        N, C, H, W = DW_SHAPE
+        self.gn, self.K, self.D, self.pad, self.fused = gn, K, D, D * (K - 1) // 2, fused
+        self.N, self.C, self.H, self.W, self.G = N, C, H, W, 16
+        self.x = torch.empty((N, C, H, W), device="cuda")
+        gn.synth_normal(self.x, seed, 1, 0.0, 1.0)
+        self.w = torch.empty((C, K, K), device="cuda")
+        gn.synth_uniform(self.w, seed, 7, -1.0 / K, 1.0 / K)
+        self.gamma = torch.empty(C, device="cuda")
+        self.beta = torch.empty(C, device="cuda")
+        gn.synth_uniform(self.gamma, seed, 2, 0.5, 1.5)
+        gn.synth_normal(self.beta, seed, 3, 0.0, 0.1)
+        self.z, self.y = torch.empty_like(self.x), torch.empty_like(self.x)
+        self.dy = torch.empty_like(self.x)
+        gn.synth_normal(self.dy, seed, 4, 0.0, 1e-2)
+        self.mean, self.rstd, self.lo = (torch.empty(N * self.G, device="cuda") for _ in range(3))
+        self.dx, self.dz = torch.empty_like(self.x), torch.empty_like(self.x)
+        self.dw = torch.zeros_like(self.w)
+        self.dgamma, self.dbeta = torch.zeros(C, device="cuda"), torch.zeros(C, device="cuda")
+        self.ws_gn = gn.workspace(N, C, H * W, self.G)
+        if fused:
+            nws = gn.dw_cba_backward_workspace_bytes(N, C, H, W, H, W, K, self.pad, 1, D, self.G)
+        else:
+            nws = int(gn.lib().soar_dw_conv_backward_workspace_bytes(N, C, H, W, H, W, K, 1, D))
+        self.ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
+        self.params = [None]
+        self.T = N * C * H * W * 4
+
+    def algorithmic_bytes(self):
+        # fwd: conv reads x, writes z; GroupNorm statistics read z; apply reads
+        # z, writes y.  bwd: the reduction reads dy, z; fused: one kernel reads
+        # dy, z, x and writes dx; unfused: GroupNorm dx reads dy, z and writes
+        # dz, dgrad reads dz and writes dx, wgrad reads dz and x.
+        return (5 + 2 + (4 if self.fused else 7)) * self.T
+
+    def kernel_bytes(self, name):
+        T = self.T
+        return {"dw_conv": 2 * T, "gn_stats_partial": T, "gn_silu_apply": 2 * T,
+                "gn_silu_bwd_reduce": 2 * T, "gn_silu_bwd_dx": 3 * T, "dw_conv_dgrad": 2 * T,
+                "dw_conv_wgrad": 2 * T, "dw_cba_bwd": 4 * T}.get(name, 0)
+
+    def kernel_flops(self, name):
+        f = 2 * self.K * self.K * self.T // 4
+        if name == "dw_cba_bwd":
+            return 2 * f
+        return f if name in ("dw_conv", "dw_conv_dgrad", "dw_conv_wgrad") else 0
+
+    def config(self):
+        return {"workload": f"CBA fwd+bwd: depthwise conv k{self.K} dilation {self.D} pad "
+                            f"{self.pad} + GN + SiLU, backward "
+                            + ("fused (dz per tile in LDS)" if self.fused else
+                               "as GN backward then depthwise backward"),
+                "N": self.N, "C": self.C, "H": self.H, "W": self.W, "G": self.G}
+
+    def __call__(self):
+        gn = self.gn
+        gn.dw_conv_forward(self.x, self.w, None, self.pad, 1, self.D, y=self.z)
+        gn.gn_silu_forward(self.z, self.gamma, self.beta, self.G, y=self.y, mean=self.mean,
+                           rstd=self.rstd, mean_lo=self.lo, ws=self.ws_gn)
+        st = gn.Stats(self.mean, self.rstd, self.lo)
+        if self.fused:
+            gn.dw_cba_backward(self.dy, self.z, self.x, self.w, self.gamma, self.beta, st, self.G,
+                               self.pad, 1, self.D, dx=self.dx, dweight=self.dw,
+                               dgamma=self.dgamma, dbeta=self.dbeta, ws=self.ws)
+            return
+        gn.gn_silu_backward(self.dy, self.z, self.gamma, self.beta, st, self.G, dx=self.dz,
+                            dgamma=self.dgamma, dbeta=self.dbeta, ws=self.ws_gn)
+        gn.dw_conv_backward(self.dz, self.x, self.w, self.pad, 1, self.D, dx=self.dx,
+                            dweight=self.dw, want_db=False, ws=self.ws)
 
 
 def bench_stream(args):
@@ -605,6 +694,8 @@ def main():
 
     if args.config in DW_CONFIGS:
         step = DwStep(gn, args.config, SEED + 7)
+    elif args.config in CBA_DW_CONFIGS:
+        step = CBADwStep(gn, args.config, SEED + 8)
     elif args.config in ("cba_pw", "cba_pw_unfused"):
         N, C, HW, G, passes, residual, blocks = CONFIGS[args.config]
         step = CBAStep(gn, N, C, HW, G, SEED_OF[args.config], fused=args.config == "cba_pw")
@@ -665,7 +756,7 @@ def main():
         if flops:
             tf = flops / (avg * 1e-3) / 1e12
             kinfo[k["kernel"]]["TFLOPs"] = round(tf, 2)
-            if isinstance(step, DwStep):  # vector FMAs, not the matrix cores
+            if isinstance(step, (DwStep, CBADwStep)):  # vector FMAs, not the matrix cores
                 kinfo[k["kernel"]]["valu_frac"] = round(tf / PEAK_VALU_F32, 4)
             else:
                 kinfo[k["kernel"]]["mfma_frac"] = round(tf / PEAK_MFMA_F32, 4)
@@ -695,6 +786,10 @@ def main():
     if isinstance(step, DwStep):
         data = (f"synthetic: x~N(0,1), w~U(-1/K,1/K), b~N(0,0.1), dy~N(0,1e-2); "
                 f"splitmix64/Box-Muller seed {SEED + 7}")
+        cfg = {**step.config(), "algorithmic_bytes_per_step": alg}
+    elif isinstance(step, CBADwStep):
+        data = (f"synthetic: x~N(0,1), w~U(-1/K,1/K), gamma~U(0.5,1.5), beta~N(0,0.1), "
+                f"dy~N(0,1e-2); splitmix64/Box-Muller seed {SEED + 8}")
         cfg = {**step.config(), "algorithmic_bytes_per_step": alg}
     else:
         data = (f"synthetic: x~N(0,1), gamma~U(0.5,1.5), beta~N(0,0.1), dy~N(0,1e-2); "

@@ -64,6 +64,20 @@ struct Tile {
     static constexpr int floats = IH * IWP;
 };
 
+// Logical block of physical block b in a grid of nb blocks, such that
+// consecutive logical blocks run on one XCD.  Workgroups are dealt to the 8
+// XCDs in turn (block b on XCD b % 8) and each XCD has its own L2.  The
+// tiles of a row of a plane share the 128-byte lines at their edges (the
+// halo), so with adjacent tiles on different XCDs those lines came from the
+// fabric twice: the k3 forward fetched 1.50x its input.  (A bijection on
+// [0, nb): the first nb % 8 XCDs take one block more.)
+__device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
+    constexpr int64_t kX = 8;
+    const int64_t q = nb / kX, r = nb - q * kX;
+    const int64_t x = b % kX, k = b / kX;
+    return x * q + min(x, r) + k;
+}
+
 // Row segment of a thread: SL4 floats of LDS row `lrow` from column c0*S.
 template <int K, int S, int D>
 __device__ __forceinline__ void load_seg(const float* tile, int lrow, int c0,
@@ -191,7 +205,8 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_conv(
     int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per) {
     __shared__ __attribute__((aligned(16))) float tile[Tile<K, S, D>::floats];
     dw_conv_body<K, S, D, FLIP, ACC, BIAS>(in, w, bias, out, C, Hi, Wi, Ho, Wo, pad, tiles_x,
-                                           tiles_y, tpp, per, blockIdx.x, tile);
+                                           tiles_y, tpp, per, xcd_block(blockIdx.x, gridDim.x),
+                                           tile);
 }
 
 // Weight and bias gradient partials: a block walks `per` tiles down one
@@ -307,7 +322,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
     __shared__ __attribute__((aligned(16))) float tile[Tile<K, S, D>::floats];
     __shared__ float red[kDwThreads / 64][K * K + 1];
     dw_wgrad_body<K, S, D>(dy, x, part, dw, db, direct, C, Hi, Wi, Ho, Wo, pad, tiles_x, tiles_y,
-                           tpp, per, blockIdx.x, tile, red);
+                           tpp, per, xcd_block(blockIdx.x, gridDim.x), tile, red);
 }
 
 // Input gradient for stride S > 1 over one 32 x 64 tile of dx per block:
@@ -426,7 +441,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_dgrad_strided(
     int64_t tiles_y, int64_t tpp, int per) {
     __shared__ float tile[DTile<K, S, D>::R * DTile<K, S, D>::W];
     dw_dgrad_strided_body<K, S, D, ACC>(dy, w, dx, C, Hi, Wi, Ho, Wo, pad, tiles_x, tiles_y,
-                                        tpp, per, blockIdx.x, tile);
+                                        tpp, per, xcd_block(blockIdx.x, gridDim.x), tile);
 }
 
 // The input gradient and the weight gradient of a small depthwise layer in
@@ -447,7 +462,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_bwd_small(
     constexpr int TW = Tile<K, S, D>::floats;
     __shared__ __attribute__((aligned(16))) float tile[TD > TW ? TD : TW];
     __shared__ float red[kDwThreads / 64][K * K + 1];
-    const int64_t b = blockIdx.x;
+    const int64_t b = xcd_block(blockIdx.x, gridDim.x);
     if (b < nbd) {
         if constexpr (S == 1)
             dw_conv_body<K, 1, D, true, ACC, false>(dy, w, nullptr, dx, C, Ho, Wo, Hi, Wi,
@@ -502,7 +517,8 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
     __shared__ __attribute__((aligned(16))) float tdz[T::floats];
     __shared__ __attribute__((aligned(16))) float tx[T::floats];
     __shared__ float red[kDwThreads / 64][KK1];
-    const int64_t plane = (int64_t)blockIdx.x / tpp, gix = (int64_t)blockIdx.x - plane * tpp;
+    const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+    const int64_t plane = blk / tpp, gix = blk - plane * tpp;
     const int64_t n = plane / C, c = plane - n * C;
     const int64_t tyg = gix / tiles_x, txg = gix - tyg * tiles_x;
     const int64_t ty0 = tyg * per, ty1 = min(ty0 + per, tiles_y);
@@ -1033,13 +1049,15 @@ bool dw_cba_fused_fits(const DwShape& sh) {
 }
 
 namespace {
-// Tiles per block of the fused CBA backward: as the weight gradient's (8
-// for K >= 7, else 4), halved while the grid would hold fewer than 2048
-// blocks.
+// Tiles per block of the fused CBA backward: 8 for K >= 5 (the block
+// reduces its K*K+1 weight-gradient sums once per block), 2 for K = 3 (more
+// blocks), halved while the grid would hold fewer than 2048 blocks.  At
+// 64 x 2048^2, 8 / 4 / 2 tiles: k7 1.72 / 1.95 / 2.36 ms, k5 1.01 / 1.04 /
+// 1.14 ms, k3 0.99 / 0.94 / 0.92 ms.
 int64_t dw_cba_per(const DwShape& sh, int64_t* tiles_x, int64_t* tiles_y, int64_t* tpp) {
     *tiles_x = (sh.Wi + kTW - 1) / kTW;
     *tiles_y = (sh.Hi + kTH - 1) / kTH;
-    int64_t per = sh.K >= 7 ? 8 : 4;
+    int64_t per = sh.K >= 5 ? 8 : 2;
     while (per > 1 && sh.N * sh.C * ((*tiles_y + per - 1) / per) * *tiles_x < 2048) per /= 2;
     *tpp = ((*tiles_y + per - 1) / per) * *tiles_x;
     return per;
