@@ -299,7 +299,8 @@ SOAR_API size_t soar_pw_cba_backward_workspace_bytes(int64_t N, int64_t C_in,
  * reaches HBM: z, dy and x are read once and dx written once after the
  * GroupNorm reduction pass.  Other shapes (or unaligned tensors with a
  * workspace large enough for it) run the two calls above with dz in the
- * workspace.  Flags: SOAR_GN_SILU, SOAR_GN_ACCUMULATE_DX.
+ * workspace; a call for dgamma / dbeta alone runs the GroupNorm backward
+ * only.  Flags: SOAR_GN_SILU, SOAR_GN_ACCUMULATE_DX.
  * Replaces: CBA backward as the autograd engine runs it, SiLUNode::backward
  * (src/nn/layers.cpp:749-771) + GroupNormNode::backward (:502-618) +
  * Conv2dNode::backward (:34-85) for CBA::forward (src/nn/blocks.cpp:442-445)
@@ -369,11 +370,12 @@ SOAR_API size_t soar_dw_cba_backward_workspace_bytes(
  * the same as soar_gn_silu_backward(dy, z, ..., dz, dgamma, dbeta) followed
  * by soar_dw_conv_backward(dz, x, weight, dx, dweight, NULL, ...).  For a
  * stride-1 convolution with "same" padding, pad = (K-1)*dil/2, a
- * configuration with a tiled kernel (K = 3, 5, 7; K = 3 with dil 2, 3, 5),
- * dx requested and at least SOAR_TUNE_DW_CBA_MIN samples x pixels, one
- * kernel forms dz over each tile and its halo in LDS and computes dx and
- * the weight-gradient partials from it, so dz never reaches HBM.  Other
- * calls run the two calls above with dz in the workspace.
+ * configuration with a tiled kernel (K = 3, 5, 7; K = 3 with dil 2, 3, 5)
+ * and at least SOAR_TUNE_DW_CBA_MIN samples x pixels, one kernel forms dz
+ * over each tile and its halo in LDS and computes dx and the
+ * weight-gradient partials from it, so dz never reaches HBM.  Other calls
+ * run the two calls above with dz in the workspace; a call for dgamma /
+ * dbeta alone runs the GroupNorm backward only.
  * Flags: SOAR_GN_SILU, SOAR_GN_ACCUMULATE_DX.
  * Replaces: CBA backward as the autograd engine runs it, SiLUNode::backward
  * (src/nn/layers.cpp:749-771) + GroupNormNode::backward (:502-618) +

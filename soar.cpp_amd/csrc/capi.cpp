@@ -773,8 +773,12 @@ SOAR_API int soar_pw_cba_backward(const float* dy, const float* z, const float* 
     if (!cba_layout(N, C_in, C_out, HW, G, t, &L))
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!dx && !dweight)  // the parameter gradients alone: the GroupNorm backward
+        return soar_gn_silu_backward(dy, z, gamma, beta, mean, rstd, mean_lo, nullptr, dgamma,
+                                     dbeta, N, C_out, HW, G, flags & SOAR_GN_SILU, workspace,
+                                     workspace_bytes, stream);
     const bool aligned = aligned16(dy) && aligned16(z) && aligned16(x) && aligned16(dx);
-    if (L.fused && aligned && (dx || dweight)) {
+    if (L.fused && aligned) {
         const size_t sb = (size_t)(N * G) * sizeof(float), cb = (size_t)C_out * sizeof(float);
         const size_t wb = (size_t)(C_in * C_out) * sizeof(float);
         if ((rc = check_dev(dy, (size_t)oe * 4, "dy")) || (rc = check_dev(z, (size_t)oe * 4, "z")) ||
@@ -817,11 +821,11 @@ SOAR_API int soar_pw_cba_backward(const float* dy, const float* z, const float* 
                     workspace_bytes, L.unfused_bytes,
                     L.fused ? "tensors not 16-byte aligned run the unfused path" : "unfused path");
     char* ws = static_cast<char*>(workspace);
-    float* dz = (dx || dweight) ? reinterpret_cast<float*>(ws) : nullptr;
+    float* dz = reinterpret_cast<float*>(ws);
     rc = soar_gn_silu_backward(dy, z, gamma, beta, mean, rstd, mean_lo, dz, dgamma, dbeta, N,
                                C_out, HW, G, flags & SOAR_GN_SILU, ws + L.dz_bytes, L.gn_bytes,
                                stream);
-    if (rc || !dz) return rc;
+    if (rc) return rc;
     return soar_pw_conv_backward(dz, x, weight, dx, dweight, nullptr, N, C_in, C_out, HW,
                                  flags & SOAR_GN_ACCUMULATE_DX, ws + L.dz_bytes + L.gn_bytes,
                                  L.pw_bytes, stream);
@@ -970,8 +974,12 @@ SOAR_API int soar_dw_cba_backward(const float* dy, const float* z, const float* 
     DwCbaLayout L;
     if (!dw_cba_layout(sh, G, t, &L))
         return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    if (!dx && !dweight)  // the parameter gradients alone: the GroupNorm backward
+        return soar_gn_silu_backward(dy, z, gamma, beta, mean, rstd, mean_lo, nullptr, dgamma,
+                                     dbeta, N, C, H_out * W_out, G, flags & SOAR_GN_SILU,
+                                     workspace, workspace_bytes, stream);
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (L.fused && dx) {
+    if (L.fused) {
         const size_t sb = (size_t)(N * G) * sizeof(float), cb = (size_t)C * sizeof(float);
         const size_t wb = (size_t)(C * K * K) * sizeof(float);
         if ((rc = check_dev(dy, (size_t)oe * 4, "dy")) || (rc = check_dev(z, (size_t)oe * 4, "z")) ||
@@ -979,7 +987,7 @@ SOAR_API int soar_dw_cba_backward(const float* dy, const float* z, const float* 
             (rc = check_dev(mean, sb, "mean")) || (rc = check_dev(rstd, sb, "rstd")) ||
             (rc = check_dev_opt(mean_lo, sb, "mean_lo")) ||
             (rc = check_dev_opt(gamma, cb, "gamma")) || (rc = check_dev_opt(beta, cb, "beta")) ||
-            (rc = check_dev(dx, (size_t)ie * 4, "dx")) ||
+            (rc = check_dev_opt(dx, (size_t)ie * 4, "dx")) ||
             (rc = check_dev_opt(dweight, wb, "dweight")) ||
             (rc = check_dev_opt(dgamma, cb, "dgamma")) || (rc = check_dev_opt(dbeta, cb, "dbeta")))
             return rc;
@@ -1012,11 +1020,11 @@ SOAR_API int soar_dw_cba_backward(const float* dy, const float* z, const float* 
         return fail(SOAR_EINVAL, "workspace of %zu bytes is smaller than the %zu this call needs",
                     workspace_bytes, L.unfused_bytes);
     char* ws = static_cast<char*>(workspace);
-    float* dz = (dx || dweight) ? reinterpret_cast<float*>(ws) : nullptr;
+    float* dz = reinterpret_cast<float*>(ws);
     rc = soar_gn_silu_backward(dy, z, gamma, beta, mean, rstd, mean_lo, dz, dgamma, dbeta, N, C,
                                H_out * W_out, G, flags & SOAR_GN_SILU, ws + L.dz_bytes,
                                L.gn_bytes, stream);
-    if (rc || !dz) return rc;
+    if (rc) return rc;
     return soar_dw_conv_backward(dz, x, weight, dx, dweight, nullptr, N, C, H_in, W_in, H_out,
                                  W_out, K, pad, stride, dil, flags & SOAR_GN_ACCUMULATE_DX,
                                  ws + L.dz_bytes + L.gn_bytes, L.dw_bytes, stream);

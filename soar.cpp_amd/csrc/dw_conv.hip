@@ -495,6 +495,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_bwd_small(
 //   dw, db partials += dz (x) x  dw_wgrad_body's FMAs
 // so dz never reaches HBM: z, dy and x are read once (with the halo) and
 // dx written once, instead of GroupNorm dx (3T) + dgrad (2T) + wgrad (2T).
+// dx or dw may be null (that product is skipped), not both.
 // With "same" padding, the dz region a dx tile reads and the x region the
 // weight gradient of that tile's dz reads are the same haloed tile (origin
 // (oy0 - pad, ox0 - pad)), so one fetch serves the three tensors.  dz is
@@ -594,6 +595,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
     for (int k = 0; k < KK1; ++k) sw[k] = 0.0f;
     const int t = threadIdx.x, ro = t >> 3, c0 = (t & 7) * kPer;
     const bool want_dw = dw != nullptr;  // block-uniform; without it `part` is null
+    const bool want_dx = dx != nullptr;
 
     fetch(ty0);
     for (int64_t ty = ty0; ty < ty1; ++ty) {
@@ -619,15 +621,17 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
         float acc[kPer];
 #pragma unroll
         for (int q = 0; q < kPer; ++q) acc[q] = 0.0f;
+        if (want_dx) {
 #pragma unroll
-        for (int ky = 0; ky < K; ++ky) {
-            float seg[T::SL4];
-            load_seg<K, 1, D>(tdz, ro + ky * D, c0, seg);
+            for (int ky = 0; ky < K; ++ky) {
+                float seg[T::SL4];
+                load_seg<K, 1, D>(tdz, ro + ky * D, c0, seg);
 #pragma unroll
-            for (int kx = 0; kx < K; ++kx)
+                for (int kx = 0; kx < K; ++kx)
 #pragma unroll
-                for (int q = 0; q < kPer; ++q)
-                    acc[q] = fmaf(wr[ky * K + kx], seg[q + kx * D], acc[q]);
+                    for (int q = 0; q < kPer; ++q)
+                        acc[q] = fmaf(wr[ky * K + kx], seg[q + kx * D], acc[q]);
+            }
         }
         // weight gradient: this tile's dz (the halo's interior) against x
         if (want_dw) {
@@ -649,7 +653,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
             }
         }
         const int64_t oy = ty * kTH + ro;
-        if (oy >= H) continue;
+        if (!want_dx || oy >= H) continue;
         float* orow = dx + plane * HW + oy * W;
         const int64_t ox = ox0 + c0;
         if (ox + kPer <= W && ((reinterpret_cast<uintptr_t>(orow + ox) & 15) == 0)) {

@@ -343,3 +343,62 @@ def test_pw_cba_backward_validation_without_gpu(L):
     assert _cba(L, 1, 8, 6, 0, 3) == soar_gn.SOAR_OK
     P = [None] * 13  # nothing requested
     assert L.soar_pw_cba_backward(*P, 1, 8, 6, 16, 3, 1, None, 0, None) == soar_gn.SOAR_OK
+
+
+def _dwcba(L, N, C, H, W, Ho, Wo, K, pad, S, D, G, flags=1, ws_bytes=0, outputs=True):
+    """soar_dw_cba_backward with NULL tensors (validation runs first)."""
+    P = [None] * 13
+    if outputs:
+        P[9] = 1  # a non-NULL dx, so the call is not a no-op (never dereferenced)
+    return L.soar_dw_cba_backward(*P, N, C, H, W, Ho, Wo, K, pad, S, D, G, flags, None,
+                                  ws_bytes, None)
+
+
+def test_dw_cba_backward_workspace_and_tuning(L):
+    assert soar_gn.tune_get(soar_gn.TUNE_DW_CBA_MIN) == 1 << 14
+    gn = (soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) + 255) // 256 * 256
+    H = W = 2048
+    # fused: the GroupNorm workspace, then one (K*K+1)-float partial per
+    # channel and block; 32 x 64 tiles, 2 per block at k3, 8 at k7
+    assert soar_gn.dw_cba_backward_workspace_bytes(1, 64, H, W, H, W, 3, 1, 1, 1, 16) == (
+        gn + 4 * (32 * 32) * 64 * 10)
+    assert soar_gn.dw_cba_backward_workspace_bytes(1, 64, H, W, H, W, 7, 3, 1, 1, 16) == (
+        gn + 4 * (8 * 32) * 64 * 50)
+    dz = 64 * H * W * 4
+    # outside the fused kernel (stride 2, padding other than "same", a K
+    # without a tiled kernel): dz, the GroupNorm workspace, the conv backward's
+    assert soar_gn.dw_cba_backward_workspace_bytes(1, 64, H, W, H // 2, W // 2, 3, 1, 2, 1,
+                                                   16) >= dz // 4
+    assert soar_gn.dw_cba_backward_workspace_bytes(1, 64, H, W, H - 2, W - 2, 3, 0, 1, 1,
+                                                   16) >= 64 * (H - 2) * (W - 2) * 4
+    assert soar_gn.dw_cba_backward_workspace_bytes(1, 64, H, W, H + 1, W + 1, 4, 2, 1, 1,
+                                                   16) >= 64 * (H + 1) * (W + 1) * 4
+    # below the size switch: unfused
+    assert soar_gn.dw_cba_backward_workspace_bytes(1, 64, 64, 64, 64, 64, 3, 1, 1, 1,
+                                                   16) >= 64 * 64 * 64 * 4
+    for bad in (-1, (1 << 40) + 1):
+        assert L.soar_gn_tune(soar_gn.TUNE_DW_CBA_MIN, bad) == soar_gn.SOAR_EINVAL
+    try:
+        soar_gn.tune(soar_gn.TUNE_DW_CBA_MIN, 1)
+        assert soar_gn.dw_cba_backward_workspace_bytes(1, 64, 64, 64, 64, 64, 3, 1, 1, 1,
+                                                       16) < 64 * 64 * 64 * 4
+        soar_gn.tune(soar_gn.TUNE_DW_CBA_MIN, 0)  # never fused
+        assert soar_gn.dw_cba_backward_workspace_bytes(1, 64, H, W, H, W, 3, 1, 1, 1, 16) > dz
+    finally:
+        soar_gn.tune(soar_gn.TUNE_DW_CBA_MIN, 1 << 14)
+    assert soar_gn.dw_cba_backward_workspace_bytes(1, 64, H, W, H, W, 3, 1, 1, 1, 6) == 0
+    assert soar_gn.dw_cba_backward_workspace_bytes(0, 64, H, W, H, W, 3, 1, 1, 1, 16) == 0
+
+
+def test_dw_cba_backward_validation_without_gpu(L):
+    args = (1, 8, 16, 16, 16, 16, 3, 1, 1, 1)
+    assert _dwcba(L, *args, 3) == soar_gn.SOAR_EINVAL
+    assert "divisible" in soar_gn.last_error()
+    assert _dwcba(L, *args, 4, flags=2) == soar_gn.SOAR_EINVAL  # no residual here
+    assert "flags" in soar_gn.last_error()
+    assert _dwcba(L, -1, *args[1:], 4) == soar_gn.SOAR_EINVAL
+    assert _dwcba(L, 1, 8, 16, 16, 16, 16, 0, 1, 1, 1, 4) == soar_gn.SOAR_EINVAL  # K = 0
+    assert _dwcba(L, 1, 8, 16, 16, 16, 16, 3, 1, 0, 1, 4) == soar_gn.SOAR_EINVAL  # stride 0
+    assert _dwcba(L, 0, *args[1:], 4) == soar_gn.SOAR_OK  # empty
+    assert _dwcba(L, *args, 4, outputs=False) == soar_gn.SOAR_OK  # nothing requested
+    assert _dwcba(L, *args, 4) == soar_gn.SOAR_ENODEV

@@ -16,7 +16,10 @@ checks, on the same device forward:
            fails;
   dgamma, dbeta: bit for bit equal to the stand-alone GroupNorm backward;
 and the fused result against the unfused entry-point path (TUNE_DW_CBA_MIN
-= 0): the same FMA order, so dx and dW agree bit for bit as well.
+= 0): the same FMA order, so dx agrees bit for bit, and so does dW on these
+grids, where both weight gradients take one tile per block (on larger grids
+the fused kernel groups 2 or 8 tiles per block where the stand-alone one
+groups 4 or 8, so dW may differ in its last bits).
 """
 import numpy as np
 import pytest
@@ -89,13 +92,11 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("N,C,H,W,K,D,G,silu,kind", CASES)
-def test_dw_cba_backward_matches_oracle(fused, oracle, N, C, H, W, K, D, G, silu, kind):
-    g = fused
+def _check_case(g, oracle, seed, N, C, H, W, K, D, G, silu, kind):
     pad = (K - 1) * D // 2
     print(f"dw_cba_backward N={N} C={C} {H}x{W} K={K} D={D} G={G} silu={silu} {kind}",
           flush=True)
-    x, w, gm, bt, dy = _inputs(N * 17 + C * 5 + H + K * 3 + D, N, C, H, W, K, kind)
+    x, w, gm, bt, dy = _inputs(seed, N, C, H, W, K, kind)
     xd, wd, gd, bd, dyd = dev(x), dev(w), dev(gm), dev(bt), dev(dy)
     z = g.dw_conv_forward(xd, wd, None, pad, 1, D)
     _, st = g.gn_silu_forward(z, gd, bd, G, eps=EPS, silu=silu)
@@ -118,9 +119,49 @@ def test_dw_cba_backward_matches_oracle(fused, oracle, N, C, H, W, K, D, G, silu
 
     # the unfused entry-point path: the same terms in the same order
     g.tune(g.TUNE_DW_CBA_MIN, 0)
-    ux, uw, ug, ub = g.dw_cba_backward(dyd, z, xd, wd, gd, bd, st, G, pad, 1, D, silu=silu)
+    try:
+        ux, uw, ug, ub = g.dw_cba_backward(dyd, z, xd, wd, gd, bd, st, G, pad, 1, D, silu=silu)
+    finally:
+        g.tune(g.TUNE_DW_CBA_MIN, 1)
     for a, b_, name in ((ux, dx, "dx"), (uw, dw, "dW"), (ug, dg, "dgamma"), (ub, db, "dbeta")):
         assert np.array_equal(host(a), host(b_)), name
+
+
+@pytest.mark.parametrize("N,C,H,W,K,D,G,silu,kind", CASES)
+def test_dw_cba_backward_matches_oracle(fused, oracle, N, C, H, W, K, D, G, silu, kind):
+    _check_case(fused, oracle, N * 17 + C * 5 + H + K * 3 + D, N, C, H, W, K, D, G, silu, kind)
+
+
+def _sweep_cases(n=20, seed=20261205):
+    """Seeded random depthwise CBA blocks: every tiled (K, dilation) with
+    "same" padding, 1-3 samples, 1-8 channels per group, planes from a
+    single row or column to several ragged tiles, both activations, data
+    with a large mean offset; then grids large enough that a block walks
+    2 and 4 tiles down its plane (ragged last group)."""
+    r = np.random.default_rng(seed)
+    kd = [(3, 1), (3, 2), (3, 3), (3, 5), (5, 1), (7, 1)]
+    out = []
+    for i in range(n):
+        K, D = kd[i % len(kd)]
+        G = int(r.choice([1, 2, 4, 8]))
+        C = G * int(r.integers(1, 9))
+        N = int(r.integers(1, 4))
+        H = int(r.choice([1, int(r.integers(2, 40)), int(r.integers(40, 140)),
+                          int(r.integers(40, 140))]))
+        W = int(r.choice([1, int(r.integers(2, 70)), int(r.integers(70, 200)),
+                          int(r.integers(70, 200))]))
+        silu = bool(r.integers(0, 2))
+        kind = "offset" if r.random() < 0.2 else "normal"
+        out.append((int(r.integers(1 << 30)), N, C, H, W, K, D, G, silu, kind))
+    out.append((11, 2, 64, 300, 260, 3, 1, 16, True, "normal"))   # 2 tiles per block
+    out.append((12, 2, 64, 520, 256, 7, 1, 16, True, "normal"))   # 4 tiles per block
+    return out
+
+
+@pytest.mark.parametrize("case", _sweep_cases(), ids=lambda c: "s{}-n{}c{}-{}x{}-k{}d{}".format(
+    c[0] % 1000, c[1], c[2], c[3], c[4], c[5], c[6]))
+def test_dw_cba_backward_seeded_sweep(fused, oracle, case):
+    _check_case(fused, oracle, *case)
 
 
 @pytest.mark.parametrize("want_dw,accumulate", [(True, True), (False, False), (False, True)])
@@ -156,6 +197,35 @@ def test_dw_cba_backward_outputs_and_accumulation(fused, oracle, want_dw, accumu
         u = host(u).astype(np.float64)
         t = p0.astype(np.float64) + u
         _within(host(got), t, 2.0 ** -24 * (np.abs(u) + np.abs(t)) + 1e-30, name)
+
+
+@pytest.mark.parametrize("K,D", [(3, 1), (7, 1), (3, 5)])
+def test_dw_cba_backward_single_outputs_in_queried_workspace(fused, K, D):
+    """dW alone runs the fused kernel without its dx product, dx alone
+    without its weight-gradient sums, and dgamma / dbeta alone the GroupNorm
+    backward only; each within the workspace the size query returns (the
+    fused path's, smaller than dz) and bit for bit the full call's outputs."""
+    import torch
+    g = fused
+    N, C, H, W, G = 2, 16, 70, 100, 4
+    pad = (K - 1) * D // 2
+    print(f"dw_cba_backward single outputs K={K} D={D}", flush=True)
+    x, w, gm, bt, dy = _inputs(57 + K + D, N, C, H, W, K)
+    xd, wd, gd, bd, dyd = dev(x), dev(w), dev(gm), dev(bt), dev(dy)
+    z = g.dw_conv_forward(xd, wd, None, pad, 1, D)
+    _, st = g.gn_silu_forward(z, gd, bd, G, eps=EPS)
+    need = g.dw_cba_backward_workspace_bytes(N, C, H, W, H, W, K, pad, 1, D, G)
+    assert 0 < need < N * C * H * W * 4
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    fx, fw, fg, fb = g.dw_cba_backward(dyd, z, xd, wd, gd, bd, st, G, pad, 1, D, ws=ws)
+    _, ow, _, _ = g.dw_cba_backward(dyd, z, xd, wd, gd, bd, st, G, pad, 1, D, want_dx=False,
+                                    want_params=False, ws=ws)
+    ox, _, _, _ = g.dw_cba_backward(dyd, z, xd, wd, gd, bd, st, G, pad, 1, D, want_dw=False,
+                                    want_params=False, ws=ws)
+    _, _, pg, pb = g.dw_cba_backward(dyd, z, xd, wd, gd, bd, st, G, pad, 1, D, want_dx=False,
+                                     want_dw=False, ws=ws)
+    for a, b_, name in ((ox, fx, "dx"), (ow, fw, "dW"), (pg, fg, "dgamma"), (pb, fb, "dbeta")):
+        assert np.array_equal(host(a), host(b_)), name
 
 
 def test_dw_cba_backward_unfused_shapes(gpu, oracle):

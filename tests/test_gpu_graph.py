@@ -192,3 +192,54 @@ def test_fused_cba_backward_graph_replays(gpu, C_in, C_out, H):
     reset()
     g = _capture(step)
     _replay_and_check(g, outs, ref, reset)
+
+
+@pytest.mark.parametrize("K,D,H", [(3, 1, 256), (7, 1, 192), (3, 5, 160)])
+def test_fused_dw_cba_backward_graph_replays(gpu, K, D, H):
+    """soar_dw_cba_backward on its fused kernel (the GroupNorm reduction and
+    finish, the fused dz / dx / dW kernel, the weight-gradient finish)
+    captured after the depthwise CBA forward (conv, GroupNorm + SiLU)."""
+    import torch
+    print(f"graph fused dw CBA backward K={K} D={D} H={H}", flush=True)
+    N, C, G = 1, 32, 8
+    pad = (K - 1) * D // 2
+    assert N * H * H >= gpu.tune_get(gpu.TUNE_DW_CBA_MIN)
+    gen = torch.Generator(device="cuda").manual_seed(H + K)
+    x = torch.randn((N, C, H, H), device="cuda", generator=gen)
+    dy = 1e-2 * torch.randn((N, C, H, H), device="cuda", generator=gen)
+    gamma = 0.5 + torch.rand(C, device="cuda", generator=gen)
+    beta = 0.1 * torch.randn(C, device="cuda", generator=gen)
+    w = (torch.rand((C, K, K), device="cuda", generator=gen) * 2 - 1) / K
+    z, y = (torch.empty((N, C, H, H), device="cuda") for _ in range(2))
+    mean, rstd, lo = (torch.empty(N * G, device="cuda") for _ in range(3))
+    dx = torch.empty_like(x)
+    dw = torch.zeros_like(w)
+    dg, db = torch.zeros(C, device="cuda"), torch.zeros(C, device="cuda")
+    fws = torch.empty(max(gpu.workspace_bytes(N, C, H * H, G), 1), dtype=torch.uint8,
+                      device="cuda")
+    bws = torch.empty(max(gpu.dw_cba_backward_workspace_bytes(N, C, H, H, H, H, K, pad, 1, D,
+                                                              G), 1),
+                      dtype=torch.uint8, device="cuda")
+    st = gpu.Stats(mean, rstd, lo)
+
+    def step():
+        gpu.dw_conv_forward(x, w, None, pad, 1, D, y=z)
+        gpu.gn_silu_forward(z, gamma, beta, G, eps=1e-5, y=y, mean=mean, rstd=rstd,
+                            mean_lo=lo, ws=fws)
+        gpu.dw_cba_backward(dy, z, x, w, gamma, beta, st, G, pad, 1, D, dx=dx, dweight=dw,
+                            dgamma=dg, dbeta=db, ws=bws)
+
+    outs = (z, y, mean, rstd, lo, dx, dw, dg, db)
+    step()
+    torch.cuda.synchronize()
+    ref = [t.clone() for t in outs]
+
+    def reset():
+        for t in (z, y, mean, rstd, lo, dx):
+            t.fill_(float("nan"))
+        for t in (dw, dg, db):
+            t.zero_()
+
+    reset()
+    g = _capture(step)
+    _replay_and_check(g, outs, ref, reset)

@@ -157,6 +157,25 @@ def test_pw_cba_backward_outputs_and_accumulation(fused, oracle, want_dx, want_d
         _within(host(got), t, 2.0 ** -24 * (np.abs(u) + np.abs(t)) + 1e-30, name)
 
 
+def test_pw_cba_backward_params_alone_in_queried_workspace(fused):
+    """dgamma / dbeta alone run the GroupNorm backward only, within the
+    workspace the size query returns (the fused path's, smaller than dz),
+    bit for bit the full call's."""
+    import torch
+    g = fused
+    N, C_in, C_out, HW, G = 1, 32, 64, 4096, 8
+    x, w, gm, bt, dy = _inputs(41, N, C_in, C_out, HW)
+    xd, wd, gd, bd, dyd = dev(x), dev(w), dev(gm), dev(bt), dev(dy)
+    z, _, st = g.pw_conv_gn_silu_forward(xd, wd, None, gd, bd, G, eps=EPS)
+    need = g.pw_cba_backward_workspace_bytes(N, C_in, C_out, HW, G)
+    assert 0 < need < N * C_out * HW * 4
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    _, _, fg, fb = g.pw_cba_backward(dyd, z, xd, wd, gd, bd, st, G, ws=ws)
+    _, _, pg, pb = g.pw_cba_backward(dyd, z, xd, wd, gd, bd, st, G, want_dx=False,
+                                     want_dw=False, ws=ws)
+    assert np.array_equal(host(pg), host(fg)) and np.array_equal(host(pb), host(fb))
+
+
 def test_pw_cba_backward_block_counts_agree(fused):
     """The pixel chunking (TUNE_PW_CBA_BLOCKS) changes only the order of the
     weight gradient's partial sums; dx is the same bit for bit."""
