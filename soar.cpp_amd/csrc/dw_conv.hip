@@ -52,9 +52,11 @@ constexpr int kDwThreads = 256;
 
 constexpr int round4(int v) { return (v + 3) / 4 * 4; }
 
-template <int K, int S, int D>
+// Input tile of a 32*RB x 64 output tile (RB output rows per thread).
+template <int K, int S, int D, int RB = 1>
 struct Tile {
-    static constexpr int IH = (kTH - 1) * S + (K - 1) * D + 1;   // input rows
+    static constexpr int TH = kTH * RB;                          // output rows
+    static constexpr int IH = (TH - 1) * S + (K - 1) * D + 1;    // input rows
     static constexpr int IW = (kTW - 1) * S + (K - 1) * D + 1;   // input columns
     static constexpr int SL = (kPer - 1) * S + (K - 1) * D + 1;  // a thread's row segment
     static constexpr int SL4 = round4(SL);
@@ -104,9 +106,9 @@ __device__ __forceinline__ void load_seg(const float* tile, int lrow, int c0,
 // A thread's share of a tile's input (element i = threadIdx.x + k*256 of
 // the LDS tile), fetched into registers so the loads of the next tile are
 // in flight while the current one is computed.
-template <int K, int S, int D>
+template <int K, int S, int D, int RB = 1>
 struct TilePrefetch {
-    static constexpr int NR = (Tile<K, S, D>::floats + kDwThreads - 1) / kDwThreads;
+    static constexpr int NR = (Tile<K, S, D, RB>::floats + kDwThreads - 1) / kDwThreads;
     float v[NR];
 
     // input rows [iy0, iy0 + IH) x columns [ix0, ix0 + IWP) of plane `ip`
@@ -116,7 +118,7 @@ struct TilePrefetch {
     // tile loop, where NR offsets would stay live in registers).
     __device__ __forceinline__ void fetch(const float* __restrict__ ip, int iy0, int ix0, int Hi,
                                           int Wi) {
-        using T = Tile<K, S, D>;
+        using T = Tile<K, S, D, RB>;
         int t = (int)threadIdx.x;
         asm volatile("" : "+v"(t));
 #pragma unroll
@@ -135,7 +137,7 @@ struct TilePrefetch {
 #pragma unroll
         for (int k = 0; k < NR; ++k) {
             const int i = (int)threadIdx.x + k * kDwThreads;
-            if (i < Tile<K, S, D>::floats) tile[i] = v[k];
+            if (i < Tile<K, S, D, RB>::floats) tile[i] = v[k];
         }
     }
 };
@@ -214,6 +216,96 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_conv(
     dw_conv_body<K, S, D, FLIP, ACC, BIAS>(in, w, bias, out, C, Hi, Wi, Ho, Wo, pad, tiles_x,
                                            tiles_y, tpp, per, xcd_block(blockIdx.x, gridDim.x),
                                            tile);
+}
+
+// Stride 1, dilation 1, with RB consecutive output rows per thread (a
+// 32*RB x 64 tile per step).  Input row i of a thread's window feeds its
+// output row j through tap row ky = i - j, so each K+2-float row segment is
+// read from LDS once for all RB rows: K + RB - 1 segment reads per RB x 8
+// outputs instead of K * RB (at K = 7 and RB = 4, 10 instead of 28), for
+// the same K*K FMAs per output.  Every output adds its terms in
+// dw_conv_body's order (bias, then ky, then kx ascending), so the results
+// are bit for bit the same.
+template <int K, bool FLIP, bool ACC, bool BIAS, int RB>
+__device__ __forceinline__ void dw_conv_rb_body(
+    const float* __restrict__ in, const float* __restrict__ w, const float* __restrict__ bias,
+    float* __restrict__ out, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo,
+    int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per, int64_t b,
+    float* __restrict__ tile) {
+    using T = Tile<K, 1, 1, RB>;
+    const int64_t plane = b / tpp, gix = b - plane * tpp;
+    const int64_t c = plane % C;
+    const int64_t tyg = gix / tiles_x, tx = gix - tyg * tiles_x;
+    const int64_t ty0 = tyg * per, ty1 = min(ty0 + per, tiles_y);
+    const int64_t ox0 = tx * kTW;
+    const float* ip = in + plane * Hi * Wi;
+    TilePrefetch<K, 1, 1, RB> pre;
+    const int ix0 = (int)(ox0 - pad), hi = (int)Hi, wi = (int)Wi;
+    pre.fetch(ip, (int)(ty0 * T::TH - pad), ix0, hi, wi);
+    float wr[K * K];
+#pragma unroll
+    for (int k = 0; k < K * K; ++k) wr[k] = w[c * K * K + (FLIP ? K * K - 1 - k : k)];
+    const float b0 = BIAS ? bias[c] : 0.0f;
+    const int t = threadIdx.x, r0 = (t >> 3) * RB, c0 = (t & 7) * kPer;
+    for (int64_t ty = ty0; ty < ty1; ++ty) {
+        if (ty > ty0) __syncthreads();  // the previous tile's LDS reads are done
+        pre.stash(tile);
+        __syncthreads();
+        if (ty + 1 < ty1) pre.fetch(ip, (int)((ty + 1) * T::TH - pad), ix0, hi, wi);
+        float acc[RB][kPer];
+#pragma unroll
+        for (int j = 0; j < RB; ++j)
+#pragma unroll
+            for (int q = 0; q < kPer; ++q) acc[j][q] = b0;
+#pragma unroll
+        for (int i = 0; i < RB + K - 1; ++i) {
+            float seg[T::SL4];
+            load_seg<K, 1, 1>(tile, r0 + i, c0, seg);
+#pragma unroll
+            for (int j = 0; j < RB; ++j) {
+                const int ky = i - j;
+                if (ky < 0 || ky >= K) continue;
+#pragma unroll
+                for (int kx = 0; kx < K; ++kx)
+#pragma unroll
+                    for (int q = 0; q < kPer; ++q)
+                        acc[j][q] = fmaf(wr[ky * K + kx], seg[q + kx], acc[j][q]);
+            }
+        }
+        const int64_t ox = ox0 + c0;
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int64_t oy = ty * T::TH + r0 + j;
+            if (oy >= Ho) break;
+            float* orow = out + plane * Ho * Wo + oy * Wo;
+            if (ox + kPer <= Wo && ((reinterpret_cast<uintptr_t>(orow + ox) & 15) == 0)) {
+                f4* o4 = reinterpret_cast<f4*>(orow + ox);
+                f4 v0 = {acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
+                f4 v1 = {acc[j][4], acc[j][5], acc[j][6], acc[j][7]};
+                if (ACC) {
+                    v0 += o4[0];
+                    v1 += o4[1];
+                }
+                o4[0] = v0;
+                o4[1] = v1;
+            } else {
+#pragma unroll
+                for (int q = 0; q < kPer; ++q)
+                    if (ox + q < Wo) orow[ox + q] = ACC ? orow[ox + q] + acc[j][q] : acc[j][q];
+            }
+        }
+    }
+}
+
+template <int K, bool FLIP, bool ACC, bool BIAS, int RB>
+__global__ __launch_bounds__(kDwThreads) void k_dw_conv_rb(
+    const float* __restrict__ in, const float* __restrict__ w, const float* __restrict__ bias,
+    float* __restrict__ out, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo,
+    int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per) {
+    __shared__ __attribute__((aligned(16))) float tile[Tile<K, 1, 1, RB>::floats];
+    dw_conv_rb_body<K, FLIP, ACC, BIAS, RB>(in, w, bias, out, C, Hi, Wi, Ho, Wo, pad, tiles_x,
+                                            tiles_y, tpp, per, xcd_block(blockIdx.x, gridDim.x),
+                                            tile);
 }
 
 // Weight and bias gradient partials: a block walks `per` tiles down one
@@ -841,6 +933,27 @@ bool fast_cfg(int64_t K, int64_t S, int64_t D, F&& f) {
     return false;
 }
 
+// Output rows per thread of the stride-1, dilation-1 forward / input
+// gradient: 2 for K = 3 and 5 (k_dw_conv_rb), 1 for K = 7 and elsewhere
+// (k_dw_conv).  At 64 x 2048^2, fwd / dgrad for 1 / 2 / 3 / 4 rows: k3
+// 0.432 / 0.414 / 0.465 / 0.432 and 0.449 / 0.425 / 0.477 / 0.443 ms, k5
+// 0.452 / 0.449 / 0.500 / 0.468 and 0.459 / 0.447 / 0.505 / 0.472 ms, k7
+// 0.605 / 0.612 / - / 0.653 ms (its FMAs, not its LDS reads, bound it, and
+// 4 rows take 215 VGPRs: 2 waves per SIMD).  Three rows leave a ragged
+// 96-row tile at the bottom of every power-of-two plane.
+template <int K>
+constexpr int conv_rb() {
+    return K == 3 || K == 5 ? 2 : 1;
+}
+
+int conv_rows_per_thread(int64_t K, int64_t S, int64_t D) {
+    if (S != 1 || D != 1) return 1;
+    if (K == 3) return conv_rb<3>();
+    if (K == 5) return conv_rb<5>();
+    if (K == 7) return conv_rb<7>();
+    return 1;
+}
+
 int64_t tiles_of(int64_t H, int64_t W, int64_t* tiles_x) {
     *tiles_x = (W + kTW - 1) / kTW;
     return ((H + kTH - 1) / kTH) * *tiles_x;
@@ -857,9 +970,9 @@ bool planes_fit_32(const DwShape& sh) {
 // while the grid would hold fewer than 4096 blocks.  Returns the tile
 // groups per plane; *per the rows per group.
 int64_t conv_groups(int64_t planes, int64_t H, int64_t W, int64_t* tiles_x, int64_t* tiles_y,
-                    int* per) {
+                    int* per, int64_t th = kTH) {
     *tiles_x = (W + kTW - 1) / kTW;
-    *tiles_y = (H + kTH - 1) / kTH;
+    *tiles_y = (H + th - 1) / th;
     int p = 4;
     while (p > 1 && planes * ((*tiles_y + p - 1) / p) * *tiles_x < 4096) p /= 2;
     *per = p;
@@ -918,15 +1031,23 @@ hipError_t launch_dw_forward(const DwShape& sh, const float* x, const float* w,
     if (sh.N * sh.C * sh.Ho * sh.Wo == 0) return hipSuccess;
     int64_t tiles_x = 0, tiles_y = 0;
     int per = 1;
-    const int64_t tpp = conv_groups(sh.N * sh.C, sh.Ho, sh.Wo, &tiles_x, &tiles_y, &per);
+    const int rb = conv_rows_per_thread(sh.K, sh.S, sh.D);
+    const int64_t tpp =
+        conv_groups(sh.N * sh.C, sh.Ho, sh.Wo, &tiles_x, &tiles_y, &per, (int64_t)kTH * rb);
     const int tok = prof_begin(s, "dw_conv");
     const bool fast = planes_fit_32(sh) && fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
         using CF = decltype(cf);
         bsel(bias != nullptr, [&](auto B) {
-            k_dw_conv<CF::k, CF::s, CF::d, false, false, B()>
-                <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
+            const dim3 grid((unsigned)(sh.N * sh.C * tpp));
+            if constexpr (CF::s == 1 && CF::d == 1 && conv_rb<CF::k>() > 1) {
+                k_dw_conv_rb<CF::k, false, false, B(), conv_rb<CF::k>()><<<grid, kDwThreads, 0, s>>>(
                     x, w, bias, y, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tiles_y,
                     tpp, per);
+            } else {
+                k_dw_conv<CF::k, CF::s, CF::d, false, false, B()><<<grid, kDwThreads, 0, s>>>(
+                    x, w, bias, y, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tiles_y,
+                    tpp, per);
+            }
         });
     });
     if (!fast)
@@ -985,15 +1106,25 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
             // dy with pad' = (K-1)*D - pad, producing dx's plane
             int64_t tiles_x = 0, tiles_y = 0;
             int per = 1;
-            const int64_t tpp = conv_groups(sh.N * sh.C, sh.Hi, sh.Wi, &tiles_x, &tiles_y, &per);
+            const int rb = conv_rows_per_thread(sh.K, sh.S, sh.D);
+            const int64_t tpp = conv_groups(sh.N * sh.C, sh.Hi, sh.Wi, &tiles_x, &tiles_y, &per,
+                                            (int64_t)kTH * rb);
             const int64_t padf = (sh.K - 1) * sh.D - sh.pad;
             done = planes_fit_32(sh) && fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
                 using CF = decltype(cf);
                 bsel(accumulate_dx, [&](auto A) {
-                    k_dw_conv<CF::k, CF::s, CF::d, true, A(), false>
-                        <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
-                            dy, w, nullptr, dx, sh.C, sh.Ho, sh.Wo, sh.Hi, sh.Wi, padf, tiles_x,
-                            tiles_y, tpp, per);
+                    const dim3 grid((unsigned)(sh.N * sh.C * tpp));
+                    if constexpr (CF::s == 1 && CF::d == 1 && conv_rb<CF::k>() > 1) {
+                        k_dw_conv_rb<CF::k, true, A(), false, conv_rb<CF::k>()>
+                            <<<grid, kDwThreads, 0, s>>>(dy, w, nullptr, dx, sh.C, sh.Ho, sh.Wo,
+                                                         sh.Hi, sh.Wi, padf, tiles_x, tiles_y,
+                                                         tpp, per);
+                    } else {
+                        k_dw_conv<CF::k, CF::s, CF::d, true, A(), false>
+                            <<<grid, kDwThreads, 0, s>>>(dy, w, nullptr, dx, sh.C, sh.Ho, sh.Wo,
+                                                         sh.Hi, sh.Wi, padf, tiles_x, tiles_y,
+                                                         tpp, per);
+                    }
                 });
             });
         }
