@@ -650,21 +650,32 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
     const float* zp = z + plane * HW;
     const float* gp = dy + plane * HW;
     const float* xp = x + plane * HW;
-    // the haloed tile's elements of this thread (TilePrefetch's order) for
-    // the three tensors, and which of them lie inside the image
+    // Consecutive tiles of the block share O = 2*PAD halo rows: local rows
+    // [kTH, kTH + O) of one tile are rows [0, O) of the next.  Their dz and
+    // x move to the top of the LDS tiles (through NS registers per thread)
+    // instead of being fetched and formed again, so after the first tile a
+    // block fetches and forms dz for its kTH new rows only.  The values are
+    // the same either way.
+    constexpr int O = 2 * PAD;
+    constexpr int NS = (O * T::IWP + kDwThreads - 1) / kDwThreads;
+    // this thread's elements (TilePrefetch's order) of local rows
+    // [lr0, IH) of the haloed tile for the three tensors, and which of them
+    // lie inside the image
     float pz[NR], pg[NR], px[NR];
     uint32_t inside = 0;
-    auto fetch = [&](int64_t ty) {
+    auto fetch = [&](int64_t ty, int lr0) {
         const int iy0 = (int)(ty * kTH) - PAD;
+        const int nel = (T::IH - lr0) * T::IWP, base = lr0 * T::IWP;
         int t = (int)threadIdx.x;
         asm volatile("" : "+v"(t));  // recomputed per tile, not hoisted
         inside = 0;
 #pragma unroll
         for (int k = 0; k < NR; ++k) {
             const int i = t + k * kDwThreads;
-            const int rw = i / T::IWP, col = i - rw * T::IWP;
+            const int li = base + i;
+            const int rw = li / T::IWP, col = li - rw * T::IWP;
             const int yy = iy0 + rw, xx = ix0 + col;
-            const bool in = i < T::floats && col < T::IW && (unsigned)yy < (unsigned)hi &&
+            const bool in = i < nel && col < T::IW && (unsigned)yy < (unsigned)hi &&
                             (unsigned)xx < (unsigned)wi;
             float a = 0.0f, g = 0.0f, v = 0.0f;
             if (in) {
@@ -689,25 +700,48 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
     const bool want_dw = dw != nullptr;  // block-uniform; without it `part` is null
     const bool want_dx = dx != nullptr;
 
-    fetch(ty0);
+    float sdz[NS], sx[NS];  // the shared halo rows on their way to the top
+    fetch(ty0, 0);
     for (int64_t ty = ty0; ty < ty1; ++ty) {
-        if (ty > ty0) __syncthreads();  // the previous tile's LDS reads are done
+        const int lr0 = ty > ty0 ? O : 0;
+        if (ty > ty0) {
+            __syncthreads();  // the previous tile's LDS reads are done
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+                const int j = t + k * kDwThreads;
+                if (j < O * T::IWP) {
+                    tdz[j] = sdz[k];
+                    tx[j] = sx[k];
+                }
+            }
+        }
+        const int nel = (T::IH - lr0) * T::IWP, base = lr0 * T::IWP;
 #pragma unroll
         for (int k = 0; k < NR; ++k) {
             const int i = t + k * kDwThreads;
-            if (i < T::floats) {
+            if (i < nel) {
                 float d = 0.0f;
                 if (inside & (1u << k)) {
                     const float xh = fmaf(pz[k] - mu, r, e);
                     const float dzs = SILU ? dsilu_fast(pg[k], fmaf(gm, xh, bt)) : pg[k];
                     d = fmaf(A, dzs, fmaf(Dc, xh, B));
                 }
-                tdz[i] = d;
-                tx[i] = px[k];
+                tdz[base + i] = d;
+                tx[base + i] = px[k];
             }
         }
         __syncthreads();
-        if (ty + 1 < ty1) fetch(ty + 1);
+        if (ty + 1 < ty1) {
+            fetch(ty + 1, O);
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+                const int j = t + k * kDwThreads;
+                if (j < O * T::IWP) {
+                    sdz[k] = tdz[kTH * T::IWP + j];
+                    sx[k] = tx[kTH * T::IWP + j];
+                }
+            }
+        }
 
         // dx for rows ty*32 + ro, columns ox0 + c0 .. +7
         float acc[kPer];
