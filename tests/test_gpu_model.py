@@ -157,6 +157,44 @@ def test_gradients_match_oracle(sm, wfile, weights):
     print("  worst gradient ratios:", [(f"{w[0]:.3f}", w[1]) for w in worst[:4]])
 
 
+def test_gradients_match_oracle_fused_cba(sm, wfile, weights):
+    """The same gate with the fused CBA backwards forced at every size
+    (TUNE_PW_CBA_MIN = TUNE_DW_CBA_MIN = 1): the host layer's pointwise and
+    depthwise CBA nodes then run soar_pw_cba_backward / soar_dw_cba_backward
+    on their fused kernels, which the default size switch keeps off at
+    64 x 64.  The library's kernel timers show that both ran."""
+    import soar_gn
+    print("case: forward_backward 64x64, fused CBA backwards", flush=True)
+    keys = (soar_gn.TUNE_PW_CBA_MIN, soar_gn.TUNE_DW_CBA_MIN)
+    old = {k: soar_gn.tune_get(k) for k in keys}
+
+    def launches():
+        return {e["kernel"]: e["launches"] for e in soar_gn.prof_summary()}
+
+    img, mask = sample(3)
+    m = model_with(sm, wfile)
+    try:
+        for k in keys:
+            soar_gn.tune(k, 1)
+        soar_gn.prof_enable(True)
+        before = launches()
+        met = m.forward_backward(img, mask)
+        after = launches()
+    finally:
+        soar_gn.prof_enable(False)
+        for k, v in old.items():
+            soar_gn.tune(k, v)
+    for name in ("pw_cba_bwd", "dw_cba_bwd"):
+        assert after.get(name, 0) > before.get(name, 0), name
+    lo, _, grads = smr.forward_backward(weights, img, mask)
+    assert abs(met["loss"] - lo.total) <= 1e-5 * abs(lo.total) + 1e-7
+    gnorm = np.sqrt(sum(float(np.sum(g.astype(np.float64) ** 2)) for g in grads.values()))
+    for i, (name, shape) in enumerate(m.tensors()):
+        g = m.read(i, grad=True, shape=shape)
+        d = float(np.linalg.norm(g.astype(np.float64) - grads[name]))
+        assert d <= 5e-5 * float(np.linalg.norm(grads[name])) + 1e-7 * gnorm, name
+
+
 @pytest.mark.parametrize("h,w,c", [(40, 50, 1), (64, 64, 3)])
 def test_gradients_other_shapes(sm, tmp_path, h, w, c):
     """Gradients through the reflection pad / crop (40 x 50) and with a
