@@ -153,9 +153,9 @@ struct TilePrefetch {
 // next).  They move to the top of the LDS tile through NS registers per
 // thread instead of being fetched again, so after its first tile a block
 // fetches its kTH new rows only.
-template <int K, int D>
+template <int K, int D, int RB = 1>
 struct HaloRows {
-    using T = Tile<K, 1, D>;
+    using T = Tile<K, 1, D, RB>;
     static constexpr int O = (K - 1) * D;
     static constexpr int NS = (O * T::IWP + kDwThreads - 1) / kDwThreads;
     float v[NS];
@@ -164,7 +164,7 @@ struct HaloRows {
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
             const int j = (int)threadIdx.x + k * kDwThreads;
-            if (j < O * T::IWP) v[k] = tile[kTH * T::IWP + j];
+            if (j < O * T::IWP) v[k] = tile[T::TH * T::IWP + j];
         }
     }
     // after every thread's reads of the previous tile are done
@@ -297,11 +297,20 @@ __device__ __forceinline__ void dw_conv_rb_body(
     for (int k = 0; k < K * K; ++k) wr[k] = w[c * K * K + (FLIP ? K * K - 1 - k : k)];
     const float b0 = BIAS ? bias[c] : 0.0f;
     const int t = threadIdx.x, r0 = (t >> 3) * RB, c0 = (t & 7) * kPer;
+    HaloRows<K, 1, RB> halo;
     for (int64_t ty = ty0; ty < ty1; ++ty) {
-        if (ty > ty0) __syncthreads();  // the previous tile's LDS reads are done
-        pre.stash(tile);
+        int lr0 = 0;
+        if (ty > ty0) {
+            __syncthreads();  // the previous tile's LDS reads are done
+            halo.put(tile);
+            lr0 = HaloRows<K, 1, RB>::O;
+        }
+        pre.stash(tile, lr0);
         __syncthreads();
-        if (ty + 1 < ty1) pre.fetch(ip, (int)((ty + 1) * T::TH - pad), ix0, hi, wi);
+        if (ty + 1 < ty1) {
+            pre.fetch(ip, (int)((ty + 1) * T::TH - pad), ix0, hi, wi, HaloRows<K, 1, RB>::O);
+            halo.take(tile);
+        }
         float acc[RB][kPer];
 #pragma unroll
         for (int j = 0; j < RB; ++j)
