@@ -293,7 +293,8 @@ SOAR_API size_t soar_pw_cba_backward_workspace_bytes(int64_t N, int64_t C_in,
  *   dgamma  += sum dz_gn * xhat, dbeta += sum dz_gn  [C_out]; each nullable
  * the same as soar_gn_silu_backward(dy, z, ..., dz, dgamma, dbeta) followed
  * by soar_pw_conv_backward(dz, x, weight, dx, dweight, NULL).  With
- * C_in, C_out <= 64, HW % 4 == 0 and at least SOAR_TUNE_PW_CBA_MIN samples
+ * C_in and C_out multiples of 8 up to 64, HW % 4 == 0 and at least
+ * SOAR_TUNE_PW_CBA_MIN samples
  * x pixels, one matrix-core kernel forms dz from z and dy in registers and
  * computes dx and the weight-gradient partials from it, so dz never
  * reaches HBM: z, dy and x are read once and dx written once after the

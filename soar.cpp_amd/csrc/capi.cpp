@@ -66,6 +66,8 @@ int device_count() {
 
 int require_device() {
     if (device_count() <= 0) return fail(SOAR_ENODEV, "no HIP device is visible");
+    void* p = nullptr;
+    (void)noalloc_scratch(&p);  // set-up; a failure is reported by the noalloc entry point
     return SOAR_OK;
 }
 

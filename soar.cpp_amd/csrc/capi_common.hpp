@@ -21,8 +21,16 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int ok();
 int hip_fail(hipError_t e, const char* what);
 int device_count();
-// SOAR_ENODEV when no HIP device is visible.
+// SOAR_ENODEV when no HIP device is visible.  Also the library's set-up on
+// the current device: its first call there resolves the device address of
+// soar_group_norm_backward_noalloc's static scratch (noalloc_scratch), so a
+// caller that has made any call on a device before capturing a graph runs
+// no symbol lookup inside the capture.
 int require_device();
+// Resolves (once per device) the current device's address of the static
+// scratch behind soar_group_norm_backward_noalloc; hipSuccess or the error
+// of the lookup.  Records no error message.
+hipError_t noalloc_scratch(void** out);
 // `p` must be device memory with at least `bytes` bytes from p to the end
 // of its allocation (a host pointer or a too-short buffer is rejected here
 // rather than faulting the GPU).

@@ -243,8 +243,8 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
 // Fused backward of a pointwise CBA block (pw_conv.hip): from the
 // GroupNorm input z, the upstream gradient dy and the convolution input x,
 // dx (=, or += with accumulate_dx) W^T dz and dw += sum dz x^T with dz the
-// GroupNorm(+SiLU) input gradient, never stored.  C_in, C_out <= 64, HW % 4
-// == 0, 16-byte aligned tensors (pw_cba_fused_fits).  The GroupNorm sums
+// GroupNorm(+SiLU) input gradient, never stored.  C_in, C_out multiples of 8
+// up to 64, HW % 4 == 0, 16-byte aligned tensors (pw_cba_fused_fits).  The GroupNorm sums
 // come from launch_backward_sums; block 0 also adds dgamma / dbeta.
 struct PwCbaArgs {
     const float* dy;  // [N][C_out][HW]

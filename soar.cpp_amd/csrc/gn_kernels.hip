@@ -916,10 +916,12 @@ __device__ __forceinline__ SmallMap small_map(int lg, int64_t cpg, int64_t HW) {
 }
 
 // Loads this thread's elements of a unit through a raw buffer descriptor on
-// the unit (wave-uniform base, 32-bit lane offset, the element step as a
-// scalar offset: no 64-bit address per element).  Lanes past the unit read
-// 0; lanes past their channel read the next channel's values, which the
-// callers never use (they test k < m.nk).
+// the unit (wave-uniform base, 32-bit lane offsets: no 64-bit address per
+// element).  The element step goes in the vector offset with the lane term,
+// since the descriptor's range check covers the vector offset only: elements
+// past the unit read 0 without touching memory; lanes past their channel
+// read the next channel's values, which the callers never use (they test
+// k < m.nk).
 constexpr int kSmallRsrcWord3 = 0x00020000;  // gfx9-family raw buffer descriptor
 
 template <int NV = kSmallPer>
@@ -932,7 +934,7 @@ __device__ __forceinline__ void small_load(const float* unit, int64_t M, int64_t
 #pragma unroll
     for (int k = 0; k < NV; ++k)
         v[k] = __builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(rs, vo, (k0 + k) * m.tpc * 4, 0));
+            float, __builtin_amdgcn_raw_buffer_load_b32(rs, vo + (k0 + k) * m.tpc * 4, 0, 0));
 }
 
 // Sums of (a, b) over the tpc threads of each channel; valid in the

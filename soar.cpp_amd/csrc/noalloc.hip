@@ -11,9 +11,13 @@
 //
 // Host code never passes `scratch` itself to a kernel or a copy: in host
 // code that name stands for a host-side shadow, not a device address.  The
-// device address comes from hipGetSymbolAddress, called once per device
-// with that device current (on the entry point's first call there), and is
-// kept per device.
+// device address comes from hipGetSymbolAddress, called once per device with
+// that device current, at the library's set-up there (require_device(), the
+// start of every entry point's first call on the device; so a caller that
+// has made any call on a device before it captures a graph runs no lookup
+// inside the capture), and is kept per device.  The lookup switches the
+// thread to relaxed capture mode, so even a first call made under capture
+// may load the scratch's code object.
 //
 // Every call on one device shares that device's array and leaves its
 // contents behind; no region needs to start at zero (each call writes every
@@ -21,6 +25,7 @@
 // one device (other streams, other threads) race on the array.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "capi_common.hpp"
@@ -34,33 +39,38 @@ constexpr int kMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
-
-// Device address of the current device's `scratch`.
-int scratch_for_current_device(void** out) {
-    using namespace soar::capi;
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-    if (dev < 0 || dev >= kMaxDevices)
-        return fail(SOAR_EINVAL, "device %d is beyond the %d the scratch table holds", dev,
-                    kMaxDevices);
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    if (!g_scratch_ptr[dev]) {
-        void* p = nullptr;
-        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || !p) {
-            (void)hipGetLastError();
-            return fail(SOAR_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s (%d)", dev,
-                        hipGetErrorString(e), (int)e);
-        }
-        g_scratch_ptr[dev] = p;
-    }
-    *out = g_scratch_ptr[dev];
-    return SOAR_OK;
-}
+std::atomic<void*> g_scratch_ptr[kMaxDevices] = {};
 
 }  // namespace
+
+namespace soar::capi {
+
+hipError_t noalloc_scratch(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+            (void)hipThreadExchangeStreamCaptureMode(&mode);
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            (void)hipThreadExchangeStreamCaptureMode(&mode);  // the caller's mode back
+            if (e != hipSuccess || !p) {
+                (void)hipGetLastError();
+                return e != hipSuccess ? e : hipErrorInvalidSymbol;
+            }
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return hipSuccess;
+}
+
+}  // namespace soar::capi
 
 extern "C" {
 
@@ -87,7 +97,10 @@ SOAR_API int soar_group_norm_backward_noalloc(const float* grad_out, const float
                     "(use soar_group_norm_backward)",
                     C, HW, need, kScratchBytes);
     void* ws = nullptr;
-    if ((rc = scratch_for_current_device(&ws))) return rc;
+    const hipError_t e = noalloc_scratch(&ws);
+    if (e != hipSuccess)
+        return fail(SOAR_EHIP, "hipGetSymbolAddress(scratch): %s (%d)", hipGetErrorString(e),
+                    (int)e);
     return gn_backward(grad_out, in, gamma, nullptr, saved_mean, saved_rstd, nullptr, grad_in,
                        grad_gamma, grad_beta, 1, (int64_t)C, (int64_t)HW, (int64_t)num_groups,
                        SOAR_GN_ACCUMULATE_DX, ws, kScratchBytes, stream, true);

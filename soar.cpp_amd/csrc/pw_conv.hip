@@ -834,20 +834,36 @@ __global__ __launch_bounds__(64 * kFbWaves, 1) void k_pw_cba_bwd(
     const bool want_dx = dx != nullptr, want_dw = part_w != nullptr;  // wave-uniform
     const auto ro = __builtin_amdgcn_make_buffer_rsrc(want_dx ? dx + n * C_in * HW : dx, (short)0,
                                                       (int)(C_in * HW * 4), kRsrcWord3);
-    const uint32_t hw4 = (uint32_t)HW * 4u, row8 = 8u * hw4;
+    const uint32_t hw4 = (uint32_t)HW * 4u;
     f4 sz[4 * TM], sg[4 * TM], sx[4 * TN];
+    // The descriptor's range check covers the vector offset only: the
+    // scalar offset is added to the address unchecked.  C_in and C_out are
+    // multiples of 8 (pw_cba_fused_fits), so an 8-row slot lies wholly
+    // inside or wholly past its tensor's rows; a slot past the end takes the
+    // last 8 rows' scalar offset instead, so no load leaves the sample.  Its
+    // values are harmless: a z/dy row past C_out has zero coefficients, so
+    // its dz is 0 (for finite inputs; a non-finite input makes its whole
+    // group NaN anyway), and an x row past C_in only reaches dW columns that
+    // are never stored.
+    const uint32_t zlim = (uint32_t)C_out - 8u, xlim = (uint32_t)C_in - 8u;
     auto gload = [&](int64_t p) {
         // lanes past the plane read its last 16 bytes (zeroed below)
         const uint32_t q = (uint32_t)min<int64_t>(p + scol, HW - 4);
         const uint32_t vo = (uint32_t)srow * hw4 + 4u * q;
+        // (the slots' scalar offsets are recomputed here on every step, a
+        // few scalar instructions, rather than hoisted into 16 registers)
+        uint32_t h4 = hw4, zl = zlim, xl = xlim;
+        asm volatile("" : "+s"(h4), "+s"(zl), "+s"(xl));
 #pragma unroll
         for (int sl = 0; sl < 4 * TM; ++sl) {
-            sz[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rz, vo, sl * row8, kNt));
-            sg[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rg, vo, sl * row8, kNt));
+            const uint32_t so = min(8u * sl, zl) * h4;
+            sz[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rz, vo, so, kNt));
+            sg[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rg, vo, so, kNt));
         }
 #pragma unroll
         for (int sl = 0; sl < 4 * TN; ++sl)
-            sx[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rx, vo, sl * row8, kNt));
+            sx[sl] = __builtin_bit_cast(
+                f4, __builtin_amdgcn_raw_buffer_load_b128(rx, vo, min(8u * sl, xl) * h4, kNt));
     };
 
     f16 accw[TM][TN], accx[TN];
@@ -925,12 +941,16 @@ __global__ __launch_bounds__(64 * kFbWaves, 1) void k_pw_cba_bwd(
                 accx[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(wt[t][s], b, accx[t], 0, 0, 0);
         }
         if (p + j < pend) {
-            // rows past C_in fall outside the descriptor and are dropped
+            // Row 4h + c of the tile: with C_in a multiple of 8 its test
+            // reduces to the wave-uniform 32 t + 8 (r / 4) < C_in, so the
+            // stores of rows past C_in are skipped by a scalar branch (the
+            // scalar row offset is not range-checked).
             const uint32_t vo = (uint32_t)(4 * h) * hw4 + 4u * (uint32_t)(p + j);
 #pragma unroll
             for (int t = 0; t < TN; ++t)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
+                    if (32 * t + 8 * (r >> 2) >= C_in) continue;
                     const uint32_t so = (uint32_t)tile_row(t, r, 0) * hw4;
                     float v = accx[t][r];
                     if (ACC)
@@ -1661,7 +1681,10 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
 
 bool pw_cba_fused_fits(int64_t C_in, int64_t C_out, int64_t HW) {
     // one dW tile; in-sample byte offsets (64 rows of HW floats) in 31 bits
-    return C_in >= 1 && C_in <= 64 && C_out >= 1 && C_out <= 64 && HW >= 4 && HW % 4 == 0 &&
+    // and whole 8-row slots: C_in and C_out multiples of 8 (k_pw_cba_bwd's
+    // loads and stores stay inside each sample's rows with scalar row offsets)
+    return C_in >= 8 && C_in <= 64 && C_in % 8 == 0 && C_out >= 8 && C_out <= 64 &&
+           C_out % 8 == 0 && HW >= 4 && HW % 4 == 0 &&
            HW <= ((int64_t)1 << 31) / 256 - 64;
 }
 

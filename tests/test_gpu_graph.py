@@ -243,3 +243,128 @@ def test_fused_dw_cba_backward_graph_replays(gpu, K, D, H):
     reset()
     g = _capture(step)
     _replay_and_check(g, outs, ref, reset)
+
+
+NOALLOC_CASES = [
+    # (C, HW, G): the multi-kernel path and the one-launch small-unit path
+    (16, 256 * 256, 4),
+    (16, 1024, 8),
+]
+
+
+def _noalloc_args(gpu, xd, dyd, gd, mean, rstd, gin, gw, gb, G, C, HW, stream):
+    import ctypes
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    return (P(dyd), P(xd), P(gd), P(mean), P(rstd), P(gin), P(gw), P(gb), G, C, HW,
+            ctypes.c_void_p(stream.cuda_stream))
+
+
+@pytest.mark.parametrize("C,HW,G", NOALLOC_CASES)
+def test_noalloc_backward_graph_replays(gpu, C, HW, G):
+    """soar_group_norm_backward_noalloc captured into a graph (its workspace
+    is the static scratch, whose address the library resolved at its set-up
+    on this device, before the capture) replays to the eager call's results
+    bit for bit, every time (the reference signature accumulates, so each
+    replay starts from the same initial gradients)."""
+    import torch
+    print(f"graph noalloc backward C={C} HW={HW} G={G}", flush=True)
+    L = gpu.lib()
+    gen = torch.Generator(device="cuda").manual_seed(C + HW)
+    x = torch.randn(C * HW, device="cuda", generator=gen)
+    dy = 1e-2 * torch.randn(C * HW, device="cuda", generator=gen)
+    gamma = 0.5 + torch.rand(C, device="cuda", generator=gen)
+    beta = 0.1 * torch.randn(C, device="cuda", generator=gen)
+    out = torch.empty_like(x)
+    mean, rstd = torch.empty(G, device="cuda"), torch.empty(G, device="cuda")
+    s0 = torch.cuda.current_stream()
+    import ctypes
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    gpu.check(L.soar_group_norm_forward(P(x), P(gamma), P(beta), P(out), P(mean), P(rstd), G, C,
+                                        HW, 1e-5, ctypes.c_void_p(s0.cuda_stream)))
+    gin = torch.empty_like(x)
+    gw, gb = torch.empty(C, device="cuda"), torch.empty(C, device="cuda")
+
+    def reset():
+        gin.fill_(0.25)
+        gw.fill_(-1.0)
+        gb.fill_(2.0)
+
+    reset()
+    gpu.check(L.soar_group_norm_backward_noalloc(
+        *_noalloc_args(gpu, x, dy, gamma, mean, rstd, gin, gw, gb, G, C, HW, s0)))
+    torch.cuda.synchronize()
+    ref = [t.clone() for t in (gin, gw, gb)]
+    reset()
+    s = torch.cuda.Stream()
+
+    def step():
+        gpu.check(L.soar_group_norm_backward_noalloc(
+            *_noalloc_args(gpu, x, dy, gamma, mean, rstd, gin, gw, gb, G, C, HW, s)))
+
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    _replay_and_check(g, (gin, gw, gb), ref, reset)
+
+
+_FIRST_CALL_UNDER_CAPTURE = r"""
+import ctypes, sys
+import torch
+sys.path.insert(0, sys.argv[1])
+import soar_gn as g
+L = g.lib()
+C, HW, G, eps = 16, 64 * 64, 4, 1e-5
+gen = torch.Generator(device="cuda").manual_seed(5)
+x = torch.randn(C * HW, device="cuda", generator=gen)
+dy = 1e-2 * torch.randn(C * HW, device="cuda", generator=gen)
+gamma = 0.5 + torch.rand(C, device="cuda", generator=gen)
+# saved statistics from torch: no library call before the capture
+xg = x.view(G, -1).double()
+mean = xg.mean(1).float()
+rstd = (1.0 / torch.sqrt(xg.var(1, unbiased=False) + eps)).float()
+bufs = [torch.zeros(C * HW, device="cuda"), torch.zeros(C, device="cuda"),
+        torch.zeros(C, device="cuda")]
+P = lambda t: ctypes.c_void_p(t.data_ptr())
+def call(name, stream, outs):
+    return getattr(L, name)(P(dy), P(x), P(gamma), P(mean), P(rstd), *map(P, outs), G, C, HW,
+                            ctypes.c_void_p(stream.cuda_stream))
+s = torch.cuda.Stream()
+s.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+rc = []
+with torch.cuda.graph(graph, stream=s):
+    rc.append(call("soar_group_norm_backward_noalloc", s, bufs))
+torch.cuda.current_stream().wait_stream(s)
+assert rc == [0], (rc, g.last_error())
+ref = [torch.zeros_like(t) for t in bufs]
+assert call("soar_group_norm_backward", torch.cuda.current_stream(), ref) == 0
+for rep in range(3):
+    for t in bufs:
+        t.zero_()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    for a, b in zip(bufs, ref):
+        assert torch.equal(a, b), rep
+print("FIRST_CALL_UNDER_CAPTURE_OK", flush=True)
+"""
+
+
+def test_noalloc_first_library_call_under_capture(gpu):
+    """In a fresh process whose first call into the library is
+    soar_group_norm_backward_noalloc inside a graph capture (so the scratch
+    address is looked up during the capture, in relaxed capture mode): the
+    capture succeeds and its replays equal soar_group_norm_backward's
+    result bit for bit."""
+    import os
+    import subprocess
+    import sys
+    from conftest import ROOT
+    print("noalloc first library call under capture (child process)", flush=True)
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_UNDER_CAPTURE,
+                        os.path.join(ROOT, "soar.cpp_amd")], capture_output=True, text=True,
+                       timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and "FIRST_CALL_UNDER_CAPTURE_OK" in r.stdout, r.stderr[-2000:]

@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 
 from conftest import GOLDEN
+from gn_checks import check_dx_correction
 
 pytestmark = pytest.mark.gpu
 
@@ -251,6 +252,11 @@ def _full_size_check(gpu, oracle, N, C, HW, G, kind, seed, samples=200000, backw
     M = (C // G) * HW
     dxt = rt[u] * (gh[c] * dz - (S1[u] + xhat * S2[u]) / M)
     assert_vals(host(dx).reshape(-1)[idx], dxt, "sampled dx")
+    # every element: the correction terms with the main term taken out
+    mean_eff = host(st.mean).astype(np.float64) + host(st.mean_lo).astype(np.float64)
+    worst = check_dx_correction(dx, x, dy, gamma, beta, mean_eff, host(st.rstd), G,
+                                f"{kind} dx")
+    print(f"dx correction: largest error / bound {worst:.3f}", flush=True)
 
 
 def test_full_size_config3(gpu, oracle):
@@ -538,6 +544,12 @@ def test_reference_signature_large_mean(gpu, oracle, C, HW, G):
         M = (C // G) * HW
         want = rt[u] * (g64[c] * dy[idx] - (S1[u] + xhat * S2[u]) / M)
         assert_vals(host(gin)[idx], want, "sampled grad_in")
+    # every element: the correction terms with the main term taken out (the
+    # backward recovers the mean's residual itself: the oracle's mean here)
+    worst = check_dx_correction(gin.view(1, C, HW), dev(x).view(1, C, HW),
+                                dev(dy).view(1, C, HW), dev(gamma), dev(beta), mt, host(rstd),
+                                G, "large-mean grad_in", silu=False)
+    print(f"grad_in correction: largest error / bound {worst:.3f}", flush=True)
 
 
 @pytest.mark.parametrize("want", ["gamma", "beta", "in+gamma", "in+beta", "in", "all"])
@@ -835,7 +847,8 @@ def test_full_size_config4_chain(gpu, oracle):
     vanishes; the output at sampled indices against closed forms; for the
     first and last blocks, dx at sampled indices against the closed form
     dx = rstd*(gamma*dz - (S1 + xhat*S2)/M) + dy on oracle statistics and
-    sums."""
+    sums; for every block, every element's correction terms
+    (gn_checks.check_dx_correction)."""
     import torch
     N, C, HW, G, B = 2, 128, 1024 * 1024, 32, 6
     seed = 20261201 + 4
@@ -897,5 +910,11 @@ def test_full_size_config4_chain(gpu, oracle):
             dz = gs * sg * (1 + z * (1 - sg))
             want = rt[u] * (g64[c] * dz - (S1[u] + xhat * S2[u]) / M) + gs
             assert_vals(host(dx).reshape(-1)[idx], want, f"block {b} sampled dx")
+        # every element of every block: the correction terms
+        st = stats[b]
+        mean_eff = host(st.mean).astype(np.float64) + host(st.mean_lo).astype(np.float64)
+        worst = check_dx_correction(dx, acts[b], g_in, *params[b], mean_eff, host(st.rstd), G,
+                                    f"block {b} dx", residual=True)
+        print(f"block {b} dx correction: largest error / bound {worst:.3f}", flush=True)
         del xh, gh
         g_in = dx

@@ -71,7 +71,8 @@ CASES = [
     (1, 16, 24, 1028, 4, False, "normal"),    # no SiLU, TM = TN = 1
     (1, 24, 8, 4100, 2, True, "normal"),      # C_out = 8: rows 8..31 of the tile are zero
     (3, 40, 64, 1000, 16, True, "normal"),    # three samples, partial x tile
-    (1, 64, 20, 2048, 4, True, "normal"),     # TM = 1, TN = 2
+    (1, 64, 24, 2048, 4, True, "normal"),     # TM = 1, TN = 2
+    (1, 64, 20, 2048, 4, True, "normal"),     # C_out % 8 != 0: the unfused calls
     (1, 8, 64, 516, 32, True, "normal"),      # TM = 2, TN = 1, one 4-pixel lane past a step
     (1, 32, 32, 4096, 8, True, "offset"),     # large mean offset: the mean residual
     (1, 32, 32, 4096, 8, False, "offset"),
@@ -196,6 +197,56 @@ def test_pw_cba_backward_block_counts_agree(fused):
     again = [host(t) for t in g.pw_cba_backward(dyd, z, xd, wd, gd, bd, st, G)]
     for a, b in zip(again, outs[-1]):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("N,C_in,C_out,HW,G,accumulate", [
+    (3, 40, 48, 2048, 8, False),   # TM = TN = 2: rows 40..63 of x/dx, 48..63 of z/dy past the end
+    (3, 40, 48, 2048, 8, True),    # dx read back and added to (the same rows)
+    (2, 24, 40, 1028, 4, False),   # TN = 1: rows 24..31 of dx past the end
+])
+def test_pw_cba_backward_tile_rows_stay_in_their_sample(fused, oracle, N, C_in, C_out, HW, G,
+                                                        accumulate):
+    """Tile rows past C_in / C_out neither read nor write outside their own
+    sample: dy, z, x and dx sit at the start of larger buffers whose tails
+    hold a sentinel (NaN behind the inputs, so a row read past the last
+    sample's z or dy would turn dx into NaN; a finite marker behind dx,
+    which must stay bit for bit), and dx of every sample, the first rows of
+    samples 1.. included, matches the float64 convolution backward of the
+    unfused dz."""
+    import torch
+    g = fused
+    print(f"pw_cba_backward sentinel tails N={N} C_in={C_in} C_out={C_out} HW={HW} G={G} "
+          f"acc={accumulate}", flush=True)
+    # the fused kernel takes the shape: its workspace holds no dz
+    assert g.pw_cba_backward_workspace_bytes(N, C_in, C_out, HW, G) < N * C_out * HW * 4
+    x, w, gm, bt, dy = _inputs(N * 7 + C_in + 3 * C_out, N, C_in, C_out, HW)
+    xd, wd, gd, bd, dyd = dev(x), dev(w), dev(gm), dev(bt), dev(dy)
+    z, _, st = g.pw_conv_gn_silu_forward(xd, wd, None, gd, bd, G, eps=EPS)
+    dz, _, _ = g.gn_silu_backward(dyd, z, gd, bd, st, G)
+    tail = 64 * HW  # more than any tile's rows past the last sample
+
+    def in_big(t, fill):
+        n = t.numel()
+        big = torch.full((n + tail,), fill, dtype=torch.float32, device="cuda")
+        big[:n].copy_(t.reshape(-1))
+        return big, big[:n].view(t.shape)
+
+    _, dyv = in_big(dyd, float("nan"))
+    _, zv = in_big(z, float("nan"))
+    _, xv = in_big(xd, float("nan"))
+    dx0 = np.random.default_rng(9).standard_normal((N, C_in, HW)).astype(np.float32)
+    dxb, dxv = in_big(dev(dx0) if accumulate else torch.zeros((N, C_in, HW), device="cuda"),
+                      12345.0)
+    dx, _, _, _ = g.pw_cba_backward(dyv, zv, xv, wd, gd, bd, st, G, dx=dxv, want_dw=False,
+                                    accumulate_dx=accumulate)
+    torch.cuda.synchronize()
+    assert dx.data_ptr() == dxb.data_ptr()
+    assert bool((dxb[N * C_in * HW:] == 12345.0).all()), "dx stores past the last sample"
+    dzh = host(dz)
+    tx, _, _ = oracle.conv1x1_bwd_f64(dzh, x, w, N, C_in, C_out, HW, want=("dx",))
+    bx, _, _ = bwd_bounds(dzh, x, w)
+    t = tx + (dx0.reshape(-1).astype(np.float64) if accumulate else 0.0)
+    _within(host(dx), t, bx.reshape(-1) + (2.0 ** -23) * np.abs(t), "dx")
 
 
 def test_pw_cba_backward_full_size(gpu):

@@ -199,7 +199,8 @@ def test_cba_sweep_vs_oracle(gpu, oracle, pw_tuning, case):
         i = int(np.argmax(ratio))
         assert ratio[i] <= 1.0, f"{name} err {err[i]:.3e} > bound {bnd.reshape(-1)[i]:.3e}"
     # the fused CBA backward (soar_pw_cba_backward; its fused kernel wherever
-    # C_in, C_out <= 64 and HW % 4 == 0, else the two calls above), against
+    # C_in and C_out are multiples of 8 up to 64 and HW % 4 == 0, else the
+    # two calls above), against
     # the stand-alone GroupNorm backward's dz on its multi-kernel path, whose
     # reduction and dx arithmetic the fused kernel shares
     keys = (gpu.TUNE_PW_CBA_MIN, gpu.TUNE_SMALL_UNIT, gpu.TUNE_FOLD_MAX)
