@@ -270,7 +270,7 @@ TensorPtr PixelShuffle::forward(const TensorPtr& input) {
     const int64_t r = (int64_t)r_, r2 = r * r;
     const int64_t C_in = input->ndim() == 4 ? input->dim(1) : input->dim(0);
     if (r <= 0 || C_in % r2 != 0)
-        throw ShapeError("PixelShuffle channels must be divisible by upscale_factor squared");
+        throw ShapeError("PixelShuffle: the channel count is not a multiple of r*r");
     to_dev(input);
     Shape os = input->shape();
     const size_t cdim = input->ndim() == 4 ? 1 : 0;
@@ -379,7 +379,7 @@ TensorPtr convex_combination(const TensorPtr& g, const TensorPtr& a, const Tenso
 }
 
 TensorPtr concat_channels(const std::vector<TensorPtr>& tensors) {
-    if (tensors.empty()) throw ShapeError("Cannot concatenate empty tensor list");
+    if (tensors.empty()) throw ShapeError("concat: no tensors given");
     const TensorPtr& t0 = tensors[0];
     const bool batched = t0->ndim() == 4;
     if (t0->ndim() != 3 && !batched)

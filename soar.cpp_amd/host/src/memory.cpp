@@ -11,7 +11,7 @@ Result<SubAllocation> DeviceSlabSubAllocator::sub_allocate(size_t size_bytes, Sh
                                                            DataType dtype,
                                                            std::string_view tag) noexcept {
     if (size_bytes == 0)
-        return Status(StatusCode::InvalidArgument, "Cannot allocate 0 bytes in device slab");
+        return Status(StatusCode::InvalidArgument, "device slab: a sub-allocation needs a nonzero size");
     const size_t aligned = (current_offset_ + alignment_ - 1) & ~(alignment_ - 1);
     if (aligned < current_offset_ || aligned > total_capacity_ ||
         total_capacity_ - aligned < size_bytes)

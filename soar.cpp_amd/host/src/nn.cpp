@@ -33,7 +33,7 @@ TensorPtr Module::forward(const TensorPtr& input) {
 }
 
 TensorPtr Module::forward(const std::vector<TensorPtr>& inputs) {
-    if (inputs.empty()) throw ShapeError("Forward called with empty input vector");
+    if (inputs.empty()) throw ShapeError("Module::forward needs at least one input tensor");
     return forward(inputs[0]);
 }
 
