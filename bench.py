@@ -64,7 +64,9 @@ STREAM_CONFIGS = {"stream_read": "read", "stream_copy": "copy", "stream_2r1w": "
                   # 16 MiB (a 1 GiB NCHW tensor), at the tensor's plane stride and
                   # with the stride padded by 4 KiB
                   "stream_planes_read": "planes_read", "stream_planes_copy": "planes_copy",
-                  "stream_planes_copy_pad4k": "planes_copy_pad"}
+                  "stream_planes_copy_pad4k": "planes_copy_pad",
+                  # all four patterns in several launch shapes + the runtime's D2D copy
+                  "stream_sweep": "sweep"}
 
 # Depthwise convolutions of the CBA blocks at 1x64x2048^2, forward + backward
 # (dx, dW, db): name -> (K, stride, dilation); pad = dilation*(K-1)/2
@@ -119,7 +121,27 @@ def parse():
                     help="train configs: skip the second, graph-off handle (for tracing)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a plain 1 GiB copy kernel (for rocprofv3 counter scaling)")
+    ap.add_argument("--tune", action="append", default=[], metavar="NAME=VALUE",
+                    help="set a library tuning key before the run (soar_gn_tune; NAME is a "
+                         "TUNE_* name of soar_gn.py without the prefix, e.g. NT_LOAD=3); "
+                         "repeatable, recorded in the JSON line's config")
     return ap.parse_args()
+
+
+def apply_tuning(args):
+    """Sets the --tune keys; returns {name: value} for the JSON line."""
+    if not args.tune:
+        return {}
+    import soar_gn as gn
+    out = {}
+    for item in args.tune:
+        name, _, value = item.partition("=")
+        key = getattr(gn, "TUNE_" + name.strip().upper(), None)
+        if key is None or not value:
+            sys.exit(f"--tune {item!r}: expected NAME=VALUE with NAME a soar_gn TUNE_* key")
+        gn.tune(key, int(value))
+        out[name.strip().upper()] = int(value)
+    return out
 
 
 def traffic_from_profiles(config):
@@ -417,6 +439,82 @@ class CBADwStep:
                             dweight=self.dw, want_db=False, ws=self.ws)
 
 
+# Other launch shapes of the four streaming patterns (libsoar_synth.so
+# soar_synth_stream_shape) and the runtime's D2D copy, over the same 1 GiB
+# buffers: is the library's shape or the memory system the ceiling?
+# (label, threads, loads in flight, chunk floats or None, persistent grid or
+# None, non-temporal loads)
+SWEEP_SHAPES = [
+    ("chunk 256 thr x 4 loads, 8192 floats, nt loads", 256, 4, 8192, None, True),
+    ("chunk 512 thr x 2 loads, 4096 floats", 512, 2, 4096, None, False),
+    ("chunk 1024 thr x 4 loads, 32768 floats", 1024, 4, 32768, None, False),
+    ("chunk 1024 thr x 4 loads, 32768 floats, nt loads", 1024, 4, 32768, None, True),
+    ("persistent 4 blocks/CU x 256 thr x 8 loads, nt loads", 256, 8, None, 1024, True),
+    ("persistent 2 blocks/CU x 1024 thr x 8 loads", 1024, 8, None, 512, False),
+]
+
+
+def bench_stream_sweep(args):
+    """Every streaming pattern in the library's shape (k_stream), in the
+    SWEEP_SHAPES, and the copy through hipMemcpyAsync D2D: median of the
+    launches between hipEvents, GB/s of the pattern's tensor bytes.
+    value = the best copy (1R1W) rate found."""
+    import torch
+    import soar_gn as gn
+    n = 1 << 28
+    a = torch.empty(n, device="cuda")
+    b = torch.empty(n, device="cuda")
+    out = torch.empty(n, device="cuda")
+    gn.synth_normal(a, SEED, 1)
+    gn.synth_normal(b, SEED, 4)
+    gn.synth_normal(out, SEED, 2)
+
+    def time_it(launch):
+        for _ in range(args.warmup):
+            launch()
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.steps)]
+        for e0, e1 in evs:
+            e0.record()
+            launch()
+            e1.record()
+        torch.cuda.synchronize()
+        ms = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
+        return ms[len(ms) // 2]
+
+    results = {}
+    t0 = time.perf_counter()
+    for pattern in ("read", "copy", "2r1w", "2r"):
+        passes = gn.STREAM_KINDS[pattern][1]
+        rows = {}
+
+        def add(label, launch):
+            ms = time_it(launch)
+            rows[label] = {"ms": round(ms, 4), "GBps": round(passes * n * 4 / (ms * 1e-3) / 1e9, 1)}
+
+        add("library shape: chunk 256 thr x 4 loads, 8192 floats (k_stream)",
+            lambda: gn.synth_stream(pattern, a, b, out))
+        for label, thr, loads, chunk, grid, ntl in SWEEP_SHAPES:
+            add(label, lambda: gn.synth_stream_shape(pattern, a, b, out, thr, loads, chunk=chunk,
+                                                     grid=grid, ntl=ntl))
+        if pattern == "copy":
+            add("runtime hipMemcpyAsync D2D", lambda: gn.synth_memcpy_d2d(out, a))
+        results[pattern] = rows
+    wall = time.perf_counter() - t0
+    best = {p: max(r.values(), key=lambda v: v["GBps"]) for p, r in results.items()}
+    value = best["copy"]["GBps"]
+    print(json.dumps({
+        "metric": "stream_sweep: best copy (1R1W) GB/s over 1 GiB buffers, across launch shapes",
+        "value": value, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": best["copy"]["ms"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic N(0,1)",
+        "config": {"workload": "streaming patterns read / copy / 2r1w / 2r in several launch "
+                               "shapes and the runtime's D2D copy, 1 GiB buffers"},
+        "frac_of_peak": round(value / PEAK_GBS, 4), "wall_s_timed": round(wall, 4),
+        "best": {p: v["GBps"] for p, v in best.items()}, "shapes": results}), flush=True)
+
+
 def bench_stream(args):
     """Streaming ceilings: one synth_stream kernel over 1 GiB buffers, each
     launch between hipEvents on the launch stream; value = tensor bytes of
@@ -496,7 +594,9 @@ def cpu_baseline():
     (the reference's idiom, src/main.cpp:675-682).  Config 3 is sampled as
     4 of its 16 groups (the same per-group size, 1/4 of the tensor) to keep
     the run within seconds; config 1 runs at full size (forward only, its
-    workload)."""
+    workload); configs 2 (forward) and 5 (forward + backward, its stress
+    input) run one full-size group each (groups are independent, so a
+    group's time scales to the config by its group count)."""
     import numpy as np
     import soar_oracle as orc
     eps = float(np.float32(1e-5))
@@ -504,12 +604,12 @@ def cpu_baseline():
     core = min(allowed)
     os.sched_setaffinity(0, {core})
     try:
-        def run(N, C, HW, G, seed):
+        def run(N, C, HW, G, seed, stress=False, backward=True):
             n = N * C * HW
-            x = orc.fill_normal(n, seed, 1)
+            x = orc.fill_stress(n, seed) if stress else orc.fill_normal(n, seed, 1)
             gamma = orc.fill_uniform(C, seed, 2, 0.5, 1.5)
             beta = orc.fill_normal(C, seed, 3, 0.0, 0.1)
-            dy = orc.fill_normal(n, seed, 4, 0.0, 1e-2)
+            dy = orc.fill_normal(n, seed, 4, 0.0, 1e-2) if backward else None
             orc.ref_gn_silu_fwd_bwd_f32(x, gamma, beta, dy, N, C, HW, G, eps)  # warm-up
             runs = [orc.ref_gn_silu_fwd_bwd_f32(x, gamma, beta, dy, N, C, HW, G, eps)
                     for _ in range(3)]
@@ -517,15 +617,25 @@ def cpu_baseline():
             return n, med("fwd_s"), med("bwd_s"), sorted(r["fwd_s"] + r["bwd_s"] for r in runs)[1]
 
         n3, f3, b3, t3 = run(1, 16, 2048 * 2048, 4, SEED + 3)
-        n1, f1, _, _ = run(1, 32, 256 * 256, 8, SEED + 1)
+        n1, f1, _, _ = run(1, 32, 256 * 256, 8, SEED + 1, backward=False)
+        n2, f2, _, _ = run(1, 4, 2048 * 2048, 1, SEED + 2, backward=False)
+        n5, f5, b5, t5 = run(1, 4, 2048 * 2048, 1, SEED + 5, stress=True)
     finally:
         os.sched_setaffinity(0, allowed)
+    group = "one full-size group (N=1 C=4 H=W=2048 G=1), same method"
     return {"value": round(8 * n3 * 4 / t3 / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"config 3 as N=1 C=16 H=W=2048 G=4 (4 of its 16 groups), fwd+bwd, "
                       f"1 warm-up + median of 3 on CPU {core} ({_host_cpu()}, {len(allowed)} "
                       f"CPUs allowed): fwd {f3 * 1e3:.1f} ms, bwd {b3 * 1e3:.1f} ms",
             "config1_fwd": {"ms": round(f1 * 1e3, 3), "GBps": round(3 * n1 * 4 / f1 / 1e9, 3),
                             "shape": "N=1 C=32 H=W=256 G=8, full size, same method"},
+            "config2_fwd": {"group_ms": round(f2 * 1e3, 2), "config_ms": round(8 * f2 * 1e3, 1),
+                            "GBps": round(3 * n2 * 4 / f2 / 1e9, 3), "shape": group + ", x 8 groups"},
+            "config5": {"group_fwd_ms": round(f5 * 1e3, 2), "group_bwd_ms": round(b5 * 1e3, 2),
+                        "config_ms": round(4 * t5 * 1e3, 1),
+                        "GBps": round(8 * n5 * 4 / t5 / 1e9, 3),
+                        "shape": "one full-size group of the stress input (N=1 C=4 H=W=2048 "
+                                 "G=1), same method, x 4 groups"},
             "config3_fwd_ms": round(f3 * 1e3, 2), "config3_bwd_ms": round(b3 * 1e3, 2)}
 
 
@@ -662,6 +772,10 @@ def main():
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has "
               "no multi-GPU path.", file=sys.stderr)
         sys.exit(2)
+    # torch first: its HIP runtime is the one the process uses, as in the
+    # tests (loading libsoar_gn.so first would bind /opt/rocm's instead)
+    import torch  # noqa: F401
+    tuning = apply_tuning(args)
     if args.config in TRAIN_CONFIGS or args.config in STREAM_CONFIGS or \
             args.config in PREDICT_CONFIGS:
         import torch
@@ -671,6 +785,8 @@ def main():
             bench_train(args)
         elif args.config in PREDICT_CONFIGS:
             bench_predict(args)
+        elif args.config == "stream_sweep":
+            bench_stream_sweep(args)
         else:
             bench_stream(args)
         return
@@ -810,6 +926,8 @@ def main():
                "eps": 1e-5, "blocks": blocks, "residual": residual,
                **({"C_in": CBA_C_IN} if args.config.startswith("cba_pw") else {}),
                "algorithmic_bytes_per_step": alg}
+    if tuning:
+        cfg["tuning"] = tuning
     out = {
         "metric": METRIC if args.config == "cfg3" else f"{args.config} achieved HBM GB/s",
         "value": round(value, 1),

@@ -472,7 +472,8 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
 #define SOAR_TUNE_NT_STORE 3 /* 1: non-temporal stores for y / dx          */
 #define SOAR_TUNE_BATCH_MB 4 /* MiB per two-pass batch, 0 = whole tensor   */
 #define SOAR_TUNE_STREAMS 5  /* 2: overlap batches on a helper stream      */
-#define SOAR_TUNE_NT_LOAD 6  /* 1: non-temporal loads in the second passes */
+#define SOAR_TUNE_NT_LOAD 6  /* non-temporal loads: bit 0 in the second    */
+                             /* passes, bit 1 in the first passes          */
 #define SOAR_TUNE_CHUNK2 7   /* elements per block-chunk of apply / dx     */
 #define SOAR_TUNE_PW_CHUNK 8 /* pixels per wave of the pointwise conv      */
                              /* (multiple of 128)                          */
@@ -516,6 +517,11 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
                                 /* kernel runs from this many samples x  */
                                 /* pixels on (0 = never); changes its    */
                                 /* workspace size                        */
+#define SOAR_TUNE_NT_TAIL_MB 19 /* with SOAR_TUNE_NT_LOAD bit 1: MiB the  */
+                                /* statistics / reduction passes read    */
+                                /* last with cached loads (the second    */
+                                /* pass walks in reverse and reads them  */
+                                /* first, from the MALL)                 */
 SOAR_API int soar_gn_tune(int key, int64_t value);
 SOAR_API int64_t soar_gn_tune_get(int key);
 

@@ -1348,7 +1348,8 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
             g_tune.streams = (int)value;
             return ok();
         case SOAR_TUNE_NT_LOAD:
-            if (value != 0 && value != 1) return fail(SOAR_EINVAL, "nt_load must be 0 or 1");
+            if (value < 0 || value > 3)
+                return fail(SOAR_EINVAL, "nt_load must be 0..3 (bit 0: second passes, bit 1: first passes)");
             g_tune.nt_load = (int)value;
             return ok();
         case SOAR_TUNE_PW_CHUNK:
@@ -1403,6 +1404,11 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
                 return fail(SOAR_EINVAL, "dw_cba_min must be in [0, 2^40]");
             g_tune.dw_cba_min = value;
             return ok();
+        case SOAR_TUNE_NT_TAIL_MB:
+            if (value < 0 || value > (1 << 20))
+                return fail(SOAR_EINVAL, "nt_tail_mb must be in [0, 2^20]");
+            g_tune.nt_tail_mb = value;
+            return ok();
         default:
             return fail(SOAR_EINVAL, "unknown tuning key %d", key);
     }
@@ -1429,6 +1435,7 @@ SOAR_API int64_t soar_gn_tune_get(int key) {
         case SOAR_TUNE_PW_CBA_MIN: return g_tune.pw_cba_min;
         case SOAR_TUNE_PW_CBA_BLOCKS: return g_tune.pw_cba_blocks;
         case SOAR_TUNE_DW_CBA_MIN: return g_tune.dw_cba_min;
+        case SOAR_TUNE_NT_TAIL_MB: return g_tune.nt_tail_mb;
         default: return -1;
     }
 }

@@ -33,6 +33,8 @@ struct Plan {
     int64_t upb_bwd = 0;     // units per backward batch
     bool vec4 = false;       // float4 path (HW % 4 == 0 and 16-byte pointers)
     int loads = 4;           // 128-bit loads in flight per thread, first passes
+    bool ntl1 = false;       // non-temporal loads in the first passes ...
+    int64_t nt_tail = 0;     // ... except for their last this many bytes read
 };
 
 // Defaults measured on MI355X at 1x64x2048^2, fwd+bwd per step:
@@ -45,6 +47,14 @@ struct Plan {
 //   same batches pipelined on two streams                1.740 / 1.628 /
 //                                                        1.544 ms
 // (each extra pair of launches costs ~2.7 us, more than the MALL saves).
+// Later, with the first passes' load policy (one box, two runs each):
+//   cached loads in the first passes                     1.429 ms
+//   non-temporal loads there                             1.395 ms
+//   non-temporal except the last 64 / 128 / 192 / 256 /
+//   384 MiB read, which the reverse-walking second pass
+//   then reads from the MALL                             1.393 / 1.384 /
+//                                                        1.378 / 1.369 /
+//                                                        1.390 ms
 struct Tuning {
     int64_t chunk = 8192;     // floats per block-chunk, multiple of 1024
     int64_t chunk2 = 4096;    // same for the second passes (128-thread
@@ -55,7 +65,12 @@ struct Tuning {
     int64_t batch_mb = 0;     // MiB read by the first pass of a batch
                               // (0: the whole tensor is one batch)
     int streams = 1;          // 2: pipeline batches over a helper stream
-    int nt_load = 1;          // non-temporal loads in the second passes
+    int nt_load = 3;          // non-temporal loads: bit 0 in the second passes
+                              // (apply / dx), bit 1 in the first passes
+                              // (statistics / reduction) except their tail:
+    int64_t nt_tail_mb = 256; // MiB the first passes read last with cached
+                              // loads (the reverse-walking second pass reads
+                              // them first, from the MALL)
     int64_t pw_chunk = 1024;  // pixels per wave of the pointwise convolution
                               // (multiple of 128); also its GroupNorm
                               // partials' chunk

@@ -249,13 +249,15 @@ __global__ __launch_bounds__(kWideThreads) void k_stats_finish_wide(
 // issued whole before its shift K (the first element) is taken from it, so
 // a chunk of 8 vectors per thread costs 8 / U memory round trips.  The
 // elements reach each of the four accumulation lanes in index order for
-// every U, so the partials do not depend on U.
-template <bool VEC, int U>
+// every U, so the partials do not depend on U.  NTL: chunk blocks b <
+// nt_end use non-temporal loads (the rest, the tail that the reverse-walking
+// second pass reads first, use cached loads, so it is still in the MALL).
+template <bool VEC, int U, bool NTL>
 __global__ __launch_bounds__(kThreads) void k_stats(
     const float* __restrict__ x, double2* __restrict__ part, float* __restrict__ mean,
     float* __restrict__ rstd, float* __restrict__ mean_lo, float* __restrict__ lo_ws,
     int64_t HW, int64_t chunk, int64_t cpp, int64_t cpg, int64_t fin_u0, int64_t fin_nu,
-    int64_t block0, float eps) {
+    int64_t block0, float eps, int64_t nt_end) {
     __shared__ double lds[4 * kWaves];
     if ((int64_t)blockIdx.x < fin_nu) {
         finish_stats_unit(fin_u0 + blockIdx.x, part, mean, rstd, mean_lo, lo_ws, HW, chunk,
@@ -274,6 +276,8 @@ __global__ __launch_bounds__(kThreads) void k_stats(
     if (VEC) {
         const f4* p4 = reinterpret_cast<const f4*>(p);
         const int64_t n4 = ck.len >> 2;
+        auto walk = [&](auto ntl) {
+        constexpr bool L = decltype(ntl)::value;
 #define SOAR_ACC4(v)                                                     \
     {                                                                    \
         float d0 = (v).x - K, d1 = (v).y - K, d2 = (v).z - K,            \
@@ -288,13 +292,13 @@ __global__ __launch_bounds__(kThreads) void k_stats(
             if (i + (U - 1) * kThreads < n4) {
                 f4 v[U];
 #pragma unroll
-                for (int u = 0; u < U; ++u) v[u] = p4[i + u * kThreads];
+                for (int u = 0; u < U; ++u) v[u] = load4<L>(&p4[i + u * kThreads]);
                 K = v[0].x;
 #pragma unroll
                 for (int u = 0; u < U; ++u) SOAR_ACC4(v[u]);
                 i += U * kThreads;
             } else {
-                const f4 v = p4[i];
+                const f4 v = load4<L>(&p4[i]);
                 K = v.x;
                 SOAR_ACC4(v);
                 i += kThreads;
@@ -303,14 +307,19 @@ __global__ __launch_bounds__(kThreads) void k_stats(
         for (; i + (U - 1) * kThreads < n4; i += U * kThreads) {
             f4 v[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) v[u] = p4[i + u * kThreads];
+            for (int u = 0; u < U; ++u) v[u] = load4<L>(&p4[i + u * kThreads]);
 #pragma unroll
             for (int u = 0; u < U; ++u) SOAR_ACC4(v[u]);
         }
         for (; i < n4; i += kThreads) {
-            f4 a = p4[i];
+            f4 a = load4<L>(&p4[i]);
             SOAR_ACC4(a);
         }
+        };
+        if (NTL && b < nt_end)
+            walk(std::true_type{});
+        else
+            walk(std::false_type{});
 #undef SOAR_ACC4
     } else {
         int64_t i = t;
@@ -694,8 +703,9 @@ __device__ void finish_bwd_unit(int64_t u, const double2* __restrict__ part,
 // LOREC: mean residual recovery (see finish_bwd_unit); also writes the
 // chunk sums of x - mu to part_x.  Only without SiLU, so dz = dy.
 // U: 128-bit loads in flight per thread, U/2 of each tensor (elements reach
-// each accumulation lane in index order for every U).
-template <bool VEC, bool SILU, bool LOREC, int U>
+// each accumulation lane in index order for every U).  NTL: chunk blocks
+// b < nt_end use non-temporal loads (as in k_stats).
+template <bool VEC, bool SILU, bool LOREC, int U, bool NTL>
 __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ gamma, const float* __restrict__ beta,
@@ -704,7 +714,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
     double* __restrict__ part_x, float* __restrict__ lo_ws,
     double2* __restrict__ plane_sums, double2* __restrict__ unit_sums, int64_t C, int64_t G,
     int64_t cpg, int64_t HW, int64_t chunk, int64_t cpp, int64_t fin_u0, int64_t fin_nu,
-    int64_t block0) {
+    int64_t block0, int64_t nt_end) {
     static_assert(!(SILU && LOREC), "the mean residual is recovered only when dz = dy");
     __shared__ float lds[2 * kWaves];
     __shared__ double ldsd[2 * kThreads];
@@ -734,13 +744,15 @@ __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
         const f4* g4 = reinterpret_cast<const f4*>(dy + base);
         const int64_t n4 = ck.len >> 2;
         constexpr int UH = U / 2;
+        auto walk = [&](auto ntl) {
+        constexpr bool L = decltype(ntl)::value;
         int64_t i = t;
         for (; i + (UH - 1) * kThreads < n4; i += UH * kThreads) {
             f4 v[UH], g[UH];
 #pragma unroll
             for (int u = 0; u < UH; ++u) {
-                v[u] = x4[i + u * kThreads];
-                g[u] = g4[i + u * kThreads];
+                v[u] = load4<L>(&x4[i + u * kThreads]);
+                g[u] = load4<L>(&g4[i + u * kThreads]);
             }
 #pragma unroll
             for (int u = 0; u < UH; ++u) {
@@ -749,10 +761,15 @@ __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
             }
         }
         for (; i < n4; i += kThreads) {
-            f4 v0 = x4[i], g0 = g4[i];
+            f4 v0 = load4<L>(&x4[i]), g0 = load4<L>(&g4[i]);
             acc(g0.x, v0.x, sa0, sb0, sc0); acc(g0.y, v0.y, sa1, sb1, sc1);
             acc(g0.z, v0.z, sa0, sb0, sc0); acc(g0.w, v0.w, sa1, sb1, sc1);
         }
+        };
+        if (NTL && b < nt_end)
+            walk(std::true_type{});
+        else
+            walk(std::false_type{});
     } else {
         const float* xp = x + base;
         const float* gp = dy + base;
@@ -1283,7 +1300,7 @@ void launch_apply(const Plan& p, const Tuning& t, const FwdArgs& a, const float*
         bsel(silu, [&](auto S) {
             bsel(res, [&](auto R) {
                 bsel(t.nt_store != 0, [&](auto N) {
-                    bsel(V() && t.nt_load != 0, [&](auto L) {
+                    bsel(V() && (t.nt_load & 1) != 0, [&](auto L) {
                         bsel(fold, [&](auto F) {
                             k_apply<V(), S(), R(), N(), L(), F()><<<grid, kThreads2, 0, s>>>(
                                 a.x, a.gamma, a.beta, a.mean, a.rstd, lo, a.y, p.C, p.G, p.cpg,
@@ -1311,7 +1328,7 @@ void launch_dx(const Plan& p, const Tuning& t, const BwdArgs& a, const double2* 
             bsel(res, [&](auto R) {
                 bsel(accum, [&](auto A) {
                     bsel(t.nt_store != 0 && !accum, [&](auto N) {
-                        bsel(V() && t.nt_load != 0, [&](auto L) {
+                        bsel(V() && (t.nt_load & 1) != 0, [&](auto L) {
                             bsel(fold, [&](auto F) {
                                 k_bwd_dx<V(), S(), R(), A(), N(), L(), F()>
                                     <<<grid, kThreads2, 0, s>>>(
@@ -1334,6 +1351,17 @@ bool fold_ok(const Plan& p, const Tuning& t, int64_t upb) {
            upb >= p.units;
 }
 
+// First chunk block of units [u0, u0 + nu) that loads with cached loads:
+// the tail of about p.nt_tail bytes (over `tensors` tensors) that the
+// reverse-walking second pass reads first, so it is still in the MALL.
+// Blocks before it use non-temporal loads when p.ntl1 is set.
+int64_t nt_end(const Plan& p, int64_t u0, int64_t nu, int tensors) {
+    const int64_t bpu = p.cpg * p.cpp;
+    const int64_t per_block = p.chunk * 4 * tensors;
+    const int64_t tail = std::min(nu * bpu, (p.nt_tail + per_block - 1) / per_block);
+    return (u0 + nu) * bpu - tail;
+}
+
 // First-pass kernels: `fin_nu` finish blocks for units [fin_u0, fin_u0 +
 // fin_nu), then chunk blocks for units [u0, u0 + nu).
 void launch_stats(const Plan& p, const FwdArgs& a, const WsView& w, int64_t fin_u0,
@@ -1350,9 +1378,11 @@ void launch_stats(const Plan& p, const FwdArgs& a, const WsView& w, int64_t fin_
     }
     bsel(p.vec4, [&](auto V) {
         loads_sel(p.loads, [&](auto U) {
-            k_stats<V(), U()><<<grid, kThreads, 0, s>>>(
-                a.x, w.part, a.mean, a.rstd, a.mean_lo, w.lo, p.HW, p.chunk, p.cpp, p.cpg,
-                fin_u0, fin_nu, u0 * bpu, a.eps);
+            bsel(V() && p.ntl1, [&](auto L) {
+                k_stats<V(), U(), L()><<<grid, kThreads, 0, s>>>(
+                    a.x, w.part, a.mean, a.rstd, a.mean_lo, w.lo, p.HW, p.chunk, p.cpp, p.cpg,
+                    fin_u0, fin_nu, u0 * bpu, a.eps, nt_end(p, u0, nu, 1));
+            });
         });
     });
     prof_end(s, tok);
@@ -1371,10 +1401,12 @@ void launch_reduce(const Plan& p, const BwdArgs& a, const WsView& w, int64_t fin
                                      : "gn_bwd_finish");
     auto go = [&](auto V, auto S, auto L) {
         loads_sel(p.loads, [&](auto U) {
-        k_bwd_reduce<V(), S(), L(), U()><<<grid, kThreads, 0, s>>>(
-            a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, w.part, w.part_x, w.lo,
-            w.plane_sums, w.unit_sums, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp, fin_u0, fin_nu,
-            u0 * bpu);
+            bsel(V() && p.ntl1, [&](auto NL) {
+                k_bwd_reduce<V(), S(), L(), U(), NL()><<<grid, kThreads, 0, s>>>(
+                    a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, w.part, w.part_x,
+                    w.lo, w.plane_sums, w.unit_sums, p.C, p.G, p.cpg, p.HW, p.chunk, p.cpp,
+                    fin_u0, fin_nu, u0 * bpu, nt_end(p, u0, nu, 2));
+            });
         });
     };
     bsel(p.vec4, [&](auto V) {
@@ -1465,6 +1497,8 @@ bool make_plan(int64_t N, int64_t C, int64_t HW, int64_t G, const Tuning& t, Pla
     if (p->blocks + p->units > 0x7fffffff || C > 0x7fffffff) return false;
     p->vec4 = (HW % 4) == 0;
     p->loads = t.loads;
+    p->ntl1 = (t.nt_load & 2) != 0;
+    p->nt_tail = t.nt_tail_mb << 20;
     p->upb_fwd = units_per_batch(*p, t, 1);
     p->upb_bwd = units_per_batch(*p, t, 2);
     return true;

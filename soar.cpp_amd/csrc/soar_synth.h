@@ -34,6 +34,18 @@ int soar_synth_copy(const float* src, float* dst, int64_t n, void* stream);
  * unchanged (they write it only if a block's sum is exactly 1234.5). */
 int soar_synth_stream(int kind, const float* a, const float* b, float* out,
                       int64_t n, void* stream);
+/* The same four kinds in other launch shapes (test of whether the library's
+ * shape or the memory system sets the ceilings): threads per block (64..1024,
+ * a multiple of 64), loads = float4 loads in flight per thread and tensor
+ * (2, 4 or 8), ntl / nts = non-temporal loads / stores.  persistent = 0:
+ * one block per chunk of `size` floats (a multiple of 4, at least 4 *
+ * threads); persistent = 1: a grid of `size` blocks striding over the
+ * buffers in tiles of loads * threads float4s. */
+int soar_synth_stream_shape(int kind, int persistent, int threads, int loads, int64_t size,
+                            int ntl, int nts, const float* a, const float* b, float* out,
+                            int64_t n, void* stream);
+/* dst = src through the runtime's device-to-device hipMemcpyAsync. */
+int soar_synth_memcpy_d2d(float* dst, const float* src, int64_t n, void* stream);
 /* The pointwise convolution's access pattern over 64 planes of plane_floats
  * floats (a multiple of 1024), plane c at a + c * stride_floats (buffers of
  * 64 * stride_floats floats, 16-byte aligned): each block walks a 1024-float

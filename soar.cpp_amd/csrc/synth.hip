@@ -3,6 +3,8 @@
 // element: value i of a stream depends only on (seed, stream id, i).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "soar_synth.h"
 
 namespace {
@@ -154,6 +156,125 @@ __global__ __launch_bounds__(256) void k_planes(const float* __restrict__ a,
     if (!WRITE && s == 1234.5f) out[w0 + t] = s;
 }
 
+// Streaming patterns in other launch shapes than the library's, to test
+// whether its shape or the memory system sets the ceilings above (same
+// kinds and sums as k_stream):
+//   k_shape_chunk    one block of blockDim.x threads per chunk of chunk4
+//                    float4s, U float4 loads (per tensor) in flight per
+//                    thread;
+//   k_shape_persist  a grid of gridDim.x blocks striding over the buffer in
+//                    tiles of U * blockDim.x float4s.
+// NTL / NTS: non-temporal loads / stores.  Every access is below n4.
+template <bool NTL>
+__device__ __forceinline__ f4 ld_s(const f4* p) {
+    if (NTL) return __builtin_nontemporal_load(p);
+    return *p;
+}
+
+template <bool NTS>
+__device__ __forceinline__ void st_s(f4 v, f4* p) {
+    if (NTS)
+        __builtin_nontemporal_store(v, p);
+    else
+        *p = v;
+}
+
+template <int KIND, int U, bool NTL, bool NTS>
+__device__ __forceinline__ void shape_tile(const f4* __restrict__ a, const f4* __restrict__ b,
+                                           f4* __restrict__ out, int64_t i, int T, float& s) {
+    f4 v[U], w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        v[u] = ld_s<NTL>(&a[i + (int64_t)u * T]);
+        if (KIND >= 2) w[u] = ld_s<NTL>(&b[i + (int64_t)u * T]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        if (KIND == 0) s += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+        if (KIND == 3) s += (v[u].x * w[u].x + v[u].y * w[u].y) + (v[u].z * w[u].z + v[u].w * w[u].w);
+        if (KIND == 1) st_s<NTS>(v[u], &out[i + (int64_t)u * T]);
+        if (KIND == 2) st_s<NTS>(v[u] + w[u], &out[i + (int64_t)u * T]);
+    }
+}
+
+template <int KIND, bool NTS>
+__device__ __forceinline__ void shape_one(const f4* __restrict__ a, const f4* __restrict__ b,
+                                          f4* __restrict__ out, int64_t i, float& s) {
+    const f4 v = a[i];
+    if (KIND == 0) s += (v.x + v.y) + (v.z + v.w);
+    if (KIND == 3) {
+        const f4 w = b[i];
+        s += (v.x * w.x + v.y * w.y) + (v.z * w.z + v.w * w.w);
+    }
+    if (KIND == 1) st_s<NTS>(v, &out[i]);
+    if (KIND == 2) st_s<NTS>(v + b[i], &out[i]);
+}
+
+template <int KIND, int U, bool NTL, bool NTS>
+__global__ __launch_bounds__(1024) void k_shape_chunk(const f4* __restrict__ a,
+                                                      const f4* __restrict__ b,
+                                                      f4* __restrict__ out, int64_t n4,
+                                                      int64_t chunk4) {
+    const int T = blockDim.x;
+    const int64_t base = (int64_t)blockIdx.x * chunk4;
+    const int64_t end = min(base + chunk4, n4);
+    float s = 0.f;
+    int64_t i = base + threadIdx.x;
+    for (; i + (int64_t)(U - 1) * T < end; i += (int64_t)U * T)
+        shape_tile<KIND, U, NTL, NTS>(a, b, out, i, T, s);
+    for (; i < end; i += T) shape_one<KIND, NTS>(a, b, out, i, s);
+    if ((KIND == 0 || KIND == 3) && s == 1234.5f) out[base] = f4{s, s, s, s};
+}
+
+template <int KIND, int U, bool NTL, bool NTS>
+__global__ __launch_bounds__(1024) void k_shape_persist(const f4* __restrict__ a,
+                                                        const f4* __restrict__ b,
+                                                        f4* __restrict__ out, int64_t n4) {
+    const int T = blockDim.x;
+    const int64_t tile = (int64_t)U * T;
+    float s = 0.f;
+    for (int64_t t0 = (int64_t)blockIdx.x * tile; t0 < n4; t0 += (int64_t)gridDim.x * tile) {
+        if (t0 + tile <= n4) {
+            shape_tile<KIND, U, NTL, NTS>(a, b, out, t0 + threadIdx.x, T, s);
+        } else {
+            for (int64_t k = t0 + threadIdx.x; k < n4; k += T) shape_one<KIND, NTS>(a, b, out, k, s);
+        }
+    }
+    if ((KIND == 0 || KIND == 3) && s == 1234.5f) out[0] = f4{s, s, s, s};
+}
+
+// Runs f(integral_constant<int, KIND>, ..U.., ..NTL.., ..NTS..) for runtime
+// values (U in {2, 4, 8}).
+template <typename F>
+void shape_sel(int kind, int u, bool ntl, bool nts, F&& f) {
+    auto with_kind = [&](auto K) {
+        auto with_u = [&](auto U) {
+            auto with_l = [&](auto L) {
+                if (nts)
+                    f(K, U, L, std::true_type{});
+                else
+                    f(K, U, L, std::false_type{});
+            };
+            if (ntl)
+                with_l(std::true_type{});
+            else
+                with_l(std::false_type{});
+        };
+        if (u == 2)
+            with_u(std::integral_constant<int, 2>{});
+        else if (u == 4)
+            with_u(std::integral_constant<int, 4>{});
+        else
+            with_u(std::integral_constant<int, 8>{});
+    };
+    switch (kind) {
+        case 0: with_kind(std::integral_constant<int, 0>{}); break;
+        case 1: with_kind(std::integral_constant<int, 1>{}); break;
+        case 2: with_kind(std::integral_constant<int, 2>{}); break;
+        default: with_kind(std::integral_constant<int, 3>{}); break;
+    }
+}
+
 inline uint64_t stream_key(uint64_t seed, uint32_t id) { return splitmix_at(seed, id); }
 
 inline dim3 grid_for(int64_t items) {
@@ -221,6 +342,50 @@ __attribute__((visibility("default"))) int soar_synth_stream(int kind, const flo
         default: k_stream<3><<<g, 256, 0, s>>>(a4, b4, o4, n4); break;
     }
     return status();
+}
+
+__attribute__((visibility("default"))) int soar_synth_stream_shape(
+    int kind, int persistent, int threads, int loads, int64_t size, int ntl, int nts,
+    const float* a, const float* b, float* out, int64_t n, void* stream) {
+    if (n <= 0) return 0;
+    if (kind < 0 || kind > 3 || !a || !out || (n % 4) || ((uintptr_t)a & 15) ||
+        ((uintptr_t)out & 15) || (kind >= 2 && (!b || ((uintptr_t)b & 15))))
+        return -1;
+    if (threads < 64 || threads > 1024 || threads % 64 || (loads != 2 && loads != 4 && loads != 8) ||
+        size < 1)
+        return -1;
+    const int64_t n4 = n / 4;
+    int64_t blocks;
+    if (persistent) {
+        blocks = size;  // the grid
+    } else {
+        if (size % 4 || size / 4 < threads) return -1;  // chunk floats
+        blocks = (n4 + size / 4 - 1) / (size / 4);
+    }
+    if (blocks > 0x7fffffff) return -1;
+    const f4* a4 = (const f4*)a;
+    const f4* b4 = (const f4*)b;
+    f4* o4 = (f4*)out;
+    const hipStream_t s = (hipStream_t)stream;
+    shape_sel(kind, loads, ntl != 0, nts != 0, [&](auto K, auto U, auto L, auto S) {
+        if (persistent)
+            k_shape_persist<K(), U(), L(), S()><<<dim3((unsigned)blocks), threads, 0, s>>>(
+                a4, b4, o4, n4);
+        else
+            k_shape_chunk<K(), U(), L(), S()><<<dim3((unsigned)blocks), threads, 0, s>>>(
+                a4, b4, o4, n4, size / 4);
+    });
+    return status();
+}
+
+__attribute__((visibility("default"))) int soar_synth_memcpy_d2d(float* dst, const float* src,
+                                                                 int64_t n, void* stream) {
+    if (n <= 0) return 0;
+    if (!dst || !src) return -1;
+    return hipMemcpyAsync(dst, src, (size_t)n * sizeof(float), hipMemcpyDeviceToDevice,
+                          (hipStream_t)stream) == hipSuccess
+               ? 0
+               : -3;
 }
 
 __attribute__((visibility("default"))) int soar_synth_planes(int write, const float* a,

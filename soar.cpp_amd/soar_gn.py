@@ -57,6 +57,7 @@ TUNE_PW_WG_TARGET = 15
 TUNE_PW_CBA_MIN = 16
 TUNE_PW_CBA_BLOCKS = 17
 TUNE_DW_CBA_MIN = 18
+TUNE_NT_TAIL_MB = 19
 
 
 class SoarUnavailable(RuntimeError):
@@ -208,6 +209,9 @@ SYNTH_SIGNATURES = {
     "soar_synth_copy": (_c.c_int, [_P, _P, _I64, _P]),
     "soar_synth_stream": (_c.c_int, [_c.c_int, _P, _P, _P, _I64, _P]),
     "soar_synth_planes": (_c.c_int, [_c.c_int, _P, _P, _I64, _I64, _P]),
+    "soar_synth_stream_shape": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _I64,
+                                           _c.c_int, _c.c_int, _P, _P, _P, _I64, _P]),
+    "soar_synth_memcpy_d2d": (_c.c_int, [_P, _P, _I64, _P]),
 }
 
 _LIB = None
@@ -690,6 +694,34 @@ def synth_stress(t, seed, center=1e3, std=1e-2, p=1e-3, out_mean=0.0, out_std=50
 
 # kinds of synth_stream: name -> (kind, tensor passes per launch)
 STREAM_KINDS = {"read": (0, 1), "copy": (1, 2), "2r1w": (2, 3), "2r": (3, 2)}
+
+
+def synth_stream_shape(kind, a, b, out, threads, loads, chunk=None, grid=None, ntl=False,
+                       nts=True, stream=None):
+    """A streaming pattern (as synth_stream) in another launch shape
+    (soar_synth_stream_shape): `chunk` floats per block, or a persistent
+    grid of `grid` blocks; `loads` float4 loads per thread and tensor in
+    flight; non-temporal loads / stores."""
+    k = STREAM_KINDS[kind][0]
+    for t in (a, b, out):
+        if t is not None and t.numel() != a.numel():
+            raise ValueError("synth_stream_shape buffers must have equal sizes")
+    persistent = grid is not None
+    rc = synth_lib().soar_synth_stream_shape(k, int(persistent), threads, loads,
+                                             grid if persistent else chunk, int(ntl), int(nts),
+                                             _ptr(a), _ptr(b), _ptr(out), a.numel(),
+                                             _stream(stream))
+    if rc:
+        raise SoarError(rc, "soar_synth_stream_shape failed")
+
+
+def synth_memcpy_d2d(dst, src, stream=None):
+    """dst = src through the runtime's device-to-device hipMemcpyAsync."""
+    if dst.numel() != src.numel():
+        raise ValueError("synth_memcpy_d2d buffers must have equal sizes")
+    rc = synth_lib().soar_synth_memcpy_d2d(_ptr(dst), _ptr(src), src.numel(), _stream(stream))
+    if rc:
+        raise SoarError(rc, "soar_synth_memcpy_d2d failed")
 
 
 def synth_stream(kind, a, b, out, stream=None):

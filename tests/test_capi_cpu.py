@@ -152,6 +152,17 @@ def test_tuning_knobs(L):
     assert L.soar_gn_tune(soar_gn.TUNE_BATCH_MB, -1) == soar_gn.SOAR_EINVAL
     assert L.soar_gn_tune(soar_gn.TUNE_CHUNK2, 1536) == soar_gn.SOAR_EINVAL
     assert L.soar_gn_tune(soar_gn.TUNE_STREAMS, 3) == soar_gn.SOAR_EINVAL
+    # non-temporal loads: a 2-bit mask (second passes, first passes)
+    for bad in (-1, 4):
+        assert L.soar_gn_tune(soar_gn.TUNE_NT_LOAD, bad) == soar_gn.SOAR_EINVAL
+    nt = soar_gn.tune_get(soar_gn.TUNE_NT_LOAD)
+    for v in (0, 1, 2, 3):
+        soar_gn.tune(soar_gn.TUNE_NT_LOAD, v)
+        assert soar_gn.tune_get(soar_gn.TUNE_NT_LOAD) == v
+    soar_gn.tune(soar_gn.TUNE_NT_LOAD, nt)
+    assert nt == 3 and soar_gn.tune_get(soar_gn.TUNE_NT_TAIL_MB) == 256
+    for bad in (-1, (1 << 20) + 1):
+        assert L.soar_gn_tune(soar_gn.TUNE_NT_TAIL_MB, bad) == soar_gn.SOAR_EINVAL
     assert soar_gn.tune_get(soar_gn.TUNE_CHUNK2) == 4096
     assert soar_gn.tune_get(soar_gn.TUNE_BATCH_MB) == 0
     soar_gn.tune(soar_gn.TUNE_CHUNK, old)

@@ -676,7 +676,7 @@ def test_kernel_timing_records(gpu, restore_tuning, fold):
 def restore_tuning(gpu):
     keys = (gpu.TUNE_CHUNK, gpu.TUNE_REVERSE, gpu.TUNE_NT_STORE, gpu.TUNE_BATCH_MB,
             gpu.TUNE_STREAMS, gpu.TUNE_NT_LOAD, gpu.TUNE_CHUNK2, gpu.TUNE_SMALL_UNIT,
-            gpu.TUNE_FOLD_MAX)
+            gpu.TUNE_FOLD_MAX, gpu.TUNE_NT_TAIL_MB)
     old = {k: gpu.tune_get(k) for k in keys}
     yield
     for k, v in old.items():
@@ -693,9 +693,10 @@ def _fwd_bwd(gpu, x, gamma, beta, dy, G, residual=False):
 
 @pytest.mark.parametrize("residual", [False, True])
 def test_tuning_variants_match(gpu, oracle, restore_tuning, residual):
-    """Unit batches, streams, reverse order, load/store flavour and the
-    second passes' chunking change only the launch schedule: results are
-    bitwise identical to the default.  Other chunk
+    """Unit batches, streams, reverse order, load/store flavour (the first
+    passes' non-temporal head / cached tail split inside the tensor with a
+    1 MiB tail) and the second passes' chunking change only the launch
+    schedule: results are bitwise identical to the default.  Other chunk
     sizes change the summation tree: results stay within the parity bar."""
     import torch
     N, C, HW, G = 2, 12, 65536 + 4096, 6   # unit = 2 x 69632 floats (544 KiB)
@@ -704,7 +705,9 @@ def test_tuning_variants_match(gpu, oracle, restore_tuning, residual):
     gd, bd = dev(gamma), dev(beta)
     base = _fwd_bwd(gpu, xd, gd, bd, dyd, G, residual)
     for key, val in ((gpu.TUNE_BATCH_MB, 1), (gpu.TUNE_STREAMS, 2), (gpu.TUNE_BATCH_MB, 2),
-                     (gpu.TUNE_NT_LOAD, 1), (gpu.TUNE_STREAMS, 1), (gpu.TUNE_REVERSE, 0),
+                     (gpu.TUNE_NT_LOAD, 1), (gpu.TUNE_NT_LOAD, 3), (gpu.TUNE_NT_TAIL_MB, 1),
+                     (gpu.TUNE_NT_TAIL_MB, 0), (gpu.TUNE_NT_LOAD, 2), (gpu.TUNE_NT_LOAD, 0),
+                     (gpu.TUNE_STREAMS, 1), (gpu.TUNE_REVERSE, 0),
                      (gpu.TUNE_NT_STORE, 0), (gpu.TUNE_CHUNK2, 1024), (gpu.TUNE_CHUNK2, 16384)):
         gpu.tune(key, val)
         got = _fwd_bwd(gpu, xd, gd, bd, dyd, G, residual)
