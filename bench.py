@@ -16,7 +16,7 @@ through the C-ABI of libsoar_gn.so on one GPU.  Prints one JSON line:
              (oracle/soar_oracle.c, one pinned core, median of 3) on a
              bounded sample of config 3, plus config 1 at full size.
 
-Other workloads (--config): the other BASELINE configs (cfg2_fwd,
+Other workloads (--config): the other BASELINE configs (cfg1_fwd, cfg2_fwd,
 cfg4_chain, cfg5), the CBA block with a pointwise conv (cba_pw), the CBA
 depthwise convolutions at 1x64x2048^2 (dw_k3, dw_k5, dw_k7, dw_k3d5,
 dw_k3s2), SOAR training steps (train_nano64/512/1024), SOAR predictions
@@ -42,6 +42,7 @@ SEED = 20261201
 
 CONFIGS = {
     # name: (N, C, HW, G, passes, residual, blocks)
+    "cfg1_fwd": (1, 32, 256 * 256, 8, "fwd", False, 1),
     "cfg2_fwd": (1, 32, 2048 * 2048, 8, "fwd", False, 1),
     "cfg3": (1, 64, 2048 * 2048, 16, "fwdbwd", False, 1),
     "cfg4_chain": (2, 128, 1024 * 1024, 32, "fwdbwd", True, 6),
@@ -51,7 +52,7 @@ CONFIGS = {
     "cba_pw": (1, 64, 2048 * 2048, 16, "fwdbwd", False, 1),
     "cba_pw_unfused": (1, 64, 2048 * 2048, 16, "fwdbwd", False, 1),
 }
-SEED_OF = {"cfg2_fwd": SEED + 2, "cfg3": SEED + 3, "cfg4_chain": SEED + 4, "cfg5": SEED + 5,
+SEED_OF = {"cfg1_fwd": SEED + 1, "cfg2_fwd": SEED + 2, "cfg3": SEED + 3, "cfg4_chain": SEED + 4, "cfg5": SEED + 5,
            "cba_pw": SEED + 6, "cba_pw_unfused": SEED + 6}
 CBA_C_IN = 64
 PEAK_MFMA_F32 = 157.3  # TFLOP/s, dense fp32 matrix
@@ -911,6 +912,8 @@ def main():
         data = (f"synthetic: x~N(0,1), gamma~U(0.5,1.5), beta~N(0,0.1), dy~N(0,1e-2); "
                 f"splitmix64/Box-Muller seed {SEED_OF[args.config]}")
         cfg = {"workload": {"cfg3": "GroupNorm+SiLU fwd+bwd, BASELINE config 3",
+                            "cfg1_fwd": "GroupNorm+SiLU fwd, BASELINE config 1 (8 MiB: "
+                                        "cache-resident, not a roofline config)",
                             "cfg2_fwd": "GroupNorm+SiLU fwd, BASELINE config 2",
                             "cfg4_chain": "6 x (x + SiLU(GN(x))) fwd+bwd, BASELINE config 4",
                             "cfg5": "GroupNorm+SiLU fwd+bwd shape of BASELINE config 5",

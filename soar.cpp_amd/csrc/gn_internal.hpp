@@ -110,6 +110,12 @@ struct Tuning {
 
 constexpr int kThreads = 256;   // first passes (stats, reduction)
 constexpr int kThreads2 = 128;  // second passes (apply, dx)
+// 128-bit loads per tensor a second-pass thread keeps in flight (at the
+// default 4096-float chunks, 8 is a thread's whole share of its chunk).
+#ifndef SOAR_GN_LOADS2
+#define SOAR_GN_LOADS2 8
+#endif
+constexpr int kLoads2 = SOAR_GN_LOADS2;
 
 // Plan for a non-empty tensor.  Returns false if the grid would not fit.
 bool make_plan(int64_t N, int64_t C, int64_t HW, int64_t G,

@@ -574,17 +574,15 @@ __global__ __launch_bounds__(kThreads2) void k_apply(
         f4* y4 = reinterpret_cast<f4*>(y + base);
         const int64_t n4 = ck.len >> 2;
         int64_t i = t;
-        for (; i + 3 * kThreads2 < n4; i += 4 * kThreads2) {
-            f4 v0 = load4<NTL>(&x4[i]), v1 = load4<NTL>(&x4[i + kThreads2]),
-               v2 = load4<NTL>(&x4[i + 2 * kThreads2]), v3 = load4<NTL>(&x4[i + 3 * kThreads2]);
-            f4 o0 = {f(v0.x), f(v0.y), f(v0.z), f(v0.w)};
-            f4 o1 = {f(v1.x), f(v1.y), f(v1.z), f(v1.w)};
-            f4 o2 = {f(v2.x), f(v2.y), f(v2.z), f(v2.w)};
-            f4 o3 = {f(v3.x), f(v3.y), f(v3.z), f(v3.w)};
-            store4<NT>(&y4[i], o0);
-            store4<NT>(&y4[i + kThreads2], o1);
-            store4<NT>(&y4[i + 2 * kThreads2], o2);
-            store4<NT>(&y4[i + 3 * kThreads2], o3);
+        for (; i + (kLoads2 - 1) * kThreads2 < n4; i += kLoads2 * kThreads2) {
+            f4 v[kLoads2];
+#pragma unroll
+            for (int u = 0; u < kLoads2; ++u) v[u] = load4<NTL>(&x4[i + u * kThreads2]);
+#pragma unroll
+            for (int u = 0; u < kLoads2; ++u) {
+                const f4 o = {f(v[u].x), f(v[u].y), f(v[u].z), f(v[u].w)};
+                store4<NT>(&y4[i + u * kThreads2], o);
+            }
         }
         for (; i < n4; i += kThreads2) {
             f4 v = load4<NTL>(&x4[i]);
@@ -861,20 +859,20 @@ __global__ __launch_bounds__(kThreads2) void k_bwd_dx(
         f4* o4 = reinterpret_cast<f4*>(dx + base);
         const int64_t n4 = ck.len >> 2;
         int64_t i = t;
-        for (; i + kThreads2 < n4; i += 2 * kThreads2) {
-            f4 v0 = load4<NTL>(&x4[i]), v1 = load4<NTL>(&x4[i + kThreads2]);
-            f4 g0 = load4<NTL>(&g4[i]), g1 = load4<NTL>(&g4[i + kThreads2]);
-            f4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0;
-            if (ACC) {
-                p0 = o4[i];
-                p1 = o4[i + kThreads2];
+        for (; i + (kLoads2 - 1) * kThreads2 < n4; i += kLoads2 * kThreads2) {
+            f4 v[kLoads2], g[kLoads2], p[kLoads2];
+#pragma unroll
+            for (int u = 0; u < kLoads2; ++u) {
+                v[u] = load4<NTL>(&x4[i + u * kThreads2]);
+                g[u] = load4<NTL>(&g4[i + u * kThreads2]);
+                p[u] = ACC ? o4[i + u * kThreads2] : f4{0.f, 0.f, 0.f, 0.f};
             }
-            f4 r0 = {f(g0.x, v0.x, p0.x), f(g0.y, v0.y, p0.y),
-                     f(g0.z, v0.z, p0.z), f(g0.w, v0.w, p0.w)};
-            f4 r1 = {f(g1.x, v1.x, p1.x), f(g1.y, v1.y, p1.y),
-                     f(g1.z, v1.z, p1.z), f(g1.w, v1.w, p1.w)};
-            store4<NT>(&o4[i], r0);
-            store4<NT>(&o4[i + kThreads2], r1);
+#pragma unroll
+            for (int u = 0; u < kLoads2; ++u) {
+                const f4 r = {f(g[u].x, v[u].x, p[u].x), f(g[u].y, v[u].y, p[u].y),
+                              f(g[u].z, v[u].z, p[u].z), f(g[u].w, v[u].w, p[u].w)};
+                store4<NT>(&o4[i + u * kThreads2], r);
+            }
         }
         for (; i < n4; i += kThreads2) {
             f4 v0 = load4<NTL>(&x4[i]), g0 = load4<NTL>(&g4[i]);
