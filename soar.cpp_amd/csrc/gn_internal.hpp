@@ -109,13 +109,27 @@ struct Tuning {
 };
 
 constexpr int kThreads = 256;   // first passes (stats, reduction)
-constexpr int kThreads2 = 128;  // second passes (apply, dx)
-// 128-bit loads per tensor a second-pass thread keeps in flight (at the
-// default 4096-float chunks, 8 is a thread's whole share of its chunk).
+// Second passes: threads per block and 128-bit loads per tensor a thread
+// keeps in flight, for the apply (k_apply) and the dx pass (k_bwd_dx).  At
+// the default 4096-float chunks both load a thread's whole share of its
+// chunk in one batch (1 GiB tensors: apply 128 x 8 337 us, 512 x 2 336 us
+// but slower at 256 MiB tensors; dx 128 x 8 520 us, 512 x 2 505 us).
+#ifndef SOAR_GN_THREADS2
+#define SOAR_GN_THREADS2 128
+#endif
 #ifndef SOAR_GN_LOADS2
 #define SOAR_GN_LOADS2 8
 #endif
+#ifndef SOAR_GN_THREADS_DX
+#define SOAR_GN_THREADS_DX 512
+#endif
+#ifndef SOAR_GN_LOADS_DX
+#define SOAR_GN_LOADS_DX 2
+#endif
+constexpr int kThreads2 = SOAR_GN_THREADS2;  // apply
 constexpr int kLoads2 = SOAR_GN_LOADS2;
+constexpr int kThreadsDx = SOAR_GN_THREADS_DX;  // dx
+constexpr int kLoadsDx = SOAR_GN_LOADS_DX;
 
 // Plan for a non-empty tensor.  Returns false if the grid would not fit.
 bool make_plan(int64_t N, int64_t C, int64_t HW, int64_t G,

@@ -423,17 +423,18 @@ __device__ __forceinline__ PlaneCoef plane_coef(
 // ======================================================================
 constexpr int64_t kFoldMax = kThreads2;  // partials per unit (one per thread)
 
-// Sum of (a, b) over a kThreads2 block in a fixed order (wave trees, then
+// Sum of (a, b) over an NT-thread block in a fixed order (wave trees, then
 // the waves in order), returned to every thread.
+template <int NT>
 __device__ __forceinline__ double2 fold_block_sum2(double a, double b) {
-    __shared__ double2 lds[kThreads2 / 64];
+    __shared__ double2 lds[NT / 64];
     a = wave_sum(a);
     b = wave_sum(b);
     if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = make_double2(a, b);
     __syncthreads();
     double2 r = lds[0];
 #pragma unroll
-    for (int i = 1; i < kThreads2 / 64; ++i) {
+    for (int i = 1; i < NT / 64; ++i) {
         r.x += lds[i].x;
         r.y += lds[i].y;
     }
@@ -445,6 +446,7 @@ struct UnitStats {
     float hi, r, lo;
 };
 
+template <int NT>
 __device__ UnitStats fold_unit_stats(int64_t u, const double2* __restrict__ part, int64_t HW,
                                      int64_t chunk, int64_t cpp, int64_t cpg, float eps) {
     __shared__ float bc[3];
@@ -456,7 +458,7 @@ __device__ UnitStats fold_unit_stats(int64_t u, const double2* __restrict__ part
         const double2 v = part[u * P + q];
         centred_add(S, Q, partial_count(q, HW, chunk, cpp), v.x, v.y, R);
     }
-    const double2 sq = fold_block_sum2(S, Q);
+    const double2 sq = fold_block_sum2<NT>(S, Q);
     if (threadIdx.x == 0) {
         const double n = (double)(cpg * HW);
         const double2 mm = centred_moments(sq.x, sq.y, n, R);
@@ -473,6 +475,7 @@ __device__ UnitStats fold_unit_stats(int64_t u, const double2* __restrict__ part
 
 // (S1, S2) of unit u from its backward partials: thread q < P adds
 // gamma_j * partial q, j = q / cpp the partial's channel.
+template <int NT>
 __device__ double2 fold_unit_sums(int64_t u, const double2* __restrict__ part,
                                   const float* __restrict__ gamma, int64_t C, int64_t cpg,
                                   int64_t cpp) {
@@ -486,7 +489,7 @@ __device__ double2 fold_unit_sums(int64_t u, const double2* __restrict__ part,
         a = g * v.x;
         b = g * v.y;
     }
-    return fold_block_sum2(a, b);
+    return fold_block_sum2<NT>(a, b);
 }
 
 // dbeta[c] += sdz, dgamma[c] += sdzx; either output may be null (the
@@ -500,16 +503,17 @@ __device__ __forceinline__ void add_params(int64_t c, double sdz, double sdzx,
 
 // dbeta[c] += sum over samples and chunks of channel c's sum(dz), dgamma[c]
 // += the same of sum(dz * xhat) (the k_param_finish step, for one channel).
+template <int NT>
 __device__ void fold_param(int64_t c, const double2* __restrict__ part, int64_t N, int64_t C,
                            int64_t cpp, float* __restrict__ dgamma, float* __restrict__ dbeta) {
     double a = 0.0, b = 0.0;
-    for (int64_t i = threadIdx.x; i < N * cpp; i += kThreads2) {
+    for (int64_t i = threadIdx.x; i < N * cpp; i += NT) {
         const int64_t n = i / cpp, q = i - n * cpp;
         const double2 v = part[(n * C + c) * cpp + q];
         a += v.x;
         b += v.y;
     }
-    const double2 r = fold_block_sum2(a, b);
+    const double2 r = fold_block_sum2<NT>(a, b);
     if (threadIdx.x == 0) add_params(c, r.x, r.y, dgamma, dbeta);
 }
 
@@ -546,7 +550,8 @@ __global__ __launch_bounds__(kThreads2) void k_apply(
         k.n = ck.plane / C;
         k.c = ck.plane - k.n * C;
         k.u = k.n * G + k.c / cpg;
-        const UnitStats st = fold_unit_stats(k.u, fa.part, HW, fa.chunk, fa.cpp, cpg, fa.eps);
+        const UnitStats st =
+            fold_unit_stats<kThreads2>(k.u, fa.part, HW, fa.chunk, fa.cpp, cpg, fa.eps);
         k.mu = st.hi;
         k.r = st.r;
         k.e = -st.lo * st.r;
@@ -810,7 +815,7 @@ __global__ void k_param_finish(const double2* __restrict__ plane_sums,
 // channel c's first chunk in sample 0 also adds channel c's dgamma / dbeta
 // (the folded k_param_finish).
 template <bool VEC, bool SILU, bool RES, bool ACC, bool NT, bool NTL, bool FOLD>
-__global__ __launch_bounds__(kThreads2) void k_bwd_dx(
+__global__ __launch_bounds__(kThreadsDx) void k_bwd_dx(
     const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ gamma, const float* __restrict__ beta,
     const float* __restrict__ mean, const float* __restrict__ rstd,
@@ -822,9 +827,9 @@ __global__ __launch_bounds__(kThreads2) void k_bwd_dx(
     const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd, mean_lo);
     double2 S;
     if (FOLD) {
-        S = fold_unit_sums(k.u, fa.part, gamma, C, cpg, fa.cpp);
+        S = fold_unit_sums<kThreadsDx>(k.u, fa.part, gamma, C, cpg, fa.cpp);
         if ((fa.dgamma || fa.dbeta) && k.n == 0 && ck.off == 0)
-            fold_param(k.c, fa.part, fa.N, C, fa.cpp, fa.dgamma, fa.dbeta);
+            fold_param<kThreadsDx>(k.c, fa.part, fa.N, C, fa.cpp, fa.dgamma, fa.dbeta);
     } else {
         S = unit_sums[k.u];
         if (fa.plane_sums && k.n == 0 && ck.off == 0 && threadIdx.x == 0) {
@@ -859,22 +864,22 @@ __global__ __launch_bounds__(kThreads2) void k_bwd_dx(
         f4* o4 = reinterpret_cast<f4*>(dx + base);
         const int64_t n4 = ck.len >> 2;
         int64_t i = t;
-        for (; i + (kLoads2 - 1) * kThreads2 < n4; i += kLoads2 * kThreads2) {
-            f4 v[kLoads2], g[kLoads2], p[kLoads2];
+        for (; i + (kLoadsDx - 1) * kThreadsDx < n4; i += kLoadsDx * kThreadsDx) {
+            f4 v[kLoadsDx], g[kLoadsDx], p[kLoadsDx];
 #pragma unroll
-            for (int u = 0; u < kLoads2; ++u) {
-                v[u] = load4<NTL>(&x4[i + u * kThreads2]);
-                g[u] = load4<NTL>(&g4[i + u * kThreads2]);
-                p[u] = ACC ? o4[i + u * kThreads2] : f4{0.f, 0.f, 0.f, 0.f};
+            for (int u = 0; u < kLoadsDx; ++u) {
+                v[u] = load4<NTL>(&x4[i + u * kThreadsDx]);
+                g[u] = load4<NTL>(&g4[i + u * kThreadsDx]);
+                p[u] = ACC ? o4[i + u * kThreadsDx] : f4{0.f, 0.f, 0.f, 0.f};
             }
 #pragma unroll
-            for (int u = 0; u < kLoads2; ++u) {
+            for (int u = 0; u < kLoadsDx; ++u) {
                 const f4 r = {f(g[u].x, v[u].x, p[u].x), f(g[u].y, v[u].y, p[u].y),
                               f(g[u].z, v[u].z, p[u].z), f(g[u].w, v[u].w, p[u].w)};
-                store4<NT>(&o4[i + u * kThreads2], r);
+                store4<NT>(&o4[i + u * kThreadsDx], r);
             }
         }
-        for (; i < n4; i += kThreads2) {
+        for (; i < n4; i += kThreadsDx) {
             f4 v0 = load4<NTL>(&x4[i]), g0 = load4<NTL>(&g4[i]);
             f4 p0 = {0.f, 0.f, 0.f, 0.f};
             if (ACC) p0 = o4[i];
@@ -886,7 +891,7 @@ __global__ __launch_bounds__(kThreads2) void k_bwd_dx(
         const float* xp = x + base;
         const float* gp = dy + base;
         float* op = dx + base;
-        for (int64_t i = t; i < ck.len; i += kThreads2)
+        for (int64_t i = t; i < ck.len; i += kThreadsDx)
             store1<NT>(&op[i], f(gp[i], xp[i], ACC ? op[i] : 0.0f));
     }
 }
@@ -1329,7 +1334,7 @@ void launch_dx(const Plan& p, const Tuning& t, const BwdArgs& a, const double2* 
                         bsel(V() && (t.nt_load & 1) != 0, [&](auto L) {
                             bsel(fold, [&](auto F) {
                                 k_bwd_dx<V(), S(), R(), A(), N(), L(), F()>
-                                    <<<grid, kThreads2, 0, s>>>(
+                                    <<<grid, kThreadsDx, 0, s>>>(
                                         a.dy, a.x, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo,
                                         unit_sums, a.dx, p.C, p.G, p.cpg, p.HW, p.chunk2,
                                         p.cpp2, block0, nb, t.reverse, fa);
