@@ -361,11 +361,14 @@ class DwStep:
 
 class CBADwStep:
     """Forward and backward of a CBA block with a depthwise conv (stride 1,
-    same padding, no bias) at 1x64x2048^2, G = 16: z = dwconv(x) (soar_dw_conv_forward),
-    y = SiLU(GroupNorm(z)) (soar_gn_silu_forward); backward fused
-    (soar_dw_cba_backward: the GroupNorm reduction, then one kernel that
-    forms dz per tile in LDS and computes dx and dW from it) or unfused
-    (soar_gn_silu_backward to dz, then soar_dw_conv_backward)."""
+    same padding, no bias) at 1x64x2048^2, G = 16.  Fused: the forward
+    soar_dw_conv_gn_silu_forward (the GroupNorm statistics in the
+    convolution's epilogue, then the finish and apply) and the backward
+    soar_dw_cba_backward (the GroupNorm reduction, then one kernel that forms
+    dz per tile in LDS and computes dx and dW from it).  Unfused: z =
+    dwconv(x) (soar_dw_conv_forward), y = SiLU(GroupNorm(z))
+    (soar_gn_silu_forward); soar_gn_silu_backward to dz, then
+    soar_dw_conv_backward."""
 
     def __init__(self, gn, name, seed):
         import torch
@@ -389,6 +392,9 @@ class CBADwStep:
         self.dw = torch.zeros_like(self.w)
         self.dgamma, self.dbeta = torch.zeros(C, device="cuda"), torch.zeros(C, device="cuda")
         self.ws_gn = gn.workspace(N, C, H * W, self.G)
+        self.ws_fwd = torch.empty(
+            max(gn.dw_conv_gn_workspace_bytes(N, C, H, W, H, W, K, self.pad, 1, D, self.G), 1),
+            dtype=torch.uint8, device="cuda")
         if fused:
             nws = gn.dw_cba_backward_workspace_bytes(N, C, H, W, H, W, K, self.pad, 1, D, self.G)
         else:
@@ -398,15 +404,17 @@ class CBADwStep:
         self.T = N * C * H * W * 4
 
     def algorithmic_bytes(self):
-        # fwd: conv reads x, writes z; GroupNorm statistics read z; apply reads
-        # z, writes y.  bwd: the reduction reads dy, z; fused: one kernel reads
-        # dy, z, x and writes dx; unfused: GroupNorm dx reads dy, z and writes
-        # dz, dgrad reads dz and writes dx, wgrad reads dz and x.
-        return (5 + 2 + (4 if self.fused else 7)) * self.T
+        # fwd: conv reads x, writes z (fused: with the GroupNorm statistics);
+        # unfused, the statistics read z again; apply reads z, writes y.  bwd:
+        # the reduction reads dy, z; fused: one kernel reads dy, z, x and
+        # writes dx; unfused: GroupNorm dx reads dy, z and writes dz, dgrad
+        # reads dz and writes dx, wgrad reads dz and x.
+        return ((4 + 2 + 4) if self.fused else (5 + 2 + 7)) * self.T
 
     def kernel_bytes(self, name):
         T = self.T
-        return {"dw_conv": 2 * T, "gn_stats_partial": T, "gn_silu_apply": 2 * T,
+        return {"dw_conv": 2 * T, "dw_conv_stats": 2 * T, "gn_stats_partial": T,
+                "gn_silu_apply": 2 * T,
                 "gn_silu_bwd_reduce": 2 * T, "gn_silu_bwd_dx": 3 * T, "dw_conv_dgrad": 2 * T,
                 "dw_conv_wgrad": 2 * T, "dw_cba_bwd": 4 * T}.get(name, 0)
 
@@ -414,20 +422,27 @@ class CBADwStep:
         f = 2 * self.K * self.K * self.T // 4
         if name == "dw_cba_bwd":
             return 2 * f
-        return f if name in ("dw_conv", "dw_conv_dgrad", "dw_conv_wgrad") else 0
+        return f if name in ("dw_conv", "dw_conv_stats", "dw_conv_dgrad", "dw_conv_wgrad") else 0
 
     def config(self):
         return {"workload": f"CBA fwd+bwd: depthwise conv k{self.K} dilation {self.D} pad "
-                            f"{self.pad} + GN + SiLU, backward "
-                            + ("fused (dz per tile in LDS)" if self.fused else
-                               "as GN backward then depthwise backward"),
+                            f"{self.pad} + GN + SiLU, "
+                            + ("GN statistics in the conv epilogue, backward fused (dz per tile "
+                               "in LDS)" if self.fused else
+                               "conv then GN forward, backward as GN backward then depthwise "
+                               "backward"),
                 "N": self.N, "C": self.C, "H": self.H, "W": self.W, "G": self.G}
 
     def __call__(self):
         gn = self.gn
-        gn.dw_conv_forward(self.x, self.w, None, self.pad, 1, self.D, y=self.z)
-        gn.gn_silu_forward(self.z, self.gamma, self.beta, self.G, y=self.y, mean=self.mean,
-                           rstd=self.rstd, mean_lo=self.lo, ws=self.ws_gn)
+        if self.fused:
+            gn.dw_conv_gn_silu_forward(self.x, self.w, None, self.gamma, self.beta, self.G,
+                                       self.pad, 1, self.D, z=self.z, y=self.y, mean=self.mean,
+                                       rstd=self.rstd, mean_lo=self.lo, ws=self.ws_fwd)
+        else:
+            gn.dw_conv_forward(self.x, self.w, None, self.pad, 1, self.D, y=self.z)
+            gn.gn_silu_forward(self.z, self.gamma, self.beta, self.G, y=self.y, mean=self.mean,
+                               rstd=self.rstd, mean_lo=self.lo, ws=self.ws_gn)
         st = gn.Stats(self.mean, self.rstd, self.lo)
         if self.fused:
             gn.dw_cba_backward(self.dy, self.z, self.x, self.w, self.gamma, self.beta, st, self.G,

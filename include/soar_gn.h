@@ -331,6 +331,37 @@ SOAR_API int soar_dw_conv_forward(const float* x, const float* weight,
                                   int64_t pad, int64_t stride, int64_t dil,
                                   void* stream);
 
+/* Bytes of workspace soar_dw_conv_gn_silu_forward needs for this shape (0
+ * for an invalid or empty shape). */
+SOAR_API size_t soar_dw_conv_gn_workspace_bytes(int64_t N, int64_t C,
+                                                int64_t H_in, int64_t W_in,
+                                                int64_t H_out, int64_t W_out,
+                                                int64_t K, int64_t pad,
+                                                int64_t stride, int64_t dil,
+                                                int64_t G);
+
+/* CBA forward of a depthwise convolution over N samples:
+ *   z = bias + w (*) x   (as soar_dw_conv_forward, bit for bit)
+ *   y = silu(GroupNorm_G(z)) (SOAR_GN_SILU) or GroupNorm_G(z), with mean,
+ *       rstd, mean_lo (nullable) as soar_gn_silu_forward writes them.
+ * For a shape with a tiled kernel, the convolution's epilogue computes the
+ * GroupNorm statistics of its own outputs (each block's tile column as
+ * float64 (mean, M2) partials in the workspace), so no separate statistics
+ * pass re-reads z: the GroupNorm finish and apply follow directly.  Other
+ * shapes, and units small enough for the one-launch GroupNorm, run the
+ * convolution and then soar_gn_silu_forward.  mean / rstd match the
+ * stand-alone forward's to float64 summation order.
+ * Replaces: CBA::forward (src/nn/blocks.cpp:442-445) with a depthwise
+ * Conv2d: Conv2d::forward (layers.cpp:353-355) + GroupNorm::forward
+ * (:641-736) + SiLU::forward (:789-795). */
+SOAR_API int soar_dw_conv_gn_silu_forward(
+    const float* x, const float* weight, const float* bias, const float* gamma,
+    const float* beta, float* z, float* y, float* mean, float* rstd,
+    float* mean_lo, int64_t N, int64_t C, int64_t H_in, int64_t W_in,
+    int64_t H_out, int64_t W_out, int64_t K, int64_t pad, int64_t stride,
+    int64_t dil, int64_t G, float eps, unsigned flags, void* workspace,
+    size_t workspace_bytes, void* stream);
+
 /* Bytes of workspace soar_dw_conv_backward needs (0 is a valid answer: the
  * generic kernels need none; (size_t)-1 for an invalid shape). */
 SOAR_API size_t soar_dw_conv_backward_workspace_bytes(

@@ -736,6 +736,26 @@ bool cba_layout(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t G, c
     return true;
 }
 
+
+// Layout of soar_dw_conv_gn_silu_forward's workspace: the GroupNorm
+// workspace of the output, then (when the convolution writes the statistics
+// partials itself) the tile-group partials.
+struct DwGnLayout {
+    Plan p;
+    soar::gn::DwStatsGeom g;
+    bool fused = false;
+    size_t gn_bytes = 0, part_bytes = 0;
+};
+
+bool dw_gn_layout(const soar::gn::DwShape& sh, int64_t G, const Tuning& t, DwGnLayout* L) {
+    if (!soar::gn::make_plan(sh.N, sh.C, sh.Ho * sh.Wo, G, t, &L->p)) return false;
+    L->gn_bytes = al256(soar::gn::workspace_bytes(L->p));
+    L->fused = !soar::gn::forward_is_small(L->p, t) && soar::gn::dw_stats_geometry(sh, &L->g) &&
+               sh.N * sh.C * L->g.tpp <= 0x7fffffff;
+    L->part_bytes = L->fused ? al256((size_t)(sh.N * sh.C * L->g.tpp) * sizeof(double2)) : 0;
+    return true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -852,6 +872,79 @@ SOAR_API int soar_dw_conv_forward(const float* x, const float* weight, const flo
     hipError_t e = soar::gn::launch_dw_forward(sh, x, weight, bias, y,
                                                static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "depthwise convolution launch");
+}
+
+SOAR_API size_t soar_dw_conv_gn_workspace_bytes(int64_t N, int64_t C, int64_t H_in, int64_t W_in,
+                                                int64_t H_out, int64_t W_out, int64_t K,
+                                                int64_t pad, int64_t stride, int64_t dil,
+                                                int64_t G) {
+    const soar::gn::DwShape sh = dw_shape(N, C, H_in, W_in, H_out, W_out, K, pad, stride, dil);
+    int64_t ie = 0, oe = 0, elems = 0;
+    if (check_dw_shape(sh, &ie, &oe) != SOAR_OK ||
+        check_shape(N, C, H_out * W_out, G, &elems) != SOAR_OK || oe == 0) {
+        g_err.clear();
+        return 0;
+    }
+    DwGnLayout L;
+    if (!dw_gn_layout(sh, G, current_tuning(), &L)) return 0;
+    return L.gn_bytes + L.part_bytes;
+}
+
+SOAR_API int soar_dw_conv_gn_silu_forward(const float* x, const float* weight, const float* bias,
+                                          const float* gamma, const float* beta, float* z,
+                                          float* y, float* mean, float* rstd, float* mean_lo,
+                                          int64_t N, int64_t C, int64_t H_in, int64_t W_in,
+                                          int64_t H_out, int64_t W_out, int64_t K, int64_t pad,
+                                          int64_t stride, int64_t dil, int64_t G, float eps,
+                                          unsigned flags, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+    const soar::gn::DwShape sh = dw_shape(N, C, H_in, W_in, H_out, W_out, K, pad, stride, dil);
+    int64_t ie = 0, oe = 0, elems = 0;
+    int rc = check_dw_shape(sh, &ie, &oe);
+    if (rc) return rc;
+    if ((rc = check_shape(N, C, H_out * W_out, G, &elems))) return rc;
+    if (flags & ~SOAR_GN_SILU)
+        return fail(SOAR_EINVAL, "unsupported flags 0x%x (SOAR_GN_SILU only)", flags);
+    if (!(eps >= 0.0f)) return fail(SOAR_EINVAL, "eps must be >= 0");
+    if (oe == 0) return ok();
+    if ((rc = require_device())) return rc;
+    const size_t sb = (size_t)(N * G) * sizeof(float);
+    if ((rc = check_dev(weight, (size_t)(C * K * K) * 4, "weight")) ||
+        (rc = check_dev_opt(bias, (size_t)C * 4, "bias")) ||
+        (ie > 0 && (rc = check_dev(x, (size_t)ie * 4, "x"))) ||
+        (rc = check_dev_opt(gamma, (size_t)C * 4, "gamma")) ||
+        (rc = check_dev_opt(beta, (size_t)C * 4, "beta")) ||
+        (rc = check_dev(z, (size_t)oe * 4, "z")) || (rc = check_dev(y, (size_t)oe * 4, "y")) ||
+        (rc = check_dev(mean, sb, "mean")) || (rc = check_dev(rstd, sb, "rstd")) ||
+        (rc = check_dev_opt(mean_lo, sb, "mean_lo")))
+        return rc;
+    if (!dw_grids_fit(sh)) return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    const Tuning t = current_tuning();
+    DwGnLayout L;
+    if (!dw_gn_layout(sh, G, t, &L))
+        return fail(SOAR_EINVAL, "shape is too large for one launch grid");
+    L.p.vec4 = L.p.vec4 && aligned16(z) && aligned16(y);
+    if ((rc = check_ws(L.p, workspace, workspace_bytes))) return rc;
+    if (workspace_bytes < L.gn_bytes + L.part_bytes)
+        return fail(SOAR_EINVAL, "workspace of %zu bytes is smaller than the %zu this call needs",
+                    workspace_bytes, L.gn_bytes + L.part_bytes);
+    if (L.fused && (rc = check_dev(workspace, L.gn_bytes + L.part_bytes, "workspace")))
+        return rc;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    soar::gn::FwdArgs a{z, gamma, beta, y, mean, rstd, mean_lo, eps, flags, workspace};
+    if (!L.fused) {
+        // no tiled kernel for the shape, or units small enough for the
+        // one-launch GroupNorm: the convolution, then the GroupNorm forward
+        hipError_t e = soar::gn::launch_dw_forward(sh, x, weight, bias, z, s);
+        if (e != hipSuccess) return hip_fail(e, "depthwise convolution launch");
+        e = soar::gn::launch_forward(L.p, t, a, s);
+        return e == hipSuccess ? ok() : hip_fail(e, "GroupNorm forward launch");
+    }
+    double2* part = reinterpret_cast<double2*>(static_cast<char*>(workspace) + L.gn_bytes);
+    hipError_t e = soar::gn::launch_dw_forward(sh, x, weight, bias, z, s, part);
+    if (e != hipSuccess) return hip_fail(e, "depthwise convolution launch");
+    e = soar::gn::launch_forward_from_tile_partials(L.p, t, a, part, L.g, H_out, W_out, s);
+    return e == hipSuccess ? ok() : hip_fail(e, "GroupNorm finish / apply launch");
 }
 
 SOAR_API size_t soar_dw_conv_backward_workspace_bytes(int64_t N, int64_t C, int64_t H_in,

@@ -37,6 +37,7 @@
 
 #include "gn_internal.hpp"
 #include "gn_math.hpp"
+#include "gn_moments.hpp"
 #include "soar_gn.h"
 
 namespace soar {
@@ -182,12 +183,20 @@ struct HaloRows {
 // registers while tile i is computed from LDS.  FLIP
 // applies the kernel rotated by 180 degrees (the stride-1 input gradient).
 // (body of block b; `tile` holds Tile<K, S, D>::floats floats)
-template <int K, int S, int D, bool FLIP, bool ACC, bool BIAS>
+// STATS (forward): the GroupNorm statistics epilogue.  Each thread sums its
+// stored outputs shifted by its first one (a data value, so the sums stay
+// small when |mean| >> std), and the block combines them into the (mean,
+// M2) of its tile column, part[b] (block_moments, gn_moments.hpp).  Block b
+// = plane * tpp + group, so a unit's partials lie together, plane-major:
+// the layout the GroupNorm finish combines (with the tiles' element counts,
+// dw_stats_geometry), so no statistics pass re-reads the output.
+// `mom`: 4 * kDwThreads / 64 doubles of LDS.
+template <int K, int S, int D, bool FLIP, bool ACC, bool BIAS, bool STATS = false>
 __device__ __forceinline__ void dw_conv_body(
     const float* __restrict__ in, const float* __restrict__ w, const float* __restrict__ bias,
     float* __restrict__ out, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo,
     int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per, int64_t b,
-    float* __restrict__ tile) {
+    float* __restrict__ tile, double2* __restrict__ part = nullptr, double* mom = nullptr) {
     using T = Tile<K, S, D>;
     const int64_t plane = b / tpp, gix = b - plane * tpp;
     const int64_t c = plane % C;
@@ -203,6 +212,8 @@ __device__ __forceinline__ void dw_conv_body(
     for (int k = 0; k < K * K; ++k) wr[k] = w[c * K * K + (FLIP ? K * K - 1 - k : k)];
     const float b0 = BIAS ? bias[c] : 0.0f;
     const int t = threadIdx.x, r = t >> 3, c0 = (t & 7) * kPer;
+    float mK = 0.0f, ms = 0.0f, mq = 0.0f;  // STATS: shift and shifted sums
+    int mcnt = 0;
     HaloRows<K, D> halo;  // stride 1 only (k7 fwd 0.610 -> 0.603 ms, k3 d5 0.476 -> 0.442 ms)
     for (int64_t ty = ty0; ty < ty1; ++ty) {
         int lr0 = 0;
@@ -240,6 +251,18 @@ __device__ __forceinline__ void dw_conv_body(
         if (oy >= Ho) continue;
         float* orow = out + plane * Ho * Wo + oy * Wo;
         const int64_t ox = ox0 + c0;
+        if constexpr (STATS) {
+            const int nv = (int)min<int64_t>(kPer, Wo - ox);  // outputs stored (<= 0: none)
+            if (ty == ty0 && nv > 0) mK = acc[0];
+#pragma unroll
+            for (int q = 0; q < kPer; ++q)
+                if (q < nv) {
+                    const float d = acc[q] - mK;
+                    ms += d;
+                    mq = fmaf(d, d, mq);
+                }
+            mcnt += max(nv, 0);
+        }
         if (ox + kPer <= Wo && ((reinterpret_cast<uintptr_t>(orow + ox) & 15) == 0)) {
             f4* o4 = reinterpret_cast<f4*>(orow + ox);
             f4 v0 = {acc[0], acc[1], acc[2], acc[3]}, v1 = {acc[4], acc[5], acc[6], acc[7]};
@@ -255,17 +278,24 @@ __device__ __forceinline__ void dw_conv_body(
                 if (ox + q < Wo) orow[ox + q] = ACC ? orow[ox + q] + acc[q] : acc[q];
         }
     }
+    if constexpr (STATS) {
+        const double2 m = block_moments<kDwThreads>(mK, ms, mq, mcnt, mom);
+        if (t == 0) part[b] = m;
+    }
 }
 
-template <int K, int S, int D, bool FLIP, bool ACC, bool BIAS>
+template <int K, int S, int D, bool FLIP, bool ACC, bool BIAS, bool STATS = false>
 __global__ __launch_bounds__(kDwThreads) void k_dw_conv(
     const float* __restrict__ in, const float* __restrict__ w, const float* __restrict__ bias,
     float* __restrict__ out, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo,
-    int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per) {
+    int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per,
+    double2* __restrict__ part) {
     __shared__ __attribute__((aligned(16))) float tile[Tile<K, S, D>::floats];
-    dw_conv_body<K, S, D, FLIP, ACC, BIAS>(in, w, bias, out, C, Hi, Wi, Ho, Wo, pad, tiles_x,
-                                           tiles_y, tpp, per, xcd_block(blockIdx.x, gridDim.x),
-                                           tile);
+    __shared__ double mom[STATS ? 4 * kDwThreads / 64 : 1];
+    dw_conv_body<K, S, D, FLIP, ACC, BIAS, STATS>(in, w, bias, out, C, Hi, Wi, Ho, Wo, pad,
+                                                  tiles_x, tiles_y, tpp, per,
+                                                  xcd_block(blockIdx.x, gridDim.x), tile, part,
+                                                  mom);
 }
 
 // Stride 1, dilation 1, with RB consecutive output rows per thread (a
@@ -275,13 +305,13 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_conv(
 // outputs instead of K * RB (at K = 7 and RB = 4, 10 instead of 28), for
 // the same K*K FMAs per output.  Every output adds its terms in
 // dw_conv_body's order (bias, then ky, then kx ascending), so the results
-// are bit for bit the same.
-template <int K, bool FLIP, bool ACC, bool BIAS, int RB>
+// are bit for bit the same.  STATS: dw_conv_body's statistics epilogue.
+template <int K, bool FLIP, bool ACC, bool BIAS, int RB, bool STATS = false>
 __device__ __forceinline__ void dw_conv_rb_body(
     const float* __restrict__ in, const float* __restrict__ w, const float* __restrict__ bias,
     float* __restrict__ out, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo,
     int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per, int64_t b,
-    float* __restrict__ tile) {
+    float* __restrict__ tile, double2* __restrict__ part = nullptr, double* mom = nullptr) {
     using T = Tile<K, 1, 1, RB>;
     const int64_t plane = b / tpp, gix = b - plane * tpp;
     const int64_t c = plane % C;
@@ -297,6 +327,8 @@ __device__ __forceinline__ void dw_conv_rb_body(
     for (int k = 0; k < K * K; ++k) wr[k] = w[c * K * K + (FLIP ? K * K - 1 - k : k)];
     const float b0 = BIAS ? bias[c] : 0.0f;
     const int t = threadIdx.x, r0 = (t >> 3) * RB, c0 = (t & 7) * kPer;
+    float mK = 0.0f, ms = 0.0f, mq = 0.0f;  // STATS: shift and shifted sums
+    int mcnt = 0;
     HaloRows<K, 1, RB> halo;
     for (int64_t ty = ty0; ty < ty1; ++ty) {
         int lr0 = 0;
@@ -337,6 +369,18 @@ __device__ __forceinline__ void dw_conv_rb_body(
             const int64_t oy = ty * T::TH + r0 + j;
             if (oy >= Ho) break;
             float* orow = out + plane * Ho * Wo + oy * Wo;
+            if constexpr (STATS) {
+                const int nv = (int)min<int64_t>(kPer, Wo - ox);  // outputs stored (<= 0: none)
+                if (ty == ty0 && j == 0 && nv > 0) mK = acc[0][0];
+#pragma unroll
+                for (int q = 0; q < kPer; ++q)
+                    if (q < nv) {
+                        const float d = acc[j][q] - mK;
+                        ms += d;
+                        mq = fmaf(d, d, mq);
+                    }
+                mcnt += max(nv, 0);
+            }
             if (ox + kPer <= Wo && ((reinterpret_cast<uintptr_t>(orow + ox) & 15) == 0)) {
                 f4* o4 = reinterpret_cast<f4*>(orow + ox);
                 f4 v0 = {acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
@@ -354,17 +398,24 @@ __device__ __forceinline__ void dw_conv_rb_body(
             }
         }
     }
+    if constexpr (STATS) {
+        const double2 m = block_moments<kDwThreads>(mK, ms, mq, mcnt, mom);
+        if (t == 0) part[b] = m;
+    }
 }
 
-template <int K, bool FLIP, bool ACC, bool BIAS, int RB>
+template <int K, bool FLIP, bool ACC, bool BIAS, int RB, bool STATS = false>
 __global__ __launch_bounds__(kDwThreads) void k_dw_conv_rb(
     const float* __restrict__ in, const float* __restrict__ w, const float* __restrict__ bias,
     float* __restrict__ out, int64_t C, int64_t Hi, int64_t Wi, int64_t Ho, int64_t Wo,
-    int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per) {
+    int64_t pad, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per,
+    double2* __restrict__ part) {
     __shared__ __attribute__((aligned(16))) float tile[Tile<K, 1, 1, RB>::floats];
-    dw_conv_rb_body<K, FLIP, ACC, BIAS, RB>(in, w, bias, out, C, Hi, Wi, Ho, Wo, pad, tiles_x,
-                                            tiles_y, tpp, per, xcd_block(blockIdx.x, gridDim.x),
-                                            tile);
+    __shared__ double mom[STATS ? 4 * kDwThreads / 64 : 1];
+    dw_conv_rb_body<K, FLIP, ACC, BIAS, RB, STATS>(in, w, bias, out, C, Hi, Wi, Ho, Wo, pad,
+                                                   tiles_x, tiles_y, tpp, per,
+                                                   xcd_block(blockIdx.x, gridDim.x), tile, part,
+                                                   mom);
 }
 
 // Weight and bias gradient partials: a block walks `per` tiles down one
@@ -1140,28 +1191,45 @@ int64_t dw_grid_blocks(const DwShape& sh, bool output_tiles) {
     return sh.N * sh.C * tpp;
 }
 
+bool dw_stats_geometry(const DwShape& sh, DwStatsGeom* g) {
+    if (!planes_fit_32(sh) || !dw_has_fast(sh.K, sh.S, sh.D)) return false;
+    int64_t tiles_y = 0;
+    int per = 1;
+    const int rb = conv_rows_per_thread(sh.K, sh.S, sh.D);
+    g->tpp = conv_groups(sh.N * sh.C, sh.Ho, sh.Wo, &g->tiles_x, &tiles_y, &per,
+                         (int64_t)kTH * rb);
+    g->rows = (int64_t)per * kTH * rb;
+    return true;
+}
+
 hipError_t launch_dw_forward(const DwShape& sh, const float* x, const float* w,
-                             const float* bias, float* y, hipStream_t s) {
+                             const float* bias, float* y, hipStream_t s, double2* part) {
     if (sh.N * sh.C * sh.Ho * sh.Wo == 0) return hipSuccess;
+    DwStatsGeom geom;
+    if (part && !dw_stats_geometry(sh, &geom)) return hipErrorInvalidValue;  // no tiled kernel
     int64_t tiles_x = 0, tiles_y = 0;
     int per = 1;
     const int rb = conv_rows_per_thread(sh.K, sh.S, sh.D);
     const int64_t tpp =
         conv_groups(sh.N * sh.C, sh.Ho, sh.Wo, &tiles_x, &tiles_y, &per, (int64_t)kTH * rb);
-    const int tok = prof_begin(s, "dw_conv");
+    const int tok = prof_begin(s, part ? "dw_conv_stats" : "dw_conv");
     const bool fast = planes_fit_32(sh) && fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
         using CF = decltype(cf);
         bsel(bias != nullptr, [&](auto B) {
-            const dim3 grid((unsigned)(sh.N * sh.C * tpp));
-            if constexpr (CF::s == 1 && CF::d == 1 && conv_rb<CF::k>() > 1) {
-                k_dw_conv_rb<CF::k, false, false, B(), conv_rb<CF::k>()><<<grid, kDwThreads, 0, s>>>(
-                    x, w, bias, y, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tiles_y,
-                    tpp, per);
-            } else {
-                k_dw_conv<CF::k, CF::s, CF::d, false, false, B()><<<grid, kDwThreads, 0, s>>>(
-                    x, w, bias, y, sh.C, sh.Hi, sh.Wi, sh.Ho, sh.Wo, sh.pad, tiles_x, tiles_y,
-                    tpp, per);
-            }
+            bsel(part != nullptr, [&](auto ST) {
+                const dim3 grid((unsigned)(sh.N * sh.C * tpp));
+                if constexpr (CF::s == 1 && CF::d == 1 && conv_rb<CF::k>() > 1) {
+                    k_dw_conv_rb<CF::k, false, false, B(), conv_rb<CF::k>(), ST()>
+                        <<<grid, kDwThreads, 0, s>>>(x, w, bias, y, sh.C, sh.Hi, sh.Wi, sh.Ho,
+                                                     sh.Wo, sh.pad, tiles_x, tiles_y, tpp, per,
+                                                     part);
+                } else {
+                    k_dw_conv<CF::k, CF::s, CF::d, false, false, B(), ST()>
+                        <<<grid, kDwThreads, 0, s>>>(x, w, bias, y, sh.C, sh.Hi, sh.Wi, sh.Ho,
+                                                     sh.Wo, sh.pad, tiles_x, tiles_y, tpp, per,
+                                                     part);
+                }
+            });
         });
     });
     if (!fast)
@@ -1232,12 +1300,12 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
                         k_dw_conv_rb<CF::k, true, A(), false, conv_rb<CF::k>()>
                             <<<grid, kDwThreads, 0, s>>>(dy, w, nullptr, dx, sh.C, sh.Ho, sh.Wo,
                                                          sh.Hi, sh.Wi, padf, tiles_x, tiles_y,
-                                                         tpp, per);
+                                                         tpp, per, nullptr);
                     } else {
                         k_dw_conv<CF::k, CF::s, CF::d, true, A(), false>
                             <<<grid, kDwThreads, 0, s>>>(dy, w, nullptr, dx, sh.C, sh.Ho, sh.Wo,
                                                          sh.Hi, sh.Wi, padf, tiles_x, tiles_y,
-                                                         tpp, per);
+                                                         tpp, per, nullptr);
                     }
                 });
             });

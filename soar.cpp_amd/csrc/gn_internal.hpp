@@ -190,6 +190,22 @@ hipError_t launch_forward_from_partials(const Plan& p, const Tuning& t, const Fw
                                         hipStream_t s);
 // Chunk-partial region of the workspace (double2 x p.blocks).
 double2* ws_partials(const Plan& p, void* ws);
+// Tile groups of the depthwise forward (dw_conv.hip): tpp per plane, tiles_x
+// across, each `rows` output rows (the last one clipped at Ho) by 64
+// columns (the last tile of a row clipped at Wo).
+struct DwStatsGeom {
+    int64_t tpp = 0, tiles_x = 0, rows = 0;
+};
+// True when the forward runs the one-launch small-unit kernels (which take
+// no partials from a producer).
+bool forward_is_small(const Plan& p, const Tuning& t);
+// The GroupNorm finish and apply from the depthwise forward's tile-group
+// partials (`part`, dw_stats_geometry's layout) instead of chunk
+// partials: mean / rstd / mean_lo, then y.  p: make_plan's plan for the
+// output, whose workspace `a.ws` holds the rest.
+hipError_t launch_forward_from_tile_partials(const Plan& p, const Tuning& t, const FwdArgs& a,
+                                             const double2* part, const DwStatsGeom& g,
+                                             int64_t Ho, int64_t Wo, hipStream_t s);
 // Plan of the GroupNorm that follows a pointwise convolution: the chunk is
 // the convolution's pixel chunk, so its epilogue partials are the plan's.
 bool make_pw_plan(int64_t N, int64_t C_out, int64_t HW, int64_t G, const Tuning& t, Plan* p);
@@ -322,8 +338,15 @@ bool dw_has_fast(int64_t K, int64_t S, int64_t D);
 size_t dw_bwd_workspace_bytes(const DwShape& sh);
 // Blocks of the tiled kernels over the output (or, for dx, input) planes.
 int64_t dw_grid_blocks(const DwShape& sh, bool output_tiles);
+// With `part` (a shape with a tiled kernel, dw_stats_geometry true), the
+// forward also writes the GroupNorm chunk partials of y: part[plane * tpp
+// + group] = (mean, M2) of the group's outputs.
 hipError_t launch_dw_forward(const DwShape& sh, const float* x, const float* w,
-                             const float* bias, float* y, hipStream_t s);
+                             const float* bias, float* y, hipStream_t s,
+                             double2* part = nullptr);
+// Tile groups of the forward (DwStatsGeom); false if the shape has no
+// tiled forward.
+bool dw_stats_geometry(const DwShape& sh, DwStatsGeom* g);
 // dx (+)= input gradient, dw += weight gradient, db += bias gradient; any
 // output may be null.
 hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x,

@@ -48,6 +48,7 @@
 
 #include "gn_internal.hpp"
 #include "gn_math.hpp"
+#include "gn_moments.hpp"
 #include "soar_gn.h"
 
 namespace soar {
@@ -57,13 +58,6 @@ namespace {
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = kThreads / 64;
-
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off);
-    return v;
-}
 
 // Sum of (a, b) over a block of NT threads in a fixed order; valid in
 // thread 0.  Ends with the block synchronised.
@@ -107,11 +101,6 @@ __device__ __forceinline__ void centred_add(double& S, double& Q, double n, doub
     Q += fma(nd, d, m2);
 }
 
-// (mean, M2) from the sums about R over N elements.
-__device__ __forceinline__ double2 centred_moments(double S, double Q, double N, double R) {
-    const double m = S / N;
-    return make_double2(R + m, fmax(Q - S * m, 0.0));
-}
 
 // Element count of chunk partial j of a unit (partials are plane-major,
 // cpp per plane; only a plane's last chunk can be short).  j < 2^31: the
@@ -183,13 +172,31 @@ __device__ __forceinline__ void store1(float* p, float v) {
 // output tolerance.  lo goes to the caller's optional mean_lo (for the
 // backward) and to the workspace (for the apply kernel of the same call).
 // ======================================================================
-template <int NT = kThreads>
-__device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
-                                  float* __restrict__ mean, float* __restrict__ rstd,
-                                  float* __restrict__ mean_lo, float* __restrict__ lo_ws,
-                                  int64_t HW, int64_t chunk, int64_t cpp, int64_t cpg,
-                                  float eps, double* lds /*[2 * NT / 64]*/) {
-    const int64_t P = cpg * cpp;  // chunk blocks per unit
+// Element count of a unit's partial j: chunk partials (the statistics
+// pass, the pointwise convolution's epilogue) ...
+struct ChunkCount {
+    int64_t HW, chunk, cpp;
+    __device__ double operator()(int64_t j) const { return partial_count(j, HW, chunk, cpp); }
+};
+
+// ... or the depthwise forward's tile groups: partial j of a unit is group
+// j % tpp of one of its planes, `rows` output rows (clipped at Ho) by 64
+// columns (clipped at Wo); dw_stats_geometry's layout.
+struct TileCount {
+    int64_t tpp, tiles_x, rows, Ho, Wo;
+    __device__ double operator()(int64_t j) const {
+        const int64_t g = (int64_t)((uint32_t)j % (uint32_t)tpp);
+        const int64_t ty = g / tiles_x, tx = g - ty * tiles_x;
+        return (double)(min(rows, Ho - ty * rows) * min((int64_t)64, Wo - tx * 64));
+    }
+};
+
+template <int NT = kThreads, typename Count>
+__device__ void finish_unit(int64_t u, const double2* __restrict__ part, int64_t P,
+                            const Count& count, double n_total, float* __restrict__ mean,
+                            float* __restrict__ rstd, float* __restrict__ mean_lo,
+                            float* __restrict__ lo_ws, float eps,
+                            double* lds /*[2 * NT / 64]*/) {
     const int64_t first = u * P;
     // Sums about partial 0's mean (centred_add), each thread over partials
     // j, j + NT, ... in order, then the block in a fixed order.
@@ -208,16 +215,15 @@ __device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
         for (int i = 0; i < kUnroll; ++i) v[i] = part[first + j0 + (int64_t)i * NT];
 #pragma unroll
         for (int i = 0; i < kUnroll; ++i)
-            centred_add(S, Q, partial_count(j0 + (int64_t)i * NT, HW, chunk, cpp),
-                        v[i].x, v[i].y, R);
+            centred_add(S, Q, count(j0 + (int64_t)i * NT), v[i].x, v[i].y, R);
     }
     for (; j0 < P; j0 += NT) {
         const double2 v = part[first + j0];
-        centred_add(S, Q, partial_count(j0, HW, chunk, cpp), v.x, v.y, R);
+        centred_add(S, Q, count(j0), v.x, v.y, R);
     }
     block_sum2<double, NT>(S, Q, lds);
     if (threadIdx.x == 0) {
-        const double n = (double)(cpg * HW);
+        const double n = n_total;
         const double2 mm = centred_moments(S, Q, n, R);
         const double var = mm.y / n;
         const float hi = (float)mm.x;
@@ -227,6 +233,26 @@ __device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
         lo_ws[u] = lo;
         if (mean_lo) mean_lo[u] = lo;
     }
+}
+
+template <int NT = kThreads>
+__device__ void finish_stats_unit(int64_t u, const double2* __restrict__ part,
+                                  float* __restrict__ mean, float* __restrict__ rstd,
+                                  float* __restrict__ mean_lo, float* __restrict__ lo_ws,
+                                  int64_t HW, int64_t chunk, int64_t cpp, int64_t cpg,
+                                  float eps, double* lds /*[2 * NT / 64]*/) {
+    finish_unit<NT>(u, part, cpg * cpp, ChunkCount{HW, chunk, cpp}, (double)(cpg * HW), mean,
+                    rstd, mean_lo, lo_ws, eps, lds);
+}
+
+// Finish of the depthwise forward's tile-group partials, one block per unit.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_stats_finish_tiles(
+    const double2* __restrict__ part, float* __restrict__ mean, float* __restrict__ rstd,
+    float* __restrict__ mean_lo, float* __restrict__ lo_ws, int64_t P, TileCount count,
+    double n_total, float eps) {
+    __shared__ double lds[2 * NT / 64];
+    finish_unit<NT>(blockIdx.x, part, P, count, n_total, mean, rstd, mean_lo, lo_ws, eps, lds);
 }
 
 // Finish-only grid for units of many chunk partials (a pointwise
@@ -341,50 +367,10 @@ __global__ __launch_bounds__(kThreads) void k_stats(
             q0 = fmaf(d0, d0, q0);
         }
     }
-    // The block's (mean, M2) without a division per thread or per step of
-    // the tree: each thread's sums, about its own K, are re-centred on its
-    // wave's reference Rw (lane 0's K; when lane 0 has no elements, no lane
-    // of the wave has) as S = n d + s, Q = q + d (2 s + n d) with d = K - Rw
-    // (the sums of x - Rw and of its square), the wave adds them, and
-    // thread 0 re-centres the waves' sums on wave 0's reference in wave
-    // order (centred_add's terms with the wave's own S in place of n d).
-    const float Rw = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(K)));
-    double S = 0.0, Q = 0.0;
-    if (cnt > 0) {
-        const double s = (double)((s0 + s1) + (s2 + s3));
-        const double q = (double)((q0 + q1) + (q2 + q3));
-        const double d = (double)K - (double)Rw;
-        const double nd = (double)cnt * d;
-        S = nd + s;
-        Q = fma(d, 2.0 * s + nd, q);
-    }
-    int n = (int)cnt;
-    n = wave_sum(n);
-    S = wave_sum(S);
-    Q = wave_sum(Q);
-    const int lane = t & 63, w = t >> 6;
-    if (lane == 0) {
-        lds[w] = (double)n;
-        lds[kWaves + w] = S;
-        lds[2 * kWaves + w] = Q;
-        lds[3 * kWaves + w] = (double)Rw;
-    }
-    __syncthreads();
-    if (t == 0) {
-        const double R0 = lds[3 * kWaves];
-        double N = lds[0], S0 = lds[kWaves], Q0 = lds[2 * kWaves];
-#pragma unroll
-        for (int i = 1; i < kWaves; ++i) {
-            const double ni = lds[i], Si = lds[kWaves + i];
-            if (ni == 0.0) continue;
-            const double d = lds[3 * kWaves + i] - R0;
-            const double nd = ni * d;
-            Q0 += fma(d, 2.0 * Si + nd, lds[2 * kWaves + i]);
-            S0 += Si + nd;
-            N += ni;
-        }
-        part[b] = centred_moments(S0, Q0, N, R0);
-    }
+    // the block's (mean, M2) (gn_moments.hpp)
+    const double2 m = block_moments<kThreads>(K, (s0 + s1) + (s2 + s3), (q0 + q1) + (q2 + q3),
+                                              (int)cnt, lds);
+    if (t == 0) part[b] = m;
 }
 
 // Per-block coefficients of plane `plane`: xhat = fma(x - mu, r, e) with
@@ -1656,6 +1642,28 @@ hipError_t launch_forward_from_partials(const Plan& p, const Tuning& t, const Fw
 }
 
 double2* ws_partials(const Plan& p, void* ws) { return ws_view(p, ws).part; }
+
+bool forward_is_small(const Plan& p, const Tuning& t) { return small_fwd(p, t); }
+
+hipError_t launch_forward_from_tile_partials(const Plan& p, const Tuning& t, const FwdArgs& a,
+                                             const double2* part, const DwStatsGeom& g,
+                                             int64_t Ho, int64_t Wo, hipStream_t s) {
+    const WsView w = ws_view(p, a.ws);
+    const int64_t P = p.cpg * g.tpp;
+    const TileCount count{g.tpp, g.tiles_x, g.rows, Ho, Wo};
+    int tok = prof_begin(s, "gn_stats_finish");
+    if (P >= kWideFinish)
+        k_stats_finish_tiles<kWideThreads><<<dim3((unsigned)p.units), kWideThreads, 0, s>>>(
+            part, a.mean, a.rstd, a.mean_lo, w.lo, P, count, (double)(p.cpg * p.HW), a.eps);
+    else
+        k_stats_finish_tiles<kThreads><<<dim3((unsigned)p.units), kThreads, 0, s>>>(
+            part, a.mean, a.rstd, a.mean_lo, w.lo, P, count, (double)(p.cpg * p.HW), a.eps);
+    prof_end(s, tok);
+    tok = prof_begin(s, (a.flags & SOAR_GN_SILU) ? "gn_silu_apply" : "gn_apply");
+    launch_apply(p, t, a, w.lo, 0, p.blocks2, s);
+    prof_end(s, tok);
+    return hipGetLastError();
+}
 
 bool make_pw_plan(int64_t N, int64_t C_out, int64_t HW, int64_t G, const Tuning& t, Plan* p) {
     Tuning tp = t;

@@ -657,7 +657,7 @@ TensorPtr CBA::forward_depthwise(const TensorPtr& input, unsigned flags) {
         gamma->to_cuda();
         beta->to_cuda();
     }
-    const int64_t G = (int64_t)norm_->num_groups(), HWo = g.Ho * g.Wo;
+    const int64_t G = (int64_t)norm_->num_groups();
     const int64_t K = (int64_t)conv_->kernel_size(), pad = (int64_t)conv_->padding();
     const int64_t S = (int64_t)conv_->stride(), D = (int64_t)conv_->dilation();
     const bool record = (input->requires_grad() || w->requires_grad() ||
@@ -669,15 +669,15 @@ TensorPtr CBA::forward_depthwise(const TensorPtr& input, unsigned flags) {
     TensorPtr mean = Tensor::create({g.N * G}, false, true);
     TensorPtr rstd = Tensor::create({g.N * G}, false, true);
     TensorPtr lo = Tensor::create({g.N * G}, false, true);
-    check(soar_dw_conv_forward(input->cuda_data(), w->cuda_data(), nullptr, z->cuda_data(), g.N,
-                               g.C_in, g.H, g.W, g.Ho, g.Wo, K, pad, S, D, exec::stream()),
-          "depthwise convolution");
-    const size_t wsb = soar_gn_workspace_bytes(g.N, g.C_out, HWo, G);
-    check(soar_gn_silu_forward(z->cuda_data(), dptr(gamma), dptr(beta), y->cuda_data(),
-                               mean->cuda_data(), rstd->cuda_data(), lo->cuda_data(), g.N,
-                               g.C_out, HWo, G, norm_->eps(), flags, workspace(wsb), wsb,
-                               exec::stream()),
-          "CBA GroupNorm forward");
+    // the GroupNorm statistics come from the convolution's epilogue
+    const size_t wsb =
+        soar_dw_conv_gn_workspace_bytes(g.N, g.C_in, g.H, g.W, g.Ho, g.Wo, K, pad, S, D, G);
+    check(soar_dw_conv_gn_silu_forward(input->cuda_data(), w->cuda_data(), nullptr, dptr(gamma),
+                                       dptr(beta), z->cuda_data(), y->cuda_data(),
+                                       mean->cuda_data(), rstd->cuda_data(), lo->cuda_data(),
+                                       g.N, g.C_in, g.H, g.W, g.Ho, g.Wo, K, pad, S, D, G,
+                                       norm_->eps(), flags, workspace(wsb), wsb, exec::stream()),
+          "CBA depthwise forward");
     if (record) {
         auto node = std::make_shared<CBADepthwiseNode>();
         node->input = input;

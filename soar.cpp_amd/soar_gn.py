@@ -112,6 +112,9 @@ SIGNATURES = {
     "soar_pw_cba_backward_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "soar_pw_cba_backward": (_c.c_int, [_P] * 13 + [_I64] * 5 + [_c.c_uint, _P, _SZ, _P]),
     "soar_dw_conv_forward": (_c.c_int, [_P, _P, _P, _P] + [_I64] * 10 + [_P]),
+    "soar_dw_conv_gn_workspace_bytes": (_SZ, [_I64] * 11),
+    "soar_dw_conv_gn_silu_forward": (_c.c_int, [_P] * 10 + [_I64] * 11 +
+                                     [_c.c_float, _c.c_uint, _P, _SZ, _P]),
     "soar_dw_conv_backward_workspace_bytes": (_SZ, [_I64] * 9),
     "soar_dw_conv_backward": (_c.c_int, [_P] * 6 + [_I64] * 10 + [_c.c_uint, _P, _SZ, _P]),
     "soar_dw_cba_backward_workspace_bytes": (_SZ, [_I64] * 11),
@@ -569,6 +572,43 @@ def dw_conv_forward(x, weight, bias, pad, stride=1, dil=1, y=None, stream=None):
     check(lib().soar_dw_conv_forward(_ptr(x), _ptr(weight), _ptr(bias), _ptr(y), N, C, H, W,
                                      Ho, Wo, K, pad, stride, dil, _stream(stream)))
     return y
+
+
+def dw_conv_gn_workspace_bytes(N, C, H, W, Ho, Wo, K, pad, stride, dil, G) -> int:
+    return int(lib().soar_dw_conv_gn_workspace_bytes(N, C, H, W, Ho, Wo, K, pad, stride, dil, G))
+
+
+def dw_conv_gn_silu_forward(x, weight, bias, gamma, beta, G, pad, stride=1, dil=1, eps=1e-5,
+                            silu=True, z=None, y=None, mean=None, rstd=None, mean_lo=None,
+                            ws=None, stream=None):
+    """CBA forward of a depthwise conv through soar_dw_conv_gn_silu_forward.
+    x [N,C,H,W], weight [C,K,K]; returns (z, y, Stats): z the convolution
+    output (the GroupNorm input the backward needs), y = silu(group_norm(z))
+    (or group_norm(z))."""
+    import torch
+    N, C, H, W = x.shape
+    K = weight.shape[-1]
+    Ho, Wo = conv_out_size(H, K, pad, stride, dil), conv_out_size(W, K, pad, stride, dil)
+    for t, n in ((x, "x"), (weight, "weight"), (bias, "bias"), (gamma, "gamma"),
+                 (beta, "beta"), (z, "z"), (y, "y"), (mean, "mean"), (rstd, "rstd"),
+                 (mean_lo, "mean_lo")):
+        _check_tensor(t, n)
+    shape = (N, C, Ho, Wo)
+    new = lambda: torch.empty(N * G, dtype=torch.float32, device=x.device)
+    z = torch.empty(shape, dtype=torch.float32, device=x.device) if z is None else z
+    y = torch.empty(shape, dtype=torch.float32, device=x.device) if y is None else y
+    mean = new() if mean is None else mean
+    rstd = new() if rstd is None else rstd
+    mean_lo = new() if mean_lo is None else mean_lo
+    if ws is None:
+        ws = torch.empty(max(dw_conv_gn_workspace_bytes(N, C, H, W, Ho, Wo, K, pad, stride, dil,
+                                                        G), 1),
+                         dtype=torch.uint8, device=x.device)
+    check(lib().soar_dw_conv_gn_silu_forward(
+        _ptr(x), _ptr(weight), _ptr(bias), _ptr(gamma), _ptr(beta), _ptr(z), _ptr(y),
+        _ptr(mean), _ptr(rstd), _ptr(mean_lo), N, C, H, W, Ho, Wo, K, pad, stride, dil, G, eps,
+        GN_SILU if silu else 0, _ptr(ws), ws.numel(), _stream(stream)))
+    return z, y, Stats(mean, rstd, mean_lo)
 
 
 def dw_conv_backward(dy, x, weight, pad, stride=1, dil=1, dx=None, dweight=None, dbias=None,

@@ -235,6 +235,42 @@ def test_pw_conv_validation_without_gpu(L):
     assert f(None, None, None, None, 8, 6, 1 << 28, None) == soar_gn.SOAR_EINVAL
 
 
+def _dwf(L, N, C, H, W, K, G, flags=1, eps=1e-5, stride=1, dil=1):
+    pad = dil * (K - 1) // 2
+    Ho = (H + 2 * pad - dil * (K - 1) - 1) // stride + 1
+    Wo = (W + 2 * pad - dil * (K - 1) - 1) // stride + 1
+    return L.soar_dw_conv_gn_silu_forward(None, None, None, None, None, None, None, None, None,
+                                          None, N, C, H, W, Ho, Wo, K, pad, stride, dil, G, eps,
+                                          flags, None, 0, None)
+
+
+def test_dw_conv_gn_workspace_bytes(L):
+    al = lambda b: (b + 255) // 256 * 256
+    gn = soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16)
+    # k7 at 64 x 2048^2: tile groups of 4 tiles of 32 x 64 outputs, 16 x 32
+    # groups per plane -> 64 x 512 partials of 16 B after the GroupNorm part
+    assert soar_gn.dw_conv_gn_workspace_bytes(1, 64, 2048, 2048, 2048, 2048, 7, 3, 1, 1, 16) \
+        == al(gn) + 64 * 512 * 16
+    # units small enough for the one-launch GroupNorm: its workspace alone
+    assert soar_gn.dw_conv_gn_workspace_bytes(1, 8, 32, 32, 32, 32, 3, 1, 1, 1, 2) == \
+        al(soar_gn.workspace_bytes(1, 8, 32 * 32, 2))
+    # no tiled kernel (K = 9): the GroupNorm workspace alone
+    assert soar_gn.dw_conv_gn_workspace_bytes(1, 8, 128, 128, 128, 128, 9, 4, 1, 1, 2) == \
+        al(soar_gn.workspace_bytes(1, 8, 128 * 128, 2))
+    assert soar_gn.dw_conv_gn_workspace_bytes(1, 6, 64, 64, 64, 64, 3, 1, 1, 1, 4) == 0  # C % G
+    assert soar_gn.dw_conv_gn_workspace_bytes(0, 8, 64, 64, 64, 64, 3, 1, 1, 1, 2) == 0
+
+
+def test_dw_conv_gn_validation_without_gpu(L):
+    assert _dwf(L, 1, 6, 64, 64, 3, 4) == soar_gn.SOAR_EINVAL
+    assert "divisible" in soar_gn.last_error()
+    assert _dwf(L, 1, 8, 64, 64, 3, 2, flags=2) == soar_gn.SOAR_EINVAL  # residual not fused
+    assert "flags" in soar_gn.last_error()
+    assert _dwf(L, 1, 8, 64, 64, 3, 2, eps=-1.0) == soar_gn.SOAR_EINVAL
+    assert _dwf(L, 1, 8, 64, 64, 0, 2) == soar_gn.SOAR_EINVAL  # kernel size
+    assert _dwf(L, 0, 8, 64, 64, 3, 2) == soar_gn.SOAR_OK  # empty
+
+
 def test_pw_chunk_tuning(L):
     assert L.soar_gn_tune(soar_gn.TUNE_PW_CHUNK, 100) == soar_gn.SOAR_EINVAL
     assert L.soar_gn_tune(soar_gn.TUNE_PW_CHUNK, 0) == soar_gn.SOAR_EINVAL
