@@ -78,6 +78,142 @@ __device__ __forceinline__ int tile_row(int mt, int r, int h) {
     return mt * 32 + (r & 3) + 8 * (r >> 2) + 4 * h;
 }
 
+// Modes of the convolution kernels (k_pw_conv below).
+enum PwMode { kPlain = 0, kStats = 1, kAccum = 2, kPlainT = 3, kAccumT = 4 };
+
+// Accumulators of an item start at the bias of their rows (zero without
+// bias, and on split-K waves other than wave 0).  (The bias loads stay
+// inside the item instead of being hoisted out of the pixel loop, where 32
+// bias values would stay live in registers.)
+template <bool BIAS>
+__device__ __forceinline__ void pw_acc_init(f16 (&acc)[2][4], const float* __restrict__ bias,
+                                            int64_t row0, int64_t rlim, int h, int v) {
+    const float* bias_i = bias;
+    asm volatile("" : "+s"(bias_i));
+    const float* bb = bias_i + row0 + 4 * h;  // bias of tile row 4h
+    const bool full = rlim >= kRowTile - 1;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int c = tile_row(mt, r, 0);
+            float bv = 0.0f;
+            if (BIAS && v == 0) bv = (full || c + 4 * h <= rlim) ? bb[c] : 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[mt][t][r] = bv;
+        }
+    }
+}
+
+// One K step (8 channels) of an item: 32 MFMAs, the four k-steps q of the
+// two m-tiles and four n-tiles.
+__device__ __forceinline__ void pw_mfma_step(f16 (&acc)[2][4], const f4 (&a)[2], const f4 (&b)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                acc[mt][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[mt][q], b[q][t], acc[mt][t], 0,
+                                                                  0, 0);
+        }
+    }
+}
+
+// Item epilogue: z rows of the tile (ACC modes add the old z) and, with
+// STATS, the item's per-row shifts in ldsK and shifted (sum, sum of
+// squares) per lane in lds, for the row-owner merge.
+template <bool FAST, int MODE>
+__device__ __forceinline__ void pw_item_epilogue(const f16 (&acc)[2][4], float* __restrict__ zs,
+                                                 int64_t p0, int64_t HW, int64_t rlim, int h,
+                                                 int j, int v, bool lane_px, uint32_t zo,
+                                                 float2* lds, float* ldsK) {
+    constexpr bool STATS = MODE == kStats, ACC = MODE == kAccum || MODE == kAccumT;
+    // ---- epilogue.  The row offsets below are computed here, not hoisted
+    // out of the item loop where 32 of them would stay live in registers.
+    int64_t hw_e = HW;
+    asm volatile("" : "+s"(hw_e));
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int tr0 = tile_row(mt, r, 0);  // half 1 holds row tr0 + 4
+            float* zr = reinterpret_cast<float*>(
+                reinterpret_cast<char*>(zs + (int64_t)tr0 * hw_e) + zo);
+            if (v == 0 && tr0 + 4 * h <= rlim) {
+                if (FAST) {
+                    if (lane_px) {
+                        f4 v = {acc[mt][0][r], acc[mt][1][r], acc[mt][2][r], acc[mt][3][r]};
+                        if (ACC) v += *reinterpret_cast<const f4*>(zr);
+                        *reinterpret_cast<f4*>(zr) = v;
+                    }
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        if (p0 + 4 * j + t < HW) zr[t] = ACC ? zr[t] + acc[mt][t][r] : acc[mt][t][r];
+                }
+            }
+        }
+    }
+    if (STATS) {
+        // shift of each row: its value at the item's first pixel, which
+        // lane j = 0 of each half-wave holds; passed on through LDS
+        if (j == 0 && v == 0) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) ldsK[tile_row(mt, r, h)] = acc[mt][0][r];
+            }
+        }
+        __syncthreads();
+        if (v != 0) return;
+        // LDS addresses: one lane base plus constants, formed here so they
+        // are not hoisted out of the item loop
+        int lb = 4 * h;
+        asm volatile("" : "+v"(lb));
+        const float* kb = ldsK + lb;
+        float2* sb = lds + lb * kLdsStride + j;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int c = tile_row(mt, r, 0);
+                const float K = kb[c];
+                float s = 0.f, q = 0.f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const bool ok = FAST ? lane_px : (p0 + 4 * j + t < HW);
+                    const float d = ok ? acc[mt][t][r] - K : 0.0f;
+                    s += d;
+                    q = fmaf(d, d, q);
+                }
+                sb[c * kLdsStride] = make_float2(s, q);
+            }
+        }
+    }
+}
+
+// Row-owner merge of an item's statistics: lane l adds the shifted sums of
+// tile row l (its 32 lanes' pairs in lds) and folds the item into the row's
+// running (count, mean, M2) in float64 with Chan's formula.
+__device__ __forceinline__ void pw_stats_merge(const float2* lds, const float* ldsK, Mom& run,
+                                               int lane, int nvalid) {
+    float S = 0.f, Q = 0.f;
+    const float4* src = reinterpret_cast<const float4*>(lds + lane * kLdsStride);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float4 u = src[i];
+        S += u.x + u.z;
+        Q += u.y + u.w;
+    }
+    const double cnt = (double)nvalid;
+    Mom m;
+    m.n = cnt;
+    m.mean = (double)ldsK[lane] + (double)S / cnt;
+    m.m2 = fmax((double)Q - (double)S * (double)S / cnt, 0.0);
+    run = chan_merge(run, m);
+}
+
 // One 64-row x 128-pixel item: z rows [row0, row0 + 64) of pixels
 // [p0, p0 + 128) of sample n, plus (STATS) the item's per-row shifted sums
 // transposed through LDS and the per-row shifts in ldsK.
@@ -96,8 +232,6 @@ __device__ __forceinline__ int tile_row(int mt, int r, int h) {
 // element (row m, channel k) at w[k * C_out + m] (dx = W^T dz straight from
 // W, no transpose kernel; the A operand then takes four 4-byte loads per
 // row and K step instead of one 16-byte load).
-enum PwMode { kPlain = 0, kStats = 1, kAccum = 2, kPlainT = 3, kAccumT = 4 };
-
 template <bool FAST, int MODE, bool BIAS, int KS, int PD>
 __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const float* __restrict__ ws,
                                         const float* __restrict__ bias, float* __restrict__ zs,
@@ -105,7 +239,6 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
                                         int64_t C_out, int64_t HW, int Kpad, int kb, int ke,
                                         int v, float2* lds, float* ldsK, float* red) {
     // xs = x + n*C_in*HW + p0, ws = w + row0*C_in, zs = z + (n*C_out + row0)*HW + p0
-    constexpr bool STATS = MODE == kStats, ACC = MODE == kAccum || MODE == kAccumT;
     constexpr bool TW = MODE == kPlainT || MODE == kAccumT;
     const bool lane_px = p0 + 4 * j < HW;
     const uint32_t hw4 = (uint32_t)HW * 4u;  // bytes per channel plane
@@ -122,26 +255,8 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
     const uint32_t wq = (uint32_t)C_out * 4u;  // TW: bytes from one channel to the next
     const uint32_t zo = (uint32_t)h * 4u * hw4 + 16u * (uint32_t)j;
 
-    // (the bias loads stay inside the item instead of being hoisted out of
-    // the pixel loop, where 32 bias values would stay live in registers)
-    const float* bias_i = bias;
-    asm volatile("" : "+s"(bias_i));
     f16 acc[2][4];
-    {
-        const float* bb = bias_i + row0 + 4 * h;  // bias of tile row 4h
-        const bool full = rlim >= kRowTile - 1;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int c = tile_row(mt, r, 0);
-                float bv = 0.0f;
-                if (BIAS && v == 0) bv = (full || c + 4 * h <= rlim) ? bb[c] : 0.0f;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) acc[mt][t][r] = bv;
-            }
-        }
-    }
+    pw_acc_init<BIAS>(acc, bias, row0, rlim, h, v);
 
     auto load_step = [&](int kk, f4 (&a)[2], f4 (&b)[4]) {
         if (FAST) {
@@ -194,18 +309,7 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
             }
         }
     };
-    auto mfma_step = [&](const f4 (&a)[2], const f4 (&b)[4]) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    acc[mt][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[mt][q], b[q][t],
-                                                                      acc[mt][t], 0, 0, 0);
-            }
-        }
-    };
+    auto mfma_step = [&](const f4 (&a)[2], const f4 (&b)[4]) { pw_mfma_step(acc, a, b); };
     // Ping-pong operand buffers: the loads of the next step are issued
     // before the MFMAs of the current one, so their latency hides behind 32
     // MFMAs.  Loads are never under a branch (past the end they load zeros,
@@ -283,68 +387,7 @@ __device__ __forceinline__ void pw_item(const float* __restrict__ xs, const floa
         }
     }
 
-    // ---- epilogue.  The row offsets below are computed here, not hoisted
-    // out of the item loop where 32 of them would stay live in registers.
-    int64_t hw_e = HW;
-    asm volatile("" : "+s"(hw_e));
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int tr0 = tile_row(mt, r, 0);  // half 1 holds row tr0 + 4
-            float* zr = reinterpret_cast<float*>(
-                reinterpret_cast<char*>(zs + (int64_t)tr0 * hw_e) + zo);
-            if (v == 0 && tr0 + 4 * h <= rlim) {
-                if (FAST) {
-                    if (lane_px) {
-                        f4 v = {acc[mt][0][r], acc[mt][1][r], acc[mt][2][r], acc[mt][3][r]};
-                        if (ACC) v += *reinterpret_cast<const f4*>(zr);
-                        *reinterpret_cast<f4*>(zr) = v;
-                    }
-                } else {
-#pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        if (p0 + 4 * j + t < HW) zr[t] = ACC ? zr[t] + acc[mt][t][r] : acc[mt][t][r];
-                }
-            }
-        }
-    }
-    if (STATS) {
-        // shift of each row: its value at the item's first pixel, which
-        // lane j = 0 of each half-wave holds; passed on through LDS
-        if (j == 0 && v == 0) {
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) ldsK[tile_row(mt, r, h)] = acc[mt][0][r];
-            }
-        }
-        __syncthreads();
-        if (v != 0) return;
-        // LDS addresses: one lane base plus constants, formed here so they
-        // are not hoisted out of the item loop
-        int lb = 4 * h;
-        asm volatile("" : "+v"(lb));
-        const float* kb = ldsK + lb;
-        float2* sb = lds + lb * kLdsStride + j;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int c = tile_row(mt, r, 0);
-                const float K = kb[c];
-                float s = 0.f, q = 0.f;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const bool ok = FAST ? lane_px : (p0 + 4 * j + t < HW);
-                    const float d = ok ? acc[mt][t][r] - K : 0.0f;
-                    s += d;
-                    q = fmaf(d, d, q);
-                }
-                sb[c * kLdsStride] = make_float2(s, q);
-            }
-        }
-    }
+    pw_item_epilogue<FAST, MODE>(acc, zs, p0, HW, rlim, h, j, v, lane_px, zo, lds, ldsK);
 }
 
 // MODE kPlain: z = w x + b;  kStats: also the GroupNorm chunk partials;
@@ -405,24 +448,7 @@ __global__ __launch_bounds__(64 * KS, PD > 1 || KS > 1 || !FAST ? 1 : 2) void k_
                 if (STATS) {
                     __syncthreads();
                 }
-                if (STATS && v == 0) {
-                    // lane owns row `lane` of the tile
-                    float S = 0.f, Q = 0.f;
-                    const float4* src = reinterpret_cast<const float4*>(lds + lane * kLdsStride);
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const float4 u = src[i];
-                        S += u.x + u.z;
-                        Q += u.y + u.w;
-                    }
-                    const double cnt = (double)nvalid;
-                    Mom m;
-                    m.n = cnt;
-                    m.mean = (double)ldsK[lane] + (double)S / cnt;
-                    m.m2 = fmax((double)Q - (double)S * (double)S / cnt, 0.0);
-                    Mom& acc = ldsM[g * kRowTile + lane];
-                    acc = chan_merge(acc, m);
-                }
+                if (STATS && v == 0) pw_stats_merge(lds, ldsK, ldsM[g * kRowTile + lane], lane, nvalid);
                 if (STATS) __syncthreads();
             }
         }
@@ -433,6 +459,164 @@ __global__ __launch_bounds__(64 * KS, PD > 1 || KS > 1 || !FAST ? 1 : 2) void k_
                 if (row < C_out) part[(n * C_out + row) * cpp + kc] = make_double2(m.mean, m.m2);
             }
         }
+    }
+}
+
+// Streamed form of k_pw_conv's fast path for grids of one-wave blocks
+// (KS = 1): the wave's items (row group, pixel item, row tile; k_pw_conv's
+// order) follow one another without draining the operand pipeline.  The
+// loads run kSd K steps ahead of the MFMAs across item boundaries, so the
+// next item's first steps are in flight while an item's epilogue stores z,
+// and, since the memory counter retires in issue order, the waits of the
+// next item's MFMAs cover those earlier loads and not the stores issued
+// after them.  The ring holds kSd + 1 steps, so an item's K steps must be a
+// multiple of kSd + 1 (pw_stream_fits); the slot of each step is then a
+// compile-time constant.  The next item's operands come from the same load
+// code with its base pointers and lane offsets selected by a wave-uniform
+// condition; after the last item the descriptors are empty and the loads
+// return zeros without touching memory.
+constexpr int kSd = 3;
+
+struct PwOff {
+    uint32_t xo, wo0, wo1;  // lane byte offsets of x and of the two W rows
+};
+
+template <int MODE, bool BIAS>
+__global__ __launch_bounds__(64, 1) void k_pw_conv_stream(
+    const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ bias,
+    float* __restrict__ z, double2* __restrict__ part, int64_t C_in, int64_t C_out, int64_t HW,
+    int64_t chunk, int64_t cpp, int Kpad, int rpw) {
+    __shared__ __attribute__((aligned(16))) float2 lds[kRowTile * kLdsStride];
+    __shared__ float ldsK[kRowTile];
+    __shared__ Mom ldsM[kRowGroup * kRowTile];
+    constexpr bool STATS = MODE == kStats, TW = MODE == kPlainT || MODE == kAccumT;
+    constexpr int NB = kSd + 1;
+    const int lane = threadIdx.x, h = lane >> 5, j = lane & 31;
+    const int64_t n = (int64_t)blockIdx.x / cpp;
+    const int64_t kc = (int64_t)blockIdx.x - n * cpp;
+    const int64_t px0 = kc * chunk, pend = min(px0 + chunk, HW);
+    const int64_t R = min<int64_t>((C_out + kRowTile - 1) / kRowTile, ((int64_t)blockIdx.y + 1) * rpw);
+    const int64_t rg0 = (int64_t)blockIdx.y * rpw;
+    if (rg0 >= R) return;
+    const float* xn = x + n * C_in * HW;
+    float* zn = z + n * C_out * HW;
+    const uint32_t hw4 = (uint32_t)HW * 4u, wq = (uint32_t)C_out * 4u;
+    const int nsteps = Kpad / 8;
+    const uint32_t zo = (uint32_t)h * 4u * hw4 + 16u * (uint32_t)j;
+
+    struct Task {
+        int64_t rg, p0;
+        int g;
+    };
+    auto next = [&](Task t) {
+        if (++t.g >= (int)min<int64_t>(kRowGroup, R - t.rg)) {
+            t.g = 0;
+            t.p0 += kItem;
+            if (t.p0 >= pend) {
+                t.p0 = px0;
+                t.rg += kRowGroup;
+            }
+        }
+        return t;
+    };
+    auto row0_of = [](const Task& t) { return (t.rg + t.g) * kRowTile; };
+    // k_pw_conv's lane offsets for a task (lanes past the plane and rows
+    // past C_out are clamped onto valid addresses; their products reach no
+    // stored output)
+    auto offs = [&](const Task& t) {
+        const int64_t rlim = C_out - 1 - row0_of(t);
+        const bool lane_px = t.p0 + 4 * j < HW;
+        const uint32_t r0 = (uint32_t)(j <= rlim ? j : (int)rlim);
+        const uint32_t r1 = (uint32_t)(32 + j <= rlim ? 32 + j : (int)rlim);
+        PwOff o;
+        o.xo = (uint32_t)h * 4u * hw4 + 4u * (uint32_t)(lane_px ? 4 * j : (int)(HW - 4 - t.p0));
+        o.wo0 = TW ? (4u * h * (uint32_t)C_out + r0) * 4u : (r0 * (uint32_t)C_in + 4u * h) * 4u;
+        o.wo1 = TW ? (4u * h * (uint32_t)C_out + r1) * 4u : (r1 * (uint32_t)C_in + 4u * h) * 4u;
+        return o;
+    };
+    auto load = [&](const float* xs, const float* ws, const PwOff& o, int kk, bool live,
+                    f4 (&a)[2], f4 (&b)[4]) {
+        const int k0 = live ? kk : 0;
+        const auto rw = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(TW ? ws + (int64_t)k0 * C_out : ws + k0), (short)0,
+            live ? 0x7fffffff : 0, kRsrcWord3);
+        const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(xs + (int64_t)k0 * HW),
+                                                          (short)0, live ? 0x7fffffff : 0,
+                                                          kRsrcWord3);
+        if (TW) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                a[0][q] = __builtin_bit_cast(float,
+                                             __builtin_amdgcn_raw_buffer_load_b32(rw, o.wo0, q * wq, 0));
+                a[1][q] = __builtin_bit_cast(float,
+                                             __builtin_amdgcn_raw_buffer_load_b32(rw, o.wo1, q * wq, 0));
+            }
+        } else {
+            a[0] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, o.wo0, 0, 0));
+            a[1] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, o.wo1, 0, 0));
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            b[q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rx, o.xo, q * hw4, 0));
+    };
+    auto wbase = [&](const Task& t) { return TW ? w + row0_of(t) : w + row0_of(t) * C_in; };
+
+    if (STATS) {
+#pragma unroll
+        for (int g = 0; g < kRowGroup; ++g) ldsM[g * kRowTile + lane] = Mom{0.0, 0.0, 0.0};
+    }
+    Task cur{rg0, px0, 0};
+    PwOff oc = offs(cur);
+    const float* xc = xn + cur.p0;
+    const float* wc = wbase(cur);
+    f4 A[NB][2], B[NB][4];
+#pragma unroll
+    for (int i = 0; i < kSd; ++i) load(xc, wc, oc, 8 * i, true, A[i], B[i]);
+    for (;;) {
+        const Task nx = next(cur);
+        const bool nv = nx.rg < R;
+        const PwOff on = offs(nx);
+        const float* xnx = xn + nx.p0;
+        const float* wnx = wbase(nx);
+        const int64_t row0 = row0_of(cur), rlim = C_out - 1 - row0;
+        f16 acc[2][4];
+        pw_acc_init<BIAS>(acc, bias, row0, rlim, h, 0);
+        for (int s0 = 0; s0 < nsteps; s0 += NB) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const int ls = s0 + i + kSd;  // the step loaded now
+                const bool here = ls < nsteps;
+                load(here ? xc : xnx, here ? wc : wnx, here ? oc : on, 8 * (here ? ls : ls - nsteps),
+                     here || nv, A[(i + kSd) % NB], B[(i + kSd) % NB]);
+                pw_mfma_step(acc, A[i], B[i]);
+                __builtin_amdgcn_sched_group_barrier(0x020, TW ? 12 : 6, 0);  // the vector loads
+                __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);           // then 32 MFMAs
+            }
+        }
+        const bool lane_px = cur.p0 + 4 * j < HW;
+        pw_item_epilogue<true, MODE>(acc, zn + row0 * HW + cur.p0, cur.p0, HW, rlim, h, j, 0,
+                                     lane_px, zo, lds, ldsK);
+        if (STATS) {
+            __syncthreads();
+            pw_stats_merge(lds, ldsK, ldsM[cur.g * kRowTile + lane], lane,
+                           (int)min<int64_t>(kItem, HW - cur.p0));
+            __syncthreads();
+            if (!nv || nx.rg != cur.rg) {
+                // the row group's chunk partials, then fresh moments
+                const int nrt = (int)min<int64_t>(kRowGroup, R - cur.rg);
+                for (int g = 0; g < nrt; ++g) {
+                    const int64_t row = (cur.rg + g) * kRowTile + lane;
+                    const Mom m = ldsM[g * kRowTile + lane];
+                    if (row < C_out) part[(n * C_out + row) * cpp + kc] = make_double2(m.mean, m.m2);
+                    ldsM[g * kRowTile + lane] = Mom{0.0, 0.0, 0.0};
+                }
+            }
+        }
+        if (!nv) break;
+        cur = nx;
+        oc = on;
+        xc = xnx;
+        wc = wnx;
     }
 }
 
@@ -732,32 +916,41 @@ __global__ __launch_bounds__(64 * WPB, 2) void k_pw_wgrad(
 // C_in, C_out <= 64 (one dW tile); the GroupNorm reduction and its finish
 // run first and leave the per-unit S1 / S2 in unit_sums.
 //
-// Block = kFbWaves waves, one per SIMD, on one pixel chunk of one sample;
-// wave w takes the 32-pixel steps at chunk start + 32 (w + kFbWaves s).
-// Per step the wave loads z and dy (rows < 32 TM) and x (rows < 32 TN)
-// with row-contiguous 16-byte loads (k_pw_wgrad's slots) through buffer
-// descriptors bounded to the sample's planes (rows past C_out / C_in read
-// zeros), forms dz in registers from per-channel coefficients in LDS, and
-// stages the dz and x rows in its own LDS area (k_pw_wgrad's layout; no
-// barrier in the loop).  Then
+// Block = kFbPairs producer waves and kFbPairs consumer waves on one pixel
+// chunk of one sample (two waves per SIMD).  The chunk is walked in windows
+// of kFbPairs 32-pixel pieces, piece q being pair q's step.  The producers
+// load a window together, two windows ahead, with row-contiguous 16-byte
+// loads (k_pw_wgrad's slots: eight rows of 128 bytes per load) through
+// buffer descriptors bounded to the sample's planes; a lane's eight rows
+// are taken at piece (q + lane group) % kFbPairs, so one load touches four
+// offsets of the planes instead of one (eight rows at one offset of planes
+// a power of two apart meet one memory channel; a read of this shape took
+// 682 us for 3 GiB with one offset per load, 450 us with four).  Each lane
+// forms dz in registers from per-channel coefficients in LDS and writes its
+// dz and x rows into the stage of the piece's pair (two stages per pair,
+// k_pw_wgrad's layout).  One block barrier per window hands the stages to
+// the consumers; consumer q then runs, for its piece,
 //   dW: k_pw_wgrad's MFMAs, A = dz rows, B = x rows, K = the 32 pixels;
 //   dx: C[ci][p] = sum_co W[co][ci] dz[co][p], A = W^T from registers
 //       (lane (h, j) holds W[2s + h][32 t + j], zero for co >= C_out),
 //       B = dz[2s + h][pixel j] read from LDS, K = the C_out channels, so
 //       lane (h, j) ends with pixel j of rows tile_row(t, r, h), stored as
-//       128-byte row pieces.
-// The next step's loads are in flight during the MFMAs.  At the end the
-// waves add their dW tiles through LDS in wave order and the block writes
-// one partial for k_sum_partials.  Block 0 also adds dgamma / dbeta from
-// the plane sums, in k_param_finish's order.
+//       128-byte row pieces,
+// while the producers form the next window.  (The producers' vector ALU
+// work and the consumers' MFMAs do not run at the same time on a SIMD:
+// fp32 MFMAs and VALU instructions of two waves of one SIMD take the sum of
+// their times.  The split serves the shared, permuted loads.)  At the end
+// the consumers add their dW tiles through LDS in pair order and the block
+// writes one partial for k_sum_partials.  Block 0 also adds dgamma / dbeta
+// from the plane sums, in k_param_finish's order.
 // ======================================================================
-constexpr int kFbWaves = 4;
+constexpr int kFbPairs = 4;
 // Cache policy of the buffer accesses: non-temporal (each byte is touched
 // once; at 64 -> 64 channels over 2048^2 pixels 1065 -> 1033 us).
 constexpr int kNt = 2;
 
-template <bool SILU, int TM, int TN, bool ACC>
-__global__ __launch_bounds__(64 * kFbWaves, 1) void k_pw_cba_bwd(
+template <bool SILU, int TM, int TN, bool ACC, bool FULL>
+__global__ __launch_bounds__(128 * kFbPairs, 1) void k_pw_cba_bwd(
     const float* __restrict__ dy, const float* __restrict__ z, const float* __restrict__ x,
     const float* __restrict__ w, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ mean,
@@ -767,14 +960,16 @@ __global__ __launch_bounds__(64 * kFbWaves, 1) void k_pw_cba_bwd(
     float* __restrict__ part_w, int64_t C_in, int64_t C_out, int64_t HW, int64_t G,
     int64_t N, int64_t chunk, int64_t cpp) {
     constexpr int kZr = 32 * TM, kXr = 32 * TN;      // staged dz rows, x rows
-    constexpr int kStage = (kZr + kXr) * kWgStride;  // floats of one wave's staging
+    constexpr int kStage = (kZr + kXr) * kWgStride;  // floats of one stage
     constexpr int kR = 16 * TM * TN;                 // dW accumulators per lane
-    static_assert(kR * 64 <= kStage, "reduction layout");
-    __shared__ __attribute__((aligned(16))) float lds_all[kFbWaves * kStage];
+    static_assert(kR * 64 * kFbPairs <= 2 * kFbPairs * kStage, "reduction layout");
+    __shared__ __attribute__((aligned(16))) float lds_all[2 * kFbPairs * kStage];
     __shared__ __attribute__((aligned(16))) float coef[64 * 8];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    float* __restrict__ lds = lds_all + wv * kStage;
+    const bool producer = wv < kFbPairs;  // wave-uniform
+    const int pr = producer ? wv : wv - kFbPairs;
+    float* __restrict__ stages = lds_all + pr * 2 * kStage;
     const int h = lane >> 5, j = lane & 31;
     const int64_t n = (int64_t)blockIdx.x / cpp, kc = (int64_t)blockIdx.x - n * cpp;
     const int64_t cpg = C_out / G;
@@ -810,63 +1005,16 @@ __global__ __launch_bounds__(64 * kFbWaves, 1) void k_pw_cba_bwd(
         if (dbeta) dbeta[c] = (float)((double)dbeta[c] + sa);
         if (dgamma) dgamma[c] = (float)((double)dgamma[c] + sb);
     }
-
-    // W^T operand of dx: k-step s, half h -> channel co = 2s + h
-    float wt[TN][16 * TM];
-#pragma unroll
-    for (int t = 0; t < TN; ++t)
-#pragma unroll
-        for (int s = 0; s < 16 * TM; ++s) {
-            const int64_t co = 2 * s + h, ci = 32 * t + j;
-            wt[t][s] = (co < C_out && ci < C_in) ? w[co * C_in + ci] : 0.0f;
-        }
     __syncthreads();
 
-    // staging slots (k_pw_wgrad's): slot sl of lane l covers row 8 sl + l/8,
-    // pixels 4 (l % 8) .. +3 of the step
-    const int srow = lane >> 3, scol = 4 * (lane & 7);
-    const auto rz = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(z + n * C_out * HW),
-                                                      (short)0, (int)(C_out * HW * 4), kRsrcWord3);
-    const auto rg = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(dy + n * C_out * HW),
-                                                      (short)0, (int)(C_out * HW * 4), kRsrcWord3);
-    const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x + n * C_in * HW),
-                                                      (short)0, (int)(C_in * HW * 4), kRsrcWord3);
-    const bool want_dx = dx != nullptr, want_dw = part_w != nullptr;  // wave-uniform
-    const auto ro = __builtin_amdgcn_make_buffer_rsrc(want_dx ? dx + n * C_in * HW : dx, (short)0,
-                                                      (int)(C_in * HW * 4), kRsrcWord3);
+    const bool want_dx = dx != nullptr, want_dw = part_w != nullptr;  // block-uniform
     const uint32_t hw4 = (uint32_t)HW * 4u;
-    f4 sz[4 * TM], sg[4 * TM], sx[4 * TN];
-    // The descriptor's range check covers the vector offset only: the
-    // scalar offset is added to the address unchecked.  C_in and C_out are
-    // multiples of 8 (pw_cba_fused_fits), so an 8-row slot lies wholly
-    // inside or wholly past its tensor's rows; a slot past the end takes the
-    // last 8 rows' scalar offset instead, so no load leaves the sample.  Its
-    // values are harmless: a z/dy row past C_out has zero coefficients, so
-    // its dz is 0 (for finite inputs; a non-finite input makes its whole
-    // group NaN anyway), and an x row past C_in only reaches dW columns that
-    // are never stored.
-    const uint32_t zlim = (uint32_t)C_out - 8u, xlim = (uint32_t)C_in - 8u;
-    auto gload = [&](int64_t p) {
-        // lanes past the plane read its last 16 bytes (zeroed below)
-        const uint32_t q = (uint32_t)min<int64_t>(p + scol, HW - 4);
-        const uint32_t vo = (uint32_t)srow * hw4 + 4u * q;
-        // (the slots' scalar offsets are recomputed here on every step, a
-        // few scalar instructions, rather than hoisted into 16 registers)
-        uint32_t h4 = hw4, zl = zlim, xl = xlim;
-        asm volatile("" : "+s"(h4), "+s"(zl), "+s"(xl));
-#pragma unroll
-        for (int sl = 0; sl < 4 * TM; ++sl) {
-            const uint32_t so = min(8u * sl, zl) * h4;
-            sz[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rz, vo, so, kNt));
-            sg[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rg, vo, so, kNt));
-        }
-#pragma unroll
-        for (int sl = 0; sl < 4 * TN; ++sl)
-            sx[sl] = __builtin_bit_cast(
-                f4, __builtin_amdgcn_raw_buffer_load_b128(rx, vo, min(8u * sl, xl) * h4, kNt));
-    };
+    const int64_t cbeg = kc * chunk, pend = min(cbeg + chunk, HW);
+    constexpr int64_t kStride = (int64_t)kWgStep * kFbPairs;
+    // block barriers: one per step of the longest pair, plus one to drain
+    const int64_t iters = (pend - cbeg + kStride - 1) / kStride;
 
-    f16 accw[TM][TN], accx[TN];
+    f16 accw[TM][TN];
 #pragma unroll
     for (int mt = 0; mt < TM; ++mt)
 #pragma unroll
@@ -874,111 +1022,227 @@ __global__ __launch_bounds__(64 * kFbWaves, 1) void k_pw_cba_bwd(
 #pragma unroll
             for (int r = 0; r < 16; ++r) accw[mt][nt][r] = 0.0f;
 
-    const int64_t pend = min(kc * chunk + chunk, HW);
-    const int64_t px0 = kc * chunk + kWgStep * wv;
-    constexpr int64_t kStride = (int64_t)kWgStep * kFbWaves;
-    gload(px0);
-    for (int64_t p = px0; p < pend; p += kStride) {
-        const bool live = p + scol < pend;  // all four pixels or none (HW % 4 == 0)
+    if (producer) {
+        // staging slots (k_pw_wgrad's): slot sl of lane l covers row
+        // 8 sl + l/8, pixels 4 (l % 8) .. +3 of the step
+        const int srow = lane >> 3, scol = 4 * (lane & 7);
+        const auto rz = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(z + n * C_out * HW),
+                                                          (short)0, (int)(C_out * HW * 4), kRsrcWord3);
+        const auto rg = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(dy + n * C_out * HW),
+                                                          (short)0, (int)(C_out * HW * 4), kRsrcWord3);
+        const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x + n * C_in * HW),
+                                                          (short)0, (int)(C_in * HW * 4), kRsrcWord3);
+        // two register sets: the loads run two steps ahead of the dz
+        // work, so a step's loads have a whole step to arrive
+        f4 az[4 * TM], ag[4 * TM], ax[4 * TN], bz[4 * TM], bg[4 * TM], bx[4 * TN];
+        // The descriptor's range check covers the vector offset only: the
+        // scalar offset is added to the address unchecked.  C_in and C_out
+        // are multiples of 8 (pw_cba_fused_fits), so an 8-row slot lies
+        // wholly inside or wholly past its tensor's rows; a slot past the
+        // end takes the last 8 rows' scalar offset instead, so no load
+        // leaves the sample.  Its values are harmless: a z/dy row past
+        // C_out has zero coefficients, so its dz is 0 (for finite inputs; a
+        // non-finite input makes its whole group NaN anyway), and an x row
+        // past C_in only reaches dW columns that are never stored.
+        // FULL (C_out = 32 TM and C_in = 32 TN, e.g. 64 -> 64): every slot
+        // is a real row, so the offsets are the plain multiples of 8 rows.
+        const uint32_t zlim = (uint32_t)C_out - 8u, xlim = (uint32_t)C_in - 8u;
+        // The block's window of kFbPairs 32-pixel pieces (one per pair's
+        // step) is loaded by all producers together: lane group g of
+        // producer q takes its rows at piece (q + g) % kFbPairs, so the
+        // eight rows of one 16-byte load lie at four different offsets of
+        // their planes.  (Eight rows at one offset of planes a power of two
+        // apart meet the same memory channel: one load's lines are then
+        // served one after another.  A read of this shape took 682 us for
+        // 3 GiB with one offset per load and 450 us with four.)  The lane
+        // writes its rows into the stage of the pair that owns the piece.
+        const int piece = (pr + srow) % kFbPairs;
+        float* __restrict__ pstages = lds_all + piece * 2 * kStage;
+        auto gload = [&](int64_t wb, f4 (&sz)[4 * TM], f4 (&sg)[4 * TM], f4 (&sx)[4 * TN]) {
+            // lanes past the plane read its last 16 bytes (zeroed below)
+            const uint32_t q = (uint32_t)min<int64_t>(wb + kWgStep * piece + scol, HW - 4);
+            const uint32_t vo = (uint32_t)srow * hw4 + 4u * q;
+            if constexpr (FULL) {
+                const uint32_t row8 = 8u * hw4;
 #pragma unroll
-        for (int sl = 0; sl < 4 * TM; ++sl) {
-            const int co = 8 * sl + srow;
-            const f4 c0 = *reinterpret_cast<const f4*>(&coef[8 * co]);
-            const f4 c1 = *reinterpret_cast<const f4*>(&coef[8 * co + 4]);
-            f4 o;
+                for (int sl = 0; sl < 4 * TM; ++sl) {
+                    sz[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rz, vo, sl * row8, kNt));
+                    sg[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rg, vo, sl * row8, kNt));
+                }
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const float xh = fmaf(sz[sl][t] - c0[0], c0[1], c0[2]);
-                const float dzs = SILU ? dsilu_fast(sg[sl][t], fmaf(c0[3], xh, c1[0])) : sg[sl][t];
-                o[t] = live ? fmaf(c1[1], dzs, fmaf(c1[3], xh, c1[2])) : 0.0f;
+                for (int sl = 0; sl < 4 * TN; ++sl)
+                    sx[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rx, vo, sl * row8, kNt));
+            } else {
+                // (the slots' scalar offsets are recomputed here on every
+                // step, a few scalar instructions, rather than hoisted into
+                // 16 registers)
+                uint32_t h4 = hw4, zl = zlim, xl = xlim;
+                asm volatile("" : "+s"(h4), "+s"(zl), "+s"(xl));
+#pragma unroll
+                for (int sl = 0; sl < 4 * TM; ++sl) {
+                    const uint32_t so = min(8u * sl, zl) * h4;
+                    sz[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rz, vo, so, kNt));
+                    sg[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rg, vo, so, kNt));
+                }
+#pragma unroll
+                for (int sl = 0; sl < 4 * TN; ++sl)
+                    sx[sl] = __builtin_bit_cast(
+                        f4, __builtin_amdgcn_raw_buffer_load_b128(rx, vo, min(8u * sl, xl) * h4, kNt));
             }
-            *reinterpret_cast<f4*>(&lds[(8 * sl + srow) * kWgStride + scol]) = o;
-        }
+        };
+        // dz and x of the lane's piece of the window at wb into LDS stage st
+        // of the piece's pair
+        auto form = [&](int64_t wb, float* __restrict__ st, const f4 (&sz)[4 * TM],
+                        const f4 (&sg)[4 * TM], const f4 (&sx)[4 * TN]) {
+            // all four pixels or none (HW % 4 == 0)
+            const bool live = wb + kWgStep * piece + scol < pend;
 #pragma unroll
-        for (int sl = 0; sl < 4 * TN; ++sl) {
-            const f4 v = live ? sx[sl] : f4{0.f, 0.f, 0.f, 0.f};
-            *reinterpret_cast<f4*>(&lds[(kZr + 8 * sl + srow) * kWgStride + scol]) = v;
-        }
-        // the next step's loads (a wave-uniform branch: the last step loads
-        // nothing, which saved its reload's 0.6% of the traffic)
-        if (p + kStride < pend) gload(p + kStride);
-        __builtin_amdgcn_sched_group_barrier(0x200, 4 * (TM + TN), 0);  // the LDS writes
-        __builtin_amdgcn_sched_group_barrier(0x020, 8 * TM + 4 * TN, 0);  // the global loads
-
-        // dW += dz x^T over the step's 32 pixels
-        if (want_dw) {
+            for (int sl = 0; sl < 4 * TM; ++sl) {
+                const int co = 8 * sl + srow;
+                const f4 c0 = *reinterpret_cast<const f4*>(&coef[8 * co]);
+                const f4 c1 = *reinterpret_cast<const f4*>(&coef[8 * co + 4]);
+                f4 o;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                f4 A[TM], B[TN];
+                for (int t = 0; t < 4; ++t) {
+                    const float xh = fmaf(sz[sl][t] - c0[0], c0[1], c0[2]);
+                    const float dzs = SILU ? dsilu_fast(sg[sl][t], fmaf(c0[3], xh, c1[0])) : sg[sl][t];
+                    o[t] = live ? fmaf(c1[1], dzs, fmaf(c1[3], xh, c1[2])) : 0.0f;
+                }
+                *reinterpret_cast<f4*>(&st[(8 * sl + srow) * kWgStride + scol]) = o;
+            }
 #pragma unroll
-                for (int t = 0; t < TM; ++t)
-                    A[t] = *reinterpret_cast<const f4*>(&lds[(32 * t + j) * kWgStride + 16 * h + 4 * i]);
-#pragma unroll
-                for (int t = 0; t < TN; ++t)
-                    B[t] = *reinterpret_cast<const f4*>(
-                        &lds[(kZr + 32 * t + j) * kWgStride + 16 * h + 4 * i]);
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-#pragma unroll
-                    for (int mt = 0; mt < TM; ++mt)
-#pragma unroll
-                        for (int nt = 0; nt < TN; ++nt)
-                            accw[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(A[mt][q], B[nt][q],
-                                                                                accw[mt][nt], 0, 0, 0);
+            for (int sl = 0; sl < 4 * TN; ++sl) {
+                const f4 v = live ? sx[sl] : f4{0.f, 0.f, 0.f, 0.f};
+                *reinterpret_cast<f4*>(&st[(kZr + 8 * sl + srow) * kWgStride + scol]) = v;
+            }
+        };
+        // Windows alternate between the register sets (a and b) and the
+        // LDS stages (0 and 1); a set is refilled with the window two ahead
+        // right after its window is formed (a wave-uniform branch: windows
+        // past the chunk load nothing).  iters + 1 barriers, as the
+        // consumer.
+        int64_t wb = cbeg;
+        gload(wb, az, ag, ax);
+        gload(wb + kStride, bz, bg, bx);
+        for (int64_t i = 0; i <= iters; i += 2) {
+            if (i < iters) {
+                form(wb, pstages, az, ag, ax);
+                if (wb + 2 * kStride < pend) gload(wb + 2 * kStride, az, ag, ax);
+                wb += kStride;
+            }
+            lds_barrier();
+            if (i + 1 <= iters) {
+                if (i + 1 < iters) {
+                    form(wb, pstages + kStage, bz, bg, bx);
+                    if (wb + 2 * kStride < pend) gload(wb + 2 * kStride, bz, bg, bx);
+                    wb += kStride;
+                }
+                lds_barrier();
             }
         }
-        if (!want_dx) continue;
-        // dx = W^T dz for the step's 32 pixels
+    } else {
+        const auto ro = __builtin_amdgcn_make_buffer_rsrc(want_dx ? dx + n * C_in * HW : dx,
+                                                          (short)0, (int)(C_in * HW * 4), kRsrcWord3);
+        // W^T operand of dx: k-step s, half h -> channel co = 2s + h
+        float wt[TN][16 * TM];
 #pragma unroll
         for (int t = 0; t < TN; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) accx[t][r] = 0.0f;
+            for (int s = 0; s < 16 * TM; ++s) {
+                const int64_t co = 2 * s + h, ci = 32 * t + j;
+                wt[t][s] = (co < C_out && ci < C_in) ? w[co * C_in + ci] : 0.0f;
+            }
+        f16 accx[TN];
+        int64_t p = cbeg + kWgStep * pr;
+        for (int64_t i = 0; i <= iters; ++i) {
+            if (i > 0) {
+                // step i - 1 of the pair, at pixels p .. p + 31
+                const float* __restrict__ st = stages + ((i - 1) & 1) * kStage;
+                // dW += dz x^T over the step's 32 pixels
+                if (want_dw) {
 #pragma unroll
-        for (int s = 0; s < 16 * TM; ++s) {
-            const float b = lds[(2 * s + h) * kWgStride + j];
+                    for (int k = 0; k < 4; ++k) {
+                        f4 A[TM], B[TN];
 #pragma unroll
-            for (int t = 0; t < TN; ++t)
-                accx[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(wt[t][s], b, accx[t], 0, 0, 0);
-        }
-        if (p + j < pend) {
-            // Row 4h + c of the tile: with C_in a multiple of 8 its test
-            // reduces to the wave-uniform 32 t + 8 (r / 4) < C_in, so the
-            // stores of rows past C_in are skipped by a scalar branch (the
-            // scalar row offset is not range-checked).
-            const uint32_t vo = (uint32_t)(4 * h) * hw4 + 4u * (uint32_t)(p + j);
+                        for (int t = 0; t < TM; ++t)
+                            A[t] = *reinterpret_cast<const f4*>(&st[(32 * t + j) * kWgStride + 16 * h + 4 * k]);
 #pragma unroll
-            for (int t = 0; t < TN; ++t)
+                        for (int t = 0; t < TN; ++t)
+                            B[t] = *reinterpret_cast<const f4*>(
+                                &st[(kZr + 32 * t + j) * kWgStride + 16 * h + 4 * k]);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    if (32 * t + 8 * (r >> 2) >= C_in) continue;
-                    const uint32_t so = (uint32_t)tile_row(t, r, 0) * hw4;
-                    float v = accx[t][r];
-                    if (ACC)
-                        v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, vo, so, 0));
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), ro, vo, so, kNt);
+                        for (int q = 0; q < 4; ++q)
+#pragma unroll
+                            for (int mt = 0; mt < TM; ++mt)
+#pragma unroll
+                                for (int nt = 0; nt < TN; ++nt)
+                                    accw[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                        A[mt][q], B[nt][q], accw[mt][nt], 0, 0, 0);
+                    }
                 }
+                if (want_dx) {
+                    // dx = W^T dz for the step's 32 pixels
+#pragma unroll
+                    for (int t = 0; t < TN; ++t)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) accx[t][r] = 0.0f;
+#pragma unroll
+                    for (int s = 0; s < 16 * TM; ++s) {
+                        const float b = st[(2 * s + h) * kWgStride + j];
+#pragma unroll
+                        for (int t = 0; t < TN; ++t)
+                            accx[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(wt[t][s], b, accx[t], 0, 0, 0);
+                    }
+                    if (p + j < pend) {
+                        // Row 4h + c of the tile: with C_in a multiple of 8
+                        // its test reduces to the wave-uniform
+                        // 32 t + 8 (r / 4) < C_in, so the stores of rows
+                        // past C_in are skipped by a scalar branch (the
+                        // scalar row offset is not range-checked).
+                        const uint32_t vo = (uint32_t)(4 * h) * hw4 + 4u * (uint32_t)(p + j);
+#pragma unroll
+                        for (int t = 0; t < TN; ++t)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                if (!FULL && 32 * t + 8 * (r >> 2) >= C_in) continue;
+                                const uint32_t so = (uint32_t)tile_row(t, r, 0) * hw4;
+                                float v = accx[t][r];
+                                if (ACC)
+                                    v += __builtin_bit_cast(
+                                        float, __builtin_amdgcn_raw_buffer_load_b32(ro, vo, so, 0));
+                                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), ro, vo,
+                                                                      so, kNt);
+                            }
+                    }
+                }
+                p += kStride;
+            }
+            lds_barrier();
         }
     }
 
     if (!want_dw) return;
-    // the waves' dW tiles added in wave order (k_pw_wgrad's reduction)
-    __syncthreads();  // every wave is done with its staging area
+    // the consumers' dW tiles added in pair order (k_pw_wgrad's reduction);
+    // the last barrier above ended every read of the stages
     float* __restrict__ red = lds_all;
+    if (!producer) {
 #pragma unroll
-    for (int mt = 0; mt < TM; ++mt)
+        for (int mt = 0; mt < TM; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < TN; ++nt)
+            for (int nt = 0; nt < TN; ++nt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                red[(wv * kR + (mt * TN + nt) * 16 + r) * 64 + lane] = accw[mt][nt][r];
+                for (int r = 0; r < 16; ++r)
+                    red[(pr * kR + (mt * TN + nt) * 16 + r) * 64 + lane] = accw[mt][nt][r];
+    }
     __syncthreads();
-    constexpr int kShare = kR / kFbWaves;
+    if (producer) return;
+    constexpr int kShare = kR / kFbPairs;
 #pragma unroll
     for (int kk = 0; kk < kShare; ++kk) {
-        const int k = wv * kShare + kk;
+        const int k = pr * kShare + kk;
         float t = red[k * 64 + lane];
 #pragma unroll
-        for (int v = 1; v < kFbWaves; ++v) t += red[(v * kR + k) * 64 + lane];
+        for (int v = 1; v < kFbPairs; ++v) t += red[(v * kR + k) * 64 + lane];
         const int mt = k / (16 * TN), nt = (k / 16) % TN, r = k % 16;
         const int64_t co = tile_row(mt, r, h), ci = 32 * nt + j;
         if (co < C_out && ci < C_in) part_w[((int64_t)blockIdx.x * C_out + co) * C_in + ci] = t;
@@ -1498,7 +1762,19 @@ hipError_t launch_pw_conv(const PwArgs& a, int64_t N, int64_t C_in, int64_t C_ou
     // 64 -> 64 channels over 2048^2 pixels the statistics variant took 483
     // instead of 556 us, the plain one 456 instead of 469); split-K and the
     // general path keep two waves per SIMD and one step in flight.
+    // The streamed kernel (kSd steps in flight across items) when the K
+    // steps fill its operand ring exactly: the statistics variant at
+    // 64 -> 64 channels over 2048^2 pixels took 484-489 us instead of
+    // 505-512 us.
+    const bool stream = fast && ks == 1 && ksteps % (kSd + 1) == 0;
     auto go = [&](auto F, auto M, auto B) {
+        if constexpr (F()) {
+            if (stream) {
+                k_pw_conv_stream<M(), B()><<<grid, 64, 0, s>>>(a.x, a.w, a.bias, a.z, part, C_in,
+                                                              C_out, HW, chunk, cpp, Kpad, rpw);
+                return;
+            }
+        }
         auto run = [&](auto K, auto D) {
             k_pw_conv<F(), M(), B(), K(), D()><<<grid, 64 * K(), 0, s>>>(
                 a.x, a.w, a.bias, a.z, part, C_in, C_out, HW, chunk, cpp, Kpad, rpw, kseg, Kpad,
@@ -1690,7 +1966,7 @@ bool pw_cba_fused_fits(int64_t C_in, int64_t C_out, int64_t HW) {
 
 PwCbaPlan make_pw_cba_plan(int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t target) {
     PwCbaPlan p;
-    constexpr int64_t kStep = (int64_t)kWgStep * kFbWaves;  // pixels per block step
+    constexpr int64_t kStep = (int64_t)kWgStep * kFbPairs;  // pixels per block step
     const int64_t per = (N * HW + std::max<int64_t>(target, 1) - 1) / std::max<int64_t>(target, 1);
     int64_t chunk = (per + kStep - 1) / kStep * kStep;
     chunk = std::max(chunk, kStep);
@@ -1708,16 +1984,19 @@ hipError_t launch_pw_cba_backward(const PwCbaPlan& p, const PwCbaArgs& a, int64_
     const int tm = C_out <= 32 ? 1 : 2, tn = C_in <= 32 ? 1 : 2;
     float* part = a.dw ? a.part_w : nullptr;
     int tok = prof_begin(s, "pw_cba_bwd");
-    auto go = [&](auto S, auto M2, auto N2, auto A) {
-        k_pw_cba_bwd<S(), M2() ? 2 : 1, N2() ? 2 : 1, A()>
-            <<<dim3((unsigned)p.blocks), 64 * kFbWaves, 0, s>>>(
+    const bool full = C_out == 32 * tm && C_in == 32 * tn;
+    auto go = [&](auto S, auto M2, auto N2, auto A, auto F) {
+        k_pw_cba_bwd<S(), M2() ? 2 : 1, N2() ? 2 : 1, A(), F()>
+            <<<dim3((unsigned)p.blocks), 128 * kFbPairs, 0, s>>>(
                 a.dy, a.z, a.x, a.w, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, a.unit_sums,
                 a.plane_sums, a.dgamma, a.dbeta, a.dx, part, C_in, C_out, HW, G, N, p.chunk,
                 p.cpp);
     };
     bsel(silu, [&](auto S) {
         bsel(tm == 2, [&](auto M2) {
-            bsel(tn == 2, [&](auto N2) { bsel(accumulate_dx, [&](auto A) { go(S, M2, N2, A); }); });
+            bsel(tn == 2, [&](auto N2) {
+                bsel(accumulate_dx, [&](auto A) { bsel(full, [&](auto F) { go(S, M2, N2, A, F); }); });
+            });
         });
     });
     prof_end(s, tok);
