@@ -149,6 +149,60 @@ struct TilePrefetch {
     }
 };
 
+// Word 3 of a raw buffer descriptor on gfx9-family parts (gfx950 included):
+// 32-bit float data format, no swizzle, no stride.
+constexpr int kRsrcWord3 = 0x00020000;
+
+// Stride 1, every tile of a block after its first: the TH new rows
+// [O, IH) of the haloed tile (the rows above move up from the previous
+// tile, HaloRows), whose first is image row y > 0 (y = TH*(tile + 1) - pad
+// + O with pad <= O).  A thread's elements (TilePrefetch's: element
+// i = t + 256 k of those rows, row i / IWP, column i % IWP) lie at fixed
+// byte offsets from row y, computed once per block.  A tile then loads
+// through a buffer descriptor based at row y whose range ends at the
+// plane's end: elements of rows past the bottom read zeros without a test,
+// and columns outside the image or past IW carry an offset past any range,
+// so they read zeros too.  Per element that leaves the load itself,
+// against a division, bounds tests and a 64-bit address before.  Byte
+// offsets within TH rows fit 31 bits (planes_fit_32).
+// ROWS: rows fetched (TH: the new rows of a halo walk; IH: a whole tile,
+// for walks that fetch every tile whole, whose later tiles start at image
+// rows y > 0 as well).
+template <int K, int D, int RB = 1, int ROWS = kTH * RB>
+struct HaloFetch {
+    using T = Tile<K, 1, D, RB>;
+    static constexpr int NEL = ROWS * T::IWP;
+    static constexpr int NF = (NEL + kDwThreads - 1) / kDwThreads;
+    static constexpr uint32_t kOut = 0x80000000u;  // past any range
+    uint32_t off[NF];
+    __device__ __forceinline__ void init(int ix0, int Wi) {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int k = 0; k < NF; ++k) {
+            const int i = t + k * kDwThreads;
+            const int r = i / T::IWP, col = i - r * T::IWP, xx = ix0 + col;
+            const bool ok = i < NEL && col < T::IW && (unsigned)xx < (unsigned)Wi;
+            off[k] = ok ? (uint32_t)(r * Wi + xx) * 4u : kOut;
+        }
+    }
+    // range (bytes) of the rows from image row y to the plane's end
+    __device__ __forceinline__ static int range(int y, int Hi, int Wi) {
+        const int64_t rem = (int64_t)(Hi - y) * Wi * 4;
+        return (int)(rem < 0 ? 0 : (rem > 0x7fffffff ? 0x7fffffff : rem));
+    }
+    __device__ __forceinline__ static auto rsrc(const float* ip, int y, int lim, int Wi) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ip + (int64_t)y * Wi), (short)0,
+                                                 lim, kRsrcWord3);
+    }
+    template <typename R, int NR>
+    __device__ __forceinline__ void load(const R& rs, float (&v)[NR]) const {
+        static_assert(NF <= NR, "prefetch slots");
+#pragma unroll
+        for (int k = 0; k < NF; ++k)
+            v[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off[k], 0, 0));
+    }
+};
+
 // Stride 1: consecutive 32-row tiles of a block overlap in O = (K-1)*D
 // input rows (local rows [kTH, kTH + O) of one are rows [0, O) of the
 // next).  They move to the top of the LDS tile through NS registers per
@@ -215,6 +269,8 @@ __device__ __forceinline__ void dw_conv_body(
     float mK = 0.0f, ms = 0.0f, mq = 0.0f;  // STATS: shift and shifted sums
     int mcnt = 0;
     HaloRows<K, D> halo;  // stride 1 only (k7 fwd 0.610 -> 0.603 ms, k3 d5 0.476 -> 0.442 ms)
+    HaloFetch<K, D> hf;   // stride 1 only (k7 fwd 0.614 -> 0.556 ms, k3 0.413 -> 0.396 ms)
+    if constexpr (S == 1) hf.init(ix0, wi);
     for (int64_t ty = ty0; ty < ty1; ++ty) {
         int lr0 = 0;
         if (ty > ty0) {
@@ -228,7 +284,8 @@ __device__ __forceinline__ void dw_conv_body(
         __syncthreads();
         if (ty + 1 < ty1) {
             if constexpr (S == 1) {
-                pre.fetch(ip, (int)((ty + 1) * kTH - pad), ix0, hi, wi, HaloRows<K, D>::O);
+                const int y = (int)((ty + 1) * kTH - pad) + HaloRows<K, D>::O;
+                hf.load(HaloFetch<K, D>::rsrc(ip, y, HaloFetch<K, D>::range(y, hi, wi), wi), pre.v);
                 halo.take(tile);
             } else {
                 pre.fetch(ip, (int)((ty + 1) * kTH * S - pad), ix0, hi, wi);
@@ -330,6 +387,8 @@ __device__ __forceinline__ void dw_conv_rb_body(
     float mK = 0.0f, ms = 0.0f, mq = 0.0f;  // STATS: shift and shifted sums
     int mcnt = 0;
     HaloRows<K, 1, RB> halo;
+    HaloFetch<K, 1, RB> hf;
+    hf.init(ix0, wi);
     for (int64_t ty = ty0; ty < ty1; ++ty) {
         int lr0 = 0;
         if (ty > ty0) {
@@ -340,7 +399,8 @@ __device__ __forceinline__ void dw_conv_rb_body(
         pre.stash(tile, lr0);
         __syncthreads();
         if (ty + 1 < ty1) {
-            pre.fetch(ip, (int)((ty + 1) * T::TH - pad), ix0, hi, wi, HaloRows<K, 1, RB>::O);
+            const int y = (int)((ty + 1) * T::TH - pad) + HaloRows<K, 1, RB>::O;
+            hf.load(HaloFetch<K, 1, RB>::rsrc(ip, y, HaloFetch<K, 1, RB>::range(y, hi, wi), wi), pre.v);
             halo.take(tile);
         }
         float acc[RB][kPer];
@@ -478,6 +538,13 @@ __device__ __forceinline__ void dw_wgrad_body(
     // k7 0.672 -> 0.677 ms (64 x 2048^2)
     constexpr bool kShare = S == 1 && D > 1;
     HaloRows<K, D> halo;
+    // whole later tiles through HaloFetch (stride 1 without shared rows,
+    // K = 7: 0.558 -> 0.521 ms at 64 x 2048^2; k5 went 0.431 -> 0.448 ms
+    // and at k3 the offsets cost two waves per SIMD, 64 -> 74 VGPRs)
+    constexpr bool kWhole = S == 1 && !kShare && K >= 7;
+    using WF = HaloFetch<K, D, 1, Tile<K, 1, D>::IH>;
+    WF wf;
+    if constexpr (kWhole) wf.init(ix0, wi);
     for (int64_t ty = ty0; ty < ty1; ++ty) {
         int lr0 = 0;
         if (ty > ty0) {
@@ -496,6 +563,9 @@ __device__ __forceinline__ void dw_wgrad_body(
             if constexpr (kShare) {
                 pre.fetch(xp, (int)((ty + 1) * kTH - pad), ix0, hi, wi, HaloRows<K, D>::O);
                 halo.take(tile);
+            } else if constexpr (kWhole) {
+                const int y = (int)((ty + 1) * kTH - pad);
+                wf.load(WF::rsrc(xp, y, WF::range(y, hi, wi), wi), pre.v);
             } else {
                 pre.fetch(xp, (int)((ty + 1) * kTH * S - pad), ix0, hi, wi);
             }
@@ -828,6 +898,13 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
     const bool want_dx = dx != nullptr;
 
     float sdz[NS], sx[NS];  // the shared halo rows on their way to the top
+    // The later tiles' new rows through HaloFetch for K >= 5 (at 64 x
+    // 2048^2 k7 1.268 -> 1.185 ms, k5 0.928 -> 0.888 ms); at k3 its offsets
+    // cost the kernel a wave per SIMD (96 -> 112 VGPRs; 0.842 -> 0.860 ms),
+    // so k3 keeps fetch().
+    constexpr bool kHF = K >= 5;
+    HaloFetch<K, D> hf;
+    if constexpr (kHF) hf.init(ix0, wi);
     fetch(ty0, 0);
     for (int64_t ty = ty0; ty < ty1; ++ty) {
         const int lr0 = ty > ty0 ? O : 0;
@@ -859,7 +936,19 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
         }
         __syncthreads();
         if (ty + 1 < ty1) {
-            fetch(ty + 1, O);
+            if constexpr (kHF) {
+                const int y = (int)((ty + 1) * kTH) - PAD + O;
+                const int lim = HaloFetch<K, D>::range(y, hi, wi);
+                hf.load(HaloFetch<K, D>::rsrc(zp, y, lim, wi), pz);
+                hf.load(HaloFetch<K, D>::rsrc(gp, y, lim, wi), pg);
+                hf.load(HaloFetch<K, D>::rsrc(xp, y, lim, wi), px);
+                inside = 0;
+#pragma unroll
+                for (int k = 0; k < HaloFetch<K, D>::NF; ++k)
+                    inside |= (uint32_t)(hf.off[k] < (uint32_t)lim) << k;
+            } else {
+                fetch(ty + 1, O);
+            }
 #pragma unroll
             for (int k = 0; k < NS; ++k) {
                 const int j = t + k * kDwThreads;
@@ -1120,10 +1209,12 @@ int64_t tiles_of(int64_t H, int64_t W, int64_t* tiles_x) {
     return ((H + kTH - 1) / kTH) * *tiles_x;
 }
 
-// k_dw_conv addresses a plane with 32-bit element offsets.
+// k_dw_conv addresses a plane with 32-bit element offsets, and HaloFetch
+// the rows of a tile with 31-bit byte offsets (64 rows: 2^23 columns).
 bool planes_fit_32(const DwShape& sh) {
     const int64_t lim = (int64_t)1 << 31;
-    return sh.Hi * sh.Wi < lim && sh.Ho * sh.Wo < lim && sh.Hi < lim && sh.Wi < lim;
+    return sh.Hi * sh.Wi < lim && sh.Ho * sh.Wo < lim && sh.Hi < lim &&
+           sh.Wi < ((int64_t)1 << 23) && sh.Wo < ((int64_t)1 << 23);
 }
 
 // Tile rows per block of k_dw_conv over `planes` planes of H x W outputs:
