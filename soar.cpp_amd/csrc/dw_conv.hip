@@ -54,7 +54,7 @@ constexpr int kDwThreads = 256;
 constexpr int round4(int v) { return (v + 3) / 4 * 4; }
 
 // Input tile of a 32*RB x 64 output tile (RB output rows per thread).
-template <int K, int S, int D, int RB = 1>
+template <int K, int S, int D, int RB = 1, bool SP = false>
 struct Tile {
     static constexpr int TH = kTH * RB;                          // output rows
     static constexpr int IH = (TH - 1) * S + (K - 1) * D + 1;    // input rows
@@ -62,8 +62,25 @@ struct Tile {
     static constexpr int SL = (kPer - 1) * S + (K - 1) * D + 1;  // a thread's row segment
     static constexpr int SL4 = round4(SL);
     // row pitch: every thread's 16-byte segment reads stay inside the row
-    static constexpr int IWP = round4(IW) > (kTW - kPer) * S + SL4 ? round4(IW)
-                                                                   : (kTW - kPer) * S + SL4;
+    static constexpr int IWP0 = round4(IW) > (kTW - kPer) * S + SL4 ? round4(IW)
+                                                                    : (kTW - kPer) * S + SL4;
+    // SP (stride 1, one row per thread): a pitch that spreads a read pass
+    // over the LDS banks.  A 16-byte read is served 16 lanes at a time, two
+    // eight-lane groups on consecutive rows; one row's eight segments start
+    // 32 bytes apart.  Measured on a k7 tap window of reads (time per row
+    // read), pitch 68 / 72 / 76 / 80 / 84 floats: 49 / 70 / 48 / 89 / 48,
+    // so the pitch takes an odd number of 16-byte chunks (k7 and k3 at
+    // dilation 3: 72 -> 76).  The kernels that read two tiles per step use
+    // it (fused CBA backward k7 1.16 -> 1.10 ms, weight gradient 0.513 ->
+    // 0.476 ms at 64 x 2048^2); the convolutions gain less than the padding
+    // costs them (k7 0.542 -> 0.551 ms) and keep the plain pitch.
+    static constexpr int pitch() {
+        int p = IWP0;
+        if (!SP || S != 1 || RB != 1) return p;
+        while ((p / 4) % 2 == 0) p += 4;
+        return p;
+    }
+    static constexpr int IWP = pitch();
     static constexpr int floats = IH * IWP;
 };
 
@@ -89,10 +106,10 @@ __device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
 }
 
 // Row segment of a thread: SL4 floats of LDS row `lrow` from column c0*S.
-template <int K, int S, int D>
+template <int K, int S, int D, int RB = 1, bool SP = false>
 __device__ __forceinline__ void load_seg(const float* tile, int lrow, int c0,
-                                         float (&seg)[Tile<K, S, D>::SL4]) {
-    using T = Tile<K, S, D>;
+                                         float (&seg)[Tile<K, S, D, RB, SP>::SL4]) {
+    using T = Tile<K, S, D, RB, SP>;
     const f4* p = reinterpret_cast<const f4*>(tile + lrow * T::IWP + c0 * S);
 #pragma unroll
     for (int q = 0; q < T::SL4 / 4; ++q) {
@@ -107,9 +124,9 @@ __device__ __forceinline__ void load_seg(const float* tile, int lrow, int c0,
 // A thread's share of a tile's input (element i = threadIdx.x + k*256 of
 // the LDS tile), fetched into registers so the loads of the next tile are
 // in flight while the current one is computed.
-template <int K, int S, int D, int RB = 1>
+template <int K, int S, int D, int RB = 1, bool SP = false>
 struct TilePrefetch {
-    static constexpr int NR = (Tile<K, S, D, RB>::floats + kDwThreads - 1) / kDwThreads;
+    static constexpr int NR = (Tile<K, S, D, RB, SP>::floats + kDwThreads - 1) / kDwThreads;
     float v[NR];
 
     // input rows [iy0, iy0 + IH) x columns [ix0, ix0 + IWP) of plane `ip`
@@ -121,7 +138,7 @@ struct TilePrefetch {
     // come from the previous tile, see HaloRows).
     __device__ __forceinline__ void fetch(const float* __restrict__ ip, int iy0, int ix0, int Hi,
                                           int Wi, int lr0 = 0) {
-        using T = Tile<K, S, D, RB>;
+        using T = Tile<K, S, D, RB, SP>;
         const int nel = (T::IH - lr0) * T::IWP, base = lr0 * T::IWP;
         int t = (int)threadIdx.x;
         asm volatile("" : "+v"(t));
@@ -139,7 +156,7 @@ struct TilePrefetch {
         }
     }
     __device__ __forceinline__ void stash(float* tile, int lr0 = 0) const {
-        using T = Tile<K, S, D, RB>;
+        using T = Tile<K, S, D, RB, SP>;
         const int nel = (T::IH - lr0) * T::IWP, base = lr0 * T::IWP;
 #pragma unroll
         for (int k = 0; k < NR; ++k) {
@@ -168,9 +185,9 @@ constexpr int kRsrcWord3 = 0x00020000;
 // ROWS: rows fetched (TH: the new rows of a halo walk; IH: a whole tile,
 // for walks that fetch every tile whole, whose later tiles start at image
 // rows y > 0 as well).
-template <int K, int D, int RB = 1, int ROWS = kTH * RB>
+template <int K, int D, int RB = 1, int ROWS = kTH * RB, bool SP = false>
 struct HaloFetch {
-    using T = Tile<K, 1, D, RB>;
+    using T = Tile<K, 1, D, RB, SP>;
     static constexpr int NEL = ROWS * T::IWP;
     static constexpr int NF = (NEL + kDwThreads - 1) / kDwThreads;
     static constexpr uint32_t kOut = 0x80000000u;  // past any range
@@ -208,9 +225,9 @@ struct HaloFetch {
 // next).  They move to the top of the LDS tile through NS registers per
 // thread instead of being fetched again, so after its first tile a block
 // fetches its kTH new rows only.
-template <int K, int D, int RB = 1>
+template <int K, int D, int RB = 1, bool SP = false>
 struct HaloRows {
-    using T = Tile<K, 1, D, RB>;
+    using T = Tile<K, 1, D, RB, SP>;
     static constexpr int O = (K - 1) * D;
     static constexpr int NS = (O * T::IWP + kDwThreads - 1) / kDwThreads;
     float v[NS];
@@ -411,7 +428,7 @@ __device__ __forceinline__ void dw_conv_rb_body(
 #pragma unroll
         for (int i = 0; i < RB + K - 1; ++i) {
             float seg[T::SL4];
-            load_seg<K, 1, 1>(tile, r0 + i, c0, seg);
+            load_seg<K, 1, 1, RB>(tile, r0 + i, c0, seg);
 #pragma unroll
             for (int j = 0; j < RB; ++j) {
                 const int ky = i - j;
@@ -490,7 +507,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_conv_rb(
 // With `direct` (one sample and one tile group per plane, so a block's sums
 // are the whole sums) the block adds them into dw and db itself, exactly as
 // k_dw_wgrad_finish would from its single partial, and no finish runs.
-// (body of block b; `tile` holds Tile<K, S, D>::floats floats)
+// (body of block b; `tile` holds Tile<K, S, D, 1, true>::floats floats)
 template <int K, int S, int D>
 __device__ __forceinline__ void dw_wgrad_body(
     const float* __restrict__ dy, const float* __restrict__ x, float* __restrict__ part,
@@ -498,7 +515,7 @@ __device__ __forceinline__ void dw_wgrad_body(
     int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x, int64_t tiles_y,
     int64_t tpp, int per, int64_t b, float* __restrict__ tile,
     float (*red)[K * K + 1]) {
-    using T = Tile<K, S, D>;
+    using T = Tile<K, S, D, 1, true>;
     constexpr int KK1 = K * K + 1;
     const int64_t plane = b / tpp, gix = b - plane * tpp;
     const int64_t n = plane / C, c = plane - n * C;
@@ -513,7 +530,7 @@ __device__ __forceinline__ void dw_wgrad_body(
     const int64_t ty0 = tyg * per, ty1 = min(ty0 + per, tiles_y);
     const int64_t ox0 = tx * kTW;
     const int ix0 = (int)(ox0 * S - pad), hi = (int)Hi, wi = (int)Wi;
-    TilePrefetch<K, S, D> pre;
+    TilePrefetch<K, S, D, 1, true> pre;
     float gn[kPer];
     // a thread's 8 dy values: two aligned 16-byte loads when the row is
     // inside the plane and 16-byte aligned, else element by element
@@ -537,12 +554,12 @@ __device__ __forceinline__ void dw_wgrad_body(
     // gradient went 0.432 -> 0.419 ms, while k3 d1 went 0.438 -> 0.451 and
     // k7 0.672 -> 0.677 ms (64 x 2048^2)
     constexpr bool kShare = S == 1 && D > 1;
-    HaloRows<K, D> halo;
+    HaloRows<K, D, 1, true> halo;
     // whole later tiles through HaloFetch (stride 1 without shared rows,
     // K = 7: 0.558 -> 0.521 ms at 64 x 2048^2; k5 went 0.431 -> 0.448 ms
     // and at k3 the offsets cost two waves per SIMD, 64 -> 74 VGPRs)
     constexpr bool kWhole = S == 1 && !kShare && K >= 7;
-    using WF = HaloFetch<K, D, 1, Tile<K, 1, D>::IH>;
+    using WF = HaloFetch<K, D, 1, Tile<K, 1, D>::IH, true>;
     WF wf;
     if constexpr (kWhole) wf.init(ix0, wi);
     for (int64_t ty = ty0; ty < ty1; ++ty) {
@@ -551,7 +568,7 @@ __device__ __forceinline__ void dw_wgrad_body(
             __syncthreads();  // the previous tile's LDS reads are done
             if constexpr (kShare) {
                 halo.put(tile);
-                lr0 = HaloRows<K, D>::O;
+                lr0 = HaloRows<K, D, 1, true>::O;
             }
         }
         pre.stash(tile, lr0);
@@ -561,7 +578,7 @@ __device__ __forceinline__ void dw_wgrad_body(
         __syncthreads();
         if (ty + 1 < ty1) {
             if constexpr (kShare) {
-                pre.fetch(xp, (int)((ty + 1) * kTH - pad), ix0, hi, wi, HaloRows<K, D>::O);
+                pre.fetch(xp, (int)((ty + 1) * kTH - pad), ix0, hi, wi, HaloRows<K, D, 1, true>::O);
                 halo.take(tile);
             } else if constexpr (kWhole) {
                 const int y = (int)((ty + 1) * kTH - pad);
@@ -576,7 +593,7 @@ __device__ __forceinline__ void dw_wgrad_body(
 #pragma unroll
         for (int ky = 0; ky < K; ++ky) {
             float seg[T::SL4];
-            load_seg<K, S, D>(tile, r * S + ky * D, c0, seg);
+            load_seg<K, S, D, 1, true>(tile, r * S + ky * D, c0, seg);
 #pragma unroll
             for (int kx = 0; kx < K; ++kx)
 #pragma unroll
@@ -615,7 +632,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_wgrad(
     float* __restrict__ dw, float* __restrict__ db, bool direct, int64_t C, int64_t Hi,
     int64_t Wi, int64_t Ho, int64_t Wo, int64_t pad, int64_t tiles_x, int64_t tiles_y,
     int64_t tpp, int per) {
-    __shared__ __attribute__((aligned(16))) float tile[Tile<K, S, D>::floats];
+    __shared__ __attribute__((aligned(16))) float tile[Tile<K, S, D, 1, true>::floats];
     __shared__ float red[kDwThreads / 64][K * K + 1];
     dw_wgrad_body<K, S, D>(dy, x, part, dw, db, direct, C, Hi, Wi, Ho, Wo, pad, tiles_x, tiles_y,
                            tpp, per, xcd_block(blockIdx.x, gridDim.x), tile, red);
@@ -755,7 +772,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_bwd_small(
     int64_t Wo, int64_t pad, int64_t dtx, int64_t dty, int64_t dtpp, int dper, int64_t wtx,
     int64_t wty, int64_t wtpp, int wper, int64_t nbd) {
     constexpr int TD = S == 1 ? Tile<K, 1, D>::floats : DTile<K, S, D>::R * DTile<K, S, D>::W;
-    constexpr int TW = Tile<K, S, D>::floats;
+    constexpr int TW = Tile<K, S, D, 1, true>::floats;  // dw_wgrad_body's tile
     __shared__ __attribute__((aligned(16))) float tile[TD > TW ? TD : TW];
     __shared__ float red[kDwThreads / 64][K * K + 1];
     const int64_t b = xcd_block(blockIdx.x, gridDim.x);
@@ -806,7 +823,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
     float* __restrict__ dgamma, float* __restrict__ dbeta, float* __restrict__ dx,
     float* __restrict__ part, float* __restrict__ dw, bool direct, int64_t N, int64_t C,
     int64_t G, int64_t H, int64_t W, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per) {
-    using T = Tile<K, 1, D>;
+    using T = Tile<K, 1, D, 1, true>;
     constexpr int KK1 = K * K + 1;
     constexpr int PAD = (K - 1) * D / 2;
     constexpr int NR = (T::floats + kDwThreads - 1) / kDwThreads;
@@ -903,7 +920,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
     // cost the kernel a wave per SIMD (96 -> 112 VGPRs; 0.842 -> 0.860 ms),
     // so k3 keeps fetch().
     constexpr bool kHF = K >= 5;
-    HaloFetch<K, D> hf;
+    HaloFetch<K, D, 1, kTH, true> hf;
     if constexpr (kHF) hf.init(ix0, wi);
     fetch(ty0, 0);
     for (int64_t ty = ty0; ty < ty1; ++ty) {
@@ -938,13 +955,13 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
         if (ty + 1 < ty1) {
             if constexpr (kHF) {
                 const int y = (int)((ty + 1) * kTH) - PAD + O;
-                const int lim = HaloFetch<K, D>::range(y, hi, wi);
-                hf.load(HaloFetch<K, D>::rsrc(zp, y, lim, wi), pz);
-                hf.load(HaloFetch<K, D>::rsrc(gp, y, lim, wi), pg);
-                hf.load(HaloFetch<K, D>::rsrc(xp, y, lim, wi), px);
+                const int lim = HaloFetch<K, D, 1, kTH, true>::range(y, hi, wi);
+                hf.load(HaloFetch<K, D, 1, kTH, true>::rsrc(zp, y, lim, wi), pz);
+                hf.load(HaloFetch<K, D, 1, kTH, true>::rsrc(gp, y, lim, wi), pg);
+                hf.load(HaloFetch<K, D, 1, kTH, true>::rsrc(xp, y, lim, wi), px);
                 inside = 0;
 #pragma unroll
-                for (int k = 0; k < HaloFetch<K, D>::NF; ++k)
+                for (int k = 0; k < HaloFetch<K, D, 1, kTH, true>::NF; ++k)
                     inside |= (uint32_t)(hf.off[k] < (uint32_t)lim) << k;
             } else {
                 fetch(ty + 1, O);
@@ -967,7 +984,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
 #pragma unroll
             for (int ky = 0; ky < K; ++ky) {
                 float seg[T::SL4];
-                load_seg<K, 1, D>(tdz, ro + ky * D, c0, seg);
+                load_seg<K, 1, D, 1, true>(tdz, ro + ky * D, c0, seg);
 #pragma unroll
                 for (int kx = 0; kx < K; ++kx)
 #pragma unroll
@@ -986,7 +1003,7 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
 #pragma unroll
             for (int ky = 0; ky < K; ++ky) {
                 float seg[T::SL4];
-                load_seg<K, 1, D>(tx, ro + ky * D, c0, seg);
+                load_seg<K, 1, D, 1, true>(tx, ro + ky * D, c0, seg);
 #pragma unroll
                 for (int kx = 0; kx < K; ++kx)
 #pragma unroll
