@@ -50,6 +50,15 @@ extern "C" {
 #define SOAR_GN_SILU 1u          /* apply SiLU after the affine GroupNorm     */
 #define SOAR_GN_RESIDUAL 2u      /* fwd: y += x;  bwd: dx += dy (x + f(x))    */
 #define SOAR_GN_ACCUMULATE_DX 4u /* bwd: dx += result instead of dx = result  */
+/* Convolution backward calls (soar_pw_conv_backward, soar_pw_cba_backward,
+ * soar_dw_conv_backward, soar_dw_cba_backward): leave the weight / bias
+ * gradient's final addition pending.  The per-block partial sums stay in
+ * the call's workspace and dweight / dbias receive them at the next
+ * soar_weight_grad_flush on this thread, added exactly as the call itself
+ * would have added them (the same float64 sums in the same order), so the
+ * gradients are bit for bit the same.  The caller keeps the workspace and
+ * the gradient buffers untouched until the flush.  dx is written at once. */
+#define SOAR_DEFER_WEIGHT_FINISH 8u
 
 /* Message for the last failing call on this thread ("" if none). */
 SOAR_API const char* soar_last_error(void);
@@ -421,6 +430,30 @@ SOAR_API int soar_dw_cba_backward(
     int64_t W_out, int64_t K, int64_t pad, int64_t stride, int64_t dil,
     int64_t G, unsigned flags, void* workspace, size_t workspace_bytes,
     void* stream);
+
+/* Runs every weight-gradient finish the calling thread's convolution
+ * backward calls left pending (SOAR_DEFER_WEIGHT_FINISH) as one kernel
+ * launch (several past 64 of them) on the stream they were queued on;
+ * `stream` must be that stream (or the queue empty).  A call that queues a
+ * finish on another stream, or one adding into weights already queued,
+ * flushes the queue first.  No counterpart in the reference, whose layers
+ * add their weight gradients in their own backward
+ * (src/nn/layers.cpp:34-85, src/cuda/ops/convolution_kernels.cu:42-133);
+ * it serves a training step that reads no weight gradient before its
+ * clip (src/engine/trainer.cpp:110-220). */
+SOAR_API int soar_weight_grad_flush(void* stream);
+
+/* Weight-gradient finishes pending on the calling thread. */
+SOAR_API size_t soar_weight_grad_pending(void);
+
+/* Drops the calling thread's pending weight-gradient finishes without
+ * running them: for a caller that abandons the backward pass that queued
+ * them (an error part way through, a retry with a new workspace arena),
+ * whose workspaces they read.  Their weight gradients keep whatever the
+ * abandoned pass left.  A pending finish whose workspace is freed or
+ * reused must be dropped before the next convolution backward call or
+ * flush on the thread, which would otherwise run it. */
+SOAR_API void soar_weight_grad_discard(void);
 
 /* Reference signatures, one sample.
  * Replaces: conv2d_dw_forward (cuda_kernels.hpp:64-66,

@@ -382,6 +382,20 @@ namespace soar::capi {
 
 thread_local bool g_quiet_call = false;
 
+DeferWeightFinish::DeferWeightFinish(bool on) : prev_(soar::gn::weight_finish_deferring()) {
+    soar::gn::weight_finish_defer(prev_ || on);
+}
+
+DeferWeightFinish::~DeferWeightFinish() { soar::gn::weight_finish_defer(prev_); }
+
+int weight_finish_room(const float* dweight, int64_t nw, const float* dbias, int64_t nb,
+                       void* stream, unsigned flags) {
+    const hipError_t e = soar::gn::weight_finish_before(
+        dweight, dweight ? nw : 0, dbias, dbias ? nb : 0, static_cast<hipStream_t>(stream),
+        (flags & SOAR_DEFER_WEIGHT_FINISH) != 0);
+    return e == hipSuccess ? SOAR_OK : hip_fail(e, "weight-gradient finish launch");
+}
+
 int gn_backward(const float* dy, const float* x, const float* gamma, const float* beta,
                 const float* mean, const float* rstd, const float* mean_lo, float* dx,
                 float* dgamma, float* dbeta, int64_t N, int64_t C, int64_t HW, int64_t G,
@@ -632,6 +646,20 @@ SOAR_API size_t soar_pw_conv_backward_workspace_bytes(int64_t N, int64_t C_in, i
     return soar::gn::pw_bwd_workspace_bytes(p);
 }
 
+SOAR_API int soar_weight_grad_flush(void* stream) {
+    if (soar::gn::weight_finish_pending() == 0) return ok();
+    if (static_cast<hipStream_t>(stream) != soar::gn::weight_finish_stream())
+        return fail(SOAR_EINVAL,
+                    "the pending weight-gradient finishes were queued on another stream");
+    const hipError_t e = soar::gn::weight_finish_flush();
+    if (e != hipSuccess) return hip_fail(e, "weight-gradient finish launch");
+    return ok();
+}
+
+SOAR_API size_t soar_weight_grad_pending(void) { return soar::gn::weight_finish_pending(); }
+
+SOAR_API void soar_weight_grad_discard(void) { soar::gn::weight_finish_discard(); }
+
 SOAR_API int soar_pw_conv_backward(const float* dz, const float* x, const float* weight,
                                    float* dx, float* dweight, float* dbias, int64_t N,
                                    int64_t C_in, int64_t C_out, int64_t HW, unsigned flags,
@@ -639,8 +667,10 @@ SOAR_API int soar_pw_conv_backward(const float* dz, const float* x, const float*
     int64_t ie = 0, oe = 0;
     int rc = check_pw_shape(N, C_in, C_out, HW, &ie, &oe);
     if (rc) return rc;
-    if (flags & ~SOAR_GN_ACCUMULATE_DX)
-        return fail(SOAR_EINVAL, "unsupported flags 0x%x (SOAR_GN_ACCUMULATE_DX only)", flags);
+    if (flags & ~(SOAR_GN_ACCUMULATE_DX | SOAR_DEFER_WEIGHT_FINISH))
+        return fail(SOAR_EINVAL,
+                    "unsupported flags 0x%x (SOAR_GN_ACCUMULATE_DX, SOAR_DEFER_WEIGHT_FINISH)",
+                    flags);
     if (oe == 0 || (!dx && !dweight && !dbias)) return ok();
     if (C_in == 0) return fail(SOAR_EINVAL, "C_in must be positive");
     if ((rc = require_device())) return rc;
@@ -670,6 +700,8 @@ SOAR_API int soar_pw_conv_backward(const float* dz, const float* x, const float*
                     workspace_bytes, need);
     if ((rc = check_dev(workspace, need, "workspace"))) return rc;
     soar::gn::PwBwdArgs a{dz, x, weight, dx, dweight, dbias, workspace};
+    if ((rc = weight_finish_room(dweight, C_out * C_in, dbias, C_out, stream, flags))) return rc;
+    DeferWeightFinish defer((flags & SOAR_DEFER_WEIGHT_FINISH) != 0);
     hipError_t e = soar::gn::launch_pw_backward(p, a, N, C_in, C_out, HW,
                                                 (flags & SOAR_GN_ACCUMULATE_DX) != 0,
                                                 t.pw_small, static_cast<hipStream_t>(stream));
@@ -784,9 +816,13 @@ SOAR_API int soar_pw_cba_backward(const float* dy, const float* z, const float* 
     int rc = check_pw_shape(N, C_in, C_out, HW, &ie, &oe);
     if (rc) return rc;
     if ((rc = check_shape(N, C_out, HW, G, &elems))) return rc;
-    if (flags & ~(SOAR_GN_SILU | SOAR_GN_ACCUMULATE_DX))
+    if (flags & ~(SOAR_GN_SILU | SOAR_GN_ACCUMULATE_DX | SOAR_DEFER_WEIGHT_FINISH))
         return fail(SOAR_EINVAL,
-                    "unsupported flags 0x%x (SOAR_GN_SILU, SOAR_GN_ACCUMULATE_DX)", flags);
+                    "unsupported flags 0x%x (SOAR_GN_SILU, SOAR_GN_ACCUMULATE_DX, "
+                    "SOAR_DEFER_WEIGHT_FINISH)",
+                    flags);
+    if ((rc = weight_finish_room(dweight, C_out * C_in, nullptr, 0, stream, flags))) return rc;
+    DeferWeightFinish defer((flags & SOAR_DEFER_WEIGHT_FINISH) != 0);
     if (oe == 0 || (!dx && !dweight && !dgamma && !dbeta)) return ok();
     if (C_in == 0) return fail(SOAR_EINVAL, "C_in must be positive");
     if ((rc = require_device())) return rc;
@@ -970,8 +1006,10 @@ SOAR_API int soar_dw_conv_backward(const float* dy, const float* x, const float*
     int64_t ie = 0, oe = 0;
     int rc = check_dw_shape(sh, &ie, &oe);
     if (rc) return rc;
-    if (flags & ~SOAR_GN_ACCUMULATE_DX)
-        return fail(SOAR_EINVAL, "unsupported flags 0x%x (SOAR_GN_ACCUMULATE_DX only)", flags);
+    if (flags & ~(SOAR_GN_ACCUMULATE_DX | SOAR_DEFER_WEIGHT_FINISH))
+        return fail(SOAR_EINVAL,
+                    "unsupported flags 0x%x (SOAR_GN_ACCUMULATE_DX, SOAR_DEFER_WEIGHT_FINISH)",
+                    flags);
     if ((!dx && !dweight && !dbias) || N * C == 0) return ok();
     if ((rc = require_device())) return rc;
     const size_t wb = (size_t)(C * K * K) * 4;
@@ -992,6 +1030,8 @@ SOAR_API int soar_dw_conv_backward(const float* dy, const float* x, const float*
         if ((rc = check_dev(workspace, need, "workspace"))) return rc;
     }
     // with no input pixels, dweight gets nothing and dx is empty
+    if ((rc = weight_finish_room(dweight, C * K * K, dbias, C, stream, flags))) return rc;
+    DeferWeightFinish defer((flags & SOAR_DEFER_WEIGHT_FINISH) != 0);
     hipError_t e = soar::gn::launch_dw_backward(sh, dy, x, weight, ie > 0 ? dx : nullptr,
                                                 ie > 0 ? dweight : nullptr, oe > 0 ? dbias : nullptr,
                                                 (flags & SOAR_GN_ACCUMULATE_DX) != 0, workspace,
@@ -1059,9 +1099,13 @@ SOAR_API int soar_dw_cba_backward(const float* dy, const float* z, const float* 
     int rc = check_dw_shape(sh, &ie, &oe);
     if (rc) return rc;
     if ((rc = check_shape(N, C, H_out * W_out, G, &elems))) return rc;
-    if (flags & ~(SOAR_GN_SILU | SOAR_GN_ACCUMULATE_DX))
+    if (flags & ~(SOAR_GN_SILU | SOAR_GN_ACCUMULATE_DX | SOAR_DEFER_WEIGHT_FINISH))
         return fail(SOAR_EINVAL,
-                    "unsupported flags 0x%x (SOAR_GN_SILU, SOAR_GN_ACCUMULATE_DX)", flags);
+                    "unsupported flags 0x%x (SOAR_GN_SILU, SOAR_GN_ACCUMULATE_DX, "
+                    "SOAR_DEFER_WEIGHT_FINISH)",
+                    flags);
+    if ((rc = weight_finish_room(dweight, C * K * K, nullptr, 0, stream, flags))) return rc;
+    DeferWeightFinish defer((flags & SOAR_DEFER_WEIGHT_FINISH) != 0);
     if (oe == 0 || (!dx && !dweight && !dgamma && !dbeta)) return ok();
     if ((rc = require_device())) return rc;
     if (!dw_grids_fit(sh)) return fail(SOAR_EINVAL, "shape is too large for one launch grid");

@@ -58,4 +58,24 @@ int gn_backward(const float* dy, const float* x, const float* gamma, const float
 // Set while a ws_scratch call runs on this thread: kernel timing is skipped.
 extern thread_local bool g_quiet_call;
 
+// For the duration of one convolution backward call: with `on` its weight-
+// gradient finishes are queued on the thread (SOAR_DEFER_WEIGHT_FINISH)
+// instead of launched.  Nested calls (a CBA backward's convolution
+// backward) keep an enclosing call's setting.
+class DeferWeightFinish {
+public:
+    explicit DeferWeightFinish(bool on);
+    ~DeferWeightFinish();
+    DeferWeightFinish(const DeferWeightFinish&) = delete;
+    DeferWeightFinish& operator=(const DeferWeightFinish&) = delete;
+
+private:
+    bool prev_;
+};
+// Before a convolution backward call launches: runs the queued finishes
+// when they add into this call's dweight / dbias, or when a deferring call
+// comes on another stream (SOAR_OK, or the launch's error status).
+int weight_finish_room(const float* dweight, int64_t nw, const float* dbias, int64_t nb,
+                       void* stream, unsigned flags);
+
 }  // namespace soar::capi

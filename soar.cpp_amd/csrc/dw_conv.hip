@@ -1380,6 +1380,9 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
         if (fused) {
             if (!direct) {
                 const int64_t KK1 = sh.K * sh.K + 1, E = sh.C * KK1;
+                hipError_t qe = hipSuccess;
+                if (weight_finish_queue({part, dw, db, E, sh.N * wtpp, KK1}, s, &qe))
+                    return qe != hipSuccess ? qe : hipGetLastError();
                 const int tok = prof_begin(s, "dw_conv_wgrad_finish");
                 k_dw_wgrad_finish<<<dim3((unsigned)((E + 63) / 64)), 1024, 0, s>>>(
                     part, dw, db, E, sh.N * wtpp, KK1);
@@ -1460,6 +1463,11 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
         });
         prof_end(s, tok);
         if (fast && direct) return hipGetLastError();  // the blocks added the sums
+        if (fast) {
+            hipError_t qe = hipSuccess;
+            if (weight_finish_queue({part, dw, db, sh.C * KK1, sh.N * tpp, KK1}, s, &qe))
+                return qe != hipSuccess ? qe : hipGetLastError();
+        }
         tok = prof_begin(s, "dw_conv_wgrad_finish");
         if (fast) {
             const int64_t E = sh.C * KK1;
@@ -1536,6 +1544,9 @@ hipError_t launch_dw_cba_backward(const DwShape& sh, const DwCbaArgs& a, int64_t
     prof_end(s, tok);
     if (a.dw && !direct) {
         const int64_t KK1 = sh.K * sh.K + 1, E = sh.C * KK1;
+        hipError_t qe = hipSuccess;
+        if (weight_finish_queue({part, a.dw, nullptr, E, sh.N * tpp, KK1}, s, &qe))
+            return qe != hipSuccess ? qe : hipGetLastError();
         tok = prof_begin(s, "dw_cba_wgrad_finish");
         k_dw_wgrad_finish<<<dim3((unsigned)((E + 63) / 64)), 1024, 0, s>>>(part, a.dw, nullptr, E,
                                                                            sh.N * tpp, KK1);

@@ -395,6 +395,36 @@ hipError_t launch_add_backward(const float* gy, float* ga, float* gb,
                                int64_t n, hipStream_t s);
 hipError_t launch_fill(float* p, float v, int64_t n, hipStream_t s);
 
+// Deferred weight-gradient finishes (wfinish.hip).  An entry adds
+// sum_g part[g][e] (float64, k_sum_partials' order) into out0[e] (kk1 = 0)
+// or, for the depthwise layout e = c*kk1 + k, into tap c*(kk1-1) + k of
+// out0 (k < kk1 - 1) or bias c of out1 (k = kk1 - 1); null outputs skip.
+struct WeightFinish {
+    const float* part;  // [G][E] fp32 partials
+    float* out0;
+    float* out1;
+    int64_t E, G, kk1;
+};
+// While a C-ABI call with SOAR_DEFER_WEIGHT_FINISH runs, its launchers
+// queue their finishes on the calling thread (weight_finish_queue returns
+// true; *err reports a flush the queue had to run first: a finish on
+// another stream, or one adding into weights already queued) instead of
+// launching them; weight_finish_flush launches everything queued, on the
+// stream it was queued on.
+void weight_finish_defer(bool on);
+bool weight_finish_deferring();
+bool weight_finish_queue(const WeightFinish& f, hipStream_t s, hipError_t* err);
+hipError_t weight_finish_flush();
+// Called by a convolution backward entry point before it launches anything:
+// flushes the queue when its weight gradients [o0, o0 + n0) and
+// [o1, o1 + n1) overlap a queued finish's (whatever `defer`: the additions
+// keep their call order) or when a deferring call comes on another stream.
+hipError_t weight_finish_before(const float* o0, int64_t n0, const float* o1, int64_t n1,
+                                hipStream_t s, bool defer);
+size_t weight_finish_pending();
+hipStream_t weight_finish_stream();
+void weight_finish_discard();
+
 // Kernel timing hooks (capi.cpp).  prof_begin returns a token passed to
 // prof_end; both are no-ops while timing is off.
 int prof_begin(hipStream_t s, const char* kernel);

@@ -1944,9 +1944,17 @@ hipError_t launch_pw_backward(const PwBwdPlan& p, const PwBwdArgs& a, int64_t N,
             });
         });
         prof_end(s, tok);
+        const int64_t E = C_out * C_in;
+        if (weight_finish_deferring()) {  // queued for the model's one finish launch
+            hipError_t qe = hipSuccess;
+            if (a.dw) weight_finish_queue({part_w, a.dw, nullptr, E, p.Gb, 0}, s, &qe);
+            if (qe == hipSuccess && a.db)
+                weight_finish_queue({part_b, a.db, nullptr, C_out, p.Gb, 0}, s, &qe);
+            if (qe != hipSuccess) return qe;
+            return hipGetLastError();
+        }
         tok = prof_begin(s, "pw_conv_wgrad_finish");
         // dW and db in one launch
-        const int64_t E = C_out * C_in;
         const int64_t nbw = a.dw ? (E + 63) / 64 : 0, nbb = a.db ? (C_out + 63) / 64 : 0;
         k_sum_partials<<<dim3((unsigned)(nbw + nbb)), 1024, 0, s>>>(part_w, a.dw, E, nbw, part_b,
                                                                     a.db, C_out, p.Gb);
@@ -2001,8 +2009,11 @@ hipError_t launch_pw_cba_backward(const PwCbaPlan& p, const PwCbaArgs& a, int64_
     });
     prof_end(s, tok);
     if (a.dw) {
-        tok = prof_begin(s, "pw_cba_wgrad_finish");
         const int64_t E = C_out * C_in;
+        hipError_t qe = hipSuccess;
+        if (weight_finish_queue({part, a.dw, nullptr, E, p.blocks, 0}, s, &qe))
+            return qe != hipSuccess ? qe : hipGetLastError();
+        tok = prof_begin(s, "pw_cba_wgrad_finish");
         k_sum_partials<<<dim3((unsigned)((E + 63) / 64)), 1024, 0, s>>>(
             part, a.dw, E, (E + 63) / 64, nullptr, nullptr, 0, p.blocks);
         prof_end(s, tok);

@@ -129,6 +129,9 @@ void with_acts(SoarModelHandle* s, int64_t h, int64_t w, F&& fn, U&& undo) {
             s->act_peak = std::max(s->act_peak, s->acts->slab().current_offset());
             return;
         } catch (const soar::OutOfMemory&) {
+            // weight-gradient finishes of the abandoned attempt read its
+            // arena, freed below (run_backward drops them too)
+            soar_weight_grad_discard();
             if (attempt >= 3) throw;
             undo();
             ensure_acts(s, s->acts->slab().total_capacity() * 2);

@@ -1,5 +1,9 @@
 #include "soar/autograd.hpp"
 
+#include "soar/core.hpp"
+#include "soar/kernels.hpp"
+#include "soar_gn.h"
+
 #include <queue>
 #include <unordered_set>
 
@@ -149,7 +153,19 @@ TensorPtr write_target(const TensorPtr& tensor, bool* fresh) {
 }
 
 void run_backward(std::shared_ptr<AutogradNode> root, const TensorPtr& root_grad) {
-    autograd::Engine::get_default_engine().execute(std::move(root), root_grad);
+    try {
+        autograd::Engine::get_default_engine().execute(std::move(root), root_grad);
+        // the convolution weight gradients whose final addition the layers
+        // left pending (SOAR_DEFER_WEIGHT_FINISH), in one launch
+        if (soar_weight_grad_pending() > 0)
+            hip::kernels::check(soar_weight_grad_flush(exec::stream()), "weight-gradient finish");
+    } catch (...) {
+        // An abandoned pass (e.g. OutOfMemory, after which the caller frees
+        // the activation arena holding the queued partials and runs the
+        // step again): its pending finishes must never run.
+        soar_weight_grad_discard();
+        throw;
+    }
 }
 
 }  // namespace soar

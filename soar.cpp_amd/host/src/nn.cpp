@@ -161,6 +161,14 @@ struct GroupNormNode : autograd::AutogradNode {
 // Gradient buffer of parameter `p` for a kernel that accumulates (+=):
 // its existing device .grad when p is a leaf that has one (no temporary,
 // no merge pass), else fresh zeros that the caller propagates.
+// SOAR_DEFER_WEIGHT_FINISH when the weight gradients of a backward call all
+// land in the parameters' own gradient buffers (direct): their final
+// addition then joins the single launch the backward pass ends with
+// (run_backward's soar_weight_grad_flush), and nothing reads those buffers
+// before it.  A fresh gradient tensor is handed on by propagate_grad right
+// after the call, so that call finishes its sums at once.
+unsigned defer_finish(bool deferrable) { return deferrable ? SOAR_DEFER_WEIGHT_FINISH : 0u; }
+
 TensorPtr param_grad_target(const TensorPtr& p, bool* direct) {
     if (!p->grad_fn() && p->grad() && p->grad()->is_cuda()) {
         *direct = true;
@@ -239,11 +247,12 @@ struct Conv2dNode : autograd::AutogradNode {
         float* px = gx ? gx->cuda_data() : nullptr;
         float* pw = gw ? gw->cuda_data() : nullptr;
         float* pb = gb ? gb->cuda_data() : nullptr;
+        const unsigned dfl = defer_finish((!gw || dw_direct) && (!gb || db_direct));
         if (kind == ConvKind::Pointwise) {
             const size_t wsb =
                 soar_pw_conv_backward_workspace_bytes(g.N, g.C_in, g.C_out, g.H * g.W);
             check(soar_pw_conv_backward(go->cuda_data(), input->cuda_data(), weight->cuda_data(),
-                                        px, pw, pb, g.N, g.C_in, g.C_out, g.H * g.W, fl,
+                                        px, pw, pb, g.N, g.C_in, g.C_out, g.H * g.W, fl | dfl,
                                         workspace(wsb), wsb, exec::stream()),
                   "pointwise convolution backward");
         } else if (kind == ConvKind::General) {
@@ -258,7 +267,7 @@ struct Conv2dNode : autograd::AutogradNode {
                                                                      g.Wo, K, stride, dil);
             check(soar_dw_conv_backward(go->cuda_data(), input->cuda_data(), weight->cuda_data(),
                                         px, pw, pb, g.N, g.C_in, g.H, g.W, g.Ho, g.Wo, K, pad,
-                                        stride, dil, fl, wsb ? workspace(wsb) : nullptr, wsb,
+                                        stride, dil, fl | dfl, wsb ? workspace(wsb) : nullptr, wsb,
                                         exec::stream()),
                   "depthwise convolution backward");
         }
@@ -307,8 +316,9 @@ struct CBAPointwiseNode : autograd::AutogradNode {
                                    gw ? gw->cuda_data() : nullptr,
                                    dg ? dg->cuda_data() : nullptr,
                                    db ? db->cuda_data() : nullptr, g.N, g.C_in, g.C_out, HW, G,
-                                   (flags & SOAR_GN_SILU) | dx_mode(gx, fresh), workspace(wsb),
-                                   wsb, exec::stream()),
+                                   (flags & SOAR_GN_SILU) | dx_mode(gx, fresh) |
+                                       defer_finish(!gw || w_direct),
+                                   workspace(wsb), wsb, exec::stream()),
               "CBA backward");
         if (dg && !g_direct) propagate_grad(gamma, std::move(dg));
         if (db && !b_direct) propagate_grad(beta, std::move(db));
@@ -360,8 +370,9 @@ struct CBADepthwiseNode : autograd::AutogradNode {
                                    dg ? dg->cuda_data() : nullptr,
                                    db ? db->cuda_data() : nullptr, g.N, g.C_in, g.H, g.W, g.Ho,
                                    g.Wo, K, pad, stride, dil, G,
-                                   (flags & SOAR_GN_SILU) | dx_mode(gx, fresh), workspace(wsb),
-                                   wsb, exec::stream()),
+                                   (flags & SOAR_GN_SILU) | dx_mode(gx, fresh) |
+                                       defer_finish(!gw || w_direct),
+                                   workspace(wsb), wsb, exec::stream()),
               "depthwise CBA backward");
         if (dg && !g_direct) propagate_grad(gamma, std::move(dg));
         if (db && !b_direct) propagate_grad(beta, std::move(db));

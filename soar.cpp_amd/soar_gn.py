@@ -34,6 +34,7 @@ SOAR_ENODEV = -4
 GN_SILU = 1
 GN_RESIDUAL = 2
 GN_ACCUMULATE_DX = 4
+DEFER_WEIGHT_FINISH = 8  # conv backward: weight-gradient addition at weight_grad_flush
 
 # bytes of the static scratch behind soar_group_norm_backward_noalloc
 # (SOAR_GN_NOALLOC_SCRATCH_BYTES)
@@ -133,6 +134,9 @@ SIGNATURES = {
     "soar_memcpy_d2d": (_c.c_int, [_P, _P, _SZ, _P]),
     "soar_memcpy_async": (_c.c_int, [_P, _P, _SZ, _c.c_int, _P]),
     "soar_prof_enable": (_c.c_int, [_c.c_int]),
+    "soar_weight_grad_flush": (_c.c_int, [_P]),
+    "soar_weight_grad_pending": (_SZ, []),
+    "soar_weight_grad_discard": (None, []),
     "soar_prof_summary": (_c.c_int, [_c.c_char_p, _SZ]),
     "soar_gn_tune": (_c.c_int, [_c.c_int, _I64]),
     "soar_gn_tune_get": (_I64, [_c.c_int]),
@@ -476,10 +480,13 @@ def pw_conv_backward_workspace_bytes(N, C_in, C_out, HW) -> int:
 
 
 def pw_conv_backward(dz, x, weight, dx=None, dweight=None, dbias=None, want_dx=True,
-                     want_dw=True, want_db=True, accumulate_dx=False, ws=None, stream=None):
+                     want_dw=True, want_db=True, accumulate_dx=False, ws=None, stream=None,
+                     defer_finish=False):
     """Backward of the pointwise conv through soar_pw_conv_backward; returns
     (dx, dweight, dbias).  dweight/dbias accumulate (fresh zeros when not
-    given); dx is written, or added to with accumulate_dx."""
+    given); dx is written, or added to with accumulate_dx.  defer_finish:
+    dweight/dbias receive their sums at the next weight_grad_flush (keep ws
+    alive until then)."""
     import torch
     N, C_out, HW = _nchw(dz)
     w = weight.reshape(weight.shape[0], -1)
@@ -501,7 +508,8 @@ def pw_conv_backward(dz, x, weight, dx=None, dweight=None, dbias=None, want_dx=T
     check(lib().soar_pw_conv_backward(
         _ptr(dz), _ptr(x), _ptr(w), _ptr(dx) if want_dx else None,
         _ptr(dweight) if want_dw else None, _ptr(dbias) if want_db else None, N, C_in, C_out,
-        HW, GN_ACCUMULATE_DX if accumulate_dx else 0, _ptr(ws), ws.numel(), _stream(stream)))
+        HW, (GN_ACCUMULATE_DX if accumulate_dx else 0) |
+        (DEFER_WEIGHT_FINISH if defer_finish else 0), _ptr(ws), ws.numel(), _stream(stream)))
     return (dx if want_dx else None, dweight if want_dw else None, dbias if want_db else None)
 
 
@@ -511,7 +519,7 @@ def pw_cba_backward_workspace_bytes(N, C_in, C_out, HW, G) -> int:
 
 def pw_cba_backward(dy, z, x, weight, gamma, beta, stats, G, silu=True, dx=None, dweight=None,
                     dgamma=None, dbeta=None, want_dx=True, want_dw=True, want_params=True,
-                    accumulate_dx=False, ws=None, stream=None):
+                    accumulate_dx=False, ws=None, stream=None, defer_finish=False):
     """Backward of a pointwise CBA block through soar_pw_cba_backward.
 
     z, stats: what pw_conv_gn_silu_forward returned; dy: the gradient at y.
@@ -540,7 +548,8 @@ def pw_cba_backward(dy, z, x, weight, gamma, beta, stats, G, silu=True, dx=None,
     if ws is None:
         ws = torch.empty(max(pw_cba_backward_workspace_bytes(N, C_in, C_out, HW, G), 1),
                          dtype=torch.uint8, device=dev)
-    flags = (GN_SILU if silu else 0) | (GN_ACCUMULATE_DX if accumulate_dx else 0)
+    flags = ((GN_SILU if silu else 0) | (GN_ACCUMULATE_DX if accumulate_dx else 0) |
+             (DEFER_WEIGHT_FINISH if defer_finish else 0))
     check(lib().soar_pw_cba_backward(
         _ptr(dy), _ptr(z), _ptr(x), _ptr(w), _ptr(gamma), _ptr(beta), _ptr(stats.mean),
         _ptr(stats.rstd), _ptr(stats.mean_lo), _ptr(dx) if want_dx else None,
@@ -613,7 +622,7 @@ def dw_conv_gn_silu_forward(x, weight, bias, gamma, beta, G, pad, stride=1, dil=
 
 def dw_conv_backward(dy, x, weight, pad, stride=1, dil=1, dx=None, dweight=None, dbias=None,
                      want_dx=True, want_dw=True, want_db=True, accumulate_dx=False, ws=None,
-                     stream=None):
+                     stream=None, defer_finish=False):
     """Backward through soar_dw_conv_backward; returns (dx, dweight, dbias).
     dweight/dbias accumulate (fresh zeros when not given)."""
     import torch
@@ -636,8 +645,8 @@ def dw_conv_backward(dy, x, weight, pad, stride=1, dil=1, dx=None, dweight=None,
     check(lib().soar_dw_conv_backward(
         _ptr(dy), _ptr(x), _ptr(weight), _ptr(dx) if want_dx else None,
         _ptr(dweight) if want_dw else None, _ptr(dbias) if want_db else None, N, C, H, W, Ho,
-        Wo, K, pad, stride, dil, GN_ACCUMULATE_DX if accumulate_dx else 0, _ptr(ws), ws.numel(),
-        _stream(stream)))
+        Wo, K, pad, stride, dil, (GN_ACCUMULATE_DX if accumulate_dx else 0) |
+        (DEFER_WEIGHT_FINISH if defer_finish else 0), _ptr(ws), ws.numel(), _stream(stream)))
     return (dx if want_dx else None, dweight if want_dw else None, dbias if want_db else None)
 
 
@@ -648,7 +657,8 @@ def dw_cba_backward_workspace_bytes(N, C, H, W, Ho, Wo, K, pad, stride, dil, G) 
 
 def dw_cba_backward(dy, z, x, weight, gamma, beta, stats, G, pad, stride=1, dil=1, silu=True,
                     dx=None, dweight=None, dgamma=None, dbeta=None, want_dx=True, want_dw=True,
-                    want_params=True, accumulate_dx=False, ws=None, stream=None):
+                    want_params=True, accumulate_dx=False, ws=None, stream=None,
+                    defer_finish=False):
     """Backward of a depthwise CBA block through soar_dw_cba_backward.
 
     z: the convolution output (the GroupNorm input), stats: its GroupNorm
@@ -676,7 +686,8 @@ def dw_cba_backward(dy, z, x, weight, gamma, beta, stats, G, pad, stride=1, dil=
     if ws is None:
         n = dw_cba_backward_workspace_bytes(N, C, H, W, Ho, Wo, K, pad, stride, dil, G)
         ws = torch.empty(max(n, 1), dtype=torch.uint8, device=dev)
-    flags = (GN_SILU if silu else 0) | (GN_ACCUMULATE_DX if accumulate_dx else 0)
+    flags = ((GN_SILU if silu else 0) | (GN_ACCUMULATE_DX if accumulate_dx else 0) |
+             (DEFER_WEIGHT_FINISH if defer_finish else 0))
     check(lib().soar_dw_cba_backward(
         _ptr(dy), _ptr(z), _ptr(x), _ptr(weight), _ptr(gamma), _ptr(beta), _ptr(stats.mean),
         _ptr(stats.rstd), _ptr(stats.mean_lo), _ptr(dx) if want_dx else None,
@@ -685,6 +696,22 @@ def dw_cba_backward(dy, z, x, weight, gamma, beta, stats, G, pad, stride=1, dil=
         _ptr(ws), ws.numel(), _stream(stream)))
     return (dx if want_dx else None, dweight if want_dw else None,
             dgamma if want_params else None, dbeta if want_params else None)
+
+
+def weight_grad_flush(stream=None):
+    """Runs the weight-gradient finishes this thread's backward calls left
+    pending (defer_finish=True) in one launch, on the stream they were
+    queued on (`stream` must be it)."""
+    check(lib().soar_weight_grad_flush(_stream(stream)))
+
+
+def weight_grad_pending() -> int:
+    return int(lib().soar_weight_grad_pending())
+
+
+def weight_grad_discard():
+    """Drops this thread's pending weight-gradient finishes unrun."""
+    lib().soar_weight_grad_discard()
 
 
 def prof_enable(on: bool = True):

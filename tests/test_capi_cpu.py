@@ -449,3 +449,40 @@ def test_dw_cba_backward_validation_without_gpu(L):
     assert _dwcba(L, 0, *args[1:], 4) == soar_gn.SOAR_OK  # empty
     assert _dwcba(L, *args, 4, outputs=False) == soar_gn.SOAR_OK  # nothing requested
     assert _dwcba(L, *args, 4) == soar_gn.SOAR_ENODEV
+
+
+def test_weight_finish_flag_and_flush_without_gpu(L):
+    """SOAR_DEFER_WEIGHT_FINISH passes the convolution backward calls'
+    validation (they then reach the device check); other flags bits and the
+    GroupNorm calls still refuse it; with nothing queued the flush is a
+    no-op on any stream."""
+    D = soar_gn.DEFER_WEIGHT_FINISH
+    assert L.soar_weight_grad_pending() == 0
+    assert L.soar_weight_grad_flush(None) == soar_gn.SOAR_OK
+    assert L.soar_weight_grad_flush(ctypes.c_void_p(0x1234)) == soar_gn.SOAR_OK
+    nodev = L.soar_is_device_available() == 0
+    rc = _cba(L, 1, 8, 6, 16, 3, flags=1 | D)
+    assert rc == (soar_gn.SOAR_ENODEV if nodev else soar_gn.SOAR_EINVAL)
+    assert _cba(L, 1, 8, 6, 16, 3, flags=1 | 16) == soar_gn.SOAR_EINVAL
+    assert "flags" in soar_gn.last_error()
+    args = (1, 8, 16, 16, 16, 16, 3, 1, 1, 1)
+    if nodev:
+        assert _dwcba(L, *args, 4, flags=1 | D) == soar_gn.SOAR_ENODEV
+    assert _dwcba(L, *args, 4, flags=1 | 16) == soar_gn.SOAR_EINVAL
+    dummy = ctypes.c_void_p(0x1000)
+    P = [dummy, dummy, dummy, None, dummy, None]
+    rc = L.soar_pw_conv_backward(*P, 1, 8, 6, 16, D, None, 0, None)
+    if nodev:
+        assert rc == soar_gn.SOAR_ENODEV
+    assert L.soar_pw_conv_backward(*P, 1, 8, 6, 16, 16, None, 0, None) == soar_gn.SOAR_EINVAL
+    rc = L.soar_dw_conv_backward(dummy, dummy, dummy, None, dummy, None, 1, 8, 16, 16, 16, 16, 3,
+                                 1, 1, 1, D, None, 0, None)
+    if nodev:
+        assert rc == soar_gn.SOAR_ENODEV
+    assert L.soar_dw_conv_backward(dummy, dummy, dummy, None, dummy, None, 1, 8, 16, 16, 16, 16,
+                                   3, 1, 1, 1, 16, None, 0, None) == soar_gn.SOAR_EINVAL
+    # the GroupNorm backward has no weight gradient to defer
+    rc = L.soar_gn_silu_backward(None, None, None, None, None, None, None, None, None, None, 1, 6,
+                                 16, 3, 1 | D, None, 0, None)
+    assert rc == soar_gn.SOAR_EINVAL
+    assert L.soar_weight_grad_pending() == 0
