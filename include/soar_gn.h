@@ -544,10 +544,12 @@ SOAR_API int soar_prof_summary(char* buf, size_t buflen);
 #define SOAR_TUNE_SMALL_UNIT 9 /* units of <= this many elements run the   */
                                /* one-launch GroupNorm; 0 = never; the     */
                                /* default is 16384                         */
-#define SOAR_TUNE_FOLD_MAX 11 /* units of <= this many chunk partials fold */
-                              /* the finish into the second pass (one     */
-                              /* launch less per direction); 0 = never,   */
-                              /* at most and by default 128               */
+#define SOAR_TUNE_FOLD_MAX 11 /* units of <= this many partials (chunks,  */
+                              /* or a depthwise forward's tile groups;    */
+                              /* past 128 only units of <= 2^20 elements) */
+                              /* fold the finish into the second pass     */
+                              /* (one launch less per direction); 0 =     */
+                              /* never, at most 4096, by default 2048     */
 #define SOAR_TUNE_PW_SMALL 10 /* pointwise convs of <= this many multiply- */
                               /* adds (weight gradient: half as many) run */
                               /* the SIMT kernels; 0 = never; the default */

@@ -1500,7 +1500,8 @@ SOAR_API int soar_gn_tune(int key, int64_t value) {
             g_tune.small_unit = value;
             return ok();
         case SOAR_TUNE_FOLD_MAX:
-            if (value < 0 || value > 128) return fail(SOAR_EINVAL, "fold_max must be in [0, 128]");
+            if (value < 0 || value > 4096)
+                return fail(SOAR_EINVAL, "fold_max must be in [0, 4096]");
             g_tune.fold_max = value;
             return ok();
         case SOAR_TUNE_PW_SMALL:

@@ -79,9 +79,10 @@ struct Tuning {
                                  // block per unit, so larger units stream
                                  // faster over many blocks (Nano 512^2 train
                                  // step: 3.73 ms at 32768, 3.64 at 16384)
-    int64_t fold_max = 128;      // units of at most this many chunk partials
-                                 // (one batch) fold the finish into the
-                                 // second pass (0: never; at most 128)
+    int64_t fold_max = 2048;     // units of at most this many partials (one
+                                 // batch; past 128 only units of at most
+                                 // 2^20 elements) fold the finish into the
+                                 // second pass (0: never; at most 4096)
     int64_t pw_small = 1 << 25;  // pointwise convolutions of at most this
                                  // many multiply-adds (weight gradient: half
                                  // as many) run the SIMT kernels (0: never)

@@ -399,15 +399,16 @@ __device__ __forceinline__ PlaneCoef plane_coef(
 }
 
 // ======================================================================
-// Folded finish for mid-size units (at most kFoldMax chunk partials per
+// Folded finish for mid-size units (at most Tuning::fold_max partials per
 // unit, one batch): instead of a finish launch between the passes, every
 // second-pass block combines its own unit's partials before its work.
 // All blocks of a unit run the same combine in the same order, so they
-// agree bit for bit.  The statistics also equal finish_stats_unit's: there
-// thread q < P holds partial q's terms alone (added to zero), the other
-// threads hold zeros, and the waves are added in order.
+// agree bit for bit, and the statistics equal the separate finish's
+// (finish_unit on kThreads threads): the block's thread t stands in for
+// that finish's threads t, t + NT, ..., runs each one's partials in that
+// one's order, and the wave sums are added in the same order.
 // ======================================================================
-constexpr int64_t kFoldMax = kThreads2;  // partials per unit (one per thread)
+constexpr int64_t kFoldMax = 4096;  // partials per unit
 
 // Sum of (a, b) over an NT-thread block in a fixed order (wave trees, then
 // the waves in order), returned to every thread.
@@ -432,23 +433,49 @@ struct UnitStats {
     float hi, r, lo;
 };
 
-template <int NT>
-__device__ UnitStats fold_unit_stats(int64_t u, const double2* __restrict__ part, int64_t HW,
-                                     int64_t chunk, int64_t cpp, int64_t cpg, float eps) {
+// Each virtual thread's partials j, j + kThreads, ... in batches of four
+// loads issued together (indices clamped into the unit, the terms past P
+// not added), so a unit of a few hundred partials costs one or two memory
+// round trips.
+template <int NT, typename Count>
+__device__ UnitStats fold_unit_stats(int64_t u, const double2* __restrict__ part, int64_t P,
+                                     const Count& count, double n_total, float eps) {
+    constexpr int V = kThreads / NT;  // threads of the separate finish per thread
+    constexpr int W = NT / 64;
+    static_assert(V * NT == kThreads && W * 64 == NT, "block size");
+    constexpr int kB = 4;
+    __shared__ double2 sw[kThreads / 64];
     __shared__ float bc[3];
-    const int64_t P = cpg * cpp;
-    const int q = threadIdx.x;
-    const double R = part[u * P].x;
-    double S = 0.0, Q = 0.0;
-    if (q < P) {
-        const double2 v = part[u * P + q];
-        centred_add(S, Q, partial_count(q, HW, chunk, cpp), v.x, v.y, R);
+    const double2* __restrict__ pu = part + u * P;
+    const double R = pu[0].x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int h = 0; h < V; ++h) {
+        double S = 0.0, Q = 0.0;
+        for (int64_t j0 = threadIdx.x + h * NT; j0 < P; j0 += kB * kThreads) {
+            double2 v[kB];
+#pragma unroll
+            for (int i = 0; i < kB; ++i) v[i] = pu[min(j0 + (int64_t)i * kThreads, P - 1)];
+#pragma unroll
+            for (int i = 0; i < kB; ++i) {
+                const int64_t j = j0 + (int64_t)i * kThreads;
+                if (j < P) centred_add(S, Q, count(j), v[i].x, v[i].y, R);
+            }
+        }
+        S = wave_sum(S);
+        Q = wave_sum(Q);
+        if (lane == 0) sw[h * W + w] = make_double2(S, Q);
     }
-    const double2 sq = fold_block_sum2<NT>(S, Q);
+    __syncthreads();
     if (threadIdx.x == 0) {
-        const double n = (double)(cpg * HW);
-        const double2 mm = centred_moments(sq.x, sq.y, n, R);
-        const double var = mm.y / n;
+        double S = sw[0].x, Q = sw[0].y;
+#pragma unroll
+        for (int i = 1; i < kThreads / 64; ++i) {
+            S += sw[i].x;
+            Q += sw[i].y;
+        }
+        const double2 mm = centred_moments(S, Q, n_total, R);
+        const double var = mm.y / n_total;
         const float hi = (float)mm.x;
         bc[0] = hi;
         bc[1] = (float)(1.0 / sqrt(var + (double)eps));
@@ -459,21 +486,20 @@ __device__ UnitStats fold_unit_stats(int64_t u, const double2* __restrict__ part
 }
 
 
-// (S1, S2) of unit u from its backward partials: thread q < P adds
-// gamma_j * partial q, j = q / cpp the partial's channel.
+// (S1, S2) of unit u from its backward partials: thread q adds gamma_j *
+// partial q, q + NT, ..., j the partial's channel.
 template <int NT>
 __device__ double2 fold_unit_sums(int64_t u, const double2* __restrict__ part,
                                   const float* __restrict__ gamma, int64_t C, int64_t cpg,
                                   int64_t cpp) {
     const int64_t P = cpg * cpp;
-    const int q = threadIdx.x;
     double a = 0.0, b = 0.0;
-    if (q < P) {
+    for (int64_t q = threadIdx.x; q < P; q += NT) {
         const double2 v = part[u * P + q];
         const int64_t plane = u * cpg + q / cpp;
         const double g = gamma ? (double)gamma[plane % C] : 1.0;
-        a = g * v.x;
-        b = g * v.y;
+        a += g * v.x;
+        b += g * v.y;
     }
     return fold_block_sum2<NT>(a, b);
 }
@@ -505,8 +531,9 @@ __device__ void fold_param(int64_t c, const double2* __restrict__ part, int64_t 
 
 // ======================================================================
 // Forward pass 2: y = f((x - mean) * (gamma*rstd) + beta) [+ x].
-// FOLD: the unit's statistics come from its chunk partials (see above);
-// the unit's first block also writes them out.
+// FOLD: the unit's statistics come from the partials (see above), chunk
+// partials (kFoldChunks) or the depthwise forward's tile groups
+// (kFoldTiles); the unit's first block also writes them out.
 // ======================================================================
 struct FoldArgs {
     const double2* part;  // chunk partials of the first pass
@@ -520,9 +547,12 @@ struct FoldArgs {
     // backward without FOLD: the per-plane sums, non-null when the dx
     // launch also runs k_param_finish's sums (every plane sum is final)
     const double2* plane_sums;
+    TileCount tiles;  // FOLD == kFoldTiles: the depthwise forward's tile groups
 };
 
-template <bool VEC, bool SILU, bool RES, bool NT, bool NTL, bool FOLD>
+constexpr int kFoldChunks = 1, kFoldTiles = 2;
+
+template <bool VEC, bool SILU, bool RES, bool NT, bool NTL, int FOLD>
 __global__ __launch_bounds__(kThreads2) void k_apply(
     const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ mean,
@@ -536,8 +566,14 @@ __global__ __launch_bounds__(kThreads2) void k_apply(
         k.n = ck.plane / C;
         k.c = ck.plane - k.n * C;
         k.u = k.n * G + k.c / cpg;
-        const UnitStats st =
-            fold_unit_stats<kThreads2>(k.u, fa.part, HW, fa.chunk, fa.cpp, cpg, fa.eps);
+        const double n = (double)(cpg * HW);
+        UnitStats st;
+        if constexpr (FOLD == kFoldTiles)
+            st = fold_unit_stats<kThreads2>(k.u, fa.part, cpg * fa.tiles.tpp, fa.tiles, n,
+                                            fa.eps);
+        else
+            st = fold_unit_stats<kThreads2>(k.u, fa.part, cpg * fa.cpp,
+                                            ChunkCount{HW, fa.chunk, fa.cpp}, n, fa.eps);
         k.mu = st.hi;
         k.r = st.r;
         k.e = -st.lo * st.r;
@@ -1276,21 +1312,24 @@ void bsel(bool b, F&& f) {
         f(std::false_type{});
 }
 
-// fold: the statistics come from the partials in the workspace (see
-// fold_unit_stats) and are written out by the kernel.
+// fold: the statistics come from partials (see fold_unit_stats) and are
+// written out by the kernel: kFoldChunks, the chunk partials in the
+// workspace; kFoldTiles, the depthwise forward's tile groups at `tpart`.
 void launch_apply(const Plan& p, const Tuning& t, const FwdArgs& a, const float* lo,
-                  int64_t block0, int64_t nb, hipStream_t s, bool fold = false) {
+                  int64_t block0, int64_t nb, hipStream_t s, int fold = 0,
+                  const double2* tpart = nullptr, const TileCount& tiles = TileCount{}) {
     const bool silu = (a.flags & SOAR_GN_SILU) != 0;
     const bool res = (a.flags & SOAR_GN_RESIDUAL) != 0;
     const dim3 grid((unsigned)nb);
-    const FoldArgs fa{ws_view(p, a.ws).part, a.mean, a.rstd, a.mean_lo, nullptr, nullptr,
-                      p.N, p.chunk, p.cpp, a.eps, nullptr};
-    bsel(p.vec4, [&](auto V) {
-        bsel(silu, [&](auto S) {
-            bsel(res, [&](auto R) {
-                bsel(t.nt_store != 0, [&](auto N) {
-                    bsel(V() && (t.nt_load & 1) != 0, [&](auto L) {
-                        bsel(fold, [&](auto F) {
+    const FoldArgs fa{fold == kFoldTiles ? tpart : ws_view(p, a.ws).part,
+                      a.mean, a.rstd, a.mean_lo, nullptr, nullptr, p.N, p.chunk, p.cpp, a.eps,
+                      nullptr, tiles};
+    auto go = [&](auto F) {
+        bsel(p.vec4, [&](auto V) {
+            bsel(silu, [&](auto S) {
+                bsel(res, [&](auto R) {
+                    bsel(t.nt_store != 0, [&](auto N) {
+                        bsel(V() && (t.nt_load & 1) != 0, [&](auto L) {
                             k_apply<V(), S(), R(), N(), L(), F()><<<grid, kThreads2, 0, s>>>(
                                 a.x, a.gamma, a.beta, a.mean, a.rstd, lo, a.y, p.C, p.G, p.cpg,
                                 p.HW, p.chunk2, p.cpp2, block0, nb, t.reverse, fa);
@@ -1299,7 +1338,13 @@ void launch_apply(const Plan& p, const Tuning& t, const FwdArgs& a, const float*
                 });
             });
         });
-    });
+    };
+    if (fold == kFoldTiles)
+        go(std::integral_constant<int, kFoldTiles>{});
+    else if (fold == kFoldChunks)
+        go(std::integral_constant<int, kFoldChunks>{});
+    else
+        go(std::integral_constant<int, 0>{});
 }
 
 // fold: S1 / S2 and dgamma / dbeta come from the partials in the workspace.
@@ -1334,10 +1379,24 @@ void launch_dx(const Plan& p, const Tuning& t, const BwdArgs& a, const double2* 
 }
 
 // Mid-size units fold the finish into the second pass: one batch, at most
-// t.fold_max (<= kFoldMax) partials per unit.
+// t.fold_max (<= kFoldMax) partials per unit, and more than kFoldAlways
+// only for units of at most kFoldBigUnit elements.  Every second-pass block
+// re-reads its unit's partials (16 bytes each, from L2): next to a 4096-
+// float chunk that is cheap up to a hundred or so, and past that it pays
+// only where the unit's blocks are few and the saved launch is a large
+// share of the pass (SOAR Nano at 1024^2, units of 2^14 to 2^19 elements,
+// 1 x 1 convolution epilogues of 256 to 4096 partials: 4.204 ms per
+// training step folding up to 128, 4.155 up to 2048).
+constexpr int64_t kFoldAlways = 128;
+constexpr int64_t kFoldBigUnit = (int64_t)1 << 20;
+
+bool fold_fits(const Plan& p, const Tuning& t, int64_t partials) {
+    return t.fold_max > 0 && partials <= std::min<int64_t>(t.fold_max, kFoldMax) &&
+           (partials <= kFoldAlways || p.cpg * p.HW <= kFoldBigUnit);
+}
+
 bool fold_ok(const Plan& p, const Tuning& t, int64_t upb) {
-    return t.fold_max > 0 && p.cpg * p.cpp <= std::min<int64_t>(t.fold_max, kFoldMax) &&
-           upb >= p.units;
+    return fold_fits(p, t, p.cpg * p.cpp) && upb >= p.units;
 }
 
 // First chunk block of units [u0, u0 + nu) that loads with cached loads:
@@ -1575,7 +1634,7 @@ hipError_t launch_forward(const Plan& p, const Tuning& t, const FwdArgs& a, hipS
     if (fold_ok(p, t, p.upb_fwd)) {
         launch_stats(p, a, w, 0, 0, 0, p.units, s);
         const int tok = prof_begin(s, apply_name);
-        launch_apply(p, t, a, w.lo, 0, p.blocks2, s, true);
+        launch_apply(p, t, a, w.lo, 0, p.blocks2, s, kFoldChunks);
         prof_end(s, tok);
         return hipGetLastError();
     }
@@ -1634,9 +1693,10 @@ hipError_t launch_forward_from_partials(const Plan& p, const Tuning& t, const Fw
         prof_end(s, tok);
         return hipGetLastError();
     }
-    launch_stats(p, a, w, 0, p.units, 0, 0, s);
+    const bool fold = fold_fits(p, t, p.cpg * p.cpp);
+    if (!fold) launch_stats(p, a, w, 0, p.units, 0, 0, s);
     const int tok = prof_begin(s, (a.flags & SOAR_GN_SILU) ? "gn_silu_apply" : "gn_apply");
-    launch_apply(p, t, a, w.lo, 0, p.blocks2, s);
+    launch_apply(p, t, a, w.lo, 0, p.blocks2, s, fold ? kFoldChunks : 0);
     prof_end(s, tok);
     return hipGetLastError();
 }
@@ -1651,6 +1711,12 @@ hipError_t launch_forward_from_tile_partials(const Plan& p, const Tuning& t, con
     const WsView w = ws_view(p, a.ws);
     const int64_t P = p.cpg * g.tpp;
     const TileCount count{g.tpp, g.tiles_x, g.rows, Ho, Wo};
+    if (fold_fits(p, t, P)) {
+        const int tok = prof_begin(s, (a.flags & SOAR_GN_SILU) ? "gn_silu_apply" : "gn_apply");
+        launch_apply(p, t, a, w.lo, 0, p.blocks2, s, kFoldTiles, part, count);
+        prof_end(s, tok);
+        return hipGetLastError();
+    }
     int tok = prof_begin(s, "gn_stats_finish");
     if (P >= kWideFinish)
         k_stats_finish_tiles<kWideThreads><<<dim3((unsigned)p.units), kWideThreads, 0, s>>>(

@@ -29,6 +29,11 @@ namespace {
 // Entries of one launch: the table travels in the kernel arguments (by
 // value, so a captured graph replays it as recorded).
 constexpr int kFinishMax = 64;
+// Entries of at most this many partials per element run one element per
+// thread (1024 per block), the others one element per lane of each of 16
+// waves (64 per block, a wave per segment).
+constexpr int64_t kNarrowG = 32;
+constexpr int kNarrowBatch = 16;  // loads a thread keeps in flight
 
 struct FinishTable {
     int n;
@@ -42,6 +47,19 @@ struct FinishTable {
 };
 static_assert(sizeof(FinishTable) < 4096, "kernel argument size");
 
+// out0 / out1 element that entry i's element e adds into (null: none)
+__device__ __forceinline__ float* finish_target(const FinishTable& t, int i, int64_t e) {
+    const int64_t kk1 = t.kk1[i];
+    if (kk1 == 0) return t.out0[i] + e;  // k_sum_partials: out0[e]
+    // k_dw_wgrad_finish: taps c*(kk1-1) + k of out0, bias c of out1
+    const int64_t c = e / kk1, k = e - c * kk1;
+    return k < kk1 - 1 ? (t.out0[i] ? t.out0[i] + c * (kk1 - 1) + k : nullptr)
+                       : (t.out1[i] ? t.out1[i] + c : nullptr);
+}
+
+// Every element's sum is the segment sums of segment_sum (segments
+// [k*G/16, (k+1)*G/16), k = 0..15, each summed from 0.0 in g order) added
+// in k order from 0.0, on either path.
 __global__ __launch_bounds__(1024) void k_weight_finish(const FinishTable t) {
     __shared__ double lds[16][64];
     const int64_t b = blockIdx.x;
@@ -56,7 +74,42 @@ __global__ __launch_bounds__(1024) void k_weight_finish(const FinishTable t) {
     }
     const int i = lo;
     const float* __restrict__ part = t.part[i];
-    const int64_t E = t.E[i], G = t.G[i], kk1 = t.kk1[i];
+    const int64_t E = t.E[i], G = t.G[i];
+    if (G <= kNarrowG) {
+        // one element per thread: its G partials in batches of loads
+        // issued together (rows clamped into range, the rest not added),
+        // each segment's sum closed into the total as g passes its end
+        const int64_t e = (b - t.first[i]) * 1024 + threadIdx.x;
+        if (e >= E) return;
+        double tsum = 0.0, sum = 0.0;
+        int k = 0;
+        int64_t end = G / 16;  // end of segment k
+        for (int64_t g0 = 0; g0 < G; g0 += kNarrowBatch) {
+            float v[kNarrowBatch];
+#pragma unroll
+            for (int u = 0; u < kNarrowBatch; ++u) v[u] = part[min(g0 + u, G - 1) * E + e];
+#pragma unroll
+            for (int u = 0; u < kNarrowBatch; ++u) {
+                const int64_t g = g0 + u;
+                if (g < G) {
+                    while (g >= end) {
+                        tsum += sum;
+                        sum = 0.0;
+                        ++k;
+                        end = (k + 1) * G / 16;
+                    }
+                    sum += (double)v[u];
+                }
+            }
+        }
+        for (; k < 16; ++k) {
+            tsum += sum;
+            sum = 0.0;
+        }
+        float* o = finish_target(t, i, e);
+        if (o) *o = (float)((double)*o + tsum);
+        return;
+    }
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int64_t e = (b - t.first[i]) * 64 + lane;
     const int64_t g0 = wv * G / 16, g1 = (wv + 1) * G / 16;
@@ -67,14 +120,7 @@ __global__ __launch_bounds__(1024) void k_weight_finish(const FinishTable t) {
         double tsum = 0.0;
 #pragma unroll
         for (int k = 0; k < 16; ++k) tsum += lds[k][lane];
-        float* o;
-        if (kk1 == 0) {  // k_sum_partials: out0[e]
-            o = t.out0[i] + e;
-        } else {  // k_dw_wgrad_finish: taps c*(kk1-1) + k of out0, bias c of out1
-            const int64_t c = e / kk1, k = e - c * kk1;
-            o = k < kk1 - 1 ? (t.out0[i] ? t.out0[i] + c * (kk1 - 1) + k : nullptr)
-                            : (t.out1[i] ? t.out1[i] + c : nullptr);
-        }
+        float* o = finish_target(t, i, e);
         if (o) *o = (float)((double)*o + tsum);
     }
 }
@@ -135,7 +181,7 @@ hipError_t weight_finish_flush() {
             t.E[i] = f.E;
             t.G[i] = f.G;
             t.kk1[i] = f.kk1;
-            blocks += (f.E + 63) / 64;
+            blocks += f.G <= kNarrowG ? (f.E + 1023) / 1024 : (f.E + 63) / 64;
         }
         t.first[t.n] = blocks;
         const int tok = prof_begin(s, "weight_grad_finish");

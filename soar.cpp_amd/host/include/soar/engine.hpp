@@ -113,6 +113,11 @@ public:
     void next_scalars(float out[3]);
     void step_device(const float* scalars);
     [[nodiscard]] const double* norm_sq() const noexcept { return norm_; }
+    // Puts the squared norm at `p` (a device double the caller keeps), e.g.
+    // next to other values read back together with it.
+    void set_norm_sq_buffer(double* p) noexcept {
+        if (p) norm_ = p;
+    }
     [[nodiscard]] float get_lr() const noexcept { return options_.lr; }
     void set_lr(float lr) noexcept { options_.lr = lr; }
     [[nodiscard]] const AdamWOptions& options() const noexcept { return options_; }

@@ -205,8 +205,10 @@ void* create(int in_channels, int num_classes, int variant, bool seeded, uint64_
             auto opt = std::make_unique<soar::optim::AdamW>(h->model->parameters(), opts);
             h->trainer = std::make_unique<soar::engine::Trainer>(
                 h->model, soar::losses::CompositeLoss(0.5f, 0.5f), std::move(opt));
+            // the 4 loss sums, then the squared gradient norm: one read-back
             h->dev_sums = static_cast<double*>(
-                h->params->allocate(4 * sizeof(double), {}, "loss_sums"));
+                h->params->allocate(5 * sizeof(double), {}, "loss_sums"));
+            h->trainer->optimizer().set_norm_sq_buffer(h->dev_sums + 4);
             h->dev_scalars = static_cast<float*>(
                 h->params->allocate(4 * sizeof(float), {}, "adamw_scalars"));
         }
@@ -438,13 +440,10 @@ SOAR_API int soar_train_step(void* handle, const float* image_data, const float*
             soar::exec::StreamScope scope(s->stream);
             run_train_step(s, channels, height, width);
         }
+        // the loss sums and the squared norm lie together (dev_sums[0..4])
         soar::hip::kernels::check(
-            soar_memcpy_async(s->pin_out, s->dev_sums, 4 * sizeof(double), 1, s->stream),
-            "loss read-back");
-        soar::hip::kernels::check(
-            soar_memcpy_async(s->pin_out + 4, s->trainer->optimizer().norm_sq(),
-                              sizeof(double), 1, s->stream),
-            "norm read-back");
+            soar_memcpy_async(s->pin_out, s->dev_sums, 5 * sizeof(double), 1, s->stream),
+            "loss and norm read-back");
         hip_check(hipStreamSynchronize(s->stream), "hipStreamSynchronize");
         s->last = s->trainer->device_step_metrics(s->pin_out, s->pin_out[4], px);
         if (out_loss) *out_loss = s->last.loss;

@@ -329,8 +329,10 @@ def test_pw_wg_target_tuning(L):
 
 def test_fold_max_tuning(L):
     old = soar_gn.tune_get(soar_gn.TUNE_FOLD_MAX)
-    assert old == 128
-    assert L.soar_gn_tune(soar_gn.TUNE_FOLD_MAX, 129) == soar_gn.SOAR_EINVAL
+    assert old == 2048
+    assert L.soar_gn_tune(soar_gn.TUNE_FOLD_MAX, 4097) == soar_gn.SOAR_EINVAL
+    soar_gn.tune(soar_gn.TUNE_FOLD_MAX, 4096)
+    assert soar_gn.tune_get(soar_gn.TUNE_FOLD_MAX) == 4096
     assert L.soar_gn_tune(soar_gn.TUNE_FOLD_MAX, -1) == soar_gn.SOAR_EINVAL
     soar_gn.tune(soar_gn.TUNE_FOLD_MAX, 0)
     assert soar_gn.tune_get(soar_gn.TUNE_FOLD_MAX) == 0

@@ -98,6 +98,55 @@ def test_dw_conv_gn_forward_matches_oracle(gpu, oracle, N, C, H, W, K, S, D, G, 
     assert np.array_equal(host(y), host(y2)) and np.array_equal(host(st.rstd), host(st2.rstd))
 
 
+FOLD_CASES = [
+    # (N, C, H, W, K, S, D, G): tile groups per unit (cpg * tpp) from a few
+    # dozen to several hundred
+    (1, 16, 512, 512, 3, 1, 1, 8),    # SOAR Nano gate_dw at 1024^2: 512 partials
+    (1, 32, 256, 256, 7, 1, 1, 8),    # LKR k7: 256
+    (2, 64, 100, 130, 5, 1, 1, 8),    # ragged tiles, two samples
+    (1, 16, 256, 256, 3, 2, 1, 4),    # stride 2
+]
+
+
+@pytest.mark.parametrize("N,C,H,W,K,S,D,G", FOLD_CASES)
+def test_dw_conv_gn_forward_folded_finish(gpu, oracle, N, C, H, W, K, S, D, G):
+    """The finish of the tile-group partials folded into the apply
+    (SOAR_TUNE_FOLD_MAX at or above the unit's partials): no finish launch,
+    and mean, rstd, mean_lo and y bit for bit those of the separate finish
+    (0: always separate), which the oracle checks."""
+    import torch
+    print(f"dw_conv_gn_forward folded N={N} C={C} {H}x{W} K={K} S={S} D={D} G={G}", flush=True)
+    x, w, b, gm, bt = _inputs(N + C + H + K + 11, N, C, H, W, K, "normal")
+    pad = D * (K - 1) // 2
+    xd, wd, gd, bd = dev(x), dev(w), dev(gm), dev(bt)
+    old = gpu.tune_get(gpu.TUNE_FOLD_MAX)
+    runs = {}
+    try:
+        for fold in (0, 4096):
+            gpu.tune(gpu.TUNE_FOLD_MAX, fold)
+            gpu.prof_summary()
+            gpu.prof_enable(True)
+            try:
+                z, y, st = gpu.dw_conv_gn_silu_forward(xd, wd, dev(b), gd, bd, G, pad, S, D,
+                                                       eps=EPS)
+                torch.cuda.synchronize()
+                names = _launches()
+            finally:
+                gpu.prof_enable(False)
+            assert "dw_conv_stats" in names, names
+            assert ("gn_stats_finish" in names) == (fold == 0), names
+            runs[fold] = [host(t) for t in (z, y, st.mean, st.rstd, st.mean_lo)]
+    finally:
+        gpu.tune(gpu.TUNE_FOLD_MAX, old)
+    for a, c in zip(runs[0], runs[4096]):
+        assert np.array_equal(a, c)
+    z, y, mean, rstd = runs[4096][:4]
+    Ho, Wo = z.shape[2], z.shape[3]
+    yt, mt, rt = oracle.gn_silu_fwd_f64(z.reshape(-1), gm, bt, N, C, Ho * Wo, G, EPS)
+    assert_stats(mean, rstd, mt, rt, "folded stats")
+    assert_vals(y, yt, "folded y")
+
+
 def test_dw_conv_gn_forward_full_size_k7(gpu, oracle):
     """The CBA LKR block's k7 depthwise conv at BASELINE config 3's shape
     (1 x 64 x 2048^2, G = 16): whole-tensor statistics against the float64

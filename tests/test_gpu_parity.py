@@ -783,12 +783,14 @@ def test_small_unit_path(gpu, oracle, restore_tuning, shape, residual):
 
 FOLD_SHAPES = [
     # (N, C, HW, G, kind): units above 32768 elements (past the small-unit
-    # kernels whatever the setting) with at most 128
-    # chunk partials, so the finish folds into the second pass
+    # kernels whatever the setting) with at most 2048 chunk partials (past
+    # 128 only in units of at most 2^20 elements), so the finish folds into
+    # the second pass
     (1, 16, 512 * 512, 8, "normal"),   # SOAR Nano stride 2 at 1024x1024: 64 partials
     (2, 32, 256 * 256, 8, "normal"),   # 32 partials per unit, two samples
     (1, 128, 64 * 64, 8, "normal"),    # 16 channels per group, one chunk each
     (3, 24, 10000, 6, "offset"),       # ragged chunks, large mean, three samples
+    (1, 32, 512 * 512, 8, "normal"),   # 2^20-element units of a few hundred partials
 ]
 
 
@@ -796,7 +798,7 @@ FOLD_SHAPES = [
 @pytest.mark.parametrize("residual", [False, True])
 def test_folded_finish(gpu, oracle, restore_tuning, shape, residual):
     """Mid-size units with the finish folded into the apply / dx pass
-    (SOAR_TUNE_FOLD_MAX = 128, the default) against the oracle, and against
+    (SOAR_TUNE_FOLD_MAX = 2048, the default) against the oracle, and against
     the separate finish launches (0): the statistics and y are bitwise
     identical (the same combine in the same order); dx, dgamma and dbeta
     agree far inside the bar (S1 / S2 are summed in another order); the
@@ -811,7 +813,7 @@ def test_folded_finish(gpu, oracle, restore_tuning, shape, residual):
     xd, dyd = dev(x).view(N, C, HW), dev(dy).view(N, C, HW)
     gd, bd = dev(gamma), dev(beta)
     runs = []
-    for fold in (128, 0):
+    for fold in (2048, 0):
         gpu.tune(gpu.TUNE_FOLD_MAX, fold)
         y, mean, rstd, lo, dx, dg, db = _fwd_bwd(gpu, xd, gd, bd, dyd, G, residual)
         assert_stats(host(mean), host(rstd), mt, rt, f"fold={fold}")
@@ -826,7 +828,7 @@ def test_folded_finish(gpu, oracle, restore_tuning, shape, residual):
         a, b = a.astype(np.float64), b.astype(np.float64)
         assert np.abs(a - b).max() <= 2e-6 * (1 + np.abs(b).max())
     # accumulation into dx and into dgamma / dbeta on the folded path
-    gpu.tune(gpu.TUNE_FOLD_MAX, 128)
+    gpu.tune(gpu.TUNE_FOLD_MAX, 2048)
     ws = gpu.workspace(N, C, HW, G)
     y, st = gpu.gn_silu_forward(xd, gd, bd, G, eps=EPS, residual=residual, ws=ws)
     dx0 = torch.full_like(xd, 0.5)

@@ -157,6 +157,52 @@ def test_pw_conv_gn_matches_unfused_device_path(gpu, oracle, pw_path, N, C_in, C
     assert_vals(host(y), host(y2), "fused vs unfused y")
 
 
+FOLD_SHAPES = [
+    # (N, C_in, C_out, HW, G, kind, silu): units past the one-launch size,
+    # 256 to 2504 chunk partials each
+    (1, 256, 128, 4096, 16, "normal", True),   # the Nano LKR at 1024^2, stride 16: 256
+    (1, 128, 256, 4096, 8, "normal", True),    # 1024 partials
+    (1, 64, 64, 70000, 16, "offset", True),    # |mean| / std ~ 1e5, ragged: 2188
+    (2, 16, 32, 40000, 4, "normal", False),    # two samples, no activation: 2504
+]
+
+
+@pytest.mark.parametrize("N,C_in,C_out,HW,G,kind,silu", FOLD_SHAPES)
+def test_pw_conv_gn_folded_finish(gpu, oracle, N, C_in, C_out, HW, G, kind, silu):
+    """The finish of the epilogue's chunk partials folded into the apply
+    (SOAR_TUNE_FOLD_MAX at or above the unit's partials): no finish launch,
+    and z, mean, rstd, mean_lo and y bit for bit those of the separate
+    finish (0)."""
+    import soar_gn
+    import torch
+    print(f"pw_conv_gn folded N={N} C_in={C_in} C_out={C_out} HW={HW} G={G} {kind}",
+          flush=True)
+    old = gpu.tune_get(gpu.TUNE_FOLD_MAX)
+    runs = {}
+    try:
+        for fold in (0, 4096):
+            gpu.tune(gpu.TUNE_FOLD_MAX, fold)
+            gpu.prof_summary()
+            gpu.prof_enable(True)
+            try:
+                _, _, _, gamma, beta, z, y, st = fused_case(gpu, oracle, N, C_in, C_out, HW,
+                                                            G, kind, silu)
+                torch.cuda.synchronize()
+                names = {r["kernel"] for r in soar_gn.prof_summary()}
+            finally:
+                gpu.prof_enable(False)
+            assert ("gn_stats_finish" in names) == (fold == 0), names
+            runs[fold] = [host(t) for t in (z, y, st.mean, st.rstd, st.mean_lo)]
+    finally:
+        gpu.tune(gpu.TUNE_FOLD_MAX, old)
+    for a, b in zip(runs[0], runs[4096]):
+        assert np.array_equal(a, b)
+    y_t, mean_t, rstd_t = oracle.gn_silu_fwd_f64(runs[4096][0], gamma, beta, N, C_out, HW, G,
+                                                 EPS, silu=silu)
+    assert_stats(runs[4096][2], runs[4096][3], mean_t, rstd_t, "folded")
+    assert_vals(runs[4096][1], y_t, "folded y")
+
+
 @pytest.mark.parametrize("chunk", [128, 512, 4096])
 def test_pw_chunk_changes_only_partial_order(gpu, oracle, chunk):
     args = (1, 32, 32, 10000, 8, "normal", True)

@@ -107,6 +107,10 @@ def _dw_cba_case(gpu, gen, K=7, N=2, C=16, H=160, W=130, G=4):
 
 CASES = {
     "pw": _pw_case,
+    # few partials per element (the finish's one-element-per-thread path)
+    "pw_narrow": lambda g, r: _pw_case(g, r, N=1, C_in=128, C_out=256, H=32, W=32),
+    # many partials per element (a wave per segment)
+    "dw_k3_wide": lambda g, r: _dw_case(g, r, K=3, N=2, C=8, H=256, W=256),
     "dw_k3": lambda g, r: _dw_case(g, r, K=3),
     "dw_k7": lambda g, r: _dw_case(g, r, K=7),
     "dw_k3_s2": lambda g, r: _dw_case(g, r, K=3, S=2),
