@@ -858,14 +858,16 @@ SOAR_API int soar_pw_cba_backward(const float* dy, const float* z, const float* 
         const unsigned gflags = flags & SOAR_GN_SILU;
         soar::gn::BwdArgs a{dy, z, gamma, beta, mean, rstd, mean_lo, nullptr, dgamma, dbeta,
                             gflags, workspace};
+        // each block folds the finish of its sample's C_out planes
         soar::gn::BwdSums sums{};
-        hipError_t e = soar::gn::launch_backward_sums(gp, a, s, &sums);
+        hipError_t e = soar::gn::launch_backward_sums(
+            gp, a, s, &sums, soar::gn::backward_sums_foldable(gp, t, a, C_out));
         if (e != hipSuccess) return hip_fail(e, "GroupNorm backward reduction launch");
         float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + L.gn_bytes);
         soar::gn::PwCbaArgs ca{dy,     z,         x,      weight,          gamma,
                                beta,   mean,      rstd,   sums.mean_lo,    sums.unit_sums,
                                sums.plane_sums, dgamma, dbeta, dx,         dweight,
-                               part};
+                               part,   sums.part, sums.cpp};
         e = soar::gn::launch_pw_cba_backward(L.cp, ca, N, C_in, C_out, HW, G, gflags != 0,
                                              (flags & SOAR_GN_ACCUMULATE_DX) != 0, s);
         if (e != hipSuccess) return hip_fail(e, "fused CBA backward launch");
@@ -1140,14 +1142,16 @@ SOAR_API int soar_dw_cba_backward(const float* dy, const float* z, const float* 
         const unsigned gflags = flags & SOAR_GN_SILU;
         soar::gn::BwdArgs a{dy, z, gamma, beta, mean, rstd, mean_lo, nullptr, dgamma, dbeta,
                             gflags, workspace};
+        // each block folds the finish of its unit's C / G planes
         soar::gn::BwdSums sums{};
-        hipError_t e = soar::gn::launch_backward_sums(gp, a, s, &sums);
+        hipError_t e = soar::gn::launch_backward_sums(
+            gp, a, s, &sums, soar::gn::backward_sums_foldable(gp, t, a, C / G));
         if (e != hipSuccess) return hip_fail(e, "GroupNorm backward reduction launch");
         float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + L.gn_bytes);
         soar::gn::DwCbaArgs da{dy,    z,         x,        weight,       gamma,
                                beta,  mean,      rstd,     sums.mean_lo, sums.unit_sums,
                                sums.plane_sums,  dgamma,   dbeta,        dx,
-                               dweight, part};
+                               dweight, part,    sums.part, sums.cpp};
         e = soar::gn::launch_dw_cba_backward(sh, da, G, gflags != 0,
                                              (flags & SOAR_GN_ACCUMULATE_DX) != 0, s);
         if (e != hipSuccess) return hip_fail(e, "fused depthwise CBA backward launch");

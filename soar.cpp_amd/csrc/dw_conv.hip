@@ -813,8 +813,12 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_bwd_small(
 // of channel c also adds dgamma[c] / dbeta[c] from the GroupNorm plane
 // sums in sample order (k_param_finish's sums).
 // ======================================================================
-template <int K, int D, bool SILU, bool ACC>
-__global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
+// (The waves per SIMD the register budget allows without the folded
+// finish, 5 at k3 and 4 at k5, held for the FOLD variants too: their extra
+// scalar code would otherwise cost a wave.)
+template <int K, int D, bool SILU, bool ACC, bool FOLD>
+__global__ __launch_bounds__(kDwThreads, D == 1 ? (K == 3 ? 5 : K == 5 ? 4 : 1) : 1)
+void k_dw_cba_bwd(
     const float* __restrict__ dy, const float* __restrict__ z, const float* __restrict__ x,
     const float* __restrict__ w, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ mean,
@@ -822,7 +826,8 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
     const double2* __restrict__ unit_sums, const double2* __restrict__ plane_sums,
     float* __restrict__ dgamma, float* __restrict__ dbeta, float* __restrict__ dx,
     float* __restrict__ part, float* __restrict__ dw, bool direct, int64_t N, int64_t C,
-    int64_t G, int64_t H, int64_t W, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per) {
+    int64_t G, int64_t H, int64_t W, int64_t tiles_x, int64_t tiles_y, int64_t tpp, int per,
+    const double2* __restrict__ gn_part, int64_t gn_cpp) {
     using T = Tile<K, 1, D, 1, true>;
     constexpr int KK1 = K * K + 1;
     constexpr int PAD = (K - 1) * D / 2;
@@ -831,6 +836,8 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
     __shared__ __attribute__((aligned(16))) float tdz[T::floats];
     __shared__ __attribute__((aligned(16))) float tx[T::floats];
     __shared__ float red[kDwThreads / 64][KK1];
+    __shared__ double2 fps[kFoldPlanes];  // the unit's plane sums (folded finish)
+    __shared__ float fgam[kFoldPlanes];   // and their channels' gamma
     const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
     const int64_t plane = blk / tpp, gix = blk - plane * tpp;
     const int64_t n = plane / C, c = plane - n * C;
@@ -845,22 +852,6 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
     const float mu = mean[u], r = rstd[u];
     const float e = mean_lo ? -mean_lo[u] * r : 0.0f;
     const float gm = gamma ? gamma[c] : 1.0f, bt = beta ? beta[c] : 0.0f;
-    const double2 S = unit_sums[u];
-    const double Md = (double)(cpg * HW);
-    const float A = gm * r;
-    const float B = (float)(-(double)r * S.x / Md);
-    const float Dc = (float)(-(double)r * S.y / Md);
-    if ((dgamma || dbeta) && n == 0 && gix == 0 && threadIdx.x == 0) {
-        double sa = 0.0, sb = 0.0;
-        for (int64_t s = 0; s < N; ++s) {
-            const double2 v = plane_sums[s * C + c];
-            sa += v.x;
-            sb += v.y;
-        }
-        if (dbeta) dbeta[c] = (float)((double)dbeta[c] + sa);
-        if (dgamma) dgamma[c] = (float)((double)dgamma[c] + sb);
-    }
-
     const float* zp = z + plane * HW;
     const float* gp = dy + plane * HW;
     const float* xp = x + plane * HW;
@@ -904,6 +895,46 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
             inside |= (uint32_t)in << k;
         }
     };
+    // the first tile's loads are in flight while the block folds the finish
+    fetch(ty0, 0);
+    // FOLD: the block folds the GroupNorm backward's finish from the
+    // reduction's partials (unit_sums and plane_sums unused), with the
+    // finish's own arithmetic.
+    constexpr bool fold = FOLD;
+    double2 S;
+    if constexpr (fold) {
+        bwd_plane_sums<kDwThreads>(gn_part, (int)(u * cpg), (int)cpg, (int)gn_cpp, fps, gamma,
+                                   (int)C, fgam);
+        __syncthreads();
+        S = bwd_unit_sums(fps, fgam, (int)cpg, (int)gn_cpp);
+    } else {
+        S = unit_sums[u];
+    }
+    const double Md = (double)(cpg * HW);
+    const float A = gm * r;
+    const float B = (float)(-(double)r * S.x / Md);
+    const float Dc = (float)(-(double)r * S.y / Md);
+    if ((dgamma || dbeta) && n == 0 && gix == 0) {  // block-uniform
+        double sa = 0.0, sb = 0.0;
+        for (int64_t s = 0; s < N; ++s) {
+            double2 v;
+            if constexpr (fold) {
+                __syncthreads();  // fps[0] read by every thread above
+                bwd_plane_sums<kDwThreads>(gn_part, (int)(s * C + c), 1, (int)gn_cpp, fps);
+                __syncthreads();
+                v = fps[0];
+            } else {
+                v = plane_sums[s * C + c];
+            }
+            sa += v.x;
+            sb += v.y;
+        }
+        if (threadIdx.x == 0) {
+            if (dbeta) dbeta[c] = (float)((double)dbeta[c] + sa);
+            if (dgamma) dgamma[c] = (float)((double)dgamma[c] + sb);
+        }
+    }
+
     float wr[K * K];
 #pragma unroll
     for (int k = 0; k < K * K; ++k) wr[k] = w[c * K * K + K * K - 1 - k];  // flipped
@@ -922,7 +953,6 @@ __global__ __launch_bounds__(kDwThreads) void k_dw_cba_bwd(
     constexpr bool kHF = K >= 5;
     HaloFetch<K, D, 1, kTH, true> hf;
     if constexpr (kHF) hf.init(ix0, wi);
-    fetch(ty0, 0);
     for (int64_t ty = ty0; ty < ty1; ++ty) {
         const int lr0 = ty > ty0 ? O : 0;
         if (ty > ty0) {
@@ -1530,14 +1560,14 @@ hipError_t launch_dw_cba_backward(const DwShape& sh, const DwCbaArgs& a, int64_t
         using CF = decltype(cf);
         if constexpr (CF::s == 1) {
             bsel(silu, [&](auto SI) {
-                bsel(accumulate_dx, [&](auto AC) {
-                    k_dw_cba_bwd<CF::k, CF::d, SI(), AC()>
+                bsel(accumulate_dx, [&](auto AC) { bsel(a.unit_sums == nullptr, [&](auto FO) {
+                    k_dw_cba_bwd<CF::k, CF::d, SI(), AC(), FO()>
                         <<<dim3((unsigned)(sh.N * sh.C * tpp)), kDwThreads, 0, s>>>(
                             a.dy, a.z, a.x, a.w, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo,
                             a.unit_sums, a.plane_sums, a.dgamma, a.dbeta, a.dx, part, a.dw,
                             direct, sh.N, sh.C, G, sh.Hi, sh.Wi, tiles_x, tiles_y, tpp,
-                            (int)per);
-                });
+                            (int)per, a.gn_part, a.gn_cpp);
+                }); });
             });
         }
     });

@@ -177,12 +177,23 @@ bool backward_is_small(const Plan& p, const Tuning& t);
 // the workspace for a fused consumer.  mean_lo is the residual the dx
 // arithmetic must use (the workspace's recovered one when the caller saved
 // none and there is no SiLU).
+// With `fold`, only the reduction runs: plane_sums and unit_sums are null
+// and the consumer forms both from the chunk partials `part` (cpp per
+// plane) with bwd_plane_sums / bwd_unit_sums, the finish's own arithmetic.
 struct BwdSums {
     const double2* plane_sums;  // [N * C]
     const double2* unit_sums;   // [N * G]
     const float* mean_lo;       // [N * G], nullable
+    const double2* part;        // [N * C][cpp] (fold)
+    int64_t cpp;
 };
-hipError_t launch_backward_sums(const Plan& p, const BwdArgs& a, hipStream_t s, BwdSums* out);
+hipError_t launch_backward_sums(const Plan& p, const BwdArgs& a, hipStream_t s, BwdSums* out,
+                                bool fold = false);
+// True if a consumer whose blocks each fold `planes` planes' partials
+// (at most kFoldPlanes) may take the sums unfinished: the mean residual is
+// not recovered and the partials fit the folded-finish limits.
+constexpr int64_t kFoldPlanes = 64;
+bool backward_sums_foldable(const Plan& p, const Tuning& t, const BwdArgs& a, int64_t planes);
 
 // GroupNorm forward whose chunk partials are already in the workspace (the
 // pointwise convolution wrote them): the finish, then the apply, over all
@@ -315,6 +326,10 @@ struct PwCbaArgs {
     float* dx;      // nullable
     float* dw;      // nullable
     float* part_w;  // [blocks][C_out][C_in] workspace (with dw)
+    // unit_sums and plane_sums null: the GroupNorm reduction's chunk
+    // partials, cpp per plane, whose finish each block folds
+    const double2* gn_part = nullptr;
+    int64_t gn_cpp = 0;
 };
 struct PwCbaPlan {
     int64_t chunk = 0, cpp = 0, blocks = 0;  // pixels per block, per plane, all
@@ -378,6 +393,11 @@ struct DwCbaArgs {
     float* dx;      // [N][C][H][W]
     float* dw;      // [C][K][K], nullable
     float* part;    // weight-gradient block partials
+    // unit_sums and plane_sums null: the GroupNorm reduction's chunk
+    // partials, cpp per plane, whose finish each block folds (C / G at most
+    // kFoldPlanes)
+    const double2* gn_part = nullptr;
+    int64_t gn_cpp = 0;
 };
 bool dw_cba_fused_fits(const DwShape& sh);
 size_t dw_cba_part_bytes(const DwShape& sh);

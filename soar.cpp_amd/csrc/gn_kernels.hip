@@ -668,40 +668,16 @@ __device__ void finish_bwd_unit(int64_t u, const double2* __restrict__ part,
         e = (double)(-lo * rstd[u]);  // the dx pass's e, in its fp32 form
         if (threadIdx.x == 0) lo_ws[u] = lo;
     }
-    int gs = 1;
-    while (gs < 64 && gs < cpp) gs <<= 1;
+    static_assert(kThreads == kBwdFinishThreads, "bwd_unit_sums follows this block's order");
+    const int gs = bwd_plane_lanes((int)cpp);  // cpp < 2^31 (the reduction's grid)
     const int ngroups = kThreads / gs;
     const int grp = (int)threadIdx.x / gs, r = (int)threadIdx.x & (gs - 1);
     double S1 = 0.0, S2 = 0.0;  // meaningful in each group's lane r == 0
     for (int64_t j = grp; j - grp < cpg; j += ngroups) {
         const bool live = j < cpg;
         const int64_t plane = u * cpg + (live ? j : 0);
-        const double2* pp = part + plane * cpp;
-        double A = 0.0, B = 0.0;
-        if (live) {
-            int64_t q = r;
-            for (; q + 3 * gs < cpp; q += 4 * gs) {
-                const double2 v0 = pp[q], v1 = pp[q + gs], v2 = pp[q + 2 * gs],
-                              v3 = pp[q + 3 * gs];
-                A += v0.x;
-                B += v0.y;
-                A += v1.x;
-                B += v1.y;
-                A += v2.x;
-                B += v2.y;
-                A += v3.x;
-                B += v3.y;
-            }
-            for (; q < cpp; q += gs) {
-                const double2 v = pp[q];
-                A += v.x;
-                B += v.y;
-            }
-        }
-        for (int off = gs >> 1; off > 0; off >>= 1) {
-            A += __shfl_xor(A, off);
-            B += __shfl_xor(B, off);
-        }
+        const double2 ab = bwd_plane_sum(part + plane * cpp, (int)cpp, gs, r, live);
+        double A = ab.x, B = ab.y;
         if (live && r == 0) {
             B = fma(e, A, B);
             plane_sums[plane] = make_double2(A, B);
@@ -1743,13 +1719,20 @@ bool make_pw_plan(int64_t N, int64_t C_out, int64_t HW, int64_t G, const Tuning&
 // dgamma/dbeta finish over all planes.
 bool backward_is_small(const Plan& p, const Tuning& t) { return small_bwd(p, t); }
 
-hipError_t launch_backward_sums(const Plan& p, const BwdArgs& a, hipStream_t s, BwdSums* out) {
+bool backward_sums_foldable(const Plan& p, const Tuning& t, const BwdArgs& a, int64_t planes) {
+    return !recover_lo(a) && planes <= kFoldPlanes && fold_fits(p, t, planes * p.cpp);
+}
+
+hipError_t launch_backward_sums(const Plan& p, const BwdArgs& a, hipStream_t s, BwdSums* out,
+                                bool fold) {
     const WsView w = ws_view(p, a.ws);
     launch_reduce(p, a, w, 0, 0, 0, p.units, s);
-    launch_reduce(p, a, w, 0, p.units, 0, 0, s);
-    out->plane_sums = w.plane_sums;
-    out->unit_sums = w.unit_sums;
+    if (!fold) launch_reduce(p, a, w, 0, p.units, 0, 0, s);
+    out->plane_sums = fold ? nullptr : w.plane_sums;
+    out->unit_sums = fold ? nullptr : w.unit_sums;
     out->mean_lo = recover_lo(a) ? w.lo : a.mean_lo;
+    out->part = w.part;
+    out->cpp = p.cpp;
     return hipGetLastError();
 }
 

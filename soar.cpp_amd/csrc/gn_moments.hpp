@@ -1,7 +1,9 @@
 // gn_moments.hpp - the block-level combine of shifted sums into (mean, M2),
 // shared by the GroupNorm statistics pass (k_stats) and the convolution
 // epilogues that produce the same chunk partials, so both combine their
-// threads' sums with the same float64 operations in the same order.
+// threads' sums with the same float64 operations in the same order; and
+// the backward finish's per-plane and per-unit sums, shared by its own
+// finish blocks and the fused CBA backward kernels that fold it.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -75,6 +77,100 @@ __device__ __forceinline__ double2 block_moments(float K, float s_f, float q_f, 
         r = centred_moments(S0, Q0, N, R0);
     }
     return r;
+}
+
+// ---- the GroupNorm backward finish's sums ----------------------------
+// Each plane's (sum dz, sum dz xhat) comes from its cpp chunk partials of
+// the reduction pass, added by a group of gs lanes (gs the power of two at
+// or above cpp, at most 64): lane r adds partials r, r + gs, ... in order,
+// then an xor butterfly over the group.  The result depends on cpp alone,
+// not on which group or block adds the plane, so a consumer that folds the
+// finish gets the finish's own bits.
+constexpr int kBwdFinishThreads = 256;  // threads of a finish block
+
+__device__ __forceinline__ int bwd_plane_lanes(int cpp) {
+    int gs = 1;
+    while (gs < 64 && gs < cpp) gs <<= 1;
+    return gs;
+}
+
+// The plane's sums in every lane of the group (lane r of gs); `live`
+// false: zeros (the group still takes part in the butterfly).
+__device__ __forceinline__ double2 bwd_plane_sum(const double2* __restrict__ pp, int cpp,
+                                                 int gs, int r, bool live) {
+    double A = 0.0, B = 0.0;
+    if (live) {
+        int q = r;
+        for (; q + 3 * gs < cpp; q += 4 * gs) {
+            const double2 v0 = pp[q], v1 = pp[q + gs], v2 = pp[q + 2 * gs], v3 = pp[q + 3 * gs];
+            A += v0.x;
+            B += v0.y;
+            A += v1.x;
+            B += v1.y;
+            A += v2.x;
+            B += v2.y;
+            A += v3.x;
+            B += v3.y;
+        }
+        for (; q < cpp; q += gs) {
+            const double2 v = pp[q];
+            A += v.x;
+            B += v.y;
+        }
+    }
+    for (int off = gs >> 1; off > 0; off >>= 1) {
+        A += __shfl_xor(A, off);
+        B += __shfl_xor(B, off);
+    }
+    return make_double2(A, B);
+}
+
+// Sums of planes plane0 + j, j < J, into ps[j] (shared memory), by the
+// block's NT threads in groups of gs lanes; with pgam, also gamma of each
+// plane's channel (1 without gamma) into pgam[j], loaded with the partials
+// so bwd_unit_sums waits for no further load.  The reduction's partials
+// number below 2^31 (its grid), so 32-bit indices.  No synchronisation.
+template <int NT>
+__device__ __forceinline__ void bwd_plane_sums(const double2* __restrict__ part, int plane0,
+                                               int J, int cpp, double2* ps,
+                                               const float* __restrict__ gamma = nullptr,
+                                               int C = 1, float* pgam = nullptr) {
+    const int gs = bwd_plane_lanes(cpp);
+    const int ngroups = NT / gs;
+    const int grp = (int)threadIdx.x / gs, r = (int)threadIdx.x & (gs - 1);
+    for (int j = grp; j - grp < J; j += ngroups) {
+        const bool live = j < J;
+        const int plane = plane0 + (live ? j : 0);
+        float gj = 1.0f;
+        if (pgam && live && r == 0 && gamma) gj = gamma[(unsigned)plane % (unsigned)C];
+        const double2 ab = bwd_plane_sum(part + (unsigned)plane * (unsigned)cpp, cpp, gs, r, live);
+        if (live && r == 0) {
+            ps[j] = ab;
+            if (pgam) pgam[j] = gj;
+        }
+    }
+}
+
+// (S1, S2) = sum_j gamma_j (A_j, B_j) of a unit from its planes' sums
+// ps[0..cpg) and their channels' gamma pgam[0..cpg), in the finish block's
+// order: each of its kBwdFinishThreads / gs groups adds its planes j,
+// j + ngroups, ... from zero, then the groups are added in order.  One
+// thread.
+__device__ __forceinline__ double2 bwd_unit_sums(const double2* ps, const float* pgam, int cpg,
+                                                 int cpp) {
+    const int ngroups = kBwdFinishThreads / bwd_plane_lanes(cpp);
+    double s1 = 0.0, s2 = 0.0;
+    for (int g = 0; g < ngroups && g < cpg; ++g) {
+        double S1 = 0.0, S2 = 0.0;
+        for (int j = g; j < cpg; j += ngroups) {
+            const double gj = (double)pgam[j];
+            S1 += gj * ps[j].x;
+            S2 += gj * ps[j].y;
+        }
+        s1 += S1;
+        s2 += S2;
+    }
+    return make_double2(s1, s2);
 }
 
 }  // namespace gn

@@ -149,6 +149,7 @@ __global__ __launch_bounds__(kThreads) void k_conv_dx(const float* __restrict__ 
 }
 
 constexpr int64_t kConvChunk = 16384;  // largest output-position chunk of a dW block
+constexpr int kConvCoW = 4;            // output channels per wave of k_conv_dw_co
 
 // Output positions per dW block: about 2048 blocks over the (co, q) rows
 // and chunks, chunks of 1024..16384 positions (a thread walks its chunk's
@@ -166,6 +167,46 @@ int64_t conv_chunk(const ConvShape& c) {
 
 int64_t conv_chunks(const ConvShape& c) {
     const int64_t ch = conv_chunk(c);
+    return (c.N * c.Ho * c.Wo + ch - 1) / ch;
+}
+
+// The dense few-channel kernels (k_conv_fwd_co / k_conv_dw_co) take the
+// shape: one group, C_out a multiple of 4 up to 64, 32-bit positions.
+bool conv_dense_small(const ConvShape& c) {
+    return c.groups == 1 && c.C_out % kConvCoW == 0 && c.C_out <= 64 && c.C_in <= 64 &&
+           c.N * c.Ho * c.Wo < ((int64_t)1 << 31) && c.H < ((int64_t)1 << 30) &&
+           c.W < ((int64_t)1 << 30);
+}
+
+// Its weight gradient (K in {1, 3}): chunks of at least kConvDenseChunk
+// positions, about 2048 blocks of 4 waves, at most 65535 chunks.  At the
+// SOAR stem on 1024^2 (16 channels, 512^2 outputs) chunks of 256 / 512 /
+// 1024 / 2048 positions took 36 / 24 / 28 / 48 us, and 2 positions per
+// lane and step 24 us against 27 with 4.
+#ifndef SOAR_CONV_DENSE_CHUNK
+#define SOAR_CONV_DENSE_CHUNK 512
+#endif
+constexpr int64_t kConvDenseChunk = SOAR_CONV_DENSE_CHUNK;
+#ifndef SOAR_CONV_DENSE_STEP
+#define SOAR_CONV_DENSE_STEP 2
+#endif
+constexpr int kConvDenseStep = SOAR_CONV_DENSE_STEP;  // positions per lane per step
+bool conv_dw_dense(const ConvShape& c) {
+    return conv_dense_small(c) && (c.K == 1 || c.K == 3);
+}
+
+int64_t conv_dense_chunk(const ConvShape& c) {
+    const int64_t pos = c.N * c.Ho * c.Wo;
+    const int64_t waves = (c.C_out / kConvCoW) * c.C_in;
+    const int64_t blocks_per_chunk = (waves + 3) / 4;
+    const int64_t want = std::max<int64_t>(1, 2048 / blocks_per_chunk);
+    int64_t ch = (pos + want - 1) / want;
+    ch = std::max<int64_t>(kConvDenseChunk, (ch + 63) / 64 * 64);
+    return std::max<int64_t>(ch, (pos + 65534) / 65535);
+}
+
+int64_t conv_dw_chunks(const ConvShape& c) {
+    const int64_t ch = conv_dw_dense(c) ? conv_dense_chunk(c) : conv_chunk(c);
     return (c.N * c.Ho * c.Wo + ch - 1) / ch;
 }
 
@@ -289,6 +330,160 @@ __global__ __launch_bounds__(kThreads) void k_conv_dw_finish(const double* __res
         } else if (q == 0 && gb) {
             gb[co] += (float)s;
         }
+    }
+}
+
+// ---- dense convolutions with few output channels (SOAR's stem: 1 or 3
+// input channels to 16, k3 stride 2, on the full-resolution image) -------
+// The generic kernels above give every output channel its own thread and
+// so read each input tap once per output channel (16 times at the stem),
+// and the weight gradient's blocks do the same per (co, q) row.
+
+// Forward: one thread per output position computes CT output channels from
+// one read of its input taps.  Every output adds its taps in k_conv_fwd's
+// order (input channel, ky, kx, taps outside the input skipped), so the
+// values are k_conv_fwd's.  groups == 1, C_out % CT == 0, N*Ho*Wo < 2^31.
+template <int CT>
+__global__ __launch_bounds__(kThreads) void k_conv_fwd_co(const float* __restrict__ in,
+                                                          const float* __restrict__ w,
+                                                          const float* __restrict__ bias,
+                                                          float* __restrict__ out, ConvShape c) {
+    const uint32_t HWo = (uint32_t)(c.Ho * c.Wo), Wo = (uint32_t)c.Wo;
+    const uint32_t P = (uint32_t)(c.N * c.Ho * c.Wo);
+    const int H = (int)c.H, W = (int)c.W, K = (int)c.K, KK = K * K, cin = (int)c.C_in;
+    const int S = (int)c.S, D = (int)c.D, pad = (int)c.pad;
+    const int64_t co0 = (int64_t)blockIdx.y * CT;
+    const uint32_t p = blockIdx.x * kThreads + threadIdx.x;  // one position per thread
+    if (p < P) {
+        const uint32_t n = p / HWo, r = p - n * HWo;
+        const uint32_t oy = r / Wo, ox = r - oy * Wo;
+        const int iy0 = (int)oy * S - pad, ix0 = (int)ox * S - pad;
+        float acc[CT];
+#pragma unroll
+        for (int j = 0; j < CT; ++j) acc[j] = 0.0f;
+        for (int q = 0; q < cin; ++q) {
+            const float* plane = in + ((int64_t)n * cin + q) * c.H * c.W;
+            const float* wq = w + (co0 * cin + q) * KK;  // + j * cin * KK: channel co0 + j
+            for (int ky = 0; ky < K; ++ky) {
+                const int iy = iy0 + ky * D;
+                if (iy < 0 || iy >= H) continue;
+                for (int kx = 0; kx < K; ++kx) {
+                    const int ix = ix0 + kx * D;
+                    if (ix < 0 || ix >= W) continue;
+                    const float x = plane[(int64_t)iy * W + ix];
+#pragma unroll
+                    for (int j = 0; j < CT; ++j)
+                        acc[j] = fmaf(wq[(int64_t)j * cin * KK + ky * K + kx], x, acc[j]);
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < CT; ++j) {
+            float* o = out + ((int64_t)n * c.C_out + co0 + j) * HWo + r;
+            *o = bias ? acc[j] + bias[co0 + j] : acc[j];
+        }
+    }
+}
+
+// dW / db partials with a wave per (kConvCoW = 4 output channels, input
+// channel q): its lanes walk positions p0 + lane, p0 + lane + 64, ... of
+// the chunk, read dy of the 4 channels and the K*K input taps once per
+// position (taps outside the input read as zero), and keep the
+// 4 x (K*K + 1) sums in float64; the wave adds its lanes in a fixed tree.
+// Same partial layout as k_conv_dw_taps (one per chunk).  groups == 1,
+// C_out % 4 == 0, K in {1, 3}, 32-bit position arithmetic.
+template <int K>
+__global__ __launch_bounds__(kThreads) void k_conv_dw_co(const float* __restrict__ go,
+                                                         const float* __restrict__ in,
+                                                         double* __restrict__ part, ConvShape c,
+                                                         int64_t chunks, int64_t csize) {
+    constexpr int KK = K * K, KK1 = KK + 1;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int64_t cin = c.C_in;
+    const int64_t task = (int64_t)blockIdx.x * (kThreads / 64) + wv;  // (channel group, q)
+    if (task >= (c.C_out / kConvCoW) * cin) return;  // (no block barrier below)
+    const int64_t co0 = task / cin * kConvCoW, q = task % cin;
+    const uint32_t HWo = (uint32_t)(c.Ho * c.Wo), Wo = (uint32_t)c.Wo;
+    const int H = (int)c.H, W = (int)c.W;
+    const int S = (int)c.S, D = (int)c.D, pad = (int)c.pad;
+    const uint32_t chunk = blockIdx.y;
+    const uint32_t p0 = (uint32_t)(chunk * csize);
+    const uint32_t end = (uint32_t)std::min<int64_t>((chunk + 1) * csize, c.N * c.Ho * c.Wo);
+    double acc[kConvCoW][KK1];
+#pragma unroll
+    for (int j = 0; j < kConvCoW; ++j)
+#pragma unroll
+        for (int k = 0; k < KK1; ++k) acc[j][k] = 0.0;
+    // kConvDenseStep positions per step (p, p + 64, ...), their loads
+    // issued together; the sums take them in position order
+    auto load = [&](uint32_t p, float* g, float* x) {
+        const uint32_t n = p / HWo, r = p - n * HWo;
+        const uint32_t oy = r / Wo, ox = r - oy * Wo;
+#pragma unroll
+        for (int j = 0; j < kConvCoW; ++j) g[j] = go[((int64_t)n * c.C_out + co0 + j) * HWo + r];
+        const float* ip = in + ((int64_t)n * cin + q) * c.H * c.W;
+        const int iy0 = (int)oy * S - pad, ix0 = (int)ox * S - pad;
+#pragma unroll
+        for (int ky = 0; ky < K; ++ky)
+#pragma unroll
+            for (int kx = 0; kx < K; ++kx) {
+                const int iy = iy0 + ky * D, ix = ix0 + kx * D;
+                const bool inside = iy >= 0 && iy < H && ix >= 0 && ix < W;
+                x[ky * K + kx] = inside ? ip[(int64_t)iy * W + ix] : 0.0f;
+            }
+    };
+    auto add = [&](const float* g, const float* x) {
+#pragma unroll
+        for (int j = 0; j < kConvCoW; ++j) {
+            acc[j][KK] += (double)g[j];
+#pragma unroll
+            for (int k = 0; k < KK; ++k) acc[j][k] += (double)g[j] * (double)x[k];
+        }
+    };
+    for (uint32_t p = p0 + lane; p < end; p += 64 * kConvDenseStep) {
+        float g[kConvDenseStep][kConvCoW], x[kConvDenseStep][KK];
+#pragma unroll
+        for (int i = 0; i < kConvDenseStep; ++i)
+            if (p + 64 * i < end) load(p + 64 * i, g[i], x[i]);
+#pragma unroll
+        for (int i = 0; i < kConvDenseStep; ++i)
+            if (p + 64 * i < end) add(g[i], x[i]);
+    }
+#pragma unroll
+    for (int j = 0; j < kConvCoW; ++j)
+#pragma unroll
+        for (int k = 0; k < KK1; ++k) {
+            double v = acc[j][k];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off);
+            if (lane == 0)
+                part[(((co0 + j) * cin + q) * KK1 + k) * chunks + chunk] =
+                    (k < KK || q == 0) ? v : 0.0;
+        }
+}
+
+// k_conv_dw_finish with a wave per row: lane l adds chunks l, l + 64, ...
+// in order, then the wave's fixed tree; for many chunks.
+__global__ __launch_bounds__(kThreads) void k_conv_dw_finish_wave(
+    const double* __restrict__ part, float* __restrict__ gw, float* __restrict__ gb,
+    ConvShape c, int64_t chunks) {
+    const int64_t KK = c.K * c.K;
+    const int64_t cig = c.C_in / c.groups;
+    const int64_t rows = c.C_out * cig * (KK + 1);
+    const int64_t r = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    double s = 0.0;
+    for (int64_t k = lane; k < chunks; k += 64) s += part[r * chunks + k];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off);
+    if (lane != 0) return;
+    const int64_t wq = r / (KK + 1), tap = r - wq * (KK + 1);
+    const int64_t co = wq / cig, q = wq - co * cig;
+    if (tap < KK) {
+        if (gw) gw[wq * KK + tap] += (float)s;
+    } else if (q == 0 && gb) {
+        gb[co] += (float)s;
     }
 }
 
@@ -1154,13 +1349,26 @@ __global__ __launch_bounds__(kThreads) void k_adamw_multi(
 hipError_t launch_conv_forward(const float* in, const float* w, const float* bias, float* out,
                                const ConvShape& c, hipStream_t s) {
     const int64_t total = c.N * c.C_out * c.Ho * c.Wo;
+    if (conv_dense_small(c)) {
+        // all of C_out per thread up to 16 channels, else tiles of 16 / 8 / 4
+        const int64_t pos = c.N * c.Ho * c.Wo;
+        const int ct = c.C_out % 16 == 0 ? 16 : c.C_out % 8 == 0 ? 8 : 4;
+        const dim3 grid((unsigned)((pos + kThreads - 1) / kThreads), (unsigned)(c.C_out / ct));
+        if (ct == 16)
+            k_conv_fwd_co<16><<<grid, kThreads, 0, s>>>(in, w, bias, out, c);
+        else if (ct == 8)
+            k_conv_fwd_co<8><<<grid, kThreads, 0, s>>>(in, w, bias, out, c);
+        else
+            k_conv_fwd_co<4><<<grid, kThreads, 0, s>>>(in, w, bias, out, c);
+        return hipGetLastError();
+    }
     k_conv_fwd<<<blocks_for(total), kThreads, 0, s>>>(in, w, bias, out, c);
     return hipGetLastError();
 }
 
 size_t conv_backward_workspace_bytes(const ConvShape& c) {
     const int64_t rows = c.C_out * (c.C_in / c.groups) * (c.K * c.K + 1);
-    return (size_t)(rows * conv_chunks(c)) * sizeof(double);
+    return (size_t)(rows * conv_dw_chunks(c)) * sizeof(double);
 }
 
 hipError_t launch_conv_backward(const float* go, const float* in, const float* w, float* gx,
@@ -1174,6 +1382,22 @@ hipError_t launch_conv_backward(const float* go, const float* in, const float* w
             k_conv_dx<false><<<blocks_for(total), kThreads, 0, s>>>(go, w, gx, c);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
+    }
+    if ((gw || gb) && conv_dw_dense(c)) {
+        const int64_t csize = conv_dense_chunk(c), chunks = conv_dw_chunks(c);
+        double* part = static_cast<double*>(ws);
+        const int64_t waves = (c.C_out / kConvCoW) * c.C_in;
+        const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)chunks);
+        if (c.K == 3)
+            k_conv_dw_co<3><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks, csize);
+        else
+            k_conv_dw_co<1><<<grid, kThreads, 0, s>>>(go, in, part, c, chunks, csize);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const int64_t rows = c.C_out * c.C_in * (c.K * c.K + 1);
+        k_conv_dw_finish_wave<<<(unsigned)((rows + 3) / 4), kThreads, 0, s>>>(part, gw, gb, c,
+                                                                             chunks);
+        return hipGetLastError();
     }
     if (gw || gb) {
         const int64_t chunks = conv_chunks(c), csize = conv_chunk(c);

@@ -37,6 +37,7 @@
 
 #include "gn_internal.hpp"
 #include "gn_math.hpp"
+#include "gn_moments.hpp"
 #include "soar_gn.h"
 
 namespace soar {
@@ -958,7 +959,8 @@ __global__ __launch_bounds__(128 * kFbPairs, 1) void k_pw_cba_bwd(
     const double2* __restrict__ unit_sums, const double2* __restrict__ plane_sums,
     float* __restrict__ dgamma, float* __restrict__ dbeta, float* __restrict__ dx,
     float* __restrict__ part_w, int64_t C_in, int64_t C_out, int64_t HW, int64_t G,
-    int64_t N, int64_t chunk, int64_t cpp) {
+    int64_t N, int64_t chunk, int64_t cpp, const double2* __restrict__ gn_part,
+    int64_t gn_cpp) {
     constexpr int kZr = 32 * TM, kXr = 32 * TN;      // staged dz rows, x rows
     constexpr int kStage = (kZr + kXr) * kWgStride;  // floats of one stage
     constexpr int kR = 16 * TM * TN;                 // dW accumulators per lane
@@ -974,6 +976,19 @@ __global__ __launch_bounds__(128 * kFbPairs, 1) void k_pw_cba_bwd(
     const int64_t n = (int64_t)blockIdx.x / cpp, kc = (int64_t)blockIdx.x - n * cpp;
     const int64_t cpg = C_out / G;
 
+    // Without unit_sums the block folds the GroupNorm backward's finish:
+    // the sums of sample n's planes (and, in block 0, of every sample's for
+    // dgamma / dbeta) from the reduction's partials, into shared memory
+    // the stages have not used yet, with the finish's own arithmetic.
+    const bool fold = unit_sums == nullptr;  // block-uniform
+    double2* fps = reinterpret_cast<double2*>(lds_all);  // [64] this sample's planes
+    double2* fpq = fps + 64;                             // [64] sample s's, block 0
+    float* fgam = reinterpret_cast<float*>(fps + 128);   // [64] their gamma
+    if (fold) {
+        bwd_plane_sums<128 * kFbPairs>(gn_part, (int)(n * C_out), (int)C_out, (int)gn_cpp, fps,
+                                       gamma, (int)C_out, fgam);
+        __syncthreads();
+    }
     // Channel c's coefficients for sample n, as k_bwd_dx forms them:
     // mu, r, e, gamma, beta, A = gamma r, B = -r S1 / M, D = -r S2 / M
     // (zeros past C_out: those rows get dz = 0).
@@ -985,7 +1000,9 @@ __global__ __launch_bounds__(128 * kFbPairs, 1) void k_pw_cba_bwd(
             const float mu = mean[u], r = rstd[u];
             const float e = mean_lo ? -mean_lo[u] * r : 0.0f;
             const float gm = gamma ? gamma[c] : 1.0f, bt = beta ? beta[c] : 0.0f;
-            const double2 S = unit_sums[u];
+            const int64_t g0 = (u - n * G) * cpg;  // the unit's first plane in the sample
+            const double2 S = fold ? bwd_unit_sums(fps + g0, fgam + g0, (int)cpg, (int)gn_cpp)
+                                   : unit_sums[u];
             const double Md = (double)(cpg * HW);
             lo = f4{mu, r, e, gm};
             hi = f4{bt, gm * r, (float)(-(double)r * S.x / Md), (float)(-(double)r * S.y / Md)};
@@ -993,17 +1010,30 @@ __global__ __launch_bounds__(128 * kFbPairs, 1) void k_pw_cba_bwd(
         *reinterpret_cast<f4*>(&coef[8 * c]) = lo;
         *reinterpret_cast<f4*>(&coef[8 * c + 4]) = hi;
     }
-    if (blockIdx.x == 0 && (int64_t)threadIdx.x < C_out && (dgamma || dbeta)) {
+    if (blockIdx.x == 0 && (dgamma || dbeta)) {
         // k_param_finish for channel c: the same sums in sample order
         const int64_t c = threadIdx.x;
         double sa = 0.0, sb = 0.0;
         for (int64_t s = 0; s < N; ++s) {
-            const double2 v = plane_sums[s * C_out + c];
-            sa += v.x;
-            sb += v.y;
+            double2 v;
+            if (fold) {  // block-uniform
+                bwd_plane_sums<128 * kFbPairs>(gn_part, (int)(s * C_out), (int)C_out,
+                                               (int)gn_cpp, fpq);
+                __syncthreads();
+                if (c < C_out) v = fpq[c];
+                __syncthreads();
+            } else if (c < C_out) {
+                v = plane_sums[s * C_out + c];
+            }
+            if (c < C_out) {
+                sa += v.x;
+                sb += v.y;
+            }
         }
-        if (dbeta) dbeta[c] = (float)((double)dbeta[c] + sa);
-        if (dgamma) dgamma[c] = (float)((double)dgamma[c] + sb);
+        if (c < C_out) {
+            if (dbeta) dbeta[c] = (float)((double)dbeta[c] + sa);
+            if (dgamma) dgamma[c] = (float)((double)dgamma[c] + sb);
+        }
     }
     __syncthreads();
 
@@ -1998,7 +2028,7 @@ hipError_t launch_pw_cba_backward(const PwCbaPlan& p, const PwCbaArgs& a, int64_
             <<<dim3((unsigned)p.blocks), 128 * kFbPairs, 0, s>>>(
                 a.dy, a.z, a.x, a.w, a.gamma, a.beta, a.mean, a.rstd, a.mean_lo, a.unit_sums,
                 a.plane_sums, a.dgamma, a.dbeta, a.dx, part, C_in, C_out, HW, G, N, p.chunk,
-                p.cpp);
+                p.cpp, a.gn_part, a.gn_cpp);
     };
     bsel(silu, [&](auto S) {
         bsel(tm == 2, [&](auto M2) {

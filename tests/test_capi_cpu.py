@@ -58,12 +58,17 @@ def test_ops_validate_on_the_host(L):
     assert L.soar_upsample_bilinear_backward(None, None, 1, 2, 2, 1 << 31, 1,
                                              None) == soar_gn.SOAR_EINVAL
     # conv workspace is pure host arithmetic: one fp64 partial per (weight
-    # tap or bias, position chunk); chunks of 1024..16384 positions, sized
-    # for about 2048 blocks over the 16 (co, q) rows: 1024 here
-    assert L.soar_conv_backward_workspace_bytes(1, 1, 16, 64, 64, 32, 32, 3, 1, 2, 1, 1) == \
+    # tap or bias, position chunk).  Grouped (or K > 3, or C_out % 4) convs:
+    # chunks of 1024..16384 positions, sized for about 2048 blocks over the
+    # 16 (co, q) rows: 1024 here
+    assert L.soar_conv_backward_workspace_bytes(1, 2, 16, 64, 64, 32, 32, 3, 1, 2, 1, 2) == \
         16 * 10 * 1 * 8
+    # dense few-channel convs (the stem): chunks of at least 512 positions,
+    # about 2048 blocks over the 4-channel wave groups: 2 and 64 chunks
+    assert L.soar_conv_backward_workspace_bytes(1, 1, 16, 64, 64, 32, 32, 3, 1, 2, 1, 1) == \
+        16 * 10 * 2 * 8
     assert L.soar_conv_backward_workspace_bytes(2, 1, 16, 256, 256, 128, 128, 3, 1, 2, 1, 1) == \
-        16 * 10 * 32 * 8
+        16 * 10 * 64 * 8
     # one row (co, q) wants 2048 chunks, capped below by 1024 positions
     assert L.soar_conv_backward_workspace_bytes(1, 1, 1, 1024, 1024, 512, 512, 3, 1, 2, 1, 1) == \
         1 * 10 * 256 * 8

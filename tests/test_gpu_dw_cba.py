@@ -132,6 +132,41 @@ def test_dw_cba_backward_matches_oracle(fused, oracle, N, C, H, W, K, D, G, silu
     _check_case(fused, oracle, N * 17 + C * 5 + H + K * 3 + D, N, C, H, W, K, D, G, silu, kind)
 
 
+@pytest.mark.parametrize("N,C,H,W,K,D,G,silu,kind", [CASES[i] for i in (0, 1, 2, 3, 8)] + [
+    (1, 16, 512, 512, 3, 1, 8, True, "normal"),    # SOAR Nano at 1024^2: 64 partials a plane
+    (1, 128, 64, 64, 7, 1, 2, True, "normal"),     # 64 planes a unit
+])
+def test_dw_cba_backward_folded_finish(fused, N, C, H, W, K, D, G, silu, kind):
+    """The GroupNorm backward's finish folded into the fused kernel (every
+    block forms its unit's plane and unit sums from the reduction's
+    partials; SOAR_TUNE_FOLD_MAX 2048): no finish launch, and dx, dW,
+    dgamma, dbeta bit for bit those of the separate finish (0)."""
+    import torch
+    g = fused
+    pad = (K - 1) * D // 2
+    print(f"dw_cba_backward folded N={N} C={C} {H}x{W} K={K} D={D} G={G}", flush=True)
+    x, w, gm, bt, dy = _inputs(N * 13 + C + H + K, N, C, H, W, K, kind)
+    xd, wd, gd, bd, dyd = dev(x), dev(w), dev(gm), dev(bt), dev(dy)
+    z = g.dw_conv_forward(xd, wd, None, pad, 1, D)
+    _, st = g.gn_silu_forward(z, gd, bd, G, eps=EPS, silu=silu)
+    runs = {}
+    for fold in (0, 2048):
+        g.tune(g.TUNE_FOLD_MAX, fold)
+        g.prof_summary()
+        g.prof_enable(True)
+        try:
+            out = g.dw_cba_backward(dyd, z, xd, wd, gd, bd, st, G, pad, 1, D, silu=silu)
+            torch.cuda.synchronize()
+            names = {r["kernel"] for r in g.prof_summary()}
+        finally:
+            g.prof_enable(False)
+        assert "dw_cba_bwd" in names, names
+        assert ("gn_bwd_finish" in names) == (fold == 0), names
+        runs[fold] = [host(t) for t in out]
+    for a, b, name in zip(runs[0], runs[2048], ("dx", "dW", "dgamma", "dbeta")):
+        assert np.array_equal(a, b), name
+
+
 def _sweep_cases(n=20, seed=20261205):
     """Seeded random depthwise CBA blocks: every tiled (K, dilation) with
     "same" padding, 1-3 samples, 1-8 channels per group, planes from a

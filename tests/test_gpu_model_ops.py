@@ -78,6 +78,9 @@ def conv_ref(x, w, b, S, pad, D, G):
 @pytest.mark.parametrize("N,Ci,Co,H,W,K,S,D,G,bias", [
     (1, 1, 16, 64, 64, 3, 2, 1, 1, False),   # the model's stem
     (2, 3, 16, 33, 47, 3, 2, 1, 1, True),    # odd sizes, RGB stem
+    (1, 1, 16, 1024, 1024, 3, 2, 1, 1, False),  # the stem at 1024^2: 512 dW chunks
+    (1, 4, 12, 40, 36, 1, 1, 1, 1, True),    # K = 1, C_out in tiles of 4
+    (2, 2, 8, 50, 30, 3, 1, 1, 1, True),     # stride 1, C_out 8
     (1, 8, 12, 20, 18, 3, 1, 2, 4, True),    # grouped, dilated
     (1, 6, 6, 11, 9, 5, 3, 1, 2, False),     # stride 3, K 5
 ])

@@ -117,6 +117,41 @@ def test_pw_cba_backward_matches_oracle(fused, oracle, N, C_in, C_out, HW, G, si
     _within(host(uw), tw, bw, "unfused dW")
 
 
+def _launch_names(g, run):
+    import torch
+    g.prof_summary()
+    g.prof_enable(True)
+    try:
+        out = run()
+        torch.cuda.synchronize()
+        return out, {r["kernel"] for r in g.prof_summary()}
+    finally:
+        g.prof_enable(False)
+
+
+@pytest.mark.parametrize("N,C_in,C_out,HW,G,silu,kind", [CASES[i] for i in (0, 1, 4, 8)])
+def test_pw_cba_backward_folded_finish(fused, N, C_in, C_out, HW, G, silu, kind):
+    """The GroupNorm backward's finish folded into the fused kernel (every
+    block forms its sample's plane and unit sums from the reduction's
+    partials; SOAR_TUNE_FOLD_MAX 2048): no finish launch, and dx, dW,
+    dgamma, dbeta bit for bit those of the separate finish (0)."""
+    g = fused
+    print(f"pw_cba_backward folded N={N} C_in={C_in} C_out={C_out} HW={HW} G={G}", flush=True)
+    x, w, gm, bt, dy = _inputs(N * 29 + C_in + C_out + HW, N, C_in, C_out, HW, kind)
+    xd, wd, gd, bd, dyd = dev(x), dev(w), dev(gm), dev(bt), dev(dy)
+    z, _, st = g.pw_conv_gn_silu_forward(xd, wd, None, gd, bd, G, eps=EPS, silu=silu)
+    runs = {}
+    for fold in (0, 2048):
+        g.tune(g.TUNE_FOLD_MAX, fold)
+        out, names = _launch_names(
+            g, lambda: g.pw_cba_backward(dyd, z, xd, wd, gd, bd, st, G, silu=silu))
+        assert "pw_cba_bwd" in names, names
+        assert ("gn_bwd_finish" in names) == (fold == 0), names
+        runs[fold] = [host(t) for t in out]
+    for a, b, name in zip(runs[0], runs[2048], ("dx", "dW", "dgamma", "dbeta")):
+        assert np.array_equal(a, b), name
+
+
 @pytest.mark.parametrize("want_dx,want_dw,accumulate", [
     (True, True, True), (True, False, False), (False, True, False), (True, False, True)])
 def test_pw_cba_backward_outputs_and_accumulation(fused, oracle, want_dx, want_dw, accumulate):
