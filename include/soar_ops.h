@@ -115,6 +115,33 @@ SOAR_API int soar_convex_combination_backward(
     const float* grad_y, const float* g, const float* a, const float* b,
     float* grad_g, float* grad_a, float* grad_b, size_t n, void* stream);
 
+/* The SOAR gates with their sigmoid folded in (no counterpart in the
+ * reference, which runs sigmoid_forward and then the gate's kernel: the
+ * same values in one launch per direction; the host layer's Fuse and Ctx
+ * blocks use them).  s = sigmoid(z) is recomputed from z as
+ * soar_sigmoid_forward computes it.
+ *   soar_sigmoid_convex_*: y = s*a + (1-s)*b (as soar_convex_combination_*
+ *   with g = s); grad_z = grad_y*(a-b) * s*(1-s), grad_a = grad_y*s,
+ *   grad_b = grad_y*(1-s) (any NULL).
+ *   soar_mul_sigmoid_broadcast_*: y[c][i] = a[c][i] * s[c] (as
+ *   soar_mul_broadcast_* with b = s); grad_a = grad_y*s[c], grad_z[c] =
+ *   (sum_i grad_y*a) * s[c]*(1-s[c]) (either NULL).
+ * flags as the _ex entry points below: SOAR_GN_ACCUMULATE_DX adds into the
+ * gradients, 0 writes them. */
+SOAR_API int soar_sigmoid_convex_forward(const float* z, const float* a,
+                                         const float* b, float* y, size_t n,
+                                         void* stream);
+SOAR_API int soar_sigmoid_convex_backward_ex(
+    const float* grad_y, const float* z, const float* a, const float* b,
+    float* grad_z, float* grad_a, float* grad_b, size_t n, unsigned flags,
+    void* stream);
+SOAR_API int soar_mul_sigmoid_broadcast_forward(const float* a, const float* z,
+                                                float* y, size_t C, size_t HW,
+                                                void* stream);
+SOAR_API int soar_mul_sigmoid_broadcast_backward_ex(
+    const float* grad_y, const float* a, const float* z, float* grad_a,
+    float* grad_z, size_t C, size_t HW, unsigned flags, void* stream);
+
 /* out[c] = mean of plane c.  Replaces: global_avg_pool_forward (cuda_kernels.hpp:37). */
 SOAR_API int soar_global_avg_pool_forward(const float* in, float* out,
                                           size_t C, size_t HW, void* stream);

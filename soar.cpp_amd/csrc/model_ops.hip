@@ -574,6 +574,81 @@ __global__ __launch_bounds__(kThreads) void k_convex_bwd(const float* __restrict
     }
 }
 
+// ---- the SOAR gates with their sigmoid folded in --------------------------
+// Fuse (blocks.cpp:333): y = s*a + (1-s)*b with s = sigmoid(z), and Ctx:
+// y[c][i] = a[c][i] * sigmoid(z[c]).  s is recomputed from z wherever it is
+// needed (sigmoidf_exact, the sigmoid kernel's own arithmetic), so the
+// values, and the gradients below, are those of the sigmoid kernel followed
+// by the convex-combination / broadcast-multiply kernel, one launch each
+// direction instead of two.
+__global__ __launch_bounds__(kThreads) void k_sigmoid_convex_fwd(const float* __restrict__ z,
+                                                                 const float* __restrict__ a,
+                                                                 const float* __restrict__ b,
+                                                                 float* __restrict__ y,
+                                                                 int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads) {
+        const float gv = sigmoidf_exact(z[i]);
+        y[i] = gv * a[i] + (1.0f - gv) * b[i];
+    }
+}
+
+// ga = gy*s, gb = gy*(1-s), gz = (gy*(a-b)) * s * (1-s)
+template <bool ACC>
+__global__ __launch_bounds__(kThreads) void k_sigmoid_convex_bwd(
+    const float* __restrict__ gy, const float* __restrict__ z, const float* __restrict__ a,
+    const float* __restrict__ b, float* __restrict__ gz, float* __restrict__ ga,
+    float* __restrict__ gb, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads) {
+        const float d = gy[i], gv = sigmoidf_exact(z[i]);
+        if (ga) put<ACC>(ga + i, d * gv);
+        if (gb) put<ACC>(gb + i, d * (1.0f - gv));
+        if (gz) {
+            const float gg = d * (a[i] - b[i]);
+            put<ACC>(gz + i, gg * gv * (1.0f - gv));
+        }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_mul_sigmoid_fwd(const float* __restrict__ a,
+                                                              const float* __restrict__ z,
+                                                              float* __restrict__ y,
+                                                              int64_t rows, int64_t HW) {
+    const int64_t n = rows * HW;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads)
+        y[i] = a[i] * sigmoidf_exact(z[i / HW]);
+}
+
+// ga = gy * s[row]; gz[row] = (float)(sum gy*a) * s * (1-s), one block per row
+template <bool ACC>
+__global__ __launch_bounds__(kThreads) void k_mul_sigmoid_bwd(const float* __restrict__ gy,
+                                                              const float* __restrict__ a,
+                                                              const float* __restrict__ z,
+                                                              float* __restrict__ ga,
+                                                              float* __restrict__ gz,
+                                                              int64_t HW) {
+    __shared__ double sh[kThreads];
+    const int64_t row = blockIdx.x;
+    const float* g = gy + row * HW;
+    const float* ar = a + row * HW;
+    const float bv = sigmoidf_exact(z[row]);
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < HW; i += kThreads) {
+        const float gv = g[i];
+        if (ga) put<ACC>(ga + row * HW + i, gv * bv);
+        if (gz) s += (double)gv * ar[i];
+    }
+    if (gz) {
+        s = block_sum(s, sh);
+        if (threadIdx.x == 0) {
+            const float gb = (float)s;
+            put<ACC>(gz + row, gb * bv * (1.0f - bv));
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Global average pool: one block per plane (layers.cpp:1306-1345).
 // ---------------------------------------------------------------------------
@@ -1465,6 +1540,36 @@ hipError_t launch_convex_backward(const float* gy, const float* g, const float* 
                                   bool acc, hipStream_t s) {
     bsel(acc, [&](auto A) {
         k_convex_bwd<A()><<<blocks_for(n), kThreads, 0, s>>>(gy, g, a, b, gg, ga, gb, n);
+    });
+    return hipGetLastError();
+}
+
+hipError_t launch_sigmoid_convex_forward(const float* z, const float* a, const float* b,
+                                         float* y, int64_t n, hipStream_t s) {
+    k_sigmoid_convex_fwd<<<blocks_for(n), kThreads, 0, s>>>(z, a, b, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_sigmoid_convex_backward(const float* gy, const float* z, const float* a,
+                                          const float* b, float* gz, float* ga, float* gb,
+                                          int64_t n, bool acc, hipStream_t s) {
+    bsel(acc, [&](auto A) {
+        k_sigmoid_convex_bwd<A()><<<blocks_for(n), kThreads, 0, s>>>(gy, z, a, b, gz, ga, gb, n);
+    });
+    return hipGetLastError();
+}
+
+hipError_t launch_mul_sigmoid_forward(const float* a, const float* z, float* y, int64_t rows,
+                                      int64_t HW, hipStream_t s) {
+    k_mul_sigmoid_fwd<<<blocks_for(rows * HW), kThreads, 0, s>>>(a, z, y, rows, HW);
+    return hipGetLastError();
+}
+
+hipError_t launch_mul_sigmoid_backward(const float* gy, const float* a, const float* z,
+                                       float* ga, float* gz, int64_t rows, int64_t HW, bool acc,
+                                       hipStream_t s) {
+    bsel(acc, [&](auto A) {
+        k_mul_sigmoid_bwd<A()><<<(unsigned)rows, kThreads, 0, s>>>(gy, a, z, ga, gz, HW);
     });
     return hipGetLastError();
 }

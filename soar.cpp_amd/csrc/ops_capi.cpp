@@ -437,6 +437,75 @@ SOAR_API int soar_convex_combination_backward(const float* grad_y, const float* 
                                                SOAR_GN_ACCUMULATE_DX, stream);
 }
 
+SOAR_API int soar_sigmoid_convex_forward(const float* z, const float* a, const float* b,
+                                         float* y, size_t n, void* stream) {
+    if (n == 0) return ok();
+    int rc;
+    if ((rc = check_count(n)) || (rc = check_dev(z, n * 4, "z")) ||
+        (rc = check_dev(a, n * 4, "a")) || (rc = check_dev(b, n * 4, "b")) ||
+        (rc = check_dev(y, n * 4, "y")))
+        return rc;
+    return launched(soar::ops::launch_sigmoid_convex_forward(z, a, b, y, (int64_t)n, S(stream)),
+                    "sigmoid_convex_forward launch");
+}
+
+SOAR_API int soar_sigmoid_convex_backward_ex(const float* grad_y, const float* z,
+                                             const float* a, const float* b, float* grad_z,
+                                             float* grad_a, float* grad_b, size_t n,
+                                             unsigned flags, void* stream) {
+    bool acc;
+    int rc;
+    if ((rc = grad_flags(flags, "sigmoid_convex_backward", &acc))) return rc;
+    if (n == 0 || (!grad_z && !grad_a && !grad_b)) return ok();
+    if ((rc = check_count(n)) || (rc = check_dev(grad_y, n * 4, "grad_y")) ||
+        (rc = check_dev(z, n * 4, "z")) || (rc = check_dev(a, n * 4, "a")) ||
+        (rc = check_dev(b, n * 4, "b")) || (rc = check_dev_opt(grad_z, n * 4, "grad_z")) ||
+        (rc = check_dev_opt(grad_a, n * 4, "grad_a")) ||
+        (rc = check_dev_opt(grad_b, n * 4, "grad_b")))
+        return rc;
+    return launched(soar::ops::launch_sigmoid_convex_backward(grad_y, z, a, b, grad_z, grad_a,
+                                                              grad_b, (int64_t)n, acc,
+                                                              S(stream)),
+                    "sigmoid_convex_backward launch");
+}
+
+SOAR_API int soar_mul_sigmoid_broadcast_forward(const float* a, const float* z, float* y,
+                                                size_t C, size_t HW, void* stream) {
+    int64_t n;
+    int rc;
+    if ((rc = check_planes(C, HW, &n))) return rc;
+    if (n == 0) return ok();
+    if ((rc = require_device()) || (rc = check_dev(a, n * 4, "a")) ||
+        (rc = check_dev(z, C * 4, "z")) || (rc = check_dev(y, n * 4, "y")))
+        return rc;
+    return launched(
+        soar::ops::launch_mul_sigmoid_forward(a, z, y, (int64_t)C, (int64_t)HW, S(stream)),
+        "mul_sigmoid_broadcast_forward launch");
+}
+
+SOAR_API int soar_mul_sigmoid_broadcast_backward_ex(const float* grad_y, const float* a,
+                                                    const float* z, float* grad_a,
+                                                    float* grad_z, size_t C, size_t HW,
+                                                    unsigned flags, void* stream) {
+    int64_t n;
+    bool acc;
+    int rc;
+    if ((rc = grad_flags(flags, "mul_sigmoid_broadcast_backward", &acc))) return rc;
+    if ((rc = check_planes(C, HW, &n))) return rc;
+    if (n == 0 || (!grad_a && !grad_z)) return ok();
+    if (C > 0x7fffffffu)
+        return fail(SOAR_EINVAL, "mul_sigmoid_broadcast_backward: C too large");
+    if ((rc = require_device()) || (rc = check_dev(grad_y, n * 4, "grad_y")) ||
+        (rc = check_dev(a, n * 4, "a")) || (rc = check_dev(z, C * 4, "z")) ||
+        (rc = check_dev_opt(grad_a, n * 4, "grad_a")) ||
+        (rc = check_dev_opt(grad_z, C * 4, "grad_z")))
+        return rc;
+    return launched(soar::ops::launch_mul_sigmoid_backward(grad_y, a, z, grad_a, grad_z,
+                                                           (int64_t)C, (int64_t)HW, acc,
+                                                           S(stream)),
+                    "mul_sigmoid_broadcast_backward launch");
+}
+
 SOAR_API int soar_global_avg_pool_forward(const float* in, float* out, size_t C, size_t HW,
                                           void* stream) {
     int64_t n;

@@ -44,6 +44,19 @@ hipError_t launch_mul_broadcast_backward(const float* gy, const float* a, const 
                                          float* ga, float* gb, int64_t rows, int64_t HW, bool acc,
                                          hipStream_t s);
 
+// The Fuse / Ctx gates with the sigmoid folded in: s = sigmoid(z) in place
+// of the gate g / b above.
+hipError_t launch_sigmoid_convex_forward(const float* z, const float* a, const float* b,
+                                         float* y, int64_t n, hipStream_t s);
+hipError_t launch_sigmoid_convex_backward(const float* gy, const float* z, const float* a,
+                                          const float* b, float* gz, float* ga, float* gb,
+                                          int64_t n, bool acc, hipStream_t s);
+hipError_t launch_mul_sigmoid_forward(const float* a, const float* z, float* y, int64_t rows,
+                                      int64_t HW, hipStream_t s);
+hipError_t launch_mul_sigmoid_backward(const float* gy, const float* a, const float* z,
+                                       float* ga, float* gz, int64_t rows, int64_t HW, bool acc,
+                                       hipStream_t s);
+
 hipError_t launch_convex_forward(const float* g, const float* a, const float* b, float* y,
                                  int64_t n, hipStream_t s);
 hipError_t launch_convex_backward(const float* gy, const float* g, const float* a,

@@ -249,6 +249,12 @@ public:
 TensorPtr mul_tensors(const TensorPtr& a, const TensorPtr& b);
 // g*a + (1-g)*b (blocks.cpp:280-320).
 TensorPtr convex_combination(const TensorPtr& g, const TensorPtr& a, const TensorPtr& b);
+// The same two gates with the gate's sigmoid folded in: convex_combination
+// (sigmoid(z), a, b) and mul_tensors(a, sigmoid(z)), the same values in one
+// launch per direction instead of two.
+TensorPtr sigmoid_convex_combination(const TensorPtr& z, const TensorPtr& a,
+                                     const TensorPtr& b);
+TensorPtr mul_sigmoid(const TensorPtr& a, const TensorPtr& z);
 // Channel concatenation of [C_i, H, W] tensors (blocks.cpp:363-418).
 TensorPtr concat_channels(const std::vector<TensorPtr>& tensors);
 // Bilinear resize to target_h x target_w through Upsample(target_h / H)

@@ -201,6 +201,64 @@ struct ConvexNode : autograd::AutogradNode {
     void release_variables() override { g = a = b = nullptr; }
 };
 
+struct SigmoidConvexNode : autograd::AutogradNode {
+    TensorPtr z, a, b;
+    std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
+        std::vector<std::shared_ptr<AutogradNode>> r;
+        for (const auto& t : {z, a, b})
+            if (t && t->grad_fn()) r.push_back(t->grad_fn());
+        return r;
+    }
+    void backward(const TensorPtr& go) override {
+        const bool wz = wants(z), wa = wants(a), wb = wants(b);
+        if (!wz && !wa && !wb) return;
+        to_dev(go);
+        bool fz = false, fa = false, fb = false;
+        TensorPtr gz = wz ? write_target(z, &fz) : nullptr;
+        TensorPtr ga = wa ? write_target(a, &fa) : nullptr;
+        TensorPtr gb = wb ? write_target(b, &fb) : nullptr;
+        const unsigned fl = joint_mode({{&gz, fz}, {&ga, fa}, {&gb, fb}});
+        check(soar_sigmoid_convex_backward_ex(
+                  go->cuda_data(), z->cuda_data(), a->cuda_data(), b->cuda_data(),
+                  gz ? gz->cuda_data() : nullptr, ga ? ga->cuda_data() : nullptr,
+                  gb ? gb->cuda_data() : nullptr, (size_t)a->numel(), fl, exec::stream()),
+              "sigmoid convex combination backward");
+        // ConvexNode's order, the gate's (through its sigmoid) last
+        if (ga && fa) propagate_grad(a, std::move(ga));
+        if (gb && fb) propagate_grad(b, std::move(gb));
+        if (gz && fz) propagate_grad(z, std::move(gz));
+    }
+    void release_variables() override { z = a = b = nullptr; }
+};
+
+struct MulSigmoidNode : autograd::AutogradNode {
+    TensorPtr a, z;
+    std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
+        std::vector<std::shared_ptr<AutogradNode>> r;
+        if (a && a->grad_fn()) r.push_back(a->grad_fn());
+        if (z && z->grad_fn()) r.push_back(z->grad_fn());
+        return r;
+    }
+    void backward(const TensorPtr& go) override {
+        const bool wa = wants(a), wz = wants(z);
+        if (!wa && !wz) return;
+        to_dev(go);
+        const Planes p = planes_of(a, "mul_sigmoid");
+        bool fa = false, fz = false;
+        TensorPtr ga = wa ? write_target(a, &fa) : nullptr;
+        TensorPtr gz = wz ? write_target(z, &fz) : nullptr;
+        const unsigned fl = joint_mode({{&ga, fa}, {&gz, fz}});
+        check(soar_mul_sigmoid_broadcast_backward_ex(
+                  go->cuda_data(), a->cuda_data(), z->cuda_data(), ga ? ga->cuda_data() : nullptr,
+                  gz ? gz->cuda_data() : nullptr, (size_t)p.rows, (size_t)(p.H * p.W), fl,
+                  exec::stream()),
+              "mul_sigmoid backward");
+        if (ga && fa) propagate_grad(a, std::move(ga));
+        if (gz && fz) propagate_grad(z, std::move(gz));
+    }
+    void release_variables() override { a = z = nullptr; }
+};
+
 struct ConcatNode : autograd::AutogradNode {
     std::vector<TensorPtr> inputs;
     std::vector<std::shared_ptr<AutogradNode>> get_inputs() const override {
@@ -373,6 +431,50 @@ TensorPtr convex_combination(const TensorPtr& g, const TensorPtr& a, const Tenso
         node->g = g;
         node->a = a;
         node->b = b;
+        out->set_grad_fn(node);
+    }
+    return out;
+}
+
+TensorPtr sigmoid_convex_combination(const TensorPtr& z, const TensorPtr& a,
+                                     const TensorPtr& b) {
+    if (z->shape() != a->shape() || a->shape() != b->shape())
+        throw ShapeError("sigmoid_convex_combination: shapes differ");
+    to_dev(z);
+    to_dev(a);
+    to_dev(b);
+    const bool record = recording({z, a, b});
+    TensorPtr out = Tensor::create(a->shape(), record, true);
+    check(soar_sigmoid_convex_forward(z->cuda_data(), a->cuda_data(), b->cuda_data(),
+                                      out->cuda_data(), (size_t)a->numel(), exec::stream()),
+          "sigmoid convex combination");
+    if (record) {
+        auto node = std::make_shared<SigmoidConvexNode>();
+        node->z = z;
+        node->a = a;
+        node->b = b;
+        out->set_grad_fn(node);
+    }
+    return out;
+}
+
+TensorPtr mul_sigmoid(const TensorPtr& a, const TensorPtr& z) {
+    const Planes p = planes_of(a, "mul_sigmoid");
+    if (z->numel() != p.rows)
+        throw ShapeError("mul_sigmoid: z " + to_string(z->shape()) +
+                         " must hold one value per channel of " + to_string(a->shape()));
+    to_dev(a);
+    to_dev(z);
+    const bool record = recording({a, z});
+    TensorPtr out = Tensor::create(a->shape(), record, true);
+    check(soar_mul_sigmoid_broadcast_forward(a->cuda_data(), z->cuda_data(), out->cuda_data(),
+                                             (size_t)p.rows, (size_t)(p.H * p.W),
+                                             exec::stream()),
+          "mul_sigmoid");
+    if (record) {
+        auto node = std::make_shared<MulSigmoidNode>();
+        node->a = a;
+        node->z = z;
         out->set_grad_fn(node);
     }
     return out;

@@ -152,6 +152,11 @@ SIGNATURES = {
     "soar_mul_broadcast_backward": (_c.c_int, [_P, _P, _P, _P, _P, _SZ, _SZ, _P]),
     "soar_convex_combination_forward": (_c.c_int, [_P, _P, _P, _P, _SZ, _P]),
     "soar_convex_combination_backward": (_c.c_int, [_P] * 7 + [_SZ, _P]),
+    "soar_sigmoid_convex_forward": (_c.c_int, [_P, _P, _P, _P, _SZ, _P]),
+    "soar_sigmoid_convex_backward_ex": (_c.c_int, [_P] * 7 + [_SZ, _c.c_uint, _P]),
+    "soar_mul_sigmoid_broadcast_forward": (_c.c_int, [_P, _P, _P, _SZ, _SZ, _P]),
+    "soar_mul_sigmoid_broadcast_backward_ex": (_c.c_int, [_P, _P, _P, _P, _P, _SZ, _SZ,
+                                                          _c.c_uint, _P]),
     "soar_global_avg_pool_forward": (_c.c_int, [_P, _P, _SZ, _SZ, _P]),
     "soar_global_avg_pool_backward": (_c.c_int, [_P, _P, _SZ, _SZ, _P]),
     "soar_upsample_bilinear_forward": (_c.c_int, [_P, _P] + [_SZ] * 5 + [_P]),

@@ -231,6 +231,79 @@ def test_sigmoid_convex_broadcast_pool(env):
                                rtol=1e-7)
 
 
+@pytest.mark.parametrize("acc", [0, 1])
+def test_sigmoid_gates_match_separate_ops(env, acc):
+    """soar_sigmoid_convex_* and soar_mul_sigmoid_broadcast_* (the Fuse / Ctx
+    gates with the sigmoid folded in) give bit for bit the values of
+    soar_sigmoid_forward followed by the gate's own entry point, and the
+    gradients of the gate's backward followed by soar_sigmoid_backward,
+    written (flags 0) or added (SOAR_GN_ACCUMULATE_DX); and match float64."""
+    gn, torch = env
+    L = gn.lib()
+    fl = gn.GN_ACCUMULATE_DX if acc else 0
+    print(f"case: sigmoid gates acc={acc}", flush=True)
+    r = np.random.default_rng(16 + acc)
+    n = 20011
+    z, a, b, gy = ((r.normal(size=n) * s).astype(F32) for s in (4, 1, 1, 1))
+    zd, ad, bd, gyd = dev(torch, z), dev(torch, a), dev(torch, b), dev(torch, gy)
+    # separate: s = sigmoid(z), then the convex combination
+    sd, y0 = torch.empty(n, device="cuda"), torch.empty(n, device="cuda")
+    ok(gn, L.soar_sigmoid_forward(P(zd), P(sd), n, None))
+    ok(gn, L.soar_convex_combination_forward(P(sd), P(ad), P(bd), P(y0), n, None))
+    y1 = torch.empty(n, device="cuda")
+    ok(gn, L.soar_sigmoid_convex_forward(P(zd), P(ad), P(bd), P(y1), n, None))
+    np.testing.assert_array_equal(host(torch, y1), host(torch, y0))
+    s64 = 1.0 / (1.0 + np.exp(-z.astype(np.float64)))
+    yt = s64 * a + (1 - s64) * b
+    assert np.all(np.abs(host(torch, y1) - yt) <= 8 * U32 * (np.abs(a) + np.abs(b)) + 1e-30)
+    base = [r.normal(size=n).astype(F32) for _ in range(3)] if acc else [np.zeros(n, F32)] * 3
+    gs, ga0, gb0, gz0 = (torch.zeros(n, device="cuda") for _ in range(4))
+    ga0.copy_(dev(torch, base[1]))
+    gb0.copy_(dev(torch, base[2]))
+    gz0.copy_(dev(torch, base[0]))
+    # (the gate's own gradient, fresh, then through the sigmoid into gz0)
+    ok(gn, L.soar_convex_combination_backward_ex(P(gyd), P(sd), P(ad), P(bd), None, P(ga0),
+                                                 P(gb0), n, fl, None))
+    ok(gn, L.soar_convex_combination_backward_ex(P(gyd), P(sd), P(ad), P(bd), P(gs), None,
+                                                 None, n, 0, None))
+    ok(gn, L.soar_sigmoid_backward_ex(P(gs), P(sd), P(gz0), n, fl, None))
+    ga1, gb1, gz1 = (dev(torch, base[k]) for k in (1, 2, 0))
+    ok(gn, L.soar_sigmoid_convex_backward_ex(P(gyd), P(zd), P(ad), P(bd), P(gz1), P(ga1),
+                                             P(gb1), n, fl, None))
+    for got, want, name in ((ga1, ga0, "grad_a"), (gb1, gb0, "grad_b"), (gz1, gz0, "grad_z")):
+        np.testing.assert_array_equal(host(torch, got), host(torch, want), err_msg=name)
+    gzt = base[0] + gy * (a.astype(np.float64) - b) * s64 * (1 - s64)
+    np.testing.assert_allclose(host(torch, gz1), gzt, rtol=1e-5, atol=1e-6)
+
+    C, HW = 37, 1023
+    A = r.normal(size=(C, HW)).astype(F32)
+    Z = (r.normal(size=C) * 3).astype(F32)
+    GY = r.normal(size=(C, HW)).astype(F32)
+    Ad, Zd, GYd = dev(torch, A), dev(torch, Z), dev(torch, GY)
+    Sd, Y0, Y1 = torch.empty(C, device="cuda"), torch.empty((C, HW), device="cuda"), \
+        torch.empty((C, HW), device="cuda")
+    ok(gn, L.soar_sigmoid_forward(P(Zd), P(Sd), C, None))
+    ok(gn, L.soar_mul_broadcast_forward(P(Ad), P(Sd), P(Y0), C, HW, None))
+    ok(gn, L.soar_mul_sigmoid_broadcast_forward(P(Ad), P(Zd), P(Y1), C, HW, None))
+    np.testing.assert_array_equal(host(torch, Y1), host(torch, Y0))
+    ga_base = r.normal(size=(C, HW)).astype(F32) if acc else np.zeros((C, HW), F32)
+    gz_base = r.normal(size=C).astype(F32) if acc else np.zeros(C, F32)
+    GA0, GS, GZ0 = dev(torch, ga_base), torch.zeros(C, device="cuda"), dev(torch, gz_base)
+    ok(gn, L.soar_mul_broadcast_backward_ex(P(GYd), P(Ad), P(Sd), P(GA0), P(GS), C, HW, fl,
+                                            None))
+    GS0 = torch.zeros(C, device="cuda")
+    ok(gn, L.soar_mul_broadcast_backward_ex(P(GYd), P(Ad), P(Sd), None, P(GS0), C, HW, 0, None))
+    ok(gn, L.soar_sigmoid_backward_ex(P(GS0), P(Sd), P(GZ0), C, fl, None))
+    GA1, GZ1 = dev(torch, ga_base), dev(torch, gz_base)
+    ok(gn, L.soar_mul_sigmoid_broadcast_backward_ex(P(GYd), P(Ad), P(Zd), P(GA1), P(GZ1), C, HW,
+                                                    fl, None))
+    np.testing.assert_array_equal(host(torch, GA1), host(torch, GA0))
+    np.testing.assert_array_equal(host(torch, GZ1), host(torch, GZ0))
+    s64 = 1.0 / (1.0 + np.exp(-Z.astype(np.float64)))
+    gzt = gz_base + (GY.astype(np.float64) * A).sum(axis=1) * s64 * (1 - s64)
+    np.testing.assert_allclose(host(torch, GZ1), gzt, rtol=1e-5, atol=1e-5)
+
+
 @pytest.mark.parametrize("C,H,W,Ho,Wo", [(3, 2, 2, 4, 4), (5, 4, 4, 16, 16), (2, 7, 5, 14, 10),
                                          (2, 6, 9, 9, 13), (1, 32, 32, 64, 64),
                                          (2, 16, 12, 5, 7), (2, 3, 3, 24, 24), (2, 3, 2, 40, 37),
