@@ -333,6 +333,32 @@ SOAR_API int soar_multi_tensor_clip_device(float* const* tensors,
                                            const double* norm_sq,
                                            float max_norm, void* stream);
 
+/* The device training step's tail in two launches (no counterpart in the
+ * reference, whose trainer clips, steps and zeroes the gradients one after
+ * another, trainer.cpp:110-220; these give the values of
+ * soar_multi_tensor_norm_sq_device, soar_multi_tensor_clip_device,
+ * soar_adamw_multi_tensor_device_scalars and, with SOAR_ADAMW_ZERO_GRAD,
+ * soar_multi_tensor_fill_device(0) in that order):
+ *   soar_multi_tensor_norm_sq_partials_device: the squared norm's block
+ *   partials of `tensors` into the workspace (no finish);
+ *   soar_adamw_clip_multi_tensor_device: every block adds those partials
+ *   (the finish; *norm_sq, a DEVICE double, receives the squared norm),
+ *   clips the gradient by max_norm / total when total = (float)
+ *   sqrt(norm_sq) > max_norm and > 1e-6, runs the AdamW update with
+ *   scalars[3] (DEVICE: lr, step_size, sqrt_bc2) and, with
+ *   SOAR_ADAMW_ZERO_GRAD, sets the gradients to zero (else leaves the
+ *   clipped ones).  No host read-back (capture-safe). */
+#define SOAR_ADAMW_ZERO_GRAD 1u
+SOAR_API int soar_multi_tensor_norm_sq_partials_device(
+    const float* const* tensors, const int64_t* numel, int n_tensors,
+    void* workspace, size_t workspace_bytes, void* stream);
+SOAR_API int soar_adamw_clip_multi_tensor_device(
+    float* const* params, float* const* grads, float* const* m,
+    float* const* v, const int64_t* numel, int n_tensors,
+    const float* scalars, float beta1, float beta2, float eps, float wd,
+    const void* norm_workspace, size_t norm_workspace_bytes, float max_norm,
+    double* norm_sq, unsigned flags, void* stream);
+
 /* tensors[k][i] = value (one launch for a whole gradient list:
  * Module::zero_grad, module.hpp:71-75, without a launch per tensor). */
 SOAR_API int soar_multi_tensor_fill_device(float* const* tensors,

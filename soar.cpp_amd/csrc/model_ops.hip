@@ -1416,6 +1416,64 @@ __global__ __launch_bounds__(kThreads) void k_adamw_multi(
     }
 }
 
+// The device training step's tail in one launch: the gradient norm's
+// finish (k_multi_norm_finish's sum of the block partials, formed by every
+// block in the same order; block 0 writes it to norm_out), the clip
+// (k_multi_clip's decision, the clipped gradient kept in a register), the
+// AdamW update (k_adamw_multi) and, with zero_grad, the gradients set to
+// zero (k_multi_set, Module::zero_grad after the step): the values of those
+// four launches.
+__global__ __launch_bounds__(kThreads) void k_adamw_clip_multi(
+    float* const* __restrict__ P, float* const* __restrict__ G, float* const* __restrict__ M,
+    float* const* __restrict__ V, const int64_t* __restrict__ numel, int n_tensors, float beta1,
+    float beta2, float eps, float wd, const float* __restrict__ scalars,
+    const double* __restrict__ part, int nparts, double* __restrict__ norm_out, float max_norm,
+    int zero_grad) {
+#pragma clang fp contract(off)
+    __shared__ double sh[kThreads];
+    __shared__ double sq_all;
+    double s = 0.0;
+    for (int b = threadIdx.x; b < nparts; b += kThreads) s += part[b];
+    s = block_sum(s, sh);
+    if (threadIdx.x == 0) {
+        sq_all = s;
+        if (blockIdx.x == 0) norm_out[0] = s;
+    }
+    __syncthreads();
+    const float total = (float)sqrt(sq_all);
+    const bool clip = total > max_norm && total > 1e-6f;  // uniform over the grid
+    const float coef = clip ? max_norm / total : 1.0f;
+    const float lr = scalars[0], step_size = scalars[1], sqrt_bc2 = scalars[2];
+    __shared__ int pref[kMaxMultiTensors + 1];
+    const ChunkMap map = build_chunk_map(numel, n_tensors, pref);
+    const float one_m_b1 = 1.0f - beta1, one_m_b2 = 1.0f - beta2;
+    const float lr_wd = lr * wd;
+    for (int c = blockIdx.x; c < map.total(); c += gridDim.x) {
+        int k;
+        int64_t first;
+        map.locate(c, &k, &first);
+        float* theta = P[k];
+        float* g = G[k];
+        float* m = M[k];
+        float* v = V[k];
+        const int64_t end = min(first + kMtChunk, numel[k]);
+        for (int64_t i = first + threadIdx.x; i < end; i += kThreads) {
+            float gv = g[i];
+            if (clip) gv = gv * coef;
+            float th = theta[i];
+            if (wd != 0.0f) th = th - lr_wd * th;
+            const float mv = beta1 * m[i] + one_m_b1 * gv;
+            const float vv = beta2 * v[i] + one_m_b2 * gv * gv;
+            const float denom = (sqrtf(vv) / sqrt_bc2) + eps;
+            th = th - step_size * (mv / denom);
+            m[i] = mv;
+            v[i] = vv;
+            theta[i] = th;
+            g[i] = zero_grad ? 0.0f : gv;
+        }
+    }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -1805,6 +1863,24 @@ hipError_t launch_adamw_multi(float* const* p, const float* const* g, float* con
     k_adamw_multi<<<kMultiBlocks, kThreads, 0, s>>>(p, g, m, v, numel, n_tensors, lr, beta1,
                                                      beta2, eps, wd, step_size, sqrt_bc2,
                                                      scalars);
+    return hipGetLastError();
+}
+
+hipError_t launch_multi_norm_partials(const float* const* t, const int64_t* numel,
+                                      int n_tensors, void* ws, hipStream_t s) {
+    k_multi_norm_sq<<<kMultiBlocks, kThreads, 0, s>>>(t, numel, n_tensors,
+                                                      static_cast<double*>(ws));
+    return hipGetLastError();
+}
+
+hipError_t launch_adamw_clip_multi(float* const* p, float* const* g, float* const* m,
+                                   float* const* v, const int64_t* numel, int n_tensors,
+                                   float beta1, float beta2, float eps, float wd,
+                                   const float* scalars, const void* norm_ws, double* norm_out,
+                                   float max_norm, bool zero_grad, hipStream_t s) {
+    k_adamw_clip_multi<<<kMultiBlocks, kThreads, 0, s>>>(
+        p, g, m, v, numel, n_tensors, beta1, beta2, eps, wd, scalars,
+        static_cast<const double*>(norm_ws), kMultiBlocks, norm_out, max_norm, zero_grad ? 1 : 0);
     return hipGetLastError();
 }
 

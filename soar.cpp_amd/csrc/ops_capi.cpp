@@ -1001,6 +1001,59 @@ SOAR_API int soar_multi_tensor_clip_device(float* const* tensors, const int64_t*
     return launched(e, "multi-tensor clip launch");
 }
 
+SOAR_API int soar_multi_tensor_norm_sq_partials_device(const float* const* tensors,
+                                                       const int64_t* numel, int n_tensors,
+                                                       void* workspace, size_t workspace_bytes,
+                                                       void* stream) {
+    if (n_tensors < 0) return fail(SOAR_EINVAL, "n_tensors is negative");
+    int rc;
+    if ((rc = require_device())) return rc;
+    if (n_tensors > 0 &&
+        ((rc = check_table(tensors, n_tensors, "tensors")) ||
+         (rc = check_table(numel, n_tensors, "numel"))))
+        return rc;
+    const size_t need = soar::ops::multi_norm_workspace_bytes();
+    if (workspace_bytes < need)
+        return fail(SOAR_EINVAL, "workspace of %zu bytes is smaller than the %zu needed",
+                    workspace_bytes, need);
+    if ((rc = check_dev(workspace, need, "workspace"))) return rc;
+    const int tok = soar::gn::prof_begin(S(stream), "grad_norm");
+    hipError_t e = soar::ops::launch_multi_norm_partials(tensors, numel, n_tensors, workspace,
+                                                         S(stream));
+    soar::gn::prof_end(S(stream), tok);
+    return launched(e, "multi-tensor norm launch");
+}
+
+SOAR_API int soar_adamw_clip_multi_tensor_device(
+    float* const* params, float* const* grads, float* const* m, float* const* v,
+    const int64_t* numel, int n_tensors, const float* scalars, float beta1, float beta2,
+    float eps, float wd, const void* norm_workspace, size_t norm_workspace_bytes,
+    float max_norm, double* norm_sq, unsigned flags, void* stream) {
+    if (flags & ~SOAR_ADAMW_ZERO_GRAD)
+        return fail(SOAR_EINVAL, "unsupported flags 0x%x (SOAR_ADAMW_ZERO_GRAD)", flags);
+    if (n_tensors < 0) return fail(SOAR_EINVAL, "n_tensors is negative");
+    int rc;
+    if ((rc = require_device()) || (rc = check_dev(norm_sq, sizeof(double), "norm_sq")) ||
+        (rc = check_dev(scalars, 3 * sizeof(float), "scalars")))
+        return rc;
+    const size_t need = soar::ops::multi_norm_workspace_bytes();
+    if (norm_workspace_bytes < need)
+        return fail(SOAR_EINVAL, "norm workspace of %zu bytes is smaller than the %zu needed",
+                    norm_workspace_bytes, need);
+    if ((rc = check_dev(norm_workspace, need, "norm_workspace"))) return rc;
+    if (n_tensors > 0 &&
+        ((rc = check_table(params, n_tensors, "params")) ||
+         (rc = check_table(grads, n_tensors, "grads")) || (rc = check_table(m, n_tensors, "m")) ||
+         (rc = check_table(v, n_tensors, "v")) || (rc = check_table(numel, n_tensors, "numel"))))
+        return rc;
+    const int tok = soar::gn::prof_begin(S(stream), "adamw_clip_multi");
+    hipError_t e = soar::ops::launch_adamw_clip_multi(
+        params, grads, m, v, numel, n_tensors, beta1, beta2, eps, wd, scalars, norm_workspace,
+        norm_sq, max_norm, (flags & SOAR_ADAMW_ZERO_GRAD) != 0, S(stream));
+    soar::gn::prof_end(S(stream), tok);
+    return launched(e, "clip + AdamW multi-tensor launch");
+}
+
 SOAR_API size_t soar_multi_tensor_norm_workspace_bytes(void) {
     return soar::ops::multi_norm_workspace_bytes();
 }

@@ -136,6 +136,15 @@ hipError_t launch_adamw_multi(float* const* p, const float* const* g, float* con
                               float sqrt_bc2, hipStream_t s, const float* scalars = nullptr);
 // Clip by the coefficient formed on the device from norm_sq[0] (see
 // k_multi_clip).
+// The norm's block partials alone (into the norm workspace), and the
+// tail that finishes them: clip + AdamW (scalars on the device) + zero_grad.
+hipError_t launch_multi_norm_partials(const float* const* t, const int64_t* numel,
+                                      int n_tensors, void* ws, hipStream_t s);
+hipError_t launch_adamw_clip_multi(float* const* p, float* const* g, float* const* m,
+                                   float* const* v, const int64_t* numel, int n_tensors,
+                                   float beta1, float beta2, float eps, float wd,
+                                   const float* scalars, const void* norm_ws, double* norm_out,
+                                   float max_norm, bool zero_grad, hipStream_t s);
 hipError_t launch_multi_clip(float* const* t, const int64_t* numel, int n_tensors,
                              const double* norm_sq, float max_norm, hipStream_t s);
 

@@ -112,6 +112,10 @@ public:
     void clip_grad_norm_device(float max_norm);
     void next_scalars(float out[3]);
     void step_device(const float* scalars);
+    // clip_grad_norm_device, step_device and zero_grad in two launches (the
+    // norm's partials, then its finish + clip + update + zero in one), the
+    // same values; norm_sq() receives the squared norm.
+    void clip_step_zero_device(float max_norm, const float* scalars);
     [[nodiscard]] const double* norm_sq() const noexcept { return norm_; }
     // Puts the squared norm at `p` (a device double the caller keeps), e.g.
     // next to other values read back together with it.

@@ -291,6 +291,27 @@ void AdamW::step_device(const float* scalars) {
           "AdamW step");
 }
 
+void AdamW::clip_step_zero_device(float max_norm, const float* scalars) {
+    const int n = (int)params_.size();
+    if (n == 0) return;
+    sync_tables();
+    auto* t = static_cast<char*>(table_);
+    const size_t nb = (size_t)n * sizeof(void*);
+    check(soar_multi_tensor_norm_sq_partials_device(
+              reinterpret_cast<const float* const*>(t + nb),
+              reinterpret_cast<const int64_t*>(t + 4 * nb), n, norm_ws_, norm_ws_bytes_,
+              exec::stream()),
+          "gradient norm");
+    check(soar_adamw_clip_multi_tensor_device(
+              reinterpret_cast<float* const*>(t), reinterpret_cast<float* const*>(t + nb),
+              reinterpret_cast<float* const*>(t + 2 * nb),
+              reinterpret_cast<float* const*>(t + 3 * nb),
+              reinterpret_cast<const int64_t*>(t + 4 * nb), n, scalars, options_.beta1,
+              options_.beta2, options_.eps, options_.weight_decay, norm_ws_, norm_ws_bytes_,
+              max_norm, norm_, SOAR_ADAMW_ZERO_GRAD, exec::stream()),
+          "clip + AdamW step");
+}
+
 void AdamW::step() {
     step_count_++;
     const int n = (int)params_.size();
@@ -415,12 +436,11 @@ void Trainer::train_step_device(const TensorPtr& image, const TensorPtr& mask,
     loss->backward(grad_out);
     logits->set_grad_fn(nullptr);
     loss->set_grad_fn(nullptr);
-    optimizer_->clip_grad_norm_device(grad_clip_);
+    // clip, step, zero_grad (trainer.cpp:110-220), the last three in one launch
     optimizer_->next_scalars(pinned_scalars);
     check(soar_memcpy_async(dev_scalars, pinned_scalars, 3 * sizeof(float), 0, exec::stream()),
           "AdamW scalars");
-    optimizer_->step_device(dev_scalars);
-    optimizer_->zero_grad();
+    optimizer_->clip_step_zero_device(grad_clip_, dev_scalars);
 }
 
 StepMetrics Trainer::device_step_metrics(const double loss_sums[4], double norm_sq,

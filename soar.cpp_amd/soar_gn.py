@@ -34,7 +34,8 @@ SOAR_ENODEV = -4
 GN_SILU = 1
 GN_RESIDUAL = 2
 GN_ACCUMULATE_DX = 4
-DEFER_WEIGHT_FINISH = 8  # conv backward: weight-gradient addition at weight_grad_flush
+DEFER_WEIGHT_FINISH = 8
+ADAMW_ZERO_GRAD = 1  # soar_adamw_clip_multi_tensor_device: zero the gradients  # conv backward: weight-gradient addition at weight_grad_flush
 
 # bytes of the static scratch behind soar_group_norm_backward_noalloc
 # (SOAR_GN_NOALLOC_SCRATCH_BYTES)
@@ -194,6 +195,10 @@ SIGNATURES = {
     "soar_adamw_multi_tensor_device_scalars": (_c.c_int, [_P, _P, _P, _P, _P, _c.c_int, _P] +
                                                [_c.c_float] * 4 + [_P]),
     "soar_multi_tensor_clip_device": (_c.c_int, [_P, _P, _c.c_int, _P, _c.c_float, _P]),
+    "soar_multi_tensor_norm_sq_partials_device": (_c.c_int, [_P, _P, _c.c_int, _P, _SZ, _P]),
+    "soar_adamw_clip_multi_tensor_device": (_c.c_int, [_P, _P, _P, _P, _P, _c.c_int, _P] +
+                                            [_c.c_float] * 4 + [_P, _SZ, _c.c_float, _P,
+                                                                _c.c_uint, _P]),
     "soar_dice_bce_loss_workspace_bytes": (_SZ, [_SZ]),
     "soar_dice_bce_loss_sums_device": (_c.c_int, [_P, _P, _SZ, _c.c_float, _P, _P, _SZ, _P]),
     "soar_dice_bce_loss_from_sums": (_c.c_int, [_P, _SZ] + [_c.c_float] * 4 + [_P]),

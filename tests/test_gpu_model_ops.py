@@ -602,3 +602,59 @@ def test_adamw_and_multi_tensor(env):
     np.testing.assert_array_equal(host(torch, xd), t1)
     # a table over the limit is refused before any launch
     assert L.soar_multi_tensor_fill_device(P(tab), P(nm), 4096, 0.0, None) == gn.SOAR_EINVAL
+
+
+@pytest.mark.parametrize("max_norm,zero", [(2.0, True), (1e9, True), (2.0, False)])
+def test_fused_clip_adamw_tail(env, max_norm, zero):
+    """soar_multi_tensor_norm_sq_partials_device + soar_adamw_clip_multi_tensor_
+    device give bit for bit what norm_sq_device, clip_device, adamw_multi_
+    tensor_device_scalars and (with SOAR_ADAMW_ZERO_GRAD) fill_device(0)
+    give: parameters, moments, the squared norm and the gradients after
+    the step; clipping on (max_norm 2) and off (1e9)."""
+    gn, torch = env
+    L = gn.lib()
+    print(f"case: fused clip + AdamW max_norm={max_norm} zero={zero}", flush=True)
+    r = np.random.default_rng(21)
+    sizes = [5, 4096, 70001, 3, 12000]
+    n = len(sizes)
+    th = [r.normal(size=s).astype(F32) for s in sizes]
+    gr = [(r.normal(size=s) * 0.05).astype(F32) for s in sizes]
+    mo = [(r.normal(size=s) * 1e-3).astype(F32) for s in sizes]
+    ve = [np.abs(r.normal(size=s) * 1e-4).astype(F32) for s in sizes]
+    wsb = L.soar_multi_tensor_norm_workspace_bytes()
+    sc = torch.tensor([1e-3, 1e-3 / 0.1, np.sqrt(1 - 0.999)], dtype=torch.float32, device="cuda")
+    runs = []
+    for fused in (False, True):
+        P_, G_, M_, V_ = ([dev(torch, a) for a in arrs] for arrs in (th, gr, mo, ve))
+        tab = lambda ts: torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64,  # noqa: E731
+                                      device="cuda")
+        tp, tg, tm, tv = tab(P_), tab(G_), tab(M_), tab(V_)
+        nm = torch.tensor(sizes, dtype=torch.int64, device="cuda")
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        norm = torch.zeros(1, dtype=torch.float64, device="cuda")
+        if fused:
+            ok(gn, L.soar_multi_tensor_norm_sq_partials_device(P(tg), P(nm), n, P(ws), wsb, None))
+            ok(gn, L.soar_adamw_clip_multi_tensor_device(
+                P(tp), P(tg), P(tm), P(tv), P(nm), n, P(sc), 0.9, 0.999, 1e-8, 1e-2, P(ws), wsb,
+                max_norm, P(norm), gn.ADAMW_ZERO_GRAD if zero else 0, None))
+        else:
+            ok(gn, L.soar_multi_tensor_norm_sq_device(P(tg), P(nm), n, P(norm), P(ws), wsb, None))
+            ok(gn, L.soar_multi_tensor_clip_device(P(tg), P(nm), n, P(norm), max_norm, None))
+            ok(gn, L.soar_adamw_multi_tensor_device_scalars(P(tp), P(tg), P(tm), P(tv), P(nm), n,
+                                                            P(sc), 0.9, 0.999, 1e-8, 1e-2,
+                                                            None))
+            if zero:
+                ok(gn, L.soar_multi_tensor_fill_device(P(tg), P(nm), n, 0.0, None))
+        runs.append([host(torch, t) for t in P_ + G_ + M_ + V_ + [norm]])
+    for k, (a, b) in enumerate(zip(*runs)):
+        np.testing.assert_array_equal(a, b, err_msg=f"tensor {k}")
+    want = sum(float(np.dot(a.astype(np.float64), a)) for a in gr)
+    assert abs(float(runs[1][-1][0]) - want) <= 1e-12 * want
+    clipped = np.sqrt(want) > max_norm
+    if zero:
+        assert all(not np.any(runs[1][n + i]) for i in range(n))
+    elif clipped:
+        assert not np.array_equal(runs[1][n], gr[0])
+    assert L.soar_adamw_clip_multi_tensor_device(None, None, None, None, None, 0, None, 0.9,
+                                                 0.999, 1e-8, 0.0, None, 0, 1.0, None, 2,
+                                                 None) == gn.SOAR_EINVAL
