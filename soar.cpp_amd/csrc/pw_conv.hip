@@ -1427,6 +1427,60 @@ __global__ __launch_bounds__(1024) void k_pw_small(const float* __restrict__ x,
                                         part);
 }
 
+// The same product for few input rows (K <= 64) over many pixels: a
+// thread per pixel loads its K inputs once and forms CT outputs from them
+// (k_pw_small gives every output its own thread, so each input is read M
+// times through the caches: 16 -> 16 channels at 256^2 pixels read 64 MB
+// for 4 MB of input).  Each output adds its K terms in k_pw_small's order
+// with one wave per block row (k = 0, 1, ..., fmaf from zero, then the
+// bias or the old value), so for K <= 32 the values are k_pw_small's.
+constexpr int kPxCT = 16;  // outputs per thread
+
+// K (the input rows) a template argument so the loops carry no bounds
+// tests; the block's CT x K weights staged in LDS (each read is one
+// address for the whole wave).
+template <int K, bool TRANS, bool ACC, bool BIAS>
+__global__ __launch_bounds__(256) void k_pw_px(const float* __restrict__ x,
+                                               const float* __restrict__ w,
+                                               const float* __restrict__ bias,
+                                               float* __restrict__ z, int M, int HW) {
+    __shared__ __attribute__((aligned(16))) float sw[kPxCT][K];
+    const int p = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    const int64_t n = blockIdx.z;
+    const int m0 = (int)blockIdx.y * kPxCT;
+    const int jn = min(kPxCT, M - m0);  // block-uniform
+    for (int i = threadIdx.x; i < kPxCT * K; i += 256) {
+        const int j = i / K, k = i - j * K;
+        sw[j][k] = j < jn ? (TRANS ? w[(int64_t)k * M + m0 + j] : w[(int64_t)(m0 + j) * K + k])
+                          : 0.0f;
+    }
+    float xv[K];
+    if (p < HW) {
+        const float* xs = x + n * (int64_t)K * HW + p;
+#pragma unroll
+        for (int k = 0; k < K; ++k) xv[k] = xs[(int64_t)k * HW];
+    }
+    __syncthreads();
+    if (p >= HW) return;
+    float* zs = z + n * (int64_t)M * HW + p;
+    for (int j = 0; j < jn; ++j) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) acc = fmaf(sw[j][k], xv[k], acc);
+        const int m = m0 + j;
+        float* zo = zs + (int64_t)m * HW;
+        if (ACC)
+            *zo = *zo + acc;
+        else
+            *zo = BIAS ? bias[m] + acc : acc;
+    }
+}
+
+// K values with a k_pw_px instance
+inline bool pw_px_k(int64_t K) {
+    return K == 4 || K == 8 || K == 16 || K == 24 || K == 32 || K == 64;
+}
+
 // dW[co][ci] += sum_(n,p) dz[n][co][p] x[n][ci][p], db[co] += sum_(n,p)
 // dz[n][co][p] for small planes.  Entry e (weights ci-fastest, then the
 // C_out bias entries from E = C_out*C_in on) belongs to T = 2^lgT
@@ -1606,6 +1660,13 @@ namespace {
 // z = W x (+ bias), or z += W x; TRANS: z = W^T x.  M output rows, K input
 // rows.  Each wave sums about 32 values of K.
 // Waves per block (K split) and K per wave of the SIMT kernel.
+// Planes of at least this many pixels take k_pw_px when it has K (at most
+// 32: the same sums as k_pw_small's one-wave blocks); K = 64, which
+// k_pw_small splits over two waves (other partial sums), from
+// kPxMinHW64 pixels on.
+constexpr int64_t kPxMinHW = 1024;
+constexpr int64_t kPxMinHW64 = 65536;  // (64 -> 32 at 16384 pixels: 10.3 vs 11 us)
+
 struct PwSmallSplit {
     int S = 1;
     int64_t seg = 0;
@@ -1652,6 +1713,38 @@ hipError_t launch_pw_small(const float* x, const float* w, const float* bias, fl
     const bool v4 = !trans && K % 4 == 0 && (uintptr_t)w % 16 == 0;
     const dim3 grid((unsigned)((M * HW + 63) / 64), (unsigned)N);
     const int tok = prof_begin(s, name);
+    if (pw_px_k(K) && HW >= kPxMinHW && (S == 1 || HW >= kPxMinHW64)) {
+        // few input rows over many pixels: a thread per pixel
+        const dim3 pg((unsigned)((HW + 255) / 256), (unsigned)((M + kPxCT - 1) / kPxCT),
+                      (unsigned)N);
+        auto px = [&](auto T, auto A, auto B) {
+            auto run = [&](auto KC) {
+                k_pw_px<decltype(KC)::value, T(), A(), B()>
+                    <<<pg, 256, 0, s>>>(x, w, bias, z, (int)M, (int)HW);
+            };
+            if (K == 4)
+                run(std::integral_constant<int, 4>{});
+            else if (K == 8)
+                run(std::integral_constant<int, 8>{});
+            else if (K == 64)
+                run(std::integral_constant<int, 64>{});
+            else if (K == 16)
+                run(std::integral_constant<int, 16>{});
+            else if (K == 24)
+                run(std::integral_constant<int, 24>{});
+            else
+                run(std::integral_constant<int, 32>{});
+        };
+        using F = std::false_type;
+        bsel(trans, [&](auto T) {
+            if (accumulate)
+                px(T, std::true_type{}, F{});
+            else
+                bsel(bias != nullptr, [&](auto B) { px(T, F{}, B); });
+        });
+        prof_end(s, tok);
+        return hipGetLastError();
+    }
     auto go = [&](auto T, auto V, auto A, auto B) {
         k_pw_small<T(), V(), A(), B()><<<grid, 64 * S, 0, s>>>(x, w, bias, z, (int)M, (int)K,
                                                                (int)HW, (int)seg);

@@ -478,6 +478,12 @@ SMALL_PW_SHAPES = [
     (4, 24, 8, 1, False),      # one pixel
     (2, 1, 3, 5, True),        # K = 1
     (3, 16, 24, 100, True),    # weight-gradient segments cross sample planes
+    # few input channels over many pixels: a thread per pixel (k_pw_px)
+    (1, 16, 16, 65536, True),  # SOAR Nano Fuse at 1024^2 (256^2 planes); dx K = 16 too
+    (2, 32, 8, 4096, False),   # K = 32, two samples; dx K = 8
+    (1, 8, 40, 1030, True),    # three output tiles, ragged pixel blocks; dx K = 40: per output
+    (1, 16, 4, 262144, False), # the Nano head's prediction at 512^2: dx K = 4
+    (1, 64, 8, 65536, True),   # K = 64 over 65536 pixels; dx K = 8
 ]
 
 
