@@ -255,6 +255,19 @@ SOAR_API int soar_pw_conv_gn_silu_forward(
     int64_t HW, int64_t G, float eps, unsigned flags, void* workspace,
     size_t workspace_bytes, void* stream);
 
+/* The same CBA forward followed by a residual add, y = (the output above)
+ * + residual ([N][C_out][HW], e.g. the SOAR LKR block's input x:
+ * blocks.cpp:469-475's x + pw2(pw1(dw(x)))), the add done by the apply pass
+ * (one launch and two tensor passes fewer than the forward and an add).
+ * Workspace as soar_pw_conv_gn_silu_forward.  No counterpart in the
+ * reference (its LKR block adds after the CBA). */
+SOAR_API int soar_pw_conv_gn_silu_add_forward(
+    const float* x, const float* weight, const float* bias,
+    const float* gamma, const float* beta, const float* residual, float* z,
+    float* y, float* mean, float* rstd, float* mean_lo, int64_t N,
+    int64_t C_in, int64_t C_out, int64_t HW, int64_t G, float eps,
+    unsigned flags, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Bytes of workspace soar_pw_conv_backward needs (0 for a bad shape). */
 SOAR_API size_t soar_pw_conv_backward_workspace_bytes(int64_t N, int64_t C_in,
                                                       int64_t C_out, int64_t HW);

@@ -559,19 +559,23 @@ SOAR_API size_t soar_pw_conv_gn_workspace_bytes(int64_t N, int64_t C_out, int64_
     return b;
 }
 
-SOAR_API int soar_pw_conv_gn_silu_forward(const float* x, const float* weight,
-                                          const float* bias, const float* gamma,
-                                          const float* beta, float* z, float* y, float* mean,
-                                          float* rstd, float* mean_lo, int64_t N, int64_t C_in,
-                                          int64_t C_out, int64_t HW, int64_t G, float eps,
-                                          unsigned flags, void* workspace,
-                                          size_t workspace_bytes, void* stream) {
+namespace {
+
+// soar_pw_conv_gn_silu_forward, and with `residual` (non-null) its
+// _add_forward form: y += residual in the apply pass (or, where the
+// one-launch small-unit GroupNorm runs, in an add after it).
+int pw_conv_gn_forward(const float* x, const float* weight, const float* bias,
+                       const float* gamma, const float* beta, const float* residual, float* z,
+                       float* y, float* mean, float* rstd, float* mean_lo, int64_t N,
+                       int64_t C_in, int64_t C_out, int64_t HW, int64_t G, float eps,
+                       unsigned flags, void* workspace, size_t workspace_bytes, void* stream) {
     int64_t ie = 0, oe = 0, elems = 0;
     int rc = check_pw_shape(N, C_in, C_out, HW, &ie, &oe);
     if (rc) return rc;
     if ((rc = check_shape(N, C_out, HW, G, &elems))) return rc;
     if (flags & ~SOAR_GN_SILU)
         return fail(SOAR_EINVAL, "unsupported flags 0x%x (SOAR_GN_SILU only)", flags);
+    if (residual && (rc = check_dev(residual, (size_t)oe * 4, "residual"))) return rc;
     if (!(eps >= 0.0f)) return fail(SOAR_EINVAL, "eps must be >= 0");
     if (oe == 0) return ok();
     if (C_in == 0) return fail(SOAR_EINVAL, "C_in must be positive");
@@ -599,14 +603,23 @@ SOAR_API int soar_pw_conv_gn_silu_forward(const float* x, const float* weight,
         soar::gn::make_plan(N, C_out, HW, G, t, &q)) {
         // Small planes: the SIMT convolution (no statistics epilogue), then
         // the GroupNorm forward over z with its own plan.
-        q.vec4 = q.vec4 && aligned16(z) && aligned16(y);
+        q.vec4 = q.vec4 && aligned16(z) && aligned16(y) && (!residual || aligned16(residual));
         if ((rc = check_ws(q, workspace, workspace_bytes))) return rc;
         hipError_t e = soar::gn::launch_pw_conv(pa, N, C_in, C_out, HW, p.chunk, nullptr, false,
                                                 t.pw_small, nullptr, 1, s);
         if (e != hipSuccess) return hip_fail(e, "pointwise convolution launch");
         soar::gn::FwdArgs a{z, gamma, beta, y, mean, rstd, mean_lo, eps, flags, workspace};
+        const bool in_apply = residual && !soar::gn::forward_is_small(q, t);
+        if (in_apply) {
+            a.flags |= SOAR_GN_RESIDUAL;
+            a.res = residual;
+        }
         e = soar::gn::launch_forward(q, t, a, s);
         if (e != hipSuccess) return hip_fail(e, "GroupNorm forward launch");
+        if (residual && !in_apply) {
+            e = soar::gn::launch_add_forward(y, residual, y, oe, s);
+            if (e != hipSuccess) return hip_fail(e, "residual add launch");
+        }
         return ok();
     }
     // small grids split K over blocks when the workspace holds the slices
@@ -627,9 +640,44 @@ SOAR_API int soar_pw_conv_gn_silu_forward(const float* x, const float* weight,
                                             kp.kz, s);
     if (e != hipSuccess) return hip_fail(e, "pointwise convolution launch");
     soar::gn::FwdArgs a{z, gamma, beta, y, mean, rstd, mean_lo, eps, flags, workspace};
+    const bool in_apply = residual && !soar::gn::forward_is_small(p, t);
+    if (in_apply) {
+        a.flags |= SOAR_GN_RESIDUAL;
+        a.res = residual;
+        if (!aligned16(residual)) p.vec4 = false;
+    }
     e = soar::gn::launch_forward_from_partials(p, t, a, s);
     if (e != hipSuccess) return hip_fail(e, "GroupNorm apply launch");
+    if (residual && !in_apply) {
+        e = soar::gn::launch_add_forward(y, residual, y, oe, s);
+        if (e != hipSuccess) return hip_fail(e, "residual add launch");
+    }
     return ok();
+}
+
+}  // namespace
+
+SOAR_API int soar_pw_conv_gn_silu_forward(const float* x, const float* weight,
+                                          const float* bias, const float* gamma,
+                                          const float* beta, float* z, float* y, float* mean,
+                                          float* rstd, float* mean_lo, int64_t N, int64_t C_in,
+                                          int64_t C_out, int64_t HW, int64_t G, float eps,
+                                          unsigned flags, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+    return pw_conv_gn_forward(x, weight, bias, gamma, beta, nullptr, z, y, mean, rstd, mean_lo,
+                              N, C_in, C_out, HW, G, eps, flags, workspace, workspace_bytes,
+                              stream);
+}
+
+SOAR_API int soar_pw_conv_gn_silu_add_forward(
+    const float* x, const float* weight, const float* bias, const float* gamma,
+    const float* beta, const float* residual, float* z, float* y, float* mean, float* rstd,
+    float* mean_lo, int64_t N, int64_t C_in, int64_t C_out, int64_t HW, int64_t G, float eps,
+    unsigned flags, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!residual) return fail(SOAR_EINVAL, "residual is NULL");
+    return pw_conv_gn_forward(x, weight, bias, gamma, beta, residual, z, y, mean, rstd,
+                              mean_lo, N, C_in, C_out, HW, G, eps, flags, workspace,
+                              workspace_bytes, stream);
 }
 
 SOAR_API size_t soar_pw_conv_backward_workspace_bytes(int64_t N, int64_t C_in, int64_t C_out,

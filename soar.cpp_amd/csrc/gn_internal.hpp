@@ -148,6 +148,9 @@ struct FwdArgs {
     float eps;
     unsigned flags;
     void* ws;
+    // with SOAR_GN_RESIDUAL: the tensor added to the output (x itself when
+    // null); the one-launch small-unit kernels take x only
+    const float* res = nullptr;
 };
 
 struct BwdArgs {

@@ -548,11 +548,14 @@ struct FoldArgs {
     // launch also runs k_param_finish's sums (every plane sum is final)
     const double2* plane_sums;
     TileCount tiles;  // FOLD == kFoldTiles: the depthwise forward's tile groups
+    const float* res;  // k_apply with XRES: the residual added instead of x
 };
 
 constexpr int kFoldChunks = 1, kFoldTiles = 2;
 
-template <bool VEC, bool SILU, bool RES, bool NT, bool NTL, int FOLD>
+// XRES (with RES): the residual is fa.res, another tensor of x's shape,
+// instead of x.
+template <bool VEC, bool SILU, bool RES, bool NT, bool NTL, int FOLD, bool XRES = false>
 __global__ __launch_bounds__(kThreads2) void k_apply(
     const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ mean,
@@ -591,35 +594,51 @@ __global__ __launch_bounds__(kThreads2) void k_apply(
     const float a = k.gm * k.r, mu = k.mu, bt = fmaf(k.gm, k.e, k.bt);
     const int64_t base = ck.plane * HW + ck.off;
     const int t = threadIdx.x;
-    auto f = [&](float v) {
+    // (the external residual is added to the rounded output, as an add
+    // after the forward would: the empty asm keeps the add from contracting
+    // with SiLU's last multiply)
+    auto f = [&](float v, float rv) {
         float z = fmaf(v - mu, a, bt);
         float o = SILU ? silu_fast(z) : z;
-        return RES ? o + v : o;
+        if constexpr (XRES) {
+            asm volatile("" : "+v"(o));
+            return o + rv;
+        } else {
+            return RES ? o + rv : o;
+        }
     };
     if (VEC) {
         const f4* x4 = reinterpret_cast<const f4*>(x + base);
+        const f4* r4 = reinterpret_cast<const f4*>((XRES ? fa.res : x) + base);
         f4* y4 = reinterpret_cast<f4*>(y + base);
         const int64_t n4 = ck.len >> 2;
         int64_t i = t;
         for (; i + (kLoads2 - 1) * kThreads2 < n4; i += kLoads2 * kThreads2) {
-            f4 v[kLoads2];
-#pragma unroll
-            for (int u = 0; u < kLoads2; ++u) v[u] = load4<NTL>(&x4[i + u * kThreads2]);
+            f4 v[kLoads2], r[kLoads2];
 #pragma unroll
             for (int u = 0; u < kLoads2; ++u) {
-                const f4 o = {f(v[u].x), f(v[u].y), f(v[u].z), f(v[u].w)};
+                v[u] = load4<NTL>(&x4[i + u * kThreads2]);
+                if (XRES) r[u] = load4<NTL>(&r4[i + u * kThreads2]);
+            }
+#pragma unroll
+            for (int u = 0; u < kLoads2; ++u) {
+                const f4 rv = XRES ? r[u] : v[u];
+                const f4 o = {f(v[u].x, rv.x), f(v[u].y, rv.y), f(v[u].z, rv.z),
+                              f(v[u].w, rv.w)};
                 store4<NT>(&y4[i + u * kThreads2], o);
             }
         }
         for (; i < n4; i += kThreads2) {
-            f4 v = load4<NTL>(&x4[i]);
-            f4 o = {f(v.x), f(v.y), f(v.z), f(v.w)};
+            const f4 v = load4<NTL>(&x4[i]);
+            const f4 rv = XRES ? load4<NTL>(&r4[i]) : v;
+            f4 o = {f(v.x, rv.x), f(v.y, rv.y), f(v.z, rv.z), f(v.w, rv.w)};
             store4<NT>(&y4[i], o);
         }
     } else {
         const float* xp = x + base;
+        const float* rp = (XRES ? fa.res : x) + base;
         float* yp = y + base;
-        for (int64_t i = t; i < ck.len; i += kThreads2) store1<NT>(&yp[i], f(xp[i]));
+        for (int64_t i = t; i < ck.len; i += kThreads2) store1<NT>(&yp[i], f(xp[i], rp[i]));
     }
 }
 
@@ -1299,17 +1318,26 @@ void launch_apply(const Plan& p, const Tuning& t, const FwdArgs& a, const float*
     const dim3 grid((unsigned)nb);
     const FoldArgs fa{fold == kFoldTiles ? tpart : ws_view(p, a.ws).part,
                       a.mean, a.rstd, a.mean_lo, nullptr, nullptr, p.N, p.chunk, p.cpp, a.eps,
-                      nullptr, tiles};
+                      nullptr, tiles, a.res};
+    // an external residual (the SOAR LKR block's x + CBA(...))
+    const bool xres = res && a.res != nullptr;
     auto go = [&](auto F) {
         bsel(p.vec4, [&](auto V) {
-            bsel(silu, [&](auto S) {
-                bsel(res, [&](auto R) {
-                    bsel(t.nt_store != 0, [&](auto N) {
-                        bsel(V() && (t.nt_load & 1) != 0, [&](auto L) {
-                            k_apply<V(), S(), R(), N(), L(), F()><<<grid, kThreads2, 0, s>>>(
-                                a.x, a.gamma, a.beta, a.mean, a.rstd, lo, a.y, p.C, p.G, p.cpg,
-                                p.HW, p.chunk2, p.cpp2, block0, nb, t.reverse, fa);
+            bsel(t.nt_store != 0, [&](auto N) {
+                bsel(V() && (t.nt_load & 1) != 0, [&](auto L) {
+                    auto launch = [&](auto S, auto R, auto X) {
+                        k_apply<V(), S(), R(), N(), L(), F(), X()><<<grid, kThreads2, 0, s>>>(
+                            a.x, a.gamma, a.beta, a.mean, a.rstd, lo, a.y, p.C, p.G, p.cpg,
+                            p.HW, p.chunk2, p.cpp2, block0, nb, t.reverse, fa);
+                    };
+                    if (xres) {
+                        bsel(silu, [&](auto S) {
+                            launch(S, std::true_type{}, std::true_type{});
                         });
+                        return;
+                    }
+                    bsel(silu, [&](auto S) {
+                        bsel(res, [&](auto R) { launch(S, R, std::false_type{}); });
                     });
                 });
             });

@@ -187,6 +187,9 @@ public:
         size_t g = 1, bool act = true);
     using Module::forward;
     TensorPtr forward(const TensorPtr& input) override;
+    // residual + forward(input) (the LKR block's skip), the add in the
+    // GroupNorm's apply pass for a pointwise conv
+    TensorPtr forward_residual(const TensorPtr& input, const TensorPtr& residual);
 
     [[nodiscard]] std::shared_ptr<Conv2d> conv() const { return conv_; }
     [[nodiscard]] std::shared_ptr<GroupNorm> norm() const { return norm_; }

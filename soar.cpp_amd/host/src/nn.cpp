@@ -656,6 +656,71 @@ TensorPtr CBA::forward(const TensorPtr& input) {
     return y;
 }
 
+// residual + forward(input) with the add done by the GroupNorm's apply pass
+// (soar_pw_conv_gn_silu_add_forward) for a pointwise conv; recorded as the
+// CBA node and an add node, as add_tensors(residual, forward(input)) would
+// be (the CBA output tensor is allocated but never written: the add node
+// only routes the gradient through it).
+TensorPtr CBA::forward_residual(const TensorPtr& input, const TensorPtr& residual) {
+    if (!conv_->pointwise()) return add_tensors(residual, forward(input));
+    const unsigned flags = act_ ? SOAR_GN_SILU : 0u;
+    const ConvGeom g = conv_geom(input, *conv_);
+    if (!input->is_cuda()) input->to_cuda();
+    if (!residual->is_cuda()) residual->to_cuda();
+    const TensorPtr w = conv_->weight();
+    const TensorPtr gamma = norm_->weight(), beta = norm_->bias();
+    w->to_cuda();
+    if (gamma) {
+        gamma->to_cuda();
+        beta->to_cuda();
+    }
+    const int64_t G = (int64_t)norm_->num_groups(), HW = g.H * g.W;
+    const bool record_cba = (input->requires_grad() || w->requires_grad() ||
+                             (gamma && gamma->requires_grad())) &&
+                            GradMode::is_enabled();
+    const bool record = (record_cba || residual->requires_grad()) && GradMode::is_enabled();
+    const Shape os = conv_out_shape(input, g);
+    if (residual->shape() != os)
+        throw ShapeError("Cannot add tensors with different shapes " +
+                         to_string(residual->shape()) + " and " + to_string(os));
+    TensorPtr z = Tensor::create(os, false, true);
+    TensorPtr y = Tensor::create(os, record, true);
+    TensorPtr mean = Tensor::create({g.N * G}, false, true);
+    TensorPtr rstd = Tensor::create({g.N * G}, false, true);
+    TensorPtr lo = Tensor::create({g.N * G}, false, true);
+    const size_t wsb = soar_pw_conv_gn_workspace_bytes(g.N, g.C_out, HW, G);
+    check(soar_pw_conv_gn_silu_add_forward(
+              input->cuda_data(), w->cuda_data(), nullptr, dptr(gamma), dptr(beta),
+              residual->cuda_data(), z->cuda_data(), y->cuda_data(), mean->cuda_data(),
+              rstd->cuda_data(), lo->cuda_data(), g.N, g.C_in, g.C_out, HW, G, norm_->eps(),
+              flags, workspace(wsb), wsb, exec::stream()),
+          "CBA forward + residual");
+    if (record) {
+        TensorPtr cba_out;  // the CBA's own output: only its gradient flows through it
+        if (record_cba) {
+            cba_out = Tensor::create(os, true, true);
+            auto node = std::make_shared<CBAPointwiseNode>();
+            node->input = input;
+            node->conv_w = w;
+            node->gamma = gamma;
+            node->beta = beta;
+            node->z = z;
+            node->mean = mean;
+            node->rstd = rstd;
+            node->mean_lo = lo;
+            node->g = g;
+            node->G = G;
+            node->flags = flags;
+            cba_out->set_grad_fn(node);
+        }
+        auto add = std::make_shared<AddNode>();
+        add->a = residual;
+        add->b = cba_out;
+        y->set_grad_fn(add);
+    }
+    return y;
+}
+
 // Depthwise conv: the conv and the GroupNorm forward, recorded as one node
 // whose backward is soar_dw_cba_backward.
 TensorPtr CBA::forward_depthwise(const TensorPtr& input, unsigned flags) {

@@ -107,6 +107,8 @@ SIGNATURES = {
     "soar_pw_conv_gn_silu_forward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                                                 _I64, _I64, _I64, _I64, _c.c_float, _c.c_uint,
                                                 _P, _SZ, _P]),
+    "soar_pw_conv_gn_silu_add_forward": (_c.c_int, [_P] * 11 + [_I64] * 5 +
+                                         [_c.c_float, _c.c_uint, _P, _SZ, _P]),
     "soar_pw_conv_backward_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "soar_pw_conv_backward": (_c.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                          _c.c_uint, _P, _SZ, _P]),
@@ -454,8 +456,9 @@ def pw_conv_gn_workspace_bytes(N, C_out, HW, G) -> int:
 
 def pw_conv_gn_silu_forward(x, weight, bias, gamma, beta, G, eps=1e-5, silu=True, z=None,
                             y=None, mean=None, rstd=None, mean_lo=None, ws=None,
-                            stream=None):
-    """CBA forward of a pointwise conv through soar_pw_conv_gn_silu_forward.
+                            stream=None, residual=None):
+    """CBA forward of a pointwise conv through soar_pw_conv_gn_silu_forward
+    (with `residual`: soar_pw_conv_gn_silu_add_forward, y += residual).
 
     Returns (z, y, Stats): z the convolution output (the GroupNorm input the
     backward needs), y = silu(group_norm(z)) (or group_norm(z))."""
@@ -478,6 +481,13 @@ def pw_conv_gn_silu_forward(x, weight, bias, gamma, beta, G, eps=1e-5, silu=True
     if ws is None:
         ws = torch.empty(max(pw_conv_gn_workspace_bytes(N, C_out, HW, G), 1),
                          dtype=torch.uint8, device=x.device)
+    if residual is not None:
+        _check_tensor(residual, "residual")
+        check(lib().soar_pw_conv_gn_silu_add_forward(
+            _ptr(x), _ptr(w), _ptr(bias), _ptr(gamma), _ptr(beta), _ptr(residual), _ptr(z),
+            _ptr(y), _ptr(mean), _ptr(rstd), _ptr(mean_lo), N, C_in, C_out, HW, G, eps,
+            GN_SILU if silu else 0, _ptr(ws), ws.numel(), _stream(stream)))
+        return z, y, Stats(mean, rstd, mean_lo)
     check(lib().soar_pw_conv_gn_silu_forward(
         _ptr(x), _ptr(w), _ptr(bias), _ptr(gamma), _ptr(beta), _ptr(z), _ptr(y), _ptr(mean),
         _ptr(rstd), _ptr(mean_lo), N, C_in, C_out, HW, G, eps, GN_SILU if silu else 0,

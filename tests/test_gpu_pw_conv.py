@@ -157,6 +157,33 @@ def test_pw_conv_gn_matches_unfused_device_path(gpu, oracle, pw_path, N, C_in, C
     assert_vals(host(y), host(y2), "fused vs unfused y")
 
 
+@pytest.mark.parametrize("N,C_in,C_out,HW,G,silu", [
+    (1, 64, 64, 16384, 8, False),   # the LKR block's pw2: epilogue statistics, folded apply
+    (2, 32, 48, 70000, 12, True),   # multi-pass apply, SiLU
+    (1, 64, 128, 64, 16, False),    # small planes: SIMT conv, one-launch GroupNorm, then an add
+    (1, 32, 16, 16384, 2, False),   # small planes: SIMT conv, two-pass GroupNorm
+])
+def test_pw_conv_gn_add_forward(gpu, oracle, N, C_in, C_out, HW, G, silu):
+    """soar_pw_conv_gn_silu_add_forward: y = the CBA forward + residual, bit
+    for bit the forward followed by the add (z and the statistics
+    unchanged), on every GroupNorm path."""
+    import torch
+    print(f"pw_conv_gn_add N={N} C_in={C_in} C_out={C_out} HW={HW} G={G} silu={silu}",
+          flush=True)
+    x, w, b = rng_inputs(HW + C_in + 7, N, C_in, C_out, HW, True)
+    r = np.random.default_rng(HW + 3)
+    gamma = r.uniform(0.5, 1.5, C_out).astype(np.float32)
+    beta = (0.1 * r.standard_normal(C_out)).astype(np.float32)
+    res = dev(r.standard_normal((N, C_out, HW)).astype(np.float32))
+    args = (dev(x), dev(w), dev(b), dev(gamma), dev(beta), G)
+    z0, y0, st0 = gpu.pw_conv_gn_silu_forward(*args, eps=EPS, silu=silu)
+    z1, y1, st1 = gpu.pw_conv_gn_silu_forward(*args, eps=EPS, silu=silu, residual=res)
+    torch.cuda.synchronize()
+    assert torch.equal(z0, z1) and torch.equal(st0.mean, st1.mean)
+    assert torch.equal(st0.rstd, st1.rstd) and torch.equal(st0.mean_lo, st1.mean_lo)
+    assert torch.equal(y1, y0 + res)
+
+
 FOLD_SHAPES = [
     # (N, C_in, C_out, HW, G, kind, silu): units past the one-launch size,
     # 256 to 2504 chunk partials each
