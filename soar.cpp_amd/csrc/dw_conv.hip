@@ -39,6 +39,7 @@
 #include "gn_math.hpp"
 #include "gn_moments.hpp"
 #include "soar_gn.h"
+#include "xcd_order.hpp"
 
 namespace soar {
 namespace gn {
@@ -83,27 +84,6 @@ struct Tile {
     static constexpr int IWP = pitch();
     static constexpr int floats = IH * IWP;
 };
-
-// Logical block of physical block b in a grid of nb blocks.  Workgroups are
-// dealt to the 8 XCDs in turn (block b on XCD b % 8) and each XCD has its
-// own L2.  Adjacent tiles of a plane row share the 128-byte lines at their
-// edges (the halo), so in the hardware order those lines came from the
-// fabric twice (the k3 forward fetched 2.0x its input).  Here, within each
-// window of 64 blocks, XCD x takes 8 consecutive tiles (physical 64 w + 8 j
-// + x -> logical 64 w + 8 x + j): neighbours share one L2 while the 64
-// blocks in flight still cover one compact band of the plane.  Measured at
-// 64 x 2048^2, fwd / dgrad / wgrad: k3 0.463 / 0.469 / 0.480 ms in the
-// hardware order, 0.429 / 0.447 / 0.439 ms here (1.11x / 1.08x / 1.03x
-// fetched); a plain per-XCD split of the grid (XCD x one contiguous eighth)
-// fetched as little but ran 0.476 / 0.494 / 0.417 ms, its XCDs far apart
-// in the plane.  A bijection on [0, nb); the last nb % 64 blocks keep
-// their order.
-__device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
-    constexpr int64_t kX = 8, kWin = kX * kX;
-    if (b >= nb / kWin * kWin) return b;
-    const int64_t w = b / kWin, j = (b / kX) % kX, x = b % kX;
-    return kWin * w + kX * x + j;
-}
 
 // Row segment of a thread: SL4 floats of LDS row `lrow` from column c0*S.
 template <int K, int S, int D, int RB = 1, bool SP = false>

@@ -39,6 +39,7 @@
 #include "gn_math.hpp"
 #include "gn_moments.hpp"
 #include "soar_gn.h"
+#include "xcd_order.hpp"
 
 namespace soar {
 namespace gn {
@@ -475,7 +476,8 @@ __global__ __launch_bounds__(64 * KS, PD > 1 || KS > 1 || !FAST ? 1 : 2) void k_
 // compile-time constant.  The next item's operands come from the same load
 // code with its base pointers and lane offsets selected by a wave-uniform
 // condition; after the last item the descriptors are empty and the loads
-// return zeros without touching memory.
+// return zeros without touching memory.  Blocks take their pixel chunks in
+// the XCD-aware order of xcd_block.
 constexpr int kSd = 3;
 
 struct PwOff {
@@ -493,8 +495,9 @@ __global__ __launch_bounds__(64, 1) void k_pw_conv_stream(
     constexpr bool STATS = MODE == kStats, TW = MODE == kPlainT || MODE == kAccumT;
     constexpr int NB = kSd + 1;
     const int lane = threadIdx.x, h = lane >> 5, j = lane & 31;
-    const int64_t n = (int64_t)blockIdx.x / cpp;
-    const int64_t kc = (int64_t)blockIdx.x - n * cpp;
+    const int64_t bx = xcd_block(blockIdx.x, gridDim.x);  // the pixel chunk
+    const int64_t n = bx / cpp;
+    const int64_t kc = bx - n * cpp;
     const int64_t px0 = kc * chunk, pend = min(px0 + chunk, HW);
     const int64_t R = min<int64_t>((C_out + kRowTile - 1) / kRowTile, ((int64_t)blockIdx.y + 1) * rpw);
     const int64_t rg0 = (int64_t)blockIdx.y * rpw;
@@ -942,8 +945,9 @@ __global__ __launch_bounds__(64 * WPB, 2) void k_pw_wgrad(
 // fp32 MFMAs and VALU instructions of two waves of one SIMD take the sum of
 // their times.  The split serves the shared, permuted loads.)  At the end
 // the consumers add their dW tiles through LDS in pair order and the block
-// writes one partial for k_sum_partials.  Block 0 also adds dgamma / dbeta
-// from the plane sums, in k_param_finish's order.
+// writes one partial for k_sum_partials (at its chunk's index: blocks take
+// their chunks in the XCD-aware order of xcd_block).  Block 0 also adds
+// dgamma / dbeta from the plane sums, in k_param_finish's order.
 // ======================================================================
 constexpr int kFbPairs = 4;
 // Cache policy of the buffer accesses: non-temporal (each byte is touched
@@ -973,7 +977,8 @@ __global__ __launch_bounds__(128 * kFbPairs, 1) void k_pw_cba_bwd(
     const int pr = producer ? wv : wv - kFbPairs;
     float* __restrict__ stages = lds_all + pr * 2 * kStage;
     const int h = lane >> 5, j = lane & 31;
-    const int64_t n = (int64_t)blockIdx.x / cpp, kc = (int64_t)blockIdx.x - n * cpp;
+    const int64_t bx = xcd_block(blockIdx.x, gridDim.x);  // the pixel chunk
+    const int64_t n = bx / cpp, kc = bx - n * cpp;
     const int64_t cpg = C_out / G;
 
     // Without unit_sums the block folds the GroupNorm backward's finish:
@@ -1275,7 +1280,7 @@ __global__ __launch_bounds__(128 * kFbPairs, 1) void k_pw_cba_bwd(
         for (int v = 1; v < kFbPairs; ++v) t += red[(v * kR + k) * 64 + lane];
         const int mt = k / (16 * TN), nt = (k / 16) % TN, r = k % 16;
         const int64_t co = tile_row(mt, r, h), ci = 32 * nt + j;
-        if (co < C_out && ci < C_in) part_w[((int64_t)blockIdx.x * C_out + co) * C_in + ci] = t;
+        if (co < C_out && ci < C_in) part_w[(bx * C_out + co) * C_in + ci] = t;
     }
 }
 

@@ -1,0 +1,44 @@
+// xcd_order.hpp - the XCD-aware block order of the convolution kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace soar {
+namespace gn {
+
+// Logical block of physical block b in a grid of nb blocks.  Workgroups are
+// dealt to the 8 XCDs in turn (block b on XCD b % 8) and each XCD has its
+// own L2.  Within each window of 64 blocks, XCD x takes 8 consecutive
+// logical blocks (physical 64 w + 8 j + x -> logical 64 w + 8 x + j), while
+// the 64 blocks in flight still cover one compact band of the data.  A
+// bijection on [0, nb); the last nb % 64 blocks keep their order.
+//
+// Depthwise tiles: adjacent tiles of a plane row share the 128-byte lines
+// at their edges (the halo), so in the hardware order those lines came from
+// the fabric twice (the k3 forward fetched 2.0x its input).  Measured at
+// 64 x 2048^2, fwd / dgrad / wgrad: k3 0.463 / 0.469 / 0.480 ms in the
+// hardware order, 0.429 / 0.447 / 0.439 ms here (1.11x / 1.08x / 1.03x
+// fetched); a plain per-XCD split of the grid (XCD x one contiguous eighth)
+// fetched as little but ran 0.476 / 0.494 / 0.417 ms, its XCDs far apart
+// in the plane.
+//
+// Pointwise pixel chunks share no lines, but a chunk reads and writes 512-
+// byte runs of every channel plane, and the runs of consecutive chunks lie
+// next to each other in the planes.  A probe that reads and writes 64
+// planes 16 MiB apart in the streamed convolution's shape (one wave per
+// SIMD, 1024-float chunks, 512-byte runs) took 490 us per GiB in the
+// hardware order and 430 us here; the streamed forward with statistics at
+// 64 -> 64 channels of 2048^2 went from 486 to 468 us, the fused CBA
+// backward from 1.01 to 0.99 ms.  (The GroupNorm passes, whose blocks read
+// 32 KiB runs, gained nothing: 1.324 ms per config-3 step either way.)
+__device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
+    constexpr int64_t kX = 8, kWin = kX * kX;
+    if (b >= nb / kWin * kWin) return b;
+    const int64_t w = b / kWin, j = (b / kX) % kX, x = b % kX;
+    return kWin * w + kX * x + j;
+}
+
+}  // namespace gn
+}  // namespace soar
