@@ -9,7 +9,8 @@
 // Conv2d (layers.cpp:326-332): taps outside the input are skipped.
 //
 // Fast kernels (template K, S, D for the configurations the model uses):
-// a 256-thread block owns a column of up to four 32 x 64 output tiles of
+// a 256-thread block owns a column of 32 x 64 output tiles (4, 8 at K = 5,
+// 16 at K = 7: conv_per) of
 // one (n, c) plane.  The input tile each needs, halo included, is staged in
 // LDS from coalesced loads (zeros outside the image); the loads of the next
 // tile go out into registers before the current tile is computed, so they
@@ -308,13 +309,22 @@ __device__ __forceinline__ void dw_conv_body(
         if constexpr (STATS) {
             const int nv = (int)min<int64_t>(kPer, Wo - ox);  // outputs stored (<= 0: none)
             if (ty == ty0 && nv > 0) mK = acc[0];
+            if (nv == kPer) {  // a whole segment: the same sums without the tests
 #pragma unroll
-            for (int q = 0; q < kPer; ++q)
-                if (q < nv) {
+                for (int q = 0; q < kPer; ++q) {
                     const float d = acc[q] - mK;
                     ms += d;
                     mq = fmaf(d, d, mq);
                 }
+            } else {
+#pragma unroll
+                for (int q = 0; q < kPer; ++q)
+                    if (q < nv) {
+                        const float d = acc[q] - mK;
+                        ms += d;
+                        mq = fmaf(d, d, mq);
+                    }
+            }
             mcnt += max(nv, 0);
         }
         if (ox + kPer <= Wo && ((reinterpret_cast<uintptr_t>(orow + ox) & 15) == 0)) {
@@ -429,13 +439,22 @@ __device__ __forceinline__ void dw_conv_rb_body(
             if constexpr (STATS) {
                 const int nv = (int)min<int64_t>(kPer, Wo - ox);  // outputs stored (<= 0: none)
                 if (ty == ty0 && j == 0 && nv > 0) mK = acc[0][0];
+                if (nv == kPer) {  // a whole segment: the same sums without the tests
 #pragma unroll
-                for (int q = 0; q < kPer; ++q)
-                    if (q < nv) {
+                    for (int q = 0; q < kPer; ++q) {
                         const float d = acc[j][q] - mK;
                         ms += d;
                         mq = fmaf(d, d, mq);
                     }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < kPer; ++q)
+                        if (q < nv) {
+                            const float d = acc[j][q] - mK;
+                            ms += d;
+                            mq = fmaf(d, d, mq);
+                        }
+                }
                 mcnt += max(nv, 0);
             }
             if (ox + kPer <= Wo && ((reinterpret_cast<uintptr_t>(orow + ox) & 15) == 0)) {
@@ -1244,15 +1263,22 @@ bool planes_fit_32(const DwShape& sh) {
            sh.Wi < ((int64_t)1 << 23) && sh.Wo < ((int64_t)1 << 23);
 }
 
-// Tile rows per block of k_dw_conv over `planes` planes of H x W outputs:
-// 4 (the next tile's input loads overlap the current tile's FMAs), halved
-// while the grid would hold fewer than 4096 blocks.  Returns the tile
-// groups per plane; *per the rows per group.
+// Tile rows per block of k_dw_conv over `planes` planes of H x W outputs
+// (the next tile's input loads overlap the current tile's FMAs, and a block
+// loads its K*K weights, fetches its first tile whole and combines its
+// statistics once): 16 at K = 7, 8 at K = 5, 4 below, halved while the grid
+// would hold fewer than 4096 blocks.  At 64 x 2048^2 (one box, two rounds),
+// 4 / 8 / 16 tiles: k7 forward 0.543 / 0.512 / 0.506 ms, with statistics
+// 0.588 / 0.536 / 0.517 ms, input gradient 0.546 / 0.515 / 0.508 ms; k5
+// forward 0.419 / 0.412 / 0.426 ms; k3 0.392 / 0.409 / 0.426 ms.  Returns
+// the tile groups per plane; *per the rows per group.
+int conv_per(int64_t K) { return K >= 7 ? 16 : K == 5 ? 8 : 4; }
+
 int64_t conv_groups(int64_t planes, int64_t H, int64_t W, int64_t* tiles_x, int64_t* tiles_y,
-                    int* per, int64_t th = kTH) {
+                    int* per, int64_t K, int64_t th = kTH) {
     *tiles_x = (W + kTW - 1) / kTW;
     *tiles_y = (H + th - 1) / th;
-    int p = 4;
+    int p = conv_per(K);
     while (p > 1 && planes * ((*tiles_y + p - 1) / p) * *tiles_x < 4096) p /= 2;
     *per = p;
     return ((*tiles_y + p - 1) / p) * *tiles_x;
@@ -1314,7 +1340,7 @@ bool dw_stats_geometry(const DwShape& sh, DwStatsGeom* g) {
     int64_t tiles_y = 0;
     int per = 1;
     const int rb = conv_rows_per_thread(sh.K, sh.S, sh.D);
-    g->tpp = conv_groups(sh.N * sh.C, sh.Ho, sh.Wo, &g->tiles_x, &tiles_y, &per,
+    g->tpp = conv_groups(sh.N * sh.C, sh.Ho, sh.Wo, &g->tiles_x, &tiles_y, &per, sh.K,
                          (int64_t)kTH * rb);
     g->rows = (int64_t)per * kTH * rb;
     return true;
@@ -1329,7 +1355,7 @@ hipError_t launch_dw_forward(const DwShape& sh, const float* x, const float* w,
     int per = 1;
     const int rb = conv_rows_per_thread(sh.K, sh.S, sh.D);
     const int64_t tpp =
-        conv_groups(sh.N * sh.C, sh.Ho, sh.Wo, &tiles_x, &tiles_y, &per, (int64_t)kTH * rb);
+        conv_groups(sh.N * sh.C, sh.Ho, sh.Wo, &tiles_x, &tiles_y, &per, sh.K, (int64_t)kTH * rb);
     const int tok = prof_begin(s, part ? "dw_conv_stats" : "dw_conv");
     const bool fast = planes_fit_32(sh) && fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
         using CF = decltype(cf);
@@ -1367,7 +1393,7 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
         // a small layer: dx and the weight gradient in one launch
         int64_t dtx = 0, dty = 0, wtx = 0, wty = 0;
         int dper = 1;
-        const int64_t dtpp = conv_groups(sh.N * sh.C, sh.Hi, sh.Wi, &dtx, &dty, &dper);
+        const int64_t dtpp = conv_groups(sh.N * sh.C, sh.Hi, sh.Wi, &dtx, &dty, &dper, sh.K);
         const int64_t wper = wgrad_per(sh);
         const int64_t wtpp = wgrad_groups(sh, wper, &wtx, &wty);
         const int64_t nbd = sh.N * sh.C * dtpp, nbw = sh.N * sh.C * wtpp;
@@ -1410,7 +1436,7 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
             int64_t tiles_x = 0, tiles_y = 0;
             int per = 1;
             const int rb = conv_rows_per_thread(sh.K, sh.S, sh.D);
-            const int64_t tpp = conv_groups(sh.N * sh.C, sh.Hi, sh.Wi, &tiles_x, &tiles_y, &per,
+            const int64_t tpp = conv_groups(sh.N * sh.C, sh.Hi, sh.Wi, &tiles_x, &tiles_y, &per, sh.K,
                                             (int64_t)kTH * rb);
             const int64_t padf = (sh.K - 1) * sh.D - sh.pad;
             done = planes_fit_32(sh) && fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
@@ -1434,7 +1460,7 @@ hipError_t launch_dw_backward(const DwShape& sh, const float* dy, const float* x
         if (!done && sh.S > 1) {
             int64_t tiles_x = 0, tiles_y = 0;
             int per = 1;
-            const int64_t tpp = conv_groups(sh.N * sh.C, sh.Hi, sh.Wi, &tiles_x, &tiles_y, &per);
+            const int64_t tpp = conv_groups(sh.N * sh.C, sh.Hi, sh.Wi, &tiles_x, &tiles_y, &per, sh.K);
             done = planes_fit_32(sh) && fast_cfg(sh.K, sh.S, sh.D, [&](auto cf) {
                 using CF = decltype(cf);
                 if constexpr (CF::s > 1) {

@@ -252,10 +252,16 @@ def _dwf(L, N, C, H, W, K, G, flags=1, eps=1e-5, stride=1, dil=1):
 def test_dw_conv_gn_workspace_bytes(L):
     al = lambda b: (b + 255) // 256 * 256
     gn = soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16)
-    # k7 at 64 x 2048^2: tile groups of 4 tiles of 32 x 64 outputs, 16 x 32
-    # groups per plane -> 64 x 512 partials of 16 B after the GroupNorm part
+    # k7 at 64 x 2048^2: tile groups of 16 tiles of 32 x 64 outputs, 4 x 32
+    # groups per plane -> 64 x 128 partials of 16 B after the GroupNorm part
     assert soar_gn.dw_conv_gn_workspace_bytes(1, 64, 2048, 2048, 2048, 2048, 7, 3, 1, 1, 16) \
-        == al(gn) + 64 * 512 * 16
+        == al(gn) + 64 * 128 * 16
+    # k5 and k3 at dilation 1 run two output rows per thread (64-row tiles),
+    # k5 in groups of 8 tiles (4 x 32 per plane), k3 of 4 (8 x 32 per plane)
+    assert soar_gn.dw_conv_gn_workspace_bytes(1, 64, 2048, 2048, 2048, 2048, 5, 2, 1, 1, 16) \
+        == al(gn) + 64 * 128 * 16
+    assert soar_gn.dw_conv_gn_workspace_bytes(1, 64, 2048, 2048, 2048, 2048, 3, 1, 1, 1, 16) \
+        == al(gn) + 64 * 256 * 16
     # units small enough for the one-launch GroupNorm: its workspace alone
     assert soar_gn.dw_conv_gn_workspace_bytes(1, 8, 32, 32, 32, 32, 3, 1, 1, 1, 2) == \
         al(soar_gn.workspace_bytes(1, 8, 32 * 32, 2))
