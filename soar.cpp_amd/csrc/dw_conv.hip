@@ -970,13 +970,13 @@ void k_dw_cba_bwd(
         for (int k = 0; k < NR; ++k) {
             const int i = t + k * kDwThreads;
             if (i < nel) {
-                float d = 0.0f;
-                if (inside & (1u << k)) {
-                    const float xh = fmaf(pz[k] - mu, r, e);
-                    const float dzs = SILU ? dsilu_fast(pg[k], fmaf(gm, xh, bt)) : pg[k];
-                    d = fmaf(A, dzs, fmaf(Dc, xh, B));
-                }
-                tdz[base + i] = d;
+                // every element computes and then selects (elements outside
+                // the image are rare, so a branch only cost its exec-mask
+                // code: k7 1.119 -> 1.103 ms at 64 x 2048^2)
+                const float xh = fmaf(pz[k] - mu, r, e);
+                const float dzs = SILU ? dsilu_fast(pg[k], fmaf(gm, xh, bt)) : pg[k];
+                const float dv = fmaf(A, dzs, fmaf(Dc, xh, B));
+                tdz[base + i] = (inside & (1u << k)) ? dv : 0.0f;
                 tx[base + i] = px[k];
             }
         }
