@@ -50,6 +50,7 @@
 #include "gn_math.hpp"
 #include "gn_moments.hpp"
 #include "soar_gn.h"
+#include "xcd_order.hpp"
 
 namespace soar {
 namespace gn {
@@ -126,9 +127,22 @@ __device__ __forceinline__ Chunk chunk_of(int64_t b, int64_t HW, int64_t chunk,
     return k;
 }
 
-// Block index of this block inside its batch [block0, block0 + nb).
+// Block index of this block inside its batch [block0, block0 + nb): the
+// XCD-aware order of xcd_block (each XCD runs 32 consecutive chunks), then
+// reversed for the passes that walk back through the MALL.  Against the
+// hardware order at config 3, statistics / apply / reduction / dx 163.7 /
+// 336.8 / 319.1 / 508.3 -> 160.0 / 332.6 / 316.0 / 501.1 us, 1.326 ->
+// 1.312 ms per step (three rounds, one box); with runs of 8 chunks per XCD
+// the apply and the reduction had lost as much as the others gained.
 __device__ __forceinline__ int64_t batch_block(int64_t block0, int64_t nb, int reverse) {
-    return block0 + (reverse ? nb - 1 - (int64_t)blockIdx.x : (int64_t)blockIdx.x);
+    const int64_t pb = xcd_block(blockIdx.x, nb);
+    return block0 + (reverse ? nb - 1 - pb : pb);
+}
+
+// The same for the chunk blocks of a launch whose first fin_nu blocks
+// finish the previous batch's units.
+__device__ __forceinline__ int64_t chunk_block(int64_t block0, int64_t fin_nu) {
+    return block0 + xcd_block((int64_t)blockIdx.x - fin_nu, (int64_t)gridDim.x - fin_nu);
 }
 
 template <bool NTL>
@@ -290,7 +304,7 @@ __global__ __launch_bounds__(kThreads) void k_stats(
                           cpp, cpg, eps, lds);
         return;
     }
-    const int64_t b = block0 + (int64_t)blockIdx.x - fin_nu;
+    const int64_t b = chunk_block(block0, fin_nu);
     const Chunk ck = chunk_of(b, HW, chunk, cpp);
     const float* p = x + ck.plane * HW + ck.off;
     const int t = threadIdx.x;
@@ -743,7 +757,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_reduce(
                         lo_ws, plane_sums, unit_sums, C, HW, cpp, cpg, ldsd);
         return;
     }
-    const int64_t b = block0 + (int64_t)blockIdx.x - fin_nu;
+    const int64_t b = chunk_block(block0, fin_nu);
     const Chunk ck = chunk_of(b, HW, chunk, cpp);
     const PlaneCoef k = plane_coef(ck.plane, C, G, cpg, gamma, beta, mean, rstd,
                                    LOREC ? nullptr : mean_lo);

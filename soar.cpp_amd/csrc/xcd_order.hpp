@@ -40,8 +40,9 @@ namespace gn {
 // hardware order, 430 us in runs of 8 blocks per XCD and 424 us in runs of
 // 32; the streamed forward with statistics at 64 -> 64 channels of 2048^2
 // went from 486 to 468 and then 460 us, the fused CBA backward from 1.01 to
-// 0.99 and then 0.97 ms.  (The GroupNorm passes, whose blocks read
-// 32 KiB runs, gained nothing: 1.324 ms per config-3 step either way.)
+// 0.99 and then 0.97 ms.  The GroupNorm passes, whose blocks stream 32 KiB
+// runs, gained nothing in runs of 8 (1.324 ms per config-3 step either
+// way) and 1% in runs of 32 (1.326 -> 1.312 ms).
 __device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
     constexpr int64_t kX = 8, kT = 32, kWin = kX * kT;  // XCDs, blocks per XCD run
     if (b >= nb / kWin * kWin) return b;
