@@ -1299,16 +1299,18 @@ bool dw_has_fast(int64_t K, int64_t S, int64_t D) {
     return fast_cfg(K, S, D, [](auto) {});
 }
 
-// Tiles per weight-gradient block: 32 for K >= 7, 16 for K = 5, 4 below
+// Tiles per weight-gradient block: 64 for K >= 7, 16 for K = 5, 4 below
 // (each block reduces its K*K+1 sums once, which at k7 costs as much as a
 // few tiles' FMAs), halved while the grid would hold fewer than 2048 blocks
 // (a block walks its tiles one after another: few large planes, e.g. 16
 // channels at 256 x 256 with k3 s2, ran 64 blocks of 4 tiles in 55 us).
-// At 64 x 2048^2, k7 8 / 16 / 32 tiles: 0.704 / 0.628 / 0.585 ms; k5 4 / 8 /
-// 16: 0.524 / 0.463 / 0.448 ms (0.446 -> 0.432 ms for 8 -> 16 on another box).  K >= 5 matches the fused CBA backward's grouping, so
-// both add the same partial sums in the same order.
+// At 64 x 2048^2, k7 8 / 16 / 32 tiles: 0.704 / 0.628 / 0.585 ms, and with
+// the XCD runs of 32 tiles 16 / 32 / 64: 0.521 / 0.487 / 0.478 ms; k5 4 / 8
+// / 16: 0.524 / 0.463 / 0.448 ms (0.446 -> 0.432 ms for 8 -> 16 on another
+// box).  K >= 5 matches the fused CBA backward's grouping, so both add the
+// same partial sums in the same order.
 int64_t wgrad_per(const DwShape& sh) {
-    int64_t per = sh.K >= 7 ? 32 : sh.K >= 5 ? 16 : 4;
+    int64_t per = sh.K >= 7 ? 64 : sh.K >= 5 ? 16 : 4;
     const int64_t tx = (sh.Wo + kTW - 1) / kTW, ty = (sh.Ho + kTH - 1) / kTH;
     while (per > 1 && sh.N * sh.C * ((ty + per - 1) / per) * tx < 2048) per /= 2;
     return per;
@@ -1525,16 +1527,17 @@ bool dw_cba_fused_fits(const DwShape& sh) {
 }
 
 namespace {
-// Tiles per block of the fused CBA backward: 32 for K >= 7 and 16 for K = 5
+// Tiles per block of the fused CBA backward: 64 for K >= 7 and 16 for K = 5
 // (the block reduces its K*K+1 weight-gradient sums once per block; the
 // stand-alone weight gradient groups the same tiles), 2 for K = 3 (more
 // blocks), halved while the grid would hold fewer than 2048 blocks.  At
-// 64 x 2048^2, k7 8 / 16 / 32 tiles: 1.39 / 1.31 / 1.29 ms; k5 16 / 8 / 4 /
-// 2: 0.934 / 0.934 / 1.04 / 1.14 ms; k3 4 / 2: 0.88 / 0.85 ms.
+// 64 x 2048^2, k7 8 / 16 / 32 tiles: 1.39 / 1.31 / 1.29 ms (later kernels,
+// with the XCD runs of 32 tiles, 16 / 32 / 64: 1.144 / 1.107 / 1.103 ms); k5
+// 16 / 8 / 4 / 2: 0.934 / 0.934 / 1.04 / 1.14 ms; k3 4 / 2: 0.88 / 0.85 ms.
 int64_t dw_cba_per(const DwShape& sh, int64_t* tiles_x, int64_t* tiles_y, int64_t* tpp) {
     *tiles_x = (sh.Wi + kTW - 1) / kTW;
     *tiles_y = (sh.Hi + kTH - 1) / kTH;
-    int64_t per = sh.K >= 7 ? 32 : sh.K >= 5 ? 16 : 2;
+    int64_t per = sh.K >= 7 ? 64 : sh.K >= 5 ? 16 : 2;
     while (per > 1 && sh.N * sh.C * ((*tiles_y + per - 1) / per) * *tiles_x < 2048) per /= 2;
     *tpp = ((*tiles_y + per - 1) / per) * *tiles_x;
     return per;

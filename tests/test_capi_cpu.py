@@ -419,11 +419,12 @@ def test_dw_cba_backward_workspace_and_tuning(L):
     gn = (soar_gn.workspace_bytes(1, 64, 2048 * 2048, 16) + 255) // 256 * 256
     H = W = 2048
     # fused: the GroupNorm workspace, then one (K*K+1)-float partial per
-    # channel and block; 32 x 64 tiles, 2 per block at k3, 32 at k7
+    # channel and block; 32 x 64 tiles, 2 per block at k3, 64 at k7 (one
+    # group per tile column of a 2048-row plane)
     assert soar_gn.dw_cba_backward_workspace_bytes(1, 64, H, W, H, W, 3, 1, 1, 1, 16) == (
         gn + 4 * (32 * 32) * 64 * 10)
     assert soar_gn.dw_cba_backward_workspace_bytes(1, 64, H, W, H, W, 7, 3, 1, 1, 16) == (
-        gn + 4 * (2 * 32) * 64 * 50)
+        gn + 4 * (1 * 32) * 64 * 50)
     dz = 64 * H * W * 4
     # outside the fused kernel (stride 2, padding other than "same", a K
     # without a tiled kernel): dz, the GroupNorm workspace, the conv backward's
