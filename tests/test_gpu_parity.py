@@ -105,6 +105,10 @@ SHAPES = [
     (3, 6, 1000, 3, "normal"),             # small planes, one chunk each
     (1, 2, 70001, 1, "normal"),            # HW % 4 != 0: scalar path, ragged chunk
     (1, 2, 70000, 2, "normal"),            # vector path, ragged last chunk
+    # 300 statistics / reduction blocks and 600 apply / dx blocks: each pass
+    # ends in a part-filled window of the XCD-aware block order (blocks past
+    # the last whole window of 256 keep their order), and a ragged last chunk
+    (1, 3, 819000, 1, "normal"),
     (2, 5, 33, 5, "normal"),               # one channel per group
     (1, 1, 1, 1, "normal"),                # single element: var = 0
     (1, 4, 1, 2, "offset"),                # HW = 1, large mean
