@@ -107,6 +107,9 @@ FUSED_SHAPES = [
     (1, 64, 64, 70000, 16, "offset", True),    # |mean| / std ~ 1e5
     (1, 130, 72, 4096, 8, "normal", True),     # general path, two row tiles
     (3, 16, 32, 1024, 8, "normal", True),      # exactly one chunk per plane
+    # 300 pixel chunks of 1024: the streamed kernel's grid ends in a part-
+    # filled window of the XCD-aware block order
+    (1, 64, 64, 300 * 1024, 16, "normal", True),
     # small grids with K >= 128: K split over blocks (slices + reduce)
     (1, 256, 128, 4096, 16, "normal", True),   # the Nano LKR at 1024^2, stride 16
     (1, 512, 256, 1024, 32, "offset", True),   # stride 32; large |mean|
